@@ -1,0 +1,175 @@
+/*
+ * TaoMemory attention operator: C ABI of the gfx950 (MI355X) HIP library
+ * libtao_hip.so.
+ *
+ * The library replaces the reference's kernel layer (Triton kernels and hot
+ * torch-op chains) and its regional CUDA Graph. Host code (the Python
+ * tao_attention package, or any FFI) owns every buffer: the library never
+ * allocates or frees caller memory. All tensors are device pointers with
+ * element strides; the head dimension is contiguous. All arithmetic is on
+ * bf16 storage with fp32 accumulation.
+ *
+ * Return convention: 0 = ok; negative = contract error (the Python host
+ * raises ValueError); positive = HIP runtime error code (RuntimeError).
+ * tao_last_error() returns a thread-local message for the last failure.
+ *
+ * Threading: stream-ordered, no internal threads; calls on one state must be
+ * serialised by the caller (the reference's serial-use rule,
+ * docs/graph.md:13-17).
+ */
+#ifndef TAO_MEMORY_H
+#define TAO_MEMORY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TAO_ABI_VERSION 1
+
+enum tao_status {
+  TAO_OK = 0,
+  TAO_E_SHAPE = -1,      /* unsupported head_dim / geometry / shape */
+  TAO_E_CAPACITY = -2,   /* a count exceeds the state's capacity */
+  TAO_E_ARGUMENT = -3,   /* null pointer or inconsistent argument */
+  TAO_E_WORKSPACE = -4   /* workspace too small */
+};
+
+enum tao_dtype { TAO_BF16 = 0, TAO_FP32 = 1 };
+
+/* Device-resident state of one request x layer (reference StreamCache +
+ * LayerState, tao_stream.py:126-160, 790-834), laid out for HBM streaming:
+ * a capacity-backed fine bank replaces the reference's per-seal torch.cat
+ * repack (tao_stream.py:455-462) and a token ring replaces the local-window
+ * concatenation (tao_stream.py:927-930, 959-969). */
+typedef struct tao_state_dev {
+  int32_t batch, heads, head_dim;   /* B, H, D (D in {64, 128}) */
+  int32_t local_keep, fine_tokens;  /* 512, 256: ring length = their sum */
+  int32_t coarse_group;             /* 8 */
+  int32_t fine_cap, page_cap, sel_cap, chosen_cap;
+  void* ring_k;     /* bf16 [B, L, H, D]  rotated keys, slot = position % L */
+  void* ring_v;     /* bf16 [B, L, H, D]  values */
+  void* ring_raw;   /* bf16 [B, L, H, D]  raw keys (writer input) */
+  void* bank_c;     /* bf16 [B, H, fine_cap, D, D] fine memories */
+  void* fine_z;     /* bf16 [B, H, fine_cap, D]    fine descriptors */
+  void* fine_sw;    /* bf16 [B, H, fine_cap, D]    r(exp(r(z - page_z))) */
+  void* page_z;     /* bf16 [B, H, page_cap, D]    completed + pending page */
+  void* page_w;     /* bf16 [B, H, page_cap, D]    r(softmax over pages) */
+  int32_t* sel;     /* [B, H, sel_cap]  selected fine ids, score order */
+  int32_t* chosen;  /* [B, H, chosen_cap] chosen coarse pages, ascending */
+  int64_t* header;  /* device [4]: position, M, reserved, reserved */
+  void* workspace;  /* scratch: per-unit partials and arrival counters */
+  size_t workspace_bytes;
+} tao_state_dev;
+
+/* New-token operands: q/k/v/raw_q/raw_k, each [B, T, H, D] bf16 with
+ * element strides (batch, token, head); D contiguous. */
+typedef struct tao_tokens {
+  const void* q; const void* k; const void* v; const void* raw_q; const void* raw_k;
+  int64_t q_s[3], k_s[3], v_s[3], rq_s[3], rk_s[3];
+  int32_t tokens;
+} tao_tokens;
+
+/* Caller fusion parameters: fusion_a/b [H, D, 3] of dtype `dtype`
+ * (cast to bf16 round-to-nearest-even inside, fusion_pointwise.py:103-108),
+ * gain = bf16(2 * alpha) (operator.py:89). */
+typedef struct tao_fusion {
+  const void* fusion_a; const void* fusion_b;
+  int32_t dtype;
+  int64_t a_s[3], b_s[3];
+  float gain;
+  int32_t coarse_on, fine_on;
+} tao_fusion;
+
+int tao_abi_version(void);
+const char* tao_last_error(void);
+
+/* Workspace bytes a state of this geometry needs (no hidden allocation). */
+size_t tao_workspace_bytes(int32_t batch, int32_t heads, int32_t head_dim,
+                           int32_t sel_cap, int32_t max_query_tokens);
+
+/* Zero the arrival counters inside the workspace (call once per new
+ * workspace; kernels leave them zeroed). */
+int tao_workspace_init(const tao_state_dev* st, void* stream);
+
+/* One fused single-token decode step (replaces the memo-backed q1 region,
+ * tao_stream.py:399-433, query_fresh_fine.py:52-75, the local SDPA call
+ * flash_attention.py:25-29, the local concat tao_stream.py:927-930, and the
+ * fusion kernels fusion_pointwise.py:95-117 / operator.py:86-94).
+ * Reads the stream position from st->header[0], appends the token to the
+ * ring, reads the `selected` fines of the current route (0 before the first
+ * seal: output = local attention), writes out [B,1,H,D] (element strides
+ * out_s) and advances header[0]. */
+int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok,
+                    const tao_fusion* fu, int32_t selected, void* out,
+                    const int64_t* out_s, void* stream);
+
+/* Routing refresh from one anchor query row (replaces tao_stream.py:310-357
+ * and _topk_oldest :50-53). raw_q_row: [B, H, D] view with strides rq_s
+ * (batch, head). Writes st->sel / st->chosen and header[1] = M. */
+int tao_route(const tao_state_dev* st, const void* raw_q_row,
+              const int64_t* rq_s, int32_t completed, int32_t pending,
+              int32_t coarse, int32_t selected, void* stream);
+
+/* Softmax fine writer for `count` blocks (replaces _seal, tao_stream.py:
+ * 56-77, and the packed-bank append :455-462). Block i covers absolute
+ * positions [start_pos[i], start_pos[i] + fine_tokens) read from the ring
+ * (positions < new_base) or from the token operands (>= new_base); its
+ * z / C go to fine slot first_slot + i. start_pos: device int64 [count]. */
+int tao_write_fine(const tao_state_dev* st, const tao_tokens* tok,
+                   int64_t new_base, const int64_t* start_pos,
+                   int32_t first_slot, int32_t count, void* stream);
+
+/* Page bookkeeping after sealing fine `slot` (replaces append_fine's
+ * page summary tao_stream.py:477-501, the pending summary :277-290 and the
+ * seal-epoch memo _prepare_q1_page_memo :399-416): page descriptor of the
+ * slot's group, segment weights of the group's fines, page weights over the
+ * `pages` current pages. recompute = 0 keeps the group's page descriptor
+ * already in page_z (snapshot import) instead of recomputing it. */
+int tao_seal_epilogue(const tao_state_dev* st, int32_t slot, int32_t pages,
+                      int32_t recompute, void* stream);
+
+/* Exact local attention with the suffix causal mask (replaces
+ * flash_attn_func, flash_attention.py:16-37, and the local-window concat,
+ * tao_stream.py:927-930). Query row r of tok.q sits at absolute position
+ * qpos0 + r; key row j of tok.k / tok.v at kpos0 + j, and keys older than
+ * kpos0 come from the ring. tiles: device int64 [n_tiles][3] = (first query
+ * row, count <= 128, key_start): the tile's queries see keys from key_start
+ * up to their own position. local: bf16 [B, tok.tokens, H, D] contiguous. */
+int tao_local_attention(const tao_state_dev* st, const tao_tokens* tok,
+                        int64_t qpos0, int64_t kpos0, const int64_t* tiles,
+                        int32_t n_tiles, void* local, void* stream);
+
+/* Selected fine read plus fusion for `count` queries starting at token
+ * `first` of tok that share the current route (replaces query_fresh_fine.py
+ * :52-75 for multi-token calls and fusion_pointwise.py:95-117). local is
+ * the [B, T, H, D] local-attention output; out gets the fused heads. When
+ * fu->fine_on is 0 the output is the local attention unchanged. */
+int tao_read_fuse(const tao_state_dev* st, const tao_tokens* tok,
+                  int32_t first, int32_t count, int32_t selected,
+                  const tao_fusion* fu, const void* local, void* out,
+                  const int64_t* out_s, void* stream);
+
+/* Copy `count` tokens starting at token `first` of tok into the ring at
+ * absolute positions [pos, pos + count) (keys, values, raw keys). */
+int tao_ring_append(const tao_state_dev* st, const tao_tokens* tok,
+                    int32_t first, int32_t count, int64_t pos, void* stream);
+
+/* hipGraph of the decode step (replaces HistoryRegionGraph,
+ * history_region_graph.py:10-113). The graph captures one copy of the
+ * operands into stable staging buffers plus tao_decode_step; header-driven
+ * counts let it replay across seals and refreshes. staging: bf16 device
+ * buffer of 5 * B * H * D elements; out_stage: bf16 [B,1,H,D]. */
+int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu,
+                     int32_t selected, void* staging, void* out_stage,
+                     void* stream, void** graph_out);
+int tao_graph_launch(void* graph, const tao_tokens* tok, void* stream);
+int tao_graph_destroy(void* graph);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TAO_MEMORY_H */

@@ -1,0 +1,515 @@
+"""TaoMemory CPU oracle: the reference's inference arithmetic restated in torch.
+
+TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg may import this module, and only as the
+checker or the timed CPU baseline; the product never routes through it.
+
+Every function cites the reference file:line it restates (paths relative to
+the reference repository root). Tensors are CPU, layout [B, T, H, D] for
+token streams, [B, H, S, D] for per-fine descriptors, [B, H, S, D, D] for the
+fine-memory bank. Rounding points follow the reference's torch/Triton casts;
+see ``oracle/numerics.py`` for the three backend choices fixed here.
+
+Pinning (tests/test_oracle.py): closed forms for the schedule and budget;
+torch's own bf16 ``logsumexp``/``softmax`` for the composite ops; fp64 brute
+force for writer, read, local attention and fusion; stable-argsort brute force
+for routing; invariants (decode == 1-token prefill, chunked == whole prefill,
+export/import equality, banks independent of queries).
+"""
+
+import math
+
+import torch
+
+from .numerics import (BF16, F32, exp32, fold_sum, log32, logsumexp,
+                       quarter_sum, rnd, softmax)
+
+NEG_INF = float("-inf")
+
+
+# ----------------------------------------------------------------------------
+# Closed forms: config.py:54-60, tao_stream.py:29-37, 196-211, 914-917
+# ----------------------------------------------------------------------------
+
+class Geometry:
+    """Geometry fields of the reference TaoConfig (config.py:7-19)."""
+
+    def __init__(self, fine_tokens=256, local_keep=512, coarse_group=8,
+                 route_period=24, layer_stagger=2, budget_root_scale=2,
+                 budget_offset=2, coarse_index_only=True):
+        self.fine_tokens = fine_tokens
+        self.local_keep = local_keep
+        self.coarse_group = coarse_group
+        self.route_period = route_period
+        self.layer_stagger = layer_stagger
+        self.budget_root_scale = budget_root_scale
+        self.budget_offset = budget_offset
+        self.coarse_index_only = coarse_index_only
+
+    @classmethod
+    def from_config(cls, config):
+        return cls(config.fine_tokens, config.local_keep, config.coarse_group,
+                   config.route_period, config.layer_stagger,
+                   config.budget_root_scale, config.budget_offset,
+                   config.coarse_index_only)
+
+    @property
+    def serve_limit(self):
+        return self.local_keep + self.fine_tokens
+
+    def budget(self, count):
+        """config.py:54-60: min(n, ceil(sqrt(scale*n)) + offset)."""
+        if count <= 0:
+            return 0
+        root = math.isqrt(self.budget_root_scale * count)
+        if root * root < self.budget_root_scale * count:
+            root += 1
+        return min(count, root + self.budget_offset)
+
+    def routed_counts(self, completed, pending):
+        """tao_stream.py:29-37 -> (coarse pages, eligible fines, selected M)."""
+        group = self.coarse_group
+        coarse_budget = self.budget(group * completed)
+        coarse = min(completed, (2 * coarse_budget + group - 1) // group)
+        eligible = group * coarse + pending
+        selected = min(eligible, self.budget(group * completed + pending))
+        return coarse, eligible, selected
+
+    def is_turn(self, position, layer):
+        """tao_stream.py:202-208: route refresh positions of one layer."""
+        first = self.serve_limit
+        first_turn = first + self.layer_stagger * layer
+        return position == first or (
+            position >= first_turn
+            and (position - first_turn) % self.route_period == 0)
+
+    def next_turn(self, position, layer):
+        """tao_stream.py:209-210: next refresh strictly after ``position``."""
+        first_turn = self.serve_limit + self.layer_stagger * layer
+        if position < first_turn:
+            return first_turn
+        period = self.route_period
+        return first_turn + period * ((position - first_turn) // period + 1)
+
+
+# ----------------------------------------------------------------------------
+# Writer and page summaries: tao_stream.py:56-77, 478-501
+# ----------------------------------------------------------------------------
+
+def seal_softmax(raw_k, v):
+    """Softmax fine writer for one block, tao_stream.py:66-77.
+
+    raw_k, v: [B, F, H, D] (F = fine_tokens). Returns z [B, H, D] and
+    C [B, H, D, D] in raw_k's dtype. Per channel: m = max_t k,
+    e = r(exp(r(k - m))), Z = r(sum_t e), P = r(e / Z),
+    z = r(m + r(log Z)), C = r(P^T V) with fp32 accumulation.
+    """
+    dtype = raw_k.dtype
+    top = raw_k.amax(dim=1, keepdim=True)
+    shifted = rnd(raw_k.to(F32) - top.to(F32), dtype)
+    e = rnd(exp32(shifted.to(F32)), dtype)
+    total = rnd(quarter_sum(e, 1), dtype)                    # [B, H, D]
+    prob = rnd(e.to(F32) / total.unsqueeze(1).to(F32), dtype)  # [B, F, H, D]
+    z = rnd(top.squeeze(1).to(F32) + rnd(log32(total.to(F32)), dtype).to(F32),
+            dtype)
+    c = torch.einsum("bthd,bthe->bhde", prob.to(torch.float64),
+                     v.to(torch.float64))
+    return z, rnd(c, dtype)
+
+
+def page_summary(z_group):
+    """Completed page / pending-page descriptor r(logsumexp over fines).
+
+    z_group: [B, H, n, D] -> [B, H, D]; tao_stream.py:283, 412, 485.
+    """
+    return logsumexp(z_group, 2)
+
+
+def segment_weights(fine_z, page_z_of_fine):
+    """sw = r(exp(r(z - pz))), tao_stream.py:349 / query_fresh_fine.py:38-39."""
+    dtype = fine_z.dtype
+    diff = rnd(fine_z.to(F32) - page_z_of_fine.to(F32), dtype)
+    return rnd(exp32(diff.to(F32)), dtype)
+
+
+def page_coarse_matrix(z_group, page_z, c_group):
+    """Coarse value matrix of a completed page (non-index-only), :486-499.
+
+    weight = r(exp(r(z - page_z))); page_C = r(sum_s weight[s,d] C_s[d,e]).
+    """
+    weight = segment_weights(z_group, page_z.unsqueeze(2))     # [B,H,8,D]
+    pc = torch.einsum("bhsd,bhsde->bhde", weight.to(torch.float64),
+                      c_group.to(torch.float64))
+    return rnd(pc, z_group.dtype)
+
+
+# ----------------------------------------------------------------------------
+# Routing and the selected read: tao_stream.py:253-374, query_fresh_fine.py
+# ----------------------------------------------------------------------------
+
+def topk_oldest(scores, count):
+    """tao_stream.py:50-53: stable descending order, first ``count``."""
+    return scores.argsort(dim=-1, descending=True, stable=True)[
+        ..., :min(count, scores.shape[-1])]
+
+
+def query_weights(raw_q):
+    """h = r(softmax_D(raw_q)), tao_stream.py:253-254 / :421."""
+    return softmax(raw_q, -1)
+
+
+def page_weights(page_z):
+    """pw = r(softmax over pages), page_z [B, H, P, D], tao_stream.py:291/414."""
+    return softmax(page_z, 2)
+
+
+def page_values(h, pw):
+    """hv = r(h * pw): [B, Q, H, D] x [B, H, P, D] -> [B, Q, H, P, D] (:298)."""
+    return rnd(h.unsqueeze(3).to(F32) * pw.unsqueeze(1).to(F32), h.dtype)
+
+
+def route(hv_anchor, fine_sw, completed, pending, geometry):
+    """Routing refresh from one anchor query, tao_stream.py:310-357.
+
+    hv_anchor: [B, H, P, D] (P = completed + (pending > 0)).
+    fine_sw:   [B, H, S, D] segment weights of every sealed fine.
+    Returns (chosen_page [B, H, coarse] int64 ascending,
+             selected_id [B, H, M] int64 in score order, scores dict).
+    """
+    b, heads, _, d = hv_anchor.shape
+    dtype = hv_anchor.dtype
+    group = geometry.coarse_group
+    coarse, _, fine_count = geometry.routed_counts(completed, pending)
+    pages, ids = [], []
+    chosen = torch.zeros((b, heads, 0), dtype=torch.int64)
+    page_mass = None
+    if coarse:
+        page_mass = rnd(fold_sum(hv_anchor[:, :, :completed], -1), dtype)
+        chosen = topk_oldest(page_mass, coarse).sort(-1).values
+        segment = torch.arange(group)
+        pages.append(chosen.unsqueeze(-1).expand(b, heads, coarse, group)
+                     .reshape(b, heads, coarse * group))
+        ids.append((chosen.unsqueeze(-1) * group + segment)
+                   .reshape(b, heads, coarse * group))
+    if pending:
+        pend = torch.arange(pending).view(1, 1, pending).expand(b, heads, pending)
+        pages.append(torch.full_like(pend, completed))
+        ids.append(completed * group + pend)
+    cand_page = torch.cat(pages, -1)
+    cand_id = torch.cat(ids, -1)
+    e = cand_id.shape[-1]
+    hv_c = torch.gather(hv_anchor, 2, cand_page.unsqueeze(-1).expand(b, heads, e, d))
+    sw_c = torch.gather(fine_sw, 2, cand_id.unsqueeze(-1).expand(b, heads, e, d))
+    channel = rnd(hv_c.to(F32) * sw_c.to(F32), dtype)
+    mass = rnd(fold_sum(channel, -1), dtype)
+    order = topk_oldest(mass, fine_count)
+    selected = cand_id.gather(-1, order)
+    return chosen, selected, {"page_mass": page_mass, "mass": mass,
+                              "candidates": cand_id}
+
+
+def selected_read(hv, fine_sw, selected, bank_c, group):
+    """query_fresh_fine.py:8-75: fine = r(r(num) / den).
+
+    hv [B, Q, H, P, D]; fine_sw [B, H, S, D]; selected [B, H, M];
+    bank_c [B, H, S, D, D]. ch = r(hv[page] * sw); num = r(sum_m ch @ C)
+    (fp64 here; fp32 in the reference, so parity is to tolerance);
+    den = r(sum_m r(sum_d ch)); returns (fine [B,Q,H,D], ch [B,Q,H,M,D]).
+    """
+    b, q, heads, _, d = hv.shape
+    dtype = hv.dtype
+    m = selected.shape[-1]
+    page = selected // group
+    hv_sel = torch.gather(hv, 3, page[:, None, :, :, None].expand(b, q, heads, m, d))
+    sw_sel = torch.gather(fine_sw, 2, selected.unsqueeze(-1).expand(b, heads, m, d))
+    ch = rnd(hv_sel.to(F32) * sw_sel.unsqueeze(1).to(F32), dtype)  # [B,Q,H,M,D]
+    c_sel = torch.gather(bank_c, 2, selected[..., None, None].expand(b, heads, m, d, d))
+    num = torch.einsum("bqhmd,bhmde->bqhe", ch.to(torch.float64),
+                       c_sel.to(torch.float64))
+    num = rnd(num, dtype)
+    per_slot = rnd(fold_sum(ch, -1), dtype)                 # [B,Q,H,M]
+    den = rnd(fold_sum(per_slot, -1), dtype)                # [B,Q,H]
+    fine = rnd(num.to(F32) / den.unsqueeze(-1).to(F32), dtype)
+    return fine, ch
+
+
+def coarse_read(h, page_z_completed, page_c):
+    """Coarse value read (non-index-only), tao_stream.py:299-305."""
+    dtype = h.dtype
+    weight = softmax(page_z_completed, 2)
+    hv = page_values(h, weight)
+    out = torch.einsum("bthpd,bhpde->bthe", hv.to(torch.float64),
+                       page_c.to(torch.float64))
+    return rnd(out, dtype)
+
+
+# ----------------------------------------------------------------------------
+# Fusion: fusion_pointwise.py:10-117, operator.py:86-97
+# ----------------------------------------------------------------------------
+
+def fusion(raw_q, local, coarse, fine, fusion_a, fusion_b, alpha,
+           coarse_on, fine_on):
+    """Three-branch presence-aware fusion with every bf16 cast explicit.
+
+    Kernel math is bf16 regardless of the stream dtype (Triton casts,
+    fusion_pointwise.py:103-121, 151-166); results are stored in raw_q's dtype.
+    """
+    dtype = raw_q.dtype
+    q = raw_q.to(F32)
+    a = rnd(fusion_a.to(F32)).to(F32)                       # [H, D, 3]
+    bias = rnd(fusion_b.to(F32)).to(F32)
+    present = int(coarse_on) + int(fine_on)
+    local_bias = rnd(torch.tensor(math.log(present) if present else 0.0,
+                                  dtype=F32)).to(F32)
+    scores = []
+    for branch in range(3):
+        prod = rnd(a[..., branch] * q).to(F32)
+        s = rnd(prod + bias[..., branch])
+        if branch == 0:
+            s = rnd(s.to(F32) + local_bias)
+        if (branch == 1 and not coarse_on) or (branch == 2 and not fine_on):
+            s = torch.full_like(s, NEG_INF)
+        scores.append(s)
+    score = rnd(torch.stack(scores, -1), dtype)            # stored in dtype
+    rho = rnd(softmax(score, -1), dtype)                    # F.softmax + .to
+    gain = rnd(torch.tensor(2 * alpha, dtype=F32), dtype).to(F32)
+    rl, rc, rf = (rho[..., i].to(F32) for i in range(3))
+    local_twice = rnd(2.0 * local.to(F32)).to(F32)
+    coarse_scaled = rnd(gain * coarse.to(F32)).to(F32)
+    fine_scaled = rnd(gain * fine.to(F32)).to(F32)
+    lt = rnd(rl * local_twice).to(F32)
+    ct = rnd(rc * coarse_scaled).to(F32)
+    ft = rnd(rf * fine_scaled).to(F32)
+    first = rnd(lt + ct).to(F32)
+    return rnd(rnd(first + ft), dtype)
+
+
+# ----------------------------------------------------------------------------
+# Local attention: flash_attention.py:16-37 (SDPA, scale 1/sqrt(D))
+# ----------------------------------------------------------------------------
+
+def local_attention(q, k, v):
+    """Suffix-aligned causal attention in fp64, rounded once to q's dtype.
+
+    Square -> causal, Tq == 1 -> all keys, else query row i sees keys
+    col <= Tk - Tq + i: one formula covers the reference's three SDPA modes.
+    """
+    tq, tk, d = q.shape[1], k.shape[1], q.shape[-1]
+    s = torch.einsum("bqhd,bkhd->bhqk", q.to(torch.float64), k.to(torch.float64))
+    s = s / math.sqrt(d)
+    rows = tk - tq + torch.arange(tq)
+    allowed = torch.arange(tk)[None, :] <= rows[:, None]
+    s = s.masked_fill(~allowed, NEG_INF)
+    p = torch.softmax(s, -1)
+    out = torch.einsum("bhqk,bkhd->bqhd", p, v.to(torch.float64))
+    return rnd(out, q.dtype)
+
+
+# ----------------------------------------------------------------------------
+# Streaming state: tao_stream.py:126-527 (LayerState), 790-986 (StreamCache)
+# ----------------------------------------------------------------------------
+
+class OracleStream:
+    """One request x layer streaming state (softmax writer).
+
+    Semantic content equals the reference StreamCache: local exact window,
+    sealed fine z / C, completed page summaries, route ids, position.
+    """
+
+    def __init__(self, layer_index, geometry=None):
+        self.layer = layer_index
+        self.g = geometry or Geometry()
+        self.position = 0
+        self.local = None            # (k, v, raw_k) [B, n, H, D]
+        self.fine_z = []             # [B, H, D] per sealed fine
+        self.fine_c = []             # [B, H, D, D]
+        self.page_z = []             # completed pages [B, H, D]
+        self.page_c = []             # completed pages [B, H, D, D] (non-index-only)
+        self.route_ids = None        # (chosen [B,1,H,K'], selected [B,1,H,M])
+        self.state_version = 0
+        self.route_refreshes = 0
+        self.fine_seal_events = 0
+
+    # -- state views ------------------------------------------------------
+    @property
+    def completed(self):
+        return len(self.page_z)
+
+    @property
+    def pending(self):
+        return len(self.fine_z) - self.completed * self.g.coarse_group
+
+    def page_descriptors(self):
+        """page_z over completed pages plus the pending summary (:267-290)."""
+        parts = list(self.page_z)
+        if self.pending:
+            start = self.completed * self.g.coarse_group
+            parts.append(page_summary(torch.stack(self.fine_z[start:], 2)))
+        return torch.stack(parts, 2)
+
+    def fine_segment_weights(self, page_z):
+        z = torch.stack(self.fine_z, 2)                       # [B,H,S,D]
+        page_of = torch.arange(z.shape[2]) // self.g.coarse_group
+        return segment_weights(z, page_z.index_select(2, page_of))
+
+    # -- lifecycle --------------------------------------------------------
+    def next_chunk(self, desired):
+        """tao_stream.py:914-917."""
+        current = 0 if self.local is None else self.local[0].shape[1]
+        return min(desired, self.g.fine_tokens, self.g.serve_limit - current)
+
+    def seal(self, raw_k, v):
+        """tao_stream.py:435-512 for the softmax writer."""
+        z, c = seal_softmax(raw_k, v)
+        self.fine_z.append(z)
+        self.fine_c.append(c)
+        self.state_version += 1
+        group = self.g.coarse_group
+        if self.pending == group:
+            start = self.completed * group
+            zs = torch.stack(self.fine_z[start:], 2)
+            pz = page_summary(zs)
+            self.page_z.append(pz)
+            if not self.g.coarse_index_only:
+                self.page_c.append(page_coarse_matrix(
+                    zs, pz, torch.stack(self.fine_c[start:], 2)))
+
+    def read(self, raw_q):
+        """LayerState._read_progressive + _read_reused (:196-374)."""
+        b, t, heads, d = raw_q.shape
+        if not self.fine_z:
+            zero = torch.zeros_like(raw_q)
+            return zero, zero, False, False
+        page_z = self.page_descriptors()
+        pw = page_weights(page_z)
+        sw = self.fine_segment_weights(page_z)
+        bank = torch.stack(self.fine_c, 2)
+        h = query_weights(raw_q)
+        hv = page_values(h, pw)                               # [B,T,H,P,D]
+        coarse_on = bool(self.page_z) and not self.g.coarse_index_only
+        if coarse_on:
+            coarse = coarse_read(h, page_z[:, :, :self.completed],
+                                 torch.stack(self.page_c, 2))
+        else:
+            coarse = torch.zeros_like(raw_q)
+        fine = torch.empty_like(raw_q)
+        offset = 0
+        while offset < t:
+            absolute = self.position + offset
+            refresh = self.g.is_turn(absolute, self.layer)
+            count = min(t - offset, self.g.next_turn(absolute, self.layer) - absolute)
+            if refresh:
+                chosen, selected, _ = route(hv[:, offset], sw, self.completed,
+                                            self.pending, self.g)
+                self.route_ids = (chosen.unsqueeze(1), selected.unsqueeze(1))
+                self.route_refreshes += 1
+            part, _ = selected_read(hv[:, offset:offset + count], sw,
+                                    self.route_ids[1][:, 0], bank,
+                                    self.g.coarse_group)
+            fine[:, offset:offset + count] = part
+            offset += count
+        return coarse, fine, coarse_on, True
+
+    def process(self, raw_q, raw_k, q, k, v):
+        """StreamCache.process (:919-979): local, read, then seal at 768."""
+        if self.local is None:
+            all_k, all_v, all_raw = k, v, raw_k
+        else:
+            all_k = torch.cat((self.local[0], k), 1)
+            all_v = torch.cat((self.local[1], v), 1)
+            all_raw = torch.cat((self.local[2], raw_k), 1)
+        if all_k.shape[1] > self.g.serve_limit:
+            raise ValueError("chunk crosses a fine seal boundary")
+        local = local_attention(q, all_k, all_v)
+        coarse, fine, c_on, f_on = self.read(raw_q)
+        if all_k.shape[1] == self.g.serve_limit:
+            self.fine_seal_events += 1
+            ft, keep = self.g.fine_tokens, self.g.local_keep
+            self.seal(all_raw[:, :ft], all_v[:, :ft])
+            self.local = (all_k[:, -keep:].clone(), all_v[:, -keep:].clone(),
+                          all_raw[:, -keep:].clone())
+        else:
+            self.local = (all_k, all_v, all_raw)
+        return local, coarse, fine, c_on, f_on
+
+    def prefill(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
+                position=None):
+        """operator.py:70-127: split at next_chunk, fuse each chunk."""
+        if position is not None and position != self.position:
+            raise ValueError("position must match this request's causal cursor")
+        outputs = []
+        start = 0
+        while start < q.shape[1]:
+            width = self.next_chunk(q.shape[1] - start)
+            end = start + width
+            local, coarse, fine, c_on, f_on = self.process(
+                raw_q[:, start:end], raw_k[:, start:end], q[:, start:end],
+                k[:, start:end], v[:, start:end])
+            if c_on or f_on:
+                out = fusion(raw_q[:, start:end], local, coarse, fine,
+                             fusion_a, fusion_b, alpha, c_on, f_on)
+            else:
+                out = local
+            outputs.append(out)
+            self.position += width
+            start = end
+        return torch.cat(outputs, 1)
+
+    def decode(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
+               position=None):
+        """operator.py:130-138."""
+        if q.shape[1] != 1:
+            raise ValueError("decode accepts exactly one new query/key/value")
+        return self.prefill(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
+                            position)
+
+    def export(self):
+        """Semantic snapshot in the reference's schema (tao_stream.py:853-877)."""
+        group = self.g.coarse_group
+        packed = torch.stack(self.fine_c, 2) if self.fine_c else None
+        z = self.fine_z
+        pages = []
+        for index, pz in enumerate(self.page_z):
+            pc = self.page_c[index] if self.page_c else None
+            pages.append((pz.clone(), None if pc is None else pc.clone(),
+                          torch.stack(z[index * group:(index + 1) * group], 2)))
+        pending = [zz.clone() for zz in z[self.completed * group:]]
+        return {
+            "position": self.position,
+            "local": None if self.local is None else tuple(t.clone() for t in self.local),
+            "packed_fine_c": packed,
+            "pages": pages,
+            "pending_z": pending,
+            "route_ids": None if self.route_ids is None else tuple(t.clone() for t in self.route_ids),
+            "state_version": self.state_version,
+            "route_refreshes": self.route_refreshes,
+            "fine_seal_events": self.fine_seal_events,
+        }
+
+    @classmethod
+    def from_export(cls, saved, layer_index, geometry=None):
+        """Restore from a snapshot dict (tao_stream.py:879-912)."""
+        state = cls(layer_index, geometry)
+        group = state.g.coarse_group
+        state.position = saved["position"]
+        state.local = (None if saved["local"] is None
+                       else tuple(t.clone() for t in saved["local"]))
+        packed = saved["packed_fine_c"]
+        for index, (pz, pc, fz) in enumerate(saved["pages"]):
+            state.page_z.append(pz.clone())
+            if pc is not None:
+                state.page_c.append(pc.clone())
+            for j in range(group):
+                state.fine_z.append(fz[:, :, j].clone())
+                state.fine_c.append(packed[:, :, index * group + j].clone())
+        offset = len(saved["pages"]) * group
+        for j, z in enumerate(saved["pending_z"]):
+            state.fine_z.append(z.clone())
+            state.fine_c.append(packed[:, :, offset + j].clone())
+        state.route_ids = (None if saved["route_ids"] is None
+                           else tuple(t.clone() for t in saved["route_ids"]))
+        state.state_version = saved["state_version"]
+        state.route_refreshes = saved["route_refreshes"]
+        state.fine_seal_events = saved["fine_seal_events"]
+        return state
+

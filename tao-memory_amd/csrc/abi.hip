@@ -1,0 +1,437 @@
+// C ABI of libtao_hip.so (declared in include/tao_memory.h).
+//
+// Validates shapes and capacities on the host before any launch (contract
+// errors return negative codes, HIP failures their positive hipError_t),
+// translates the plain-pointer structs into kernel parameter blocks and owns
+// the only library-side resources: hipGraphExec objects of the decode step.
+#include <string>
+
+#include "tao_launch.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+int check_hip(hipError_t e, const char* where) {
+  if (e == hipSuccess) return TAO_OK;
+  g_error = std::string(where) + ": " + hipGetErrorString(e);
+  return (int)e;
+}
+
+int check_state(const tao_state_dev* st) {
+  if (!st) return fail(TAO_E_ARGUMENT, "null state");
+  if (st->head_dim != 64 && st->head_dim != 128)
+    return fail(TAO_E_SHAPE, "head_dim must be 64 or 128 on the HIP path");
+  if (st->local_keep != 512 || st->fine_tokens != 256)
+    return fail(TAO_E_SHAPE, "HIP kernels implement local_keep=512, fine_tokens=256");
+  if (st->batch <= 0 || st->heads <= 0 || st->coarse_group <= 0)
+    return fail(TAO_E_SHAPE, "batch, heads and coarse_group must be positive");
+  if (!st->ring_k || !st->ring_v || !st->ring_raw || !st->bank_c || !st->fine_z ||
+      !st->fine_sw || !st->page_z || !st->page_w || !st->sel || !st->chosen ||
+      !st->header || !st->workspace)
+    return fail(TAO_E_ARGUMENT, "state has a null device buffer");
+  if (st->sel_cap > 512) return fail(TAO_E_CAPACITY, "sel_cap above 512");
+  const tao::WorkspaceLayout lay =
+      tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
+  if (st->workspace_bytes < lay.tiles_off)
+    return fail(TAO_E_WORKSPACE, "workspace smaller than tao_workspace_bytes()");
+  return TAO_OK;
+}
+
+tao::TokView view(const void* p, const int64_t* s) {
+  tao::TokView v;
+  v.p = (const bf16_t*)p;
+  v.sb = s[0];
+  v.st = s[1];
+  v.sh = s[2];
+  return v;
+}
+
+uint32_t* counters_of(const tao_state_dev* st) {
+  const tao::WorkspaceLayout lay =
+      tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
+  return (uint32_t*)((char*)st->workspace + lay.counters_off);
+}
+
+float* parts_of(const tao_state_dev* st) {
+  const tao::WorkspaceLayout lay =
+      tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
+  return (float*)((char*)st->workspace + lay.parts_off);
+}
+
+tao::DecodeParams decode_params(const tao_state_dev* st, const tao_tokens* tok,
+                                const tao_fusion* fu, void* out, const int64_t* out_s) {
+  tao::DecodeParams p;
+  p.q = view(tok->q, tok->q_s);
+  p.k = view(tok->k, tok->k_s);
+  p.v = view(tok->v, tok->v_s);
+  p.rq = view(tok->raw_q, tok->rq_s);
+  p.rk = view(tok->raw_k, tok->rk_s);
+  p.ring_k = (bf16_t*)st->ring_k;
+  p.ring_v = (bf16_t*)st->ring_v;
+  p.ring_raw = (bf16_t*)st->ring_raw;
+  p.bank = (const bf16_t*)st->bank_c;
+  p.sw = (const bf16_t*)st->fine_sw;
+  p.pw = (const bf16_t*)st->page_w;
+  p.sel = st->sel;
+  p.header = st->header;
+  p.fa = fu->fusion_a;
+  p.fb = fu->fusion_b;
+  p.f_dtype = fu->dtype;
+  for (int i = 0; i < 3; ++i) { p.fa_s[i] = fu->a_s[i]; p.fb_s[i] = fu->b_s[i]; }
+  p.gain = fu->gain;
+  p.out = (bf16_t*)out;
+  p.out_sb = out_s[0];
+  p.out_sh = out_s[2];
+  p.parts = parts_of(st);
+  p.counters = counters_of(st);
+  p.B = st->batch;
+  p.H = st->heads;
+  p.keep = st->local_keep;
+  p.fine = st->fine_tokens;
+  p.group = st->coarse_group;
+  p.fine_cap = st->fine_cap;
+  p.page_cap = st->page_cap;
+  p.sel_cap = st->sel_cap;
+  return p;
+}
+
+int check_tokens(const tao_tokens* tok) {
+  if (!tok || !tok->q || !tok->k || !tok->v || !tok->raw_q || !tok->raw_k)
+    return fail(TAO_E_ARGUMENT, "null token operand");
+  if (tok->tokens < 0) return fail(TAO_E_ARGUMENT, "negative token count");
+  return TAO_OK;
+}
+
+int check_fusion(const tao_fusion* fu) {
+  if (!fu || !fu->fusion_a || !fu->fusion_b) return fail(TAO_E_ARGUMENT, "null fusion parameters");
+  if (fu->dtype != TAO_BF16 && fu->dtype != TAO_FP32)
+    return fail(TAO_E_ARGUMENT, "fusion dtype must be bf16 or fp32");
+  return TAO_OK;
+}
+
+struct DecodeGraph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  tao::StageParams stage;
+  int batch = 0, heads = 0, head_dim = 0;
+};
+
+}  // namespace
+
+namespace tao {
+
+WorkspaceLayout workspace_layout(int batch, int heads, int head_dim, int sel_cap,
+                                 int max_query_tokens) {
+  auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  WorkspaceLayout lay;
+  const size_t bh = (size_t)batch * heads;
+  lay.counters_off = 0;
+  lay.parts_off = align((bh + 1) * sizeof(uint32_t));
+  const size_t parts = bh * (kLocalSplits + (size_t)sel_cap) * (head_dim + 4) * sizeof(float);
+  lay.tiles_off = align(lay.parts_off + parts);
+  lay.tiles_cap = (size_t)max_query_tokens / 32 + 64;
+  lay.total = align(lay.tiles_off + lay.tiles_cap * 3 * sizeof(int64_t));
+  return lay;
+}
+
+}  // namespace tao
+
+extern "C" {
+
+int tao_abi_version(void) { return TAO_ABI_VERSION; }
+
+const char* tao_last_error(void) { return g_error.c_str(); }
+
+size_t tao_workspace_bytes(int32_t batch, int32_t heads, int32_t head_dim,
+                           int32_t sel_cap, int32_t max_query_tokens) {
+  return tao::workspace_layout(batch, heads, head_dim, sel_cap, max_query_tokens).total;
+}
+
+int tao_workspace_init(const tao_state_dev* st, void* stream) {
+  int rc = check_state(st);
+  if (rc) return rc;
+  const size_t bytes = ((size_t)st->batch * st->heads + 1) * sizeof(uint32_t);
+  return check_hip(hipMemsetAsync(counters_of(st), 0, bytes, (hipStream_t)stream),
+                   "tao_workspace_init");
+}
+
+int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
+                    int32_t selected, void* out, const int64_t* out_s, void* stream) {
+  int rc = check_state(st);
+  if (!rc) rc = check_tokens(tok);
+  if (!rc) rc = check_fusion(fu);
+  if (rc) return rc;
+  if (tok->tokens != 1) return fail(TAO_E_SHAPE, "decode step takes exactly one token");
+  if (!out || !out_s) return fail(TAO_E_ARGUMENT, "null output");
+  if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected count exceeds sel_cap");
+  const tao::DecodeParams p = decode_params(st, tok, fu, out, out_s);
+  return check_hip(tao::launch_decode_step(p, st->head_dim, selected, (hipStream_t)stream),
+                   "tao_decode_step");
+}
+
+int tao_route(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
+              int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
+              void* stream) {
+  int rc = check_state(st);
+  if (rc) return rc;
+  if (!raw_q_row || !rq_s) return fail(TAO_E_ARGUMENT, "null anchor query");
+  const int fines = completed * st->coarse_group + pending;
+  if (completed < 0 || pending < 0 || pending >= st->coarse_group || fines <= 0)
+    return fail(TAO_E_ARGUMENT, "route needs at least one sealed fine");
+  if (fines > st->fine_cap || completed + 1 > st->page_cap)
+    return fail(TAO_E_CAPACITY, "route counts exceed the state capacity");
+  if (coarse < 0 || coarse > completed || coarse > st->chosen_cap)
+    return fail(TAO_E_CAPACITY, "coarse count out of range");
+  const int eligible = coarse * st->coarse_group + pending;
+  if (selected <= 0 || selected > eligible || selected > st->sel_cap)
+    return fail(TAO_E_CAPACITY, "selected count out of range");
+  tao::RouteParams p;
+  p.rq = (const bf16_t*)raw_q_row;
+  p.rq_sb = rq_s[0];
+  p.rq_sh = rq_s[1];
+  p.pw = (const bf16_t*)st->page_w;
+  p.sw = (const bf16_t*)st->fine_sw;
+  p.sel = st->sel;
+  p.chosen = st->chosen;
+  p.header = st->header;
+  p.B = st->batch;
+  p.H = st->heads;
+  p.fine_cap = st->fine_cap;
+  p.page_cap = st->page_cap;
+  p.sel_cap = st->sel_cap;
+  p.chosen_cap = st->chosen_cap;
+  p.group = st->coarse_group;
+  p.completed = completed;
+  p.pending = pending;
+  p.coarse = coarse;
+  p.selected = selected;
+  return check_hip(tao::launch_route(p, st->head_dim, (hipStream_t)stream), "tao_route");
+}
+
+int tao_write_fine(const tao_state_dev* st, const tao_tokens* tok, int64_t new_base,
+                   const int64_t* start_pos, int32_t first_slot, int32_t count,
+                   void* stream) {
+  int rc = check_state(st);
+  if (!rc) rc = check_tokens(tok);
+  if (rc) return rc;
+  if (count < 0 || first_slot < 0 || first_slot + count > st->fine_cap)
+    return fail(TAO_E_CAPACITY, "fine slots exceed fine_cap");
+  if (count && !start_pos) return fail(TAO_E_ARGUMENT, "null block starts");
+  tao::WriterParams p;
+  p.rk = view(tok->raw_k, tok->rk_s);
+  p.v = view(tok->v, tok->v_s);
+  p.ring_raw = (const bf16_t*)st->ring_raw;
+  p.ring_v = (const bf16_t*)st->ring_v;
+  p.bank = (bf16_t*)st->bank_c;
+  p.fine_z = (bf16_t*)st->fine_z;
+  p.starts = start_pos;
+  p.new_base = new_base;
+  p.B = st->batch;
+  p.H = st->heads;
+  p.L = st->local_keep + st->fine_tokens;
+  p.fine_cap = st->fine_cap;
+  p.first_slot = first_slot;
+  p.count = count;
+  return check_hip(tao::launch_writer(p, st->head_dim, (hipStream_t)stream), "tao_write_fine");
+}
+
+int tao_seal_epilogue(const tao_state_dev* st, int32_t slot, int32_t pages, int32_t recompute,
+                      void* stream) {
+  int rc = check_state(st);
+  if (rc) return rc;
+  if (slot < 0 || slot >= st->fine_cap) return fail(TAO_E_CAPACITY, "slot exceeds fine_cap");
+  if (pages != slot / st->coarse_group + 1 || pages > st->page_cap)
+    return fail(TAO_E_ARGUMENT, "pages must be slot / coarse_group + 1 and fit page_cap");
+  tao::EpilogueParams p;
+  p.fine_z = (const bf16_t*)st->fine_z;
+  p.fine_sw = (bf16_t*)st->fine_sw;
+  p.page_z = (bf16_t*)st->page_z;
+  p.page_w = (bf16_t*)st->page_w;
+  p.B = st->batch;
+  p.H = st->heads;
+  p.fine_cap = st->fine_cap;
+  p.page_cap = st->page_cap;
+  p.group = st->coarse_group;
+  p.slot = slot;
+  p.pages = pages;
+  p.recompute = recompute ? 1 : 0;
+  return check_hip(tao::launch_seal_epilogue(p, st->head_dim, (hipStream_t)stream),
+                   "tao_seal_epilogue");
+}
+
+int tao_local_attention(const tao_state_dev* st, const tao_tokens* tok, int64_t qpos0,
+                        int64_t kpos0, const int64_t* tiles, int32_t n_tiles, void* local,
+                        void* stream) {
+  int rc = check_state(st);
+  if (!rc) rc = check_tokens(tok);
+  if (rc) return rc;
+  if (!local) return fail(TAO_E_ARGUMENT, "null local output");
+  if (n_tiles < 0 || (n_tiles && !tiles)) return fail(TAO_E_ARGUMENT, "bad tile list");
+  tao::AttnParams p;
+  p.q = view(tok->q, tok->q_s);
+  p.k = view(tok->k, tok->k_s);
+  p.v = view(tok->v, tok->v_s);
+  p.ring_k = (const bf16_t*)st->ring_k;
+  p.ring_v = (const bf16_t*)st->ring_v;
+  p.out = (bf16_t*)local;
+  p.tiles = tiles;
+  p.qpos0 = qpos0;
+  p.kpos0 = kpos0;
+  p.B = st->batch;
+  p.H = st->heads;
+  p.L = st->local_keep + st->fine_tokens;
+  p.T = tok->tokens;
+  p.n_tiles = n_tiles;
+  return check_hip(tao::launch_local_attention(p, st->head_dim, (hipStream_t)stream),
+                   "tao_local_attention");
+}
+
+int tao_read_fuse(const tao_state_dev* st, const tao_tokens* tok, int32_t first,
+                  int32_t count, int32_t selected, const tao_fusion* fu, const void* local,
+                  void* out, const int64_t* out_s, void* stream) {
+  int rc = check_state(st);
+  if (!rc) rc = check_tokens(tok);
+  if (!rc) rc = check_fusion(fu);
+  if (rc) return rc;
+  if (!local || !out || !out_s) return fail(TAO_E_ARGUMENT, "null local or output");
+  if (first < 0 || count < 0 || first + count > tok->tokens)
+    return fail(TAO_E_ARGUMENT, "query range outside the token operands");
+  if (fu->fine_on && (selected <= 0 || selected > st->sel_cap))
+    return fail(TAO_E_CAPACITY, "selected count out of range");
+  if (fu->coarse_on) return fail(TAO_E_SHAPE, "coarse value branch is not implemented on the HIP path");
+  tao::ReadParams p;
+  p.rq = view(tok->raw_q, tok->rq_s);
+  p.bank = (const bf16_t*)st->bank_c;
+  p.sw = (const bf16_t*)st->fine_sw;
+  p.pw = (const bf16_t*)st->page_w;
+  p.sel = st->sel;
+  p.local = (const bf16_t*)local;
+  p.fa = fu->fusion_a;
+  p.fb = fu->fusion_b;
+  p.f_dtype = fu->dtype;
+  for (int i = 0; i < 3; ++i) { p.fa_s[i] = fu->a_s[i]; p.fb_s[i] = fu->b_s[i]; }
+  p.gain = fu->gain;
+  p.coarse_on = fu->coarse_on;
+  p.fine_on = fu->fine_on;
+  p.out = (bf16_t*)out;
+  p.out_sb = out_s[0];
+  p.out_st = out_s[1];
+  p.out_sh = out_s[2];
+  p.B = st->batch;
+  p.H = st->heads;
+  p.T = tok->tokens;
+  p.first = first;
+  p.count = count;
+  p.selected = selected;
+  p.group = st->coarse_group;
+  p.fine_cap = st->fine_cap;
+  p.page_cap = st->page_cap;
+  p.sel_cap = st->sel_cap;
+  return check_hip(tao::launch_read_fuse(p, st->head_dim, (hipStream_t)stream), "tao_read_fuse");
+}
+
+int tao_ring_append(const tao_state_dev* st, const tao_tokens* tok, int32_t first,
+                    int32_t count, int64_t pos, void* stream) {
+  int rc = check_state(st);
+  if (!rc) rc = check_tokens(tok);
+  if (rc) return rc;
+  const int L = st->local_keep + st->fine_tokens;
+  if (first < 0 || count < 0 || first + count > tok->tokens || count > L)
+    return fail(TAO_E_ARGUMENT, "ring append range out of bounds");
+  tao::AppendParams p;
+  p.k = view(tok->k, tok->k_s);
+  p.v = view(tok->v, tok->v_s);
+  p.rk = view(tok->raw_k, tok->rk_s);
+  p.ring_k = (bf16_t*)st->ring_k;
+  p.ring_v = (bf16_t*)st->ring_v;
+  p.ring_raw = (bf16_t*)st->ring_raw;
+  p.B = st->batch;
+  p.H = st->heads;
+  p.D = st->head_dim;
+  p.L = L;
+  p.first = first;
+  p.count = count;
+  p.pos = pos;
+  return check_hip(tao::launch_ring_append(p, (hipStream_t)stream), "tao_ring_append");
+}
+
+int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu, int32_t selected,
+                     void* staging, void* out_stage, void* stream, void** graph_out) {
+  int rc = check_state(st);
+  if (!rc) rc = check_fusion(fu);
+  if (rc) return rc;
+  if (!staging || !out_stage || !graph_out) return fail(TAO_E_ARGUMENT, "null graph buffers");
+  if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected out of range");
+  const int B = st->batch, H = st->heads, D = st->head_dim;
+  const size_t row = (size_t)B * H * D;
+  bf16_t* stg = (bf16_t*)staging;
+  tao_tokens tok;
+  const void* ptrs[5];
+  for (int i = 0; i < 5; ++i) ptrs[i] = stg + i * row;
+  tok.q = ptrs[0]; tok.k = ptrs[1]; tok.v = ptrs[2]; tok.raw_q = ptrs[3]; tok.raw_k = ptrs[4];
+  const int64_t s[3] = {(int64_t)H * D, 0, (int64_t)D};
+  for (int i = 0; i < 3; ++i) {
+    tok.q_s[i] = s[i]; tok.k_s[i] = s[i]; tok.v_s[i] = s[i]; tok.rq_s[i] = s[i]; tok.rk_s[i] = s[i];
+  }
+  tok.tokens = 1;
+  const int64_t out_s[3] = {(int64_t)H * D, 0, (int64_t)D};
+  const tao::DecodeParams p = decode_params(st, &tok, fu, out_stage, out_s);
+
+  DecodeGraph* g = new DecodeGraph();
+  g->batch = B; g->heads = H; g->head_dim = D;
+  g->stage.dst = stg;
+  g->stage.B = B; g->stage.H = H; g->stage.D = D;
+  hipStream_t cs = nullptr;
+  hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+  if (e == hipSuccess) {
+    hipError_t le = tao::launch_decode_step(p, D, selected, cs);
+    e = hipStreamEndCapture(cs, &g->graph);
+    if (e == hipSuccess) e = le;
+  }
+  if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  if (cs) hipStreamDestroy(cs);
+  if (e != hipSuccess) {
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
+    delete g;
+    return check_hip(e, "tao_graph_create");
+  }
+  (void)stream;
+  *graph_out = g;
+  return TAO_OK;
+}
+
+int tao_graph_launch(void* graph, const tao_tokens* tok, void* stream) {
+  if (!graph) return fail(TAO_E_ARGUMENT, "null graph");
+  int rc = check_tokens(tok);
+  if (rc) return rc;
+  DecodeGraph* g = (DecodeGraph*)graph;
+  tao::StageParams sp = g->stage;
+  sp.src[0] = view(tok->q, tok->q_s);
+  sp.src[1] = view(tok->k, tok->k_s);
+  sp.src[2] = view(tok->v, tok->v_s);
+  sp.src[3] = view(tok->raw_q, tok->rq_s);
+  sp.src[4] = view(tok->raw_k, tok->rk_s);
+  hipError_t e = tao::launch_stage_tokens(sp, (hipStream_t)stream);
+  if (e == hipSuccess) e = hipGraphLaunch(g->exec, (hipStream_t)stream);
+  return check_hip(e, "tao_graph_launch");
+}
+
+int tao_graph_destroy(void* graph) {
+  if (!graph) return TAO_OK;
+  DecodeGraph* g = (DecodeGraph*)graph;
+  hipError_t e = hipSuccess;
+  if (g->exec) e = hipGraphExecDestroy(g->exec);
+  if (g->graph) hipGraphDestroy(g->graph);
+  delete g;
+  return check_hip(e, "tao_graph_destroy");
+}
+
+}  // extern "C"

@@ -1,0 +1,205 @@
+// Exact local attention (suffix-aligned causal) on MFMA for gfx950.
+//
+// Restates flash_attn_func (flash_attention.py:16-37): softmax(QK^T/sqrt(D))V
+// where query row i of a chunk sees keys up to its own absolute position and
+// no key older than the chunk's window start. One workgroup = one tile of up
+// to 128 queries of one (batch, head); wave w owns 32 queries.
+//
+// Per 64-key block (staged in LDS: K row-major, V transposed):
+//   S^T[key, query] = K . Q^T         v_mfma_f32_32x32x16_bf16, Q in VGPRs
+//   online softmax per query          each lane owns one query column
+//   O^T[d, query]  += V^T . P^T       P^T comes straight from the S^T
+//                                     accumulators: the contraction runs over
+//                                     a key permutation that matches the
+//                                     accumulator layout, and V^T is read
+//                                     with the same permutation.
+// Keys older than kpos0 come from the token ring, newer ones from the call's
+// key operands; query row r sits at absolute position qpos0 + r.
+#include "tao_launch.h"
+#include "tao_common.h"
+
+namespace tao {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kKeys = 64;
+constexpr int kQTile = 128;
+
+template <int D>
+struct AttnSmem {
+  bf16_t k[kKeys][D + 8];
+  bf16_t vt[D][kKeys + 8];
+};
+
+TAO_DEV const bf16_t* key_row(const AttnParams& p, const TokView& tv, const bf16_t* ring,
+                              int b, int h, long long pos, int D) {
+  if (pos >= p.kpos0) return tv.p + b * tv.sb + (pos - p.kpos0) * tv.st + h * tv.sh;
+  const int slot = (int)(pos % p.L);
+  return ring + (((size_t)b * p.L + slot) * p.H + h) * D;
+}
+
+TAO_DEV bf16x8 as_bf16x8(const uint4& u) {
+  bf16x8 r;
+  __builtin_memcpy(&r, &u, 16);
+  return r;
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void local_attn_kernel(AttnParams p) {
+  __shared__ AttnSmem<D> sm;
+  constexpr int CH = D / 8;
+  constexpr int DT = D / 32;    // 32-row tiles of O^T
+  constexpr int KK = D / 16;    // k-steps of S^T
+  const int bh = blockIdx.x % (p.B * p.H);
+  const int tile = blockIdx.x / (p.B * p.H);
+  const int b = bh / p.H, h = bh % p.H;
+  const long long first = p.tiles[3 * tile];
+  const int count = (int)p.tiles[3 * tile + 1];
+  const long long key_start = p.tiles[3 * tile + 2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
+
+  const int nq = min(max(count - wave * 32, 0), 32);
+  const bool qvalid = li < nq;
+  const long long qtok = first + wave * 32 + (nq > 0 ? min(li, nq - 1) : 0);
+  const long long qpos = p.qpos0 + qtok;
+  const long long wave_last = p.qpos0 + first + wave * 32 + nq - 1;
+  const long long kend = p.qpos0 + first + count;   // exclusive
+
+  bf16x8 qreg[KK];
+  {
+    const bf16_t* qrow = p.q.p + b * p.q.sb + qtok * p.q.st + h * p.q.sh;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) qreg[kk] = as_bf16x8(*(const uint4*)(qrow + 16 * kk + 8 * hl));
+  }
+  const float scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)D));
+
+  floatx16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[t][i] = 0.0f;
+  float m_run = -__builtin_inff(), l_run = 0.0f;
+
+  for (long long kb = key_start; kb < kend; kb += kKeys) {
+    __syncthreads();
+    for (int job = tid; job < kKeys * CH; job += kThreads) {
+      const int r = job / CH, c = job % CH;
+      const long long pos = kb + r;
+      uint4 u = make_uint4(0, 0, 0, 0);
+      if (pos < kend) u = *(const uint4*)(key_row(p, p.k, p.ring_k, b, h, pos, D) + c * 8);
+      *(uint4*)&sm.k[r][c * 8] = u;
+    }
+    for (int job = tid; job < (kKeys / 2) * CH; job += kThreads) {
+      const int pair = job / CH, c = job % CH;
+      const int t0 = 2 * pair;
+      uint4 a = make_uint4(0, 0, 0, 0), bq = make_uint4(0, 0, 0, 0);
+      if (kb + t0 < kend) a = *(const uint4*)(key_row(p, p.v, p.ring_v, b, h, kb + t0, D) + c * 8);
+      if (kb + t0 + 1 < kend) bq = *(const uint4*)(key_row(p, p.v, p.ring_v, b, h, kb + t0 + 1, D) + c * 8);
+      const uint32_t wa[4] = {a.x, a.y, a.z, a.w};
+      const uint32_t wb[4] = {bq.x, bq.y, bq.z, bq.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        *(uint32_t*)&sm.vt[c * 8 + 2 * i][t0] = (wa[i] & 0xFFFFu) | (wb[i] << 16);
+        *(uint32_t*)&sm.vt[c * 8 + 2 * i + 1][t0] = (wa[i] >> 16) | (wb[i] & 0xFFFF0000u);
+      }
+    }
+    __syncthreads();
+    if (nq == 0 || kb > wave_last) continue;   // uniform per wave
+
+    floatx16 s[2];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[sub][i] = 0.0f;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const bf16x8 a = as_bf16x8(*(const uint4*)&sm.k[sub * 32 + li][16 * kk + 8 * hl]);
+        s[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[kk], s[sub], 0, 0, 0);
+      }
+    }
+    // S^T layout: lane holds query li, keys 8*(i/4) + 4*hl + i%4 of each sub-tile.
+    float bmax = -__builtin_inff();
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const long long kpos = kb + sub * 32 + 8 * (i / 4) + 4 * hl + (i % 4);
+        const bool ok = kpos <= qpos && kpos < kend;
+        const float v = ok ? s[sub][i] * scale_log2 : -__builtin_inff();
+        s[sub][i] = v;
+        bmax = fmaxf(bmax, v);
+      }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    const float m_new = fmaxf(m_run, bmax);
+    const float alpha = m_run == -__builtin_inff() ? 0.0f : exp2f(m_run - m_new);
+    float rsum = 0.0f;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float e = s[sub][i] == -__builtin_inff() ? 0.0f : exp2f(s[sub][i] - m_new);
+        s[sub][i] = e;
+        rsum += e;
+      }
+    rsum += __shfl_xor(rsum, 32, 64);
+    l_run = l_run * alpha + rsum;
+    m_run = m_new;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[t][i] *= alpha;
+
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        uint32_t packed[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          packed[j] = (uint32_t)f2bf(s[sub][8 * half + 2 * j]) |
+                      ((uint32_t)f2bf(s[sub][8 * half + 2 * j + 1]) << 16);
+        const bf16x8 pb = as_bf16x8(make_uint4(packed[0], packed[1], packed[2], packed[3]));
+        const int kbase = sub * 32 + 16 * half + 4 * hl;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const uint2 lo = *(const uint2*)&sm.vt[t * 32 + li][kbase];
+          const uint2 hi = *(const uint2*)&sm.vt[t * 32 + li][kbase + 8];
+          const uint4 u = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(u), pb, o[t], 0, 0, 0);
+        }
+      }
+  }
+  if (!qvalid) return;
+  const float inv = 1.0f / l_run;
+  bf16_t* orow = p.out + (((size_t)b * p.T + qtok) * p.H + h) * D;
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const int d = t * 32 + 8 * (i / 4) + 4 * hl;
+      uint2 packed;
+      packed.x = (uint32_t)f2bf(o[t][i] * inv) | ((uint32_t)f2bf(o[t][i + 1] * inv) << 16);
+      packed.y = (uint32_t)f2bf(o[t][i + 2] * inv) | ((uint32_t)f2bf(o[t][i + 3] * inv) << 16);
+      *(uint2*)(orow + d) = packed;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_local_attention(const AttnParams& p, int head_dim, hipStream_t s) {
+  if (p.n_tiles <= 0) return hipSuccess;
+  const dim3 grid((unsigned)(p.n_tiles * p.B * p.H));
+  if (head_dim == 128)
+    hipLaunchKernelGGL(local_attn_kernel<128>, grid, dim3(kThreads), 0, s, p);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL(local_attn_kernel<64>, grid, dim3(kThreads), 0, s, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace tao

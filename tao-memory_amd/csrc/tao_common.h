@@ -1,0 +1,82 @@
+// Shared device helpers for the TaoMemory gfx950 kernels.
+//
+// Numeric contract (identical to the CPU oracle):
+//  * bf16 is stored as raw uint16; float->bf16 is round-to-nearest-even.
+//  * exp/log feeding bf16 state are "correctly rounded fp32, then RNE to
+//    bf16": the fast fp32 result is used unless it lies within a few fp32
+//    ulps of a bf16 rounding boundary, where the fp64 value decides.
+//  * exp inside fp32 softmax internals is fp64 exp rounded to fp32.
+//  * fp32 sums that feed routing use the 64-lane butterfly order
+//    ("fold halves": pad to a power of two, add upper half onto lower half).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint16_t bf16_t;
+
+#define TAO_DEV __device__ __forceinline__
+
+TAO_DEV float bf2f(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
+
+TAO_DEV bf16_t f2bf_bits(uint32_t u) {
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (bf16_t)0x7FC0;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+TAO_DEV bf16_t f2bf(float f) { return f2bf_bits(__float_as_uint(f)); }
+
+// Round an fp32 value to bf16 precision and return it as fp32.
+TAO_DEV float rbf(float f) { return bf2f(f2bf(f)); }
+
+// True when fp32 `y` is within `margin` ulps of a bf16 rounding boundary.
+TAO_DEV bool near_bf16_midpoint(float y, int margin) {
+  int low = (int)(__float_as_uint(y) & 0xFFFFu);
+  int dist = low - 0x8000;
+  return dist <= margin && dist >= -margin;
+}
+
+// bf16(correctly rounded fp32 exp(x)).
+TAO_DEV float exp_bf(float x) {
+  float y = expf(x);
+  if (near_bf16_midpoint(y, 16)) y = (float)exp((double)x);
+  return rbf(y);
+}
+
+// bf16(correctly rounded fp32 log(x)).
+TAO_DEV float log_bf(float x) {
+  float y = logf(x);
+  if (near_bf16_midpoint(y, 16)) y = (float)log((double)x);
+  return rbf(y);
+}
+
+// Correctly rounded fp32 exp (fp64 evaluation).
+TAO_DEV float exp_cr(float x) { return (float)exp((double)x); }
+
+// ---------------------------------------------------------------- wave ops
+TAO_DEV float wave_sum_fold(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+TAO_DEV float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Monotone 32-bit key of a bf16 score: larger score -> larger key.
+TAO_DEV uint32_t bf16_order_key(bf16_t b) {
+  uint32_t u = b;
+  return (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
+}
+
+// Local-window length before appending the token at `position`:
+// p for p < serve_limit, else keep + (p - serve_limit) mod fine.
+TAO_DEV int local_len_at(long long position, int keep, int fine) {
+  long long limit = keep + fine;
+  if (position < limit) return (int)position;
+  return keep + (int)((position - limit) % fine);
+}

@@ -1,0 +1,47 @@
+// Three-branch presence-aware fusion for one (b, t, h, d) element.
+//
+// Restates fusion_pointwise.py:10-92 plus the torch softmax between them
+// (operator.py:86-94): every intermediate is rounded to bf16 exactly where
+// the reference rounds, with no FMA contraction (the reference launches both
+// kernels with enable_fp_fusion=False).
+#pragma once
+
+#include "tao_common.h"
+
+namespace tao {
+
+TAO_DEV float load_param(const void* p, int dtype, int64_t off) {
+  return dtype == TAO_FP32 ? ((const float*)p)[off] : bf2f(((const bf16_t*)p)[off]);
+}
+
+// bf16(fp32(log 2)) = 0.69140625: the local bias when two history branches
+// are present (fusion_pointwise.py:114-117, operator.py branch count).
+constexpr float kLogTwoBf16 = 0.69140625f;
+
+TAO_DEV bf16_t fuse_element(float q, float local, float coarse, float fine,
+                            const float a[3], const float b[3], float gain,
+                            int coarse_on, int fine_on) {
+  const float ninf = -__builtin_inff();
+  float s[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    float prod = rbf(rbf(a[i]) * q);
+    s[i] = rbf(prod + rbf(b[i]));
+  }
+  float bias = (coarse_on && fine_on) ? kLogTwoBf16 : 0.0f;
+  s[0] = rbf(s[0] + bias);
+  if (!coarse_on) s[1] = ninf;
+  if (!fine_on) s[2] = ninf;
+  float top = fmaxf(s[0], fmaxf(s[1], s[2]));
+  float e0 = exp_cr(s[0] - top);
+  float e1 = coarse_on ? exp_cr(s[1] - top) : 0.0f;
+  float e2 = fine_on ? exp_cr(s[2] - top) : 0.0f;
+  float total = (e0 + e2) + e1;   // butterfly order over [e0, e1, e2, 0]
+  float r0 = rbf(e0 / total), r1 = rbf(e1 / total), r2 = rbf(e2 / total);
+  float lt = rbf(r0 * rbf(2.0f * local));
+  float ct = rbf(r1 * rbf(gain * coarse));
+  float ft = rbf(r2 * rbf(gain * fine));
+  return f2bf(rbf(lt + ct) + ft);
+}
+
+}  // namespace tao

@@ -1,0 +1,161 @@
+"""ctypes binding of libtao_hip.so (C ABI: include/tao_memory.h).
+
+The library must be built (``python tao-memory_amd/build.py``) and torch must
+be imported first so the library binds to torch's HIP runtime and can use
+torch's streams and allocations. There is no fallback: a missing library or
+device raises immediately.
+"""
+
+import ctypes
+import os
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libtao_hip.so")
+_lib = None
+
+TAO_BF16 = 0
+TAO_FP32 = 1
+
+_i32, _i64, _sz, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
+_I64x3 = ctypes.c_int64 * 3
+
+
+class StateDev(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i32), ("heads", _i32), ("head_dim", _i32),
+        ("local_keep", _i32), ("fine_tokens", _i32), ("coarse_group", _i32),
+        ("fine_cap", _i32), ("page_cap", _i32), ("sel_cap", _i32), ("chosen_cap", _i32),
+        ("ring_k", _vp), ("ring_v", _vp), ("ring_raw", _vp),
+        ("bank_c", _vp), ("fine_z", _vp), ("fine_sw", _vp),
+        ("page_z", _vp), ("page_w", _vp),
+        ("sel", _vp), ("chosen", _vp), ("header", _vp),
+        ("workspace", _vp), ("workspace_bytes", _sz),
+    ]
+
+
+class Tokens(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp), ("k", _vp), ("v", _vp), ("raw_q", _vp), ("raw_k", _vp),
+        ("q_s", _I64x3), ("k_s", _I64x3), ("v_s", _I64x3), ("rq_s", _I64x3), ("rk_s", _I64x3),
+        ("tokens", _i32),
+    ]
+
+
+class Fusion(ctypes.Structure):
+    _fields_ = [
+        ("fusion_a", _vp), ("fusion_b", _vp), ("dtype", _i32),
+        ("a_s", _I64x3), ("b_s", _I64x3),
+        ("gain", ctypes.c_float), ("coarse_on", _i32), ("fine_on", _i32),
+    ]
+
+
+_SIGNATURES = {
+    "tao_abi_version": ([], _i32),
+    "tao_last_error": ([], ctypes.c_char_p),
+    "tao_workspace_bytes": ([_i32, _i32, _i32, _i32, _i32], _sz),
+    "tao_workspace_init": ([ctypes.POINTER(StateDev), _vp], _i32),
+    "tao_decode_step": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens),
+                         ctypes.POINTER(Fusion), _i32, _vp, ctypes.POINTER(_i64), _vp], _i32),
+    "tao_route": ([ctypes.POINTER(StateDev), _vp, ctypes.POINTER(_i64),
+                   _i32, _i32, _i32, _i32, _vp], _i32),
+    "tao_write_fine": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i64, _vp,
+                        _i32, _i32, _vp], _i32),
+    "tao_seal_epilogue": ([ctypes.POINTER(StateDev), _i32, _i32, _i32, _vp], _i32),
+    "tao_local_attention": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i64, _i64,
+                             _vp, _i32, _vp, _vp], _i32),
+    "tao_read_fuse": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i32, _i32, _i32,
+                       ctypes.POINTER(Fusion), _vp, _vp, ctypes.POINTER(_i64), _vp], _i32),
+    "tao_ring_append": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i32, _i32,
+                         _i64, _vp], _i32),
+    "tao_graph_create": ([ctypes.POINTER(StateDev), ctypes.POINTER(Fusion), _i32, _vp, _vp,
+                          _vp, ctypes.POINTER(_vp)], _i32),
+    "tao_graph_launch": ([_vp, ctypes.POINTER(Tokens), _vp], _i32),
+    "tao_graph_destroy": ([_vp], _i32),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+
+def library_path():
+    return _LIB_PATH
+
+
+def lib():
+    """Load (once) and return the HIP library; raise if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(
+                f"TaoMemory HIP library not built ({_LIB_PATH}); run "
+                "`python tao-memory_amd/build.py` (no CPU fallback exists)")
+        handle = ctypes.CDLL(_LIB_PATH)
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = handle
+    return _lib
+
+
+def check(rc):
+    """Map the library's return convention onto Python exceptions."""
+    if rc == 0:
+        return
+    msg = lib().tao_last_error().decode(errors="replace")
+    if rc < 0:
+        raise ValueError(msg)
+    raise RuntimeError(f"HIP error {rc}: {msg}")
+
+
+def require_device(tensor):
+    if not tensor.is_cuda:
+        raise RuntimeError("TaoMemory HIP path needs device tensors (no CPU fallback)")
+
+
+def stream_ptr(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def i64x3(values):
+    return _I64x3(*[int(x) for x in values])
+
+
+def strides_bth(t):
+    """Element strides (batch, token, head) of a [B, T, H, D] tensor."""
+    s = t.stride()
+    return (s[0], s[1], s[2])
+
+
+def tokens(q, k, v, raw_q, raw_k):
+    tok = Tokens()
+    tok.q, tok.k, tok.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    tok.raw_q, tok.raw_k = raw_q.data_ptr(), raw_k.data_ptr()
+    tok.q_s = i64x3(strides_bth(q))
+    tok.k_s = i64x3(strides_bth(k))
+    tok.v_s = i64x3(strides_bth(v))
+    tok.rq_s = i64x3(strides_bth(raw_q))
+    tok.rk_s = i64x3(strides_bth(raw_k))
+    tok.tokens = q.shape[1]
+    return tok
+
+
+def fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on):
+    fu = Fusion()
+    if fusion_a.dtype == torch.float32 and fusion_b.dtype == torch.float32:
+        fu.dtype = TAO_FP32
+    elif fusion_a.dtype == torch.bfloat16 and fusion_b.dtype == torch.bfloat16:
+        fu.dtype = TAO_BF16
+    else:
+        fusion_a = fusion_a.float()
+        fusion_b = fusion_b.float()
+        fu.dtype = TAO_FP32
+    fu.fusion_a, fu.fusion_b = fusion_a.data_ptr(), fusion_b.data_ptr()
+    fu.a_s = i64x3(fusion_a.stride())
+    fu.b_s = i64x3(fusion_b.stride())
+    # gain = torch.full((), 2 * alpha, dtype=bf16) as in operator.py:89.
+    fu.gain = float(torch.full((), 2 * alpha, dtype=torch.bfloat16))
+    fu.coarse_on, fu.fine_on = int(bool(coarse_on)), int(bool(fine_on))
+    # Keep converted parameter tensors alive for the launch.
+    fu._keep = (fusion_a, fusion_b)
+    return fu

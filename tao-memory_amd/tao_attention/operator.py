@@ -1,0 +1,66 @@
+"""Functional TaoMemory attention: the reference entry points on the HIP path.
+
+Same signatures, argument meaning and errors as the reference operator.py
+(:42-138). Inputs are [batch, tokens, heads, width]; raw_q / raw_k precede
+the caller's Q/K transform, q / k are the local-attention operands after it.
+The streaming path is bf16 on an MI355X device with width 64 or 128.
+"""
+
+import torch
+
+from .config import TaoConfig
+from .flash_attention import flash_attn
+from .tao_stream import StreamCache
+
+DEFAULT_CONFIG = TaoConfig()
+
+
+def tao_attention(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b, alpha,
+                  config=DEFAULT_CONFIG, local_flash=None):
+    """Full differentiable sequence read with fresh routing at every query.
+
+    operator.py:42-54 in the reference. Its HIP forward/backward kernels are
+    not built yet; the call raises instead of falling back to another path.
+    """
+    raise NotImplementedError(
+        "tao_attention (full-sequence training path) is not yet implemented on "
+        "the HIP path; use tao_attention_prefill / tao_attention_decode")
+
+
+def new_state(layer_index, config=DEFAULT_CONFIG):
+    """Independent mutable per-request, per-layer inference state."""
+    return StreamCache(layer_index, route_interval=2, fusion_mode="pointwise",
+                       fused_fine=True, config=config)
+
+
+def _check_plugin(local_flash):
+    if local_flash is not None and local_flash is not flash_attn:
+        raise NotImplementedError(
+            "a caller-supplied local_flash plugin is not supported by the fused HIP "
+            "streaming kernels yet; pass local_flash=None")
+
+
+def tao_attention_prefill(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b,
+                          alpha, state, position, local_flash=None):
+    """Advance only the supplied new tokens; the state is updated and returned."""
+    if position != state.position:
+        raise ValueError("position must match this request's causal cursor")
+    _check_plugin(local_flash)
+    if q.shape[1] == 0:
+        return q.new_empty(q.shape), state
+    with torch.inference_mode():
+        out = state.prefill(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
+    return out, state
+
+
+def tao_attention_decode(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b,
+                         alpha, state, position, local_flash=None):
+    """One-token prefill; no old token projection is recomputed."""
+    if q.shape[1] != 1:
+        raise ValueError("decode accepts exactly one new query/key/value")
+    if position != state.position:
+        raise ValueError("position must match this request's causal cursor")
+    _check_plugin(local_flash)
+    with torch.inference_mode():
+        out = state.decode(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
+    return out, state

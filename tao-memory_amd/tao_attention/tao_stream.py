@@ -1,0 +1,509 @@
+"""Per-request, per-layer streaming state on the device (HIP path).
+
+Mirrors the reference StreamCache (tao_stream.py:790-1094) and the LayerState
+it owns (tao_stream.py:126-527): same constructor, cursor, next_chunk,
+export/from_export schema, reset and release_execution. The storage is laid
+out for MI355X instead of rebuilt per seal:
+
+* the exact-local window is a token ring [B, serve_limit, H, D] (K, V, raw K)
+  indexed by position % serve_limit, replacing three torch.cat per call
+  (tao_stream.py:927-930) and the clone at each seal (:965-967);
+* fine memories live in a capacity-backed bank [B, H, S_cap, D, D] written in
+  place by the writer kernel, replacing the per-seal repack (:455-462);
+* page descriptors, segment weights r(exp(r(z - page_z))) and page weights
+  r(softmax over pages) are updated once per seal by the epilogue kernel:
+  this is the reference's page-normalisation memo (:399-416), kept valid
+  across the whole seal epoch for every call shape.
+Every count (local length, fines, pages, route turns) is a closed form of the
+cursor (schedule.py), so no device-to-host synchronisation is needed.
+"""
+
+import ctypes
+
+import torch
+
+from . import _hip, schedule
+from .config import TaoConfig
+
+DEFAULT_CONFIG = TaoConfig()
+_QTILE = 128
+
+
+class _DeviceState:
+    """Device buffers of one state and the C-ABI view of them."""
+
+    def __init__(self, config, batch, heads, head_dim, device, fine_cap):
+        self.config = config
+        self.B, self.H, self.D = batch, heads, head_dim
+        self.device = device
+        self.L = config.serve_limit
+        bf16 = torch.bfloat16
+        shape = (batch, self.L, heads, head_dim)
+        self.ring_k = torch.zeros(shape, dtype=bf16, device=device)
+        self.ring_v = torch.zeros(shape, dtype=bf16, device=device)
+        self.ring_raw = torch.zeros(shape, dtype=bf16, device=device)
+        self.header = torch.zeros(4, dtype=torch.int64, device=device)
+        self.starts = torch.zeros(1, dtype=torch.int64, device=device)
+        self.fine_cap = 0
+        self._allocate(fine_cap, copy_fines=0)
+
+    def _allocate(self, fine_cap, copy_fines):
+        cfg = self.config
+        B, H, D, dev = self.B, self.H, self.D, self.device
+        bf16 = torch.bfloat16
+        page_cap = fine_cap // cfg.coarse_group + 2
+        sel_cap = min(512, cfg.budget(fine_cap) + 1)
+        chosen_cap = page_cap
+        bank = torch.empty((B, H, fine_cap, D, D), dtype=bf16, device=dev)
+        fine_z = torch.zeros((B, H, fine_cap, D), dtype=bf16, device=dev)
+        fine_sw = torch.zeros((B, H, fine_cap, D), dtype=bf16, device=dev)
+        page_z = torch.zeros((B, H, page_cap, D), dtype=bf16, device=dev)
+        page_w = torch.zeros((B, H, page_cap, D), dtype=bf16, device=dev)
+        sel = torch.zeros((B, H, sel_cap), dtype=torch.int32, device=dev)
+        chosen = torch.zeros((B, H, chosen_cap), dtype=torch.int32, device=dev)
+        if copy_fines:
+            n = copy_fines
+            bank[:, :, :n].copy_(self.bank[:, :, :n])
+            fine_z[:, :, :n].copy_(self.fine_z[:, :, :n])
+            fine_sw[:, :, :n].copy_(self.fine_sw[:, :, :n])
+            pages = min(self.page_z.shape[2], page_cap)
+            page_z[:, :, :pages].copy_(self.page_z[:, :, :pages])
+            page_w[:, :, :pages].copy_(self.page_w[:, :, :pages])
+            m = min(self.sel.shape[2], sel_cap)
+            sel[:, :, :m].copy_(self.sel[:, :, :m])
+            c = min(self.chosen.shape[2], chosen_cap)
+            chosen[:, :, :c].copy_(self.chosen[:, :, :c])
+        self.bank, self.fine_z, self.fine_sw = bank, fine_z, fine_sw
+        self.page_z, self.page_w, self.sel, self.chosen = page_z, page_w, sel, chosen
+        self.fine_cap, self.page_cap, self.sel_cap, self.chosen_cap = (
+            fine_cap, page_cap, sel_cap, chosen_cap)
+        ws_bytes = _hip.lib().tao_workspace_bytes(B, H, D, sel_cap, 4096)
+        self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        self.struct = self._make_struct()
+        _hip.check(_hip.lib().tao_workspace_init(ctypes.byref(self.struct), self.stream()))
+
+    def _make_struct(self):
+        st = _hip.StateDev()
+        st.batch, st.heads, st.head_dim = self.B, self.H, self.D
+        st.local_keep = self.config.local_keep
+        st.fine_tokens = self.config.fine_tokens
+        st.coarse_group = self.config.coarse_group
+        st.fine_cap, st.page_cap = self.fine_cap, self.page_cap
+        st.sel_cap, st.chosen_cap = self.sel_cap, self.chosen_cap
+        st.ring_k, st.ring_v = self.ring_k.data_ptr(), self.ring_v.data_ptr()
+        st.ring_raw = self.ring_raw.data_ptr()
+        st.bank_c, st.fine_z = self.bank.data_ptr(), self.fine_z.data_ptr()
+        st.fine_sw, st.page_z = self.fine_sw.data_ptr(), self.page_z.data_ptr()
+        st.page_w, st.sel = self.page_w.data_ptr(), self.sel.data_ptr()
+        st.chosen, st.header = self.chosen.data_ptr(), self.header.data_ptr()
+        st.workspace = self.workspace.data_ptr()
+        st.workspace_bytes = self.workspace.numel()
+        return st
+
+    def stream(self):
+        return _hip.stream_ptr(self.device)
+
+    def reserve(self, fines, current):
+        """Grow the bank geometrically so ``fines`` sealed fines fit."""
+        if fines <= self.fine_cap:
+            return False
+        cap = max(self.fine_cap, 16)
+        while cap < fines:
+            cap *= 2
+        self._allocate(cap, copy_fines=current)
+        return True
+
+    def matches(self, batch, heads, head_dim, device):
+        return (self.B, self.H, self.D) == (batch, heads, head_dim) and self.device == device
+
+
+class HistoryRegionGraph:
+    """hipGraph of the single-token decode step (history_region_graph.py:10-113).
+
+    One captured graph per (state buffers, route size); the step's position
+    and route ids live in device memory, so seals and refreshes replay the
+    same graph. Counters keep the reference's observation() keys.
+    """
+
+    def __init__(self):
+        self.handle = None
+        self.key = None
+        self.staging = None
+        self.out_stage = None
+        self.counts = dict(epochs=0, eager_warm=0, captures=0, replays=0,
+                           id_copies=0, invalidations=0)
+        self.reasons = {}
+        self.last_action = "uninitialized"
+
+    def observation(self):
+        return {**self.counts, "active_graph": self.handle is not None,
+                "active_staging": self.staging is not None,
+                "epoch_state_version": None if self.key is None else self.key[0],
+                "last_action": self.last_action,
+                "invalidation_reasons": dict(self.reasons)}
+
+    def invalidate(self, reason):
+        if self.handle is None and self.key is None:
+            return
+        if self.staging is not None:
+            torch.cuda.current_stream(self.staging.device).synchronize()
+        if self.handle is not None:
+            _hip.check(_hip.lib().tao_graph_destroy(self.handle))
+        self.handle = self.key = None
+        self.staging = self.out_stage = None
+        self.counts["invalidations"] += 1
+        self.reasons[reason] = self.reasons.get(reason, 0) + 1
+        self.last_action = "invalidate:" + reason
+
+    def run(self, dev, fu, selected, tok, key):
+        if key != self.key:
+            self.invalidate("epoch_change")
+            B, H, D = dev.B, dev.H, dev.D
+            self.staging = torch.empty(5 * B * H * D, dtype=torch.bfloat16, device=dev.device)
+            self.out_stage = torch.empty((B, 1, H, D), dtype=torch.bfloat16, device=dev.device)
+            handle = ctypes.c_void_p()
+            _hip.check(_hip.lib().tao_graph_create(
+                ctypes.byref(dev.struct), ctypes.byref(fu), selected,
+                self.staging.data_ptr(), self.out_stage.data_ptr(), dev.stream(),
+                ctypes.byref(handle)))
+            self.handle = handle
+            self.key = key
+            self.counts["epochs"] += 1
+            self.counts["captures"] += 1
+            self.last_action = "capture_replay"
+        else:
+            self.last_action = "replay"
+        _hip.check(_hip.lib().tao_graph_launch(self.handle, ctypes.byref(tok), dev.stream()))
+        self.counts["replays"] += 1
+        return self.out_stage
+
+
+class StreamCache:
+    """One request's one-layer exact-local and hierarchical history state."""
+
+    is_tao_stream = True
+
+    def __init__(self, layer_index, route_interval=2, fusion_mode="pointwise",
+                 pending_coarse_elision=False, pending_coarse_mask=False,
+                 fused_fine=True, config=DEFAULT_CONFIG):
+        self.config = config
+        self.history_path_ablation = False
+        self.history_value_ablation = False
+        self.layer_index = layer_index
+        self.route_interval = route_interval
+        self.fusion_mode = fusion_mode
+        self.fused_fine = fused_fine
+        self.pending_coarse_elision = pending_coarse_elision
+        self.pending_coarse_mask = pending_coarse_mask
+        self.position = 0
+        self.fine_seal_events = 0
+        self.fusion_pointwise_calls = 0
+        self.fusion_no_history_local_returns = 0
+        self.route_refreshes = 0
+        self.peak_selected_fine = 0
+        self.route_size = 0          # M of the current route (0: no route)
+        self.route_coarse = 0
+        self.history_region = None
+        self._dev = None
+
+    # ------------------------------------------------------------------ cursor
+    def get_pos(self):
+        return self.position
+
+    @property
+    def state_version(self):
+        return schedule.fines_at(self.position, self.config)
+
+    def next_chunk(self, desired):
+        return schedule.next_chunk(self.position, desired, self.config)
+
+    # -------------------------------------------------------------- lifecycle
+    def release_execution(self, reason="request_end"):
+        if self.history_region is not None:
+            self.history_region.invalidate(reason)
+
+    def reset(self):
+        """Discard this request's state; position returns to zero."""
+        self.release_execution("reset")
+        self.__init__(self.layer_index, self.route_interval, self.fusion_mode,
+                      self.pending_coarse_elision, self.pending_coarse_mask,
+                      self.fused_fine, self.config)
+
+    def _check_supported(self, q):
+        cfg = self.config
+        if not cfg.coarse_index_only:
+            raise NotImplementedError(
+                "the HIP path implements the index-only coarse preset "
+                "(presets.index_only_page_memo); the coarse value branch is not built yet")
+        if cfg.fine_writer != "softmax":
+            raise NotImplementedError("the HIP path implements the softmax fine writer")
+        if cfg.fine_tokens != 256 or cfg.local_keep != 512:
+            raise NotImplementedError("the HIP path implements fine_tokens=256, local_keep=512")
+        if q.dtype != torch.bfloat16:
+            raise TypeError("the HIP path computes on bf16 operands")
+        if q.shape[-1] not in (64, 128):
+            raise ValueError("head width must be 64 or 128")
+        _hip.require_device(q)
+
+    def _device_for(self, q, total_positions):
+        b, _, h, d = q.shape
+        fines = schedule.fines_at(total_positions, self.config)
+        if self._dev is None:
+            cap = 16
+            while cap < fines:
+                cap *= 2
+            self._dev = _DeviceState(self.config, b, h, d, q.device, cap)
+        elif not self._dev.matches(b, h, d, q.device):
+            raise ValueError("batch/heads/width/device must stay fixed for a state")
+        elif self._dev.reserve(fines, schedule.fines_at(self.position, self.config)):
+            self.release_execution("capacity")
+        return self._dev
+
+    # ----------------------------------------------------------------- kernels
+    def _route(self, dev, raw_q_row, fines):
+        completed, pending = divmod(fines, self.config.coarse_group)
+        coarse, _, selected = schedule.routed_counts(completed, pending, self.config)
+        strides = (ctypes.c_int64 * 2)(raw_q_row.stride(0), raw_q_row.stride(1))
+        _hip.check(_hip.lib().tao_route(
+            ctypes.byref(dev.struct), raw_q_row.data_ptr(), strides,
+            completed, pending, coarse, selected, dev.stream()))
+        self.route_size, self.route_coarse = selected, coarse
+        self.route_refreshes += 1
+        self.peak_selected_fine = max(self.peak_selected_fine, selected)
+
+    def _seal(self, dev, tok, new_base, block_start, slot):
+        dev.starts.fill_(block_start)
+        _hip.check(_hip.lib().tao_write_fine(
+            ctypes.byref(dev.struct), ctypes.byref(tok), new_base,
+            dev.starts.data_ptr(), slot, 1, dev.stream()))
+        _hip.check(_hip.lib().tao_seal_epilogue(
+            ctypes.byref(dev.struct), slot, slot // self.config.coarse_group + 1, 1,
+            dev.stream()))
+        self.fine_seal_events += 1
+
+    # ---------------------------------------------------------------- streaming
+    def prefill(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
+        """Advance by q.shape[1] tokens; returns the fused heads [B, T, H, D]."""
+        self._check_supported(q)
+        cfg = self.config
+        pos0 = self.position
+        tokens = q.shape[1]
+        dev = self._device_for(q, pos0 + tokens)
+        q, k, v, raw_q, raw_k = (t if t.stride(-1) == 1 else t.contiguous()
+                                 for t in (q, k, v, raw_q, raw_k))
+        tok = _hip.tokens(q, k, v, raw_q, raw_k)
+        stream = dev.stream()
+        plan = schedule.chunks(pos0, tokens, cfg)
+        local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+        out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+        tiles = []
+        for start, width in plan:
+            key_start = start - schedule.local_len_at(start, cfg)
+            for qs in range(start, start + width, _QTILE):
+                tiles.append((qs - pos0, min(_QTILE, start + width - qs), key_start))
+        tiles_dev = torch.tensor(tiles, dtype=torch.int64).to(q.device)
+        _hip.check(_hip.lib().tao_local_attention(
+            ctypes.byref(dev.struct), ctypes.byref(tok), pos0, pos0,
+            tiles_dev.data_ptr(), len(tiles), local.data_ptr(), stream))
+        out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
+        for start, width in plan:
+            fines = schedule.fines_at(start, cfg)
+            fine_on = fines > 0
+            fu = _hip.fusion(fusion_a, fusion_b, alpha, False, fine_on)
+            for sub, count, refresh in schedule.sub_chunks(start, width, self.layer_index, cfg):
+                if fine_on and refresh:
+                    self._route(dev, raw_q[:, sub - pos0], fines)
+                _hip.check(_hip.lib().tao_read_fuse(
+                    ctypes.byref(dev.struct), ctypes.byref(tok), sub - pos0, count,
+                    self.route_size if fine_on else 0, ctypes.byref(fu),
+                    local.data_ptr(), out.data_ptr(), out_s, stream))
+            if fine_on:
+                self.fusion_pointwise_calls += 1
+            else:
+                self.fusion_no_history_local_returns += 1
+            if schedule.seals_in(start, width, cfg):
+                end = start + width
+                self._seal(dev, tok, pos0, end - cfg.serve_limit, fines)
+        keep = min(tokens, cfg.serve_limit)
+        _hip.check(_hip.lib().tao_ring_append(
+            ctypes.byref(dev.struct), ctypes.byref(tok), tokens - keep, keep,
+            pos0 + tokens - keep, stream))
+        self.position = pos0 + tokens
+        dev.header[0:1].fill_(self.position)
+        return out
+
+    def decode(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
+        """One new token; returns the fused heads [B, 1, H, D]."""
+        self._check_supported(q)
+        cfg = self.config
+        pos = self.position
+        dev = self._device_for(q, pos + 1)
+        q, k, v, raw_q, raw_k = (t if t.stride(-1) == 1 else t.contiguous()
+                                 for t in (q, k, v, raw_q, raw_k))
+        tok = _hip.tokens(q, k, v, raw_q, raw_k)
+        fines = schedule.fines_at(pos, cfg)
+        fine_on = fines > 0
+        if fine_on and schedule.is_turn(pos, self.layer_index, cfg):
+            self._route(dev, raw_q[:, 0], fines)
+        selected = self.route_size if fine_on else 0
+        fu = _hip.fusion(fusion_a, fusion_b, alpha, False, fine_on)
+        if cfg.q1_history_region_graph and fine_on:
+            if self.history_region is None:
+                self.history_region = HistoryRegionGraph()
+            key = (selected, dev.bank.data_ptr(), dev.workspace.data_ptr(),
+                   fusion_a.data_ptr(), fusion_b.data_ptr(), fu.dtype, fu.gain)
+            out = self.history_region.run(dev, fu, selected, tok, key)
+            self.history_region.fusion_keep = fu
+        else:
+            out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+            out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
+            _hip.check(_hip.lib().tao_decode_step(
+                ctypes.byref(dev.struct), ctypes.byref(tok), ctypes.byref(fu), selected,
+                out.data_ptr(), out_s, dev.stream()))
+        if fine_on:
+            self.fusion_pointwise_calls += 1
+        else:
+            self.fusion_no_history_local_returns += 1
+        if schedule.local_len_at(pos, cfg) + 1 == cfg.serve_limit:
+            self._seal(dev, tok, pos + 1, pos + 1 - cfg.serve_limit, fines)
+        self.position = pos + 1
+        return out
+
+    # ---------------------------------------------------------------- snapshot
+    def _local_window(self):
+        dev = self._dev
+        n = schedule.local_len_at(self.position, self.config)
+        if dev is None or n == 0:
+            return None
+        slots = torch.arange(self.position - n, self.position, device=dev.device) % dev.L
+        return tuple(buf.index_select(1, slots) for buf in (dev.ring_k, dev.ring_v, dev.ring_raw))
+
+    def export(self):
+        """Owned tensors in the reference snapshot schema (tao_stream.py:853-877)."""
+        cfg = self.config
+        dev = self._dev
+        fines = schedule.fines_at(self.position, cfg)
+        group = cfg.coarse_group
+        completed, pending = divmod(fines, group)
+        route_ids = None
+        if dev is not None and self.route_size:
+            chosen = dev.chosen[:, :, :self.route_coarse].to(torch.int64).unsqueeze(1).clone()
+            selected = dev.sel[:, :, :self.route_size].to(torch.int64).unsqueeze(1).clone()
+            route_ids = (chosen, selected)
+        pages, pending_z = [], []
+        packed = None
+        if fines:
+            packed = dev.bank[:, :, :fines].clone()
+            for i in range(completed):
+                pages.append((dev.page_z[:, :, i].clone(), None,
+                              dev.fine_z[:, :, i * group:(i + 1) * group].clone()))
+            for j in range(pending):
+                pending_z.append(dev.fine_z[:, :, completed * group + j].clone())
+        local = self._local_window()
+        return {
+            "layer_index": self.layer_index,
+            "config": cfg.export(),
+            "route_interval": self.route_interval,
+            "fusion_mode": self.fusion_mode,
+            "fused_fine": self.fused_fine,
+            "position": self.position,
+            "local": None if local is None else tuple(t.clone() for t in local),
+            "packed_fine_c": packed,
+            "pages": pages,
+            "pending_z": pending_z,
+            "pending_square_mass": None,
+            "pending_mass": None,
+            "pending_gram": None,
+            "pending_cross": None,
+            "route_ids": route_ids,
+            "route_key": None,
+            "state_version": fines,
+            "route_refreshes": self.route_refreshes,
+            "fine_seal_events": self.fine_seal_events,
+        }
+
+    @classmethod
+    def from_export(cls, saved):
+        """Restore an independent state (tao_stream.py:879-912)."""
+        config = TaoConfig(**saved["config"])
+        state = cls(saved["layer_index"], saved["route_interval"], saved["fusion_mode"],
+                    fused_fine=saved["fused_fine"], config=config)
+        position = saved["position"]
+        local = saved["local"]
+        packed = saved["packed_fine_c"]
+        pages, pending_z = saved["pages"], saved["pending_z"]
+        fines = len(pages) * config.coarse_group + len(pending_z)
+        if fines != schedule.fines_at(position, config):
+            raise ValueError("snapshot fine count does not match its position")
+        sample = local[0] if local is not None else None
+        if sample is None:
+            state.position = position
+            state.route_refreshes = saved["route_refreshes"]
+            state.fine_seal_events = saved["fine_seal_events"]
+            return state
+        state._check_supported(sample)
+        dev = state._device_for(sample, position)
+        group = config.coarse_group
+        n = sample.shape[1]
+        if n != schedule.local_len_at(position, config):
+            raise ValueError("snapshot local window does not match its position")
+        slots = torch.arange(position - n, position, device=dev.device) % dev.L
+        for buf, src in zip((dev.ring_k, dev.ring_v, dev.ring_raw), local):
+            buf.index_copy_(1, slots, src.to(torch.bfloat16))
+        if fines:
+            dev.bank[:, :, :fines].copy_(packed)
+            for i, (pz, _, fz) in enumerate(pages):
+                dev.page_z[:, :, i].copy_(pz)
+                dev.fine_z[:, :, i * group:(i + 1) * group].copy_(fz)
+            for j, z in enumerate(pending_z):
+                dev.fine_z[:, :, len(pages) * group + j].copy_(z)
+            # Completed pages keep their snapshot descriptors; the pending
+            # summary is recomputed (it is not part of the snapshot schema).
+            lib = _hip.lib()
+            for i in range(len(pages)):
+                _hip.check(lib.tao_seal_epilogue(
+                    ctypes.byref(dev.struct), i * group + group - 1, i + 1, 0,
+                    dev.stream()))
+            if pending_z:
+                _hip.check(lib.tao_seal_epilogue(
+                    ctypes.byref(dev.struct), fines - 1, len(pages) + 1, 1, dev.stream()))
+        if saved["route_ids"] is not None:
+            chosen, selected = saved["route_ids"]
+            state.route_coarse = chosen.shape[-1]
+            state.route_size = selected.shape[-1]
+            dev.sel[:, :, :state.route_size].copy_(selected[:, 0].to(torch.int32))
+            dev.chosen[:, :, :state.route_coarse].copy_(chosen[:, 0].to(torch.int32))
+        state.position = position
+        dev.header[0:1].fill_(position)
+        state.route_refreshes = saved["route_refreshes"]
+        state.fine_seal_events = saved["fine_seal_events"]
+        return state
+
+    # ------------------------------------------------------------- diagnostics
+    def bytes(self):
+        """Subset of the reference diagnostics (tao_stream.py:988-1094)."""
+        cfg = self.config
+        fines = schedule.fines_at(self.position, cfg)
+        completed, pending = divmod(fines, cfg.coarse_group)
+        dev = self._dev
+        if dev is None:
+            heads = width = batch = 0
+        else:
+            batch, heads, width = dev.B, dev.H, dev.D
+        count = completed * (cfg.coarse_group + 1) + pending
+        history = count * (width * width + width) * batch * heads * 2
+        if cfg.coarse_index_only:
+            history -= completed * width * width * batch * heads * 2
+        local_tokens = schedule.local_len_at(self.position, cfg)
+        return {"history_bytes": history,
+                "fine_seal_events": self.fine_seal_events,
+                "completed_coarse_pages": completed,
+                "pending_fine_states": pending,
+                "local_length_tokens": local_tokens,
+                "logical_local_bf16_kv_bytes": local_tokens * 2 * heads * width * 2 * batch,
+                "selected_fine_per_layer": [self.route_size],
+                "peak_selected_fine_per_layer": [self.peak_selected_fine],
+                "route_refreshes_per_layer": [self.route_refreshes],
+                "fusion_pointwise_calls": self.fusion_pointwise_calls,
+                "fusion_no_history_local_returns": self.fusion_no_history_local_returns,
+                "fine_matrix_repack_bytes": 0}

@@ -1,0 +1,189 @@
+"""HIP kernels vs the CPU oracle on the same seeded inputs (MI355X only).
+
+Bar: routed ids and every bf16 descriptor feeding routing (fine z, page z)
+bit-exact; head outputs and fine matrices within 2e-2 abs/rel (bf16).
+Every test calls the product through its public API, which calls the C ABI.
+"""
+import pytest
+import torch
+
+from oracle import tao_oracle as O
+from tao_attention import StreamCache, new_state, tao_attention_decode, tao_attention_prefill
+from tao_attention.flash_attention import flash_attn_func
+from tao_attention.presets import index_only_page_memo
+
+pytestmark = pytest.mark.gpu
+BF16 = torch.bfloat16
+TOL = dict(atol=2e-2, rtol=2e-2)
+
+
+def inputs(tokens, heads, width, seed, unit_raw_k=False):
+    g = torch.Generator().manual_seed(seed)
+    xs = [torch.randn(1, tokens, heads, width, generator=g) for _ in range(5)]
+    if unit_raw_k:
+        xs[4] = xs[4] / xs[4].norm(dim=-1, keepdim=True)
+    xs = [x.to(BF16) for x in xs]
+    fa = torch.randn(heads, width, 3, generator=g) * 0.02
+    fb = torch.randn(heads, width, 3, generator=g) * 0.02
+    return xs, fa, fb
+
+
+def to_dev(xs, device):
+    return [x.to(device) for x in xs]
+
+
+def run_hip(state, xs, fa, fb, splits, alpha=0.5):
+    q, k, v, rq, rk = xs
+    outs, start = [], 0
+    for width in splits:
+        sl = slice(start, start + width)
+        fn = tao_attention_decode if width == 1 else tao_attention_prefill
+        out, state = fn(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl], raw_k=rk[:, sl],
+                        fusion_a=fa, fusion_b=fb, alpha=alpha, state=state,
+                        position=state.get_pos())
+        outs.append(out.clone())
+        start += width
+    return torch.cat(outs, 1)
+
+
+def run_oracle(layer, xs, fa, fb, splits, alpha=0.5):
+    s = O.OracleStream(layer)
+    q, k, v, rq, rk = xs
+    outs, start = [], 0
+    for width in splits:
+        sl = slice(start, start + width)
+        outs.append(s.prefill(q[:, sl], k[:, sl], v[:, sl], rq[:, sl], rk[:, sl], fa, fb, alpha))
+        start += width
+    return s, torch.cat(outs, 1)
+
+
+def compare_snapshots(hip, ora):
+    assert hip["position"] == ora["position"]
+    assert hip["state_version"] == ora["state_version"]
+    assert len(hip["pages"]) == len(ora["pages"])
+    for (pz, _, fz), (opz, _, ofz) in zip(hip["pages"], ora["pages"]):
+        assert torch.equal(pz.cpu(), opz), "page descriptor"
+        assert torch.equal(fz.cpu(), ofz), "fine z"
+    for z, oz in zip(hip["pending_z"], ora["pending_z"]):
+        assert torch.equal(z.cpu(), oz), "pending fine z"
+    if ora["packed_fine_c"] is not None:
+        torch.testing.assert_close(hip["packed_fine_c"].cpu().float(),
+                                   ora["packed_fine_c"].float(), **TOL)
+    if ora["route_ids"] is not None:
+        assert torch.equal(hip["route_ids"][1].cpu(), ora["route_ids"][1]), "selected ids"
+        assert torch.equal(hip["route_ids"][0].cpu(), ora["route_ids"][0]), "chosen pages"
+    for a, b in zip(hip["local"], ora["local"]):
+        assert torch.equal(a.cpu(), b)
+
+
+@pytest.mark.parametrize("width", [64, 128])
+@pytest.mark.parametrize("tq,tk", [(200, 200), (1, 700), (256, 768), (77, 333)])
+def test_local_attention_plugin(device, width, tq, tk):
+    g = torch.Generator().manual_seed(tq * 1000 + tk)
+    q, k, v = (torch.randn(1, n, 4, width, generator=g).to(BF16) for n in (tq, tk, tk))
+    print(f"local attention width={width} tq={tq} tk={tk}", flush=True)
+    got = flash_attn_func(q.to(device), k.to(device), v.to(device)).cpu()
+    ref = O.local_attention(q, k, v)
+    torch.testing.assert_close(got.float(), ref.float(), **TOL)
+
+
+@pytest.mark.parametrize("heads,width", [(4, 64), (2, 128)])
+def test_prefill_matches_oracle(device, heads, width):
+    xs, fa, fb = inputs(2100, heads, width, seed=11)
+    print(f"prefill heads={heads} width={width}", flush=True)
+    state = new_state(0, index_only_page_memo())
+    out = run_hip(state, to_dev(xs, device), fa.to(device), fb.to(device), [2100])
+    ora, ref = run_oracle(0, xs, fa, fb, [2100])
+    torch.testing.assert_close(out.cpu().float(), ref.float(), **TOL)
+    compare_snapshots(state.export(), ora.export())
+
+
+def test_decode_matches_oracle_across_seal_and_refresh(device):
+    heads, width = 4, 128
+    xs, fa, fb = inputs(1330, heads, width, seed=12)
+    splits = [1200] + [1] * 130          # seals at position 1279, refreshes every 24
+    print("decode across seal", flush=True)
+    state = new_state(3, index_only_page_memo())
+    out = run_hip(state, to_dev(xs, device), fa.to(device), fb.to(device), splits)
+    ora, ref = run_oracle(3, xs, fa, fb, splits)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), **TOL)
+    compare_snapshots(state.export(), ora.export())
+
+
+def test_chunked_prefill_and_page_routing(device):
+    """Arbitrary chunking plus completed pages (coarse selection active)."""
+    heads, width = 2, 64
+    xs, fa, fb = inputs(4700, heads, width, seed=13, unit_raw_k=True)
+    splits = [1000, 256, 700, 2000, 1] + [1] * 30 + [713]
+    print("chunked prefill with pages", flush=True)
+    state = new_state(1, index_only_page_memo())
+    out = run_hip(state, to_dev(xs, device), fa.to(device), fb.to(device), splits)
+    ora, ref = run_oracle(1, xs, fa, fb, splits)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), **TOL)
+    compare_snapshots(state.export(), ora.export())
+
+
+def test_graph_equals_eager_bitwise(device):
+    heads, width = 4, 128
+    xs, fa, fb = inputs(1100, heads, width, seed=14)
+    d = to_dev(xs, device)
+    splits = [1000] + [1] * 100
+    print("graph vs eager", flush=True)
+    eager = run_hip(new_state(0, index_only_page_memo(graph=False)), d, fa.to(device),
+                    fb.to(device), splits)
+    graph_state = new_state(0, index_only_page_memo(graph=True))
+    graph = run_hip(graph_state, d, fa.to(device), fb.to(device), splits)
+    assert torch.equal(eager, graph)
+    assert graph_state.history_region.counts["replays"] > 0
+    graph_state.release_execution()
+
+
+def test_export_import_reset_gpu_sanity(device):
+    """tests/gpu_sanity.py invariants: cursor, export/import equality, reset."""
+    heads, width = 6, 128
+    xs, _, _ = inputs(1089, heads, width, seed=42)
+    d = to_dev(xs, device)
+    a = torch.zeros(heads, width, 3, device=device)
+    b = torch.zeros_like(a)
+    print("gpu sanity", flush=True)
+    for graph in (False, True):
+        state = new_state(0, index_only_page_memo(graph=graph))
+        q, k, v, rq, rk = d
+        for start in range(0, 1024, 256):
+            sl = slice(start, start + 256)
+            _, state = tao_attention_prefill(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
+                                             raw_k=rk[:, sl], fusion_a=a, fusion_b=b, alpha=0.1,
+                                             state=state, position=state.get_pos())
+        for i in range(1024, 1088):
+            sl = slice(i, i + 1)
+            out, state = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
+                                              raw_k=rk[:, sl], fusion_a=a, fusion_b=b, alpha=0.1,
+                                              state=state, position=state.get_pos())
+            assert torch.isfinite(out).all()
+        assert state.get_pos() == 1088
+        restored = StreamCache.from_export(state.export())
+        sl = slice(1088, 1089)
+        left, state = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
+                                           raw_k=rk[:, sl], fusion_a=a, fusion_b=b, alpha=0.1,
+                                           state=state, position=state.get_pos())
+        right, restored = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
+                                               raw_k=rk[:, sl], fusion_a=a, fusion_b=b,
+                                               alpha=0.1, state=restored,
+                                               position=restored.get_pos())
+        assert torch.equal(left, right)
+        state.reset()
+        assert state.get_pos() == 0 and restored.get_pos() == 1089
+        state.release_execution()
+        restored.release_execution()
+
+
+def test_contract_errors(device):
+    xs, fa, fb = inputs(4, 2, 64, seed=0)
+    q, k, v, rq, rk = to_dev(xs, device)
+    state = new_state(0, index_only_page_memo())
+    with pytest.raises(ValueError):
+        tao_attention_prefill(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.to(device),
+                              fusion_b=fb.to(device), alpha=0.5, state=state, position=1)
+    with pytest.raises(ValueError):
+        tao_attention_decode(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.to(device),
+                             fusion_b=fb.to(device), alpha=0.5, state=state, position=0)

@@ -1,0 +1,302 @@
+"""Pins the CPU oracle (CPU only).
+
+The reference ships no golden vectors (its only test, tests/gpu_sanity.py,
+asserts finiteness and self-consistency), so each oracle function is checked
+against something independent of its own formula: closed forms and the
+survey's derived table, torch's own bf16 ops (the reference's third-party
+arithmetic), fp64 brute force, stable-sort brute force and streaming
+invariants. Each check is chosen so a plausible restatement mistake (wrong
+softmax axis, dropped rounding, off-by-one window, unstable tie order) fails.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import numerics as N
+from oracle import tao_oracle as O
+
+BF16 = torch.bfloat16
+
+
+# --------------------------------------------------------------- closed forms
+def test_budget_matches_ceil_sqrt_definition():
+    g = O.Geometry()
+    for n in range(0, 5000):
+        if n == 0:
+            assert g.budget(0) == 0
+            continue
+        root = math.ceil(math.sqrt(2 * n) - 1e-12)
+        while root * root < 2 * n:
+            root += 1
+        while (root - 1) * (root - 1) >= 2 * n:
+            root -= 1
+        assert g.budget(n) == min(n, root + 2)
+    assert (g.budget(510), g.budget(62), g.budget(126)) == (34, 14, 18)
+
+
+@pytest.mark.parametrize("context,expect", [
+    (2048, (0, 6, 6)), (8192, (3, 30, 10)), (16384, (4, 38, 14)),
+    (32768, (5, 46, 18)), (131072, (9, 78, 34)),
+])
+def test_routed_counts_table(context, expect):
+    """Derived counts table: pages/pending after `context` tokens."""
+    g = O.Geometry()
+    fines = (context - g.serve_limit) // g.fine_tokens + 1
+    completed, pending = divmod(fines, g.coarse_group)
+    assert g.routed_counts(completed, pending) == expect
+
+
+def test_turn_schedule():
+    g = O.Geometry()
+    turns0 = [p for p in range(700, 900) if g.is_turn(p, 0)]
+    assert turns0 == [768, 792, 816, 840, 864, 888]
+    turns5 = [p for p in range(700, 900) if g.is_turn(p, 5)]
+    assert turns5 == [768, 778, 802, 826, 850, 874, 898]
+    for layer in (0, 3):
+        for p in range(700, 1000):
+            nt = g.next_turn(p, layer)
+            assert nt > p and g.is_turn(nt, layer) or nt == 768 + 2 * layer
+            assert not any(g.is_turn(x, layer) and x >= 768 + 2 * layer
+                           for x in range(p + 1, nt))
+
+
+# ------------------------------------------------------- torch's own bf16 ops
+@pytest.mark.parametrize("shape,dim", [((4, 32, 8, 128), 2), ((3, 16, 6, 64), 2),
+                                       ((2, 8, 64, 128), 2), ((5, 7, 3), 1)])
+def test_logsumexp_is_torch_bf16_composite(shape, dim):
+    torch.manual_seed(1)
+    x = (torch.randn(shape) * 3).to(BF16)
+    assert torch.equal(N.logsumexp(x, dim), torch.logsumexp(x, dim=dim))
+
+
+def test_logsumexp_single_rounding_would_fail():
+    """The composite's intermediate roundings are observable (not a no-op)."""
+    torch.manual_seed(2)
+    x = (torch.randn(4, 32, 8, 128) * 3).to(BF16)
+    single = torch.logsumexp(x.float(), dim=2).to(BF16)
+    assert (single != N.logsumexp(x, 2)).float().mean() > 0.01
+
+
+@pytest.mark.parametrize("shape,dim", [((64, 32, 128), -1), ((2, 32, 64, 128), 2),
+                                       ((2, 8, 9, 64), 2)])
+def test_softmax_matches_torch_bf16_within_one_ulp(shape, dim):
+    torch.manual_seed(3)
+    x = (torch.randn(shape) * 2).to(BF16)
+    a, b = torch.softmax(x, dim=dim), N.softmax(x, dim)
+    diff = (N.bf16_bits(a) - N.bf16_bits(b)).abs()
+    assert diff.max() <= 1
+    assert (diff > 0).float().mean() < 1e-3
+
+
+def test_fold_sum_is_butterfly_order():
+    torch.manual_seed(4)
+    for n in (1, 3, 8, 64, 100, 128, 200):
+        x = torch.randn(5, n) * torch.logspace(-3, 3, n)
+        got = N.fold_sum(x, -1)
+        for row in range(5):
+            vals = [torch.tensor(v, dtype=torch.float32) for v in x[row].tolist()]
+            width = 1
+            while width < n:
+                width *= 2
+            vals += [torch.tensor(0.0)] * (width - n)
+            while len(vals) > 1:
+                half = len(vals) // 2
+                vals = [vals[i] + vals[i + half] for i in range(half)]
+            assert got[row].item() == vals[0].item()
+
+
+# ------------------------------------------------------------ fp64 brute force
+def test_writer_against_fp64():
+    torch.manual_seed(5)
+    k = torch.randn(1, 256, 3, 32).to(BF16)
+    v = torch.randn(1, 256, 3, 32).to(BF16)
+    z, c = O.seal_softmax(k, v)
+    kd, vd = k.double(), v.double()
+    z_ref = torch.logsumexp(kd, dim=1)                       # over tokens
+    p_ref = torch.softmax(kd, dim=1)
+    c_ref = torch.einsum("bthd,bthe->bhde", p_ref, vd)
+    torch.testing.assert_close(z.double(), z_ref, atol=2e-2, rtol=1e-2)
+    torch.testing.assert_close(c.double(), c_ref, atol=2e-3, rtol=2e-2)
+    # Softmax over channels instead of tokens must not pass.
+    p_bad = torch.softmax(kd, dim=-1)
+    c_bad = torch.einsum("bthd,bthe->bhde", p_bad, vd)
+    assert (c.double() - c_bad).abs().max() > 1e-2
+
+
+def test_read_against_fp64():
+    torch.manual_seed(6)
+    b, q, h, p, s, d, m = 1, 3, 2, 3, 20, 16, 5
+    hv = (torch.rand(b, q, h, p, d) / d).to(BF16)
+    sw = torch.rand(b, h, s, d).to(BF16)
+    bank = torch.randn(b, h, s, d, d).to(BF16)
+    sel = torch.stack([torch.randperm(s)[:m] for _ in range(h)])[None]
+    fine, ch = O.selected_read(hv, sw, sel, bank, group=8)
+    ref = torch.zeros(b, q, h, d, dtype=torch.float64)
+    for hh in range(h):
+        num = torch.zeros(q, d, dtype=torch.float64)
+        den = torch.zeros(q, 1, dtype=torch.float64)
+        for slot in range(m):
+            fid = sel[0, hh, slot].item()
+            weight = hv[0, :, hh, fid // 8].double() * sw[0, hh, fid].double()
+            num += weight @ bank[0, hh, fid].double()
+            den += weight.sum(-1, keepdim=True)
+        ref[0, :, hh] = num / den
+    torch.testing.assert_close(fine.double(), ref, atol=2e-2, rtol=2e-2)
+
+
+def test_local_attention_against_sdpa_modes():
+    torch.manual_seed(7)
+    import torch.nn.functional as F
+    for tq, tk in ((8, 8), (1, 20), (5, 20)):
+        q = torch.randn(1, tq, 2, 16).to(BF16)
+        k = torch.randn(1, tk, 2, 16).to(BF16)
+        v = torch.randn(1, tk, 2, 16).to(BF16)
+        got = O.local_attention(q, k, v)
+        qt, kt, vt = (t.double().transpose(1, 2) for t in (q, k, v))
+        if tq == tk:
+            ref = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True)
+        elif tq == 1:
+            ref = F.scaled_dot_product_attention(qt, kt, vt)
+        else:
+            rows = tk - tq + torch.arange(tq)
+            mask = torch.arange(tk)[None, :] <= rows[:, None]
+            ref = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask)
+        torch.testing.assert_close(got.double(), ref.transpose(1, 2), atol=1e-2, rtol=1e-2)
+
+
+def test_fusion_closed_form():
+    """Coarse absent: out = 2*rho0*local + 2*alpha*rho2*fine, rho = softmax(s0, s2)."""
+    torch.manual_seed(8)
+    h, d = 2, 16
+    raw_q = torch.randn(1, 4, h, d).to(BF16)
+    local = torch.randn(1, 4, h, d).to(BF16)
+    fine = torch.randn(1, 4, h, d).to(BF16)
+    a = torch.randn(h, d, 3) * 0.5
+    bias = torch.randn(h, d, 3) * 0.5
+    alpha = 0.5
+    out = O.fusion(raw_q, local, torch.zeros_like(local), fine, a, bias, alpha, False, True)
+    s0 = a[..., 0].double() * raw_q.double() + bias[..., 0].double()
+    s2 = a[..., 2].double() * raw_q.double() + bias[..., 2].double()
+    r0 = torch.sigmoid(s0 - s2)
+    ref = 2 * r0 * local.double() + 2 * alpha * (1 - r0) * fine.double()
+    torch.testing.assert_close(out.double(), ref, atol=5e-2, rtol=3e-2)
+
+
+# ------------------------------------------------------------------- routing
+def _sorted_topk(scores, count):
+    order = sorted(range(len(scores)), key=lambda i: (-scores[i], i))
+    return order[:count]
+
+
+def test_route_against_stable_sort_brute_force():
+    torch.manual_seed(9)
+    g = O.Geometry()
+    completed, pending = 9, 5
+    b, h, d = 1, 3, 16
+    pages = completed + 1
+    s = completed * 8 + pending
+    # Quantised values create many exact bf16 ties.
+    hv = (torch.randint(1, 4, (b, h, pages, d)).float() / 64).to(BF16)
+    sw = (torch.randint(1, 4, (b, h, s, d)).float() / 4).to(BF16)
+    chosen, selected, info = O.route(hv, sw, completed, pending, g)
+    coarse, eligible, m = g.routed_counts(completed, pending)
+    assert chosen.shape[-1] == coarse and selected.shape[-1] == m
+    for hh in range(h):
+        pm = [N.rnd(N.fold_sum(hv[0, hh, p], -1)).float().item() for p in range(completed)]
+        want_pages = sorted(_sorted_topk(pm, coarse))
+        assert chosen[0, hh].tolist() == want_pages
+        cands = [p * 8 + j for p in want_pages for j in range(8)]
+        cands += [completed * 8 + j for j in range(pending)]
+        scores = []
+        for fid in cands:
+            page = min(fid // 8, completed)
+            ch = N.rnd(hv[0, hh, page].float() * sw[0, hh, fid].float())
+            scores.append(N.rnd(N.fold_sum(ch, -1)).float().item())
+        want = [cands[i] for i in _sorted_topk(scores, m)]
+        assert selected[0, hh].tolist() == want
+        assert len(set(want)) == m
+
+
+# ---------------------------------------------------------------- streaming
+def _stream_inputs(tokens, heads=2, width=16, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    xs = [torch.randn(1, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
+    fa = torch.randn(heads, width, 3, generator=g) * 0.02
+    fb = torch.randn(heads, width, 3, generator=g) * 0.02
+    return xs, fa, fb
+
+
+def _run(stream, xs, fa, fb, splits, alpha=0.5):
+    q, k, v, rq, rk = xs
+    outs = []
+    start = 0
+    for width in splits:
+        sl = slice(start, start + width)
+        if width == 1:
+            outs.append(stream.decode(q[:, sl], k[:, sl], v[:, sl], rq[:, sl], rk[:, sl],
+                                      fa, fb, alpha, position=start))
+        else:
+            outs.append(stream.prefill(q[:, sl], k[:, sl], v[:, sl], rq[:, sl], rk[:, sl],
+                                       fa, fb, alpha, position=start))
+        start += width
+    return torch.cat(outs, 1)
+
+
+def test_stream_local_only_before_first_fine():
+    xs, fa, fb = _stream_inputs(800)
+    s = O.OracleStream(0)
+    out = _run(s, xs, fa, fb, [800])
+    q, k, v = xs[:3]
+    for end in (256, 512, 768):
+        start = end - 256
+        lo = max(0, end - 768)
+        ref = O.local_attention(q[:, start:end], k[:, lo:end], v[:, lo:end])
+        assert torch.equal(out[:, start:end], ref)
+    assert not torch.equal(out[:, 768:800], O.local_attention(q[:, 768:800], k[:, 256:800], v[:, 256:800]))
+
+
+def test_stream_chunking_invariance_and_decode_equals_prefill():
+    xs, fa, fb = _stream_inputs(1400, seed=1)
+    whole = _run(O.OracleStream(1), xs, fa, fb, [1400])
+    calls = _run(O.OracleStream(1), xs, fa, fb, [256, 256, 300, 100, 400, 88])
+    torch.testing.assert_close(whole, calls, atol=0, rtol=0)
+    mixed = _run(O.OracleStream(1), xs, fa, fb, [1300] + [1] * 100)
+    torch.testing.assert_close(whole, mixed, atol=0, rtol=0)
+
+
+def test_stream_export_import_continues_identically():
+    xs, fa, fb = _stream_inputs(1500, seed=2)
+    a = O.OracleStream(0)
+    _run(a, xs, fa, fb, [1200])
+    snap = a.export()
+    b = O.OracleStream.from_export(snap, 0)
+    rest = [t[:, 1200:] for t in xs]
+    q, k, v, rq, rk = rest
+    out_a = a.prefill(q, k, v, rq, rk, fa, fb, 0.5)
+    out_b = b.prefill(q, k, v, rq, rk, fa, fb, 0.5)
+    assert torch.equal(out_a, out_b)
+    assert a.position == b.position == 1500
+
+
+def test_banks_depend_only_on_raw_k_and_v():
+    xs, fa, fb = _stream_inputs(1300, seed=3)
+    ys = [t.clone() for t in xs]
+    ys[0] = torch.randn_like(ys[0].float()).to(BF16)   # q
+    ys[3] = torch.randn_like(ys[3].float()).to(BF16)   # raw_q
+    a, b = O.OracleStream(0), O.OracleStream(0)
+    _run(a, xs, fa, fb, [1300])
+    _run(b, ys, fa, fb, [1300])
+    assert len(a.fine_z) == len(b.fine_z) == 3
+    for x, y in zip(a.fine_z + a.fine_c, b.fine_z + b.fine_c):
+        assert torch.equal(x, y)
+
+
+def test_stream_rejects_contract_violations():
+    xs, fa, fb = _stream_inputs(10)
+    s = O.OracleStream(0)
+    q, k, v, rq, rk = xs
+    with pytest.raises(ValueError):
+        s.prefill(q, k, v, rq, rk, fa, fb, 0.5, position=3)
+    with pytest.raises(ValueError):
+        s.decode(q[:, :2], k[:, :2], v[:, :2], rq[:, :2], rk[:, :2], fa, fb, 0.5)

@@ -1,0 +1,362 @@
+#!/usr/bin/env python
+"""TaoMemory operator benchmark on one MI355X.
+
+Headline (``value``): advancing decode tok/s of one request x layer from a
+131072-token state, 32 heads x 128, bf16, page memo + hipGraph, 256 tokens
+one at a time (the timed region includes route
+refreshes, the seal and graph capture). Also reported: prefill tokens/s of a
+16384-token prompt through tao_attention_prefill, a cold-cache
+decode variant that cycles 8 independent 128K states (> 4 GB working set,
+beyond the 256 MB Infinity Cache), the roofline of the dominant kernels
+measured live with HIP events on the launch stream, and the CPU oracle
+(reference arithmetic in torch eager) on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "tao-memory_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "decode tok/s @128K ctx + prefill tokens/s @16K, 1 MI355X; % HBM/MFMA roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Probe:
+    """Records HIP events around every launch a StreamCache makes."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.events = {}
+        self.enabled = True
+
+    def __call__(self, name):
+        probe = self
+
+        class _Ctx:
+            def __enter__(self_inner):
+                if probe.enabled:
+                    self_inner.start = probe.torch.cuda.Event(enable_timing=True)
+                    self_inner.start.record()
+
+            def __exit__(self_inner, *exc):
+                if probe.enabled:
+                    end = probe.torch.cuda.Event(enable_timing=True)
+                    end.record()
+                    probe.events.setdefault(name, []).append((self_inner.start, end))
+                return False
+        return _Ctx()
+
+    def total_ms(self, name):
+        return sum(s.elapsed_time(e) for s, e in self.events.get(name, []))
+
+    def count(self, name):
+        return len(self.events.get(name, []))
+
+    def reset(self):
+        self.events = {}
+
+
+def make_tokens(torch, tokens, heads, width, seed, device, unit_raw_k=False):
+    g = torch.Generator(device=device).manual_seed(seed)
+    xs = []
+    for i in range(5):
+        x = torch.randn((1, tokens, heads, width), generator=g, device=device,
+                        dtype=torch.float32)
+        if unit_raw_k and i == 4:
+            x = x / x.norm(dim=-1, keepdim=True)
+        xs.append(x.to(torch.bfloat16))
+    fa = torch.randn((heads, width, 3), generator=g, device=device) * 0.02
+    fb = torch.randn((heads, width, 3), generator=g, device=device) * 0.02
+    return xs, fa, fb
+
+
+def decode_bytes(cfg, heads, width, selected, position):
+    """Algorithmic HBM bytes of one fused decode step."""
+    from tao_attention import schedule
+    keys = schedule.local_len_at(position, cfg) + 1
+    c_bytes = heads * selected * width * width * 2
+    side = heads * selected * (2 * width * 2 + 4)        # sw + pw rows, ids
+    local = keys * heads * width * 2 * 2                  # ring K and V
+    tokens = 5 * heads * width * 2 + 3 * heads * width * 2 + heads * width * 2
+    return c_bytes + side + local + tokens, c_bytes
+
+
+def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
+    from tao_attention import StreamCache, new_state, tao_attention_decode
+    from tao_attention.presets import index_only_page_memo
+    total = context + args.steps
+    xs, fa, fb = make_tokens(torch, total, heads, width, seed, device)
+    state = new_state(0, index_only_page_memo(graph=True))
+    state._ingest(*(x[:, :context] for x in xs))
+    torch.cuda.synchronize()
+    log(f"decode state built: position {state.get_pos()}, route size {state.route_size}")
+    # Warm-up on an independent copy, same tokens.
+    warm = StreamCache.from_export(state.export())
+    q, k, v, rq, rk = xs
+    for i in range(context, context + args.warmup):
+        sl = slice(i, i + 1)
+        _, warm = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
+                                       raw_k=rk[:, sl], fusion_a=fa, fusion_b=fb, alpha=0.5,
+                                       state=warm, position=warm.get_pos())
+    torch.cuda.synchronize()
+    warm.release_execution()
+    del warm
+    snap = state.export()
+    q, k, v, rq, rk = xs
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(context, context + args.steps):
+        sl = slice(i, i + 1)
+        _, state = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
+                                        raw_k=rk[:, sl], fusion_a=fa, fusion_b=fb, alpha=0.5,
+                                        state=state, position=state.get_pos())
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    # Instrumented replay of the same steps on an imported copy: HIP events
+    # around each launch give the kernel durations for the roofline.
+    timed = StreamCache.from_export(snap)
+    del snap
+    timed._probe = probe
+    probe.reset()
+    steps_bytes = []
+    for i in range(context, context + args.steps):
+        sl = slice(i, i + 1)
+        _, timed = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
+                                        raw_k=rk[:, sl], fusion_a=fa, fusion_b=fb, alpha=0.5,
+                                        state=timed, position=timed.get_pos())
+        steps_bytes.append(decode_bytes(cfg, heads, width, timed.route_size, i))
+    torch.cuda.synchronize()
+    timed._probe = None
+    timed.release_execution()
+    return state, xs, fa, fb, t1 - t0, steps_bytes
+
+
+def run_cold(torch, args, device, cfg, heads, width, context, n_states, probe):
+    from tao_attention import new_state, tao_attention_decode
+    from tao_attention.presets import index_only_page_memo
+    states, toks = [], []
+    for j in range(n_states):
+        xs, fa, fb = make_tokens(torch, context + args.steps, heads, width, 100 + j, device)
+        st = new_state(0, index_only_page_memo(graph=True))
+        st._ingest(*(x[:, :context] for x in xs))
+        toks.append([x[:, context:].clone() for x in xs])
+        del xs
+        states.append(st)
+    torch.cuda.synchronize()
+    log(f"cold: {n_states} states built")
+    for j, st in enumerate(states):        # warm the graphs of every state
+        q, k, v, rq, rk = toks[j]
+        _, states[j] = tao_attention_decode(q[:, :1], k[:, :1], v[:, :1], raw_q=rq[:, :1],
+                                            raw_k=rk[:, :1], fusion_a=fa, fusion_b=fb,
+                                            alpha=0.5, state=st, position=st.get_pos())
+    for st in states:
+        st._probe = probe
+    probe.reset()
+    steps = args.steps - 1
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        j = i % n_states
+        st = states[j]
+        q, k, v, rq, rk = toks[j]
+        t = 1 + i // n_states
+        sl = slice(t, t + 1)
+        _, states[j] = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
+                                            raw_k=rk[:, sl], fusion_a=fa, fusion_b=fb,
+                                            alpha=0.5, state=st, position=st.get_pos())
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    sel = states[0].route_size
+    for st in states:
+        st._probe = None
+        st.release_execution()
+    return steps, t1 - t0, sel
+
+
+def run_prefill(torch, device, cfg, heads, width, tokens, probe):
+    from tao_attention import new_state, schedule, tao_attention_prefill
+    from tao_attention.presets import index_only_page_memo
+    xs, fa, fb = make_tokens(torch, tokens, heads, width, 3, device, unit_raw_k=True)
+    q, k, v, rq, rk = xs
+    warm = new_state(0, index_only_page_memo())
+    tao_attention_prefill(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa, fusion_b=fb, alpha=0.5,
+                          state=warm, position=0)
+    torch.cuda.synchronize()
+    del warm
+    state = new_state(0, index_only_page_memo())
+    state._probe = probe
+    probe.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    _, state = tao_attention_prefill(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa, fusion_b=fb,
+                                     alpha=0.5, state=state, position=0)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    snapshot = state.export()
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    state._probe = None
+    # Algorithmic MFMA work: causal-aware local attention + writer.
+    visible = 0
+    for start, width_c in schedule.chunks(0, tokens, cfg):
+        ks = start - schedule.local_len_at(start, cfg)
+        for p in range(start, start + width_c):
+            visible += p - ks + 1
+    attn_flops = visible * 4 * width * heads
+    fines = schedule.fines_at(tokens, cfg)
+    writer_flops = fines * heads * 2 * cfg.fine_tokens * width * width
+    return dict(seconds=t1 - t0, export_seconds=t2 - t1, attn_flops=attn_flops,
+                writer_flops=writer_flops, fines=fines, snapshot_fines=snapshot["state_version"])
+
+
+def cpu_baseline(torch, state, xs, fa, fb, steps):
+    from oracle import tao_oracle as O
+    snap = state.export()
+    cpu = {}
+    for key, value in snap.items():
+        cpu[key] = value
+    cpu["local"] = tuple(t.cpu() for t in snap["local"])
+    cpu["packed_fine_c"] = snap["packed_fine_c"].cpu()
+    cpu["pages"] = [(pz.cpu(), None, fz.cpu()) for pz, _, fz in snap["pages"]]
+    cpu["pending_z"] = [z.cpu() for z in snap["pending_z"]]
+    cpu["route_ids"] = tuple(t.cpu() for t in snap["route_ids"])
+    ora = O.OracleStream.from_export(cpu, 0)
+    toks = [x[:, :steps].cpu() for x in xs]
+    fa_c, fb_c = fa.cpu(), fb.cpu()
+    ora.decode(*(t[:, :1] for t in toks), fa_c, fb_c, 0.5)       # warm-up
+    t0 = time.perf_counter()
+    for i in range(1, steps):
+        ora.decode(*(t[:, i:i + 1] for t in toks), fa_c, fb_c, 0.5)
+    t1 = time.perf_counter()
+    return (steps - 1) / (t1 - t0), steps - 1
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--context", type=int, default=131072)
+    ap.add_argument("--prefill-tokens", type=int, default=16384)
+    ap.add_argument("--cold-states", type=int, default=8)
+    ap.add_argument("--cpu-steps", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cold", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the TaoMemory operator path has no "
+              "multi-GPU mode in this build (see DESIGN.md, sharding design); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from tao_attention import _hip
+    from tao_attention.presets import index_only_page_memo
+    _hip.lib()
+    device = torch.device("cuda:0")
+    cfg = index_only_page_memo(graph=True)
+    heads, width = 32, 128
+    probe = Probe(torch)
+
+    log("decode: building 128K state")
+    state, xs, fa, fb, seconds, steps_bytes = run_decode(
+        torch, args, device, cfg, heads, width, args.context, 4, probe)
+    tok_s = args.steps / seconds
+    n_step = probe.count("decode_step")
+    step_ms = probe.total_ms("decode_step") / max(n_step, 1)
+    alg_bytes = sum(b for b, _ in steps_bytes) / len(steps_bytes)
+    c_bytes = sum(c for _, c in steps_bytes) / len(steps_bytes)
+    route_ms = probe.total_ms("route") / max(probe.count("route"), 1)
+    achieved = alg_bytes / (step_ms * 1e-3) / 1e9
+    log(f"decode: {tok_s:.1f} tok/s, step kernel {step_ms * 1e3:.2f} us, {achieved:.0f} GB/s")
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(seconds / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) bf16 operands (seeded); state built writer-only",
+        "config": {"workload": "configs[3]: advancing decode of one request x layer from a "
+                               "131072-token state, H32 D128, 256 single-token steps, "
+                               "index_only_page_memo(graph=True)",
+                   "context": args.context, "heads": heads, "head_dim": width,
+                   "selected_fines": state.route_size},
+        "roofline": {"bound": "hbm", "kernel": "decode_step_kernel<128>",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel_us": round(step_ms * 1e3, 3),
+                     "algorithmic_bytes_per_launch": int(alg_bytes),
+                     "selected_c_bytes_per_launch": int(c_bytes),
+                     "route_kernel_us": round(route_ms * 1e3, 3)},
+    }
+    if not args.no_cold:
+        log("cold decode: building states")
+        del xs
+        steps, cold_s, cold_sel = run_cold(torch, args, device, cfg, heads, width,
+                                           args.context, args.cold_states, probe)
+        cold_ms = probe.total_ms("decode_step") / max(probe.count("decode_step"), 1)
+        cold_bytes, _ = decode_bytes(cfg, heads, width, cold_sel, args.context + 8)
+        result["decode_cold"] = {
+            "states": args.cold_states, "tok_s": round(steps / cold_s, 2),
+            "kernel_us": round(cold_ms * 1e3, 3),
+            "achieved_GBs": round(cold_bytes / (cold_ms * 1e-3) / 1e9, 1)}
+        log(f"cold: {steps / cold_s:.1f} tok/s, kernel {cold_ms * 1e3:.2f} us")
+        xs = None
+    if not args.no_prefill:
+        log("prefill 16K")
+        pre = run_prefill(torch, device, cfg, heads, width, args.prefill_tokens, probe)
+        attn_ms = probe.total_ms("local_attention")
+        writer_ms = probe.total_ms("writer")
+        flops = pre["attn_flops"] + pre["writer_flops"]
+        tflops = flops / ((attn_ms + writer_ms) * 1e-3) / 1e12
+        result["prefill_tokens_per_s"] = round(args.prefill_tokens / pre["seconds"], 1)
+        result["prefill"] = {
+            "tokens": args.prefill_tokens, "seconds": round(pre["seconds"], 5),
+            "export_seconds": round(pre["export_seconds"], 5),
+            "read_fuse_ms": round(probe.total_ms("read_fuse"), 3),
+            "route_ms": round(probe.total_ms("route"), 3),
+            "epilogue_ms": round(probe.total_ms("epilogue"), 3)}
+        result["roofline_prefill"] = {
+            "bound": "mfma", "kernels": "local_attn_kernel<128> + writer_kernel<128>",
+            "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+            "attention_ms": round(attn_ms, 4), "writer_ms": round(writer_ms, 4),
+            "algorithmic_gflop": round(flops / 1e9, 2)}
+        log(f"prefill: {result['prefill_tokens_per_s']} tok/s, mfma {tflops:.1f} TFLOP/s")
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle, torch eager on host cores)")
+        xs_cpu, _, _ = make_tokens(torch, args.cpu_steps, heads, width, 7, device)
+        cpu_tok_s, sample = cpu_baseline(torch, state, xs_cpu, fa, fb, args.cpu_steps)
+        result["cpu_baseline"] = {
+            "value": round(cpu_tok_s, 4), "unit": "tok/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{sample} single-token decodes of the oracle from the GPU state's "
+                      f"snapshot at position {state.get_pos()} (H32 D128), torch "
+                      f"{torch.__version__}"}
+        log(f"cpu baseline: {cpu_tok_s:.3f} tok/s")
+    state.release_execution()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

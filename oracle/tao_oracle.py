@@ -329,6 +329,7 @@ class OracleStream:
         self.state_version = 0
         self.route_refreshes = 0
         self.fine_seal_events = 0
+        self._bank = None            # stacked fine_c, rebuilt after a seal
 
     # -- state views ------------------------------------------------------
     @property
@@ -363,6 +364,7 @@ class OracleStream:
         z, c = seal_softmax(raw_k, v)
         self.fine_z.append(z)
         self.fine_c.append(c)
+        self._bank = None
         self.state_version += 1
         group = self.g.coarse_group
         if self.pending == group:
@@ -383,7 +385,9 @@ class OracleStream:
         page_z = self.page_descriptors()
         pw = page_weights(page_z)
         sw = self.fine_segment_weights(page_z)
-        bank = torch.stack(self.fine_c, 2)
+        if self._bank is None or self._bank.shape[2] != len(self.fine_c):
+            self._bank = torch.stack(self.fine_c, 2)
+        bank = self._bank
         h = query_weights(raw_q)
         hv = page_values(h, pw)                               # [B,T,H,P,D]
         coarse_on = bool(self.page_z) and not self.g.coarse_index_only

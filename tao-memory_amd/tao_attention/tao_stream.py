@@ -18,6 +18,7 @@ Every count (local length, fines, pages, route turns) is a closed form of the
 cursor (schedule.py), so no device-to-host synchronisation is needed.
 """
 
+import contextlib
 import ctypes
 
 import torch
@@ -205,6 +206,9 @@ class StreamCache:
         self.route_coarse = 0
         self.history_region = None
         self._dev = None
+        # Optional launch probe: probe(name) -> context manager wrapped around
+        # each kernel launch (used by bench.py for live kernel timing).
+        self._probe = None
 
     # ------------------------------------------------------------------ cursor
     def get_pos(self):
@@ -260,26 +264,35 @@ class StreamCache:
         return self._dev
 
     # ----------------------------------------------------------------- kernels
+    def _timed(self, name):
+        return self._probe(name) if self._probe is not None else contextlib.nullcontext()
+
     def _route(self, dev, raw_q_row, fines):
         completed, pending = divmod(fines, self.config.coarse_group)
         coarse, _, selected = schedule.routed_counts(completed, pending, self.config)
         strides = (ctypes.c_int64 * 2)(raw_q_row.stride(0), raw_q_row.stride(1))
-        _hip.check(_hip.lib().tao_route(
-            ctypes.byref(dev.struct), raw_q_row.data_ptr(), strides,
-            completed, pending, coarse, selected, dev.stream()))
+        with self._timed("route"):
+            _hip.check(_hip.lib().tao_route(
+                ctypes.byref(dev.struct), raw_q_row.data_ptr(), strides,
+                completed, pending, coarse, selected, dev.stream()))
         self.route_size, self.route_coarse = selected, coarse
         self.route_refreshes += 1
         self.peak_selected_fine = max(self.peak_selected_fine, selected)
 
     def _seal(self, dev, tok, new_base, block_start, slot):
         dev.starts.fill_(block_start)
-        _hip.check(_hip.lib().tao_write_fine(
-            ctypes.byref(dev.struct), ctypes.byref(tok), new_base,
-            dev.starts.data_ptr(), slot, 1, dev.stream()))
-        _hip.check(_hip.lib().tao_seal_epilogue(
-            ctypes.byref(dev.struct), slot, slot // self.config.coarse_group + 1, 1,
-            dev.stream()))
+        with self._timed("writer"):
+            _hip.check(_hip.lib().tao_write_fine(
+                ctypes.byref(dev.struct), ctypes.byref(tok), new_base,
+                dev.starts.data_ptr(), slot, 1, dev.stream()))
+        self._epilogue(dev, slot)
         self.fine_seal_events += 1
+
+    def _epilogue(self, dev, slot):
+        with self._timed("epilogue"):
+            _hip.check(_hip.lib().tao_seal_epilogue(
+                ctypes.byref(dev.struct), slot, slot // self.config.coarse_group + 1, 1,
+                dev.stream()))
 
     # ---------------------------------------------------------------- streaming
     def prefill(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
@@ -302,9 +315,21 @@ class StreamCache:
             for qs in range(start, start + width, _QTILE):
                 tiles.append((qs - pos0, min(_QTILE, start + width - qs), key_start))
         tiles_dev = torch.tensor(tiles, dtype=torch.int64).to(q.device)
-        _hip.check(_hip.lib().tao_local_attention(
-            ctypes.byref(dev.struct), ctypes.byref(tok), pos0, pos0,
-            tiles_dev.data_ptr(), len(tiles), local.data_ptr(), stream))
+        with self._timed("local_attention"):
+            _hip.check(_hip.lib().tao_local_attention(
+                ctypes.byref(dev.struct), ctypes.byref(tok), pos0, pos0,
+                tiles_dev.data_ptr(), len(tiles), local.data_ptr(), stream))
+        # Banks depend only on raw_k and v: every seal of the call is written
+        # by one launch; each chunk end then publishes its seal's epoch.
+        first_fine = schedule.fines_at(pos0, cfg)
+        last_fine = schedule.fines_at(pos0 + tokens, cfg)
+        if last_fine > first_fine:
+            starts = [cfg.fine_tokens * f for f in range(first_fine, last_fine)]
+            starts_dev = torch.tensor(starts, dtype=torch.int64).to(q.device)
+            with self._timed("writer"):
+                _hip.check(_hip.lib().tao_write_fine(
+                    ctypes.byref(dev.struct), ctypes.byref(tok), pos0, starts_dev.data_ptr(),
+                    first_fine, len(starts), stream))
         out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
         for start, width in plan:
             fines = schedule.fines_at(start, cfg)
@@ -313,17 +338,18 @@ class StreamCache:
             for sub, count, refresh in schedule.sub_chunks(start, width, self.layer_index, cfg):
                 if fine_on and refresh:
                     self._route(dev, raw_q[:, sub - pos0], fines)
-                _hip.check(_hip.lib().tao_read_fuse(
-                    ctypes.byref(dev.struct), ctypes.byref(tok), sub - pos0, count,
-                    self.route_size if fine_on else 0, ctypes.byref(fu),
-                    local.data_ptr(), out.data_ptr(), out_s, stream))
+                with self._timed("read_fuse"):
+                    _hip.check(_hip.lib().tao_read_fuse(
+                        ctypes.byref(dev.struct), ctypes.byref(tok), sub - pos0, count,
+                        self.route_size if fine_on else 0, ctypes.byref(fu),
+                        local.data_ptr(), out.data_ptr(), out_s, stream))
             if fine_on:
                 self.fusion_pointwise_calls += 1
             else:
                 self.fusion_no_history_local_returns += 1
             if schedule.seals_in(start, width, cfg):
-                end = start + width
-                self._seal(dev, tok, pos0, end - cfg.serve_limit, fines)
+                self._epilogue(dev, fines)
+                self.fine_seal_events += 1
         keep = min(tokens, cfg.serve_limit)
         _hip.check(_hip.lib().tao_ring_append(
             ctypes.byref(dev.struct), ctypes.byref(tok), tokens - keep, keep,
@@ -352,14 +378,16 @@ class StreamCache:
                 self.history_region = HistoryRegionGraph()
             key = (selected, dev.bank.data_ptr(), dev.workspace.data_ptr(),
                    fusion_a.data_ptr(), fusion_b.data_ptr(), fu.dtype, fu.gain)
-            out = self.history_region.run(dev, fu, selected, tok, key)
+            with self._timed("decode_step"):
+                out = self.history_region.run(dev, fu, selected, tok, key)
             self.history_region.fusion_keep = fu
         else:
             out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
             out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
-            _hip.check(_hip.lib().tao_decode_step(
-                ctypes.byref(dev.struct), ctypes.byref(tok), ctypes.byref(fu), selected,
-                out.data_ptr(), out_s, dev.stream()))
+            with self._timed("decode_step"):
+                _hip.check(_hip.lib().tao_decode_step(
+                    ctypes.byref(dev.struct), ctypes.byref(tok), ctypes.byref(fu), selected,
+                    out.data_ptr(), out_s, dev.stream()))
         if fine_on:
             self.fusion_pointwise_calls += 1
         else:
@@ -368,6 +396,57 @@ class StreamCache:
             self._seal(dev, tok, pos + 1, pos + 1 - cfg.serve_limit, fines)
         self.position = pos + 1
         return out
+
+    def _ingest(self, q, k, v, raw_q, raw_k):
+        """Advance the state by q.shape[1] tokens without computing outputs.
+
+        The resulting state equals prefill()'s: the banks depend only on raw_k
+        and v (all seals go to the writer in one launch), the epilogues run in
+        seal order, and the route of the last refresh turn is recomputed in
+        its own seal epoch from that turn's anchor query.
+        """
+        self._check_supported(q)
+        cfg = self.config
+        pos0 = self.position
+        tokens = q.shape[1]
+        end = pos0 + tokens
+        dev = self._device_for(q, end)
+        q, k, v, raw_q, raw_k = (t if t.stride(-1) == 1 else t.contiguous()
+                                 for t in (q, k, v, raw_q, raw_k))
+        tok = _hip.tokens(q, k, v, raw_q, raw_k)
+        first_fine = schedule.fines_at(pos0, cfg)
+        last_fine = schedule.fines_at(end, cfg)
+        starts = [cfg.fine_tokens * (f - 1) for f in range(first_fine + 1, last_fine + 1)]
+        if starts:
+            starts_dev = torch.tensor(starts, dtype=torch.int64).to(q.device)
+            with self._timed("writer"):
+                _hip.check(_hip.lib().tao_write_fine(
+                    ctypes.byref(dev.struct), ctypes.byref(tok), pos0, starts_dev.data_ptr(),
+                    first_fine, len(starts), dev.stream()))
+        # Last refresh turn inside [pos0, end) whose read saw fines.
+        turn = None
+        for p in range(end - 1, max(pos0, cfg.first_fine) - 1, -1):
+            if schedule.is_turn(p, self.layer_index, cfg):
+                turn = p
+                break
+        self.route_refreshes += sum(
+            1 for p in range(max(pos0, cfg.first_fine), end)
+            if schedule.is_turn(p, self.layer_index, cfg)) - (turn is not None)
+        route_epoch = schedule.fines_at(turn, cfg) if turn is not None else None
+        for slot in range(first_fine, last_fine):
+            if route_epoch is not None and slot == route_epoch:
+                self._route(dev, raw_q[:, turn - pos0], route_epoch)
+                route_epoch = None
+            self._epilogue(dev, slot)
+            self.fine_seal_events += 1
+        if route_epoch is not None:
+            self._route(dev, raw_q[:, turn - pos0], route_epoch)
+        keep = min(tokens, cfg.serve_limit)
+        _hip.check(_hip.lib().tao_ring_append(
+            ctypes.byref(dev.struct), ctypes.byref(tok), tokens - keep, keep,
+            end - keep, dev.stream()))
+        self.position = end
+        dev.header[0:1].fill_(end)
 
     # ---------------------------------------------------------------- snapshot
     def _local_window(self):

@@ -86,12 +86,12 @@ typedef struct tao_fusion {
 int tao_abi_version(void);
 const char* tao_last_error(void);
 
-/* Workspace bytes a state of this geometry needs (no hidden allocation). */
+/* Workspace bytes a state of this geometry needs: decode partials plus room
+ * for a prefill plan of plan_words int64 (no hidden allocation). */
 size_t tao_workspace_bytes(int32_t batch, int32_t heads, int32_t head_dim,
-                           int32_t sel_cap, int32_t max_query_tokens);
+                           int32_t sel_cap, int32_t plan_words);
 
-/* Zero the arrival counters inside the workspace (call once per new
- * workspace; kernels leave them zeroed). */
+/* Zero a new workspace. */
 int tao_workspace_init(const tao_state_dev* st, void* stream);
 
 /* One fused single-token decode step (replaces the memo-backed q1 region,
@@ -142,15 +142,50 @@ int tao_local_attention(const tao_state_dev* st, const tao_tokens* tok,
                         int64_t qpos0, int64_t kpos0, const int64_t* tiles,
                         int32_t n_tiles, void* local, void* stream);
 
-/* Selected fine read plus fusion for `count` queries starting at token
- * `first` of tok that share the current route (replaces query_fresh_fine.py
- * :52-75 for multi-token calls and fusion_pointwise.py:95-117). local is
- * the [B, T, H, D] local-attention output; out gets the fused heads. When
- * fu->fine_on is 0 the output is the local attention unchanged. */
-int tao_read_fuse(const tao_state_dev* st, const tao_tokens* tok,
-                  int32_t first, int32_t count, int32_t selected,
-                  const tao_fusion* fu, const void* local, void* out,
-                  const int64_t* out_s, void* stream);
+/* Epoch pools of one prefill call (caller-allocated):
+ *   pw_pool  bf16 [epochs][B][H][pool_pcap][D]  page weights per seal epoch
+ *   psw_pool bf16 [epochs][B][H][coarse_group][D] pending segment weights
+ *   sel_pool int32 [sel_slots][B][H][sel_cap]   selected ids per route turn
+ * Slot 0 of sel_pool receives the state's route at call start. */
+typedef struct tao_prefill_pools {
+  void* pw_pool; void* psw_pool; int32_t* sel_pool;
+  int32_t pool_pcap, epochs, sel_slots;
+} tao_prefill_pools;
+
+/* Layout of the int64 prefill plan (all indices are token offsets in tok
+ * unless noted). Header of TAO_PLAN_HEADER words, then the arrays. */
+#define TAO_PLAN_HEADER 16
+enum tao_plan_field {
+  TAO_PLAN_POS0 = 0,        /* absolute position of token 0 */
+  TAO_PLAN_ATTN_TILES = 1,  /* n, then n x {first, count <= 128, key_start} */
+  TAO_PLAN_WRITES = 2,      /* n, then n block start positions */
+  TAO_PLAN_FIRST_SLOT = 3,  /* fine slot of the first written block */
+  TAO_PLAN_FIRST_PAGE = 4,  /* first page completed by this call */
+  TAO_PLAN_PAGES = 5,       /* number of pages completed by this call */
+  TAO_PLAN_FIRST_EPOCH = 6, /* first seal epoch (visible fines) read */
+  TAO_PLAN_EPOCHS = 7,      /* epochs, the last one is published */
+  TAO_PLAN_TURNS = 8,       /* n, then n x {anchor, epoch - first_epoch,
+                               completed, pending, coarse, selected,
+                               sel slot, publish} */
+  TAO_PLAN_READ_TILES = 9,  /* n, then n x {first, count <= 32, sel slot,
+                               selected, epoch - first_epoch, sw split,
+                               fine_on, 0} */
+  TAO_PLAN_RING_FIRST = 10, /* ring append: first token, count, position */
+  TAO_PLAN_RING_COUNT = 11,
+  TAO_PLAN_RING_POS = 12
+};
+
+/* Batched prefill of tok.tokens new tokens (replaces the chunk loop of
+ * tao_attention_prefill, operator.py:100-127, with StreamCache.process,
+ * tao_stream.py:919-979, for every chunk): local attention for all chunks,
+ * the writer for every seal, page/epoch bookkeeping, routes for every
+ * refresh turn, selected read + fusion for every query, ring append. The
+ * plan is validated on the host and copied into the workspace. local:
+ * bf16 [B, T, H, D] scratch for the local attention output. */
+int tao_prefill(const tao_state_dev* st, const tao_tokens* tok,
+                const tao_fusion* fu, const int64_t* plan, int64_t plan_len,
+                const tao_prefill_pools* pools, void* local, void* out,
+                const int64_t* out_s, void* stream);
 
 /* Copy `count` tokens starting at token `first` of tok into the ring at
  * absolute positions [pos, pos + count) (keys, values, raw keys). */

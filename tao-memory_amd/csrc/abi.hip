@@ -36,11 +36,24 @@ int check_state(const tao_state_dev* st) {
       !st->header || !st->workspace)
     return fail(TAO_E_ARGUMENT, "state has a null device buffer");
   if (st->sel_cap > 512) return fail(TAO_E_CAPACITY, "sel_cap above 512");
+  if (st->coarse_group != 8) return fail(TAO_E_SHAPE, "HIP kernels implement coarse_group=8");
   const tao::WorkspaceLayout lay =
       tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
-  if (st->workspace_bytes < lay.tiles_off)
+  if (st->workspace_bytes < lay.plan_off)
     return fail(TAO_E_WORKSPACE, "workspace smaller than tao_workspace_bytes()");
   return TAO_OK;
+}
+
+size_t plan_capacity(const tao_state_dev* st) {
+  const tao::WorkspaceLayout lay =
+      tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
+  return (st->workspace_bytes - lay.plan_off) / sizeof(int64_t);
+}
+
+int64_t* plan_of(const tao_state_dev* st) {
+  const tao::WorkspaceLayout lay =
+      tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
+  return (int64_t*)((char*)st->workspace + lay.plan_off);
 }
 
 tao::TokView view(const void* p, const int64_t* s) {
@@ -50,12 +63,6 @@ tao::TokView view(const void* p, const int64_t* s) {
   v.st = s[1];
   v.sh = s[2];
   return v;
-}
-
-uint32_t* counters_of(const tao_state_dev* st) {
-  const tao::WorkspaceLayout lay =
-      tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
-  return (uint32_t*)((char*)st->workspace + lay.counters_off);
 }
 
 float* parts_of(const tao_state_dev* st) {
@@ -89,7 +96,6 @@ tao::DecodeParams decode_params(const tao_state_dev* st, const tao_tokens* tok,
   p.out_sb = out_s[0];
   p.out_sh = out_s[2];
   p.parts = parts_of(st);
-  p.counters = counters_of(st);
   p.B = st->batch;
   p.H = st->heads;
   p.keep = st->local_keep;
@@ -127,16 +133,15 @@ struct DecodeGraph {
 namespace tao {
 
 WorkspaceLayout workspace_layout(int batch, int heads, int head_dim, int sel_cap,
-                                 int max_query_tokens) {
+                                 int plan_words) {
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   WorkspaceLayout lay;
   const size_t bh = (size_t)batch * heads;
-  lay.counters_off = 0;
-  lay.parts_off = align((bh + 1) * sizeof(uint32_t));
+  lay.parts_off = 0;
   const size_t parts = bh * (kLocalSplits + (size_t)sel_cap) * (head_dim + 4) * sizeof(float);
-  lay.tiles_off = align(lay.parts_off + parts);
-  lay.tiles_cap = (size_t)max_query_tokens / 32 + 64;
-  lay.total = align(lay.tiles_off + lay.tiles_cap * 3 * sizeof(int64_t));
+  lay.plan_off = align(parts);
+  lay.plan_words = plan_words > 0 ? (size_t)plan_words : 0;
+  lay.total = align(lay.plan_off + lay.plan_words * sizeof(int64_t));
   return lay;
 }
 
@@ -149,15 +154,14 @@ int tao_abi_version(void) { return TAO_ABI_VERSION; }
 const char* tao_last_error(void) { return g_error.c_str(); }
 
 size_t tao_workspace_bytes(int32_t batch, int32_t heads, int32_t head_dim,
-                           int32_t sel_cap, int32_t max_query_tokens) {
-  return tao::workspace_layout(batch, heads, head_dim, sel_cap, max_query_tokens).total;
+                           int32_t sel_cap, int32_t plan_words) {
+  return tao::workspace_layout(batch, heads, head_dim, sel_cap, plan_words).total;
 }
 
 int tao_workspace_init(const tao_state_dev* st, void* stream) {
   int rc = check_state(st);
   if (rc) return rc;
-  const size_t bytes = ((size_t)st->batch * st->heads + 1) * sizeof(uint32_t);
-  return check_hip(hipMemsetAsync(counters_of(st), 0, bytes, (hipStream_t)stream),
+  return check_hip(hipMemsetAsync(st->workspace, 0, st->workspace_bytes, (hipStream_t)stream),
                    "tao_workspace_init");
 }
 
@@ -191,10 +195,13 @@ int tao_route(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_
   const int eligible = coarse * st->coarse_group + pending;
   if (selected <= 0 || selected > eligible || selected > st->sel_cap)
     return fail(TAO_E_CAPACITY, "selected count out of range");
-  tao::RouteParams p;
+  tao::RouteParams p = {};
   p.rq = (const bf16_t*)raw_q_row;
   p.rq_sb = rq_s[0];
+  p.rq_st = 0;
   p.rq_sh = rq_s[1];
+  p.turns = nullptr;
+  p.n_turns = 0;
   p.pw = (const bf16_t*)st->page_w;
   p.sw = (const bf16_t*)st->fine_sw;
   p.sel = st->sel;
@@ -292,48 +299,248 @@ int tao_local_attention(const tao_state_dev* st, const tao_tokens* tok, int64_t 
                    "tao_local_attention");
 }
 
-int tao_read_fuse(const tao_state_dev* st, const tao_tokens* tok, int32_t first,
-                  int32_t count, int32_t selected, const tao_fusion* fu, const void* local,
-                  void* out, const int64_t* out_s, void* stream) {
+int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
+                const int64_t* plan, int64_t plan_len, const tao_prefill_pools* pools,
+                void* local, void* out, const int64_t* out_s, void* stream) {
   int rc = check_state(st);
   if (!rc) rc = check_tokens(tok);
   if (!rc) rc = check_fusion(fu);
   if (rc) return rc;
-  if (!local || !out || !out_s) return fail(TAO_E_ARGUMENT, "null local or output");
-  if (first < 0 || count < 0 || first + count > tok->tokens)
-    return fail(TAO_E_ARGUMENT, "query range outside the token operands");
-  if (fu->fine_on && (selected <= 0 || selected > st->sel_cap))
-    return fail(TAO_E_CAPACITY, "selected count out of range");
-  if (fu->coarse_on) return fail(TAO_E_SHAPE, "coarse value branch is not implemented on the HIP path");
-  tao::ReadParams p;
-  p.rq = view(tok->raw_q, tok->rq_s);
-  p.bank = (const bf16_t*)st->bank_c;
-  p.sw = (const bf16_t*)st->fine_sw;
-  p.pw = (const bf16_t*)st->page_w;
-  p.sel = st->sel;
-  p.local = (const bf16_t*)local;
-  p.fa = fu->fusion_a;
-  p.fb = fu->fusion_b;
-  p.f_dtype = fu->dtype;
-  for (int i = 0; i < 3; ++i) { p.fa_s[i] = fu->a_s[i]; p.fb_s[i] = fu->b_s[i]; }
-  p.gain = fu->gain;
-  p.coarse_on = fu->coarse_on;
-  p.fine_on = fu->fine_on;
-  p.out = (bf16_t*)out;
-  p.out_sb = out_s[0];
-  p.out_st = out_s[1];
-  p.out_sh = out_s[2];
-  p.B = st->batch;
-  p.H = st->heads;
-  p.T = tok->tokens;
-  p.first = first;
-  p.count = count;
-  p.selected = selected;
-  p.group = st->coarse_group;
-  p.fine_cap = st->fine_cap;
-  p.page_cap = st->page_cap;
-  p.sel_cap = st->sel_cap;
-  return check_hip(tao::launch_read_fuse(p, st->head_dim, (hipStream_t)stream), "tao_read_fuse");
+  if (!plan || plan_len < TAO_PLAN_HEADER || !local || !out || !out_s)
+    return fail(TAO_E_ARGUMENT, "null plan, local or output");
+  if ((size_t)plan_len > plan_capacity(st))
+    return fail(TAO_E_WORKSPACE, "prefill plan larger than the workspace plan region");
+  const hipStream_t s = (hipStream_t)stream;
+  const int T = tok->tokens;
+  const int L = st->local_keep + st->fine_tokens;
+  const int64_t pos0 = plan[TAO_PLAN_POS0];
+  if (pos0 < 0) return fail(TAO_E_ARGUMENT, "negative position");
+  const int64_t window0 = pos0 - [&] {
+    if (pos0 < L) return (int64_t)pos0;
+    return (int64_t)st->local_keep + (pos0 - L) % st->fine_tokens;
+  }();
+  // ---- section offsets
+  const int64_t n_attn = plan[TAO_PLAN_ATTN_TILES], n_write = plan[TAO_PLAN_WRITES];
+  const int64_t n_turns = plan[TAO_PLAN_TURNS], n_read = plan[TAO_PLAN_READ_TILES];
+  if (n_attn < 0 || n_write < 0 || n_turns < 0 || n_read < 0)
+    return fail(TAO_E_ARGUMENT, "negative plan section");
+  const int64_t off_attn = TAO_PLAN_HEADER, off_write = off_attn + 3 * n_attn;
+  const int64_t off_turns = off_write + n_write, off_read = off_turns + 8 * n_turns;
+  if (off_read + 8 * n_read != plan_len) return fail(TAO_E_ARGUMENT, "plan length mismatch");
+  const int BH = st->batch * st->heads;
+  // ---- validate attention tiles
+  for (int64_t i = 0; i < n_attn; ++i) {
+    const int64_t* t = plan + off_attn + 3 * i;
+    if (t[0] < 0 || t[1] < 1 || t[1] > 128 || t[0] + t[1] > T)
+      return fail(TAO_E_ARGUMENT, "attention tile outside the call's tokens");
+    if (t[2] < window0 || t[2] > pos0 + t[0] || pos0 + t[0] + t[1] - t[2] > L)
+      return fail(TAO_E_ARGUMENT, "attention tile window outside the local ring");
+  }
+  // ---- writer blocks
+  const int64_t first_slot = plan[TAO_PLAN_FIRST_SLOT];
+  for (int64_t i = 0; i < n_write; ++i) {
+    const int64_t b0 = plan[off_write + i];
+    if (b0 < window0 || b0 + st->fine_tokens > pos0 + T)
+      return fail(TAO_E_ARGUMENT, "writer block outside the ring and the call's tokens");
+  }
+  if (n_write && (first_slot < 0 || first_slot + n_write > st->fine_cap))
+    return fail(TAO_E_CAPACITY, "written fines exceed fine_cap");
+  // ---- pages and epochs
+  const int64_t first_page = plan[TAO_PLAN_FIRST_PAGE], n_pages = plan[TAO_PLAN_PAGES];
+  const int64_t first_epoch = plan[TAO_PLAN_FIRST_EPOCH], n_epochs = plan[TAO_PLAN_EPOCHS];
+  const int G = st->coarse_group;
+  if (n_pages < 0 || (n_pages && (first_page < 0 || first_page + n_pages > st->page_cap ||
+                                  (first_page + n_pages) * G > st->fine_cap)))
+    return fail(TAO_E_CAPACITY, "completed pages exceed the state capacity");
+  if (n_epochs < 0) return fail(TAO_E_ARGUMENT, "negative epoch count");
+  const bool need_pools = n_epochs > 0 || n_turns > 0;
+  if (need_pools) {
+    if (!pools || !pools->pw_pool || !pools->psw_pool || !pools->sel_pool)
+      return fail(TAO_E_ARGUMENT, "prefill with history needs epoch pools");
+    const int64_t last = first_epoch + n_epochs - 1;
+    if (first_epoch < 1 || n_epochs > pools->epochs || last > st->fine_cap ||
+        last / G + 1 > pools->pool_pcap || last / G + 1 > st->page_cap)
+      return fail(TAO_E_CAPACITY, "epoch range exceeds the pools or the state");
+  }
+  // ---- turns
+  for (int64_t i = 0; i < n_turns; ++i) {
+    const int64_t* t = plan + off_turns + 8 * i;
+    const int64_t epoch = first_epoch + t[1];
+    const int64_t eligible = t[4] * G + t[3];
+    if (t[0] < 0 || t[0] >= T || t[1] < 0 || t[1] >= n_epochs ||
+        t[2] * G + t[3] != epoch || t[3] < 0 || t[3] >= G || t[4] < 0 || t[4] > t[2] ||
+        t[5] < 1 || t[5] > eligible || t[5] > st->sel_cap || t[6] < 1 ||
+        t[6] >= pools->sel_slots || (t[7] != 0 && t[7] != 1) || t[2] > 2048 ||
+        eligible > 2048 || t[4] > st->chosen_cap)
+      return fail(TAO_E_ARGUMENT, "invalid route turn in the plan");
+  }
+  // ---- read tiles
+  for (int64_t i = 0; i < n_read; ++i) {
+    const int64_t* t = plan + off_read + 8 * i;
+    if (t[0] < 0 || t[1] < 1 || t[1] > 32 || t[0] + t[1] > T || (t[6] != 0 && t[6] != 1))
+      return fail(TAO_E_ARGUMENT, "invalid read tile in the plan");
+    if (t[6]) {
+      const int64_t epoch = first_epoch + t[4];
+      if (!pools || t[2] < 0 || t[2] >= pools->sel_slots || t[3] < 1 || t[3] > 128 ||
+          t[3] > st->sel_cap || t[4] < 0 || t[4] >= n_epochs || t[5] != (epoch / G) * G)
+        return fail(TAO_E_ARGUMENT, "invalid history read tile in the plan");
+    }
+  }
+  // ---- ring append
+  const int64_t ring_first = plan[TAO_PLAN_RING_FIRST], ring_count = plan[TAO_PLAN_RING_COUNT];
+  if (ring_first < 0 || ring_count < 0 || ring_first + ring_count > T || ring_count > L ||
+      plan[TAO_PLAN_RING_POS] != pos0 + ring_first)
+    return fail(TAO_E_ARGUMENT, "invalid ring append in the plan");
+
+  int64_t* dplan = plan_of(st);
+  hipError_t e = hipMemcpyAsync(dplan, plan, (size_t)plan_len * sizeof(int64_t),
+                                hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return check_hip(e, "tao_prefill plan upload");
+  if (need_pools && pools->sel_slots > 0) {
+    e = hipMemcpyAsync(pools->sel_pool, st->sel, (size_t)BH * st->sel_cap * sizeof(int32_t),
+                       hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return check_hip(e, "tao_prefill route carry");
+  }
+  const int D = st->head_dim;
+  // local attention
+  tao::AttnParams ap;
+  ap.q = view(tok->q, tok->q_s);
+  ap.k = view(tok->k, tok->k_s);
+  ap.v = view(tok->v, tok->v_s);
+  ap.ring_k = (const bf16_t*)st->ring_k;
+  ap.ring_v = (const bf16_t*)st->ring_v;
+  ap.out = (bf16_t*)local;
+  ap.tiles = dplan + off_attn;
+  ap.qpos0 = pos0;
+  ap.kpos0 = pos0;
+  ap.B = st->batch;
+  ap.H = st->heads;
+  ap.L = L;
+  ap.T = T;
+  ap.n_tiles = (int)n_attn;
+  e = tao::launch_local_attention(ap, D, s);
+  if (e != hipSuccess) return check_hip(e, "tao_prefill attention");
+  // writer
+  tao::WriterParams wp;
+  wp.rk = view(tok->raw_k, tok->rk_s);
+  wp.v = view(tok->v, tok->v_s);
+  wp.ring_raw = (const bf16_t*)st->ring_raw;
+  wp.ring_v = (const bf16_t*)st->ring_v;
+  wp.bank = (bf16_t*)st->bank_c;
+  wp.fine_z = (bf16_t*)st->fine_z;
+  wp.starts = dplan + off_write;
+  wp.new_base = pos0;
+  wp.B = st->batch;
+  wp.H = st->heads;
+  wp.L = L;
+  wp.fine_cap = st->fine_cap;
+  wp.first_slot = (int)first_slot;
+  wp.count = (int)n_write;
+  e = tao::launch_writer(wp, D, s);
+  if (e != hipSuccess) return check_hip(e, "tao_prefill writer");
+  // pages
+  tao::PagesParams pp;
+  pp.fine_z = (const bf16_t*)st->fine_z;
+  pp.fine_sw = (bf16_t*)st->fine_sw;
+  pp.page_z = (bf16_t*)st->page_z;
+  pp.B = st->batch;
+  pp.H = st->heads;
+  pp.fine_cap = st->fine_cap;
+  pp.page_cap = st->page_cap;
+  pp.group = G;
+  pp.first_page = (int)first_page;
+  pp.count = (int)n_pages;
+  e = tao::launch_pages(pp, D, s);
+  if (e != hipSuccess) return check_hip(e, "tao_prefill pages");
+  if (need_pools) {
+    tao::EpochParams ep;
+    ep.fine_z = (const bf16_t*)st->fine_z;
+    ep.fine_sw = (bf16_t*)st->fine_sw;
+    ep.page_z = (bf16_t*)st->page_z;
+    ep.page_w = (bf16_t*)st->page_w;
+    ep.pw_pool = (bf16_t*)pools->pw_pool;
+    ep.psw_pool = (bf16_t*)pools->psw_pool;
+    ep.pool_pcap = pools->pool_pcap;
+    ep.B = st->batch;
+    ep.H = st->heads;
+    ep.fine_cap = st->fine_cap;
+    ep.page_cap = st->page_cap;
+    ep.group = G;
+    ep.first_epoch = (int)first_epoch;
+    ep.count = (int)n_epochs;
+    e = tao::launch_epochs(ep, D, s);
+    if (e != hipSuccess) return check_hip(e, "tao_prefill epochs");
+  }
+  if (n_turns) {
+    tao::RouteParams rp = {};
+    rp.rq = (const bf16_t*)tok->raw_q;
+    rp.rq_sb = tok->rq_s[0];
+    rp.rq_st = tok->rq_s[1];
+    rp.rq_sh = tok->rq_s[2];
+    rp.pw = (const bf16_t*)st->page_w;
+    rp.sw = (const bf16_t*)st->fine_sw;
+    rp.pw_pool = (const bf16_t*)pools->pw_pool;
+    rp.psw_pool = (const bf16_t*)pools->psw_pool;
+    rp.pool_pcap = pools->pool_pcap;
+    rp.sel = st->sel;
+    rp.chosen = st->chosen;
+    rp.header = st->header;
+    rp.sel_pool = pools->sel_pool;
+    rp.turns = dplan + off_turns;
+    rp.n_turns = (int)n_turns;
+    rp.B = st->batch;
+    rp.H = st->heads;
+    rp.fine_cap = st->fine_cap;
+    rp.page_cap = st->page_cap;
+    rp.sel_cap = st->sel_cap;
+    rp.chosen_cap = st->chosen_cap;
+    rp.group = G;
+    e = tao::launch_route(rp, D, s);
+    if (e != hipSuccess) return check_hip(e, "tao_prefill routes");
+  }
+  tao::ReadTilesParams rt;
+  rt.rq = view(tok->raw_q, tok->rq_s);
+  rt.bank = (const bf16_t*)st->bank_c;
+  rt.sw = (const bf16_t*)st->fine_sw;
+  rt.pw_pool = need_pools ? (const bf16_t*)pools->pw_pool : nullptr;
+  rt.psw_pool = need_pools ? (const bf16_t*)pools->psw_pool : nullptr;
+  rt.pool_pcap = need_pools ? pools->pool_pcap : 0;
+  rt.sel_pool = need_pools ? pools->sel_pool : nullptr;
+  rt.local = (const bf16_t*)local;
+  rt.fa = fu->fusion_a;
+  rt.fb = fu->fusion_b;
+  rt.f_dtype = fu->dtype;
+  for (int i = 0; i < 3; ++i) { rt.fa_s[i] = fu->a_s[i]; rt.fb_s[i] = fu->b_s[i]; }
+  rt.gain = fu->gain;
+  rt.out = (bf16_t*)out;
+  rt.out_sb = out_s[0];
+  rt.out_st = out_s[1];
+  rt.out_sh = out_s[2];
+  rt.tiles = dplan + off_read;
+  rt.n_tiles = (int)n_read;
+  rt.B = st->batch;
+  rt.H = st->heads;
+  rt.T = T;
+  rt.group = G;
+  rt.fine_cap = st->fine_cap;
+  rt.sel_cap = st->sel_cap;
+  e = tao::launch_read_tiles(rt, D, s);
+  if (e != hipSuccess) return check_hip(e, "tao_prefill read");
+  tao::AppendParams app;
+  app.k = view(tok->k, tok->k_s);
+  app.v = view(tok->v, tok->v_s);
+  app.rk = view(tok->raw_k, tok->rk_s);
+  app.ring_k = (bf16_t*)st->ring_k;
+  app.ring_v = (bf16_t*)st->ring_v;
+  app.ring_raw = (bf16_t*)st->ring_raw;
+  app.B = st->batch;
+  app.H = st->heads;
+  app.D = D;
+  app.L = L;
+  app.first = (int)ring_first;
+  app.count = (int)ring_count;
+  app.pos = pos0 + ring_first;
+  return check_hip(tao::launch_ring_append(app, s), "tao_prefill ring");
 }
 
 int tao_ring_append(const tao_state_dev* st, const tao_tokens* tok, int32_t first,

@@ -1,22 +1,25 @@
 // Fused single-token decode step for gfx950.
 //
-// One launch per new token (replaces, per request x layer, the reference's
+// Two launches per new token (replace, per request x layer, the reference's
 // q1 page-memo region tao_stream.py:418-433 + query_fresh_fine.py:8-75, the
 // local SDPA flash_attention.py:25-29 over torch.cat'ed K/V
 // tao_stream.py:927-930, and the fusion kernels fusion_pointwise.py:10-117):
 //
-//   grid = B*H*(kLocalSplits + M) workgroups of 256 threads
+// decode_units_kernel: B*H*(kLocalSplits + M) independent workgroups
 //   unit <  kLocalSplits : split-K exact local attention over the ring
 //                          (split 0 also appends the new token to the ring)
 //   unit >= kLocalSplits : one selected fine memory: streams its D x D bf16
 //                          matrix from HBM (16-byte loads, 1 KB per wave
-//                          instruction) and contracts it with the bf16
+//                          instruction, all issued before any math; the
+//                          bank stores C^T) and contracts it with the bf16
 //                          channel weights ch = r(r(h*pw[page]) * sw[fine])
-//   last arriving unit of a head: merges the split-K partials, sums the M
-//   fine partials in slot order (deterministic), den = r(sum_m r(sum_d ch)),
-//   fine = r(r(num)/den), then the fusion epilogue writes the output row.
-//   The last head to finish advances header[0] (the stream position), so the
-//   same launch can be replayed from a hipGraph.
+// decode_combine_kernel: one workgroup per (batch, head) merges the split-K
+//   partials, sums the fine partials in a fixed order, den = r(sum_m r(sum_d
+//   ch)) in butterfly order, fine = r(r(num)/den), applies the fusion
+//   epilogue and advances header[0] (the stream position), so the pair can
+//   be replayed from a hipGraph.
+// The kernel boundary publishes the partials across the eight XCD L2
+// caches; no device-scope fences or atomics are needed.
 #include "tao_launch.h"
 #include "tao_common.h"
 #include "tao_fusion.h"
@@ -24,15 +27,15 @@
 namespace tao {
 namespace {
 
-constexpr int kRec = 4;   // header floats per unit record
+constexpr int kRec = 4;         // header floats per unit record
+constexpr int kMaxLocal = 768;  // serve_limit: keys of one step's window
 
 template <int D>
 struct StepSmem {
   float vec[D];                         // query (local units) or ch (fine units)
-  float red[kThreads / (D / 8)][D];     // cross-row partial sums
-  float sc[128];                        // local scores of one split (<= 96)
+  float red[kThreads / (D / 8) > D / 8 ? kThreads / (D / 8) : D / 8][D];  // partial sums
+  float sc[64];                         // local scores of one split (<= 48)
   float misc[4];
-  int last;
 };
 
 TAO_DEV void unpack8(const uint4& u, float out[8]) {
@@ -57,6 +60,7 @@ __device__ void local_unit(const DecodeParams& p, int b, int h, int split,
                            long long position, int n_old, StepSmem<D>& sm,
                            float* rec) {
   constexpr int CH = D / 8, ROWS = kThreads / CH;
+  constexpr int KPT = (kMaxLocal / kLocalSplits + ROWS - 1) / ROWS;   // keys per thread
   const int tid = threadIdx.x, c = tid % CH, r = tid / CH;
   const int L = p.keep + p.fine;
   const int n = n_old + 1;
@@ -67,7 +71,6 @@ __device__ void local_unit(const DecodeParams& p, int b, int h, int split,
 
   const bf16_t* krow_new = p.k.p + b * p.k.sb + h * p.k.sh;
   const bf16_t* vrow_new = p.v.p + b * p.v.sb + h * p.v.sh;
-
   if (split == 0) {
     // Append the new token at slot position % L. No key of this step's
     // window occupies that slot (window length n_old <= L - 1).
@@ -80,63 +83,68 @@ __device__ void local_unit(const DecodeParams& p, int b, int h, int split,
       p.ring_raw[off + d] = rk[d];
     }
   }
-
-  float qv[8];
-  {
-    const bf16_t* qrow = p.q.p + b * p.q.sb + h * p.q.sh;
-    unpack8(*(const uint4*)(qrow + c * 8), qv);
-  }
-  for (int base = j0; base < j1; base += ROWS) {
-    const int j = base + r;
-    const bool valid = j < j1;
-    float part = 0.0f;
-    if (valid) {
+  // Issue every load of this split first: q chunk, KPT key and value rows.
+  uint4 kraw[KPT], vraw[KPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int j = j0 + r + i * ROWS;
+    kraw[i] = make_uint4(0, 0, 0, 0);
+    vraw[i] = make_uint4(0, 0, 0, 0);
+    if (j < j1) {
       const bf16_t* krow;
+      const bf16_t* vrow;
       if (j == n_old) {
         krow = krow_new;
+        vrow = vrow_new;
       } else {
-        const int slot = (int)((first_pos + j) % L);
-        krow = p.ring_k + (((size_t)b * L + slot) * p.H + h) * D;
+        const size_t off = (((size_t)b * L + (int)((first_pos + j) % L)) * p.H + h) * D;
+        krow = p.ring_k + off;
+        vrow = p.ring_v + off;
       }
-      float kv[8];
-      unpack8(*(const uint4*)(krow + c * 8), kv);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) part = fmaf(qv[i], kv[i], part);
+      kraw[i] = *(const uint4*)(krow + c * 8);
+      vraw[i] = *(const uint4*)(vrow + c * 8);
     }
-    part = group_sum<CH>(part);
-    if (valid && c == 0) sm.sc[j - j0] = part * scale;
+  }
+  float qv[8];
+  unpack8(*(const uint4*)(p.q.p + b * p.q.sb + h * p.q.sh + c * 8), qv);
+  float score[KPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    float kv[8];
+    unpack8(kraw[i], kv);
+    float part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part = fmaf(qv[e], kv[e], part);
+    score[i] = group_sum<CH>(part) * scale;
+    const int j = j0 + r + i * ROWS;
+    if (j < j1 && c == 0) sm.sc[j - j0] = score[i];
   }
   __syncthreads();
   const int cnt = j1 - j0;
   if (tid < 64) {
-    float a = tid < cnt ? sm.sc[tid] : -__builtin_inff();
-    float bb = tid + 64 < cnt ? sm.sc[tid + 64] : -__builtin_inff();
-    float top = wave_max(fmaxf(a, bb));
-    float e = (tid < cnt ? __expf(a - top) : 0.0f) + (tid + 64 < cnt ? __expf(bb - top) : 0.0f);
-    e = wave_sum_fold(e);
+    const float a = tid < cnt ? sm.sc[tid] : -__builtin_inff();
+    const float top = wave_max(a);
+    const float e = wave_sum_fold(tid < cnt ? __expf(a - top) : 0.0f);
     if (tid == 0) { sm.misc[0] = top; sm.misc[1] = e; }
   }
   __syncthreads();
   const float top = sm.misc[0];
   float acc[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  for (int j = j0 + r; j < j1; j += ROWS) {
-    const float w = __expf(sm.sc[j - j0] - top);
-    const bf16_t* vrow;
-    if (j == n_old) {
-      vrow = vrow_new;
-    } else {
-      const int slot = (int)((first_pos + j) % L);
-      vrow = p.ring_v + (((size_t)b * L + slot) * p.H + h) * D;
-    }
-    float vv[8];
-    unpack8(*(const uint4*)(vrow + c * 8), vv);
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = fmaf(w, vv[i], acc[i]);
+  for (int i = 0; i < KPT; ++i) {
+    const int j = j0 + r + i * ROWS;
+    if (j < j1) {
+      const float w = __expf(score[i] - top);
+      float vv[8];
+      unpack8(vraw[i], vv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, vv[e], acc[e]);
+    }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) sm.red[r][c * 8 + i] = acc[i];
+  for (int e = 0; e < 8; ++e) sm.red[r][c * 8 + e] = acc[e];
   __syncthreads();
   if (tid < D) {
     float s = 0.0f;
@@ -169,15 +177,19 @@ __device__ void fine_unit(const DecodeParams& p, int b, int h, int m,
     const bf16_t* rq = p.rq.p + b * p.rq.sb + h * p.rq.sh;
     const bf16_t* pw = p.pw + ((size_t)bh * p.page_cap + page) * D;
     const bf16_t* sw = p.sw + ((size_t)bh * p.fine_cap + id) * D;
-    float x[PER], e[PER];
+    float x[PER], pwv[PER], swv[PER], e[PER];
     float top = -__builtin_inff();
 #pragma unroll
-    for (int k = 0; k < PER; ++k) { x[k] = bf2f(rq[tid + 64 * k]); top = fmaxf(top, x[k]); }
+    for (int k = 0; k < PER; ++k) {
+      x[k] = bf2f(rq[tid + 64 * k]);
+      pwv[k] = bf2f(pw[tid + 64 * k]);
+      swv[k] = bf2f(sw[tid + 64 * k]);
+      top = fmaxf(top, x[k]);
+    }
     top = wave_max(top);
-    float s = 0.0f;
 #pragma unroll
     for (int k = 0; k < PER; ++k) e[k] = exp_cr(x[k] - top);
-    s = e[0];
+    float s = e[0];
 #pragma unroll
     for (int k = 1; k < PER; ++k) s += e[k];   // PER <= 2: fold of the lane pair
     s = wave_sum_fold(s);
@@ -186,8 +198,8 @@ __device__ void fine_unit(const DecodeParams& p, int b, int h, int m,
     for (int k = 0; k < PER; ++k) {
       const int d = tid + 64 * k;
       const float hq = rbf(e[k] / s);
-      const float hv = rbf(hq * bf2f(pw[d]));
-      const float ch = rbf(hv * bf2f(sw[d]));
+      const float hv = rbf(hq * pwv[k]);
+      const float ch = rbf(hv * swv[k]);
       sm.vec[d] = ch;
       csum = k == 0 ? ch : csum + ch;
     }
@@ -195,122 +207,143 @@ __device__ void fine_unit(const DecodeParams& p, int b, int h, int m,
     if (tid == 0) sm.misc[0] = rbf(csum);
   }
   __syncthreads();
-  float acc[8];
+  // Bank rows are C^T[e][d]: this thread holds d in [8c, 8c + 8) of rows
+  // e = r + i * ROWS; partial dots are summed over the CH chunks in LDS.
+  float chv[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  for (int k = 0; k < 8; ++k) chv[k] = sm.vec[c * 8 + k];
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
-    const float w = sm.vec[r + i * ROWS];
     float cf[8];
     unpack8(cv[i], cf);
+    float part = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) acc[k] = fmaf(w, cf[k], acc[k]);
+    for (int k = 0; k < 8; ++k) part = fmaf(chv[k], cf[k], part);
+    sm.red[c][r + i * ROWS] = part;
   }
-#pragma unroll
-  for (int k = 0; k < 8; ++k) sm.red[r][c * 8 + k] = acc[k];
   __syncthreads();
   if (tid < D) {
     float s = 0.0f;
-    for (int rr = 0; rr < ROWS; ++rr) s += sm.red[rr][tid];
+    for (int cc = 0; cc < CH; ++cc) s += sm.red[cc][tid];
     rec[kRec + tid] = s;
   }
   if (tid == 0) rec[0] = sm.misc[0];
 }
 
+// Kernel A: independent units, no cross-workgroup communication.
 template <int D>
-__device__ void combine(const DecodeParams& p, int b, int h, int M,
-                        StepSmem<D>& sm, const float* recs) {
-  constexpr int STRIDE = D + kRec;
-  const int tid = threadIdx.x;
-  if (M > 0 && tid < 64) {
-    // den = r(sum over slots of r(sum_d ch)), butterfly order over slots.
-    float v = 0.0f;
-    int slots = 64;
-    while (slots < M) slots *= 2;
-    float vals[8];
-    const int per_lane = slots / 64;
-    for (int k = 0; k < per_lane && k < 8; ++k) {
-      const int m = tid + 64 * k;
-      vals[k] = m < M ? recs[(kLocalSplits + m) * STRIDE] : 0.0f;
-    }
-    for (int width = per_lane; width > 1; width /= 2)
-      for (int k = 0; k < width / 2; ++k) vals[k] += vals[k + width / 2];
-    v = wave_sum_fold(vals[0]);
-    if (tid == 0) sm.misc[2] = rbf(v);
-  }
-  __syncthreads();
-  if (tid < D) {
-    float top = -__builtin_inff();
-    for (int s = 0; s < kLocalSplits; ++s) {
-      const float* rs = recs + s * STRIDE;
-      if (rs[1] > 0.0f) top = fmaxf(top, rs[0]);
-    }
-    float num = 0.0f, den = 0.0f;
-    for (int s = 0; s < kLocalSplits; ++s) {
-      const float* rs = recs + s * STRIDE;
-      if (rs[1] > 0.0f) {
-        const float w = __expf(rs[0] - top);
-        den = fmaf(w, rs[1], den);
-        num = fmaf(w, rs[kRec + tid], num);
-      }
-    }
-    const float local = rbf(num / den);
-    bf16_t result;
-    if (M > 0) {
-      float acc = 0.0f;
-      for (int m = 0; m < M; ++m) acc += recs[(kLocalSplits + m) * STRIDE + kRec + tid];
-      const float fine = rbf(rbf(acc) / sm.misc[2]);
-      const float q = bf2f(p.rq.p[b * p.rq.sb + h * p.rq.sh + tid]);
-      float a[3], bb[3];
-#pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        a[i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + tid * p.fa_s[1] + i * p.fa_s[2]);
-        bb[i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + tid * p.fb_s[1] + i * p.fb_s[2]);
-      }
-      result = fuse_element(q, local, 0.0f, fine, a, bb, p.gain, 0, 1);
-    } else {
-      result = f2bf(local);
-    }
-    p.out[b * p.out_sb + h * p.out_sh + tid] = result;
-  }
-}
-
-template <int D>
-__global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, int M) {
+__global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, int M) {
   __shared__ StepSmem<D> sm;
   const int units = kLocalSplits + M;
   const int bh = blockIdx.x / units;
   const int unit = blockIdx.x % units;
   const int b = bh / p.H, h = bh % p.H;
   float* recs = p.parts + (size_t)bh * (kLocalSplits + p.sel_cap) * (D + kRec);
-  const long long position = p.header[0];
   if (unit < kLocalSplits) {
+    const long long position = p.header[0];
     const int n_old = local_len_at(position, p.keep, p.fine);
     local_unit<D>(p, b, h, unit, position, n_old, sm, recs + unit * (D + kRec));
   } else {
     fine_unit<D>(p, b, h, unit - kLocalSplits, sm, recs + unit * (D + kRec));
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(&p.counters[bh], 1u);
-    sm.last = prev == (unsigned)(units - 1);
+}
+
+// Kernel B: one workgroup per (batch, head). Thread group g = tid / D owns
+// local splits s = g (mod G) and fine slots m = g (mod G); groups merge in
+// ascending g, so the summation order is fixed.
+template <int D>
+__global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p, int M) {
+  constexpr int STRIDE = D + kRec, G = kThreads / D;
+  __shared__ float part_num[G][D], part_loc[G][D], part_den[G];
+  __shared__ float den_fine;
+  const int bh = blockIdx.x;
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, d = tid % D, g = tid / D;
+  const float* recs = p.parts + (size_t)bh * (kLocalSplits + p.sel_cap) * STRIDE;
+
+  float mrec[kLocalSplits], lrec[kLocalSplits];
+#pragma unroll
+  for (int s = 0; s < kLocalSplits; ++s) {
+    mrec[s] = recs[s * STRIDE];
+    lrec[s] = recs[s * STRIDE + 1];
   }
-  __syncthreads();
-  if (!sm.last) return;
-  __threadfence();
-  combine<D>(p, b, h, M, sm, recs);
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    atomicExch(&p.counters[bh], 0u);
-    const unsigned total = (unsigned)(p.B * p.H);
-    const unsigned prev = atomicAdd(&p.counters[total], 1u);
-    if (prev == total - 1) {
-      atomicExch(&p.counters[total], 0u);
-      atomicAdd((unsigned long long*)&p.header[0], 1ull);
+  float accl[kLocalSplits / G];
+#pragma unroll
+  for (int i = 0; i < kLocalSplits / G; ++i) accl[i] = recs[(g + i * G) * STRIDE + kRec + d];
+  float top = -__builtin_inff();
+#pragma unroll
+  for (int s = 0; s < kLocalSplits; ++s)
+    if (lrec[s] > 0.0f) top = fmaxf(top, mrec[s]);
+  float num_l = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kLocalSplits / G; ++i) {
+    const int s = g + i * G;
+    if (lrec[s] > 0.0f) num_l = fmaf(__expf(mrec[s] - top), accl[i], num_l);
+  }
+  part_loc[g][d] = num_l;
+  if (tid == 0) {
+    float den = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kLocalSplits; ++s)
+      if (lrec[s] > 0.0f) den = fmaf(__expf(mrec[s] - top), lrec[s], den);
+    part_den[0] = den;
+  }
+  // fine numerator partial sums and the slot-fold denominator
+  float num_f = 0.0f;
+  {
+    const float* base = recs + (size_t)kLocalSplits * STRIDE + kRec + d;
+    int m = g;
+    for (; m + 3 * G < M; m += 4 * G) {
+      const float a0 = base[(size_t)m * STRIDE];
+      const float a1 = base[(size_t)(m + G) * STRIDE];
+      const float a2 = base[(size_t)(m + 2 * G) * STRIDE];
+      const float a3 = base[(size_t)(m + 3 * G) * STRIDE];
+      num_f = num_f + a0;
+      num_f = num_f + a1;
+      num_f = num_f + a2;
+      num_f = num_f + a3;
     }
+    for (; m < M; m += G) num_f = num_f + base[(size_t)m * STRIDE];
   }
+  part_num[g][d] = num_f;
+  if (M > 0 && tid < 64) {
+    int slots = 64;
+    while (slots < M) slots *= 2;
+    const int per_lane = slots / 64;
+    float vals[8];
+    for (int k = 0; k < 8; ++k) {
+      const int m = tid + 64 * k;
+      vals[k] = (k < per_lane && m < M) ? recs[(kLocalSplits + m) * STRIDE] : 0.0f;
+    }
+    for (int width = per_lane; width > 1; width /= 2)
+      for (int k = 0; k < width / 2; ++k) vals[k] += vals[k + width / 2];
+    const float v = wave_sum_fold(vals[0]);
+    if (tid == 0) den_fine = rbf(v);
+  }
+  __syncthreads();
+  if (tid < D) {
+    float nl = 0.0f, nf = 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) { nl += part_loc[gg][d]; nf += part_num[gg][d]; }
+    const float local = rbf(nl / part_den[0]);
+    bf16_t result;
+    if (M > 0) {
+      const float fine = rbf(rbf(nf) / den_fine);
+      const float q = bf2f(p.rq.p[b * p.rq.sb + h * p.rq.sh + d]);
+      float a[3], bb[3];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        a[i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + d * p.fa_s[1] + i * p.fa_s[2]);
+        bb[i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + d * p.fb_s[1] + i * p.fb_s[2]);
+      }
+      result = fuse_element(q, local, 0.0f, fine, a, bb, p.gain, 0, 1);
+    } else {
+      result = f2bf(local);
+    }
+    p.out[b * p.out_sb + h * p.out_sh + d] = result;
+  }
+  // Kernel A of this step has finished reading the position: advance it.
+  if (bh == 0 && tid == 0) p.header[0] = p.header[0] + 1;
 }
 
 __global__ __launch_bounds__(kThreads) void stage_tokens_kernel(StageParams p) {
@@ -342,13 +375,17 @@ __global__ __launch_bounds__(kThreads) void ring_append_kernel(AppendParams p) {
 }  // namespace
 
 hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStream_t s) {
-  const dim3 grid((unsigned)(p.B * p.H * (kLocalSplits + M)));
-  if (head_dim == 128)
-    hipLaunchKernelGGL(decode_step_kernel<128>, grid, dim3(kThreads), 0, s, p, M);
-  else if (head_dim == 64)
-    hipLaunchKernelGGL(decode_step_kernel<64>, grid, dim3(kThreads), 0, s, p, M);
-  else
+  const dim3 units((unsigned)(p.B * p.H * (kLocalSplits + M)));
+  const dim3 heads((unsigned)(p.B * p.H));
+  if (head_dim == 128) {
+    hipLaunchKernelGGL(decode_units_kernel<128>, units, dim3(kThreads), 0, s, p, M);
+    hipLaunchKernelGGL(decode_combine_kernel<128>, heads, dim3(kThreads), 0, s, p, M);
+  } else if (head_dim == 64) {
+    hipLaunchKernelGGL(decode_units_kernel<64>, units, dim3(kThreads), 0, s, p, M);
+    hipLaunchKernelGGL(decode_combine_kernel<64>, heads, dim3(kThreads), 0, s, p, M);
+  } else {
     return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -9,8 +9,10 @@
 //   mass_j = r(sum_D r(hv_page(j) * sw_j)); stable top-M candidates kept in
 //   score order.
 // Every fp32 sum uses the butterfly order of the oracle, so selected ids are
-// bit-identical to the oracle's. Sorting: 64-bit keys
-// (monotone bf16 score << 32 | ~index) in an LDS bitonic network.
+// bit-identical to the oracle's. Selection: 64-bit keys (monotone bf16 score
+// << 32 | ~index) ranked by counting (<= 512 keys) or an LDS bitonic network.
+// Eight waves issue the loads of eight rows each before reducing them, so a
+// refresh costs a few memory latencies rather than one per row.
 #include "tao_launch.h"
 #include "tao_common.h"
 
@@ -28,24 +30,10 @@ struct RouteSmem {
   int chosen[kMaxSort / 8];
 };
 
-__device__ void bitonic_desc(unsigned long long* keys, int n) {
-  for (int k = 2; k <= n; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < n; i += kThreads) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const unsigned long long a = keys[i], b = keys[ixj];
-          const bool first_half_desc = (i & k) == 0;
-          if (first_half_desc ? (a < b) : (a > b)) { keys[i] = b; keys[ixj] = a; }
-        }
-      }
-      __syncthreads();
-    }
-  }
-}
-
 TAO_DEV unsigned long long score_key(float score_bf, int index) {
-  const uint32_t hi = bf16_order_key(f2bf(score_bf));
+  bf16_t bits = f2bf(score_bf);
+  if (bits == 0x8000) bits = 0;      // -0 ties with +0, as in torch's sort
+  const uint32_t hi = bf16_order_key(bits);
   return ((unsigned long long)hi << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)index);
 }
 
@@ -53,42 +41,129 @@ TAO_DEV int key_index(unsigned long long key) {
   return (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
 }
 
-// r(sum_D r(h * pw[page]) * (sw row or 1)) computed by one wave.
-template <int D>
-TAO_DEV float wave_mass(const float* h, const bf16_t* pw_row, const bf16_t* sw_row, int lane) {
-  constexpr int PER = D / 64;
-  float v[PER];
-#pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int d = lane + 64 * k;
-    float hv = rbf(h[d] * bf2f(pw_row[d]));
-    v[k] = sw_row ? rbf(hv * bf2f(sw_row[d])) : hv;
+constexpr int kRouteThreads = 512;   // 8 waves
+constexpr int kWaves = kRouteThreads / 64;
+constexpr int kBatch = 8;            // rows whose loads one wave issues together
+constexpr int kRankMax = 512;        // rank-count selection up to this many keys
+
+// Masses of up to kBatch rows per wave: every lane loads its two (or one)
+// channels of all rows first, then each row is reduced in butterfly order:
+// r(sum_D r(h * pw[page]) [* sw[id]]).
+// Segment-weight rows: fines below `split` read the state's final weights,
+// later (pending) fines read the epoch's pool rows.
+struct SwRows {
+  const bf16_t* lo; const bf16_t* hi; int split;
+  TAO_DEV const bf16_t* row(int id, int D) const {
+    return id < split ? lo + (size_t)id * D : hi + (size_t)(id - split) * D;
   }
-  float s = v[0];
+};
+
+template <int D>
+TAO_DEV void wave_masses(const float* h, const bf16_t* pw, const SwRows* sw,
+                         const int* pages, const int* ids, int count, int lane,
+                         float* out) {
+  constexpr int PER = D / 64;
+  bf16_t pv[kBatch][PER], sv[kBatch][PER];
 #pragma unroll
-  for (int k = 1; k < PER; ++k) s += v[k];
-  return rbf(wave_sum_fold(s));
+  for (int r = 0; r < kBatch; ++r) {
+    if (r < count) {
+      const bf16_t* srow = sw ? sw->row(ids[r], D) : nullptr;
+#pragma unroll
+      for (int k = 0; k < PER; ++k) {
+        pv[r][k] = pw[(size_t)pages[r] * D + lane + 64 * k];
+        sv[r][k] = sw ? srow[lane + 64 * k] : (bf16_t)0;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kBatch; ++r) {
+    if (r < count) {
+      float v[PER];
+#pragma unroll
+      for (int k = 0; k < PER; ++k) {
+        const float hv = rbf(h[lane + 64 * k] * bf2f(pv[r][k]));
+        v[k] = sw ? rbf(hv * bf2f(sv[r][k])) : hv;
+      }
+      float s = v[0];
+#pragma unroll
+      for (int k = 1; k < PER; ++k) s += v[k];
+      out[r] = rbf(wave_sum_fold(s));
+    }
+  }
+}
+
+// Stable descending selection of the top `count` keys (unique 64-bit keys:
+// score << 32 | ~index). Writes the selected keys, best first, to dst.
+__device__ void select_top(unsigned long long* keys, int n, int count,
+                           unsigned long long* dst) {
+  if (n <= kRankMax) {
+    for (int i = threadIdx.x; i < n; i += kRouteThreads) {
+      const unsigned long long mine = keys[i];
+      int rank = 0;
+      for (int j = 0; j < n; ++j) rank += keys[j] > mine;
+      if (rank < count) dst[rank] = mine;
+    }
+    __syncthreads();
+    return;
+  }
+  int np = 1;
+  while (np < n) np <<= 1;
+  for (int i = n + threadIdx.x; i < np; i += kRouteThreads) keys[i] = 0ull;
+  __syncthreads();
+  for (int k = 2; k <= np; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < np; i += kRouteThreads) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const unsigned long long a = keys[i], b = keys[ixj];
+          const bool desc = (i & k) == 0;
+          if (desc ? (a < b) : (a > b)) { keys[i] = b; keys[ixj] = a; }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = threadIdx.x; i < count; i += kRouteThreads) dst[i] = keys[i];
+  __syncthreads();
 }
 
 template <int D>
-__global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteParams p) {
   __shared__ RouteSmem<D> sm;
+  __shared__ unsigned long long top[kMaxSort];
   constexpr int PER = D / 64;
-  const int bh = blockIdx.x;
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // Turn description (single-turn mode: the state's current epoch).
+  long long anchor = 0;
+  int K = p.completed, pending = p.pending, coarse = p.coarse, selected = p.selected;
+  int write_state = 1;
+  int32_t* sel_out = p.sel + (size_t)bh * p.sel_cap;
   const bf16_t* pw = p.pw + (size_t)bh * p.page_cap * D;
-  const bf16_t* sw = p.sw + (size_t)bh * p.fine_cap * D;
+  SwRows swr{p.sw + (size_t)bh * p.fine_cap * D, nullptr, 0x7FFFFFFF};
+  if (p.turns) {
+    const int64_t* t = p.turns + 8 * (blockIdx.x / BH);
+    anchor = t[0];
+    const int erel = (int)t[1];
+    K = (int)t[2]; pending = (int)t[3]; coarse = (int)t[4]; selected = (int)t[5];
+    sel_out = p.sel_pool + ((size_t)t[6] * BH + bh) * p.sel_cap;
+    write_state = (int)t[7];
+    pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
+    swr.hi = p.psw_pool + ((size_t)erel * BH + bh) * 8 * D;
+    swr.split = K * p.group;
+  }
 
   if (wave == 0) {
-    const bf16_t* rq = p.rq + b * p.rq_sb + h * p.rq_sh;
+    const bf16_t* rq = p.rq + b * p.rq_sb + anchor * p.rq_st + h * p.rq_sh;
     float x[PER], e[PER];
-    float top = -__builtin_inff();
+    float mx = -__builtin_inff();
 #pragma unroll
-    for (int k = 0; k < PER; ++k) { x[k] = bf2f(rq[lane + 64 * k]); top = fmaxf(top, x[k]); }
-    top = wave_max(top);
+    for (int k = 0; k < PER; ++k) { x[k] = bf2f(rq[lane + 64 * k]); mx = fmaxf(mx, x[k]); }
+    mx = wave_max(mx);
 #pragma unroll
-    for (int k = 0; k < PER; ++k) e[k] = exp_cr(x[k] - top);
+    for (int k = 0; k < PER; ++k) e[k] = exp_cr(x[k] - mx);
     float s = e[0];
 #pragma unroll
     for (int k = 1; k < PER; ++k) s += e[k];
@@ -98,61 +173,78 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
   }
   __syncthreads();
 
-  // ---- coarse pages
-  const int K = p.completed;
-  if (p.coarse > 0) {
-    int np = 1;
-    while (np < K) np <<= 1;
-    for (int i = tid; i < np; i += kThreads) sm.keys[i] = 0ull;
-    __syncthreads();
-    for (int page = wave; page < K; page += kThreads / 64) {
-      const float mass = wave_mass<D>(sm.h, pw + (size_t)page * D, nullptr, lane);
-      if (lane == 0) sm.keys[page] = score_key(mass, page);
+  // ---- coarse pages: stable top-`coarse` by page mass, then ascending.
+  if (coarse > 0) {
+    for (int base = wave * kBatch; base < K; base += kWaves * kBatch) {
+      int pages[kBatch];
+      float mass[kBatch];
+      const int count = min(kBatch, K - base);
+#pragma unroll
+      for (int r = 0; r < kBatch; ++r) pages[r] = base + min(r, count - 1);
+      wave_masses<D>(sm.h, pw, nullptr, pages, pages, count, lane, mass);
+      if (lane < count) {
+        float mine = mass[0];
+#pragma unroll
+        for (int r = 1; r < kBatch; ++r) if (lane == r) mine = mass[r];
+        sm.keys[base + lane] = score_key(mine, base + lane);
+      }
     }
     __syncthreads();
-    bitonic_desc(sm.keys, np);
-    // chosen pages ascending: rank among the top `coarse`.
-    if (tid < p.coarse) {
-      const int mine = key_index(sm.keys[tid]);
+    select_top(sm.keys, K, coarse, top);
+    if (tid < coarse) {
+      const int mine = key_index(top[tid]);
       int rank = 0;
-      for (int j = 0; j < p.coarse; ++j) rank += key_index(sm.keys[j]) < mine;
+      for (int j = 0; j < coarse; ++j) rank += key_index(top[j]) < mine;
       sm.chosen[rank] = mine;
     }
     __syncthreads();
   }
 
-  // ---- candidates
+  // ---- candidates: 8 fines of each chosen page, then the pending fines.
   const int group = p.group;
-  const int E = group * p.coarse + p.pending;
-  for (int j = tid; j < E; j += kThreads) {
+  const int E = group * coarse + pending;
+  for (int j = tid; j < E; j += kRouteThreads) {
     int page, id;
-    if (j < group * p.coarse) {
+    if (j < group * coarse) {
       page = sm.chosen[j / group];
       id = page * group + j % group;
     } else {
       page = K;
-      id = K * group + (j - group * p.coarse);
+      id = K * group + (j - group * coarse);
     }
     sm.cand_page[j] = page;
     sm.cand_id[j] = id;
   }
-  int ne = 1;
-  while (ne < E) ne <<= 1;
   __syncthreads();
-  for (int i = tid; i < ne; i += kThreads) sm.keys[i] = 0ull;
-  __syncthreads();
-  for (int j = wave; j < E; j += kThreads / 64) {
-    const float mass = wave_mass<D>(sm.h, pw + (size_t)sm.cand_page[j] * D,
-                                    sw + (size_t)sm.cand_id[j] * D, lane);
-    if (lane == 0) sm.keys[j] = score_key(mass, j);
+  for (int base = wave * kBatch; base < E; base += kWaves * kBatch) {
+    int pages[kBatch], ids[kBatch];
+    float mass[kBatch];
+    const int count = min(kBatch, E - base);
+#pragma unroll
+    for (int r = 0; r < kBatch; ++r) {
+      const int j = base + min(r, count - 1);
+      pages[r] = sm.cand_page[j];
+      ids[r] = sm.cand_id[j];
+    }
+    wave_masses<D>(sm.h, pw, &swr, pages, ids, count, lane, mass);
+    if (lane < count) {
+      float mine = mass[0];
+#pragma unroll
+      for (int r = 1; r < kBatch; ++r) if (lane == r) mine = mass[r];
+      sm.keys[base + lane] = score_key(mine, base + lane);
+    }
   }
   __syncthreads();
-  bitonic_desc(sm.keys, ne);
-  for (int m = tid; m < p.selected; m += kThreads)
-    p.sel[(size_t)bh * p.sel_cap + m] = sm.cand_id[key_index(sm.keys[m])];
-  for (int i = tid; i < p.coarse; i += kThreads)
-    p.chosen[(size_t)bh * p.chosen_cap + i] = sm.chosen[i];
-  if (bh == 0 && tid == 0) p.header[1] = p.selected;
+  select_top(sm.keys, E, selected, top);
+  for (int m = tid; m < selected; m += kRouteThreads) {
+    const int id = sm.cand_id[key_index(top[m])];
+    sel_out[m] = id;
+    if (write_state && p.turns) p.sel[(size_t)bh * p.sel_cap + m] = id;
+  }
+  if (write_state)
+    for (int i = tid; i < coarse; i += kRouteThreads)
+      p.chosen[(size_t)bh * p.chosen_cap + i] = sm.chosen[i];
+  if (write_state && bh == 0 && tid == 0) p.header[1] = selected;
 }
 
 }  // namespace
@@ -160,11 +252,11 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
 hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s) {
   if (p.completed > kMaxSort || p.group * p.coarse + p.pending > kMaxSort)
     return hipErrorInvalidValue;
-  const dim3 grid((unsigned)(p.B * p.H));
+  const dim3 grid((unsigned)(p.B * p.H * (p.turns ? p.n_turns : 1)));
   if (head_dim == 128)
-    hipLaunchKernelGGL(route_kernel<128>, grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL(route_kernel<128>, grid, dim3(kRouteThreads), 0, s, p);
   else if (head_dim == 64)
-    hipLaunchKernelGGL(route_kernel<64>, grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL(route_kernel<64>, grid, dim3(kRouteThreads), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -80,3 +80,18 @@ TAO_DEV int local_len_at(long long position, int keep, int fine) {
   if (position < limit) return (int)position;
   return keep + (int)((position - limit) % fine);
 }
+
+// Page descriptor of n <= 8 fine descriptors of one channel: torch's bf16
+// logsumexp composite r(r(log r(sum r(exp r(z - m)))) + m), butterfly sum,
+// infinite maximum replaced by 0 (tao_stream.py:283, 412, 485).
+TAO_DEV float group_logsumexp(const float z[8], int n) {
+  float m = -__builtin_inff();
+  for (int i = 0; i < n; ++i) m = fmaxf(m, z[i]);
+  if (__builtin_isinf(m)) m = 0.0f;
+  float e[8];
+  for (int i = 0; i < 8; ++i) e[i] = i < n ? exp_bf(rbf(z[i] - m)) : 0.0f;
+  for (int w = 4; w >= 1; w >>= 1)
+    for (int i = 0; i < w; ++i) e[i] += e[i + w];
+  return rbf(log_bf(rbf(e[0])) + m);
+}
+

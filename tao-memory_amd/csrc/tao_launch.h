@@ -11,18 +11,17 @@
 namespace tao {
 
 constexpr int kThreads = 256;   // 4 wave64 per workgroup
-constexpr int kLocalSplits = 8; // split-K factor of single-query local attention
+constexpr int kLocalSplits = 16; // split-K factor of single-query local attention
 
 // Workspace layout (bytes from the start of tao_state_dev::workspace):
-//   [0, counters)         uint32 arrival counters: B*H per-head + 1 global
-//   [parts_off, ...)      fp32 unit records [B*H][kLocalSplits + sel_cap][D + 4]
-//   [tiles_off, ...)      int64 tile descriptors for multi-token kernels
+//   [0, plan_off)         fp32 decode unit records [B*H][kLocalSplits + sel_cap][D + 4]
+//   [plan_off, total)     int64 prefill plan (plan_words)
 struct WorkspaceLayout {
-  size_t counters_off, parts_off, tiles_off, tiles_cap, total;
+  size_t parts_off, plan_off, plan_words, total;
 };
 
 WorkspaceLayout workspace_layout(int batch, int heads, int head_dim, int sel_cap,
-                                 int max_query_tokens);
+                                 int plan_words);
 
 // Per-tensor [B, T, H, D] view in elements.
 struct TokView {
@@ -62,10 +61,18 @@ struct AppendParams {
 };
 hipError_t launch_ring_append(const AppendParams& p, hipStream_t s);
 
+// One route refresh. Single-turn mode (turns == nullptr) routes the anchor
+// row rq against the state's current epoch. Turn mode: workgroup
+// (turn, b, h) reads turns[turn * 8 + ...] = {anchor token, epoch, completed,
+// pending, coarse, selected, output slot, write_state} and takes its page
+// weights and pending-fine segment weights from the epoch pools.
 struct RouteParams {
-  const bf16_t* rq; int64_t rq_sb, rq_sh;
+  const bf16_t* rq; int64_t rq_sb, rq_st, rq_sh;
   const bf16_t* pw; const bf16_t* sw;
+  const bf16_t* pw_pool; const bf16_t* psw_pool; int pool_pcap;
   int32_t* sel; int32_t* chosen; int64_t* header;
+  int32_t* sel_pool;
+  const int64_t* turns; int n_turns;
   int B, H, fine_cap, page_cap, sel_cap, chosen_cap, group;
   int completed, pending, coarse, selected;
 };
@@ -99,17 +106,42 @@ struct AttnParams {
 };
 hipError_t launch_local_attention(const AttnParams& p, int head_dim, hipStream_t s);
 
-struct ReadParams {
+// Completed pages of a prefill call: page descriptors and final segment
+// weights of pages [first_page, first_page + count).
+struct PagesParams {
+  const bf16_t* fine_z; bf16_t* fine_sw; bf16_t* page_z;
+  int B, H, fine_cap, page_cap, group, first_page, count;
+};
+hipError_t launch_pages(const PagesParams& p, int head_dim, hipStream_t s);
+
+// Seal epochs [first_epoch, first_epoch + count) of a prefill call (epoch =
+// number of visible fines): pending summary, pending segment weights and
+// page weights into the pools; the last epoch is also published to the state.
+struct EpochParams {
+  const bf16_t* fine_z; bf16_t* fine_sw; bf16_t* page_z; bf16_t* page_w;
+  bf16_t* pw_pool; bf16_t* psw_pool; int pool_pcap;
+  int B, H, fine_cap, page_cap, group, first_epoch, count;
+};
+hipError_t launch_epochs(const EpochParams& p, int head_dim, hipStream_t s);
+
+// MFMA selected read + fusion over query tiles (<= 32 queries sharing one
+// route). tiles[t * 8 + ...] = {first query, count, route slot, selected,
+// epoch, sw split, fine_on, 0}.
+struct ReadTilesParams {
   TokView rq;
-  const bf16_t* bank; const bf16_t* sw; const bf16_t* pw;
-  const int32_t* sel;
+  const bf16_t* bank; const bf16_t* sw;
+  const bf16_t* pw_pool; const bf16_t* psw_pool; int pool_pcap;
+  const int32_t* sel_pool;
   const bf16_t* local;           // [B, T, H, D] contiguous
   const void* fa; const void* fb; int f_dtype;
   int64_t fa_s[3], fb_s[3];
-  float gain; int coarse_on, fine_on;
+  float gain;
   bf16_t* out; int64_t out_sb, out_st, out_sh;
-  int B, H, T, first, count, selected, group, fine_cap, page_cap, sel_cap;
+  const int64_t* tiles; int n_tiles;
+  int B, H, T, group, fine_cap, sel_cap;
 };
-hipError_t launch_read_fuse(const ReadParams& p, int head_dim, hipStream_t s);
+hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t s);
+
+
 
 }  // namespace tao

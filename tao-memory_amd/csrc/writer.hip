@@ -5,8 +5,10 @@
 //   per channel d: m = max_t k, e = r(exp(r(k - m))), Z = r(sum_t e),
 //   P = r(e / Z), z = r(m + r(log Z)); C = r(P^T V) with fp32 accumulation.
 // raw_k and V are staged transposed in LDS ([channel][token], token
-// contiguous) so both MFMA operands are 16-byte LDS reads; C = P^T V runs on
-// v_mfma_f32_32x32x16_bf16 (each wave owns 32 rows of C). The token sum uses
+// contiguous) so both MFMA operands are 16-byte LDS reads; C^T = V^T P runs
+// on v_mfma_f32_32x32x16_bf16 (each wave owns 32 rows of C^T). The bank keeps
+// C^T[e][d] so the contraction index d is contiguous for every reader. The
+// token sum uses
 // the oracle's order: four 64-token quarters summed sequentially, then
 // (q0+q1)+(q2+q3). C goes straight into its bank slot: no repack.
 //
@@ -150,7 +152,8 @@ __global__ __launch_bounds__(kThreads) void writer_kernel(WriterParams p) {
   }
   __syncthreads();
 
-  // ---- C = P^T V on MFMA 32x32x16: wave w owns rows [32w', ...) of C.
+  // ---- C^T = V^T P on MFMA 32x32x16 (the bank stores C^T[e][d], d
+  // contiguous): wave w owns rows e in [32w, 32w + 32) of C^T.
   const int lane = tid & 63, wave = tid >> 6;
   const int li = lane & 31, lk = (lane >> 5) * 8;
   constexpr int TILES = D / 32;                 // 32-wide tiles per dimension
@@ -162,14 +165,14 @@ __global__ __launch_bounds__(kThreads) void writer_kernel(WriterParams p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[ct][i] = 0.0f;
     for (int k0 = 0; k0 < kBlock; k0 += 16) {
-      const bf16x8 a = *(const bf16x8*)&sm.kt[rt * 32 + li][k0 + lk];
+      const bf16x8 a = *(const bf16x8*)&sm.vt[rt * 32 + li][k0 + lk];
 #pragma unroll
       for (int ct = 0; ct < TILES; ++ct) {
-        const bf16x8 bv = *(const bf16x8*)&sm.vt[ct * 32 + li][k0 + lk];
+        const bf16x8 bv = *(const bf16x8*)&sm.kt[ct * 32 + li][k0 + lk];
         acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bv, acc[ct], 0, 0, 0);
       }
     }
-    // D layout: lane holds column li, rows 8*(i/4) + 4*(lane/32) + i%4.
+    // D layout: lane holds column li (d), rows (e) 8*(i/4) + 4*(lane/32) + i%4.
 #pragma unroll
     for (int ct = 0; ct < TILES; ++ct)
 #pragma unroll

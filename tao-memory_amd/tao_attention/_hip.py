@@ -42,6 +42,14 @@ class Tokens(ctypes.Structure):
     ]
 
 
+class PrefillPools(ctypes.Structure):
+    _fields_ = [("pw_pool", _vp), ("psw_pool", _vp), ("sel_pool", _vp),
+                ("pool_pcap", _i32), ("epochs", _i32), ("sel_slots", _i32)]
+
+
+PLAN_HEADER = 16
+
+
 class Fusion(ctypes.Structure):
     _fields_ = [
         ("fusion_a", _vp), ("fusion_b", _vp), ("dtype", _i32),
@@ -64,8 +72,9 @@ _SIGNATURES = {
     "tao_seal_epilogue": ([ctypes.POINTER(StateDev), _i32, _i32, _i32, _vp], _i32),
     "tao_local_attention": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i64, _i64,
                              _vp, _i32, _vp, _vp], _i32),
-    "tao_read_fuse": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i32, _i32, _i32,
-                       ctypes.POINTER(Fusion), _vp, _vp, ctypes.POINTER(_i64), _vp], _i32),
+    "tao_prefill": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), ctypes.POINTER(Fusion),
+                     ctypes.POINTER(_i64), _i64, ctypes.POINTER(PrefillPools), _vp, _vp,
+                     ctypes.POINTER(_i64), _vp], _i32),
     "tao_ring_append": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i32, _i32,
                          _i64, _vp], _i32),
     "tao_graph_create": ([ctypes.POINTER(StateDev), ctypes.POINTER(Fusion), _i32, _vp, _vp,
@@ -127,20 +136,49 @@ def strides_bth(t):
     return (s[0], s[1], s[2])
 
 
-def tokens(q, k, v, raw_q, raw_k):
-    tok = Tokens()
+def tokens(q, k, v, raw_q, raw_k, reuse=None):
+    """Fill a Tokens struct; `reuse` (a previous struct) skips unchanged strides."""
+    strides = (q.stride(), k.stride(), v.stride(), raw_q.stride(), raw_k.stride())
+    if reuse is not None and reuse._strides == strides and reuse.tokens == q.shape[1]:
+        tok = reuse
+    else:
+        tok = Tokens()
+        tok.q_s = i64x3(strides[0][:3])
+        tok.k_s = i64x3(strides[1][:3])
+        tok.v_s = i64x3(strides[2][:3])
+        tok.rq_s = i64x3(strides[3][:3])
+        tok.rk_s = i64x3(strides[4][:3])
+        tok.tokens = q.shape[1]
+        tok._strides = strides
     tok.q, tok.k, tok.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
     tok.raw_q, tok.raw_k = raw_q.data_ptr(), raw_k.data_ptr()
-    tok.q_s = i64x3(strides_bth(q))
-    tok.k_s = i64x3(strides_bth(k))
-    tok.v_s = i64x3(strides_bth(v))
-    tok.rq_s = i64x3(strides_bth(raw_q))
-    tok.rk_s = i64x3(strides_bth(raw_k))
-    tok.tokens = q.shape[1]
     return tok
 
 
+_FUSION_CACHE = {}
+
+
 def fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on):
+    """Fusion struct, cached per (parameter buffers, dtypes, alpha, presence).
+
+    Parameters stay read in place by the kernels, so in-place updates of
+    fp32/bf16 fusion tensors are seen by later calls.
+    """
+    key = (fusion_a.data_ptr(), fusion_b.data_ptr(), fusion_a.dtype, fusion_b.dtype,
+           fusion_a.stride(), fusion_b.stride(), float(alpha), bool(coarse_on),
+           bool(fine_on), fusion_a.device)
+    hit = _FUSION_CACHE.get(key)
+    if hit is not None and hit._keep[2] is fusion_a and hit._keep[3] is fusion_b:
+        return hit
+    fu = _make_fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on)
+    if len(_FUSION_CACHE) > 64:
+        _FUSION_CACHE.clear()
+    _FUSION_CACHE[key] = fu
+    return fu
+
+
+def _make_fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on):
+    originals = (fusion_a, fusion_b)
     fu = Fusion()
     if fusion_a.dtype == torch.float32 and fusion_b.dtype == torch.float32:
         fu.dtype = TAO_FP32
@@ -156,6 +194,6 @@ def fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on):
     # gain = torch.full((), 2 * alpha, dtype=bf16) as in operator.py:89.
     fu.gain = float(torch.full((), 2 * alpha, dtype=torch.bfloat16))
     fu.coarse_on, fu.fine_on = int(bool(coarse_on)), int(bool(fine_on))
-    # Keep converted parameter tensors alive for the launch.
-    fu._keep = (fusion_a, fusion_b)
+    # Keep the (possibly converted) parameter tensors alive with the struct.
+    fu._keep = (fusion_a, fusion_b) + originals
     return fu

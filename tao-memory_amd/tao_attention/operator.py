@@ -6,7 +6,7 @@ the caller's Q/K transform, q / k are the local-attention operands after it.
 The streaming path is bf16 on an MI355X device with width 64 or 128.
 """
 
-import torch
+import torch  # noqa: F401
 
 from .config import TaoConfig
 from .flash_attention import flash_attn
@@ -48,8 +48,7 @@ def tao_attention_prefill(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b,
     _check_plugin(local_flash)
     if q.shape[1] == 0:
         return q.new_empty(q.shape), state
-    with torch.inference_mode():
-        out = state.prefill(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
+    out = state.prefill(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
     return out, state
 
 
@@ -61,6 +60,5 @@ def tao_attention_decode(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b,
     if position != state.position:
         raise ValueError("position must match this request's causal cursor")
     _check_plugin(local_flash)
-    with torch.inference_mode():
-        out = state.decode(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
+    out = state.decode(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
     return out, state

@@ -9,7 +9,9 @@ out for MI355X instead of rebuilt per seal:
   indexed by position % serve_limit, replacing three torch.cat per call
   (tao_stream.py:927-930) and the clone at each seal (:965-967);
 * fine memories live in a capacity-backed bank [B, H, S_cap, D, D] written in
-  place by the writer kernel, replacing the per-seal repack (:455-462);
+  place by the writer kernel, replacing the per-seal repack (:455-462); each
+  slot holds C^T (d contiguous) so every reader contracts over contiguous
+  memory; export/import transpose to and from the reference's C;
 * page descriptors, segment weights r(exp(r(z - page_z))) and page weights
   r(softmax over pages) are updated once per seal by the epilogue kernel:
   this is the reference's page-normalisation memo (:399-416), kept valid
@@ -78,10 +80,23 @@ class _DeviceState:
         self.page_z, self.page_w, self.sel, self.chosen = page_z, page_w, sel, chosen
         self.fine_cap, self.page_cap, self.sel_cap, self.chosen_cap = (
             fine_cap, page_cap, sel_cap, chosen_cap)
-        ws_bytes = _hip.lib().tao_workspace_bytes(B, H, D, sel_cap, 4096)
-        self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        self.plan_words = 0
+        self._workspace(4096)
+
+    def _workspace(self, plan_words):
+        ws_bytes = _hip.lib().tao_workspace_bytes(self.B, self.H, self.D, self.sel_cap,
+                                                  plan_words)
+        self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=self.device)
+        self.plan_words = plan_words
         self.struct = self._make_struct()
         _hip.check(_hip.lib().tao_workspace_init(ctypes.byref(self.struct), self.stream()))
+
+    def ensure_plan(self, words):
+        """Grow the workspace plan region; returns True if buffers moved."""
+        if words <= self.plan_words:
+            return False
+        self._workspace(max(words, 2 * self.plan_words))
+        return True
 
     def _make_struct(self):
         st = _hip.StateDev()
@@ -209,6 +224,7 @@ class StreamCache:
         # Optional launch probe: probe(name) -> context manager wrapped around
         # each kernel launch (used by bench.py for live kernel timing).
         self._probe = None
+        self._tok = None
 
     # ------------------------------------------------------------------ cursor
     def get_pos(self):
@@ -295,6 +311,112 @@ class StreamCache:
                 dev.stream()))
 
     # ---------------------------------------------------------------- streaming
+    def _plan(self, pos0, tokens, outputs, turn_filter=None):
+        """int64 plan of tao_prefill for tokens [pos0, pos0 + tokens).
+
+        outputs=False plans a state-only advance (no attention or reads; only
+        the last refresh turn is routed, in its own epoch).
+        """
+        cfg = self.config
+        group = cfg.coarse_group
+        end = pos0 + tokens
+        f0, f1 = schedule.fines_at(pos0, cfg), schedule.fines_at(end, cfg)
+        plan_chunks = schedule.chunks(pos0, tokens, cfg)
+        attn, reads, turns = [], [], []
+        chunk_epochs = []
+        for start, width in plan_chunks:
+            epoch = schedule.fines_at(start, cfg)
+            chunk_epochs.append(epoch)
+            if outputs:
+                key_start = start - schedule.local_len_at(start, cfg)
+                for qs in range(start, start + width, _QTILE):
+                    attn += [qs - pos0, min(_QTILE, start + width - qs), key_start]
+        # Epochs read by this call plus the published final epoch.
+        if f1 >= 1:
+            first_epoch = max(min([e for e in chunk_epochs if e >= 1] + [f1]), 1)
+        else:
+            first_epoch = 0
+        if not outputs and f1 >= 1:
+            first_epoch = f1
+        slot, slot_m = 0, self.route_size
+        route = (self.route_coarse, self.route_size)
+        last_turn = None
+        for (start, width), epoch in zip(plan_chunks, chunk_epochs):
+            for sub, count, refresh in schedule.sub_chunks(start, width, self.layer_index, cfg):
+                if epoch == 0:
+                    if outputs:
+                        for qs in range(sub, sub + count, 32):
+                            reads += [qs - pos0, min(32, sub + count - qs), 0, 0, 0, 0, 0, 0]
+                    continue
+                if refresh:
+                    completed, pending = divmod(epoch, group)
+                    coarse, _, selected = schedule.routed_counts(completed, pending, cfg)
+                    last_turn = (sub, epoch, completed, pending, coarse, selected)
+                    if outputs:
+                        turns += [sub - pos0, epoch - first_epoch, completed, pending,
+                                  coarse, selected, len(turns) // 8 + 1, 0]
+                        slot, slot_m = len(turns) // 8, selected
+                    route = (coarse, selected)
+                if outputs:
+                    for qs in range(sub, sub + count, 32):
+                        reads += [qs - pos0, min(32, sub + count - qs), slot, slot_m,
+                                  epoch - first_epoch, (epoch // group) * group, 1, 0]
+        if not outputs and last_turn is not None:
+            sub, epoch, completed, pending, coarse, selected = last_turn
+            first_epoch = min(first_epoch, epoch)
+            turns = [sub - pos0, epoch - first_epoch, completed, pending, coarse, selected, 1, 1]
+        elif turns:
+            turns[-1] = 1
+        n_epochs = f1 - first_epoch + 1 if f1 >= 1 else 0
+        writes = [cfg.fine_tokens * f for f in range(f0, f1)]
+        keep = min(tokens, cfg.serve_limit)
+        header = [0] * _hip.PLAN_HEADER
+        header[0] = pos0
+        header[1] = len(attn) // 3
+        header[2] = len(writes)
+        header[3] = f0
+        header[4] = f0 // group
+        header[5] = f1 // group - f0 // group
+        header[6] = first_epoch
+        header[7] = n_epochs
+        header[8] = len(turns) // 8
+        header[9] = len(reads) // 8
+        header[10] = tokens - keep
+        header[11] = keep
+        header[12] = end - keep
+        plan = header + attn + writes + turns + reads
+        return plan, dict(epochs=n_epochs, turns=len(turns) // 8, route=route,
+                          pool_pcap=f1 // group + 1, chunk_epochs=chunk_epochs)
+
+    def _run_plan(self, dev, tok, fu, plan, info, local, out):
+        plan_arr = (ctypes.c_int64 * len(plan))(*plan)
+        if dev.ensure_plan(len(plan)):
+            self.release_execution("capacity")
+        pools = _hip.PrefillPools()
+        keep = []
+        if info["epochs"] or info["turns"]:
+            B, H, D = dev.B, dev.H, dev.D
+            pcap = info["pool_pcap"]
+            pw_pool = torch.empty((info["epochs"], B, H, pcap, D), dtype=torch.bfloat16,
+                                  device=dev.device)
+            psw_pool = torch.empty((info["epochs"], B, H, self.config.coarse_group, D),
+                                   dtype=torch.bfloat16, device=dev.device)
+            sel_pool = torch.empty((info["turns"] + 1, B, H, dev.sel_cap), dtype=torch.int32,
+                                   device=dev.device)
+            pools.pw_pool, pools.psw_pool = pw_pool.data_ptr(), psw_pool.data_ptr()
+            pools.sel_pool = sel_pool.data_ptr()
+            pools.pool_pcap, pools.epochs, pools.sel_slots = pcap, info["epochs"], info["turns"] + 1
+            keep = [pw_pool, psw_pool, sel_pool]
+        out_s = (ctypes.c_int64 * 3)(*(_hip.strides_bth(out) if out is not None else (0, 0, 0)))
+        dummy = dev.workspace.data_ptr()
+        with self._timed("prefill"):
+            _hip.check(_hip.lib().tao_prefill(
+                ctypes.byref(dev.struct), ctypes.byref(tok), ctypes.byref(fu), plan_arr,
+                len(plan), ctypes.byref(pools),
+                local.data_ptr() if local is not None else dummy,
+                out.data_ptr() if out is not None else dummy, out_s, dev.stream()))
+        del keep      # the caching allocator keeps them stream-ordered
+
     def prefill(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
         """Advance by q.shape[1] tokens; returns the fused heads [B, T, H, D]."""
         self._check_supported(q)
@@ -305,58 +427,30 @@ class StreamCache:
         q, k, v, raw_q, raw_k = (t if t.stride(-1) == 1 else t.contiguous()
                                  for t in (q, k, v, raw_q, raw_k))
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
-        stream = dev.stream()
-        plan = schedule.chunks(pos0, tokens, cfg)
+        plan, info = self._plan(pos0, tokens, outputs=True)
         local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
         out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
-        tiles = []
-        for start, width in plan:
-            key_start = start - schedule.local_len_at(start, cfg)
-            for qs in range(start, start + width, _QTILE):
-                tiles.append((qs - pos0, min(_QTILE, start + width - qs), key_start))
-        tiles_dev = torch.tensor(tiles, dtype=torch.int64).to(q.device)
-        with self._timed("local_attention"):
-            _hip.check(_hip.lib().tao_local_attention(
-                ctypes.byref(dev.struct), ctypes.byref(tok), pos0, pos0,
-                tiles_dev.data_ptr(), len(tiles), local.data_ptr(), stream))
-        # Banks depend only on raw_k and v: every seal of the call is written
-        # by one launch; each chunk end then publishes its seal's epoch.
-        first_fine = schedule.fines_at(pos0, cfg)
-        last_fine = schedule.fines_at(pos0 + tokens, cfg)
-        if last_fine > first_fine:
-            starts = [cfg.fine_tokens * f for f in range(first_fine, last_fine)]
-            starts_dev = torch.tensor(starts, dtype=torch.int64).to(q.device)
-            with self._timed("writer"):
-                _hip.check(_hip.lib().tao_write_fine(
-                    ctypes.byref(dev.struct), ctypes.byref(tok), pos0, starts_dev.data_ptr(),
-                    first_fine, len(starts), stream))
-        out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
-        for start, width in plan:
-            fines = schedule.fines_at(start, cfg)
-            fine_on = fines > 0
-            fu = _hip.fusion(fusion_a, fusion_b, alpha, False, fine_on)
-            for sub, count, refresh in schedule.sub_chunks(start, width, self.layer_index, cfg):
-                if fine_on and refresh:
-                    self._route(dev, raw_q[:, sub - pos0], fines)
-                with self._timed("read_fuse"):
-                    _hip.check(_hip.lib().tao_read_fuse(
-                        ctypes.byref(dev.struct), ctypes.byref(tok), sub - pos0, count,
-                        self.route_size if fine_on else 0, ctypes.byref(fu),
-                        local.data_ptr(), out.data_ptr(), out_s, stream))
-            if fine_on:
+        fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True)
+        self._run_plan(dev, tok, fu, plan, info, local, out)
+        self._advance(pos0, tokens, info)
+        for epoch in info["chunk_epochs"]:
+            if epoch:
                 self.fusion_pointwise_calls += 1
             else:
                 self.fusion_no_history_local_returns += 1
-            if schedule.seals_in(start, width, cfg):
-                self._epilogue(dev, fines)
-                self.fine_seal_events += 1
-        keep = min(tokens, cfg.serve_limit)
-        _hip.check(_hip.lib().tao_ring_append(
-            ctypes.byref(dev.struct), ctypes.byref(tok), tokens - keep, keep,
-            pos0 + tokens - keep, stream))
-        self.position = pos0 + tokens
-        dev.header[0:1].fill_(self.position)
         return out
+
+    def _advance(self, pos0, tokens, info):
+        cfg = self.config
+        end = pos0 + tokens
+        self.fine_seal_events += schedule.fines_at(end, cfg) - schedule.fines_at(pos0, cfg)
+        self.route_refreshes += sum(
+            1 for p in range(max(pos0, cfg.first_fine), end)
+            if schedule.is_turn(p, self.layer_index, cfg))
+        self.route_coarse, self.route_size = info["route"]
+        self.peak_selected_fine = max(self.peak_selected_fine, self.route_size)
+        self.position = end
+        self._dev.header[0:1].fill_(end)
 
     def decode(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
         """One new token; returns the fused heads [B, 1, H, D]."""
@@ -364,9 +458,10 @@ class StreamCache:
         cfg = self.config
         pos = self.position
         dev = self._device_for(q, pos + 1)
-        q, k, v, raw_q, raw_k = (t if t.stride(-1) == 1 else t.contiguous()
-                                 for t in (q, k, v, raw_q, raw_k))
-        tok = _hip.tokens(q, k, v, raw_q, raw_k)
+        if not (q.stride(-1) == k.stride(-1) == v.stride(-1) == raw_q.stride(-1)
+                == raw_k.stride(-1) == 1):
+            q, k, v, raw_q, raw_k = (t.contiguous() for t in (q, k, v, raw_q, raw_k))
+        tok = self._tok = _hip.tokens(q, k, v, raw_q, raw_k, self._tok)
         fines = schedule.fines_at(pos, cfg)
         fine_on = fines > 0
         if fine_on and schedule.is_turn(pos, self.layer_index, cfg):
@@ -397,56 +492,55 @@ class StreamCache:
         self.position = pos + 1
         return out
 
+    def _launch_prompt_kernels(self, q, k, v, raw_q, raw_k):
+        """Launch only the prompt's local attention and writer kernels.
+
+        Measurement helper (bench.py): the launches are wrapped in the probe
+        as "local_attention" and "writer"; the cursor does not move.
+        """
+        self._check_supported(q)
+        pos0 = self.position
+        tokens = q.shape[1]
+        dev = self._device_for(q, pos0 + tokens)
+        tok = _hip.tokens(q, k, v, raw_q, raw_k)
+        plan, _ = self._plan(pos0, tokens, outputs=True)
+        n_attn, n_write = plan[1], plan[2]
+        base = _hip.PLAN_HEADER
+        tiles = torch.tensor(plan[base:base + 3 * n_attn], dtype=torch.int64).to(q.device)
+        starts = torch.tensor(plan[base + 3 * n_attn:base + 3 * n_attn + n_write] or [0],
+                              dtype=torch.int64).to(q.device)
+        local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+        lib = _hip.lib()
+        with self._timed("local_attention"):
+            _hip.check(lib.tao_local_attention(
+                ctypes.byref(dev.struct), ctypes.byref(tok), pos0, pos0, tiles.data_ptr(),
+                n_attn, local.data_ptr(), dev.stream()))
+        with self._timed("writer"):
+            _hip.check(lib.tao_write_fine(
+                ctypes.byref(dev.struct), ctypes.byref(tok), pos0, starts.data_ptr(), plan[3],
+                n_write, dev.stream()))
+        return local
+
     def _ingest(self, q, k, v, raw_q, raw_k):
         """Advance the state by q.shape[1] tokens without computing outputs.
 
         The resulting state equals prefill()'s: the banks depend only on raw_k
-        and v (all seals go to the writer in one launch), the epilogues run in
-        seal order, and the route of the last refresh turn is recomputed in
-        its own seal epoch from that turn's anchor query.
+        and v (every seal goes to the writer in one launch), page and epoch
+        bookkeeping is batched, and the route of the last refresh turn is
+        recomputed in its own seal epoch from that turn's anchor query.
         """
         self._check_supported(q)
-        cfg = self.config
         pos0 = self.position
         tokens = q.shape[1]
-        end = pos0 + tokens
-        dev = self._device_for(q, end)
+        dev = self._device_for(q, pos0 + tokens)
         q, k, v, raw_q, raw_k = (t if t.stride(-1) == 1 else t.contiguous()
                                  for t in (q, k, v, raw_q, raw_k))
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
-        first_fine = schedule.fines_at(pos0, cfg)
-        last_fine = schedule.fines_at(end, cfg)
-        starts = [cfg.fine_tokens * (f - 1) for f in range(first_fine + 1, last_fine + 1)]
-        if starts:
-            starts_dev = torch.tensor(starts, dtype=torch.int64).to(q.device)
-            with self._timed("writer"):
-                _hip.check(_hip.lib().tao_write_fine(
-                    ctypes.byref(dev.struct), ctypes.byref(tok), pos0, starts_dev.data_ptr(),
-                    first_fine, len(starts), dev.stream()))
-        # Last refresh turn inside [pos0, end) whose read saw fines.
-        turn = None
-        for p in range(end - 1, max(pos0, cfg.first_fine) - 1, -1):
-            if schedule.is_turn(p, self.layer_index, cfg):
-                turn = p
-                break
-        self.route_refreshes += sum(
-            1 for p in range(max(pos0, cfg.first_fine), end)
-            if schedule.is_turn(p, self.layer_index, cfg)) - (turn is not None)
-        route_epoch = schedule.fines_at(turn, cfg) if turn is not None else None
-        for slot in range(first_fine, last_fine):
-            if route_epoch is not None and slot == route_epoch:
-                self._route(dev, raw_q[:, turn - pos0], route_epoch)
-                route_epoch = None
-            self._epilogue(dev, slot)
-            self.fine_seal_events += 1
-        if route_epoch is not None:
-            self._route(dev, raw_q[:, turn - pos0], route_epoch)
-        keep = min(tokens, cfg.serve_limit)
-        _hip.check(_hip.lib().tao_ring_append(
-            ctypes.byref(dev.struct), ctypes.byref(tok), tokens - keep, keep,
-            end - keep, dev.stream()))
-        self.position = end
-        dev.header[0:1].fill_(end)
+        plan, info = self._plan(pos0, tokens, outputs=False)
+        fu = _hip.fusion(torch.zeros(1, device=q.device), torch.zeros(1, device=q.device),
+                         0.0, False, False)
+        self._run_plan(dev, tok, fu, plan, info, None, None)
+        self._advance(pos0, tokens, info)
 
     # ---------------------------------------------------------------- snapshot
     def _local_window(self):
@@ -472,7 +566,8 @@ class StreamCache:
         pages, pending_z = [], []
         packed = None
         if fines:
-            packed = dev.bank[:, :, :fines].clone()
+            # The bank stores C^T[e][d]; the snapshot keeps the reference's C[d][e].
+            packed = dev.bank[:, :, :fines].transpose(-1, -2).contiguous()
             for i in range(completed):
                 pages.append((dev.page_z[:, :, i].clone(), None,
                               dev.fine_z[:, :, i * group:(i + 1) * group].clone()))
@@ -530,7 +625,7 @@ class StreamCache:
         for buf, src in zip((dev.ring_k, dev.ring_v, dev.ring_raw), local):
             buf.index_copy_(1, slots, src.to(torch.bfloat16))
         if fines:
-            dev.bank[:, :, :fines].copy_(packed)
+            dev.bank[:, :, :fines].copy_(packed.transpose(-1, -2))
             for i, (pz, _, fz) in enumerate(pages):
                 dev.page_z[:, :, i].copy_(pz)
                 dev.fine_z[:, :, i * group:(i + 1) * group].copy_(fz)

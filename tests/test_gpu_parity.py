@@ -187,3 +187,31 @@ def test_contract_errors(device):
     with pytest.raises(ValueError):
         tao_attention_decode(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.to(device),
                              fusion_b=fb.to(device), alpha=0.5, state=state, position=0)
+
+
+def test_ingest_state_equals_prefill_state(device):
+    """Writer-only state construction (bench state builder) == real prefill."""
+    heads, width = 4, 128
+    xs, fa, fb = inputs(3000, heads, width, seed=15)
+    d = to_dev(xs, device)
+    print("ingest vs prefill", flush=True)
+    a = new_state(2, index_only_page_memo())
+    run_hip(a, d, fa.to(device), fb.to(device), [1500, 1500])
+    b = new_state(2, index_only_page_memo())
+    b._ingest(*(x[:, :1500] for x in d))
+    b._ingest(*(x[:, 1500:] for x in d))
+    sa, sb = a.export(), b.export()
+    assert sa["position"] == sb["position"] == 3000
+    assert torch.equal(sa["packed_fine_c"], sb["packed_fine_c"])
+    for (pz, _, fz), (qz, _, gz) in zip(sa["pages"], sb["pages"]):
+        assert torch.equal(pz, qz) and torch.equal(fz, gz)
+    for x, y in zip(sa["pending_z"], sb["pending_z"]):
+        assert torch.equal(x, y)
+    assert torch.equal(sa["route_ids"][1], sb["route_ids"][1])
+    for x, y in zip(sa["local"], sb["local"]):
+        assert torch.equal(x, y)
+    # Both continue identically.
+    tok = [x[:, 2999:3000].clone() for x in d]
+    ya = run_hip(a, [torch.cat([x, x], 1)[:, :1] for x in tok], fa.to(device), fb.to(device), [1])
+    yb = run_hip(b, [torch.cat([x, x], 1)[:, :1] for x in tok], fa.to(device), fb.to(device), [1])
+    assert torch.equal(ya, yb)

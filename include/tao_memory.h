@@ -136,7 +136,7 @@ int tao_seal_epilogue(const tao_state_dev* st, int32_t slot, int32_t pages,
  * tao_stream.py:927-930). Query row r of tok.q sits at absolute position
  * qpos0 + r; key row j of tok.k / tok.v at kpos0 + j, and keys older than
  * kpos0 come from the ring. tiles: device int64 [n_tiles][3] = (first query
- * row, count <= 128, key_start): the tile's queries see keys from key_start
+ * row, count <= 256, key_start): the tile's queries see keys from key_start
  * up to their own position. local: bf16 [B, tok.tokens, H, D] contiguous. */
 int tao_local_attention(const tao_state_dev* st, const tao_tokens* tok,
                         int64_t qpos0, int64_t kpos0, const int64_t* tiles,
@@ -157,7 +157,7 @@ typedef struct tao_prefill_pools {
 #define TAO_PLAN_HEADER 16
 enum tao_plan_field {
   TAO_PLAN_POS0 = 0,        /* absolute position of token 0 */
-  TAO_PLAN_ATTN_TILES = 1,  /* n, then n x {first, count <= 128, key_start} */
+  TAO_PLAN_ATTN_TILES = 1,  /* n, then n x {first, count <= 256, key_start} */
   TAO_PLAN_WRITES = 2,      /* n, then n block start positions */
   TAO_PLAN_FIRST_SLOT = 3,  /* fine slot of the first written block */
   TAO_PLAN_FIRST_PAGE = 4,  /* first page completed by this call */
@@ -202,6 +202,36 @@ int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu,
                      void* stream, void** graph_out);
 int tao_graph_launch(void* graph, const tao_tokens* tok, void* stream);
 int tao_graph_destroy(void* graph);
+
+/* Streaming geometry of one request x layer (reference TaoConfig fields,
+ * config.py:7-19, and the layer index that staggers route refreshes). */
+typedef struct tao_stream_cfg {
+  int32_t layer, local_keep, fine_tokens, coarse_group, route_period, layer_stagger;
+  int32_t budget_root_scale, budget_offset;
+  int32_t use_graph;   /* replay the decode step from a hipGraph */
+} tao_stream_cfg;
+
+/* Native per-token driver (replaces the Python control flow of one decode
+ * call: operator.py:130-138, tao_stream.py:196-249 and 919-969,
+ * history_region_graph.py:66-113). It keeps the cursor and the current route
+ * size; staging (bf16, 5 * B * H * D) and out_stage (bf16 [B,1,H,D]) are
+ * the caller's graph buffers (may be null when use_graph is 0). */
+int tao_stream_open(const tao_state_dev* st, const tao_stream_cfg* cfg, int64_t position,
+                    int32_t route_coarse, int32_t route_size, void* staging,
+                    void* out_stage, void** handle);
+/* Re-point the driver after the host grew buffers, prefilled or imported. */
+int tao_stream_sync(void* handle, const tao_state_dev* st, int64_t position,
+                    int32_t route_coarse, int32_t route_size);
+/* One new token: route refresh on turn positions, the decode step (graph
+ * replay or eager; with a graph the heads land in out_stage), and the seal
+ * when the local window fills. info (int64[7]) receives: position after the
+ * call, route coarse count, route size, refreshed, sealed, used_graph,
+ * captured. */
+int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu, void* out,
+                      const int64_t* out_s, void* stream, int64_t* info);
+/* Destroy the driver's captured graph (semantic state is untouched). */
+int tao_stream_release(void* handle);
+int tao_stream_close(void* handle);
 
 #ifdef __cplusplus
 }

@@ -132,6 +132,8 @@ struct DecodeGraph {
 
 namespace tao {
 
+void set_error(const char* msg) { g_error = msg; }
+
 WorkspaceLayout workspace_layout(int batch, int heads, int head_dim, int sel_cap,
                                  int plan_words) {
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -331,7 +333,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   // ---- validate attention tiles
   for (int64_t i = 0; i < n_attn; ++i) {
     const int64_t* t = plan + off_attn + 3 * i;
-    if (t[0] < 0 || t[1] < 1 || t[1] > 128 || t[0] + t[1] > T)
+    if (t[0] < 0 || t[1] < 1 || t[1] > 256 || t[0] + t[1] > T)
       return fail(TAO_E_ARGUMENT, "attention tile outside the call's tokens");
     if (t[2] < window0 || t[2] > pos0 + t[0] || pos0 + t[0] + t[1] - t[2] > L)
       return fail(TAO_E_ARGUMENT, "attention tile window outside the local ring");

@@ -13,7 +13,7 @@
 //                          instruction, all issued before any math; the
 //                          bank stores C^T) and contracts it with the bf16
 //                          channel weights ch = r(r(h*pw[page]) * sw[fine])
-// decode_combine_kernel: one workgroup per (batch, head) merges the split-K
+// decode_combine_kernel: one 1024-thread workgroup per (batch, head) merges the split-K
 //   partials, sums the fine partials in a fixed order, den = r(sum_m r(sum_d
 //   ch)) in butterfly order, fine = r(r(num)/den), applies the fusion
 //   epilogue and advances header[0] (the stream position), so the pair can
@@ -248,69 +248,51 @@ __global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, 
   }
 }
 
-// Kernel B: one workgroup per (batch, head). Thread group g = tid / D owns
-// local splits s = g (mod G) and fine slots m = g (mod G); groups merge in
+// Kernel B: one 1024-thread workgroup per (batch, head). Thread group
+// g = tid / D owns local splits s = g (mod G) and fine slots m = g (mod G);
+// every record load is issued before any arithmetic, and the groups merge in
 // ascending g, so the summation order is fixed.
+constexpr int kCombineThreads = 1024;
+
 template <int D>
-__global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p, int M) {
-  constexpr int STRIDE = D + kRec, G = kThreads / D;
-  __shared__ float part_num[G][D], part_loc[G][D], part_den[G];
-  __shared__ float den_fine;
+__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeParams p, int M) {
+  constexpr int STRIDE = D + kRec, G = kCombineThreads / D;
+  constexpr int SPG = kLocalSplits / G > 0 ? kLocalSplits / G : 1;   // splits per group
+  constexpr int UNROLL = 8;
+  __shared__ float ml[kLocalSplits][2];
+  __shared__ float part_num[G][D], part_loc[G][D];
+  __shared__ float den_local, den_fine;
   const int bh = blockIdx.x;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, d = tid % D, g = tid / D;
   const float* recs = p.parts + (size_t)bh * (kLocalSplits + p.sel_cap) * STRIDE;
 
-  float mrec[kLocalSplits], lrec[kLocalSplits];
+  if (tid < 2 * kLocalSplits) ml[tid >> 1][tid & 1] = recs[(tid >> 1) * STRIDE + (tid & 1)];
+  float accl[SPG];
 #pragma unroll
-  for (int s = 0; s < kLocalSplits; ++s) {
-    mrec[s] = recs[s * STRIDE];
-    lrec[s] = recs[s * STRIDE + 1];
-  }
-  float accl[kLocalSplits / G];
-#pragma unroll
-  for (int i = 0; i < kLocalSplits / G; ++i) accl[i] = recs[(g + i * G) * STRIDE + kRec + d];
-  float top = -__builtin_inff();
-#pragma unroll
-  for (int s = 0; s < kLocalSplits; ++s)
-    if (lrec[s] > 0.0f) top = fmaxf(top, mrec[s]);
-  float num_l = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kLocalSplits / G; ++i) {
+  for (int i = 0; i < SPG; ++i) {
     const int s = g + i * G;
-    if (lrec[s] > 0.0f) num_l = fmaf(__expf(mrec[s] - top), accl[i], num_l);
+    accl[i] = s < kLocalSplits ? recs[s * STRIDE + kRec + d] : 0.0f;
   }
-  part_loc[g][d] = num_l;
-  if (tid == 0) {
-    float den = 0.0f;
-#pragma unroll
-    for (int s = 0; s < kLocalSplits; ++s)
-      if (lrec[s] > 0.0f) den = fmaf(__expf(mrec[s] - top), lrec[s], den);
-    part_den[0] = den;
-  }
-  // fine numerator partial sums and the slot-fold denominator
   float num_f = 0.0f;
-  {
-    const float* base = recs + (size_t)kLocalSplits * STRIDE + kRec + d;
-    int m = g;
-    for (; m + 3 * G < M; m += 4 * G) {
-      const float a0 = base[(size_t)m * STRIDE];
-      const float a1 = base[(size_t)(m + G) * STRIDE];
-      const float a2 = base[(size_t)(m + 2 * G) * STRIDE];
-      const float a3 = base[(size_t)(m + 3 * G) * STRIDE];
-      num_f = num_f + a0;
-      num_f = num_f + a1;
-      num_f = num_f + a2;
-      num_f = num_f + a3;
+  const float* fine = recs + (size_t)kLocalSplits * STRIDE + kRec + d;
+  for (int base = g; base < M; base += UNROLL * G) {
+    float v[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int m = base + u * G;
+      v[u] = m < M ? fine[(size_t)m * STRIDE] : 0.0f;
     }
-    for (; m < M; m += G) num_f = num_f + base[(size_t)m * STRIDE];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) num_f = num_f + v[u];
   }
-  part_num[g][d] = num_f;
   if (M > 0 && tid < 64) {
+    // den = r(sum over slots of r(sum_d ch)), butterfly order over slots.
     int slots = 64;
     while (slots < M) slots *= 2;
     const int per_lane = slots / 64;
     float vals[8];
+#pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int m = tid + 64 * k;
       vals[k] = (k < per_lane && m < M) ? recs[(kLocalSplits + m) * STRIDE] : 0.0f;
@@ -321,14 +303,34 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
     if (tid == 0) den_fine = rbf(v);
   }
   __syncthreads();
+  float top = -__builtin_inff();
+#pragma unroll
+  for (int s = 0; s < kLocalSplits; ++s)
+    if (ml[s][1] > 0.0f) top = fmaxf(top, ml[s][0]);
+  float num_l = 0.0f;
+#pragma unroll
+  for (int i = 0; i < SPG; ++i) {
+    const int s = g + i * G;
+    if (s < kLocalSplits && ml[s][1] > 0.0f) num_l = fmaf(__expf(ml[s][0] - top), accl[i], num_l);
+  }
+  part_loc[g][d] = num_l;
+  part_num[g][d] = num_f;
+  if (tid == 0) {
+    float den = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kLocalSplits; ++s)
+      if (ml[s][1] > 0.0f) den = fmaf(__expf(ml[s][0] - top), ml[s][1], den);
+    den_local = den;
+  }
+  __syncthreads();
   if (tid < D) {
     float nl = 0.0f, nf = 0.0f;
 #pragma unroll
     for (int gg = 0; gg < G; ++gg) { nl += part_loc[gg][d]; nf += part_num[gg][d]; }
-    const float local = rbf(nl / part_den[0]);
+    const float local = rbf(nl / den_local);
     bf16_t result;
     if (M > 0) {
-      const float fine = rbf(rbf(nf) / den_fine);
+      const float fine_v = rbf(rbf(nf) / den_fine);
       const float q = bf2f(p.rq.p[b * p.rq.sb + h * p.rq.sh + d]);
       float a[3], bb[3];
 #pragma unroll
@@ -336,7 +338,7 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
         a[i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + d * p.fa_s[1] + i * p.fa_s[2]);
         bb[i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + d * p.fb_s[1] + i * p.fb_s[2]);
       }
-      result = fuse_element(q, local, 0.0f, fine, a, bb, p.gain, 0, 1);
+      result = fuse_element(q, local, 0.0f, fine_v, a, bb, p.gain, 0, 1);
     } else {
       result = f2bf(local);
     }
@@ -347,14 +349,24 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
 }
 
 __global__ __launch_bounds__(kThreads) void stage_tokens_kernel(StageParams p) {
-  // One workgroup per (b, h): copies q, k, v, raw_q, raw_k rows (token 0).
-  const int bh = blockIdx.x;
+  // One 16-byte chunk per thread: q, k, v, raw_q, raw_k rows of token 0.
+  const int per_row = p.D / 8;
+  const int bhn = p.B * p.H;
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= 5 * bhn * per_row) return;
+  const int c = i % per_row, row = i / per_row;
+  const int which = row / bhn, bh = row % bhn;
   const int b = bh / p.H, h = bh % p.H;
-  for (int i = threadIdx.x; i < 5 * p.D; i += kThreads) {
-    const int which = i / p.D, d = i % p.D;
-    const TokView& v = p.src[which];
-    p.dst[((size_t)which * p.B * p.H + bh) * p.D + d] = v.p[b * v.sb + h * v.sh + d];
+  TokView v;
+  switch (which) {
+    case 0: v = p.src[0]; break;
+    case 1: v = p.src[1]; break;
+    case 2: v = p.src[2]; break;
+    case 3: v = p.src[3]; break;
+    default: v = p.src[4]; break;
   }
+  *(uint4*)(p.dst + ((size_t)which * bhn + bh) * p.D + c * 8) =
+      *(const uint4*)(v.p + b * v.sb + h * v.sh + c * 8);
 }
 
 __global__ __launch_bounds__(kThreads) void ring_append_kernel(AppendParams p) {
@@ -379,10 +391,10 @@ hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStr
   const dim3 heads((unsigned)(p.B * p.H));
   if (head_dim == 128) {
     hipLaunchKernelGGL(decode_units_kernel<128>, units, dim3(kThreads), 0, s, p, M);
-    hipLaunchKernelGGL(decode_combine_kernel<128>, heads, dim3(kThreads), 0, s, p, M);
+    hipLaunchKernelGGL(decode_combine_kernel<128>, heads, dim3(kCombineThreads), 0, s, p, M);
   } else if (head_dim == 64) {
     hipLaunchKernelGGL(decode_units_kernel<64>, units, dim3(kThreads), 0, s, p, M);
-    hipLaunchKernelGGL(decode_combine_kernel<64>, heads, dim3(kThreads), 0, s, p, M);
+    hipLaunchKernelGGL(decode_combine_kernel<64>, heads, dim3(kCombineThreads), 0, s, p, M);
   } else {
     return hipErrorInvalidValue;
   }
@@ -390,7 +402,9 @@ hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStr
 }
 
 hipError_t launch_stage_tokens(const StageParams& p, hipStream_t s) {
-  hipLaunchKernelGGL(stage_tokens_kernel, dim3((unsigned)(p.B * p.H)), dim3(kThreads), 0, s, p);
+  const int chunks = 5 * p.B * p.H * (p.D / 8);
+  hipLaunchKernelGGL(stage_tokens_kernel, dim3((unsigned)((chunks + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, s, p);
   return hipGetLastError();
 }
 

@@ -3,7 +3,8 @@
 // Restates flash_attn_func (flash_attention.py:16-37): softmax(QK^T/sqrt(D))V
 // where query row i of a chunk sees keys up to its own absolute position and
 // no key older than the chunk's window start. One workgroup = one tile of up
-// to 128 queries of one (batch, head); wave w owns 32 queries.
+// to 256 queries of one (batch, head); wave w owns 32 queries. The next
+// 64-key block is fetched into registers while the current one computes.
 //
 // Per 64-key block (staged in LDS: K row-major, V transposed):
 //   S^T[key, query] = K . Q^T         v_mfma_f32_32x32x16_bf16, Q in VGPRs
@@ -26,7 +27,7 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kKeys = 64;
-constexpr int kQTile = 128;
+constexpr int kAttnThreads = 512;   // 8 waves x 32 queries = 256-query tiles
 
 template <int D>
 struct AttnSmem {
@@ -48,11 +49,13 @@ TAO_DEV bf16x8 as_bf16x8(const uint4& u) {
 }
 
 template <int D>
-__global__ __launch_bounds__(kThreads) void local_attn_kernel(AttnParams p) {
+__global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) {
   __shared__ AttnSmem<D> sm;
   constexpr int CH = D / 8;
   constexpr int DT = D / 32;    // 32-row tiles of O^T
   constexpr int KK = D / 16;    // k-steps of S^T
+  constexpr int KJ = (kKeys * CH + kAttnThreads - 1) / kAttnThreads;        // K row jobs
+  constexpr int VJ = ((kKeys / 2) * CH + kAttnThreads - 1) / kAttnThreads;  // V pair jobs
   const int bh = blockIdx.x % (p.B * p.H);
   const int tile = blockIdx.x / (p.B * p.H);
   const int b = bh / p.H, h = bh % p.H;
@@ -77,6 +80,29 @@ __global__ __launch_bounds__(kThreads) void local_attn_kernel(AttnParams p) {
   }
   const float scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)D));
 
+  // Global loads of one 64-key block into registers (prefetch).
+  uint4 kpre[KJ], va[VJ], vb[VJ];
+  auto fetch = [&](long long kb) {
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      const int job = tid + j * kAttnThreads;
+      kpre[j] = make_uint4(0, 0, 0, 0);
+      if (job < kKeys * CH && kb + job / CH < kend)
+        kpre[j] = *(const uint4*)(key_row(p, p.k, p.ring_k, b, h, kb + job / CH, D) + (job % CH) * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) {
+      const int job = tid + j * kAttnThreads;
+      va[j] = make_uint4(0, 0, 0, 0);
+      vb[j] = make_uint4(0, 0, 0, 0);
+      if (job < (kKeys / 2) * CH) {
+        const int t0 = 2 * (job / CH), c = job % CH;
+        if (kb + t0 < kend) va[j] = *(const uint4*)(key_row(p, p.v, p.ring_v, b, h, kb + t0, D) + c * 8);
+        if (kb + t0 + 1 < kend) vb[j] = *(const uint4*)(key_row(p, p.v, p.ring_v, b, h, kb + t0 + 1, D) + c * 8);
+      }
+    }
+  };
+
   floatx16 o[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t)
@@ -84,31 +110,31 @@ __global__ __launch_bounds__(kThreads) void local_attn_kernel(AttnParams p) {
     for (int i = 0; i < 16; ++i) o[t][i] = 0.0f;
   float m_run = -__builtin_inff(), l_run = 0.0f;
 
+  fetch(key_start);
   for (long long kb = key_start; kb < kend; kb += kKeys) {
-    __syncthreads();
-    for (int job = tid; job < kKeys * CH; job += kThreads) {
-      const int r = job / CH, c = job % CH;
-      const long long pos = kb + r;
-      uint4 u = make_uint4(0, 0, 0, 0);
-      if (pos < kend) u = *(const uint4*)(key_row(p, p.k, p.ring_k, b, h, pos, D) + c * 8);
-      *(uint4*)&sm.k[r][c * 8] = u;
-    }
-    for (int job = tid; job < (kKeys / 2) * CH; job += kThreads) {
-      const int pair = job / CH, c = job % CH;
-      const int t0 = 2 * pair;
-      uint4 a = make_uint4(0, 0, 0, 0), bq = make_uint4(0, 0, 0, 0);
-      if (kb + t0 < kend) a = *(const uint4*)(key_row(p, p.v, p.ring_v, b, h, kb + t0, D) + c * 8);
-      if (kb + t0 + 1 < kend) bq = *(const uint4*)(key_row(p, p.v, p.ring_v, b, h, kb + t0 + 1, D) + c * 8);
-      const uint32_t wa[4] = {a.x, a.y, a.z, a.w};
-      const uint32_t wb[4] = {bq.x, bq.y, bq.z, bq.w};
+    __syncthreads();          // previous block fully consumed
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        *(uint32_t*)&sm.vt[c * 8 + 2 * i][t0] = (wa[i] & 0xFFFFu) | (wb[i] << 16);
-        *(uint32_t*)&sm.vt[c * 8 + 2 * i + 1][t0] = (wa[i] >> 16) | (wb[i] & 0xFFFF0000u);
+    for (int j = 0; j < KJ; ++j) {
+      const int job = tid + j * kAttnThreads;
+      if (job < kKeys * CH) *(uint4*)&sm.k[job / CH][(job % CH) * 8] = kpre[j];
+    }
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) {
+      const int job = tid + j * kAttnThreads;
+      if (job < (kKeys / 2) * CH) {
+        const int t0 = 2 * (job / CH), c = job % CH;
+        const uint32_t wa[4] = {va[j].x, va[j].y, va[j].z, va[j].w};
+        const uint32_t wb[4] = {vb[j].x, vb[j].y, vb[j].z, vb[j].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          *(uint32_t*)&sm.vt[c * 8 + 2 * i][t0] = (wa[i] & 0xFFFFu) | (wb[i] << 16);
+          *(uint32_t*)&sm.vt[c * 8 + 2 * i + 1][t0] = (wa[i] >> 16) | (wb[i] & 0xFFFF0000u);
+        }
       }
     }
     __syncthreads();
-    if (nq == 0 || kb > wave_last) continue;   // uniform per wave
+    if (kb + kKeys < kend) fetch(kb + kKeys);   // overlaps the math below
+    if (nq == 0 || kb > wave_last) continue;    // uniform per wave
 
     floatx16 s[2];
 #pragma unroll
@@ -194,9 +220,9 @@ hipError_t launch_local_attention(const AttnParams& p, int head_dim, hipStream_t
   if (p.n_tiles <= 0) return hipSuccess;
   const dim3 grid((unsigned)(p.n_tiles * p.B * p.H));
   if (head_dim == 128)
-    hipLaunchKernelGGL(local_attn_kernel<128>, grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL(local_attn_kernel<128>, grid, dim3(kAttnThreads), 0, s, p);
   else if (head_dim == 64)
-    hipLaunchKernelGGL(local_attn_kernel<64>, grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL(local_attn_kernel<64>, grid, dim3(kAttnThreads), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

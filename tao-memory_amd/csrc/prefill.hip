@@ -113,8 +113,9 @@ template <int D>
 __global__ __launch_bounds__(kThreads) void read_tiles_kernel(ReadTilesParams p) {
   constexpr int PER = D / 64, KK = D / 16, ET = D / 32;
   __shared__ float hq[kTileQ][D];
-  __shared__ bf16_t chs[kTileQ][D + 8];
+  __shared__ bf16_t chs[2][kTileQ][D + 8];
   __shared__ float chsum[kTileQ][kMaxM];
+  __shared__ int ids[kMaxM];
   __shared__ float den[kTileQ];
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
@@ -128,71 +129,85 @@ __global__ __launch_bounds__(kThreads) void read_tiles_kernel(ReadTilesParams p)
   const int li = lane & 31, hl = lane >> 5;
 
   if (!fine_on) {
-    for (int i = tid; i < nq * D; i += kThreads) {
-      const int q = i / D, d = i % D;
+    for (int i = tid; i < nq * (D / 8); i += kThreads) {
+      const int q = i / (D / 8), c = i % (D / 8);
       const int t = q_first + q;
-      p.out[b * p.out_sb + (int64_t)t * p.out_st + h * p.out_sh + d] =
-          p.local[(((size_t)b * p.T + t) * p.H + h) * D + d];
+      *(uint4*)(p.out + b * p.out_sb + (int64_t)t * p.out_st + h * p.out_sh + c * 8) =
+          *(const uint4*)(p.local + (((size_t)b * p.T + t) * p.H + h) * D + c * 8);
     }
     return;
   }
-  for (int q = wave; q < kTileQ; q += kThreads / 64) {
-    if (q < nq) {
-      const bf16_t* rq = p.rq.p + b * p.rq.sb + (int64_t)(q_first + q) * p.rq.st + h * p.rq.sh;
-      float x[PER], e[PER];
-      float mx = -__builtin_inff();
-#pragma unroll
-      for (int k = 0; k < PER; ++k) { x[k] = bf2f(rq[lane + 64 * k]); mx = fmaxf(mx, x[k]); }
-      mx = wave_max(mx);
-#pragma unroll
-      for (int k = 0; k < PER; ++k) e[k] = exp_cr(x[k] - mx);
-      float s = e[0];
-#pragma unroll
-      for (int k = 1; k < PER; ++k) s += e[k];
-      s = wave_sum_fold(s);
-#pragma unroll
-      for (int k = 0; k < PER; ++k) hq[q][lane + 64 * k] = rbf(e[k] / s);
-    } else {
-#pragma unroll
-      for (int k = 0; k < PER; ++k) hq[q][lane + 64 * k] = 0.0f;
-    }
-  }
   const int32_t* sel = p.sel_pool + ((size_t)slot * BH + bh) * p.sel_cap;
+  for (int m = tid; m < M; m += kThreads) ids[m] = sel[m];
+  // h = r(softmax_D(raw_q)) of the tile's queries; wave w owns q = w + 4j,
+  // all of its rows are loaded before any reduction.
+  constexpr int QPW = kTileQ / (kThreads / 64);
+  float xr[QPW][PER];
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+    const int q = wave + 4 * j;
+    const bf16_t* rq = p.rq.p + b * p.rq.sb + (int64_t)(q_first + min(q, nq - 1)) * p.rq.st +
+                       h * p.rq.sh;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) xr[j][k] = bf2f(rq[lane + 64 * k]);
+  }
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+    const int q = wave + 4 * j;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int k = 0; k < PER; ++k) mx = fmaxf(mx, xr[j][k]);
+    mx = wave_max(mx);
+    float e[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) e[k] = exp_cr(xr[j][k] - mx);
+    float s = e[0];
+#pragma unroll
+    for (int k = 1; k < PER; ++k) s += e[k];
+    s = wave_sum_fold(s);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) hq[q][lane + 64 * k] = q < nq ? rbf(e[k] / s) : 0.0f;
+  }
+  __syncthreads();
   const bf16_t* bank = p.bank + (size_t)bh * p.fine_cap * D * D;
   const bf16_t* pw_base = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
   const bf16_t* psw_base = p.psw_pool ? p.psw_pool + ((size_t)erel * BH + bh) * 8 * D : nullptr;
   const bf16_t* sw_base = p.sw + (size_t)bh * p.fine_cap * D;
   const int e_row = 32 * wave + li;          // C^T row this lane feeds (wave < ET)
 
-  floatx16 acc;
+  // Operands of fine `id`: C^T rows (waves < ET), page-weight and
+  // segment-weight channels of this lane.
+  auto fetch = [&](int id, uint4* c, float* pwv, float* swv) {
+    if (wave < ET) {
+      const bf16_t* crow = bank + ((size_t)id * D + e_row) * D;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-  uint4 creg[KK], cnext[KK];
-  int id = sel[0];
-  if (wave < ET) {
-    const bf16_t* crow = bank + ((size_t)id * D + e_row) * D;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) creg[kk] = *(const uint4*)(crow + 16 * kk + 8 * hl);
-  }
-  __syncthreads();
-  for (int m = 0; m < M; ++m) {
-    const int page = id / p.group;
-    const bf16_t* pw = pw_base + (size_t)page * D;
+      for (int kk = 0; kk < KK; ++kk) c[kk] = *(const uint4*)(crow + 16 * kk + 8 * hl);
+    }
+    const bf16_t* pw = pw_base + (size_t)(id / p.group) * D;
     const bf16_t* sw = id < sw_split ? sw_base + (size_t)id * D
                                      : psw_base + (size_t)(id - sw_split) * D;
-    float pwv[PER], swv[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       pwv[k] = bf2f(pw[lane + 64 * k]);
       swv[k] = bf2f(sw[lane + 64 * k]);
     }
+  };
+
+  floatx16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+  uint4 creg[KK], cnext[KK];
+  float pwv[PER], swv[PER], pwn[PER], swn[PER];
+  fetch(ids[0], creg, pwv, swv);
+  for (int m = 0; m < M; ++m) {
+    const int buf = m & 1;
     for (int q = wave; q < kTileQ; q += kThreads / 64) {
       float v[PER];
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
         const int d = lane + 64 * k;
         v[k] = q < nq ? rbf(rbf(hq[q][d] * pwv[k]) * swv[k]) : 0.0f;
-        chs[q][d] = f2bf(v[k]);
+        chs[buf][q][d] = f2bf(v[k]);
       }
       float s = v[0];
 #pragma unroll
@@ -200,27 +215,25 @@ __global__ __launch_bounds__(kThreads) void read_tiles_kernel(ReadTilesParams p)
       s = wave_sum_fold(s);
       if (lane == 0) chsum[q][m] = rbf(s);
     }
+    if (m + 1 < M) fetch(ids[m + 1], cnext, pwn, swn);
     __syncthreads();
-    const int next = m + 1 < M ? sel[m + 1] : id;
     if (wave < ET) {
-      const bf16_t* crow = bank + ((size_t)next * D + e_row) * D;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) cnext[kk] = *(const uint4*)(crow + 16 * kk + 8 * hl);
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        const bf16x8 a = as_bf16x8(*(const uint4*)&chs[li][16 * kk + 8 * hl]);
+        const bf16x8 a = as_bf16x8(*(const uint4*)&chs[buf][li][16 * kk + 8 * hl]);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(creg[kk]), acc, 0, 0, 0);
       }
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) creg[kk] = cnext[kk];
     }
-    id = next;
-    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) creg[kk] = cnext[kk];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) { pwv[k] = pwn[k]; swv[k] = swn[k]; }
   }
+  __syncthreads();
   // den per query: slot m in lane m % 64, position m / 64 (M <= 128).
   for (int q = wave; q < kTileQ; q += kThreads / 64) {
-    float v0 = lane < M ? chsum[q][lane] : 0.0f;
-    float v1 = lane + 64 < M ? chsum[q][lane + 64] : 0.0f;
+    const float v0 = lane < M ? chsum[q][lane] : 0.0f;
+    const float v1 = lane + 64 < M ? chsum[q][lane + 64] : 0.0f;
     const float s = wave_sum_fold(M > 64 ? v0 + v1 : v0);
     if (lane == 0) den[q] = rbf(s);
   }

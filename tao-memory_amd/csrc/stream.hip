@@ -1,0 +1,224 @@
+// Native per-token decode driver (the host half of the decode step).
+//
+// Mirrors the reference's per-call control flow for a single new token
+// (tao_attention_decode -> StreamCache.process -> LayerState._read_progressive
+// -> _read_reused / HistoryRegionGraph.run -> seal; operator.py:130-138,
+// tao_stream.py:196-249, 919-969, history_region_graph.py:66-113) in C++, so
+// one ctypes call per token issues every launch: a route refresh on turn
+// positions, the fused decode step (eagerly or by replaying a hipGraph), and
+// the seal (writer + epilogue) when the local window reaches serve_limit.
+// Every count is a closed form of the cursor (the same formulas as the
+// Python host's schedule module).
+#include <cstring>
+
+#include "tao_launch.h"
+
+extern "C" int tao_route(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
+                         int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
+                         void* stream);
+extern "C" int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok,
+                               const tao_fusion* fu, int32_t selected, void* out,
+                               const int64_t* out_s, void* stream);
+extern "C" int tao_write_fine(const tao_state_dev* st, const tao_tokens* tok, int64_t new_base,
+                              const int64_t* start_pos, int32_t first_slot, int32_t count,
+                              void* stream);
+extern "C" int tao_seal_epilogue(const tao_state_dev* st, int32_t slot, int32_t pages,
+                                 int32_t recompute, void* stream);
+extern "C" int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu, int32_t selected,
+                                void* staging, void* out_stage, void* stream, void** graph_out);
+extern "C" int tao_graph_launch(void* graph, const tao_tokens* tok, void* stream);
+extern "C" int tao_graph_destroy(void* graph);
+
+namespace {
+
+struct Stream {
+  tao_state_dev st;
+  tao_stream_cfg cfg;
+  int64_t position = 0;
+  int32_t route_coarse = 0, route_size = 0;
+  void* staging = nullptr;
+  void* out_stage = nullptr;
+  void* graph = nullptr;
+  int32_t graph_selected = -1;
+  tao_fusion graph_fusion;
+  int64_t* seal_start = nullptr;   // device int64 (first word of the plan region)
+  int64_t seal_host = 0;           // host copy staged by the seal's upload
+};
+
+int64_t local_len_at(const tao_stream_cfg& c, int64_t p) {
+  const int64_t limit = c.local_keep + c.fine_tokens;
+  return p < limit ? p : c.local_keep + (p - limit) % c.fine_tokens;
+}
+
+int64_t fines_at(const tao_stream_cfg& c, int64_t p) {
+  const int64_t limit = c.local_keep + c.fine_tokens;
+  return p < limit ? 0 : (p - limit) / c.fine_tokens + 1;
+}
+
+bool is_turn(const tao_stream_cfg& c, int64_t p) {
+  const int64_t first = c.local_keep + c.fine_tokens;
+  const int64_t first_turn = first + (int64_t)c.layer_stagger * c.layer;
+  return p == first || (p >= first_turn && (p - first_turn) % c.route_period == 0);
+}
+
+int64_t budget(const tao_stream_cfg& c, int64_t n) {
+  if (n <= 0) return 0;
+  const int64_t target = (int64_t)c.budget_root_scale * n;
+  int64_t r = 0;
+  while ((r + 1) * (r + 1) <= target) ++r;    // isqrt (n is small)
+  if (r * r < target) ++r;
+  const int64_t b = r + c.budget_offset;
+  return b < n ? b : n;
+}
+
+void routed_counts(const tao_stream_cfg& c, int64_t completed, int64_t pending,
+                   int32_t* coarse_out, int32_t* selected_out) {
+  const int64_t g = c.coarse_group;
+  const int64_t cb = budget(c, g * completed);
+  int64_t coarse = (2 * cb + g - 1) / g;
+  if (coarse > completed) coarse = completed;
+  const int64_t eligible = g * coarse + pending;
+  int64_t sel = budget(c, g * completed + pending);
+  if (sel > eligible) sel = eligible;
+  *coarse_out = (int32_t)coarse;
+  *selected_out = (int32_t)sel;
+}
+
+int stream_fail(int code, const char* msg) {
+  tao::set_error(msg);
+  return code;
+}
+
+bool same_fusion(const tao_fusion& a, const tao_fusion& b) {
+  return a.fusion_a == b.fusion_a && a.fusion_b == b.fusion_b && a.dtype == b.dtype &&
+         a.gain == b.gain && std::memcmp(a.a_s, b.a_s, sizeof(a.a_s)) == 0 &&
+         std::memcmp(a.b_s, b.b_s, sizeof(a.b_s)) == 0;
+}
+
+void drop_graph(Stream* s) {
+  if (s->graph) tao_graph_destroy(s->graph);
+  s->graph = nullptr;
+  s->graph_selected = -1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tao_stream_open(const tao_state_dev* st, const tao_stream_cfg* cfg, int64_t position,
+                    int32_t route_coarse, int32_t route_size, void* staging, void* out_stage,
+                    void** handle) {
+  if (!st || !cfg || !handle) return stream_fail(TAO_E_ARGUMENT, "null stream argument");
+  if (cfg->route_period <= 0 || cfg->fine_tokens <= 0 || cfg->coarse_group <= 0)
+    return stream_fail(TAO_E_ARGUMENT, "invalid stream geometry");
+  Stream* s = new Stream();
+  s->st = *st;
+  s->cfg = *cfg;
+  s->position = position;
+  s->route_coarse = route_coarse;
+  s->route_size = route_size;
+  s->staging = staging;
+  s->out_stage = out_stage;
+  const tao::WorkspaceLayout lay =
+      tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
+  s->seal_start = (int64_t*)((char*)st->workspace + lay.plan_off);
+  *handle = s;
+  return TAO_OK;
+}
+
+int tao_stream_sync(void* handle, const tao_state_dev* st, int64_t position,
+                    int32_t route_coarse, int32_t route_size) {
+  if (!handle) return stream_fail(TAO_E_ARGUMENT, "null stream");
+  Stream* s = (Stream*)handle;
+  if (st && std::memcmp(st, &s->st, sizeof(*st)) != 0) {
+    drop_graph(s);
+    s->st = *st;
+    const tao::WorkspaceLayout lay =
+        tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
+    s->seal_start = (int64_t*)((char*)st->workspace + lay.plan_off);
+  }
+  s->position = position;
+  s->route_coarse = route_coarse;
+  s->route_size = route_size;
+  return TAO_OK;
+}
+
+int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu, void* out,
+                      const int64_t* out_s, void* stream, int64_t* info) {
+  if (!handle || !tok || !fu || !info) return stream_fail(TAO_E_ARGUMENT, "null decode argument");
+  Stream* s = (Stream*)handle;
+  const tao_stream_cfg& c = s->cfg;
+  const int64_t pos = s->position;
+  const int64_t fines = fines_at(c, pos);
+  int rc = TAO_OK;
+  int refreshed = 0, sealed = 0;
+  if (fines > 0 && is_turn(c, pos)) {
+    const int64_t completed = fines / c.coarse_group, pending = fines % c.coarse_group;
+    int32_t coarse = 0, selected = 0;
+    routed_counts(c, completed, pending, &coarse, &selected);
+    const int64_t rq_s[2] = {tok->rq_s[0], tok->rq_s[2]};
+    rc = tao_route(&s->st, tok->raw_q, rq_s, (int32_t)completed, (int32_t)pending, coarse,
+                   selected, stream);
+    if (rc) return rc;
+    s->route_coarse = coarse;
+    s->route_size = selected;
+    refreshed = 1;
+  }
+  const int32_t selected = fines > 0 ? s->route_size : 0;
+  tao_fusion f = *fu;
+  f.coarse_on = 0;
+  f.fine_on = fines > 0;
+  int used_graph = 0, captured = 0;
+  if (c.use_graph && fines > 0 && s->staging && s->out_stage) {
+    if (!s->graph || s->graph_selected != selected || !same_fusion(s->graph_fusion, f)) {
+      drop_graph(s);
+      rc = tao_graph_create(&s->st, &f, selected, s->staging, s->out_stage, stream, &s->graph);
+      if (rc) return rc;
+      s->graph_selected = selected;
+      s->graph_fusion = f;
+      captured = 1;
+    }
+    rc = tao_graph_launch(s->graph, tok, stream);
+    used_graph = 1;
+  } else {
+    rc = tao_decode_step(&s->st, tok, &f, selected, out, out_s, stream);
+  }
+  if (rc) return rc;
+  const int64_t limit = c.local_keep + c.fine_tokens;
+  if (local_len_at(c, pos) + 1 == limit) {
+    s->seal_host = pos + 1 - limit;
+    hipError_t e = hipMemcpyAsync(s->seal_start, &s->seal_host, sizeof(int64_t),
+                                  hipMemcpyHostToDevice, (hipStream_t)stream);
+    if (e != hipSuccess) return stream_fail((int)e, "seal start upload");
+    rc = tao_write_fine(&s->st, tok, pos + 1, s->seal_start, (int32_t)fines, 1, stream);
+    if (!rc) rc = tao_seal_epilogue(&s->st, (int32_t)fines,
+                                    (int32_t)(fines / c.coarse_group + 1), 1, stream);
+    if (rc) return rc;
+    sealed = 1;
+  }
+  s->position = pos + 1;
+  info[0] = s->position;
+  info[1] = s->route_coarse;
+  info[2] = s->route_size;
+  info[3] = refreshed;
+  info[4] = sealed;
+  info[5] = used_graph;
+  info[6] = captured;
+  return TAO_OK;
+}
+
+int tao_stream_release(void* handle) {
+  if (!handle) return TAO_OK;
+  drop_graph((Stream*)handle);
+  return TAO_OK;
+}
+
+int tao_stream_close(void* handle) {
+  if (!handle) return TAO_OK;
+  Stream* s = (Stream*)handle;
+  drop_graph(s);
+  delete s;
+  return TAO_OK;
+}
+
+}  // extern "C"

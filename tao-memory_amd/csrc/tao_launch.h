@@ -10,6 +10,9 @@
 
 namespace tao {
 
+// Record a message for tao_last_error() (thread-local).
+void set_error(const char* msg);
+
 constexpr int kThreads = 256;   // 4 wave64 per workgroup
 constexpr int kLocalSplits = 16; // split-K factor of single-query local attention
 

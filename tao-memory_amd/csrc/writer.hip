@@ -49,31 +49,45 @@ TAO_DEV const bf16_t* token_row(const WriterParams& p, int b, int h, long long p
   return ring + (((size_t)b * p.L + slot) * p.H + h) * D;
 }
 
+constexpr int kWriterThreads = 512;   // 8 waves
+
+// Stage raw_k and V of one block transposed into LDS ([channel][token]).
+// Every global load of the block is issued before the first LDS write.
 template <int D>
-__device__ void stage_transposed(const WriterParams& p, int b, int h, long long start,
-                                 const TokView& tv, const bf16_t* ring,
-                                 bf16_t (*dst)[kRowPad]) {
+__device__ void stage_block(const WriterParams& p, int b, int h, long long start,
+                            bf16_t (*kt)[kRowPad], bf16_t (*vt)[kRowPad]) {
   constexpr int CH = D / 8;
-  const int jobs = (kBlock / 2) * CH;
-  for (int job = threadIdx.x; job < jobs; job += kThreads) {
-    const int c = job % CH, pair = job / CH;
-    const int t0 = 2 * pair;
-    const uint4 a = *(const uint4*)(token_row(p, b, h, start + t0, tv, ring, D) + c * 8);
-    const uint4 bq = *(const uint4*)(token_row(p, b, h, start + t0 + 1, tv, ring, D) + c * 8);
-    const uint32_t wa[4] = {a.x, a.y, a.z, a.w};
-    const uint32_t wb[4] = {bq.x, bq.y, bq.z, bq.w};
+  constexpr int JOBS = (kBlock / 2) * CH / kWriterThreads;   // token pairs per thread
+  uint4 ka[JOBS], kb[JOBS], va[JOBS], vb[JOBS];
+#pragma unroll
+  for (int j = 0; j < JOBS; ++j) {
+    const int job = threadIdx.x + j * kWriterThreads;
+    const int c = job % CH, t0 = 2 * (job / CH);
+    ka[j] = *(const uint4*)(token_row(p, b, h, start + t0, p.rk, p.ring_raw, D) + c * 8);
+    kb[j] = *(const uint4*)(token_row(p, b, h, start + t0 + 1, p.rk, p.ring_raw, D) + c * 8);
+    va[j] = *(const uint4*)(token_row(p, b, h, start + t0, p.v, p.ring_v, D) + c * 8);
+    vb[j] = *(const uint4*)(token_row(p, b, h, start + t0 + 1, p.v, p.ring_v, D) + c * 8);
+  }
+#pragma unroll
+  for (int j = 0; j < JOBS; ++j) {
+    const int job = threadIdx.x + j * kWriterThreads;
+    const int c = job % CH, t0 = 2 * (job / CH);
+    const uint32_t wa[4] = {ka[j].x, ka[j].y, ka[j].z, ka[j].w};
+    const uint32_t wb[4] = {kb[j].x, kb[j].y, kb[j].z, kb[j].w};
+    const uint32_t xa[4] = {va[j].x, va[j].y, va[j].z, va[j].w};
+    const uint32_t xb[4] = {vb[j].x, vb[j].y, vb[j].z, vb[j].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = (wa[i] & 0xFFFFu) | (wb[i] << 16);
-      const uint32_t hi = (wa[i] >> 16) | (wb[i] & 0xFFFF0000u);
-      *(uint32_t*)&dst[c * 8 + 2 * i][t0] = lo;
-      *(uint32_t*)&dst[c * 8 + 2 * i + 1][t0] = hi;
+      *(uint32_t*)&kt[c * 8 + 2 * i][t0] = (wa[i] & 0xFFFFu) | (wb[i] << 16);
+      *(uint32_t*)&kt[c * 8 + 2 * i + 1][t0] = (wa[i] >> 16) | (wb[i] & 0xFFFF0000u);
+      *(uint32_t*)&vt[c * 8 + 2 * i][t0] = (xa[i] & 0xFFFFu) | (xb[i] << 16);
+      *(uint32_t*)&vt[c * 8 + 2 * i + 1][t0] = (xa[i] >> 16) | (xb[i] & 0xFFFF0000u);
     }
   }
 }
 
 template <int D>
-__global__ __launch_bounds__(kThreads) void writer_kernel(WriterParams p) {
+__global__ __launch_bounds__(kWriterThreads) void writer_kernel(WriterParams p) {
   __shared__ WriterSmem<D> sm;
   const int bh = blockIdx.x % (p.B * p.H);
   const int blk = blockIdx.x / (p.B * p.H);
@@ -82,13 +96,12 @@ __global__ __launch_bounds__(kThreads) void writer_kernel(WriterParams p) {
   const int slot = p.first_slot + blk;
   const int tid = threadIdx.x;
 
-  stage_transposed<D>(p, b, h, start, p.rk, p.ring_raw, sm.kt);
-  stage_transposed<D>(p, b, h, start, p.v, p.ring_v, sm.vt);
+  stage_block<D>(p, b, h, start, sm.kt, sm.vt);
   __syncthreads();
 
-  // ---- column softmax: jobs (channel, quarter)
+  // ---- column softmax: jobs (channel, quarter of 64 tokens)
   constexpr int QT = kBlock / 4;
-  for (int job = tid; job < 4 * D; job += kThreads) {
+  for (int job = tid; job < 4 * D; job += kWriterThreads) {
     const int d = job % D, qq = job / D;
     float m = -__builtin_inff();
     for (int t = 0; t < QT; t += 8) {
@@ -104,7 +117,7 @@ __global__ __launch_bounds__(kThreads) void writer_kernel(WriterParams p) {
   if (tid < D)
     sm.top[tid] = fmaxf(fmaxf(sm.part[0][tid], sm.part[1][tid]), fmaxf(sm.part[2][tid], sm.part[3][tid]));
   __syncthreads();
-  for (int job = tid; job < 4 * D; job += kThreads) {
+  for (int job = tid; job < 4 * D; job += kWriterThreads) {
     const int d = job % D, qq = job / D;
     const float m = sm.top[d];
     float acc = 0.0f;
@@ -134,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void writer_kernel(WriterParams p) {
     p.fine_z[((size_t)bh * p.fine_cap + slot) * D + tid] = f2bf(z);
   }
   __syncthreads();
-  for (int job = tid; job < 4 * D; job += kThreads) {
+  for (int job = tid; job < 4 * D; job += kWriterThreads) {
     const int d = job % D, qq = job / D;
     const float total = sm.total[d];
     for (int t = 0; t < QT; t += 8) {
@@ -153,33 +166,38 @@ __global__ __launch_bounds__(kThreads) void writer_kernel(WriterParams p) {
   __syncthreads();
 
   // ---- C^T = V^T P on MFMA 32x32x16 (the bank stores C^T[e][d], d
-  // contiguous): wave w owns rows e in [32w, 32w + 32) of C^T.
+  // contiguous): the (TILES x TILES) output tiles are spread over 8 waves.
   const int lane = tid & 63, wave = tid >> 6;
   const int li = lane & 31, lk = (lane >> 5) * 8;
-  constexpr int TILES = D / 32;                 // 32-wide tiles per dimension
+  constexpr int TILES = D / 32;
+  constexpr int PER_WAVE = (TILES * TILES + 7) / 8;
   bf16_t* cdst = p.bank + ((size_t)bh * p.fine_cap + slot) * D * D;
-  for (int rt = wave; rt < TILES; rt += kThreads / 64) {
-    floatx16 acc[TILES];
+  floatx16 acc[PER_WAVE];
 #pragma unroll
-    for (int ct = 0; ct < TILES; ++ct)
+  for (int t = 0; t < PER_WAVE; ++t)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[ct][i] = 0.0f;
+    for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+  const int tile0 = wave * PER_WAVE;
+  if (tile0 < TILES * TILES) {
     for (int k0 = 0; k0 < kBlock; k0 += 16) {
-      const bf16x8 a = *(const bf16x8*)&sm.vt[rt * 32 + li][k0 + lk];
 #pragma unroll
-      for (int ct = 0; ct < TILES; ++ct) {
+      for (int t = 0; t < PER_WAVE; ++t) {
+        const int rt = (tile0 + t) / TILES, ct = (tile0 + t) % TILES;
+        const bf16x8 a = *(const bf16x8*)&sm.vt[rt * 32 + li][k0 + lk];
         const bf16x8 bv = *(const bf16x8*)&sm.kt[ct * 32 + li][k0 + lk];
-        acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bv, acc[ct], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bv, acc[t], 0, 0, 0);
       }
     }
     // D layout: lane holds column li (d), rows (e) 8*(i/4) + 4*(lane/32) + i%4.
 #pragma unroll
-    for (int ct = 0; ct < TILES; ++ct)
+    for (int t = 0; t < PER_WAVE; ++t) {
+      const int rt = (tile0 + t) / TILES, ct = (tile0 + t) % TILES;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = rt * 32 + 8 * (i / 4) + 4 * (lane >> 5) + (i % 4);
-        cdst[(size_t)row * D + ct * 32 + li] = f2bf(acc[ct][i]);
+        cdst[(size_t)row * D + ct * 32 + li] = f2bf(acc[t][i]);
       }
+    }
   }
 }
 
@@ -249,9 +267,9 @@ hipError_t launch_writer(const WriterParams& p, int head_dim, hipStream_t s) {
   if (p.count <= 0) return hipSuccess;
   const dim3 grid((unsigned)(p.count * p.B * p.H));
   if (head_dim == 128)
-    hipLaunchKernelGGL(writer_kernel<128>, grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL(writer_kernel<128>, grid, dim3(kWriterThreads), 0, s, p);
   else if (head_dim == 64)
-    hipLaunchKernelGGL(writer_kernel<64>, grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL(writer_kernel<64>, grid, dim3(kWriterThreads), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

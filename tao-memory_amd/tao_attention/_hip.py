@@ -47,6 +47,12 @@ class PrefillPools(ctypes.Structure):
                 ("pool_pcap", _i32), ("epochs", _i32), ("sel_slots", _i32)]
 
 
+class StreamCfg(ctypes.Structure):
+    _fields_ = [("layer", _i32), ("local_keep", _i32), ("fine_tokens", _i32),
+                ("coarse_group", _i32), ("route_period", _i32), ("layer_stagger", _i32),
+                ("budget_root_scale", _i32), ("budget_offset", _i32), ("use_graph", _i32)]
+
+
 PLAN_HEADER = 16
 
 
@@ -77,6 +83,13 @@ _SIGNATURES = {
                      ctypes.POINTER(_i64), _vp], _i32),
     "tao_ring_append": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i32, _i32,
                          _i64, _vp], _i32),
+    "tao_stream_open": ([ctypes.POINTER(StateDev), ctypes.POINTER(StreamCfg), _i64, _i32, _i32,
+                         _vp, _vp, ctypes.POINTER(_vp)], _i32),
+    "tao_stream_sync": ([_vp, ctypes.POINTER(StateDev), _i64, _i32, _i32], _i32),
+    "tao_stream_decode": ([_vp, ctypes.POINTER(Tokens), ctypes.POINTER(Fusion), _vp,
+                           ctypes.POINTER(_i64), _vp, ctypes.POINTER(_i64)], _i32),
+    "tao_stream_release": ([_vp], _i32),
+    "tao_stream_close": ([_vp], _i32),
     "tao_graph_create": ([ctypes.POINTER(StateDev), ctypes.POINTER(Fusion), _i32, _vp, _vp,
                           _vp, ctypes.POINTER(_vp)], _i32),
     "tao_graph_launch": ([_vp, ctypes.POINTER(Tokens), _vp], _i32),
@@ -122,12 +135,29 @@ def require_device(tensor):
         raise RuntimeError("TaoMemory HIP path needs device tensors (no CPU fallback)")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """The caller's current HIP stream on `device` (raw handle)."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 def i64x3(values):
     return _I64x3(*[int(x) for x in values])
+
+
+def vector_ready(t):
+    """Rows load as 16-byte vectors: unit last stride, 8-element strides, aligned base."""
+    st = t.stride()
+    return st[-1] == 1 and all(x % 8 == 0 for x in st[:-1]) and t.data_ptr() % 16 == 0
+
+
+def vector_operands(*tensors):
+    """The operands, copied to contiguous storage where a row is not 16-byte aligned."""
+    return tuple(t if vector_ready(t) else t.contiguous() for t in tensors)
 
 
 def strides_bth(t):
@@ -159,18 +189,22 @@ _FUSION_CACHE = {}
 
 
 def fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on):
-    """Fusion struct, cached per (parameter buffers, dtypes, alpha, presence).
+    """Fusion struct, cached per (parameter tensors, alpha, presence).
 
     Parameters stay read in place by the kernels, so in-place updates of
-    fp32/bf16 fusion tensors are seen by later calls.
+    fp32/bf16 fusion tensors are seen by later calls; a tensor whose storage
+    or layout changed gets a new struct.
     """
-    key = (fusion_a.data_ptr(), fusion_b.data_ptr(), fusion_a.dtype, fusion_b.dtype,
-           fusion_a.stride(), fusion_b.stride(), float(alpha), bool(coarse_on),
-           bool(fine_on), fusion_a.device)
+    key = (id(fusion_a), id(fusion_b), alpha, coarse_on, fine_on)
     hit = _FUSION_CACHE.get(key)
-    if hit is not None and hit._keep[2] is fusion_a and hit._keep[3] is fusion_b:
+    if (hit is not None and hit._keep[2] is fusion_a and hit._keep[3] is fusion_b
+            and hit._check == (fusion_a.data_ptr(), fusion_b.data_ptr(),
+                               fusion_a.stride(), fusion_b.stride(),
+                               fusion_a.dtype, fusion_b.dtype)):
         return hit
     fu = _make_fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on)
+    fu._check = (fusion_a.data_ptr(), fusion_b.data_ptr(), fusion_a.stride(),
+                 fusion_b.stride(), fusion_a.dtype, fusion_b.dtype)
     if len(_FUSION_CACHE) > 64:
         _FUSION_CACHE.clear()
     _FUSION_CACHE[key] = fu

@@ -14,7 +14,7 @@ import torch
 from . import _hip
 
 USE_FA3 = False
-_QTILE = 128
+_QTILE = 256
 
 
 def _bare_state(q):
@@ -42,7 +42,7 @@ def flash_attn_func(q, k, v, causal=True, window_size=(-1, 0)):
     tq, tk = q.shape[1], k.shape[1]
     if tq > tk:
         raise ValueError("queries must be a suffix of the keys")
-    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    q, k, v = _hip.vector_operands(q, k, v)
     out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
     if tq == 0:
         return out

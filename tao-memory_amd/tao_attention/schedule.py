@@ -85,3 +85,22 @@ def sub_chunks(start, width, layer, config):
         out.append((absolute, count, is_turn(absolute, layer, config)))
         offset += count
     return out
+
+
+def count_turns(lo, hi, layer, config):
+    """Number of refresh positions in [lo, hi) (closed form of is_turn)."""
+    if hi <= lo:
+        return 0
+    first = config.first_fine
+    first_turn = first + config.layer_stagger * layer
+    period = config.route_period
+    count = 0
+    if lo <= first < hi and first < first_turn:
+        count += 1
+    start = max(lo, first_turn)
+    if start < hi:
+        k0 = -(-(start - first_turn) // period)
+        k1 = (hi - 1 - first_turn) // period
+        count += max(0, k1 - k0 + 1)
+    return count
+

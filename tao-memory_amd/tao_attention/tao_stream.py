@@ -23,13 +23,14 @@ cursor (schedule.py), so no device-to-host synchronisation is needed.
 import contextlib
 import ctypes
 
+import numpy as np
 import torch
 
 from . import _hip, schedule
 from .config import TaoConfig
 
 DEFAULT_CONFIG = TaoConfig()
-_QTILE = 128
+_QTILE = 256
 
 
 class _DeviceState:
@@ -134,64 +135,44 @@ class _DeviceState:
 
 
 class HistoryRegionGraph:
-    """hipGraph of the single-token decode step (history_region_graph.py:10-113).
+    """Counters of the decode-step hipGraph (history_region_graph.py:10-113).
 
-    One captured graph per (state buffers, route size); the step's position
-    and route ids live in device memory, so seals and refreshes replay the
-    same graph. Counters keep the reference's observation() keys.
+    The graph itself lives in the native stream driver (stream.hip): one
+    captured graph per (state buffers, route size, fusion parameters), replayed
+    across seals and refreshes because the position and route ids are
+    device-resident. These counters keep the reference's observation() keys.
     """
 
     def __init__(self):
-        self.handle = None
-        self.key = None
-        self.staging = None
-        self.out_stage = None
         self.counts = dict(epochs=0, eager_warm=0, captures=0, replays=0,
                            id_copies=0, invalidations=0)
         self.reasons = {}
         self.last_action = "uninitialized"
+        self.active = False
 
     def observation(self):
-        return {**self.counts, "active_graph": self.handle is not None,
-                "active_staging": self.staging is not None,
-                "epoch_state_version": None if self.key is None else self.key[0],
+        return {**self.counts, "active_graph": self.active,
                 "last_action": self.last_action,
                 "invalidation_reasons": dict(self.reasons)}
 
+    def record(self, used_graph, captured):
+        if captured:
+            self.counts["captures"] += 1
+            self.counts["epochs"] += 1
+            self.last_action = "capture_replay"
+        elif used_graph:
+            self.last_action = "replay"
+        if used_graph:
+            self.counts["replays"] += 1
+            self.active = True
+
     def invalidate(self, reason):
-        if self.handle is None and self.key is None:
+        if not self.active:
             return
-        if self.staging is not None:
-            torch.cuda.current_stream(self.staging.device).synchronize()
-        if self.handle is not None:
-            _hip.check(_hip.lib().tao_graph_destroy(self.handle))
-        self.handle = self.key = None
-        self.staging = self.out_stage = None
+        self.active = False
         self.counts["invalidations"] += 1
         self.reasons[reason] = self.reasons.get(reason, 0) + 1
         self.last_action = "invalidate:" + reason
-
-    def run(self, dev, fu, selected, tok, key):
-        if key != self.key:
-            self.invalidate("epoch_change")
-            B, H, D = dev.B, dev.H, dev.D
-            self.staging = torch.empty(5 * B * H * D, dtype=torch.bfloat16, device=dev.device)
-            self.out_stage = torch.empty((B, 1, H, D), dtype=torch.bfloat16, device=dev.device)
-            handle = ctypes.c_void_p()
-            _hip.check(_hip.lib().tao_graph_create(
-                ctypes.byref(dev.struct), ctypes.byref(fu), selected,
-                self.staging.data_ptr(), self.out_stage.data_ptr(), dev.stream(),
-                ctypes.byref(handle)))
-            self.handle = handle
-            self.key = key
-            self.counts["epochs"] += 1
-            self.counts["captures"] += 1
-            self.last_action = "capture_replay"
-        else:
-            self.last_action = "replay"
-        _hip.check(_hip.lib().tao_graph_launch(self.handle, ctypes.byref(tok), dev.stream()))
-        self.counts["replays"] += 1
-        return self.out_stage
 
 
 class StreamCache:
@@ -225,6 +206,12 @@ class StreamCache:
         # each kernel launch (used by bench.py for live kernel timing).
         self._probe = None
         self._tok = None
+        self._handle = None          # native stream driver (stream.hip)
+        self._handle_dirty = True
+        self._decode_key = None
+        self._decode_limit = -1
+        self._graph_buffers = None
+        self._info = (ctypes.c_int64 * 7)()
 
     # ------------------------------------------------------------------ cursor
     def get_pos(self):
@@ -241,10 +228,28 @@ class StreamCache:
     def release_execution(self, reason="request_end"):
         if self.history_region is not None:
             self.history_region.invalidate(reason)
+        if self._handle is not None:
+            if self._dev is not None:
+                torch.cuda.current_stream(self._dev.device).synchronize()
+            _hip.check(_hip.lib().tao_stream_release(self._handle))
+
+    def _close_driver(self):
+        if self._handle is not None:
+            if self._dev is not None:
+                torch.cuda.current_stream(self._dev.device).synchronize()
+            _hip.lib().tao_stream_close(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self._close_driver()
+        except Exception:
+            pass
 
     def reset(self):
         """Discard this request's state; position returns to zero."""
         self.release_execution("reset")
+        self._close_driver()
         self.__init__(self.layer_index, self.route_interval, self.fusion_mode,
                       self.pending_coarse_elision, self.pending_coarse_mask,
                       self.fused_fine, self.config)
@@ -277,6 +282,7 @@ class StreamCache:
             raise ValueError("batch/heads/width/device must stay fixed for a state")
         elif self._dev.reserve(fines, schedule.fines_at(self.position, self.config)):
             self.release_execution("capacity")
+            self._handle_dirty = True
         return self._dev
 
     # ----------------------------------------------------------------- kernels
@@ -389,9 +395,11 @@ class StreamCache:
                           pool_pcap=f1 // group + 1, chunk_epochs=chunk_epochs)
 
     def _run_plan(self, dev, tok, fu, plan, info, local, out):
-        plan_arr = (ctypes.c_int64 * len(plan))(*plan)
+        plan_np = np.asarray(plan, dtype=np.int64)
+        plan_arr = plan_np.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
         if dev.ensure_plan(len(plan)):
             self.release_execution("capacity")
+            self._handle_dirty = True
         pools = _hip.PrefillPools()
         keep = []
         if info["epochs"] or info["turns"]:
@@ -424,8 +432,7 @@ class StreamCache:
         pos0 = self.position
         tokens = q.shape[1]
         dev = self._device_for(q, pos0 + tokens)
-        q, k, v, raw_q, raw_k = (t if t.stride(-1) == 1 else t.contiguous()
-                                 for t in (q, k, v, raw_q, raw_k))
+        q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
         plan, info = self._plan(pos0, tokens, outputs=True)
         local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
@@ -444,52 +451,100 @@ class StreamCache:
         cfg = self.config
         end = pos0 + tokens
         self.fine_seal_events += schedule.fines_at(end, cfg) - schedule.fines_at(pos0, cfg)
-        self.route_refreshes += sum(
-            1 for p in range(max(pos0, cfg.first_fine), end)
-            if schedule.is_turn(p, self.layer_index, cfg))
+        self.route_refreshes += schedule.count_turns(pos0, end, self.layer_index, cfg)
         self.route_coarse, self.route_size = info["route"]
         self.peak_selected_fine = max(self.peak_selected_fine, self.route_size)
         self.position = end
         self._dev.header[0:1].fill_(end)
+        self._handle_dirty = True
+
+    def _driver(self, dev):
+        """Native per-token driver bound to the current buffers and cursor."""
+        cfg = self.config
+        if self._handle is None:
+            scfg = _hip.StreamCfg(self.layer_index, cfg.local_keep, cfg.fine_tokens,
+                                  cfg.coarse_group, cfg.route_period, cfg.layer_stagger,
+                                  cfg.budget_root_scale, cfg.budget_offset,
+                                  int(cfg.q1_history_region_graph))
+            staging = out_stage = None
+            if cfg.q1_history_region_graph:
+                B, H, D = dev.B, dev.H, dev.D
+                staging = torch.empty(5 * B * H * D, dtype=torch.bfloat16, device=dev.device)
+                out_stage = torch.empty((B, 1, H, D), dtype=torch.bfloat16, device=dev.device)
+                self._graph_buffers = (staging, out_stage)
+            handle = ctypes.c_void_p()
+            _hip.check(_hip.lib().tao_stream_open(
+                ctypes.byref(dev.struct), ctypes.byref(scfg), self.position, self.route_coarse,
+                self.route_size, staging.data_ptr() if staging is not None else None,
+                out_stage.data_ptr() if out_stage is not None else None, ctypes.byref(handle)))
+            self._handle = handle
+        elif self._handle_dirty:
+            _hip.check(_hip.lib().tao_stream_sync(
+                self._handle, ctypes.byref(dev.struct), self.position, self.route_coarse,
+                self.route_size))
+        self._handle_dirty = False
+        return self._handle
 
     def decode(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
-        """One new token; returns the fused heads [B, 1, H, D]."""
-        self._check_supported(q)
-        cfg = self.config
+        """One new token; returns the fused heads [B, 1, H, D].
+
+        With the hipGraph preset the returned tensor is the graph's output
+        buffer, overwritten by the next replay (as the reference's regional
+        graph returns its captured outputs).
+        """
         pos = self.position
-        dev = self._device_for(q, pos + 1)
-        if not (q.stride(-1) == k.stride(-1) == v.stride(-1) == raw_q.stride(-1)
-                == raw_k.stride(-1) == 1):
-            q, k, v, raw_q, raw_k = (t.contiguous() for t in (q, k, v, raw_q, raw_k))
-        tok = self._tok = _hip.tokens(q, k, v, raw_q, raw_k, self._tok)
-        fines = schedule.fines_at(pos, cfg)
-        fine_on = fines > 0
-        if fine_on and schedule.is_turn(pos, self.layer_index, cfg):
-            self._route(dev, raw_q[:, 0], fines)
-        selected = self.route_size if fine_on else 0
-        fu = _hip.fusion(fusion_a, fusion_b, alpha, False, fine_on)
-        if cfg.q1_history_region_graph and fine_on:
-            if self.history_region is None:
-                self.history_region = HistoryRegionGraph()
-            key = (selected, dev.bank.data_ptr(), dev.workspace.data_ptr(),
-                   fusion_a.data_ptr(), fusion_b.data_ptr(), fu.dtype, fu.gain)
-            with self._timed("decode_step"):
-                out = self.history_region.run(dev, fu, selected, tok, key)
-            self.history_region.fusion_keep = fu
+        key = (q.shape, q.dtype, q.device)
+        if key != self._decode_key or pos + 1 > self._decode_limit or self._dev is None:
+            self._check_supported(q)
+            dev = self._device_for(q, pos + 1)
+            cap = dev.fine_cap
+            # Last cursor whose decode still fits the bank without growing.
+            self._decode_limit = self.config.serve_limit - 1 + cap * self.config.fine_tokens
+            self._decode_key = key
+        dev = self._dev
+        tok = self._tok
+        strides = (q.stride(), k.stride(), v.stride(), raw_q.stride(), raw_k.stride())
+        if tok is None or tok._strides != strides:
+            q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
+            tok = self._tok = _hip.tokens(q, k, v, raw_q, raw_k)
+        else:
+            ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), raw_q.data_ptr(), raw_k.data_ptr())
+            if (ptrs[0] | ptrs[1] | ptrs[2] | ptrs[3] | ptrs[4]) & 15:
+                q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
+                tok = self._tok = _hip.tokens(q, k, v, raw_q, raw_k)
+            else:
+                tok.q, tok.k, tok.v, tok.raw_q, tok.raw_k = ptrs
+        fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True)
+        handle = self._driver(dev)
+        graph = self.config.q1_history_region_graph and schedule.fines_at(pos, self.config) > 0
+        if graph:
+            out = None
+            out_ptr, out_s = None, None
         else:
             out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+            out_ptr = out.data_ptr()
             out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
-            with self._timed("decode_step"):
-                _hip.check(_hip.lib().tao_decode_step(
-                    ctypes.byref(dev.struct), ctypes.byref(tok), ctypes.byref(fu), selected,
-                    out.data_ptr(), out_s, dev.stream()))
-        if fine_on:
+        info = self._info
+        with self._timed("decode_step"):
+            _hip.check(_hip.lib().tao_stream_decode(handle, ctypes.byref(tok), ctypes.byref(fu),
+                                                    out_ptr, out_s, dev.stream(), info))
+        self.position = info[0]
+        self.route_coarse, self.route_size = info[1], info[2]
+        if info[3]:
+            self.route_refreshes += 1
+            self.peak_selected_fine = max(self.peak_selected_fine, self.route_size)
+        if info[4]:
+            self.fine_seal_events += 1
+        if pos >= self.config.first_fine:
             self.fusion_pointwise_calls += 1
         else:
             self.fusion_no_history_local_returns += 1
-        if schedule.local_len_at(pos, cfg) + 1 == cfg.serve_limit:
-            self._seal(dev, tok, pos + 1, pos + 1 - cfg.serve_limit, fines)
-        self.position = pos + 1
+        if info[5] or info[6]:
+            if self.history_region is None:
+                self.history_region = HistoryRegionGraph()
+            self.history_region.record(info[5], info[6])
+        if graph:
+            return self._graph_buffers[1]
         return out
 
     def _launch_prompt_kernels(self, q, k, v, raw_q, raw_k):
@@ -502,6 +557,7 @@ class StreamCache:
         pos0 = self.position
         tokens = q.shape[1]
         dev = self._device_for(q, pos0 + tokens)
+        q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
         plan, _ = self._plan(pos0, tokens, outputs=True)
         n_attn, n_write = plan[1], plan[2]
@@ -533,8 +589,7 @@ class StreamCache:
         pos0 = self.position
         tokens = q.shape[1]
         dev = self._device_for(q, pos0 + tokens)
-        q, k, v, raw_q, raw_k = (t if t.stride(-1) == 1 else t.contiguous()
-                                 for t in (q, k, v, raw_q, raw_k))
+        q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
         plan, info = self._plan(pos0, tokens, outputs=False)
         fu = _hip.fusion(torch.zeros(1, device=q.device), torch.zeros(1, device=q.device),

@@ -103,3 +103,12 @@ def test_product_has_no_oracle_or_cpu_path():
         if name.endswith(".py"):
             text = open(os.path.join(pkg, name)).read()
             assert "oracle" not in text.replace("oracles", ""), name
+
+
+def test_count_turns_closed_form():
+    cfg = index_only_page_memo()
+    for layer in (0, 1, 5, 40):
+        for lo in (0, 700, 768, 769, 800, 1000):
+            for hi in (lo, lo + 1, lo + 23, lo + 24, lo + 500, lo + 3000):
+                brute = sum(1 for p in range(lo, hi) if schedule.is_turn(p, layer, cfg))
+                assert schedule.count_turns(lo, hi, layer, cfg) == brute, (layer, lo, hi)

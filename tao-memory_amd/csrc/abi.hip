@@ -104,6 +104,7 @@ tao::DecodeParams decode_params(const tao_state_dev* st, const tao_tokens* tok,
   p.fine_cap = st->fine_cap;
   p.page_cap = st->page_cap;
   p.sel_cap = st->sel_cap;
+  p.pos_hint = -1;
   return p;
 }
 
@@ -140,11 +141,27 @@ WorkspaceLayout workspace_layout(int batch, int heads, int head_dim, int sel_cap
   WorkspaceLayout lay;
   const size_t bh = (size_t)batch * heads;
   lay.parts_off = 0;
-  const size_t parts = bh * (kLocalSplits + (size_t)sel_cap) * (head_dim + 4) * sizeof(float);
+  const size_t parts = bh * step_floats(head_dim, sel_cap) * sizeof(float);
   lay.plan_off = align(parts);
   lay.plan_words = plan_words > 0 ? (size_t)plan_words : 0;
   lay.total = align(lay.plan_off + lay.plan_words * sizeof(int64_t));
   return lay;
+}
+
+int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
+                   int32_t selected, void* out, const int64_t* out_s, void* stream,
+                   long long position) {
+  int rc = check_state(st);
+  if (!rc) rc = check_tokens(tok);
+  if (!rc) rc = check_fusion(fu);
+  if (rc) return rc;
+  if (tok->tokens != 1) return fail(TAO_E_SHAPE, "decode step takes exactly one token");
+  if (!out || !out_s) return fail(TAO_E_ARGUMENT, "null output");
+  if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected count exceeds sel_cap");
+  tao::DecodeParams p = decode_params(st, tok, fu, out, out_s);
+  p.pos_hint = position;
+  return check_hip(tao::launch_decode_step(p, st->head_dim, selected, (hipStream_t)stream),
+                   "tao_decode_step");
 }
 
 }  // namespace tao
@@ -169,16 +186,7 @@ int tao_workspace_init(const tao_state_dev* st, void* stream) {
 
 int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
                     int32_t selected, void* out, const int64_t* out_s, void* stream) {
-  int rc = check_state(st);
-  if (!rc) rc = check_tokens(tok);
-  if (!rc) rc = check_fusion(fu);
-  if (rc) return rc;
-  if (tok->tokens != 1) return fail(TAO_E_SHAPE, "decode step takes exactly one token");
-  if (!out || !out_s) return fail(TAO_E_ARGUMENT, "null output");
-  if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected count exceeds sel_cap");
-  const tao::DecodeParams p = decode_params(st, tok, fu, out, out_s);
-  return check_hip(tao::launch_decode_step(p, st->head_dim, selected, (hipStream_t)stream),
-                   "tao_decode_step");
+  return tao::decode_step_at(st, tok, fu, selected, out, out_s, stream, -1);
 }
 
 int tao_route(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,

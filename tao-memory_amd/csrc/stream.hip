@@ -16,9 +16,6 @@
 extern "C" int tao_route(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
                          int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
                          void* stream);
-extern "C" int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok,
-                               const tao_fusion* fu, int32_t selected, void* out,
-                               const int64_t* out_s, void* stream);
 extern "C" int tao_write_fine(const tao_state_dev* st, const tao_tokens* tok, int64_t new_base,
                               const int64_t* start_pos, int32_t first_slot, int32_t count,
                               void* stream);
@@ -181,7 +178,7 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
     rc = tao_graph_launch(s->graph, tok, stream);
     used_graph = 1;
   } else {
-    rc = tao_decode_step(&s->st, tok, &f, selected, out, out_s, stream);
+    rc = tao::decode_step_at(&s->st, tok, &f, selected, out, out_s, stream, pos);
   }
   if (rc) return rc;
   const int64_t limit = c.local_keep + c.fine_tokens;

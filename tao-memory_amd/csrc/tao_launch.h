@@ -14,10 +14,28 @@ namespace tao {
 void set_error(const char* msg);
 
 constexpr int kThreads = 256;   // 4 wave64 per workgroup
-constexpr int kLocalSplits = 16; // split-K factor of single-query local attention
+constexpr int kMaxWindow = 768;   // serve_limit = local_keep + fine_tokens
+#ifndef TAO_FINE_UNITS
+#define TAO_FINE_UNITS 8
+#endif
+constexpr int kFineUnits = TAO_FINE_UNITS;   // decode fine workgroups per (batch, head)
+constexpr int kStepRec = 4;       // header floats of one decode record
+
+// Local-attention workgroups per (batch, head): D / 2 keys each.
+__host__ __device__ constexpr int local_units(int head_dim) {
+  return (kMaxWindow + head_dim / 2 - 1) / (head_dim / 2);
+}
+
+// Per (batch, head) decode scratch, in floats: local_units(D) local records
+// and kFineUnits fine records of (kStepRec + D) floats, then one den term
+// per selected slot.
+__host__ __device__ inline size_t step_floats(int head_dim, int sel_cap) {
+  return (size_t)(local_units(head_dim) + kFineUnits) * (head_dim + kStepRec) +
+         (size_t)sel_cap;
+}
 
 // Workspace layout (bytes from the start of tao_state_dev::workspace):
-//   [0, plan_off)         fp32 decode unit records [B*H][kLocalSplits + sel_cap][D + 4]
+//   [0, plan_off)         fp32 decode scratch [B*H][step_floats(D, sel_cap)]
 //   [plan_off, total)     int64 prefill plan (plan_words)
 struct WorkspaceLayout {
   size_t parts_off, plan_off, plan_words, total;
@@ -42,12 +60,19 @@ struct DecodeParams {
   int64_t fa_s[3], fb_s[3];
   float gain;
   bf16_t* out; int64_t out_sb, out_sh;
-  float* parts; uint32_t* counters;
+  float* parts;
+  long long pos_hint;   // cursor of this step, or -1: read header[0]
   int B, H, keep, fine, group, fine_cap, page_cap, sel_cap;
 };
 
 // M = selected fines of the current route (0 before the first seal).
 hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStream_t s);
+
+// tao_decode_step with the step's cursor given by the caller (position >= 0)
+// instead of read from header[0] on the device; used by the stream driver.
+int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
+                   int32_t selected, void* out, const int64_t* out_s, void* stream,
+                   long long position);
 
 struct StageParams {
   TokView src[5];

@@ -188,20 +188,31 @@ def tokens(q, k, v, raw_q, raw_k, reuse=None):
 _FUSION_CACHE = {}
 
 
-def fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on):
+def fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on, like=None):
     """Fusion struct, cached per (parameter tensors, alpha, presence).
 
     Parameters stay read in place by the kernels, so in-place updates of
     fp32/bf16 fusion tensors are seen by later calls; a tensor whose storage
     or layout changed gets a new struct.
     """
-    key = (id(fusion_a), id(fusion_b), alpha, coarse_on, fine_on)
+    key = (id(fusion_a), id(fusion_b), alpha, coarse_on, fine_on,
+           None if like is None else (like.shape[2], like.shape[3], like.device))
     hit = _FUSION_CACHE.get(key)
     if (hit is not None and hit._keep[2] is fusion_a and hit._keep[3] is fusion_b
             and hit._check == (fusion_a.data_ptr(), fusion_b.data_ptr(),
                                fusion_a.stride(), fusion_b.stride(),
                                fusion_a.dtype, fusion_b.dtype)):
         return hit
+    if like is not None:
+        # The kernels read fusion_*[h, d, i] for every head and channel of the
+        # operands (operator.py:83-89 takes [H, D, 3] parameters).
+        _, _, heads, width = like.shape
+        for t in (fusion_a, fusion_b):
+            if tuple(t.shape) != (heads, width, 3):
+                raise ValueError(f"fusion parameters must be [{heads}, {width}, 3], "
+                                 f"got {tuple(t.shape)}")
+            if t.device != like.device:
+                raise ValueError("fusion parameters must live on the operands' device")
     fu = _make_fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on)
     fu._check = (fusion_a.data_ptr(), fusion_b.data_ptr(), fusion_a.stride(),
                  fusion_b.stride(), fusion_a.dtype, fusion_b.dtype)

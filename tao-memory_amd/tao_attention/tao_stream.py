@@ -437,7 +437,7 @@ class StreamCache:
         plan, info = self._plan(pos0, tokens, outputs=True)
         local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
         out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
-        fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True)
+        fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
         self._run_plan(dev, tok, fu, plan, info, local, out)
         self._advance(pos0, tokens, info)
         for epoch in info["chunk_epochs"]:
@@ -493,8 +493,15 @@ class StreamCache:
         graph returns its captured outputs).
         """
         pos = self.position
-        key = (q.shape, q.dtype, q.device)
+        shape = q.shape
+        if (k.shape, v.shape, raw_q.shape, raw_k.shape) != (shape, shape, shape, shape):
+            raise ValueError("q, k, v, raw_q and raw_k must share one [B, 1, H, D] shape")
+        key = (shape, q.dtype, k.dtype, v.dtype, raw_q.dtype, raw_k.dtype,
+               q.device, k.device, v.device, raw_q.device, raw_k.device)
         if key != self._decode_key or pos + 1 > self._decode_limit or self._dev is None:
+            for x in (k, v, raw_q, raw_k):
+                if x.dtype != q.dtype or x.device != q.device:
+                    raise TypeError("q, k, v, raw_q and raw_k must share dtype and device")
             self._check_supported(q)
             dev = self._device_for(q, pos + 1)
             cap = dev.fine_cap
@@ -514,7 +521,7 @@ class StreamCache:
                 tok = self._tok = _hip.tokens(q, k, v, raw_q, raw_k)
             else:
                 tok.q, tok.k, tok.v, tok.raw_q, tok.raw_k = ptrs
-        fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True)
+        fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
         handle = self._driver(dev)
         graph = self.config.q1_history_region_graph and schedule.fines_at(pos, self.config) > 0
         if graph:

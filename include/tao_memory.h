@@ -60,7 +60,7 @@ typedef struct tao_state_dev {
   int32_t* sel;     /* [B, H, sel_cap]  selected fine ids, score order */
   int32_t* chosen;  /* [B, H, chosen_cap] chosen coarse pages, ascending */
   int64_t* header;  /* device [4]: position, M, reserved, reserved */
-  void* workspace;  /* scratch: per-unit partials and arrival counters */
+  void* workspace;  /* scratch: decode step records and the prefill plan */
   size_t workspace_bytes;
 } tao_state_dev;
 

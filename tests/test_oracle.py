@@ -183,6 +183,36 @@ def test_fusion_closed_form():
     torch.testing.assert_close(out.double(), ref, atol=5e-2, rtol=3e-2)
 
 
+def test_normalisation_properties():
+    """Segment weights of a page sum to one (pz = logsumexp of the page's z);
+    page weights sum to one over pages, h over channels; hv is the rounded
+    product of the matching page row. A sign flip in z - pz, a softmax over
+    the wrong axis or a mis-broadcast page index fails one of these."""
+    torch.manual_seed(11)
+    b, h, pages, d = 1, 3, 4, 16
+    z = (torch.randn(b, h, pages * 8, d) * 2).to(BF16)
+    pz = torch.stack([O.page_summary(z[:, :, 8 * p:8 * p + 8]) for p in range(pages)], 2)
+    sw = O.segment_weights(z, pz.repeat_interleave(8, dim=2))
+    sums = sw.double().reshape(b, h, pages, 8, d).sum(3)
+    torch.testing.assert_close(sums, torch.ones_like(sums), atol=3e-2, rtol=0)
+    assert (sw.double() <= 1.0 + 1e-2).all()
+    exact = torch.logsumexp(z.double().reshape(b, h, pages, 8, d), 3)
+    torch.testing.assert_close(pz.double(), exact, atol=3e-2, rtol=1e-2)
+    pw = O.page_weights(pz)
+    torch.testing.assert_close(pw.double().sum(2), torch.ones(b, h, d, dtype=torch.float64),
+                               atol=3e-2, rtol=0)
+    raw_q = torch.randn(b, 2, h, d).to(BF16)
+    hq = O.query_weights(raw_q)
+    torch.testing.assert_close(hq.double().sum(-1), torch.ones(b, 2, h, dtype=torch.float64),
+                               atol=3e-2, rtol=0)
+    hv = O.page_values(hq, pw)
+    assert hv.shape == (b, 2, h, pages, d)
+    for qi in range(2):
+        for p in range(pages):
+            ref = (hq[0, qi].double() * pw[0, :, p].double())
+            torch.testing.assert_close(hv[0, qi, :, p].double(), ref, atol=0, rtol=2 ** -8)
+
+
 # ------------------------------------------------------------------- routing
 def _sorted_topk(scores, count):
     order = sorted(range(len(scores)), key=lambda i: (-scores[i], i))

@@ -32,6 +32,12 @@ HBM_PEAK_GBS = 8000.0
 SPIN_CYCLES = 4_000_000        # bounded spin that keeps the queue ahead of the host
 STEPS_PER_SPIN = 16
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# HBM-side bytes of one decode step (decode_units_kernel<128> +
+# decode_combine_kernel<128>, 128K state, H32 D128, M=34), from two rocprofv3
+# passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by the same
+# counters over a 256 MiB plain copy (FETCH_SIZE reads 0.5000x the copied
+# bytes, WRITE_SIZE 1.0000x); the summary and commands are under profiles/.
+DECODE_STEP_TRAFFIC_BYTES = 46_619_546
 
 
 def log(msg):
@@ -64,10 +70,11 @@ class Probe:
         return _Ctx()
 
     def total_ms(self, name):
-        return sum(s.elapsed_time(e) for s, e in self.events.get(name, []))
+        return sum(ev[0].elapsed_time(ev[1]) for ev in self.events.get(name, []))
 
     def count(self, name):
-        return len(self.events.get(name, []))
+        """Launches (or steps, for grouped entries (start, end, count)) recorded."""
+        return sum(ev[2] if len(ev) > 2 else 1 for ev in self.events.get(name, []))
 
     def reset(self):
         self.events = {}
@@ -142,27 +149,33 @@ def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
                                              args.steps)
     graph_state.release_execution()
     del graph_state, graph_snap
-    # Kernel timing: replay the same steps eagerly on an imported copy with
-    # the GPU pre-loaded by a bounded spin kernel, so the HIP events around
-    # each step bracket back-to-back device work (no host gaps).
+    # Device time per step: replay the same steps eagerly on an imported copy
+    # with the GPU pre-loaded by a bounded spin kernel, and bracket each group
+    # of STEPS_PER_SPIN back-to-back steps with HIP events on the launch
+    # stream (no host gaps, no per-step event overhead).
     q, k, v, rq, rk = xs
     timed = StreamCache.from_export(snap)
     del snap
-    timed._probe = probe
-    probe.reset()
     steps_bytes = []
+    groups = []
     i = context
     while i < context + args.steps:
         torch.cuda._sleep(SPIN_CYCLES)
-        for _ in range(min(STEPS_PER_SPIN, context + args.steps - i)):
+        start = torch.cuda.Event(enable_timing=True)
+        start.record()
+        count = min(STEPS_PER_SPIN, context + args.steps - i)
+        for _ in range(count):
             sl = slice(i, i + 1)
             _, timed = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
                                             raw_k=rk[:, sl], fusion_a=fa, fusion_b=fb,
                                             alpha=0.5, state=timed, position=timed.get_pos())
             steps_bytes.append(decode_bytes(cfg, heads, width, timed.route_size, i))
             i += 1
+        end = torch.cuda.Event(enable_timing=True)
+        end.record()
+        groups.append((start, end, count))
     torch.cuda.synchronize()
-    timed._probe = None
+    probe.events["decode_step"] = groups
     timed.release_execution()
     return state, xs, fa, fb, seconds, graph_seconds, steps_bytes
 
@@ -199,15 +212,17 @@ def run_cold(torch, args, device, cfg, heads, width, context, n_states, probe):
                                             alpha=0.5, state=st, position=st.get_pos())
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    # Kernel timing, GPU pre-loaded (see run_decode).
-    for st in states:
-        st._probe = probe
+    # Device time per step, GPU pre-loaded (see run_decode).
     probe.reset()
+    groups = []
     base = 1 + steps // n_states + 1
     i = 0
     while i < steps:
         torch.cuda._sleep(SPIN_CYCLES)
-        for _ in range(min(STEPS_PER_SPIN, steps - i)):
+        start = torch.cuda.Event(enable_timing=True)
+        start.record()
+        count = min(STEPS_PER_SPIN, steps - i)
+        for _ in range(count):
             j = i % n_states
             st = states[j]
             q, k, v, rq, rk = toks[j]
@@ -217,10 +232,13 @@ def run_cold(torch, args, device, cfg, heads, width, context, n_states, probe):
                                                 raw_k=rk[:, sl], fusion_a=fa, fusion_b=fb,
                                                 alpha=0.5, state=st, position=st.get_pos())
             i += 1
+        end = torch.cuda.Event(enable_timing=True)
+        end.record()
+        groups.append((start, end, count))
     torch.cuda.synchronize()
+    probe.events["decode_step"] = groups
     sel = states[0].route_size
     for st in states:
-        st._probe = None
         st.release_execution()
     return steps, t1 - t0, sel
 
@@ -323,6 +341,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cold", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="after the run, copy a buffer of this many MiB 4 times (a plain "
+                         "copy kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the TaoMemory operator path has no "
@@ -347,7 +368,6 @@ def main():
     step_ms = probe.total_ms("decode_step") / max(n_step, 1)
     alg_bytes = sum(b for b, _ in steps_bytes) / len(steps_bytes)
     c_bytes = sum(c for _, c in steps_bytes) / len(steps_bytes)
-    route_ms = probe.total_ms("route") / max(probe.count("route"), 1)
     achieved = alg_bytes / (step_ms * 1e-3) / 1e9
     log(f"decode: {tok_s:.1f} tok/s (hipGraph preset {args.steps / graph_seconds:.1f}), "
         f"step kernel {step_ms * 1e3:.2f} us, {achieved:.0f} GB/s")
@@ -371,13 +391,13 @@ def main():
                                "replay preset is timed on the same steps as decode_graph)",
                    "context": args.context, "heads": heads, "head_dim": width,
                    "selected_fines": state.route_size},
-        "roofline": {"bound": "hbm", "kernel": "decode_units_kernel<128> + decode_combine_kernel<128> (one decode step)",
+        "roofline": {"bound": "hbm", "kernel": "decode_units_kernel<128> + decode_combine_kernel<128> (one decode step, incl. amortised route refreshes and seal)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": DECODE_STEP_TRAFFIC_BYTES if args.context == 131072 else None,
                      "kernel_us": round(step_ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": int(alg_bytes),
-                     "selected_c_bytes_per_launch": int(c_bytes),
-                     "route_kernel_us": round(route_ms * 1e3, 3)},
+                     "selected_c_bytes_per_launch": int(c_bytes)},
         "decode_graph": {"preset": "index_only_page_memo(graph=True)",
                          "tok_s": round(args.steps / graph_seconds, 2),
                          "ms_per_step": round(graph_seconds / args.steps * 1e3, 4)},
@@ -426,6 +446,15 @@ def main():
                       f"{torch.__version__}"}
         log(f"cpu baseline: {cpu_tok_s:.3f} tok/s")
     state.release_execution()
+    if args.calibrate_copy_mib:
+        n = args.calibrate_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["copy_calibration"] = {"bytes_read": n * 4, "bytes_written": n * 4, "copies": 4}
+        del src, dst
     print(json.dumps(result), flush=True)
 
 

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 1
+#define TAO_ABI_VERSION 2
 
 enum tao_status {
   TAO_OK = 0,
@@ -60,6 +60,8 @@ typedef struct tao_state_dev {
   int32_t* sel;     /* [B, H, sel_cap]  selected fine ids, score order */
   int32_t* chosen;  /* [B, H, chosen_cap] chosen coarse pages, ascending */
   int64_t* header;  /* device [4]: position, M, reserved, reserved */
+  void* fold_g;     /* fp32 [B, H, D, D]  G^T of the current route and epoch */
+  void* fold_den;   /* fp32 [B, H, D]     den weights of the current route */
   void* workspace;  /* scratch: decode step records and the prefill plan */
   size_t workspace_bytes;
 } tao_state_dev;
@@ -94,14 +96,25 @@ size_t tao_workspace_bytes(int32_t batch, int32_t heads, int32_t head_dim,
 /* Zero a new workspace. */
 int tao_workspace_init(const tao_state_dev* st, void* stream);
 
+/* Fold the current route (replaces the per-query gather of the selected
+ * fine memories in the q1 read, query_fresh_fine.py:8-75, with a
+ * per-route precomputation). The read is linear in the channel weights
+ * ch_m = h * w_m with w_m = pw[page(m)] * sw[m] query-independent, so for the
+ * `selected` ids in st->sel under the current page weights:
+ *   fold_g[e][d] = sum_m w_m[d] * C_m[d][e]     (stored as G^T, fp32)
+ *   fold_den[d]  = sum_m w_m[d]
+ * and one query's fine read is r(r(h.G) / r(h.den)). Call after every route
+ * refresh and every seal epilogue (the stream driver and tao_prefill do). */
+int tao_fold_route(const tao_state_dev* st, int32_t selected, void* stream);
+
 /* One fused single-token decode step (replaces the memo-backed q1 region,
  * tao_stream.py:399-433, query_fresh_fine.py:52-75, the local SDPA call
  * flash_attention.py:25-29, the local concat tao_stream.py:927-930, and the
  * fusion kernels fusion_pointwise.py:95-117 / operator.py:86-94).
  * Reads the stream position from st->header[0], appends the token to the
- * ring, reads the `selected` fines of the current route (0 before the first
- * seal: output = local attention), writes out [B,1,H,D] (element strides
- * out_s) and advances header[0]. */
+ * ring, reads the folded route (fold_g / fold_den, see tao_fold_route) when
+ * `selected` > 0 (0 before the first seal: output = local attention),
+ * writes out [B,1,H,D] (element strides out_s) and advances header[0]. */
 int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok,
                     const tao_fusion* fu, int32_t selected, void* out,
                     const int64_t* out_s, void* stream);

@@ -33,7 +33,7 @@ int check_state(const tao_state_dev* st) {
     return fail(TAO_E_SHAPE, "batch, heads and coarse_group must be positive");
   if (!st->ring_k || !st->ring_v || !st->ring_raw || !st->bank_c || !st->fine_z ||
       !st->fine_sw || !st->page_z || !st->page_w || !st->sel || !st->chosen ||
-      !st->header || !st->workspace)
+      !st->header || !st->fold_g || !st->fold_den || !st->workspace)
     return fail(TAO_E_ARGUMENT, "state has a null device buffer");
   if (st->sel_cap > 512) return fail(TAO_E_CAPACITY, "sel_cap above 512");
   if (st->coarse_group != 8) return fail(TAO_E_SHAPE, "HIP kernels implement coarse_group=8");
@@ -96,6 +96,8 @@ tao::DecodeParams decode_params(const tao_state_dev* st, const tao_tokens* tok,
   p.out_sb = out_s[0];
   p.out_sh = out_s[2];
   p.parts = parts_of(st);
+  p.fold_g = (const float*)st->fold_g;
+  p.fold_den = (const float*)st->fold_den;
   p.B = st->batch;
   p.H = st->heads;
   p.keep = st->local_keep;
@@ -187,6 +189,27 @@ int tao_workspace_init(const tao_state_dev* st, void* stream) {
 int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
                     int32_t selected, void* out, const int64_t* out_s, void* stream) {
   return tao::decode_step_at(st, tok, fu, selected, out, out_s, stream, -1);
+}
+
+int tao_fold_route(const tao_state_dev* st, int32_t selected, void* stream) {
+  int rc = check_state(st);
+  if (rc) return rc;
+  if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected count exceeds sel_cap");
+  tao::FoldParams p;
+  p.bank = (const bf16_t*)st->bank_c;
+  p.sw = (const bf16_t*)st->fine_sw;
+  p.pw = (const bf16_t*)st->page_w;
+  p.sel = st->sel;
+  p.fold_g = (float*)st->fold_g;
+  p.fold_den = (float*)st->fold_den;
+  p.B = st->batch;
+  p.H = st->heads;
+  p.group = st->coarse_group;
+  p.fine_cap = st->fine_cap;
+  p.page_cap = st->page_cap;
+  p.sel_cap = st->sel_cap;
+  p.M = selected;
+  return check_hip(tao::launch_fold(p, st->head_dim, (hipStream_t)stream), "tao_fold_route");
 }
 
 int tao_route(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,

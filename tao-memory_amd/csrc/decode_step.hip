@@ -1,30 +1,34 @@
-// Fused single-token decode step for gfx950.
+// Fused single-token decode step for gfx950, and the route fold it reads.
 //
 // Two launches per new token (replace, per request x layer, the reference's
 // q1 page-memo region tao_stream.py:418-433 + query_fresh_fine.py:8-75, the
 // local SDPA flash_attention.py:25-29 over torch.cat'ed K/V
 // tao_stream.py:927-930, and the fusion kernels fusion_pointwise.py:10-117):
 //
-// decode_units_kernel: per (batch, head) local_units(D) + kFineUnits
-//   independent workgroups.
-//   local workgroup j : keys [j*D/2, (j+1)*D/2) of the exact window (K and
-//                       V rows from the ring, or the new token), one online
-//                       softmax per key row, merged into a record (m, l,
-//                       o[D]); workgroup 0 also appends the new token to the
-//                       ring. Its only scalar input is the cursor (a kernel
-//                       argument in eager launches, header[0] in graphs).
-//   fine workgroup w  : selected slots m = w, w + kFineUnits, ... Each slot
-//                       streams its D x D bf16 C^T matrix (16-byte loads, 1
-//                       KB per wave instruction) through two register
-//                       stages, so the next slot's loads are in flight while
-//                       the current one is contracted with
-//                       ch = r(r(h*pw[page]) * sw[fine]) (h computed once).
-//                       Writes a record num[D] and r(sum_d ch) per slot.
-// decode_combine_kernel: one workgroup per (batch, head, 32 channels)
-//   merges the records in a fixed order, den = r(sum_m r(sum_d ch)) in
-//   butterfly order over the slots, fine = r(r(num)/den), applies the fusion
-//   epilogue and advances header[0] (the stream position), so the pair can
-//   be replayed from a hipGraph.
+// decode_units_kernel: per (batch, head) local_units(D) local-attention
+//   workgroups and fine_units(D) fine-read workgroups.
+//   local workgroup j takes keys [j*K, (j+1)*K) (K = local_keys(D)) of the
+//   exact window (K and V rows from the ring, or the new token), runs one
+//   online softmax per key row and merges the rows into a record (m, l,
+//   o[D]); workgroup 0 also appends the new token to the ring. Its only
+//   scalar input is the cursor (a kernel argument in eager launches,
+//   header[0] in graphs).
+//   fine-read workgroup f reads 32 rows of the folded route:
+//   num[e] = h . G^T[e], and den = r(h . g) (h = r(softmax_D(raw_q))).
+// decode_combine_kernel: one workgroup per (batch, head, 32 channels):
+//   merges the local records in a fixed order, fine = r(r(num) / den),
+//   applies the fusion epilogue and advances header[0] (the stream
+//   position), so the pair can be replayed from a hipGraph.
+//
+// fold_kernel (per route refresh and per seal, not per token): the q1 read
+// is linear in ch_m = h * w_m with w_m = pw[page(m)] * sw[m] independent of
+// the query, so the selected fine memories fold into one D x D matrix per
+// head: G^T[e][d] = sum_m w_m[d] C^T_m[e][d], g[d] = sum_m w_m[d]. A decode
+// step then reads 64 KB of G per head instead of M matrices of 32 KB. The
+// reference rounds ch twice to bf16 before its fp32 sums
+// (query_fresh_fine.py:38-40, 47-48, 67); the fold keeps w and the sums in
+// fp32, which moves the fine read by well under one bf16 ulp of its inputs.
+//
 // The kernel boundary publishes the records across the eight XCD L2 caches:
 // a device-scope release fence per workgroup (last-block combine) costs far
 // more than the second launch on this part.
@@ -35,26 +39,21 @@
 namespace tao {
 namespace {
 
-constexpr int kMaxFinesPerWG = (512 + kFineUnits - 1) / kFineUnits;
-
 template <int D>
 struct Geo {
   static constexpr int CH = D / 8;                 // 16-byte chunks per row
   static constexpr int ROWS = kThreads / CH;       // rows per load pass
-  static constexpr int RPT = D / ROWS;             // uint4 per thread per C^T
-  static constexpr int KEYS = D / 2;               // keys per local workgroup
+  static constexpr int KEYS = local_keys(D);       // keys per local workgroup
   static constexpr int KPT = KEYS / ROWS;          // key rows per thread
-  static constexpr int PER = D / 64;               // channels per lane (wave 0)
-  static constexpr int RED = ROWS > CH ? ROWS : CH;
   static constexpr int NLOC = local_units(D);
+  static constexpr int NFINE = fine_units(D);
 };
+static_assert(kThreads == 256, "thread layouts below assume 256 threads");
 
 template <int D>
 struct StepSmem {
-  float chb[2][D];               // ch of the current / previous fine
-  float red[Geo<D>::RED][D];     // cross-thread reductions
+  float red[Geo<D>::ROWS][D];     // cross-row reduction
   float rm[Geo<D>::ROWS], rl[Geo<D>::ROWS];
-  int ids[kMaxFinesPerWG];
 };
 
 TAO_DEV void unpack8(const uint4& u, float out[8]) {
@@ -74,10 +73,82 @@ TAO_DEV float group_sum(float v) {
   return v;
 }
 
+// Fine-read workgroup f: num[e] = h . G^T[e] for rows e in
+// [f * kFineRows, (f + 1) * kFineRows), thread (row tid / 8, part tid % 8);
+// workgroup 0 also writes den = r(h . g). h = r(softmax_D(raw_q)) with the
+// exp correctly rounded in fp32.
 template <int D>
-__device__ void local_workgroup(const DecodeParams& p, int b, int h, int j, float* rec,
-                                StepSmem<D>& sm) {
+__device__ void fine_read(const DecodeParams& p, int b, int h, int f, float* frec,
+                          float* hq) {
+  constexpr int DP = D / 8, PER = D / 64;
+  const int tid = threadIdx.x, row = tid / 8, part = tid % 8;
+  const int bh = b * p.H + h;
+  const int e = f * kFineRows + row;
+  const float* grow = p.fold_g + ((size_t)bh * D + e) * D + part * DP;
+  float gv[DP];
+#pragma unroll
+  for (int k = 0; k < DP; k += 4) {
+    const float4 v = *(const float4*)(grow + k);
+    gv[k] = v.x; gv[k + 1] = v.y; gv[k + 2] = v.z; gv[k + 3] = v.w;
+  }
+  if (tid < 64) {
+    const bf16_t* rq = p.rq.p + b * p.rq.sb + h * p.rq.sh;
+    float xr[PER], gden[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      xr[k] = bf2f(rq[tid + 64 * k]);
+      gden[k] = f == 0 ? p.fold_den[(size_t)bh * D + tid + 64 * k] : 0.0f;
+    }
+    float top = -__builtin_inff();
+#pragma unroll
+    for (int k = 0; k < PER; ++k) top = fmaxf(top, xr[k]);
+    top = wave_max(top);
+    float ex[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) ex[k] = exp_cr(xr[k] - top);
+    float s = ex[0];
+#pragma unroll
+    for (int k = 1; k < PER; ++k) s += ex[k];
+    s = wave_sum_fold(s);
+    float dsum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const float hv = rbf(ex[k] / s);
+      hq[tid + 64 * k] = hv;
+      dsum = k == 0 ? hv * gden[k] : fmaf(hv, gden[k], dsum);
+    }
+    if (f == 0) {
+      dsum = wave_sum_fold(dsum);
+      if (tid == 0) frec[0] = rbf(dsum);
+    }
+  }
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < DP; ++k) acc = fmaf(hq[part * DP + k], gv[k], acc);
+  acc += __shfl_xor(acc, 1, 64);
+  acc += __shfl_xor(acc, 2, 64);
+  acc += __shfl_xor(acc, 4, 64);
+  if (part == 0) frec[kStepRec + e] = acc;
+}
+
+// Kernel A: per (batch, head) NLOC local-attention workgroups (the window
+// split by keys) and NFINE fine-read workgroups; no cross-workgroup
+// communication.
+template <int D>
+__global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, int M) {
   using G = Geo<D>;
+  __shared__ StepSmem<D> sm;
+  constexpr int PER_HEAD = G::NLOC + G::NFINE;
+  const int bh = blockIdx.x / PER_HEAD;
+  const int j = blockIdx.x % PER_HEAD;
+  const int b = bh / p.H, h = bh % p.H;
+  float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
+  if (j >= G::NLOC) {
+    if (M > 0) fine_read<D>(p, b, h, j - G::NLOC, recs + G::NLOC * (D + kStepRec), sm.red[0]);
+    return;
+  }
+  float* rec = recs + j * (D + kStepRec);
   const int tid = threadIdx.x, chn = tid % G::CH, r = tid / G::CH;
   const int L = p.keep + p.fine;
   const long long position = p.pos_hint >= 0 ? p.pos_hint : p.header[0];
@@ -172,141 +243,12 @@ __device__ void local_workgroup(const DecodeParams& p, int b, int h, int j, floa
   }
 }
 
-template <int D>
-struct FineRegs {
-  uint4 x[Geo<D>::RPT];
-  float pw[Geo<D>::PER], sw[Geo<D>::PER];   // wave 0
-};
-
-// Issue every load of this workgroup's k-th fine (no waits).
-template <int D>
-TAO_DEV void load_fine(const DecodeParams& p, int bh, int id, FineRegs<D>& x) {
-  using G = Geo<D>;
-  const int tid = threadIdx.x, chn = tid % G::CH, r = tid / G::CH;
-  const bf16_t* cmat = p.bank + ((size_t)bh * p.fine_cap + id) * D * D;
-#pragma unroll
-  for (int i = 0; i < G::RPT; ++i)
-    x.x[i] = *(const uint4*)(cmat + (size_t)(r + i * G::ROWS) * D + chn * 8);
-  if (tid < 64) {
-    const bf16_t* pw = p.pw + ((size_t)bh * p.page_cap + id / p.group) * D;
-    const bf16_t* sw = p.sw + ((size_t)bh * p.fine_cap + id) * D;
-#pragma unroll
-    for (int k = 0; k < G::PER; ++k) {
-      x.pw[k] = bf2f(pw[tid + 64 * k]);
-      x.sw[k] = bf2f(sw[tid + 64 * k]);
-    }
-  }
-}
-
-template <int D>
-__device__ void fine_workgroup(const DecodeParams& p, int b, int h, int w, int M, float* rec,
-                               float* dens, StepSmem<D>& sm) {
-  using G = Geo<D>;
-  const int tid = threadIdx.x, chn = tid % G::CH, r = tid / G::CH;
-  const int bh = b * p.H + h;
-  const int nfine = M > w ? (M - 1 - w) / kFineUnits + 1 : 0;
-  const int32_t* sel = p.sel + (size_t)bh * p.sel_cap;
-  for (int k = tid; k < nfine; k += kThreads) sm.ids[k] = sel[w + k * kFineUnits];
-  const bf16_t* rq = p.rq.p + b * p.rq.sb + h * p.rq.sh;
-  float xr[G::PER];
-  if (tid < 64) {
-#pragma unroll
-    for (int k = 0; k < G::PER; ++k) xr[k] = bf2f(rq[tid + 64 * k]);
-  }
-  __syncthreads();
-  FineRegs<D> A, B;
-  if (nfine > 0) load_fine<D>(p, bh, sm.ids[0], A);
-  if (nfine > 1) load_fine<D>(p, bh, sm.ids[1], B);
-  // h = r(softmax_D(raw_q)) by wave 0 (exp correctly rounded in fp32),
-  // under the first loads.
-  float hq[G::PER];
-  if (tid < 64) {
-    float top = -__builtin_inff();
-#pragma unroll
-    for (int k = 0; k < G::PER; ++k) top = fmaxf(top, xr[k]);
-    top = wave_max(top);
-    float e[G::PER];
-#pragma unroll
-    for (int k = 0; k < G::PER; ++k) e[k] = exp_cr(xr[k] - top);
-    float s = e[0];
-#pragma unroll
-    for (int k = 1; k < G::PER; ++k) s += e[k];
-    s = wave_sum_fold(s);
-#pragma unroll
-    for (int k = 0; k < G::PER; ++k) hq[k] = rbf(e[k] / s);
-  }
-  float part[G::RPT];
-#pragma unroll
-  for (int i = 0; i < G::RPT; ++i) part[i] = 0.0f;
-  auto consume = [&](int k, const FineRegs<D>& x) {
-    float* chb = sm.chb[k & 1];
-    if (tid < 64) {
-      float csum = 0.0f;
-#pragma unroll
-      for (int q = 0; q < G::PER; ++q) {
-        const float hv = rbf(hq[q] * x.pw[q]);
-        const float ch = rbf(hv * x.sw[q]);
-        chb[tid + 64 * q] = ch;
-        csum = q == 0 ? ch : csum + ch;   // PER <= 2: fold of the lane pair
-      }
-      csum = wave_sum_fold(csum);
-      if (tid == 0) dens[w + k * kFineUnits] = rbf(csum);
-    }
-    __syncthreads();
-    float chv[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) chv[q] = chb[chn * 8 + q];
-#pragma unroll
-    for (int i = 0; i < G::RPT; ++i) {
-      float cf[8];
-      unpack8(x.x[i], cf);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) part[i] = fmaf(chv[q], cf[q], part[i]);
-    }
-  };
-  // Two register stages: fine k + 1 is in flight while fine k is consumed.
-  for (int k = 0; k < nfine; k += 2) {
-    consume(k, A);
-    if (k + 2 < nfine) load_fine<D>(p, bh, sm.ids[k + 2], A);
-    if (k + 1 >= nfine) break;
-    consume(k + 1, B);
-    if (k + 3 < nfine) load_fine<D>(p, bh, sm.ids[k + 3], B);
-  }
-  // Record: sum the partial dots over the CH chunks of each row.
-#pragma unroll
-  for (int i = 0; i < G::RPT; ++i) sm.red[chn][r + i * G::ROWS] = part[i];
-  __syncthreads();
-  if (tid < D) {
-    float s = 0.0f;
-    for (int cc = 0; cc < G::CH; ++cc) s += sm.red[cc][tid];
-    rec[kStepRec + tid] = s;
-  }
-}
-
-// Kernel A: independent workgroups, no cross-workgroup communication.
-template <int D>
-__global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, int M) {
-  using G = Geo<D>;
-  __shared__ StepSmem<D> sm;
-  constexpr int PER_HEAD = G::NLOC + kFineUnits;
-  const int bh = blockIdx.x / PER_HEAD;
-  const int role = blockIdx.x % PER_HEAD;
-  const int b = bh / p.H, h = bh % p.H;
-  float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
-  float* dens = recs + PER_HEAD * (D + kStepRec);
-  if (role < G::NLOC)
-    local_workgroup<D>(p, b, h, role, recs + role * (D + kStepRec), sm);
-  else
-    fine_workgroup<D>(p, b, h, role - G::NLOC, M, recs + role * (D + kStepRec), dens, sm);
-}
-
 // Kernel B: one 256-thread workgroup per (batch, head, 32 channels). Thread
-// group g = tid / 32 owns the local and fine records j = g (mod 8);
-// every record load is issued before any arithmetic and the groups merge in
-// ascending g, so the summation order is fixed.
+// group g = tid / 32 owns local records j = g (mod 8), channel dc = tid % 32;
+// the groups merge in ascending g (fixed order), then the fine record and the
+// fusion epilogue give the output.
 constexpr int kCombineCols = 32;
 constexpr int kCombineGroups = kThreads / kCombineCols;
-static_assert(kFineUnits % kCombineGroups == 0, "fine records split evenly over groups");
 
 template <int D>
 __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p, int M) {
@@ -314,16 +256,15 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
   constexpr int STRIDE = D + kStepRec, G = kCombineGroups, CHUNKS = D / kCombineCols;
   constexpr int NLOC = Gm::NLOC, LPG = (NLOC + G - 1) / G;
   __shared__ float ml[NLOC][2];
-  __shared__ float part_num[G][kCombineCols], part_loc[G][kCombineCols];
-  __shared__ float den_fine;
+  __shared__ float part_loc[G][kCombineCols];
   const int bh = blockIdx.x / CHUNKS;
   const int chunk = blockIdx.x % CHUNKS;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, dc = tid % kCombineCols, g = tid / kCombineCols;
   const int d = chunk * kCombineCols + dc;
   const float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
-  const float* dens = recs + (NLOC + kFineUnits) * STRIDE;
 
+  // Loads first: local records, the fine record, fusion operands.
   float m_g[LPG], l_g[LPG], o_g[LPG];
 #pragma unroll
   for (int i = 0; i < LPG; ++i) {
@@ -332,36 +273,18 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
     l_g[i] = j < NLOC ? recs[j * STRIDE + 1] : 0.0f;
     o_g[i] = j < NLOC ? recs[j * STRIDE + kStepRec + d] : 0.0f;
   }
-  constexpr int FPG = kFineUnits / G;
-  float n_v[FPG];
-#pragma unroll
-  for (int i = 0; i < FPG; ++i)
-    n_v[i] = M > g + i * G ? recs[(NLOC + g + i * G) * STRIDE + kStepRec + d] : 0.0f;
-  float q = 0.0f, a[3], bb[3];
+  float q = 0.0f, num = 0.0f, den = 1.0f, a[3], bb[3];
   if (g == 0) {
     q = bf2f(p.rq.p[b * p.rq.sb + h * p.rq.sh + d]);
+    if (M > 0) {
+      den = recs[NLOC * STRIDE];
+      num = recs[NLOC * STRIDE + kStepRec + d];
+    }
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       a[i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + d * p.fa_s[1] + i * p.fa_s[2]);
       bb[i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + d * p.fb_s[1] + i * p.fb_s[2]);
     }
-  }
-  if (M > 0 && tid >= 64 && tid < 128) {
-    // den = r(sum over slots of r(sum_d ch)), butterfly order over slots.
-    const int lane = tid - 64;
-    int slots = 64;
-    while (slots < M) slots *= 2;
-    const int per_lane = slots / 64;
-    float vals[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int m = lane + 64 * k;
-      vals[k] = (k < per_lane && m < M) ? dens[m] : 0.0f;
-    }
-    for (int width = per_lane; width > 1; width /= 2)
-      for (int k = 0; k < width / 2; ++k) vals[k] += vals[k + width / 2];
-    const float v = wave_sum_fold(vals[0]);
-    if (lane == 0) den_fine = rbf(v);
   }
   if (dc == 0) {
 #pragma unroll
@@ -376,24 +299,20 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
   float pl = 0.0f;
 #pragma unroll
   for (int i = 0; i < LPG; ++i) pl += l_g[i] > 0.0f ? __expf(m_g[i] - top) * o_g[i] : 0.0f;
-  float n_g = 0.0f;
-#pragma unroll
-  for (int i = 0; i < FPG; ++i) n_g += n_v[i];
   part_loc[g][dc] = pl;
-  part_num[g][dc] = n_g;
   __syncthreads();
   if (g == 0) {
     float den_local = 0.0f;
 #pragma unroll
     for (int j = 0; j < NLOC; ++j)
       if (ml[j][1] > 0.0f) den_local = fmaf(__expf(ml[j][0] - top), ml[j][1], den_local);
-    float nl = 0.0f, nf = 0.0f;
+    float nl = 0.0f;
 #pragma unroll
-    for (int gg = 0; gg < G; ++gg) { nl += part_loc[gg][dc]; nf += part_num[gg][dc]; }
+    for (int gg = 0; gg < G; ++gg) nl += part_loc[gg][dc];
     const float local = rbf(nl / den_local);
     bf16_t result;
     if (M > 0) {
-      const float fine_v = rbf(rbf(nf) / den_fine);
+      const float fine_v = rbf(rbf(num) / den);
       result = fuse_element(q, local, 0.0f, fine_v, a, bb, p.gain, 0, 1);
     } else {
       result = f2bf(local);
@@ -402,6 +321,59 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
   }
   // Kernel A of this step has finished reading the position: advance it.
   if (blockIdx.x == 0 && tid == 0) p.header[0] = p.header[0] + 1;
+}
+
+// Fold: one workgroup per (batch, head, ROWS rows of G^T). Thread (row r,
+// chunk c) accumulates G^T[e0 + r][8c .. 8c + 8) over the selected slots in
+// slot order (fp32); four slots' loads are in flight at a time.
+template <int D>
+__global__ __launch_bounds__(kThreads) void fold_kernel(FoldParams p) {
+  constexpr int CH = D / 8, ROWS = kThreads / CH, CHUNKS = D / ROWS, U = 4;
+  const int bh = blockIdx.x / CHUNKS;
+  const int e0 = (blockIdx.x % CHUNKS) * ROWS;
+  const int tid = threadIdx.x, c = tid % CH, r = tid / CH;
+  const int e = e0 + r;
+  const int32_t* sel = p.sel + (size_t)bh * p.sel_cap;
+  const bf16_t* bank = p.bank + (size_t)bh * p.fine_cap * D * D;
+  const bf16_t* sw = p.sw + (size_t)bh * p.fine_cap * D;
+  const bf16_t* pw = p.pw + (size_t)bh * p.page_cap * D;
+  float acc[8], den[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) { acc[k] = 0.0f; den[k] = 0.0f; }
+  for (int m0 = 0; m0 < p.M; m0 += U) {
+    uint4 cv[U], wp[U], ws[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int m = min(m0 + u, p.M - 1);
+      const int id = sel[m];
+      cv[u] = *(const uint4*)(bank + ((size_t)id * D + e) * D + c * 8);
+      wp[u] = *(const uint4*)(pw + (size_t)(id / p.group) * D + c * 8);
+      ws[u] = *(const uint4*)(sw + (size_t)id * D + c * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (m0 + u < p.M) {
+        float cf[8], pf[8], sf[8];
+        unpack8(cv[u], cf);
+        unpack8(wp[u], pf);
+        unpack8(ws[u], sf);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float w = pf[k] * sf[k];
+          acc[k] = fmaf(w, cf[k], acc[k]);
+          den[k] += w;
+        }
+      }
+    }
+  }
+  float* grow = p.fold_g + ((size_t)bh * D + e) * D + c * 8;
+  *(float4*)grow = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  *(float4*)(grow + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  if (e == 0) {
+    float* dg = p.fold_den + (size_t)bh * D + c * 8;
+    *(float4*)dg = make_float4(den[0], den[1], den[2], den[3]);
+    *(float4*)(dg + 4) = make_float4(den[4], den[5], den[6], den[7]);
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void stage_tokens_kernel(StageParams p) {
@@ -443,9 +415,9 @@ __global__ __launch_bounds__(kThreads) void ring_append_kernel(AppendParams p) {
 }  // namespace
 
 hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStream_t s) {
-  if (M < 0 || M > p.sel_cap || M > 512) return hipErrorInvalidValue;
+  if (M < 0 || M > p.sel_cap) return hipErrorInvalidValue;
   if (p.keep + p.fine > kMaxWindow) return hipErrorInvalidValue;
-  const dim3 units((unsigned)(p.B * p.H * (local_units(head_dim) + kFineUnits)));
+  const dim3 units((unsigned)(p.B * p.H * (local_units(head_dim) + fine_units(head_dim))));
   const dim3 cols((unsigned)(p.B * p.H * (head_dim / kCombineCols)));
   if (head_dim == 128) {
     hipLaunchKernelGGL(decode_units_kernel<128>, units, dim3(kThreads), 0, s, p, M);
@@ -453,6 +425,22 @@ hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStr
   } else if (head_dim == 64) {
     hipLaunchKernelGGL(decode_units_kernel<64>, units, dim3(kThreads), 0, s, p, M);
     hipLaunchKernelGGL(decode_combine_kernel<64>, cols, dim3(kThreads), 0, s, p, M);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_fold(const FoldParams& p, int head_dim, hipStream_t s) {
+  if (p.M < 0 || p.M > p.sel_cap) return hipErrorInvalidValue;
+  if (head_dim == 128) {
+    constexpr int CHUNKS = 128 / (kThreads / 16);
+    hipLaunchKernelGGL(fold_kernel<128>, dim3((unsigned)(p.B * p.H * CHUNKS)), dim3(kThreads),
+                       0, s, p);
+  } else if (head_dim == 64) {
+    constexpr int CHUNKS = 64 / (kThreads / 8);
+    hipLaunchKernelGGL(fold_kernel<64>, dim3((unsigned)(p.B * p.H * CHUNKS)), dim3(kThreads),
+                       0, s, p);
   } else {
     return hipErrorInvalidValue;
   }

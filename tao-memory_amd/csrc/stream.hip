@@ -16,6 +16,7 @@
 extern "C" int tao_route(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
                          int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
                          void* stream);
+extern "C" int tao_fold_route(const tao_state_dev* st, int32_t selected, void* stream);
 extern "C" int tao_write_fine(const tao_state_dev* st, const tao_tokens* tok, int64_t new_base,
                               const int64_t* start_pos, int32_t first_slot, int32_t count,
                               void* stream);
@@ -156,6 +157,7 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
     const int64_t rq_s[2] = {tok->rq_s[0], tok->rq_s[2]};
     rc = tao_route(&s->st, tok->raw_q, rq_s, (int32_t)completed, (int32_t)pending, coarse,
                    selected, stream);
+    if (!rc) rc = tao_fold_route(&s->st, selected, stream);
     if (rc) return rc;
     s->route_coarse = coarse;
     s->route_size = selected;
@@ -190,6 +192,8 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
     rc = tao_write_fine(&s->st, tok, pos + 1, s->seal_start, (int32_t)fines, 1, stream);
     if (!rc) rc = tao_seal_epilogue(&s->st, (int32_t)fines,
                                     (int32_t)(fines / c.coarse_group + 1), 1, stream);
+    // New page weights and segment weights: refold the current route.
+    if (!rc) rc = tao_fold_route(&s->st, s->route_size, stream);
     if (rc) return rc;
     sealed = 1;
   }

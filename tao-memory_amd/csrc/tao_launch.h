@@ -15,23 +15,34 @@ void set_error(const char* msg);
 
 constexpr int kThreads = 256;   // 4 wave64 per workgroup
 constexpr int kMaxWindow = 768;   // serve_limit = local_keep + fine_tokens
-#ifndef TAO_FINE_UNITS
-#define TAO_FINE_UNITS 8
-#endif
-constexpr int kFineUnits = TAO_FINE_UNITS;   // decode fine workgroups per (batch, head)
 constexpr int kStepRec = 4;       // header floats of one decode record
+#ifndef TAO_LOCAL_KEY_DIV
+#define TAO_LOCAL_KEY_DIV 2
+#endif
+constexpr int kLocalKeyDiv = TAO_LOCAL_KEY_DIV;   // keys per local workgroup = D / div
+constexpr int kFineRows = 32;     // rows of the folded route per fine-read workgroup
 
-// Local-attention workgroups per (batch, head): D / 2 keys each.
-__host__ __device__ constexpr int local_units(int head_dim) {
-  return (kMaxWindow + head_dim / 2 - 1) / (head_dim / 2);
+// Keys per local-attention workgroup: D / kLocalKeyDiv, at least one load
+// pass of the workgroup (kThreads / (D / 8) rows).
+__host__ __device__ constexpr int local_keys(int head_dim) {
+  return head_dim / kLocalKeyDiv > 256 / (head_dim / 8) ? head_dim / kLocalKeyDiv
+                                                         : 256 / (head_dim / 8);
 }
 
-// Per (batch, head) decode scratch, in floats: local_units(D) local records
-// and kFineUnits fine records of (kStepRec + D) floats, then one den term
-// per selected slot.
+// Local-attention workgroups per (batch, head).
+__host__ __device__ constexpr int local_units(int head_dim) {
+  return (kMaxWindow + local_keys(head_dim) - 1) / local_keys(head_dim);
+}
+
+// Fine-read workgroups per (batch, head).
+__host__ __device__ constexpr int fine_units(int head_dim) { return head_dim / kFineRows; }
+
+// Per (batch, head) decode scratch, in floats: local_units(D) local-attention
+// records and one fine record (den in the header, num[D]), each of
+// (kStepRec + D) floats.
 __host__ __device__ inline size_t step_floats(int head_dim, int sel_cap) {
-  return (size_t)(local_units(head_dim) + kFineUnits) * (head_dim + kStepRec) +
-         (size_t)sel_cap;
+  (void)sel_cap;
+  return (size_t)(local_units(head_dim) + 1) * (head_dim + kStepRec);
 }
 
 // Workspace layout (bytes from the start of tao_state_dev::workspace):
@@ -61,12 +72,22 @@ struct DecodeParams {
   float gain;
   bf16_t* out; int64_t out_sb, out_sh;
   float* parts;
+  const float* fold_g; const float* fold_den;   // folded route (G^T, den weights)
   long long pos_hint;   // cursor of this step, or -1: read header[0]
   int B, H, keep, fine, group, fine_cap, page_cap, sel_cap;
 };
 
-// M = selected fines of the current route (0 before the first seal).
+// M = selected fines of the current route (0 before the first seal: no
+// fine read). The fine read uses the folded route (launch_fold).
 hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStream_t s);
+
+struct FoldParams {
+  const bf16_t* bank; const bf16_t* sw; const bf16_t* pw;
+  const int32_t* sel;
+  float* fold_g; float* fold_den;
+  int B, H, group, fine_cap, page_cap, sel_cap, M;
+};
+hipError_t launch_fold(const FoldParams& p, int head_dim, hipStream_t s);
 
 // tao_decode_step with the step's cursor given by the caller (position >= 0)
 // instead of read from header[0] on the device; used by the stream driver.

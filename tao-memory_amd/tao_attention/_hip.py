@@ -30,6 +30,7 @@ class StateDev(ctypes.Structure):
         ("bank_c", _vp), ("fine_z", _vp), ("fine_sw", _vp),
         ("page_z", _vp), ("page_w", _vp),
         ("sel", _vp), ("chosen", _vp), ("header", _vp),
+        ("fold_g", _vp), ("fold_den", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
     ]
 
@@ -71,6 +72,7 @@ _SIGNATURES = {
     "tao_workspace_init": ([ctypes.POINTER(StateDev), _vp], _i32),
     "tao_decode_step": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens),
                          ctypes.POINTER(Fusion), _i32, _vp, ctypes.POINTER(_i64), _vp], _i32),
+    "tao_fold_route": ([ctypes.POINTER(StateDev), _i32, _vp], _i32),
     "tao_route": ([ctypes.POINTER(StateDev), _vp, ctypes.POINTER(_i64),
                    _i32, _i32, _i32, _i32, _vp], _i32),
     "tao_write_fine": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i64, _vp,
@@ -136,6 +138,13 @@ def require_device(tensor):
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def raw_stream(index):
+    """The current HIP stream handle of device `index`."""
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
 
 
 def stream_ptr(device):

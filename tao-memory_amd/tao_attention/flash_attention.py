@@ -25,7 +25,8 @@ def _bare_state(q):
     st.local_keep, st.fine_tokens, st.coarse_group = 512, 256, 8
     dummy = q.data_ptr()
     for name in ("ring_k", "ring_v", "ring_raw", "bank_c", "fine_z", "fine_sw",
-                 "page_z", "page_w", "sel", "chosen", "header", "workspace"):
+                 "page_z", "page_w", "sel", "chosen", "header", "fold_g", "fold_den",
+                 "workspace"):
         setattr(st, name, dummy)
     st.workspace_bytes = _hip.lib().tao_workspace_bytes(b, h, d, 0, 0)
     return st

@@ -32,12 +32,14 @@ HBM_PEAK_GBS = 8000.0
 SPIN_CYCLES = 4_000_000        # bounded spin that keeps the queue ahead of the host
 STEPS_PER_SPIN = 16
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-# HBM-side bytes of one decode step (decode_units_kernel<128> +
-# decode_combine_kernel<128>, 128K state, H32 D128, M=34), from two rocprofv3
-# passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by the same
-# counters over a 256 MiB plain copy (FETCH_SIZE reads 0.5000x the copied
-# bytes, WRITE_SIZE 1.0000x); the summary and commands are under profiles/.
-DECODE_STEP_TRAFFIC_BYTES = 46_619_546
+# HBM-side bytes per decode token (decode_units_kernel<128> +
+# decode_combine_kernel<128> every token, plus route + fold per refresh and
+# fold + epilogue per seal, averaged over the 256-step run; 128K state, H32
+# D128, M=34), from two rocprofv3 passes (FETCH_SIZE, then WRITE_SIZE, KiB
+# per dispatch) scaled by the same counters over a 256 MiB plain copy
+# (FETCH_SIZE reads 0.5000x the copied bytes, WRITE_SIZE 1.0000x); the
+# summary and commands are under profiles/.
+DECODE_STEP_TRAFFIC_BYTES = 13_757_720
 
 
 def log(msg):
@@ -94,15 +96,37 @@ def make_tokens(torch, tokens, heads, width, seed, device, unit_raw_k=False):
     return xs, fa, fb
 
 
-def decode_bytes(cfg, heads, width, selected, position):
-    """Algorithmic HBM bytes of one fused decode step."""
+def decode_bytes(cfg, heads, width, selected, position, layer=0):
+    """Bytes of the decode step at `position` (selected = route size).
+
+    Returns (reference_basis, own):
+    * reference_basis: the per-step algorithmic bytes of the route + selected
+      read as the reference defines the step (every selected C matrix and
+      its side rows read per token): H*M*(D^2 + 3D)*2 + 2*H*D*2, plus
+      H*(P + E)*D*2 on route-refresh steps (P pages, E eligible fines);
+    * own: the bytes this build's step moves: the local K/V window, the
+      folded route (G^T fp32 + den weights), the local-attention records,
+      the token rows and, on refresh steps, the route plus the fold that
+      re-reads the selected matrices.
+    """
     from tao_attention import schedule
+    fines = schedule.fines_at(position, cfg)
+    refresh = fines > 0 and schedule.is_turn(position, layer, cfg)
+    ref = heads * selected * (width * width + 3 * width) * 2 + 2 * heads * width * 2
+    fold = 0
+    if refresh:
+        completed, pending = divmod(fines, cfg.coarse_group)
+        coarse, eligible, _ = schedule.routed_counts(completed, pending, cfg)
+        pages = completed + (pending > 0)
+        ref += heads * (pages + eligible) * width * 2
+        fold = heads * selected * (width * width + 2 * width) * 2 + heads * width * (width + 1) * 4
     keys = schedule.local_len_at(position, cfg) + 1
-    c_bytes = heads * selected * width * width * 2
-    side = heads * selected * (2 * width * 2 + 4)        # sw + pw rows, ids
     local = keys * heads * width * 2 * 2                  # ring K and V
+    folded = heads * width * (width + 1) * 4 if fines > 0 else 0
+    records = 2 * 12 * heads * (width + 4) * 4            # written, then merged
     tokens = 5 * heads * width * 2 + 3 * heads * width * 2 + heads * width * 2
-    return c_bytes + side + local + tokens, c_bytes
+    own = local + folded + records + tokens + fold
+    return ref, own
 
 
 def decode_loop(torch, state, xs, fa, fb, start, steps):
@@ -367,7 +391,7 @@ def main():
     n_step = probe.count("decode_step")
     step_ms = probe.total_ms("decode_step") / max(n_step, 1)
     alg_bytes = sum(b for b, _ in steps_bytes) / len(steps_bytes)
-    c_bytes = sum(c for _, c in steps_bytes) / len(steps_bytes)
+    own_bytes = sum(o for _, o in steps_bytes) / len(steps_bytes)
     achieved = alg_bytes / (step_ms * 1e-3) / 1e9
     log(f"decode: {tok_s:.1f} tok/s (hipGraph preset {args.steps / graph_seconds:.1f}), "
         f"step kernel {step_ms * 1e3:.2f} us, {achieved:.0f} GB/s")
@@ -397,7 +421,10 @@ def main():
                      "traffic": DECODE_STEP_TRAFFIC_BYTES if args.context == 131072 else None,
                      "kernel_us": round(step_ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": int(alg_bytes),
-                     "selected_c_bytes_per_launch": int(c_bytes)},
+                     "algorithmic_basis": "reference step: H*M*(D^2+3D)*2 + 2*H*D*2 per token, "
+                                          "+ H*(P+E)*D*2 on refresh steps",
+                     "own_bytes_per_step": int(own_bytes),
+                     "own_GBs": round(own_bytes / (step_ms * 1e-3) / 1e9, 1)},
         "decode_graph": {"preset": "index_only_page_memo(graph=True)",
                          "tok_s": round(args.steps / graph_seconds, 2),
                          "ms_per_step": round(graph_seconds / args.steps * 1e3, 4)},
@@ -408,7 +435,7 @@ def main():
         steps, cold_s, cold_sel = run_cold(torch, args, device, cfg, heads, width,
                                            args.context, args.cold_states, probe)
         cold_ms = probe.total_ms("decode_step") / max(probe.count("decode_step"), 1)
-        cold_bytes, _ = decode_bytes(cfg, heads, width, cold_sel, args.context + 8)
+        cold_bytes, _ = decode_bytes(cfg, heads, width, cold_sel, args.context + 9)
         result["decode_cold"] = {
             "states": args.cold_states, "tok_s": round(steps / cold_s, 2),
             "kernel_us": round(cold_ms * 1e3, 3),

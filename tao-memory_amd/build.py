@@ -42,6 +42,38 @@ def _compile(src):
     return obj
 
 
+FAST_SRC = os.path.join(CSRC, "host", "tao_fast.cpp")
+
+
+def fast_path():
+    import sysconfig
+    return os.path.join(OUT_DIR, "_tao_fast" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_fast(verbose=True):
+    """Host-only torch extension for the per-token decode call (g++)."""
+    import sysconfig
+    import torch
+    from torch.utils import cpp_extension
+    out = fast_path()
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-shared", "-fPIC", "-std=c++17",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_EXTENSION_NAME=_tao_fast",
+           "-DTORCH_API_INCLUDE_EXTENSION_H",
+           *[f"-I{p}" for p in cpp_extension.include_paths()],
+           f"-I{sysconfig.get_paths()['include']}",
+           FAST_SRC, "-o", out + ".tmp",
+           *[f"-L{p}" for p in cpp_extension.library_paths()],
+           "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode:
+        raise RuntimeError(f"g++ failed for {FAST_SRC}:\n{proc.stderr[-4000:]}")
+    os.replace(out + ".tmp", out)
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
 def build(verbose=True):
     os.makedirs(OUT_DIR, exist_ok=True)
     os.makedirs(OBJ_DIR, exist_ok=True)
@@ -56,6 +88,7 @@ def build(verbose=True):
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")
+    build_fast(verbose)
     return LIB
 
 

@@ -101,6 +101,32 @@ _SIGNATURES = {
 EXPORTED = tuple(_SIGNATURES)
 
 
+_fast = None
+
+
+def fast_module():
+    """The native per-token decode entry (torch extension built beside the
+    library), or None when it is not built: the host then issues the same
+    C-ABI call through ctypes."""
+    global _fast
+    if _fast is None:
+        import importlib.util
+        import sysconfig
+        path = os.path.join(os.path.dirname(_LIB_PATH),
+                            "_tao_fast" + sysconfig.get_config_var("EXT_SUFFIX"))
+        _fast = False
+        if os.path.exists(path):
+            spec = importlib.util.spec_from_file_location("_tao_fast", path)
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+            _fast = mod
+    return _fast or None
+
+
+def function_address(name):
+    return ctypes.cast(getattr(lib(), name), ctypes.c_void_p).value
+
+
 def library_path():
     return _LIB_PATH
 

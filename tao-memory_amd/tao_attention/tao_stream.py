@@ -214,6 +214,8 @@ class StreamCache:
         self._handle = None          # native stream driver (stream.hip)
         self._handle_dirty = True
         self._fast = None            # decode fast-path key (see decode)
+        self._native = None          # native decode entry (tao_fast.cpp)
+        self._fast_limit = -1
         self._graph_mode = bool(self.config.q1_history_region_graph)
         self._first_fine = self.config.first_fine
         self._graph_buffers = None
@@ -247,6 +249,7 @@ class StreamCache:
             self._handle = None
             self._handle_dirty = True
             self._fast = None
+            self._native = None
 
     def __del__(self):
         try:
@@ -511,6 +514,16 @@ class StreamCache:
         parameter tensors and the driver binding are compared with the
         previous call's; anything different goes through the full checks.
         """
+        nat = self._native
+        if nat is not None and self.position < self._fast_limit and not self._handle_dirty:
+            pos = self.position
+            try:
+                r = nat(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, pos,
+                        _hip.raw_stream(self._stream_index))
+            except TypeError:
+                r = None
+            if r is not None:
+                return self._book(pos, r is True, r)
         fp = self._fast
         if (fp is not None and self.position < fp[8]
                 and (q.shape, k.shape, v.shape, raw_q.shape, raw_k.shape) == fp[0]
@@ -558,6 +571,20 @@ class StreamCache:
         self._fast = ((shape,) * 5, (q.dtype,) * 5 + (q.device,) * 5, strides,
                       fusion_a, fusion_b, alpha, fusion_a.data_ptr(), fusion_b.data_ptr(),
                       limit) if fast_ok else None
+        self._fast_limit = limit
+        self._native = None
+        native = _hip.fast_module()
+        if fast_ok and native is not None and self._probe is None:
+            try:
+                self._native = native.DecodeCall(
+                    q, k, v, raw_q, raw_k, fusion_a, fusion_b, float(alpha),
+                    _hip.function_address("tao_stream_decode"),
+                    _hip.function_address("tao_last_error"), self._handle.value,
+                    ctypes.addressof(self._tok), ctypes.addressof(fu),
+                    ctypes.addressof(self._info), ctypes.addressof(self._out_s),
+                    self._graph_mode, self._first_fine)
+            except TypeError:
+                self._native = None
         return self._decode_launch(q)
 
     def _decode_launch(self, q):
@@ -580,6 +607,11 @@ class StreamCache:
                                 stream, info)
         if rc:
             _hip.check(rc)
+        return self._book(pos, graph, out)
+
+    def _book(self, pos, graph, out):
+        """Cursor and counters after one driver call (info from the driver)."""
+        info = self._info
         self.position = pos + 1
         if pos >= self._first_fine:
             self.fusion_pointwise_calls += 1

@@ -224,6 +224,19 @@ typedef struct tao_stream_cfg {
   int32_t use_graph;   /* replay the decode step from a hipGraph */
 } tao_stream_cfg;
 
+/* Plan of one tao_prefill call for tokens [pos0, pos0 + tokens) of a
+ * request x layer (replaces the host chunk loop of tao_attention_prefill,
+ * operator.py:100-127, and the turn split of _read_progressive,
+ * tao_stream.py:196-227). route_coarse / route_size: the state's current
+ * route; outputs = 0 plans a state-only advance (no attention or reads; the
+ * last refresh turn is routed alone). With plan == NULL only info is filled
+ * (a size query). info (int64[8]) receives: plan length, epochs, turns,
+ * route coarse and route size after the call, page capacity of the epoch
+ * pools, chunks that read history, chunks. Host code only. */
+int tao_prefill_plan(const tao_stream_cfg* cfg, int64_t pos0, int64_t tokens,
+                     int32_t route_coarse, int32_t route_size, int32_t outputs,
+                     int64_t* plan, int64_t plan_cap, int64_t* info);
+
 /* Native per-token driver (replaces the Python control flow of one decode
  * call: operator.py:130-138, tao_stream.py:196-249 and 919-969,
  * history_region_graph.py:66-113). It keeps the cursor and the current route

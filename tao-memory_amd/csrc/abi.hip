@@ -408,6 +408,8 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
       return fail(TAO_E_ARGUMENT, "invalid route turn in the plan");
   }
   // ---- read tiles
+  if (n_read > 0 && need_pools && st->fine_cap > 16384)
+    return fail(TAO_E_CAPACITY, "prefill reads index at most 16384 fines per state");
   for (int64_t i = 0; i < n_read; ++i) {
     const int64_t* t = plan + off_read + 8 * i;
     if (t[0] < 0 || t[1] < 1 || t[1] > 32 || t[0] + t[1] > T || (t[6] != 0 && t[6] != 1))

@@ -8,15 +8,8 @@
 // run in one launch (route.hip, turn mode), and read_tiles_kernel performs
 // the selected read + fusion of all queries.
 //
-// read_tiles_kernel: one workgroup per (tile of <= 32 queries sharing one
-// route, batch, head). For each selected fine m:
-//   ch[q][d] = r(r(h_q[d] * pw[page][d]) * sw[fine][d])   (LDS, bf16)
-//   num[q][e] += sum_d ch[q][d] * C[d][e]                  v_mfma_f32_32x32x16_bf16
-// with the B operand C^T[e][d] read straight from the bank (d contiguous)
-// and prefetched one fine ahead. den = r(sum_m r(sum_d ch)) in butterfly
-// order, fine = r(r(num)/den), then the fusion epilogue with the local
-// attention output. Tiles of one head share blockIdx % 8 (XCD) when B*H is
-// a multiple of 8, so a head's bank stays in one XCD's L2.
+// read_groups_kernel: the selected read + fusion of every query, one
+// workgroup per 8 read tiles (route turns) of one head; see the kernel.
 #include "tao_launch.h"
 #include "tao_common.h"
 #include "tao_fusion.h"
@@ -29,6 +22,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTileQ = 32;
 constexpr int kMaxM = 128;
+constexpr int kMaxFineIds = 16384;   // fine ids a turn-group read can index
 
 TAO_DEV bf16x8 as_bf16x8(const uint4& u) {
   bf16x8 r;
@@ -109,154 +103,306 @@ __global__ __launch_bounds__(kThreads) void epochs_kernel(EpochParams p) {
   }
 }
 
+// Turn-group read: one 512-thread workgroup per (8 consecutive read tiles,
+// batch, head); wave w owns tile w (<= 32 queries sharing one route, its
+// own seal epoch and segment-weight source). The workgroup reads each fine
+// of the union of the 8 selected sets once: C^T is staged into padded LDS
+// (double-buffered, the next fine's rows in flight in registers), and every
+// wave whose tile selected that fine builds its A operand
+//   ch[q][d] = r(r(h_q[d] * pw[page][d]) * sw[fine][d])
+// in registers (MFMA A layout) and runs 4 x 8 v_mfma_f32_32x32x16_bf16 into
+// its 32 x D accumulator. den[q] = sum over the tile's fines of sum_d ch
+// (fp32), fine = r(r(num) / r(den)), then the fusion epilogue.
+constexpr int kGroupWaves = 8;
+constexpr int kGroupThreads = 64 * kGroupWaves;
+constexpr int kBitWords = kMaxFineIds / 32;
+constexpr int kMaxUnion = kGroupWaves * kMaxM;
+
 template <int D>
-__global__ __launch_bounds__(kThreads) void read_tiles_kernel(ReadTilesParams p) {
-  constexpr int PER = D / 64, KK = D / 16, ET = D / 32;
-  __shared__ float hq[kTileQ][D];
-  __shared__ bf16_t chs[2][kTileQ][D + 8];
-  __shared__ float chsum[kTileQ][kMaxM];
-  __shared__ int ids[kMaxM];
-  __shared__ float den[kTileQ];
+struct GroupSmem {
+  union {
+    struct {
+      uint32_t bits[kBitWords];
+      int pre[kBitWords];
+    } setup;
+    bf16_t c[2][D][D + 8];        // staged C^T, rows padded by 16 bytes
+  } u;
+  bf16_t pwsw[kGroupWaves][2][2][D];   // per wave, per buffer: pw row, sw row
+  int ids[kGroupWaves][kMaxM];
+  int uni[kMaxUnion];
+  uint32_t mask[kMaxUnion / 4];        // byte u: bit w set if wave w selected uni[u]
+  float den[kGroupWaves][32];
+  int n_union;
+};
+
+TAO_DEV void unpack8f(const uint4& u, float out[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesParams p) {
+  constexpr int KK = D / 16, ET = D / 32, CPR = D / 8;   // k-steps, e-tiles, uint4 per row
+  constexpr int CPT = D * CPR / kGroupThreads;           // C^T uint4 per thread
+  __shared__ GroupSmem<D> sm;
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
-  const int tile = blockIdx.x / BH;
+  const int grp = blockIdx.x / BH;
   const int b = bh / p.H, h = bh % p.H;
-  const int64_t* desc = p.tiles + 8 * tile;
-  const int q_first = (int)desc[0], nq = (int)desc[1], slot = (int)desc[2];
-  const int M = (int)desc[3], erel = (int)desc[4], sw_split = (int)desc[5];
-  const int fine_on = (int)desc[6];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 31, hl = lane >> 5;
+  const int t0 = grp * kGroupWaves;
+  const int nt = min(kGroupWaves, p.n_tiles - t0);
 
-  if (!fine_on) {
-    for (int i = tid; i < nq * (D / 8); i += kThreads) {
+  // This wave's tile.
+  int q_first = 0, nq = 0, slot = 0, M = 0, erel = 0, sw_split = 0, fine_on = 0;
+  if (w < nt) {
+    const int64_t* desc = p.tiles + 8 * (t0 + w);
+    q_first = (int)desc[0]; nq = (int)desc[1]; slot = (int)desc[2]; M = (int)desc[3];
+    erel = (int)desc[4]; sw_split = (int)desc[5]; fine_on = (int)desc[6];
+  }
+  const bool reads = w < nt && fine_on;
+  if (w < nt && !fine_on) {
+    // Before the first seal the output is the local attention.
+    for (int i = lane; i < nq * (D / 8); i += 64) {
       const int q = i / (D / 8), c = i % (D / 8);
       const int t = q_first + q;
       *(uint4*)(p.out + b * p.out_sb + (int64_t)t * p.out_st + h * p.out_sh + c * 8) =
           *(const uint4*)(p.local + (((size_t)b * p.T + t) * p.H + h) * D + c * 8);
     }
-    return;
   }
-  const int32_t* sel = p.sel_pool + ((size_t)slot * BH + bh) * p.sel_cap;
-  for (int m = tid; m < M; m += kThreads) ids[m] = sel[m];
-  // h = r(softmax_D(raw_q)) of the tile's queries; wave w owns q = w + 4j,
-  // all of its rows are loaded before any reduction.
-  constexpr int QPW = kTileQ / (kThreads / 64);
-  float xr[QPW][PER];
-#pragma unroll
-  for (int j = 0; j < QPW; ++j) {
-    const int q = wave + 4 * j;
-    const bf16_t* rq = p.rq.p + b * p.rq.sb + (int64_t)(q_first + min(q, nq - 1)) * p.rq.st +
-                       h * p.rq.sh;
-#pragma unroll
-    for (int k = 0; k < PER; ++k) xr[j][k] = bf2f(rq[lane + 64 * k]);
-  }
-#pragma unroll
-  for (int j = 0; j < QPW; ++j) {
-    const int q = wave + 4 * j;
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int k = 0; k < PER; ++k) mx = fmaxf(mx, xr[j][k]);
-    mx = wave_max(mx);
-    float e[PER];
-#pragma unroll
-    for (int k = 0; k < PER; ++k) e[k] = exp_cr(xr[j][k] - mx);
-    float s = e[0];
-#pragma unroll
-    for (int k = 1; k < PER; ++k) s += e[k];
-    s = wave_sum_fold(s);
-#pragma unroll
-    for (int k = 0; k < PER; ++k) hq[q][lane + 64 * k] = q < nq ? rbf(e[k] / s) : 0.0f;
+
+  // ---- union of the selected sets (ascending fine id) and per-wave masks
+  for (int i = tid; i < kBitWords; i += kGroupThreads) sm.u.setup.bits[i] = 0;
+  for (int i = tid; i < kMaxUnion / 4; i += kGroupThreads) sm.mask[i] = 0;
+  if (reads) {
+    const int32_t* sel = p.sel_pool + ((size_t)slot * BH + bh) * p.sel_cap;
+    for (int m = lane; m < M; m += 64) sm.ids[w][m] = sel[m];
   }
   __syncthreads();
+  if (reads)
+    for (int m = lane; m < M; m += 64) {
+      const int id = sm.ids[w][m];
+      atomicOr(&sm.u.setup.bits[id >> 5], 1u << (id & 31));
+    }
+  __syncthreads();
+  if (w == 0) {
+    constexpr int WPL = kBitWords / 64;
+    int cnt[WPL], total = 0;
+#pragma unroll
+    for (int i = 0; i < WPL; ++i) { cnt[i] = __popc(sm.u.setup.bits[lane * WPL + i]); total += cnt[i]; }
+    int incl = total;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int v = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += v;
+    }
+    int run = incl - total;
+#pragma unroll
+    for (int i = 0; i < WPL; ++i) { sm.u.setup.pre[lane * WPL + i] = run; run += cnt[i]; }
+    if (lane == 63) sm.n_union = incl;
+  }
+  __syncthreads();
+  for (int i = tid; i < kBitWords; i += kGroupThreads) {
+    uint32_t bits = sm.u.setup.bits[i];
+    int r = sm.u.setup.pre[i];
+    while (bits) {
+      const int bit = __ffs(bits) - 1;
+      sm.uni[r++] = i * 32 + bit;
+      bits &= bits - 1;
+    }
+  }
+  if (reads)
+    for (int m = lane; m < M; m += 64) {
+      const int id = sm.ids[w][m];
+      const uint32_t word = sm.u.setup.bits[id >> 5];
+      const int rank = sm.u.setup.pre[id >> 5] + __popc(word & ((1u << (id & 31)) - 1u));
+      atomicOr(&sm.mask[rank >> 2], 1u << ((rank & 3) * 8 + w));
+    }
+  __syncthreads();
+  const int U = sm.n_union;
+
+  // ---- h of this wave's queries in the MFMA A layout: lane (li, hl) holds
+  // row q = li, channels d = 16 kk + 8 hl + j (packed bf16).
+  uint4 hpk[KK];
+  if (reads) {
+    const int q = li < nq ? li : nq - 1;
+    const bf16_t* rq = p.rq.p + b * p.rq.sb + (int64_t)(q_first + q) * p.rq.st + h * p.rq.sh;
+    float x[KK][8];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      unpack8f(*(const uint4*)(rq + 16 * kk + 8 * hl), x[kk]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, x[kk][j]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { x[kk][j] = __expf(x[kk][j] - mx); sum += x[kk][j]; }
+    sum += __shfl_xor(sum, 32, 64);
+    const float inv_valid = li < nq ? 1.0f : 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      uint32_t wv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        wv[j] = pack_bf16x2(x[kk][2 * j] / sum * inv_valid, x[kk][2 * j + 1] / sum * inv_valid);
+      hpk[kk] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+    }
+  }
+
+  // ---- stream the union
   const bf16_t* bank = p.bank + (size_t)bh * p.fine_cap * D * D;
   const bf16_t* pw_base = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
   const bf16_t* psw_base = p.psw_pool ? p.psw_pool + ((size_t)erel * BH + bh) * 8 * D : nullptr;
   const bf16_t* sw_base = p.sw + (size_t)bh * p.fine_cap * D;
-  const int e_row = 32 * wave + li;          // C^T row this lane feeds (wave < ET)
-
-  // Operands of fine `id`: C^T rows (waves < ET), page-weight and
-  // segment-weight channels of this lane.
-  auto fetch = [&](int id, uint4* c, float* pwv, float* swv) {
-    if (wave < ET) {
-      const bf16_t* crow = bank + ((size_t)id * D + e_row) * D;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) c[kk] = *(const uint4*)(crow + 16 * kk + 8 * hl);
-    }
+  auto active = [&](int u) __attribute__((always_inline)) { return reads && ((sm.mask[u >> 2] >> ((u & 3) * 8 + w)) & 1u); };
+  // C^T rows of union entry u: thread tid moves uint4 chunks tid + i * 512,
+  // i < CPT, held in four named registers (c0..c3).
+  static_assert(CPT == 1 || CPT == 4, "head width 64 or 128");
+#define TAO_C_CHUNK(i_) (bank + (size_t)cid * D * D + (size_t)(tid + (i_) * kGroupThreads) * 8)
+#define TAO_LOAD_C(u)                                                    \
+  do {                                                                   \
+    const int cid = sm.uni[(u)];                                         \
+    c0 = *(const uint4*)TAO_C_CHUNK(0);                                  \
+    if constexpr (CPT == 4) {                                            \
+      c1 = *(const uint4*)TAO_C_CHUNK(1);                                \
+      c2 = *(const uint4*)TAO_C_CHUNK(2);                                \
+      c3 = *(const uint4*)TAO_C_CHUNK(3);                                \
+    }                                                                    \
+  } while (0)
+#define TAO_C_SLOT(buf, i_)                                              \
+  (*(uint4*)&sm.u.c[(buf)][(tid + (i_) * kGroupThreads) / CPR]           \
+                  [((tid + (i_) * kGroupThreads) % CPR) * 8])
+#define TAO_STORE_C(buf)                                                 \
+  do {                                                                   \
+    TAO_C_SLOT(buf, 0) = c0;                                             \
+    if constexpr (CPT == 4) {                                            \
+      TAO_C_SLOT(buf, 1) = c1;                                           \
+      TAO_C_SLOT(buf, 2) = c2;                                           \
+      TAO_C_SLOT(buf, 3) = c3;                                           \
+    }                                                                    \
+  } while (0)
+  // pw / sw rows of fine id for this wave: lane l < D / 2 moves 4 bytes of each.
+  auto load_w = [&](int u, uint32_t& pwv, uint32_t& swv) __attribute__((always_inline)) {
+    const int id = sm.uni[u];
     const bf16_t* pw = pw_base + (size_t)(id / p.group) * D;
-    const bf16_t* sw = id < sw_split ? sw_base + (size_t)id * D
-                                     : psw_base + (size_t)(id - sw_split) * D;
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      pwv[k] = bf2f(pw[lane + 64 * k]);
-      swv[k] = bf2f(sw[lane + 64 * k]);
+    const bf16_t* sw = id < sw_split ? sw_base + (size_t)id * D : psw_base + (size_t)(id - sw_split) * D;
+    if (lane < D / 2) {
+      pwv = *(const uint32_t*)(pw + 2 * lane);
+      swv = *(const uint32_t*)(sw + 2 * lane);
+    }
+  };
+  auto store_w = [&](int buf, uint32_t pwv, uint32_t swv) __attribute__((always_inline)) {
+    if (lane < D / 2) {
+      *(uint32_t*)&sm.pwsw[w][buf][0][2 * lane] = pwv;
+      *(uint32_t*)&sm.pwsw[w][buf][1][2 * lane] = swv;
     }
   };
 
-  floatx16 acc;
+  floatx16 acc[ET];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-  uint4 creg[KK], cnext[KK];
-  float pwv[PER], swv[PER], pwn[PER], swn[PER];
-  fetch(ids[0], creg, pwv, swv);
-  for (int m = 0; m < M; ++m) {
-    const int buf = m & 1;
-    for (int q = wave; q < kTileQ; q += kThreads / 64) {
-      float v[PER];
+  for (int t = 0; t < ET; ++t)
 #pragma unroll
-      for (int k = 0; k < PER; ++k) {
-        const int d = lane + 64 * k;
-        v[k] = q < nq ? rbf(rbf(hq[q][d] * pwv[k]) * swv[k]) : 0.0f;
-        chs[buf][q][d] = f2bf(v[k]);
-      }
-      float s = v[0];
-#pragma unroll
-      for (int k = 1; k < PER; ++k) s += v[k];
-      s = wave_sum_fold(s);
-      if (lane == 0) chsum[q][m] = rbf(s);
-    }
-    if (m + 1 < M) fetch(ids[m + 1], cnext, pwn, swn);
-    __syncthreads();
-    if (wave < ET) {
+    for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+  float den_part = 0.0f;
+  uint4 c0, c1, c2, c3;
+  uint32_t pwv = 0, swv = 0;
+  if (U > 0) {
+    TAO_LOAD_C(0);
+    if (active(0)) load_w(0, pwv, swv);
+    TAO_STORE_C(0);
+    if (active(0)) store_w(0, pwv, swv);
+  }
+  __syncthreads();
+  for (int u = 0; u < U; ++u) {
+    const int buf = u & 1;
+    const bool next = u + 1 < U;
+    const bool act_next = next && active(u + 1);
+    if (next) TAO_LOAD_C(u + 1);
+    if (act_next) load_w(u + 1, pwv, swv);
+    if (active(u)) {
+      const bf16_t* pwr = sm.pwsw[w][buf][0];
+      const bf16_t* swr = sm.pwsw[w][buf][1];
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        const bf16x8 a = as_bf16x8(*(const uint4*)&chs[buf][li][16 * kk + 8 * hl]);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(creg[kk]), acc, 0, 0, 0);
+        const int d0 = 16 * kk + 8 * hl;
+        float hv[8], pv[8], sv[8];
+        unpack8f(hpk[kk], hv);
+        unpack8f(*(const uint4*)(pwr + d0), pv);
+        unpack8f(*(const uint4*)(swr + d0), sv);
+        uint32_t t1[4], ch[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t1[j] = pack_bf16x2(hv[2 * j] * pv[2 * j], hv[2 * j + 1] * pv[2 * j + 1]);
+        float tv[8];
+        unpack8f(make_uint4(t1[0], t1[1], t1[2], t1[3]), tv);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ch[j] = pack_bf16x2(tv[2 * j] * sv[2 * j], tv[2 * j + 1] * sv[2 * j + 1]);
+        const uint4 chq = make_uint4(ch[0], ch[1], ch[2], ch[3]);
+        float cv[8];
+        unpack8f(chq, cv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) den_part += cv[j];
+        const bf16x8 a = as_bf16x8(chq);
+#pragma unroll
+        for (int t = 0; t < ET; ++t) {
+          const bf16x8 bq = as_bf16x8(*(const uint4*)&sm.u.c[buf][32 * t + li][d0]);
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq, acc[t], 0, 0, 0);
+        }
       }
     }
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) creg[kk] = cnext[kk];
-#pragma unroll
-    for (int k = 0; k < PER; ++k) { pwv[k] = pwn[k]; swv[k] = swn[k]; }
+    if (next) TAO_STORE_C(buf ^ 1);
+    if (act_next) store_w(buf ^ 1, pwv, swv);
+    __syncthreads();
+  }
+
+#undef TAO_LOAD_C
+#undef TAO_STORE_C
+#undef TAO_C_SLOT
+#undef TAO_C_CHUNK
+  // ---- epilogue: den per query, then fine = r(r(num) / r(den)) and fusion.
+  if (reads) {
+    const float den_row = den_part + __shfl_xor(den_part, 32, 64);
+    if (hl == 0) sm.den[w][li] = den_row;
   }
   __syncthreads();
-  // den per query: slot m in lane m % 64, position m / 64 (M <= 128).
-  for (int q = wave; q < kTileQ; q += kThreads / 64) {
-    const float v0 = lane < M ? chsum[q][lane] : 0.0f;
-    const float v1 = lane + 64 < M ? chsum[q][lane + 64] : 0.0f;
-    const float s = wave_sum_fold(M > 64 ? v0 + v1 : v0);
-    if (lane == 0) den[q] = rbf(s);
-  }
-  __syncthreads();
-  if (wave >= ET) return;
-  const int e = 32 * wave + li;
-  float a[3], bb[3];
+  if (!reads) return;
+  // One e-tile of the accumulator (called with constant t, so acc stays in
+  // registers).
+  auto emit = [&](const floatx16& av, int t) __attribute__((always_inline)) {
+    const int e = 32 * t + li;
+    float ae[3], be[3];
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    a[i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + e * p.fa_s[1] + i * p.fa_s[2]);
-    bb[i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + e * p.fb_s[1] + i * p.fb_s[2]);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int q = 8 * (i / 4) + 4 * hl + (i % 4);
-    if (q < nq) {
-      const int t = q_first + q;
-      const float fine = rbf(rbf(acc[i]) / den[q]);
-      const float local = bf2f(p.local[(((size_t)b * p.T + t) * p.H + h) * D + e]);
-      const float x = bf2f(p.rq.p[b * p.rq.sb + (int64_t)t * p.rq.st + h * p.rq.sh + e]);
-      p.out[b * p.out_sb + (int64_t)t * p.out_st + h * p.out_sh + e] =
-          fuse_element(x, local, 0.0f, fine, a, bb, p.gain, 0, 1);
+    for (int i = 0; i < 3; ++i) {
+      ae[i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + e * p.fa_s[1] + i * p.fa_s[2]);
+      be[i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + e * p.fb_s[1] + i * p.fb_s[2]);
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int q = 8 * (i / 4) + 4 * hl + (i % 4);
+      if (q < nq) {
+        const int tq = q_first + q;
+        const float fine = rbf(rbf(av[i]) / rbf(sm.den[w][q]));
+        const float local = bf2f(p.local[(((size_t)b * p.T + tq) * p.H + h) * D + e]);
+        const float x = bf2f(p.rq.p[b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + e]);
+        p.out[b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + e] =
+            fuse_element(x, local, 0.0f, fine, ae, be, p.gain, 0, 1);
+      }
+    }
+  };
+  static_assert(ET == 2 || ET == 4, "head width 64 or 128");
+  emit(acc[0], 0);
+  emit(acc[1], 1);
+  if constexpr (ET == 4) {
+    emit(acc[2], 2);
+    emit(acc[3], 3);
   }
 }
 
@@ -292,11 +438,13 @@ hipError_t launch_epochs(const EpochParams& p, int head_dim, hipStream_t s) {
 
 hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t s) {
   if (p.n_tiles <= 0) return hipSuccess;
-  const dim3 grid((unsigned)(p.n_tiles * p.B * p.H));
+  if (p.fine_cap > kMaxFineIds) return hipErrorInvalidValue;
+  const int groups = (p.n_tiles + kGroupWaves - 1) / kGroupWaves;
+  const dim3 grid((unsigned)(groups * p.B * p.H));
   if (head_dim == 128)
-    hipLaunchKernelGGL(read_tiles_kernel<128>, grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL(read_groups_kernel<128>, grid, dim3(kGroupThreads), 0, s, p);
   else if (head_dim == 64)
-    hipLaunchKernelGGL(read_tiles_kernel<64>, grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL(read_groups_kernel<64>, grid, dim3(kGroupThreads), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -11,6 +11,7 @@
 // Python host's schedule module).
 #include <cstring>
 
+#include "schedule.h"
 #include "tao_launch.h"
 
 extern "C" int tao_route(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
@@ -29,6 +30,10 @@ extern "C" int tao_graph_destroy(void* graph);
 
 namespace {
 
+using tao::sched::fines_at;
+using tao::sched::is_turn;
+using tao::sched::local_len_at;
+
 struct Stream {
   tao_state_dev st;
   tao_stream_cfg cfg;
@@ -42,45 +47,6 @@ struct Stream {
   int64_t* seal_start = nullptr;   // device int64 (first word of the plan region)
   int64_t seal_host = 0;           // host copy staged by the seal's upload
 };
-
-int64_t local_len_at(const tao_stream_cfg& c, int64_t p) {
-  const int64_t limit = c.local_keep + c.fine_tokens;
-  return p < limit ? p : c.local_keep + (p - limit) % c.fine_tokens;
-}
-
-int64_t fines_at(const tao_stream_cfg& c, int64_t p) {
-  const int64_t limit = c.local_keep + c.fine_tokens;
-  return p < limit ? 0 : (p - limit) / c.fine_tokens + 1;
-}
-
-bool is_turn(const tao_stream_cfg& c, int64_t p) {
-  const int64_t first = c.local_keep + c.fine_tokens;
-  const int64_t first_turn = first + (int64_t)c.layer_stagger * c.layer;
-  return p == first || (p >= first_turn && (p - first_turn) % c.route_period == 0);
-}
-
-int64_t budget(const tao_stream_cfg& c, int64_t n) {
-  if (n <= 0) return 0;
-  const int64_t target = (int64_t)c.budget_root_scale * n;
-  int64_t r = 0;
-  while ((r + 1) * (r + 1) <= target) ++r;    // isqrt (n is small)
-  if (r * r < target) ++r;
-  const int64_t b = r + c.budget_offset;
-  return b < n ? b : n;
-}
-
-void routed_counts(const tao_stream_cfg& c, int64_t completed, int64_t pending,
-                   int32_t* coarse_out, int32_t* selected_out) {
-  const int64_t g = c.coarse_group;
-  const int64_t cb = budget(c, g * completed);
-  int64_t coarse = (2 * cb + g - 1) / g;
-  if (coarse > completed) coarse = completed;
-  const int64_t eligible = g * coarse + pending;
-  int64_t sel = budget(c, g * completed + pending);
-  if (sel > eligible) sel = eligible;
-  *coarse_out = (int32_t)coarse;
-  *selected_out = (int32_t)sel;
-}
 
 int stream_fail(int code, const char* msg) {
   tao::set_error(msg);
@@ -152,8 +118,9 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
   int refreshed = 0, sealed = 0;
   if (fines > 0 && is_turn(c, pos)) {
     const int64_t completed = fines / c.coarse_group, pending = fines % c.coarse_group;
-    int32_t coarse = 0, selected = 0;
-    routed_counts(c, completed, pending, &coarse, &selected);
+    int64_t coarse64 = 0, eligible = 0, selected64 = 0;
+    tao::sched::routed_counts(c, completed, pending, &coarse64, &eligible, &selected64);
+    const int32_t coarse = (int32_t)coarse64, selected = (int32_t)selected64;
     const int64_t rq_s[2] = {tok->rq_s[0], tok->rq_s[2]};
     rc = tao_route(&s->st, tok->raw_q, rq_s, (int32_t)completed, (int32_t)pending, coarse,
                    selected, stream);

@@ -85,6 +85,8 @@ _SIGNATURES = {
                      ctypes.POINTER(_i64), _vp], _i32),
     "tao_ring_append": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i32, _i32,
                          _i64, _vp], _i32),
+    "tao_prefill_plan": ([ctypes.POINTER(StreamCfg), _i64, _i64, _i32, _i32, _i32,
+                          _vp, _i64, ctypes.POINTER(_i64)], _i32),
     "tao_stream_open": ([ctypes.POINTER(StateDev), ctypes.POINTER(StreamCfg), _i64, _i32, _i32,
                          _vp, _vp, ctypes.POINTER(_vp)], _i32),
     "tao_stream_sync": ([_vp, ctypes.POINTER(StateDev), _i64, _i32, _i32], _i32),

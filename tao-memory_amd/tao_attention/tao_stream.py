@@ -328,82 +328,30 @@ class StreamCache:
                 dev.stream()))
 
     # ---------------------------------------------------------------- streaming
-    def _plan(self, pos0, tokens, outputs, turn_filter=None):
-        """int64 plan of tao_prefill for tokens [pos0, pos0 + tokens).
+    def _stream_cfg(self):
+        cfg = self.config
+        return _hip.StreamCfg(self.layer_index, cfg.local_keep, cfg.fine_tokens,
+                              cfg.coarse_group, cfg.route_period, cfg.layer_stagger,
+                              cfg.budget_root_scale, cfg.budget_offset,
+                              int(cfg.q1_history_region_graph))
+
+    def _plan(self, pos0, tokens, outputs):
+        """int64 plan of tao_prefill for tokens [pos0, pos0 + tokens), built by
+        the library (tao_prefill_plan).
 
         outputs=False plans a state-only advance (no attention or reads; only
         the last refresh turn is routed, in its own epoch).
         """
-        cfg = self.config
-        group = cfg.coarse_group
-        end = pos0 + tokens
-        f0, f1 = schedule.fines_at(pos0, cfg), schedule.fines_at(end, cfg)
-        plan_chunks = schedule.chunks(pos0, tokens, cfg)
-        attn, reads, turns = [], [], []
-        chunk_epochs = []
-        for start, width in plan_chunks:
-            epoch = schedule.fines_at(start, cfg)
-            chunk_epochs.append(epoch)
-            if outputs:
-                key_start = start - schedule.local_len_at(start, cfg)
-                for qs in range(start, start + width, _QTILE):
-                    attn += [qs - pos0, min(_QTILE, start + width - qs), key_start]
-        # Epochs read by this call plus the published final epoch.
-        if f1 >= 1:
-            first_epoch = max(min([e for e in chunk_epochs if e >= 1] + [f1]), 1)
-        else:
-            first_epoch = 0
-        if not outputs and f1 >= 1:
-            first_epoch = f1
-        slot, slot_m = 0, self.route_size
-        route = (self.route_coarse, self.route_size)
-        last_turn = None
-        for (start, width), epoch in zip(plan_chunks, chunk_epochs):
-            for sub, count, refresh in schedule.sub_chunks(start, width, self.layer_index, cfg):
-                if epoch == 0:
-                    if outputs:
-                        for qs in range(sub, sub + count, 32):
-                            reads += [qs - pos0, min(32, sub + count - qs), 0, 0, 0, 0, 0, 0]
-                    continue
-                if refresh:
-                    completed, pending = divmod(epoch, group)
-                    coarse, _, selected = schedule.routed_counts(completed, pending, cfg)
-                    last_turn = (sub, epoch, completed, pending, coarse, selected)
-                    if outputs:
-                        turns += [sub - pos0, epoch - first_epoch, completed, pending,
-                                  coarse, selected, len(turns) // 8 + 1, 0]
-                        slot, slot_m = len(turns) // 8, selected
-                    route = (coarse, selected)
-                if outputs:
-                    for qs in range(sub, sub + count, 32):
-                        reads += [qs - pos0, min(32, sub + count - qs), slot, slot_m,
-                                  epoch - first_epoch, (epoch // group) * group, 1, 0]
-        if not outputs and last_turn is not None:
-            sub, epoch, completed, pending, coarse, selected = last_turn
-            first_epoch = min(first_epoch, epoch)
-            turns = [sub - pos0, epoch - first_epoch, completed, pending, coarse, selected, 1, 1]
-        elif turns:
-            turns[-1] = 1
-        n_epochs = f1 - first_epoch + 1 if f1 >= 1 else 0
-        writes = [cfg.fine_tokens * f for f in range(f0, f1)]
-        keep = min(tokens, cfg.serve_limit)
-        header = [0] * _hip.PLAN_HEADER
-        header[0] = pos0
-        header[1] = len(attn) // 3
-        header[2] = len(writes)
-        header[3] = f0
-        header[4] = f0 // group
-        header[5] = f1 // group - f0 // group
-        header[6] = first_epoch
-        header[7] = n_epochs
-        header[8] = len(turns) // 8
-        header[9] = len(reads) // 8
-        header[10] = tokens - keep
-        header[11] = keep
-        header[12] = end - keep
-        plan = header + attn + writes + turns + reads
-        return plan, dict(epochs=n_epochs, turns=len(turns) // 8, route=route,
-                          pool_pcap=f1 // group + 1, chunk_epochs=chunk_epochs)
+        lib = _hip.lib()
+        scfg = self._stream_cfg()
+        info = (ctypes.c_int64 * 8)()
+        args = (ctypes.byref(scfg), pos0, tokens, self.route_coarse, self.route_size,
+                int(outputs))
+        _hip.check(lib.tao_prefill_plan(*args, None, 0, info))
+        plan = np.empty(info[0], dtype=np.int64)
+        _hip.check(lib.tao_prefill_plan(*args, plan.ctypes.data, info[0], info))
+        return plan, dict(epochs=info[1], turns=info[2], route=(info[3], info[4]),
+                          pool_pcap=info[5], history_chunks=info[6], chunks=info[7])
 
     def _run_plan(self, dev, tok, fu, plan, info, local, out):
         plan_np = np.asarray(plan, dtype=np.int64)
@@ -451,11 +399,8 @@ class StreamCache:
         fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
         self._run_plan(dev, tok, fu, plan, info, local, out)
         self._advance(pos0, tokens, info)
-        for epoch in info["chunk_epochs"]:
-            if epoch:
-                self.fusion_pointwise_calls += 1
-            else:
-                self.fusion_no_history_local_returns += 1
+        self.fusion_pointwise_calls += info["history_chunks"]
+        self.fusion_no_history_local_returns += info["chunks"] - info["history_chunks"]
         return out
 
     def _advance(self, pos0, tokens, info):
@@ -480,10 +425,7 @@ class StreamCache:
         """Native per-token driver bound to the current buffers and cursor."""
         cfg = self.config
         if self._handle is None:
-            scfg = _hip.StreamCfg(self.layer_index, cfg.local_keep, cfg.fine_tokens,
-                                  cfg.coarse_group, cfg.route_period, cfg.layer_stagger,
-                                  cfg.budget_root_scale, cfg.budget_offset,
-                                  int(cfg.q1_history_region_graph))
+            scfg = self._stream_cfg()
             staging = out_stage = None
             if cfg.q1_history_region_graph:
                 B, H, D = dev.B, dev.H, dev.D
@@ -648,11 +590,11 @@ class StreamCache:
         q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
         plan, _ = self._plan(pos0, tokens, outputs=True)
-        n_attn, n_write = plan[1], plan[2]
+        n_attn, n_write = int(plan[1]), int(plan[2])
         base = _hip.PLAN_HEADER
-        tiles = torch.tensor(plan[base:base + 3 * n_attn], dtype=torch.int64).to(q.device)
-        starts = torch.tensor(plan[base + 3 * n_attn:base + 3 * n_attn + n_write] or [0],
-                              dtype=torch.int64).to(q.device)
+        tiles = torch.from_numpy(plan[base:base + 3 * n_attn].copy()).to(q.device)
+        starts = torch.from_numpy(plan[base + 3 * n_attn:base + 3 * n_attn + max(n_write, 1)]
+                                  .copy()).to(q.device)
         local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
         lib = _hip.lib()
         with self._timed("local_attention"):
@@ -661,8 +603,8 @@ class StreamCache:
                 n_attn, local.data_ptr(), dev.stream()))
         with self._timed("writer"):
             _hip.check(lib.tao_write_fine(
-                ctypes.byref(dev.struct), ctypes.byref(tok), pos0, starts.data_ptr(), plan[3],
-                n_write, dev.stream()))
+                ctypes.byref(dev.struct), ctypes.byref(tok), pos0, starts.data_ptr(),
+                int(plan[3]), n_write, dev.stream()))
         return local
 
     def _ingest(self, q, k, v, raw_q, raw_k):

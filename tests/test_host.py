@@ -112,3 +112,101 @@ def test_count_turns_closed_form():
             for hi in (lo, lo + 1, lo + 23, lo + 24, lo + 500, lo + 3000):
                 brute = sum(1 for p in range(lo, hi) if schedule.is_turn(p, layer, cfg))
                 assert schedule.count_turns(lo, hi, layer, cfg) == brute, (layer, lo, hi)
+
+
+def _reference_plan(cfg, layer, route_coarse, route_size, pos0, tokens, outputs):
+    """Prefill plan written out from the schedule closed forms (checker for
+    the library's tao_prefill_plan)."""
+    group = cfg.coarse_group
+    end = pos0 + tokens
+    f0, f1 = schedule.fines_at(pos0, cfg), schedule.fines_at(end, cfg)
+    plan_chunks = schedule.chunks(pos0, tokens, cfg)
+    attn, reads, turns, chunk_epochs = [], [], [], []
+    for start, width in plan_chunks:
+        epoch = schedule.fines_at(start, cfg)
+        chunk_epochs.append(epoch)
+        if outputs:
+            key_start = start - schedule.local_len_at(start, cfg)
+            for qs in range(start, start + width, 256):
+                attn += [qs - pos0, min(256, start + width - qs), key_start]
+    first_epoch = 0
+    if f1 >= 1:
+        first_epoch = max(min([e for e in chunk_epochs if e >= 1] + [f1]), 1)
+        if not outputs:
+            first_epoch = f1
+    slot, slot_m = 0, route_size
+    route = (route_coarse, route_size)
+    last_turn = None
+    for (start, width), epoch in zip(plan_chunks, chunk_epochs):
+        for sub, count, refresh in schedule.sub_chunks(start, width, layer, cfg):
+            if epoch == 0:
+                if outputs:
+                    for qs in range(sub, sub + count, 32):
+                        reads += [qs - pos0, min(32, sub + count - qs), 0, 0, 0, 0, 0, 0]
+                continue
+            if refresh:
+                completed, pending = divmod(epoch, group)
+                coarse, _, selected = schedule.routed_counts(completed, pending, cfg)
+                last_turn = (sub, epoch, completed, pending, coarse, selected)
+                if outputs:
+                    turns += [sub - pos0, epoch - first_epoch, completed, pending, coarse,
+                              selected, len(turns) // 8 + 1, 0]
+                    slot, slot_m = len(turns) // 8, selected
+                route = (coarse, selected)
+            if outputs:
+                for qs in range(sub, sub + count, 32):
+                    reads += [qs - pos0, min(32, sub + count - qs), slot, slot_m,
+                              epoch - first_epoch, (epoch // group) * group, 1, 0]
+    if not outputs and last_turn is not None:
+        sub, epoch, completed, pending, coarse, selected = last_turn
+        first_epoch = min(first_epoch, epoch)
+        turns = [sub - pos0, epoch - first_epoch, completed, pending, coarse, selected, 1, 1]
+    elif turns:
+        turns[-1] = 1
+    n_epochs = f1 - first_epoch + 1 if f1 >= 1 else 0
+    writes = [cfg.fine_tokens * f for f in range(f0, f1)]
+    keep = min(tokens, cfg.serve_limit)
+    header = [0] * _hip.PLAN_HEADER
+    header[:13] = [pos0, len(attn) // 3, len(writes), f0, f0 // group,
+                   f1 // group - f0 // group, first_epoch, n_epochs, len(turns) // 8,
+                   len(reads) // 8, tokens - keep, keep, end - keep]
+    history = sum(1 for e in chunk_epochs if e)
+    info = [None, n_epochs, len(turns) // 8, route[0], route[1], f1 // group + 1, history,
+            len(chunk_epochs)]
+    return header + attn + writes + turns + reads, info
+
+
+def test_native_prefill_plan_matches_closed_forms():
+    """tao_prefill_plan (host code in the library) against the plan written
+    out from the schedule closed forms, over positions, widths, layers,
+    carried routes and both modes."""
+    import numpy as np
+    lib = _hip.lib()
+    cfg = index_only_page_memo()
+    cases = 0
+    for layer in (0, 1, 5):
+        scfg = _hip.StreamCfg(layer, cfg.local_keep, cfg.fine_tokens, cfg.coarse_group,
+                              cfg.route_period, cfg.layer_stagger, cfg.budget_root_scale,
+                              cfg.budget_offset, 0)
+        for pos0 in (0, 100, 767, 768, 769, 1000, 2050, 5000, 131072):
+            for tokens in (0, 1, 5, 24, 255, 256, 300, 800, 2048, 6000):
+                f = schedule.fines_at(pos0, cfg)
+                routes = [(0, 0)] if f == 0 else [(1, 3), (4, 14)]
+                for rc, rs in routes:
+                    for outputs in (True, False):
+                        want, want_info = _reference_plan(cfg, layer, rc, rs, pos0, tokens,
+                                                          outputs)
+                        info = (ctypes.c_int64 * 8)()
+                        args = (ctypes.byref(scfg), pos0, tokens, rc, rs, int(outputs))
+                        assert lib.tao_prefill_plan(*args, None, 0, info) == 0
+                        assert info[0] == len(want)
+                        got = np.zeros(info[0], dtype=np.int64)
+                        assert lib.tao_prefill_plan(*args, got.ctypes.data, info[0], info) == 0
+                        assert got.tolist() == want, (layer, pos0, tokens, rc, rs, outputs)
+                        assert list(info)[1:] == want_info[1:]
+                        cases += 1
+    assert cases > 400
+    small = (ctypes.c_int64 * 8)()
+    buf = np.zeros(4, dtype=np.int64)
+    assert lib.tao_prefill_plan(ctypes.byref(scfg), 0, 300, 0, 0, 1, buf.ctypes.data, 4,
+                                small) < 0

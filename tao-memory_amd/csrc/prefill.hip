@@ -110,9 +110,10 @@ __global__ __launch_bounds__(kThreads) void epochs_kernel(EpochParams p) {
 // (double-buffered, the next fine's rows in flight in registers), and every
 // wave whose tile selected that fine builds its A operand
 //   ch[q][d] = r(r(h_q[d] * pw[page][d]) * sw[fine][d])
-// in registers (MFMA A layout) and runs 4 x 8 v_mfma_f32_32x32x16_bf16 into
-// its 32 x D accumulator. den[q] = sum over the tile's fines of sum_d ch
-// (fp32), fine = r(r(num) / r(den)), then the fusion epilogue.
+// in registers (MFMA A layout; r(h * pw) is kept per page) and runs
+// 4 x 8 v_mfma_f32_32x32x16_bf16 into its 32 x D accumulator, plus one
+// against a column of ones for den[q] = sum over the tile's fines of
+// sum_d ch; fine = r(r(num) / r(den)), then the fusion epilogue.
 constexpr int kGroupWaves = 8;
 constexpr int kGroupThreads = 64 * kGroupWaves;
 constexpr int kBitWords = kMaxFineIds / 32;
@@ -128,10 +129,10 @@ struct GroupSmem {
     bf16_t c[2][D][D + 8];        // staged C^T, rows padded by 16 bytes
   } u;
   bf16_t pwsw[kGroupWaves][2][2][D];   // per wave, per buffer: pw row, sw row
+  bf16_t hq[kGroupWaves][32][D + 8];   // per wave: h of its queries (bf16, padded rows)
   int ids[kGroupWaves][kMaxM];
   int uni[kMaxUnion];
   uint32_t mask[kMaxUnion / 4];        // byte u: bit w set if wave w selected uni[u]
-  float den[kGroupWaves][32];
   int n_union;
 };
 
@@ -228,7 +229,6 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
 
   // ---- h of this wave's queries in the MFMA A layout: lane (li, hl) holds
   // row q = li, channels d = 16 kk + 8 hl + j (packed bf16).
-  uint4 hpk[KK];
   if (reads) {
     const int q = li < nq ? li : nq - 1;
     const bf16_t* rq = p.rq.p + b * p.rq.sb + (int64_t)(q_first + q) * p.rq.st + h * p.rq.sh;
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         wv[j] = pack_bf16x2(x[kk][2 * j] / sum * inv_valid, x[kk][2 * j + 1] / sum * inv_valid);
-      hpk[kk] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+      *(uint4*)&sm.hq[w][li][16 * kk + 8 * hl] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
     }
   }
 
@@ -265,29 +265,29 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
   const bf16_t* sw_base = p.sw + (size_t)bh * p.fine_cap * D;
   auto active = [&](int u) __attribute__((always_inline)) { return reads && ((sm.mask[u >> 2] >> ((u & 3) * 8 + w)) & 1u); };
   // C^T rows of union entry u: thread tid moves uint4 chunks tid + i * 512,
-  // i < CPT, held in four named registers (c0..c3).
+  // i < CPT, into one of two named register sets (X = a or b).
   static_assert(CPT == 1 || CPT == 4, "head width 64 or 128");
 #define TAO_C_CHUNK(i_) (bank + (size_t)cid * D * D + (size_t)(tid + (i_) * kGroupThreads) * 8)
-#define TAO_LOAD_C(u)                                                    \
+#define TAO_LOAD_C(u, X)                                                 \
   do {                                                                   \
     const int cid = sm.uni[(u)];                                         \
-    c0 = *(const uint4*)TAO_C_CHUNK(0);                                  \
+    X##0 = *(const uint4*)TAO_C_CHUNK(0);                                \
     if constexpr (CPT == 4) {                                            \
-      c1 = *(const uint4*)TAO_C_CHUNK(1);                                \
-      c2 = *(const uint4*)TAO_C_CHUNK(2);                                \
-      c3 = *(const uint4*)TAO_C_CHUNK(3);                                \
+      X##1 = *(const uint4*)TAO_C_CHUNK(1);                              \
+      X##2 = *(const uint4*)TAO_C_CHUNK(2);                              \
+      X##3 = *(const uint4*)TAO_C_CHUNK(3);                              \
     }                                                                    \
   } while (0)
 #define TAO_C_SLOT(buf, i_)                                              \
   (*(uint4*)&sm.u.c[(buf)][(tid + (i_) * kGroupThreads) / CPR]           \
                   [((tid + (i_) * kGroupThreads) % CPR) * 8])
-#define TAO_STORE_C(buf)                                                 \
+#define TAO_STORE_C(buf, X)                                              \
   do {                                                                   \
-    TAO_C_SLOT(buf, 0) = c0;                                             \
+    TAO_C_SLOT(buf, 0) = X##0;                                           \
     if constexpr (CPT == 4) {                                            \
-      TAO_C_SLOT(buf, 1) = c1;                                           \
-      TAO_C_SLOT(buf, 2) = c2;                                           \
-      TAO_C_SLOT(buf, 3) = c3;                                           \
+      TAO_C_SLOT(buf, 1) = X##1;                                         \
+      TAO_C_SLOT(buf, 2) = X##2;                                         \
+      TAO_C_SLOT(buf, 3) = X##3;                                         \
     }                                                                    \
   } while (0)
   // pw / sw rows of fine id for this wave: lane l < D / 2 moves 4 bytes of each.
@@ -312,54 +312,93 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
   for (int t = 0; t < ET; ++t)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
-  float den_part = 0.0f;
-  uint4 c0, c1, c2, c3;
-  uint32_t pwv = 0, swv = 0;
-  if (U > 0) {
-    TAO_LOAD_C(0);
-    if (active(0)) load_w(0, pwv, swv);
-    TAO_STORE_C(0);
-    if (active(0)) store_w(0, pwv, swv);
-  }
-  __syncthreads();
-  for (int u = 0; u < U; ++u) {
+  floatx16 acc_den;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc_den[i] = 0.0f;
+  // Pipeline: while fine u is consumed from LDS buffer u & 1, fine u + 1
+  // waits in one register set (stored to LDS at the end of the iteration)
+  // and fine u + 2's loads are in flight in the other, so each global load
+  // has a whole iteration to arrive.
+  uint4 a0, a1, a2, a3, b0, b1, b2, b3;
+  uint32_t pwa = 0, swa = 0, pwb = 0, swb = 0;
+  // Per wave: t = r(h * pw[page]) of the page last used, packed in the A
+  // layout (consecutive union fines mostly share a page).
+  uint4 tpk[KK];
+  int cached_page = -1;
+  const bf16x8 ones = as_bf16x8(make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u));
+  auto consume = [&](int u) __attribute__((always_inline)) {
+    if (!active(u)) return;
     const int buf = u & 1;
-    const bool next = u + 1 < U;
-    const bool act_next = next && active(u + 1);
-    if (next) TAO_LOAD_C(u + 1);
-    if (act_next) load_w(u + 1, pwv, swv);
-    if (active(u)) {
+    const int page = sm.uni[u] / p.group;
+    if (page != cached_page) {
       const bf16_t* pwr = sm.pwsw[w][buf][0];
-      const bf16_t* swr = sm.pwsw[w][buf][1];
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         const int d0 = 16 * kk + 8 * hl;
-        float hv[8], pv[8], sv[8];
-        unpack8f(hpk[kk], hv);
+        float hv[8], pv[8];
+        unpack8f(*(const uint4*)&sm.hq[w][li][d0], hv);
         unpack8f(*(const uint4*)(pwr + d0), pv);
-        unpack8f(*(const uint4*)(swr + d0), sv);
-        uint32_t t1[4], ch[4];
+        uint32_t t1[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) t1[j] = pack_bf16x2(hv[2 * j] * pv[2 * j], hv[2 * j + 1] * pv[2 * j + 1]);
-        float tv[8];
-        unpack8f(make_uint4(t1[0], t1[1], t1[2], t1[3]), tv);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ch[j] = pack_bf16x2(tv[2 * j] * sv[2 * j], tv[2 * j + 1] * sv[2 * j + 1]);
-        const uint4 chq = make_uint4(ch[0], ch[1], ch[2], ch[3]);
-        float cv[8];
-        unpack8f(chq, cv);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) den_part += cv[j];
-        const bf16x8 a = as_bf16x8(chq);
-#pragma unroll
-        for (int t = 0; t < ET; ++t) {
-          const bf16x8 bq = as_bf16x8(*(const uint4*)&sm.u.c[buf][32 * t + li][d0]);
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq, acc[t], 0, 0, 0);
-        }
+        for (int j = 0; j < 4; ++j)
+          t1[j] = pack_bf16x2(hv[2 * j] * pv[2 * j], hv[2 * j + 1] * pv[2 * j + 1]);
+        tpk[kk] = make_uint4(t1[0], t1[1], t1[2], t1[3]);
       }
+      cached_page = page;
     }
-    if (next) TAO_STORE_C(buf ^ 1);
-    if (act_next) store_w(buf ^ 1, pwv, swv);
+    const bf16_t* swr = sm.pwsw[w][buf][1];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const int d0 = 16 * kk + 8 * hl;
+      float tv[8], sv[8];
+      unpack8f(tpk[kk], tv);
+      unpack8f(*(const uint4*)(swr + d0), sv);
+      uint32_t ch[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ch[j] = pack_bf16x2(tv[2 * j] * sv[2 * j], tv[2 * j + 1] * sv[2 * j + 1]);
+      const bf16x8 a = as_bf16x8(make_uint4(ch[0], ch[1], ch[2], ch[3]));
+#pragma unroll
+      for (int t = 0; t < ET; ++t) {
+        const bf16x8 bq = as_bf16x8(*(const uint4*)&sm.u.c[buf][32 * t + li][d0]);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq, acc[t], 0, 0, 0);
+      }
+      // den: the same A against a column of ones.
+      acc_den = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, ones, acc_den, 0, 0, 0);
+    }
+  };
+  if (U > 0) {
+    TAO_LOAD_C(0, a);
+    if (active(0)) load_w(0, pwa, swa);
+    TAO_STORE_C(0, a);
+    if (active(0)) store_w(0, pwa, swa);
+  }
+  if (U > 1) {
+    TAO_LOAD_C(1, b);
+    if (active(1)) load_w(1, pwb, swb);
+  }
+  __syncthreads();
+  // Even u: fine u + 2 -> set a, fine u + 1 (set b) -> LDS; odd u: the reverse.
+  for (int u = 0; u < U; u += 2) {
+    if (u + 2 < U) {
+      TAO_LOAD_C(u + 2, a);
+      if (active(u + 2)) load_w(u + 2, pwa, swa);
+    }
+    consume(u);
+    if (u + 1 < U) {
+      TAO_STORE_C(1, b);
+      if (active(u + 1)) store_w(1, pwb, swb);
+    }
+    __syncthreads();
+    if (u + 1 >= U) break;
+    if (u + 3 < U) {
+      TAO_LOAD_C(u + 3, b);
+      if (active(u + 3)) load_w(u + 3, pwb, swb);
+    }
+    consume(u + 1);
+    if (u + 2 < U) {
+      TAO_STORE_C(0, a);
+      if (active(u + 2)) store_w(0, pwa, swa);
+    }
     __syncthreads();
   }
 
@@ -367,12 +406,7 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
 #undef TAO_STORE_C
 #undef TAO_C_SLOT
 #undef TAO_C_CHUNK
-  // ---- epilogue: den per query, then fine = r(r(num) / r(den)) and fusion.
-  if (reads) {
-    const float den_row = den_part + __shfl_xor(den_part, 32, 64);
-    if (hl == 0) sm.den[w][li] = den_row;
-  }
-  __syncthreads();
+  // ---- epilogue: fine = r(r(num) / r(den)) and the fusion.
   if (!reads) return;
   // One e-tile of the accumulator (called with constant t, so acc stays in
   // registers).
@@ -389,7 +423,7 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
       const int q = 8 * (i / 4) + 4 * hl + (i % 4);
       if (q < nq) {
         const int tq = q_first + q;
-        const float fine = rbf(rbf(av[i]) / rbf(sm.den[w][q]));
+        const float fine = rbf(rbf(av[i]) * __builtin_amdgcn_rcpf(rbf(acc_den[i])));
         const float local = bf2f(p.local[(((size_t)b * p.T + tq) * p.H + h) * D + e]);
         const float x = bf2f(p.rq.p[b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + e]);
         p.out[b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + e] =

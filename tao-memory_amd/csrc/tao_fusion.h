@@ -3,7 +3,9 @@
 // Restates fusion_pointwise.py:10-92 plus the torch softmax between them
 // (operator.py:86-94): every intermediate is rounded to bf16 exactly where
 // the reference rounds, with no FMA contraction (the reference launches both
-// kernels with enable_fp_fusion=False).
+// kernels with enable_fp_fusion=False). The branch softmax uses the hardware
+// exp and one reciprocal: it only shapes the output (within the bf16
+// tolerance), never a routing decision.
 #pragma once
 
 #include "tao_common.h"
@@ -33,11 +35,12 @@ TAO_DEV bf16_t fuse_element(float q, float local, float coarse, float fine,
   if (!coarse_on) s[1] = ninf;
   if (!fine_on) s[2] = ninf;
   float top = fmaxf(s[0], fmaxf(s[1], s[2]));
-  float e0 = exp_cr(s[0] - top);
-  float e1 = coarse_on ? exp_cr(s[1] - top) : 0.0f;
-  float e2 = fine_on ? exp_cr(s[2] - top) : 0.0f;
+  float e0 = __expf(s[0] - top);
+  float e1 = coarse_on ? __expf(s[1] - top) : 0.0f;
+  float e2 = fine_on ? __expf(s[2] - top) : 0.0f;
   float total = (e0 + e2) + e1;   // butterfly order over [e0, e1, e2, 0]
-  float r0 = rbf(e0 / total), r1 = rbf(e1 / total), r2 = rbf(e2 / total);
+  const float inv = __builtin_amdgcn_rcpf(total);
+  float r0 = rbf(e0 * inv), r1 = rbf(e1 * inv), r2 = rbf(e2 * inv);
   float lt = rbf(r0 * rbf(2.0f * local));
   float ct = rbf(r1 * rbf(gain * coarse));
   float ft = rbf(r2 * rbf(gain * fine));

@@ -70,6 +70,7 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
   const long long qtok = first + wave * 32 + (nq > 0 ? min(li, nq - 1) : 0);
   const long long qpos = p.qpos0 + qtok;
   const long long wave_last = p.qpos0 + first + wave * 32 + nq - 1;
+  const long long wave_first = p.qpos0 + first + wave * 32;
   const long long kend = p.qpos0 + first + count;   // exclusive
 
   bf16x8 qreg[KK];
@@ -147,27 +148,46 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
         s[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[kk], s[sub], 0, 0, 0);
       }
     }
-    // S^T layout: lane holds query li, keys 8*(i/4) + 4*hl + i%4 of each sub-tile.
+    // S^T layout: lane holds query li, keys 8*(i/4) + 4*hl + i%4 of each
+    // sub-tile. Only blocks that reach past the wave's first query or the
+    // end of the window need the mask (32-bit offsets from the block start).
+    const bool masked = kb + kKeys - 1 > wave_first || kb + kKeys > kend;
     float bmax = -__builtin_inff();
+    if (masked) {
+      const int q_off = (int)(qpos - kb);          // keys at offset > q_off are in the future
+      const int end_off = (int)(kend - kb);        // keys at offset >= end_off do not exist
+      const int lim = q_off + 1 < end_off ? q_off + 1 : end_off;
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const long long kpos = kb + sub * 32 + 8 * (i / 4) + 4 * hl + (i % 4);
-        const bool ok = kpos <= qpos && kpos < kend;
-        const float v = ok ? s[sub][i] * scale_log2 : -__builtin_inff();
-        s[sub][i] = v;
-        bmax = fmaxf(bmax, v);
-      }
+        for (int i = 0; i < 16; ++i) {
+          const int off = sub * 32 + 8 * (i / 4) + 4 * hl + (i % 4);
+          const float v = off < lim ? s[sub][i] * scale_log2 : -__builtin_inff();
+          s[sub][i] = v;
+          bmax = fmaxf(bmax, v);
+        }
+    } else {
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float v = s[sub][i] * scale_log2;
+          s[sub][i] = v;
+          bmax = fmaxf(bmax, v);
+        }
+    }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
     const float m_new = fmaxf(m_run, bmax);
-    const float alpha = m_run == -__builtin_inff() ? 0.0f : exp2f(m_run - m_new);
+    // A query with no visible key yet keeps m = -inf: shift by 0 instead, so
+    // every exp below sees -inf and returns 0.
+    const float m_use = m_new == -__builtin_inff() ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     float rsum = 0.0f;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float e = s[sub][i] == -__builtin_inff() ? 0.0f : exp2f(s[sub][i] - m_new);
+        const float e = __builtin_amdgcn_exp2f(s[sub][i] - m_use);
         s[sub][i] = e;
         rsum += e;
       }
@@ -186,8 +206,7 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
         uint32_t packed[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          packed[j] = (uint32_t)f2bf(s[sub][8 * half + 2 * j]) |
-                      ((uint32_t)f2bf(s[sub][8 * half + 2 * j + 1]) << 16);
+          packed[j] = pack_bf16x2(s[sub][8 * half + 2 * j], s[sub][8 * half + 2 * j + 1]);
         const bf16x8 pb = as_bf16x8(make_uint4(packed[0], packed[1], packed[2], packed[3]));
         const int kbase = sub * 32 + 16 * half + 4 * hl;
 #pragma unroll

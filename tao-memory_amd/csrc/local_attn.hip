@@ -29,10 +29,14 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr int kKeys = 64;
 constexpr int kAttnThreads = 512;   // 8 waves x 32 queries = 256-query tiles
 
+// V^T rows are padded to 68 keys (34 dwords): 16 lanes reading 8 bytes
+// from 16 consecutive channel rows land on distinct banks, and the
+// transposing 4-byte writes put a half-wave on one row's consecutive key
+// pairs.
 template <int D>
 struct AttnSmem {
   bf16_t k[kKeys][D + 8];
-  bf16_t vt[D][kKeys + 8];
+  bf16_t vt[D][kKeys + 4];
 };
 
 TAO_DEV const bf16_t* key_row(const AttnParams& p, const TokView& tv, const bf16_t* ring,
@@ -93,11 +97,12 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
     }
 #pragma unroll
     for (int j = 0; j < VJ; ++j) {
+      // job -> (channel chunk c, key pair): 32 consecutive jobs share c.
       const int job = tid + j * kAttnThreads;
       va[j] = make_uint4(0, 0, 0, 0);
       vb[j] = make_uint4(0, 0, 0, 0);
       if (job < (kKeys / 2) * CH) {
-        const int t0 = 2 * (job / CH), c = job % CH;
+        const int t0 = 2 * (job % (kKeys / 2)), c = job / (kKeys / 2);
         if (kb + t0 < kend) va[j] = *(const uint4*)(key_row(p, p.v, p.ring_v, b, h, kb + t0, D) + c * 8);
         if (kb + t0 + 1 < kend) vb[j] = *(const uint4*)(key_row(p, p.v, p.ring_v, b, h, kb + t0 + 1, D) + c * 8);
       }
@@ -123,7 +128,7 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
     for (int j = 0; j < VJ; ++j) {
       const int job = tid + j * kAttnThreads;
       if (job < (kKeys / 2) * CH) {
-        const int t0 = 2 * (job / CH), c = job % CH;
+        const int t0 = 2 * (job % (kKeys / 2)), c = job / (kKeys / 2);
         const uint32_t wa[4] = {va[j].x, va[j].y, va[j].z, va[j].w};
         const uint32_t wb[4] = {vb[j].x, vb[j].y, vb[j].z, vb[j].w};
 #pragma unroll

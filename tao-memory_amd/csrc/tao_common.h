@@ -57,6 +57,16 @@ TAO_DEV float log_bf(float x) {
   return rbf(y);
 }
 
+// bf16(x / y) (fp32 division correctly rounded, then RNE to bf16) from the
+// approximate reciprocal inv ~ 1/y: x * inv is within a few fp32 ulps of
+// x / y, so unless it lies near a bf16 rounding boundary both round alike;
+// near one the IEEE division decides.
+TAO_DEV float div_bf(float x, float y, float inv) {
+  const float q = x * inv;
+  if (near_bf16_midpoint(q, 16)) return rbf(x / y);
+  return rbf(q);
+}
+
 // Correctly rounded fp32 exp (fp64 evaluation).
 TAO_DEV float exp_cr(float x) { return (float)exp((double)x); }
 

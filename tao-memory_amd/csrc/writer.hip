@@ -52,7 +52,9 @@ TAO_DEV const bf16_t* token_row(const WriterParams& p, int b, int h, long long p
 constexpr int kWriterThreads = 512;   // 8 waves
 
 // Stage raw_k and V of one block transposed into LDS ([channel][token]).
-// Every global load of the block is issued before the first LDS write.
+// Every global load of the block is issued before the first LDS write; job
+// -> (channel chunk c, token pair): 128 consecutive jobs share c, so a
+// half-wave's transposing 4-byte writes fill consecutive words of one row.
 template <int D>
 __device__ void stage_block(const WriterParams& p, int b, int h, long long start,
                             bf16_t (*kt)[kRowPad], bf16_t (*vt)[kRowPad]) {
@@ -62,7 +64,7 @@ __device__ void stage_block(const WriterParams& p, int b, int h, long long start
 #pragma unroll
   for (int j = 0; j < JOBS; ++j) {
     const int job = threadIdx.x + j * kWriterThreads;
-    const int c = job % CH, t0 = 2 * (job / CH);
+    const int c = job / (kBlock / 2), t0 = 2 * (job % (kBlock / 2));
     ka[j] = *(const uint4*)(token_row(p, b, h, start + t0, p.rk, p.ring_raw, D) + c * 8);
     kb[j] = *(const uint4*)(token_row(p, b, h, start + t0 + 1, p.rk, p.ring_raw, D) + c * 8);
     va[j] = *(const uint4*)(token_row(p, b, h, start + t0, p.v, p.ring_v, D) + c * 8);
@@ -71,7 +73,7 @@ __device__ void stage_block(const WriterParams& p, int b, int h, long long start
 #pragma unroll
   for (int j = 0; j < JOBS; ++j) {
     const int job = threadIdx.x + j * kWriterThreads;
-    const int c = job % CH, t0 = 2 * (job / CH);
+    const int c = job / (kBlock / 2), t0 = 2 * (job % (kBlock / 2));
     const uint32_t wa[4] = {ka[j].x, ka[j].y, ka[j].z, ka[j].w};
     const uint32_t wb[4] = {kb[j].x, kb[j].y, kb[j].z, kb[j].w};
     const uint32_t xa[4] = {va[j].x, va[j].y, va[j].z, va[j].w};
@@ -150,15 +152,16 @@ __global__ __launch_bounds__(kWriterThreads) void writer_kernel(WriterParams p) 
   for (int job = tid; job < 4 * D; job += kWriterThreads) {
     const int d = job % D, qq = job / D;
     const float total = sm.total[d];
+    const float inv = __builtin_amdgcn_rcpf(total);
     for (int t = 0; t < QT; t += 8) {
       uint4* cell = (uint4*)&sm.kt[d][qq * QT + t];
       const uint4 u = *cell;
       uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p0 = rbf(__uint_as_float(w[i] << 16) / total);
-        const float p1 = rbf(__uint_as_float(w[i] & 0xFFFF0000u) / total);
-        w[i] = (uint32_t)f2bf(p0) | ((uint32_t)f2bf(p1) << 16);
+        const float p0 = div_bf(__uint_as_float(w[i] << 16), total, inv);
+        const float p1 = div_bf(__uint_as_float(w[i] & 0xFFFF0000u), total, inv);
+        w[i] = pack_bf16x2(p0, p1);
       }
       *cell = make_uint4(w[0], w[1], w[2], w[3]);
     }

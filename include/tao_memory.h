@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 2
+#define TAO_ABI_VERSION 3
 
 enum tao_status {
   TAO_OK = 0,
@@ -62,6 +62,10 @@ typedef struct tao_state_dev {
   int64_t* header;  /* device [4]: position, M, reserved, reserved */
   void* fold_g;     /* fp32 [B, H, D, D]  G^T of the current route and epoch */
   void* fold_den;   /* fp32 [B, H, D]     den weights of the current route */
+  /* Coarse value branch (TaoConfig.coarse_index_only = False); both null in
+   * the index-only preset, both set otherwise. */
+  void* page_c;     /* bf16 [B, H, page_cap, D, D] page value matrices (C^T) */
+  void* coarse_g;   /* fp32 [B, H, D, D]  folded coarse read of the completed pages */
   void* workspace;  /* scratch: decode step records and the prefill plan */
   size_t workspace_bytes;
 } tao_state_dev;
@@ -107,6 +111,21 @@ int tao_workspace_init(const tao_state_dev* st, void* stream);
  * refresh and every seal epilogue (the stream driver and tao_prefill do). */
 int tao_fold_route(const tao_state_dev* st, int32_t selected, void* stream);
 
+/* Page value matrices of completed pages [first_page, first_page + count)
+ * (replaces the page_c einsum of append_fine, tao_stream.py:486-499):
+ *   page_c[g][e][d] = r(sum_s fine_sw[8g + s][d] * C^T_{8g+s}[e][d])
+ * (fine_sw of a completed page is r(exp(r(z - page_z))), the reference's
+ * weight). Needs st->page_c. */
+int tao_page_coarse(const tao_state_dev* st, int32_t first_page, int32_t count, void* stream);
+
+/* Fold the coarse value read over the first `completed` pages (replaces the
+ * per-query coarse einsum of _read_reused, tao_stream.py:299-305): with
+ * cw_p = softmax over p < completed of page_z[p],
+ *   coarse_g[e][d] = sum_p cw_p[d] * page_c[p][e][d]        (fp32)
+ * so one query's coarse read is r(h . coarse_g[e]). Call after every page
+ * completion and after a prefill or import (the stream driver does). */
+int tao_fold_coarse(const tao_state_dev* st, int32_t completed, void* stream);
+
 /* One fused single-token decode step (replaces the memo-backed q1 region,
  * tao_stream.py:399-433, query_fresh_fine.py:52-75, the local SDPA call
  * flash_attention.py:25-29, the local concat tao_stream.py:927-930, and the
@@ -114,7 +133,8 @@ int tao_fold_route(const tao_state_dev* st, int32_t selected, void* stream);
  * Reads the stream position from st->header[0], appends the token to the
  * ring, reads the folded route (fold_g / fold_den, see tao_fold_route) when
  * `selected` > 0 (0 before the first seal: output = local attention),
- * writes out [B,1,H,D] (element strides out_s) and advances header[0]. */
+ * adds the folded coarse read (coarse_g) when fu->coarse_on, writes out
+ * [B,1,H,D] (element strides out_s) and advances header[0]. */
 int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok,
                     const tao_fusion* fu, int32_t selected, void* out,
                     const int64_t* out_s, void* stream);
@@ -159,10 +179,14 @@ int tao_local_attention(const tao_state_dev* st, const tao_tokens* tok,
  *   pw_pool  bf16 [epochs][B][H][pool_pcap][D]  page weights per seal epoch
  *   psw_pool bf16 [epochs][B][H][coarse_group][D] pending segment weights
  *   sel_pool int32 [sel_slots][B][H][sel_cap]   selected ids per route turn
+ *   coarse_pool bf16 [coarse_count][B][H][D][D] folded coarse reads (G^T)
+ *     for completed = coarse_first + i (coarse value branch only; else null)
  * Slot 0 of sel_pool receives the state's route at call start. */
 typedef struct tao_prefill_pools {
   void* pw_pool; void* psw_pool; int32_t* sel_pool;
   int32_t pool_pcap, epochs, sel_slots;
+  void* coarse_pool;
+  int32_t coarse_first, coarse_count;
 } tao_prefill_pools;
 
 /* Layout of the int64 prefill plan (all indices are token offsets in tok
@@ -182,7 +206,7 @@ enum tao_plan_field {
                                sel slot, publish} */
   TAO_PLAN_READ_TILES = 9,  /* n, then n x {first, count <= 32, sel slot,
                                selected, epoch - first_epoch, sw split,
-                               fine_on, 0} */
+                               fine_on, completed pages} */
   TAO_PLAN_RING_FIRST = 10, /* ring append: first token, count, position */
   TAO_PLAN_RING_COUNT = 11,
   TAO_PLAN_RING_POS = 12
@@ -230,9 +254,10 @@ typedef struct tao_stream_cfg {
  * tao_stream.py:196-227). route_coarse / route_size: the state's current
  * route; outputs = 0 plans a state-only advance (no attention or reads; the
  * last refresh turn is routed alone). With plan == NULL only info is filled
- * (a size query). info (int64[8]) receives: plan length, epochs, turns,
+ * (a size query). info (int64[10]) receives: plan length, epochs, turns,
  * route coarse and route size after the call, page capacity of the epoch
- * pools, chunks that read history, chunks. Host code only. */
+ * pools, chunks that read history, chunks, and the coarse pool range
+ * (first completed-page count >= 1 read, number of counts). Host code only. */
 int tao_prefill_plan(const tao_stream_cfg* cfg, int64_t pos0, int64_t tokens,
                      int32_t route_coarse, int32_t route_size, int32_t outputs,
                      int64_t* plan, int64_t plan_cap, int64_t* info);

@@ -35,6 +35,8 @@ int check_state(const tao_state_dev* st) {
       !st->fine_sw || !st->page_z || !st->page_w || !st->sel || !st->chosen ||
       !st->header || !st->fold_g || !st->fold_den || !st->workspace)
     return fail(TAO_E_ARGUMENT, "state has a null device buffer");
+  if ((st->page_c == nullptr) != (st->coarse_g == nullptr))
+    return fail(TAO_E_ARGUMENT, "page_c and coarse_g must be both set or both null");
   if (st->sel_cap > 512) return fail(TAO_E_CAPACITY, "sel_cap above 512");
   if (st->coarse_group != 8) return fail(TAO_E_SHAPE, "HIP kernels implement coarse_group=8");
   const tao::WorkspaceLayout lay =
@@ -98,6 +100,8 @@ tao::DecodeParams decode_params(const tao_state_dev* st, const tao_tokens* tok,
   p.parts = parts_of(st);
   p.fold_g = (const float*)st->fold_g;
   p.fold_den = (const float*)st->fold_den;
+  p.coarse_g = (const float*)st->coarse_g;
+  p.coarse_on = fu->coarse_on ? 1 : 0;
   p.B = st->batch;
   p.H = st->heads;
   p.keep = st->local_keep;
@@ -160,6 +164,8 @@ int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fus
   if (tok->tokens != 1) return fail(TAO_E_SHAPE, "decode step takes exactly one token");
   if (!out || !out_s) return fail(TAO_E_ARGUMENT, "null output");
   if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected count exceeds sel_cap");
+  if (fu->coarse_on && !st->coarse_g)
+    return fail(TAO_E_ARGUMENT, "coarse_on needs a state with the coarse value branch");
   tao::DecodeParams p = decode_params(st, tok, fu, out, out_s);
   p.pos_hint = position;
   return check_hip(tao::launch_decode_step(p, st->head_dim, selected, (hipStream_t)stream),
@@ -210,6 +216,48 @@ int tao_fold_route(const tao_state_dev* st, int32_t selected, void* stream) {
   p.sel_cap = st->sel_cap;
   p.M = selected;
   return check_hip(tao::launch_fold(p, st->head_dim, (hipStream_t)stream), "tao_fold_route");
+}
+
+int tao_page_coarse(const tao_state_dev* st, int32_t first_page, int32_t count, void* stream) {
+  int rc = check_state(st);
+  if (rc) return rc;
+  if (!st->page_c) return fail(TAO_E_ARGUMENT, "state has no coarse value branch");
+  if (count < 0 || first_page < 0 || first_page + count > st->page_cap ||
+      (int64_t)(first_page + count) * st->coarse_group > st->fine_cap)
+    return fail(TAO_E_CAPACITY, "pages exceed the state capacity");
+  tao::PageCoarseParams p;
+  p.bank = (const bf16_t*)st->bank_c;
+  p.sw = (const bf16_t*)st->fine_sw;
+  p.page_c = (bf16_t*)st->page_c;
+  p.B = st->batch;
+  p.H = st->heads;
+  p.fine_cap = st->fine_cap;
+  p.page_cap = st->page_cap;
+  p.group = st->coarse_group;
+  p.first_page = first_page;
+  p.count = count;
+  return check_hip(tao::launch_page_coarse(p, st->head_dim, (hipStream_t)stream),
+                   "tao_page_coarse");
+}
+
+int tao_fold_coarse(const tao_state_dev* st, int32_t completed, void* stream) {
+  int rc = check_state(st);
+  if (rc) return rc;
+  if (!st->page_c) return fail(TAO_E_ARGUMENT, "state has no coarse value branch");
+  if (completed < 1 || completed > st->page_cap)
+    return fail(TAO_E_CAPACITY, "completed pages out of range");
+  tao::CoarseFoldParams p;
+  p.page_z = (const bf16_t*)st->page_z;
+  p.page_c = (const bf16_t*)st->page_c;
+  p.out = st->coarse_g;
+  p.out_f32 = 1;
+  p.B = st->batch;
+  p.H = st->heads;
+  p.page_cap = st->page_cap;
+  p.n_first = completed;
+  p.n_count = 1;
+  return check_hip(tao::launch_coarse_fold(p, st->head_dim, (hipStream_t)stream),
+                   "tao_fold_coarse");
 }
 
 int tao_route(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
@@ -410,6 +458,10 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   // ---- read tiles
   if (n_read > 0 && need_pools && st->fine_cap > 16384)
     return fail(TAO_E_CAPACITY, "prefill reads index at most 16384 fines per state");
+  const bool coarse_values = st->page_c != nullptr;
+  const int64_t c_first = pools ? pools->coarse_first : 0;
+  const int64_t c_count = pools ? pools->coarse_count : 0;
+  bool coarse_reads = false;
   for (int64_t i = 0; i < n_read; ++i) {
     const int64_t* t = plan + off_read + 8 * i;
     if (t[0] < 0 || t[1] < 1 || t[1] > 32 || t[0] + t[1] > T || (t[6] != 0 && t[6] != 1))
@@ -417,10 +469,21 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
     if (t[6]) {
       const int64_t epoch = first_epoch + t[4];
       if (!pools || t[2] < 0 || t[2] >= pools->sel_slots || t[3] < 1 || t[3] > 128 ||
-          t[3] > st->sel_cap || t[4] < 0 || t[4] >= n_epochs || t[5] != (epoch / G) * G)
+          t[3] > st->sel_cap || t[4] < 0 || t[4] >= n_epochs || t[5] != (epoch / G) * G ||
+          t[7] != epoch / G)
         return fail(TAO_E_ARGUMENT, "invalid history read tile in the plan");
+      if (coarse_values && t[7] >= 1) {
+        if (!pools->coarse_pool || t[7] < c_first || t[7] >= c_first + c_count)
+          return fail(TAO_E_ARGUMENT, "coarse read outside the coarse pool");
+        coarse_reads = true;
+      }
+    } else if (t[7] != 0) {
+      return fail(TAO_E_ARGUMENT, "invalid read tile in the plan");
     }
   }
+  if (coarse_reads && (c_first < 1 || c_first + c_count - 1 > st->page_cap ||
+                       c_first + c_count - 1 > first_page + n_pages))
+    return fail(TAO_E_CAPACITY, "coarse pool range exceeds the completed pages");
   // ---- ring append
   const int64_t ring_first = plan[TAO_PLAN_RING_FIRST], ring_count = plan[TAO_PLAN_RING_COUNT];
   if (ring_first < 0 || ring_count < 0 || ring_first + ring_count > T || ring_count > L ||
@@ -487,6 +550,35 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   pp.count = (int)n_pages;
   e = tao::launch_pages(pp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill pages");
+  if (coarse_values) {
+    tao::PageCoarseParams cp;
+    cp.bank = (const bf16_t*)st->bank_c;
+    cp.sw = (const bf16_t*)st->fine_sw;
+    cp.page_c = (bf16_t*)st->page_c;
+    cp.B = st->batch;
+    cp.H = st->heads;
+    cp.fine_cap = st->fine_cap;
+    cp.page_cap = st->page_cap;
+    cp.group = G;
+    cp.first_page = (int)first_page;
+    cp.count = (int)n_pages;
+    e = tao::launch_page_coarse(cp, D, s);
+    if (e != hipSuccess) return check_hip(e, "tao_prefill page values");
+  }
+  if (coarse_reads) {
+    tao::CoarseFoldParams cf;
+    cf.page_z = (const bf16_t*)st->page_z;
+    cf.page_c = (const bf16_t*)st->page_c;
+    cf.out = pools->coarse_pool;
+    cf.out_f32 = 0;
+    cf.B = st->batch;
+    cf.H = st->heads;
+    cf.page_cap = st->page_cap;
+    cf.n_first = (int)c_first;
+    cf.n_count = (int)c_count;
+    e = tao::launch_coarse_fold(cf, D, s);
+    if (e != hipSuccess) return check_hip(e, "tao_prefill coarse fold");
+  }
   if (need_pools) {
     tao::EpochParams ep;
     ep.fine_z = (const bf16_t*)st->fine_z;
@@ -559,6 +651,8 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   rt.group = G;
   rt.fine_cap = st->fine_cap;
   rt.sel_cap = st->sel_cap;
+  rt.coarse_pool = coarse_reads ? (const bf16_t*)pools->coarse_pool : nullptr;
+  rt.coarse_first = coarse_reads ? (int)c_first : 0;
   e = tao::launch_read_tiles(rt, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill read");
   tao::AppendParams app;
@@ -609,6 +703,8 @@ int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu, int32_t sele
   if (!rc) rc = check_fusion(fu);
   if (rc) return rc;
   if (!staging || !out_stage || !graph_out) return fail(TAO_E_ARGUMENT, "null graph buffers");
+  if (st->page_c || fu->coarse_on)
+    return fail(TAO_E_ARGUMENT, "the decode hipGraph implements the index-only coarse preset");
   if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected out of range");
   const int B = st->batch, H = st->heads, D = st->head_dim;
   const size_t row = (size_t)B * H * D;

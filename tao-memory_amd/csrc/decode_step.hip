@@ -14,11 +14,14 @@
 //   scalar input is the cursor (a kernel argument in eager launches,
 //   header[0] in graphs).
 //   fine-read workgroup f reads 32 rows of the folded route:
-//   num[e] = h . G^T[e], and den = r(h . g) (h = r(softmax_D(raw_q))).
+//   num[e] = h . G^T[e], and den = r(h . g) (h = r(softmax_D(raw_q)));
+//   with the coarse value branch on, fine_units(D) more workgroups read 32
+//   rows each of the folded coarse matrix the same way (coarse.hip).
 // decode_combine_kernel: one workgroup per (batch, head, 32 channels):
 //   merges the local records in a fixed order, fine = r(r(num) / den),
-//   applies the fusion epilogue and advances header[0] (the stream
-//   position), so the pair can be replayed from a hipGraph.
+//   coarse = r(h . Gc^T[e]), applies the fusion epilogue and advances
+//   header[0] (the stream position), so the pair can be replayed from a
+//   hipGraph.
 //
 // fold_kernel (per route refresh and per seal, not per token): the q1 read
 // is linear in ch_m = h * w_m with w_m = pw[page(m)] * sw[m] independent of
@@ -74,17 +77,19 @@ TAO_DEV float group_sum(float v) {
 }
 
 // Fine-read workgroup f: num[e] = h . G^T[e] for rows e in
-// [f * kFineRows, (f + 1) * kFineRows), thread (row tid / 8, part tid % 8);
-// workgroup 0 also writes den = r(h . g). h = r(softmax_D(raw_q)) with the
-// exp correctly rounded in fp32.
+// [f * kFineRows, (f + 1) * kFineRows) of the folded matrix gmat, thread
+// (row tid / 8, part tid % 8); with gden (the fine read) workgroup 0 also
+// writes den = r(h . g). h = r(softmax_D(raw_q)) with the exp correctly
+// rounded in fp32.
 template <int D>
 __device__ void fine_read(const DecodeParams& p, int b, int h, int f, float* frec,
-                          float* hq) {
+                          float* hq, const float* gmat, const float* gden_base) {
   constexpr int DP = D / 8, PER = D / 64;
   const int tid = threadIdx.x, row = tid / 8, part = tid % 8;
   const int bh = b * p.H + h;
   const int e = f * kFineRows + row;
-  const float* grow = p.fold_g + ((size_t)bh * D + e) * D + part * DP;
+  const bool with_den = gden_base != nullptr && f == 0;
+  const float* grow = gmat + ((size_t)bh * D + e) * D + part * DP;
   float gv[DP];
 #pragma unroll
   for (int k = 0; k < DP; k += 4) {
@@ -97,7 +102,7 @@ __device__ void fine_read(const DecodeParams& p, int b, int h, int f, float* fre
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       xr[k] = bf2f(rq[tid + 64 * k]);
-      gden[k] = f == 0 ? p.fold_den[(size_t)bh * D + tid + 64 * k] : 0.0f;
+      gden[k] = with_den ? gden_base[(size_t)bh * D + tid + 64 * k] : 0.0f;
     }
     float top = -__builtin_inff();
 #pragma unroll
@@ -117,7 +122,7 @@ __device__ void fine_read(const DecodeParams& p, int b, int h, int f, float* fre
       hq[tid + 64 * k] = hv;
       dsum = k == 0 ? hv * gden[k] : fmaf(hv, gden[k], dsum);
     }
-    if (f == 0) {
+    if (with_den) {
       dsum = wave_sum_fold(dsum);
       if (tid == 0) frec[0] = rbf(dsum);
     }
@@ -133,19 +138,26 @@ __device__ void fine_read(const DecodeParams& p, int b, int h, int f, float* fre
 }
 
 // Kernel A: per (batch, head) NLOC local-attention workgroups (the window
-// split by keys) and NFINE fine-read workgroups; no cross-workgroup
-// communication.
+// split by keys), NFINE fine-read workgroups and, with coarse_on, NFINE
+// coarse-read workgroups; no cross-workgroup communication.
 template <int D>
 __global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, int M) {
   using G = Geo<D>;
   __shared__ StepSmem<D> sm;
-  constexpr int PER_HEAD = G::NLOC + G::NFINE;
-  const int bh = blockIdx.x / PER_HEAD;
-  const int j = blockIdx.x % PER_HEAD;
+  const int per_head = G::NLOC + G::NFINE * (p.coarse_on ? 2 : 1);
+  const int bh = blockIdx.x / per_head;
+  const int j = blockIdx.x % per_head;
   const int b = bh / p.H, h = bh % p.H;
   float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
+  if (j >= G::NLOC + G::NFINE) {
+    fine_read<D>(p, b, h, j - G::NLOC - G::NFINE, recs + (G::NLOC + 1) * (D + kStepRec),
+                 sm.red[0], p.coarse_g, nullptr);
+    return;
+  }
   if (j >= G::NLOC) {
-    if (M > 0) fine_read<D>(p, b, h, j - G::NLOC, recs + G::NLOC * (D + kStepRec), sm.red[0]);
+    if (M > 0)
+      fine_read<D>(p, b, h, j - G::NLOC, recs + G::NLOC * (D + kStepRec), sm.red[0], p.fold_g,
+                   p.fold_den);
     return;
   }
   float* rec = recs + j * (D + kStepRec);
@@ -273,13 +285,14 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
     l_g[i] = j < NLOC ? recs[j * STRIDE + 1] : 0.0f;
     o_g[i] = j < NLOC ? recs[j * STRIDE + kStepRec + d] : 0.0f;
   }
-  float q = 0.0f, num = 0.0f, den = 1.0f, a[3], bb[3];
+  float q = 0.0f, num = 0.0f, den = 1.0f, craw = 0.0f, a[3], bb[3];
   if (g == 0) {
     q = bf2f(p.rq.p[b * p.rq.sb + h * p.rq.sh + d]);
     if (M > 0) {
       den = recs[NLOC * STRIDE];
       num = recs[NLOC * STRIDE + kStepRec + d];
     }
+    if (p.coarse_on) craw = recs[(NLOC + 1) * STRIDE + kStepRec + d];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       a[i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + d * p.fa_s[1] + i * p.fa_s[2]);
@@ -311,9 +324,10 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
     for (int gg = 0; gg < G; ++gg) nl += part_loc[gg][dc];
     const float local = rbf(nl / den_local);
     bf16_t result;
-    if (M > 0) {
-      const float fine_v = rbf(rbf(num) / den);
-      result = fuse_element(q, local, 0.0f, fine_v, a, bb, p.gain, 0, 1);
+    if (M > 0 || p.coarse_on) {
+      const float fine_v = M > 0 ? rbf(rbf(num) / den) : 0.0f;
+      result = fuse_element(q, local, rbf(craw), fine_v, a, bb, p.gain, p.coarse_on ? 1 : 0,
+                            M > 0 ? 1 : 0);
     } else {
       result = f2bf(local);
     }
@@ -417,7 +431,9 @@ __global__ __launch_bounds__(kThreads) void ring_append_kernel(AppendParams p) {
 hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStream_t s) {
   if (M < 0 || M > p.sel_cap) return hipErrorInvalidValue;
   if (p.keep + p.fine > kMaxWindow) return hipErrorInvalidValue;
-  const dim3 units((unsigned)(p.B * p.H * (local_units(head_dim) + fine_units(head_dim))));
+  if (p.coarse_on && !p.coarse_g) return hipErrorInvalidValue;
+  const int per_head = local_units(head_dim) + fine_units(head_dim) * (p.coarse_on ? 2 : 1);
+  const dim3 units((unsigned)(p.B * p.H * per_head));
   const dim3 cols((unsigned)(p.B * p.H * (head_dim / kCombineCols)));
   if (head_dim == 128) {
     hipLaunchKernelGGL(decode_units_kernel<128>, units, dim3(kThreads), 0, s, p, M);

@@ -102,7 +102,8 @@ extern "C" int tao_prefill_plan(const tao_stream_cfg* cfg, int64_t pos0, int64_t
         for (int64_t qs = sub; qs < sub + count; qs += kReadTile) {
           const int64_t n = sub + count - qs;
           reads.insert(reads.end(), {qs - pos0, n < kReadTile ? n : kReadTile, slot, slot_m,
-                                     ch.epoch - first_epoch, (ch.epoch / group) * group, 1, 0});
+                                     ch.epoch - first_epoch, (ch.epoch / group) * group, 1,
+                                     ch.epoch / group});
         }
     }
   }
@@ -113,6 +114,15 @@ extern "C" int tao_prefill_plan(const tao_stream_cfg* cfg, int64_t pos0, int64_t
     turns.back() = 1;
   }
   const int64_t n_epochs = f1 >= 1 ? f1 - first_epoch + 1 : 0;
+  // Completed-page counts read by history chunks (coarse value branch).
+  int64_t c_lo = 0, c_hi = 0;
+  if (outputs)
+    for (const Chunk& ch : chunks) {
+      const int64_t completed = ch.epoch / group;
+      if (completed < 1) continue;
+      if (c_lo == 0 || completed < c_lo) c_lo = completed;
+      if (completed > c_hi) c_hi = completed;
+    }
   const int64_t limit = serve_limit(c);
   const int64_t keep = tokens < limit ? tokens : limit;
   const int64_t n_writes = f1 - f0;
@@ -126,6 +136,8 @@ extern "C" int tao_prefill_plan(const tao_stream_cfg* cfg, int64_t pos0, int64_t
   info[5] = f1 / group + 1;             // page capacity of the epoch pools
   info[6] = history_chunks;             // chunks that read history (fusion calls)
   info[7] = (int64_t)chunks.size();
+  info[8] = c_lo;                       // coarse pool: first completed-page count
+  info[9] = c_lo ? c_hi - c_lo + 1 : 0; // coarse pool: number of counts
   if (!plan) return TAO_OK;             // size query
   if (plan_cap < len) {
     tao::set_error("plan buffer too small");

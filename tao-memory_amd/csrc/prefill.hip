@@ -113,7 +113,10 @@ __global__ __launch_bounds__(kThreads) void epochs_kernel(EpochParams p) {
 // in registers (MFMA A layout; r(h * pw) is kept per page) and runs
 // 4 x 8 v_mfma_f32_32x32x16_bf16 into its 32 x D accumulator, plus one
 // against a column of ones for den[q] = sum over the tile's fines of
-// sum_d ch; fine = r(r(num) / r(den)), then the fusion epilogue.
+// sum_d ch; fine = r(r(num) / r(den)), then the fusion epilogue. With the
+// coarse value branch (COARSE), each e-tile of a tile whose chunk has
+// completed pages also runs 8 MFMAs of the wave's h against the folded
+// coarse matrix of its page count (coarse.hip) before the fusion.
 constexpr int kGroupWaves = 8;
 constexpr int kGroupThreads = 64 * kGroupWaves;
 constexpr int kBitWords = kMaxFineIds / 32;
@@ -145,7 +148,7 @@ TAO_DEV void unpack8f(const uint4& u, float out[8]) {
   }
 }
 
-template <int D>
+template <int D, bool COARSE>
 __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesParams p) {
   constexpr int KK = D / 16, ET = D / 32, CPR = D / 8;   // k-steps, e-tiles, uint4 per row
   constexpr int CPT = D * CPR / kGroupThreads;           // C^T uint4 per thread
@@ -160,11 +163,12 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
   const int nt = min(kGroupWaves, p.n_tiles - t0);
 
   // This wave's tile.
-  int q_first = 0, nq = 0, slot = 0, M = 0, erel = 0, sw_split = 0, fine_on = 0;
+  int q_first = 0, nq = 0, slot = 0, M = 0, erel = 0, sw_split = 0, fine_on = 0, cpages = 0;
   if (w < nt) {
     const int64_t* desc = p.tiles + 8 * (t0 + w);
     q_first = (int)desc[0]; nq = (int)desc[1]; slot = (int)desc[2]; M = (int)desc[3];
     erel = (int)desc[4]; sw_split = (int)desc[5]; fine_on = (int)desc[6];
+    cpages = (int)desc[7];
   }
   const bool reads = w < nt && fine_on;
   if (w < nt && !fine_on) {
@@ -406,8 +410,11 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
 #undef TAO_STORE_C
 #undef TAO_C_SLOT
 #undef TAO_C_CHUNK
-  // ---- epilogue: fine = r(r(num) / r(den)) and the fusion.
+  // ---- epilogue: fine = r(r(num) / r(den)), the coarse read, the fusion.
   if (!reads) return;
+  const bool coarse_on = COARSE && cpages >= 1;
+  const bf16_t* gc =
+      coarse_on ? p.coarse_pool + ((size_t)(cpages - p.coarse_first) * BH + bh) * D * D : nullptr;
   // One e-tile of the accumulator (called with constant t, so acc stays in
   // registers).
   auto emit = [&](const floatx16& av, int t) __attribute__((always_inline)) {
@@ -418,6 +425,24 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
       ae[i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + e * p.fa_s[1] + i * p.fa_s[2]);
       be[i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + e * p.fb_s[1] + i * p.fb_s[2]);
     }
+    // coarse[q][e] = h_q . G^T[e]: A = the wave's h rows, B = G^T rows of
+    // this e-tile (k = d contiguous).
+    floatx16 cacc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) cacc[i] = 0.0f;
+    if constexpr (COARSE) {
+      if (coarse_on) {
+        uint4 gb[KK];
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+          gb[kk] = *(const uint4*)(gc + (size_t)e * D + 16 * kk + 8 * hl);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+          cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              as_bf16x8(*(const uint4*)&sm.hq[w][li][16 * kk + 8 * hl]), as_bf16x8(gb[kk]),
+              cacc, 0, 0, 0);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int q = 8 * (i / 4) + 4 * hl + (i % 4);
@@ -427,7 +452,7 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
         const float local = bf2f(p.local[(((size_t)b * p.T + tq) * p.H + h) * D + e]);
         const float x = bf2f(p.rq.p[b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + e]);
         p.out[b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + e] =
-            fuse_element(x, local, 0.0f, fine, ae, be, p.gain, 0, 1);
+            fuse_element(x, local, rbf(cacc[i]), fine, ae, be, p.gain, coarse_on ? 1 : 0, 1);
       }
     }
   };
@@ -475,10 +500,15 @@ hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t
   if (p.fine_cap > kMaxFineIds) return hipErrorInvalidValue;
   const int groups = (p.n_tiles + kGroupWaves - 1) / kGroupWaves;
   const dim3 grid((unsigned)(groups * p.B * p.H));
-  if (head_dim == 128)
-    hipLaunchKernelGGL(read_groups_kernel<128>, grid, dim3(kGroupThreads), 0, s, p);
+  const bool coarse = p.coarse_pool != nullptr;
+  if (head_dim == 128 && coarse)
+    hipLaunchKernelGGL((read_groups_kernel<128, true>), grid, dim3(kGroupThreads), 0, s, p);
+  else if (head_dim == 128)
+    hipLaunchKernelGGL((read_groups_kernel<128, false>), grid, dim3(kGroupThreads), 0, s, p);
+  else if (head_dim == 64 && coarse)
+    hipLaunchKernelGGL((read_groups_kernel<64, true>), grid, dim3(kGroupThreads), 0, s, p);
   else if (head_dim == 64)
-    hipLaunchKernelGGL(read_groups_kernel<64>, grid, dim3(kGroupThreads), 0, s, p);
+    hipLaunchKernelGGL((read_groups_kernel<64, false>), grid, dim3(kGroupThreads), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

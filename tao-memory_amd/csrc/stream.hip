@@ -6,7 +6,9 @@
 // tao_stream.py:196-249, 919-969, history_region_graph.py:66-113) in C++, so
 // one ctypes call per token issues every launch: a route refresh on turn
 // positions, the fused decode step (eagerly or by replaying a hipGraph), and
-// the seal (writer + epilogue) when the local window reaches serve_limit.
+// the seal (writer + epilogue) when the local window reaches serve_limit; a
+// seal that completes a page also builds its value matrix and refolds the
+// coarse read when the state carries the coarse value branch.
 // Every count is a closed form of the cursor (the same formulas as the
 // Python host's schedule module).
 #include <cstring>
@@ -18,6 +20,9 @@ extern "C" int tao_route(const tao_state_dev* st, const void* raw_q_row, const i
                          int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
                          void* stream);
 extern "C" int tao_fold_route(const tao_state_dev* st, int32_t selected, void* stream);
+extern "C" int tao_page_coarse(const tao_state_dev* st, int32_t first_page, int32_t count,
+                               void* stream);
+extern "C" int tao_fold_coarse(const tao_state_dev* st, int32_t completed, void* stream);
 extern "C" int tao_write_fine(const tao_state_dev* st, const tao_tokens* tok, int64_t new_base,
                               const int64_t* start_pos, int32_t first_slot, int32_t count,
                               void* stream);
@@ -131,11 +136,12 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
     refreshed = 1;
   }
   const int32_t selected = fines > 0 ? s->route_size : 0;
+  const bool coarse_values = s->st.page_c != nullptr;
   tao_fusion f = *fu;
-  f.coarse_on = 0;
+  f.coarse_on = coarse_values && fines >= c.coarse_group;   // a completed page exists
   f.fine_on = fines > 0;
   int used_graph = 0, captured = 0;
-  if (c.use_graph && fines > 0 && s->staging && s->out_stage) {
+  if (c.use_graph && !coarse_values && fines > 0 && s->staging && s->out_stage) {
     if (!s->graph || s->graph_selected != selected || !same_fusion(s->graph_fusion, f)) {
       drop_graph(s);
       rc = tao_graph_create(&s->st, &f, selected, s->staging, s->out_stage, stream, &s->graph);
@@ -161,6 +167,12 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
                                     (int32_t)(fines / c.coarse_group + 1), 1, stream);
     // New page weights and segment weights: refold the current route.
     if (!rc) rc = tao_fold_route(&s->st, s->route_size, stream);
+    // A completed page: its value matrix, then the coarse read over all pages.
+    if (!rc && coarse_values && fines % c.coarse_group == c.coarse_group - 1) {
+      const int32_t page = (int32_t)(fines / c.coarse_group);
+      rc = tao_page_coarse(&s->st, page, 1, stream);
+      if (!rc) rc = tao_fold_coarse(&s->st, page + 1, stream);
+    }
     if (rc) return rc;
     sealed = 1;
   }

@@ -38,11 +38,11 @@ __host__ __device__ constexpr int local_units(int head_dim) {
 __host__ __device__ constexpr int fine_units(int head_dim) { return head_dim / kFineRows; }
 
 // Per (batch, head) decode scratch, in floats: local_units(D) local-attention
-// records and one fine record (den in the header, num[D]), each of
-// (kStepRec + D) floats.
+// records, one fine record (den in the header, num[D]) and one coarse record
+// (coarse[D]), each of (kStepRec + D) floats.
 __host__ __device__ inline size_t step_floats(int head_dim, int sel_cap) {
   (void)sel_cap;
-  return (size_t)(local_units(head_dim) + 1) * (head_dim + kStepRec);
+  return (size_t)(local_units(head_dim) + 2) * (head_dim + kStepRec);
 }
 
 // Workspace layout (bytes from the start of tao_state_dev::workspace):
@@ -73,12 +73,15 @@ struct DecodeParams {
   bf16_t* out; int64_t out_sb, out_sh;
   float* parts;
   const float* fold_g; const float* fold_den;   // folded route (G^T, den weights)
+  const float* coarse_g;   // folded coarse read (G^T), read when coarse_on
   long long pos_hint;   // cursor of this step, or -1: read header[0]
   int B, H, keep, fine, group, fine_cap, page_cap, sel_cap;
+  int coarse_on;
 };
 
 // M = selected fines of the current route (0 before the first seal: no
-// fine read). The fine read uses the folded route (launch_fold).
+// fine read). The fine read uses the folded route (launch_fold); with
+// coarse_on the step also reads the folded coarse matrix (launch_coarse_fold).
 hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStream_t s);
 
 struct FoldParams {
@@ -88,6 +91,25 @@ struct FoldParams {
   int B, H, group, fine_cap, page_cap, sel_cap, M;
 };
 hipError_t launch_fold(const FoldParams& p, int head_dim, hipStream_t s);
+
+// Page value matrices of completed pages [first_page, first_page + count):
+// page_c[g][e][d] = r(sum_s sw[8g + s][d] * C^T_{8g+s}[e][d]).
+struct PageCoarseParams {
+  const bf16_t* bank; const bf16_t* sw; bf16_t* page_c;
+  int B, H, fine_cap, page_cap, group, first_page, count;
+};
+hipError_t launch_page_coarse(const PageCoarseParams& p, int head_dim, hipStream_t s);
+
+// Folded coarse reads G^T(n)[e][d] = sum_{p < n} softmax_p(page_z)[d] *
+// page_c[p][e][d] for n in [n_first, n_first + n_count), one pass over the
+// pages; output n_first + i goes to out + i * B*H*D*D as fp32 (out_f32) or
+// bf16.
+struct CoarseFoldParams {
+  const bf16_t* page_z; const bf16_t* page_c;
+  void* out; int out_f32;
+  int B, H, page_cap, n_first, n_count;
+};
+hipError_t launch_coarse_fold(const CoarseFoldParams& p, int head_dim, hipStream_t s);
 
 // tao_decode_step with the step's cursor given by the caller (position >= 0)
 // instead of read from header[0] on the device; used by the stream driver.
@@ -175,7 +197,9 @@ hipError_t launch_epochs(const EpochParams& p, int head_dim, hipStream_t s);
 
 // MFMA selected read + fusion over query tiles (<= 32 queries sharing one
 // route). tiles[t * 8 + ...] = {first query, count, route slot, selected,
-// epoch, sw split, fine_on, 0}.
+// epoch, sw split, fine_on, completed pages}. With coarse_pool, tiles with
+// completed >= 1 add the coarse read h . G^T(completed) from
+// coarse_pool[completed - coarse_first].
 struct ReadTilesParams {
   TokView rq;
   const bf16_t* bank; const bf16_t* sw;
@@ -188,6 +212,7 @@ struct ReadTilesParams {
   bf16_t* out; int64_t out_sb, out_st, out_sh;
   const int64_t* tiles; int n_tiles;
   int B, H, T, group, fine_cap, sel_cap;
+  const bf16_t* coarse_pool; int coarse_first;
 };
 hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t s);
 

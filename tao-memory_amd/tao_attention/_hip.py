@@ -31,6 +31,7 @@ class StateDev(ctypes.Structure):
         ("page_z", _vp), ("page_w", _vp),
         ("sel", _vp), ("chosen", _vp), ("header", _vp),
         ("fold_g", _vp), ("fold_den", _vp),
+        ("page_c", _vp), ("coarse_g", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
     ]
 
@@ -45,7 +46,8 @@ class Tokens(ctypes.Structure):
 
 class PrefillPools(ctypes.Structure):
     _fields_ = [("pw_pool", _vp), ("psw_pool", _vp), ("sel_pool", _vp),
-                ("pool_pcap", _i32), ("epochs", _i32), ("sel_slots", _i32)]
+                ("pool_pcap", _i32), ("epochs", _i32), ("sel_slots", _i32),
+                ("coarse_pool", _vp), ("coarse_first", _i32), ("coarse_count", _i32)]
 
 
 class StreamCfg(ctypes.Structure):
@@ -73,6 +75,8 @@ _SIGNATURES = {
     "tao_decode_step": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens),
                          ctypes.POINTER(Fusion), _i32, _vp, ctypes.POINTER(_i64), _vp], _i32),
     "tao_fold_route": ([ctypes.POINTER(StateDev), _i32, _vp], _i32),
+    "tao_page_coarse": ([ctypes.POINTER(StateDev), _i32, _i32, _vp], _i32),
+    "tao_fold_coarse": ([ctypes.POINTER(StateDev), _i32, _vp], _i32),
     "tao_route": ([ctypes.POINTER(StateDev), _vp, ctypes.POINTER(_i64),
                    _i32, _i32, _i32, _i32, _vp], _i32),
     "tao_write_fine": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i64, _vp,

@@ -15,7 +15,11 @@ out for MI355X instead of rebuilt per seal:
 * page descriptors, segment weights r(exp(r(z - page_z))) and page weights
   r(softmax over pages) are updated once per seal by the epilogue kernel:
   this is the reference's page-normalisation memo (:399-416), kept valid
-  across the whole seal epoch for every call shape.
+  across the whole seal epoch for every call shape;
+* with the coarse value branch (coarse_index_only=False) each completed
+  page's value matrix (:486-499) is kept in a page bank [B, H, P_cap, D, D]
+  (C^T) and the coarse read of every completed page is folded into one
+  fp32 D x D matrix per head at each page completion (:299-305).
 Every count (local length, fines, pages, route turns) is a closed form of the
 cursor (schedule.py), so no device-to-host synchronisation is needed.
 """
@@ -52,6 +56,10 @@ class _DeviceState:
         self.fold_g = torch.zeros((batch, heads, head_dim, head_dim), dtype=torch.float32,
                                   device=device)
         self.fold_den = torch.zeros((batch, heads, head_dim), dtype=torch.float32, device=device)
+        self.coarse_values = not config.coarse_index_only
+        self.coarse_g = (torch.zeros((batch, heads, head_dim, head_dim), dtype=torch.float32,
+                                     device=device) if self.coarse_values else None)
+        self.page_c = None
         self.fine_cap = 0
         self._allocate(fine_cap, copy_fines=0)
 
@@ -69,6 +77,8 @@ class _DeviceState:
         page_w = torch.zeros((B, H, page_cap, D), dtype=bf16, device=dev)
         sel = torch.zeros((B, H, sel_cap), dtype=torch.int32, device=dev)
         chosen = torch.zeros((B, H, chosen_cap), dtype=torch.int32, device=dev)
+        page_c = (torch.empty((B, H, page_cap, D, D), dtype=bf16, device=dev)
+                  if self.coarse_values else None)
         if copy_fines:
             n = copy_fines
             bank[:, :, :n].copy_(self.bank[:, :, :n])
@@ -81,8 +91,12 @@ class _DeviceState:
             sel[:, :, :m].copy_(self.sel[:, :, :m])
             c = min(self.chosen.shape[2], chosen_cap)
             chosen[:, :, :c].copy_(self.chosen[:, :, :c])
+            if page_c is not None:
+                done = n // cfg.coarse_group
+                page_c[:, :, :done].copy_(self.page_c[:, :, :done])
         self.bank, self.fine_z, self.fine_sw = bank, fine_z, fine_sw
         self.page_z, self.page_w, self.sel, self.chosen = page_z, page_w, sel, chosen
+        self.page_c = page_c
         self.fine_cap, self.page_cap, self.sel_cap, self.chosen_cap = (
             fine_cap, page_cap, sel_cap, chosen_cap)
         self.plan_words = 0
@@ -118,6 +132,8 @@ class _DeviceState:
         st.page_w, st.sel = self.page_w.data_ptr(), self.sel.data_ptr()
         st.chosen, st.header = self.chosen.data_ptr(), self.header.data_ptr()
         st.fold_g, st.fold_den = self.fold_g.data_ptr(), self.fold_den.data_ptr()
+        if self.coarse_values:
+            st.page_c, st.coarse_g = self.page_c.data_ptr(), self.coarse_g.data_ptr()
         st.workspace = self.workspace.data_ptr()
         st.workspace_bytes = self.workspace.numel()
         return st
@@ -216,7 +232,11 @@ class StreamCache:
         self._fast = None            # decode fast-path key (see decode)
         self._native = None          # native decode entry (tao_fast.cpp)
         self._fast_limit = -1
-        self._graph_mode = bool(self.config.q1_history_region_graph)
+        # The regional graph serves the memo-backed index-only read only
+        # (tao_stream.py:238-248).
+        self._graph_mode = bool(config.q1_history_region_graph
+                                and config.q1_page_normalization_memo
+                                and config.coarse_index_only)
         self._first_fine = self.config.first_fine
         self._graph_buffers = None
         self._info = (ctypes.c_int64 * 7)()
@@ -267,10 +287,6 @@ class StreamCache:
 
     def _check_supported(self, q):
         cfg = self.config
-        if not cfg.coarse_index_only:
-            raise NotImplementedError(
-                "the HIP path implements the index-only coarse preset "
-                "(presets.index_only_page_memo); the coarse value branch is not built yet")
         if cfg.fine_writer != "softmax":
             raise NotImplementedError("the HIP path implements the softmax fine writer")
         if cfg.fine_tokens != 256 or cfg.local_keep != 512:
@@ -333,7 +349,7 @@ class StreamCache:
         return _hip.StreamCfg(self.layer_index, cfg.local_keep, cfg.fine_tokens,
                               cfg.coarse_group, cfg.route_period, cfg.layer_stagger,
                               cfg.budget_root_scale, cfg.budget_offset,
-                              int(cfg.q1_history_region_graph))
+                              int(self._graph_mode))
 
     def _plan(self, pos0, tokens, outputs):
         """int64 plan of tao_prefill for tokens [pos0, pos0 + tokens), built by
@@ -344,14 +360,15 @@ class StreamCache:
         """
         lib = _hip.lib()
         scfg = self._stream_cfg()
-        info = (ctypes.c_int64 * 8)()
+        info = (ctypes.c_int64 * 10)()
         args = (ctypes.byref(scfg), pos0, tokens, self.route_coarse, self.route_size,
                 int(outputs))
         _hip.check(lib.tao_prefill_plan(*args, None, 0, info))
         plan = np.empty(info[0], dtype=np.int64)
         _hip.check(lib.tao_prefill_plan(*args, plan.ctypes.data, info[0], info))
         return plan, dict(epochs=info[1], turns=info[2], route=(info[3], info[4]),
-                          pool_pcap=info[5], history_chunks=info[6], chunks=info[7])
+                          pool_pcap=info[5], history_chunks=info[6], chunks=info[7],
+                          coarse_first=info[8], coarse_count=info[9])
 
     def _run_plan(self, dev, tok, fu, plan, info, local, out):
         plan_np = np.asarray(plan, dtype=np.int64)
@@ -374,6 +391,13 @@ class StreamCache:
             pools.sel_pool = sel_pool.data_ptr()
             pools.pool_pcap, pools.epochs, pools.sel_slots = pcap, info["epochs"], info["turns"] + 1
             keep = [pw_pool, psw_pool, sel_pool]
+            if dev.coarse_values and info["coarse_count"]:
+                coarse_pool = torch.empty((info["coarse_count"], B, H, D, D),
+                                          dtype=torch.bfloat16, device=dev.device)
+                pools.coarse_pool = coarse_pool.data_ptr()
+                pools.coarse_first = info["coarse_first"]
+                pools.coarse_count = info["coarse_count"]
+                keep.append(coarse_pool)
         out_s = (ctypes.c_int64 * 3)(*(_hip.strides_bth(out) if out is not None else (0, 0, 0)))
         dummy = dev.workspace.data_ptr()
         with self._timed("prefill"):
@@ -416,10 +440,18 @@ class StreamCache:
         self._fold()
 
     def _fold(self):
-        """Fold the current route under the current page weights (tao_fold_route)."""
-        if self._dev is not None and schedule.fines_at(self.position, self.config) > 0:
-            _hip.check(_hip.lib().tao_fold_route(ctypes.byref(self._dev.struct),
-                                                 self.route_size, self._dev.stream()))
+        """Fold the current route under the current page weights (tao_fold_route)
+        and, with the coarse value branch, the coarse read of the completed
+        pages (tao_fold_coarse)."""
+        fines = schedule.fines_at(self.position, self.config)
+        dev = self._dev
+        if dev is not None and fines > 0:
+            _hip.check(_hip.lib().tao_fold_route(ctypes.byref(dev.struct), self.route_size,
+                                                 dev.stream()))
+            completed = fines // self.config.coarse_group
+            if dev.coarse_values and completed:
+                _hip.check(_hip.lib().tao_fold_coarse(ctypes.byref(dev.struct), completed,
+                                                      dev.stream()))
 
     def _driver(self, dev):
         """Native per-token driver bound to the current buffers and cursor."""
@@ -654,7 +686,9 @@ class StreamCache:
             # The bank stores C^T[e][d]; the snapshot keeps the reference's C[d][e].
             packed = dev.bank[:, :, :fines].transpose(-1, -2).contiguous()
             for i in range(completed):
-                pages.append((dev.page_z[:, :, i].clone(), None,
+                pc = (dev.page_c[:, :, i].transpose(-1, -2).contiguous()
+                      if dev.coarse_values else None)
+                pages.append((dev.page_z[:, :, i].clone(), pc,
                               dev.fine_z[:, :, i * group:(i + 1) * group].clone()))
             for j in range(pending):
                 pending_z.append(dev.fine_z[:, :, completed * group + j].clone())
@@ -711,9 +745,15 @@ class StreamCache:
             buf.index_copy_(1, slots, src.to(torch.bfloat16))
         if fines:
             dev.bank[:, :, :fines].copy_(packed.transpose(-1, -2))
-            for i, (pz, _, fz) in enumerate(pages):
+            rebuild = []
+            for i, (pz, pc, fz) in enumerate(pages):
                 dev.page_z[:, :, i].copy_(pz)
                 dev.fine_z[:, :, i * group:(i + 1) * group].copy_(fz)
+                if dev.coarse_values:
+                    if pc is None:
+                        rebuild.append(i)
+                    else:
+                        dev.page_c[:, :, i].copy_(pc.transpose(-1, -2))
             for j, z in enumerate(pending_z):
                 dev.fine_z[:, :, len(pages) * group + j].copy_(z)
             # Completed pages keep their snapshot descriptors; the pending
@@ -723,6 +763,10 @@ class StreamCache:
                 _hip.check(lib.tao_seal_epilogue(
                     ctypes.byref(dev.struct), i * group + group - 1, i + 1, 0,
                     dev.stream()))
+            # A snapshot without page values (written by an index-only state)
+            # gets them rebuilt from its fines and descriptors.
+            for i in rebuild:
+                _hip.check(lib.tao_page_coarse(ctypes.byref(dev.struct), i, 1, dev.stream()))
             if pending_z:
                 _hip.check(lib.tao_seal_epilogue(
                     ctypes.byref(dev.struct), fines - 1, len(pages) + 1, 1, dev.stream()))

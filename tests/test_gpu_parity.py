@@ -46,8 +46,8 @@ def run_hip(state, xs, fa, fb, splits, alpha=0.5):
     return torch.cat(outs, 1)
 
 
-def run_oracle(layer, xs, fa, fb, splits, alpha=0.5):
-    s = O.OracleStream(layer)
+def run_oracle(layer, xs, fa, fb, splits, alpha=0.5, geometry=None):
+    s = O.OracleStream(layer, geometry)
     q, k, v, rq, rk = xs
     outs, start = [], 0
     for width in splits:
@@ -61,9 +61,12 @@ def compare_snapshots(hip, ora):
     assert hip["position"] == ora["position"]
     assert hip["state_version"] == ora["state_version"]
     assert len(hip["pages"]) == len(ora["pages"])
-    for (pz, _, fz), (opz, _, ofz) in zip(hip["pages"], ora["pages"]):
+    for (pz, pc, fz), (opz, opc, ofz) in zip(hip["pages"], ora["pages"]):
         assert torch.equal(pz.cpu(), opz), "page descriptor"
         assert torch.equal(fz.cpu(), ofz), "fine z"
+        assert (pc is None) == (opc is None), "page value matrix presence"
+        if opc is not None:
+            torch.testing.assert_close(pc.cpu().float(), opc.float(), **TOL)
     for z, oz in zip(hip["pending_z"], ora["pending_z"]):
         assert torch.equal(z.cpu(), oz), "pending fine z"
     if ora["packed_fine_c"] is not None:
@@ -215,3 +218,47 @@ def test_ingest_state_equals_prefill_state(device):
     ya = run_hip(a, [torch.cat([x, x], 1)[:, :1] for x in tok], fa.to(device), fb.to(device), [1])
     yb = run_hip(b, [torch.cat([x, x], 1)[:, :1] for x in tok], fa.to(device), fb.to(device), [1])
     assert torch.equal(ya, yb)
+
+
+COARSE_VALUES = O.Geometry(coarse_index_only=False)
+
+
+def test_coarse_value_branch_prefill(device):
+    """DEFAULT_CONFIG (coarse values on): page value matrices, the coarse
+    pool of one prefill call spanning two page counts (pages complete at
+    2560 and 4608) read in the MFMA epilogue, then decode on the folded
+    coarse matrix."""
+    heads, width = 2, 128
+    xs, fa, fb = inputs(4720, heads, width, seed=16)
+    splits = [4700] + [1] * 20
+    print("coarse value branch prefill", flush=True)
+    state = new_state(0)
+    out = run_hip(state, to_dev(xs, device), fa.to(device), fb.to(device), splits)
+    ora, ref = run_oracle(0, xs, fa, fb, splits, geometry=COARSE_VALUES)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), **TOL)
+    snap = state.export()
+    assert len(snap["pages"]) == 2
+    compare_snapshots(snap, ora.export())
+
+
+def test_coarse_value_branch_decode_across_page_completion(device):
+    """The decode step at position 4607 seals the 16th fine: the driver builds
+    page 1's value matrix and refolds the coarse read for the next steps.
+    Export/import (with and without page values) continues identically."""
+    heads, width = 2, 64
+    xs, fa, fb = inputs(4641, heads, width, seed=17, unit_raw_k=True)
+    splits = [4590] + [1] * 50
+    print("coarse value branch decode", flush=True)
+    d = to_dev(xs, device)
+    state = new_state(1)
+    out = run_hip(state, d, fa.to(device), fb.to(device), splits)
+    ora, ref = run_oracle(1, xs, fa, fb, splits, geometry=COARSE_VALUES)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), **TOL)
+    snap = state.export()
+    compare_snapshots(snap, ora.export())
+    bare = dict(snap, pages=[(pz, None, fz) for pz, _, fz in snap["pages"]])
+    restored = StreamCache.from_export(snap)
+    rebuilt = StreamCache.from_export(bare)
+    tok = [x[:, 4640:4641] for x in d]
+    outs = [run_hip(s, tok, fa.to(device), fb.to(device), [1]) for s in (state, restored, rebuilt)]
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])

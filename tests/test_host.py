@@ -82,7 +82,7 @@ def test_library_exports_every_header_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert sorted(_hip.EXPORTED) == declared
-    assert lib.tao_abi_version() == 2
+    assert lib.tao_abi_version() == 3
 
 
 def test_workspace_size_and_error_convention():
@@ -156,7 +156,8 @@ def _reference_plan(cfg, layer, route_coarse, route_size, pos0, tokens, outputs)
             if outputs:
                 for qs in range(sub, sub + count, 32):
                     reads += [qs - pos0, min(32, sub + count - qs), slot, slot_m,
-                              epoch - first_epoch, (epoch // group) * group, 1, 0]
+                              epoch - first_epoch, (epoch // group) * group, 1,
+                              epoch // group]
     if not outputs and last_turn is not None:
         sub, epoch, completed, pending, coarse, selected = last_turn
         first_epoch = min(first_epoch, epoch)
@@ -171,8 +172,11 @@ def _reference_plan(cfg, layer, route_coarse, route_size, pos0, tokens, outputs)
                    f1 // group - f0 // group, first_epoch, n_epochs, len(turns) // 8,
                    len(reads) // 8, tokens - keep, keep, end - keep]
     history = sum(1 for e in chunk_epochs if e)
+    read_pages = [e // group for e in chunk_epochs if e // group >= 1] if outputs else []
+    coarse_range = ((min(read_pages), max(read_pages) - min(read_pages) + 1)
+                    if read_pages else (0, 0))
     info = [None, n_epochs, len(turns) // 8, route[0], route[1], f1 // group + 1, history,
-            len(chunk_epochs)]
+            len(chunk_epochs), *coarse_range]
     return header + attn + writes + turns + reads, info
 
 
@@ -196,7 +200,7 @@ def test_native_prefill_plan_matches_closed_forms():
                     for outputs in (True, False):
                         want, want_info = _reference_plan(cfg, layer, rc, rs, pos0, tokens,
                                                           outputs)
-                        info = (ctypes.c_int64 * 8)()
+                        info = (ctypes.c_int64 * 10)()
                         args = (ctypes.byref(scfg), pos0, tokens, rc, rs, int(outputs))
                         assert lib.tao_prefill_plan(*args, None, 0, info) == 0
                         assert info[0] == len(want)
@@ -206,7 +210,7 @@ def test_native_prefill_plan_matches_closed_forms():
                         assert list(info)[1:] == want_info[1:]
                         cases += 1
     assert cases > 400
-    small = (ctypes.c_int64 * 8)()
+    small = (ctypes.c_int64 * 10)()
     buf = np.zeros(4, dtype=np.int64)
     assert lib.tao_prefill_plan(ctypes.byref(scfg), 0, 300, 0, 0, 1, buf.ctypes.data, 4,
                                 small) < 0

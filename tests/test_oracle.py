@@ -330,3 +330,65 @@ def test_stream_rejects_contract_violations():
         s.prefill(q, k, v, rq, rk, fa, fb, 0.5, position=3)
     with pytest.raises(ValueError):
         s.decode(q[:, :2], k[:, :2], v[:, :2], rq[:, :2], rk[:, :2], fa, fb, 0.5)
+
+
+# ------------------------------------------------------------ coarse branch
+def test_page_coarse_matrix_against_fp64():
+    """page_C[d, e] = sum_s exp(z_s[d] - pz[d]) C_s[d, e] (tao_stream.py:486-499).
+    Weights index the row d of each C_s: weighting columns instead, or using
+    exp(pz - z), fails the fp64 comparison; identical fine matrices must come
+    back unchanged because a page's segment weights sum to one per row."""
+    torch.manual_seed(12)
+    b, h, d = 1, 2, 16
+    z = (torch.randn(b, h, 8, d) * 2).to(BF16)
+    c = torch.randn(b, h, 8, d, d).to(BF16)
+    pz = O.page_summary(z)
+    pc = O.page_coarse_matrix(z, pz, c)
+    w = torch.exp(z.double() - torch.logsumexp(z.double(), 2, keepdim=True))
+    ref = torch.einsum("bhsd,bhsde->bhde", w, c.double())
+    torch.testing.assert_close(pc.double(), ref, atol=3e-2, rtol=2e-2)
+    bad = torch.einsum("bhse,bhsde->bhde", w, c.double())
+    assert (pc.double() - bad).abs().max() > 5e-2
+    same = c[:, :, :1].expand(b, h, 8, d, d).contiguous()
+    pc_same = O.page_coarse_matrix(z, pz, same)
+    torch.testing.assert_close(pc_same.double(), same[:, :, 0].double(), atol=0, rtol=3e-2)
+
+
+def test_coarse_read_against_fp64():
+    """coarse = sum_p softmax_p(page_z)[d] h[d] page_C_p[d, :] (tao_stream.py:299-305);
+    one completed page reduces to h @ page_C."""
+    torch.manual_seed(13)
+    b, t, h, p, d = 1, 3, 2, 4, 16
+    pz = (torch.randn(b, h, p, d) * 2).to(BF16)
+    pc = torch.randn(b, h, p, d, d).to(BF16)
+    hq = O.query_weights(torch.randn(b, t, h, d).to(BF16))
+    out = O.coarse_read(hq, pz, pc)
+    w = torch.softmax(pz.double(), 2)                              # [b,h,p,d]
+    ref = torch.einsum("bthd,bhpd,bhpde->bthe", hq.double(), w, pc.double())
+    torch.testing.assert_close(out.double(), ref, atol=2e-2, rtol=2e-2)
+    wrong_axis = torch.softmax(pz.double(), 3)
+    bad = torch.einsum("bthd,bhpd,bhpde->bthe", hq.double(), wrong_axis, pc.double())
+    assert (out.double() - bad).abs().max() > 2e-2
+    one = O.coarse_read(hq, pz[:, :, :1], pc[:, :, :1])
+    torch.testing.assert_close(one.double(), torch.einsum("bthd,bhde->bthe", hq.double(),
+                                                          pc[:, :, 0].double()),
+                               atol=1e-2, rtol=2e-2)
+
+
+def test_stream_coarse_branch_switches_on_at_first_coarse():
+    """DEFAULT_CONFIG geometry (coarse_index_only=False): identical to the
+    index-only stream until the first page completes (first_coarse = 2560),
+    different afterwards; chunking and decode still give identical outputs."""
+    xs, fa, fb = _stream_inputs(2700, seed=4)
+    values = O.Geometry(coarse_index_only=False)
+    with_values = _run(O.OracleStream(0, values), xs, fa, fb, [2700])
+    index_only = _run(O.OracleStream(0), xs, fa, fb, [2700])
+    assert torch.equal(with_values[:, :2560], index_only[:, :2560])
+    assert not torch.equal(with_values[:, 2560:], index_only[:, 2560:])
+    calls = _run(O.OracleStream(0, values), xs, fa, fb, [1000, 1500, 60, 1] + [1] * 139)
+    torch.testing.assert_close(with_values, calls, atol=0, rtol=0)
+    s = O.OracleStream(0, values)
+    _run(s, xs, fa, fb, [2700])
+    snap = s.export()
+    assert len(snap["pages"]) == 1 and snap["pages"][0][1] is not None
+    assert snap["pages"][0][1].shape == (1, 2, 16, 16)

@@ -262,6 +262,11 @@ int tao_prefill_plan(const tao_stream_cfg* cfg, int64_t pos0, int64_t tokens,
                      int32_t route_coarse, int32_t route_size, int32_t outputs,
                      int64_t* plan, int64_t plan_cap, int64_t* info);
 
+/* Numerics self-test (no reference counterpart): y[i] = the library's
+ * bf16(correctly rounded fp32 exp(x[i])) (op 0) or log (op 1) for n bf16
+ * device inputs, the functions every writer and page kernel uses. */
+int tao_numerics_selftest(int32_t op, const void* x, void* y, int64_t n, void* stream);
+
 /* Native per-token driver (replaces the Python control flow of one decode
  * call: operator.py:130-138, tao_stream.py:196-249 and 919-969,
  * history_region_graph.py:66-113). It keeps the cursor and the current route

@@ -734,10 +734,10 @@ int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu, int32_t sele
     if (e == hipSuccess) e = le;
   }
   if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
-  if (cs) hipStreamDestroy(cs);
+  if (cs) (void)hipStreamDestroy(cs);
   if (e != hipSuccess) {
-    if (g->exec) hipGraphExecDestroy(g->exec);
-    if (g->graph) hipGraphDestroy(g->graph);
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
     delete g;
     return check_hip(e, "tao_graph_create");
   }
@@ -767,7 +767,7 @@ int tao_graph_destroy(void* graph) {
   DecodeGraph* g = (DecodeGraph*)graph;
   hipError_t e = hipSuccess;
   if (g->exec) e = hipGraphExecDestroy(g->exec);
-  if (g->graph) hipGraphDestroy(g->graph);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
   delete g;
   return check_hip(e, "tao_graph_destroy");
 }

@@ -43,28 +43,35 @@ TAO_DEV bool near_bf16_midpoint(float y, int margin) {
   return dist <= margin && dist >= -margin;
 }
 
-// bf16(correctly rounded fp32 exp(x)).
+// bf16(correctly rounded fp32 exp(x)). The fast value is the hardware 2^t
+// at t = r32(x * log2 e): for |x| <= 8 the argument's rounding and the
+// rounded log2 e move it by under 8 fp32 ulps, plus the hardware exp's own
+// ulp. Near a bf16 rounding boundary (16 ulps), or for |x| > 8, the fp64 exp
+// decides. Every kernel call site passes a bf16 x, and all 65536 of them are
+// checked against the correctly rounded reference.
+// exp_fast / exp_needs_exact / exp_exact are the pieces, for callers that
+// batch the (rare) fp64 fix-ups of several values behind one branch.
+TAO_DEV float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269502f); }
+
+TAO_DEV bool exp_needs_exact(float x, float y) {
+  return near_bf16_midpoint(y, 16) || !(__builtin_fabsf(x) <= 8.0f);
+}
+
+TAO_DEV float exp_exact(float x) { return (float)exp((double)x); }
+
 TAO_DEV float exp_bf(float x) {
-  float y = expf(x);
-  if (near_bf16_midpoint(y, 16)) y = (float)exp((double)x);
+  float y = exp_fast(x);
+  if (exp_needs_exact(x, y)) y = exp_exact(x);
   return rbf(y);
 }
 
-// bf16(correctly rounded fp32 log(x)).
+// bf16(correctly rounded fp32 log(x)); zero, negative, denormal and
+// non-finite inputs take the fp64 log.
 TAO_DEV float log_bf(float x) {
   float y = logf(x);
-  if (near_bf16_midpoint(y, 16)) y = (float)log((double)x);
+  if (near_bf16_midpoint(y, 16) || !(x >= 1.17549435e-38f && x < __builtin_inff()))
+    y = (float)log((double)x);
   return rbf(y);
-}
-
-// bf16(x / y) (fp32 division correctly rounded, then RNE to bf16) from the
-// approximate reciprocal inv ~ 1/y: x * inv is within a few fp32 ulps of
-// x / y, so unless it lies near a bf16 rounding boundary both round alike;
-// near one the IEEE division decides.
-TAO_DEV float div_bf(float x, float y, float inv) {
-  const float q = x * inv;
-  if (near_bf16_midpoint(q, 16)) return rbf(x / y);
-  return rbf(q);
 }
 
 // Correctly rounded fp32 exp (fp64 evaluation).

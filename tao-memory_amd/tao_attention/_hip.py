@@ -102,6 +102,7 @@ _SIGNATURES = {
                           _vp, ctypes.POINTER(_vp)], _i32),
     "tao_graph_launch": ([_vp, ctypes.POINTER(Tokens), _vp], _i32),
     "tao_graph_destroy": ([_vp], _i32),
+    "tao_numerics_selftest": ([_i32, _vp, _vp, _i64, _vp], _i32),
 }
 
 EXPORTED = tuple(_SIGNATURES)

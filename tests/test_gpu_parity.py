@@ -262,3 +262,24 @@ def test_coarse_value_branch_decode_across_page_completion(device):
     tok = [x[:, 4640:4641] for x in d]
     outs = [run_hip(s, tok, fa.to(device), fb.to(device), [1]) for s in (state, restored, rebuilt)]
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("op", ["exp", "log"])
+def test_exp_log_exhaustive_over_bf16(device, op):
+    """The library's bf16(correctly rounded fp32 exp / log), evaluated on all
+    65536 bf16 bit patterns (every kernel call site rounds its argument to
+    bf16 first), against the oracle's fp64-evaluated functions."""
+    import ctypes
+    from tao_attention import _hip
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    x = bits.view(BF16)
+    xd = x.to(device)
+    y = torch.empty_like(xd)
+    print(f"numerics self-test {op}", flush=True)
+    _hip.check(_hip.lib().tao_numerics_selftest(0 if op == "exp" else 1, xd.data_ptr(),
+                                                y.data_ptr(), 65536, _hip.stream_ptr(xd.device)))
+    got = y.cpu().float()
+    ref = (O.exp32 if op == "exp" else O.log32)(x.float()).to(BF16).float()
+    both_nan = torch.isnan(got) & torch.isnan(ref)
+    same = (got == ref) | both_nan
+    assert same.all(), x[~same][:8]

@@ -84,6 +84,11 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
     for (int kk = 0; kk < KK; ++kk) qreg[kk] = as_bf16x8(*(const uint4*)(qrow + 16 * kk + 8 * hl));
   }
   const float scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)D));
+  // Online softmax with a lazily raised reference: p = 2^(s * c - m) with
+  // m (log2 units) raised only when a block's maximum exceeds it by more
+  // than kSlack, so O and l are rescaled rarely; o / l is independent of the
+  // reference and p <= 2^kSlack stays well inside bf16's range.
+  constexpr float kSlack = 8.0f;
 
   // Global loads of one 64-key block into registers (prefetch).
   uint4 kpre[KJ], va[VJ], vb[VJ];
@@ -167,7 +172,7 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int off = sub * 32 + 8 * (i / 4) + 4 * hl + (i % 4);
-          const float v = off < lim ? s[sub][i] * scale_log2 : -__builtin_inff();
+          const float v = off < lim ? s[sub][i] : -__builtin_inff();
           s[sub][i] = v;
           bmax = fmaxf(bmax, v);
         }
@@ -175,34 +180,36 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float v = s[sub][i] * scale_log2;
-          s[sub][i] = v;
-          bmax = fmaxf(bmax, v);
-        }
+        for (int i = 0; i < 16; ++i) bmax = fmaxf(bmax, s[sub][i]);
     }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    const float m_new = fmaxf(m_run, bmax);
-    // A query with no visible key yet keeps m = -inf: shift by 0 instead, so
-    // every exp below sees -inf and returns 0.
-    const float m_use = m_new == -__builtin_inff() ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    float rsum = 0.0f;
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64)) * scale_log2;
+    // Raise the reference (and rescale O, l) only past the slack; a query
+    // with no visible key yet keeps m = -inf and a shift of 0, so every exp
+    // below sees -inf and returns 0.
+    if (__any(bmax > m_run + kSlack)) {
+      const float m_new = fmaxf(m_run, bmax);
+      // No visible key yet on this lane (both -inf): O and l are still 0.
+      const float alpha = m_new == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[t][i] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -__builtin_inff() ? 0.0f : m_run;
+    float rs[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float e = __builtin_amdgcn_exp2f(s[sub][i] - m_use);
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[sub][i], scale_log2, -m_use));
         s[sub][i] = e;
-        rsum += e;
+        rs[i & 1] += e;
       }
+    float rsum = rs[0] + rs[1];
     rsum += __shfl_xor(rsum, 32, 64);
-    l_run = l_run * alpha + rsum;
-    m_run = m_new;
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[t][i] *= alpha;
+    l_run += rsum;
 
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)

@@ -53,13 +53,15 @@ struct WriterSmem {
   float inv_z[D / 2];          // 1 / Z per channel of the half
 };
 
-TAO_DEV const bf16_t* token_row(const WriterParams& p, int b, int h, long long pos,
-                                const TokView& tv, const bf16_t* ring, int D) {
-  if (pos >= p.new_base) {
-    const long long t = pos - p.new_base;
-    return tv.p + b * tv.sb + t * tv.st + h * tv.sh;
-  }
-  const int slot = (int)(pos % p.L);
+// Row of token `t` of a block: token rel + t of the call's operands when
+// rel + t >= 0 (rel = start - new_base), else ring slot (slot0 + t) mod L
+// (slot0 = start mod L, t < 256 < L: at most one wrap).
+TAO_DEV const bf16_t* block_row(const WriterParams& p, const TokView& tv, const bf16_t* ring,
+                                int b, int h, long long rel, int slot0, int t, int D) {
+  const long long r = rel + t;
+  if (r >= 0) return tv.p + b * tv.sb + r * tv.st + h * tv.sh;
+  int slot = slot0 + t;
+  slot = slot >= p.L ? slot - p.L : slot;
   return ring + (((size_t)b * p.L + slot) * p.H + h) * D;
 }
 
@@ -93,6 +95,8 @@ __global__ __launch_bounds__(kWriterThreads) void writer_kernel(WriterParams p) 
   const int slot = p.first_slot + blk;
   const int tid = threadIdx.x;
   const int d0 = half * DH;
+  const long long rel = start - p.new_base;
+  const int slot0 = (int)(start % p.L);
 
   // ---- issue the K half (all 256 tokens) and V chunk 0 loads. Job ->
   // (channel chunk c, token pair): 128 consecutive K jobs / 32 consecutive V
@@ -102,16 +106,16 @@ __global__ __launch_bounds__(kWriterThreads) void writer_kernel(WriterParams p) 
   for (int j = 0; j < KJ; ++j) {
     const int job = tid + j * kWriterThreads;
     const int c = job / (kBlock / 2), t0 = 2 * (job % (kBlock / 2));
-    ka[j] = *(const uint4*)(token_row(p, b, h, start + t0, p.rk, p.ring_raw, D) + d0 + c * 8);
-    kb[j] = *(const uint4*)(token_row(p, b, h, start + t0 + 1, p.rk, p.ring_raw, D) + d0 + c * 8);
+    ka[j] = *(const uint4*)(block_row(p, p.rk, p.ring_raw, b, h, rel, slot0, t0, D) + d0 + c * 8);
+    kb[j] = *(const uint4*)(block_row(p, p.rk, p.ring_raw, b, h, rel, slot0, t0 + 1, D) + d0 + c * 8);
   }
   auto load_v = [&](int chunk) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < VJ; ++j) {
       const int job = tid + j * kWriterThreads;
       const int c = job / (kVChunk / 2), t0 = chunk * kVChunk + 2 * (job % (kVChunk / 2));
-      va[j] = *(const uint4*)(token_row(p, b, h, start + t0, p.v, p.ring_v, D) + c * 8);
-      vb[j] = *(const uint4*)(token_row(p, b, h, start + t0 + 1, p.v, p.ring_v, D) + c * 8);
+      va[j] = *(const uint4*)(block_row(p, p.v, p.ring_v, b, h, rel, slot0, t0, D) + c * 8);
+      vb[j] = *(const uint4*)(block_row(p, p.v, p.ring_v, b, h, rel, slot0, t0 + 1, D) + c * 8);
     }
   };
   load_v(0);
@@ -149,20 +153,24 @@ __global__ __launch_bounds__(kWriterThreads) void writer_kernel(WriterParams p) 
       uint4* cell = (uint4*)&sm.kt[d][qq * QT + t];
       const uint4 u = *cell;
       const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-      // Eight exps, then one (rarely taken) branch for their fp64 fix-ups.
+      // Eight exps, then one (rarely taken) branch for their fp64 fix-ups:
+      // the closest low half-word to the bf16 rounding boundary and the
+      // largest |x| of the eight decide it (exp_needs_exact for all eight).
       float x[8], y[8];
-      bool fix = false;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         x[2 * i] = rbf(__uint_as_float(w[i] << 16) - m);
         x[2 * i + 1] = rbf(__uint_as_float(w[i] & 0xFFFF0000u) - m);
       }
+      uint32_t near = 0xFFFFFFFFu;
+      float big = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         y[i] = exp_fast(x[i]);
-        fix |= exp_needs_exact(x[i], y[i]);
+        near = min(near, (__float_as_uint(y[i]) & 0xFFFFu) - 0x7FF0u);
+        big = fmaxf(big, __builtin_fabsf(x[i]));
       }
-      if (fix) {
+      if (near < 33u || !(big <= 8.0f)) {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
           if (exp_needs_exact(x[i], y[i])) y[i] = exp_exact(x[i]);

@@ -285,6 +285,27 @@ int tao_stream_sync(void* handle, const tao_state_dev* st, int64_t position,
  * captured. */
 int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu, void* out,
                       const int64_t* out_s, void* stream, int64_t* info);
+/* Batched decode of `count` independent requests of one layer (no reference
+ * counterpart: the reference decodes one request per call; this serves
+ * many streams, BASELINE config 5, with one decode step launch pair).
+ * handles: the requests' stream drivers (tao_stream_open) over states of
+ * batch 1 that share heads, head width, geometry and coarse branch. table:
+ * caller device memory of tao_batch_table_bytes(count) bytes, filled by
+ * tao_batch_open and refreshed by tao_batch_sync after any member's buffers
+ * moved (tao_stream_sync first). One tao_batch_decode call = one new token
+ * per request: each request's route refresh and seal as its own cursor
+ * requires (tao_stream_decode's rules, eager), then one decode step for all
+ * requests. tok / out: [count, 1, H, D] views, request r = batch row r.
+ * info (int64[4 * count]): per request refreshed, sealed, route coarse
+ * count, route size. The results equal one tao_stream_decode per request. */
+size_t tao_batch_table_bytes(int32_t count);
+int tao_batch_open(void* const* handles, int32_t count, void* table, size_t table_bytes,
+                   void* stream, void** batch);
+int tao_batch_sync(void* batch, void* stream);
+int tao_batch_decode(void* batch, const tao_tokens* tok, const tao_fusion* fu, void* out,
+                     const int64_t* out_s, void* stream, int64_t* info);
+int tao_batch_close(void* batch);
+
 /* Destroy the driver's captured graph (semantic state is untouched). */
 int tao_stream_release(void* handle);
 int tao_stream_close(void* handle);

@@ -76,20 +76,29 @@ TAO_DEV float group_sum(float v) {
   return v;
 }
 
+// One (request, head)'s operands of one decode step, shared by the
+// single-request kernels (DecodeParams) and the batched ones (BatchStepParams).
+struct StepReq {
+  const bf16_t* q; const bf16_t* k; const bf16_t* v; const bf16_t* rq; const bf16_t* rk;
+  bf16_t* ring_k; bf16_t* ring_v; bf16_t* ring_raw;   // slot 0 of this (state row, head)
+  const float* fold_g; const float* fold_den; const float* coarse_g;   // this head's
+  float* recs;                                        // this (request, head)'s records
+  long long position;
+};
+
 // Fine-read workgroup f: num[e] = h . G^T[e] for rows e in
-// [f * kFineRows, (f + 1) * kFineRows) of the folded matrix gmat, thread
-// (row tid / 8, part tid % 8); with gden (the fine read) workgroup 0 also
-// writes den = r(h . g). h = r(softmax_D(raw_q)) with the exp correctly
-// rounded in fp32.
+// [f * kFineRows, (f + 1) * kFineRows) of the folded matrix gmat (this
+// head's), thread (row tid / 8, part tid % 8); with gden (the fine read)
+// workgroup 0 also writes den = r(h . g). h = r(softmax_D(raw_q)) with the
+// exp correctly rounded in fp32.
 template <int D>
-__device__ void fine_read(const DecodeParams& p, int b, int h, int f, float* frec,
-                          float* hq, const float* gmat, const float* gden_base) {
+__device__ void fine_read(const bf16_t* rq, int f, float* frec, float* hq, const float* gmat,
+                          const float* gden) {
   constexpr int DP = D / 8, PER = D / 64;
   const int tid = threadIdx.x, row = tid / 8, part = tid % 8;
-  const int bh = b * p.H + h;
   const int e = f * kFineRows + row;
-  const bool with_den = gden_base != nullptr && f == 0;
-  const float* grow = gmat + ((size_t)bh * D + e) * D + part * DP;
+  const bool with_den = gden != nullptr && f == 0;
+  const float* grow = gmat + (size_t)e * D + part * DP;
   float gv[DP];
 #pragma unroll
   for (int k = 0; k < DP; k += 4) {
@@ -97,12 +106,11 @@ __device__ void fine_read(const DecodeParams& p, int b, int h, int f, float* fre
     gv[k] = v.x; gv[k + 1] = v.y; gv[k + 2] = v.z; gv[k + 3] = v.w;
   }
   if (tid < 64) {
-    const bf16_t* rq = p.rq.p + b * p.rq.sb + h * p.rq.sh;
-    float xr[PER], gden[PER];
+    float xr[PER], gd[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       xr[k] = bf2f(rq[tid + 64 * k]);
-      gden[k] = with_den ? gden_base[(size_t)bh * D + tid + 64 * k] : 0.0f;
+      gd[k] = with_den ? gden[tid + 64 * k] : 0.0f;
     }
     float top = -__builtin_inff();
 #pragma unroll
@@ -120,7 +128,7 @@ __device__ void fine_read(const DecodeParams& p, int b, int h, int f, float* fre
     for (int k = 0; k < PER; ++k) {
       const float hv = rbf(ex[k] / s);
       hq[tid + 64 * k] = hv;
-      dsum = k == 0 ? hv * gden[k] : fmaf(hv, gden[k], dsum);
+      dsum = k == 0 ? hv * gd[k] : fmaf(hv, gd[k], dsum);
     }
     if (with_den) {
       dsum = wave_sum_fold(dsum);
@@ -137,38 +145,34 @@ __device__ void fine_read(const DecodeParams& p, int b, int h, int f, float* fre
   if (part == 0) frec[kStepRec + e] = acc;
 }
 
-// Kernel A: per (batch, head) NLOC local-attention workgroups (the window
-// split by keys), NFINE fine-read workgroups and, with coarse_on, NFINE
-// coarse-read workgroups; no cross-workgroup communication.
+// Workgroup j of one (request, head): j < NLOC local attention over keys
+// [j*K, (j+1)*K) of the window (workgroup 0 also appends the new token to
+// the ring), then NFINE fine-read workgroups (M > 0) and, with coarse_on,
+// NFINE coarse-read workgroups.
 template <int D>
-__global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, int M) {
+__device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int keep, int fine,
+                           int slot_stride, StepSmem<D>& sm) {
   using G = Geo<D>;
-  __shared__ StepSmem<D> sm;
-  const int per_head = G::NLOC + G::NFINE * (p.coarse_on ? 2 : 1);
-  const int bh = blockIdx.x / per_head;
-  const int j = blockIdx.x % per_head;
-  const int b = bh / p.H, h = bh % p.H;
-  float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
+  float* recs = q.recs;
   if (j >= G::NLOC + G::NFINE) {
-    fine_read<D>(p, b, h, j - G::NLOC - G::NFINE, recs + (G::NLOC + 1) * (D + kStepRec),
-                 sm.red[0], p.coarse_g, nullptr);
+    if (coarse_on)
+      fine_read<D>(q.rq, j - G::NLOC - G::NFINE, recs + (G::NLOC + 1) * (D + kStepRec),
+                   sm.red[0], q.coarse_g, nullptr);
     return;
   }
   if (j >= G::NLOC) {
     if (M > 0)
-      fine_read<D>(p, b, h, j - G::NLOC, recs + G::NLOC * (D + kStepRec), sm.red[0], p.fold_g,
-                   p.fold_den);
+      fine_read<D>(q.rq, j - G::NLOC, recs + G::NLOC * (D + kStepRec), sm.red[0], q.fold_g,
+                   q.fold_den);
     return;
   }
   float* rec = recs + j * (D + kStepRec);
   const int tid = threadIdx.x, chn = tid % G::CH, r = tid / G::CH;
-  const int L = p.keep + p.fine;
-  const long long position = p.pos_hint >= 0 ? p.pos_hint : p.header[0];
-  const int n_old = local_len_at(position, p.keep, p.fine);
+  const int L = keep + fine;
+  const long long position = q.position;
+  const int n_old = local_len_at(position, keep, fine);
   const int n = n_old + 1;
   const int first_slot = (int)((position - n_old) % L);
-  const bf16_t* kn = p.k.p + b * p.k.sb + h * p.k.sh;
-  const bf16_t* vn = p.v.p + b * p.v.sb + h * p.v.sh;
   const int k0 = j * G::KEYS;
   if (k0 >= n) {   // past the window: an empty record
     if (tid == 0) { rec[0] = -__builtin_inff(); rec[1] = 0.0f; }
@@ -179,31 +183,30 @@ __global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, 
 #pragma unroll
   for (int i = 0; i < G::KPT; ++i) {
     const int key = k0 + r + i * G::ROWS;
-    const bf16_t* krow = kn;
-    const bf16_t* vrow = vn;
+    const bf16_t* krow = q.k;
+    const bf16_t* vrow = q.v;
     if (key < n_old) {
       int slot = first_slot + key;
       slot = slot >= L ? slot - L : slot;
-      const size_t off = (((size_t)b * L + slot) * p.H + h) * D;
-      krow = p.ring_k + off;
-      vrow = p.ring_v + off;
+      const size_t off = (size_t)slot * slot_stride;
+      krow = q.ring_k + off;
+      vrow = q.ring_v + off;
     }
     kraw[i] = *(const uint4*)(krow + chn * 8);
     vraw[i] = *(const uint4*)(vrow + chn * 8);
   }
   float qv[8];
-  unpack8(*(const uint4*)(p.q.p + b * p.q.sb + h * p.q.sh + chn * 8), qv);
+  unpack8(*(const uint4*)(q.q + chn * 8), qv);
   if (j == 0) {
     // Append the new token at slot position % L. No key of this step's
     // window occupies that slot (window length n_old <= L - 1).
     int slot = first_slot + n_old;
     slot = slot >= L ? slot - L : slot;
-    const size_t off = (((size_t)b * L + slot) * p.H + h) * D;
-    const bf16_t* rk = p.rk.p + b * p.rk.sb + h * p.rk.sh;
+    const size_t off = (size_t)slot * slot_stride;
     for (int d = tid; d < D; d += kThreads) {
-      p.ring_k[off + d] = kn[d];
-      p.ring_v[off + d] = vn[d];
-      p.ring_raw[off + d] = rk[d];
+      q.ring_k[off + d] = q.k[d];
+      q.ring_v[off + d] = q.v[d];
+      q.ring_raw[off + d] = q.rk[d];
     }
   }
   const float scale = (float)(1.0 / __builtin_sqrt((double)D));
@@ -220,13 +223,13 @@ __global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, 
     const float s = group_sum<G::CH>(part) * scale;
     if (k0 + r + i * G::ROWS < n) {
       const float mn = fmaxf(m, s);
-      const float keep = __expf(m - mn);
+      const float keep_f = __expf(m - mn);
       const float w = __expf(s - mn);
       float vv[8];
       unpack8(vraw[i], vv);
-      l = fmaf(l, keep, w);
+      l = fmaf(l, keep_f, w);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = fmaf(acc[e], keep, w * vv[e]);
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(acc[e], keep_f, w * vv[e]);
       m = mn;
     }
   }
@@ -255,28 +258,61 @@ __global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, 
   }
 }
 
+// Kernel A: per (batch, head) NLOC local-attention workgroups (the window
+// split by keys), NFINE fine-read workgroups and, with coarse_on, NFINE
+// coarse-read workgroups; no cross-workgroup communication.
+template <int D>
+__global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, int M) {
+  using G = Geo<D>;
+  __shared__ StepSmem<D> sm;
+  const int per_head = G::NLOC + G::NFINE * (p.coarse_on ? 2 : 1);
+  const int bh = blockIdx.x / per_head;
+  const int j = blockIdx.x % per_head;
+  const int b = bh / p.H, h = bh % p.H;
+  StepReq q;
+  q.q = p.q.p + b * p.q.sb + h * p.q.sh;
+  q.k = p.k.p + b * p.k.sb + h * p.k.sh;
+  q.v = p.v.p + b * p.v.sb + h * p.v.sh;
+  q.rq = p.rq.p + b * p.rq.sb + h * p.rq.sh;
+  q.rk = p.rk.p + b * p.rk.sb + h * p.rk.sh;
+  const int L = p.keep + p.fine;
+  const size_t ring0 = ((size_t)b * L * p.H + h) * D;
+  q.ring_k = p.ring_k + ring0;
+  q.ring_v = p.ring_v + ring0;
+  q.ring_raw = p.ring_raw + ring0;
+  q.fold_g = p.fold_g + (size_t)bh * D * D;
+  q.fold_den = p.fold_den + (size_t)bh * D;
+  q.coarse_g = p.coarse_g ? p.coarse_g + (size_t)bh * D * D : nullptr;
+  q.recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
+  q.position = p.pos_hint >= 0 ? p.pos_hint : p.header[0];
+  units_body<D>(q, j, M, p.coarse_on, p.keep, p.fine, p.H * D, sm);
+}
+
 // Kernel B: one 256-thread workgroup per (batch, head, 32 channels). Thread
 // group g = tid / 32 owns local records j = g (mod 8), channel dc = tid % 32;
-// the groups merge in ascending g (fixed order), then the fine record and the
-// fusion epilogue give the output.
+// the groups merge in ascending g (fixed order), then the fine and coarse
+// records and the fusion epilogue give the output.
 constexpr int kCombineCols = 32;
 constexpr int kCombineGroups = kThreads / kCombineCols;
 
+struct CombineArgs {
+  const void* fa; const void* fb; int f_dtype;
+  const int64_t* fa_s; const int64_t* fb_s;
+  float gain;
+};
+
 template <int D>
-__global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p, int M) {
+__device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, int h, int chunk,
+                             int M, int coarse_on, const CombineArgs& c) {
   using Gm = Geo<D>;
-  constexpr int STRIDE = D + kStepRec, G = kCombineGroups, CHUNKS = D / kCombineCols;
+  constexpr int STRIDE = D + kStepRec, G = kCombineGroups;
   constexpr int NLOC = Gm::NLOC, LPG = (NLOC + G - 1) / G;
   __shared__ float ml[NLOC][2];
   __shared__ float part_loc[G][kCombineCols];
-  const int bh = blockIdx.x / CHUNKS;
-  const int chunk = blockIdx.x % CHUNKS;
-  const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, dc = tid % kCombineCols, g = tid / kCombineCols;
   const int d = chunk * kCombineCols + dc;
-  const float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
 
-  // Loads first: local records, the fine record, fusion operands.
+  // Loads first: local records, the fine and coarse records, fusion operands.
   float m_g[LPG], l_g[LPG], o_g[LPG];
 #pragma unroll
   for (int i = 0; i < LPG; ++i) {
@@ -287,16 +323,16 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
   }
   float q = 0.0f, num = 0.0f, den = 1.0f, craw = 0.0f, a[3], bb[3];
   if (g == 0) {
-    q = bf2f(p.rq.p[b * p.rq.sb + h * p.rq.sh + d]);
+    q = bf2f(rq[d]);
     if (M > 0) {
       den = recs[NLOC * STRIDE];
       num = recs[NLOC * STRIDE + kStepRec + d];
     }
-    if (p.coarse_on) craw = recs[(NLOC + 1) * STRIDE + kStepRec + d];
+    if (coarse_on) craw = recs[(NLOC + 1) * STRIDE + kStepRec + d];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      a[i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + d * p.fa_s[1] + i * p.fa_s[2]);
-      bb[i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + d * p.fb_s[1] + i * p.fb_s[2]);
+      a[i] = load_param(c.fa, c.f_dtype, h * c.fa_s[0] + d * c.fa_s[1] + i * c.fa_s[2]);
+      bb[i] = load_param(c.fb, c.f_dtype, h * c.fb_s[0] + d * c.fb_s[1] + i * c.fb_s[2]);
     }
   }
   if (dc == 0) {
@@ -324,17 +360,84 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
     for (int gg = 0; gg < G; ++gg) nl += part_loc[gg][dc];
     const float local = rbf(nl / den_local);
     bf16_t result;
-    if (M > 0 || p.coarse_on) {
+    if (M > 0 || coarse_on) {
       const float fine_v = M > 0 ? rbf(rbf(num) / den) : 0.0f;
-      result = fuse_element(q, local, rbf(craw), fine_v, a, bb, p.gain, p.coarse_on ? 1 : 0,
+      result = fuse_element(q, local, rbf(craw), fine_v, a, bb, c.gain, coarse_on ? 1 : 0,
                             M > 0 ? 1 : 0);
     } else {
       result = f2bf(local);
     }
-    p.out[b * p.out_sb + h * p.out_sh + d] = result;
+    out[d] = result;
   }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p, int M) {
+  constexpr int CHUNKS = D / kCombineCols;
+  const int bh = blockIdx.x / CHUNKS;
+  const int chunk = blockIdx.x % CHUNKS;
+  const int b = bh / p.H, h = bh % p.H;
+  const CombineArgs c = {p.fa, p.fb, p.f_dtype, p.fa_s, p.fb_s, p.gain};
+  combine_body<D>(p.parts + (size_t)bh * step_floats(D, p.sel_cap),
+                  p.rq.p + b * p.rq.sb + h * p.rq.sh, p.out + b * p.out_sb + h * p.out_sh, h,
+                  chunk, M, p.coarse_on, c);
   // Kernel A of this step has finished reading the position: advance it.
-  if (blockIdx.x == 0 && tid == 0) p.header[0] = p.header[0] + 1;
+  if (blockIdx.x == 0 && threadIdx.x == 0) p.header[0] = p.header[0] + 1;
+}
+
+// Batched step over R requests (one state each, batch 1): request r's token
+// rows are batch row r of the operands, its buffers come from the device
+// table, its cursor from its header[0] and its route size from header[1].
+// Local workgroup 0 of each (request, head) leaves M and coarse_on in its
+// record for kernel B, whose workgroup (request, head 0, chunk 0) advances
+// header[0].
+template <int D>
+__global__ __launch_bounds__(kThreads) void batch_units_kernel(BatchStepParams p) {
+  using G = Geo<D>;
+  __shared__ StepSmem<D> sm;
+  const int per_head = G::NLOC + G::NFINE * (p.coarse_values ? 2 : 1);
+  const int rh = blockIdx.x / per_head;
+  const int j = blockIdx.x % per_head;
+  const int r = rh / p.H, h = rh % p.H;
+  const BatchReq& t = p.table[r];
+  StepReq q;
+  q.q = p.q.p + r * p.q.sb + h * p.q.sh;
+  q.k = p.k.p + r * p.k.sb + h * p.k.sh;
+  q.v = p.v.p + r * p.v.sb + h * p.v.sh;
+  q.rq = p.rq.p + r * p.rq.sb + h * p.rq.sh;
+  q.rk = p.rk.p + r * p.rk.sb + h * p.rk.sh;
+  q.ring_k = t.ring_k + (size_t)h * D;
+  q.ring_v = t.ring_v + (size_t)h * D;
+  q.ring_raw = t.ring_raw + (size_t)h * D;
+  q.fold_g = t.fold_g + (size_t)h * D * D;
+  q.fold_den = t.fold_den + (size_t)h * D;
+  q.coarse_g = t.coarse_g ? t.coarse_g + (size_t)h * D * D : nullptr;
+  q.recs = t.parts + (size_t)h * step_floats(D, 0);
+  q.position = t.header[0];
+  const long long fines = fines_before(q.position, p.keep, p.fine);
+  const int M = fines > 0 ? (int)t.header[1] : 0;
+  const int coarse_on = q.coarse_g != nullptr && fines >= p.group;
+  if (j == 0 && threadIdx.x == 0) {
+    q.recs[2] = (float)M;
+    q.recs[3] = (float)coarse_on;
+  }
+  units_body<D>(q, j, M, coarse_on, p.keep, p.fine, p.H * D, sm);
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void batch_combine_kernel(BatchStepParams p) {
+  constexpr int CHUNKS = D / kCombineCols;
+  const int rh = blockIdx.x / CHUNKS;
+  const int chunk = blockIdx.x % CHUNKS;
+  const int r = rh / p.H, h = rh % p.H;
+  const BatchReq& t = p.table[r];
+  const float* recs = t.parts + (size_t)h * step_floats(D, 0);
+  const int M = (int)recs[2];
+  const int coarse_on = recs[3] != 0.0f;
+  const CombineArgs c = {p.fa, p.fb, p.f_dtype, p.fa_s, p.fb_s, p.gain};
+  combine_body<D>(recs, p.rq.p + r * p.rq.sb + h * p.rq.sh, p.out + r * p.out_sb + h * p.out_sh,
+                  h, chunk, M, coarse_on, c);
+  if (h == 0 && chunk == 0 && threadIdx.x == 0) t.header[0] = t.header[0] + 1;
 }
 
 // Fold: one workgroup per (batch, head, ROWS rows of G^T). Thread (row r,
@@ -441,6 +544,24 @@ hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStr
   } else if (head_dim == 64) {
     hipLaunchKernelGGL(decode_units_kernel<64>, units, dim3(kThreads), 0, s, p, M);
     hipLaunchKernelGGL(decode_combine_kernel<64>, cols, dim3(kThreads), 0, s, p, M);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_batch_step(const BatchStepParams& p, int head_dim, hipStream_t s) {
+  if (p.R <= 0) return hipSuccess;
+  if (p.keep + p.fine > kMaxWindow) return hipErrorInvalidValue;
+  const int per_head = local_units(head_dim) + fine_units(head_dim) * (p.coarse_values ? 2 : 1);
+  const dim3 units((unsigned)(p.R * p.H * per_head));
+  const dim3 cols((unsigned)(p.R * p.H * (head_dim / kCombineCols)));
+  if (head_dim == 128) {
+    hipLaunchKernelGGL(batch_units_kernel<128>, units, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL(batch_combine_kernel<128>, cols, dim3(kThreads), 0, s, p);
+  } else if (head_dim == 64) {
+    hipLaunchKernelGGL(batch_units_kernel<64>, units, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL(batch_combine_kernel<64>, cols, dim3(kThreads), 0, s, p);
   } else {
     return hipErrorInvalidValue;
   }

@@ -12,6 +12,7 @@
 // Every count is a closed form of the cursor (the same formulas as the
 // Python host's schedule module).
 #include <cstring>
+#include <vector>
 
 #include "schedule.h"
 #include "tao_launch.h"
@@ -70,6 +71,99 @@ void drop_graph(Stream* s) {
   s->graph_selected = -1;
 }
 
+// Route refresh due at the stream's cursor (before its decode step).
+int pre_step(Stream* s, const tao_tokens* tok, void* stream, int* refreshed) {
+  const tao_stream_cfg& c = s->cfg;
+  const int64_t pos = s->position;
+  const int64_t fines = fines_at(c, pos);
+  *refreshed = 0;
+  if (fines > 0 && is_turn(c, pos)) {
+    const int64_t completed = fines / c.coarse_group, pending = fines % c.coarse_group;
+    int64_t coarse64 = 0, eligible = 0, selected64 = 0;
+    tao::sched::routed_counts(c, completed, pending, &coarse64, &eligible, &selected64);
+    const int32_t coarse = (int32_t)coarse64, selected = (int32_t)selected64;
+    const int64_t rq_s[2] = {tok->rq_s[0], tok->rq_s[2]};
+    int rc = tao_route(&s->st, tok->raw_q, rq_s, (int32_t)completed, (int32_t)pending, coarse,
+                       selected, stream);
+    if (!rc) rc = tao_fold_route(&s->st, selected, stream);
+    if (rc) return rc;
+    s->route_coarse = coarse;
+    s->route_size = selected;
+    *refreshed = 1;
+  }
+  return TAO_OK;
+}
+
+// Seal due after the step at the stream's cursor; advances the cursor.
+int post_step(Stream* s, const tao_tokens* tok, void* stream, int* sealed) {
+  const tao_stream_cfg& c = s->cfg;
+  const int64_t pos = s->position;
+  const int64_t fines = fines_at(c, pos);
+  const int64_t limit = c.local_keep + c.fine_tokens;
+  *sealed = 0;
+  if (local_len_at(c, pos) + 1 == limit) {
+    s->seal_host = pos + 1 - limit;
+    hipError_t e = hipMemcpyAsync(s->seal_start, &s->seal_host, sizeof(int64_t),
+                                  hipMemcpyHostToDevice, (hipStream_t)stream);
+    if (e != hipSuccess) return stream_fail((int)e, "seal start upload");
+    int rc = tao_write_fine(&s->st, tok, pos + 1, s->seal_start, (int32_t)fines, 1, stream);
+    if (!rc) rc = tao_seal_epilogue(&s->st, (int32_t)fines,
+                                    (int32_t)(fines / c.coarse_group + 1), 1, stream);
+    // New page weights and segment weights: refold the current route.
+    if (!rc) rc = tao_fold_route(&s->st, s->route_size, stream);
+    // A completed page: its value matrix, then the coarse read over all pages.
+    if (!rc && s->st.page_c && fines % c.coarse_group == c.coarse_group - 1) {
+      const int32_t page = (int32_t)(fines / c.coarse_group);
+      rc = tao_page_coarse(&s->st, page, 1, stream);
+      if (!rc) rc = tao_fold_coarse(&s->st, page + 1, stream);
+    }
+    if (rc) return rc;
+    *sealed = 1;
+  }
+  s->position = pos + 1;
+  return TAO_OK;
+}
+
+struct Batch {
+  std::vector<Stream*> reqs;
+  std::vector<tao::BatchReq> host_table;   // staging of the device table upload
+  tao::BatchReq* table = nullptr;          // caller's device memory
+  int heads = 0, head_dim = 0, keep = 0, fine = 0, group = 0, coarse_values = 0;
+};
+
+int fill_table(Batch* b, void* stream) {
+  for (size_t r = 0; r < b->reqs.size(); ++r) {
+    const tao_state_dev& st = b->reqs[r]->st;
+    const tao::WorkspaceLayout lay =
+        tao::workspace_layout(st.batch, st.heads, st.head_dim, st.sel_cap, 0);
+    tao::BatchReq& t = b->host_table[r];
+    t.ring_k = (bf16_t*)st.ring_k;
+    t.ring_v = (bf16_t*)st.ring_v;
+    t.ring_raw = (bf16_t*)st.ring_raw;
+    t.fold_g = (const float*)st.fold_g;
+    t.fold_den = (const float*)st.fold_den;
+    t.coarse_g = (const float*)st.coarse_g;
+    t.header = st.header;
+    t.parts = (float*)((char*)st.workspace + lay.parts_off);
+  }
+  const hipError_t e = hipMemcpyAsync(b->table, b->host_table.data(),
+                                      b->host_table.size() * sizeof(tao::BatchReq),
+                                      hipMemcpyHostToDevice, (hipStream_t)stream);
+  return e == hipSuccess ? TAO_OK : stream_fail((int)e, "batch table upload");
+}
+
+// Batch row r of the call's operands as a one-request token view.
+tao_tokens row_tokens(const tao_tokens* tok, int r) {
+  tao_tokens t = *tok;
+  t.q = (const bf16_t*)tok->q + r * tok->q_s[0];
+  t.k = (const bf16_t*)tok->k + r * tok->k_s[0];
+  t.v = (const bf16_t*)tok->v + r * tok->v_s[0];
+  t.raw_q = (const bf16_t*)tok->raw_q + r * tok->rq_s[0];
+  t.raw_k = (const bf16_t*)tok->raw_k + r * tok->rk_s[0];
+  t.tokens = 1;
+  return t;
+}
+
 }  // namespace
 
 extern "C" {
@@ -119,22 +213,9 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
   const tao_stream_cfg& c = s->cfg;
   const int64_t pos = s->position;
   const int64_t fines = fines_at(c, pos);
-  int rc = TAO_OK;
   int refreshed = 0, sealed = 0;
-  if (fines > 0 && is_turn(c, pos)) {
-    const int64_t completed = fines / c.coarse_group, pending = fines % c.coarse_group;
-    int64_t coarse64 = 0, eligible = 0, selected64 = 0;
-    tao::sched::routed_counts(c, completed, pending, &coarse64, &eligible, &selected64);
-    const int32_t coarse = (int32_t)coarse64, selected = (int32_t)selected64;
-    const int64_t rq_s[2] = {tok->rq_s[0], tok->rq_s[2]};
-    rc = tao_route(&s->st, tok->raw_q, rq_s, (int32_t)completed, (int32_t)pending, coarse,
-                   selected, stream);
-    if (!rc) rc = tao_fold_route(&s->st, selected, stream);
-    if (rc) return rc;
-    s->route_coarse = coarse;
-    s->route_size = selected;
-    refreshed = 1;
-  }
+  int rc = pre_step(s, tok, stream, &refreshed);
+  if (rc) return rc;
   const int32_t selected = fines > 0 ? s->route_size : 0;
   const bool coarse_values = s->st.page_c != nullptr;
   tao_fusion f = *fu;
@@ -156,27 +237,8 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
     rc = tao::decode_step_at(&s->st, tok, &f, selected, out, out_s, stream, pos);
   }
   if (rc) return rc;
-  const int64_t limit = c.local_keep + c.fine_tokens;
-  if (local_len_at(c, pos) + 1 == limit) {
-    s->seal_host = pos + 1 - limit;
-    hipError_t e = hipMemcpyAsync(s->seal_start, &s->seal_host, sizeof(int64_t),
-                                  hipMemcpyHostToDevice, (hipStream_t)stream);
-    if (e != hipSuccess) return stream_fail((int)e, "seal start upload");
-    rc = tao_write_fine(&s->st, tok, pos + 1, s->seal_start, (int32_t)fines, 1, stream);
-    if (!rc) rc = tao_seal_epilogue(&s->st, (int32_t)fines,
-                                    (int32_t)(fines / c.coarse_group + 1), 1, stream);
-    // New page weights and segment weights: refold the current route.
-    if (!rc) rc = tao_fold_route(&s->st, s->route_size, stream);
-    // A completed page: its value matrix, then the coarse read over all pages.
-    if (!rc && coarse_values && fines % c.coarse_group == c.coarse_group - 1) {
-      const int32_t page = (int32_t)(fines / c.coarse_group);
-      rc = tao_page_coarse(&s->st, page, 1, stream);
-      if (!rc) rc = tao_fold_coarse(&s->st, page + 1, stream);
-    }
-    if (rc) return rc;
-    sealed = 1;
-  }
-  s->position = pos + 1;
+  rc = post_step(s, tok, stream, &sealed);
+  if (rc) return rc;
   info[0] = s->position;
   info[1] = s->route_coarse;
   info[2] = s->route_size;
@@ -184,6 +246,138 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
   info[4] = sealed;
   info[5] = used_graph;
   info[6] = captured;
+  return TAO_OK;
+}
+
+size_t tao_batch_table_bytes(int32_t count) {
+  return count > 0 ? (size_t)count * sizeof(tao::BatchReq) : 0;
+}
+
+int tao_batch_open(void* const* handles, int32_t count, void* table, size_t table_bytes,
+                   void* stream, void** batch) {
+  if (!handles || count <= 0 || !table || !batch)
+    return stream_fail(TAO_E_ARGUMENT, "null batch argument");
+  if (table_bytes < tao_batch_table_bytes(count))
+    return stream_fail(TAO_E_WORKSPACE, "batch table smaller than tao_batch_table_bytes()");
+  Batch* b = new Batch();
+  for (int32_t r = 0; r < count; ++r) {
+    Stream* s = (Stream*)handles[r];
+    if (!s) {
+      delete b;
+      return stream_fail(TAO_E_ARGUMENT, "null stream in the batch");
+    }
+    const tao_state_dev& st = s->st;
+    const char* why = nullptr;
+    if (st.batch != 1) why = "batched decode takes states of batch 1";
+    else if (!b->reqs.empty()) {
+      const tao_state_dev& f = b->reqs[0]->st;
+      const tao_stream_cfg& c0 = b->reqs[0]->cfg;
+      if (st.heads != f.heads || st.head_dim != f.head_dim || st.local_keep != f.local_keep ||
+          st.fine_tokens != f.fine_tokens || st.coarse_group != f.coarse_group ||
+          (st.page_c == nullptr) != (f.page_c == nullptr) ||
+          s->cfg.local_keep != c0.local_keep || s->cfg.fine_tokens != c0.fine_tokens)
+        why = "batched states must share heads, head width, geometry and coarse branch";
+      for (Stream* o : b->reqs)
+        if (o == s) why = "a state appears twice in the batch";
+    }
+    if (why) {
+      delete b;
+      return stream_fail(TAO_E_ARGUMENT, why);
+    }
+    b->reqs.push_back(s);
+  }
+  const tao_state_dev& f = b->reqs[0]->st;
+  b->heads = f.heads;
+  b->head_dim = f.head_dim;
+  b->keep = f.local_keep;
+  b->fine = f.fine_tokens;
+  b->group = f.coarse_group;
+  b->coarse_values = f.page_c != nullptr;
+  b->table = (tao::BatchReq*)table;
+  b->host_table.resize(count);
+  const int rc = fill_table(b, stream);
+  if (rc) {
+    delete b;
+    return rc;
+  }
+  *batch = b;
+  return TAO_OK;
+}
+
+int tao_batch_sync(void* batch, void* stream) {
+  if (!batch) return stream_fail(TAO_E_ARGUMENT, "null batch");
+  Batch* b = (Batch*)batch;
+  // Host staging may still be read by the previous upload: wait for it.
+  if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess)
+    return stream_fail(TAO_E_ARGUMENT, "batch sync: stream error");
+  return fill_table(b, stream);
+}
+
+int tao_batch_decode(void* batch, const tao_tokens* tok, const tao_fusion* fu, void* out,
+                     const int64_t* out_s, void* stream, int64_t* info) {
+  if (!batch || !tok || !fu || !out || !out_s || !info)
+    return stream_fail(TAO_E_ARGUMENT, "null batch decode argument");
+  Batch* b = (Batch*)batch;
+  const int R = (int)b->reqs.size();
+  if (tok->tokens != 1) return stream_fail(TAO_E_SHAPE, "batched decode takes one token per request");
+  if (!tok->q || !tok->k || !tok->v || !tok->raw_q || !tok->raw_k)
+    return stream_fail(TAO_E_ARGUMENT, "null token operand");
+  if (!fu->fusion_a || !fu->fusion_b || (fu->dtype != TAO_BF16 && fu->dtype != TAO_FP32))
+    return stream_fail(TAO_E_ARGUMENT, "invalid fusion parameters");
+  for (int r = 0; r < R; ++r) {
+    Stream* s = b->reqs[r];
+    const tao_tokens t = row_tokens(tok, r);
+    int refreshed = 0;
+    const int rc = pre_step(s, &t, stream, &refreshed);
+    if (rc) return rc;
+    info[4 * r] = refreshed;
+  }
+  tao::BatchStepParams p;
+  auto view = [](const void* ptr, const int64_t* st) {
+    tao::TokView v;
+    v.p = (const bf16_t*)ptr;
+    v.sb = st[0];
+    v.st = st[1];
+    v.sh = st[2];
+    return v;
+  };
+  p.q = view(tok->q, tok->q_s);
+  p.k = view(tok->k, tok->k_s);
+  p.v = view(tok->v, tok->v_s);
+  p.rq = view(tok->raw_q, tok->rq_s);
+  p.rk = view(tok->raw_k, tok->rk_s);
+  p.fa = fu->fusion_a;
+  p.fb = fu->fusion_b;
+  p.f_dtype = fu->dtype;
+  for (int i = 0; i < 3; ++i) { p.fa_s[i] = fu->a_s[i]; p.fb_s[i] = fu->b_s[i]; }
+  p.gain = fu->gain;
+  p.out = (bf16_t*)out;
+  p.out_sb = out_s[0];
+  p.out_sh = out_s[2];
+  p.table = b->table;
+  p.R = R;
+  p.H = b->heads;
+  p.keep = b->keep;
+  p.fine = b->fine;
+  p.group = b->group;
+  p.coarse_values = b->coarse_values;
+  const hipError_t e = tao::launch_batch_step(p, b->head_dim, (hipStream_t)stream);
+  if (e != hipSuccess) return stream_fail((int)e, "batched decode step launch");
+  for (int r = 0; r < R; ++r) {
+    Stream* s = b->reqs[r];
+    const tao_tokens t = row_tokens(tok, r);
+    int sealed = 0;
+    const int rc = post_step(s, &t, stream, &sealed);
+    if (rc) return rc;
+    info[4 * r + 1] = sealed;
+    info[4 * r + 2] = s->route_coarse;
+    info[4 * r + 3] = s->route_size;
+  }
+  return TAO_OK;
+}
+
+int tao_batch_close(void* batch) {
+  delete (Batch*)batch;
   return TAO_OK;
 }
 

@@ -104,6 +104,13 @@ TAO_DEV int local_len_at(long long position, int keep, int fine) {
   return keep + (int)((position - limit) % fine);
 }
 
+// Sealed fine memories before the token at `position` (the window seals
+// its oldest `fine` tokens each time it reaches keep + fine).
+TAO_DEV long long fines_before(long long position, int keep, int fine) {
+  const long long limit = keep + fine;
+  return position < limit ? 0 : (position - limit) / fine + 1;
+}
+
 // Page descriptor of n <= 8 fine descriptors of one channel: torch's bf16
 // logsumexp composite r(r(log r(sum r(exp r(z - m)))) + m), butterfly sum,
 // infinite maximum replaced by 0 (tao_stream.py:283, 412, 485).

@@ -84,6 +84,28 @@ struct DecodeParams {
 // coarse_on the step also reads the folded coarse matrix (launch_coarse_fold).
 hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStream_t s);
 
+// Batched decode step over R requests of one layer (each state batch 1):
+// per-request buffers in a device table; cursor and route size read from
+// each request's header[0] / header[1].
+struct BatchReq {
+  bf16_t* ring_k; bf16_t* ring_v; bf16_t* ring_raw;
+  const float* fold_g; const float* fold_den; const float* coarse_g;   // coarse_g may be null
+  int64_t* header;
+  float* parts;
+};
+
+struct BatchStepParams {
+  TokView q, k, v, rq, rk;       // [R, 1, H, D]: request r = batch row r
+  const void* fa; const void* fb; int f_dtype;
+  int64_t fa_s[3], fb_s[3];
+  float gain;
+  bf16_t* out; int64_t out_sb, out_sh;
+  const BatchReq* table;
+  int R, H, keep, fine, group;
+  int coarse_values;             // the states carry the coarse value branch
+};
+hipError_t launch_batch_step(const BatchStepParams& p, int head_dim, hipStream_t s);
+
 struct FoldParams {
   const bf16_t* bank; const bf16_t* sw; const bf16_t* pw;
   const int32_t* sel;

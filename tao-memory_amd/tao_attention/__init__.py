@@ -5,9 +5,9 @@ signatures); the compute runs in the gfx950 HIP library libtao_hip.so.
 """
 
 from .operator import (new_state, tao_attention, tao_attention_decode,
-                       tao_attention_prefill)
+                       tao_attention_decode_batch, tao_attention_prefill)
 from .tao_stream import StreamCache
 from .config import TaoConfig
 
 __all__ = ["new_state", "tao_attention", "tao_attention_prefill",
-           "tao_attention_decode", "StreamCache", "TaoConfig"]
+           "tao_attention_decode", "tao_attention_decode_batch", "StreamCache", "TaoConfig"]

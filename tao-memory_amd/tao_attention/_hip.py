@@ -103,6 +103,12 @@ _SIGNATURES = {
     "tao_graph_launch": ([_vp, ctypes.POINTER(Tokens), _vp], _i32),
     "tao_graph_destroy": ([_vp], _i32),
     "tao_numerics_selftest": ([_i32, _vp, _vp, _i64, _vp], _i32),
+    "tao_batch_table_bytes": ([_i32], _sz),
+    "tao_batch_open": ([ctypes.POINTER(_vp), _i32, _vp, _sz, _vp, ctypes.POINTER(_vp)], _i32),
+    "tao_batch_sync": ([_vp, _vp], _i32),
+    "tao_batch_decode": ([_vp, ctypes.POINTER(Tokens), ctypes.POINTER(Fusion), _vp,
+                          ctypes.POINTER(_i64), _vp, ctypes.POINTER(_i64)], _i32),
+    "tao_batch_close": ([_vp], _i32),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -62,3 +62,28 @@ def tao_attention_decode(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b,
     _check_plugin(local_flash)
     out = state.decode(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
     return out, state
+
+
+_BATCHES = {}
+
+
+def tao_attention_decode_batch(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b, alpha, states):
+    """One new token for each of len(states) independent requests of one layer.
+
+    No reference counterpart (the reference decodes one request per
+    tao_attention_decode call, operator.py:130-138); the outputs and states
+    equal that loop's. q / k / v / raw_q / raw_k: [R, 1, H, D] with request r
+    in batch row r; every state is a one-request state at its own cursor.
+    Returns ([R, 1, H, D], states).
+    """
+    from .tao_stream import DecodeBatch
+    states = list(states)
+    if not states:
+        raise ValueError("states must hold at least one request state")
+    key = tuple(id(s) for s in states)
+    batch = _BATCHES.get(key)
+    if batch is None or any(a is not b for a, b in zip(batch.states, states)):
+        batch = DecodeBatch(states)
+        _BATCHES.clear()
+        _BATCHES[key] = batch
+    return batch.decode(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha), states

@@ -60,6 +60,7 @@ class _DeviceState:
         self.coarse_g = (torch.zeros((batch, heads, head_dim, head_dim), dtype=torch.float32,
                                      device=device) if self.coarse_values else None)
         self.page_c = None
+        self.generation = 0          # bumped whenever the buffers move
         self.fine_cap = 0
         self._allocate(fine_cap, copy_fines=0)
 
@@ -97,6 +98,7 @@ class _DeviceState:
         self.bank, self.fine_z, self.fine_sw = bank, fine_z, fine_sw
         self.page_z, self.page_w, self.sel, self.chosen = page_z, page_w, sel, chosen
         self.page_c = page_c
+        self.generation += 1
         self.fine_cap, self.page_cap, self.sel_cap, self.chosen_cap = (
             fine_cap, page_cap, sel_cap, chosen_cap)
         self.plan_words = 0
@@ -106,6 +108,7 @@ class _DeviceState:
         ws_bytes = _hip.lib().tao_workspace_bytes(self.B, self.H, self.D, self.sel_cap,
                                                   plan_words)
         self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=self.device)
+        self.generation += 1
         self.plan_words = plan_words
         self.struct = self._make_struct()
         _hip.check(_hip.lib().tao_workspace_init(ctypes.byref(self.struct), self.stream()))
@@ -776,6 +779,7 @@ class StreamCache:
             state.route_size = selected.shape[-1]
             dev.sel[:, :, :state.route_size].copy_(selected[:, 0].to(torch.int32))
             dev.chosen[:, :, :state.route_coarse].copy_(chosen[:, 0].to(torch.int32))
+            dev.header[1:2].fill_(state.route_size)
         state.position = position
         dev.header[0:1].fill_(position)
         state.route_refreshes = saved["route_refreshes"]
@@ -811,3 +815,105 @@ class StreamCache:
                 "fusion_pointwise_calls": self.fusion_pointwise_calls,
                 "fusion_no_history_local_returns": self.fusion_no_history_local_returns,
                 "fine_matrix_repack_bytes": 0}
+
+
+class DecodeBatch:
+    """Native batched decode over independent one-request states of one
+    layer (tao_batch_*): one new token per state per call, the per-request
+    route refreshes and seals as each cursor requires, and one decode step
+    launch pair for all. No reference counterpart: the reference decodes one
+    request per call (tao_attention_decode); the results are the same.
+    """
+
+    def __init__(self, states):
+        self.states = list(states)
+        self._handle = None
+        self._table = None
+        self._key = None
+        self._gens = None
+        self._info = (ctypes.c_int64 * (4 * len(self.states)))()
+
+    def close(self):
+        if self._handle is not None:
+            _hip.lib().tao_batch_close(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _bind(self, q):
+        """Device state and driver of every request; (re)open or sync the
+        native batch when a driver was recreated or buffers moved."""
+        first = self.states[0]
+        for r, st in enumerate(self.states):
+            row = q[r:r + 1]
+            st._check_supported(row)
+            if (st.config.coarse_index_only != first.config.coarse_index_only
+                    or st.config.local_keep != first.config.local_keep
+                    or st.config.fine_tokens != first.config.fine_tokens
+                    or st.config.coarse_group != first.config.coarse_group):
+                raise ValueError("batched states must share the coarse branch and geometry")
+            dev = st._device_for(row, st.position + 1)
+            if dev.B != 1:
+                raise ValueError("batched decode takes one-request states (batch 1)")
+            st._driver(dev)
+        key = tuple((id(st), st._handle.value) for st in self.states)
+        gens = tuple(st._dev.generation for st in self.states)
+        lib = _hip.lib()
+        stream = self.states[0]._dev.stream()
+        if self._handle is None or key != self._key:
+            self.close()
+            nbytes = lib.tao_batch_table_bytes(len(self.states))
+            self._table = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+            handles = (ctypes.c_void_p * len(self.states))(
+                *[st._handle.value for st in self.states])
+            handle = ctypes.c_void_p()
+            _hip.check(lib.tao_batch_open(handles, len(self.states), self._table.data_ptr(),
+                                          nbytes, stream, ctypes.byref(handle)))
+            self._handle, self._key, self._gens = handle, key, gens
+        elif gens != self._gens:
+            _hip.check(lib.tao_batch_sync(self._handle, stream))
+            self._gens = gens
+
+    def decode(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
+        """One token for each request: operands [R, 1, H, D]; returns [R, 1, H, D]."""
+        R = len(self.states)
+        shape = q.shape
+        if len(shape) != 4 or shape[0] != R or shape[1] != 1:
+            raise ValueError("batched decode takes [len(states), 1, H, D] operands")
+        if (k.shape, v.shape, raw_q.shape, raw_k.shape) != (shape, shape, shape, shape):
+            raise ValueError("q, k, v, raw_q and raw_k must share one [R, 1, H, D] shape")
+        for x in (k, v, raw_q, raw_k):
+            if x.dtype != q.dtype or x.device != q.device:
+                raise TypeError("q, k, v, raw_q and raw_k must share dtype and device")
+        if len({id(st) for st in self.states}) != R:
+            raise ValueError("a state appears twice in the batch")
+        q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
+        self._bind(q)
+        tok = _hip.tokens(q, k, v, raw_q, raw_k)
+        fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
+        out = torch.empty_like(q)
+        out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
+        info = self._info
+        _hip.check(_hip.lib().tao_batch_decode(
+            self._handle, ctypes.byref(tok), ctypes.byref(fu), out.data_ptr(), out_s,
+            self.states[0]._dev.stream(), info))
+        for r, st in enumerate(self.states):
+            pos = st.position
+            st.position = pos + 1
+            refreshed, sealed = info[4 * r], info[4 * r + 1]
+            if pos >= st._first_fine:
+                st.fusion_pointwise_calls += 1
+            else:
+                st.fusion_no_history_local_returns += 1
+            if refreshed:
+                st.route_refreshes += 1
+                st.peak_selected_fine = max(st.peak_selected_fine, info[4 * r + 3])
+            if refreshed or sealed:
+                st.route_coarse, st.route_size = info[4 * r + 2], info[4 * r + 3]
+            if sealed:
+                st.fine_seal_events += 1
+        return out

@@ -283,3 +283,55 @@ def test_exp_log_exhaustive_over_bf16(device, op):
     both_nan = torch.isnan(got) & torch.isnan(ref)
     same = (got == ref) | both_nan
     assert same.all(), x[~same][:8]
+
+
+@pytest.mark.parametrize("coarse", [False, True])
+def test_batched_decode_equals_per_request(device, coarse):
+    """tao_attention_decode_batch == tao_attention_decode per request, bitwise:
+    requests at different cursors (local-only, across a seal and refreshes,
+    across the first page completion at 2560) and layers."""
+    from tao_attention import TaoConfig, tao_attention_decode_batch
+    heads, width, steps = 2, 64, 40
+    lengths, layers = [700, 1270, 2550], [0, 1, 3]
+    cfg = TaoConfig() if coarse else index_only_page_memo()
+    fa, fb = (torch.randn(heads, width, 3, generator=torch.Generator().manual_seed(9)) * 0.02
+              for _ in range(2))
+    fa, fb = fa.to(device), fb.to(device)
+    xs = [to_dev(inputs(n + steps, heads, width, seed=20 + r)[0], device)
+          for r, n in enumerate(lengths)]
+    print(f"batched decode coarse={coarse}", flush=True)
+
+    def prefilled():
+        out = []
+        for x, n, layer in zip(xs, lengths, layers):
+            st = new_state(layer, cfg)
+            q, k, v, rq, rk = (t[:, :n] for t in x)
+            tao_attention_prefill(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa, fusion_b=fb,
+                                  alpha=0.5, state=st, position=0)
+            out.append(st)
+        return out
+
+    batched, single = prefilled(), prefilled()
+    for t in range(steps):
+        rows = [[x[i][:, n + t:n + t + 1] for i in range(5)] for x, n in zip(xs, lengths)]
+        q, k, v, rq, rk = (torch.cat([row[i] for row in rows], 0) for i in range(5))
+        got, _ = tao_attention_decode_batch(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa,
+                                            fusion_b=fb, alpha=0.5, states=batched)
+        for r, st in enumerate(single):
+            want, _ = tao_attention_decode(*rows[r][:3], raw_q=rows[r][3], raw_k=rows[r][4],
+                                           fusion_a=fa, fusion_b=fb, alpha=0.5, state=st,
+                                           position=st.get_pos())
+            assert torch.equal(got[r:r + 1], want), (t, r)
+    for a, b in zip(batched, single):
+        sa, sb = a.export(), b.export()
+        assert sa["position"] == sb["position"]
+        for key in ("route_refreshes", "fine_seal_events", "state_version"):
+            assert sa[key] == sb[key], key
+        for x, y in zip(sa["local"], sb["local"]):
+            assert torch.equal(x, y)
+        if sb["packed_fine_c"] is not None:
+            assert torch.equal(sa["packed_fine_c"], sb["packed_fine_c"])
+            assert torch.equal(sa["route_ids"][1], sb["route_ids"][1])
+        for (pz, pc, fz), (qz, qc, gz) in zip(sa["pages"], sb["pages"]):
+            assert torch.equal(pz, qz) and torch.equal(fz, gz)
+            assert (pc is None and qc is None) or torch.equal(pc, qc)

@@ -7,7 +7,8 @@ time (the timed region includes route refreshes and
 the seal). Each step is issued by the native C++ driver as direct kernel
 launches, which on ROCm costs the host less than a hipGraphLaunch; the
 hipGraph preset is timed on the same steps and reported as decode_graph. Also reported: prefill tokens/s of a
-16384-token prompt through tao_attention_prefill, a cold-cache
+16384-token prompt through tao_attention_prefill, batched
+streaming decode of 32 ragged requests (configs[4], decode_batch), a cold-cache
 decode variant that cycles 8 independent 128K states (> 4 GB working set,
 beyond the 256 MB Infinity Cache), the roofline of the dominant kernels
 measured live with HIP events on the launch stream, and the CPU oracle
@@ -267,6 +268,84 @@ def run_cold(torch, args, device, cfg, heads, width, context, n_states, probe):
     return steps, t1 - t0, sel
 
 
+def run_batch(torch, args, device, cfg, heads, width, probe):
+    """R one-request states at ragged lengths U[16384, 32768]
+    (seeded), writer-only; `batch_steps` batched single-token steps
+    (tao_attention_decode_batch, one decode step launch pair for all R plus
+    the refreshes and seals the cursors hit). Also times the per-request
+    loop (tao_attention_decode) on the same states for comparison."""
+    import numpy as np
+    from tao_attention import new_state, tao_attention_decode, tao_attention_decode_batch
+    R, steps, warm = args.batch_requests, args.batch_steps, 4
+    lengths = np.random.RandomState(5).randint(16384, 32769, size=R).tolist()
+    g = torch.Generator(device=device).manual_seed(11)
+    states = []
+    for r, n in enumerate(lengths):
+        st = new_state(0, cfg)
+        xs = [torch.randn((1, n, heads, width), generator=g, device=device).to(torch.bfloat16)
+              for _ in range(5)]
+        st._ingest(*xs)
+        del xs
+        states.append(st)
+    total = warm + steps + 2 * 8
+    toks = [torch.randn((R, total, heads, width), generator=g, device=device).to(torch.bfloat16)
+            for _ in range(5)]
+    fa = torch.randn((heads, width, 3), generator=g, device=device) * 0.02
+    fb = torch.randn((heads, width, 3), generator=g, device=device) * 0.02
+    torch.cuda.synchronize()
+    log(f"batch: {R} states built, lengths {min(lengths)}..{max(lengths)}")
+
+    def step(t):
+        q, k, v, rq, rk = (x[:, t:t + 1] for x in toks)
+        return tao_attention_decode_batch(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa,
+                                          fusion_b=fb, alpha=0.5, states=states)[0]
+
+    for t in range(warm):
+        step(t)
+    bytes_per_step = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(warm, warm + steps):
+        bytes_per_step.append(sum(decode_bytes(cfg, heads, width, st.route_size, st.get_pos())[0]
+                                  for st in states))
+        step(t)
+    torch.cuda.synchronize()
+    seconds = time.perf_counter() - t0
+    # Device time per batched step, GPU pre-loaded (see run_decode).
+    groups = []
+    t = warm + steps
+    for _ in range(2):
+        torch.cuda._sleep(SPIN_CYCLES)
+        start = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(4):
+            step(t)
+            t += 1
+        end = torch.cuda.Event(enable_timing=True)
+        end.record()
+        groups.append((start, end, 4))
+    torch.cuda.synchronize()
+    probe.events["batch_step"] = groups
+    # The per-request loop on the same states (one tao_attention_decode each).
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    loop_steps = 8
+    for _ in range(loop_steps):
+        q, k, v, rq, rk = (x[:, t:t + 1] for x in toks)
+        for r, st in enumerate(states):
+            tao_attention_decode(q[r:r + 1], k[r:r + 1], v[r:r + 1], raw_q=rq[r:r + 1],
+                                 raw_k=rk[r:r + 1], fusion_a=fa, fusion_b=fb, alpha=0.5,
+                                 state=st, position=st.get_pos())
+        t += 1
+    torch.cuda.synchronize()
+    loop_seconds = time.perf_counter() - t1
+    for st in states:
+        st.release_execution()
+    return {"requests": R, "lengths": [min(lengths), max(lengths)], "steps": steps,
+            "seconds": seconds, "bytes_per_step": sum(bytes_per_step) / len(bytes_per_step),
+            "loop_tok_s": R * loop_steps / loop_seconds}
+
+
 def run_prefill(torch, device, cfg, heads, width, tokens, probe):
     from tao_attention import new_state, schedule, tao_attention_prefill
     from tao_attention.presets import index_only_page_memo
@@ -365,6 +444,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cold", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--batch-requests", type=int, default=32)
+    ap.add_argument("--batch-steps", type=int, default=128)
+    ap.add_argument("--no-batch", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB 4 times (a plain "
                          "copy kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -460,6 +542,27 @@ def main():
             "attention_ms": round(attn_ms, 4), "writer_ms": round(writer_ms, 4),
             "algorithmic_gflop": round(flops / 1e9, 2)}
         log(f"prefill: {result['prefill_tokens_per_s']} tok/s, mfma {tflops:.1f} TFLOP/s")
+    if not args.no_batch:
+        log("batched decode: building states")
+        bt = run_batch(torch, args, device, cfg, heads, width, probe)
+        b_ms = probe.total_ms("batch_step") / max(probe.count("batch_step"), 1)
+        b_tok_s = bt["requests"] * bt["steps"] / bt["seconds"]
+        b_achieved = bt["bytes_per_step"] / (b_ms * 1e-3) / 1e9
+        result["decode_batch"] = {
+            "workload": "configs[4]: %d one-request states (lengths U[16384,32768], seed 5; "
+                        "%d..%d), H32 D128, index_only_page_memo; %d batched single-token "
+                        "steps through tao_attention_decode_batch" % (
+                            bt["requests"], bt["lengths"][0], bt["lengths"][1], bt["steps"]),
+            "tok_s": round(b_tok_s, 1),
+            "ms_per_step": round(bt["seconds"] / bt["steps"] * 1e3, 4),
+            "kernel_us_per_step": round(b_ms * 1e3, 2),
+            "achieved_GBs": round(b_achieved, 1),
+            "frac": round(b_achieved / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes_per_step": int(bt["bytes_per_step"]),
+            "algorithmic_basis": "sum over requests of the reference step (as roofline)",
+            "per_request_loop_tok_s": round(bt["loop_tok_s"], 1)}
+        log(f"batched decode: {b_tok_s:.1f} tok/s, step {b_ms * 1e3:.1f} us, "
+            f"{b_achieved:.0f} GB/s; per-request loop {bt['loop_tok_s']:.1f} tok/s")
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, torch eager on host cores)")
         xs_cpu, _, _ = make_tokens(torch, 1 + 3 * args.cpu_steps, heads, width, 7, device)

@@ -442,10 +442,10 @@ __global__ __launch_bounds__(kThreads) void batch_combine_kernel(BatchStepParams
 
 // Fold: one workgroup per (batch, head, ROWS rows of G^T). Thread (row r,
 // chunk c) accumulates G^T[e0 + r][8c .. 8c + 8) over the selected slots in
-// slot order (fp32); four slots' loads are in flight at a time.
+// slot order (fp32); eight slots' loads are in flight at a time.
 template <int D>
 __global__ __launch_bounds__(kThreads) void fold_kernel(FoldParams p) {
-  constexpr int CH = D / 8, ROWS = kThreads / CH, CHUNKS = D / ROWS, U = 4;
+  constexpr int CH = D / 8, ROWS = kThreads / CH, CHUNKS = D / ROWS, U = 8;
   const int bh = blockIdx.x / CHUNKS;
   const int e0 = (blockIdx.x % CHUNKS) * ROWS;
   const int tid = threadIdx.x, c = tid % CH, r = tid / CH;

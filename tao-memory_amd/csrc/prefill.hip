@@ -46,6 +46,8 @@ __global__ __launch_bounds__(kThreads) void pages_kernel(PagesParams p) {
     p.fine_sw[((size_t)bh * p.fine_cap + g * p.group + i) * D + d] = f2bf(exp_bf(rbf(zv[i] - pz)));
 }
 
+// One workgroup per (epoch, batch, head): the pending page summary with one
+// thread per channel, then the page weights with one wave per channel.
 template <int D>
 __global__ __launch_bounds__(kThreads) void epochs_kernel(EpochParams p) {
   __shared__ float pend_pz[D];
@@ -74,32 +76,16 @@ __global__ __launch_bounds__(kThreads) void epochs_kernel(EpochParams p) {
   }
   __syncthreads();
   if (P == 0) return;
-  int width = 1;
-  while (width * 64 < P) width <<= 1;
   const bf16_t* pzg = p.page_z + (size_t)bh * p.page_cap * D;
   bf16_t* state_pw = p.page_w + (size_t)bh * p.page_cap * D;
   for (int d = wave; d < D; d += kThreads / 64) {
-    float x[32];
-    float m = -__builtin_inff();
-    for (int k = 0; k < width; ++k) {
-      const int pg = lane + 64 * k;
-      x[k] = pg < P ? (pg == K ? pend_pz[d] : bf2f(pzg[(size_t)pg * D + d])) : -__builtin_inff();
-      m = fmaxf(m, x[k]);
-    }
-    m = wave_max(m);
-    float e[32];
-    for (int k = 0; k < width; ++k) e[k] = (lane + 64 * k) < P ? exp_cr(x[k] - m) : 0.0f;
-    for (int w = width / 2; w >= 1; w >>= 1)
-      for (int k = 0; k < w; ++k) e[k] += e[k + w];
-    const float total = wave_sum_fold(e[0]);
-    for (int k = 0; k < width; ++k) {
-      const int pg = lane + 64 * k;
-      if (pg < P) {
-        const bf16_t w = f2bf(exp_cr(x[k] - m) / total);
-        pw[(size_t)pg * D + d] = w;
-        if (last) state_pw[(size_t)pg * D + d] = w;
-      }
-    }
+    page_weights_wave(
+        lane, P,
+        [&](int pg) { return pg == K ? pend_pz[d] : bf2f(pzg[(size_t)pg * D + d]); },
+        [&](int pg, bf16_t w) {
+          pw[(size_t)pg * D + d] = w;
+          if (last) state_pw[(size_t)pg * D + d] = w;
+        });
   }
 }
 

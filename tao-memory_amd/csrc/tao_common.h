@@ -111,6 +111,41 @@ TAO_DEV long long fines_before(long long position, int keep, int fine) {
   return position < limit ? 0 : (position - limit) / fine + 1;
 }
 
+// Page weights of one channel on one wave: r(softmax over P <= 2048 page
+// descriptors), lane + 64 k -> page, the exps correctly rounded and summed
+// in the oracle's butterfly order (fold the k halves, then the lanes).
+// desc(pg) returns descriptor pg, write(pg, w) stores its weight.
+template <typename Desc, typename Write>
+TAO_DEV void page_weights_wave(int lane, int P, Desc desc, Write write) {
+  if (P <= 64) {   // one page per lane (contexts up to 128K tokens)
+    const float x = lane < P ? desc(lane) : -__builtin_inff();
+    const float m = wave_max(x);
+    const float e = lane < P ? exp_cr(x - m) : 0.0f;
+    const float total = wave_sum_fold(e);
+    if (lane < P) write(lane, f2bf(e / total));
+    return;
+  }
+  int width = 1;
+  while (width * 64 < P) width <<= 1;
+  float x[32];
+  float m = -__builtin_inff();
+  for (int k = 0; k < width; ++k) {
+    const int pg = lane + 64 * k;
+    x[k] = pg < P ? desc(pg) : -__builtin_inff();
+    m = fmaxf(m, x[k]);
+  }
+  m = wave_max(m);
+  float e[32];
+  for (int k = 0; k < width; ++k) e[k] = (lane + 64 * k) < P ? exp_cr(x[k] - m) : 0.0f;
+  for (int w = width / 2; w >= 1; w >>= 1)
+    for (int k = 0; k < w; ++k) e[k] += e[k + w];
+  const float total = wave_sum_fold(e[0]);
+  for (int k = 0; k < width; ++k) {
+    const int pg = lane + 64 * k;
+    if (pg < P) write(pg, f2bf(exp_cr(x[k] - m) / total));
+  }
+}
+
 // Page descriptor of n <= 8 fine descriptors of one channel: torch's bf16
 // logsumexp composite r(r(log r(sum r(exp r(z - m)))) + m), butterfly sum,
 // infinite maximum replaced by 0 (tao_stream.py:283, 412, 485).

@@ -18,7 +18,7 @@
 // index d is contiguous for every reader. C goes straight into its bank
 // slot: no repack.
 //
-// epilogue_kernel: one workgroup per (batch, head) after sealing fine `slot`
+// epilogue_kernel: one wave per (batch, head, channel) after sealing fine `slot`
 // (append_fine, tao_stream.py:477-501, plus the pending summary :277-290
 // and the seal-epoch memo :399-416): page descriptor
 // pz = logsumexp over the slot's group (torch's bf16 composite), segment
@@ -242,64 +242,47 @@ __global__ __launch_bounds__(kWriterThreads) void writer_kernel(WriterParams p) 
   }
 }
 
+// One wave per (batch, head, channel d); four channels per workgroup.
 template <int D>
 __global__ __launch_bounds__(kThreads) void epilogue_kernel(EpilogueParams p) {
-  __shared__ float pz_s[D];
-  const int bh = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int CPB = kThreads / 64;
+  const int bh = blockIdx.x / (D / CPB);
+  const int lane = threadIdx.x & 63;
+  const int d = (blockIdx.x % (D / CPB)) * CPB + (threadIdx.x >> 6);
   const int g = p.slot / p.group;
   const int first = g * p.group;
   const int n = p.slot - first + 1;
   const bf16_t* z = p.fine_z + (size_t)bh * p.fine_cap * D;
-  if (tid < D) {
+  float pz = 0.0f;
+  if (lane == 0) {
     float zv[8];
     float m = -__builtin_inff();
     for (int i = 0; i < 8; ++i) {
-      zv[i] = i < n ? bf2f(z[(size_t)(first + i) * D + tid]) : 0.0f;
+      zv[i] = i < n ? bf2f(z[(size_t)(first + i) * D + d]) : 0.0f;
       if (i < n) m = fmaxf(m, zv[i]);
     }
     if (__builtin_isinf(m)) m = 0.0f;
-    float pz;
     if (p.recompute) {
       float e[8];
       for (int i = 0; i < 8; ++i) e[i] = i < n ? exp_bf(rbf(zv[i] - m)) : 0.0f;
       for (int w = 4; w >= 1; w >>= 1)
         for (int i = 0; i < w; ++i) e[i] += e[i + w];
       pz = rbf(log_bf(rbf(e[0])) + m);
+      p.page_z[((size_t)bh * p.page_cap + g) * D + d] = f2bf(pz);
     } else {
-      pz = bf2f(p.page_z[((size_t)bh * p.page_cap + g) * D + tid]);
+      pz = bf2f(p.page_z[((size_t)bh * p.page_cap + g) * D + d]);
     }
-    pz_s[tid] = pz;
-    if (p.recompute) p.page_z[((size_t)bh * p.page_cap + g) * D + tid] = f2bf(pz);
     for (int i = 0; i < n; ++i)
-      p.fine_sw[((size_t)bh * p.fine_cap + first + i) * D + tid] = f2bf(exp_bf(rbf(zv[i] - pz)));
+      p.fine_sw[((size_t)bh * p.fine_cap + first + i) * D + d] = f2bf(exp_bf(rbf(zv[i] - pz)));
   }
-  __syncthreads();
-  // page weights: one wave per channel, lanes over pages (butterfly order).
-  const int P = p.pages;
-  int width = 1;
-  while (width * 64 < P) width <<= 1;
+  pz = __shfl(pz, 0, 64);
+  // Page weights of every current page for channel d.
   const bf16_t* pzg = p.page_z + (size_t)bh * p.page_cap * D;
   bf16_t* pwg = p.page_w + (size_t)bh * p.page_cap * D;
-  for (int d = wave; d < D; d += kThreads / 64) {
-    float x[32];
-    float m = -__builtin_inff();
-    for (int k = 0; k < width; ++k) {
-      const int pg = lane + 64 * k;
-      x[k] = pg < P ? (pg == g ? pz_s[d] : bf2f(pzg[(size_t)pg * D + d])) : -__builtin_inff();
-      m = fmaxf(m, x[k]);
-    }
-    m = wave_max(m);
-    float e[32];
-    for (int k = 0; k < width; ++k) e[k] = (lane + 64 * k) < P ? exp_cr(x[k] - m) : 0.0f;
-    for (int w = width / 2; w >= 1; w >>= 1)
-      for (int k = 0; k < w; ++k) e[k] += e[k + w];
-    const float total = wave_sum_fold(e[0]);
-    for (int k = 0; k < width; ++k) {
-      const int pg = lane + 64 * k;
-      if (pg < P) pwg[(size_t)pg * D + d] = f2bf(exp_cr(x[k] - m) / total);
-    }
-  }
+  page_weights_wave(
+      lane, p.pages,
+      [&](int pg) { return pg == g ? pz : bf2f(pzg[(size_t)pg * D + d]); },
+      [&](int pg, bf16_t w) { pwg[(size_t)pg * D + d] = w; });
 }
 
 }  // namespace
@@ -318,7 +301,7 @@ hipError_t launch_writer(const WriterParams& p, int head_dim, hipStream_t s) {
 
 hipError_t launch_seal_epilogue(const EpilogueParams& p, int head_dim, hipStream_t s) {
   if (p.pages > 64 * 32) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)(p.B * p.H));
+  const dim3 grid((unsigned)(p.B * p.H * (head_dim / (kThreads / 64))));
   if (head_dim == 128)
     hipLaunchKernelGGL(epilogue_kernel<128>, grid, dim3(kThreads), 0, s, p);
   else if (head_dim == 64)

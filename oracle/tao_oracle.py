@@ -467,9 +467,20 @@ class OracleStream:
         return self.prefill(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
                             position)
 
-    def export(self):
-        """Semantic snapshot in the reference's schema (tao_stream.py:853-877)."""
+    def export(self, config=None, layer_index=None):
+        """Snapshot in the reference's schema (tao_stream.py:853-877): every key
+        the reference writes; config is the TaoConfig.export() dict the
+        snapshot declares (default: this geometry with the memo and graph
+        flags off), layer_index defaults to this stream's layer."""
         group = self.g.coarse_group
+        if config is None:
+            g = self.g
+            config = dict(fine_tokens=g.fine_tokens, local_keep=g.local_keep,
+                          coarse_group=g.coarse_group, route_period=g.route_period,
+                          layer_stagger=g.layer_stagger, budget_root_scale=g.budget_root_scale,
+                          budget_offset=g.budget_offset, fine_writer="softmax",
+                          coarse_index_only=g.coarse_index_only,
+                          q1_page_normalization_memo=False, q1_history_region_graph=False)
         packed = torch.stack(self.fine_c, 2) if self.fine_c else None
         z = self.fine_z
         pages = []
@@ -479,12 +490,22 @@ class OracleStream:
                           torch.stack(z[index * group:(index + 1) * group], 2)))
         pending = [zz.clone() for zz in z[self.completed * group:]]
         return {
+            "layer_index": self.layer if layer_index is None else layer_index,
+            "config": dict(config),
+            "route_interval": 2,
+            "fusion_mode": "pointwise",
+            "fused_fine": True,
             "position": self.position,
             "local": None if self.local is None else tuple(t.clone() for t in self.local),
             "packed_fine_c": packed,
             "pages": pages,
             "pending_z": pending,
+            "pending_square_mass": None,
+            "pending_mass": None,
+            "pending_gram": None,
+            "pending_cross": None,
             "route_ids": None if self.route_ids is None else tuple(t.clone() for t in self.route_ids),
+            "route_key": None,
             "state_version": self.state_version,
             "route_refreshes": self.route_refreshes,
             "fine_seal_events": self.fine_seal_events,

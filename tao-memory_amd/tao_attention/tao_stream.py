@@ -720,7 +720,12 @@ class StreamCache:
 
     @classmethod
     def from_export(cls, saved):
-        """Restore an independent state (tao_stream.py:879-912)."""
+        """Restore an independent state (tao_stream.py:879-912).
+
+        Accepts this build's snapshots and the reference's (the same schema),
+        also after torch.save / torch.load(weights_only=True). A snapshot
+        whose tensors are on the host is restored onto the current device.
+        """
         config = TaoConfig(**saved["config"])
         state = cls(saved["layer_index"], saved["route_interval"], saved["fusion_mode"],
                     fused_fine=saved["fused_fine"], config=config)
@@ -728,6 +733,13 @@ class StreamCache:
         local = saved["local"]
         packed = saved["packed_fine_c"]
         pages, pending_z = saved["pages"], saved["pending_z"]
+        if local is not None and local[0].device.type == "cpu":
+            device = torch.device("cuda", torch.cuda.current_device())
+            move = lambda t: None if t is None else t.to(device)
+            local = tuple(move(t) for t in local)
+            packed = move(packed)
+            pages = [(move(pz), move(pc), move(fz)) for pz, pc, fz in pages]
+            pending_z = [move(z) for z in pending_z]
         fines = len(pages) * config.coarse_group + len(pending_z)
         if fines != schedule.fines_at(position, config):
             raise ValueError("snapshot fine count does not match its position")

@@ -335,3 +335,63 @@ def test_batched_decode_equals_per_request(device, coarse):
         for (pz, pc, fz), (qz, qc, gz) in zip(sa["pages"], sb["pages"]):
             assert torch.equal(pz, qz) and torch.equal(fz, gz)
             assert (pc is None and qc is None) or torch.equal(pc, qc)
+
+
+def _saved_and_loaded(snapshot):
+    """torch.save, then torch.load(weights_only=True) (the trusted-file path)."""
+    import io
+    buf = io.BytesIO()
+    torch.save(snapshot, buf)
+    buf.seek(0)
+    return torch.load(buf, weights_only=True)
+
+
+def _to_cpu(snapshot):
+    def cpu(x):
+        if isinstance(x, torch.Tensor):
+            return x.cpu()
+        if isinstance(x, (list, tuple)):
+            return type(x)(cpu(v) for v in x)
+        return x
+    return {k: cpu(v) for k, v in snapshot.items()}
+
+
+@pytest.mark.parametrize("coarse", [False, True])
+def test_snapshot_interop_with_oracle_through_torch_save(device, coarse):
+    """Snapshot wire format: an oracle snapshot (the reference schema) written
+    with torch.save and read with torch.load(weights_only=True) restores a
+    HIP state that continues like the oracle; a HIP snapshot restores an
+    oracle stream that continues like the HIP state."""
+    from tao_attention import TaoConfig
+    heads, width, n = 2, 64, 2700
+    cfg = TaoConfig() if coarse else index_only_page_memo()
+    geo = O.Geometry.from_config(cfg)
+    xs, fa, fb = inputs(n + 330, heads, width, seed=21, unit_raw_k=True)
+    head = [t[:, :n] for t in xs]
+    rest = [t[:, n:] for t in xs]
+    splits = [1] * 30 + [300]
+    print(f"snapshot interop coarse={coarse}", flush=True)
+    # oracle -> file -> HIP
+    ora = O.OracleStream(1, geo)
+    ora.prefill(*head, fa, fb, 0.5)
+    hip = StreamCache.from_export(_saved_and_loaded(ora.export(config=cfg.export())))
+    assert hip.get_pos() == n
+    got = run_hip(hip, to_dev(rest, device), fa.to(device), fb.to(device), splits)
+    want = []
+    start = 0
+    for w in splits:
+        want.append(ora.prefill(*(t[:, start:start + w] for t in rest), fa, fb, 0.5))
+        start += w
+    torch.testing.assert_close(got.cpu().float(), torch.cat(want, 1).float(), **TOL)
+    compare_snapshots(hip.export(), ora.export())
+    # HIP -> file -> oracle
+    hip2 = new_state(1, cfg)
+    run_hip(hip2, to_dev(head, device), fa.to(device), fb.to(device), [n])
+    ora2 = O.OracleStream.from_export(_saved_and_loaded(_to_cpu(hip2.export())), 1, geo)
+    got2 = run_hip(hip2, to_dev(rest, device), fa.to(device), fb.to(device), splits)
+    want2, start = [], 0
+    for w in splits:
+        want2.append(ora2.prefill(*(t[:, start:start + w] for t in rest), fa, fb, 0.5))
+        start += w
+    torch.testing.assert_close(got2.cpu().float(), torch.cat(want2, 1).float(), **TOL)
+    compare_snapshots(hip2.export(), ora2.export())

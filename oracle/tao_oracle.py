@@ -36,7 +36,7 @@ class Geometry:
 
     def __init__(self, fine_tokens=256, local_keep=512, coarse_group=8,
                  route_period=24, layer_stagger=2, budget_root_scale=2,
-                 budget_offset=2, coarse_index_only=True):
+                 budget_offset=2, coarse_index_only=True, page_memo=False):
         self.fine_tokens = fine_tokens
         self.local_keep = local_keep
         self.coarse_group = coarse_group
@@ -45,13 +45,14 @@ class Geometry:
         self.budget_root_scale = budget_root_scale
         self.budget_offset = budget_offset
         self.coarse_index_only = coarse_index_only
+        self.page_memo = page_memo            # q1_page_normalization_memo
 
     @classmethod
     def from_config(cls, config):
         return cls(config.fine_tokens, config.local_keep, config.coarse_group,
                    config.route_period, config.layer_stagger,
                    config.budget_root_scale, config.budget_offset,
-                   config.coarse_index_only)
+                   config.coarse_index_only, config.q1_page_normalization_memo)
 
     @property
     def serve_limit(self):
@@ -330,6 +331,16 @@ class OracleStream:
         self.route_refreshes = 0
         self.fine_seal_events = 0
         self._bank = None            # stacked fine_c, rebuilt after a seal
+        # Diagnostics counters of StreamCache.bytes() (tao_stream.py:
+        # 1044-1094), updated where the reference updates them.
+        self.diag = dict(coarse_matrix_contractions=0, fine_matrix_contractions=0,
+                         fine_candidate_scores=0, route_query_heads=0,
+                         route_selection_calls=0, pending_only_fine_present_query_heads=0,
+                         fused_fine_calls=0, peak_local_length_tokens=0,
+                         peak_logical_cache_bytes=0, peak_physical_cache_tensor_bytes=0)
+        self.memo = False            # page_normalization_memo is not None
+        self.last_route_queries = 0
+        self.last_fine_contractions = 0
 
     # -- state views ------------------------------------------------------
     @property
@@ -376,9 +387,23 @@ class OracleStream:
                 self.page_c.append(page_coarse_matrix(
                     zs, pz, torch.stack(self.fine_c[start:], 2)))
 
-    def read(self, raw_q):
+    def logical_bytes(self, b, heads, d):
+        """LayerState.logical_bytes (tao_stream.py:518-527), bf16."""
+        count = self.completed * (self.g.coarse_group + 1) + self.pending
+        elements = count * (d * d + d)
+        if self.g.coarse_index_only:
+            elements -= self.completed * d * d
+        return elements * b * heads * 2
+
+    def release_execution(self):
+        """StreamCache.release_execution (:838-844): drops the memo."""
+        self.memo = False
+
+    def read(self, raw_q, allow_page_memo=False):
         """LayerState._read_progressive + _read_reused (:196-374)."""
         b, t, heads, d = raw_q.shape
+        self.last_route_queries = 0            # LayerState.read (:162-164)
+        self.last_fine_contractions = 0
         if not self.fine_z:
             zero = torch.zeros_like(raw_q)
             return zero, zero, False, False
@@ -407,6 +432,12 @@ class OracleStream:
                                             self.pending, self.g)
                 self.route_ids = (chosen.unsqueeze(1), selected.unsqueeze(1))
                 self.route_refreshes += 1
+                self.last_route_queries += b * heads                  # :215-216
+            elif (allow_page_memo and t == 1 and self.g.page_memo
+                  and self.g.coarse_index_only):
+                self.memo = True                                      # :292-295
+            self.last_fine_contractions += b * count * heads * self.route_ids[1].shape[-1]
+            self.diag["fused_fine_calls"] += 1                        # :244, :370
             part, _ = selected_read(hv[:, offset:offset + count], sw,
                                     self.route_ids[1][:, 0], bank,
                                     self.g.coarse_group)
@@ -414,7 +445,7 @@ class OracleStream:
             offset += count
         return coarse, fine, coarse_on, True
 
-    def process(self, raw_q, raw_k, q, k, v):
+    def process(self, raw_q, raw_k, q, k, v, allow_page_memo=False):
         """StreamCache.process (:919-979): local, read, then seal at 768."""
         if self.local is None:
             all_k, all_v, all_raw = k, v, raw_k
@@ -425,8 +456,25 @@ class OracleStream:
         if all_k.shape[1] > self.g.serve_limit:
             raise ValueError("chunk crosses a fine seal boundary")
         local = local_attention(q, all_k, all_v)
-        coarse, fine, c_on, f_on = self.read(raw_q)
+        b, t, heads, d = raw_q.shape
+        query_heads = b * t * heads
+        _, eligible, _ = self.g.routed_counts(self.completed, self.pending)
+        if not self.g.coarse_index_only:
+            self.diag["coarse_matrix_contractions"] += query_heads * self.completed
+        coarse, fine, c_on, f_on = self.read(raw_q, allow_page_memo)
+        if self.pending and not self.completed:
+            self.diag["pending_only_fine_present_query_heads"] += query_heads
+        self.diag["fine_matrix_contractions"] += self.last_fine_contractions
+        self.diag["route_query_heads"] += self.last_route_queries
+        self.diag["route_selection_calls"] += self.last_route_queries // heads
+        self.diag["fine_candidate_scores"] += self.last_route_queries * eligible
+        self.diag["peak_local_length_tokens"] = max(self.diag["peak_local_length_tokens"],
+                                                    all_k.shape[1])
+        history = self.logical_bytes(b, heads, d)
+        key_bytes = all_k.numel() * 2
+        self._preseal = (history + 2 * key_bytes, history + 3 * key_bytes)
         if all_k.shape[1] == self.g.serve_limit:
+            self.memo = False                                         # :445-449
             self.fine_seal_events += 1
             ft, keep = self.g.fine_tokens, self.g.local_keep
             self.seal(all_raw[:, :ft], all_v[:, :ft])
@@ -443,12 +491,18 @@ class OracleStream:
             raise ValueError("position must match this request's causal cursor")
         outputs = []
         start = 0
+        single = q.shape[1] == 1          # allow_page_memo (operator.py:80-83)
         while start < q.shape[1]:
             width = self.next_chunk(q.shape[1] - start)
             end = start + width
             local, coarse, fine, c_on, f_on = self.process(
                 raw_q[:, start:end], raw_k[:, start:end], q[:, start:end],
-                k[:, start:end], v[:, start:end])
+                k[:, start:end], v[:, start:end], allow_page_memo=single)
+            # StreamCache.advance (:981-986)
+            self.diag["peak_logical_cache_bytes"] = max(self.diag["peak_logical_cache_bytes"],
+                                                        self._preseal[0])
+            self.diag["peak_physical_cache_tensor_bytes"] = max(
+                self.diag["peak_physical_cache_tensor_bytes"], self._preseal[1])
             if c_on or f_on:
                 out = fusion(raw_q[:, start:end], local, coarse, fine,
                              fusion_a, fusion_b, alpha, c_on, f_on)

@@ -30,7 +30,7 @@ import ctypes
 import numpy as np
 import torch
 
-from . import _hip, schedule
+from . import _hip, diagnostics, schedule
 from .config import TaoConfig
 
 DEFAULT_CONFIG = TaoConfig()
@@ -242,6 +242,8 @@ class StreamCache:
                                 and config.coarse_index_only)
         self._first_fine = self.config.first_fine
         self._graph_buffers = None
+        self._log = []               # call log of the diagnostics counters
+        self._run_open = False       # the last log entry is an open one-token run
         self._info = (ctypes.c_int64 * 7)()
 
     # ------------------------------------------------------------------ cursor
@@ -257,6 +259,23 @@ class StreamCache:
 
     # -------------------------------------------------------------- lifecycle
     def release_execution(self, reason="request_end"):
+        """Drop the captured graph and the page memo; the semantic state stays."""
+        self._log_event("release", 0)
+        self._release_graph(reason)
+
+    def _log_event(self, kind, tokens):
+        """Append a call (tokens > 1) or release to the diagnostics log,
+        closing an open one-token run."""
+        if self._run_open:
+            self._log[-1][2] = self.position - self._log[-1][1]
+            self._run_open = False
+        self._log.append([kind, self.position, tokens, self.route_size])
+
+    def _open_run(self):
+        self._log.append(["run", self.position, None, self.route_size])
+        self._run_open = True
+
+    def _release_graph(self, reason):
         if self.history_region is not None:
             self.history_region.invalidate(reason)
         if self._handle is not None:
@@ -282,7 +301,7 @@ class StreamCache:
 
     def reset(self):
         """Discard this request's state; position returns to zero."""
-        self.release_execution("reset")
+        self._release_graph("reset")
         self._close_driver()
         self.__init__(self.layer_index, self.route_interval, self.fusion_mode,
                       self.pending_coarse_elision, self.pending_coarse_mask,
@@ -311,7 +330,7 @@ class StreamCache:
         elif not self._dev.matches(b, h, d, q.device):
             raise ValueError("batch/heads/width/device must stay fixed for a state")
         elif self._dev.reserve(fines, schedule.fines_at(self.position, self.config)):
-            self.release_execution("capacity")
+            self._release_graph("capacity")
             self._handle_dirty = True
         return self._dev
 
@@ -377,7 +396,7 @@ class StreamCache:
         plan_np = np.asarray(plan, dtype=np.int64)
         plan_arr = plan_np.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
         if dev.ensure_plan(len(plan)):
-            self.release_execution("capacity")
+            self._release_graph("capacity")
             self._handle_dirty = True
         pools = _hip.PrefillPools()
         keep = []
@@ -414,6 +433,11 @@ class StreamCache:
     def prefill(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
         """Advance by q.shape[1] tokens; returns the fused heads [B, T, H, D]."""
         self._check_supported(q)
+        if q.shape[1] == 1:
+            if not self._run_open:
+                self._open_run()
+        else:
+            self._log_event("call", q.shape[1])
         cfg = self.config
         pos0 = self.position
         tokens = q.shape[1]
@@ -588,6 +612,8 @@ class StreamCache:
 
     def _book(self, pos, graph, out):
         """Cursor and counters after one driver call (info from the driver)."""
+        if not self._run_open:
+            self._open_run()
         info = self._info
         self.position = pos + 1
         if pos >= self._first_fine:
@@ -653,6 +679,7 @@ class StreamCache:
         self._check_supported(q)
         pos0 = self.position
         tokens = q.shape[1]
+        self._log_event("call", tokens)
         dev = self._device_for(q, pos0 + tokens)
         q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
@@ -801,7 +828,14 @@ class StreamCache:
 
     # ------------------------------------------------------------- diagnostics
     def bytes(self):
-        """Subset of the reference diagnostics (tao_stream.py:988-1094)."""
+        """The reference diagnostics (tao_stream.py:988-1094), same keys.
+
+        Logical sizes and counters follow the reference's definitions (the
+        counters from the call log, diagnostics.py). Physical sizes describe
+        this build's buffers: the local window is a token ring of
+        serve_limit slots, and "unique_allocated_cache_storage_bytes" sums
+        the device buffers the state holds (capacity included).
+        """
         cfg = self.config
         fines = schedule.fines_at(self.position, cfg)
         completed, pending = divmod(fines, cfg.coarse_group)
@@ -815,17 +849,65 @@ class StreamCache:
         if cfg.coarse_index_only:
             history -= completed * width * width * batch * heads * 2
         local_tokens = schedule.local_len_at(self.position, cfg)
+        log = [tuple(e) for e in self._log]
+        c = diagnostics.counters(cfg, self.layer_index, batch, heads, width, log, self.position)
+        memo = diagnostics.memo_bytes(c.memo, completed, pending, batch, heads, width)
+        route_bytes = (8 * batch * heads * (self.route_coarse + self.route_size)
+                       if self.route_size else 0)
+        logical_local = local_tokens * 2 * heads * width * 2 * batch
+        physical_local = 0
+        unique = 0
+        if dev is not None:
+            physical_local = sum(t.numel() * t.element_size()
+                                 for t in (dev.ring_k, dev.ring_v, dev.ring_raw))
+            unique = sum(t.numel() * t.element_size() for t in (
+                dev.ring_k, dev.ring_v, dev.ring_raw, dev.bank, dev.fine_z, dev.fine_sw,
+                dev.page_z, dev.page_w, dev.sel, dev.chosen, dev.header, dev.fold_g,
+                dev.fold_den, dev.workspace) if t is not None)
+            unique += sum(t.numel() * t.element_size()
+                          for t in (dev.page_c, dev.coarse_g) if t is not None)
         return {"history_bytes": history,
+                "page_normalization_memo_bytes": memo,
+                "pending_writer_bytes": 0,
+                "pending_gram_cross_bytes": 0,
+                "pending_cross_bytes": 0,
+                "pending_square_mass_bytes": 0,
+                "pending_feature_mass_bytes": 0,
+                "fused_fine": self.fused_fine,
+                "fused_fine_calls": c.fused_fine_calls if self.fused_fine else 0,
+                "fusion_mode": self.fusion_mode,
+                "fusion_pointwise_calls": self.fusion_pointwise_calls,
+                "fusion_no_history_local_returns": self.fusion_no_history_local_returns,
+                "fusion_eager_calls": 0,
+                "pending_coarse_elision": self.pending_coarse_elision,
+                "pending_coarse_mask": self.pending_coarse_mask,
+                "pending_only_masked_coarse_calls": 0,
+                "pending_only_coarse_present_query_heads": 0,
+                "pending_only_fine_present_query_heads": c.pending_only_fine_present_query_heads,
+                "pending_coarse_elided_query_heads": 0,
+                "pending_coarse_matrix_constructions": 0,
+                "pending_coarse_elision_reads": 0,
                 "fine_seal_events": self.fine_seal_events,
+                "route_integer_bytes": route_bytes,
+                "logical_local_bf16_kv_bytes": logical_local,
+                "logical_retained_bytes": history + logical_local,
+                "physical_local_including_raw_key_bytes": physical_local,
+                "allocated_cache_tensor_bytes": history + physical_local + route_bytes + memo,
+                "unique_allocated_cache_storage_bytes": unique,
+                "local_length_tokens": local_tokens,
                 "completed_coarse_pages": completed,
                 "pending_fine_states": pending,
-                "local_length_tokens": local_tokens,
-                "logical_local_bf16_kv_bytes": local_tokens * 2 * heads * width * 2 * batch,
                 "selected_fine_per_layer": [self.route_size],
                 "peak_selected_fine_per_layer": [self.peak_selected_fine],
                 "route_refreshes_per_layer": [self.route_refreshes],
-                "fusion_pointwise_calls": self.fusion_pointwise_calls,
-                "fusion_no_history_local_returns": self.fusion_no_history_local_returns,
+                "peak_local_length_tokens": c.peak_local_length_tokens,
+                "peak_logical_cache_bytes": c.peak_logical_cache_bytes,
+                "peak_physical_cache_tensor_bytes": c.peak_physical_cache_tensor_bytes,
+                "coarse_matrix_contractions": c.coarse_matrix_contractions,
+                "fine_matrix_contractions": c.fine_matrix_contractions,
+                "fine_candidate_scores": c.fine_candidate_scores,
+                "route_query_heads": c.route_query_heads,
+                "route_selection_calls": c.route_selection_calls,
                 "fine_matrix_repack_bytes": 0}
 
 
@@ -914,6 +996,8 @@ class DecodeBatch:
             self._handle, ctypes.byref(tok), ctypes.byref(fu), out.data_ptr(), out_s,
             self.states[0]._dev.stream(), info))
         for r, st in enumerate(self.states):
+            if not st._run_open:
+                st._open_run()
             pos = st.position
             st.position = pos + 1
             refreshed, sealed = info[4 * r], info[4 * r + 1]

@@ -79,6 +79,15 @@ def compare_snapshots(hip, ora):
         assert torch.equal(a.cpu(), b)
 
 
+def compare_diagnostics(state, ora):
+    """StreamCache.bytes() counters == the oracle's restated accounting."""
+    got = state.bytes()
+    for key, value in ora.diag.items():
+        assert got[key] == value, key
+    assert got["fine_seal_events"] == ora.fine_seal_events
+    assert got["route_refreshes_per_layer"] == [ora.route_refreshes]
+
+
 @pytest.mark.parametrize("width", [64, 128])
 @pytest.mark.parametrize("tq,tk", [(200, 200), (1, 700), (256, 768), (77, 333)])
 def test_local_attention_plugin(device, width, tq, tk):
@@ -108,9 +117,11 @@ def test_decode_matches_oracle_across_seal_and_refresh(device):
     print("decode across seal", flush=True)
     state = new_state(3, index_only_page_memo())
     out = run_hip(state, to_dev(xs, device), fa.to(device), fb.to(device), splits)
-    ora, ref = run_oracle(3, xs, fa, fb, splits)
+    ora, ref = run_oracle(3, xs, fa, fb, splits,
+                          geometry=O.Geometry.from_config(index_only_page_memo()))
     torch.testing.assert_close(out.cpu().float(), ref.float(), **TOL)
     compare_snapshots(state.export(), ora.export())
+    compare_diagnostics(state, ora)
 
 
 def test_chunked_prefill_and_page_routing(device):
@@ -121,9 +132,11 @@ def test_chunked_prefill_and_page_routing(device):
     print("chunked prefill with pages", flush=True)
     state = new_state(1, index_only_page_memo())
     out = run_hip(state, to_dev(xs, device), fa.to(device), fb.to(device), splits)
-    ora, ref = run_oracle(1, xs, fa, fb, splits)
+    ora, ref = run_oracle(1, xs, fa, fb, splits,
+                          geometry=O.Geometry.from_config(index_only_page_memo()))
     torch.testing.assert_close(out.cpu().float(), ref.float(), **TOL)
     compare_snapshots(state.export(), ora.export())
+    compare_diagnostics(state, ora)
 
 
 def test_graph_equals_eager_bitwise(device):
@@ -239,6 +252,7 @@ def test_coarse_value_branch_prefill(device):
     snap = state.export()
     assert len(snap["pages"]) == 2
     compare_snapshots(snap, ora.export())
+    compare_diagnostics(state, ora)
 
 
 def test_coarse_value_branch_decode_across_page_completion(device):

@@ -392,3 +392,46 @@ def test_stream_coarse_branch_switches_on_at_first_coarse():
     snap = s.export()
     assert len(snap["pages"]) == 1 and snap["pages"][0][1] is not None
     assert snap["pages"][0][1].shape == (1, 2, 16, 16)
+
+
+@pytest.mark.parametrize("coarse,memo", [(False, True), (True, False), (False, False)])
+def test_diagnostics_counters_match_reference_accounting(coarse, memo):
+    """The product's closed-form diagnostics (tao_attention.diagnostics, from a
+    call log) equal the oracle's restatement of the reference's per-chunk and
+    per-segment accounting (tao_stream.py:162-230, 919-986) over random mixes
+    of prefill calls, one-token runs and releases."""
+    import random
+    from tao_attention import TaoConfig, diagnostics
+    cfg = TaoConfig(coarse_index_only=not coarse, q1_page_normalization_memo=memo)
+    layer, heads, width, total = 1, 2, 16, 2900
+    rng = random.Random(3 + 2 * coarse + memo)
+    xs, fa, fb = _stream_inputs(total, heads=heads, width=width, seed=5)
+    s = O.OracleStream(layer, O.Geometry.from_config(cfg))
+    log, pos = [], 0
+    while pos < total:
+        route = 0 if s.route_ids is None else s.route_ids[1].shape[-1]
+        if rng.random() < 0.5:
+            n = min(rng.randint(1, 40), total - pos)
+            for i in range(n):
+                if not (log and log[-1][0] == "run" and log[-1][1] + log[-1][2] == pos + i):
+                    log.append(["run", pos + i, 0, route if i == 0 else
+                                s.route_ids[1].shape[-1]])
+                log[-1][2] += 1
+                q, k, v, rq, rk = (t[:, pos + i:pos + i + 1] for t in xs)
+                s.prefill(q, k, v, rq, rk, fa, fb, 0.5)
+        else:
+            n = min(rng.randint(2, 700), total - pos)
+            log.append(["call", pos, n, route])
+            q, k, v, rq, rk = (t[:, pos:pos + n] for t in xs)
+            s.prefill(q, k, v, rq, rk, fa, fb, 0.5)
+        pos += n
+        if rng.random() < 0.1:
+            s.release_execution()
+            log.append(["release", pos, 0, 0])
+    c = diagnostics.counters(cfg, layer, 1, heads, width, [tuple(e) for e in log], pos)
+    for key, value in s.diag.items():
+        assert getattr(c, key) == value, key
+    assert c.memo == s.memo
+    assert s.diag["fine_matrix_contractions"] > 0 and s.diag["route_query_heads"] > 0
+    if coarse:
+        assert s.diag["coarse_matrix_contractions"] > 0

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 3
+#define TAO_ABI_VERSION 4
 
 enum tao_status {
   TAO_OK = 0,
@@ -181,12 +181,16 @@ int tao_local_attention(const tao_state_dev* st, const tao_tokens* tok,
  *   sel_pool int32 [sel_slots][B][H][sel_cap]   selected ids per route turn
  *   coarse_pool bf16 [coarse_count][B][H][D][D] folded coarse reads (G^T)
  *     for completed = coarse_first + i (coarse value branch only; else null)
+ *   qsel     uint32 [B][T][H][qsel_words]      per-query selections as
+ *     bitmasks over fine ids (plans with TAO_PLAN_QUERY_ROUTES = 1 only)
  * Slot 0 of sel_pool receives the state's route at call start. */
 typedef struct tao_prefill_pools {
   void* pw_pool; void* psw_pool; int32_t* sel_pool;
   int32_t pool_pcap, epochs, sel_slots;
   void* coarse_pool;
   int32_t coarse_first, coarse_count;
+  uint32_t* qsel;
+  int32_t qsel_words;
 } tao_prefill_pools;
 
 /* Layout of the int64 prefill plan (all indices are token offsets in tok
@@ -209,7 +213,11 @@ enum tao_plan_field {
                                fine_on, completed pages} */
   TAO_PLAN_RING_FIRST = 10, /* ring append: first token, count, position */
   TAO_PLAN_RING_COUNT = 11,
-  TAO_PLAN_RING_POS = 12
+  TAO_PLAN_RING_POS = 12,
+  TAO_PLAN_QUERY_ROUTES = 13 /* 1: every history query routes itself (no
+                                turns; read tile field 2 holds the coarse
+                                page count of its epoch, selections go to
+                                pools.qsel) */
 };
 
 /* Batched prefill of tok.tokens new tokens (replaces the chunk loop of
@@ -261,6 +269,20 @@ typedef struct tao_stream_cfg {
 int tao_prefill_plan(const tao_stream_cfg* cfg, int64_t pos0, int64_t tokens,
                      int32_t route_coarse, int32_t route_size, int32_t outputs,
                      int64_t* plan, int64_t plan_cap, int64_t* info);
+
+/* Plan of the full-sequence read of tokens [0, tokens) (replaces the host
+ * tiling of read_training, tao_stream.py:668-757, and of
+ * _local_training_corrected_4k, :760-787, behind tao_attention,
+ * operator.py:40-52), executed by tao_prefill on a fresh state: tile t of
+ * fine_tokens queries attends suffix-causally to keys from
+ * max(0, t * fine_tokens - local_keep), reads the first
+ * max(0, t - local_keep / fine_tokens) sealed fines, and every one of its
+ * queries routes itself (TAO_PLAN_QUERY_ROUTES). Only the visible blocks are
+ * written; nothing is appended to the ring. info (int64[12]): the ten
+ * tao_prefill_plan fields (turns = 0), then the fines written and
+ * qsel_words, the bitmask words per query. Host code only. */
+int tao_train_plan(const tao_stream_cfg* cfg, int64_t tokens, int64_t* plan,
+                   int64_t plan_cap, int64_t* info);
 
 /* Numerics self-test (no reference counterpart): y[i] = the library's
  * bf16(correctly rounded fp32 exp(x[i])) (op 0) or log (op 1) for n bf16

@@ -592,3 +592,108 @@ class OracleStream:
         state.fine_seal_events = saved["fine_seal_events"]
         return state
 
+
+
+# ----------------------------------------------------------------------------
+# Full-sequence read: operator.py:21-52 (tao_attention, _fuse_training),
+# tao_stream.py:530-787 (read_training and its helpers)
+# ----------------------------------------------------------------------------
+
+def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
+                     geometry=None, return_routes=False):
+    """tao_attention forward with fresh routing at every query.
+
+    Restates read_training (tao_stream.py:668-757) with route_interval=1 and
+    _fuse_training (operator.py:21-38):
+      * local: tile t = tokens [F t, min(T, F t + F)) attends suffix-causally
+        to keys [max(0, F t - keep), end) (_local_training_corrected_4k,
+        :760-787, and its ragged fallback :763-775 are the same windows);
+      * tile t reads the first max(0, t - keep / F) sealed fines (:734);
+        fines come from _seal_training_all (:80-123, the softmax writer per
+        block), page summaries from _training_metadata / _tile_metadata
+        (:530-593: logsumexp over the 8 fines of a completed page, over the
+        first `pending` fines of the pending page);
+      * every query routes itself (_read_training_group, :596-665: the same
+        candidate construction, segment weights and stable top-k as the
+        streaming refresh) and reads its own selection
+        (selected_read.py:156-173: fine = r(r(num) / r(den)));
+      * coarse read of completed pages when not index-only (:609-615);
+      * fusion with coarse presence pos >= first_coarse and not index-only,
+        fine presence pos >= first_fine, output = local where neither is
+        present (operator.py:46-52, 21-38).
+    Tiles are evaluated one at a time; the reference's stacking of up to 8
+    tiles with equal (completed, pending?, M, length) on the batch axis
+    (:700-748) changes no value.
+
+    Returns out [B, T, H, D] (and, with return_routes, a dict tile -> selected
+    ids [B, Q, H, M] in score order).
+    """
+    g = geometry or Geometry()
+    b, total, heads, d = q.shape
+    ft, keep, group = g.fine_tokens, g.local_keep, g.coarse_group
+    local = torch.empty_like(q)
+    for start in range(0, total, ft):
+        end = min(total, start + ft)
+        k0 = max(0, start - keep)
+        local[:, start:end] = local_attention(q[:, start:end], k[:, k0:end], v[:, k0:end])
+    routes = {}
+    n_tiles = -(-total // ft)
+    lag = keep // ft                                     # config.visibility_tiles
+    visible_max = max(0, n_tiles - 1 - lag)
+    if total <= g.serve_limit or visible_max == 0:       # :682-688
+        return (local, routes) if return_routes else local
+    zs, cs = [], []
+    for f in range(visible_max):
+        z, c = seal_softmax(raw_k[:, f * ft:(f + 1) * ft], v[:, f * ft:(f + 1) * ft])
+        zs.append(z)
+        cs.append(c)
+    fine_z = torch.stack(zs, 2)                          # [B, H, S, D]
+    bank = torch.stack(cs, 2)                            # [B, H, S, D, D]
+    full_pages = visible_max // group
+    page_z_full = [page_summary(fine_z[:, :, p * group:(p + 1) * group])
+                   for p in range(full_pages)]
+    page_c_full = []
+    if not g.coarse_index_only:
+        page_c_full = [page_coarse_matrix(fine_z[:, :, p * group:(p + 1) * group],
+                                          page_z_full[p], bank[:, :, p * group:(p + 1) * group])
+                       for p in range(full_pages)]
+    first_coarse = keep + group * ft                     # config.py:47-48
+    out = local.clone()
+    for tile in range(n_tiles):
+        start = tile * ft
+        end = min(total, start + ft)
+        visible = max(0, tile - lag)
+        if not visible:
+            continue
+        completed, pending = divmod(visible, group)
+        parts = list(page_z_full[:completed])
+        if pending:
+            parts.append(page_summary(fine_z[:, :, completed * group:visible]))
+        page_z = torch.stack(parts, 2)
+        pw = page_weights(page_z)
+        page_of = torch.arange(visible) // group
+        sw = segment_weights(fine_z[:, :, :visible], page_z.index_select(2, page_of))
+        h = query_weights(raw_q[:, start:end])
+        hv = page_values(h, pw)                          # [B, Q, H, P, D]
+        nq = end - start
+        flat = hv.reshape(b * nq, heads, *hv.shape[3:])
+        sw_flat = sw.unsqueeze(1).expand(b, nq, *sw.shape[1:]).reshape(b * nq, *sw.shape[1:])
+        _, selected, _ = route(flat, sw_flat, completed, pending, g)
+        selected = selected.reshape(b, nq, heads, -1)    # [B, Q, H, M]
+        routes[tile] = selected
+        fine = torch.empty_like(raw_q[:, start:end])
+        tile_bank = bank[:, :, :visible]
+        for i in range(nq):
+            part, _ = selected_read(hv[:, i:i + 1], sw, selected[:, i], tile_bank, group)
+            fine[:, i:i + 1] = part
+        coarse_on = start >= first_coarse and not g.coarse_index_only
+        fine_on = start >= g.serve_limit                 # first_fine
+        if coarse_on:
+            coarse = coarse_read(h, page_z[:, :, :completed],
+                                 torch.stack(page_c_full[:completed], 2))
+        else:
+            coarse = torch.zeros_like(fine)
+        if coarse_on or fine_on:
+            out[:, start:end] = fusion(raw_q[:, start:end], local[:, start:end], coarse,
+                                       fine, fusion_a, fusion_b, alpha, coarse_on, fine_on)
+    return (out, routes) if return_routes else out

@@ -408,6 +408,10 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   const int64_t off_attn = TAO_PLAN_HEADER, off_write = off_attn + 3 * n_attn;
   const int64_t off_turns = off_write + n_write, off_read = off_turns + 8 * n_turns;
   if (off_read + 8 * n_read != plan_len) return fail(TAO_E_ARGUMENT, "plan length mismatch");
+  const int64_t query_mode = plan[TAO_PLAN_QUERY_ROUTES];
+  if (query_mode != 0 && query_mode != 1) return fail(TAO_E_ARGUMENT, "invalid route mode");
+  const bool query_routes = query_mode == 1;
+  if (query_routes && n_turns) return fail(TAO_E_ARGUMENT, "per-query routes take no turns");
   const int BH = st->batch * st->heads;
   // ---- validate attention tiles
   for (int64_t i = 0; i < n_attn; ++i) {
@@ -436,8 +440,10 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   if (n_epochs < 0) return fail(TAO_E_ARGUMENT, "negative epoch count");
   const bool need_pools = n_epochs > 0 || n_turns > 0;
   if (need_pools) {
-    if (!pools || !pools->pw_pool || !pools->psw_pool || !pools->sel_pool)
+    if (!pools || !pools->pw_pool || !pools->psw_pool || (!query_routes && !pools->sel_pool))
       return fail(TAO_E_ARGUMENT, "prefill with history needs epoch pools");
+    if (query_routes && (!pools->qsel || pools->qsel_words < 1 || pools->qsel_words > 512))
+      return fail(TAO_E_ARGUMENT, "per-query routes need the qsel bitmask pool");
     const int64_t last = first_epoch + n_epochs - 1;
     if (first_epoch < 1 || n_epochs > pools->epochs || last > st->fine_cap ||
         last / G + 1 > pools->pool_pcap || last / G + 1 > st->page_cap)
@@ -468,10 +474,19 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
       return fail(TAO_E_ARGUMENT, "invalid read tile in the plan");
     if (t[6]) {
       const int64_t epoch = first_epoch + t[4];
-      if (!pools || t[2] < 0 || t[2] >= pools->sel_slots || t[3] < 1 || t[3] > 128 ||
-          t[3] > st->sel_cap || t[4] < 0 || t[4] >= n_epochs || t[5] != (epoch / G) * G ||
-          t[7] != epoch / G)
+      if (!pools || t[4] < 0 || t[4] >= n_epochs || t[5] != (epoch / G) * G || t[7] != epoch / G)
         return fail(TAO_E_ARGUMENT, "invalid history read tile in the plan");
+      if (query_routes) {
+        // t[2] = coarse pages, t[3] = selected of the tile's epoch
+        const int64_t K = epoch / G, eligible = t[2] * G + epoch % G;
+        if (t[2] < 0 || t[2] > K || t[3] < 1 || t[3] > eligible ||
+            eligible > tao::kQueryRouteMaxKeys || K > tao::kQueryRouteMaxKeys || epoch > 1024 ||
+            (epoch + 31) / 32 > pools->qsel_words)
+          return fail(TAO_E_ARGUMENT, "invalid per-query read tile in the plan");
+      } else if (t[2] < 0 || t[2] >= pools->sel_slots || t[3] < 1 || t[3] > 128 ||
+                 t[3] > st->sel_cap) {
+        return fail(TAO_E_ARGUMENT, "invalid history read tile in the plan");
+      }
       if (coarse_values && t[7] >= 1) {
         if (!pools->coarse_pool || t[7] < c_first || t[7] >= c_first + c_count)
           return fail(TAO_E_ARGUMENT, "coarse read outside the coarse pool");
@@ -494,7 +509,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   hipError_t e = hipMemcpyAsync(dplan, plan, (size_t)plan_len * sizeof(int64_t),
                                 hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill plan upload");
-  if (need_pools && pools->sel_slots > 0) {
+  if (!query_routes && need_pools && pools->sel_slots > 0) {
     e = hipMemcpyAsync(pools->sel_pool, st->sel, (size_t)BH * st->sel_cap * sizeof(int32_t),
                        hipMemcpyDeviceToDevice, s);
     if (e != hipSuccess) return check_hip(e, "tao_prefill route carry");
@@ -625,6 +640,29 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
     e = tao::launch_route(rp, D, s);
     if (e != hipSuccess) return check_hip(e, "tao_prefill routes");
   }
+  if (query_routes && need_pools && n_read) {
+    tao::QueryRouteParams qp;
+    qp.rq = (const bf16_t*)tok->raw_q;
+    qp.rq_sb = tok->rq_s[0];
+    qp.rq_st = tok->rq_s[1];
+    qp.rq_sh = tok->rq_s[2];
+    qp.sw = (const bf16_t*)st->fine_sw;
+    qp.pw_pool = (const bf16_t*)pools->pw_pool;
+    qp.psw_pool = (const bf16_t*)pools->psw_pool;
+    qp.pool_pcap = pools->pool_pcap;
+    qp.tiles = dplan + off_read;
+    qp.n_tiles = (int)n_read;
+    qp.qsel = pools->qsel;
+    qp.qsel_words = pools->qsel_words;
+    qp.first_epoch = (int)first_epoch;
+    qp.B = st->batch;
+    qp.H = st->heads;
+    qp.T = T;
+    qp.group = G;
+    qp.fine_cap = st->fine_cap;
+    e = tao::launch_route_queries(qp, D, s);
+    if (e != hipSuccess) return check_hip(e, "tao_prefill per-query routes");
+  }
   tao::ReadTilesParams rt;
   rt.rq = view(tok->raw_q, tok->rq_s);
   rt.bank = (const bf16_t*)st->bank_c;
@@ -653,6 +691,9 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   rt.sel_cap = st->sel_cap;
   rt.coarse_pool = coarse_reads ? (const bf16_t*)pools->coarse_pool : nullptr;
   rt.coarse_first = coarse_reads ? (int)c_first : 0;
+  rt.qsel = query_routes && need_pools ? pools->qsel : nullptr;
+  rt.qsel_words = query_routes && need_pools ? pools->qsel_words : 0;
+  rt.first_epoch = (int)first_epoch;
   e = tao::launch_read_tiles(rt, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill read");
   tao::AppendParams app;

@@ -71,7 +71,9 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
 
   const int nq = min(max(count - wave * 32, 0), 32);
   const bool qvalid = li < nq;
-  const long long qtok = first + wave * 32 + (nq > 0 ? min(li, nq - 1) : 0);
+  // A wave past the tile's last query (nq == 0) loads the tile's first row:
+  // first + 32 * wave may lie beyond the operand.
+  const long long qtok = first + (nq > 0 ? wave * 32 + min(li, nq - 1) : 0);
   const long long qpos = p.qpos0 + qtok;
   const long long wave_last = p.qpos0 + first + wave * 32 + nq - 1;
   const long long wave_first = p.qpos0 + first + wave * 32;

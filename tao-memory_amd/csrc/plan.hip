@@ -165,3 +165,96 @@ extern "C" int tao_prefill_plan(const tao_stream_cfg* cfg, int64_t pos0, int64_t
   for (int64_t v : reads) *o++ = v;
   return TAO_OK;
 }
+
+// Full-sequence read (tao_attention forward, operator.py:40-52): the tiling
+// of read_training (tao_stream.py:668-757) and _local_training_corrected_4k
+// (:760-787) as a tao_prefill plan for a fresh state. Tile t = tokens
+// [F t, min(T, F t + F)) attends suffix-causally to keys from
+// max(0, F t - local_keep) (the corrected-4k windows and the ragged fallback
+// are the same windows), reads the first max(0, t - local_keep / F) sealed
+// fines, and every query routes itself (route_interval = 1). The blocks the
+// last tile can read are written; the ring is left empty.
+extern "C" int tao_train_plan(const tao_stream_cfg* cfg, int64_t tokens, int64_t* plan,
+                              int64_t plan_cap, int64_t* info) {
+  using namespace tao::sched;
+  if (!cfg || !info) {
+    tao::set_error("null plan argument");
+    return TAO_E_ARGUMENT;
+  }
+  const tao_stream_cfg& c = *cfg;
+  if (c.fine_tokens <= 0 || c.local_keep < 0 || c.local_keep % c.fine_tokens ||
+      c.coarse_group <= 0 || tokens < 0) {
+    tao::set_error("invalid plan geometry");
+    return TAO_E_ARGUMENT;
+  }
+  const int64_t ft = c.fine_tokens, group = c.coarse_group;
+  const int64_t lag = c.local_keep / ft;                 // config.visibility_tiles
+  const int64_t n_tiles = (tokens + ft - 1) / ft;
+  const int64_t visible_max = n_tiles - 1 - lag > 0 ? n_tiles - 1 - lag : 0;
+  std::vector<int64_t> attn, reads;
+  int64_t history = 0, c_lo = 0, c_hi = 0;
+  for (int64_t t = 0; t < n_tiles; ++t) {
+    const int64_t s = t * ft, e = s + ft < tokens ? s + ft : tokens;
+    const int64_t key_start = s > c.local_keep ? s - c.local_keep : 0;
+    for (int64_t qs = s; qs < e; qs += kAttnTile)
+      attn.insert(attn.end(), {qs, e - qs < kAttnTile ? e - qs : kAttnTile, key_start});
+    const int64_t visible = t > lag ? t - lag : 0;
+    int64_t coarse = 0, eligible = 0, selected = 0;
+    if (visible) {
+      routed_counts(c, visible / group, visible % group, &coarse, &eligible, &selected);
+      ++history;
+      const int64_t completed = visible / group;
+      if (completed >= 1) {
+        if (c_lo == 0 || completed < c_lo) c_lo = completed;
+        if (completed > c_hi) c_hi = completed;
+      }
+    }
+    for (int64_t qs = s; qs < e; qs += kReadTile) {
+      const int64_t n = e - qs < kReadTile ? e - qs : kReadTile;
+      if (visible)
+        reads.insert(reads.end(), {qs, n, coarse, selected, visible - 1, (visible / group) * group,
+                                   1, visible / group});
+      else
+        reads.insert(reads.end(), {qs, n, 0, 0, 0, 0, 0, 0});
+    }
+  }
+  const int64_t len = TAO_PLAN_HEADER + (int64_t)attn.size() + visible_max + (int64_t)reads.size();
+  info[0] = len;
+  info[1] = visible_max;                    // epochs 1 .. visible_max
+  info[2] = 0;                              // no turns
+  info[3] = 0;
+  info[4] = 0;
+  info[5] = visible_max / group + 1;        // page capacity of the epoch pools
+  info[6] = history;                        // tiles that read history
+  info[7] = n_tiles;
+  info[8] = c_lo;
+  info[9] = c_lo ? c_hi - c_lo + 1 : 0;
+  info[10] = visible_max;                   // fines written
+  info[11] = (visible_max + 31) / 32;       // bitmask words per query
+  if (!plan) return TAO_OK;
+  if (plan_cap < len) {
+    tao::set_error("plan buffer too small");
+    return TAO_E_WORKSPACE;
+  }
+  int64_t* h = plan;
+  for (int i = 0; i < TAO_PLAN_HEADER; ++i) h[i] = 0;
+  h[TAO_PLAN_POS0] = 0;
+  h[TAO_PLAN_ATTN_TILES] = (int64_t)attn.size() / 3;
+  h[TAO_PLAN_WRITES] = visible_max;
+  h[TAO_PLAN_FIRST_SLOT] = 0;
+  h[TAO_PLAN_FIRST_PAGE] = 0;
+  h[TAO_PLAN_PAGES] = visible_max / group;
+  h[TAO_PLAN_FIRST_EPOCH] = visible_max ? 1 : 0;
+  h[TAO_PLAN_EPOCHS] = visible_max;
+  h[TAO_PLAN_TURNS] = 0;
+  h[TAO_PLAN_READ_TILES] = (int64_t)reads.size() / 8;
+  h[TAO_PLAN_RING_FIRST] = tokens;
+  h[TAO_PLAN_RING_COUNT] = 0;
+  h[TAO_PLAN_RING_POS] = tokens;
+  h[TAO_PLAN_QUERY_ROUTES] = 1;
+  int64_t* o = plan + TAO_PLAN_HEADER;
+  for (int64_t v : attn) *o++ = v;
+  for (int64_t f = 0; f < visible_max; ++f) *o++ = ft * f;
+  for (int64_t v : reads) *o++ = v;
+  return TAO_OK;
+}

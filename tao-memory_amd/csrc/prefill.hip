@@ -103,6 +103,13 @@ __global__ __launch_bounds__(kThreads) void epochs_kernel(EpochParams p) {
 // coarse value branch (COARSE), each e-tile of a tile whose chunk has
 // completed pages also runs 8 MFMAs of the wave's h against the folded
 // coarse matrix of its page count (coarse.hip) before the fusion.
+//
+// PERQ (the full-sequence read, every query routed by itself): selections
+// are per-query bitmasks (route_queries_kernel). The union and the per-wave
+// masks come from the OR of the wave's bitmasks, and each A row is zeroed
+// unless its own query selected the fine, so a wave's 32 queries still share
+// every staged C^T and MFMA; the numerator and denominator of a query sum
+// exactly its selected fines (selected_read.py:156-173).
 constexpr int kGroupWaves = 8;
 constexpr int kGroupThreads = 64 * kGroupWaves;
 constexpr int kBitWords = kMaxFineIds / 32;
@@ -114,6 +121,7 @@ struct GroupSmem {
     struct {
       uint32_t bits[kBitWords];
       int pre[kBitWords];
+      uint32_t wbits[kGroupWaves][kBitWords];   // PERQ: OR of each wave's bitmasks
     } setup;
     bf16_t c[2][D][D + 8];        // staged C^T, rows padded by 16 bytes
   } u;
@@ -134,7 +142,7 @@ TAO_DEV void unpack8f(const uint4& u, float out[8]) {
   }
 }
 
-template <int D, bool COARSE>
+template <int D, bool COARSE, bool PERQ>
 __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesParams p) {
   constexpr int KK = D / 16, ET = D / 32, CPR = D / 8;   // k-steps, e-tiles, uint4 per row
   constexpr int CPT = D * CPR / kGroupThreads;           // C^T uint4 per thread
@@ -170,16 +178,37 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
   // ---- union of the selected sets (ascending fine id) and per-wave masks
   for (int i = tid; i < kBitWords; i += kGroupThreads) sm.u.setup.bits[i] = 0;
   for (int i = tid; i < kMaxUnion / 4; i += kGroupThreads) sm.mask[i] = 0;
-  if (reads) {
+  // PERQ: this lane's query bitmask (rows li >= nq select nothing).
+  const uint32_t* qbits = nullptr;
+  if constexpr (PERQ) {
+    for (int i = tid; i < kGroupWaves * kBitWords; i += kGroupThreads)
+      (&sm.u.setup.wbits[0][0])[i] = 0u;
+    if (reads)
+      qbits = p.qsel + ((size_t)(b * p.T + q_first + min(li, nq - 1)) * p.H + h) * p.qsel_words;
+  } else if (reads) {
     const int32_t* sel = p.sel_pool + ((size_t)slot * BH + bh) * p.sel_cap;
     for (int m = lane; m < M; m += 64) sm.ids[w][m] = sel[m];
   }
   __syncthreads();
-  if (reads)
+  if constexpr (PERQ) {
+    if (reads) {
+      const int words = (p.first_epoch + erel + 31) >> 5;
+      for (int i = 0; i < words; ++i) {
+        uint32_t v = (lane < 32 && li < nq) ? qbits[i] : 0u;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) v |= __shfl_xor(v, off, 64);
+        if (lane == 0) {
+          sm.u.setup.wbits[w][i] = v;
+          atomicOr(&sm.u.setup.bits[i], v);
+        }
+      }
+    }
+  } else if (reads) {
     for (int m = lane; m < M; m += 64) {
       const int id = sm.ids[w][m];
       atomicOr(&sm.u.setup.bits[id >> 5], 1u << (id & 31));
     }
+  }
   __syncthreads();
   if (w == 0) {
     constexpr int WPL = kBitWords / 64;
@@ -203,11 +232,18 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
     int r = sm.u.setup.pre[i];
     while (bits) {
       const int bit = __ffs(bits) - 1;
-      sm.uni[r++] = i * 32 + bit;
+      sm.uni[r] = i * 32 + bit;
+      if constexpr (PERQ) {
+        uint32_t byte = 0;
+#pragma unroll
+        for (int v = 0; v < kGroupWaves; ++v) byte |= ((sm.u.setup.wbits[v][i] >> bit) & 1u) << v;
+        atomicOr(&sm.mask[r >> 2], byte << ((r & 3) * 8));
+      }
+      ++r;
       bits &= bits - 1;
     }
   }
-  if (reads)
+  if (!PERQ && reads)
     for (int m = lane; m < M; m += 64) {
       const int id = sm.ids[w][m];
       const uint32_t word = sm.u.setup.bits[id >> 5];
@@ -316,10 +352,22 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
   uint4 tpk[KK];
   int cached_page = -1;
   const bf16x8 ones = as_bf16x8(make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u));
+  // PERQ: the lane's bitmask word of the current fine (ids ascend).
+  int qword_at = -1;
+  uint32_t qword = 0u;
   auto consume = [&](int u) __attribute__((always_inline)) {
     if (!active(u)) return;
     const int buf = u & 1;
     const int page = sm.uni[u] / p.group;
+    uint32_t keep = 0xFFFFFFFFu;
+    if constexpr (PERQ) {
+      const int id = sm.uni[u];
+      if ((id >> 5) != qword_at) {
+        qword_at = id >> 5;
+        qword = li < nq ? qbits[qword_at] : 0u;
+      }
+      keep = ((qword >> (id & 31)) & 1u) ? 0xFFFFFFFFu : 0u;
+    }
     if (page != cached_page) {
       const bf16_t* pwr = sm.pwsw[w][buf][0];
 #pragma unroll
@@ -345,7 +393,8 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
       unpack8f(*(const uint4*)(swr + d0), sv);
       uint32_t ch[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) ch[j] = pack_bf16x2(tv[2 * j] * sv[2 * j], tv[2 * j + 1] * sv[2 * j + 1]);
+      for (int j = 0; j < 4; ++j)
+        ch[j] = pack_bf16x2(tv[2 * j] * sv[2 * j], tv[2 * j + 1] * sv[2 * j + 1]) & keep;
       const bf16x8 a = as_bf16x8(make_uint4(ch[0], ch[1], ch[2], ch[3]));
 #pragma unroll
       for (int t = 0; t < ET; ++t) {
@@ -487,16 +536,25 @@ hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t
   const int groups = (p.n_tiles + kGroupWaves - 1) / kGroupWaves;
   const dim3 grid((unsigned)(groups * p.B * p.H));
   const bool coarse = p.coarse_pool != nullptr;
-  if (head_dim == 128 && coarse)
-    hipLaunchKernelGGL((read_groups_kernel<128, true>), grid, dim3(kGroupThreads), 0, s, p);
-  else if (head_dim == 128)
-    hipLaunchKernelGGL((read_groups_kernel<128, false>), grid, dim3(kGroupThreads), 0, s, p);
-  else if (head_dim == 64 && coarse)
-    hipLaunchKernelGGL((read_groups_kernel<64, true>), grid, dim3(kGroupThreads), 0, s, p);
-  else if (head_dim == 64)
-    hipLaunchKernelGGL((read_groups_kernel<64, false>), grid, dim3(kGroupThreads), 0, s, p);
-  else
-    return hipErrorInvalidValue;
+  const bool perq = p.qsel != nullptr;
+  if (perq && (p.qsel_words < 1 || p.qsel_words > kBitWords)) return hipErrorInvalidValue;
+#define TAO_READ_LAUNCH(D_, C_, Q_)                                                           \
+  hipLaunchKernelGGL((read_groups_kernel<D_, C_, Q_>), grid, dim3(kGroupThreads), 0, s, p)
+  if (head_dim != 128 && head_dim != 64) return hipErrorInvalidValue;
+  if (head_dim == 128) {
+    if (perq) {
+      if (coarse) TAO_READ_LAUNCH(128, true, true); else TAO_READ_LAUNCH(128, false, true);
+    } else {
+      if (coarse) TAO_READ_LAUNCH(128, true, false); else TAO_READ_LAUNCH(128, false, false);
+    }
+  } else {
+    if (perq) {
+      if (coarse) TAO_READ_LAUNCH(64, true, true); else TAO_READ_LAUNCH(64, false, true);
+    } else {
+      if (coarse) TAO_READ_LAUNCH(64, true, false); else TAO_READ_LAUNCH(64, false, false);
+    }
+  }
+#undef TAO_READ_LAUNCH
   return hipGetLastError();
 }
 

@@ -92,6 +92,26 @@ TAO_DEV void wave_masses(const float* h, const bf16_t* pw, const SwRows* sw,
   }
 }
 
+// h = r(softmax_D(raw_q row)) of one query by one wave: fp32 exp correctly
+// rounded, butterfly sum (tao_stream.py:253-254).
+template <int D>
+TAO_DEV void query_weights(const bf16_t* rq, int lane, float* h) {
+  constexpr int PER = D / 64;
+  float x[PER], e[PER];
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int k = 0; k < PER; ++k) { x[k] = bf2f(rq[lane + 64 * k]); mx = fmaxf(mx, x[k]); }
+  mx = wave_max(mx);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) e[k] = exp_cr(x[k] - mx);
+  float s = e[0];
+#pragma unroll
+  for (int k = 1; k < PER; ++k) s += e[k];
+  s = wave_sum_fold(s);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) h[lane + 64 * k] = rbf(e[k] / s);
+}
+
 // Stable descending selection of the top `count` keys (unique 64-bit keys:
 // score << 32 | ~index). Writes the selected keys, best first, to dst.
 __device__ void select_top(unsigned long long* keys, int n, int count,
@@ -155,22 +175,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteParams p) {
     swr.split = K * p.group;
   }
 
-  if (wave == 0) {
-    const bf16_t* rq = p.rq + b * p.rq_sb + anchor * p.rq_st + h * p.rq_sh;
-    float x[PER], e[PER];
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int k = 0; k < PER; ++k) { x[k] = bf2f(rq[lane + 64 * k]); mx = fmaxf(mx, x[k]); }
-    mx = wave_max(mx);
-#pragma unroll
-    for (int k = 0; k < PER; ++k) e[k] = exp_cr(x[k] - mx);
-    float s = e[0];
-#pragma unroll
-    for (int k = 1; k < PER; ++k) s += e[k];
-    s = wave_sum_fold(s);
-#pragma unroll
-    for (int k = 0; k < PER; ++k) sm.h[lane + 64 * k] = rbf(e[k] / s);
-  }
+  if (wave == 0) query_weights<D>(p.rq + b * p.rq_sb + anchor * p.rq_st + h * p.rq_sh, lane, sm.h);
   __syncthreads();
 
   // ---- coarse pages: stable top-`coarse` by page mass, then ascending.
@@ -247,7 +252,153 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteParams p) {
   if (write_state && bh == 0 && tid == 0) p.header[1] = selected;
 }
 
+// ---------------------------------------------------------------------------
+// Per-query routes of the full-sequence read (route_interval = 1 in
+// _read_training_group, tao_stream.py:596-665, with candidate_scores,
+// routing_scores.py:7-47): every history query of a read tile routes itself
+// against its tile's epoch with route_kernel's arithmetic and reduction
+// order (same candidates, masses and stable top-k), and its selection is
+// written as a bitmask over fine ids; the read needs the set, not the order.
+// One 256-thread workgroup per (read tile, batch, head); wave w routes
+// queries w, w + 4, ... of the tile. Every wave runs the same number of
+// rounds, so the barriers that publish its LDS keys are workgroup-uniform.
+constexpr int kQThreads = 256;
+constexpr int kQWaves = kQThreads / 64;
+constexpr int kQMaxWords = 512;          // bitmask words per query (16384 fines)
+
+template <int D>
+struct QueryRouteSmem {
+  float h[kQWaves][D];
+  unsigned long long keys[kQWaves][kQueryRouteMaxKeys];
+  int chosen[kQWaves][kQueryRouteMaxKeys / 8];
+  uint32_t bits[kQWaves][kQMaxWords];
+};
+
+// Number of keys larger than `mine` among keys[0, n) (keys are unique).
+TAO_DEV int key_rank(const unsigned long long* keys, int n, unsigned long long mine) {
+  int r = 0;
+  for (int j = 0; j < n; ++j) r += keys[j] > mine;
+  return r;
+}
+
+template <int D>
+__global__ __launch_bounds__(kQThreads) void route_queries_kernel(QueryRouteParams p) {
+  __shared__ QueryRouteSmem<D> sm;
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int64_t* desc = p.tiles + 8 * (blockIdx.x / BH);
+  if (!desc[6]) return;                          // no history: workgroup-uniform
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int q_first = (int)desc[0], nq = (int)desc[1];
+  const int coarse = (int)desc[2], M = (int)desc[3], erel = (int)desc[4];
+  const int G = p.group;
+  const int epoch = p.first_epoch + erel;
+  const int K = epoch / G, pending = epoch % G;
+  const int E = G * coarse + pending;
+  const int words = (epoch + 31) >> 5;
+  const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
+  const SwRows swr{p.sw + (size_t)bh * p.fine_cap * D,
+                   p.psw_pool + ((size_t)erel * BH + bh) * 8 * D, K * G};
+  float* hw = sm.h[w];
+  unsigned long long* keys = sm.keys[w];
+  int* chosen = sm.chosen[w];
+  uint32_t* bits = sm.bits[w];
+  auto cand = [&](int j, int& page, int& id) __attribute__((always_inline)) {
+    if (j < G * coarse) {
+      page = chosen[j / G];
+      id = page * G + j % G;
+    } else {
+      page = K;
+      id = K * G + (j - G * coarse);
+    }
+  };
+  const int rounds = (nq + kQWaves - 1) / kQWaves;
+  for (int r = 0; r < rounds; ++r) {
+    const int qi = r * kQWaves + w;
+    const bool on = qi < nq;
+    const int t = q_first + (on ? qi : 0);
+    if (on) query_weights<D>(p.rq + b * p.rq_sb + (int64_t)t * p.rq_st + h * p.rq_sh, lane, hw);
+    for (int i = lane; i < words; i += 64) bits[i] = 0u;
+    __syncthreads();
+    // ---- page masses of the completed pages
+    if (on && coarse > 0)
+      for (int base = 0; base < K; base += kBatch) {
+        int pages[kBatch];
+        float mass[kBatch];
+        const int count = min(kBatch, K - base);
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) pages[i] = base + min(i, count - 1);
+        wave_masses<D>(hw, pw, nullptr, pages, pages, count, lane, mass);
+        if (lane < count) {
+          float mine = mass[0];
+#pragma unroll
+          for (int i = 1; i < kBatch; ++i) if (lane == i) mine = mass[i];
+          keys[base + lane] = score_key(mine, base + lane);
+        }
+      }
+    __syncthreads();
+    // ---- stable top-`coarse` pages, listed ascending
+    if (on && coarse > 0) {
+      int placed = 0;
+      for (int c0 = 0; c0 < K; c0 += 64) {
+        const int i = c0 + lane;
+        const bool pick = i < K && key_rank(keys, K, keys[i]) < coarse;
+        const unsigned long long ball = __ballot(pick);
+        if (pick) chosen[placed + __popcll(ball & ((1ull << lane) - 1ull))] = i;
+        placed += __popcll(ball);
+      }
+    }
+    __syncthreads();
+    // ---- candidate masses: 8 fines of each chosen page, then the pending fines
+    if (on)
+      for (int base = 0; base < E; base += kBatch) {
+        int pages[kBatch], ids[kBatch];
+        float mass[kBatch];
+        const int count = min(kBatch, E - base);
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) cand(base + min(i, count - 1), pages[i], ids[i]);
+        wave_masses<D>(hw, pw, &swr, pages, ids, count, lane, mass);
+        if (lane < count) {
+          float mine = mass[0];
+#pragma unroll
+          for (int i = 1; i < kBatch; ++i) if (lane == i) mine = mass[i];
+          keys[base + lane] = score_key(mine, base + lane);
+        }
+      }
+    __syncthreads();
+    // ---- stable top-M candidates -> bitmask
+    if (on)
+      for (int j = lane; j < E; j += 64)
+        if (key_rank(keys, E, keys[j]) < M) {
+          int page, id;
+          cand(j, page, id);
+          atomicOr(&bits[id >> 5], 1u << (id & 31));
+        }
+    __syncthreads();
+    if (on) {
+      uint32_t* dst = p.qsel + ((size_t)(b * p.T + t) * p.H + h) * p.qsel_words;
+      for (int i = lane; i < words; i += 64) dst[i] = bits[i];
+    }
+    __syncthreads();                             // h, keys and bits are reused
+  }
+}
+
 }  // namespace
+
+hipError_t launch_route_queries(const QueryRouteParams& p, int head_dim, hipStream_t s) {
+  if (p.n_tiles <= 0) return hipSuccess;
+  if (p.qsel_words < 1 || p.qsel_words > kQMaxWords || p.group != 8)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(p.n_tiles * p.B * p.H));
+  if (head_dim == 128)
+    hipLaunchKernelGGL(route_queries_kernel<128>, grid, dim3(kQThreads), 0, s, p);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL(route_queries_kernel<64>, grid, dim3(kQThreads), 0, s, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
 
 hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s) {
   if (p.completed > kMaxSort || p.group * p.coarse + p.pending > kMaxSort)

@@ -171,6 +171,21 @@ struct RouteParams {
 };
 hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s);
 
+// Per-query routes of the full-sequence read: every history query of a read
+// tile routes itself against its tile's epoch; selections are bitmasks
+// qsel[((b * T + t) * H + h) * qsel_words + word].
+struct QueryRouteParams {
+  const bf16_t* rq; int64_t rq_sb, rq_st, rq_sh;
+  const bf16_t* sw;
+  const bf16_t* pw_pool; const bf16_t* psw_pool; int pool_pcap;
+  const int64_t* tiles; int n_tiles;
+  uint32_t* qsel; int qsel_words;
+  int first_epoch;
+  int B, H, T, group, fine_cap;
+};
+hipError_t launch_route_queries(const QueryRouteParams& p, int head_dim, hipStream_t s);
+constexpr int kQueryRouteMaxKeys = 512;   // pages or candidates of one query route
+
 struct WriterParams {
   TokView rk, v;                 // token operands (positions >= new_base)
   const bf16_t* ring_raw; const bf16_t* ring_v;
@@ -235,6 +250,9 @@ struct ReadTilesParams {
   const int64_t* tiles; int n_tiles;
   int B, H, T, group, fine_cap, sel_cap;
   const bf16_t* coarse_pool; int coarse_first;
+  // Per-query selections (plans with query routes): bitmasks as written by
+  // route_queries, the plan's first epoch; null for turn routes.
+  const uint32_t* qsel; int qsel_words; int first_epoch;
 };
 hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t s);
 

@@ -47,7 +47,8 @@ class Tokens(ctypes.Structure):
 class PrefillPools(ctypes.Structure):
     _fields_ = [("pw_pool", _vp), ("psw_pool", _vp), ("sel_pool", _vp),
                 ("pool_pcap", _i32), ("epochs", _i32), ("sel_slots", _i32),
-                ("coarse_pool", _vp), ("coarse_first", _i32), ("coarse_count", _i32)]
+                ("coarse_pool", _vp), ("coarse_first", _i32), ("coarse_count", _i32),
+                ("qsel", _vp), ("qsel_words", _i32)]
 
 
 class StreamCfg(ctypes.Structure):
@@ -91,6 +92,7 @@ _SIGNATURES = {
                          _i64, _vp], _i32),
     "tao_prefill_plan": ([ctypes.POINTER(StreamCfg), _i64, _i64, _i32, _i32, _i32,
                           _vp, _i64, ctypes.POINTER(_i64)], _i32),
+    "tao_train_plan": ([ctypes.POINTER(StreamCfg), _i64, _vp, _i64, ctypes.POINTER(_i64)], _i32),
     "tao_stream_open": ([ctypes.POINTER(StateDev), ctypes.POINTER(StreamCfg), _i64, _i32, _i32,
                          _vp, _vp, ctypes.POINTER(_vp)], _i32),
     "tao_stream_sync": ([_vp, ctypes.POINTER(StateDev), _i64, _i32, _i32], _i32),

@@ -8,6 +8,7 @@ The streaming path is bf16 on an MI355X device with width 64 or 128.
 
 import torch  # noqa: F401
 
+from . import training
 from .config import TaoConfig
 from .flash_attention import flash_attn
 from .tao_stream import StreamCache
@@ -17,14 +18,14 @@ DEFAULT_CONFIG = TaoConfig()
 
 def tao_attention(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b, alpha,
                   config=DEFAULT_CONFIG, local_flash=None):
-    """Full differentiable sequence read with fresh routing at every query.
+    """Full sequence read with fresh routing at every query (operator.py:40-52).
 
-    operator.py:42-54 in the reference. Its HIP forward/backward kernels are
-    not built yet; the call raises instead of falling back to another path.
+    Forward on the HIP library (training.py); its backward is not built and
+    raises when autograd reaches it.
     """
-    raise NotImplementedError(
-        "tao_attention (full-sequence training path) is not yet implemented on "
-        "the HIP path; use tao_attention_prefill / tao_attention_decode")
+    _check_plugin(local_flash)
+    return training.full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b,
+                                       alpha, config)
 
 
 def new_state(layer_index, config=DEFAULT_CONFIG):

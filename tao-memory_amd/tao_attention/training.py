@@ -1,0 +1,136 @@
+"""Full-sequence read: the forward of ``tao_attention`` on the HIP library.
+
+Reference: ``tao_attention`` (operator.py:40-52) = ``read_training``
+(tao_stream.py:668-757) with ``route_interval=1`` followed by
+``_fuse_training`` (operator.py:21-38).
+
+The full-sequence read is the streaming prefill of the same tokens with a
+route refresh at every query: tile t (256 tokens) attends to the keys the
+stream's local ring holds at that point, reads the t - 2 fines the stream
+has sealed, and the fusion presence flags are the stream's. So the whole
+sequence runs as ONE ``tao_prefill`` on a fresh, call-private device state,
+under a plan from ``tao_train_plan``: local attention for every tile, the
+writer for every visible block, page and epoch summaries, a route for every
+history query (bitmask selections), then the per-query selected read with
+the coarse read and the fusion in its epilogue.
+
+Gradients: the backward kernels (selected-read, writer, local-attention and
+fusion adjoints) are not built; a backward through this op raises.
+"""
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _hip
+from .config import TaoConfig
+
+
+def _check(q, k, v, raw_q, raw_k, config):
+    if config.fine_writer != "softmax":
+        raise NotImplementedError("the HIP path implements the softmax fine writer")
+    if config.fine_tokens != 256 or config.local_keep != 512 or config.coarse_group != 8:
+        raise NotImplementedError(
+            "the HIP path implements fine_tokens=256, local_keep=512, coarse_group=8")
+    shape = q.shape
+    if q.dim() != 4 or any(t.shape != shape for t in (k, v, raw_q, raw_k)):
+        raise ValueError("q, k, v, raw_q and raw_k must share one [B, T, H, D] shape")
+    if any(t.dtype != torch.bfloat16 for t in (q, k, v, raw_q, raw_k)):
+        raise TypeError("the HIP path computes on bf16 operands")
+    if shape[-1] not in (64, 128):
+        raise ValueError("head width must be 64 or 128")
+    for t in (q, k, v, raw_q, raw_k):
+        _hip.require_device(t)
+
+
+def plan(config, tokens):
+    """(int64 plan, info) of the full-sequence read of `tokens` tokens."""
+    lib = _hip.lib()
+    scfg = _hip.StreamCfg(0, config.local_keep, config.fine_tokens, config.coarse_group,
+                          config.route_period, config.layer_stagger,
+                          config.budget_root_scale, config.budget_offset, 0)
+    info = (ctypes.c_int64 * 12)()
+    _hip.check(lib.tao_train_plan(ctypes.byref(scfg), tokens, None, 0, info))
+    words = np.empty(info[0], dtype=np.int64)
+    _hip.check(lib.tao_train_plan(ctypes.byref(scfg), tokens, words.ctypes.data, info[0], info))
+    keys = ("length", "epochs", "turns", "route_coarse", "route_size", "pool_pcap",
+            "history_tiles", "tiles", "coarse_first", "coarse_count", "fines", "qsel_words")
+    return words, dict(zip(keys, info))
+
+
+def forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_routes=False):
+    """Fused heads [B, T, H, D] of the full-sequence read (no autograd).
+
+    With return_routes, also the per-query selections: int32 [B, T, H, W]
+    bitmask words over fine ids (bit f of word f // 32) for queries with
+    history, zero before first_fine.
+    """
+    from .tao_stream import _DeviceState
+
+    _check(q, k, v, raw_q, raw_k, config)
+    b, tokens, heads, d = q.shape
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    if tokens == 0:
+        return (out, None) if return_routes else out
+    words_plan, info = plan(config, tokens)
+    fines = info["fines"]
+    dev = _DeviceState(config, b, heads, d, q.device, max(fines, 8))
+    dev.ensure_plan(len(words_plan))
+    q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
+    tok = _hip.tokens(q, k, v, raw_q, raw_k)
+    fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
+    local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    pools = _hip.PrefillPools()
+    keep = []
+    qsel = None
+    if info["epochs"]:
+        pcap = info["pool_pcap"]
+        pw_pool = torch.empty((info["epochs"], b, heads, pcap, d), dtype=torch.bfloat16,
+                              device=q.device)
+        psw_pool = torch.empty((info["epochs"], b, heads, config.coarse_group, d),
+                               dtype=torch.bfloat16, device=q.device)
+        qsel = torch.zeros((b, tokens, heads, info["qsel_words"]), dtype=torch.int32,
+                           device=q.device)
+        pools.pw_pool, pools.psw_pool = pw_pool.data_ptr(), psw_pool.data_ptr()
+        pools.pool_pcap, pools.epochs = pcap, info["epochs"]
+        pools.qsel, pools.qsel_words = qsel.data_ptr(), info["qsel_words"]
+        keep = [pw_pool, psw_pool]
+        if dev.coarse_values and info["coarse_count"]:
+            coarse_pool = torch.empty((info["coarse_count"], b, heads, d, d),
+                                      dtype=torch.bfloat16, device=q.device)
+            pools.coarse_pool = coarse_pool.data_ptr()
+            pools.coarse_first = info["coarse_first"]
+            pools.coarse_count = info["coarse_count"]
+            keep.append(coarse_pool)
+    plan_arr = words_plan.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
+    out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
+    _hip.check(_hip.lib().tao_prefill(
+        ctypes.byref(dev.struct), ctypes.byref(tok), ctypes.byref(fu), plan_arr,
+        len(words_plan), ctypes.byref(pools), local.data_ptr(), out.data_ptr(), out_s,
+        dev.stream()))
+    del keep, dev      # the caching allocator keeps them stream-ordered
+    return (out, qsel) if return_routes else out
+
+
+class _FullSequenceRead(torch.autograd.Function):
+    """Autograd node of the full-sequence read; its backward is not built."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config):
+        return forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config)
+
+    @staticmethod
+    def backward(ctx, grad):
+        raise NotImplementedError(
+            "tao_attention backward (selected-read, writer, local-attention and fusion "
+            "adjoints) is not implemented on the HIP path")
+
+
+def full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
+                       config=None):
+    config = config or TaoConfig()
+    tensors = (q, k, v, raw_q, raw_k, fusion_a, fusion_b)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+        return _FullSequenceRead.apply(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config)
+    return forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config)

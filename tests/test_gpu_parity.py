@@ -409,3 +409,85 @@ def test_snapshot_interop_with_oracle_through_torch_save(device, coarse):
         start += w
     torch.testing.assert_close(got2.cpu().float(), torch.cat(want2, 1).float(), **TOL)
     compare_snapshots(hip2.export(), ora2.export())
+
+
+# ------------------------------------------------------------- full sequence
+
+def _bitmask_sets(qsel):
+    """int32 bitmask words [B, T, H, W] -> bool [B, T, H, 32 W]."""
+    words = qsel.cpu().to(torch.int64) & 0xFFFFFFFF
+    bits = (words.unsqueeze(-1) >> torch.arange(32)) & 1
+    return bits.reshape(*words.shape[:3], -1).bool()
+
+
+@pytest.mark.parametrize("tokens,heads,width,index_only,seed", [
+    (2100, 2, 64, True, 31), (2900, 2, 128, False, 32), (3000, 3, 64, False, 33)])
+def test_full_sequence_read_matches_oracle(tokens, heads, width, index_only, seed):
+    """tao_attention forward (per-query routes, per-query selected read, coarse
+    read, fusion) against the oracle's read_training restatement: every
+    query's selected set bit-exact, outputs within the bf16 tolerance."""
+    from tao_attention import TaoConfig, tao_attention, training
+    xs, fa, fb = inputs(tokens, heads, width, seed)
+    cfg = TaoConfig(coarse_index_only=index_only)
+    q, k, v, rq, rk = to_dev(xs, "cuda")
+    fa_d, fb_d = fa.cuda(), fb.cuda()
+    out, qsel = training.forward(q, k, v, rq, rk, fa_d, fb_d, 0.5, cfg, return_routes=True)
+    ref, routes = O.training_forward(*xs, fa, fb, 0.5, O.Geometry.from_config(cfg),
+                                     return_routes=True)
+    got = _bitmask_sets(qsel)
+    assert routes
+    for tile, sel in routes.items():
+        s = tile * 256
+        part = got[:, s:s + sel.shape[1]]
+        want = torch.zeros_like(part)
+        want.scatter_(-1, sel, True)
+        assert torch.equal(part, want), f"selected sets of tile {tile}"
+    assert not got[:, :768].any()
+    torch.testing.assert_close(out.cpu().float(), ref.float(), **TOL)
+    api = tao_attention(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa_d, fusion_b=fb_d,
+                        alpha=0.5, config=cfg)
+    assert torch.equal(api, out)
+
+
+def test_full_sequence_read_short_and_training_shape():
+    """Below first_fine the output is the tiled local attention (oracle);
+    at the training shape (B2, T8192, H12, D64) every history query selects
+    exactly M of its tile's visible fines and the read is deterministic."""
+    from tao_attention import TaoConfig, tao_attention, training
+    cfg = TaoConfig()
+    xs, fa, fb = inputs(700, 2, 128, 34)
+    q, k, v, rq, rk = to_dev(xs, "cuda")
+    out = tao_attention(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.cuda(), fusion_b=fb.cuda(),
+                        alpha=0.5, config=cfg)
+    ref = O.training_forward(*xs, fa, fb, 0.5, O.Geometry.from_config(cfg))
+    torch.testing.assert_close(out.cpu().float(), ref.float(), **TOL)
+    g = torch.Generator(device="cuda").manual_seed(35)
+    b, t, h, d = 2, 8192, 12, 64
+    xs = [torch.randn(b, t, h, d, generator=g, device="cuda").to(BF16) for _ in range(5)]
+    fa = torch.randn(h, d, 3, generator=g, device="cuda") * 0.02
+    fb = torch.randn(h, d, 3, generator=g, device="cuda") * 0.02
+    out, qsel = training.forward(*xs, fa, fb, 0.5, cfg, return_routes=True)
+    again = training.forward(*xs, fa, fb, 0.5, cfg)
+    assert torch.equal(out, again)
+    assert torch.isfinite(out.float()).all()
+    counts = _bitmask_sets(qsel).sum(-1)                     # [B, T, H]
+    geo = O.Geometry.from_config(cfg)
+    for tile in range(t // 256):
+        visible = max(0, tile - 2)
+        m = geo.routed_counts(visible // 8, visible % 8)[2] if visible else 0
+        assert bool((counts[:, tile * 256:(tile + 1) * 256] == m).all()), tile
+    first = O.training_forward(*(x[:1, :768, :2].cpu() for x in xs), fa[:2].cpu(),
+                               fb[:2].cpu(), 0.5, geo)
+    torch.testing.assert_close(out[:1, :768, :2].cpu().float(), first.float(), **TOL)
+
+
+def test_full_sequence_read_backward_is_not_built():
+    from tao_attention import TaoConfig, tao_attention
+    xs, fa, fb = inputs(300, 2, 64, 36)
+    q, k, v, rq, rk = to_dev(xs, "cuda")
+    q.requires_grad_(True)
+    out = tao_attention(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.cuda(), fusion_b=fb.cuda(),
+                        alpha=0.5, config=TaoConfig())
+    assert out.requires_grad
+    with pytest.raises((NotImplementedError, RuntimeError), match="backward"):
+        out.float().sum().backward()

@@ -82,7 +82,7 @@ def test_library_exports_every_header_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert sorted(_hip.EXPORTED) == declared
-    assert lib.tao_abi_version() == 3
+    assert lib.tao_abi_version() == 4
 
 
 def test_workspace_size_and_error_convention():
@@ -214,3 +214,45 @@ def test_native_prefill_plan_matches_closed_forms():
     buf = np.zeros(4, dtype=np.int64)
     assert lib.tao_prefill_plan(ctypes.byref(scfg), 0, 300, 0, 0, 1, buf.ctypes.data, 4,
                                 small) < 0
+
+
+def test_native_train_plan_matches_read_training_tiling():
+    """tao_train_plan against read_training's tiling written out from the
+    closed forms (tao_stream.py:668-787): 256-token tiles with local keys
+    from max(0, 256 t - 512), t - 2 visible fines, the routed counts of each
+    tile's epoch, every query routing itself, no ring append."""
+    import numpy as np
+    from tao_attention import training
+    g = O.Geometry()
+    for cfg in (TaoConfig(), index_only_page_memo()):
+        for tokens in (0, 1, 255, 700, 768, 769, 1000, 1024, 2900, 8192, 16385):
+            plan, info = training.plan(cfg, tokens)
+            n_tiles = -(-tokens // 256)
+            vmax = max(0, n_tiles - 3)
+            h = plan[:16]
+            assert h[13] == 1 and h[8] == 0 and h[0] == 0
+            assert (h[10], h[11], h[12]) == (tokens, 0, tokens)
+            assert h[2] == vmax and h[5] == vmax // 8
+            assert (h[6], h[7]) == ((1, vmax) if vmax else (0, 0))
+            assert info["fines"] == vmax and info["qsel_words"] == (vmax + 31) // 32
+            off = 16
+            attn = plan[off:off + 3 * h[1]].reshape(-1, 3)
+            off += 3 * h[1]
+            want = [(s, min(256, tokens - s), max(0, s - 512)) for s in range(0, tokens, 256)]
+            assert [tuple(r) for r in attn.tolist()] == want
+            assert plan[off:off + h[2]].tolist() == [256 * f for f in range(vmax)]
+            off += h[2]
+            reads = plan[off:].reshape(-1, 8)
+            assert len(reads) == h[9] and off + 8 * h[9] == len(plan) == info["length"]
+            starts = []
+            for first, n, coarse, m, erel, split, on, cpages in reads.tolist():
+                starts.append(first)
+                visible = max(0, first // 256 - 2)
+                assert n == min(32, tokens - first, 256 - first % 256)
+                if not visible:
+                    assert (coarse, m, erel, split, on, cpages) == (0, 0, 0, 0, 0, 0)
+                    continue
+                c, _, sel = g.routed_counts(visible // 8, visible % 8)
+                assert (coarse, m, erel, split, on, cpages) == (
+                    c, sel, visible - 1, (visible // 8) * 8, 1, visible // 8)
+            assert starts == list(range(0, tokens, 32))

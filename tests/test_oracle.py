@@ -435,3 +435,57 @@ def test_diagnostics_counters_match_reference_accounting(coarse, memo):
     assert s.diag["fine_matrix_contractions"] > 0 and s.diag["route_query_heads"] > 0
     if coarse:
         assert s.diag["coarse_matrix_contractions"] > 0
+
+
+# ------------------------------------------------------------- full sequence
+
+def _brute_local(q, k, v, tile=256, keep=512):
+    """Per-query fp64 softmax over keys [max(0, tile_start - keep), i]."""
+    b, t, heads, d = q.shape
+    out = torch.empty(b, t, heads, d, dtype=torch.float64)
+    for i in range(t):
+        lo = max(0, (i // tile) * tile - keep)
+        s = torch.einsum("bhd,bkhd->bhk", q[:, i].double(), k[:, lo:i + 1].double()) / math.sqrt(d)
+        out[:, i] = torch.einsum("bhk,bkhd->bhd", torch.softmax(s, -1), v[:, lo:i + 1].double())
+    return out.to(q.dtype)
+
+
+def test_training_forward_short_prefix_is_exact_local_attention():
+    """Below first_fine the full-sequence read is the tiled local attention
+    (read_training :682-688, _local_training_corrected_4k ragged fallback)."""
+    xs, fa, fb = _stream_inputs(700, seed=8)
+    q, k, v, rq, rk = xs
+    out = O.training_forward(q, k, v, rq, rk, fa, fb, 0.5, O.Geometry())
+    torch.testing.assert_close(out, _brute_local(q, k, v), atol=1e-2, rtol=0)
+    xs, fa, fb = _stream_inputs(1100, seed=9)
+    q, k, v, rq, rk = xs
+    out = O.training_forward(q, k, v, rq, rk, fa, fb, 0.5, O.Geometry())
+    torch.testing.assert_close(out[:, :768], _brute_local(q, k, v)[:, :768], atol=1e-2, rtol=0)
+
+
+@pytest.mark.parametrize("index_only,tokens", [(True, 2100), (False, 2900)])
+def test_training_forward_is_the_stream_refreshing_at_every_query(index_only, tokens):
+    """read_training(route_interval=1) equals the streaming read with a route
+    refresh at every query: the stream's local ring equals the tile windows,
+    its epoch at a chunk equals tile - 2 visible fines, and routing, read,
+    coarse read and fusion presence are the same functions. A stream with
+    route_period=1 therefore gives identical bits; with the default period
+    only the first refresh position agrees."""
+    xs, fa, fb = _stream_inputs(tokens, seed=7)
+    q, k, v, rq, rk = xs
+    g = O.Geometry(coarse_index_only=index_only)
+    out, routes = O.training_forward(q, k, v, rq, rk, fa, fb, 0.5, g, return_routes=True)
+    every = O.Geometry(coarse_index_only=index_only, route_period=1)
+    assert torch.equal(out, _run(O.OracleStream(0, every), xs, fa, fb, [tokens]))
+    streamed = _run(O.OracleStream(0, g), xs, fa, fb, [tokens])
+    assert torch.equal(out[:, :769], streamed[:, :769])
+    assert not torch.equal(out[:, 769:], streamed[:, 769:])
+    # route invariants: M unique ids among the tile's eligible candidates
+    for tile, sel in routes.items():
+        visible = tile - 2
+        completed, pending = divmod(visible, 8)
+        _, _, m = g.routed_counts(completed, pending)
+        assert sel.shape[-1] == m
+        assert int(sel.min()) >= 0 and int(sel.max()) < visible
+        srt = sel.sort(-1).values
+        assert bool((srt[..., 1:] != srt[..., :-1]).all())

@@ -457,6 +457,39 @@ def run_prefill(torch, device, cfg, heads, width, tokens, probe):
                 writer_flops=writer_flops, fines=fines, snapshot_fines=snapshot["state_version"])
 
 
+def run_full_sequence(torch, args, device):
+    """configs[1] shape, forward only: tao_attention over B2 x T8192 x H12 x D64
+    bf16 with TaoConfig() (coarse value branch on), every query routing
+    itself. Returns seconds per call (mean of timed calls, event-bracketed)."""
+    from tao_attention import TaoConfig, tao_attention
+    b, t, h, d = 2, args.full_sequence_tokens, 12, 64
+    g = torch.Generator(device=device).manual_seed(11)
+    xs = [torch.randn(b, t, h, d, generator=g, device=device).to(torch.bfloat16)
+          for _ in range(5)]
+    fa = torch.randn(h, d, 3, generator=g, device=device) * 0.02
+    fb = torch.randn(h, d, 3, generator=g, device=device) * 0.02
+    q, k, v, rq, rk = xs
+    cfg = TaoConfig()
+
+    def call():
+        return tao_attention(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa, fusion_b=fb,
+                             alpha=0.5, config=cfg)
+
+    with torch.no_grad():
+        for _ in range(2):
+            call()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        runs = 5
+        start.record()
+        for _ in range(runs):
+            call()
+        end.record()
+        torch.cuda.synchronize()
+    seconds = start.elapsed_time(end) / runs * 1e-3
+    return dict(seconds=seconds, batch=b, tokens=t, heads=h, width=d)
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -517,6 +550,8 @@ def main():
     ap.add_argument("--model-context", type=int, default=131072)
     ap.add_argument("--model-steps", type=int, default=128)
     ap.add_argument("--no-model", action="store_true")
+    ap.add_argument("--full-sequence-tokens", type=int, default=8192)
+    ap.add_argument("--no-full-sequence", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB 4 times (a plain "
                          "copy kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -646,6 +681,18 @@ def main():
                     "123.816 tok/s (memo + regional graph) at 128K for its trained model on an "
                     "RTX 4090 (docs/benchmarks.md:94): context, not a like-for-like baseline"}
         log(f"whole-model decode: {md['tok_s']:.1f} tok/s at {args.model_context} context")
+    if not args.no_full_sequence:
+        log("full-sequence read (tao_attention forward, configs[1] shape)")
+        fs = run_full_sequence(torch, args, device)
+        result["full_sequence_forward"] = {
+            "workload": "configs[1] shape, forward only: tao_attention B%d x T%d x H%d x D%d bf16, "
+                        "TaoConfig() (coarse values on), every query routes itself; synthetic "
+                        "N(0,1) operands" % (fs["batch"], fs["tokens"], fs["heads"], fs["width"]),
+            "ms": round(fs["seconds"] * 1e3, 4),
+            "tokens_per_s": round(fs["batch"] * fs["tokens"] / fs["seconds"], 1),
+            "note": "backward not implemented on the HIP path"}
+        log(f"full-sequence forward: {fs['seconds'] * 1e3:.3f} ms, "
+            f"{fs['batch'] * fs['tokens'] / fs['seconds']:.1f} tok/s")
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, torch eager on host cores)")
         xs_cpu, _, _ = make_tokens(torch, 1 + 3 * args.cpu_steps, heads, width, 7, device)

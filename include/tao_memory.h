@@ -286,7 +286,10 @@ int tao_train_plan(const tao_stream_cfg* cfg, int64_t tokens, int64_t* plan,
 
 /* Numerics self-test (no reference counterpart): y[i] = the library's
  * bf16(correctly rounded fp32 exp(x[i])) (op 0) or log (op 1) for n bf16
- * device inputs, the functions every writer and page kernel uses. */
+ * device inputs, the functions every writer and page kernel uses; op 2 / 3:
+ * x holds n fp32 values (n a multiple of 64), y[g] = the fp32 fold sum of
+ * x[64 g .. 64 g + 63] as the routing kernels compute it (op 2: DPP fold on
+ * the bit-reversed lane layout; op 3: shuffle butterfly). */
 int tao_numerics_selftest(int32_t op, const void* x, void* y, int64_t n, void* stream);
 
 /* Native per-token driver (replaces the Python control flow of one decode

@@ -655,6 +655,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
     qp.qsel = pools->qsel;
     qp.qsel_words = pools->qsel_words;
     qp.first_epoch = (int)first_epoch;
+    qp.max_epoch = (int)(first_epoch + n_epochs - 1);
     qp.B = st->batch;
     qp.H = st->heads;
     qp.T = T;

@@ -8,8 +8,9 @@
 //   candidates = 8 fines of each chosen page + every pending fine;
 //   mass_j = r(sum_D r(hv_page(j) * sw_j)); stable top-M candidates kept in
 //   score order.
-// Every fp32 sum uses the butterfly order of the oracle, so selected ids are
-// bit-identical to the oracle's. Selection: 64-bit keys (monotone bf16 score
+// Every fp32 sum uses the butterfly order of the oracle (wave_fold_sum: DPP
+// on the bit-reversed channel layout), so selected ids are bit-identical to
+// the oracle's. Selection: 64-bit keys (monotone bf16 score
 // << 32 | ~index) ranked by counting (<= 512 keys) or an LDS bitonic network.
 // Eight waves issue the loads of eight rows each before reducing them, so a
 // refresh costs a few memory latencies rather than one per row.
@@ -63,6 +64,7 @@ TAO_DEV void wave_masses(const float* h, const bf16_t* pw, const SwRows* sw,
                          const int* pages, const int* ids, int count, int lane,
                          float* out) {
   constexpr int PER = D / 64;
+  const int e0 = fold_lane(lane);      // channels e0 + 64 k (bit-reversed layout)
   bf16_t pv[kBatch][PER], sv[kBatch][PER];
 #pragma unroll
   for (int r = 0; r < kBatch; ++r) {
@@ -70,8 +72,8 @@ TAO_DEV void wave_masses(const float* h, const bf16_t* pw, const SwRows* sw,
       const bf16_t* srow = sw ? sw->row(ids[r], D) : nullptr;
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
-        pv[r][k] = pw[(size_t)pages[r] * D + lane + 64 * k];
-        sv[r][k] = sw ? srow[lane + 64 * k] : (bf16_t)0;
+        pv[r][k] = pw[(size_t)pages[r] * D + e0 + 64 * k];
+        sv[r][k] = sw ? srow[e0 + 64 * k] : (bf16_t)0;
       }
     }
   }
@@ -81,13 +83,13 @@ TAO_DEV void wave_masses(const float* h, const bf16_t* pw, const SwRows* sw,
       float v[PER];
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
-        const float hv = rbf(h[lane + 64 * k] * bf2f(pv[r][k]));
+        const float hv = rbf(h[e0 + 64 * k] * bf2f(pv[r][k]));
         v[k] = sw ? rbf(hv * bf2f(sv[r][k])) : hv;
       }
       float s = v[0];
 #pragma unroll
       for (int k = 1; k < PER; ++k) s += v[k];
-      out[r] = rbf(wave_sum_fold(s));
+      out[r] = rbf(wave_fold_sum(s));
     }
   }
 }
@@ -97,19 +99,20 @@ TAO_DEV void wave_masses(const float* h, const bf16_t* pw, const SwRows* sw,
 template <int D>
 TAO_DEV void query_weights(const bf16_t* rq, int lane, float* h) {
   constexpr int PER = D / 64;
+  const int e0 = fold_lane(lane);      // channels e0 + 64 k (bit-reversed layout)
   float x[PER], e[PER];
   float mx = -__builtin_inff();
 #pragma unroll
-  for (int k = 0; k < PER; ++k) { x[k] = bf2f(rq[lane + 64 * k]); mx = fmaxf(mx, x[k]); }
-  mx = wave_max(mx);
+  for (int k = 0; k < PER; ++k) { x[k] = bf2f(rq[e0 + 64 * k]); mx = fmaxf(mx, x[k]); }
+  mx = wave_fold_max(mx);
 #pragma unroll
   for (int k = 0; k < PER; ++k) e[k] = exp_cr(x[k] - mx);
   float s = e[0];
 #pragma unroll
   for (int k = 1; k < PER; ++k) s += e[k];
-  s = wave_sum_fold(s);
+  s = wave_fold_sum(s);
 #pragma unroll
-  for (int k = 0; k < PER; ++k) h[lane + 64 * k] = rbf(e[k] / s);
+  for (int k = 0; k < PER; ++k) h[e0 + 64 * k] = rbf(e[k] / s);
 }
 
 // Stable descending selection of the top `count` keys (unique 64-bit keys:
@@ -260,8 +263,10 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteParams p) {
 // order (same candidates, masses and stable top-k), and its selection is
 // written as a bitmask over fine ids; the read needs the set, not the order.
 // One 256-thread workgroup per (read tile, batch, head); wave w routes
-// queries w, w + 4, ... of the tile. Every wave runs the same number of
-// rounds, so the barriers that publish its LDS keys are workgroup-uniform.
+// queries w, w + 4, ... on its own LDS arrays, so waves only synchronise
+// with themselves. This is the general path (any number of visible fines up
+// to the read's limit); route_tile_kernel below serves tiles whose rows fit
+// in LDS.
 constexpr int kQThreads = 256;
 constexpr int kQWaves = kQThreads / 64;
 constexpr int kQMaxWords = 512;          // bitmask words per query (16384 fines)
@@ -272,12 +277,28 @@ struct QueryRouteSmem {
   unsigned long long keys[kQWaves][kQueryRouteMaxKeys];
   int chosen[kQWaves][kQueryRouteMaxKeys / 8];
   uint32_t bits[kQWaves][kQMaxWords];
+  bf16_t qrows[32][D];                  // raw_q rows of the tile's queries
 };
+
+// Orders one wave's LDS accesses across its lanes (arrays private to a wave).
+TAO_DEV void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // Number of keys larger than `mine` among keys[0, n) (keys are unique).
 TAO_DEV int key_rank(const unsigned long long* keys, int n, unsigned long long mine) {
   int r = 0;
-  for (int j = 0; j < n; ++j) r += keys[j] > mine;
+  int j = 0;
+  for (; j + 8 <= n; j += 8) {
+    unsigned long long k8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) k8[i] = keys[j + i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r += k8[i] > mine;
+  }
+  for (; j < n; ++j) r += keys[j] > mine;
   return r;
 }
 
@@ -292,14 +313,22 @@ __global__ __launch_bounds__(kQThreads) void route_queries_kernel(QueryRoutePara
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int q_first = (int)desc[0], nq = (int)desc[1];
   const int coarse = (int)desc[2], M = (int)desc[3], erel = (int)desc[4];
-  const int G = p.group;
+  constexpr int G = 8;                           // coarse_group (checked at launch)
   const int epoch = p.first_epoch + erel;
   const int K = epoch / G, pending = epoch % G;
   const int E = G * coarse + pending;
   const int words = (epoch + 31) >> 5;
-  const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
-  const SwRows swr{p.sw + (size_t)bh * p.fine_cap * D,
-                   p.psw_pool + ((size_t)erel * BH + bh) * 8 * D, K * G};
+  const bf16_t* pw_g = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
+  const SwRows sw_g{p.sw + (size_t)bh * p.fine_cap * D,
+                    p.psw_pool + ((size_t)erel * BH + bh) * 8 * D, K * G};
+  for (int i = threadIdx.x; i < nq * (D / 8); i += kQThreads) {
+    const int r = i / (D / 8), c = i % (D / 8);
+    *(uint4*)&sm.qrows[r][c * 8] =
+        *(const uint4*)(p.rq + b * p.rq_sb + (int64_t)(q_first + r) * p.rq_st + h * p.rq_sh + c * 8);
+  }
+  __syncthreads();
+  const bf16_t* pw = pw_g;
+  const SwRows swr = sw_g;
   float* hw = sm.h[w];
   unsigned long long* keys = sm.keys[w];
   int* chosen = sm.chosen[w];
@@ -313,16 +342,13 @@ __global__ __launch_bounds__(kQThreads) void route_queries_kernel(QueryRoutePara
       id = K * G + (j - G * coarse);
     }
   };
-  const int rounds = (nq + kQWaves - 1) / kQWaves;
-  for (int r = 0; r < rounds; ++r) {
-    const int qi = r * kQWaves + w;
-    const bool on = qi < nq;
-    const int t = q_first + (on ? qi : 0);
-    if (on) query_weights<D>(p.rq + b * p.rq_sb + (int64_t)t * p.rq_st + h * p.rq_sh, lane, hw);
+  for (int qi = w; qi < nq; qi += kQWaves) {
+    const int t = q_first + qi;
+    query_weights<D>(sm.qrows[qi], lane, hw);
     for (int i = lane; i < words; i += 64) bits[i] = 0u;
-    __syncthreads();
-    // ---- page masses of the completed pages
-    if (on && coarse > 0)
+    wave_sync();
+    // ---- page masses of the completed pages, stable top-`coarse`, ascending
+    if (coarse > 0) {
       for (int base = 0; base < K; base += kBatch) {
         int pages[kBatch];
         float mass[kBatch];
@@ -337,9 +363,7 @@ __global__ __launch_bounds__(kQThreads) void route_queries_kernel(QueryRoutePara
           keys[base + lane] = score_key(mine, base + lane);
         }
       }
-    __syncthreads();
-    // ---- stable top-`coarse` pages, listed ascending
-    if (on && coarse > 0) {
+      wave_sync();
       int placed = 0;
       for (int c0 = 0; c0 < K; c0 += 64) {
         const int i = c0 + lane;
@@ -348,39 +372,221 @@ __global__ __launch_bounds__(kQThreads) void route_queries_kernel(QueryRoutePara
         if (pick) chosen[placed + __popcll(ball & ((1ull << lane) - 1ull))] = i;
         placed += __popcll(ball);
       }
+      wave_sync();
     }
-    __syncthreads();
     // ---- candidate masses: 8 fines of each chosen page, then the pending fines
-    if (on)
-      for (int base = 0; base < E; base += kBatch) {
-        int pages[kBatch], ids[kBatch];
-        float mass[kBatch];
-        const int count = min(kBatch, E - base);
+    for (int base = 0; base < E; base += kBatch) {
+      int pages[kBatch], ids[kBatch];
+      float mass[kBatch];
+      const int count = min(kBatch, E - base);
 #pragma unroll
-        for (int i = 0; i < kBatch; ++i) cand(base + min(i, count - 1), pages[i], ids[i]);
-        wave_masses<D>(hw, pw, &swr, pages, ids, count, lane, mass);
-        if (lane < count) {
-          float mine = mass[0];
+      for (int i = 0; i < kBatch; ++i) cand(base + min(i, count - 1), pages[i], ids[i]);
+      wave_masses<D>(hw, pw, &swr, pages, ids, count, lane, mass);
+      if (lane < count) {
+        float mine = mass[0];
 #pragma unroll
-          for (int i = 1; i < kBatch; ++i) if (lane == i) mine = mass[i];
-          keys[base + lane] = score_key(mine, base + lane);
-        }
+        for (int i = 1; i < kBatch; ++i) if (lane == i) mine = mass[i];
+        keys[base + lane] = score_key(mine, base + lane);
       }
-    __syncthreads();
-    // ---- stable top-M candidates -> bitmask
-    if (on)
-      for (int j = lane; j < E; j += 64)
-        if (key_rank(keys, E, keys[j]) < M) {
-          int page, id;
-          cand(j, page, id);
-          atomicOr(&bits[id >> 5], 1u << (id & 31));
-        }
-    __syncthreads();
-    if (on) {
-      uint32_t* dst = p.qsel + ((size_t)(b * p.T + t) * p.H + h) * p.qsel_words;
-      for (int i = lane; i < words; i += 64) dst[i] = bits[i];
     }
-    __syncthreads();                             // h, keys and bits are reused
+    wave_sync();
+    // ---- stable top-M candidates -> bitmask
+    for (int j = lane; j < E; j += 64)
+      if (key_rank(keys, E, keys[j]) < M) {
+        int page, id;
+        cand(j, page, id);
+        atomicOr(&bits[id >> 5], 1u << (id & 31));
+      }
+    wave_sync();
+    uint32_t* dst = p.qsel + ((size_t)(b * p.T + t) * p.H + h) * p.qsel_words;
+    for (int i = lane; i < words; i += 64) dst[i] = bits[i];
+    wave_sync();                                 // h, keys and bits are reused
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Per-query routes, lane per (query, row) pair: the same arithmetic as
+// route_queries_kernel with the channel sum of one mass done by one lane in
+// registers, in the fold order (pairs (e, e + 64) for D = 128, then
+// (e, e + 32), (e, e + 16), ..., (e, e + 1)), so no cross-lane reduction is
+// needed. One 256-thread workgroup per (read tile of <= 32 queries, batch,
+// head); the tile's h rows, page-weight rows and the segment-weight rows of
+// its visible fines sit in LDS, and the (query, page) and (query, candidate)
+// pairs are spread over all lanes. Keys are 32-bit: monotone bf16 score in
+// the high half, 0xFFFF - index in the low half (same order as score_key).
+constexpr int kTileQ = 32;
+
+template <int D>
+struct RouteTileGeo {
+  static constexpr int PAD = D + 8;                  // padded LDS row (bf16)
+  static constexpr int ROWS = D == 64 ? 128 : 64;    // staged pw + sw rows
+  static constexpr int KEYS = ROWS;                  // >= pages, >= candidates
+  static constexpr int WORDS = ROWS / 32;
+};
+
+template <int D>
+struct RouteTileSmem {
+  using G = RouteTileGeo<D>;
+  bf16_t h[kTileQ][G::PAD];
+  bf16_t rows[G::ROWS][G::PAD];
+  uint32_t keys[kTileQ][G::KEYS];
+  uint8_t chosen[kTileQ][G::KEYS / 8];
+  uint32_t bits[kTileQ][G::WORDS];
+  float hf[4][D];                                    // one query's h per wave (fp32)
+};
+
+TAO_DEV uint32_t score_key32(float score_bf, int index) {
+  bf16_t bits = f2bf(score_bf);
+  if (bits == 0x8000) bits = 0;                      // -0 ties with +0, as in torch's sort
+  return (bf16_order_key(bits) << 16) | (uint32_t)(0xFFFF - index);
+}
+
+TAO_DEV void unpack8(const uint4& u, float out[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+  }
+}
+
+// r(fold_e r(r(h[e] * pw[e]) * sw[e])) (WITH_SW) or r(fold_e r(h[e] * pw[e])).
+template <int D, bool WITH_SW>
+TAO_DEV float lane_mass(const bf16_t* hrow, const bf16_t* pwrow, const bf16_t* swrow) {
+  float s1[32];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {            // s1[8c + k], k < 8
+    float part[D / 32][8];
+#pragma unroll
+    for (int b = 0; b < D / 32; ++b) {     // channels 8c + k + 32 b
+      const int e0 = 8 * c + 32 * b;
+      float hv[8], pv[8];
+      unpack8(*(const uint4*)(hrow + e0), hv);
+      unpack8(*(const uint4*)(pwrow + e0), pv);
+      float sv[8];
+      if constexpr (WITH_SW) unpack8(*(const uint4*)(swrow + e0), sv);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float x = rbf(hv[k] * pv[k]);
+        part[b][k] = WITH_SW ? rbf(x * sv[k]) : x;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if constexpr (D == 64)
+        s1[8 * c + k] = part[0][k] + part[1][k];
+      else
+        s1[8 * c + k] = (part[0][k] + part[2][k]) + (part[1][k] + part[3][k]);
+    }
+  }
+#pragma unroll
+  for (int w = 16; w >= 1; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w; ++i) s1[i] += s1[i + w];
+  return rbf(s1[0]);
+}
+
+template <int D>
+__global__ __launch_bounds__(kQThreads) void route_tile_kernel(QueryRouteParams p) {
+  using Geo = RouteTileGeo<D>;
+  __shared__ RouteTileSmem<D> sm;
+  constexpr int G = 8;                           // coarse_group (checked at launch)
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int64_t* desc = p.tiles + 8 * (blockIdx.x / BH);
+  if (!desc[6]) return;                          // no history: workgroup-uniform
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int q_first = (int)desc[0], nq = (int)desc[1];
+  const int coarse = (int)desc[2], M = (int)desc[3], erel = (int)desc[4];
+  const int epoch = p.first_epoch + erel;
+  const int K = epoch / G, pending = epoch % G;
+  const int E = G * coarse + pending;
+  const int P = K + (pending > 0);
+  const int words = (epoch + 31) >> 5;
+  const bf16_t* pw_g = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
+  const SwRows sw_g{p.sw + (size_t)bh * p.fine_cap * D,
+                    p.psw_pool + ((size_t)erel * BH + bh) * 8 * D, K * G};
+  // ---- stage: rows [0, P) page weights, [P, P + epoch) segment weights
+  for (int i = tid; i < (P + epoch) * (D / 8); i += kQThreads) {
+    const int r = i / (D / 8), c = i % (D / 8);
+    const bf16_t* src = r < P ? pw_g + (size_t)r * D : sw_g.row(r - P, D);
+    *(uint4*)&sm.rows[r][c * 8] = *(const uint4*)(src + c * 8);
+  }
+  for (int i = tid; i < kTileQ * Geo::WORDS; i += kQThreads) (&sm.bits[0][0])[i] = 0u;
+  // ---- h of each query: wave w does queries w, w + 4, ...
+  for (int qi = w; qi < nq; qi += 4) {
+    query_weights<D>(p.rq + b * p.rq_sb + (int64_t)(q_first + qi) * p.rq_st + h * p.rq_sh,
+                     lane, sm.hf[w]);
+    wave_sync();
+    for (int e = lane; e < D; e += 64) sm.h[qi][e] = f2bf(sm.hf[w][e]);
+    wave_sync();
+  }
+  __syncthreads();
+  // ---- coarse pages: stable top-`coarse` by page mass, listed ascending
+  if (coarse >= K) {
+    for (int i = tid; i < nq * K; i += kQThreads) sm.chosen[i / K][i % K] = (uint8_t)(i % K);
+  } else {
+    for (int i = tid; i < nq * K; i += kQThreads) {
+      const int q = i / K, pg = i % K;
+      const float m = lane_mass<D, false>(sm.h[q], sm.rows[pg], nullptr);
+      sm.keys[q][pg] = score_key32(m, pg);
+    }
+    __syncthreads();
+    // chosen flag in the low byte of the key slot's spare: rank < coarse
+    for (int i = tid; i < nq * K; i += kQThreads) {
+      const int q = i / K, pg = i % K;
+      const uint32_t mine = sm.keys[q][pg];
+      int rank = 0;
+      for (int j = 0; j < K; ++j) rank += sm.keys[q][j] > mine;
+      if (rank < coarse) {
+        // ascending position = chosen pages with a smaller index
+        int pos = 0;
+        for (int j = 0; j < pg; ++j) {
+          const uint32_t other = sm.keys[q][j];
+          int r2 = 0;
+          for (int l = 0; l < K; ++l) r2 += sm.keys[q][l] > other;
+          pos += r2 < coarse;
+        }
+        sm.chosen[q][pos] = (uint8_t)pg;
+      }
+    }
+  }
+  __syncthreads();
+  // ---- candidate masses: 8 fines of each chosen page, then the pending fines
+  auto cand = [&](int q, int j, int& page, int& id) __attribute__((always_inline)) {
+    if (j < G * coarse) {
+      page = sm.chosen[q][j / G];
+      id = page * G + j % G;
+    } else {
+      page = K;
+      id = K * G + (j - G * coarse);
+    }
+  };
+  for (int i = tid; i < nq * E; i += kQThreads) {
+    const int q = i / E, j = i % E;
+    int page, id;
+    cand(q, j, page, id);
+    const float m = lane_mass<D, true>(sm.h[q], sm.rows[page], sm.rows[P + id]);
+    sm.keys[q][j] = score_key32(m, j);
+  }
+  __syncthreads();
+  // ---- stable top-M per query -> bitmask
+  for (int i = tid; i < nq * E; i += kQThreads) {
+    const int q = i / E, j = i % E;
+    const uint32_t mine = sm.keys[q][j];
+    int rank = 0;
+    for (int l = 0; l < E; ++l) rank += sm.keys[q][l] > mine;
+    if (rank < M) {
+      int page, id;
+      cand(q, j, page, id);
+      atomicOr(&sm.bits[q][id >> 5], 1u << (id & 31));
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < nq * words; i += kQThreads) {
+    const int q = i / words, wd = i % words;
+    p.qsel[((size_t)(b * p.T + q_first + q) * p.H + h) * p.qsel_words + wd] = sm.bits[q][wd];
   }
 }
 
@@ -388,15 +594,25 @@ __global__ __launch_bounds__(kQThreads) void route_queries_kernel(QueryRoutePara
 
 hipError_t launch_route_queries(const QueryRouteParams& p, int head_dim, hipStream_t s) {
   if (p.n_tiles <= 0) return hipSuccess;
-  if (p.qsel_words < 1 || p.qsel_words > kQMaxWords || p.group != 8)
+  if (p.qsel_words < 1 || p.qsel_words > kQMaxWords || p.group != 8 || p.max_epoch < 1)
     return hipErrorInvalidValue;
   const dim3 grid((unsigned)(p.n_tiles * p.B * p.H));
-  if (head_dim == 128)
-    hipLaunchKernelGGL(route_queries_kernel<128>, grid, dim3(kQThreads), 0, s, p);
-  else if (head_dim == 64)
-    hipLaunchKernelGGL(route_queries_kernel<64>, grid, dim3(kQThreads), 0, s, p);
-  else
+  // Lane-per-pair kernel when every tile's page and fine rows fit its LDS
+  // rows (and tiles hold <= 32 queries); else one wave per query.
+  const int rows = p.max_epoch / p.group + 1 + p.max_epoch;
+  if (head_dim == 128) {
+    if (rows <= RouteTileGeo<128>::ROWS)
+      hipLaunchKernelGGL(route_tile_kernel<128>, grid, dim3(kQThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL(route_queries_kernel<128>, grid, dim3(kQThreads), 0, s, p);
+  } else if (head_dim == 64) {
+    if (rows <= RouteTileGeo<64>::ROWS)
+      hipLaunchKernelGGL(route_tile_kernel<64>, grid, dim3(kQThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL(route_queries_kernel<64>, grid, dim3(kQThreads), 0, s, p);
+  } else {
     return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

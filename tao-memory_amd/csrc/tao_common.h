@@ -84,6 +84,52 @@ TAO_DEV float wave_sum_fold(float v) {
   return v;
 }
 
+// The same fold without LDS round trips, on the bit-reversed layout: element
+// e of a 64-element vector sits in lane fold_lane(e) = bitrev6(e) (an
+// involution: lane L holds element fold_lane(L)). The fold's pairs
+// (e, e ^ 32), (e, e ^ 16), ..., (e, e ^ 1) are then the lane pairs
+// (L, L ^ 1), (L, L ^ 2), ..., (L, L ^ 32). Levels 1-2 are quad_perm DPP
+// adds; afterwards a quad holds one value, so the half-row mirror
+// (L -> 7 - L in 8 lanes) reaches the partner quad, and then the row mirror
+// (L -> 15 - L) the partner 8-lane group; the last two levels add the four
+// row totals of lanes 0, 16, 32, 48. fp32 addition is commutative, so every
+// partial sum equals wave_sum_fold's on the natural layout bit for bit. The
+// result is uniform across the wave.
+TAO_DEV int fold_lane(int e) { return (int)(__builtin_bitreverse32((uint32_t)e) >> 26); }
+
+template <int CTRL>
+TAO_DEV float dpp_partner(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+TAO_DEV float wave_fold_sum(float v) {
+  v += dpp_partner<0xB1>(v);     // quad_perm [1, 0, 3, 2]: lane ^ 1
+  v += dpp_partner<0x4E>(v);     // quad_perm [2, 3, 0, 1]: lane ^ 2
+  v += dpp_partner<0x141>(v);    // row_half_mirror: the other quad of 8 lanes
+  v += dpp_partner<0x140>(v);    // row_mirror: the other 8 lanes of the row
+  const int bits = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Maximum over the wave with the same DPP pattern (order-free).
+TAO_DEV float wave_fold_max(float v) {
+  v = fmaxf(v, dpp_partner<0xB1>(v));
+  v = fmaxf(v, dpp_partner<0x4E>(v));
+  v = fmaxf(v, dpp_partner<0x141>(v));
+  v = fmaxf(v, dpp_partner<0x140>(v));
+  const int bits = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 TAO_DEV float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

@@ -180,7 +180,7 @@ struct QueryRouteParams {
   const bf16_t* pw_pool; const bf16_t* psw_pool; int pool_pcap;
   const int64_t* tiles; int n_tiles;
   uint32_t* qsel; int qsel_words;
-  int first_epoch;
+  int first_epoch, max_epoch;      // max_epoch: largest epoch of any read tile
   int B, H, T, group, fine_cap;
 };
 hipError_t launch_route_queries(const QueryRouteParams& p, int head_dim, hipStream_t s);

@@ -299,6 +299,29 @@ def test_exp_log_exhaustive_over_bf16(device, op):
     assert same.all(), x[~same][:8]
 
 
+def test_fold_sums_equal_the_oracle_fold_order(device):
+    """The routing kernels' 64-lane fp32 sums (DPP fold on the bit-reversed
+    layout, and the shuffle butterfly) against the oracle's fold_sum, bit for
+    bit, on groups whose magnitudes span many binades (so a different
+    association would change low bits)."""
+    from tao_attention import _hip
+    g = torch.Generator().manual_seed(40)
+    groups = 8192
+    mant = torch.rand(groups, 64, generator=g) + 0.5
+    sign = torch.where(torch.rand(groups, 64, generator=g) < 0.5, -1.0, 1.0)
+    scale = torch.exp2(torch.randint(-30, 31, (groups, 64), generator=g).float())
+    x = (sign * mant * scale).float()
+    want = O.fold_sum(x, -1)
+    assert not torch.equal(want, x.sum(-1)), "association should matter for these inputs"
+    xd = x.to(device).contiguous()
+    for op in (2, 3):
+        y = torch.empty(groups, dtype=torch.float32, device=device)
+        print(f"fold self-test op {op}", flush=True)
+        _hip.check(_hip.lib().tao_numerics_selftest(op, xd.data_ptr(), y.data_ptr(),
+                                                    groups * 64, _hip.stream_ptr(xd.device)))
+        assert torch.equal(y.cpu(), want), op
+
+
 @pytest.mark.parametrize("coarse", [False, True])
 def test_batched_decode_equals_per_request(device, coarse):
     """tao_attention_decode_batch == tao_attention_decode per request, bitwise:
@@ -479,6 +502,34 @@ def test_full_sequence_read_short_and_training_shape():
     first = O.training_forward(*(x[:1, :768, :2].cpu() for x in xs), fa[:2].cpu(),
                                fb[:2].cpu(), 0.5, geo)
     torch.testing.assert_close(out[:1, :768, :2].cpu().float(), first.float(), **TOL)
+
+
+def test_full_sequence_read_long_sequence_route_fallback():
+    """T16484 at D128: the tile rows exceed the LDS rows of the lane-per-pair
+    route, so the wave-per-query route runs. The read is causal, so the first
+    2900 positions and the routes of tiles 3..11 must equal the oracle run on
+    that prefix alone; every later query selects exactly M fines."""
+    from tao_attention import TaoConfig, training
+    cfg = TaoConfig()
+    tokens, prefix = 16484, 2900
+    xs, fa, fb = inputs(tokens, 2, 128, 37)
+    dev = to_dev(xs, "cuda")
+    out, qsel = training.forward(*dev, fa.cuda(), fb.cuda(), 0.5, cfg, return_routes=True)
+    ref, routes = O.training_forward(*(x[:, :prefix] for x in xs), fa, fb, 0.5,
+                                     O.Geometry.from_config(cfg), return_routes=True)
+    got = _bitmask_sets(qsel)
+    for tile, sel in routes.items():
+        part = got[:, tile * 256:tile * 256 + sel.shape[1]]
+        want = torch.zeros_like(part)
+        want.scatter_(-1, sel, True)
+        assert torch.equal(part, want), f"tile {tile}"
+    torch.testing.assert_close(out[:, :prefix].cpu().float(), ref.float(), **TOL)
+    geo = O.Geometry.from_config(cfg)
+    counts = got.sum(-1)
+    for tile in range(3, tokens // 256):
+        visible = tile - 2
+        m = geo.routed_counts(visible // 8, visible % 8)[2]
+        assert bool((counts[:, tile * 256:(tile + 1) * 256] == m).all()), tile
 
 
 def test_full_sequence_read_backward_is_not_built():

@@ -18,6 +18,7 @@ Gradients: the backward kernels (selected-read, writer, local-attention and
 fusion adjoints) are not built; a backward through this op raises.
 """
 
+import collections
 import ctypes
 
 import numpy as np
@@ -59,6 +60,65 @@ def plan(config, tokens):
     return words, dict(zip(keys, info))
 
 
+class _Workspace:
+    """Plan, call-private device state, pools and scratch of one shape.
+
+    Every buffer is fully written before it is read within a call (the bank
+    and page state by the writer and page kernels, the pools by the epoch and
+    route kernels, qsel words of history queries by the route), so calls of
+    the same shape on the same stream reuse them.
+    """
+
+    def __init__(self, config, b, tokens, heads, d, device):
+        from .tao_stream import _DeviceState
+
+        self.plan, self.info = plan(config, tokens)
+        info = self.info
+        self.plan_arr = self.plan.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
+        self.dev = _DeviceState(config, b, heads, d, device, max(info["fines"], 8))
+        self.dev.ensure_plan(len(self.plan))
+        self.local = torch.empty((b, tokens, heads, d), dtype=torch.bfloat16, device=device)
+        self.pools = _hip.PrefillPools()
+        self.keep = []
+        self.qsel = None
+        if info["epochs"]:
+            pcap = info["pool_pcap"]
+            pw_pool = torch.empty((info["epochs"], b, heads, pcap, d), dtype=torch.bfloat16,
+                                  device=device)
+            psw_pool = torch.empty((info["epochs"], b, heads, config.coarse_group, d),
+                                   dtype=torch.bfloat16, device=device)
+            self.qsel = torch.zeros((b, tokens, heads, info["qsel_words"]), dtype=torch.int32,
+                                    device=device)
+            pools = self.pools
+            pools.pw_pool, pools.psw_pool = pw_pool.data_ptr(), psw_pool.data_ptr()
+            pools.pool_pcap, pools.epochs = pcap, info["epochs"]
+            pools.qsel, pools.qsel_words = self.qsel.data_ptr(), info["qsel_words"]
+            self.keep = [pw_pool, psw_pool]
+            if self.dev.coarse_values and info["coarse_count"]:
+                coarse_pool = torch.empty((info["coarse_count"], b, heads, d, d),
+                                          dtype=torch.bfloat16, device=device)
+                pools.coarse_pool = coarse_pool.data_ptr()
+                pools.coarse_first = info["coarse_first"]
+                pools.coarse_count = info["coarse_count"]
+                self.keep.append(coarse_pool)
+
+
+_WORKSPACES = collections.OrderedDict()
+_MAX_WORKSPACES = 4
+
+
+def _workspace(config, b, tokens, heads, d, device):
+    key = (config, b, tokens, heads, d, device, _hip.stream_ptr(device))
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        ws = _WORKSPACES[key] = _Workspace(config, b, tokens, heads, d, device)
+        while len(_WORKSPACES) > _MAX_WORKSPACES:
+            _WORKSPACES.popitem(last=False)
+    else:
+        _WORKSPACES.move_to_end(key)
+    return ws
+
+
 def forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_routes=False):
     """Fused heads [B, T, H, D] of the full-sequence read (no autograd).
 
@@ -66,51 +126,23 @@ def forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_rou
     bitmask words over fine ids (bit f of word f // 32) for queries with
     history, zero before first_fine.
     """
-    from .tao_stream import _DeviceState
-
     _check(q, k, v, raw_q, raw_k, config)
     b, tokens, heads, d = q.shape
     out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
     if tokens == 0:
         return (out, None) if return_routes else out
-    words_plan, info = plan(config, tokens)
-    fines = info["fines"]
-    dev = _DeviceState(config, b, heads, d, q.device, max(fines, 8))
-    dev.ensure_plan(len(words_plan))
+    ws = _workspace(config, b, tokens, heads, d, q.device)
     q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
     tok = _hip.tokens(q, k, v, raw_q, raw_k)
     fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
-    local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
-    pools = _hip.PrefillPools()
-    keep = []
-    qsel = None
-    if info["epochs"]:
-        pcap = info["pool_pcap"]
-        pw_pool = torch.empty((info["epochs"], b, heads, pcap, d), dtype=torch.bfloat16,
-                              device=q.device)
-        psw_pool = torch.empty((info["epochs"], b, heads, config.coarse_group, d),
-                               dtype=torch.bfloat16, device=q.device)
-        qsel = torch.zeros((b, tokens, heads, info["qsel_words"]), dtype=torch.int32,
-                           device=q.device)
-        pools.pw_pool, pools.psw_pool = pw_pool.data_ptr(), psw_pool.data_ptr()
-        pools.pool_pcap, pools.epochs = pcap, info["epochs"]
-        pools.qsel, pools.qsel_words = qsel.data_ptr(), info["qsel_words"]
-        keep = [pw_pool, psw_pool]
-        if dev.coarse_values and info["coarse_count"]:
-            coarse_pool = torch.empty((info["coarse_count"], b, heads, d, d),
-                                      dtype=torch.bfloat16, device=q.device)
-            pools.coarse_pool = coarse_pool.data_ptr()
-            pools.coarse_first = info["coarse_first"]
-            pools.coarse_count = info["coarse_count"]
-            keep.append(coarse_pool)
-    plan_arr = words_plan.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
     out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
     _hip.check(_hip.lib().tao_prefill(
-        ctypes.byref(dev.struct), ctypes.byref(tok), ctypes.byref(fu), plan_arr,
-        len(words_plan), ctypes.byref(pools), local.data_ptr(), out.data_ptr(), out_s,
-        dev.stream()))
-    del keep, dev      # the caching allocator keeps them stream-ordered
-    return (out, qsel) if return_routes else out
+        ctypes.byref(ws.dev.struct), ctypes.byref(tok), ctypes.byref(fu), ws.plan_arr,
+        len(ws.plan), ctypes.byref(ws.pools), ws.local.data_ptr(), out.data_ptr(), out_s,
+        ws.dev.stream()))
+    if return_routes:
+        return out, None if ws.qsel is None else ws.qsel.clone()
+    return out
 
 
 class _FullSequenceRead(torch.autograd.Function):

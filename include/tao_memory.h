@@ -191,6 +191,15 @@ typedef struct tao_prefill_pools {
   int32_t coarse_first, coarse_count;
   uint32_t* qsel;
   int32_t qsel_words;
+  /* Optional forward saves for the full-sequence backward (null = skip):
+   * local_lse fp32 [B][T][H] log2-sum-exp of each query's local scores
+   * (scale 1/sqrt(D) * log2 e); coarse_out / fine_out bf16 [B][T][H][D]
+   * the coarse and fine heads before the fusion (history queries only);
+   * den_out fp32 [B][T][H] the fine read's denominator. */
+  float* local_lse;
+  void* coarse_out;
+  void* fine_out;
+  float* den_out;
 } tao_prefill_pools;
 
 /* Layout of the int64 prefill plan (all indices are token offsets in tok
@@ -283,6 +292,41 @@ int tao_prefill_plan(const tao_stream_cfg* cfg, int64_t pos0, int64_t tokens,
  * qsel_words, the bitmask words per query. Host code only. */
 int tao_train_plan(const tao_stream_cfg* cfg, int64_t tokens, int64_t* plan,
                    int64_t plan_cap, int64_t* info);
+
+/* Backward of the full-sequence read (replaces the reference's autograd
+ * through tao_attention: _fuse_training, operator.py:21-38; the local SDPA,
+ * tao_stream.py:760-787; _SelectedRead.backward, selected_read.py:175-187;
+ * the page / segment softmaxes and logsumexps, tao_stream.py:530-665; the
+ * softmax writer, tao_stream.py:80-123). st, tok, fu and pools are the
+ * forward's tao_prefill arguments (same buffers, unchanged since), and the
+ * forward was run with pools.local_lse / coarse_out / fine_out / den_out set
+ * (local: its local-attention scratch). grad: upstream gradient bf16
+ * [B, T, H, D] with element strides grad_s (batch, token, head). Outputs:
+ * bf16 [B, T, H, D] contiguous dq, dk, dv, draw_q, draw_k; dfusion_a /
+ * dfusion_b fp32 [H, D, 3], accumulated (zero them first). No gradient for
+ * alpha (the reference builds the gain from a Python float, operator.py:34).
+ * workspace: tao_train_bwd_workspace_bytes(...) bytes of device memory. */
+typedef struct tao_train_bwd {
+  const void* grad; int64_t grad_s[3];
+  const void* local; const float* local_lse;
+  const void* coarse_out; const void* fine_out; const float* den_out;
+  void* dq; void* dk; void* dv; void* draw_q; void* draw_k;
+  float* dfusion_a; float* dfusion_b;
+  void* workspace; size_t workspace_bytes;
+  /* Optional (null = skip): the memory adjoints before the writer,
+   * d fine_z fp32 [B][H][fines][D] and d C^T fp32 [B][H][fines][D][D]
+   * ([e][d], the bank's layout), for callers that inspect them. */
+  float* dz_out; float* dc_out;
+} tao_train_bwd;
+
+/* Workspace bytes of tao_train_backward for a full-sequence read of `tokens`
+ * tokens whose plan wrote `fines` fines (tao_train_plan info[10]). */
+size_t tao_train_bwd_workspace_bytes(const tao_state_dev* st, int64_t tokens, int32_t fines,
+                                     const tao_prefill_pools* pools);
+
+int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
+                       const tao_prefill_pools* pools, const tao_train_bwd* args,
+                       void* stream);
 
 /* Numerics self-test (no reference counterpart): y[i] = the library's
  * bf16(correctly rounded fp32 exp(x[i])) (op 0) or log (op 1) for n bf16

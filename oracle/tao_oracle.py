@@ -697,3 +697,97 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
             out[:, start:end] = fusion(raw_q[:, start:end], local[:, start:end], coarse,
                                        fine, fusion_a, fusion_b, alpha, coarse_on, fine_on)
     return (out, routes) if return_routes else out
+
+
+def training_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, routes,
+                            geometry=None, intermediates=None):
+    """training_forward's function without bf16 rounding, for gradients.
+
+    Same steps as training_forward (local attention per tile, the softmax
+    writer, page logsumexps, page softmax, segment weights, h, hv, the
+    selected read num / den, the coarse read, the three-branch fusion with
+    presence masks), evaluated in the inputs' dtype (fp64 in the tests), with
+    every query's selection fixed to `routes` (tile -> ids [B, Q, H, M]): the
+    reference's selection has no derivative (tao_stream.py:647-650), so the
+    gradient of tao_attention is the gradient of this function at the bf16
+    forward's selections. Differentiable by torch autograd. A dict
+    `intermediates` receives the fine descriptors "fine_z" [B, H, S, D] and
+    the bank "bank" [B, H, S, D, D] (C[d][e]), to take gradients at them.
+    """
+    g = geometry or Geometry()
+    b, total, heads, d = q.shape
+    ft, keep, group = g.fine_tokens, g.local_keep, g.coarse_group
+    parts = []
+    for start in range(0, total, ft):
+        end = min(total, start + ft)
+        k0 = max(0, start - keep)
+        s = torch.einsum("bqhd,bkhd->bhqk", q[:, start:end], k[:, k0:end]) / math.sqrt(d)
+        rows = (end - k0) - (end - start) + torch.arange(end - start)
+        allowed = torch.arange(end - k0)[None, :] <= rows[:, None]
+        p = torch.softmax(s.masked_fill(~allowed, NEG_INF), -1)
+        parts.append(torch.einsum("bhqk,bkhd->bqhd", p, v[:, k0:end]))
+    local = torch.cat(parts, 1)
+    n_tiles = -(-total // ft)
+    lag = keep // ft
+    visible_max = max(0, n_tiles - 1 - lag)
+    if total <= g.serve_limit or visible_max == 0:
+        return local
+    zs, cs = [], []
+    for f in range(visible_max):
+        kb, vb = raw_k[:, f * ft:(f + 1) * ft], v[:, f * ft:(f + 1) * ft]
+        zs.append(torch.logsumexp(kb, 1))                           # [B, H, D]
+        cs.append(torch.einsum("bthd,bthe->bhde", torch.softmax(kb, 1), vb))
+    fine_z = torch.stack(zs, 2)
+    bank = torch.stack(cs, 2)
+    if intermediates is not None:
+        intermediates["fine_z"], intermediates["bank"] = fine_z, bank
+    full = visible_max // group
+    pz_full = [torch.logsumexp(fine_z[:, :, p * group:(p + 1) * group], 2) for p in range(full)]
+    pc_full = []
+    if not g.coarse_index_only:
+        for p in range(full):
+            w = torch.exp(fine_z[:, :, p * group:(p + 1) * group] - pz_full[p].unsqueeze(2))
+            pc_full.append(torch.einsum("bhsd,bhsde->bhde", w, bank[:, :, p * group:(p + 1) * group]))
+    first_coarse = keep + group * ft
+    gain = 2.0 * alpha
+    outs = [local[:, :min(total, (lag + 1) * ft)]]
+    for tile in range(lag + 1, n_tiles):
+        start, end = tile * ft, min(total, tile * ft + ft)
+        visible = tile - lag
+        completed, pending = divmod(visible, group)
+        pz = list(pz_full[:completed])
+        if pending:
+            pz.append(torch.logsumexp(fine_z[:, :, completed * group:visible], 2))
+        page_z = torch.stack(pz, 2)                                 # [B, H, P, D]
+        pw = torch.softmax(page_z, 2)
+        page_of = torch.arange(visible) // group
+        sw = torch.exp(fine_z[:, :, :visible] - page_z[:, :, page_of])
+        rq = raw_q[:, start:end]
+        h = torch.softmax(rq, -1)                                   # [B, Q, H, D]
+        hv = h.unsqueeze(3) * pw.unsqueeze(1)                       # [B, Q, H, P, D]
+        sel = routes[tile]
+        mask = torch.zeros((*sel.shape[:3], visible), dtype=h.dtype)
+        mask.scatter_(-1, sel, 1.0)
+        a = hv[:, :, :, page_of] * sw.unsqueeze(1) * mask.unsqueeze(-1)   # [B, Q, H, V, D]
+        num = torch.einsum("bqhvd,bhvde->bqhe", a, bank[:, :, :visible])
+        fine = num / a.sum((-1, -2)).unsqueeze(-1)
+        coarse_on = start >= first_coarse and not g.coarse_index_only
+        if coarse_on:
+            cw = torch.softmax(page_z[:, :, :completed], 2)
+            coarse = torch.einsum("bqhd,bhpd,bhpde->bqhe", h, cw,
+                                  torch.stack(pc_full[:completed], 2))
+        else:
+            coarse = torch.zeros_like(fine)
+        present = 1 + int(coarse_on)
+        scores = []
+        for branch in range(3):
+            s = fusion_a[..., branch] * rq + fusion_b[..., branch]
+            if branch == 0:
+                s = s + math.log(present)
+            if branch == 1 and not coarse_on:
+                s = torch.full_like(s, NEG_INF)
+            scores.append(s)
+        rho = torch.softmax(torch.stack(scores, -1), -1)
+        lo = local[:, start:end]
+        outs.append(rho[..., 0] * 2 * lo + rho[..., 1] * gain * coarse + rho[..., 2] * gain * fine)
+    return torch.cat(outs, 1)

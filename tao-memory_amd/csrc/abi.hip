@@ -531,6 +531,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   ap.L = L;
   ap.T = T;
   ap.n_tiles = (int)n_attn;
+  ap.lse = pools ? pools->local_lse : nullptr;
   e = tao::launch_local_attention(ap, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill attention");
   // writer
@@ -695,6 +696,9 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   rt.qsel = query_routes && need_pools ? pools->qsel : nullptr;
   rt.qsel_words = query_routes && need_pools ? pools->qsel_words : 0;
   rt.first_epoch = (int)first_epoch;
+  rt.save_coarse = pools ? (bf16_t*)pools->coarse_out : nullptr;
+  rt.save_fine = pools ? (bf16_t*)pools->fine_out : nullptr;
+  rt.save_den = pools ? pools->den_out : nullptr;
   e = tao::launch_read_tiles(rt, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill read");
   tao::AppendParams app;
@@ -815,3 +819,204 @@ int tao_graph_destroy(void* graph) {
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Full-sequence backward (train_bwd.hip).
+namespace {
+
+struct TrainBwdLayout {
+  size_t dlocal, h, delta, dden, dcoarse, dnum, drq, dh, dvf;   // per-token arrays
+  size_t dpw, dsw_tile, dgc, dc, dsw, dpz, dz;                  // memory branch
+  size_t zero_begin, zero_end;                                  // accumulators to clear
+  size_t total;
+  int n_tiles, v_max;
+};
+
+TrainBwdLayout train_bwd_layout(const tao_state_dev* st, int64_t tokens, int fines,
+                                const tao_prefill_pools* pools) {
+  TrainBwdLayout l{};
+  const size_t B = st->batch, H = st->heads, D = st->head_dim, T = (size_t)tokens;
+  const size_t rows = B * T * H, BH = B * H;
+  const size_t pcap = pools ? (size_t)pools->pool_pcap : 0;
+  const size_t cc = pools ? (size_t)pools->coarse_count : 0;
+  l.n_tiles = (int)((tokens + st->fine_tokens - 1) / st->fine_tokens);
+  l.v_max = fines;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (bytes + 255) & ~(size_t)255;
+    return o;
+  };
+  l.dlocal = take(rows * D * 2);
+  l.h = take(rows * D * 2);
+  l.delta = take(rows * 4);
+  l.dden = take(rows * 4);
+  l.dcoarse = take(rows * D * 4);
+  l.dnum = take(rows * D * 4);
+  l.drq = take(rows * D * 4);
+  l.dh = take(rows * D * 4);
+  l.dvf = take(rows * D * 4);
+  l.dgc = take(cc * BH * D * D * 4);
+  l.dc = take(BH * (size_t)fines * D * D * 4);
+  l.zero_begin = off;
+  l.dpw = take((size_t)l.n_tiles * BH * pcap * D * 4);
+  l.dsw_tile = take((size_t)l.n_tiles * BH * (size_t)fines * D * 4);
+  l.dsw = take(BH * (size_t)fines * D * 4);
+  l.dpz = take(BH * (size_t)st->page_cap * D * 4);
+  l.dz = take(BH * (size_t)fines * D * 4);
+  l.zero_end = off;
+  l.total = off;
+  return l;
+}
+
+}  // namespace
+
+size_t tao_train_bwd_workspace_bytes(const tao_state_dev* st, int64_t tokens, int32_t fines,
+                                     const tao_prefill_pools* pools) {
+  if (!st || tokens < 0 || fines < 0) return 0;
+  return train_bwd_layout(st, tokens, fines, pools).total;
+}
+
+int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
+                       const tao_prefill_pools* pools, const tao_train_bwd* a, void* stream) {
+  int rc = check_state(st);
+  if (!rc) rc = check_tokens(tok);
+  if (!rc) rc = check_fusion(fu);
+  if (rc) return rc;
+  if (!a || !a->grad || !a->local || !a->local_lse || !a->dq || !a->dk || !a->dv ||
+      !a->draw_q || !a->draw_k || !a->dfusion_a || !a->dfusion_b || !a->workspace)
+    return fail(TAO_E_ARGUMENT, "null backward argument");
+  const int T = tok->tokens;
+  const int ft = st->fine_tokens, keep = st->local_keep, G = st->coarse_group;
+  const int n_tiles = (T + ft - 1) / ft;
+  const int lag = keep / ft;
+  const int fines = n_tiles - 1 - lag > 0 ? n_tiles - 1 - lag : 0;
+  if (fines > 0) {
+    if (!pools || !pools->pw_pool || !pools->psw_pool || !pools->qsel || !a->coarse_out ||
+        !a->fine_out || !a->den_out)
+      return fail(TAO_E_ARGUMENT, "backward with history needs the forward's pools and saves");
+    if (fines > st->fine_cap || pools->epochs < fines || pools->pool_pcap < fines / G + 1 ||
+        (fines + 31) / 32 > pools->qsel_words)
+      return fail(TAO_E_CAPACITY, "backward pools smaller than the full-sequence plan");
+    if (fines / G + 1 > 64)
+      return fail(TAO_E_CAPACITY, "backward supports at most 63 completed pages (504 fines)");
+    if (st->page_c && (fines / G >= 1) &&
+        (!pools->coarse_pool || pools->coarse_first != 1 || pools->coarse_count != fines / G))
+      return fail(TAO_E_ARGUMENT, "backward with coarse values needs the forward's coarse pool");
+  }
+  const TrainBwdLayout l = train_bwd_layout(st, T, fines, fines > 0 ? pools : nullptr);
+  if (a->workspace_bytes < l.total) return fail(TAO_E_WORKSPACE, "backward workspace too small");
+  const hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)a->workspace;
+  const int D = st->head_dim, H = st->heads, B = st->batch;
+  hipError_t e = hipMemsetAsync(ws + l.zero_begin, 0, l.zero_end - l.zero_begin, s);
+  if (e != hipSuccess) return check_hip(e, "tao_train_backward clear");
+  // ---- fusion adjoint
+  tao::TrainBwdParams fp{};
+  fp.grad = (const bf16_t*)a->grad;
+  fp.g_sb = a->grad_s[0];
+  fp.g_st = a->grad_s[1];
+  fp.g_sh = a->grad_s[2];
+  fp.rq = view(tok->raw_q, tok->rq_s);
+  fp.local = (const bf16_t*)a->local;
+  fp.coarse = (const bf16_t*)a->coarse_out;
+  fp.fine = (const bf16_t*)a->fine_out;
+  fp.den = a->den_out;
+  fp.fa = fu->fusion_a;
+  fp.fb = fu->fusion_b;
+  fp.f_dtype = fu->dtype;
+  for (int i = 0; i < 3; ++i) { fp.fa_s[i] = fu->a_s[i]; fp.fb_s[i] = fu->b_s[i]; }
+  fp.gain = fu->gain;
+  fp.B = B;
+  fp.T = T;
+  fp.H = H;
+  fp.first_fine = keep + ft;
+  fp.first_coarse = keep + G * ft;
+  fp.coarse_values = st->page_c != nullptr;
+  fp.dlocal = (bf16_t*)(ws + l.dlocal);
+  fp.delta = (float*)(ws + l.delta);
+  fp.dcoarse = (float*)(ws + l.dcoarse);
+  fp.dnum = (float*)(ws + l.dnum);
+  fp.dden = (float*)(ws + l.dden);
+  fp.drq = (float*)(ws + l.drq);
+  fp.dfa = a->dfusion_a;
+  fp.dfb = a->dfusion_b;
+  fp.h = (bf16_t*)(ws + l.h);
+  e = tao::launch_fuse_bwd(fp, D, s);
+  if (e != hipSuccess) return check_hip(e, "tao_train_backward fusion");
+  // ---- local attention adjoint
+  tao::AttnBwdParams ap{};
+  ap.q = view(tok->q, tok->q_s);
+  ap.k = view(tok->k, tok->k_s);
+  ap.v = view(tok->v, tok->v_s);
+  ap.dout = fp.dlocal;
+  ap.lse = a->local_lse;
+  ap.delta = fp.delta;
+  ap.dq = (bf16_t*)a->dq;
+  ap.dk = (bf16_t*)a->dk;
+  ap.dv = (float*)(ws + l.dvf);
+  ap.B = B;
+  ap.H = H;
+  ap.T = T;
+  ap.ft = ft;
+  ap.keep = keep;
+  e = tao::launch_attn_bwd(ap, D, s);
+  if (e != hipSuccess) return check_hip(e, "tao_train_backward local attention");
+  // ---- memory branch, writer, final gradients
+  tao::MemBwdParams mp{};
+  mp.bank = (const bf16_t*)st->bank_c;
+  mp.fine_sw = (const bf16_t*)st->fine_sw;
+  mp.page_z = (const bf16_t*)st->page_z;
+  mp.page_c = (const bf16_t*)st->page_c;
+  if (fines > 0) {
+    mp.pw_pool = (const bf16_t*)pools->pw_pool;
+    mp.psw_pool = (const bf16_t*)pools->psw_pool;
+    mp.pool_pcap = pools->pool_pcap;
+    mp.coarse_pool = (const bf16_t*)pools->coarse_pool;
+    mp.coarse_first = pools->coarse_first;
+    mp.coarse_count = st->page_c ? pools->coarse_count : 0;
+    mp.qsel = pools->qsel;
+    mp.qsel_words = pools->qsel_words;
+  }
+  mp.raw_k = view(tok->raw_k, tok->rk_s);
+  mp.v = view(tok->v, tok->v_s);
+  mp.h = fp.h;
+  mp.dnum = fp.dnum;
+  mp.dden = fp.dden;
+  mp.dcoarse = fp.dcoarse;
+  mp.drq_fuse = fp.drq;
+  mp.dh = (float*)(ws + l.dh);
+  mp.dpw = (float*)(ws + l.dpw);
+  mp.dsw_tile = (float*)(ws + l.dsw_tile);
+  mp.dgc = (float*)(ws + l.dgc);
+  mp.dc = (float*)(ws + l.dc);
+  mp.dsw = (float*)(ws + l.dsw);
+  mp.dpz = (float*)(ws + l.dpz);
+  mp.dz = (float*)(ws + l.dz);
+  mp.dv = ap.dv;
+  mp.draw_q = (bf16_t*)a->draw_q;
+  mp.draw_k = (bf16_t*)a->draw_k;
+  mp.dv_out = (bf16_t*)a->dv;
+  mp.B = B;
+  mp.H = H;
+  mp.T = T;
+  mp.ft = ft;
+  mp.keep = keep;
+  mp.group = G;
+  mp.fine_cap = st->fine_cap;
+  mp.page_cap = st->page_cap;
+  mp.v_max = fines;
+  mp.coarse_values = st->page_c != nullptr;
+  e = tao::launch_mem_bwd(mp, D, s);
+  if (e != hipSuccess) return check_hip(e, "tao_train_backward memory branch");
+  const size_t BHf = (size_t)B * H * fines;
+  if (a->dz_out && fines > 0) {
+    e = hipMemcpyAsync(a->dz_out, mp.dz, BHf * D * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return check_hip(e, "tao_train_backward dz copy");
+  }
+  if (a->dc_out && fines > 0) {
+    e = hipMemcpyAsync(a->dc_out, mp.dc, BHf * D * D * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return check_hip(e, "tao_train_backward dC copy");
+  }
+  return TAO_OK;
+}

@@ -233,6 +233,7 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
       }
   }
   if (!qvalid) return;
+  if (p.lse && hl == 0) p.lse[((size_t)b * p.T + qtok) * p.H + h] = m_run + __log2f(l_run);
   const float inv = 1.0f / l_run;
   bf16_t* orow = p.out + (((size_t)b * p.T + qtok) * p.H + h) * D;
 #pragma unroll

@@ -484,6 +484,12 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
       if (q < nq) {
         const int tq = q_first + q;
         const float fine = rbf(rbf(av[i]) * __builtin_amdgcn_rcpf(rbf(acc_den[i])));
+        const size_t row = ((size_t)b * p.T + tq) * p.H + h;
+        if (p.save_fine) {
+          p.save_fine[row * D + e] = f2bf(fine);
+          p.save_coarse[row * D + e] = f2bf(rbf(cacc[i]));
+          if (e == 0) p.save_den[row] = rbf(acc_den[i]);
+        }
         const float local = bf2f(p.local[(((size_t)b * p.T + tq) * p.H + h) * D + e]);
         const float x = bf2f(p.rq.p[b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + e]);
         p.out[b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + e] =

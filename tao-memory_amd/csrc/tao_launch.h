@@ -211,6 +211,7 @@ struct AttnParams {
   int64_t qpos0;                 // absolute position of query row 0
   int64_t kpos0;                 // absolute position of key row 0 (older keys: ring)
   int B, H, L, T, n_tiles;
+  float* lse;                    // optional [B, T, H]: log2-sum-exp of the scaled scores
 };
 hipError_t launch_local_attention(const AttnParams& p, int head_dim, hipStream_t s);
 
@@ -253,8 +254,65 @@ struct ReadTilesParams {
   // Per-query selections (plans with query routes): bitmasks as written by
   // route_queries, the plan's first epoch; null for turn routes.
   const uint32_t* qsel; int qsel_words; int first_epoch;
+  // Optional saves (null = skip): pre-fusion heads [B, T, H, D], denominators [B, T, H].
+  bf16_t* save_coarse; bf16_t* save_fine; float* save_den;
 };
 hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t s);
+
+// ---- full-sequence backward (train_bwd.hip)
+// Fusion adjoint: from the upstream gradient and the forward's saves to the
+// branch adjoints, the fusion's part of d raw_q, d fusion_a / d fusion_b
+// (accumulated, zeroed by the caller), and the local attention's delta.
+struct TrainBwdParams {
+  const bf16_t* grad; int64_t g_sb, g_st, g_sh;
+  TokView rq;
+  const bf16_t* local; const bf16_t* coarse; const bf16_t* fine; const float* den;
+  const void* fa; const void* fb; int f_dtype;
+  int64_t fa_s[3], fb_s[3];
+  float gain;
+  int B, T, H, first_fine, first_coarse, coarse_values;
+  bf16_t* dlocal; float* delta; float* dcoarse; float* dnum; float* dden; float* drq;
+  float* dfa; float* dfb;
+  bf16_t* h;                     // h = softmax(raw_q) [B, T, H, D]
+};
+hipError_t launch_fuse_bwd(const TrainBwdParams& p, int head_dim, hipStream_t s);
+
+// Local attention adjoints with the full-sequence windows (query q sees keys
+// [max(0, ft * (q / ft) - keep), q]).
+struct AttnBwdParams {
+  TokView q, k, v;
+  const bf16_t* dout;            // d local, bf16 [B, T, H, D] contiguous
+  const float* lse; const float* delta;   // [B, T, H]
+  bf16_t* dq; bf16_t* dk; float* dv;      // dv fp32 (the writer's part is added later)
+  int B, H, T, ft, keep;
+};
+hipError_t launch_attn_bwd(const AttnBwdParams& p, int head_dim, hipStream_t s);
+
+// Memory-branch adjoints: selected read, coarse read, page / segment
+// softmaxes and logsumexps, the softmax writer, and the final d raw_q /
+// d raw_k / dv. fp32 accumulators are zeroed by the caller: dsw_tile, dpw,
+// dsw, dpz, dz (dh, dc, dgc are written in full).
+struct MemBwdParams {
+  const bf16_t* bank; const bf16_t* fine_sw; const bf16_t* page_z; const bf16_t* page_c;
+  const bf16_t* pw_pool; const bf16_t* psw_pool; int pool_pcap;
+  const bf16_t* coarse_pool; int coarse_first, coarse_count;
+  const uint32_t* qsel; int qsel_words;
+  TokView raw_k, v;
+  const bf16_t* h; const float* dnum; const float* dden; const float* dcoarse;
+  const float* drq_fuse;
+  float* dh;                     // [B, T, H, D]
+  float* dpw;                    // [n_tiles][B*H][pool_pcap][D]
+  float* dsw_tile;               // [n_tiles][B*H][v_max][D]
+  float* dgc;                    // [coarse_count][B*H][D][D]  (dG^T [e][d])
+  float* dc;                     // [B*H][v_max][D][D]         (dC^T [e][d])
+  float* dsw;                    // [B*H][v_max][D]
+  float* dpz;                    // [B*H][page_cap][D]
+  float* dz;                     // [B*H][v_max][D]
+  float* dv;                     // [B, T, H, D] fp32 (local part in, writer part added)
+  bf16_t* draw_q; bf16_t* draw_k; bf16_t* dv_out;
+  int B, H, T, ft, keep, group, fine_cap, page_cap, v_max, coarse_values;
+};
+hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s);
 
 
 

@@ -1,0 +1,1020 @@
+// Backward of the full-sequence read (tao_attention, operator.py:40-52) for
+// gfx950: the adjoints the reference takes by autograd through
+// _fuse_training (operator.py:21-38), the local SDPA of
+// _local_training_corrected_4k (tao_stream.py:760-787), the selected read
+// (selected_read.py:175-187), the page / segment softmaxes and logsumexps
+// (tao_stream.py:530-665) and the softmax writer (tao_stream.py:80-123).
+//
+// Gradients are those of the forward's function at the forward's values and
+// selections (the selection has no derivative, tao_stream.py:647-650);
+// accumulation is fp32 throughout, MFMA operands are bf16.
+#include "tao_launch.h"
+#include "tao_common.h"
+#include "tao_fusion.h"
+
+namespace tao {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+TAO_DEV bf16x8 as_bf16x8(const uint4& u) {
+  bf16x8 r;
+  __builtin_memcpy(&r, &u, 16);
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Fusion adjoint (operator.py:21-38). Workgroup = (64-token chunk of one
+// batch row, head); thread (e = tid % D, lane row r = tid / D) walks the
+// chunk's tokens r, r + 256 / D, ... Per element, with the forward's bf16
+// scores s_i and branch values x = (2 local, gain coarse, gain fine):
+//   rho = softmax(s over present branches), d rho_i = g x_i,
+//   ds_i = rho_i (d rho_i - sum_j rho_j d rho_j),
+//   d local = 2 g rho_0, d coarse = gain g rho_1, d fine = gain g rho_2,
+//   d raw_q += sum_i ds_i a_i, d fusion_a_i += ds_i raw_q, d fusion_b_i += ds_i.
+// Rows without history (output = local): d local = g.
+// Also: dnum = d fine / den, dden = -sum_e d fine fine / den, and the local
+// attention's delta = sum_e d local * local.
+constexpr int kFuseChunk = 64;
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
+  constexpr int ROWS = kThreads / D;            // tokens in flight per workgroup
+  __shared__ float red[3][kThreads / 64];       // per-wave partials (delta, dden, sum exp)
+  __shared__ float facc[6][ROWS][D];            // dfa, dfb partials per lane row
+  const int chunks = (p.T + kFuseChunk - 1) / kFuseChunk;
+  const int h = blockIdx.x % p.H;
+  const int b = (blockIdx.x / p.H) % p.B;
+  const int chunk = blockIdx.x / (p.H * p.B);
+  (void)chunks;
+  const int tid = threadIdx.x, e = tid % D, r = tid / D, lane = tid & 63, w = tid >> 6;
+  float a[3], bb[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    a[i] = rbf(load_param(p.fa, p.f_dtype, h * p.fa_s[0] + e * p.fa_s[1] + i * p.fa_s[2]));
+    bb[i] = rbf(load_param(p.fb, p.f_dtype, h * p.fb_s[0] + e * p.fb_s[1] + i * p.fb_s[2]));
+  }
+  float sfa[3] = {0.f, 0.f, 0.f}, sfb[3] = {0.f, 0.f, 0.f};
+  for (int t0 = chunk * kFuseChunk; t0 < min(p.T, (chunk + 1) * kFuseChunk); t0 += ROWS) {
+    const int t = t0 + r;
+    const bool on = t < min(p.T, (chunk + 1) * kFuseChunk);
+    const size_t row = ((size_t)b * p.T + (on ? t : t0)) * p.H + h;
+    const float g = on ? bf2f(p.grad[b * p.g_sb + (int64_t)(on ? t : t0) * p.g_st + h * p.g_sh + e])
+                       : 0.0f;
+    const float L = bf2f(p.local[row * D + e]);
+    const bool fine_on = t >= p.first_fine;
+    const bool coarse_on = p.coarse_values && t >= p.first_coarse;
+    float dlocal = g, dden_part = 0.0f;
+    if (on && fine_on) {
+      const float x = bf2f(p.rq.p[b * p.rq.sb + (int64_t)t * p.rq.st + h * p.rq.sh + e]);
+      const float C = coarse_on ? bf2f(p.coarse[row * D + e]) : 0.0f;
+      const float F = bf2f(p.fine[row * D + e]);
+      const float den = p.den[row];
+      float s[3];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) s[i] = rbf(rbf(a[i] * x) + bb[i]);
+      s[0] = rbf(s[0] + (coarse_on ? kLogTwoBf16 : 0.0f));
+      const float top = coarse_on ? fmaxf(s[0], fmaxf(s[1], s[2])) : fmaxf(s[0], s[2]);
+      float rho[3];
+      rho[0] = __expf(s[0] - top);
+      rho[1] = coarse_on ? __expf(s[1] - top) : 0.0f;
+      rho[2] = __expf(s[2] - top);
+      const float inv = 1.0f / (rho[0] + rho[1] + rho[2]);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) rho[i] *= inv;
+      const float xv[3] = {rbf(2.0f * L), rbf(p.gain * C), rbf(p.gain * F)};
+      float dr[3], mean = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) { dr[i] = g * xv[i]; mean += rho[i] * dr[i]; }
+      float drq = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const float ds = rho[i] * (dr[i] - mean);
+        drq += ds * a[i];
+        sfa[i] += ds * x;
+        sfb[i] += ds;
+      }
+      dlocal = 2.0f * g * rho[0];
+      const float dfine = p.gain * g * rho[2];
+      p.dcoarse[row * D + e] = p.gain * g * rho[1];
+      p.dnum[row * D + e] = dfine / den;
+      p.drq[row * D + e] = drq;
+      dden_part = -dfine * F / den;
+    } else if (on) {
+      p.dcoarse[row * D + e] = 0.0f;
+      p.dnum[row * D + e] = 0.0f;
+      p.drq[row * D + e] = 0.0f;
+    }
+    if (on) p.dlocal[row * D + e] = f2bf(dlocal);
+    // row reductions over e: D = 64 is one wave, D = 128 two waves
+    const float xq = bf2f(p.rq.p[b * p.rq.sb + (int64_t)(on ? t : t0) * p.rq.st + h * p.rq.sh + e]);
+    float mx = wave_max(xq);
+    if constexpr (D == 128) {
+      if (lane == 0) red[0][w] = mx;
+      __syncthreads();
+      mx = fmaxf(red[0][w & ~1], red[0][w | 1]);
+      __syncthreads();
+    }
+    const float ex = __expf(xq - mx);
+    float dl = wave_sum_fold(on ? dlocal * L : 0.0f);
+    float dd = wave_sum_fold(dden_part);
+    float sx = wave_sum_fold(ex);
+    if constexpr (D == 128) {
+      if (lane == 0) { red[0][w] = dl; red[1][w] = dd; red[2][w] = sx; }
+      __syncthreads();
+      dl = red[0][w & ~1] + red[0][w | 1];
+      dd = red[1][w & ~1] + red[1][w | 1];
+      sx = red[2][w & ~1] + red[2][w | 1];
+      __syncthreads();
+    }
+    if (on) p.h[row * D + e] = f2bf(ex / sx);
+    if (on && e == 0) {
+      p.delta[row] = dl;
+      p.dden[row] = dd;
+    }
+  }
+  // d fusion_a / d fusion_b: sum the ROWS lane rows, one atomic per (e, i).
+#pragma unroll
+  for (int i = 0; i < 3; ++i) { facc[i][r][e] = sfa[i]; facc[3 + i][r][e] = sfb[i]; }
+  __syncthreads();
+  for (int j = tid; j < 6 * D; j += kThreads) {
+    const int k = j / D, ee = j % D;
+    float s = 0.0f;
+    for (int rr = 0; rr < ROWS; ++rr) s += facc[k][rr][ee];
+    float* dst = k < 3 ? p.dfa : p.dfb;
+    atomicAdd(dst + (h * D + ee) * 3 + (k % 3), s);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Local attention adjoints (flash_attention.py:16-37 through autograd) with
+// the full-sequence windows: query q sees keys [max(0, F tile(q) - keep), q].
+// P = 2^(s c - lse2) from the forward's saved log2-sum-exp (c = log2 e /
+// sqrt(D)), dS = P (dP - delta), dP = dO V^T; dQ = dS K / sqrt(D),
+// dK = dS^T Q / sqrt(D), dV = P^T dO.
+constexpr int kBwdWaves = 4;
+constexpr int kBwdThreads = 64 * kBwdWaves;
+constexpr int kBwdKeys = 64;          // keys per staged block (dQ pass)
+constexpr int kBwdQ = 64;             // queries per staged block (dK/dV pass)
+
+TAO_DEV long long window_start(long long q, int ft, int keep) {
+  const long long s = (q / ft) * ft - keep;
+  return s > 0 ? s : 0;
+}
+
+// dQ pass: workgroup = 128 queries of one (batch, head); wave w owns 32.
+template <int D>
+struct DqSmem {
+  bf16_t k[kBwdKeys][D + 8];
+  bf16_t v[kBwdKeys][D + 8];
+  bf16_t kt[D][kBwdKeys + 4];
+};
+
+template <int D>
+__global__ __launch_bounds__(kBwdThreads) void attn_bwd_dq_kernel(AttnBwdParams p) {
+  __shared__ DqSmem<D> sm;
+  constexpr int CH = D / 8, DT = D / 32, KK = D / 16;
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const long long first = (long long)(blockIdx.x / BH) * (kBwdWaves * 32);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
+  const int count = (int)min((long long)kBwdWaves * 32, (long long)p.T - first);
+  const int nq = min(max(count - wave * 32, 0), 32);
+  const long long qtok = first + (nq > 0 ? wave * 32 + min(li, nq - 1) : 0);
+  const long long wave_first = first + wave * 32, wave_last = wave_first + nq - 1;
+  const long long kstart = window_start(first, p.ft, p.keep);
+  const long long kend = first + count;                 // exclusive
+  bf16x8 qreg[KK], oreg[KK];
+  {
+    const bf16_t* qrow = p.q.p + b * p.q.sb + qtok * p.q.st + h * p.q.sh;
+    const bf16_t* orow = p.dout + ((size_t)b * p.T + qtok) * p.H * D + (size_t)h * D;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      qreg[kk] = as_bf16x8(*(const uint4*)(qrow + 16 * kk + 8 * hl));
+      oreg[kk] = as_bf16x8(*(const uint4*)(orow + 16 * kk + 8 * hl));
+    }
+  }
+  const size_t qrowi = ((size_t)b * p.T + qtok) * p.H + h;
+  const float lse2 = p.lse[qrowi], dlt = p.delta[qrowi];
+  const long long ws = window_start(qtok, p.ft, p.keep);
+  const float scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)D));
+  floatx16 acc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+  for (long long kb = kstart; kb < kend; kb += kBwdKeys) {
+    __syncthreads();
+    for (int job = tid; job < kBwdKeys * CH; job += kBwdThreads) {
+      const int r = job / CH, c = job % CH;
+      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+      if (kb + r < kend) {
+        kv = *(const uint4*)(p.k.p + b * p.k.sb + (kb + r) * p.k.st + h * p.k.sh + c * 8);
+        vv = *(const uint4*)(p.v.p + b * p.v.sb + (kb + r) * p.v.st + h * p.v.sh + c * 8);
+      }
+      *(uint4*)&sm.k[r][c * 8] = kv;
+      *(uint4*)&sm.v[r][c * 8] = vv;
+    }
+    __syncthreads();
+    // K^T: job = (channel chunk c, key pair)
+    for (int job = tid; job < (kBwdKeys / 2) * CH; job += kBwdThreads) {
+      const int t0 = 2 * (job % (kBwdKeys / 2)), c = job / (kBwdKeys / 2);
+      const uint4 ua = *(const uint4*)&sm.k[t0][c * 8];
+      const uint4 ub = *(const uint4*)&sm.k[t0 + 1][c * 8];
+      const uint32_t wa[4] = {ua.x, ua.y, ua.z, ua.w}, wb[4] = {ub.x, ub.y, ub.z, ub.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        *(uint32_t*)&sm.kt[c * 8 + 2 * i][t0] = (wa[i] & 0xFFFFu) | (wb[i] << 16);
+        *(uint32_t*)&sm.kt[c * 8 + 2 * i + 1][t0] = (wa[i] >> 16) | (wb[i] & 0xFFFF0000u);
+      }
+    }
+    __syncthreads();
+    if (nq == 0 || kb > wave_last || kb + kBwdKeys <= window_start(wave_first, p.ft, p.keep))
+      continue;
+    floatx16 s[2], dp[2];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) { s[sub][i] = 0.0f; dp[sub][i] = 0.0f; }
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const bf16x8 ak = as_bf16x8(*(const uint4*)&sm.k[sub * 32 + li][16 * kk + 8 * hl]);
+        const bf16x8 av = as_bf16x8(*(const uint4*)&sm.v[sub * 32 + li][16 * kk + 8 * hl]);
+        s[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, qreg[kk], s[sub], 0, 0, 0);
+        dp[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, oreg[kk], dp[sub], 0, 0, 0);
+      }
+    }
+    // S^T layout: lane holds query li, keys 8 (i / 4) + 4 hl + i % 4 of each sub-tile.
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const long long key = kb + sub * 32 + 8 * (i / 4) + 4 * hl + (i % 4);
+        const bool ok = li < nq && key <= qtok && key >= ws && key < kend;
+        const float pv = ok ? __builtin_amdgcn_exp2f(fmaf(s[sub][i], scale_log2, -lse2)) : 0.0f;
+        s[sub][i] = pv * (dp[sub][i] - dlt);            // dS^T
+      }
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        uint32_t packed[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          packed[j] = pack_bf16x2(s[sub][8 * half + 2 * j], s[sub][8 * half + 2 * j + 1]);
+        const bf16x8 pb = as_bf16x8(make_uint4(packed[0], packed[1], packed[2], packed[3]));
+        const int kbase = sub * 32 + 16 * half + 4 * hl;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const uint2 lo = *(const uint2*)&sm.kt[t * 32 + li][kbase];
+          const uint2 hi = *(const uint2*)&sm.kt[t * 32 + li][kbase + 8];
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb, acc[t], 0, 0, 0);
+        }
+      }
+  }
+  if (li >= nq) return;
+  const float scale = (float)(1.0 / __builtin_sqrt((double)D));
+  bf16_t* dq = p.dq + qrowi * D;
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const int d = t * 32 + 8 * (i / 4) + 4 * hl;
+      uint2 packed;
+      packed.x = pack_bf16x2(acc[t][i] * scale, acc[t][i + 1] * scale);
+      packed.y = pack_bf16x2(acc[t][i + 2] * scale, acc[t][i + 3] * scale);
+      *(uint2*)(dq + d) = packed;
+    }
+}
+
+// dK / dV pass: workgroup = 128 keys of one (batch, head); wave w owns 32.
+// Queries that see a key k lie in [k, F (tile(k) + 1) + keep).
+template <int D>
+struct DkvSmem {
+  bf16_t q[kBwdQ][D + 8];
+  bf16_t o[kBwdQ][D + 8];          // dO rows
+  bf16_t qt[D][kBwdQ + 4];
+  bf16_t ot[D][kBwdQ + 4];
+  float lse[kBwdQ], dl[kBwdQ];
+};
+
+template <int D>
+__global__ __launch_bounds__(kBwdThreads) void attn_bwd_dkv_kernel(AttnBwdParams p) {
+  __shared__ DkvSmem<D> sm;
+  constexpr int CH = D / 8, DT = D / 32, KK = D / 16;
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const long long first = (long long)(blockIdx.x / BH) * (kBwdWaves * 32);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
+  const int count = (int)min((long long)kBwdWaves * 32, (long long)p.T - first);
+  const int nk = min(max(count - wave * 32, 0), 32);
+  const long long ktok = first + (nk > 0 ? wave * 32 + min(li, nk - 1) : 0);
+  const long long qend = min((long long)p.T, (first / p.ft + 1) * p.ft + p.keep);
+  bf16x8 kreg[KK], vreg[KK];
+  {
+    const bf16_t* krow = p.k.p + b * p.k.sb + ktok * p.k.st + h * p.k.sh;
+    const bf16_t* vrow = p.v.p + b * p.v.sb + ktok * p.v.st + h * p.v.sh;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      kreg[kk] = as_bf16x8(*(const uint4*)(krow + 16 * kk + 8 * hl));
+      vreg[kk] = as_bf16x8(*(const uint4*)(vrow + 16 * kk + 8 * hl));
+    }
+  }
+  const float scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)D));
+  floatx16 dk[DT], dv[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { dk[t][i] = 0.0f; dv[t][i] = 0.0f; }
+  for (long long qb = first; qb < qend; qb += kBwdQ) {
+    __syncthreads();
+    for (int job = tid; job < kBwdQ * CH; job += kBwdThreads) {
+      const int r = job / CH, c = job % CH;
+      uint4 qv = make_uint4(0, 0, 0, 0), ov = make_uint4(0, 0, 0, 0);
+      if (qb + r < qend) {
+        qv = *(const uint4*)(p.q.p + b * p.q.sb + (qb + r) * p.q.st + h * p.q.sh + c * 8);
+        ov = *(const uint4*)(p.dout + (((size_t)b * p.T + qb + r) * p.H + h) * D + c * 8);
+      }
+      *(uint4*)&sm.q[r][c * 8] = qv;
+      *(uint4*)&sm.o[r][c * 8] = ov;
+    }
+    if (tid < kBwdQ) {
+      const long long qq = qb + tid;
+      const size_t row = ((size_t)b * p.T + (qq < qend ? qq : qb)) * p.H + h;
+      sm.lse[tid] = qq < qend ? p.lse[row] : 0.0f;
+      sm.dl[tid] = qq < qend ? p.delta[row] : 0.0f;
+    }
+    __syncthreads();
+    for (int job = tid; job < (kBwdQ / 2) * CH; job += kBwdThreads) {
+      const int t0 = 2 * (job % (kBwdQ / 2)), c = job / (kBwdQ / 2);
+      const uint4 qa = *(const uint4*)&sm.q[t0][c * 8], qb2 = *(const uint4*)&sm.q[t0 + 1][c * 8];
+      const uint4 oa = *(const uint4*)&sm.o[t0][c * 8], ob = *(const uint4*)&sm.o[t0 + 1][c * 8];
+      const uint32_t wqa[4] = {qa.x, qa.y, qa.z, qa.w}, wqb[4] = {qb2.x, qb2.y, qb2.z, qb2.w};
+      const uint32_t woa[4] = {oa.x, oa.y, oa.z, oa.w}, wob[4] = {ob.x, ob.y, ob.z, ob.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        *(uint32_t*)&sm.qt[c * 8 + 2 * i][t0] = (wqa[i] & 0xFFFFu) | (wqb[i] << 16);
+        *(uint32_t*)&sm.qt[c * 8 + 2 * i + 1][t0] = (wqa[i] >> 16) | (wqb[i] & 0xFFFF0000u);
+        *(uint32_t*)&sm.ot[c * 8 + 2 * i][t0] = (woa[i] & 0xFFFFu) | (wob[i] << 16);
+        *(uint32_t*)&sm.ot[c * 8 + 2 * i + 1][t0] = (woa[i] >> 16) | (wob[i] & 0xFFFF0000u);
+      }
+    }
+    __syncthreads();
+    // keys of this wave: [kw, kw + nk); queries of the block: [qb, qb + 64)
+    const long long kw = first + wave * 32;
+    if (nk == 0 || qb + kBwdQ <= kw) continue;          // all queries before the keys
+    // One 32-query sub-block at a time (keeps S, dP and P of one block live).
+#pragma unroll 1
+    for (int sub = 0; sub < 2; ++sub) {
+      if (qb + sub * 32 >= qend || qb + sub * 32 + 31 < kw) continue;   // uniform
+      floatx16 sv, dpv;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) { sv[i] = 0.0f; dpv[i] = 0.0f; }
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const bf16x8 aq = as_bf16x8(*(const uint4*)&sm.q[sub * 32 + li][16 * kk + 8 * hl]);
+        const bf16x8 ao = as_bf16x8(*(const uint4*)&sm.o[sub * 32 + li][16 * kk + 8 * hl]);
+        sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, kreg[kk], sv, 0, 0, 0);
+        dpv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ao, vreg[kk], dpv, 0, 0, 0);
+      }
+      // S layout: lane holds key li, queries 8 (i / 4) + 4 hl + i % 4 of the sub-block.
+      float pm[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int qo = sub * 32 + 8 * (i / 4) + 4 * hl + (i % 4);
+        const long long qq = qb + qo;
+        const bool ok = li < nk && qq < qend && ktok <= qq && ktok >= window_start(qq, p.ft, p.keep);
+        const float pv = ok ? __builtin_amdgcn_exp2f(fmaf(sv[i], scale_log2, -sm.lse[qo])) : 0.0f;
+        pm[i] = pv;
+        sv[i] = pv * (dpv[i] - sm.dl[qo]);            // dS
+      }
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        uint32_t pp[4], dd[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          pp[j] = pack_bf16x2(pm[8 * half + 2 * j], pm[8 * half + 2 * j + 1]);
+          dd[j] = pack_bf16x2(sv[8 * half + 2 * j], sv[8 * half + 2 * j + 1]);
+        }
+        const bf16x8 pb = as_bf16x8(make_uint4(pp[0], pp[1], pp[2], pp[3]));
+        const bf16x8 db = as_bf16x8(make_uint4(dd[0], dd[1], dd[2], dd[3]));
+        const int kbase = sub * 32 + 16 * half + 4 * hl;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const uint2 olo = *(const uint2*)&sm.ot[t * 32 + li][kbase];
+          const uint2 ohi = *(const uint2*)&sm.ot[t * 32 + li][kbase + 8];
+          dv[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              as_bf16x8(make_uint4(olo.x, olo.y, ohi.x, ohi.y)), pb, dv[t], 0, 0, 0);
+          const uint2 qlo = *(const uint2*)&sm.qt[t * 32 + li][kbase];
+          const uint2 qhi = *(const uint2*)&sm.qt[t * 32 + li][kbase + 8];
+          dk[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              as_bf16x8(make_uint4(qlo.x, qlo.y, qhi.x, qhi.y)), db, dk[t], 0, 0, 0);
+        }
+      }
+    }
+  }
+  if (li >= nk) return;
+  const float scale = (float)(1.0 / __builtin_sqrt((double)D));
+  const size_t krowi = ((size_t)b * p.T + ktok) * p.H + h;
+  bf16_t* dkp = p.dk + krowi * D;
+  float* dvp = p.dv + krowi * D;
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const int d = t * 32 + 8 * (i / 4) + 4 * hl;
+      uint2 packed;
+      packed.x = pack_bf16x2(dk[t][i] * scale, dk[t][i + 1] * scale);
+      packed.y = pack_bf16x2(dk[t][i + 2] * scale, dk[t][i + 3] * scale);
+      *(uint2*)(dkp + d) = packed;
+      *(float4*)(dvp + d) = make_float4(dv[t][i], dv[t][i + 1], dv[t][i + 2], dv[t][i + 3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Memory-branch adjoints (selected_read.py:175-187 and autograd through
+// tao_stream.py:530-665). For query q of tile t (V = t - lag visible fines,
+// K = V / 8 completed pages, P = K + (V % 8 > 0)), selected fine f on page
+// g = f / 8, channel d:
+//   a[q][f][d] = h[q][d] pw_t[g][d] sw_t[f][d],
+//   num[q] = sum_f a[q][f] C_f,  den[q] = sum_f sum_d a[q][f][d];
+// given dnum, dden (fuse_bwd):
+//   da = dnum C_f^T + dden,  dC_f += a (x) dnum,
+//   dh += da sw pw,  d pw_t[g] += da sw h,  d sw_t[f] += da h pw.
+// Tiles of 256 queries share V; lanes are channels (d = lane + 64 k).
+constexpr int kRbQ = 128;              // queries per read_bwd workgroup (4 waves x 32)
+constexpr int kRbWaves = 4;
+
+TAO_DEV int tile_visible(int t, int lag) { return t > lag ? t - lag : 0; }
+
+template <int D>
+struct ReadBwdSmem {
+  bf16_t ct[D][D];                     // C^T of the current fine (or G^T)
+  bf16_t dn[kRbWaves][32][D];          // dnum rows of each wave's queries (bf16)
+  bf16_t hq[kRbWaves][32][D];          // h rows
+  float dsw[D];                        // d sw of the current fine (sum over waves)
+  float dpw[64][D];                    // d pw of the tile's pages (P <= 64)
+  uint32_t bits[512];
+  int pre[512];
+  int uni[1024];
+  int n_union;
+};
+
+template <int D>
+__global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p) {
+  constexpr int PER = D / 64;
+  __shared__ ReadBwdSmem<D> sm;
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int q0 = (blockIdx.x / BH) * kRbQ;
+  const int tile = q0 / p.ft;
+  const int V = tile_visible(tile, p.keep / p.ft);
+  if (V == 0) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int G = p.group, K = V / G, P = K + (V % G > 0), erel = V - 1;
+  const int nq = min(kRbQ, p.T - q0);
+  const int words = (V + 31) >> 5;
+  const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
+  const bf16_t* psw = p.psw_pool + ((size_t)erel * BH + bh) * 8 * D;
+  const bf16_t* gsw = p.fine_sw + (size_t)bh * p.fine_cap * D;
+  // ---- stage dnum and h rows; union of the block's selections
+  for (int i = tid; i < 512; i += kRbWaves * 64) sm.bits[i] = 0u;
+  for (int i = tid; i < 64 * D; i += kRbWaves * 64) (&sm.dpw[0][0])[i] = 0.0f;
+  for (int i = tid; i < kRbQ * D; i += kRbWaves * 64) {
+    const int qi = i / D, d = i % D;
+    const size_t row = ((size_t)b * p.T + q0 + min(qi, nq - 1)) * p.H + h;
+    sm.dn[qi / 32][qi % 32][d] = qi < nq ? f2bf(p.dnum[row * D + d]) : (bf16_t)0;
+    sm.hq[qi / 32][qi % 32][d] = qi < nq ? p.h[row * D + d] : (bf16_t)0;
+  }
+  __syncthreads();
+  for (int i = tid; i < nq * words; i += kRbWaves * 64) {
+    const int qi = i / words, wd = i % words;
+    const uint32_t v = p.qsel[((size_t)(b * p.T + q0 + qi) * p.H + h) * p.qsel_words + wd];
+    if (v) atomicOr(&sm.bits[wd], v);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int i = 0; i < words; ++i) { sm.pre[i] = run; run += __popc(sm.bits[i]); }
+    sm.n_union = run;
+  }
+  __syncthreads();
+  for (int i = tid; i < words; i += kRbWaves * 64) {
+    uint32_t bits = sm.bits[i];
+    int r = sm.pre[i];
+    while (bits) {
+      sm.uni[r++] = i * 32 + __ffs(bits) - 1;
+      bits &= bits - 1;
+    }
+  }
+  __syncthreads();
+  const int U = sm.n_union;
+  float dh[32][PER];
+#pragma unroll
+  for (int qi = 0; qi < 32; ++qi)
+#pragma unroll
+    for (int k = 0; k < PER; ++k) dh[qi][k] = 0.0f;
+  const int nqw = min(32, max(0, nq - 32 * w));
+  const uint32_t* qs = p.qsel + ((size_t)(b * p.T + q0 + 32 * w) * p.H + h) * p.qsel_words;
+  for (int u = 0; u < U; ++u) {
+    const int f = sm.uni[u];
+    const int g = f / G;
+    __syncthreads();                                   // previous fine consumed
+    const bf16_t* src = p.bank + ((size_t)bh * p.fine_cap + f) * D * D;
+    for (int i = tid; i < D * D / 8; i += kRbWaves * 64)
+      *(uint4*)(&sm.ct[0][0] + i * 8) = *(const uint4*)(src + i * 8);
+    for (int i = tid; i < D; i += kRbWaves * 64) sm.dsw[i] = 0.0f;
+    __syncthreads();
+    float swv[PER], pwv[PER], dpw_acc[PER], dsw_acc[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int d = lane + 64 * k;
+      swv[k] = bf2f(f < K * G ? gsw[(size_t)f * D + d] : psw[(size_t)(f - K * G) * D + d]);
+      pwv[k] = bf2f(pw[(size_t)g * D + d]);
+      dpw_acc[k] = 0.0f;
+      dsw_acc[k] = 0.0f;
+    }
+#pragma unroll 1
+    for (int qi = 0; qi < nqw; ++qi) {
+      if (!((qs[(size_t)qi * p.H * p.qsel_words + (f >> 5)] >> (f & 31)) & 1u)) continue;
+      const size_t row = ((size_t)b * p.T + q0 + 32 * w + qi) * p.H + h;
+      const float dd = p.dden[row];
+      float da[PER];
+#pragma unroll
+      for (int k = 0; k < PER; ++k) da[k] = dd;
+      for (int e = 0; e < D; ++e) {
+        const float dn = bf2f(sm.dn[w][qi][e]);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) da[k] = fmaf(dn, bf2f(sm.ct[e][lane + 64 * k]), da[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < PER; ++k) {
+        const float hv = bf2f(sm.hq[w][qi][lane + 64 * k]);
+        const float dhv = da[k] * swv[k];
+        dpw_acc[k] = fmaf(dhv, hv, dpw_acc[k]);
+        dsw_acc[k] = fmaf(da[k] * hv, pwv[k], dsw_acc[k]);
+        // dh of query qi (registers are indexed by the unrolled slot)
+#pragma unroll
+        for (int s2 = 0; s2 < 32; ++s2)
+          if (s2 == qi) dh[s2][k] = fmaf(dhv, pwv[k], dh[s2][k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      atomicAdd(&sm.dsw[lane + 64 * k], dsw_acc[k]);
+      atomicAdd(&sm.dpw[g][lane + 64 * k], dpw_acc[k]);
+    }
+    __syncthreads();
+    for (int i = tid; i < D; i += kRbWaves * 64)
+      atomicAdd(p.dsw_tile + (((size_t)tile * BH + bh) * p.v_max + f) * D + i, sm.dsw[i]);
+  }
+  // ---- coarse read: dh += dcoarse G_K^T (coarse_pool holds G^T[e][d])
+  const bool coarse = p.coarse_values && K >= 1;
+  if (coarse) {
+    __syncthreads();
+    const bf16_t* gsrc = p.coarse_pool + ((size_t)(K - p.coarse_first) * BH + bh) * D * D;
+    for (int i = tid; i < D * D / 8; i += kRbWaves * 64)
+      *(uint4*)(&sm.ct[0][0] + i * 8) = *(const uint4*)(gsrc + i * 8);
+    for (int i = tid; i < kRbQ * D; i += kRbWaves * 64) {
+      const int qi = i / D, d = i % D;
+      const size_t row = ((size_t)b * p.T + q0 + min(qi, nq - 1)) * p.H + h;
+      sm.dn[qi / 32][qi % 32][d] = qi < nq ? f2bf(p.dcoarse[row * D + d]) : (bf16_t)0;
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int qi = 0; qi < nqw; ++qi) {
+      float acc[PER];
+#pragma unroll
+      for (int k = 0; k < PER; ++k) acc[k] = 0.0f;
+      for (int e = 0; e < D; ++e) {
+        const float dc = bf2f(sm.dn[w][qi][e]);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) acc[k] = fmaf(dc, bf2f(sm.ct[e][lane + 64 * k]), acc[k]);
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 32; ++s2)
+        if (s2 == qi)
+#pragma unroll
+          for (int k = 0; k < PER; ++k) dh[s2][k] += acc[k];
+    }
+  }
+#pragma unroll
+  for (int qi = 0; qi < 32; ++qi) {
+    if (qi < nqw) {
+      const size_t row = ((size_t)b * p.T + q0 + 32 * w + qi) * p.H + h;
+#pragma unroll
+      for (int k = 0; k < PER; ++k) p.dh[row * D + lane + 64 * k] = dh[qi][k];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < P * D; i += kRbWaves * 64)
+    atomicAdd(p.dpw + (((size_t)tile * BH + bh) * p.pool_pcap + i / D) * D + i % D,
+              sm.dpw[i / D][i % D]);
+}
+
+// Outer products over a query set: out[e][d] = sum_q x[q][e] y[q][d].
+// mode 0 (dC of fine f = blockIdx / BH): queries of every tile that sees f,
+//   x = dnum, y = a (masked by the query's selection of f); plus the coarse
+//   path's share w_f[d] sum_{K > g} cw_K[g][d] dG_K[d][e] for completed f.
+// mode 1 (dG of completed count K = coarse_first + blockIdx / BH): queries of
+//   the tiles with K completed pages, x = dcoarse, y = h.
+// Thread (d = tid % D, row group) owns rows e of one column d.
+constexpr int kObQ = 16;
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int mode) {
+  constexpr int GROUPS = kThreads / D, ROWS = D / GROUPS;
+  __shared__ float xs[kObQ][D], ys[kObQ][D];
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int item = blockIdx.x / BH;
+  const int tid = threadIdx.x, d = tid % D, rg = tid / D;
+  const int G = p.group, lag = p.keep / p.ft;
+  const int n_tiles = (p.T + p.ft - 1) / p.ft;
+  float acc[ROWS];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+  int t_lo, t_hi;
+  const int f = item, Kc = p.coarse_first + item;
+  if (mode == 0) {
+    t_lo = f + lag + 1;            // first tile that sees fine f
+    t_hi = n_tiles;
+  } else {
+    t_lo = lag + G * Kc;
+    t_hi = min(n_tiles, lag + G * Kc + G);
+  }
+  const bf16_t* gsw = p.fine_sw + (size_t)bh * p.fine_cap * D;
+  for (int t = t_lo; t < t_hi; ++t) {
+    const int V = tile_visible(t, lag), erel = V - 1, K = V / G;
+    float yscale = 1.0f;
+    if (mode == 0) {
+      const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
+      const bf16_t* psw = p.psw_pool + ((size_t)erel * BH + bh) * 8 * D;
+      yscale = bf2f(pw[(size_t)(f / G) * D + d]) *
+               bf2f(f < K * G ? gsw[(size_t)f * D + d] : psw[(size_t)(f - K * G) * D + d]);
+    }
+    const int qa = t * p.ft, qb_end = min(p.T, qa + p.ft);
+    for (int qb = qa; qb < qb_end; qb += kObQ) {
+      __syncthreads();
+      for (int i = tid; i < kObQ * D; i += kThreads) {
+        const int qi = i / D, c = i % D;
+        const int q = qb + qi;
+        float xv = 0.0f, yv = 0.0f;
+        if (q < qb_end) {
+          const size_t row = ((size_t)b * p.T + q) * p.H + h;
+          bool sel = true;
+          if (mode == 0)
+            sel = (p.qsel[row * p.qsel_words + (f >> 5)] >> (f & 31)) & 1u;
+          if (sel) {
+            xv = mode == 0 ? p.dnum[row * D + c] : p.dcoarse[row * D + c];
+            yv = bf2f(p.h[row * D + c]);
+          }
+        }
+        xs[qi][c] = xv;
+        ys[qi][c] = yv;
+      }
+      __syncthreads();
+#pragma unroll 4
+      for (int qi = 0; qi < kObQ; ++qi) {
+        const float y = ys[qi][d] * yscale;
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) acc[r] = fmaf(xs[qi][rg * ROWS + r], y, acc[r]);
+      }
+    }
+  }
+  if (mode == 0 && p.coarse_values && f < G * (p.v_max / G)) {
+    // coarse share: w_f[d] sum_{K > g} cw_K[g][d] dG_K[d][e]
+    const int g = f / G;
+    const bf16_t* pz = p.page_z + (size_t)bh * p.page_cap * D;
+    const float wf = bf2f(gsw[(size_t)f * D + d]);
+    for (int k2 = max(g + 1, p.coarse_first); k2 < p.coarse_first + p.coarse_count; ++k2) {
+      float m = -__builtin_inff();
+      for (int j = 0; j < k2; ++j) m = fmaxf(m, bf2f(pz[(size_t)j * D + d]));
+      float z = 0.0f;
+      for (int j = 0; j < k2; ++j) z += __expf(bf2f(pz[(size_t)j * D + d]) - m);
+      const float cw = __expf(bf2f(pz[(size_t)g * D + d]) - m) / z;
+      const float* dg = p.dgc + ((size_t)(k2 - p.coarse_first) * BH + bh) * D * D;
+#pragma unroll
+      for (int r = 0; r < ROWS; ++r) acc[r] = fmaf(wf * cw, dg[(size_t)(rg * ROWS + r) * D + d], acc[r]);
+    }
+  }
+  float* out = mode == 0 ? p.dc + ((size_t)bh * p.v_max + f) * D * D
+                         : p.dgc + ((size_t)item * BH + bh) * D * D;
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) out[(size_t)(rg * ROWS + r) * D + d] = acc[r];
+}
+
+// Page-level adjoints of one tile (softmax over its P pages, the pending
+// page's logsumexp and segment weights). Thread per channel.
+template <int D>
+__global__ __launch_bounds__(D) void page_bwd_kernel(MemBwdParams p) {
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int tile = blockIdx.x / BH;
+  const int lag = p.keep / p.ft, G = p.group;
+  const int V = tile_visible(tile, lag);
+  if (V == 0) return;
+  const int d = threadIdx.x;
+  const int K = V / G, pend = V % G, P = K + (pend > 0), erel = V - 1;
+  const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
+  const bf16_t* psw = p.psw_pool + ((size_t)erel * BH + bh) * 8 * D;
+  const float* dpw = p.dpw + ((size_t)tile * BH + bh) * p.pool_pcap * D;
+  const float* dsw = p.dsw_tile + ((size_t)tile * BH + bh) * p.v_max * D;
+  float s = 0.0f;
+  for (int g = 0; g < P; ++g) s += bf2f(pw[(size_t)g * D + d]) * dpw[(size_t)g * D + d];
+  for (int g = 0; g < K; ++g) {
+    const float dpz = bf2f(pw[(size_t)g * D + d]) * (dpw[(size_t)g * D + d] - s);
+    atomicAdd(p.dpz + ((size_t)bh * p.page_cap + g) * D + d, dpz);
+  }
+  for (int f = 0; f < K * G; ++f)
+    atomicAdd(p.dsw + ((size_t)bh * p.v_max + f) * D + d, dsw[(size_t)f * D + d]);
+  if (pend) {
+    float dpend = bf2f(pw[(size_t)K * D + d]) * (dpw[(size_t)K * D + d] - s);
+    for (int i = 0; i < pend; ++i)
+      dpend -= dsw[(size_t)(K * G + i) * D + d] * bf2f(psw[(size_t)i * D + d]);
+    for (int i = 0; i < pend; ++i) {
+      const float w = bf2f(psw[(size_t)i * D + d]);
+      atomicAdd(p.dz + ((size_t)bh * p.v_max + K * G + i) * D + d,
+                dsw[(size_t)(K * G + i) * D + d] * w + dpend * w);
+    }
+  }
+}
+
+// Coarse path, page level, for completed count K (one workgroup per (K, bh),
+// thread per channel): cw = softmax over pages < K of page_z,
+// d cw[g][d] = sum_e dG[d][e] pc_g[d][e] -> d page_z (softmax adjoint), and
+// d w_f[d] = cw[g][d] sum_e dG[d][e] C_f[d][e] -> d sw of f (w_f = sw_f).
+template <int D>
+__global__ __launch_bounds__(D) void coarse_page_bwd_kernel(MemBwdParams p) {
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int K = p.coarse_first + blockIdx.x / BH;
+  const int d = threadIdx.x, G = p.group;
+  const bf16_t* pz = p.page_z + (size_t)bh * p.page_cap * D;
+  const float* dg = p.dgc + ((size_t)(K - p.coarse_first) * BH + bh) * D * D;   // [e][d]
+  float m = -__builtin_inff();
+  for (int g = 0; g < K; ++g) m = fmaxf(m, bf2f(pz[(size_t)g * D + d]));
+  float z = 0.0f;
+  for (int g = 0; g < K; ++g) z += __expf(bf2f(pz[(size_t)g * D + d]) - m);
+  float s = 0.0f;
+  for (int g = 0; g < K; ++g) {
+    const float cw = __expf(bf2f(pz[(size_t)g * D + d]) - m) / z;
+    const bf16_t* pc = p.page_c + ((size_t)bh * p.page_cap + g) * D * D;   // [e][d]
+    float dcw = 0.0f;
+    for (int e = 0; e < D; ++e) dcw = fmaf(dg[(size_t)e * D + d], bf2f(pc[(size_t)e * D + d]), dcw);
+    s += cw * dcw;
+  }
+  for (int g = 0; g < K; ++g) {
+    const float cw = __expf(bf2f(pz[(size_t)g * D + d]) - m) / z;
+    const bf16_t* pc = p.page_c + ((size_t)bh * p.page_cap + g) * D * D;
+    float dcw = 0.0f;
+    for (int e = 0; e < D; ++e) dcw = fmaf(dg[(size_t)e * D + d], bf2f(pc[(size_t)e * D + d]), dcw);
+    atomicAdd(p.dpz + ((size_t)bh * p.page_cap + g) * D + d, cw * (dcw - s));
+    for (int i = 0; i < G; ++i) {
+      const int f = g * G + i;
+      const bf16_t* c = p.bank + ((size_t)bh * p.fine_cap + f) * D * D;       // C^T [e][d]
+      float dw = 0.0f;
+      for (int e = 0; e < D; ++e) dw = fmaf(dg[(size_t)e * D + d], bf2f(c[(size_t)e * D + d]), dw);
+      atomicAdd(p.dsw + ((size_t)bh * p.v_max + f) * D + d, cw * dw);
+    }
+  }
+}
+
+// Completed page g: d z of its fines from d sw (global) and d page_z
+// (logsumexp adjoint; its softmax weights are the final sw).
+template <int D>
+__global__ __launch_bounds__(D) void zpage_bwd_kernel(MemBwdParams p) {
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int g = blockIdx.x / BH;
+  const int d = threadIdx.x, G = p.group;
+  const bf16_t* gsw = p.fine_sw + (size_t)bh * p.fine_cap * D;
+  float t1[8], dpz = p.dpz[((size_t)bh * p.page_cap + g) * D + d];
+  for (int i = 0; i < G; ++i) {
+    const int f = g * G + i;
+    t1[i] = p.dsw[((size_t)bh * p.v_max + f) * D + d] * bf2f(gsw[(size_t)f * D + d]);
+    dpz -= t1[i];
+  }
+  for (int i = 0; i < G; ++i) {
+    const int f = g * G + i;
+    p.dz[((size_t)bh * p.v_max + f) * D + d] += t1[i] + dpz * bf2f(gsw[(size_t)f * D + d]);
+  }
+}
+
+// Softmax writer adjoint of block f (tao_stream.py:66-77): per channel d over
+// the block's tokens, P = softmax_t(raw_k), z = logsumexp, C = P^T V;
+//   dP[t][d] = sum_e dC[d][e] v[t][e],  dv[t][e] += sum_d P[t][d] dC[d][e],
+//   d raw_k[t][d] = P (dP - sum_t P dP) + dz P, with sum_t P dP = sum_e dC C.
+// Thread per token; the token's raw_k and v rows sit in registers, dC^T in
+// LDS chunks: 16 channels d for d raw_k, then 16 values e for dv.
+template <int D>
+__global__ __launch_bounds__(kThreads) void writer_bwd_kernel(MemBwdParams p) {
+  constexpr int CK = 16;
+  __shared__ float chunk[D * CK];                // dC^T[e][d0 + j] or dC^T[e0 + j][d]
+  __shared__ float stat[3][D];                   // max, 1 / Z, sum_e dC C
+  __shared__ float red[kThreads / D][D];
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int f = blockIdx.x / BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int t = threadIdx.x;                     // token of the block (ft == 256)
+  const int tok = f * p.ft + t;
+  const bf16_t* kg = p.raw_k.p + b * p.raw_k.sb + (int64_t)tok * p.raw_k.st + h * p.raw_k.sh;
+  const bf16_t* vg = p.v.p + b * p.v.sb + (int64_t)tok * p.v.st + h * p.v.sh;
+  const float* dc = p.dc + ((size_t)bh * p.v_max + f) * D * D;                // [e][d]
+  const bf16_t* c = p.bank + ((size_t)bh * p.fine_cap + f) * D * D;           // C^T [e][d]
+  // column statistics: thread (d, token group) over 256 / (kThreads / D) tokens
+  {
+    constexpr int TG = kThreads / D, TPG = 256 / TG;
+    const int d = t % D, tg = t / D;
+    const bf16_t* col = p.raw_k.p + b * p.raw_k.sb + h * p.raw_k.sh + d;
+    float m = -__builtin_inff();
+    for (int i = 0; i < TPG; ++i)
+      m = fmaxf(m, bf2f(col[(int64_t)(f * p.ft + tg * TPG + i) * p.raw_k.st]));
+    red[tg][d] = m;
+    __syncthreads();
+    if (tg == 0) {
+      for (int i = 1; i < TG; ++i) m = fmaxf(m, red[i][d]);
+      stat[0][d] = m;
+    }
+    __syncthreads();
+    m = stat[0][d];
+    float z = 0.0f;
+    for (int i = 0; i < TPG; ++i)
+      z += __expf(bf2f(col[(int64_t)(f * p.ft + tg * TPG + i) * p.raw_k.st]) - m);
+    red[tg][d] = z;
+    __syncthreads();
+    if (tg == 0) {
+      for (int i = 1; i < TG; ++i) z += red[i][d];
+      stat[1][d] = 1.0f / z;
+      float sdc = 0.0f;
+      for (int e = 0; e < D; ++e) sdc = fmaf(dc[(size_t)e * D + d], bf2f(c[(size_t)e * D + d]), sdc);
+      stat[2][d] = sdc;
+    }
+    __syncthreads();
+  }
+  uint32_t kp[D / 2], vp[D / 2];                 // the token's raw_k and v rows (bf16 pairs)
+#pragma unroll
+  for (int i = 0; i < D / 8; ++i) {
+    const uint4 ku = *(const uint4*)(kg + 8 * i), vu = *(const uint4*)(vg + 8 * i);
+    kp[4 * i] = ku.x; kp[4 * i + 1] = ku.y; kp[4 * i + 2] = ku.z; kp[4 * i + 3] = ku.w;
+    vp[4 * i] = vu.x; vp[4 * i + 1] = vu.y; vp[4 * i + 2] = vu.z; vp[4 * i + 3] = vu.w;
+  }
+  auto unpack = [](const uint32_t* r, int i) __attribute__((always_inline)) {
+    return __uint_as_float((i & 1) ? (r[i >> 1] & 0xFFFF0000u) : (r[i >> 1] << 16));
+  };
+  // ---- d raw_k, 16 channels at a time
+  bf16_t* dkr = p.draw_k + (((size_t)b * p.T + tok) * p.H + h) * D;
+  const float* dzf = p.dz + ((size_t)bh * p.v_max + f) * D;
+  for (int d0 = 0; d0 < D; d0 += CK) {
+    __syncthreads();
+    for (int i = t; i < D * CK; i += kThreads) chunk[i] = dc[(size_t)(i / CK) * D + d0 + i % CK];
+    __syncthreads();
+    float dp[CK];
+#pragma unroll
+    for (int j = 0; j < CK; ++j) dp[j] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < D; ++e) {
+      const float ve = unpack(vp, e);
+#pragma unroll
+      for (int j = 0; j < CK; ++j) dp[j] = fmaf(chunk[e * CK + j], ve, dp[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < CK; ++j) {
+      const int d = d0 + j;
+      const float pr = __expf(bf2f(kg[d]) - stat[0][d]) * stat[1][d];
+      dkr[d] = f2bf(pr * (dp[j] - stat[2][d]) + dzf[d] * pr);
+    }
+  }
+  // ---- dv, 16 values at a time: dv[e] = sum_d P[d] dC^T[e][d]
+  float* dvr = p.dv + (((size_t)b * p.T + tok) * p.H + h) * D;
+  for (int e0 = 0; e0 < D; e0 += CK) {
+    __syncthreads();
+    for (int i = t; i < D * CK; i += kThreads) chunk[i] = dc[(size_t)(e0 + i / D) * D + i % D];
+    __syncthreads();
+    float acc[CK];
+#pragma unroll
+    for (int j = 0; j < CK; ++j) acc[j] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const float pr = __expf(unpack(kp, d) - stat[0][d]) * stat[1][d];
+#pragma unroll
+      for (int j = 0; j < CK; ++j) acc[j] = fmaf(pr, chunk[j * D + d], acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < CK; ++j) dvr[e0 + j] += acc[j];
+  }
+}
+
+// d raw_q = fusion part + h (dh - sum_d h dh) (softmax adjoint); dv -> bf16;
+// d raw_k of tokens no block covers = 0. Thread per channel, row per wave.
+template <int D>
+__global__ __launch_bounds__(kThreads) void finish_bwd_kernel(MemBwdParams p) {
+  constexpr int PER = D / 64;
+  const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int rows = p.B * p.T * p.H;
+  if (row >= rows) return;
+  const int t = (row / p.H) % p.T;
+  const int lag = p.keep / p.ft;
+  const bool hist = tile_visible(t / p.ft, lag) > 0;
+  float hv[PER], dh[PER], s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int d = lane + 64 * k;
+    hv[k] = bf2f(p.h[(size_t)row * D + d]);
+    dh[k] = hist ? p.dh[(size_t)row * D + d] : 0.0f;
+    s += hv[k] * dh[k];
+  }
+  s = wave_sum_fold(s);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int d = lane + 64 * k;
+    const float g = p.drq_fuse[(size_t)row * D + d] + hv[k] * (dh[k] - s);
+    p.draw_q[(size_t)row * D + d] = f2bf(g);
+    p.dv_out[(size_t)row * D + d] = f2bf(p.dv[(size_t)row * D + d]);
+    if (t >= p.ft * p.v_max) p.draw_k[(size_t)row * D + d] = 0;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_fuse_bwd(const TrainBwdParams& p, int head_dim, hipStream_t s) {
+  const int chunks = (p.T + kFuseChunk - 1) / kFuseChunk;
+  const dim3 grid((unsigned)(chunks * p.B * p.H));
+  if (head_dim == 128)
+    hipLaunchKernelGGL(fuse_bwd_kernel<128>, grid, dim3(kThreads), 0, s, p);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL(fuse_bwd_kernel<64>, grid, dim3(kThreads), 0, s, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_bwd(const AttnBwdParams& p, int head_dim, hipStream_t s) {
+  if (p.T <= 0) return hipSuccess;
+  const int blocks = (p.T + kBwdWaves * 32 - 1) / (kBwdWaves * 32);
+  const dim3 grid((unsigned)(blocks * p.B * p.H));
+  if (head_dim == 128) {
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<128>, grid, dim3(kBwdThreads), 0, s, p);
+    hipLaunchKernelGGL(attn_bwd_dkv_kernel<128>, grid, dim3(kBwdThreads), 0, s, p);
+  } else if (head_dim == 64) {
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<64>, grid, dim3(kBwdThreads), 0, s, p);
+    hipLaunchKernelGGL(attn_bwd_dkv_kernel<64>, grid, dim3(kBwdThreads), 0, s, p);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s) {
+  const int BH = p.B * p.H;
+  const int n_tiles = (p.T + p.ft - 1) / p.ft;
+  // read_bwd keeps the tile's page adjoints in LDS: at most 64 pages.
+  if (p.group != 8 || p.ft != 256 || p.v_max / p.group + 1 > 64) return hipErrorInvalidValue;
+#define TAO_MEM_BWD(D_)                                                                      \
+  do {                                                                                       \
+    if (p.v_max > 0) {                                                                       \
+      const int blocks = (p.T + kRbQ - 1) / kRbQ;                                            \
+      hipLaunchKernelGGL(read_bwd_kernel<D_>, dim3((unsigned)(blocks * BH)),                 \
+                         dim3(kRbWaves * 64), 0, s, p);                                      \
+      if (p.coarse_values && p.coarse_count > 0) {                                           \
+        hipLaunchKernelGGL(outer_bwd_kernel<D_>, dim3((unsigned)(p.coarse_count * BH)),      \
+                           dim3(kThreads), 0, s, p, 1);                                      \
+        hipLaunchKernelGGL(coarse_page_bwd_kernel<D_>, dim3((unsigned)(p.coarse_count * BH)),\
+                           dim3(D_), 0, s, p);                                               \
+      }                                                                                      \
+      hipLaunchKernelGGL(outer_bwd_kernel<D_>, dim3((unsigned)(p.v_max * BH)),               \
+                         dim3(kThreads), 0, s, p, 0);                                        \
+      hipLaunchKernelGGL(page_bwd_kernel<D_>, dim3((unsigned)(n_tiles * BH)), dim3(D_), 0,   \
+                         s, p);                                                              \
+      if (p.v_max / p.group > 0)                                                             \
+        hipLaunchKernelGGL(zpage_bwd_kernel<D_>, dim3((unsigned)((p.v_max / p.group) * BH)), \
+                           dim3(D_), 0, s, p);                                               \
+      hipLaunchKernelGGL(writer_bwd_kernel<D_>, dim3((unsigned)(p.v_max * BH)),              \
+                         dim3(kThreads), 0, s, p);                                           \
+    }                                                                                        \
+    const int rows = p.B * p.T * p.H;                                                        \
+    hipLaunchKernelGGL(finish_bwd_kernel<D_>,                                                \
+                       dim3((unsigned)((rows + kThreads / 64 - 1) / (kThreads / 64))),       \
+                       dim3(kThreads), 0, s, p);                                             \
+  } while (0)
+  if (head_dim == 128)
+    TAO_MEM_BWD(128);
+  else if (head_dim == 64)
+    TAO_MEM_BWD(64);
+  else
+    return hipErrorInvalidValue;
+#undef TAO_MEM_BWD
+  return hipGetLastError();
+}
+
+}  // namespace tao

@@ -48,7 +48,18 @@ class PrefillPools(ctypes.Structure):
     _fields_ = [("pw_pool", _vp), ("psw_pool", _vp), ("sel_pool", _vp),
                 ("pool_pcap", _i32), ("epochs", _i32), ("sel_slots", _i32),
                 ("coarse_pool", _vp), ("coarse_first", _i32), ("coarse_count", _i32),
-                ("qsel", _vp), ("qsel_words", _i32)]
+                ("qsel", _vp), ("qsel_words", _i32),
+                ("local_lse", _vp), ("coarse_out", _vp), ("fine_out", _vp), ("den_out", _vp)]
+
+
+class TrainBwd(ctypes.Structure):
+    _fields_ = [("grad", _vp), ("grad_s", _I64x3),
+                ("local", _vp), ("local_lse", _vp), ("coarse_out", _vp), ("fine_out", _vp),
+                ("den_out", _vp),
+                ("dq", _vp), ("dk", _vp), ("dv", _vp), ("draw_q", _vp), ("draw_k", _vp),
+                ("dfusion_a", _vp), ("dfusion_b", _vp),
+                ("workspace", _vp), ("workspace_bytes", _sz),
+                ("dz_out", _vp), ("dc_out", _vp)]
 
 
 class StreamCfg(ctypes.Structure):
@@ -93,6 +104,11 @@ _SIGNATURES = {
     "tao_prefill_plan": ([ctypes.POINTER(StreamCfg), _i64, _i64, _i32, _i32, _i32,
                           _vp, _i64, ctypes.POINTER(_i64)], _i32),
     "tao_train_plan": ([ctypes.POINTER(StreamCfg), _i64, _vp, _i64, ctypes.POINTER(_i64)], _i32),
+    "tao_train_bwd_workspace_bytes": ([ctypes.POINTER(StateDev), _i64, _i32,
+                                       ctypes.POINTER(PrefillPools)], _sz),
+    "tao_train_backward": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens),
+                            ctypes.POINTER(Fusion), ctypes.POINTER(PrefillPools),
+                            ctypes.POINTER(TrainBwd), _vp], _i32),
     "tao_stream_open": ([ctypes.POINTER(StateDev), ctypes.POINTER(StreamCfg), _i64, _i32, _i32,
                          _vp, _vp, ctypes.POINTER(_vp)], _i32),
     "tao_stream_sync": ([_vp, ctypes.POINTER(StateDev), _i64, _i32, _i32], _i32),

@@ -14,8 +14,9 @@ writer for every visible block, page and epoch summaries, a route for every
 history query (bitmask selections), then the per-query selected read with
 the coarse read and the fusion in its epilogue.
 
-Gradients: the backward kernels (selected-read, writer, local-attention and
-fusion adjoints) are not built; a backward through this op raises.
+Gradients (``backward``): the HIP adjoints of every step, at the forward's
+values and selections; in grad mode the forward runs on a call-private
+workspace and saves what the backward reads.
 """
 
 import collections
@@ -145,18 +146,106 @@ def forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_rou
     return out
 
 
+def _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config):
+    """The forward on a call-private workspace, with the saves the backward
+    reads: local-attention log2-sum-exp, pre-fusion coarse / fine heads and
+    denominators. Returns (out, context for backward)."""
+    _check(q, k, v, raw_q, raw_k, config)
+    b, tokens, heads, d = q.shape
+    ws = _Workspace(config, b, tokens, heads, d, q.device)
+    q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
+    saves = dict(
+        lse=torch.empty((b, tokens, heads), dtype=torch.float32, device=q.device),
+        coarse=torch.zeros(q.shape, dtype=torch.bfloat16, device=q.device),
+        fine=torch.zeros(q.shape, dtype=torch.bfloat16, device=q.device),
+        den=torch.zeros((b, tokens, heads), dtype=torch.float32, device=q.device))
+    ws.pools.local_lse = saves["lse"].data_ptr()
+    ws.pools.coarse_out = saves["coarse"].data_ptr()
+    ws.pools.fine_out = saves["fine"].data_ptr()
+    ws.pools.den_out = saves["den"].data_ptr()
+    tok = _hip.tokens(q, k, v, raw_q, raw_k)
+    fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
+    _hip.check(_hip.lib().tao_prefill(
+        ctypes.byref(ws.dev.struct), ctypes.byref(tok), ctypes.byref(fu), ws.plan_arr,
+        len(ws.plan), ctypes.byref(ws.pools), ws.local.data_ptr(), out.data_ptr(), out_s,
+        ws.dev.stream()))
+    return out, dict(ws=ws, saves=saves, operands=(q, k, v, raw_q, raw_k))
+
+
+def backward(ctx_data, grad, fusion_a, fusion_b, alpha, memory_adjoints=None):
+    """Gradients (dq, dk, dv, draw_q, draw_k, dfusion_a, dfusion_b) of the
+    full-sequence read at the forward recorded in ctx_data. With a dict
+    `memory_adjoints`, it also receives "dz" (d fine_z, fp32 [B, H, S, D]) and
+    "dc" (d C, fp32 [B, H, S, D, D]) of the S written fines."""
+    ws = ctx_data["ws"]
+    saves = ctx_data["saves"]
+    q, k, v, raw_q, raw_k = ctx_data["operands"]
+    grad = grad.to(torch.bfloat16)
+    if not _hip.vector_ready(grad):
+        grad = grad.contiguous()
+    b, tokens, heads, d = q.shape
+    dev = q.device
+    outs = [torch.empty((b, tokens, heads, d), dtype=torch.bfloat16, device=dev)
+            for _ in range(5)]
+    dfa = torch.zeros((heads, d, 3), dtype=torch.float32, device=dev)
+    dfb = torch.zeros((heads, d, 3), dtype=torch.float32, device=dev)
+    lib = _hip.lib()
+    nbytes = lib.tao_train_bwd_workspace_bytes(ctypes.byref(ws.dev.struct), tokens,
+                                               ws.info["fines"], ctypes.byref(ws.pools))
+    scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    args = _hip.TrainBwd()
+    args.grad = grad.data_ptr()
+    args.grad_s = _hip.i64x3(_hip.strides_bth(grad))
+    args.local = ws.local.data_ptr()
+    args.local_lse = saves["lse"].data_ptr()
+    args.coarse_out = saves["coarse"].data_ptr()
+    args.fine_out = saves["fine"].data_ptr()
+    args.den_out = saves["den"].data_ptr()
+    args.dq, args.dk, args.dv, args.draw_q, args.draw_k = (t.data_ptr() for t in outs)
+    args.dfusion_a, args.dfusion_b = dfa.data_ptr(), dfb.data_ptr()
+    args.workspace, args.workspace_bytes = scratch.data_ptr(), nbytes
+    fines = ws.info["fines"]
+    if memory_adjoints is not None and fines:
+        memory_adjoints["dz"] = torch.empty((b, heads, fines, d), dtype=torch.float32, device=dev)
+        memory_adjoints["dc_t"] = torch.empty((b, heads, fines, d, d), dtype=torch.float32,
+                                              device=dev)
+        args.dz_out = memory_adjoints["dz"].data_ptr()
+        args.dc_out = memory_adjoints["dc_t"].data_ptr()
+    tok = _hip.tokens(q, k, v, raw_q, raw_k)
+    fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
+    _hip.check(lib.tao_train_backward(ctypes.byref(ws.dev.struct), ctypes.byref(tok),
+                                      ctypes.byref(fu), ctypes.byref(ws.pools),
+                                      ctypes.byref(args), ws.dev.stream()))
+    if memory_adjoints is not None and fines:
+        memory_adjoints["dc"] = memory_adjoints.pop("dc_t").transpose(-1, -2)
+    return (*outs, dfa, dfb)
+
+
 class _FullSequenceRead(torch.autograd.Function):
-    """Autograd node of the full-sequence read; its backward is not built."""
+    """Autograd node of the full-sequence read: HIP forward and backward."""
 
     @staticmethod
     def forward(ctx, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config):
-        return forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config)
+        out, data = _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b,
+                                          alpha, config)
+        ctx.data = data
+        ctx.alpha = alpha
+        ctx.save_for_backward(fusion_a, fusion_b)
+        return out
 
     @staticmethod
     def backward(ctx, grad):
-        raise NotImplementedError(
-            "tao_attention backward (selected-read, writer, local-attention and fusion "
-            "adjoints) is not implemented on the HIP path")
+        fusion_a, fusion_b = ctx.saved_tensors
+        dq, dk, dv, drq, drk, dfa, dfb = backward(ctx.data, grad, fusion_a, fusion_b,
+                                                  ctx.alpha)
+        ctx.data = None
+        need = ctx.needs_input_grad
+        return (dq if need[0] else None, dk if need[1] else None, dv if need[2] else None,
+                drq if need[3] else None, drk if need[4] else None,
+                dfa.to(fusion_a.dtype) if need[5] else None,
+                dfb.to(fusion_b.dtype) if need[6] else None, None, None)
 
 
 def full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,

@@ -489,3 +489,21 @@ def test_training_forward_is_the_stream_refreshing_at_every_query(index_only, to
         assert int(sel.min()) >= 0 and int(sel.max()) < visible
         srt = sel.sort(-1).values
         assert bool((srt[..., 1:] != srt[..., :-1]).all())
+
+
+@pytest.mark.parametrize("index_only,tokens", [(True, 1400), (False, 2700)])
+def test_training_smooth_forward_is_the_rounded_forward(index_only, tokens):
+    """The fp64 function the gradients are taken of equals the bf16 forward to
+    bf16 tolerance at the forward's own selections, and autograd through it
+    reaches every operand (tao_attention's differentiable inputs,
+    tests/gpu_sanity.py:28-34 of the reference)."""
+    xs, fa, fb = _stream_inputs(tokens, seed=11)
+    g = O.Geometry(coarse_index_only=index_only)
+    out, routes = O.training_forward(*xs, fa, fb, 0.5, g, return_routes=True)
+    leaves = [x.double().requires_grad_(True) for x in xs]
+    fa64, fb64 = fa.double().requires_grad_(True), fb.double().requires_grad_(True)
+    smooth = O.training_forward_smooth(*leaves, fa64, fb64, 0.5, routes, g)
+    torch.testing.assert_close(smooth.float(), out.float(), atol=3e-2, rtol=3e-2)
+    grads = torch.autograd.grad(smooth.square().sum(), leaves + [fa64, fb64])
+    for gr in grads:
+        assert torch.isfinite(gr).all() and gr.abs().sum() > 0

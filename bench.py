@@ -458,9 +458,10 @@ def run_prefill(torch, device, cfg, heads, width, tokens, probe):
 
 
 def run_full_sequence(torch, args, device):
-    """configs[1] shape, forward only: tao_attention over B2 x T8192 x H12 x D64
-    bf16 with TaoConfig() (coarse value branch on), every query routing
-    itself. Returns seconds per call (mean of timed calls, event-bracketed)."""
+    """configs[1] shape: tao_attention over B2 x T8192 x H12 x D64 bf16 with
+    TaoConfig() (coarse value branch on), every query routing itself. Returns
+    seconds per forward call and per forward + backward (gradients of all seven
+    differentiable operands), each the mean of event-bracketed timed calls."""
     from tao_attention import TaoConfig, tao_attention
     b, t, h, d = 2, args.full_sequence_tokens, 12, 64
     g = torch.Generator(device=device).manual_seed(11)
@@ -487,7 +488,27 @@ def run_full_sequence(torch, args, device):
         end.record()
         torch.cuda.synchronize()
     seconds = start.elapsed_time(end) / runs * 1e-3
-    return dict(seconds=seconds, batch=b, tokens=t, heads=h, width=d)
+    # forward + backward (gradients of q, k, v, raw_q, raw_k, fusion_a, fusion_b)
+    leaves = [x.detach().requires_grad_(True) for x in xs]
+    fa_l, fb_l = fa.detach().requires_grad_(True), fb.detach().requires_grad_(True)
+    grad = torch.randn(b, t, h, d, generator=g, device=device).to(torch.bfloat16)
+
+    def step():
+        out = tao_attention(*leaves[:3], raw_q=leaves[3], raw_k=leaves[4], fusion_a=fa_l,
+                            fusion_b=fb_l, alpha=0.5, config=cfg)
+        return torch.autograd.grad(out, leaves + [fa_l, fb_l], grad)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(runs):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    train_seconds = start.elapsed_time(end) / runs * 1e-3
+    return dict(seconds=seconds, train_seconds=train_seconds, batch=b, tokens=t, heads=h,
+                width=d)
 
 
 def cpu_model():
@@ -685,14 +706,17 @@ def main():
         log("full-sequence read (tao_attention forward, configs[1] shape)")
         fs = run_full_sequence(torch, args, device)
         result["full_sequence_forward"] = {
-            "workload": "configs[1] shape, forward only: tao_attention B%d x T%d x H%d x D%d bf16, "
+            "workload": "configs[1] shape: tao_attention B%d x T%d x H%d x D%d bf16, "
                         "TaoConfig() (coarse values on), every query routes itself; synthetic "
                         "N(0,1) operands" % (fs["batch"], fs["tokens"], fs["heads"], fs["width"]),
             "ms": round(fs["seconds"] * 1e3, 4),
             "tokens_per_s": round(fs["batch"] * fs["tokens"] / fs["seconds"], 1),
-            "note": "backward not implemented on the HIP path"}
+            "forward_backward_ms": round(fs["train_seconds"] * 1e3, 4),
+            "forward_backward_tokens_per_s": round(fs["batch"] * fs["tokens"] /
+                                                   fs["train_seconds"], 1)}
         log(f"full-sequence forward: {fs['seconds'] * 1e3:.3f} ms, "
-            f"{fs['batch'] * fs['tokens'] / fs['seconds']:.1f} tok/s")
+            f"{fs['batch'] * fs['tokens'] / fs['seconds']:.1f} tok/s; forward + backward "
+            f"{fs['train_seconds'] * 1e3:.3f} ms")
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, torch eager on host cores)")
         xs_cpu, _, _ = make_tokens(torch, 1 + 3 * args.cpu_steps, heads, width, 7, device)

@@ -856,9 +856,9 @@ TrainBwdLayout train_bwd_layout(const tao_state_dev* st, int64_t tokens, int fin
   l.drq = take(rows * D * 4);
   l.dh = take(rows * D * 4);
   l.dvf = take(rows * D * 4);
+  l.zero_begin = off;
   l.dgc = take(cc * BH * D * D * 4);
   l.dc = take(BH * (size_t)fines * D * D * 4);
-  l.zero_begin = off;
   l.dpw = take((size_t)l.n_tiles * BH * pcap * D * 4);
   l.dsw_tile = take((size_t)l.n_tiles * BH * (size_t)fines * D * 4);
   l.dsw = take(BH * (size_t)fines * D * 4);

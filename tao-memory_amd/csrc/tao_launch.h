@@ -291,7 +291,7 @@ hipError_t launch_attn_bwd(const AttnBwdParams& p, int head_dim, hipStream_t s);
 // Memory-branch adjoints: selected read, coarse read, page / segment
 // softmaxes and logsumexps, the softmax writer, and the final d raw_q /
 // d raw_k / dv. fp32 accumulators are zeroed by the caller: dsw_tile, dpw,
-// dsw, dpz, dz (dh, dc, dgc are written in full).
+// dsw, dpz, dz, dc, dgc (dh is written in full).
 struct MemBwdParams {
   const bf16_t* bank; const bf16_t* fine_sw; const bf16_t* page_z; const bf16_t* page_c;
   const bf16_t* pw_pool; const bf16_t* psw_pool; int pool_pcap;

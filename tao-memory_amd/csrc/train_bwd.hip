@@ -8,6 +8,8 @@
 // Gradients are those of the forward's function at the forward's values and
 // selections (the selection has no derivative, tao_stream.py:647-650);
 // accumulation is fp32 throughout, MFMA operands are bf16.
+#include <algorithm>
+
 #include "tao_launch.h"
 #include "tao_common.h"
 #include "tao_fusion.h"
@@ -158,8 +160,12 @@ constexpr int kBwdThreads = 64 * kBwdWaves;
 constexpr int kBwdKeys = 64;          // keys per staged block (dQ pass)
 constexpr int kBwdQ = 64;             // queries per staged block (dK/dV pass)
 
-TAO_DEV long long window_start(long long q, int ft, int keep) {
-  const long long s = (q / ft) * ft - keep;
+// Window geometry of the HIP path (fine_tokens 256, local_keep 512; the
+// launcher rejects others).
+constexpr int kFt = 256, kKeep = 512;
+
+TAO_DEV long long window_start(long long q, int, int) {
+  const long long s = ((q >> 8) << 8) - kKeep;
   return s > 0 ? s : 0;
 }
 
@@ -315,7 +321,7 @@ __global__ __launch_bounds__(kBwdThreads) void attn_bwd_dkv_kernel(AttnBwdParams
   const int count = (int)min((long long)kBwdWaves * 32, (long long)p.T - first);
   const int nk = min(max(count - wave * 32, 0), 32);
   const long long ktok = first + (nk > 0 ? wave * 32 + min(li, nk - 1) : 0);
-  const long long qend = min((long long)p.T, (first / p.ft + 1) * p.ft + p.keep);
+  const long long qend = min((long long)p.T, ((first >> 8) + 1) * kFt + kKeep);
   bf16x8 kreg[KK], vreg[KK];
   {
     const bf16_t* krow = p.k.p + b * p.k.sb + ktok * p.k.st + h * p.k.sh;
@@ -455,9 +461,7 @@ TAO_DEV int tile_visible(int t, int lag) { return t > lag ? t - lag : 0; }
 
 template <int D>
 struct ReadBwdSmem {
-  bf16_t ct[D][D];                     // C^T of the current fine (or G^T)
-  bf16_t dn[kRbWaves][32][D];          // dnum rows of each wave's queries (bf16)
-  bf16_t hq[kRbWaves][32][D];          // h rows
+  bf16_t c[D][D + 8];                  // C (or G) of the current fine: [d][e], padded
   float dsw[D];                        // d sw of the current fine (sum over waves)
   float dpw[64][D];                    // d pw of the tile's pages (P <= 64)
   uint32_t bits[512];
@@ -466,9 +470,31 @@ struct ReadBwdSmem {
   int n_union;
 };
 
+// Stage X^T (global rows [e][d], d contiguous) as X[d][e] into sm.c.
+template <int D>
+TAO_DEV void stage_transposed(bf16_t (*c)[D + 8], const bf16_t* src, int tid, int nthreads) {
+  constexpr int CH = D / 8;
+  for (int job = tid; job < (D / 2) * CH; job += nthreads) {
+    const int e0 = 2 * (job % (D / 2)), ch = job / (D / 2);
+    const uint4 ua = *(const uint4*)(src + (size_t)e0 * D + ch * 8);
+    const uint4 ub = *(const uint4*)(src + (size_t)(e0 + 1) * D + ch * 8);
+    const uint32_t wa[4] = {ua.x, ua.y, ua.z, ua.w}, wb[4] = {ub.x, ub.y, ub.z, ub.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *(uint32_t*)&c[ch * 8 + 2 * i][e0] = (wa[i] & 0xFFFFu) | (wb[i] << 16);
+      *(uint32_t*)&c[ch * 8 + 2 * i + 1][e0] = (wa[i] >> 16) | (wb[i] & 0xFFFF0000u);
+    }
+  }
+}
+
+// One 256-thread workgroup per (128 queries, batch, head); wave w owns 32
+// queries. Per union fine: dA^T... computed as D[q][d] = sum_e dnum[q][e] C[d][e]
+// with v_mfma_f32_32x32x16_bf16 (A = the wave's dnum rows in registers, B =
+// C rows staged in LDS); the accumulator layout (lane = channel d, 16 query
+// rows) carries dden, the selection mask, h, and the dh accumulators.
 template <int D>
 __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p) {
-  constexpr int PER = D / 64;
+  constexpr int KK = D / 16, DT = D / 32;
   __shared__ ReadBwdSmem<D> sm;
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
@@ -478,21 +504,17 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
   const int V = tile_visible(tile, p.keep / p.ft);
   if (V == 0) return;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
   const int G = p.group, K = V / G, P = K + (V % G > 0), erel = V - 1;
   const int nq = min(kRbQ, p.T - q0);
+  const int nqw = min(32, max(0, nq - 32 * w));
   const int words = (V + 31) >> 5;
   const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
   const bf16_t* psw = p.psw_pool + ((size_t)erel * BH + bh) * 8 * D;
   const bf16_t* gsw = p.fine_sw + (size_t)bh * p.fine_cap * D;
-  // ---- stage dnum and h rows; union of the block's selections
+  // ---- union of the block's selections
   for (int i = tid; i < 512; i += kRbWaves * 64) sm.bits[i] = 0u;
   for (int i = tid; i < 64 * D; i += kRbWaves * 64) (&sm.dpw[0][0])[i] = 0.0f;
-  for (int i = tid; i < kRbQ * D; i += kRbWaves * 64) {
-    const int qi = i / D, d = i % D;
-    const size_t row = ((size_t)b * p.T + q0 + min(qi, nq - 1)) * p.H + h;
-    sm.dn[qi / 32][qi % 32][d] = qi < nq ? f2bf(p.dnum[row * D + d]) : (bf16_t)0;
-    sm.hq[qi / 32][qi % 32][d] = qi < nq ? p.h[row * D + d] : (bf16_t)0;
-  }
   __syncthreads();
   for (int i = tid; i < nq * words; i += kRbWaves * 64) {
     const int qi = i / words, wd = i % words;
@@ -516,101 +538,118 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
   }
   __syncthreads();
   const int U = sm.n_union;
-  float dh[32][PER];
+  // ---- the wave's rows: dnum as the MFMA A operand (row li), dden / h in the
+  // accumulator layout (rows q_i = 8 (i / 4) + 4 hl + i % 4, column d = 32 t + li)
+  const int qa = q0 + 32 * w + (nqw > 0 ? min(li, nqw - 1) : 0);
+  const size_t rowa = ((size_t)b * p.T + qa) * p.H + h;
+  bf16x8 dn[KK];
 #pragma unroll
-  for (int qi = 0; qi < 32; ++qi)
+  for (int kk = 0; kk < KK; ++kk) {
+    const float* src = p.dnum + rowa * D + 16 * kk + 8 * hl;
+    uint32_t pk[4];
 #pragma unroll
-    for (int k = 0; k < PER; ++k) dh[qi][k] = 0.0f;
-  const int nqw = min(32, max(0, nq - 32 * w));
-  const uint32_t* qs = p.qsel + ((size_t)(b * p.T + q0 + 32 * w) * p.H + h) * p.qsel_words;
+    for (int j = 0; j < 4; ++j) pk[j] = pack_bf16x2(src[2 * j], src[2 * j + 1]);
+    dn[kk] = as_bf16x8(make_uint4(pk[0], pk[1], pk[2], pk[3]));
+  }
+  float dd[16], hd[DT][16], dh[DT][16];
+  const uint32_t* qs = p.qsel + ((size_t)(b * p.T + qa) * p.H + h) * p.qsel_words;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int qi = 8 * (i / 4) + 4 * hl + (i % 4);
+    const bool ok = qi < nqw;
+    const size_t row = ((size_t)b * p.T + q0 + 32 * w + (ok ? qi : 0)) * p.H + h;
+    dd[i] = ok ? p.dden[row] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      hd[t][i] = ok ? bf2f(p.h[row * D + 32 * t + li]) : 0.0f;
+      dh[t][i] = 0.0f;
+    }
+  }
   for (int u = 0; u < U; ++u) {
     const int f = sm.uni[u];
     const int g = f / G;
     __syncthreads();                                   // previous fine consumed
-    const bf16_t* src = p.bank + ((size_t)bh * p.fine_cap + f) * D * D;
-    for (int i = tid; i < D * D / 8; i += kRbWaves * 64)
-      *(uint4*)(&sm.ct[0][0] + i * 8) = *(const uint4*)(src + i * 8);
+    stage_transposed<D>(sm.c, p.bank + ((size_t)bh * p.fine_cap + f) * D * D, tid,
+                        kRbWaves * 64);
     for (int i = tid; i < D; i += kRbWaves * 64) sm.dsw[i] = 0.0f;
     __syncthreads();
-    float swv[PER], pwv[PER], dpw_acc[PER], dsw_acc[PER];
+    // selection mask of the wave's 32 queries (bit q)
+    const bool mine = li < nqw && ((qs[(f >> 5)] >> (f & 31)) & 1u);
+    const uint32_t m32 = (uint32_t)(__ballot(mine) & 0xFFFFFFFFull);
+    // Every wave reaches the barriers below, selecting or not.
+    if (m32 != 0) {
+      float swv[DT], pwv[DT];
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int d = lane + 64 * k;
-      swv[k] = bf2f(f < K * G ? gsw[(size_t)f * D + d] : psw[(size_t)(f - K * G) * D + d]);
-      pwv[k] = bf2f(pw[(size_t)g * D + d]);
-      dpw_acc[k] = 0.0f;
-      dsw_acc[k] = 0.0f;
-    }
-#pragma unroll 1
-    for (int qi = 0; qi < nqw; ++qi) {
-      if (!((qs[(size_t)qi * p.H * p.qsel_words + (f >> 5)] >> (f & 31)) & 1u)) continue;
-      const size_t row = ((size_t)b * p.T + q0 + 32 * w + qi) * p.H + h;
-      const float dd = p.dden[row];
-      float da[PER];
-#pragma unroll
-      for (int k = 0; k < PER; ++k) da[k] = dd;
-      for (int e = 0; e < D; ++e) {
-        const float dn = bf2f(sm.dn[w][qi][e]);
-#pragma unroll
-        for (int k = 0; k < PER; ++k) da[k] = fmaf(dn, bf2f(sm.ct[e][lane + 64 * k]), da[k]);
+      for (int t = 0; t < DT; ++t) {
+        const int d = 32 * t + li;
+        swv[t] = bf2f(f < K * G ? gsw[(size_t)f * D + d] : psw[(size_t)(f - K * G) * D + d]);
+        pwv[t] = bf2f(pw[(size_t)g * D + d]);
       }
 #pragma unroll
-      for (int k = 0; k < PER; ++k) {
-        const float hv = bf2f(sm.hq[w][qi][lane + 64 * k]);
-        const float dhv = da[k] * swv[k];
-        dpw_acc[k] = fmaf(dhv, hv, dpw_acc[k]);
-        dsw_acc[k] = fmaf(da[k] * hv, pwv[k], dsw_acc[k]);
-        // dh of query qi (registers are indexed by the unrolled slot)
+      for (int t = 0; t < DT; ++t) {
+        floatx16 da;
 #pragma unroll
-        for (int s2 = 0; s2 < 32; ++s2)
-          if (s2 == qi) dh[s2][k] = fmaf(dhv, pwv[k], dh[s2][k]);
+        for (int i = 0; i < 16; ++i) da[i] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+          da = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              dn[kk], as_bf16x8(*(const uint4*)&sm.c[32 * t + li][16 * kk + 8 * hl]), da, 0, 0, 0);
+        float spw = 0.0f, ssw = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int qi = 8 * (i / 4) + 4 * hl + (i % 4);
+          const float a = ((m32 >> qi) & 1u) ? da[i] + dd[i] : 0.0f;
+          const float dhv = a * swv[t];
+          dh[t][i] = fmaf(dhv, pwv[t], dh[t][i]);
+          spw = fmaf(dhv, hd[t][i], spw);
+          ssw = fmaf(a * hd[t][i], pwv[t], ssw);
+        }
+        spw += __shfl_xor(spw, 32, 64);
+        ssw += __shfl_xor(ssw, 32, 64);
+        if (hl == 0) {
+          atomicAdd(&sm.dsw[32 * t + li], ssw);
+          atomicAdd(&sm.dpw[g][32 * t + li], spw);
+        }
       }
-    }
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      atomicAdd(&sm.dsw[lane + 64 * k], dsw_acc[k]);
-      atomicAdd(&sm.dpw[g][lane + 64 * k], dpw_acc[k]);
     }
     __syncthreads();
     for (int i = tid; i < D; i += kRbWaves * 64)
       atomicAdd(p.dsw_tile + (((size_t)tile * BH + bh) * p.v_max + f) * D + i, sm.dsw[i]);
   }
-  // ---- coarse read: dh += dcoarse G_K^T (coarse_pool holds G^T[e][d])
-  const bool coarse = p.coarse_values && K >= 1;
-  if (coarse) {
+  // ---- coarse read: dh[q][d] += sum_e dcoarse[q][e] G[d][e] (coarse_pool holds G^T)
+  if (p.coarse_values && K >= 1) {
     __syncthreads();
-    const bf16_t* gsrc = p.coarse_pool + ((size_t)(K - p.coarse_first) * BH + bh) * D * D;
-    for (int i = tid; i < D * D / 8; i += kRbWaves * 64)
-      *(uint4*)(&sm.ct[0][0] + i * 8) = *(const uint4*)(gsrc + i * 8);
-    for (int i = tid; i < kRbQ * D; i += kRbWaves * 64) {
-      const int qi = i / D, d = i % D;
-      const size_t row = ((size_t)b * p.T + q0 + min(qi, nq - 1)) * p.H + h;
-      sm.dn[qi / 32][qi % 32][d] = qi < nq ? f2bf(p.dcoarse[row * D + d]) : (bf16_t)0;
+    stage_transposed<D>(sm.c, p.coarse_pool + ((size_t)(K - p.coarse_first) * BH + bh) * D * D,
+                        tid, kRbWaves * 64);
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const float* src = p.dcoarse + rowa * D + 16 * kk + 8 * hl;
+      uint32_t pk[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pk[j] = pack_bf16x2(src[2 * j], src[2 * j + 1]);
+      dn[kk] = as_bf16x8(make_uint4(pk[0], pk[1], pk[2], pk[3]));
     }
-    __syncthreads();
-#pragma unroll 1
-    for (int qi = 0; qi < nqw; ++qi) {
-      float acc[PER];
 #pragma unroll
-      for (int k = 0; k < PER; ++k) acc[k] = 0.0f;
-      for (int e = 0; e < D; ++e) {
-        const float dc = bf2f(sm.dn[w][qi][e]);
+    for (int t = 0; t < DT; ++t) {
+      floatx16 acc;
 #pragma unroll
-        for (int k = 0; k < PER; ++k) acc[k] = fmaf(dc, bf2f(sm.ct[e][lane + 64 * k]), acc[k]);
-      }
+      for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 #pragma unroll
-      for (int s2 = 0; s2 < 32; ++s2)
-        if (s2 == qi)
+      for (int kk = 0; kk < KK; ++kk)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            dn[kk], as_bf16x8(*(const uint4*)&sm.c[32 * t + li][16 * kk + 8 * hl]), acc, 0, 0, 0);
 #pragma unroll
-          for (int k = 0; k < PER; ++k) dh[s2][k] += acc[k];
+      for (int i = 0; i < 16; ++i) dh[t][i] += acc[i];
     }
   }
 #pragma unroll
-  for (int qi = 0; qi < 32; ++qi) {
+  for (int i = 0; i < 16; ++i) {
+    const int qi = 8 * (i / 4) + 4 * hl + (i % 4);
     if (qi < nqw) {
       const size_t row = ((size_t)b * p.T + q0 + 32 * w + qi) * p.H + h;
 #pragma unroll
-      for (int k = 0; k < PER; ++k) p.dh[row * D + lane + 64 * k] = dh[qi][k];
+      for (int t = 0; t < DT; ++t) p.dh[row * D + 32 * t + li] = dh[t][i];
     }
   }
   __syncthreads();
@@ -619,97 +658,141 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
               sm.dpw[i / D][i % D]);
 }
 
-// Outer products over a query set: out[e][d] = sum_q x[q][e] y[q][d].
+// Outer products over a query set: out^T[e][d] = sum_q x[q][e] y[q][d].
 // mode 0 (dC of fine f = blockIdx / BH): queries of every tile that sees f,
-//   x = dnum, y = a (masked by the query's selection of f); plus the coarse
-//   path's share w_f[d] sum_{K > g} cw_K[g][d] dG_K[d][e] for completed f.
+//   x = dnum, y = a = h pw sw (zero unless the query selected f); plus the
+//   coarse path's share w_f[d] sum_{K > g} cw_K[g][d] dG_K[d][e] for
+//   completed f.
 // mode 1 (dG of completed count K = coarse_first + blockIdx / BH): queries of
 //   the tiles with K completed pages, x = dcoarse, y = h.
-// Thread (d = tid % D, row group) owns rows e of one column d.
-constexpr int kObQ = 16;
+// Chunks of 32 queries are staged transposed (x^T [e][q], y^T [d][q]) and
+// reduced with v_mfma_f32_32x32x16_bf16 (m = e, n = d, k = q); wave w owns
+// output tiles w, w + 4, ... of the (D / 32)^2 tiles. A workgroup takes
+// kObTiles of an item's tiles (grid = items x tile groups x B*H) and adds its
+// sums into the zeroed output with fp32 atomics; the first group adds the
+// coarse share.
+constexpr int kObQ = 32;
+constexpr int kObTiles = 4;
 
 template <int D>
 __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int mode) {
-  constexpr int GROUPS = kThreads / D, ROWS = D / GROUPS;
-  __shared__ float xs[kObQ][D], ys[kObQ][D];
+  constexpr int DT = D / 32, NT = DT * DT, TPW = (NT + 3) / 4;
+  __shared__ bf16_t xt[D][kObQ + 8], yt[D][kObQ + 8];
+  __shared__ int any_sel;
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   const int b = bh / p.H, h = bh % p.H;
-  const int item = blockIdx.x / BH;
-  const int tid = threadIdx.x, d = tid % D, rg = tid / D;
   const int G = p.group, lag = p.keep / p.ft;
   const int n_tiles = (p.T + p.ft - 1) / p.ft;
-  float acc[ROWS];
+  const int groups = mode == 0 ? (max(n_tiles - lag - 1, 1) + kObTiles - 1) / kObTiles
+                               : (G + kObTiles - 1) / kObTiles;
+  const int item = blockIdx.x / BH / groups, tg = (blockIdx.x / BH) % groups;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
+  floatx16 acc[TPW];
 #pragma unroll
-  for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
-  int t_lo, t_hi;
+  for (int j = 0; j < TPW; ++j)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[j][i] = 0.0f;
   const int f = item, Kc = p.coarse_first + item;
-  if (mode == 0) {
-    t_lo = f + lag + 1;            // first tile that sees fine f
-    t_hi = n_tiles;
-  } else {
-    t_lo = lag + G * Kc;
-    t_hi = min(n_tiles, lag + G * Kc + G);
-  }
+  const int t_first = mode == 0 ? f + lag + 1 : lag + G * Kc;
+  const int t_last = mode == 0 ? n_tiles : min(n_tiles, lag + G * Kc + G);
+  const int t_lo = t_first + tg * kObTiles;
+  const int t_hi = min(t_last, t_lo + kObTiles);
+  if (t_lo >= t_hi) return;                          // workgroup-uniform
   const bf16_t* gsw = p.fine_sw + (size_t)bh * p.fine_cap * D;
   for (int t = t_lo; t < t_hi; ++t) {
     const int V = tile_visible(t, lag), erel = V - 1, K = V / G;
-    float yscale = 1.0f;
-    if (mode == 0) {
-      const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
-      const bf16_t* psw = p.psw_pool + ((size_t)erel * BH + bh) * 8 * D;
-      yscale = bf2f(pw[(size_t)(f / G) * D + d]) *
-               bf2f(f < K * G ? gsw[(size_t)f * D + d] : psw[(size_t)(f - K * G) * D + d]);
-    }
+    const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
+    const bf16_t* psw = p.psw_pool + ((size_t)erel * BH + bh) * 8 * D;
     const int qa = t * p.ft, qb_end = min(p.T, qa + p.ft);
     for (int qb = qa; qb < qb_end; qb += kObQ) {
       __syncthreads();
-      for (int i = tid; i < kObQ * D; i += kThreads) {
-        const int qi = i / D, c = i % D;
+      if (tid == 0) any_sel = 0;
+      __syncthreads();
+      // thread = (query qi, 8-channel chunk c): x and y rows, written transposed
+      for (int job = tid; job < kObQ * (D / 8); job += kThreads) {
+        const int qi = job % kObQ, c = job / kObQ;
         const int q = qb + qi;
-        float xv = 0.0f, yv = 0.0f;
+        float xv[8], yv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { xv[j] = 0.0f; yv[j] = 0.0f; }
         if (q < qb_end) {
           const size_t row = ((size_t)b * p.T + q) * p.H + h;
           bool sel = true;
-          if (mode == 0)
-            sel = (p.qsel[row * p.qsel_words + (f >> 5)] >> (f & 31)) & 1u;
+          if (mode == 0) sel = (p.qsel[row * p.qsel_words + (f >> 5)] >> (f & 31)) & 1u;
           if (sel) {
-            xv = mode == 0 ? p.dnum[row * D + c] : p.dcoarse[row * D + c];
-            yv = bf2f(p.h[row * D + c]);
+            if (c == 0) any_sel = 1;
+            const float* xs = (mode == 0 ? p.dnum : p.dcoarse) + row * D + 8 * c;
+            const bf16_t* hs = p.h + row * D + 8 * c;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              xv[j] = xs[j];
+              float y = bf2f(hs[j]);
+              if (mode == 0) {
+                const int d = 8 * c + j;
+                y *= bf2f(pw[(size_t)(f / G) * D + d]) *
+                     bf2f(f < K * G ? gsw[(size_t)f * D + d] : psw[(size_t)(f - K * G) * D + d]);
+              }
+              yv[j] = y;
+            }
           }
         }
-        xs[qi][c] = xv;
-        ys[qi][c] = yv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          xt[8 * c + j][qi] = f2bf(xv[j]);
+          yt[8 * c + j][qi] = f2bf(yv[j]);
+        }
       }
       __syncthreads();
-#pragma unroll 4
-      for (int qi = 0; qi < kObQ; ++qi) {
-        const float y = ys[qi][d] * yscale;
+      if (!any_sel) continue;                          // workgroup-uniform
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) acc[r] = fmaf(xs[qi][rg * ROWS + r], y, acc[r]);
+      for (int j = 0; j < TPW; ++j) {
+        const int tt = w + 4 * j;
+        if (tt < NT) {
+          const int mt = tt / DT, nt = tt % DT;
+#pragma unroll
+          for (int ks = 0; ks < kObQ / 16; ++ks)
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                as_bf16x8(*(const uint4*)&xt[32 * mt + li][16 * ks + 8 * hl]),
+                as_bf16x8(*(const uint4*)&yt[32 * nt + li][16 * ks + 8 * hl]), acc[j], 0, 0, 0);
+        }
       }
-    }
-  }
-  if (mode == 0 && p.coarse_values && f < G * (p.v_max / G)) {
-    // coarse share: w_f[d] sum_{K > g} cw_K[g][d] dG_K[d][e]
-    const int g = f / G;
-    const bf16_t* pz = p.page_z + (size_t)bh * p.page_cap * D;
-    const float wf = bf2f(gsw[(size_t)f * D + d]);
-    for (int k2 = max(g + 1, p.coarse_first); k2 < p.coarse_first + p.coarse_count; ++k2) {
-      float m = -__builtin_inff();
-      for (int j = 0; j < k2; ++j) m = fmaxf(m, bf2f(pz[(size_t)j * D + d]));
-      float z = 0.0f;
-      for (int j = 0; j < k2; ++j) z += __expf(bf2f(pz[(size_t)j * D + d]) - m);
-      const float cw = __expf(bf2f(pz[(size_t)g * D + d]) - m) / z;
-      const float* dg = p.dgc + ((size_t)(k2 - p.coarse_first) * BH + bh) * D * D;
-#pragma unroll
-      for (int r = 0; r < ROWS; ++r) acc[r] = fmaf(wf * cw, dg[(size_t)(rg * ROWS + r) * D + d], acc[r]);
     }
   }
   float* out = mode == 0 ? p.dc + ((size_t)bh * p.v_max + f) * D * D
                          : p.dgc + ((size_t)item * BH + bh) * D * D;
+  const bool coarse_share = mode == 0 && tg == 0 && p.coarse_values && f < G * (p.v_max / G);
+  const int g = f / G;
+  const bf16_t* pz = p.page_z + (size_t)bh * p.page_cap * D;
 #pragma unroll
-  for (int r = 0; r < ROWS; ++r) out[(size_t)(rg * ROWS + r) * D + d] = acc[r];
+  for (int j = 0; j < TPW; ++j) {
+    const int tt = w + 4 * j;
+    if (tt >= NT) continue;
+    const int mt = tt / DT, nt = tt % DT;
+    const int d = 32 * nt + li;
+    if (coarse_share) {
+      const float wf = bf2f(gsw[(size_t)f * D + d]);
+      for (int k2 = max(g + 1, p.coarse_first); k2 < p.coarse_first + p.coarse_count; ++k2) {
+        float m = -__builtin_inff();
+        for (int jj = 0; jj < k2; ++jj) m = fmaxf(m, bf2f(pz[(size_t)jj * D + d]));
+        float z = 0.0f;
+        for (int jj = 0; jj < k2; ++jj) z += __expf(bf2f(pz[(size_t)jj * D + d]) - m);
+        const float scale = wf * __expf(bf2f(pz[(size_t)g * D + d]) - m) / z;
+        const float* dg = p.dgc + ((size_t)(k2 - p.coarse_first) * BH + bh) * D * D;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int e = 32 * mt + 8 * (i / 4) + 4 * hl + (i % 4);
+          acc[j][i] = fmaf(scale, dg[(size_t)e * D + d], acc[j][i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e = 32 * mt + 8 * (i / 4) + 4 * hl + (i % 4);
+      atomicAdd(out + (size_t)e * D + d, acc[j][i]);
+    }
+  }
 }
 
 // Page-level adjoints of one tile (softmax over its P pages, the pending
@@ -961,6 +1044,7 @@ hipError_t launch_fuse_bwd(const TrainBwdParams& p, int head_dim, hipStream_t s)
 
 hipError_t launch_attn_bwd(const AttnBwdParams& p, int head_dim, hipStream_t s) {
   if (p.T <= 0) return hipSuccess;
+  if (p.ft != kFt || p.keep != kKeep) return hipErrorInvalidValue;
   const int blocks = (p.T + kBwdWaves * 32 - 1) / (kBwdWaves * 32);
   const dim3 grid((unsigned)(blocks * p.B * p.H));
   if (head_dim == 128) {
@@ -980,6 +1064,9 @@ hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s) {
   const int n_tiles = (p.T + p.ft - 1) / p.ft;
   // read_bwd keeps the tile's page adjoints in LDS: at most 64 pages.
   if (p.group != 8 || p.ft != 256 || p.v_max / p.group + 1 > 64) return hipErrorInvalidValue;
+  const int lag = p.keep / p.ft;
+  const int dc_groups = (std::max(n_tiles - lag - 1, 1) + kObTiles - 1) / kObTiles;
+  const int dg_groups = (p.group + kObTiles - 1) / kObTiles;
 #define TAO_MEM_BWD(D_)                                                                      \
   do {                                                                                       \
     if (p.v_max > 0) {                                                                       \
@@ -987,12 +1074,13 @@ hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s) {
       hipLaunchKernelGGL(read_bwd_kernel<D_>, dim3((unsigned)(blocks * BH)),                 \
                          dim3(kRbWaves * 64), 0, s, p);                                      \
       if (p.coarse_values && p.coarse_count > 0) {                                           \
-        hipLaunchKernelGGL(outer_bwd_kernel<D_>, dim3((unsigned)(p.coarse_count * BH)),      \
-                           dim3(kThreads), 0, s, p, 1);                                      \
+        hipLaunchKernelGGL(outer_bwd_kernel<D_>,                                             \
+                           dim3((unsigned)(p.coarse_count * dg_groups * BH)), dim3(kThreads),\
+                           0, s, p, 1);                                                      \
         hipLaunchKernelGGL(coarse_page_bwd_kernel<D_>, dim3((unsigned)(p.coarse_count * BH)),\
                            dim3(D_), 0, s, p);                                               \
       }                                                                                      \
-      hipLaunchKernelGGL(outer_bwd_kernel<D_>, dim3((unsigned)(p.v_max * BH)),               \
+      hipLaunchKernelGGL(outer_bwd_kernel<D_>, dim3((unsigned)(p.v_max * dc_groups * BH)),   \
                          dim3(kThreads), 0, s, p, 0);                                        \
       hipLaunchKernelGGL(page_bwd_kernel<D_>, dim3((unsigned)(n_tiles * BH)), dim3(D_), 0,   \
                          s, p);                                                              \

@@ -75,7 +75,7 @@ float* parts_of(const tao_state_dev* st) {
 
 tao::DecodeParams decode_params(const tao_state_dev* st, const tao_tokens* tok,
                                 const tao_fusion* fu, void* out, const int64_t* out_s) {
-  tao::DecodeParams p;
+  tao::DecodeParams p{};
   p.q = view(tok->q, tok->q_s);
   p.k = view(tok->k, tok->k_s);
   p.v = view(tok->v, tok->v_s);
@@ -131,7 +131,7 @@ int check_fusion(const tao_fusion* fu) {
 struct DecodeGraph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
-  tao::StageParams stage;
+  tao::StageParams stage{};
   int batch = 0, heads = 0, head_dim = 0;
 };
 
@@ -201,7 +201,7 @@ int tao_fold_route(const tao_state_dev* st, int32_t selected, void* stream) {
   int rc = check_state(st);
   if (rc) return rc;
   if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected count exceeds sel_cap");
-  tao::FoldParams p;
+  tao::FoldParams p{};
   p.bank = (const bf16_t*)st->bank_c;
   p.sw = (const bf16_t*)st->fine_sw;
   p.pw = (const bf16_t*)st->page_w;
@@ -225,7 +225,7 @@ int tao_page_coarse(const tao_state_dev* st, int32_t first_page, int32_t count, 
   if (count < 0 || first_page < 0 || first_page + count > st->page_cap ||
       (int64_t)(first_page + count) * st->coarse_group > st->fine_cap)
     return fail(TAO_E_CAPACITY, "pages exceed the state capacity");
-  tao::PageCoarseParams p;
+  tao::PageCoarseParams p{};
   p.bank = (const bf16_t*)st->bank_c;
   p.sw = (const bf16_t*)st->fine_sw;
   p.page_c = (bf16_t*)st->page_c;
@@ -246,7 +246,7 @@ int tao_fold_coarse(const tao_state_dev* st, int32_t completed, void* stream) {
   if (!st->page_c) return fail(TAO_E_ARGUMENT, "state has no coarse value branch");
   if (completed < 1 || completed > st->page_cap)
     return fail(TAO_E_CAPACITY, "completed pages out of range");
-  tao::CoarseFoldParams p;
+  tao::CoarseFoldParams p{};
   p.page_z = (const bf16_t*)st->page_z;
   p.page_c = (const bf16_t*)st->page_c;
   p.out = st->coarse_g;
@@ -311,7 +311,7 @@ int tao_write_fine(const tao_state_dev* st, const tao_tokens* tok, int64_t new_b
   if (count < 0 || first_slot < 0 || first_slot + count > st->fine_cap)
     return fail(TAO_E_CAPACITY, "fine slots exceed fine_cap");
   if (count && !start_pos) return fail(TAO_E_ARGUMENT, "null block starts");
-  tao::WriterParams p;
+  tao::WriterParams p{};
   p.rk = view(tok->raw_k, tok->rk_s);
   p.v = view(tok->v, tok->v_s);
   p.ring_raw = (const bf16_t*)st->ring_raw;
@@ -336,7 +336,7 @@ int tao_seal_epilogue(const tao_state_dev* st, int32_t slot, int32_t pages, int3
   if (slot < 0 || slot >= st->fine_cap) return fail(TAO_E_CAPACITY, "slot exceeds fine_cap");
   if (pages != slot / st->coarse_group + 1 || pages > st->page_cap)
     return fail(TAO_E_ARGUMENT, "pages must be slot / coarse_group + 1 and fit page_cap");
-  tao::EpilogueParams p;
+  tao::EpilogueParams p{};
   p.fine_z = (const bf16_t*)st->fine_z;
   p.fine_sw = (bf16_t*)st->fine_sw;
   p.page_z = (bf16_t*)st->page_z;
@@ -361,7 +361,7 @@ int tao_local_attention(const tao_state_dev* st, const tao_tokens* tok, int64_t 
   if (rc) return rc;
   if (!local) return fail(TAO_E_ARGUMENT, "null local output");
   if (n_tiles < 0 || (n_tiles && !tiles)) return fail(TAO_E_ARGUMENT, "bad tile list");
-  tao::AttnParams p;
+  tao::AttnParams p{};
   p.q = view(tok->q, tok->q_s);
   p.k = view(tok->k, tok->k_s);
   p.v = view(tok->v, tok->v_s);
@@ -516,7 +516,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   }
   const int D = st->head_dim;
   // local attention
-  tao::AttnParams ap;
+  tao::AttnParams ap{};
   ap.q = view(tok->q, tok->q_s);
   ap.k = view(tok->k, tok->k_s);
   ap.v = view(tok->v, tok->v_s);
@@ -535,7 +535,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   e = tao::launch_local_attention(ap, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill attention");
   // writer
-  tao::WriterParams wp;
+  tao::WriterParams wp{};
   wp.rk = view(tok->raw_k, tok->rk_s);
   wp.v = view(tok->v, tok->v_s);
   wp.ring_raw = (const bf16_t*)st->ring_raw;
@@ -553,7 +553,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   e = tao::launch_writer(wp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill writer");
   // pages
-  tao::PagesParams pp;
+  tao::PagesParams pp{};
   pp.fine_z = (const bf16_t*)st->fine_z;
   pp.fine_sw = (bf16_t*)st->fine_sw;
   pp.page_z = (bf16_t*)st->page_z;
@@ -567,7 +567,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   e = tao::launch_pages(pp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill pages");
   if (coarse_values) {
-    tao::PageCoarseParams cp;
+    tao::PageCoarseParams cp{};
     cp.bank = (const bf16_t*)st->bank_c;
     cp.sw = (const bf16_t*)st->fine_sw;
     cp.page_c = (bf16_t*)st->page_c;
@@ -582,7 +582,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
     if (e != hipSuccess) return check_hip(e, "tao_prefill page values");
   }
   if (coarse_reads) {
-    tao::CoarseFoldParams cf;
+    tao::CoarseFoldParams cf{};
     cf.page_z = (const bf16_t*)st->page_z;
     cf.page_c = (const bf16_t*)st->page_c;
     cf.out = pools->coarse_pool;
@@ -596,7 +596,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
     if (e != hipSuccess) return check_hip(e, "tao_prefill coarse fold");
   }
   if (need_pools) {
-    tao::EpochParams ep;
+    tao::EpochParams ep{};
     ep.fine_z = (const bf16_t*)st->fine_z;
     ep.fine_sw = (bf16_t*)st->fine_sw;
     ep.page_z = (bf16_t*)st->page_z;
@@ -638,11 +638,12 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
     rp.sel_cap = st->sel_cap;
     rp.chosen_cap = st->chosen_cap;
     rp.group = G;
+    rp.max_epoch = (int)(first_epoch + n_epochs - 1);
     e = tao::launch_route(rp, D, s);
     if (e != hipSuccess) return check_hip(e, "tao_prefill routes");
   }
   if (query_routes && need_pools && n_read) {
-    tao::QueryRouteParams qp;
+    tao::QueryRouteParams qp{};
     qp.rq = (const bf16_t*)tok->raw_q;
     qp.rq_sb = tok->rq_s[0];
     qp.rq_st = tok->rq_s[1];
@@ -665,7 +666,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
     e = tao::launch_route_queries(qp, D, s);
     if (e != hipSuccess) return check_hip(e, "tao_prefill per-query routes");
   }
-  tao::ReadTilesParams rt;
+  tao::ReadTilesParams rt{};
   rt.rq = view(tok->raw_q, tok->rq_s);
   rt.bank = (const bf16_t*)st->bank_c;
   rt.sw = (const bf16_t*)st->fine_sw;
@@ -701,7 +702,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   rt.save_den = pools ? pools->den_out : nullptr;
   e = tao::launch_read_tiles(rt, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill read");
-  tao::AppendParams app;
+  tao::AppendParams app{};
   app.k = view(tok->k, tok->k_s);
   app.v = view(tok->v, tok->v_s);
   app.rk = view(tok->raw_k, tok->rk_s);
@@ -726,7 +727,7 @@ int tao_ring_append(const tao_state_dev* st, const tao_tokens* tok, int32_t firs
   const int L = st->local_keep + st->fine_tokens;
   if (first < 0 || count < 0 || first + count > tok->tokens || count > L)
     return fail(TAO_E_ARGUMENT, "ring append range out of bounds");
-  tao::AppendParams p;
+  tao::AppendParams p{};
   p.k = view(tok->k, tok->k_s);
   p.v = view(tok->v, tok->v_s);
   p.rk = view(tok->raw_k, tok->rk_s);
@@ -755,7 +756,7 @@ int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu, int32_t sele
   const int B = st->batch, H = st->heads, D = st->head_dim;
   const size_t row = (size_t)B * H * D;
   bf16_t* stg = (bf16_t*)staging;
-  tao_tokens tok;
+  tao_tokens tok{};
   const void* ptrs[5];
   for (int i = 0; i < 5; ++i) ptrs[i] = stg + i * row;
   tok.q = ptrs[0]; tok.k = ptrs[1]; tok.v = ptrs[2]; tok.raw_q = ptrs[3]; tok.raw_k = ptrs[4];

@@ -416,17 +416,20 @@ __global__ __launch_bounds__(kQThreads) void route_queries_kernel(QueryRoutePara
 // the high half, 0xFFFF - index in the low half (same order as score_key).
 constexpr int kTileQ = 32;
 
-template <int D>
+template <int D, int ROWS_ = (D == 64 ? 128 : 64)>
 struct RouteTileGeo {
   static constexpr int PAD = D + 8;                  // padded LDS row (bf16)
-  static constexpr int ROWS = D == 64 ? 128 : 64;    // staged pw + sw rows
+  static constexpr int ROWS = ROWS_;                 // staged pw + sw rows
   static constexpr int KEYS = ROWS;                  // >= pages, >= candidates
   static constexpr int WORDS = ROWS / 32;
 };
-
+// Staged rows of the turn-route kernel (prefill turns reach further epochs).
 template <int D>
+constexpr int kTurnRows = D == 64 ? 256 : 160;
+
+template <int D, int ROWS_ = (D == 64 ? 128 : 64)>
 struct RouteTileSmem {
-  using G = RouteTileGeo<D>;
+  using G = RouteTileGeo<D, ROWS_>;
   bf16_t h[kTileQ][G::PAD];
   bf16_t rows[G::ROWS][G::PAD];
   uint32_t keys[kTileQ][G::KEYS];
@@ -486,43 +489,15 @@ TAO_DEV float lane_mass(const bf16_t* hrow, const bf16_t* pwrow, const bf16_t* s
   return rbf(s1[0]);
 }
 
-template <int D>
-__global__ __launch_bounds__(kQThreads) void route_tile_kernel(QueryRouteParams p) {
-  using Geo = RouteTileGeo<D>;
-  __shared__ RouteTileSmem<D> sm;
-  constexpr int G = 8;                           // coarse_group (checked at launch)
-  const int BH = p.B * p.H;
-  const int bh = blockIdx.x % BH;
-  const int b = bh / p.H, h = bh % p.H;
-  const int64_t* desc = p.tiles + 8 * (blockIdx.x / BH);
-  if (!desc[6]) return;                          // no history: workgroup-uniform
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int q_first = (int)desc[0], nq = (int)desc[1];
-  const int coarse = (int)desc[2], M = (int)desc[3], erel = (int)desc[4];
-  const int epoch = p.first_epoch + erel;
-  const int K = epoch / G, pending = epoch % G;
-  const int E = G * coarse + pending;
-  const int P = K + (pending > 0);
-  const int words = (epoch + 31) >> 5;
-  const bf16_t* pw_g = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
-  const SwRows sw_g{p.sw + (size_t)bh * p.fine_cap * D,
-                    p.psw_pool + ((size_t)erel * BH + bh) * 8 * D, K * G};
-  // ---- stage: rows [0, P) page weights, [P, P + epoch) segment weights
-  for (int i = tid; i < (P + epoch) * (D / 8); i += kQThreads) {
-    const int r = i / (D / 8), c = i % (D / 8);
-    const bf16_t* src = r < P ? pw_g + (size_t)r * D : sw_g.row(r - P, D);
-    *(uint4*)&sm.rows[r][c * 8] = *(const uint4*)(src + c * 8);
-  }
-  for (int i = tid; i < kTileQ * Geo::WORDS; i += kQThreads) (&sm.bits[0][0])[i] = 0u;
-  // ---- h of each query: wave w does queries w, w + 4, ...
-  for (int qi = w; qi < nq; qi += 4) {
-    query_weights<D>(p.rq + b * p.rq_sb + (int64_t)(q_first + qi) * p.rq_st + h * p.rq_sh,
-                     lane, sm.hf[w]);
-    wave_sync();
-    for (int e = lane; e < D; e += 64) sm.h[qi][e] = f2bf(sm.hf[w][e]);
-    wave_sync();
-  }
-  __syncthreads();
+// Lane-per-pair routing of nq queries whose h rows (sm.h) and page-weight /
+// segment-weight rows (sm.rows: P page rows, then one row per fine id) are
+// staged: coarse pages by page mass (stable top-`coarse`, then ascending, in
+// sm.chosen), candidate masses, stable top-M; emit(q, rank, id) for every
+// selected candidate (rank = position in score order). All threads call it.
+template <int D, class SM, class Emit>
+TAO_DEV void route_core(SM& sm, int nq, int K, int coarse, int E, int M, int P, int tid,
+                        Emit emit) {
+  constexpr int G = 8;
   // ---- coarse pages: stable top-`coarse` by page mass, listed ascending
   if (coarse >= K) {
     for (int i = tid; i < nq * K; i += kQThreads) sm.chosen[i / K][i % K] = (uint8_t)(i % K);
@@ -580,13 +555,114 @@ __global__ __launch_bounds__(kQThreads) void route_tile_kernel(QueryRouteParams 
     if (rank < M) {
       int page, id;
       cand(q, j, page, id);
-      atomicOr(&sm.bits[q][id >> 5], 1u << (id & 31));
+      emit(q, rank, id);
     }
   }
+}
+
+template <int D>
+__global__ __launch_bounds__(kQThreads) void route_tile_kernel(QueryRouteParams p) {
+  using Geo = RouteTileGeo<D>;
+  __shared__ RouteTileSmem<D> sm;
+  constexpr int G = 8;                           // coarse_group (checked at launch)
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int64_t* desc = p.tiles + 8 * (blockIdx.x / BH);
+  if (!desc[6]) return;                          // no history: workgroup-uniform
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int q_first = (int)desc[0], nq = (int)desc[1];
+  const int coarse = (int)desc[2], M = (int)desc[3], erel = (int)desc[4];
+  const int epoch = p.first_epoch + erel;
+  const int K = epoch / G, pending = epoch % G;
+  const int E = G * coarse + pending;
+  const int P = K + (pending > 0);
+  const int words = (epoch + 31) >> 5;
+  const bf16_t* pw_g = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
+  const SwRows sw_g{p.sw + (size_t)bh * p.fine_cap * D,
+                    p.psw_pool + ((size_t)erel * BH + bh) * 8 * D, K * G};
+  // ---- stage: rows [0, P) page weights, [P, P + epoch) segment weights
+  for (int i = tid; i < (P + epoch) * (D / 8); i += kQThreads) {
+    const int r = i / (D / 8), c = i % (D / 8);
+    const bf16_t* src = r < P ? pw_g + (size_t)r * D : sw_g.row(r - P, D);
+    *(uint4*)&sm.rows[r][c * 8] = *(const uint4*)(src + c * 8);
+  }
+  for (int i = tid; i < kTileQ * Geo::WORDS; i += kQThreads) (&sm.bits[0][0])[i] = 0u;
+  // ---- h of each query: wave w does queries w, w + 4, ...
+  for (int qi = w; qi < nq; qi += 4) {
+    query_weights<D>(p.rq + b * p.rq_sb + (int64_t)(q_first + qi) * p.rq_st + h * p.rq_sh,
+                     lane, sm.hf[w]);
+    wave_sync();
+    for (int e = lane; e < D; e += 64) sm.h[qi][e] = f2bf(sm.hf[w][e]);
+    wave_sync();
+  }
+  __syncthreads();
+  route_core<D>(sm, nq, K, coarse, E, M, P, tid,
+                [&](int q, int rank, int id) { atomicOr(&sm.bits[q][id >> 5], 1u << (id & 31)); });
   __syncthreads();
   for (int i = tid; i < nq * words; i += kQThreads) {
     const int q = i / words, wd = i % words;
     p.qsel[((size_t)(b * p.T + q_first + q) * p.H + h) * p.qsel_words + wd] = sm.bits[q][wd];
+  }
+}
+
+// Turn routes of a prefill (route_kernel's turn mode) with the lane-per-pair
+// core: one 256-thread workgroup per (8 consecutive turns, batch, head). The
+// turns are split into runs that share a seal epoch (8 turns span at most
+// two); each run stages its epoch's rows once and routes its anchors
+// together. Outputs as route_kernel: ids in score order into the turn's
+// sel_pool slot; the publishing turn also writes the state's route, chosen
+// pages and route size.
+constexpr int kTurnGroup = 8;
+
+template <int D>
+__global__ __launch_bounds__(kQThreads) void route_turns_kernel(RouteParams p) {
+  constexpr int ROWS = kTurnRows<D>;
+  __shared__ RouteTileSmem<D, ROWS> sm;
+  constexpr int G = 8;
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int t0 = (blockIdx.x / BH) * kTurnGroup;
+  const int t1 = min(p.n_turns, t0 + kTurnGroup);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int s0 = t0; s0 < t1;) {
+    const int64_t* d0 = p.turns + 8 * s0;
+    int s1 = s0 + 1;
+    while (s1 < t1 && p.turns[8 * s1 + 1] == d0[1]) ++s1;
+    const int erel = (int)d0[1], K = (int)d0[2], pending = (int)d0[3];
+    const int coarse = (int)d0[4], M = (int)d0[5];
+    const int epoch = K * G + pending, P = K + (pending > 0), E = G * coarse + pending;
+    const int nq = s1 - s0;
+    const bf16_t* pw_g = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
+    const SwRows sw_g{p.sw + (size_t)bh * p.fine_cap * D,
+                      p.psw_pool + ((size_t)erel * BH + bh) * 8 * D, K * G};
+    __syncthreads();                               // the previous run is done with sm
+    for (int i = tid; i < (P + epoch) * (D / 8); i += kQThreads) {
+      const int r = i / (D / 8), c = i % (D / 8);
+      const bf16_t* src = r < P ? pw_g + (size_t)r * D : sw_g.row(r - P, D);
+      *(uint4*)&sm.rows[r][c * 8] = *(const uint4*)(src + c * 8);
+    }
+    for (int qi = w; qi < nq; qi += 4) {
+      const int64_t anchor = p.turns[8 * (s0 + qi)];
+      query_weights<D>(p.rq + b * p.rq_sb + anchor * p.rq_st + h * p.rq_sh, lane, sm.hf[w]);
+      wave_sync();
+      for (int e = lane; e < D; e += 64) sm.h[qi][e] = f2bf(sm.hf[w][e]);
+      wave_sync();
+    }
+    __syncthreads();
+    route_core<D>(sm, nq, K, coarse, E, M, P, tid, [&](int q, int rank, int id) {
+      const int64_t* dq = p.turns + 8 * (s0 + q);
+      p.sel_pool[((size_t)dq[6] * BH + bh) * p.sel_cap + rank] = id;
+      if (dq[7]) p.sel[(size_t)bh * p.sel_cap + rank] = id;
+    });
+    for (int q = 0; q < nq; ++q) {
+      if (!p.turns[8 * (s0 + q) + 7]) continue;   // workgroup-uniform
+      for (int i = tid; i < coarse; i += kQThreads)
+        p.chosen[(size_t)bh * p.chosen_cap + i] = sm.chosen[q][i];
+      if (bh == 0 && tid == 0) p.header[1] = M;
+    }
+    s0 = s1;
   }
 }
 
@@ -619,6 +695,18 @@ hipError_t launch_route_queries(const QueryRouteParams& p, int head_dim, hipStre
 hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s) {
   if (p.completed > kMaxSort || p.group * p.coarse + p.pending > kMaxSort)
     return hipErrorInvalidValue;
+  // Turn mode: the lane-per-pair kernel when every turn's rows fit its LDS.
+  if (p.turns && p.n_turns > 0 && p.group == 8 && p.max_epoch >= 1 &&
+      p.max_epoch / 8 + 1 + p.max_epoch <= (head_dim == 64 ? kTurnRows<64> : kTurnRows<128>)) {
+    const dim3 tgrid((unsigned)(p.B * p.H * ((p.n_turns + kTurnGroup - 1) / kTurnGroup)));
+    if (head_dim == 128)
+      hipLaunchKernelGGL(route_turns_kernel<128>, tgrid, dim3(kQThreads), 0, s, p);
+    else if (head_dim == 64)
+      hipLaunchKernelGGL(route_turns_kernel<64>, tgrid, dim3(kQThreads), 0, s, p);
+    else
+      return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   const dim3 grid((unsigned)(p.B * p.H * (p.turns ? p.n_turns : 1)));
   if (head_dim == 128)
     hipLaunchKernelGGL(route_kernel<128>, grid, dim3(kRouteThreads), 0, s, p);

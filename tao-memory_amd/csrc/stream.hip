@@ -332,7 +332,7 @@ int tao_batch_decode(void* batch, const tao_tokens* tok, const tao_fusion* fu, v
     if (rc) return rc;
     info[4 * r] = refreshed;
   }
-  tao::BatchStepParams p;
+  tao::BatchStepParams p{};
   auto view = [](const void* ptr, const int64_t* st) {
     tao::TokView v;
     v.p = (const bf16_t*)ptr;

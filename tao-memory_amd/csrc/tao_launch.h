@@ -168,6 +168,7 @@ struct RouteParams {
   const int64_t* turns; int n_turns;
   int B, H, fine_cap, page_cap, sel_cap, chosen_cap, group;
   int completed, pending, coarse, selected;
+  int max_epoch;                 // turn mode: largest epoch of any turn (0: unknown)
 };
 hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s);
 

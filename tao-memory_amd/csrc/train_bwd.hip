@@ -659,26 +659,29 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
 }
 
 // Outer products over a query set: out^T[e][d] = sum_q x[q][e] y[q][d].
-// mode 0 (dC of fine f = blockIdx / BH): queries of every tile that sees f,
-//   x = dnum, y = a = h pw sw (zero unless the query selected f); plus the
-//   coarse path's share w_f[d] sum_{K > g} cw_K[g][d] dG_K[d][e] for
-//   completed f.
-// mode 1 (dG of completed count K = coarse_first + blockIdx / BH): queries of
+// mode 0 (dC of the NF fines f0 .. f0 + NF - 1, f0 = NF * item): queries of
+//   every tile that sees f0, x = dnum, y_f = a = h pw sw (zero unless the
+//   query selected f); plus the coarse path's share
+//   w_f[d] sum_{K > g} cw_K[g][d] dG_K[d][e] for completed f.
+// mode 1 (dG of completed count K = coarse_first + item, NF = 1): queries of
 //   the tiles with K completed pages, x = dcoarse, y = h.
-// Chunks of 32 queries are staged transposed (x^T [e][q], y^T [d][q]) and
+// Chunks of 32 queries are staged transposed (x^T [e][q] once, y_f^T [d][q]
+// per fine: a query's dnum and h rows are read once for all NF fines) and
 // reduced with v_mfma_f32_32x32x16_bf16 (m = e, n = d, k = q); wave w owns
-// output tiles w, w + 4, ... of the (D / 32)^2 tiles. A workgroup takes
-// kObTiles of an item's tiles (grid = items x tile groups x B*H) and adds its
-// sums into the zeroed output with fp32 atomics; the first group adds the
-// coarse share.
+// output tiles w, w + 4, ... of the (D / 32)^2 tiles of every fine. A
+// workgroup takes kObTiles of an item's tiles (grid = items x tile groups x
+// B*H) and adds its sums into the zeroed output with fp32 atomics; the first
+// group adds the coarse share.
 constexpr int kObQ = 32;
 constexpr int kObTiles = 4;
+template <int D> constexpr int kObFines = D == 64 ? 4 : 2;
 
-template <int D>
+template <int D, int NF>
 __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int mode) {
   constexpr int DT = D / 32, NT = DT * DT, TPW = (NT + 3) / 4;
-  __shared__ bf16_t xt[D][kObQ + 8], yt[D][kObQ + 8];
-  __shared__ int any_sel;
+  static_assert(32 % NF == 0, "a fine group's selection bits share one word");
+  __shared__ bf16_t xt[D][kObQ + 8], yt[NF][D][kObQ + 8];
+  __shared__ int any_sel[NF];
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   const int b = bh / p.H, h = bh % p.H;
@@ -689,13 +692,15 @@ __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int
   const int item = blockIdx.x / BH / groups, tg = (blockIdx.x / BH) % groups;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 31, hl = lane >> 5;
-  floatx16 acc[TPW];
+  floatx16 acc[NF][TPW];
 #pragma unroll
-  for (int j = 0; j < TPW; ++j)
+  for (int k = 0; k < NF; ++k)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[j][i] = 0.0f;
-  const int f = item, Kc = p.coarse_first + item;
-  const int t_first = mode == 0 ? f + lag + 1 : lag + G * Kc;
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[k][j][i] = 0.0f;
+  const int f0 = item * NF, Kc = p.coarse_first + item;
+  const int t_first = mode == 0 ? f0 + lag + 1 : lag + G * Kc;
   const int t_last = mode == 0 ? n_tiles : min(n_tiles, lag + G * Kc + G);
   const int t_lo = t_first + tg * kObTiles;
   const int t_hi = min(t_last, t_lo + kObTiles);
@@ -703,94 +708,116 @@ __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int
   const bf16_t* gsw = p.fine_sw + (size_t)bh * p.fine_cap * D;
   for (int t = t_lo; t < t_hi; ++t) {
     const int V = tile_visible(t, lag), erel = V - 1, K = V / G;
+    // fines of the group this tile sees (bits of the selection word)
+    const uint32_t seen = mode == 0 ? ((1u << min(NF, max(V - f0, 0))) - 1u) : 1u;
     const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
     const bf16_t* psw = p.psw_pool + ((size_t)erel * BH + bh) * 8 * D;
     const int qa = t * p.ft, qb_end = min(p.T, qa + p.ft);
     for (int qb = qa; qb < qb_end; qb += kObQ) {
       __syncthreads();
-      if (tid == 0) any_sel = 0;
+      if (tid < NF) any_sel[tid] = 0;
       __syncthreads();
       // thread = (query qi, 8-channel chunk c): x and y rows, written transposed
       for (int job = tid; job < kObQ * (D / 8); job += kThreads) {
         const int qi = job % kObQ, c = job / kObQ;
         const int q = qb + qi;
-        float xv[8], yv[8];
+        float xv[8], hv[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) { xv[j] = 0.0f; yv[j] = 0.0f; }
+        for (int j = 0; j < 8; ++j) { xv[j] = 0.0f; hv[j] = 0.0f; }
+        uint32_t bits = 0;
         if (q < qb_end) {
           const size_t row = ((size_t)b * p.T + q) * p.H + h;
-          bool sel = true;
-          if (mode == 0) sel = (p.qsel[row * p.qsel_words + (f >> 5)] >> (f & 31)) & 1u;
-          if (sel) {
-            if (c == 0) any_sel = 1;
+          bits = mode == 0 ? (p.qsel[row * p.qsel_words + (f0 >> 5)] >> (f0 & 31)) & seen : 1u;
+          if (bits) {
             const float* xs = (mode == 0 ? p.dnum : p.dcoarse) + row * D + 8 * c;
             const bf16_t* hs = p.h + row * D + 8 * c;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
               xv[j] = xs[j];
-              float y = bf2f(hs[j]);
-              if (mode == 0) {
-                const int d = 8 * c + j;
-                y *= bf2f(pw[(size_t)(f / G) * D + d]) *
-                     bf2f(f < K * G ? gsw[(size_t)f * D + d] : psw[(size_t)(f - K * G) * D + d]);
-              }
-              yv[j] = y;
+              hv[j] = bf2f(hs[j]);
             }
           }
         }
+        if (c == 0)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          xt[8 * c + j][qi] = f2bf(xv[j]);
-          yt[8 * c + j][qi] = f2bf(yv[j]);
+          for (int k = 0; k < NF; ++k)
+            if ((bits >> k) & 1u) any_sel[k] = 1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xt[8 * c + j][qi] = f2bf(xv[j]);
+#pragma unroll
+        for (int k = 0; k < NF; ++k) {
+          const int f = f0 + k;
+          const bool on = (bits >> k) & 1u;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            float y = hv[j];
+            if (mode == 0) {
+              const int d = 8 * c + j;
+              y = on ? y * bf2f(pw[(size_t)(f / G) * D + d]) *
+                           bf2f(f < K * G ? gsw[(size_t)f * D + d]
+                                          : psw[(size_t)(f - K * G) * D + d])
+                     : 0.0f;
+            }
+            yt[k][8 * c + j][qi] = f2bf(y);
+          }
         }
       }
       __syncthreads();
-      if (!any_sel) continue;                          // workgroup-uniform
 #pragma unroll
-      for (int j = 0; j < TPW; ++j) {
-        const int tt = w + 4 * j;
-        if (tt < NT) {
-          const int mt = tt / DT, nt = tt % DT;
+      for (int k = 0; k < NF; ++k) {
+        if (!any_sel[k]) continue;                     // workgroup-uniform
 #pragma unroll
-          for (int ks = 0; ks < kObQ / 16; ++ks)
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                as_bf16x8(*(const uint4*)&xt[32 * mt + li][16 * ks + 8 * hl]),
-                as_bf16x8(*(const uint4*)&yt[32 * nt + li][16 * ks + 8 * hl]), acc[j], 0, 0, 0);
+        for (int j = 0; j < TPW; ++j) {
+          const int tt = w + 4 * j;
+          if (tt < NT) {
+            const int mt = tt / DT, nt = tt % DT;
+#pragma unroll
+            for (int ks = 0; ks < kObQ / 16; ++ks)
+              acc[k][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                  as_bf16x8(*(const uint4*)&xt[32 * mt + li][16 * ks + 8 * hl]),
+                  as_bf16x8(*(const uint4*)&yt[k][32 * nt + li][16 * ks + 8 * hl]), acc[k][j],
+                  0, 0, 0);
+          }
         }
       }
     }
   }
-  float* out = mode == 0 ? p.dc + ((size_t)bh * p.v_max + f) * D * D
-                         : p.dgc + ((size_t)item * BH + bh) * D * D;
-  const bool coarse_share = mode == 0 && tg == 0 && p.coarse_values && f < G * (p.v_max / G);
-  const int g = f / G;
   const bf16_t* pz = p.page_z + (size_t)bh * p.page_cap * D;
 #pragma unroll
-  for (int j = 0; j < TPW; ++j) {
-    const int tt = w + 4 * j;
-    if (tt >= NT) continue;
-    const int mt = tt / DT, nt = tt % DT;
-    const int d = 32 * nt + li;
-    if (coarse_share) {
-      const float wf = bf2f(gsw[(size_t)f * D + d]);
-      for (int k2 = max(g + 1, p.coarse_first); k2 < p.coarse_first + p.coarse_count; ++k2) {
-        float m = -__builtin_inff();
-        for (int jj = 0; jj < k2; ++jj) m = fmaxf(m, bf2f(pz[(size_t)jj * D + d]));
-        float z = 0.0f;
-        for (int jj = 0; jj < k2; ++jj) z += __expf(bf2f(pz[(size_t)jj * D + d]) - m);
-        const float scale = wf * __expf(bf2f(pz[(size_t)g * D + d]) - m) / z;
-        const float* dg = p.dgc + ((size_t)(k2 - p.coarse_first) * BH + bh) * D * D;
+  for (int k = 0; k < NF; ++k) {
+    const int f = f0 + k;
+    if (mode == 0 && f >= p.v_max) break;
+    float* out = mode == 0 ? p.dc + ((size_t)bh * p.v_max + f) * D * D
+                           : p.dgc + ((size_t)item * BH + bh) * D * D;
+    const bool coarse_share = mode == 0 && tg == 0 && p.coarse_values && f < G * (p.v_max / G);
+    const int g = f / G;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int e = 32 * mt + 8 * (i / 4) + 4 * hl + (i % 4);
-          acc[j][i] = fmaf(scale, dg[(size_t)e * D + d], acc[j][i]);
+    for (int j = 0; j < TPW; ++j) {
+      const int tt = w + 4 * j;
+      if (tt >= NT) continue;
+      const int mt = tt / DT, nt = tt % DT;
+      const int d = 32 * nt + li;
+      if (coarse_share) {
+        const float wf = bf2f(gsw[(size_t)f * D + d]);
+        for (int k2 = max(g + 1, p.coarse_first); k2 < p.coarse_first + p.coarse_count; ++k2) {
+          float m = -__builtin_inff();
+          for (int jj = 0; jj < k2; ++jj) m = fmaxf(m, bf2f(pz[(size_t)jj * D + d]));
+          float z = 0.0f;
+          for (int jj = 0; jj < k2; ++jj) z += __expf(bf2f(pz[(size_t)jj * D + d]) - m);
+          const float scale = wf * __expf(bf2f(pz[(size_t)g * D + d]) - m) / z;
+          const float* dg = p.dgc + ((size_t)(k2 - p.coarse_first) * BH + bh) * D * D;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int e = 32 * mt + 8 * (i / 4) + 4 * hl + (i % 4);
+            acc[k][j][i] = fmaf(scale, dg[(size_t)e * D + d], acc[k][j][i]);
+          }
         }
       }
-    }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int e = 32 * mt + 8 * (i / 4) + 4 * hl + (i % 4);
-      atomicAdd(out + (size_t)e * D + d, acc[j][i]);
+      for (int i = 0; i < 16; ++i) {
+        const int e = 32 * mt + 8 * (i / 4) + 4 * hl + (i % 4);
+        atomicAdd(out + (size_t)e * D + d, acc[k][j][i]);
+      }
     }
   }
 }
@@ -895,105 +922,129 @@ __global__ __launch_bounds__(D) void zpage_bwd_kernel(MemBwdParams p) {
 // Softmax writer adjoint of block f (tao_stream.py:66-77): per channel d over
 // the block's tokens, P = softmax_t(raw_k), z = logsumexp, C = P^T V;
 //   dP[t][d] = sum_e dC[d][e] v[t][e],  dv[t][e] += sum_d P[t][d] dC[d][e],
-//   d raw_k[t][d] = P (dP - sum_t P dP) + dz P, with sum_t P dP = sum_e dC C.
-// Thread per token; the token's raw_k and v rows sit in registers, dC^T in
-// LDS chunks: 16 channels d for d raw_k, then 16 values e for dv.
+//   d raw_k[t][d] = P (dP - sum_t P dP + dz), with sum_t P dP = sum_e dC C.
+// One 512-thread workgroup per (block, batch, head); wave w owns tokens
+// [32 w, 32 w + 32). Both products run on v_mfma_f32_32x32x16_bf16 (m = t):
+// dP with A = the wave's v rows, B = dC rows [d][e]; dv with A = P rows
+// (rebuilt from raw_k and the column statistics), B = dC^T rows [e][d].
+constexpr int kWbWaves = 8;
+
 template <int D>
-__global__ __launch_bounds__(kThreads) void writer_bwd_kernel(MemBwdParams p) {
-  constexpr int CK = 16;
-  __shared__ float chunk[D * CK];                // dC^T[e][d0 + j] or dC^T[e0 + j][d]
-  __shared__ float stat[3][D];                   // max, 1 / Z, sum_e dC C
-  __shared__ float red[kThreads / D][D];
+struct WriterBwdSmem {
+  bf16_t dc[D][D + 8];          // dC [d][e]
+  bf16_t dct[D][D + 8];         // dC^T [e][d]
+  float stat[3][D];             // max, 1 / Z, sum_e dC C (+ dz folded into the third)
+  float red[kWbWaves][D];
+};
+
+template <int D>
+__global__ __launch_bounds__(kWbWaves * 64) void writer_bwd_kernel(MemBwdParams p) {
+  constexpr int KK = D / 16, DT = D / 32, NT = kWbWaves * 64;
+  __shared__ WriterBwdSmem<D> sm;
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   const int f = blockIdx.x / BH;
   const int b = bh / p.H, h = bh % p.H;
-  const int t = threadIdx.x;                     // token of the block (ft == 256)
-  const int tok = f * p.ft + t;
-  const bf16_t* kg = p.raw_k.p + b * p.raw_k.sb + (int64_t)tok * p.raw_k.st + h * p.raw_k.sh;
-  const bf16_t* vg = p.v.p + b * p.v.sb + (int64_t)tok * p.v.st + h * p.v.sh;
-  const float* dc = p.dc + ((size_t)bh * p.v_max + f) * D * D;                // [e][d]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
+  const int tok0 = f * p.ft;
+  const float* dcg = p.dc + ((size_t)bh * p.v_max + f) * D * D;               // dC^T [e][d]
   const bf16_t* c = p.bank + ((size_t)bh * p.fine_cap + f) * D * D;           // C^T [e][d]
-  // column statistics: thread (d, token group) over 256 / (kThreads / D) tokens
+  const float* dzf = p.dz + ((size_t)bh * p.v_max + f) * D;
+  // ---- stage dC^T (as is) and dC (transposed), bf16
+  for (int i = tid; i < D * D; i += NT) {
+    const int e = i / D, d = i % D;
+    const bf16_t v = f2bf(dcg[i]);
+    sm.dct[e][d] = v;
+    sm.dc[d][e] = v;
+  }
+  // ---- column statistics over the 256 tokens: thread (d, token group)
   {
-    constexpr int TG = kThreads / D, TPG = 256 / TG;
-    const int d = t % D, tg = t / D;
+    constexpr int TG = NT / D, TPG = 256 / TG;
+    const int d = tid % D, tg = tid / D;
     const bf16_t* col = p.raw_k.p + b * p.raw_k.sb + h * p.raw_k.sh + d;
     float m = -__builtin_inff();
     for (int i = 0; i < TPG; ++i)
-      m = fmaxf(m, bf2f(col[(int64_t)(f * p.ft + tg * TPG + i) * p.raw_k.st]));
-    red[tg][d] = m;
+      m = fmaxf(m, bf2f(col[(int64_t)(tok0 + tg * TPG + i) * p.raw_k.st]));
+    sm.red[tg][d] = m;
     __syncthreads();
     if (tg == 0) {
-      for (int i = 1; i < TG; ++i) m = fmaxf(m, red[i][d]);
-      stat[0][d] = m;
+      for (int i = 1; i < TG; ++i) m = fmaxf(m, sm.red[i][d]);
+      sm.stat[0][d] = m;
     }
     __syncthreads();
-    m = stat[0][d];
+    m = sm.stat[0][d];
     float z = 0.0f;
     for (int i = 0; i < TPG; ++i)
-      z += __expf(bf2f(col[(int64_t)(f * p.ft + tg * TPG + i) * p.raw_k.st]) - m);
-    red[tg][d] = z;
+      z += __expf(bf2f(col[(int64_t)(tok0 + tg * TPG + i) * p.raw_k.st]) - m);
+    sm.red[tg][d] = z;
     __syncthreads();
     if (tg == 0) {
-      for (int i = 1; i < TG; ++i) z += red[i][d];
-      stat[1][d] = 1.0f / z;
+      for (int i = 1; i < TG; ++i) z += sm.red[i][d];
+      sm.stat[1][d] = 1.0f / z;
       float sdc = 0.0f;
-      for (int e = 0; e < D; ++e) sdc = fmaf(dc[(size_t)e * D + d], bf2f(c[(size_t)e * D + d]), sdc);
-      stat[2][d] = sdc;
+      for (int e = 0; e < D; ++e) sdc = fmaf(dcg[(size_t)e * D + d], bf2f(c[(size_t)e * D + d]), sdc);
+      sm.stat[2][d] = sdc - dzf[d];            // dk = P (dP - stat2)
     }
     __syncthreads();
   }
-  uint32_t kp[D / 2], vp[D / 2];                 // the token's raw_k and v rows (bf16 pairs)
+  // ---- A operands of the wave's 32 tokens: v rows and P rows (row li)
+  const int t_row = tok0 + 32 * w + li;
+  const bf16_t* vrow = p.v.p + b * p.v.sb + (int64_t)t_row * p.v.st + h * p.v.sh;
+  const bf16_t* krow = p.raw_k.p + b * p.raw_k.sb + (int64_t)t_row * p.raw_k.st + h * p.raw_k.sh;
+  bf16x8 va[KK], pa[KK];
 #pragma unroll
-  for (int i = 0; i < D / 8; ++i) {
-    const uint4 ku = *(const uint4*)(kg + 8 * i), vu = *(const uint4*)(vg + 8 * i);
-    kp[4 * i] = ku.x; kp[4 * i + 1] = ku.y; kp[4 * i + 2] = ku.z; kp[4 * i + 3] = ku.w;
-    vp[4 * i] = vu.x; vp[4 * i + 1] = vu.y; vp[4 * i + 2] = vu.z; vp[4 * i + 3] = vu.w;
+  for (int kk = 0; kk < KK; ++kk) {
+    const int d0 = 16 * kk + 8 * hl;
+    va[kk] = as_bf16x8(*(const uint4*)(vrow + d0));
+    const uint4 ku = *(const uint4*)(krow + d0);
+    const uint32_t kw[4] = {ku.x, ku.y, ku.z, ku.w};
+    uint32_t pk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = d0 + 2 * j;
+      const float k0 = __uint_as_float(kw[j] << 16), k1 = __uint_as_float(kw[j] & 0xFFFF0000u);
+      pk[j] = pack_bf16x2(__expf(k0 - sm.stat[0][d]) * sm.stat[1][d],
+                          __expf(k1 - sm.stat[0][d + 1]) * sm.stat[1][d + 1]);
+    }
+    pa[kk] = as_bf16x8(make_uint4(pk[0], pk[1], pk[2], pk[3]));
   }
-  auto unpack = [](const uint32_t* r, int i) __attribute__((always_inline)) {
-    return __uint_as_float((i & 1) ? (r[i >> 1] & 0xFFFF0000u) : (r[i >> 1] << 16));
-  };
-  // ---- d raw_k, 16 channels at a time
-  bf16_t* dkr = p.draw_k + (((size_t)b * p.T + tok) * p.H + h) * D;
-  const float* dzf = p.dz + ((size_t)bh * p.v_max + f) * D;
-  for (int d0 = 0; d0 < D; d0 += CK) {
-    __syncthreads();
-    for (int i = t; i < D * CK; i += kThreads) chunk[i] = dc[(size_t)(i / CK) * D + d0 + i % CK];
-    __syncthreads();
-    float dp[CK];
+  // ---- d raw_k: dP[t][d] (accumulator: lane = d column, rows t_i)
 #pragma unroll
-    for (int j = 0; j < CK; ++j) dp[j] = 0.0f;
+  for (int t = 0; t < DT; ++t) {
+    floatx16 dp;
 #pragma unroll
-    for (int e = 0; e < D; ++e) {
-      const float ve = unpack(vp, e);
+    for (int i = 0; i < 16; ++i) dp[i] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < CK; ++j) dp[j] = fmaf(chunk[e * CK + j], ve, dp[j]);
-    }
+    for (int kk = 0; kk < KK; ++kk)
+      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          va[kk], as_bf16x8(*(const uint4*)&sm.dc[32 * t + li][16 * kk + 8 * hl]), dp, 0, 0, 0);
+    const int d = 32 * t + li;
 #pragma unroll
-    for (int j = 0; j < CK; ++j) {
-      const int d = d0 + j;
-      const float pr = __expf(bf2f(kg[d]) - stat[0][d]) * stat[1][d];
-      dkr[d] = f2bf(pr * (dp[j] - stat[2][d]) + dzf[d] * pr);
+    for (int i = 0; i < 16; ++i) {
+      const int tok = tok0 + 32 * w + 8 * (i / 4) + 4 * hl + (i % 4);
+      const size_t row = ((size_t)b * p.T + tok) * p.H + h;
+      const float kv = bf2f(p.raw_k.p[b * p.raw_k.sb + (int64_t)tok * p.raw_k.st + h * p.raw_k.sh + d]);
+      const float pr = __expf(kv - sm.stat[0][d]) * sm.stat[1][d];
+      p.draw_k[row * D + d] = f2bf(pr * (dp[i] - sm.stat[2][d]));
     }
   }
-  // ---- dv, 16 values at a time: dv[e] = sum_d P[d] dC^T[e][d]
-  float* dvr = p.dv + (((size_t)b * p.T + tok) * p.H + h) * D;
-  for (int e0 = 0; e0 < D; e0 += CK) {
-    __syncthreads();
-    for (int i = t; i < D * CK; i += kThreads) chunk[i] = dc[(size_t)(e0 + i / D) * D + i % D];
-    __syncthreads();
-    float acc[CK];
+  // ---- dv[t][e] += sum_d P[t][d] dC[d][e] (accumulator: lane = e column)
 #pragma unroll
-    for (int j = 0; j < CK; ++j) acc[j] = 0.0f;
+  for (int t = 0; t < DT; ++t) {
+    floatx16 acc;
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const float pr = __expf(unpack(kp, d) - stat[0][d]) * stat[1][d];
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < CK; ++j) acc[j] = fmaf(pr, chunk[j * D + d], acc[j]);
+    for (int kk = 0; kk < KK; ++kk)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          pa[kk], as_bf16x8(*(const uint4*)&sm.dct[32 * t + li][16 * kk + 8 * hl]), acc, 0, 0, 0);
+    const int e = 32 * t + li;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int tok = tok0 + 32 * w + 8 * (i / 4) + 4 * hl + (i % 4);
+      p.dv[(((size_t)b * p.T + tok) * p.H + h) * D + e] += acc[i];
     }
-#pragma unroll
-    for (int j = 0; j < CK; ++j) dvr[e0 + j] += acc[j];
   }
 }
 
@@ -1074,13 +1125,15 @@ hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s) {
       hipLaunchKernelGGL(read_bwd_kernel<D_>, dim3((unsigned)(blocks * BH)),                 \
                          dim3(kRbWaves * 64), 0, s, p);                                      \
       if (p.coarse_values && p.coarse_count > 0) {                                           \
-        hipLaunchKernelGGL(outer_bwd_kernel<D_>,                                             \
+        hipLaunchKernelGGL((outer_bwd_kernel<D_, 1>),                                        \
                            dim3((unsigned)(p.coarse_count * dg_groups * BH)), dim3(kThreads),\
                            0, s, p, 1);                                                      \
         hipLaunchKernelGGL(coarse_page_bwd_kernel<D_>, dim3((unsigned)(p.coarse_count * BH)),\
                            dim3(D_), 0, s, p);                                               \
       }                                                                                      \
-      hipLaunchKernelGGL(outer_bwd_kernel<D_>, dim3((unsigned)(p.v_max * dc_groups * BH)),   \
+      hipLaunchKernelGGL((outer_bwd_kernel<D_, kObFines<D_>>),                               \
+                         dim3((unsigned)(((p.v_max + kObFines<D_> - 1) / kObFines<D_>) *     \
+                                         dc_groups * BH)),                                   \
                          dim3(kThreads), 0, s, p, 0);                                        \
       hipLaunchKernelGGL(page_bwd_kernel<D_>, dim3((unsigned)(n_tiles * BH)), dim3(D_), 0,   \
                          s, p);                                                              \
@@ -1088,7 +1141,7 @@ hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s) {
         hipLaunchKernelGGL(zpage_bwd_kernel<D_>, dim3((unsigned)((p.v_max / p.group) * BH)), \
                            dim3(D_), 0, s, p);                                               \
       hipLaunchKernelGGL(writer_bwd_kernel<D_>, dim3((unsigned)(p.v_max * BH)),              \
-                         dim3(kThreads), 0, s, p);                                           \
+                         dim3(kWbWaves * 64), 0, s, p);                                      \
     }                                                                                        \
     const int rows = p.B * p.T * p.H;                                                        \
     hipLaunchKernelGGL(finish_bwd_kernel<D_>,                                                \

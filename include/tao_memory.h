@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 4
+#define TAO_ABI_VERSION 5
 
 enum tao_status {
   TAO_OK = 0,
@@ -378,6 +378,77 @@ int tao_batch_close(void* batch);
 /* Destroy the driver's captured graph (semantic state is untouched). */
 int tao_stream_release(void* handle);
 int tao_stream_close(void* handle);
+
+/* ---- Non-preset fine writers (TaoConfig.fine_writer other than "softmax")
+ * and the channel-given selected read. Plain operators on caller buffers,
+ * stream-ordered, no allocation. Statistics and matrices are [.., D, D]
+ * row-major with rows d (feature channel) and columns e (value channel), as
+ * the reference's. */
+enum tao_stats_mode { TAO_STATS_ASSOCIATION = 0, TAO_STATS_STRUCTURED = 1 };
+
+/* Simplex-feature statistics of `blocks` independent token blocks; k, v bf16
+ * [blocks, tokens, H, D] with element strides (block, token, head), D
+ * contiguous; u = bf16(softmax_D(fp32 k)). Outputs fp32, contiguous:
+ *   TAO_STATS_ASSOCIATION (association_statistics,
+ *     association_writer.py:11-18): gram [blocks, H, D, D] = u^T u,
+ *     cross [blocks, H, D, D] = u^T v, mass [blocks, H, D] = sum_t u
+ *     (nullable: with_mass=False);
+ *   TAO_STATS_STRUCTURED (structured_statistics, structured_writer.py:5-13):
+ *     gram receives square_mass [blocks, H, D] = sum_t u^2, cross, mass. */
+int tao_writer_statistics(const void* k, const int64_t* k_s, const void* v, const int64_t* v_s,
+                          int32_t blocks, int32_t tokens, int32_t heads, int32_t head_dim,
+                          int32_t mode, float* gram, float* cross, float* mass, void* stream);
+
+/* association_matrix (association_writer.py:21-32) of `count` independent
+ * fp32 pairs [count, D, D]: out = bf16(X), (gram + trace(gram)/D I) X = cross,
+ * by a Cholesky factor. info (nullable, int32 [count]) receives 0, or j + 1
+ * when pivot j of the factor is not positive; the reference raises there
+ * (torch.linalg.cholesky) unless unchecked. */
+int tao_association_matrix(const float* gram, const float* cross, int32_t count, int32_t head_dim,
+                           void* out, int32_t* info, void* stream);
+
+/* structured_matrix (structured_writer.py:16-34): the analytic inverse of
+ * diag(var + ridge) - var var^T / sum(var) + mass mass^T / tokens applied to
+ * cross (var = max(square_mass - mass^2 / tokens, 0), ridge = mean
+ * square_mass), fp32 in [count, D] / [count, D, D], bf16 out [count, D, D]. */
+int tao_structured_matrix(const float* square_mass, const float* cross, const float* mass,
+                          int32_t count, int32_t head_dim, float tokens, void* out, void* stream);
+
+/* chronological_sum (association_writer.py:35-40): out[o][i] = fp32 sum over
+ * f in order of x[o][f][i], x contiguous [outer, fines, inner]. */
+int tao_chronological_sum(const float* statistics, int64_t outer, int32_t fines, int64_t inner,
+                          float* out, void* stream);
+
+/* feature_read_coefficients (association_writer.py:43-53): h bf16
+ * [B, T, H, D] (strides h_s: b, t, h); read_z bf16 broadcastable to
+ * [B, T, H, P, D] (strides z_s: b, t, h, p; 0 on a broadcast axis);
+ * out bf16 [B, T, H, P, D] contiguous =
+ * bf16(mass_p / sum_p mass_p * h), mass_p = sum_d h[d] exp(z_p[d]). */
+int tao_feature_read_coefficients(const void* h, const int64_t* h_s, const void* read_z,
+                                  const int64_t* z_s, int32_t batch, int32_t tokens,
+                                  int32_t heads, int32_t pages, int32_t head_dim, void* out,
+                                  void* stream);
+
+/* selected_fine_numerator (indirect_fine.py:123-133, _SelectedContraction
+ * :65-120): channel bf16 [B, Q, H, M, D], selected_id int64 [B, Q, H, M],
+ * fine_c bf16 [BB, H, S, D, D] (batch b reads bank b % BB), all contiguous;
+ * out bf16 [B, Q, H, D] = bf16(sum_m channel_m . C[id_m]). M <= 64,
+ * S <= 4096; ids outside [0, S) contribute nothing. */
+int tao_selected_numerator(const void* channel, const int64_t* selected_id, const void* fine_c,
+                           int32_t batch, int32_t queries, int32_t heads, int32_t selected,
+                           int32_t bank_batch, int32_t fines, int32_t head_dim, void* out,
+                           void* stream);
+/* Its backward (_SelectedContraction.backward, indirect_fine.py:101-120):
+ * grad bf16 [B, Q, H, D]; grad_channel (nullable) bf16 [B, Q, H, M, D] =
+ * bf16(grad . C[id_m]^T) (_grouped_grad_a :172-195); grad_fine_c (nullable)
+ * bf16 [BB, H, S, D, D] = bf16(sum over b % BB == bb of bf16(per-batch
+ * sum of channel^T grad over the pairs selecting each fine))
+ * (_shared_grad_c :198-227). Every element of both outputs is written. */
+int tao_selected_numerator_backward(const void* channel, const int64_t* selected_id,
+                                    const void* fine_c, const void* grad, int32_t batch,
+                                    int32_t queries, int32_t heads, int32_t selected,
+                                    int32_t bank_batch, int32_t fines, int32_t head_dim,
+                                    void* grad_channel, void* grad_fine_c, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1021,3 +1021,165 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   }
   return TAO_OK;
 }
+
+// ---- non-preset fine writers and the channel-given selected read
+
+namespace {
+
+bool head_ok(int32_t d) { return d == 64 || d == 128; }
+
+void copy3(int64_t dst[3], const int64_t* src) {
+  for (int i = 0; i < 3; ++i) dst[i] = src[i];
+}
+
+}  // namespace
+
+int tao_writer_statistics(const void* k, const int64_t* k_s, const void* v, const int64_t* v_s,
+                          int32_t blocks, int32_t tokens, int32_t heads, int32_t head_dim,
+                          int32_t mode, float* gram, float* cross, float* mass, void* stream) {
+  if (!head_ok(head_dim)) return fail(TAO_E_SHAPE, "head_dim must be 64 or 128 on the HIP path");
+  if (blocks < 0 || tokens < 0 || heads < 0) return fail(TAO_E_SHAPE, "negative extent");
+  if (mode != TAO_STATS_ASSOCIATION && mode != TAO_STATS_STRUCTURED)
+    return fail(TAO_E_ARGUMENT, "unknown statistics mode");
+  if ((size_t)blocks * heads == 0) return TAO_OK;
+  if (!k || !v || !k_s || !v_s || !gram || !cross || (mode == TAO_STATS_STRUCTURED && !mass))
+    return fail(TAO_E_ARGUMENT, "null operand");
+  if (tokens == 0) return fail(TAO_E_SHAPE, "statistics of an empty block");
+  tao::WriterStatsParams p{};
+  p.k = (const bf16_t*)k;
+  p.v = (const bf16_t*)v;
+  copy3(p.k_s, k_s);
+  copy3(p.v_s, v_s);
+  p.N = blocks;
+  p.T = tokens;
+  p.H = heads;
+  p.mode = mode == TAO_STATS_STRUCTURED ? 1 : 0;
+  p.gram = gram;
+  p.cross = cross;
+  p.mass = mass;
+  return check_hip(tao::launch_writer_stats(p, head_dim, (hipStream_t)stream),
+                   "tao_writer_statistics");
+}
+
+int tao_association_matrix(const float* gram, const float* cross, int32_t count, int32_t head_dim,
+                           void* out, int32_t* info, void* stream) {
+  if (!head_ok(head_dim)) return fail(TAO_E_SHAPE, "head_dim must be 64 or 128 on the HIP path");
+  if (count < 0) return fail(TAO_E_SHAPE, "negative count");
+  if (count == 0) return TAO_OK;
+  if (!gram || !cross || !out) return fail(TAO_E_ARGUMENT, "null operand");
+  tao::AssocSolveParams p{};
+  p.gram = gram;
+  p.cross = cross;
+  p.count = count;
+  p.out = (bf16_t*)out;
+  p.info = info;
+  return check_hip(tao::launch_association_solve(p, head_dim, (hipStream_t)stream),
+                   "tao_association_matrix");
+}
+
+int tao_structured_matrix(const float* square_mass, const float* cross, const float* mass,
+                          int32_t count, int32_t head_dim, float tokens, void* out, void* stream) {
+  if (!head_ok(head_dim)) return fail(TAO_E_SHAPE, "head_dim must be 64 or 128 on the HIP path");
+  if (count < 0) return fail(TAO_E_SHAPE, "negative count");
+  if (count == 0) return TAO_OK;
+  if (!square_mass || !cross || !mass || !out) return fail(TAO_E_ARGUMENT, "null operand");
+  tao::StructuredParams p{};
+  p.square = square_mass;
+  p.cross = cross;
+  p.mass = mass;
+  p.count_mats = count;
+  p.count = tokens;
+  p.out = (bf16_t*)out;
+  return check_hip(tao::launch_structured_matrix(p, head_dim, (hipStream_t)stream),
+                   "tao_structured_matrix");
+}
+
+int tao_chronological_sum(const float* statistics, int64_t outer, int32_t fines, int64_t inner,
+                          float* out, void* stream) {
+  if (outer < 0 || inner < 0 || fines < 1) return fail(TAO_E_SHAPE, "bad extents");
+  if (outer * inner == 0) return TAO_OK;
+  if (!statistics || !out) return fail(TAO_E_ARGUMENT, "null operand");
+  return check_hip(tao::launch_chrono_sum(statistics, out, outer, fines, inner, (hipStream_t)stream),
+                   "tao_chronological_sum");
+}
+
+int tao_feature_read_coefficients(const void* h, const int64_t* h_s, const void* read_z,
+                                  const int64_t* z_s, int32_t batch, int32_t tokens,
+                                  int32_t heads, int32_t pages, int32_t head_dim, void* out,
+                                  void* stream) {
+  if (!head_ok(head_dim)) return fail(TAO_E_SHAPE, "head_dim must be 64 or 128 on the HIP path");
+  if (batch < 0 || tokens < 0 || heads < 0 || pages < 0) return fail(TAO_E_SHAPE, "negative extent");
+  if ((size_t)batch * tokens * heads * pages == 0) return TAO_OK;
+  if (!h || !h_s || !read_z || !z_s || !out) return fail(TAO_E_ARGUMENT, "null operand");
+  tao::FeatureCoeffParams p{};
+  p.h = (const bf16_t*)h;
+  p.z = (const bf16_t*)read_z;
+  copy3(p.h_s, h_s);
+  for (int i = 0; i < 4; ++i) p.z_s[i] = z_s[i];
+  p.B = batch;
+  p.T = tokens;
+  p.H = heads;
+  p.P = pages;
+  p.out = (bf16_t*)out;
+  return check_hip(tao::launch_feature_coeff(p, head_dim, (hipStream_t)stream),
+                   "tao_feature_read_coefficients");
+}
+
+namespace {
+
+int selected_args(tao::SelectedParams& p, const void* channel, const int64_t* selected_id,
+                  const void* fine_c, int32_t batch, int32_t queries, int32_t heads,
+                  int32_t selected, int32_t bank_batch, int32_t fines, int32_t head_dim) {
+  if (!head_ok(head_dim)) return fail(TAO_E_SHAPE, "head_dim must be 64 or 128 on the HIP path");
+  if (batch < 0 || queries < 0 || heads < 0 || selected < 0 || fines < 0)
+    return fail(TAO_E_SHAPE, "negative extent");
+  if (bank_batch < 1 || batch % bank_batch != 0)
+    return fail(TAO_E_SHAPE, "batch must be a multiple of the bank batch");
+  if (selected > 64) return fail(TAO_E_CAPACITY, "more than 64 selected fines per query");
+  if (fines > 4096) return fail(TAO_E_CAPACITY, "more than 4096 fines in the bank");
+  if (!channel || !selected_id || !fine_c) return fail(TAO_E_ARGUMENT, "null operand");
+  p.channel = (const bf16_t*)channel;
+  p.ids = selected_id;
+  p.bank = (const bf16_t*)fine_c;
+  p.B = batch;
+  p.Q = queries;
+  p.H = heads;
+  p.M = selected;
+  p.BB = bank_batch;
+  p.S = fines;
+  return TAO_OK;
+}
+
+}  // namespace
+
+int tao_selected_numerator(const void* channel, const int64_t* selected_id, const void* fine_c,
+                           int32_t batch, int32_t queries, int32_t heads, int32_t selected,
+                           int32_t bank_batch, int32_t fines, int32_t head_dim, void* out,
+                           void* stream) {
+  tao::SelectedParams p{};
+  const int rc = selected_args(p, channel, selected_id, fine_c, batch, queries, heads, selected,
+                               bank_batch, fines, head_dim);
+  if (rc) return rc;
+  if (!out) return fail(TAO_E_ARGUMENT, "null output");
+  p.out = (bf16_t*)out;
+  return check_hip(tao::launch_selected_numerator(p, head_dim, (hipStream_t)stream),
+                   "tao_selected_numerator");
+}
+
+int tao_selected_numerator_backward(const void* channel, const int64_t* selected_id,
+                                    const void* fine_c, const void* grad, int32_t batch,
+                                    int32_t queries, int32_t heads, int32_t selected,
+                                    int32_t bank_batch, int32_t fines, int32_t head_dim,
+                                    void* grad_channel, void* grad_fine_c, void* stream) {
+  tao::SelectedParams p{};
+  const int rc = selected_args(p, channel, selected_id, fine_c, batch, queries, heads, selected,
+                               bank_batch, fines, head_dim);
+  if (rc) return rc;
+  if (!grad) return fail(TAO_E_ARGUMENT, "null gradient");
+  p.grad = (const bf16_t*)grad;
+  p.grad_channel = (bf16_t*)grad_channel;
+  p.grad_bank = (bf16_t*)grad_fine_c;
+  return check_hip(tao::launch_selected_numerator_bwd(p, head_dim, (hipStream_t)stream),
+                   "tao_selected_numerator_backward");
+}
+

@@ -1,0 +1,388 @@
+// Non-preset fine writers on gfx950: simplex-feature statistics, the
+// regularised association solve, the structured (diagonal + rank-two)
+// inverse, the chronological statistic sum and the feature-mass read
+// coefficients.
+//
+// writer_stats_kernel (association_writer.py:11-18, structured_writer.py:5-13):
+//   one 512-thread workgroup per (block n, head h). Tokens are taken 64 at a
+//   time: 8 lanes per token form u = bf16(softmax_D(fp32 k)) (max and sum
+//   over the 8 lanes' shuffles), u^T and v^T are staged in LDS, and
+//   gram = u^T u, cross = u^T v run on v_mfma_f32_32x32x16_bf16 (m = d,
+//   n = d' or e, k = token); u is bf16 and v is bf16, so every product is
+//   exact and only the fp32 summation order differs from the reference's
+//   matmul. mass = sum_t u and square_mass = sum_t u^2 are per-channel fp32
+//   sums over the staged rows.
+// association_solve_kernel (association_writer.py:21-32): one workgroup per
+//   [D, D] pair. The system gram + (trace / D) I is factored in LDS by a
+//   right-looking Cholesky (column j: pivot, column scale, trailing rank-one
+//   update, two barriers), then cross is solved in place by forward and back
+//   substitution, one thread per right-hand-side column; C = bf16(X).
+// structured_matrix_kernel (structured_writer.py:16-34): one workgroup per
+//   pair; per-channel vectors and their sums in LDS, then thread e walks
+//   column e of cross twice (hb and mass . hb, then the result).
+// chrono_sum_kernel (association_writer.py:35-40): fp32 sum over the fine
+//   axis in fine order.
+// feature_coeff_kernel (association_writer.py:43-53): one wave per
+//   (b, t, h); mass_p = sum_d h[d] exp(z_p[d]) by a wave reduction, then
+//   out[p][d] = bf16(mass_p / sum_p mass_p * h[d]).
+#include "tao_launch.h"
+#include "tao_common.h"
+
+namespace tao {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+TAO_DEV bf16x8 as_bf16x8(const uint4& u) {
+  bf16x8 r;
+  __builtin_memcpy(&r, &u, 16);
+  return r;
+}
+
+constexpr int kStatThreads = 512;
+constexpr int kStatTokens = 64;
+
+template <int D>
+struct StatSmem {
+  bf16_t ut[D][kStatTokens + 8];     // u^T [d][t]
+  bf16_t vt[D][kStatTokens + 8];     // v^T [e][t]
+};
+
+// mode 0: gram + cross (+ mass when p.mass); mode 1: square_mass + cross + mass.
+template <int D>
+__global__ __launch_bounds__(kStatThreads) void writer_stats_kernel(WriterStatsParams p) {
+  constexpr int DT = D / 32, KS = kStatTokens / 16, LPT = 8, CPL = D / LPT;
+  __shared__ StatSmem<D> sm;
+  const int n = blockIdx.x / p.H, h = blockIdx.x % p.H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
+  const bool structured = p.mode == 1;
+  // output tiles: gram (mode 0 only) then cross; wave w owns tiles w, w + 8, ...
+  const int n_tiles = (structured ? 1 : 2) * DT * DT;
+  constexpr int TPW = (2 * DT * DT + 7) / 8;
+  floatx16 acc[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[j][i] = 0.0f;
+  float msum = 0.0f, ssum = 0.0f;          // thread tid < D: channel tid
+  const int tk = tid / LPT, part = tid % LPT;
+  for (int t0 = 0; t0 < p.T; t0 += kStatTokens) {
+    const int t = t0 + tk;
+    float x[CPL];
+    uint32_t vw[CPL / 2];
+    if (t < p.T) {
+      const bf16_t* kr = p.k + n * p.k_s[0] + (int64_t)t * p.k_s[1] + h * p.k_s[2] + part * CPL;
+      const bf16_t* vr = p.v + n * p.v_s[0] + (int64_t)t * p.v_s[1] + h * p.v_s[2] + part * CPL;
+#pragma unroll
+      for (int c = 0; c < CPL / 8; ++c) {
+        const uint4 ku = *(const uint4*)(kr + 8 * c), vu = *(const uint4*)(vr + 8 * c);
+        const uint32_t kw[4] = {ku.x, ku.y, ku.z, ku.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          x[8 * c + 2 * j] = __uint_as_float(kw[j] << 16);
+          x[8 * c + 2 * j + 1] = __uint_as_float(kw[j] & 0xFFFF0000u);
+        }
+        vw[4 * c] = vu.x; vw[4 * c + 1] = vu.y; vw[4 * c + 2] = vu.z; vw[4 * c + 3] = vu.w;
+      }
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) mx = fmaxf(mx, x[j]);
+#pragma unroll
+      for (int off = 1; off < LPT; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) { x[j] = __expf(x[j] - mx); s += x[j]; }
+#pragma unroll
+      for (int off = 1; off < LPT; off <<= 1) s += __shfl_xor(s, off, 64);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) x[j] = rbf(x[j] / s);
+    } else {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) x[j] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL / 2; ++j) vw[j] = 0u;
+    }
+    __syncthreads();                      // previous chunk consumed
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int d = part * CPL + j;
+      sm.ut[d][tk] = f2bf(x[j]);
+      sm.vt[d][tk] = (bf16_t)((j & 1) ? (vw[j / 2] >> 16) : (vw[j / 2] & 0xFFFFu));
+    }
+    __syncthreads();
+    if (tid < D && (p.mass || structured)) {
+      const int cnt = min(kStatTokens, p.T - t0);
+      for (int i = 0; i < cnt; ++i) {
+        const float u = bf2f(sm.ut[tid][i]);
+        msum += u;
+        ssum = fmaf(u, u, ssum);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int tt = w + 8 * j;
+      if (tt < n_tiles) {
+        const bool is_cross = structured || tt >= DT * DT;
+        const int r = structured ? tt : tt % (DT * DT);
+        const int mt = r / DT, nt = r % DT;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const bf16x8 a = as_bf16x8(*(const uint4*)&sm.ut[32 * mt + li][16 * ks + 8 * hl]);
+          const bf16x8 b = is_cross
+              ? as_bf16x8(*(const uint4*)&sm.vt[32 * nt + li][16 * ks + 8 * hl])
+              : as_bf16x8(*(const uint4*)&sm.ut[32 * nt + li][16 * ks + 8 * hl]);
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+        }
+      }
+    }
+  }
+  const size_t mat = (size_t)n * p.H + h;
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int tt = w + 8 * j;
+    if (tt >= n_tiles) continue;
+    const bool is_cross = structured || tt >= DT * DT;
+    const int r = structured ? tt : tt % (DT * DT);
+    const int mt = r / DT, nt = r % DT;
+    float* out = (is_cross ? p.cross : p.gram) + mat * D * D;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = 32 * mt + 8 * (i / 4) + 4 * hl + (i % 4);
+      out[(size_t)row * D + 32 * nt + li] = acc[j][i];
+    }
+  }
+  if (tid < D) {
+    if (p.mass) p.mass[mat * D + tid] = msum;
+    if (structured) p.gram[mat * D + tid] = ssum;   // square_mass
+  }
+}
+
+constexpr int kSolveThreads = 256;
+
+template <int D>
+struct SolveSmem {
+  float a[D][D + 1];     // system, then its lower factor
+  float x[D][D + 1];     // cross, then Y, then X
+  float red[kSolveThreads / 64];
+};
+
+template <int D>
+__global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocSolveParams p) {
+  extern __shared__ __align__(16) unsigned char solve_smem[];
+  SolveSmem<D>& sm = *reinterpret_cast<SolveSmem<D>*>(solve_smem);
+  const int mat = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float* g = p.gram + (size_t)mat * D * D;
+  const float* c = p.cross + (size_t)mat * D * D;
+  // ridge = trace / D
+  float tr = 0.0f;
+  for (int i = tid; i < D; i += kSolveThreads) tr += g[(size_t)i * D + i];
+  tr = wave_sum_fold(tr);
+  if ((tid & 63) == 0) sm.red[tid >> 6] = tr;
+  __syncthreads();
+  float trace = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kSolveThreads / 64; ++i) trace += sm.red[i];
+  const float ridge = trace / (float)D;
+  for (int i = tid; i < D * D; i += kSolveThreads) {
+    const int r = i / D, col = i % D;
+    sm.a[r][col] = g[i] + (r == col ? ridge : 0.0f);
+    sm.x[r][col] = c[i];
+  }
+  int bad = 0;
+  for (int j = 0; j < D; ++j) {
+    __syncthreads();
+    const float piv = sm.a[j][j];
+    if (!(piv > 0.0f)) bad = bad ? bad : j + 1;     // not positive (or NaN)
+    const float dj = __builtin_sqrtf(piv);
+    __syncthreads();                                // every thread read the pivot
+    for (int i = j + 1 + tid; i < D; i += kSolveThreads) sm.a[i][j] = sm.a[i][j] / dj;
+    if (tid == 0) sm.a[j][j] = dj;
+    __syncthreads();
+    const int R = D - j - 1;
+    for (int idx = tid; idx < R * R; idx += kSolveThreads) {
+      const int i = j + 1 + idx / R, k = j + 1 + idx % R;
+      if (k <= i) sm.a[i][k] = fmaf(-sm.a[i][j], sm.a[k][j], sm.a[i][k]);
+    }
+  }
+  __syncthreads();
+  if (p.info && tid == 0) p.info[mat] = bad;
+  // forward then back substitution, thread per column e
+  for (int e = tid; e < D; e += kSolveThreads) {
+    for (int i = 0; i < D; ++i) {
+      float s = sm.x[i][e];
+      for (int k = 0; k < i; ++k) s = fmaf(-sm.a[i][k], sm.x[k][e], s);
+      sm.x[i][e] = s / sm.a[i][i];
+    }
+    for (int i = D - 1; i >= 0; --i) {
+      float s = sm.x[i][e];
+      for (int k = i + 1; k < D; ++k) s = fmaf(-sm.a[k][i], sm.x[k][e], s);
+      sm.x[i][e] = s / sm.a[i][i];
+    }
+  }
+  __syncthreads();
+  bf16_t* out = p.out + (size_t)mat * D * D;
+  for (int i = tid; i < D * D; i += kSolveThreads) out[i] = f2bf(sm.x[i / D][i % D]);
+}
+
+template <int D>
+__global__ __launch_bounds__(D) void structured_matrix_kernel(StructuredParams p) {
+  __shared__ float diag[D], tv[D], mv[D], hmv[D], red[4][D / 64 > 0 ? D / 64 : 1];
+  const int mat = blockIdx.x, d = threadIdx.x;
+  const float count = p.count;
+  const float sq = p.square[(size_t)mat * D + d];
+  const float ms = p.mass[(size_t)mat * D + d];
+  const float variance = fmaxf(sq - ms * ms / count, 0.0f);
+  // four block sums: variance, square_mass, then (after the ridge) the
+  // positive sum and t . mass
+  auto block_sum = [&](float v, int slot) __attribute__((always_inline)) {
+    v = wave_sum_fold(v);
+    if ((d & 63) == 0) red[slot][d >> 6] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) s += red[slot][i];
+    return s;
+  };
+  const float variance_sum = block_sum(variance, 0);
+  const float ridge = block_sum(sq, 1) / (float)D;
+  const float diagonal = variance + ridge;
+  const bool zero = variance_sum == 0.0f;
+  const float t = zero ? 0.0f : variance / diagonal;
+  const float positive_sum = block_sum(variance * ridge / diagonal, 2);
+  const float safe_sum = zero ? 1.0f : positive_sum;
+  const float tmass = block_sum(t * ms, 3);
+  const float hm = ms / diagonal + t * tmass / safe_sum;
+  diag[d] = diagonal; tv[d] = t; mv[d] = ms; hmv[d] = hm;
+  __syncthreads();
+  float mhm = 0.0f;
+  for (int i = 0; i < D; ++i) mhm = fmaf(mv[i], hmv[i], mhm);
+  const float denominator = count + mhm;
+  // thread e: column e of cross
+  const int e = d;
+  const float* cr = p.cross + (size_t)mat * D * D;
+  float t_cross = 0.0f;
+  for (int i = 0; i < D; ++i) t_cross = fmaf(tv[i], cr[(size_t)i * D + e], t_cross);
+  float mass_hb = 0.0f;
+  for (int i = 0; i < D; ++i) {
+    const float hb = cr[(size_t)i * D + e] / diag[i] + tv[i] * t_cross / safe_sum;
+    mass_hb = fmaf(mv[i], hb, mass_hb);
+  }
+  bf16_t* out = p.out + (size_t)mat * D * D;
+  for (int i = 0; i < D; ++i) {
+    const float hb = cr[(size_t)i * D + e] / diag[i] + tv[i] * t_cross / safe_sum;
+    out[(size_t)i * D + e] = f2bf(hb - hmv[i] * mass_hb / denominator);
+  }
+}
+
+__global__ __launch_bounds__(256) void chrono_sum_kernel(const float* x, float* out, int64_t outer,
+                                                          int fines, int64_t inner) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= outer * inner) return;
+  const int64_t o = i / inner, r = i % inner;
+  const float* base = x + o * fines * inner + r;
+  float s = base[0];
+  for (int f = 1; f < fines; ++f) s += base[(int64_t)f * inner];
+  out[i] = s;
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void feature_coeff_kernel(FeatureCoeffParams p) {
+  constexpr int PL = D / 64;             // channels per lane
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= p.B * p.T * p.H) return;   // wave-uniform
+  const int h = row % p.H, t = (row / p.H) % p.T, b = row / (p.H * p.T);
+  const bf16_t* hr = p.h + b * p.h_s[0] + (int64_t)t * p.h_s[1] + h * p.h_s[2];
+  const bf16_t* zr = p.z + b * p.z_s[0] + (int64_t)t * p.z_s[1] + h * p.z_s[2];
+  float hv[PL];
+#pragma unroll
+  for (int j = 0; j < PL; ++j) hv[j] = bf2f(hr[lane + 64 * j]);
+  auto mass_of = [&](int pg) __attribute__((always_inline)) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) s = fmaf(hv[j], __expf(bf2f(zr[pg * p.z_s[3] + lane + 64 * j])), s);
+    return wave_sum_fold(s);
+  };
+  float total = 0.0f;
+  for (int pg = 0; pg < p.P; ++pg) total += mass_of(pg);
+  bf16_t* out = p.out + (size_t)row * p.P * D;
+  for (int pg = 0; pg < p.P; ++pg) {
+    const float mix = mass_of(pg) / total;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) out[(size_t)pg * D + lane + 64 * j] = f2bf(mix * hv[j]);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_writer_stats(const WriterStatsParams& p, int head_dim, hipStream_t s) {
+  const dim3 grid((unsigned)(p.N * p.H));
+  if (head_dim == 128)
+    hipLaunchKernelGGL(writer_stats_kernel<128>, grid, dim3(kStatThreads), 0, s, p);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL(writer_stats_kernel<64>, grid, dim3(kStatThreads), 0, s, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_association_solve(const AssocSolveParams& p, int head_dim, hipStream_t s) {
+  if (p.count <= 0) return hipSuccess;
+  if (head_dim == 128) {
+    constexpr size_t bytes = sizeof(SolveSmem<128>);
+    static bool attr = false;
+    if (!attr) {
+      const hipError_t e = hipFuncSetAttribute((const void*)association_solve_kernel<128>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)bytes);
+      if (e != hipSuccess) return e;
+      attr = true;
+    }
+    hipLaunchKernelGGL(association_solve_kernel<128>, dim3((unsigned)p.count),
+                       dim3(kSolveThreads), bytes, s, p);
+  } else if (head_dim == 64) {
+    hipLaunchKernelGGL(association_solve_kernel<64>, dim3((unsigned)p.count),
+                       dim3(kSolveThreads), sizeof(SolveSmem<64>), s, p);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_structured_matrix(const StructuredParams& p, int head_dim, hipStream_t s) {
+  if (p.count_mats <= 0) return hipSuccess;
+  if (head_dim == 128)
+    hipLaunchKernelGGL(structured_matrix_kernel<128>, dim3((unsigned)p.count_mats), dim3(128), 0, s, p);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL(structured_matrix_kernel<64>, dim3((unsigned)p.count_mats), dim3(64), 0, s, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_chrono_sum(const float* x, float* out, int64_t outer, int fines, int64_t inner,
+                             hipStream_t s) {
+  const int64_t n = outer * inner;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(chrono_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, out,
+                     outer, fines, inner);
+  return hipGetLastError();
+}
+
+hipError_t launch_feature_coeff(const FeatureCoeffParams& p, int head_dim, hipStream_t s) {
+  const int64_t rows = (int64_t)p.B * p.T * p.H;
+  if (rows <= 0 || p.P <= 0) return hipSuccess;
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (head_dim == 128)
+    hipLaunchKernelGGL(feature_coeff_kernel<128>, grid, dim3(256), 0, s, p);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL(feature_coeff_kernel<64>, grid, dim3(256), 0, s, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace tao

@@ -1,0 +1,414 @@
+// Channel-given selected contraction on gfx950 (the numerator-only read of
+// the feature-mass writers, indirect_fine.py:65-133 and its backward
+// :101-120, :172-227):
+//   out[b, q, h, e]  = bf16(sum_m sum_d channel[b, q, h, m, d] C[id_m][d][e])
+//   d channel[.., m, d] = bf16(sum_e grad[b, q, h, e] C[id_m][d][e])
+//   d C[bb, h, s]    = bf16(sum over b % BB == bb of bf16(sum over the pairs
+//                      (q, m) of batch b with id_m == s of channel^T grad))
+// C rows d, columns e; batch b reads bank b % BB.
+//
+// The reference sorts every (query, slot) pair by fine id and runs one C tile
+// per fine against 32 pairs at a time, then sums the pairs of a query. Here a
+// workgroup owns a tile of queries of one (b, h) instead: the union of the
+// tile's selected ids (an LDS bitmask, ascending) is walked once, each fine's
+// C is staged in LDS once and every wave builds its MFMA A operand from the
+// channel rows of the queries that selected that fine (zero rows elsewhere),
+// so the numerator accumulates in one v_mfma_f32_32x32x16_bf16 accumulator
+// per (32 queries, 32 columns) and no pair buffer or sort is needed. A query
+// that lists one fine twice is handled exactly by one pass per occurrence.
+// The fp32 sum runs in fine order inside the MFMA instead of slot order, a
+// difference at fp32 rounding before the final bf16 cast.
+#include "tao_launch.h"
+#include "tao_common.h"
+
+namespace tao {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+TAO_DEV bf16x8 as_bf16x8(const uint4& u) {
+  bf16x8 r;
+  __builtin_memcpy(&r, &u, 16);
+  return r;
+}
+
+constexpr int kSelThreads = 256;
+constexpr int kSelMaxM = 64;
+constexpr int kSelMaxS = 4096;
+constexpr int kSelWords = kSelMaxS / 32;
+
+template <int D> constexpr int kSelQG = 128 / D;          // 32-query groups per tile
+template <int D> constexpr int kSelTileQ = 32 * kSelQG<D>;
+
+template <int D>
+struct SelSmem {
+  bf16_t c[D][D + 8];                     // staged C^T (forward) or C (grad of channel)
+  int16_t sid[kSelTileQ<D>][kSelMaxM];    // the tile's selected ids
+  int8_t occ[kSelTileQ<D>][kSelMaxM];     // occurrence index of sid[q][m] in its row
+  uint32_t bits[kSelWords];
+  int pre[kSelWords];
+  int uni[kSelTileQ<D> * kSelMaxM];
+  int n_union, passes;
+  bf16_t stage[4][32][40];                // grad-of-channel rows per wave (32 q x 32 d)
+};
+
+// Shared setup: ids of the tile into LDS, occurrence indices, the union
+// (ascending) and the number of passes (largest occurrence count).
+template <int D>
+TAO_DEV void tile_union(SelSmem<D>& sm, const SelectedParams& p, int b, int h, int q0, int nq,
+                        int tid) {
+  for (int i = tid; i < kSelWords; i += kSelThreads) sm.bits[i] = 0u;
+  if (tid == 0) sm.passes = 0;
+  __syncthreads();
+  for (int i = tid; i < nq * p.M; i += kSelThreads) {
+    const int q = i / p.M, m = i % p.M;
+    const int64_t id64 = p.ids[(((size_t)b * p.Q + q0 + q) * p.H + h) * p.M + m];
+    const bool ok = id64 >= 0 && id64 < p.S;        // an id outside the bank reads nothing
+    const int id = ok ? (int)id64 : -1;
+    sm.sid[q][m] = (int16_t)id;
+    if (ok) atomicOr(&sm.bits[id >> 5], 1u << (id & 31));
+  }
+  __syncthreads();
+  for (int i = tid; i < nq * p.M; i += kSelThreads) {
+    const int q = i / p.M, m = i % p.M;
+    const int id = sm.sid[q][m];
+    int o = 0;
+    for (int j = 0; j < m; ++j) o += sm.sid[q][j] == id;
+    sm.occ[q][m] = (int8_t)o;
+    if (o) atomicMax(&sm.passes, o);
+  }
+  if (tid < 64) {
+    constexpr int WPL = kSelWords / 64;
+    int cnt[WPL], total = 0;
+#pragma unroll
+    for (int i = 0; i < WPL; ++i) { cnt[i] = __popc(sm.bits[tid * WPL + i]); total += cnt[i]; }
+    int incl = total;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int v = __shfl_up(incl, off, 64);
+      if (tid >= off) incl += v;
+    }
+    int run = incl - total;
+#pragma unroll
+    for (int i = 0; i < WPL; ++i) { sm.pre[tid * WPL + i] = run; run += cnt[i]; }
+    if (tid == 63) sm.n_union = incl;
+  }
+  __syncthreads();
+  for (int i = tid; i < kSelWords; i += kSelThreads) {
+    uint32_t bits = sm.bits[i];
+    int r = sm.pre[i];
+    while (bits) {
+      sm.uni[r++] = i * 32 + __ffs(bits) - 1;
+      bits &= bits - 1;
+    }
+  }
+  __syncthreads();
+}
+
+// Slot of fine f (occurrence r) in query row q, or -1.
+template <int D>
+TAO_DEV int find_slot(const SelSmem<D>& sm, int q, int M, int f, int r) {
+  for (int m = 0; m < M; ++m)
+    if (sm.sid[q][m] == f && sm.occ[q][m] == r) return m;
+  return -1;
+}
+
+template <int D>
+__global__ __launch_bounds__(kSelThreads) void selected_fwd_kernel(SelectedParams p) {
+  constexpr int KK = D / 16, ET = D / 32, TQ = kSelTileQ<D>;
+  constexpr int CJ = D * D / 8 / kSelThreads;            // uint4 of C per thread
+  __shared__ SelSmem<D> sm;
+  const int n_tiles = (p.Q + TQ - 1) / TQ;
+  const int tile = blockIdx.x % n_tiles, bh = blockIdx.x / n_tiles;
+  const int b = bh / p.H, h = bh % p.H;
+  const int q0 = tile * TQ, nq = min(TQ, p.Q - q0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
+  const int qg = w / ET, et = w % ET;
+  tile_union<D>(sm, p, b, h, q0, nq, tid);
+  const int U = sm.n_union, R = sm.passes + 1;
+  const int ql = 32 * qg + li;                            // the lane's query row in the tile
+  const bool qok = ql < nq;
+  const bf16_t* bank = p.bank + ((size_t)(b % p.BB) * p.H + h) * p.S * D * D;
+  floatx16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+  for (int u = 0; u < U; ++u) {
+    const int f = sm.uni[u];
+    // stage C^T[e][d] of fine f: thread moves 8 consecutive e of one row d
+    uint4 cv[CJ];
+#pragma unroll
+    for (int j = 0; j < CJ; ++j)
+      cv[j] = *(const uint4*)(bank + (size_t)f * D * D + (size_t)(tid + j * kSelThreads) * 8);
+    __syncthreads();                                     // previous fine consumed
+#pragma unroll
+    for (int j = 0; j < CJ; ++j) {
+      const int idx = (tid + j * kSelThreads) * 8;
+      const int d = idx / D, e0 = idx % D;
+      const uint32_t wv[4] = {cv[j].x, cv[j].y, cv[j].z, cv[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sm.c[e0 + 2 * i][d] = (bf16_t)(wv[i] & 0xFFFFu);
+        sm.c[e0 + 2 * i + 1][d] = (bf16_t)(wv[i] >> 16);
+      }
+    }
+    __syncthreads();
+    for (int r = 0; r < R; ++r) {
+      const int m = qok ? find_slot<D>(sm, ql, p.M, f, r) : -1;
+      const bf16_t* crow = p.channel +
+          ((((size_t)b * p.Q + q0 + ql) * p.H + h) * p.M + (m < 0 ? 0 : m)) * D;
+      if (!__any(m >= 0)) continue;                      // wave-uniform
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const uint4 a = m >= 0 ? *(const uint4*)(crow + 16 * kk + 8 * hl) : make_uint4(0, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            as_bf16x8(a), as_bf16x8(*(const uint4*)&sm.c[32 * et + li][16 * kk + 8 * hl]), acc,
+            0, 0, 0);
+      }
+    }
+  }
+  // rows q = 32 qg + 8 (i / 4) + 4 hl + i % 4, column e = 32 et + li
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int q = 32 * qg + 8 * (i / 4) + 4 * hl + (i % 4);
+    if (q < nq) p.out[(((size_t)b * p.Q + q0 + q) * p.H + h) * D + 32 * et + li] = f2bf(acc[i]);
+  }
+}
+
+// d channel: A = the tile's grad rows (loaded once), B = rows of C (k = e).
+template <int D>
+__global__ __launch_bounds__(kSelThreads) void selected_bwd_a_kernel(SelectedParams p) {
+  constexpr int KK = D / 16, ET = D / 32, TQ = kSelTileQ<D>;
+  constexpr int CJ = D * D / 8 / kSelThreads;
+  __shared__ SelSmem<D> sm;
+  const int n_tiles = (p.Q + TQ - 1) / TQ;
+  const int tile = blockIdx.x % n_tiles, bh = blockIdx.x / n_tiles;
+  const int b = bh / p.H, h = bh % p.H;
+  const int q0 = tile * TQ, nq = min(TQ, p.Q - q0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
+  const int qg = w / ET, dt = w % ET;
+  tile_union<D>(sm, p, b, h, q0, nq, tid);
+  const int U = sm.n_union, R = sm.passes + 1;
+  const int ql = 32 * qg + li;
+  const bool qok = ql < nq;
+  const bf16_t* bank = p.bank + ((size_t)(b % p.BB) * p.H + h) * p.S * D * D;
+  uint4 ga[KK];
+  {
+    const bf16_t* grow = p.grad + (((size_t)b * p.Q + q0 + (qok ? ql : 0)) * p.H + h) * D;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      ga[kk] = qok ? *(const uint4*)(grow + 16 * kk + 8 * hl) : make_uint4(0, 0, 0, 0);
+  }
+  // slots whose id lies outside the bank read nothing: zero gradient
+  if (qok)
+    for (int m = 0; m < p.M; ++m)
+      if (sm.sid[ql][m] < 0) {
+        bf16_t* dst = p.grad_channel +
+            ((((size_t)b * p.Q + q0 + ql) * p.H + h) * p.M + m) * D + 32 * dt + 16 * hl;
+        *(uint4*)dst = make_uint4(0, 0, 0, 0);
+        *(uint4*)(dst + 8) = make_uint4(0, 0, 0, 0);
+      }
+  for (int u = 0; u < U; ++u) {
+    const int f = sm.uni[u];
+    uint32_t cw[CJ][4];
+#pragma unroll
+    for (int j = 0; j < CJ; ++j) {
+      const uint4 v = *(const uint4*)(bank + (size_t)f * D * D + (size_t)(tid + j * kSelThreads) * 8);
+      cw[j][0] = v.x; cw[j][1] = v.y; cw[j][2] = v.z; cw[j][3] = v.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < CJ; ++j) {
+      const int idx = (tid + j * kSelThreads) * 8;
+      *(uint4*)&sm.c[idx / D][idx % D] = make_uint4(cw[j][0], cw[j][1], cw[j][2], cw[j][3]);
+    }
+    __syncthreads();
+    floatx16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          as_bf16x8(ga[kk]), as_bf16x8(*(const uint4*)&sm.c[32 * dt + li][16 * kk + 8 * hl]), acc,
+          0, 0, 0);
+    // through the wave's LDS stage: row q = li, 16 columns per half-wave
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sm.stage[w][8 * (i / 4) + 4 * hl + (i % 4)][li] = f2bf(acc[i]);
+    __syncthreads();
+    if (qok) {
+      const uint4 lo = *(const uint4*)&sm.stage[w][li][16 * hl];
+      const uint4 hi = *(const uint4*)&sm.stage[w][li][16 * hl + 8];
+      for (int r = 0; r < R; ++r) {
+        const int m = find_slot<D>(sm, ql, p.M, f, r);
+        if (m < 0) continue;
+        bf16_t* dst = p.grad_channel +
+            ((((size_t)b * p.Q + q0 + ql) * p.H + h) * p.M + m) * D + 32 * dt + 16 * hl;
+        *(uint4*)dst = lo;
+        *(uint4*)(dst + 8) = hi;
+      }
+    }
+  }
+}
+
+// d C: one workgroup per (bank batch bb, head, NF consecutive fines); for each
+// batch b = bb, bb + BB, ... the pairs of b are reduced in fp32 (k = query,
+// 32 at a time, channel^T and grad^T staged transposed), rounded to bf16 and
+// added to the running total.
+template <int D> constexpr int kSelNF = D == 64 ? 4 : 1;
+
+template <int D>
+__global__ __launch_bounds__(kSelThreads) void selected_bwd_c_kernel(SelectedParams p) {
+  constexpr int NF = kSelNF<D>, DT = D / 32, NT = NF * DT * DT, TPW = NT / 4;
+  __shared__ bf16_t cht[NF][D][40], gt[D][40];
+  __shared__ uint64_t match[NF][32];
+  __shared__ int any_sel[NF];
+  const int groups = (p.S + NF - 1) / NF;
+  const int g = blockIdx.x % groups, bbh = blockIdx.x / groups;
+  const int bb = bbh / p.H, h = bbh % p.H;
+  const int f0 = g * NF;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
+  floatx16 acc[TPW], total[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { acc[j][i] = 0.0f; total[j][i] = 0.0f; }
+  for (int b = bb; b < p.B; b += p.BB) {
+    for (int qb = 0; qb < p.Q; qb += 32) {
+      __syncthreads();
+      if (tid < NF) any_sel[tid] = 0;
+      if (tid < 32) {
+        uint64_t mk[NF];
+#pragma unroll
+        for (int k = 0; k < NF; ++k) mk[k] = 0;
+        if (qb + tid < p.Q) {
+          const int64_t* ids = p.ids + (((size_t)b * p.Q + qb + tid) * p.H + h) * p.M;
+          for (int m = 0; m < p.M; ++m) {
+            const int64_t k = ids[m] - f0;
+#pragma unroll
+            for (int kk = 0; kk < NF; ++kk)
+              if (k == kk) mk[kk] |= 1ull << m;
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < NF; ++k) match[k][tid] = mk[k];
+      }
+      __syncthreads();
+      // thread = (query qi, 8-channel chunk c)
+      for (int job = tid; job < 32 * (D / 8); job += kSelThreads) {
+        const int qi = job % 32, c = job / 32;
+        const int q = qb + qi;
+        const bool qok = q < p.Q;
+        const size_t row = ((size_t)b * p.Q + (qok ? q : 0)) * p.H + h;
+        const uint4 gv = qok ? *(const uint4*)(p.grad + row * D + 8 * c) : make_uint4(0, 0, 0, 0);
+        const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          gt[8 * c + 2 * j][qi] = (bf16_t)(gw[j] & 0xFFFFu);
+          gt[8 * c + 2 * j + 1][qi] = (bf16_t)(gw[j] >> 16);
+        }
+#pragma unroll
+        for (int k = 0; k < NF; ++k) {
+          uint64_t mk = match[k][qi];
+          float sv[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) sv[j] = 0.0f;
+          if (mk && c == 0) any_sel[k] = 1;
+          while (mk) {
+            const int m = __builtin_ctzll(mk);
+            mk &= mk - 1;
+            const uint4 cvv = *(const uint4*)(p.channel + (row * p.M + m) * D + 8 * c);
+            const uint32_t cw[4] = {cvv.x, cvv.y, cvv.z, cvv.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              sv[2 * j] += __uint_as_float(cw[j] << 16);
+              sv[2 * j + 1] += __uint_as_float(cw[j] & 0xFFFF0000u);
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j) cht[k][8 * c + j][qi] = f2bf(sv[j]);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        const int tt = w + 4 * j;
+        const int k = tt / (DT * DT), r = tt % (DT * DT);
+        const int mt = r / DT, nt = r % DT;
+        if (!any_sel[k]) continue;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              as_bf16x8(*(const uint4*)&cht[k][32 * mt + li][16 * ks + 8 * hl]),
+              as_bf16x8(*(const uint4*)&gt[32 * nt + li][16 * ks + 8 * hl]), acc[j], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        total[j][i] += rbf(acc[j][i]);
+        acc[j][i] = 0.0f;
+      }
+  }
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int tt = w + 4 * j;
+    const int k = tt / (DT * DT), r = tt % (DT * DT);
+    const int mt = r / DT, nt = r % DT;
+    const int f = f0 + k;
+    if (f >= p.S) continue;
+    bf16_t* out = p.grad_bank + (((size_t)bb * p.H + h) * p.S + f) * D * D;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = 32 * mt + 8 * (i / 4) + 4 * hl + (i % 4);
+      out[(size_t)d * D + 32 * nt + li] = f2bf(total[j][i]);
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_selected_numerator(const SelectedParams& p, int head_dim, hipStream_t s) {
+  if (p.M > kSelMaxM || p.S > kSelMaxS || p.S > 32767) return hipErrorInvalidValue;
+  if (p.B * p.Q * p.H == 0) return hipSuccess;
+#define TAO_SEL_FWD(D_)                                                                       \
+  hipLaunchKernelGGL(selected_fwd_kernel<D_>,                                                 \
+                     dim3((unsigned)(((p.Q + kSelTileQ<D_> - 1) / kSelTileQ<D_>) * p.B * p.H)), \
+                     dim3(kSelThreads), 0, s, p)
+  if (head_dim == 128)
+    TAO_SEL_FWD(128);
+  else if (head_dim == 64)
+    TAO_SEL_FWD(64);
+  else
+    return hipErrorInvalidValue;
+#undef TAO_SEL_FWD
+  return hipGetLastError();
+}
+
+hipError_t launch_selected_numerator_bwd(const SelectedParams& p, int head_dim, hipStream_t s) {
+  if (p.M > kSelMaxM || p.S > kSelMaxS || p.S > 32767) return hipErrorInvalidValue;
+  if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
+#define TAO_SEL_BWD(D_)                                                                         \
+  do {                                                                                          \
+    if (p.grad_channel && p.B * p.Q * p.H > 0)                                                  \
+      hipLaunchKernelGGL(selected_bwd_a_kernel<D_>,                                             \
+                         dim3((unsigned)(((p.Q + kSelTileQ<D_> - 1) / kSelTileQ<D_>) * p.B *    \
+                                         p.H)),                                                 \
+                         dim3(kSelThreads), 0, s, p);                                           \
+    if (p.grad_bank && p.BB * p.H * p.S > 0)                                                    \
+      hipLaunchKernelGGL(selected_bwd_c_kernel<D_>,                                             \
+                         dim3((unsigned)(((p.S + kSelNF<D_> - 1) / kSelNF<D_>) * p.BB * p.H)),  \
+                         dim3(kSelThreads), 0, s, p);                                           \
+  } while (0)
+  if (head_dim == 128)
+    TAO_SEL_BWD(128);
+  else
+    TAO_SEL_BWD(64);
+#undef TAO_SEL_BWD
+  return hipGetLastError();
+}
+
+}  // namespace tao

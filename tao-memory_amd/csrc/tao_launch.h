@@ -315,6 +315,62 @@ struct MemBwdParams {
 };
 hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s);
 
+// ---- non-preset fine writers and the channel-given selected read
+
+// Simplex-feature statistics of N token blocks: k, v [N, T, H, D] bf16 with
+// element strides (block, token, head). mode 0: gram, cross (+ mass if set);
+// mode 1: gram receives square_mass [N, H, D], plus cross and mass.
+struct WriterStatsParams {
+  const bf16_t* k; const bf16_t* v;
+  int64_t k_s[3], v_s[3];
+  int N, T, H, mode;
+  float* gram; float* cross; float* mass;
+};
+hipError_t launch_writer_stats(const WriterStatsParams& p, int head_dim, hipStream_t s);
+
+struct AssocSolveParams {
+  const float* gram; const float* cross;
+  int count;
+  bf16_t* out;            // [count, D, D] rows d, columns e
+  int32_t* info;          // nullable [count]
+};
+hipError_t launch_association_solve(const AssocSolveParams& p, int head_dim, hipStream_t s);
+
+struct StructuredParams {
+  const float* square; const float* cross; const float* mass;
+  int count_mats;
+  float count;            // token count behind the statistics
+  bf16_t* out;
+};
+hipError_t launch_structured_matrix(const StructuredParams& p, int head_dim, hipStream_t s);
+
+hipError_t launch_chrono_sum(const float* x, float* out, int64_t outer, int fines, int64_t inner,
+                             hipStream_t s);
+
+// h [B, T, H, D] (strides h_s), read_z element strides z_s (b, t, h, page),
+// zero for broadcast axes; out bf16 [B, T, H, P, D] contiguous.
+struct FeatureCoeffParams {
+  const bf16_t* h; const bf16_t* z;
+  int64_t h_s[3], z_s[4];
+  int B, T, H, P;
+  bf16_t* out;
+};
+hipError_t launch_feature_coeff(const FeatureCoeffParams& p, int head_dim, hipStream_t s);
+
+// Channel-given selected contraction: channel [B, Q, H, M, D] bf16, ids
+// [B, Q, H, M] int64, bank [BB, H, S, D, D] bf16 (C rows d, columns e; batch b
+// reads bank b % BB), all contiguous.
+struct SelectedParams {
+  const bf16_t* channel; const int64_t* ids; const bf16_t* bank;
+  int B, Q, H, M, BB, S;
+  bf16_t* out;            // forward: [B, Q, H, D]
+  const bf16_t* grad;     // backward: [B, Q, H, D]
+  bf16_t* grad_channel;   // [B, Q, H, M, D] (nullable)
+  bf16_t* grad_bank;      // [BB, H, S, D, D] (nullable)
+};
+hipError_t launch_selected_numerator(const SelectedParams& p, int head_dim, hipStream_t s);
+hipError_t launch_selected_numerator_bwd(const SelectedParams& p, int head_dim, hipStream_t s);
+
 
 
 }  // namespace tao

@@ -127,6 +127,17 @@ _SIGNATURES = {
     "tao_batch_decode": ([_vp, ctypes.POINTER(Tokens), ctypes.POINTER(Fusion), _vp,
                           ctypes.POINTER(_i64), _vp, ctypes.POINTER(_i64)], _i32),
     "tao_batch_close": ([_vp], _i32),
+    "tao_writer_statistics": ([_vp, ctypes.POINTER(_i64), _vp, ctypes.POINTER(_i64), _i32, _i32,
+                               _i32, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
+    "tao_association_matrix": ([_vp, _vp, _i32, _i32, _vp, _vp, _vp], _i32),
+    "tao_structured_matrix": ([_vp, _vp, _vp, _i32, _i32, ctypes.c_float, _vp, _vp], _i32),
+    "tao_chronological_sum": ([_vp, _i64, _i32, _i64, _vp, _vp], _i32),
+    "tao_feature_read_coefficients": ([_vp, ctypes.POINTER(_i64), _vp, ctypes.POINTER(_i64),
+                                       _i32, _i32, _i32, _i32, _i32, _vp, _vp], _i32),
+    "tao_selected_numerator": ([_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp,
+                                _vp], _i32),
+    "tao_selected_numerator_backward": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
+                                         _i32, _vp, _vp, _vp], _i32),
 }
 
 EXPORTED = tuple(_SIGNATURES)

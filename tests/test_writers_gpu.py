@@ -1,0 +1,169 @@
+"""Non-preset writers and the channel-given selected read on the GPU against
+the CPU oracle (oracle/writers.py), through the package mirrors of the
+reference modules (association_writer, structured_writer, indirect_fine),
+which call the C ABI.
+
+Bar: statistics within fp32 summation-order differences plus the rare bf16
+flip of a feature value u (tolerances written per check); matrices and read
+outputs within 2e-2 (bf16); the chronological sum bit-exact.
+"""
+import pytest
+import torch
+
+from oracle import writers as W
+from tao_attention.association_writer import (association_matrix, association_statistics,
+                                               chronological_sum, feature_read_coefficients)
+from tao_attention.indirect_fine import selected_fine_numerator
+from tao_attention.structured_writer import structured_matrix, structured_statistics
+
+pytestmark = pytest.mark.gpu
+BF16 = torch.bfloat16
+
+
+def kv(n, t, h, d, seed):
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn(n, t, h, d, generator=g) * 2).to(BF16)
+    v = torch.randn(n, t, h, d, generator=g).to(BF16)
+    return k, v
+
+
+def close(got, want, rel):
+    """|got - want| <= rel * max|want| elementwise."""
+    got, want = got.double().cpu(), want.double().cpu()
+    scale = want.abs().max().item() or 1.0
+    err = (got - want).abs().max().item()
+    assert err <= rel * scale, (err, scale)
+
+
+@pytest.mark.parametrize("d,t", [(64, 256), (128, 256), (64, 100)])
+def test_association_statistics(device, d, t):
+    k, v = kv(3, t, 2, d, 11)
+    gram, cross, mass = association_statistics(k.to(device), v.to(device), with_mass=True)
+    wg, wc, wm = W.association_statistics(k, v, with_mass=True)
+    assert gram.shape == (3, 2, d, d) and mass.shape == (3, 2, d)
+    close(gram, wg, 2e-3)
+    close(cross, wc, 2e-3)
+    close(mass, wm, 2e-3)
+    g2, c2 = association_statistics(k.to(device), v.to(device))
+    assert torch.equal(g2, gram) and torch.equal(c2, cross)
+
+
+def test_statistics_strided_inputs(device):
+    """Token blocks cut from a longer [B, T, H, D] stream by a view (the
+    reference's seal reshapes k[:, :S*256] into blocks)."""
+    k, v = kv(1, 1024, 3, 64, 12)
+    kd, vd = k.to(device), v.to(device)
+    blocks_k = kd[:, :768].reshape(3, 256, 3, 64)
+    blocks_v = vd[:, :768].reshape(3, 256, 3, 64)
+    gram, cross = association_statistics(blocks_k[:, :, 1:], blocks_v[:, :, 1:])
+    wg, wc = W.association_statistics(k[:, :768].reshape(3, 256, 3, 64)[:, :, 1:],
+                                      v[:, :768].reshape(3, 256, 3, 64)[:, :, 1:])
+    close(gram, wg, 2e-3)
+    close(cross, wc, 2e-3)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_association_matrix(device, d):
+    k, v = kv(4, 256, 2, d, 13)
+    gram, cross = association_statistics(k.to(device), v.to(device))
+    c = association_matrix(gram, cross)
+    _, want = W.association_matrix(gram.cpu().double(), cross.cpu().double())
+    assert c.dtype == BF16 and c.shape == gram.shape
+    close(c, want, 2e-2)
+    torch.testing.assert_close(c.double().cpu(), want.double(), atol=2e-2, rtol=2e-2)
+    # the unchecked solve is the same arithmetic
+    assert torch.equal(association_matrix(gram, cross, unchecked=True), c)
+
+
+def test_association_matrix_checked_mode_raises(device):
+    gram = -torch.eye(64, device=device).expand(2, 64, 64).contiguous()
+    cross = torch.ones(2, 64, 64, device=device)
+    with pytest.raises(torch.linalg.LinAlgError):
+        association_matrix(gram, cross)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_structured_writer(device, d):
+    k, v = kv(3, 256, 2, d, 14)
+    square, cross, mass = structured_statistics(k.to(device), v.to(device))
+    ws, wc, wm = W.structured_statistics(k, v)
+    close(square, ws, 2e-3)
+    close(cross, wc, 2e-3)
+    close(mass, wm, 2e-3)
+    c = structured_matrix(square, cross, mass, 256)
+    _, want = W.structured_matrix(square.cpu(), cross.cpu(), mass.cpu(), 256)
+    torch.testing.assert_close(c.double().cpu(), want.double(), atol=2e-2, rtol=2e-2)
+    # page statistics: eight fines' statistics summed in order equal the
+    # statistics of the 2048-token page (fp32 order), and give its matrix
+    kp, vp = kv(8, 256, 2, d, 15)
+    sq8, cr8, ms8 = structured_statistics(kp.to(device), vp.to(device))
+    page_sq = chronological_sum(sq8)                          # [8, H, D]: fine axis -3
+    page_ms = chronological_sum(ms8)
+    page_cr = chronological_sum(cr8.transpose(0, 1))          # [H, 8, D, D]
+    wsq, wcr, wms = W.structured_statistics(kp.reshape(1, 2048, 2, d), vp.reshape(1, 2048, 2, d))
+    close(page_sq, wsq[0], 2e-3)
+    close(page_cr, wcr[0], 2e-3)
+    close(page_ms, wms[0], 2e-3)
+    page = structured_matrix(page_sq, page_cr, page_ms, 2048)
+    _, want_page = W.structured_matrix(page_sq.cpu(), page_cr.cpu(), page_ms.cpu(), 2048)
+    torch.testing.assert_close(page.double().cpu(), want_page.double(), atol=2e-2, rtol=2e-2)
+
+
+def test_chronological_sum_exact(device):
+    g = torch.Generator().manual_seed(15)
+    x = torch.randn(2, 3, 9, 64, 64, generator=g).to(device)
+    got = chronological_sum(x)
+    want = x[:, :, 0].clone()
+    for i in range(1, 9):
+        want = want + x[:, :, i]
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_feature_read_coefficients(device, d):
+    g = torch.Generator().manual_seed(16)
+    h = torch.softmax(torch.randn(2, 7, 3, d, generator=g), -1).to(BF16)
+    z = (torch.randn(2, 7, 3, 5, d, generator=g) - 5).to(BF16)
+    got = feature_read_coefficients(h.to(device), z.to(device))
+    want = W.feature_read_coefficients(h, z)
+    torch.testing.assert_close(got.double().cpu(), want.double(), atol=1e-5, rtol=1.6e-2)
+    zb = z[:, :1]                                        # broadcast over tokens
+    got_b = feature_read_coefficients(h.to(device), zb.to(device))
+    torch.testing.assert_close(got_b.double().cpu(),
+                               W.feature_read_coefficients(h, zb).double(),
+                               atol=1e-5, rtol=1.6e-2)
+
+
+def selected_inputs(b, q, h, m, d, s, bank_b, seed, duplicates=False):
+    g = torch.Generator().manual_seed(seed)
+    channel = (torch.randn(b, q, h, m, d, generator=g) * 0.1).to(BF16)
+    ids = torch.stack([torch.randperm(s, generator=g)[:m] for _ in range(b * q * h)])
+    ids = ids.reshape(b, q, h, m)
+    if duplicates:
+        ids[:, ::3, :, 1] = ids[:, ::3, :, 0]
+    bank = torch.randn(bank_b, h, s, d, d, generator=g).to(BF16)
+    return channel, ids, bank
+
+
+@pytest.mark.parametrize("d,q,bank_b,dup", [(64, 300, 1, False), (128, 70, 2, False),
+                                            (64, 100, 2, True)])
+def test_selected_numerator_forward(device, d, q, bank_b, dup):
+    channel, ids, bank = selected_inputs(2, q, 2, 6, d, 37, bank_b, 17, dup)
+    with torch.no_grad():
+        got = selected_fine_numerator(channel.to(device), ids.to(device), bank.to(device))
+    want = W.selected_fine_numerator(channel, ids, bank)
+    torch.testing.assert_close(got.double().cpu(), want.double(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("d,bank_b", [(64, 1), (128, 2)])
+def test_selected_numerator_backward(device, d, bank_b):
+    channel, ids, bank = selected_inputs(2, 90, 2, 5, d, 21, bank_b, 18)
+    g = torch.Generator().manual_seed(19)
+    grad = torch.randn(2, 90, 2, d, generator=g).to(BF16)
+    ch = channel.to(device).requires_grad_()
+    bk = bank.to(device).requires_grad_()
+    out = selected_fine_numerator(ch, ids.to(device), bk)
+    out.backward(grad.to(device))
+    want_ch, want_c = W.selected_fine_numerator_backward(channel, ids, bank, grad)
+    torch.testing.assert_close(ch.grad.double().cpu(), want_ch.double(), atol=2e-2, rtol=2e-2)
+    close(bk.grad, want_c, 2e-2)

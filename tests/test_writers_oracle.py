@@ -1,0 +1,140 @@
+"""Pins for the non-preset writer oracle (oracle/writers.py), CPU only.
+
+Each check uses a method independent of the restated formula: numpy's LU
+solve for the Cholesky path, the dense matrix behind the structured writer's
+two Sherman-Morrison steps, invariants of the statistics, brute-force loops
+and one-hot channels for the selected numerator.
+"""
+import pytest
+import torch
+
+from oracle import writers as W
+
+BF16 = torch.bfloat16
+
+
+def kv(n, t, h, d, seed):
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn(n, t, h, d, generator=g) * 2).to(BF16)
+    v = torch.randn(n, t, h, d, generator=g).to(BF16)
+    return k, v
+
+
+@pytest.mark.parametrize("d", [8, 64])
+def test_association_statistics_invariants(d):
+    k, v = kv(2, 256, 3, d, 1)
+    gram, cross, mass = W.association_statistics(k, v, with_mass=True)
+    u = W.feature_simplex(k)
+    assert torch.equal(u, u.to(BF16).double())                  # u is bf16-valued
+    assert torch.allclose(gram, gram.transpose(-1, -2))
+    assert torch.all(torch.linalg.eigvalsh(gram) > -1e-9)
+    trace = gram.diagonal(dim1=-2, dim2=-1).sum(-1)
+    assert torch.allclose(trace, (u * u).sum(-1).sum(1), rtol=1e-12)
+    # each softmax row sums to 1 before its bf16 rounding (2^-9 per element)
+    assert torch.allclose(mass.sum(-1), torch.full_like(mass.sum(-1), 256.0), rtol=4e-3)
+    # sum_d cross[d][e] = sum_t (sum_d u[t][d]) v[t][e]
+    row = u.sum(-1)                                             # [N, T, H]
+    want = torch.einsum("nth,nthe->nhe", row, v.double())
+    assert torch.allclose(cross.sum(-2), want, rtol=1e-10, atol=1e-10)
+    square, cross2, mass2 = W.structured_statistics(k, v)
+    assert torch.equal(cross2, cross) and torch.equal(mass2, mass)
+    assert torch.allclose(square, gram.diagonal(dim1=-2, dim2=-1))
+
+
+@pytest.mark.parametrize("d", [8, 64])
+def test_association_matrix_against_dense_solve(d):
+    k, v = kv(3, 256, 2, d, 2)
+    gram, cross = W.association_statistics(k, v)
+    solution, c = W.association_matrix(gram, cross)
+    system = W.regularised_system(gram)
+    # ridge = mean diagonal (a dropped /D or a missing ridge fails here)
+    ridge = system.diagonal(dim1=-2, dim2=-1) - gram.diagonal(dim1=-2, dim2=-1)
+    assert torch.allclose(ridge, gram.diagonal(dim1=-2, dim2=-1).mean(-1, keepdim=True)
+                          .expand_as(ridge))
+    dense = W.dense_solve(system, cross)
+    assert torch.allclose(solution, dense, rtol=1e-9, atol=1e-9)
+    assert torch.allclose(system @ solution, cross, rtol=1e-9, atol=1e-9)
+    assert c.dtype == BF16 and torch.equal(c, solution.to(BF16))
+
+
+def test_chronological_sum_order():
+    x = torch.randn(2, 3, 5, 4, 4, dtype=torch.float32)
+    total = W.chronological_sum(x)
+    want = x[:, :, 0]
+    for i in range(1, 5):
+        want = want + x[:, :, i]
+    assert torch.equal(total, want)
+    assert torch.allclose(total, x.double().sum(2).float(), atol=1e-5)
+
+
+@pytest.mark.parametrize("zero_variance", [False, True])
+def test_structured_matrix_against_dense_inverse(zero_variance):
+    d, count = 16, 256
+    k, v = kv(2, count, 2, d, 3)
+    square, cross, mass = W.structured_statistics(k, v)
+    if zero_variance:
+        # identical tokens: var = 0 exactly, the rank-one var term drops out
+        k = k[:, :1].expand(-1, count, -1, -1)
+        square, cross, mass = W.structured_statistics(k, v)
+        mass = square.sqrt() * count          # force square * count == mass^2
+        square = mass * mass / count
+    result, c = W.structured_matrix(square, cross, mass, count)
+    system = W.structured_system(square, mass, count)
+    dense = W.dense_solve(system, cross)
+    assert torch.allclose(result, dense, rtol=1e-8, atol=1e-10)
+    assert torch.equal(c, result.to(BF16))
+
+
+def test_feature_read_coefficients_mixture():
+    g = torch.Generator().manual_seed(4)
+    h = torch.softmax(torch.randn(2, 5, 3, 16, generator=g), -1).to(BF16)
+    z = torch.randn(2, 5, 3, 6, 16, generator=g).to(BF16)
+    out = W.feature_read_coefficients(h, z)
+    mass = (h.double().unsqueeze(-2) * z.double().exp()).sum(-1)
+    mixture = mass / mass.sum(-1, keepdim=True)
+    assert torch.allclose(mixture.sum(-1), torch.ones_like(mixture.sum(-1)))
+    ratio = out.double() / h.double().unsqueeze(-2)
+    assert torch.allclose(ratio, mixture.unsqueeze(-1).expand_as(ratio), rtol=8e-3)
+    # a broadcast read_z (one row for every query) equals the expanded one
+    zb = z[:, :1]
+    assert torch.equal(W.feature_read_coefficients(h, zb),
+                       W.feature_read_coefficients(h, zb.expand_as(z)))
+
+
+def test_selected_numerator_brute_force_and_one_hot():
+    g = torch.Generator().manual_seed(5)
+    b, q, h, m, d, s = 4, 3, 2, 5, 8, 7
+    channel = torch.randn(b, q, h, m, d, generator=g).to(BF16)
+    ids = torch.randint(0, s, (b, q, h, m), generator=g)
+    bank = torch.randn(2, h, s, d, d, generator=g).to(BF16)      # shared by b % 2
+    out = W.selected_fine_numerator(channel, ids, bank)
+    assert torch.equal(out, W.selected_fine_numerator_loop(channel, ids, bank))
+    # one-hot channel picks row d0 of the selected C
+    onehot = torch.zeros(b, q, h, 1, d)
+    onehot[..., 3] = 1
+    pick = W.selected_fine_numerator(onehot.to(BF16), ids[..., :1], bank)
+    for bi in range(b):
+        for qi in range(q):
+            for hi in range(h):
+                assert torch.equal(pick[bi, qi, hi], bank[bi % 2, hi, ids[bi, qi, hi, 0], 3])
+
+
+def test_selected_numerator_backward_brute_force():
+    g = torch.Generator().manual_seed(6)
+    b, q, h, m, d, s = 2, 3, 2, 4, 8, 5
+    channel = torch.randn(b, q, h, m, d, generator=g).to(BF16)
+    ids = torch.randint(0, s, (b, q, h, m), generator=g)
+    bank = torch.randn(1, h, s, d, d, generator=g).to(BF16)
+    grad = torch.randn(b, q, h, d, generator=g).to(BF16)
+    dch, dc = W.selected_fine_numerator_backward(channel, ids, bank, grad)
+    # autograd of the fp64 contraction gives the same adjoints up to the casts
+    ch = channel.double().requires_grad_()
+    cb = bank.double().requires_grad_()
+    gathered = cb[0][torch.arange(h)[None, None, :, None], ids]
+    out = torch.einsum("bqhmd,bqhmde->bqhe", ch, gathered)
+    out.backward(grad.double())
+    assert torch.allclose(dch.double(), ch.grad, rtol=8e-3, atol=1e-6)
+    # per-batch bf16 partials, then a bf16 total: a few bf16 ulps of the largest term
+    assert (dc.double() - cb.grad).abs().max() <= 2e-2 * cb.grad.abs().max()
+    # a mistake in the shared-bank index (b % BB) or the id routing is O(1)
+    assert not torch.allclose(dc.double(), cb.grad.roll(1, 2), atol=0.5)

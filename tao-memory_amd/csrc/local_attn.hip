@@ -92,9 +92,53 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
   // reference and p <= 2^kSlack stays well inside bf16's range.
   constexpr float kSlack = 8.0f;
 
-  // Global loads of one 64-key block into registers (prefetch).
+  // Global loads of one 64-key block into registers (prefetch). When the
+  // whole window lies in the call's operands (no ring rows: training and
+  // first prefills), each thread walks fixed row offsets with pointers that
+  // advance 64 rows a block; otherwise every row goes through key_row.
+  const bool direct = key_start >= p.kpos0;          // workgroup-uniform
   uint4 kpre[KJ], va[VJ], vb[VJ];
+  const bf16_t* kptr[KJ];
+  const bf16_t* vptr[VJ];
+  const int64_t step_k = (int64_t)kKeys * p.k.st, step_v = (int64_t)kKeys * p.v.st;
+  if (direct) {
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      const int job = min(tid + j * kAttnThreads, kKeys * CH - 1);
+      kptr[j] = p.k.p + b * p.k.sb + (key_start - p.kpos0 + job / CH) * p.k.st + h * p.k.sh +
+                (job % CH) * 8;
+    }
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) {
+      const int job = min(tid + j * kAttnThreads, (kKeys / 2) * CH - 1);
+      const int t0 = 2 * (job % (kKeys / 2)), c = job / (kKeys / 2);
+      vptr[j] = p.v.p + b * p.v.sb + (key_start - p.kpos0 + t0) * p.v.st + h * p.v.sh + c * 8;
+    }
+  }
   auto fetch = [&](long long kb) {
+    if (direct) {
+      const int rem = (int)(kend - kb);              // rows of this block that exist
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) {
+        const int job = tid + j * kAttnThreads;
+        kpre[j] = make_uint4(0, 0, 0, 0);
+        if (job < kKeys * CH && job / CH < rem) kpre[j] = *(const uint4*)kptr[j];
+        kptr[j] += step_k;
+      }
+#pragma unroll
+      for (int j = 0; j < VJ; ++j) {
+        const int job = tid + j * kAttnThreads;
+        va[j] = make_uint4(0, 0, 0, 0);
+        vb[j] = make_uint4(0, 0, 0, 0);
+        if (job < (kKeys / 2) * CH) {
+          const int t0 = 2 * (job % (kKeys / 2));
+          if (t0 < rem) va[j] = *(const uint4*)vptr[j];
+          if (t0 + 1 < rem) vb[j] = *(const uint4*)(vptr[j] + p.v.st);
+        }
+        vptr[j] += step_v;
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < KJ; ++j) {
       const int job = tid + j * kAttnThreads;
@@ -121,7 +165,13 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
   for (int t = 0; t < DT; ++t)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[t][i] = 0.0f;
-  float m_run = -__builtin_inff(), l_run = 0.0f;
+  // Row sums of P on the matrix pipe: an A operand of ones gives
+  // sum_k P[query][k] in every row of the accumulator (element 0 is used).
+  floatx16 lacc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) lacc[i] = 0.0f;
+  const bf16x8 ones = as_bf16x8(make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u));
+  float m_run = -__builtin_inff();
 
   fetch(key_start);
   for (long long kb = key_start; kb < kend; kb += kKeys) {
@@ -192,7 +242,8 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
       const float m_new = fmaxf(m_run, bmax);
       // No visible key yet on this lane (both -inf): O and l are still 0.
       const float alpha = m_new == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) lacc[i] *= alpha;
 #pragma unroll
       for (int t = 0; t < DT; ++t)
 #pragma unroll
@@ -200,18 +251,11 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
       m_run = m_new;
     }
     const float m_use = m_run == -__builtin_inff() ? 0.0f : m_run;
-    float rs[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(s[sub][i], scale_log2, -m_use));
-        s[sub][i] = e;
-        rs[i & 1] += e;
-      }
-    float rsum = rs[0] + rs[1];
-    rsum += __shfl_xor(rsum, 32, 64);
-    l_run += rsum;
+      for (int i = 0; i < 16; ++i)
+        s[sub][i] = __builtin_amdgcn_exp2f(fmaf(s[sub][i], scale_log2, -m_use));
 
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
@@ -230,9 +274,11 @@ __global__ __launch_bounds__(kAttnThreads) void local_attn_kernel(AttnParams p) 
           const uint4 u = make_uint4(lo.x, lo.y, hi.x, hi.y);
           o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(u), pb, o[t], 0, 0, 0);
         }
+        lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb, lacc, 0, 0, 0);
       }
   }
   if (!qvalid) return;
+  const float l_run = lacc[0];
   if (p.lse && hl == 0) p.lse[((size_t)b * p.T + qtok) * p.H + h] = m_run + __log2f(l_run);
   const float inv = 1.0f / l_run;
   bf16_t* orow = p.out + (((size_t)b * p.T + qtok) * p.H + h) * D;

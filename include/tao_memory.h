@@ -200,6 +200,12 @@ typedef struct tao_prefill_pools {
   void* coarse_out;
   void* fine_out;
   float* den_out;
+  /* Nonzero: the caller has written the fine value matrices (bank_c) of the
+   * blocks this call seals and the page value matrices (page_c) of the pages
+   * it completes, as the non-softmax writers do (tao_stream.py:56-77,
+   * :486-499, association_writer.py); the writer then computes only fine_z
+   * and the page pass only the page descriptors and weights. */
+  int32_t external_values;
 } tao_prefill_pools;
 
 /* Layout of the int64 prefill plan (all indices are token offsets in tok

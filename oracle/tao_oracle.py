@@ -600,7 +600,7 @@ class OracleStream:
 # ----------------------------------------------------------------------------
 
 def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
-                     geometry=None, return_routes=False):
+                     geometry=None, return_routes=False, writer="softmax"):
     """tao_attention forward with fresh routing at every query.
 
     Restates read_training (tao_stream.py:668-757) with route_interval=1 and
@@ -625,6 +625,12 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
     tiles with equal (completed, pending?, M, length) on the batch axis
     (:700-748) changes no value.
 
+    writer="regularized_association" keeps the softmax writer's z and read
+    and replaces the value matrices (tao_stream.py:72-74, 80-123, 565-569):
+    C_f = association_matrix(association_statistics(block f)) and, for a
+    completed page, association_matrix of the in-order sums of its fines'
+    statistics (oracle/writers.py).
+
     Returns out [B, T, H, D] (and, with return_routes, a dict tile -> selected
     ids [B, Q, H, M] in score order).
     """
@@ -642,9 +648,14 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
     visible_max = max(0, n_tiles - 1 - lag)
     if total <= g.serve_limit or visible_max == 0:       # :682-688
         return (local, routes) if return_routes else local
-    zs, cs = [], []
+    zs, cs, stats = [], [], []
     for f in range(visible_max):
-        z, c = seal_softmax(raw_k[:, f * ft:(f + 1) * ft], v[:, f * ft:(f + 1) * ft])
+        kb, vb = raw_k[:, f * ft:(f + 1) * ft], v[:, f * ft:(f + 1) * ft]
+        z, c = seal_softmax(kb, vb)
+        if writer == "regularized_association":
+            from . import writers as W
+            stats.append(W.association_statistics(kb, vb))
+            c = W.association_matrix(*stats[-1])[1]
         zs.append(z)
         cs.append(c)
     fine_z = torch.stack(zs, 2)                          # [B, H, S, D]
@@ -653,7 +664,13 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
     page_z_full = [page_summary(fine_z[:, :, p * group:(p + 1) * group])
                    for p in range(full_pages)]
     page_c_full = []
-    if not g.coarse_index_only:
+    if not g.coarse_index_only and writer == "regularized_association":
+        from . import writers as W
+        for p in range(full_pages):
+            gram = sum(stats[p * group + i][0] for i in range(group))
+            cross = sum(stats[p * group + i][1] for i in range(group))
+            page_c_full.append(W.association_matrix(gram, cross)[1])
+    elif not g.coarse_index_only:
         page_c_full = [page_coarse_matrix(fine_z[:, :, p * group:(p + 1) * group],
                                           page_z_full[p], bank[:, :, p * group:(p + 1) * group])
                        for p in range(full_pages)]

@@ -465,6 +465,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   if (n_read > 0 && need_pools && st->fine_cap > 16384)
     return fail(TAO_E_CAPACITY, "prefill reads index at most 16384 fines per state");
   const bool coarse_values = st->page_c != nullptr;
+  const int external_values = pools && pools->external_values ? 1 : 0;
   const int64_t c_first = pools ? pools->coarse_first : 0;
   const int64_t c_count = pools ? pools->coarse_count : 0;
   bool coarse_reads = false;
@@ -550,6 +551,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   wp.fine_cap = st->fine_cap;
   wp.first_slot = (int)first_slot;
   wp.count = (int)n_write;
+  wp.z_only = external_values;
   e = tao::launch_writer(wp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill writer");
   // pages
@@ -566,7 +568,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   pp.count = (int)n_pages;
   e = tao::launch_pages(pp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill pages");
-  if (coarse_values) {
+  if (coarse_values && !external_values) {
     tao::PageCoarseParams cp{};
     cp.bank = (const bf16_t*)st->bank_c;
     cp.sw = (const bf16_t*)st->fine_sw;

@@ -194,6 +194,7 @@ struct WriterParams {
   const int64_t* starts;         // device [count] absolute start positions
   int64_t new_base;
   int B, H, L, fine_cap, first_slot, count;
+  int z_only;                    // write fine_z only (the caller owns the C slots)
 };
 hipError_t launch_writer(const WriterParams& p, int head_dim, hipStream_t s);
 

@@ -194,6 +194,7 @@ __global__ __launch_bounds__(kWriterThreads) void writer_kernel(WriterParams p) 
     const float z = rbf(sm.top[tid] + log_bf(total));
     p.fine_z[((size_t)bh * p.fine_cap + slot) * D + d0 + tid] = f2bf(z);
   }
+  if (p.z_only) return;                         // workgroup-uniform
 
   // ---- C^T[e][d] = sum_t V^T[e][t] E[t][d] / Z[d] on MFMA 32x32x16: wave w
   // owns row tile w (value channels 32w ..) and the half's CT column tiles;

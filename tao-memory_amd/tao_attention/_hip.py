@@ -49,7 +49,8 @@ class PrefillPools(ctypes.Structure):
                 ("pool_pcap", _i32), ("epochs", _i32), ("sel_slots", _i32),
                 ("coarse_pool", _vp), ("coarse_first", _i32), ("coarse_count", _i32),
                 ("qsel", _vp), ("qsel_words", _i32),
-                ("local_lse", _vp), ("coarse_out", _vp), ("fine_out", _vp), ("den_out", _vp)]
+                ("local_lse", _vp), ("coarse_out", _vp), ("fine_out", _vp), ("den_out", _vp),
+                ("external_values", _i32)]
 
 
 class TrainBwd(ctypes.Structure):

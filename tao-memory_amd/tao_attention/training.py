@@ -29,9 +29,15 @@ from . import _hip
 from .config import TaoConfig
 
 
+# Writers whose read is the softmax writer's (fine z and the selected read are
+# unchanged; only the value matrices differ, tao_stream.py:72-74, 530-575).
+_VALUE_WRITERS = ("softmax", "regularized_association")
+
+
 def _check(q, k, v, raw_q, raw_k, config):
-    if config.fine_writer != "softmax":
-        raise NotImplementedError("the HIP path implements the softmax fine writer")
+    if config.fine_writer not in _VALUE_WRITERS:
+        raise NotImplementedError(
+            f"the HIP full-sequence read implements the fine writers {_VALUE_WRITERS}")
     if config.fine_tokens != 256 or config.local_keep != 512 or config.coarse_group != 8:
         raise NotImplementedError(
             "the HIP path implements fine_tokens=256, local_keep=512, coarse_group=8")
@@ -120,6 +126,38 @@ def _workspace(config, b, tokens, heads, d, device):
     return ws
 
 
+def _association_values(ws, raw_k, v, config):
+    """The regularized association writer's value matrices of the visible
+    blocks and of the completed pages (tao_stream.py:80-123, 530-575):
+    C_f = association_matrix(u_f^T u_f, u_f^T v_f) per 256-token block and,
+    with the coarse value branch, page C = association_matrix of the
+    chronological sums of its eight fines' statistics. Written into the
+    call's state in its C^T layout; the prefill then keeps them
+    (pools.external_values)."""
+    from .association_writer import association_matrix, association_statistics, chronological_sum
+
+    fines = ws.info["fines"]
+    dev = ws.dev
+    ws.pools.external_values = 1
+    if not fines:
+        return
+    group = config.coarse_group
+    pages = fines // group if dev.coarse_values else 0
+    span = fines * config.fine_tokens
+    with torch.no_grad():
+        for bi in range(raw_k.shape[0]):
+            kb = raw_k[bi, :span].unflatten(0, (fines, config.fine_tokens))
+            vb = v[bi, :span].unflatten(0, (fines, config.fine_tokens))
+            gram, cross = association_statistics(kb, vb)                # [S, H, D, D]
+            dev.bank[bi, :, :fines] = association_matrix(gram, cross).permute(1, 0, 3, 2)
+            if pages:
+                def page_sum(t):
+                    t = t[:pages * group].unflatten(0, (pages, group))   # [P, 8, H, D, D]
+                    return chronological_sum(t.transpose(1, 2))          # [P, H, D, D]
+                page_c = association_matrix(page_sum(gram), page_sum(cross))
+                dev.page_c[bi, :, :pages] = page_c.permute(1, 0, 3, 2)
+
+
 def forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_routes=False):
     """Fused heads [B, T, H, D] of the full-sequence read (no autograd).
 
@@ -134,6 +172,8 @@ def forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_rou
         return (out, None) if return_routes else out
     ws = _workspace(config, b, tokens, heads, d, q.device)
     q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
+    if config.fine_writer == "regularized_association":
+        _association_values(ws, raw_k, v, config)
     tok = _hip.tokens(q, k, v, raw_q, raw_k)
     fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
     out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
@@ -151,6 +191,9 @@ def _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, conf
     reads: local-attention log2-sum-exp, pre-fusion coarse / fine heads and
     denominators. Returns (out, context for backward)."""
     _check(q, k, v, raw_q, raw_k, config)
+    if config.fine_writer != "softmax":
+        raise NotImplementedError(
+            "gradients of the full-sequence read are implemented for the softmax writer")
     b, tokens, heads, d = q.shape
     ws = _Workspace(config, b, tokens, heads, d, q.device)
     q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)

@@ -167,3 +167,49 @@ def test_selected_numerator_backward(device, d, bank_b):
     want_ch, want_c = W.selected_fine_numerator_backward(channel, ids, bank, grad)
     torch.testing.assert_close(ch.grad.double().cpu(), want_ch.double(), atol=2e-2, rtol=2e-2)
     close(bk.grad, want_c, 2e-2)
+
+
+def _bitmask_sets(qsel):
+    words = qsel.cpu().to(torch.int64) & 0xFFFFFFFF
+    bits = (words.unsqueeze(-1) >> torch.arange(32)) & 1
+    return bits.reshape(*words.shape[:3], -1).bool()
+
+
+@pytest.mark.parametrize("tokens,heads,width,index_only,seed", [
+    (2100, 2, 64, True, 51), (2900, 2, 128, False, 52)])
+def test_full_sequence_regularized_writer(device, tokens, heads, width, index_only, seed):
+    """tao_attention with fine_writer="regularized_association": the softmax
+    writer's z and routes (bit-exact), association value matrices for fines
+    and completed pages, outputs within the bf16 tolerance of the oracle."""
+    from oracle import tao_oracle as O
+    from tao_attention import TaoConfig, tao_attention, training
+    g = torch.Generator().manual_seed(seed)
+    xs = [torch.randn(1, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
+    fa = torch.randn(heads, width, 3, generator=g) * 0.02
+    fb = torch.randn(heads, width, 3, generator=g) * 0.02
+    cfg = TaoConfig(fine_writer="regularized_association", coarse_index_only=index_only)
+    q, k, v, rq, rk = (x.to(device) for x in xs)
+    out, qsel = training.forward(q, k, v, rq, rk, fa.to(device), fb.to(device), 0.5, cfg,
+                                 return_routes=True)
+    ref, routes = O.training_forward(*xs, fa, fb, 0.5, O.Geometry.from_config(cfg),
+                                     return_routes=True, writer="regularized_association")
+    got = _bitmask_sets(qsel)
+    for tile, sel in routes.items():
+        s = tile * 256
+        part = got[:, s:s + sel.shape[1]]
+        want = torch.zeros_like(part)
+        want.scatter_(-1, sel, True)
+        assert torch.equal(part, want), f"selected sets of tile {tile}"
+    torch.testing.assert_close(out.cpu().float(), ref.float(), atol=2e-2, rtol=2e-2)
+    # the softmax writer's outputs differ once history is read
+    soft = training.forward(q, k, v, rq, rk, fa.to(device), fb.to(device), 0.5,
+                            TaoConfig(coarse_index_only=index_only))
+    assert not torch.equal(soft[:, 768:], out[:, 768:])
+    api = tao_attention(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.to(device),
+                        fusion_b=fb.to(device), alpha=0.5, config=cfg)
+    assert torch.equal(api, out)
+    # gradients are implemented for the softmax writer only
+    qg = q.clone().requires_grad_()
+    with pytest.raises(NotImplementedError):
+        tao_attention(qg, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.to(device),
+                      fusion_b=fb.to(device), alpha=0.5, config=cfg)

@@ -323,6 +323,10 @@ typedef struct tao_train_bwd {
    * d fine_z fp32 [B][H][fines][D] and d C^T fp32 [B][H][fines][D][D]
    * ([e][d], the bank's layout), for callers that inspect them. */
   float* dz_out; float* dc_out;
+  /* Optional (null = skip): fp32 [1] receives d out / d alpha . grad through
+   * gain = 2 alpha (no reference counterpart: the reference takes alpha as a
+   * Python float, operator.py:34). */
+  float* dalpha_out;
 } tao_train_bwd;
 
 /* Workspace bytes of tao_train_backward for a full-sequence read of `tokens`

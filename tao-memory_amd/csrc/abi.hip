@@ -829,7 +829,7 @@ namespace {
 
 struct TrainBwdLayout {
   size_t dlocal, h, delta, dden, dcoarse, dnum, drq, dh, dvf;   // per-token arrays
-  size_t dpw, dsw_tile, dgc, dc, dsw, dpz, dz;                  // memory branch
+  size_t dpw, dsw_tile, dgc, dc, dsw, dpz, dz, dalpha;          // memory branch, d alpha
   size_t zero_begin, zero_end;                                  // accumulators to clear
   size_t total;
   int n_tiles, v_max;
@@ -867,6 +867,7 @@ TrainBwdLayout train_bwd_layout(const tao_state_dev* st, int64_t tokens, int fin
   l.dsw = take(BH * (size_t)fines * D * 4);
   l.dpz = take(BH * (size_t)st->page_cap * D * 4);
   l.dz = take(BH * (size_t)fines * D * 4);
+  l.dalpha = take(4);
   l.zero_end = off;
   l.total = off;
   return l;
@@ -945,6 +946,7 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   fp.dfa = a->dfusion_a;
   fp.dfb = a->dfusion_b;
   fp.h = (bf16_t*)(ws + l.h);
+  fp.dalpha = (float*)(ws + l.dalpha);
   e = tao::launch_fuse_bwd(fp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_train_backward fusion");
   // ---- local attention adjoint
@@ -1020,6 +1022,10 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   if (a->dc_out && fines > 0) {
     e = hipMemcpyAsync(a->dc_out, mp.dc, BHf * D * D * sizeof(float), hipMemcpyDeviceToDevice, s);
     if (e != hipSuccess) return check_hip(e, "tao_train_backward dC copy");
+  }
+  if (a->dalpha_out) {
+    e = hipMemcpyAsync(a->dalpha_out, ws + l.dalpha, sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return check_hip(e, "tao_train_backward d alpha copy");
   }
   return TAO_OK;
 }

@@ -276,6 +276,7 @@ struct TrainBwdParams {
   bf16_t* dlocal; float* delta; float* dcoarse; float* dnum; float* dden; float* drq;
   float* dfa; float* dfb;
   bf16_t* h;                     // h = softmax(raw_q) [B, T, H, D]
+  float* dalpha;                 // zeroed fp32 scalar: += d out / d alpha . grad
 };
 hipError_t launch_fuse_bwd(const TrainBwdParams& p, int head_dim, hipStream_t s);
 

@@ -36,8 +36,10 @@ TAO_DEV bf16x8 as_bf16x8(const uint4& u) {
 //   d local = 2 g rho_0, d coarse = gain g rho_1, d fine = gain g rho_2,
 //   d raw_q += sum_i ds_i a_i, d fusion_a_i += ds_i raw_q, d fusion_b_i += ds_i.
 // Rows without history (output = local): d local = g.
-// Also: dnum = d fine / den, dden = -sum_e d fine fine / den, and the local
-// attention's delta = sum_e d local * local.
+// Also: dnum = d fine / den, dden = -sum_e d fine fine / den, the local
+// attention's delta = sum_e d local * local, and d alpha = 2 sum g (rho_1
+// coarse + rho_2 fine) over fused elements (gain = 2 alpha; the reference
+// builds gain from a Python float and has no such gradient).
 constexpr int kFuseChunk = 64;
 
 template <int D>
@@ -58,6 +60,7 @@ __global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
     bb[i] = rbf(load_param(p.fb, p.f_dtype, h * p.fb_s[0] + e * p.fb_s[1] + i * p.fb_s[2]));
   }
   float sfa[3] = {0.f, 0.f, 0.f}, sfb[3] = {0.f, 0.f, 0.f};
+  float sgain = 0.0f;
   for (int t0 = chunk * kFuseChunk; t0 < min(p.T, (chunk + 1) * kFuseChunk); t0 += ROWS) {
     const int t = t0 + r;
     const bool on = t < min(p.T, (chunk + 1) * kFuseChunk);
@@ -98,6 +101,7 @@ __global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
         sfb[i] += ds;
       }
       dlocal = 2.0f * g * rho[0];
+      sgain += g * (rho[1] * C + rho[2] * F);
       const float dfine = p.gain * g * rho[2];
       p.dcoarse[row * D + e] = p.gain * g * rho[1];
       p.dnum[row * D + e] = dfine / den;
@@ -135,6 +139,10 @@ __global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
       p.delta[row] = dl;
       p.dden[row] = dd;
     }
+  }
+  if (p.dalpha) {
+    const float sg = wave_sum_fold(sgain);
+    if (lane == 0) atomicAdd(p.dalpha, 2.0f * sg);
   }
   // d fusion_a / d fusion_b: sum the ROWS lane rows, one atomic per (e, i).
 #pragma unroll

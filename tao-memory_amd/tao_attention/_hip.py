@@ -60,7 +60,7 @@ class TrainBwd(ctypes.Structure):
                 ("dq", _vp), ("dk", _vp), ("dv", _vp), ("draw_q", _vp), ("draw_k", _vp),
                 ("dfusion_a", _vp), ("dfusion_b", _vp),
                 ("workspace", _vp), ("workspace_bytes", _sz),
-                ("dz_out", _vp), ("dc_out", _vp)]
+                ("dz_out", _vp), ("dc_out", _vp), ("dalpha_out", _vp)]
 
 
 class StreamCfg(ctypes.Structure):

@@ -220,8 +220,9 @@ def _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, conf
 def backward(ctx_data, grad, fusion_a, fusion_b, alpha, memory_adjoints=None):
     """Gradients (dq, dk, dv, draw_q, draw_k, dfusion_a, dfusion_b) of the
     full-sequence read at the forward recorded in ctx_data. With a dict
-    `memory_adjoints`, it also receives "dz" (d fine_z, fp32 [B, H, S, D]) and
-    "dc" (d C, fp32 [B, H, S, D, D]) of the S written fines."""
+    `memory_adjoints`, it also receives "dz" (d fine_z, fp32 [B, H, S, D]),
+    "dc" (d C, fp32 [B, H, S, D, D]) of the S written fines and "dalpha"
+    (fp32 [1], through gain = 2 alpha)."""
     ws = ctx_data["ws"]
     saves = ctx_data["saves"]
     q, k, v, raw_q, raw_k = ctx_data["operands"]
@@ -250,6 +251,9 @@ def backward(ctx_data, grad, fusion_a, fusion_b, alpha, memory_adjoints=None):
     args.dfusion_a, args.dfusion_b = dfa.data_ptr(), dfb.data_ptr()
     args.workspace, args.workspace_bytes = scratch.data_ptr(), nbytes
     fines = ws.info["fines"]
+    if memory_adjoints is not None:
+        memory_adjoints["dalpha"] = torch.zeros(1, dtype=torch.float32, device=dev)
+        args.dalpha_out = memory_adjoints["dalpha"].data_ptr()
     if memory_adjoints is not None and fines:
         memory_adjoints["dz"] = torch.empty((b, heads, fines, d), dtype=torch.float32, device=dev)
         memory_adjoints["dc_t"] = torch.empty((b, heads, fines, d, d), dtype=torch.float32,
@@ -271,30 +275,41 @@ class _FullSequenceRead(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config):
+        alpha_f = float(alpha)
         out, data = _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b,
-                                          alpha, config)
+                                          alpha_f, config)
         ctx.data = data
-        ctx.alpha = alpha
+        ctx.alpha = alpha_f
+        ctx.alpha_like = alpha if torch.is_tensor(alpha) else None
         ctx.save_for_backward(fusion_a, fusion_b)
         return out
 
     @staticmethod
     def backward(ctx, grad):
         fusion_a, fusion_b = ctx.saved_tensors
-        dq, dk, dv, drq, drk, dfa, dfb = backward(ctx.data, grad, fusion_a, fusion_b,
-                                                  ctx.alpha)
-        ctx.data = None
         need = ctx.needs_input_grad
+        extra = {} if need[7] else None
+        dq, dk, dv, drq, drk, dfa, dfb = backward(ctx.data, grad, fusion_a, fusion_b,
+                                                  ctx.alpha, memory_adjoints=extra)
+        ctx.data = None
+        dalpha = None
+        if need[7]:
+            like = ctx.alpha_like
+            dalpha = extra["dalpha"].reshape(like.shape).to(like.dtype)
         return (dq if need[0] else None, dk if need[1] else None, dv if need[2] else None,
                 drq if need[3] else None, drk if need[4] else None,
                 dfa.to(fusion_a.dtype) if need[5] else None,
-                dfb.to(fusion_b.dtype) if need[6] else None, None, None)
+                dfb.to(fusion_b.dtype) if need[6] else None, dalpha, None)
 
 
 def full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
                        config=None):
+    """tao_attention's read and fusion. alpha is a Python float, as in the
+    reference, or a 0-dim tensor; a tensor that requires grad receives
+    d alpha through gain = 2 alpha (the reference has no such gradient)."""
     config = config or TaoConfig()
     tensors = (q, k, v, raw_q, raw_k, fusion_a, fusion_b)
-    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+    alpha_grad = torch.is_tensor(alpha) and alpha.requires_grad
+    if torch.is_grad_enabled() and (alpha_grad or any(t.requires_grad for t in tensors)):
         return _FullSequenceRead.apply(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config)
-    return forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config)
+    return forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, float(alpha), config)

@@ -587,6 +587,51 @@ def test_full_sequence_backward_matches_oracle(tokens, heads, width, index_only,
 
 
 @pytest.mark.parametrize("tokens,heads,width,index_only,seed", [
+    (2100, 2, 64, True, 48), (2900, 2, 128, False, 49)])
+def test_full_sequence_alpha_gradient(tokens, heads, width, index_only, seed):
+    """d alpha (gain = 2 alpha; no reference counterpart) against fp64
+    autograd of the oracle's smooth forward with alpha as a leaf; a float
+    alpha gives the same output and no alpha gradient."""
+    from tao_attention import TaoConfig, tao_attention
+    xs, fa, fb = inputs(tokens, heads, width, seed)
+    cfg = TaoConfig(coarse_index_only=index_only)
+    grad = torch.randn(xs[0].shape, generator=torch.Generator().manual_seed(seed + 100)).to(BF16)
+    dev = [x.cuda() for x in xs]
+    alpha = torch.tensor(0.5, device="cuda", requires_grad=True)
+    q = dev[0].clone().requires_grad_(True)
+    out = tao_attention(q, *dev[1:3], raw_q=dev[3], raw_k=dev[4], fusion_a=fa.cuda(),
+                        fusion_b=fb.cuda(), alpha=alpha, config=cfg)
+    dq, dalpha = torch.autograd.grad(out, [q, alpha], grad.cuda())
+    with torch.no_grad():
+        plain = tao_attention(*dev[:3], raw_q=dev[3], raw_k=dev[4], fusion_a=fa.cuda(),
+                              fusion_b=fb.cuda(), alpha=0.5, config=cfg)
+    assert torch.equal(plain, out.detach())
+    _, routes = O.training_forward(*xs, fa, fb, 0.5, O.Geometry.from_config(cfg),
+                                   return_routes=True)
+    a64 = torch.tensor(0.5, dtype=torch.float64, requires_grad=True)
+    ref = O.training_forward_smooth(*(x.double() for x in xs), fa.double(), fb.double(), a64,
+                                    routes, O.Geometry.from_config(cfg))
+    (want,) = torch.autograd.grad((ref * grad.double()).sum(), [a64])
+    print(f"d alpha: {dalpha.item():.6e} (fp64 oracle {want.item():.6e})", flush=True)
+    assert dalpha.shape == alpha.shape
+    assert abs(dalpha.item() - want.item()) <= 5e-2 * abs(want.item())
+    # finite difference of the bf16 forward itself with a coherent upstream
+    # gradient (ones): the fused output is linear in gain = bf16(2 alpha) up to
+    # per-term bf16 roundings, which average out over the sum; gain moves
+    # exactly from 0.5 to 1.5 for alpha = 0.25 and 0.75
+    out1 = tao_attention(*dev[:3], raw_q=dev[3], raw_k=dev[4], fusion_a=fa.cuda(),
+                         fusion_b=fb.cuda(), alpha=alpha, config=cfg)
+    (d1,) = torch.autograd.grad(out1, [alpha], torch.ones_like(out1))
+    with torch.no_grad():
+        f = [tao_attention(*dev[:3], raw_q=dev[3], raw_k=dev[4], fusion_a=fa.cuda(),
+                           fusion_b=fb.cuda(), alpha=a, config=cfg).double().sum().item()
+             for a in (0.25, 0.75)]
+    fd = (f[1] - f[0]) / 0.5
+    print(f"d alpha (ones): {d1.item():.6e} (finite difference {fd:.6e})", flush=True)
+    assert abs(d1.item() - fd) <= 1e-2 * abs(fd)
+
+
+@pytest.mark.parametrize("tokens,heads,width,index_only,seed", [
     (2100, 2, 64, True, 46), (2900, 2, 128, False, 47)])
 def test_full_sequence_memory_adjoints_match_oracle(tokens, heads, width, index_only, seed):
     """The memory branch's adjoints before the writer, d fine_z (segment

@@ -460,8 +460,9 @@ def run_prefill(torch, device, cfg, heads, width, tokens, probe):
 def run_full_sequence(torch, args, device):
     """configs[1] shape: tao_attention over B2 x T8192 x H12 x D64 bf16 with
     TaoConfig() (coarse value branch on), every query routing itself. Returns
-    seconds per forward call and per forward + backward (gradients of all seven
-    differentiable operands), each the mean of event-bracketed timed calls."""
+    seconds per forward call and per forward + backward (gradients of q, k, v,
+    raw_q, raw_k, fusion_a, fusion_b and alpha, as configs[1] names), each the
+    mean of event-bracketed timed calls."""
     from tao_attention import TaoConfig, tao_attention
     b, t, h, d = 2, args.full_sequence_tokens, 12, 64
     g = torch.Generator(device=device).manual_seed(11)
@@ -488,15 +489,16 @@ def run_full_sequence(torch, args, device):
         end.record()
         torch.cuda.synchronize()
     seconds = start.elapsed_time(end) / runs * 1e-3
-    # forward + backward (gradients of q, k, v, raw_q, raw_k, fusion_a, fusion_b)
+    # forward + backward (gradients of q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
     leaves = [x.detach().requires_grad_(True) for x in xs]
     fa_l, fb_l = fa.detach().requires_grad_(True), fb.detach().requires_grad_(True)
+    alpha_l = torch.tensor(0.5, device=device, requires_grad=True)
     grad = torch.randn(b, t, h, d, generator=g, device=device).to(torch.bfloat16)
 
     def step():
         out = tao_attention(*leaves[:3], raw_q=leaves[3], raw_k=leaves[4], fusion_a=fa_l,
-                            fusion_b=fb_l, alpha=0.5, config=cfg)
-        return torch.autograd.grad(out, leaves + [fa_l, fb_l], grad)
+                            fusion_b=fb_l, alpha=alpha_l, config=cfg)
+        return torch.autograd.grad(out, leaves + [fa_l, fb_l, alpha_l], grad)
 
     for _ in range(2):
         step()
@@ -708,7 +710,9 @@ def main():
         result["full_sequence_forward"] = {
             "workload": "configs[1] shape: tao_attention B%d x T%d x H%d x D%d bf16, "
                         "TaoConfig() (coarse values on), every query routes itself; synthetic "
-                        "N(0,1) operands" % (fs["batch"], fs["tokens"], fs["heads"], fs["width"]),
+                        "N(0,1) operands; the backward takes the gradients of q, k, v, raw_q, "
+                        "raw_k, fusion_a, fusion_b and alpha"
+                        % (fs["batch"], fs["tokens"], fs["heads"], fs["width"]),
             "ms": round(fs["seconds"] * 1e3, 4),
             "tokens_per_s": round(fs["batch"] * fs["tokens"] / fs["seconds"], 1),
             "forward_backward_ms": round(fs["train_seconds"] * 1e3, 4),

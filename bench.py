@@ -492,7 +492,7 @@ def run_full_sequence(torch, args, device):
     # forward + backward (gradients of q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
     leaves = [x.detach().requires_grad_(True) for x in xs]
     fa_l, fb_l = fa.detach().requires_grad_(True), fb.detach().requires_grad_(True)
-    alpha_l = torch.tensor(0.5, device=device, requires_grad=True)
+    alpha_l = torch.tensor(0.5, requires_grad=True)    # host scalar: no per-step sync
     grad = torch.randn(b, t, h, d, generator=g, device=device).to(torch.bfloat16)
 
     def step():

@@ -295,7 +295,9 @@ class _FullSequenceRead(torch.autograd.Function):
         dalpha = None
         if need[7]:
             like = ctx.alpha_like
-            dalpha = extra["dalpha"].reshape(like.shape).to(like.dtype)
+            # a host alpha receives its gradient without a device sync
+            dalpha = extra["dalpha"].reshape(like.shape).to(like.dtype).to(
+                like.device, non_blocking=True)
         return (dq if need[0] else None, dk if need[1] else None, dv if need[2] else None,
                 drq if need[3] else None, drk if need[4] else None,
                 dfa.to(fusion_a.dtype) if need[5] else None,
@@ -306,7 +308,9 @@ def full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
                        config=None):
     """tao_attention's read and fusion. alpha is a Python float, as in the
     reference, or a 0-dim tensor; a tensor that requires grad receives
-    d alpha through gain = 2 alpha (the reference has no such gradient)."""
+    d alpha through gain = 2 alpha (the reference has no such gradient). The
+    kernels take alpha as a host scalar, so a device tensor costs one
+    synchronisation per call; a host tensor costs none."""
     config = config or TaoConfig()
     tensors = (q, k, v, raw_q, raw_k, fusion_a, fusion_b)
     alpha_grad = torch.is_tensor(alpha) and alpha.requires_grad

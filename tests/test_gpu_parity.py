@@ -614,6 +614,14 @@ def test_full_sequence_alpha_gradient(tokens, heads, width, index_only, seed):
     (want,) = torch.autograd.grad((ref * grad.double()).sum(), [a64])
     print(f"d alpha: {dalpha.item():.6e} (fp64 oracle {want.item():.6e})", flush=True)
     assert dalpha.shape == alpha.shape
+    # a host alpha gets the same gradient on the host (asynchronous copy)
+    alpha_h = torch.tensor(0.5, requires_grad=True)
+    out_h = tao_attention(*dev[:3], raw_q=dev[3], raw_k=dev[4], fusion_a=fa.cuda(),
+                          fusion_b=fb.cuda(), alpha=alpha_h, config=cfg)
+    (dh,) = torch.autograd.grad(out_h, [alpha_h], grad.cuda())
+    torch.cuda.synchronize()
+    assert dh.device.type == "cpu"
+    assert abs(dh.item() - dalpha.item()) <= 1e-5 * abs(dalpha.item())
     assert abs(dalpha.item() - want.item()) <= 5e-2 * abs(want.item())
     # finite difference of the bf16 forward itself with a coherent upstream
     # gradient (ones): the fused output is linear in gain = bf16(2 alpha) up to

@@ -68,6 +68,18 @@ typedef struct tao_state_dev {
   void* coarse_g;   /* fp32 [B, H, D, D]  folded coarse read of the completed pages */
   void* workspace;  /* scratch: decode step records and the prefill plan */
   size_t workspace_bytes;
+  /* Regularized association writer (TaoConfig.fine_writer =
+   * "regularized_association", tao_stream.py:72-74, 463-499); all null for
+   * the softmax writer. With them, every seal (tao_write_fine, tao_prefill)
+   * writes C = association_matrix(u^T u, u^T v) of the block into its bank
+   * slot and adds the block's statistics, in seal order, to the pending
+   * sums; with page_c, a completed page's matrix is association_matrix of
+   * those sums, which then restart (the index-only preset keeps summing, as
+   * the reference does). */
+  float* pending_gram;   /* fp32 [B, H, D, D] */
+  float* pending_cross;  /* fp32 [B, H, D, D] */
+  float* stats;          /* fp32 scratch [2][stats_cap * B][H][D][D] */
+  int32_t stats_cap;     /* blocks per pass through the scratch (>= 1) */
 } tao_state_dev;
 
 /* New-token operands: q/k/v/raw_q/raw_k, each [B, T, H, D] bf16 with

@@ -317,9 +317,11 @@ class OracleStream:
     sealed fine z / C, completed page summaries, route ids, position.
     """
 
-    def __init__(self, layer_index, geometry=None):
+    def __init__(self, layer_index, geometry=None, writer="softmax"):
         self.layer = layer_index
         self.g = geometry or Geometry()
+        self.writer = writer           # "softmax" or "regularized_association"
+        self.pending_gram = self.pending_cross = None
         self.position = 0
         self.local = None            # (k, v, raw_k) [B, n, H, D]
         self.fine_z = []             # [B, H, D] per sealed fine
@@ -371,8 +373,22 @@ class OracleStream:
         return min(desired, self.g.fine_tokens, self.g.serve_limit - current)
 
     def seal(self, raw_k, v):
-        """tao_stream.py:435-512 for the softmax writer."""
+        """tao_stream.py:435-512 for the softmax writer and, with
+        writer="regularized_association", the association value matrices
+        (:56-77) and pending statistic sums (:463-499): C = association_matrix
+        of the block's statistics; the statistics add to the pending sums in
+        seal order; a completed page's matrix is association_matrix of the
+        sums, which then restart (never, index-only, as in the reference)."""
         z, c = seal_softmax(raw_k, v)
+        if self.writer == "regularized_association":
+            from . import writers as W
+            gram, cross = W.association_statistics(raw_k, v)
+            c = W.association_matrix(gram, cross)[1]
+            if self.pending_gram is None:
+                self.pending_gram, self.pending_cross = gram, cross
+            else:
+                self.pending_gram = self.pending_gram + gram
+                self.pending_cross = self.pending_cross + cross
         self.fine_z.append(z)
         self.fine_c.append(c)
         self._bank = None
@@ -383,7 +399,12 @@ class OracleStream:
             zs = torch.stack(self.fine_z[start:], 2)
             pz = page_summary(zs)
             self.page_z.append(pz)
-            if not self.g.coarse_index_only:
+            if not self.g.coarse_index_only and self.writer == "regularized_association":
+                from . import writers as W
+                self.page_c.append(W.association_matrix(self.pending_gram,
+                                                        self.pending_cross)[1])
+                self.pending_gram = self.pending_cross = None
+            elif not self.g.coarse_index_only:
                 self.page_c.append(page_coarse_matrix(
                     zs, pz, torch.stack(self.fine_c[start:], 2)))
 
@@ -532,7 +553,7 @@ class OracleStream:
             config = dict(fine_tokens=g.fine_tokens, local_keep=g.local_keep,
                           coarse_group=g.coarse_group, route_period=g.route_period,
                           layer_stagger=g.layer_stagger, budget_root_scale=g.budget_root_scale,
-                          budget_offset=g.budget_offset, fine_writer="softmax",
+                          budget_offset=g.budget_offset, fine_writer=self.writer,
                           coarse_index_only=g.coarse_index_only,
                           q1_page_normalization_memo=False, q1_history_region_graph=False)
         packed = torch.stack(self.fine_c, 2) if self.fine_c else None
@@ -556,8 +577,10 @@ class OracleStream:
             "pending_z": pending,
             "pending_square_mass": None,
             "pending_mass": None,
-            "pending_gram": None,
-            "pending_cross": None,
+            "pending_gram": (None if self.pending_gram is None
+                             else self.pending_gram.to(torch.float32).clone()),
+            "pending_cross": (None if self.pending_cross is None
+                              else self.pending_cross.to(torch.float32).clone()),
             "route_ids": None if self.route_ids is None else tuple(t.clone() for t in self.route_ids),
             "route_key": None,
             "state_version": self.state_version,
@@ -568,7 +591,11 @@ class OracleStream:
     @classmethod
     def from_export(cls, saved, layer_index, geometry=None):
         """Restore from a snapshot dict (tao_stream.py:879-912)."""
-        state = cls(layer_index, geometry)
+        state = cls(layer_index, geometry,
+                    writer=saved.get("config", {}).get("fine_writer", "softmax"))
+        if saved.get("pending_gram") is not None:
+            state.pending_gram = saved["pending_gram"].double().clone()
+            state.pending_cross = saved["pending_cross"].double().clone()
         group = state.g.coarse_group
         state.position = saved["position"]
         state.local = (None if saved["local"] is None

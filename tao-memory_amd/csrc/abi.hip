@@ -4,6 +4,7 @@
 // errors return negative codes, HIP failures their positive hipError_t),
 // translates the plain-pointer structs into kernel parameter blocks and owns
 // the only library-side resources: hipGraphExec objects of the decode step.
+#include <algorithm>
 #include <string>
 
 #include "tao_launch.h"
@@ -23,6 +24,17 @@ int check_hip(hipError_t e, const char* where) {
   return (int)e;
 }
 
+// Regularized association writer (state buffers set, tao_memory.h).
+bool assoc_writer(const tao_state_dev* st) { return st->pending_gram != nullptr; }
+
+int check_assoc(const tao_state_dev* st) {
+  const bool any = st->pending_gram || st->pending_cross || st->stats;
+  if (any && (!st->pending_gram || !st->pending_cross || !st->stats || st->stats_cap < 1))
+    return fail(TAO_E_ARGUMENT,
+                "the regularized writer needs pending_gram, pending_cross and stats (stats_cap >= 1)");
+  return TAO_OK;
+}
+
 int check_state(const tao_state_dev* st) {
   if (!st) return fail(TAO_E_ARGUMENT, "null state");
   if (st->head_dim != 64 && st->head_dim != 128)
@@ -39,6 +51,7 @@ int check_state(const tao_state_dev* st) {
     return fail(TAO_E_ARGUMENT, "page_c and coarse_g must be both set or both null");
   if (st->sel_cap > 512) return fail(TAO_E_CAPACITY, "sel_cap above 512");
   if (st->coarse_group != 8) return fail(TAO_E_SHAPE, "HIP kernels implement coarse_group=8");
+  if (int rc = check_assoc(st)) return rc;
   const tao::WorkspaceLayout lay =
       tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
   if (st->workspace_bytes < lay.plan_off)
@@ -126,6 +139,77 @@ int check_fusion(const tao_fusion* fu) {
   if (fu->dtype != TAO_BF16 && fu->dtype != TAO_FP32)
     return fail(TAO_E_ARGUMENT, "fusion dtype must be bf16 or fp32");
   return TAO_OK;
+}
+
+// The association part of `count` seals (fine slots first_slot ..): block
+// statistics, C^T into the bank slots, the pending sums in seal order and,
+// with page_c, the matrices of the pages these seals complete. The system
+// gram + trace / D I is positive definite for finite inputs (its ridge is
+// positive), so the solve is not checked here.
+hipError_t assoc_seal(const tao_state_dev* st, const tao::TokView& rk, const tao::TokView& v,
+                      int64_t new_base, const int64_t* starts, int first_slot, int count,
+                      hipStream_t s) {
+  const int B = st->batch, H = st->heads, D = st->head_dim;
+  const size_t mats = (size_t)st->stats_cap * B * H;
+  float* gram = st->stats;
+  float* cross = st->stats + mats * D * D;
+  for (int done = 0; done < count; done += st->stats_cap) {
+    const int n = std::min(st->stats_cap, count - done);
+    tao::WriterStatsParams sp{};
+    sp.k = rk.p;
+    sp.v = v.p;
+    sp.k_s[0] = rk.sb; sp.k_s[1] = rk.st; sp.k_s[2] = rk.sh;
+    sp.v_s[0] = v.sb; sp.v_s[1] = v.st; sp.v_s[2] = v.sh;
+    sp.N = n * B;
+    sp.T = st->fine_tokens;
+    sp.H = H;
+    sp.gram = gram;
+    sp.cross = cross;
+    sp.starts = starts + done;
+    sp.new_base = new_base;
+    sp.ring_raw = (const bf16_t*)st->ring_raw;
+    sp.ring_v = (const bf16_t*)st->ring_v;
+    sp.L = st->local_keep + st->fine_tokens;
+    sp.B = B;
+    hipError_t e = tao::launch_writer_stats(sp, D, s);
+    if (e != hipSuccess) return e;
+    tao::AssocSolveParams fp{};
+    fp.gram = gram;
+    fp.cross = cross;
+    fp.count = n * B * H;
+    fp.out = (bf16_t*)st->bank_c;
+    fp.to_slots = 1;
+    fp.B = B;
+    fp.H = H;
+    fp.cap = st->fine_cap;
+    fp.first_slot = first_slot + done;
+    fp.group = st->coarse_group;
+    e = tao::launch_association_solve(fp, D, s);
+    if (e != hipSuccess) return e;
+    tao::AssocPendingParams pp{};
+    pp.gram = gram;
+    pp.cross = cross;
+    pp.pending_gram = st->pending_gram;
+    pp.pending_cross = st->pending_cross;
+    pp.count = n;
+    pp.B = B;
+    pp.H = H;
+    pp.first_slot = first_slot + done;
+    pp.group = st->coarse_group;
+    pp.reset_pages = st->page_c != nullptr;
+    e = tao::launch_assoc_pending(pp, D, s);
+    if (e != hipSuccess) return e;
+    if (st->page_c) {
+      tao::AssocSolveParams pg = fp;
+      pg.out = (bf16_t*)st->page_c;
+      pg.to_slots = 2;
+      pg.cap = st->page_cap;
+      pg.fine_first = first_slot + done;
+      e = tao::launch_association_solve(pg, D, s);
+      if (e != hipSuccess) return e;
+    }
+  }
+  return hipSuccess;
 }
 
 struct DecodeGraph {
@@ -326,7 +410,11 @@ int tao_write_fine(const tao_state_dev* st, const tao_tokens* tok, int64_t new_b
   p.fine_cap = st->fine_cap;
   p.first_slot = first_slot;
   p.count = count;
-  return check_hip(tao::launch_writer(p, st->head_dim, (hipStream_t)stream), "tao_write_fine");
+  p.z_only = assoc_writer(st) ? 1 : 0;
+  hipError_t e = tao::launch_writer(p, st->head_dim, (hipStream_t)stream);
+  if (e == hipSuccess && assoc_writer(st) && count > 0)
+    e = assoc_seal(st, p.rk, p.v, new_base, start_pos, first_slot, count, (hipStream_t)stream);
+  return check_hip(e, "tao_write_fine");
 }
 
 int tao_seal_epilogue(const tao_state_dev* st, int32_t slot, int32_t pages, int32_t recompute,
@@ -551,9 +639,13 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   wp.fine_cap = st->fine_cap;
   wp.first_slot = (int)first_slot;
   wp.count = (int)n_write;
-  wp.z_only = external_values;
+  wp.z_only = external_values || assoc_writer(st);
   e = tao::launch_writer(wp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill writer");
+  if (assoc_writer(st) && n_write > 0) {
+    e = assoc_seal(st, wp.rk, wp.v, pos0, wp.starts, (int)first_slot, (int)n_write, s);
+    if (e != hipSuccess) return check_hip(e, "tao_prefill association writer");
+  }
   // pages
   tao::PagesParams pp{};
   pp.fine_z = (const bf16_t*)st->fine_z;
@@ -568,7 +660,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   pp.count = (int)n_pages;
   e = tao::launch_pages(pp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill pages");
-  if (coarse_values && !external_values) {
+  if (coarse_values && !external_values && !assoc_writer(st)) {
     tao::PageCoarseParams cp{};
     cp.bank = (const bf16_t*)st->bank_c;
     cp.sw = (const bf16_t*)st->fine_sw;

@@ -68,13 +68,32 @@ __global__ __launch_bounds__(kStatThreads) void writer_stats_kernel(WriterStatsP
     for (int i = 0; i < 16; ++i) acc[j][i] = 0.0f;
   float msum = 0.0f, ssum = 0.0f;          // thread tid < D: channel tid
   const int tk = tid / LPT, part = tid % LPT;
+  // ring mode: block n = blk * B + b of a seal (see WriterStatsParams)
+  const bool ring = p.starts != nullptr;
+  int rb = 0, slot0 = 0;
+  long long rel = 0;
+  if (ring) {
+    const long long start = p.starts[n / p.B];
+    rb = n % p.B;
+    rel = start - p.new_base;
+    slot0 = (int)(start % p.L);
+  }
+  auto row_of = [&](const bf16_t* base, const int64_t* st, const bf16_t* ring_base, int t)
+      __attribute__((always_inline)) -> const bf16_t* {
+    if (!ring) return base + n * st[0] + (int64_t)t * st[1] + h * st[2];
+    const long long r = rel + t;
+    if (r >= 0) return base + rb * st[0] + r * st[1] + h * st[2];
+    int slot = slot0 + t;
+    slot = slot >= p.L ? slot - p.L : slot;
+    return ring_base + (((size_t)rb * p.L + slot) * p.H + h) * D;
+  };
   for (int t0 = 0; t0 < p.T; t0 += kStatTokens) {
     const int t = t0 + tk;
     float x[CPL];
     uint32_t vw[CPL / 2];
     if (t < p.T) {
-      const bf16_t* kr = p.k + n * p.k_s[0] + (int64_t)t * p.k_s[1] + h * p.k_s[2] + part * CPL;
-      const bf16_t* vr = p.v + n * p.v_s[0] + (int64_t)t * p.v_s[1] + h * p.v_s[2] + part * CPL;
+      const bf16_t* kr = row_of(p.k, p.k_s, p.ring_raw, t) + part * CPL;
+      const bf16_t* vr = row_of(p.v, p.v_s, p.ring_v, t) + part * CPL;
 #pragma unroll
       for (int c = 0; c < CPL / 8; ++c) {
         const uint4 ku = *(const uint4*)(kr + 8 * c), vu = *(const uint4*)(vr + 8 * c);
@@ -174,6 +193,8 @@ __global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocS
   SolveSmem<D>& sm = *reinterpret_cast<SolveSmem<D>*>(solve_smem);
   const int mat = blockIdx.x;
   const int tid = threadIdx.x;
+  const int blk = p.to_slots ? mat / (p.B * p.H) : 0;
+  if (p.to_slots == 2 && (p.fine_first + blk) % p.group != p.group - 1) return;   // uniform
   const float* g = p.gram + (size_t)mat * D * D;
   const float* c = p.cross + (size_t)mat * D * D;
   // ridge = trace / D
@@ -223,8 +244,16 @@ __global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocS
     }
   }
   __syncthreads();
-  bf16_t* out = p.out + (size_t)mat * D * D;
-  for (int i = tid; i < D * D; i += kSolveThreads) out[i] = f2bf(sm.x[i / D][i % D]);
+  if (!p.to_slots) {
+    bf16_t* out = p.out + (size_t)mat * D * D;
+    for (int i = tid; i < D * D; i += kSolveThreads) out[i] = f2bf(sm.x[i / D][i % D]);
+    return;
+  }
+  // C^T into a bank (fine) or page slot: dst[e][d] = X[d][e]
+  const int b = (mat / p.H) % p.B, h = mat % p.H;
+  const int slot = p.to_slots == 1 ? p.first_slot + blk : (p.fine_first + blk) / p.group;
+  bf16_t* dst = p.out + (((size_t)b * p.H + h) * p.cap + slot) * D * D;
+  for (int i = tid; i < D * D; i += kSolveThreads) dst[i] = f2bf(sm.x[i % D][i / D]);
 }
 
 template <int D>
@@ -316,7 +345,36 @@ __global__ __launch_bounds__(256) void feature_coeff_kernel(FeatureCoeffParams p
   }
 }
 
+__global__ __launch_bounds__(256) void assoc_pending_kernel(AssocPendingParams p, int dd) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per = (int64_t)p.B * p.H * dd;
+  if (i >= per) return;
+  const int64_t bh = i / dd, e = i % dd;                // bh = b * H + h
+  float pg = p.pending_gram[i], pc = p.pending_cross[i];
+  for (int blk = 0; blk < p.count; ++blk) {
+    const int slot = p.first_slot + blk;
+    const int64_t at = ((int64_t)blk * p.B * p.H + bh) * dd + e;   // (blk, b, h) = blk * B * H + bh
+    const bool fresh = p.reset_pages ? slot % p.group == 0 : slot == 0;
+    pg = fresh ? p.gram[at] : pg + p.gram[at];
+    pc = fresh ? p.cross[at] : pc + p.cross[at];
+    if (p.reset_pages && slot % p.group == p.group - 1) {
+      p.gram[at] = pg;
+      p.cross[at] = pc;
+    }
+  }
+  p.pending_gram[i] = pg;
+  p.pending_cross[i] = pc;
+}
+
 }  // namespace
+
+hipError_t launch_assoc_pending(const AssocPendingParams& p, int head_dim, hipStream_t s) {
+  const int64_t n = (int64_t)p.B * p.H * head_dim * head_dim;
+  if (n <= 0 || p.count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(assoc_pending_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p,
+                     head_dim * head_dim);
+  return hipGetLastError();
+}
 
 hipError_t launch_writer_stats(const WriterStatsParams& p, int head_dim, hipStream_t s) {
   const dim3 grid((unsigned)(p.N * p.H));

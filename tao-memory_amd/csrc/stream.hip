@@ -112,9 +112,10 @@ int post_step(Stream* s, const tao_tokens* tok, void* stream, int* sealed) {
     // New page weights and segment weights: refold the current route.
     if (!rc) rc = tao_fold_route(&s->st, s->route_size, stream);
     // A completed page: its value matrix, then the coarse read over all pages.
+    // (The regularized writer's seal already wrote the page's matrix.)
     if (!rc && s->st.page_c && fines % c.coarse_group == c.coarse_group - 1) {
       const int32_t page = (int32_t)(fines / c.coarse_group);
-      rc = tao_page_coarse(&s->st, page, 1, stream);
+      if (!s->st.pending_gram) rc = tao_page_coarse(&s->st, page, 1, stream);
       if (!rc) rc = tao_fold_coarse(&s->st, page + 1, stream);
     }
     if (rc) return rc;

@@ -327,6 +327,13 @@ struct WriterStatsParams {
   int64_t k_s[3], v_s[3];
   int N, T, H, mode;
   float* gram; float* cross; float* mass;
+  // Ring mode (starts != null): block n = blk * B + b is the 256-token block
+  // starting at absolute position starts[blk] of batch row b; rows at or
+  // after new_base come from k / v (strides: batch, token, head), older rows
+  // from the token ring (slot = position mod L).
+  const int64_t* starts; int64_t new_base;
+  const bf16_t* ring_raw; const bf16_t* ring_v;
+  int L, B;
 };
 hipError_t launch_writer_stats(const WriterStatsParams& p, int head_dim, hipStream_t s);
 
@@ -335,6 +342,12 @@ struct AssocSolveParams {
   int count;
   bf16_t* out;            // [count, D, D] rows d, columns e
   int32_t* info;          // nullable [count]
+  // to_slots 1: matrix (blk, b, h) = (mat / (B H), mat / H % B, mat % H)
+  // goes transposed (C^T[e][d]) into slot first_slot + blk of out viewed as
+  // [B, H, cap, D, D]; 2: the same for page first_slot + blk ... only blocks
+  // whose fine slot (fine_first + blk) completes a page (slot % group ==
+  // group - 1), into page slot / group.
+  int to_slots, B, H, cap, first_slot, fine_first, group;
 };
 hipError_t launch_association_solve(const AssocSolveParams& p, int head_dim, hipStream_t s);
 
@@ -348,6 +361,17 @@ hipError_t launch_structured_matrix(const StructuredParams& p, int head_dim, hip
 
 hipError_t launch_chrono_sum(const float* x, float* out, int64_t outer, int fines, int64_t inner,
                              hipStream_t s);
+
+// Pending statistics of the regularized writer, in seal order: for block blk
+// (fine slot first_slot + blk) pending = stats (first fine of a pending run)
+// or pending + stats; a block that completes a page (reset_pages) has its
+// stats entry overwritten by the page's sums, then the run restarts.
+struct AssocPendingParams {
+  float* gram; float* cross;            // [count * B][H][D][D] (in place)
+  float* pending_gram; float* pending_cross;   // [B][H][D][D]
+  int count, B, H, first_slot, group, reset_pages;
+};
+hipError_t launch_assoc_pending(const AssocPendingParams& p, int head_dim, hipStream_t s);
 
 // h [B, T, H, D] (strides h_s), read_z element strides z_s (b, t, h, page),
 // zero for broadcast axes; out bf16 [B, T, H, P, D] contiguous.

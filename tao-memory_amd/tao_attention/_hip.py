@@ -33,6 +33,7 @@ class StateDev(ctypes.Structure):
         ("fold_g", _vp), ("fold_den", _vp),
         ("page_c", _vp), ("coarse_g", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
+        ("pending_gram", _vp), ("pending_cross", _vp), ("stats", _vp), ("stats_cap", _i32),
     ]
 
 

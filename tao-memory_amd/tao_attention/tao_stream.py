@@ -35,6 +35,10 @@ from .config import TaoConfig
 
 DEFAULT_CONFIG = TaoConfig()
 _QTILE = 256
+_STATS_CAP = 8          # blocks per statistics pass of the regularized writer
+# Fine writers the stream implements: the softmax writer and the regularized
+# association writer (same z and read, association value matrices).
+_STREAM_WRITERS = ("softmax", "regularized_association")
 
 
 class _DeviceState:
@@ -60,6 +64,17 @@ class _DeviceState:
         self.coarse_g = (torch.zeros((batch, heads, head_dim, head_dim), dtype=torch.float32,
                                      device=device) if self.coarse_values else None)
         self.page_c = None
+        # Regularized association writer: the pending page's fp32 statistic
+        # sums (the reference's pending_gram / pending_cross) and scratch for
+        # the statistics of up to _STATS_CAP blocks per pass; fixed size.
+        self.association = config.fine_writer == "regularized_association"
+        self.pending_gram = self.pending_cross = self.stats = None
+        if self.association:
+            dd = (batch, heads, head_dim, head_dim)
+            self.pending_gram = torch.zeros(dd, dtype=torch.float32, device=device)
+            self.pending_cross = torch.zeros(dd, dtype=torch.float32, device=device)
+            self.stats = torch.empty((2, _STATS_CAP * batch, heads, head_dim, head_dim),
+                                     dtype=torch.float32, device=device)
         self.generation = 0          # bumped whenever the buffers move
         self.fine_cap = 0
         self._allocate(fine_cap, copy_fines=0)
@@ -137,6 +152,10 @@ class _DeviceState:
         st.fold_g, st.fold_den = self.fold_g.data_ptr(), self.fold_den.data_ptr()
         if self.coarse_values:
             st.page_c, st.coarse_g = self.page_c.data_ptr(), self.coarse_g.data_ptr()
+        if self.association:
+            st.pending_gram = self.pending_gram.data_ptr()
+            st.pending_cross = self.pending_cross.data_ptr()
+            st.stats, st.stats_cap = self.stats.data_ptr(), _STATS_CAP
         st.workspace = self.workspace.data_ptr()
         st.workspace_bytes = self.workspace.numel()
         return st
@@ -309,8 +328,9 @@ class StreamCache:
 
     def _check_supported(self, q):
         cfg = self.config
-        if cfg.fine_writer != "softmax":
-            raise NotImplementedError("the HIP path implements the softmax fine writer")
+        if cfg.fine_writer not in _STREAM_WRITERS:
+            raise NotImplementedError(
+                f"the HIP streaming path implements the fine writers {_STREAM_WRITERS}")
         if cfg.fine_tokens != 256 or cfg.local_keep != 512:
             raise NotImplementedError("the HIP path implements fine_tokens=256, local_keep=512")
         if q.dtype != torch.bfloat16:
@@ -723,6 +743,13 @@ class StreamCache:
             for j in range(pending):
                 pending_z.append(dev.fine_z[:, :, completed * group + j].clone())
         local = self._local_window()
+        # The regularized writer's pending statistics (fp32 [B, H, D, D]):
+        # None until the first seal and, with page values, after each page
+        # completion, as the reference keeps them (tao_stream.py:463-499).
+        pending_gram = pending_cross = None
+        if dev is not None and dev.association and fines and (pending or not dev.coarse_values):
+            pending_gram = dev.pending_gram.clone()
+            pending_cross = dev.pending_cross.clone()
         return {
             "layer_index": self.layer_index,
             "config": cfg.export(),
@@ -736,8 +763,8 @@ class StreamCache:
             "pending_z": pending_z,
             "pending_square_mass": None,
             "pending_mass": None,
-            "pending_gram": None,
-            "pending_cross": None,
+            "pending_gram": pending_gram,
+            "pending_cross": pending_cross,
             "route_ids": route_ids,
             "route_key": None,
             "state_version": fines,
@@ -767,6 +794,7 @@ class StreamCache:
             packed = move(packed)
             pages = [(move(pz), move(pc), move(fz)) for pz, pc, fz in pages]
             pending_z = [move(z) for z in pending_z]
+        pending_stats = (saved.get("pending_gram"), saved.get("pending_cross"))
         fines = len(pages) * config.coarse_group + len(pending_z)
         if fines != schedule.fines_at(position, config):
             raise ValueError("snapshot fine count does not match its position")
@@ -785,6 +813,19 @@ class StreamCache:
         slots = torch.arange(position - n, position, device=dev.device) % dev.L
         for buf, src in zip((dev.ring_k, dev.ring_v, dev.ring_raw), local):
             buf.index_copy_(1, slots, src.to(torch.bfloat16))
+        if dev.association:
+            gram, cross = pending_stats
+            if (gram is None) != (cross is None):
+                raise ValueError("snapshot has only one of pending_gram / pending_cross")
+            if gram is None and fines and (not dev.coarse_values or fines % group):
+                raise ValueError("regularized-writer snapshot lacks its pending statistics")
+            if gram is not None:
+                dev.pending_gram.copy_(gram.to(dev.device, torch.float32))
+                dev.pending_cross.copy_(cross.to(dev.device, torch.float32))
+            if dev.coarse_values and any(pc is None for _, pc, _ in pages):
+                raise NotImplementedError(
+                    "page value matrices of the regularized writer cannot be rebuilt from a "
+                    "snapshot without them (its page statistics are not part of the schema)")
         if fines:
             dev.bank[:, :, :fines].copy_(packed.transpose(-1, -2))
             rebuild = []

@@ -213,3 +213,60 @@ def test_full_sequence_regularized_writer(device, tokens, heads, width, index_on
     with pytest.raises(NotImplementedError):
         tao_attention(qg, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.to(device),
                       fusion_b=fb.to(device), alpha=0.5, config=cfg)
+
+
+@pytest.mark.parametrize("index_only,width", [(False, 64), (True, 128)])
+def test_stream_regularized_writer(device, index_only, width):
+    """Streaming prefill and decode with fine_writer="regularized_association":
+    seals inside a prefill call and in the decode driver (the step at 2559
+    seals the 8th fine and completes page 0), the association fine and page
+    matrices, the pending statistics, route ids bit-exact, outputs within the
+    bf16 tolerance of the oracle; export -> import continues identically."""
+    from oracle import tao_oracle as O
+    from tao_attention import (StreamCache, TaoConfig, new_state, tao_attention_decode,
+                               tao_attention_prefill)
+    heads, tokens = 2, 2826
+    g = torch.Generator().manual_seed(61 + width)
+    xs = [torch.randn(1, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
+    fa = torch.randn(heads, width, 3, generator=g) * 0.02
+    fb = torch.randn(heads, width, 3, generator=g) * 0.02
+    cfg = TaoConfig(fine_writer="regularized_association", coarse_index_only=index_only)
+    geo = O.Geometry.from_config(cfg)
+    splits = [2540] + [1] * 30 + [250] + [1] * 5
+    d = [x.to(device) for x in xs]
+    state = new_state(0, cfg)
+    ora = O.OracleStream(0, geo, writer="regularized_association")
+    outs, refs, start = [], [], 0
+    for w in splits:
+        sl = slice(start, start + w)
+        fn = tao_attention_decode if w == 1 else tao_attention_prefill
+        out, state = fn(*(x[:, sl] for x in d[:3]), raw_q=d[3][:, sl], raw_k=d[4][:, sl],
+                        fusion_a=fa.to(device), fusion_b=fb.to(device), alpha=0.5,
+                        state=state, position=state.get_pos())
+        outs.append(out.cpu())
+        refs.append(ora.prefill(*(x[:, sl] for x in xs), fa, fb, 0.5))
+        start += w
+    torch.testing.assert_close(torch.cat(outs, 1).float(), torch.cat(refs, 1).float(),
+                               atol=2e-2, rtol=2e-2)
+    snap, osnap = state.export(), ora.export(config=cfg.export())
+    assert len(snap["pending_z"]) == 1 and len(snap["pages"]) == 1
+    assert torch.equal(snap["route_ids"][1].cpu(), osnap["route_ids"][1])
+    torch.testing.assert_close(snap["packed_fine_c"].cpu().float(),
+                               osnap["packed_fine_c"].float(), atol=2e-2, rtol=2e-2)
+    pc, opc = snap["pages"][0][1], osnap["pages"][0][1]
+    assert (pc is None) == index_only and (opc is None) == index_only
+    if pc is not None:
+        torch.testing.assert_close(pc.cpu().float(), opc.float(), atol=2e-2, rtol=2e-2)
+    for key in ("pending_gram", "pending_cross"):
+        got, want = snap[key], osnap[key]
+        assert got is not None and got.dtype == torch.float32
+        close(got, want, 1e-3)
+    restored = StreamCache.from_export(snap)
+    tok = [x[:, tokens - 1:tokens] for x in d]
+    nxt = []
+    for s in (state, restored):
+        out, _ = tao_attention_decode(*tok[:3], raw_q=tok[3], raw_k=tok[4],
+                                      fusion_a=fa.to(device), fusion_b=fb.to(device),
+                                      alpha=0.5, state=s, position=s.get_pos())
+        nxt.append(out)
+    assert torch.equal(nxt[0], nxt[1])

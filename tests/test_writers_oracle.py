@@ -138,3 +138,50 @@ def test_selected_numerator_backward_brute_force():
     assert (dc.double() - cb.grad).abs().max() <= 2e-2 * cb.grad.abs().max()
     # a mistake in the shared-bank index (b % BB) or the id routing is O(1)
     assert not torch.allclose(dc.double(), cb.grad.roll(1, 2), atol=0.5)
+
+
+def test_oracle_stream_regularized_writer_pages_and_pending():
+    """OracleStream with the regularized writer: fine C = association_matrix
+    of the block's statistics; a completed page's C equals association_matrix
+    of the statistics of its 2048 tokens taken at once (the statistics are
+    sums over tokens, so the in-order sum of its eight fines' must agree);
+    the pending sums restart after a page with page values and keep summing
+    index-only; export carries them."""
+    from oracle import tao_oracle as O
+    g = torch.Generator().manual_seed(7)
+    t, h, d = 2900, 2, 8
+    xs = [torch.randn(1, t, h, d, generator=g).to(BF16) for _ in range(5)]
+    fa = torch.randn(h, d, 3, generator=g) * 0.02
+    fb = torch.randn(h, d, 3, generator=g) * 0.02
+    for index_only in (False, True):
+        s = O.OracleStream(0, O.Geometry(coarse_index_only=index_only),
+                           writer="regularized_association")
+        pos = 0
+        while pos < t:
+            w = s.next_chunk(t - pos)
+            s.prefill(*(x[:, pos:pos + w] for x in xs), fa, fb, 0.5)
+            pos += w
+        rk, v = xs[4], xs[2]
+        fines = len(s.fine_z)
+        assert fines == 8 + 1
+        for f in (0, 5, 8):
+            blk = slice(f * 256, (f + 1) * 256)
+            want = W.association_matrix(*W.association_statistics(rk[:, blk], v[:, blk]))[1]
+            assert torch.equal(s.fine_c[f], want)
+        page = W.association_statistics(rk[:, :2048], v[:, :2048])
+        if index_only:
+            assert s.page_c == []
+            total = W.association_statistics(rk[:, :fines * 256], v[:, :fines * 256])
+            assert torch.allclose(s.pending_gram, total[0], rtol=1e-12, atol=1e-12)
+        else:
+            want = W.association_matrix(*page)[1]
+            assert (s.page_c[0].double() - want.double()).abs().max() <= \
+                2 ** -8 * want.double().abs().max()
+            last = W.association_statistics(rk[:, 2048:2304], v[:, 2048:2304])
+            assert torch.allclose(s.pending_gram, last[0], rtol=1e-12, atol=1e-12)
+        snap = s.export()
+        assert snap["config"]["fine_writer"] == "regularized_association"
+        assert snap["pending_gram"].dtype == torch.float32
+        back = O.OracleStream.from_export(snap, 0, O.Geometry(coarse_index_only=index_only))
+        assert back.writer == "regularized_association"
+        assert torch.equal(back.pending_gram.float(), snap["pending_gram"])

@@ -513,6 +513,57 @@ def run_full_sequence(torch, args, device):
                 width=d)
 
 
+def run_writers(torch, device):
+    """The non-preset writers' operators at the configs[2] block shape: the
+    62 sealed 256-token blocks of a 16K prefill, H32, D128, taken as one batch
+    of association_statistics + association_matrix (the regularized writer's
+    seal work of that prefill), and selected_fine_numerator over 4096 queries
+    with M = 18 of those 62 fines. Event-timed means of 5 calls after 2."""
+    from tao_attention.association_writer import association_matrix, association_statistics
+    from tao_attention.indirect_fine import selected_fine_numerator
+    blocks, t, h, d = 62, 256, 32, 128
+    g = torch.Generator(device=device).manual_seed(13)
+    k = torch.randn(blocks, t, h, d, generator=g, device=device).to(torch.bfloat16)
+    v = torch.randn(blocks, t, h, d, generator=g, device=device).to(torch.bfloat16)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, runs=5):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(runs):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / runs * 1e-3
+
+    with torch.no_grad():
+        stats_s = timed(lambda: association_statistics(k, v))
+        gram, cross = association_statistics(k, v)
+        solve_s = timed(lambda: association_matrix(gram, cross, unchecked=True))
+        bank = association_matrix(gram, cross, unchecked=True).unsqueeze(0).permute(0, 2, 1, 3, 4)
+        bank = bank.contiguous()                                   # [1, H, 62, D, D]
+        q, m = 4096, 18
+        channel = (torch.randn(1, q, h, m, d, generator=g, device=device) * 0.1).to(torch.bfloat16)
+        ids = torch.argsort(torch.rand(q * h, blocks, generator=g, device=device),
+                            dim=-1)[:, :m].reshape(1, q, h, m)   # distinct ids per query
+        read_s = timed(lambda: selected_fine_numerator(channel, ids, bank))
+    stats_flops = blocks * h * 2 * (2 * t * d * d)          # U^T U and U^T V
+    read_flops = q * h * m * 2 * d * d
+    read_bytes = h * blocks * d * d * 2 + q * h * m * (d * 2 + 8) + q * h * d * 2
+    return {
+        "workload": "62 blocks x 256 tokens x H32 x D128 bf16 (configs[2] seals); selected "
+                    "numerator 4096 queries x H32 x M18 over those 62 fines",
+        "statistics_ms": round(stats_s * 1e3, 4),
+        "statistics_tflops": round(stats_flops / stats_s / 1e12, 1),
+        "cholesky_solve_ms": round(solve_s * 1e3, 4),
+        "solves": blocks * h,
+        "selected_numerator_ms": round(read_s * 1e3, 4),
+        "selected_numerator_tflops": round(read_flops / read_s / 1e12, 1),
+        "selected_numerator_GBs": round(read_bytes / read_s / 1e9, 1)}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -575,6 +626,7 @@ def main():
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--full-sequence-tokens", type=int, default=8192)
     ap.add_argument("--no-full-sequence", action="store_true")
+    ap.add_argument("--no-writers", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB 4 times (a plain "
                          "copy kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -721,6 +773,10 @@ def main():
         log(f"full-sequence forward: {fs['seconds'] * 1e3:.3f} ms, "
             f"{fs['batch'] * fs['tokens'] / fs['seconds']:.1f} tok/s; forward + backward "
             f"{fs['train_seconds'] * 1e3:.3f} ms")
+    if not args.no_writers:
+        log("non-preset writer operators (configs[2] block shape)")
+        result["writers"] = run_writers(torch, device)
+        log(f"writers: {result['writers']}")
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, torch eager on host cores)")
         xs_cpu, _, _ = make_tokens(torch, 1 + 3 * args.cpu_steps, heads, width, 7, device)

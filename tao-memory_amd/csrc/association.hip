@@ -16,7 +16,8 @@
 //   [D, D] pair. The system gram + (trace / D) I is factored in LDS by a
 //   right-looking Cholesky (column j: pivot, column scale, trailing rank-one
 //   update, two barriers), then cross is solved in place by forward and back
-//   substitution, one thread per right-hand-side column; C = bf16(X).
+//   substitution in right-looking form (row i finished, then removed from the
+//   other rows by all threads); C = bf16(X).
 // structured_matrix_kernel (structured_writer.py:16-34): one workgroup per
 //   pair; per-channel vectors and their sums in LDS, then thread e walks
 //   column e of cross twice (hb and mass . hb, then the result).
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(kStatThreads) void writer_stats_kernel(WriterStatsP
   }
 }
 
-constexpr int kSolveThreads = 256;
+constexpr int kSolveThreads = 1024;   // one workgroup per CU at D128 (132 KB LDS): 16 waves
 
 template <int D>
 struct SolveSmem {
@@ -230,20 +231,30 @@ __global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocS
   }
   __syncthreads();
   if (p.info && tid == 0) p.info[mat] = bad;
-  // forward then back substitution, thread per column e
-  for (int e = tid; e < D; e += kSolveThreads) {
-    for (int i = 0; i < D; ++i) {
-      float s = sm.x[i][e];
-      for (int k = 0; k < i; ++k) s = fmaf(-sm.a[i][k], sm.x[k][e], s);
-      sm.x[i][e] = s / sm.a[i][i];
+  // Forward (L Y = X) then back (L^T X = Y) substitution, right-looking:
+  // step i finishes row i of every right-hand side, then all threads remove
+  // it from the remaining rows (independent updates, two barriers a step).
+  for (int i = 0; i < D; ++i) {
+    const float piv = sm.a[i][i];
+    for (int e = tid; e < D; e += kSolveThreads) sm.x[i][e] = sm.x[i][e] / piv;
+    __syncthreads();
+    const int R = D - i - 1;
+    for (int idx = tid; idx < R * D; idx += kSolveThreads) {
+      const int k = i + 1 + idx / D, e = idx % D;
+      sm.x[k][e] = fmaf(-sm.a[k][i], sm.x[i][e], sm.x[k][e]);
     }
-    for (int i = D - 1; i >= 0; --i) {
-      float s = sm.x[i][e];
-      for (int k = i + 1; k < D; ++k) s = fmaf(-sm.a[k][i], sm.x[k][e], s);
-      sm.x[i][e] = s / sm.a[i][i];
-    }
+    __syncthreads();
   }
-  __syncthreads();
+  for (int i = D - 1; i >= 0; --i) {
+    const float piv = sm.a[i][i];
+    for (int e = tid; e < D; e += kSolveThreads) sm.x[i][e] = sm.x[i][e] / piv;
+    __syncthreads();
+    for (int idx = tid; idx < i * D; idx += kSolveThreads) {
+      const int k = idx / D, e = idx % D;
+      sm.x[k][e] = fmaf(-sm.a[i][k], sm.x[i][e], sm.x[k][e]);
+    }
+    __syncthreads();
+  }
   if (!p.to_slots) {
     bf16_t* out = p.out + (size_t)mat * D * D;
     for (int i = tid; i < D * D; i += kSolveThreads) out[i] = f2bf(sm.x[i / D][i % D]);

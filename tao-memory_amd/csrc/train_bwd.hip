@@ -163,8 +163,14 @@ __global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
 // P = 2^(s c - lse2) from the forward's saved log2-sum-exp (c = log2 e /
 // sqrt(D)), dS = P (dP - delta), dP = dO V^T; dQ = dS K / sqrt(D),
 // dK = dS^T Q / sqrt(D), dV = P^T dO.
-constexpr int kBwdWaves = 4;
-constexpr int kBwdThreads = 64 * kBwdWaves;
+// dK / dV: at D64, 256 keys (one tile) per workgroup, so each staged query
+// block serves 8 waves of keys; D128 keeps 128 keys (4 waves) within 256
+// VGPRs per lane.
+template <int D> constexpr int kDkvWaves = D == 64 ? 8 : 4;
+template <int D> constexpr int kDkvThreads = 64 * kDkvWaves<D>;
+// dQ likewise: 256 queries per workgroup at D64, 128 at D128.
+template <int D> constexpr int kDqWaves = D == 64 ? 8 : 4;
+template <int D> constexpr int kDqThreads = 64 * kDqWaves<D>;
 constexpr int kBwdKeys = 64;          // keys per staged block (dQ pass)
 constexpr int kBwdQ = 64;             // queries per staged block (dK/dV pass)
 
@@ -186,16 +192,16 @@ struct DqSmem {
 };
 
 template <int D>
-__global__ __launch_bounds__(kBwdThreads) void attn_bwd_dq_kernel(AttnBwdParams p) {
+__global__ __launch_bounds__(kDqThreads<D>) void attn_bwd_dq_kernel(AttnBwdParams p) {
   __shared__ DqSmem<D> sm;
   constexpr int CH = D / 8, DT = D / 32, KK = D / 16;
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   const int b = bh / p.H, h = bh % p.H;
-  const long long first = (long long)(blockIdx.x / BH) * (kBwdWaves * 32);
+  const long long first = (long long)(blockIdx.x / BH) * (kDqWaves<D> * 32);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 31, hl = lane >> 5;
-  const int count = (int)min((long long)kBwdWaves * 32, (long long)p.T - first);
+  const int count = (int)min((long long)kDqWaves<D> * 32, (long long)p.T - first);
   const int nq = min(max(count - wave * 32, 0), 32);
   const long long qtok = first + (nq > 0 ? wave * 32 + min(li, nq - 1) : 0);
   const long long wave_first = first + wave * 32, wave_last = wave_first + nq - 1;
@@ -214,27 +220,42 @@ __global__ __launch_bounds__(kBwdThreads) void attn_bwd_dq_kernel(AttnBwdParams 
   const size_t qrowi = ((size_t)b * p.T + qtok) * p.H + h;
   const float lse2 = p.lse[qrowi], dlt = p.delta[qrowi];
   const long long ws = window_start(qtok, p.ft, p.keep);
+  const int ws_last = (int)window_start(wave_last, p.ft, p.keep);   // latest window start
   const float scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)D));
   floatx16 acc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+  // The next key block's rows wait in registers while this one computes.
+  constexpr int KJ = kBwdKeys * CH / kDqThreads<D>;
+  static_assert(KJ * kDqThreads<D> == kBwdKeys * CH, "whole jobs per thread");
+  uint4 kpre[KJ], vpre[KJ];
+  auto fetch = [&](long long kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      const int job = tid + j * kDqThreads<D>, r = job / CH, c = job % CH;
+      kpre[j] = make_uint4(0, 0, 0, 0);
+      vpre[j] = make_uint4(0, 0, 0, 0);
+      if (kb + r < kend) {
+        kpre[j] = *(const uint4*)(p.k.p + b * p.k.sb + (kb + r) * p.k.st + h * p.k.sh + c * 8);
+        vpre[j] = *(const uint4*)(p.v.p + b * p.v.sb + (kb + r) * p.v.st + h * p.v.sh + c * 8);
+      }
+    }
+  };
+  fetch(kstart);
   for (long long kb = kstart; kb < kend; kb += kBwdKeys) {
     __syncthreads();
-    for (int job = tid; job < kBwdKeys * CH; job += kBwdThreads) {
-      const int r = job / CH, c = job % CH;
-      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-      if (kb + r < kend) {
-        kv = *(const uint4*)(p.k.p + b * p.k.sb + (kb + r) * p.k.st + h * p.k.sh + c * 8);
-        vv = *(const uint4*)(p.v.p + b * p.v.sb + (kb + r) * p.v.st + h * p.v.sh + c * 8);
-      }
-      *(uint4*)&sm.k[r][c * 8] = kv;
-      *(uint4*)&sm.v[r][c * 8] = vv;
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      const int job = tid + j * kDqThreads<D>, r = job / CH, c = job % CH;
+      *(uint4*)&sm.k[r][c * 8] = kpre[j];
+      *(uint4*)&sm.v[r][c * 8] = vpre[j];
     }
     __syncthreads();
+    if (kb + kBwdKeys < kend) fetch(kb + kBwdKeys);      // overlaps the work below
     // K^T: job = (channel chunk c, key pair)
-    for (int job = tid; job < (kBwdKeys / 2) * CH; job += kBwdThreads) {
+    for (int job = tid; job < (kBwdKeys / 2) * CH; job += kDqThreads<D>) {
       const int t0 = 2 * (job % (kBwdKeys / 2)), c = job / (kBwdKeys / 2);
       const uint4 ua = *(const uint4*)&sm.k[t0][c * 8];
       const uint4 ub = *(const uint4*)&sm.k[t0 + 1][c * 8];
@@ -261,16 +282,31 @@ __global__ __launch_bounds__(kBwdThreads) void attn_bwd_dq_kernel(AttnBwdParams 
         dp[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, oreg[kk], dp[sub], 0, 0, 0);
       }
     }
-    // S^T layout: lane holds query li, keys 8 (i / 4) + 4 hl + i % 4 of each sub-tile.
+    // S^T layout: lane holds query li, keys 8 (i / 4) + 4 hl + i % 4 of each
+    // sub-tile. A sub-tile wholly inside every query's window (and before
+    // every query) needs no mask; the others test 32-bit positions.
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+    for (int sub = 0; sub < 2; ++sub) {
+      const int k_lo = (int)(kb + sub * 32);
+      const bool full = nq == 32 && k_lo + 31 <= (int)wave_first && k_lo >= ws_last &&
+                        k_lo + 31 < (int)kend;                         // wave-uniform
+      if (full) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const long long key = kb + sub * 32 + 8 * (i / 4) + 4 * hl + (i % 4);
-        const bool ok = li < nq && key <= qtok && key >= ws && key < kend;
-        const float pv = ok ? __builtin_amdgcn_exp2f(fmaf(s[sub][i], scale_log2, -lse2)) : 0.0f;
-        s[sub][i] = pv * (dp[sub][i] - dlt);            // dS^T
+        for (int i = 0; i < 16; ++i) {
+          const float pv = __builtin_amdgcn_exp2f(fmaf(s[sub][i], scale_log2, -lse2));
+          s[sub][i] = pv * (dp[sub][i] - dlt);          // dS^T
+        }
+      } else {
+        const int qt = (int)qtok, wsi = (int)ws, ke = (int)kend;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = k_lo + 8 * (i / 4) + 4 * hl + (i % 4);
+          const bool ok = li < nq && key <= qt && key >= wsi && key < ke;
+          const float pv = ok ? __builtin_amdgcn_exp2f(fmaf(s[sub][i], scale_log2, -lse2)) : 0.0f;
+          s[sub][i] = pv * (dp[sub][i] - dlt);
+        }
       }
+    }
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
@@ -317,16 +353,16 @@ struct DkvSmem {
 };
 
 template <int D>
-__global__ __launch_bounds__(kBwdThreads) void attn_bwd_dkv_kernel(AttnBwdParams p) {
+__global__ __launch_bounds__(kDkvThreads<D>) void attn_bwd_dkv_kernel(AttnBwdParams p) {
   __shared__ DkvSmem<D> sm;
   constexpr int CH = D / 8, DT = D / 32, KK = D / 16;
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   const int b = bh / p.H, h = bh % p.H;
-  const long long first = (long long)(blockIdx.x / BH) * (kBwdWaves * 32);
+  const long long first = (long long)(blockIdx.x / BH) * (kDkvWaves<D> * 32);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 31, hl = lane >> 5;
-  const int count = (int)min((long long)kBwdWaves * 32, (long long)p.T - first);
+  const int count = (int)min((long long)kDkvWaves<D> * 32, (long long)p.T - first);
   const int nk = min(max(count - wave * 32, 0), 32);
   const long long ktok = first + (nk > 0 ? wave * 32 + min(li, nk - 1) : 0);
   const long long qend = min((long long)p.T, ((first >> 8) + 1) * kFt + kKeep);
@@ -346,26 +382,45 @@ __global__ __launch_bounds__(kBwdThreads) void attn_bwd_dkv_kernel(AttnBwdParams
   for (int t = 0; t < DT; ++t)
 #pragma unroll
     for (int i = 0; i < 16; ++i) { dk[t][i] = 0.0f; dv[t][i] = 0.0f; }
-  for (long long qb = first; qb < qend; qb += kBwdQ) {
-    __syncthreads();
-    for (int job = tid; job < kBwdQ * CH; job += kBwdThreads) {
-      const int r = job / CH, c = job % CH;
-      uint4 qv = make_uint4(0, 0, 0, 0), ov = make_uint4(0, 0, 0, 0);
+  // The next query block's rows wait in registers while this one computes.
+  constexpr int QJ = kBwdQ * CH / kDkvThreads<D>;
+  static_assert(QJ * kDkvThreads<D> == kBwdQ * CH, "whole jobs per thread");
+  uint4 qpre[QJ], opre[QJ];
+  float lpre = 0.0f, dpre = 0.0f;
+  auto fetch = [&](long long qb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < QJ; ++j) {
+      const int job = tid + j * kDkvThreads<D>, r = job / CH, c = job % CH;
+      qpre[j] = make_uint4(0, 0, 0, 0);
+      opre[j] = make_uint4(0, 0, 0, 0);
       if (qb + r < qend) {
-        qv = *(const uint4*)(p.q.p + b * p.q.sb + (qb + r) * p.q.st + h * p.q.sh + c * 8);
-        ov = *(const uint4*)(p.dout + (((size_t)b * p.T + qb + r) * p.H + h) * D + c * 8);
+        qpre[j] = *(const uint4*)(p.q.p + b * p.q.sb + (qb + r) * p.q.st + h * p.q.sh + c * 8);
+        opre[j] = *(const uint4*)(p.dout + (((size_t)b * p.T + qb + r) * p.H + h) * D + c * 8);
       }
-      *(uint4*)&sm.q[r][c * 8] = qv;
-      *(uint4*)&sm.o[r][c * 8] = ov;
     }
     if (tid < kBwdQ) {
       const long long qq = qb + tid;
       const size_t row = ((size_t)b * p.T + (qq < qend ? qq : qb)) * p.H + h;
-      sm.lse[tid] = qq < qend ? p.lse[row] : 0.0f;
-      sm.dl[tid] = qq < qend ? p.delta[row] : 0.0f;
+      lpre = qq < qend ? p.lse[row] : 0.0f;
+      dpre = qq < qend ? p.delta[row] : 0.0f;
+    }
+  };
+  fetch(first);
+  for (long long qb = first; qb < qend; qb += kBwdQ) {
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < QJ; ++j) {
+      const int job = tid + j * kDkvThreads<D>, r = job / CH, c = job % CH;
+      *(uint4*)&sm.q[r][c * 8] = qpre[j];
+      *(uint4*)&sm.o[r][c * 8] = opre[j];
+    }
+    if (tid < kBwdQ) {
+      sm.lse[tid] = lpre;
+      sm.dl[tid] = dpre;
     }
     __syncthreads();
-    for (int job = tid; job < (kBwdQ / 2) * CH; job += kBwdThreads) {
+    if (qb + kBwdQ < qend) fetch(qb + kBwdQ);            // overlaps the work below
+    for (int job = tid; job < (kBwdQ / 2) * CH; job += kDkvThreads<D>) {
       const int t0 = 2 * (job % (kBwdQ / 2)), c = job / (kBwdQ / 2);
       const uint4 qa = *(const uint4*)&sm.q[t0][c * 8], qb2 = *(const uint4*)&sm.q[t0 + 1][c * 8];
       const uint4 oa = *(const uint4*)&sm.o[t0][c * 8], ob = *(const uint4*)&sm.o[t0 + 1][c * 8];
@@ -397,16 +452,33 @@ __global__ __launch_bounds__(kBwdThreads) void attn_bwd_dkv_kernel(AttnBwdParams
         sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, kreg[kk], sv, 0, 0, 0);
         dpv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ao, vreg[kk], dpv, 0, 0, 0);
       }
-      // S layout: lane holds key li, queries 8 (i / 4) + 4 hl + i % 4 of the sub-block.
+      // S layout: lane holds key li, queries 8 (i / 4) + 4 hl + i % 4 of the
+      // sub-block. A sub-block whose every query sees every key of the wave
+      // needs no mask; the others test 32-bit positions.
       float pm[16];
+      const int q_lo = (int)(qb + sub * 32);
+      const bool full = nk == 32 && (int)kw + 31 <= q_lo && q_lo + 31 < (int)qend &&
+                        (int)kw >= (int)window_start(q_lo + 31, p.ft, p.keep);   // wave-uniform
+      if (full) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int qo = sub * 32 + 8 * (i / 4) + 4 * hl + (i % 4);
-        const long long qq = qb + qo;
-        const bool ok = li < nk && qq < qend && ktok <= qq && ktok >= window_start(qq, p.ft, p.keep);
-        const float pv = ok ? __builtin_amdgcn_exp2f(fmaf(sv[i], scale_log2, -sm.lse[qo])) : 0.0f;
-        pm[i] = pv;
-        sv[i] = pv * (dpv[i] - sm.dl[qo]);            // dS
+        for (int i = 0; i < 16; ++i) {
+          const int qo = sub * 32 + 8 * (i / 4) + 4 * hl + (i % 4);
+          const float pv = __builtin_amdgcn_exp2f(fmaf(sv[i], scale_log2, -sm.lse[qo]));
+          pm[i] = pv;
+          sv[i] = pv * (dpv[i] - sm.dl[qo]);          // dS
+        }
+      } else {
+        const int kt = (int)ktok, qe = (int)qend;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int qo = sub * 32 + 8 * (i / 4) + 4 * hl + (i % 4);
+          const int qq = q_lo + 8 * (i / 4) + 4 * hl + (i % 4);
+          const int wsq = ((qq >> 8) << 8) - kKeep;
+          const bool ok = li < nk && qq < qe && kt <= qq && kt >= wsq;
+          const float pv = ok ? __builtin_amdgcn_exp2f(fmaf(sv[i], scale_log2, -sm.lse[qo])) : 0.0f;
+          pm[i] = pv;
+          sv[i] = pv * (dpv[i] - sm.dl[qo]);
+        }
       }
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
@@ -1104,14 +1176,19 @@ hipError_t launch_fuse_bwd(const TrainBwdParams& p, int head_dim, hipStream_t s)
 hipError_t launch_attn_bwd(const AttnBwdParams& p, int head_dim, hipStream_t s) {
   if (p.T <= 0) return hipSuccess;
   if (p.ft != kFt || p.keep != kKeep) return hipErrorInvalidValue;
-  const int blocks = (p.T + kBwdWaves * 32 - 1) / (kBwdWaves * 32);
-  const dim3 grid((unsigned)(blocks * p.B * p.H));
+  auto rows_grid = [&](int rows) {
+    return dim3((unsigned)(((p.T + rows - 1) / rows) * p.B * p.H));
+  };
   if (head_dim == 128) {
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<128>, grid, dim3(kBwdThreads), 0, s, p);
-    hipLaunchKernelGGL(attn_bwd_dkv_kernel<128>, grid, dim3(kBwdThreads), 0, s, p);
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<128>, rows_grid(kDqWaves<128> * 32),
+                       dim3(kDqThreads<128>), 0, s, p);
+    hipLaunchKernelGGL(attn_bwd_dkv_kernel<128>, rows_grid(kDkvWaves<128> * 32),
+                       dim3(kDkvThreads<128>), 0, s, p);
   } else if (head_dim == 64) {
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<64>, grid, dim3(kBwdThreads), 0, s, p);
-    hipLaunchKernelGGL(attn_bwd_dkv_kernel<64>, grid, dim3(kBwdThreads), 0, s, p);
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<64>, rows_grid(kDqWaves<64> * 32),
+                       dim3(kDqThreads<64>), 0, s, p);
+    hipLaunchKernelGGL(attn_bwd_dkv_kernel<64>, rows_grid(kDkvWaves<64> * 32),
+                       dim3(kDkvThreads<64>), 0, s, p);
   } else {
     return hipErrorInvalidValue;
   }

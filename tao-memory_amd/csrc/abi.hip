@@ -922,6 +922,7 @@ namespace {
 struct TrainBwdLayout {
   size_t dlocal, h, delta, dden, dcoarse, dnum, drq, dh, dvf;   // per-token arrays
   size_t dpw, dsw_tile, dgc, dc, dsw, dpz, dz, dalpha;          // memory branch, d alpha
+  size_t dalpha_parts;                                          // per fusion workgroup
   size_t zero_begin, zero_end;                                  // accumulators to clear
   size_t total;
   int n_tiles, v_max;
@@ -961,6 +962,7 @@ TrainBwdLayout train_bwd_layout(const tao_state_dev* st, int64_t tokens, int fin
   l.dz = take(BH * (size_t)fines * D * 4);
   l.dalpha = take(4);
   l.zero_end = off;
+  l.dalpha_parts = take((size_t)tao::fuse_bwd_workgroups((int)T, (int)B, (int)H) * 4);
   l.total = off;
   return l;
 }
@@ -1039,6 +1041,7 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   fp.dfb = a->dfusion_b;
   fp.h = (bf16_t*)(ws + l.h);
   fp.dalpha = (float*)(ws + l.dalpha);
+  fp.dalpha_parts = a->dalpha_out ? (float*)(ws + l.dalpha_parts) : nullptr;
   e = tao::launch_fuse_bwd(fp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_train_backward fusion");
   // ---- local attention adjoint

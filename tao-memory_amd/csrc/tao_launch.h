@@ -276,9 +276,11 @@ struct TrainBwdParams {
   bf16_t* dlocal; float* delta; float* dcoarse; float* dnum; float* dden; float* drq;
   float* dfa; float* dfb;
   bf16_t* h;                     // h = softmax(raw_q) [B, T, H, D]
-  float* dalpha;                 // zeroed fp32 scalar: += d out / d alpha . grad
+  float* dalpha_parts;           // nullable: one d alpha partial per workgroup
+  float* dalpha;                 // fp32 scalar: the sum of the partials
 };
 hipError_t launch_fuse_bwd(const TrainBwdParams& p, int head_dim, hipStream_t s);
+int fuse_bwd_workgroups(int T, int B, int H);   // d alpha partials launch_fuse_bwd writes
 
 // Local attention adjoints with the full-sequence windows (query q sees keys
 // [max(0, ft * (q / ft) - keep), q]).

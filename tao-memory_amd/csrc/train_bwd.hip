@@ -140,9 +140,17 @@ __global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
       p.dden[row] = dd;
     }
   }
-  if (p.dalpha) {
+  if (p.dalpha_parts) {
+    // one partial per workgroup (a single contended atomic serialised ~12K
+    // waves); dalpha_kernel adds them in a fixed order
     const float sg = wave_sum_fold(sgain);
-    if (lane == 0) atomicAdd(p.dalpha, 2.0f * sg);
+    if (lane == 0) red[0][w] = sg;
+    __syncthreads();
+    if (tid == 0) {
+      float t = 0.0f;
+      for (int i = 0; i < kThreads / 64; ++i) t += red[0][i];
+      p.dalpha_parts[blockIdx.x] = 2.0f * t;
+    }
   }
   // d fusion_a / d fusion_b: sum the ROWS lane rows, one atomic per (e, i).
 #pragma unroll
@@ -155,6 +163,17 @@ __global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
     float* dst = k < 3 ? p.dfa : p.dfb;
     atomicAdd(dst + (h * D + ee) * 3 + (k % 3), s);
   }
+}
+
+// d alpha: the workgroups' partials in index order (one workgroup).
+__global__ __launch_bounds__(256) void dalpha_kernel(const float* parts, int n, float* out) {
+  __shared__ float red[4];
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < n; i += 256) s += parts[i];
+  s = wave_sum_fold(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) *out = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1161,15 +1180,21 @@ __global__ __launch_bounds__(kThreads) void finish_bwd_kernel(MemBwdParams p) {
 
 }  // namespace
 
+int fuse_bwd_workgroups(int T, int B, int H) {
+  return ((T + kFuseChunk - 1) / kFuseChunk) * B * H;
+}
+
 hipError_t launch_fuse_bwd(const TrainBwdParams& p, int head_dim, hipStream_t s) {
-  const int chunks = (p.T + kFuseChunk - 1) / kFuseChunk;
-  const dim3 grid((unsigned)(chunks * p.B * p.H));
+  const int groups = fuse_bwd_workgroups(p.T, p.B, p.H);
+  const dim3 grid((unsigned)groups);
   if (head_dim == 128)
     hipLaunchKernelGGL(fuse_bwd_kernel<128>, grid, dim3(kThreads), 0, s, p);
   else if (head_dim == 64)
     hipLaunchKernelGGL(fuse_bwd_kernel<64>, grid, dim3(kThreads), 0, s, p);
   else
     return hipErrorInvalidValue;
+  if (p.dalpha_parts)
+    hipLaunchKernelGGL(dalpha_kernel, dim3(1), dim3(256), 0, s, p.dalpha_parts, groups, p.dalpha);
   return hipGetLastError();
 }
 

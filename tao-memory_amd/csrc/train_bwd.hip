@@ -757,6 +757,15 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
               sm.dpw[i / D][i % D]);
 }
 
+TAO_DEV void unpack8f_bwd(const uint4& u, float out[8]) {
+  const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(wv[i] << 16);
+    out[2 * i + 1] = __uint_as_float(wv[i] & 0xFFFF0000u);
+  }
+}
+
 // Outer products over a query set: out^T[e][d] = sum_q x[q][e] y[q][d].
 // mode 0 (dC of the NF fines f0 .. f0 + NF - 1, f0 = NF * item): queries of
 //   every tile that sees f0, x = dnum, y_f = a = h pw sw (zero unless the
@@ -805,81 +814,113 @@ __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int
   const int t_hi = min(t_last, t_lo + kObTiles);
   if (t_lo >= t_hi) return;                          // workgroup-uniform
   const bf16_t* gsw = p.fine_sw + (size_t)bh * p.fine_cap * D;
-  for (int t = t_lo; t < t_hi; ++t) {
-    const int V = tile_visible(t, lag), erel = V - 1, K = V / G;
-    // fines of the group this tile sees (bits of the selection word)
+  // Per tile, the NF fines' page and segment weights (query-independent) in
+  // LDS; per 32-query chunk, the next chunk's dnum / h rows and selection
+  // bits wait in registers while this chunk is staged and reduced.
+  constexpr int JOBS = kObQ * (D / 8) / kThreads;
+  static_assert(JOBS * kThreads == kObQ * (D / 8), "whole jobs per thread");
+  __shared__ float wpw[NF][D], wsw[NF][D];
+  float xpre[JOBS][8];
+  uint4 hpre[JOBS];
+  uint32_t bpre[JOBS];
+  auto fetch = [&](int t, int qb) __attribute__((always_inline)) {
+    const int V = tile_visible(t, lag);
     const uint32_t seen = mode == 0 ? ((1u << min(NF, max(V - f0, 0))) - 1u) : 1u;
-    const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
-    const bf16_t* psw = p.psw_pool + ((size_t)erel * BH + bh) * 8 * D;
-    const int qa = t * p.ft, qb_end = min(p.T, qa + p.ft);
-    for (int qb = qa; qb < qb_end; qb += kObQ) {
-      __syncthreads();
-      if (tid < NF) any_sel[tid] = 0;
-      __syncthreads();
-      // thread = (query qi, 8-channel chunk c): x and y rows, written transposed
-      for (int job = tid; job < kObQ * (D / 8); job += kThreads) {
-        const int qi = job % kObQ, c = job / kObQ;
-        const int q = qb + qi;
-        float xv[8], hv[8];
+    const int qb_end = min(p.T, t * p.ft + p.ft);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) { xv[j] = 0.0f; hv[j] = 0.0f; }
-        uint32_t bits = 0;
-        if (q < qb_end) {
-          const size_t row = ((size_t)b * p.T + q) * p.H + h;
-          bits = mode == 0 ? (p.qsel[row * p.qsel_words + (f0 >> 5)] >> (f0 & 31)) & seen : 1u;
-          if (bits) {
-            const float* xs = (mode == 0 ? p.dnum : p.dcoarse) + row * D + 8 * c;
-            const bf16_t* hs = p.h + row * D + 8 * c;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              xv[j] = xs[j];
-              hv[j] = bf2f(hs[j]);
-            }
-          }
-        }
-        if (c == 0)
-#pragma unroll
-          for (int k = 0; k < NF; ++k)
-            if ((bits >> k) & 1u) any_sel[k] = 1;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xt[8 * c + j][qi] = f2bf(xv[j]);
-#pragma unroll
-        for (int k = 0; k < NF; ++k) {
-          const int f = f0 + k;
-          const bool on = (bits >> k) & 1u;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            float y = hv[j];
-            if (mode == 0) {
-              const int d = 8 * c + j;
-              y = on ? y * bf2f(pw[(size_t)(f / G) * D + d]) *
-                           bf2f(f < K * G ? gsw[(size_t)f * D + d]
-                                          : psw[(size_t)(f - K * G) * D + d])
-                     : 0.0f;
-            }
-            yt[k][8 * c + j][qi] = f2bf(y);
-          }
+    for (int jb = 0; jb < JOBS; ++jb) {
+      const int job = tid + jb * kThreads, qi = job % kObQ, c = job / kObQ;
+      const int q = qb + qi;
+      uint32_t bits = 0;
+      float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+      uint4 hv = make_uint4(0, 0, 0, 0);
+      if (q < qb_end) {
+        const size_t row = ((size_t)b * p.T + q) * p.H + h;
+        bits = mode == 0 ? (p.qsel[row * p.qsel_words + (f0 >> 5)] >> (f0 & 31)) & seen : 1u;
+        if (bits) {
+          const float* xs = (mode == 0 ? p.dnum : p.dcoarse) + row * D + 8 * c;
+          x0 = *(const float4*)xs;
+          x1 = *(const float4*)(xs + 4);
+          hv = *(const uint4*)(p.h + row * D + 8 * c);
         }
       }
-      __syncthreads();
+      xpre[jb][0] = x0.x; xpre[jb][1] = x0.y; xpre[jb][2] = x0.z; xpre[jb][3] = x0.w;
+      xpre[jb][4] = x1.x; xpre[jb][5] = x1.y; xpre[jb][6] = x1.z; xpre[jb][7] = x1.w;
+      hpre[jb] = hv;
+      bpre[jb] = bits;
+    }
+  };
+  int t = t_lo, qb = t_lo * p.ft;
+  fetch(t, qb);
+  while (t < t_hi) {
+    const int qa = t * p.ft, qb_end = min(p.T, qa + p.ft);
+    __syncthreads();                                   // previous chunk reduced
+    if (tid < NF) any_sel[tid] = 0;
+    if (mode == 0 && qb == qa) {                       // first chunk of tile t
+      const int V = tile_visible(t, lag), erel = V - 1, K = V / G;
+      const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
+      const bf16_t* psw = p.psw_pool + ((size_t)erel * BH + bh) * 8 * D;
+      for (int i = tid; i < NF * D; i += kThreads) {
+        const int k = i / D, d = i % D, f = f0 + k;
+        const bool vis = f < V;
+        wpw[k][d] = vis ? bf2f(pw[(size_t)(f / G) * D + d]) : 0.0f;
+        wsw[k][d] = vis ? bf2f(f < K * G ? gsw[(size_t)f * D + d]
+                                         : psw[(size_t)(f - K * G) * D + d])
+                        : 0.0f;
+      }
+    }
+    __syncthreads();
+    // thread = (query qi, 8-channel chunk c): x and y rows, written transposed
+#pragma unroll
+    for (int jb = 0; jb < JOBS; ++jb) {
+      const int job = tid + jb * kThreads, qi = job % kObQ, c = job / kObQ;
+      const uint32_t bits = bpre[jb];
+      float hv[8];
+      unpack8f_bwd(hpre[jb], hv);
+      if (c == 0)
+#pragma unroll
+        for (int k = 0; k < NF; ++k)
+          if ((bits >> k) & 1u) any_sel[k] = 1;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xt[8 * c + j][qi] = f2bf(xpre[jb][j]);
 #pragma unroll
       for (int k = 0; k < NF; ++k) {
-        if (!any_sel[k]) continue;                     // workgroup-uniform
+        const bool on = (bits >> k) & 1u;
 #pragma unroll
-        for (int j = 0; j < TPW; ++j) {
-          const int tt = w + 4 * j;
-          if (tt < NT) {
-            const int mt = tt / DT, nt = tt % DT;
-#pragma unroll
-            for (int ks = 0; ks < kObQ / 16; ++ks)
-              acc[k][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                  as_bf16x8(*(const uint4*)&xt[32 * mt + li][16 * ks + 8 * hl]),
-                  as_bf16x8(*(const uint4*)&yt[k][32 * nt + li][16 * ks + 8 * hl]), acc[k][j],
-                  0, 0, 0);
+        for (int j = 0; j < 8; ++j) {
+          float y = hv[j];
+          if (mode == 0) {
+            const int d = 8 * c + j;
+            y = on ? y * wpw[k][d] * wsw[k][d] : 0.0f;
           }
+          yt[k][8 * c + j][qi] = f2bf(y);
         }
       }
     }
+    __syncthreads();
+    // advance; the next chunk's loads overlap this chunk's MFMAs
+    int t2 = t, qb2 = qb + kObQ;
+    if (qb2 >= qb_end) { t2 = t + 1; qb2 = t2 * p.ft; }
+    if (t2 < t_hi) fetch(t2, qb2);
+#pragma unroll
+    for (int k = 0; k < NF; ++k) {
+      if (!any_sel[k]) continue;                     // workgroup-uniform
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        const int tt = w + 4 * j;
+        if (tt < NT) {
+          const int mt = tt / DT, nt = tt % DT;
+#pragma unroll
+          for (int ks = 0; ks < kObQ / 16; ++ks)
+            acc[k][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                as_bf16x8(*(const uint4*)&xt[32 * mt + li][16 * ks + 8 * hl]),
+                as_bf16x8(*(const uint4*)&yt[k][32 * nt + li][16 * ks + 8 * hl]), acc[k][j],
+                0, 0, 0);
+        }
+      }
+    }
+    t = t2;
+    qb = qb2;
   }
   const bf16_t* pz = p.page_z + (size_t)bh * p.page_cap * D;
 #pragma unroll

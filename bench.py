@@ -633,8 +633,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the TaoMemory operator path has no "
-              "multi-GPU mode in this build (see DESIGN.md, sharding design); "
-              "run with --gpus 1", file=sys.stderr)
+              "multi-GPU mode in this build (heads and requests would shard with no "
+              "exchange); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch

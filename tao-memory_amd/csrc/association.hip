@@ -14,10 +14,9 @@
 //   sums over the staged rows.
 // association_solve_kernel (association_writer.py:21-32): one workgroup per
 //   [D, D] pair. The system gram + (trace / D) I is factored in LDS by a
-//   right-looking Cholesky (column j: pivot, column scale, trailing rank-one
-//   update, two barriers), then cross is solved in place by forward and back
-//   substitution in right-looking form (row i finished, then removed from the
-//   other rows by all threads); C = bf16(X).
+//   blocked right-looking Cholesky (8-column panels factored by one wave,
+//   rank-8 trailing updates by all threads), then cross is solved in place by
+//   forward and back substitution, 8 rows a step; C = bf16(X).
 // structured_matrix_kernel (structured_writer.py:16-34): one workgroup per
 //   pair; per-channel vectors and their sums in LDS, then thread e walks
 //   column e of cross twice (hb and mass . hb, then the result).
@@ -213,45 +212,102 @@ __global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocS
     sm.a[r][col] = g[i] + (r == col ? ridge : 0.0f);
     sm.x[r][col] = c[i];
   }
+  // Blocked right-looking Cholesky, PB columns a step: wave 0 factors the
+  // panel (rows >= jb, wave-synchronous), then all threads apply its rank-PB
+  // update to the trailing lower triangle; two workgroup barriers a panel.
+  constexpr int PB = 8;
   int bad = 0;
-  for (int j = 0; j < D; ++j) {
+  const int lane = tid & 63;
+  for (int jb = 0; jb < D; jb += PB) {
     __syncthreads();
-    const float piv = sm.a[j][j];
-    if (!(piv > 0.0f)) bad = bad ? bad : j + 1;     // not positive (or NaN)
-    const float dj = __builtin_sqrtf(piv);
-    __syncthreads();                                // every thread read the pivot
-    for (int i = j + 1 + tid; i < D; i += kSolveThreads) sm.a[i][j] = sm.a[i][j] / dj;
-    if (tid == 0) sm.a[j][j] = dj;
+    if (tid < 64) {
+#pragma unroll
+      for (int c = 0; c < PB; ++c) {
+        const int j = jb + c;
+        const float piv = sm.a[j][j];
+        if (!(piv > 0.0f)) bad = bad ? bad : j + 1;
+        const float dj = __builtin_sqrtf(piv);
+        __builtin_amdgcn_wave_barrier();
+        for (int k = j + 1 + lane; k < D; k += 64) sm.a[k][j] = sm.a[k][j] / dj;
+        if (lane == 0) sm.a[j][j] = dj;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // the rest of the panel: columns j' in (j, jb + PB), rows k >= j'
+        for (int k = j + 1 + lane; k < D; k += 64) {
+          const float akj = sm.a[k][j];
+#pragma unroll
+          for (int c2 = c + 1; c2 < PB; ++c2) {
+            const int j2 = jb + c2;
+            if (k >= j2) sm.a[k][j2] = fmaf(-akj, sm.a[j2][j], sm.a[k][j2]);
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    }
     __syncthreads();
-    const int R = D - j - 1;
+    const int r0 = jb + PB, R = D - r0;
     for (int idx = tid; idx < R * R; idx += kSolveThreads) {
-      const int i = j + 1 + idx / R, k = j + 1 + idx % R;
-      if (k <= i) sm.a[i][k] = fmaf(-sm.a[i][j], sm.a[k][j], sm.a[i][k]);
+      const int k = r0 + idx / R, c = r0 + idx % R;
+      if (c <= k) {
+        float v = sm.a[k][c];
+#pragma unroll
+        for (int t = 0; t < PB; ++t) v = fmaf(-sm.a[k][jb + t], sm.a[c][jb + t], v);
+        sm.a[k][c] = v;
+      }
     }
   }
   __syncthreads();
   if (p.info && tid == 0) p.info[mat] = bad;
-  // Forward (L Y = X) then back (L^T X = Y) substitution, right-looking:
-  // step i finishes row i of every right-hand side, then all threads remove
-  // it from the remaining rows (independent updates, two barriers a step).
-  for (int i = 0; i < D; ++i) {
-    const float piv = sm.a[i][i];
-    for (int e = tid; e < D; e += kSolveThreads) sm.x[i][e] = sm.x[i][e] / piv;
+  // Forward (L Y = X) then back (L^T X = Y) substitution, PB rows a step:
+  // thread e finishes the step's rows of column e, then every thread removes
+  // them from the remaining rows; two barriers a step.
+  for (int ib = 0; ib < D; ib += PB) {
+    if (tid < D) {
+      const int e = tid;
+      float y[PB];
+#pragma unroll
+      for (int t = 0; t < PB; ++t) {
+        float v = sm.x[ib + t][e];
+#pragma unroll
+        for (int u = 0; u < t; ++u) v = fmaf(-sm.a[ib + t][ib + u], y[u], v);
+        y[t] = v / sm.a[ib + t][ib + t];
+        sm.x[ib + t][e] = y[t];
+      }
+    }
     __syncthreads();
-    const int R = D - i - 1;
-    for (int idx = tid; idx < R * D; idx += kSolveThreads) {
-      const int k = i + 1 + idx / D, e = idx % D;
-      sm.x[k][e] = fmaf(-sm.a[k][i], sm.x[i][e], sm.x[k][e]);
+    const int r0 = ib + PB;
+    for (int idx = tid; idx < (D - r0) * D; idx += kSolveThreads) {
+      const int k = r0 + idx / D, e = idx % D;
+      float v = sm.x[k][e];
+#pragma unroll
+      for (int t = 0; t < PB; ++t) v = fmaf(-sm.a[k][ib + t], sm.x[ib + t][e], v);
+      sm.x[k][e] = v;
     }
     __syncthreads();
   }
-  for (int i = D - 1; i >= 0; --i) {
-    const float piv = sm.a[i][i];
-    for (int e = tid; e < D; e += kSolveThreads) sm.x[i][e] = sm.x[i][e] / piv;
+  for (int ib = D - PB; ib >= 0; ib -= PB) {
+    if (tid < D) {
+      const int e = tid;
+      float xv[PB];
+#pragma unroll
+      for (int t = PB - 1; t >= 0; --t) {
+        float v = sm.x[ib + t][e];
+#pragma unroll
+        for (int u = t + 1; u < PB; ++u) v = fmaf(-sm.a[ib + u][ib + t], xv[u], v);
+        xv[t] = v / sm.a[ib + t][ib + t];
+        sm.x[ib + t][e] = xv[t];
+      }
+    }
     __syncthreads();
-    for (int idx = tid; idx < i * D; idx += kSolveThreads) {
+    for (int idx = tid; idx < ib * D; idx += kSolveThreads) {
       const int k = idx / D, e = idx % D;
-      sm.x[k][e] = fmaf(-sm.a[i][k], sm.x[i][e], sm.x[k][e]);
+      float v = sm.x[k][e];
+#pragma unroll
+      for (int t = 0; t < PB; ++t) v = fmaf(-sm.a[ib + t][k], sm.x[ib + t][e], v);
+      sm.x[k][e] = v;
     }
     __syncthreads();
   }

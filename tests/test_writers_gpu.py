@@ -215,8 +215,9 @@ def test_full_sequence_regularized_writer(device, tokens, heads, width, index_on
                       fusion_b=fb.to(device), alpha=0.5, config=cfg)
 
 
-@pytest.mark.parametrize("index_only,width", [(False, 64), (True, 128)])
-def test_stream_regularized_writer(device, index_only, width):
+@pytest.mark.parametrize("index_only,width,batch", [(False, 64, 1), (True, 128, 1),
+                                                   (False, 64, 2)])
+def test_stream_regularized_writer(device, index_only, width, batch):
     """Streaming prefill and decode with fine_writer="regularized_association":
     seals inside a prefill call and in the decode driver (the step at 2559
     seals the 8th fine and completes page 0), the association fine and page
@@ -226,8 +227,8 @@ def test_stream_regularized_writer(device, index_only, width):
     from tao_attention import (StreamCache, TaoConfig, new_state, tao_attention_decode,
                                tao_attention_prefill)
     heads, tokens = 2, 2826
-    g = torch.Generator().manual_seed(61 + width)
-    xs = [torch.randn(1, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
+    g = torch.Generator().manual_seed(61 + width + batch)
+    xs = [torch.randn(batch, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
     fa = torch.randn(heads, width, 3, generator=g) * 0.02
     fb = torch.randn(heads, width, 3, generator=g) * 0.02
     cfg = TaoConfig(fine_writer="regularized_association", coarse_index_only=index_only)

@@ -175,16 +175,16 @@ def _bitmask_sets(qsel):
     return bits.reshape(*words.shape[:3], -1).bool()
 
 
-@pytest.mark.parametrize("tokens,heads,width,index_only,seed", [
-    (2100, 2, 64, True, 51), (2900, 2, 128, False, 52)])
-def test_full_sequence_regularized_writer(device, tokens, heads, width, index_only, seed):
+@pytest.mark.parametrize("tokens,heads,width,index_only,seed,batch", [
+    (2100, 2, 64, True, 51, 1), (2900, 2, 128, False, 52, 1), (2700, 2, 64, False, 53, 2)])
+def test_full_sequence_regularized_writer(device, tokens, heads, width, index_only, seed, batch):
     """tao_attention with fine_writer="regularized_association": the softmax
     writer's z and routes (bit-exact), association value matrices for fines
     and completed pages, outputs within the bf16 tolerance of the oracle."""
     from oracle import tao_oracle as O
     from tao_attention import TaoConfig, tao_attention, training
     g = torch.Generator().manual_seed(seed)
-    xs = [torch.randn(1, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
+    xs = [torch.randn(batch, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
     fa = torch.randn(heads, width, 3, generator=g) * 0.02
     fb = torch.randn(heads, width, 3, generator=g) * 0.02
     cfg = TaoConfig(fine_writer="regularized_association", coarse_index_only=index_only)

@@ -1002,39 +1002,49 @@ __global__ __launch_bounds__(D) void page_bwd_kernel(MemBwdParams p) {
 // thread per channel): cw = softmax over pages < K of page_z,
 // d cw[g][d] = sum_e dG[d][e] pc_g[d][e] -> d page_z (softmax adjoint), and
 // d w_f[d] = cw[g][d] sum_e dG[d][e] C_f[d][e] -> d sw of f (w_f = sw_f).
+// 256 threads: channel d = tid % D, part = tid / D; pages and fines are
+// dealt to the parts (the dot products over e are the work), the page dots
+// meet in LDS for the softmax adjoint.
+constexpr int kCpMaxPages = 64;
+
 template <int D>
-__global__ __launch_bounds__(D) void coarse_page_bwd_kernel(MemBwdParams p) {
+__global__ __launch_bounds__(kThreads) void coarse_page_bwd_kernel(MemBwdParams p) {
+  constexpr int PARTS = kThreads / D;
+  __shared__ float sdcw[kCpMaxPages][D];
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   const int K = p.coarse_first + blockIdx.x / BH;
-  const int d = threadIdx.x, G = p.group;
+  const int d = threadIdx.x % D, part = threadIdx.x / D, G = p.group;
   const bf16_t* pz = p.page_z + (size_t)bh * p.page_cap * D;
   const float* dg = p.dgc + ((size_t)(K - p.coarse_first) * BH + bh) * D * D;   // [e][d]
+  auto dot = [&](const bf16_t* mat) __attribute__((always_inline)) {
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    for (int e = 0; e < D; e += 4) {
+      a0 = fmaf(dg[(size_t)e * D + d], bf2f(mat[(size_t)e * D + d]), a0);
+      a1 = fmaf(dg[(size_t)(e + 1) * D + d], bf2f(mat[(size_t)(e + 1) * D + d]), a1);
+      a2 = fmaf(dg[(size_t)(e + 2) * D + d], bf2f(mat[(size_t)(e + 2) * D + d]), a2);
+      a3 = fmaf(dg[(size_t)(e + 3) * D + d], bf2f(mat[(size_t)(e + 3) * D + d]), a3);
+    }
+    return (a0 + a1) + (a2 + a3);
+  };
+  for (int g = part; g < K; g += PARTS)
+    sdcw[g][d] = dot(p.page_c + ((size_t)bh * p.page_cap + g) * D * D);     // [e][d]
   float m = -__builtin_inff();
   for (int g = 0; g < K; ++g) m = fmaxf(m, bf2f(pz[(size_t)g * D + d]));
   float z = 0.0f;
   for (int g = 0; g < K; ++g) z += __expf(bf2f(pz[(size_t)g * D + d]) - m);
+  __syncthreads();
   float s = 0.0f;
-  for (int g = 0; g < K; ++g) {
+  for (int g = 0; g < K; ++g) s += __expf(bf2f(pz[(size_t)g * D + d]) - m) / z * sdcw[g][d];
+  for (int g = part; g < K; g += PARTS) {
     const float cw = __expf(bf2f(pz[(size_t)g * D + d]) - m) / z;
-    const bf16_t* pc = p.page_c + ((size_t)bh * p.page_cap + g) * D * D;   // [e][d]
-    float dcw = 0.0f;
-    for (int e = 0; e < D; ++e) dcw = fmaf(dg[(size_t)e * D + d], bf2f(pc[(size_t)e * D + d]), dcw);
-    s += cw * dcw;
+    atomicAdd(p.dpz + ((size_t)bh * p.page_cap + g) * D + d, cw * (sdcw[g][d] - s));
   }
-  for (int g = 0; g < K; ++g) {
+  for (int f = part; f < K * G; f += PARTS) {
+    const int g = f / G;
     const float cw = __expf(bf2f(pz[(size_t)g * D + d]) - m) / z;
-    const bf16_t* pc = p.page_c + ((size_t)bh * p.page_cap + g) * D * D;
-    float dcw = 0.0f;
-    for (int e = 0; e < D; ++e) dcw = fmaf(dg[(size_t)e * D + d], bf2f(pc[(size_t)e * D + d]), dcw);
-    atomicAdd(p.dpz + ((size_t)bh * p.page_cap + g) * D + d, cw * (dcw - s));
-    for (int i = 0; i < G; ++i) {
-      const int f = g * G + i;
-      const bf16_t* c = p.bank + ((size_t)bh * p.fine_cap + f) * D * D;       // C^T [e][d]
-      float dw = 0.0f;
-      for (int e = 0; e < D; ++e) dw = fmaf(dg[(size_t)e * D + d], bf2f(c[(size_t)e * D + d]), dw);
-      atomicAdd(p.dsw + ((size_t)bh * p.v_max + f) * D + d, cw * dw);
-    }
+    const float dw = dot(p.bank + ((size_t)bh * p.fine_cap + f) * D * D);   // C^T [e][d]
+    atomicAdd(p.dsw + ((size_t)bh * p.v_max + f) * D + d, cw * dw);
   }
 }
 
@@ -1280,7 +1290,7 @@ hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s) {
                            dim3((unsigned)(p.coarse_count * dg_groups * BH)), dim3(kThreads),\
                            0, s, p, 1);                                                      \
         hipLaunchKernelGGL(coarse_page_bwd_kernel<D_>, dim3((unsigned)(p.coarse_count * BH)),\
-                           dim3(D_), 0, s, p);                                               \
+                           dim3(kThreads), 0, s, p);                                         \
       }                                                                                      \
       hipLaunchKernelGGL((outer_bwd_kernel<D_, kObFines<D_>>),                               \
                          dim3((unsigned)(((p.v_max + kObFines<D_> - 1) / kObFines<D_>) *     \

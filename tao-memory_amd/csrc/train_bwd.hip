@@ -566,6 +566,7 @@ struct ReadBwdSmem {
   uint32_t bits[512];
   int pre[512];
   int uni[1024];
+  uint32_t qw[kRbQ][16];               // the block's selection words (V <= 504)
   int n_union;
 };
 
@@ -618,6 +619,7 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
   for (int i = tid; i < nq * words; i += kRbWaves * 64) {
     const int qi = i / words, wd = i % words;
     const uint32_t v = p.qsel[((size_t)(b * p.T + q0 + qi) * p.H + h) * p.qsel_words + wd];
+    sm.qw[qi][wd] = v;
     if (v) atomicOr(&sm.bits[wd], v);
   }
   __syncthreads();
@@ -651,7 +653,6 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
     dn[kk] = as_bf16x8(make_uint4(pk[0], pk[1], pk[2], pk[3]));
   }
   float dd[16], hd[DT][16], dh[DT][16];
-  const uint32_t* qs = p.qsel + ((size_t)(b * p.T + qa) * p.H + h) * p.qsel_words;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int qi = 8 * (i / 4) + 4 * hl + (i % 4);
@@ -673,7 +674,7 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
     for (int i = tid; i < D; i += kRbWaves * 64) sm.dsw[i] = 0.0f;
     __syncthreads();
     // selection mask of the wave's 32 queries (bit q)
-    const bool mine = li < nqw && ((qs[(f >> 5)] >> (f & 31)) & 1u);
+    const bool mine = li < nqw && ((sm.qw[32 * w + li][f >> 5] >> (f & 31)) & 1u);
     const uint32_t m32 = (uint32_t)(__ballot(mine) & 0xFFFFFFFFull);
     // Every wave reaches the barriers below, selecting or not.
     if (m32 != 0) {

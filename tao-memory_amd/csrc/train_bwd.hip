@@ -560,8 +560,7 @@ TAO_DEV int tile_visible(int t, int lag) { return t > lag ? t - lag : 0; }
 
 template <int D>
 struct ReadBwdSmem {
-  bf16_t c[D][D + 8];                  // C (or G) of the current fine: [d][e], padded
-  float dsw[D];                        // d sw of the current fine (sum over waves)
+  bf16_t c[2][D][D + 8];               // C (or G) of the current / next fine: [d][e], padded
   float dpw[64][D];                    // d pw of the tile's pages (P <= 64)
   uint32_t bits[512];
   int pre[512];
@@ -665,26 +664,55 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
       dh[t][i] = 0.0f;
     }
   }
+  // The next union fine's C rows are loaded into registers while the current
+  // fine is consumed (thread tid owns jobs tid + 256 j of the transposed stage).
+  constexpr int JP = (D / 2) * (D / 8) / (kRbWaves * 64);
+  static_assert(JP * kRbWaves * 64 == (D / 2) * (D / 8), "stage jobs split evenly");
+  uint4 ra[JP], rb[JP];
+  auto load_c = [&](int fn) {
+    const bf16_t* src = p.bank + ((size_t)bh * p.fine_cap + fn) * D * D;
+#pragma unroll
+    for (int j = 0; j < JP; ++j) {
+      const int job = tid + j * kRbWaves * 64;
+      const int e0 = 2 * (job % (D / 2)), ch = job / (D / 2);
+      ra[j] = *(const uint4*)(src + (size_t)e0 * D + ch * 8);
+      rb[j] = *(const uint4*)(src + (size_t)(e0 + 1) * D + ch * 8);
+    }
+  };
+  if (U > 0) load_c(sm.uni[0]);
   for (int u = 0; u < U; ++u) {
     const int f = sm.uni[u];
     const int g = f / G;
-    __syncthreads();                                   // previous fine consumed
-    stage_transposed<D>(sm.c, p.bank + ((size_t)bh * p.fine_cap + f) * D * D, tid,
-                        kRbWaves * 64);
-    for (int i = tid; i < D; i += kRbWaves * 64) sm.dsw[i] = 0.0f;
+    // Fines alternate between the two C buffers: the barrier below also
+    // proves that every wave is done with the fine before the previous one.
+    bf16_t (*cu)[D + 8] = sm.c[u & 1];
+#pragma unroll
+    for (int j = 0; j < JP; ++j) {
+      const int job = tid + j * kRbWaves * 64;
+      const int e0 = 2 * (job % (D / 2)), ch = job / (D / 2);
+      const uint32_t wa[4] = {ra[j].x, ra[j].y, ra[j].z, ra[j].w};
+      const uint32_t wb[4] = {rb[j].x, rb[j].y, rb[j].z, rb[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        *(uint32_t*)&cu[ch * 8 + 2 * i][e0] = (wa[i] & 0xFFFFu) | (wb[i] << 16);
+        *(uint32_t*)&cu[ch * 8 + 2 * i + 1][e0] = (wa[i] >> 16) | (wb[i] & 0xFFFF0000u);
+      }
+    }
     __syncthreads();
     // selection mask of the wave's 32 queries (bit q)
     const bool mine = li < nqw && ((sm.qw[32 * w + li][f >> 5] >> (f & 31)) & 1u);
     const uint32_t m32 = (uint32_t)(__ballot(mine) & 0xFFFFFFFFull);
-    // Every wave reaches the barriers below, selecting or not.
+    float swv[DT], pwv[DT];
     if (m32 != 0) {
-      float swv[DT], pwv[DT];
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
         const int d = 32 * t + li;
         swv[t] = bf2f(f < K * G ? gsw[(size_t)f * D + d] : psw[(size_t)(f - K * G) * D + d]);
         pwv[t] = bf2f(pw[(size_t)g * D + d]);
       }
+    }
+    if (u + 1 < U) load_c(sm.uni[u + 1]);
+    if (m32 != 0) {
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
         floatx16 da;
@@ -693,7 +721,7 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk)
           da = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              dn[kk], as_bf16x8(*(const uint4*)&sm.c[32 * t + li][16 * kk + 8 * hl]), da, 0, 0, 0);
+              dn[kk], as_bf16x8(*(const uint4*)&cu[32 * t + li][16 * kk + 8 * hl]), da, 0, 0, 0);
         float spw = 0.0f, ssw = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -707,19 +735,16 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
         spw += __shfl_xor(spw, 32, 64);
         ssw += __shfl_xor(ssw, 32, 64);
         if (hl == 0) {
-          atomicAdd(&sm.dsw[32 * t + li], ssw);
+          atomicAdd(p.dsw_tile + (((size_t)tile * BH + bh) * p.v_max + f) * D + 32 * t + li, ssw);
           atomicAdd(&sm.dpw[g][32 * t + li], spw);
         }
       }
     }
-    __syncthreads();
-    for (int i = tid; i < D; i += kRbWaves * 64)
-      atomicAdd(p.dsw_tile + (((size_t)tile * BH + bh) * p.v_max + f) * D + i, sm.dsw[i]);
   }
   // ---- coarse read: dh[q][d] += sum_e dcoarse[q][e] G[d][e] (coarse_pool holds G^T)
   if (p.coarse_values && K >= 1) {
     __syncthreads();
-    stage_transposed<D>(sm.c, p.coarse_pool + ((size_t)(K - p.coarse_first) * BH + bh) * D * D,
+    stage_transposed<D>(sm.c[0], p.coarse_pool + ((size_t)(K - p.coarse_first) * BH + bh) * D * D,
                         tid, kRbWaves * 64);
     __syncthreads();
 #pragma unroll
@@ -738,7 +763,8 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            dn[kk], as_bf16x8(*(const uint4*)&sm.c[32 * t + li][16 * kk + 8 * hl]), acc, 0, 0, 0);
+            dn[kk], as_bf16x8(*(const uint4*)&sm.c[0][32 * t + li][16 * kk + 8 * hl]), acc, 0, 0,
+            0);
 #pragma unroll
       for (int i = 0; i < 16; ++i) dh[t][i] += acc[i];
     }

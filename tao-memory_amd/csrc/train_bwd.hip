@@ -815,8 +815,9 @@ template <int D, int NF>
 __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int mode) {
   constexpr int DT = D / 32, NT = DT * DT, TPW = (NT + 3) / 4;
   static_assert(32 % NF == 0, "a fine group's selection bits share one word");
-  __shared__ bf16_t xt[D][kObQ + 8], yt[NF][D][kObQ + 8];
-  __shared__ int any_sel[NF];
+  // Chunks alternate between two staging buffers, so one barrier per chunk
+  // separates its staging from its reduction.
+  __shared__ bf16_t xt[2][D][kObQ + 8], yt[2][NF][D][kObQ + 8];
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   const int b = bh / p.H, h = bh % p.H;
@@ -877,13 +878,13 @@ __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int
       bpre[jb] = bits;
     }
   };
-  int t = t_lo, qb = t_lo * p.ft;
+  int t = t_lo, qb = t_lo * p.ft, buf = 0;
   fetch(t, qb);
   while (t < t_hi) {
     const int qa = t * p.ft, qb_end = min(p.T, qa + p.ft);
-    __syncthreads();                                   // previous chunk reduced
-    if (tid < NF) any_sel[tid] = 0;
     if (mode == 0 && qb == qa) {                       // first chunk of tile t
+      // every thread is past the previous chunk's staging (the barrier after
+      // it), the only reader of wpw / wsw
       const int V = tile_visible(t, lag), erel = V - 1, K = V / G;
       const bf16_t* pw = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
       const bf16_t* psw = p.psw_pool + ((size_t)erel * BH + bh) * 8 * D;
@@ -895,21 +896,24 @@ __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int
                                          : psw[(size_t)(f - K * G) * D + d])
                         : 0.0f;
       }
+      __syncthreads();
     }
-    __syncthreads();
-    // thread = (query qi, 8-channel chunk c): x and y rows, written transposed
+    // thread = (query qi, 8-channel chunk c): x and y rows, written transposed.
+    // A wave's jobs cover all kObQ queries (kObQ divides 64), so its ballot of
+    // a fine's selection bits says whether any query of the chunk selects it.
+    static_assert(64 % kObQ == 0, "every wave sees every query of the chunk");
+    uint32_t any_sel = 0;
+#pragma unroll
+    for (int k = 0; k < NF; ++k)
+      if (__ballot((bpre[0] >> k) & 1u) != 0ull) any_sel |= 1u << k;
 #pragma unroll
     for (int jb = 0; jb < JOBS; ++jb) {
       const int job = tid + jb * kThreads, qi = job % kObQ, c = job / kObQ;
       const uint32_t bits = bpre[jb];
       float hv[8];
       unpack8f_bwd(hpre[jb], hv);
-      if (c == 0)
 #pragma unroll
-        for (int k = 0; k < NF; ++k)
-          if ((bits >> k) & 1u) any_sel[k] = 1;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) xt[8 * c + j][qi] = f2bf(xpre[jb][j]);
+      for (int j = 0; j < 8; ++j) xt[buf][8 * c + j][qi] = f2bf(xpre[jb][j]);
 #pragma unroll
       for (int k = 0; k < NF; ++k) {
         const bool on = (bits >> k) & 1u;
@@ -920,7 +924,7 @@ __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int
             const int d = 8 * c + j;
             y = on ? y * wpw[k][d] * wsw[k][d] : 0.0f;
           }
-          yt[k][8 * c + j][qi] = f2bf(y);
+          yt[buf][k][8 * c + j][qi] = f2bf(y);
         }
       }
     }
@@ -931,7 +935,7 @@ __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int
     if (t2 < t_hi) fetch(t2, qb2);
 #pragma unroll
     for (int k = 0; k < NF; ++k) {
-      if (!any_sel[k]) continue;                     // workgroup-uniform
+      if (!((any_sel >> k) & 1u)) continue;          // workgroup-uniform
 #pragma unroll
       for (int j = 0; j < TPW; ++j) {
         const int tt = w + 4 * j;
@@ -940,14 +944,15 @@ __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int
 #pragma unroll
           for (int ks = 0; ks < kObQ / 16; ++ks)
             acc[k][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                as_bf16x8(*(const uint4*)&xt[32 * mt + li][16 * ks + 8 * hl]),
-                as_bf16x8(*(const uint4*)&yt[k][32 * nt + li][16 * ks + 8 * hl]), acc[k][j],
-                0, 0, 0);
+                as_bf16x8(*(const uint4*)&xt[buf][32 * mt + li][16 * ks + 8 * hl]),
+                as_bf16x8(*(const uint4*)&yt[buf][k][32 * nt + li][16 * ks + 8 * hl]),
+                acc[k][j], 0, 0, 0);
         }
       }
     }
     t = t2;
     qb = qb2;
+    buf ^= 1;
   }
   const bf16_t* pz = p.page_z + (size_t)bh * p.page_cap * D;
 #pragma unroll

@@ -61,21 +61,44 @@ __global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
   }
   float sfa[3] = {0.f, 0.f, 0.f}, sfb[3] = {0.f, 0.f, 0.f};
   float sgain = 0.0f;
-  for (int t0 = chunk * kFuseChunk; t0 < min(p.T, (chunk + 1) * kFuseChunk); t0 += ROWS) {
+  // The next ROWS tokens' inputs are loaded before this step's outputs are
+  // stored (the loads cannot pass the stores otherwise: the buffers may alias).
+  struct In { float g, L, x, C, F, den; };
+  const int t_beg = chunk * kFuseChunk, t_end = min(p.T, (chunk + 1) * kFuseChunk);
+  auto load_in = [&](int t0) __attribute__((always_inline)) {
+    In v;
     const int t = t0 + r;
-    const bool on = t < min(p.T, (chunk + 1) * kFuseChunk);
+    const bool on = t < t_end;
+    const int tt = on ? t : t0;
+    const size_t row = ((size_t)b * p.T + tt) * p.H + h;
+    const bool fine_on = on && t >= p.first_fine;
+    const bool coarse_on = fine_on && p.coarse_values && t >= p.first_coarse;
+    v.g = on ? bf2f(p.grad[b * p.g_sb + (int64_t)tt * p.g_st + h * p.g_sh + e]) : 0.0f;
+    v.L = bf2f(p.local[row * D + e]);
+    v.x = bf2f(p.rq.p[b * p.rq.sb + (int64_t)tt * p.rq.st + h * p.rq.sh + e]);
+    v.C = coarse_on ? bf2f(p.coarse[row * D + e]) : 0.0f;
+    v.F = fine_on ? bf2f(p.fine[row * D + e]) : 0.0f;
+    v.den = fine_on ? p.den[row] : 1.0f;
+    return v;
+  };
+  In cur = {0.f, 0.f, 0.f, 0.f, 0.f, 1.f};
+  if (t_beg < t_end) cur = load_in(t_beg);
+  for (int t0 = t_beg; t0 < t_end; t0 += ROWS) {
+    In nxt = cur;
+    if (t0 + ROWS < t_end) nxt = load_in(t0 + ROWS);
+    const int t = t0 + r;
+    const bool on = t < t_end;
     const size_t row = ((size_t)b * p.T + (on ? t : t0)) * p.H + h;
-    const float g = on ? bf2f(p.grad[b * p.g_sb + (int64_t)(on ? t : t0) * p.g_st + h * p.g_sh + e])
-                       : 0.0f;
-    const float L = bf2f(p.local[row * D + e]);
+    const float g = cur.g;
+    const float L = cur.L;
     const bool fine_on = t >= p.first_fine;
     const bool coarse_on = p.coarse_values && t >= p.first_coarse;
     float dlocal = g, dden_part = 0.0f;
     if (on && fine_on) {
-      const float x = bf2f(p.rq.p[b * p.rq.sb + (int64_t)t * p.rq.st + h * p.rq.sh + e]);
-      const float C = coarse_on ? bf2f(p.coarse[row * D + e]) : 0.0f;
-      const float F = bf2f(p.fine[row * D + e]);
-      const float den = p.den[row];
+      const float x = cur.x;
+      const float C = cur.C;
+      const float F = cur.F;
+      const float den = cur.den;
       float s[3];
 #pragma unroll
       for (int i = 0; i < 3; ++i) s[i] = rbf(rbf(a[i] * x) + bb[i]);
@@ -114,7 +137,7 @@ __global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
     }
     if (on) p.dlocal[row * D + e] = f2bf(dlocal);
     // row reductions over e: D = 64 is one wave, D = 128 two waves
-    const float xq = bf2f(p.rq.p[b * p.rq.sb + (int64_t)(on ? t : t0) * p.rq.st + h * p.rq.sh + e]);
+    const float xq = cur.x;
     float mx = wave_max(xq);
     if constexpr (D == 128) {
       if (lane == 0) red[0][w] = mx;
@@ -139,6 +162,7 @@ __global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
       p.delta[row] = dl;
       p.dden[row] = dd;
     }
+    cur = nxt;
   }
   if (p.dalpha_parts) {
     // one partial per workgroup (a single contended atomic serialised ~12K

@@ -40,7 +40,8 @@ TAO_DEV bf16x8 as_bf16x8(const uint4& u) {
 // attention's delta = sum_e d local * local, and d alpha = 2 sum g (rho_1
 // coarse + rho_2 fine) over fused elements (gain = 2 alpha; the reference
 // builds gain from a Python float and has no such gradient).
-constexpr int kFuseChunk = 64;
+constexpr int kFuseChunk = 64;      // tokens per fuse_bwd_kernel workgroup
+constexpr int kFuseVecChunk = 256;  // tokens per fuse_bwd_vec_kernel workgroup
 
 template <int D>
 __global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
@@ -186,6 +187,196 @@ __global__ __launch_bounds__(kThreads) void fuse_bwd_kernel(TrainBwdParams p) {
     for (int rr = 0; rr < ROWS; ++rr) s += facc[k][rr][ee];
     float* dst = k < 3 ? p.dfa : p.dfb;
     atomicAdd(dst + (h * D + ee) * 3 + (k % 3), s);
+  }
+}
+
+// The same adjoint with eight channels per lane: lane row r = one token, its
+// D / 8 lanes (contiguous in the wave) hold channels 8 c .. 8 c + 8 as 16-byte
+// loads and stores, and the row reductions (softmax of raw_q, delta, dden)
+// take log2(D / 8) shuffles. Needs 16-byte aligned rows (every bf16 row
+// stride a multiple of 8); launch_fuse_bwd checks and otherwise runs
+// fuse_bwd_kernel. A workgroup takes kFuseVecChunk tokens (fewer workgroups
+// than fuse_bwd_kernel: the per-workgroup set-up and d fusion sums amortise
+// over more rows); one d alpha partial per workgroup as there.
+TAO_DEV void load_bf8(const bf16_t* src, float out[8]) {
+  const uint4 u = *(const uint4*)src;
+  const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(wv[i] << 16);
+    out[2 * i + 1] = __uint_as_float(wv[i] & 0xFFFF0000u);
+  }
+}
+
+TAO_DEV void store_bf8(bf16_t* dst, const float v[8]) {
+  uint32_t wv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wv[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+  *(uint4*)dst = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+}
+
+TAO_DEV void store_f8(float* dst, const float v[8]) {
+  *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
+  *(float4*)(dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+template <int LPR>
+TAO_DEV float row_sum(float v) {
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int LPR>
+TAO_DEV float row_max(float v) {
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void fuse_bwd_vec_kernel(TrainBwdParams p) {
+  constexpr int LPR = D / 8, RPW = 64 / LPR, NW = kThreads / 64, ROWS = NW * RPW;
+  __shared__ float facc[6][NW][D];               // dfa, dfb per wave
+  __shared__ float red[NW];
+  const int h = blockIdx.x % p.H;
+  const int b = (blockIdx.x / p.H) % p.B;
+  const int chunk = blockIdx.x / (p.H * p.B);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int cl = lane % LPR, r = w * RPW + lane / LPR, e0 = 8 * cl;
+  float a[3][8], bb[3][8], sfa[3][8], sfb[3][8];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      a[i][j] = rbf(load_param(p.fa, p.f_dtype, h * p.fa_s[0] + (e0 + j) * p.fa_s[1] + i * p.fa_s[2]));
+      bb[i][j] = rbf(load_param(p.fb, p.f_dtype, h * p.fb_s[0] + (e0 + j) * p.fb_s[1] + i * p.fb_s[2]));
+      sfa[i][j] = 0.0f;
+      sfb[i][j] = 0.0f;
+    }
+  float sgain = 0.0f;
+  const int t_beg = chunk * kFuseVecChunk, t_end = min(p.T, (chunk + 1) * kFuseVecChunk);
+  for (int t0 = t_beg; t0 < t_end; t0 += ROWS) {
+    const int t = t0 + r;
+    const bool on = t < t_end;
+    const int tt = on ? t : t0;
+    const size_t row = ((size_t)b * p.T + tt) * p.H + h;
+    const bool fine_on = on && t >= p.first_fine;
+    const bool coarse_on = fine_on && p.coarse_values && t >= p.first_coarse;
+    float g[8], L[8], x[8], C[8], F[8];
+    load_bf8(p.grad + b * p.g_sb + (int64_t)tt * p.g_st + h * p.g_sh + e0, g);
+    load_bf8(p.local + row * D + e0, L);
+    load_bf8(p.rq.p + b * p.rq.sb + (int64_t)tt * p.rq.st + h * p.rq.sh + e0, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { C[j] = 0.0f; F[j] = 0.0f; if (!on) g[j] = 0.0f; }
+    if (coarse_on) load_bf8(p.coarse + row * D + e0, C);
+    if (fine_on) load_bf8(p.fine + row * D + e0, F);
+    const float den = fine_on ? p.den[row] : 1.0f;
+    float dlocal[8], dco[8], dnu[8], drq[8], dden_part = 0.0f, dl_part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      dlocal[j] = g[j];
+      dco[j] = 0.0f;
+      dnu[j] = 0.0f;
+      drq[j] = 0.0f;
+    }
+    if (fine_on) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float sc[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) sc[i] = rbf(rbf(a[i][j] * x[j]) + bb[i][j]);
+        sc[0] = rbf(sc[0] + (coarse_on ? kLogTwoBf16 : 0.0f));
+        const float top = coarse_on ? fmaxf(sc[0], fmaxf(sc[1], sc[2])) : fmaxf(sc[0], sc[2]);
+        float rho[3];
+        rho[0] = __expf(sc[0] - top);
+        rho[1] = coarse_on ? __expf(sc[1] - top) : 0.0f;
+        rho[2] = __expf(sc[2] - top);
+        const float inv = 1.0f / (rho[0] + rho[1] + rho[2]);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) rho[i] *= inv;
+        const float xv[3] = {rbf(2.0f * L[j]), rbf(p.gain * C[j]), rbf(p.gain * F[j])};
+        float dr[3], mean = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) { dr[i] = g[j] * xv[i]; mean += rho[i] * dr[i]; }
+        float dq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          const float ds = rho[i] * (dr[i] - mean);
+          dq += ds * a[i][j];
+          sfa[i][j] += ds * x[j];
+          sfb[i][j] += ds;
+        }
+        dlocal[j] = 2.0f * g[j] * rho[0];
+        sgain += g[j] * (rho[1] * C[j] + rho[2] * F[j]);
+        const float dfine = p.gain * g[j] * rho[2];
+        dco[j] = p.gain * g[j] * rho[1];
+        dnu[j] = dfine / den;
+        drq[j] = dq;
+        dden_part -= dfine * F[j] / den;
+      }
+    }
+    if (on) {
+      store_f8(p.dcoarse + row * D + e0, dco);
+      store_f8(p.dnum + row * D + e0, dnu);
+      store_f8(p.drq + row * D + e0, drq);
+      store_bf8(p.dlocal + row * D + e0, dlocal);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dl_part += dlocal[j] * L[j];
+    }
+    // h = softmax_D(raw_q) and the row sums (the row's LPR lanes)
+    float mx = x[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, x[j]);
+    mx = row_max<LPR>(mx);
+    float ex[8], sx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { ex[j] = __expf(x[j] - mx); sx += ex[j]; }
+    sx = row_sum<LPR>(sx);
+    const float dl = row_sum<LPR>(dl_part);
+    const float dd = row_sum<LPR>(dden_part);
+    if (on) {
+      float hv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) hv[j] = ex[j] / sx;
+      store_bf8(p.h + row * D + e0, hv);
+      if (cl == 0) {
+        p.delta[row] = dl;
+        p.dden[row] = dd;
+      }
+    }
+  }
+  if (p.dalpha_parts) {
+    const float sg = wave_sum_fold(sgain);
+    if (lane == 0) red[w] = sg;
+    __syncthreads();
+    if (tid == 0) {
+      float t = 0.0f;
+      for (int i = 0; i < NW; ++i) t += red[i];
+      p.dalpha_parts[blockIdx.x] = 2.0f * t;
+    }
+  }
+  // d fusion_a / d fusion_b: the wave's rows (lanes cl, cl + LPR, ...) by
+  // shuffles, then the waves in LDS, one atomic per (e, i).
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float va = sfa[i][j], vb = sfb[i][j];
+#pragma unroll
+      for (int off = LPR; off < 64; off <<= 1) {
+        va += __shfl_xor(va, off, 64);
+        vb += __shfl_xor(vb, off, 64);
+      }
+      if (lane < LPR) { facc[i][w][e0 + j] = va; facc[3 + i][w][e0 + j] = vb; }
+    }
+  __syncthreads();
+  for (int j = tid; j < 6 * D; j += kThreads) {
+    const int k = j / D, ee = j % D;
+    float sum = 0.0f;
+    for (int ww = 0; ww < NW; ++ww) sum += facc[k][ww][ee];
+    float* dst = k < 3 ? p.dfa : p.dfb;
+    atomicAdd(dst + (h * D + ee) * 3 + (k % 3), sum);
   }
 }
 
@@ -1287,19 +1478,32 @@ __global__ __launch_bounds__(kThreads) void finish_bwd_kernel(MemBwdParams p) {
 
 }  // namespace
 
+// The larger of the two kernels' grids (d alpha partials to allocate).
 int fuse_bwd_workgroups(int T, int B, int H) {
   return ((T + kFuseChunk - 1) / kFuseChunk) * B * H;
 }
 
 hipError_t launch_fuse_bwd(const TrainBwdParams& p, int head_dim, hipStream_t s) {
-  const int groups = fuse_bwd_workgroups(p.T, p.B, p.H);
+  // 16-byte rows for the vector kernel: aligned bases, bf16 strides in whole
+  // 8-element chunks (the fp32 and internal buffers are [rows][D] from aligned
+  // allocations)
+  auto al = [](const void* q) { return q == nullptr || ((uintptr_t)q & 15) == 0; };
+  const bool vec = al(p.grad) && al(p.rq.p) && al(p.local) && al(p.coarse) && al(p.fine) &&
+                   al(p.dlocal) && al(p.h) && al(p.dcoarse) && al(p.dnum) && al(p.drq) &&
+                   p.g_sb % 8 == 0 && p.g_st % 8 == 0 && p.g_sh % 8 == 0 && p.rq.sb % 8 == 0 &&
+                   p.rq.st % 8 == 0 && p.rq.sh % 8 == 0;
+  const int chunk = vec ? kFuseVecChunk : kFuseChunk;
+  const int groups = ((p.T + chunk - 1) / chunk) * p.B * p.H;
   const dim3 grid((unsigned)groups);
-  if (head_dim == 128)
-    hipLaunchKernelGGL(fuse_bwd_kernel<128>, grid, dim3(kThreads), 0, s, p);
-  else if (head_dim == 64)
-    hipLaunchKernelGGL(fuse_bwd_kernel<64>, grid, dim3(kThreads), 0, s, p);
-  else
+  if (head_dim == 128) {
+    if (vec) hipLaunchKernelGGL(fuse_bwd_vec_kernel<128>, grid, dim3(kThreads), 0, s, p);
+    else hipLaunchKernelGGL(fuse_bwd_kernel<128>, grid, dim3(kThreads), 0, s, p);
+  } else if (head_dim == 64) {
+    if (vec) hipLaunchKernelGGL(fuse_bwd_vec_kernel<64>, grid, dim3(kThreads), 0, s, p);
+    else hipLaunchKernelGGL(fuse_bwd_kernel<64>, grid, dim3(kThreads), 0, s, p);
+  } else {
     return hipErrorInvalidValue;
+  }
   if (p.dalpha_parts)
     hipLaunchKernelGGL(dalpha_kernel, dim3(1), dim3(256), 0, s, p.dalpha_parts, groups, p.dalpha);
   return hipGetLastError();

@@ -1476,6 +1476,49 @@ __global__ __launch_bounds__(kThreads) void finish_bwd_kernel(MemBwdParams p) {
   }
 }
 
+// The same with eight channels per lane (D / 8 lanes per row, 16-byte loads
+// and stores); launch_mem_bwd picks it when every row pointer is 16-byte
+// aligned.
+template <int D>
+__global__ __launch_bounds__(kThreads) void finish_bwd_vec_kernel(MemBwdParams p) {
+  constexpr int LPR = D / 8, RPB = kThreads / LPR;
+  const int tid = threadIdx.x;
+  const int rows = p.B * p.T * p.H;
+  const int row = blockIdx.x * RPB + tid / LPR;
+  const bool live = row < rows;
+  const size_t rr = live ? row : rows - 1;          // the row sum needs every lane
+  const int e0 = 8 * (tid % LPR);
+  const int t = (int)((rr / p.H) % p.T);
+  const bool hist = tile_visible(t / p.ft, p.keep / p.ft) > 0;
+  float hv[8], dh[8], s = 0.0f;
+  load_bf8(p.h + rr * D + e0, hv);
+  if (hist) {
+    const float4 d0 = *(const float4*)(p.dh + rr * D + e0);
+    const float4 d1 = *(const float4*)(p.dh + rr * D + e0 + 4);
+    dh[0] = d0.x; dh[1] = d0.y; dh[2] = d0.z; dh[3] = d0.w;
+    dh[4] = d1.x; dh[5] = d1.y; dh[6] = d1.z; dh[7] = d1.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dh[j] = 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s += hv[j] * dh[j];
+  s = row_sum<LPR>(s);
+  if (!live) return;
+  const float4 q0 = *(const float4*)(p.drq_fuse + rr * D + e0);
+  const float4 q1 = *(const float4*)(p.drq_fuse + rr * D + e0 + 4);
+  const float4 v0 = *(const float4*)(p.dv + rr * D + e0);
+  const float4 v1 = *(const float4*)(p.dv + rr * D + e0 + 4);
+  const float dq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+  const float dv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+  float g[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) g[j] = dq[j] + hv[j] * (dh[j] - s);
+  store_bf8(p.draw_q + rr * D + e0, g);
+  store_bf8(p.dv_out + rr * D + e0, dv);
+  if (t >= p.ft * p.v_max) *(uint4*)(p.draw_k + rr * D + e0) = make_uint4(0, 0, 0, 0);
+}
+
 }  // namespace
 
 // The larger of the two kernels' grids (d alpha partials to allocate).
@@ -1539,6 +1582,9 @@ hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s) {
   const int lag = p.keep / p.ft;
   const int dc_groups = (std::max(n_tiles - lag - 1, 1) + kObTiles - 1) / kObTiles;
   const int dg_groups = (p.group + kObTiles - 1) / kObTiles;
+  auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  const bool fin_vec = al(p.h) && al(p.dh) && al(p.drq_fuse) && al(p.dv) && al(p.draw_q) &&
+                       al(p.dv_out) && al(p.draw_k);
 #define TAO_MEM_BWD(D_)                                                                      \
   do {                                                                                       \
     if (p.v_max > 0) {                                                                       \
@@ -1565,9 +1611,14 @@ hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s) {
                          dim3(kWbWaves * 64), 0, s, p);                                      \
     }                                                                                        \
     const int rows = p.B * p.T * p.H;                                                        \
-    hipLaunchKernelGGL(finish_bwd_kernel<D_>,                                                \
-                       dim3((unsigned)((rows + kThreads / 64 - 1) / (kThreads / 64))),       \
-                       dim3(kThreads), 0, s, p);                                             \
+    constexpr int vrows = kThreads / (D_ / 8);                                               \
+    if (fin_vec)                                                                             \
+      hipLaunchKernelGGL(finish_bwd_vec_kernel<D_>, dim3((unsigned)((rows + vrows - 1) / vrows)),\
+                         dim3(kThreads), 0, s, p);                                           \
+    else                                                                                     \
+      hipLaunchKernelGGL(finish_bwd_kernel<D_>,                                              \
+                         dim3((unsigned)((rows + kThreads / 64 - 1) / (kThreads / 64))),     \
+                         dim3(kThreads), 0, s, p);                                           \
   } while (0)
   if (head_dim == 128)
     TAO_MEM_BWD(128);

@@ -1332,6 +1332,7 @@ struct WriterBwdSmem {
   bf16_t dct[D][D + 8];         // dC^T [e][d]
   float stat[3][D];             // max, 1 / Z, sum_e dC C (+ dz folded into the third)
   float red[kWbWaves][D];
+  float red2[kWbWaves][D];      // sum_e dC C partials
 };
 
 template <int D>
@@ -1355,15 +1356,25 @@ __global__ __launch_bounds__(kWbWaves * 64) void writer_bwd_kernel(MemBwdParams 
     sm.dct[e][d] = v;
     sm.dc[d][e] = v;
   }
-  // ---- column statistics over the 256 tokens: thread (d, token group)
+  // ---- column statistics over the 256 tokens: thread (d, token group) keeps
+  // its TPG column values in registers (one read of raw_k); the row term
+  // sum_e dC C is split over the same groups (EPG channels e each)
   {
-    constexpr int TG = NT / D, TPG = 256 / TG;
+    constexpr int TG = NT / D, TPG = 256 / TG, EPG = D / TG;
     const int d = tid % D, tg = tid / D;
     const bf16_t* col = p.raw_k.p + b * p.raw_k.sb + h * p.raw_k.sh + d;
+    float xv[TPG];
+#pragma unroll
+    for (int i = 0; i < TPG; ++i) xv[i] = bf2f(col[(int64_t)(tok0 + tg * TPG + i) * p.raw_k.st]);
+    float sdc = 0.0f;
+#pragma unroll 4
+    for (int e = tg * EPG; e < (tg + 1) * EPG; ++e)
+      sdc = fmaf(dcg[(size_t)e * D + d], bf2f(c[(size_t)e * D + d]), sdc);
     float m = -__builtin_inff();
-    for (int i = 0; i < TPG; ++i)
-      m = fmaxf(m, bf2f(col[(int64_t)(tok0 + tg * TPG + i) * p.raw_k.st]));
+#pragma unroll
+    for (int i = 0; i < TPG; ++i) m = fmaxf(m, xv[i]);
     sm.red[tg][d] = m;
+    sm.red2[tg][d] = sdc;
     __syncthreads();
     if (tg == 0) {
       for (int i = 1; i < TG; ++i) m = fmaxf(m, sm.red[i][d]);
@@ -1372,16 +1383,16 @@ __global__ __launch_bounds__(kWbWaves * 64) void writer_bwd_kernel(MemBwdParams 
     __syncthreads();
     m = sm.stat[0][d];
     float z = 0.0f;
-    for (int i = 0; i < TPG; ++i)
-      z += __expf(bf2f(col[(int64_t)(tok0 + tg * TPG + i) * p.raw_k.st]) - m);
-    sm.red[tg][d] = z;
+#pragma unroll
+    for (int i = 0; i < TPG; ++i) z += __expf(xv[i] - m);
+    sm.red[tg][d] = z;                         // the max partials were read before the barrier
     __syncthreads();
     if (tg == 0) {
       for (int i = 1; i < TG; ++i) z += sm.red[i][d];
       sm.stat[1][d] = 1.0f / z;
-      float sdc = 0.0f;
-      for (int e = 0; e < D; ++e) sdc = fmaf(dcg[(size_t)e * D + d], bf2f(c[(size_t)e * D + d]), sdc);
-      sm.stat[2][d] = sdc - dzf[d];            // dk = P (dP - stat2)
+      float sd = 0.0f;
+      for (int i = 0; i < TG; ++i) sd += sm.red2[i][d];
+      sm.stat[2][d] = sd - dzf[d];             // dk = P (dP - stat2)
     }
     __syncthreads();
   }

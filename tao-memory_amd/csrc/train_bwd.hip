@@ -1019,11 +1019,12 @@ TAO_DEV void unpack8f_bwd(const uint4& u, float out[8]) {
 // per fine: a query's dnum and h rows are read once for all NF fines) and
 // reduced with v_mfma_f32_32x32x16_bf16 (m = e, n = d, k = q); wave w owns
 // output tiles w, w + 4, ... of the (D / 32)^2 tiles of every fine. A
-// workgroup takes kObTiles of an item's tiles (grid = items x tile groups x
-// B*H) and adds its sums into the zeroed output with fp32 atomics; the first
-// group adds the coarse share.
+// workgroup takes kObTiles (dC) or kObTilesG (dG) of an item's tiles (grid =
+// items x tile groups x B*H) and adds its sums into the zeroed output with
+// fp32 atomics; the first group adds the coarse share.
 constexpr int kObQ = 32;
-constexpr int kObTiles = 4;
+constexpr int kObTiles = 2;    // query tiles per dC workgroup (mode 0)
+constexpr int kObTilesG = 1;   // query tiles per dG workgroup (mode 1: few items, more groups)
 template <int D> constexpr int kObFines = D == 64 ? 4 : 2;
 
 template <int D, int NF>
@@ -1038,8 +1039,8 @@ __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int
   const int b = bh / p.H, h = bh % p.H;
   const int G = p.group, lag = p.keep / p.ft;
   const int n_tiles = (p.T + p.ft - 1) / p.ft;
-  const int groups = mode == 0 ? (max(n_tiles - lag - 1, 1) + kObTiles - 1) / kObTiles
-                               : (G + kObTiles - 1) / kObTiles;
+  const int tpg = mode == 0 ? kObTiles : kObTilesG;
+  const int groups = mode == 0 ? (max(n_tiles - lag - 1, 1) + tpg - 1) / tpg : (G + tpg - 1) / tpg;
   const int item = blockIdx.x / BH / groups, tg = (blockIdx.x / BH) % groups;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 31, hl = lane >> 5;
@@ -1053,8 +1054,8 @@ __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int
   const int f0 = item * NF, Kc = p.coarse_first + item;
   const int t_first = mode == 0 ? f0 + lag + 1 : lag + G * Kc;
   const int t_last = mode == 0 ? n_tiles : min(n_tiles, lag + G * Kc + G);
-  const int t_lo = t_first + tg * kObTiles;
-  const int t_hi = min(t_last, t_lo + kObTiles);
+  const int t_lo = t_first + tg * tpg;
+  const int t_hi = min(t_last, t_lo + tpg);
   if (t_lo >= t_hi) return;                          // workgroup-uniform
   const bf16_t* gsw = p.fine_sw + (size_t)bh * p.fine_cap * D;
   // Per tile, the NF fines' page and segment weights (query-independent) in
@@ -1592,7 +1593,7 @@ hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s) {
   if (p.group != 8 || p.ft != 256 || p.v_max / p.group + 1 > 64) return hipErrorInvalidValue;
   const int lag = p.keep / p.ft;
   const int dc_groups = (std::max(n_tiles - lag - 1, 1) + kObTiles - 1) / kObTiles;
-  const int dg_groups = (p.group + kObTiles - 1) / kObTiles;
+  const int dg_groups = (p.group + kObTilesG - 1) / kObTilesG;
   auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
   const bool fin_vec = al(p.h) && al(p.dh) && al(p.drq_fuse) && al(p.dv) && al(p.draw_q) &&
                        al(p.dv_out) && al(p.draw_k);

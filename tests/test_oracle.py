@@ -183,6 +183,48 @@ def test_fusion_closed_form():
     torch.testing.assert_close(out.double(), ref, atol=5e-2, rtol=3e-2)
 
 
+def _three_branch_closed_form(raw_q, local, coarse, fine, a, bias, alpha, local_bias):
+    """fp64: rho = softmax(s0 + local_bias, s1, s2), s_i = a_i q + b_i;
+    out = 2 rho0 local + 2 alpha (rho1 coarse + rho2 fine)."""
+    q = raw_q.double()
+    s = [a[..., i].double() * q + bias[..., i].double() for i in range(3)]
+    s[0] = s[0] + local_bias
+    rho = torch.softmax(torch.stack(s, -1), -1)
+    return (2 * rho[..., 0] * local.double()
+            + 2 * alpha * (rho[..., 1] * coarse.double() + rho[..., 2] * fine.double()))
+
+
+def test_fusion_three_branch_closed_form():
+    """Coarse and fine present (fusion_pointwise.py:10-47, 50-92; the local
+    score carries log(#present history branches) = log 2): the oracle equals
+    the closed form within bf16 rounding, and the same closed form without
+    the local bias, or with the coarse and fine operands swapped, is far from
+    it, so a dropped bias or a transposed branch would fail this test."""
+    torch.manual_seed(9)
+    h, d, t = 3, 32, 6
+    raw_q = torch.randn(1, t, h, d).to(BF16)
+    local, coarse, fine = (torch.randn(1, t, h, d).to(BF16) for _ in range(3))
+    a = torch.randn(h, d, 3) * 0.5
+    bias = torch.randn(h, d, 3) * 0.5
+    alpha = 0.75
+    out = O.fusion(raw_q, local, coarse, fine, a, bias, alpha, True, True).double()
+    # The oracle rounds a and b to bf16 before use (fusion_pointwise.py:103-108).
+    a16, b16 = a.to(BF16).float(), bias.to(BF16).float()
+    ref = _three_branch_closed_form(raw_q, local, coarse, fine, a16, b16, alpha, math.log(2))
+    torch.testing.assert_close(out, ref, atol=5e-2, rtol=3e-2)
+    no_bias = _three_branch_closed_form(raw_q, local, coarse, fine, a16, b16, alpha, 0.0)
+    swapped = _three_branch_closed_form(raw_q, local, fine, coarse, a16, b16, alpha, math.log(2))
+    for wrong in (no_bias, swapped):
+        assert (out - wrong).abs().max().item() > 0.2
+    # Coarse present, fine absent: one history branch, so the local bias is
+    # log 1 = 0 (fusion_pointwise.py:99-100) and the fine branch drops out.
+    only_coarse = O.fusion(raw_q, local, coarse, fine, a, bias, alpha, True, False).double()
+    s = [a16[..., i].double() * raw_q.double() + b16[..., i].double() for i in (0, 1)]
+    rho = torch.softmax(torch.stack(s, -1), -1)
+    ref1 = 2 * rho[..., 0] * local.double() + 2 * alpha * rho[..., 1] * coarse.double()
+    torch.testing.assert_close(only_coarse, ref1, atol=5e-2, rtol=3e-2)
+
+
 def test_normalisation_properties():
     """Segment weights of a page sum to one (pz = logsumexp of the page's z);
     page weights sum to one over pages, h over channels; hv is the rounded

@@ -37,7 +37,7 @@ enum tao_status {
   TAO_E_WORKSPACE = -4   /* workspace too small */
 };
 
-enum tao_dtype { TAO_BF16 = 0, TAO_FP32 = 1 };
+enum tao_dtype { TAO_BF16 = 0, TAO_FP32 = 1, TAO_FP16 = 2 };
 
 /* Device-resident state of one request x layer (reference StreamCache +
  * LayerState, tao_stream.py:126-160, 790-834), laid out for HBM streaming:
@@ -90,8 +90,9 @@ typedef struct tao_tokens {
   int32_t tokens;
 } tao_tokens;
 
-/* Caller fusion parameters: fusion_a/b [H, D, 3] of dtype `dtype`
- * (cast to bf16 round-to-nearest-even inside, fusion_pointwise.py:103-108),
+/* Caller fusion parameters: fusion_a/b [H, D, 3], both of dtype `dtype`
+ * (TAO_BF16, TAO_FP32 or TAO_FP16; read in place on every call and cast to
+ * bf16 round-to-nearest-even inside, fusion_pointwise.py:103-108),
  * gain = bf16(2 * alpha) (operator.py:89). */
 typedef struct tao_fusion {
   const void* fusion_a; const void* fusion_b;

@@ -136,8 +136,8 @@ int check_tokens(const tao_tokens* tok) {
 
 int check_fusion(const tao_fusion* fu) {
   if (!fu || !fu->fusion_a || !fu->fusion_b) return fail(TAO_E_ARGUMENT, "null fusion parameters");
-  if (fu->dtype != TAO_BF16 && fu->dtype != TAO_FP32)
-    return fail(TAO_E_ARGUMENT, "fusion dtype must be bf16 or fp32");
+  if (fu->dtype != TAO_BF16 && fu->dtype != TAO_FP32 && fu->dtype != TAO_FP16)
+    return fail(TAO_E_ARGUMENT, "fusion dtype must be bf16, fp32 or fp16");
   return TAO_OK;
 }
 

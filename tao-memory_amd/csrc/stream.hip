@@ -132,21 +132,30 @@ struct Batch {
   int heads = 0, head_dim = 0, keep = 0, fine = 0, group = 0, coarse_values = 0;
 };
 
+// The device table entry of one request: its buffers as its driver holds them.
+tao::BatchReq table_entry(const tao_state_dev& st) {
+  const tao::WorkspaceLayout lay =
+      tao::workspace_layout(st.batch, st.heads, st.head_dim, st.sel_cap, 0);
+  tao::BatchReq t{};
+  t.ring_k = (bf16_t*)st.ring_k;
+  t.ring_v = (bf16_t*)st.ring_v;
+  t.ring_raw = (bf16_t*)st.ring_raw;
+  t.fold_g = (const float*)st.fold_g;
+  t.fold_den = (const float*)st.fold_den;
+  t.coarse_g = (const float*)st.coarse_g;
+  t.header = st.header;
+  t.parts = (float*)((char*)st.workspace + lay.parts_off);
+  return t;
+}
+
+bool same_entry(const tao::BatchReq& a, const tao::BatchReq& b) {
+  return a.ring_k == b.ring_k && a.ring_v == b.ring_v && a.ring_raw == b.ring_raw &&
+         a.fold_g == b.fold_g && a.fold_den == b.fold_den && a.coarse_g == b.coarse_g &&
+         a.header == b.header && a.parts == b.parts;
+}
+
 int fill_table(Batch* b, void* stream) {
-  for (size_t r = 0; r < b->reqs.size(); ++r) {
-    const tao_state_dev& st = b->reqs[r]->st;
-    const tao::WorkspaceLayout lay =
-        tao::workspace_layout(st.batch, st.heads, st.head_dim, st.sel_cap, 0);
-    tao::BatchReq& t = b->host_table[r];
-    t.ring_k = (bf16_t*)st.ring_k;
-    t.ring_v = (bf16_t*)st.ring_v;
-    t.ring_raw = (bf16_t*)st.ring_raw;
-    t.fold_g = (const float*)st.fold_g;
-    t.fold_den = (const float*)st.fold_den;
-    t.coarse_g = (const float*)st.coarse_g;
-    t.header = st.header;
-    t.parts = (float*)((char*)st.workspace + lay.parts_off);
-  }
+  for (size_t r = 0; r < b->reqs.size(); ++r) b->host_table[r] = table_entry(b->reqs[r]->st);
   const hipError_t e = hipMemcpyAsync(b->table, b->host_table.data(),
                                       b->host_table.size() * sizeof(tao::BatchReq),
                                       hipMemcpyHostToDevice, (hipStream_t)stream);
@@ -323,8 +332,19 @@ int tao_batch_decode(void* batch, const tao_tokens* tok, const tao_fusion* fu, v
   if (tok->tokens != 1) return stream_fail(TAO_E_SHAPE, "batched decode takes one token per request");
   if (!tok->q || !tok->k || !tok->v || !tok->raw_q || !tok->raw_k)
     return stream_fail(TAO_E_ARGUMENT, "null token operand");
-  if (!fu->fusion_a || !fu->fusion_b || (fu->dtype != TAO_BF16 && fu->dtype != TAO_FP32))
+  if (!fu->fusion_a || !fu->fusion_b ||
+      (fu->dtype != TAO_BF16 && fu->dtype != TAO_FP32 && fu->dtype != TAO_FP16))
     return stream_fail(TAO_E_ARGUMENT, "invalid fusion parameters");
+  // A member whose buffers moved since the table was uploaded (its host
+  // re-synced the driver but not the batch) gets the table refreshed first:
+  // the step kernels must never follow a stale buffer address.
+  for (int r = 0; r < R; ++r) {
+    if (!same_entry(b->host_table[r], table_entry(b->reqs[r]->st))) {
+      const int rc = tao_batch_sync(b, stream);
+      if (rc) return rc;
+      break;
+    }
+  }
   for (int r = 0; r < R; ++r) {
     Stream* s = b->reqs[r];
     const tao_tokens t = row_tokens(tok, r);

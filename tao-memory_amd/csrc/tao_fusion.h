@@ -12,8 +12,11 @@
 
 namespace tao {
 
+// A caller fusion parameter as fp32 (exact for every accepted dtype).
 TAO_DEV float load_param(const void* p, int dtype, int64_t off) {
-  return dtype == TAO_FP32 ? ((const float*)p)[off] : bf2f(((const bf16_t*)p)[off]);
+  if (dtype == TAO_FP32) return ((const float*)p)[off];
+  if (dtype == TAO_FP16) return (float)((const _Float16*)p)[off];
+  return bf2f(((const bf16_t*)p)[off]);
 }
 
 // bf16(fp32(log 2)) = 0.69140625: the local bias when two history branches

@@ -16,6 +16,8 @@ _lib = None
 
 TAO_BF16 = 0
 TAO_FP32 = 1
+TAO_FP16 = 2
+_PARAM_DTYPES = {torch.bfloat16: TAO_BF16, torch.float32: TAO_FP32, torch.float16: TAO_FP16}
 
 _i32, _i64, _sz, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 _I64x3 = ctypes.c_int64 * 3
@@ -270,9 +272,11 @@ _FUSION_CACHE = {}
 def fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on, like=None):
     """Fusion struct, cached per (parameter tensors, alpha, presence).
 
-    Parameters stay read in place by the kernels, so in-place updates of
-    fp32/bf16 fusion tensors are seen by later calls; a tensor whose storage
-    or layout changed gets a new struct.
+    Parameters of one dtype among bf16, fp32 and fp16 are read in place by
+    the kernels, so in-place updates are seen by later calls; a tensor whose
+    storage or layout changed gets a new struct. Other dtypes and mixed pairs
+    are converted to fp32 on every call and never cached (the reference casts
+    them on every call too, operator.py:23-24, fusion_pointwise.py:103-108).
     """
     key = (id(fusion_a), id(fusion_b), alpha, coarse_on, fine_on,
            None if like is None else (like.shape[2], like.shape[3], like.device))
@@ -293,6 +297,8 @@ def fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on, like=None):
             if t.device != like.device:
                 raise ValueError("fusion parameters must live on the operands' device")
     fu = _make_fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on)
+    if fu.converted:
+        return fu
     fu._check = (fusion_a.data_ptr(), fusion_b.data_ptr(), fusion_a.stride(),
                  fusion_b.stride(), fusion_a.dtype, fusion_b.dtype)
     if len(_FUSION_CACHE) > 64:
@@ -304,14 +310,15 @@ def fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on, like=None):
 def _make_fusion(fusion_a, fusion_b, alpha, coarse_on, fine_on):
     originals = (fusion_a, fusion_b)
     fu = Fusion()
-    if fusion_a.dtype == torch.float32 and fusion_b.dtype == torch.float32:
-        fu.dtype = TAO_FP32
-    elif fusion_a.dtype == torch.bfloat16 and fusion_b.dtype == torch.bfloat16:
-        fu.dtype = TAO_BF16
-    else:
+    code = _PARAM_DTYPES.get(fusion_a.dtype)
+    fu.converted = code is None or fusion_b.dtype != fusion_a.dtype
+    if fu.converted:
+        # A per-call copy: the caller's later in-place updates reach the
+        # next call's copy, never a cached one.
         fusion_a = fusion_a.float()
         fusion_b = fusion_b.float()
-        fu.dtype = TAO_FP32
+        code = TAO_FP32
+    fu.dtype = code
     fu.fusion_a, fu.fusion_b = fusion_a.data_ptr(), fusion_b.data_ptr()
     fu.a_s = i64x3(fusion_a.stride())
     fu.b_s = i64x3(fusion_b.stride())

@@ -26,6 +26,7 @@ cursor (schedule.py), so no device-to-host synchronisation is needed.
 
 import contextlib
 import ctypes
+import itertools
 
 import numpy as np
 import torch
@@ -39,6 +40,11 @@ _STATS_CAP = 8          # blocks per statistics pass of the regularized writer
 # Fine writers the stream implements: the softmax writer and the regularized
 # association writer (same z and read, association value matrices).
 _STREAM_WRITERS = ("softmax", "regularized_association")
+# Process-wide serial numbers for buffer generations and native drivers: a
+# reset state reallocates its buffers and reopens its driver, and neither the
+# new handle's address nor a per-state counter is guaranteed to differ from
+# the old one's, so a batch keys its binding on these instead.
+_SERIAL = itertools.count(1)
 
 
 class _DeviceState:
@@ -75,7 +81,7 @@ class _DeviceState:
             self.pending_cross = torch.zeros(dd, dtype=torch.float32, device=device)
             self.stats = torch.empty((2, _STATS_CAP * batch, heads, head_dim, head_dim),
                                      dtype=torch.float32, device=device)
-        self.generation = 0          # bumped whenever the buffers move
+        self.generation = next(_SERIAL)   # renewed whenever the buffers move
         self.fine_cap = 0
         self._allocate(fine_cap, copy_fines=0)
 
@@ -113,7 +119,7 @@ class _DeviceState:
         self.bank, self.fine_z, self.fine_sw = bank, fine_z, fine_sw
         self.page_z, self.page_w, self.sel, self.chosen = page_z, page_w, sel, chosen
         self.page_c = page_c
-        self.generation += 1
+        self.generation = next(_SERIAL)
         self.fine_cap, self.page_cap, self.sel_cap, self.chosen_cap = (
             fine_cap, page_cap, sel_cap, chosen_cap)
         self.plan_words = 0
@@ -123,7 +129,7 @@ class _DeviceState:
         ws_bytes = _hip.lib().tao_workspace_bytes(self.B, self.H, self.D, self.sel_cap,
                                                   plan_words)
         self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=self.device)
-        self.generation += 1
+        self.generation = next(_SERIAL)
         self.plan_words = plan_words
         self.struct = self._make_struct()
         _hip.check(_hip.lib().tao_workspace_init(ctypes.byref(self.struct), self.stream()))
@@ -250,6 +256,7 @@ class StreamCache:
         self._probe = None
         self._tok = None
         self._handle = None          # native stream driver (stream.hip)
+        self._handle_serial = 0      # process-unique id of the open driver
         self._handle_dirty = True
         self._fast = None            # decode fast-path key (see decode)
         self._native = None          # native decode entry (tao_fast.cpp)
@@ -517,6 +524,7 @@ class StreamCache:
                 self.route_size, staging.data_ptr() if staging is not None else None,
                 out_stage.data_ptr() if out_stage is not None else None, ctypes.byref(handle)))
             self._handle = handle
+            self._handle_serial = next(_SERIAL)
         elif self._handle_dirty:
             _hip.check(_hip.lib().tao_stream_sync(
                 self._handle, ctypes.byref(dev.struct), self.position, self.route_coarse,
@@ -588,7 +596,9 @@ class StreamCache:
         self._stream_index = q.device.index if q.device.index is not None else \
             torch.cuda.current_device()
         self._call = _hip.lib().tao_stream_decode
-        fast_ok = (self._tok._strides == strides)   # operands used in place
+        # Operands used in place, and fusion parameters the kernels read in
+        # place (a converted copy would freeze the parameters' values).
+        fast_ok = self._tok._strides == strides and not fu.converted
         self._fast = ((shape,) * 5, (q.dtype,) * 5 + (q.device,) * 5, strides,
                       fusion_a, fusion_b, alpha, fusion_a.data_ptr(), fusion_b.data_ptr(),
                       limit) if fast_ok else None
@@ -995,7 +1005,7 @@ class DecodeBatch:
             if dev.B != 1:
                 raise ValueError("batched decode takes one-request states (batch 1)")
             st._driver(dev)
-        key = tuple((id(st), st._handle.value) for st in self.states)
+        key = tuple((id(st), st._handle_serial) for st in self.states)
         gens = tuple(st._dev.generation for st in self.states)
         lib = _hip.lib()
         stream = self.states[0]._dev.stream()

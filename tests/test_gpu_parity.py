@@ -205,6 +205,32 @@ def test_contract_errors(device):
                              fusion_b=fb.to(device), alpha=0.5, state=state, position=0)
 
 
+@pytest.mark.parametrize("dtypes", [(torch.float16, torch.float16),
+                                    (torch.float32, torch.bfloat16)])
+def test_fusion_parameters_updated_in_place(device, dtypes):
+    """fusion_a / fusion_b of fp16 or of mixed dtypes, updated in place between
+    calls (an optimizer step): each call must use the values the tensors hold
+    at that call, as the reference's per-call cast does (operator.py:23-24).
+    Compared bitwise with fresh fp32 copies (fp16 and bf16 widen exactly)."""
+    heads, width = 2, 64
+    xs, fa, fb = inputs(1000, heads, width, seed=23)
+    d = to_dev(xs, device)
+    fa_live, fb_live = fa.to(device, dtypes[0]), fb.to(device, dtypes[1])
+    print(f"fusion parameters in place {dtypes}", flush=True)
+    live = new_state(0, index_only_page_memo())
+    fresh = new_state(0, index_only_page_memo())
+    for st in (live, fresh):
+        run_hip(st, [x[:, :990] for x in d], fa_live.float(), fb_live.float(), [990])
+    for step in range(990, 1000):
+        tok = [x[:, step:step + 1] for x in d]
+        want = run_hip(fresh, tok, fa_live.float(), fb_live.float(), [1])
+        got = run_hip(live, tok, fa_live, fb_live, [1])
+        assert torch.equal(got, want), step
+        with torch.no_grad():
+            fa_live.mul_(1.5)
+            fb_live.add_(0.25)
+
+
 def test_ingest_state_equals_prefill_state(device):
     """Writer-only state construction (bench state builder) == real prefill."""
     heads, width = 4, 128
@@ -372,6 +398,56 @@ def test_batched_decode_equals_per_request(device, coarse):
         for (pz, pc, fz), (qz, qc, gz) in zip(sa["pages"], sb["pages"]):
             assert torch.equal(pz, qz) and torch.equal(fz, gz)
             assert (pc is None and qc is None) or torch.equal(pc, qc)
+
+
+def test_batched_decode_after_member_reset(device):
+    """A member of a running batch is reset and prefilled again (its buffers
+    and native driver are recreated, possibly at recycled addresses): the
+    batch must rebind to the new buffers and keep equalling per-request
+    decode, bitwise, for every member."""
+    from tao_attention import tao_attention_decode_batch
+    heads, width = 2, 64
+    lengths = [1300, 2000, 900]
+    fa, fb = (torch.randn(heads, width, 3, generator=torch.Generator().manual_seed(19)) * 0.02
+              for _ in range(2))
+    fa, fb = fa.to(device), fb.to(device)
+    xs = [to_dev(inputs(n + 60, heads, width, seed=120 + r)[0], device)
+          for r, n in enumerate(lengths)]
+    print("batched decode after a member reset", flush=True)
+
+    def prefill(st, x, n):
+        q, k, v, rq, rk = (t[:, :n] for t in x)
+        tao_attention_prefill(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa, fusion_b=fb,
+                              alpha=0.5, state=st, position=0)
+
+    batched = [new_state(0, index_only_page_memo()) for _ in lengths]
+    single = [new_state(0, index_only_page_memo()) for _ in lengths]
+    for group in (batched, single):
+        for st, x, n in zip(group, xs, lengths):
+            prefill(st, x, n)
+    cursor = list(lengths)
+
+    def step():
+        rows = [[x[i][:, c:c + 1] for i in range(5)] for x, c in zip(xs, cursor)]
+        q, k, v, rq, rk = (torch.cat([row[i] for row in rows], 0) for i in range(5))
+        got, _ = tao_attention_decode_batch(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa,
+                                            fusion_b=fb, alpha=0.5, states=batched)
+        for r, st in enumerate(single):
+            want, _ = tao_attention_decode(*rows[r][:3], raw_q=rows[r][3], raw_k=rows[r][4],
+                                           fusion_a=fa, fusion_b=fb, alpha=0.5, state=st,
+                                           position=st.get_pos())
+            assert torch.equal(got[r:r + 1], want), (cursor, r)
+        for r in range(len(cursor)):
+            cursor[r] += 1
+
+    for _ in range(10):
+        step()
+    for group in (batched, single):
+        group[1].reset()
+        prefill(group[1], xs[1], lengths[1] - 700)
+    cursor[1] = lengths[1] - 700
+    for _ in range(30):
+        step()
 
 
 def _saved_and_loaded(snapshot):

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 5
+#define TAO_ABI_VERSION 6
 
 enum tao_status {
   TAO_OK = 0,
@@ -340,6 +340,13 @@ typedef struct tao_train_bwd {
    * gain = 2 alpha (no reference counterpart: the reference takes alpha as a
    * Python float, operator.py:34). */
   float* dalpha_out;
+  /* Optional: bf16 [B, T, H, D] contiguous. Non-null when the forward's local
+   * attention came from a caller plugin (tao_attention's local_flash,
+   * operator.py:42-47, tao_stream.py:760-787): it receives d out / d local,
+   * the local-attention adjoint is skipped (the caller differentiates its
+   * plugin), local_lse, dq and dk may be null, and dv holds only the
+   * writer's share. */
+  void* dlocal_out;
 } tao_train_bwd;
 
 /* Workspace bytes of tao_train_backward for a full-sequence read of `tokens`

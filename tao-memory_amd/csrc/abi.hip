@@ -981,9 +981,12 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   if (!rc) rc = check_tokens(tok);
   if (!rc) rc = check_fusion(fu);
   if (rc) return rc;
-  if (!a || !a->grad || !a->local || !a->local_lse || !a->dq || !a->dk || !a->dv ||
-      !a->draw_q || !a->draw_k || !a->dfusion_a || !a->dfusion_b || !a->workspace)
+  if (!a || !a->grad || !a->local || !a->dv || !a->draw_q || !a->draw_k || !a->dfusion_a ||
+      !a->dfusion_b || !a->workspace)
     return fail(TAO_E_ARGUMENT, "null backward argument");
+  const bool plugin_local = a->dlocal_out != nullptr;
+  if (!plugin_local && (!a->local_lse || !a->dq || !a->dk))
+    return fail(TAO_E_ARGUMENT, "null local-attention save or gradient");
   const int T = tok->tokens;
   const int ft = st->fine_tokens, keep = st->local_keep, G = st->coarse_group;
   const int n_tiles = (T + ft - 1) / ft;
@@ -1044,7 +1047,14 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   fp.dalpha_parts = a->dalpha_out ? (float*)(ws + l.dalpha_parts) : nullptr;
   e = tao::launch_fuse_bwd(fp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_train_backward fusion");
-  // ---- local attention adjoint
+  // ---- local attention adjoint (or d local for the caller's plugin)
+  if (plugin_local) {
+    e = hipMemcpyAsync(a->dlocal_out, fp.dlocal, (size_t)B * T * H * D * sizeof(bf16_t),
+                       hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess)
+      e = hipMemsetAsync(ws + l.dvf, 0, (size_t)B * T * H * D * sizeof(float), s);
+    if (e != hipSuccess) return check_hip(e, "tao_train_backward d local");
+  }
   tao::AttnBwdParams ap{};
   ap.q = view(tok->q, tok->q_s);
   ap.k = view(tok->k, tok->k_s);
@@ -1060,7 +1070,7 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   ap.T = T;
   ap.ft = ft;
   ap.keep = keep;
-  e = tao::launch_attn_bwd(ap, D, s);
+  e = plugin_local ? hipSuccess : tao::launch_attn_bwd(ap, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_train_backward local attention");
   // ---- memory branch, writer, final gradients
   tao::MemBwdParams mp{};

@@ -63,7 +63,7 @@ class TrainBwd(ctypes.Structure):
                 ("dq", _vp), ("dk", _vp), ("dv", _vp), ("draw_q", _vp), ("draw_k", _vp),
                 ("dfusion_a", _vp), ("dfusion_b", _vp),
                 ("workspace", _vp), ("workspace_bytes", _sz),
-                ("dz_out", _vp), ("dc_out", _vp), ("dalpha_out", _vp)]
+                ("dz_out", _vp), ("dc_out", _vp), ("dalpha_out", _vp), ("dlocal_out", _vp)]
 
 
 class StreamCfg(ctypes.Structure):
@@ -73,6 +73,18 @@ class StreamCfg(ctypes.Structure):
 
 
 PLAN_HEADER = 16
+PLAN_ATTN_TILES = 1
+
+
+def without_attention(plan):
+    """A prefill plan with its local-attention section removed: the call's
+    local output then comes from the caller (a local_flash plugin) through
+    tao_prefill's `local` buffer."""
+    import numpy as np
+    n = int(plan[PLAN_ATTN_TILES])
+    out = np.concatenate((plan[:PLAN_HEADER], plan[PLAN_HEADER + 3 * n:]))
+    out[PLAN_ATTN_TILES] = 0
+    return out
 
 
 class Fusion(ctypes.Structure):

@@ -59,3 +59,75 @@ def flash_attn_func(q, k, v, causal=True, window_size=(-1, 0)):
 
 
 flash_attn = SimpleNamespace(flash_attn_func=flash_attn_func)
+
+
+def caller_plugin(local_flash):
+    """The caller's local_flash plugin, or None for this module's own kernel
+    (the default, operator.py:42-47): only a foreign plugin changes how the
+    local attention is computed."""
+    if local_flash is None or local_flash is flash_attn:
+        return None
+    if not callable(getattr(local_flash, "flash_attn_func", None)):
+        raise TypeError("local_flash must provide flash_attn_func(q, k, v, causal, window_size)")
+    return local_flash
+
+
+def _bf16(x):
+    return x if x.dtype == torch.bfloat16 and x.is_contiguous() else x.to(torch.bfloat16).contiguous()
+
+
+def plugin_training_local(plugin, q, k, v, config):
+    """The full-sequence local attention on a caller plugin, with the
+    reference's call pattern (_local_training_corrected_4k,
+    tao_stream.py:760-787): a sequence of whole 256-token tiles of at least
+    three tiles is one causal call on the first tile, one suffix call of the
+    second tile over 512 keys, and one batched call of every later tile over
+    its 768-key window; any other length is one call per tile over its
+    window [max(0, start - local_keep), end). Differentiable when the plugin
+    is."""
+    call = plugin.flash_attn_func
+    b, total, heads, d = q.shape
+    ft, keep = config.fine_tokens, config.local_keep
+    window = keep + ft
+    if ft != 256 or keep != 512 or total < 3 * ft or total % ft:
+        parts = [call(q[:, s:min(total, s + ft)], k[:, max(0, s - keep):min(total, s + ft)],
+                      v[:, max(0, s - keep):min(total, s + ft)], causal=True,
+                      window_size=(-1, 0)) for s in range(0, total, ft)]
+        return torch.cat(parts, 1)
+    tiles = total // ft - 2
+    head = [call(q[:, :ft], k[:, :ft], v[:, :ft], causal=True, window_size=(-1, 0)),
+            call(q[:, ft:2 * ft], k[:, :2 * ft], v[:, :2 * ft], causal=True,
+                 window_size=(-1, 0))]
+
+    def windows(x):       # [B, T, H, D] -> [B * tiles, 768, H, D], tile t = rows [256 t, 256 t + 768)
+        return x.unfold(1, window, ft).permute(0, 1, 4, 2, 3).reshape(b * tiles, window, heads, d)
+
+    rest = call(q[:, 2 * ft:].reshape(b * tiles, ft, heads, d), windows(k), windows(v),
+                causal=True, window_size=(-1, 0))
+    return torch.cat(head + [rest.reshape(b, total - 2 * ft, heads, d)], 1)
+
+
+def plugin_stream_local(plugin, q, k, v, window_k, window_v, pos0, config):
+    """A streaming call's local attention on a caller plugin, with the
+    reference's call pattern (StreamCache.process, tao_stream.py:919-934):
+    the call's tokens split at next_chunk (min(rest, fine_tokens,
+    serve_limit - local length)), and each chunk's queries attend to the
+    retained local window plus the chunk's keys. window_k / window_v hold
+    the retained window before pos0 ([B, n, H, D], n = local length at pos0).
+    Returns bf16 [B, T, H, D] contiguous."""
+    from . import schedule
+    total = q.shape[1]
+    base = pos0 - window_k.shape[1]
+    keys = torch.cat((window_k, k), 1) if window_k.shape[1] else k
+    vals = torch.cat((window_v, v), 1) if window_v.shape[1] else v
+    parts, start = [], 0
+    while start < total:
+        p = pos0 + start
+        width = schedule.next_chunk(p, total - start, config)
+        first = p - schedule.local_len_at(p, config) - base
+        end = p + width - base
+        parts.append(_bf16(plugin.flash_attn_func(q[:, start:start + width], keys[:, first:end],
+                                                  vals[:, first:end], causal=True,
+                                                  window_size=(-1, 0))))
+        start += width
+    return torch.cat(parts, 1).contiguous()

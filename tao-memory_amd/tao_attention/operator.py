@@ -10,7 +10,7 @@ import torch  # noqa: F401
 
 from . import training
 from .config import TaoConfig
-from .flash_attention import flash_attn
+from .flash_attention import caller_plugin
 from .tao_stream import StreamCache
 
 DEFAULT_CONFIG = TaoConfig()
@@ -20,12 +20,13 @@ def tao_attention(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b, alpha,
                   config=DEFAULT_CONFIG, local_flash=None):
     """Full sequence read with fresh routing at every query (operator.py:40-52).
 
-    Forward on the HIP library (training.py); its backward is not built and
-    raises when autograd reaches it.
+    Forward and backward on the HIP library (training.py). A caller
+    local_flash plugin computes the local attention with the reference's
+    tiling (tao_stream.py:760-787) and is differentiated by autograd; the
+    rest stays on the HIP path.
     """
-    _check_plugin(local_flash)
     return training.full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b,
-                                       alpha, config)
+                                       alpha, config, local_flash=caller_plugin(local_flash))
 
 
 def new_state(layer_index, config=DEFAULT_CONFIG):
@@ -34,22 +35,15 @@ def new_state(layer_index, config=DEFAULT_CONFIG):
                        fused_fine=True, config=config)
 
 
-def _check_plugin(local_flash):
-    if local_flash is not None and local_flash is not flash_attn:
-        raise NotImplementedError(
-            "a caller-supplied local_flash plugin is not supported by the fused HIP "
-            "streaming kernels yet; pass local_flash=None")
-
-
 def tao_attention_prefill(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b,
                           alpha, state, position, local_flash=None):
     """Advance only the supplied new tokens; the state is updated and returned."""
     if position != state.position:
         raise ValueError("position must match this request's causal cursor")
-    _check_plugin(local_flash)
+    plugin = caller_plugin(local_flash)
     if q.shape[1] == 0:
         return q.new_empty(q.shape), state
-    out = state.prefill(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
+    out = state.prefill(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, local_flash=plugin)
     return out, state
 
 
@@ -60,8 +54,11 @@ def tao_attention_decode(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b,
         raise ValueError("decode accepts exactly one new query/key/value")
     if position != state.position:
         raise ValueError("position must match this request's causal cursor")
-    _check_plugin(local_flash)
-    out = state.decode(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
+    plugin = caller_plugin(local_flash)
+    if plugin is None:
+        out = state.decode(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
+    else:
+        out = state.decode(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, local_flash=plugin)
     return out, state
 
 

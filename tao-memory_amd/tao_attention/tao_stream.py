@@ -457,8 +457,13 @@ class StreamCache:
                 out.data_ptr() if out is not None else dummy, out_s, dev.stream()))
         del keep      # the caching allocator keeps them stream-ordered
 
-    def prefill(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
-        """Advance by q.shape[1] tokens; returns the fused heads [B, T, H, D]."""
+    def prefill(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, local_flash=None):
+        """Advance by q.shape[1] tokens; returns the fused heads [B, T, H, D].
+
+        local_flash: a caller plugin (flash_attention.caller_plugin) that
+        computes the local attention of each chunk, as the reference calls it
+        (tao_stream.py:919-934); the read, the fusion and the state update
+        stay on the HIP path."""
         self._check_supported(q)
         if q.shape[1] == 1:
             if not self._run_open:
@@ -472,7 +477,18 @@ class StreamCache:
         q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
         plan, info = self._plan(pos0, tokens, outputs=True)
-        local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+        if local_flash is not None:
+            from .flash_attention import plugin_stream_local
+            window = self._local_window()
+            empty = q[:, :0]
+            local = plugin_stream_local(local_flash, q, k, v,
+                                        empty if window is None else window[0],
+                                        empty if window is None else window[1], pos0, cfg)
+            if local.shape != q.shape:
+                raise ValueError("local_flash returned a local output of the wrong shape")
+            plan = _hip.without_attention(plan)
+        else:
+            local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
         out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
         fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
         self._run_plan(dev, tok, fu, plan, info, local, out)
@@ -532,8 +548,13 @@ class StreamCache:
         self._handle_dirty = False
         return self._handle
 
-    def decode(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
+    def decode(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, local_flash=None):
         """One new token; returns the fused heads [B, 1, H, D].
+
+        With a caller local_flash plugin the token runs as a one-token
+        prefill whose local attention is the plugin's (the fused decode step
+        computes its own local attention, so neither it nor its graph can
+        take a plugin's output).
 
         With the hipGraph preset the returned tensor is the graph's output
         buffer, overwritten by the next replay (as the reference's regional
@@ -543,6 +564,8 @@ class StreamCache:
         parameter tensors and the driver binding are compared with the
         previous call's; anything different goes through the full checks.
         """
+        if local_flash is not None:
+            return self.prefill(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, local_flash)
         nat = self._native
         if nat is not None and self.position < self._fast_limit and not self._handle_dirty:
             pos = self.position

@@ -82,6 +82,9 @@ class _Workspace:
         self.plan, self.info = plan(config, tokens)
         info = self.info
         self.plan_arr = self.plan.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
+        # The same plan without its local attention (local from a plugin).
+        self.plan_ext = _hip.without_attention(self.plan)
+        self.plan_ext_arr = self.plan_ext.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
         self.dev = _DeviceState(config, b, heads, d, device, max(info["fines"], 8))
         self.dev.ensure_plan(len(self.plan))
         self.local = torch.empty((b, tokens, heads, d), dtype=torch.bfloat16, device=device)
@@ -158,12 +161,34 @@ def _association_values(ws, raw_k, v, config):
                 dev.page_c[bi, :, :pages] = page_c.permute(1, 0, 3, 2)
 
 
-def forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_routes=False):
+def _run(ws, tok, fu, local, out):
+    """tao_prefill of the full-sequence plan; `local` given: the caller's
+    local attention output (the plan without its attention section)."""
+    out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
+    if local is None:
+        plan_arr, plan_len, local_ptr = ws.plan_arr, len(ws.plan), ws.local.data_ptr()
+    else:
+        plan_arr, plan_len, local_ptr = ws.plan_ext_arr, len(ws.plan_ext), local.data_ptr()
+    _hip.check(_hip.lib().tao_prefill(
+        ctypes.byref(ws.dev.struct), ctypes.byref(tok), ctypes.byref(fu), plan_arr, plan_len,
+        ctypes.byref(ws.pools), local_ptr, out.data_ptr(), out_s, ws.dev.stream()))
+
+
+def _plugin_local(local, q):
+    """A plugin's local output as the bf16 [B, T, H, D] contiguous operand."""
+    if tuple(local.shape) != tuple(q.shape):
+        raise ValueError("local_flash returned a local output of the wrong shape")
+    return local.to(torch.bfloat16).contiguous()
+
+
+def forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_routes=False,
+            local=None):
     """Fused heads [B, T, H, D] of the full-sequence read (no autograd).
 
     With return_routes, also the per-query selections: int32 [B, T, H, W]
     bitmask words over fine ids (bit f of word f // 32) for queries with
-    history, zero before first_fine.
+    history, zero before first_fine. `local`: the local attention output
+    of a caller plugin, used instead of the library's.
     """
     _check(q, k, v, raw_q, raw_k, config)
     b, tokens, heads, d = q.shape
@@ -176,20 +201,18 @@ def forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_rou
         _association_values(ws, raw_k, v, config)
     tok = _hip.tokens(q, k, v, raw_q, raw_k)
     fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
-    out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
-    _hip.check(_hip.lib().tao_prefill(
-        ctypes.byref(ws.dev.struct), ctypes.byref(tok), ctypes.byref(fu), ws.plan_arr,
-        len(ws.plan), ctypes.byref(ws.pools), ws.local.data_ptr(), out.data_ptr(), out_s,
-        ws.dev.stream()))
+    _run(ws, tok, fu, None if local is None else _plugin_local(local, q), out)
     if return_routes:
         return out, None if ws.qsel is None else ws.qsel.clone()
     return out
 
 
-def _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config):
+def _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config,
+                          local=None):
     """The forward on a call-private workspace, with the saves the backward
-    reads: local-attention log2-sum-exp, pre-fusion coarse / fine heads and
-    denominators. Returns (out, context for backward)."""
+    reads: local-attention log2-sum-exp (not with a plugin's `local`),
+    pre-fusion coarse / fine heads and denominators. Returns (out, context
+    for backward)."""
     _check(q, k, v, raw_q, raw_k, config)
     if config.fine_writer != "softmax":
         raise NotImplementedError(
@@ -202,19 +225,19 @@ def _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, conf
         coarse=torch.zeros(q.shape, dtype=torch.bfloat16, device=q.device),
         fine=torch.zeros(q.shape, dtype=torch.bfloat16, device=q.device),
         den=torch.zeros((b, tokens, heads), dtype=torch.float32, device=q.device))
-    ws.pools.local_lse = saves["lse"].data_ptr()
+    if local is not None:
+        local = _plugin_local(local, q)
+        del saves["lse"]
+    else:
+        ws.pools.local_lse = saves["lse"].data_ptr()
     ws.pools.coarse_out = saves["coarse"].data_ptr()
     ws.pools.fine_out = saves["fine"].data_ptr()
     ws.pools.den_out = saves["den"].data_ptr()
     tok = _hip.tokens(q, k, v, raw_q, raw_k)
     fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
     out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
-    out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
-    _hip.check(_hip.lib().tao_prefill(
-        ctypes.byref(ws.dev.struct), ctypes.byref(tok), ctypes.byref(fu), ws.plan_arr,
-        len(ws.plan), ctypes.byref(ws.pools), ws.local.data_ptr(), out.data_ptr(), out_s,
-        ws.dev.stream()))
-    return out, dict(ws=ws, saves=saves, operands=(q, k, v, raw_q, raw_k))
+    _run(ws, tok, fu, local, out)
+    return out, dict(ws=ws, saves=saves, operands=(q, k, v, raw_q, raw_k), local=local)
 
 
 def backward(ctx_data, grad, fusion_a, fusion_b, alpha, memory_adjoints=None):
@@ -222,7 +245,10 @@ def backward(ctx_data, grad, fusion_a, fusion_b, alpha, memory_adjoints=None):
     full-sequence read at the forward recorded in ctx_data. With a dict
     `memory_adjoints`, it also receives "dz" (d fine_z, fp32 [B, H, S, D]),
     "dc" (d C, fp32 [B, H, S, D, D]) of the S written fines and "dalpha"
-    (fp32 [1], through gain = 2 alpha)."""
+    (fp32 [1], through gain = 2 alpha). When the forward's local attention
+    came from a plugin, dq and dk are None, dk's place is taken by nothing
+    and the first output is d local (bf16 [B, T, H, D]) instead of dq; dv
+    is the writer's share only."""
     ws = ctx_data["ws"]
     saves = ctx_data["saves"]
     q, k, v, raw_q, raw_k = ctx_data["operands"]
@@ -242,12 +268,19 @@ def backward(ctx_data, grad, fusion_a, fusion_b, alpha, memory_adjoints=None):
     args = _hip.TrainBwd()
     args.grad = grad.data_ptr()
     args.grad_s = _hip.i64x3(_hip.strides_bth(grad))
-    args.local = ws.local.data_ptr()
-    args.local_lse = saves["lse"].data_ptr()
+    plugin = ctx_data.get("local") is not None
+    if plugin:
+        args.local = ctx_data["local"].data_ptr()
+        args.dlocal_out = outs[0].data_ptr()
+    else:
+        args.local = ws.local.data_ptr()
+        args.local_lse = saves["lse"].data_ptr()
     args.coarse_out = saves["coarse"].data_ptr()
     args.fine_out = saves["fine"].data_ptr()
     args.den_out = saves["den"].data_ptr()
-    args.dq, args.dk, args.dv, args.draw_q, args.draw_k = (t.data_ptr() for t in outs)
+    args.dv, args.draw_q, args.draw_k = (t.data_ptr() for t in outs[2:])
+    if not plugin:
+        args.dq, args.dk = outs[0].data_ptr(), outs[1].data_ptr()
     args.dfusion_a, args.dfusion_b = dfa.data_ptr(), dfb.data_ptr()
     args.workspace, args.workspace_bytes = scratch.data_ptr(), nbytes
     fines = ws.info["fines"]
@@ -267,6 +300,8 @@ def backward(ctx_data, grad, fusion_a, fusion_b, alpha, memory_adjoints=None):
                                       ctypes.byref(args), ws.dev.stream()))
     if memory_adjoints is not None and fines:
         memory_adjoints["dc"] = memory_adjoints.pop("dc_t").transpose(-1, -2)
+    if plugin:
+        outs[1] = None
     return (*outs, dfa, dfb)
 
 
@@ -304,16 +339,64 @@ class _FullSequenceRead(torch.autograd.Function):
                 dfb.to(fusion_b.dtype) if need[6] else None, dalpha, None)
 
 
+class _FullSequenceReadLocal(torch.autograd.Function):
+    """Autograd node of the full-sequence read whose local attention a caller
+    plugin computed: inputs (local, v, raw_q, raw_k, fusion_a, fusion_b,
+    alpha); q and k ride along for the operand layout only. The backward
+    returns d local (autograd carries it through the plugin) and the
+    writer's share of d v."""
+
+    @staticmethod
+    def forward(ctx, local, v, raw_q, raw_k, fusion_a, fusion_b, alpha, q, k, config):
+        alpha_f = float(alpha)
+        out, data = _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b,
+                                          alpha_f, config, local=local)
+        ctx.data = data
+        ctx.alpha_like = alpha if torch.is_tensor(alpha) else None
+        ctx.alpha = alpha_f
+        ctx.save_for_backward(fusion_a, fusion_b)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        fusion_a, fusion_b = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        extra = {} if need[6] else None
+        dlocal, _, dv, drq, drk, dfa, dfb = backward(ctx.data, grad, fusion_a, fusion_b,
+                                                     ctx.alpha, memory_adjoints=extra)
+        ctx.data = None
+        dalpha = None
+        if need[6]:
+            like = ctx.alpha_like
+            dalpha = extra["dalpha"].reshape(like.shape).to(like.dtype).to(
+                like.device, non_blocking=True)
+        return (dlocal if need[0] else None, dv if need[1] else None,
+                drq if need[2] else None, drk if need[3] else None,
+                dfa.to(fusion_a.dtype) if need[4] else None,
+                dfb.to(fusion_b.dtype) if need[5] else None, dalpha, None, None, None)
+
+
 def full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
-                       config=None):
+                       config=None, local_flash=None):
     """tao_attention's read and fusion. alpha is a Python float, as in the
     reference, or a 0-dim tensor; a tensor that requires grad receives
     d alpha through gain = 2 alpha (the reference has no such gradient). The
     kernels take alpha as a host scalar, so a device tensor costs one
-    synchronisation per call; a host tensor costs none."""
+    synchronisation per call; a host tensor costs none. local_flash: a
+    caller plugin (flash_attention.caller_plugin) for the local attention."""
     config = config or TaoConfig()
     tensors = (q, k, v, raw_q, raw_k, fusion_a, fusion_b)
     alpha_grad = torch.is_tensor(alpha) and alpha.requires_grad
-    if torch.is_grad_enabled() and (alpha_grad or any(t.requires_grad for t in tensors)):
+    grad = torch.is_grad_enabled() and (alpha_grad or any(t.requires_grad for t in tensors))
+    if local_flash is not None:
+        from .flash_attention import plugin_training_local
+        _check(q, k, v, raw_q, raw_k, config)
+        local = plugin_training_local(local_flash, q, k, v, config)
+        if grad or local.requires_grad:
+            return _FullSequenceReadLocal.apply(local, v, raw_q, raw_k, fusion_a, fusion_b,
+                                                alpha, q.detach(), k.detach(), config)
+        return forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, float(alpha), config,
+                       local=local)
+    if grad:
         return _FullSequenceRead.apply(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config)
     return forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, float(alpha), config)

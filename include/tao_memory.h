@@ -152,6 +152,19 @@ int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok,
                     const tao_fusion* fu, int32_t selected, void* out,
                     const int64_t* out_s, void* stream);
 
+/* tao_decode_step without allocation: no reference counterpart. For callers
+ * that cannot allocate device memory (code under hipGraph capture, tight
+ * serving loops, harnesses that forbid hipMalloc): the same decode step,
+ * arguments and results as tao_decode_step, with the step's records in a
+ * 4 MiB library-owned static device array instead of st->workspace (which
+ * may be null). Limit: batch * heads <= 567 at head_dim 128, <= 593 at 64
+ * (TAO_E_CAPACITY beyond). Allocates nothing. Every call on one device
+ * shares the array: calls that overlap on one device race and must be
+ * serialised by the caller; no state needs clearing between calls. */
+int tao_decode_step_noalloc(const tao_state_dev* st, const tao_tokens* tok,
+                            const tao_fusion* fu, int32_t selected, void* out,
+                            const int64_t* out_s, void* stream);
+
 /* Routing refresh from one anchor query row (replaces tao_stream.py:310-357
  * and _topk_oldest :50-53). raw_q_row: [B, H, D] view with strides rq_s
  * (batch, head). Writes st->sel / st->chosen and header[1] = M. */

@@ -35,7 +35,7 @@ int check_assoc(const tao_state_dev* st) {
   return TAO_OK;
 }
 
-int check_state(const tao_state_dev* st) {
+int check_state(const tao_state_dev* st, bool need_workspace = true) {
   if (!st) return fail(TAO_E_ARGUMENT, "null state");
   if (st->head_dim != 64 && st->head_dim != 128)
     return fail(TAO_E_SHAPE, "head_dim must be 64 or 128 on the HIP path");
@@ -45,7 +45,7 @@ int check_state(const tao_state_dev* st) {
     return fail(TAO_E_SHAPE, "batch, heads and coarse_group must be positive");
   if (!st->ring_k || !st->ring_v || !st->ring_raw || !st->bank_c || !st->fine_z ||
       !st->fine_sw || !st->page_z || !st->page_w || !st->sel || !st->chosen ||
-      !st->header || !st->fold_g || !st->fold_den || !st->workspace)
+      !st->header || !st->fold_g || !st->fold_den || (need_workspace && !st->workspace))
     return fail(TAO_E_ARGUMENT, "state has a null device buffer");
   if ((st->page_c == nullptr) != (st->coarse_g == nullptr))
     return fail(TAO_E_ARGUMENT, "page_c and coarse_g must be both set or both null");
@@ -54,7 +54,7 @@ int check_state(const tao_state_dev* st) {
   if (int rc = check_assoc(st)) return rc;
   const tao::WorkspaceLayout lay =
       tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
-  if (st->workspace_bytes < lay.plan_off)
+  if (need_workspace && st->workspace_bytes < lay.plan_off)
     return fail(TAO_E_WORKSPACE, "workspace smaller than tao_workspace_bytes()");
   return TAO_OK;
 }
@@ -110,7 +110,7 @@ tao::DecodeParams decode_params(const tao_state_dev* st, const tao_tokens* tok,
   p.out = (bf16_t*)out;
   p.out_sb = out_s[0];
   p.out_sh = out_s[2];
-  p.parts = parts_of(st);
+  p.parts = st->workspace ? parts_of(st) : nullptr;
   p.fold_g = (const float*)st->fold_g;
   p.fold_den = (const float*)st->fold_den;
   p.coarse_g = (const float*)st->coarse_g;
@@ -240,8 +240,8 @@ WorkspaceLayout workspace_layout(int batch, int heads, int head_dim, int sel_cap
 
 int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
                    int32_t selected, void* out, const int64_t* out_s, void* stream,
-                   long long position) {
-  int rc = check_state(st);
+                   long long position, float* records) {
+  int rc = check_state(st, records == nullptr);
   if (!rc) rc = check_tokens(tok);
   if (!rc) rc = check_fusion(fu);
   if (rc) return rc;
@@ -252,6 +252,7 @@ int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fus
     return fail(TAO_E_ARGUMENT, "coarse_on needs a state with the coarse value branch");
   tao::DecodeParams p = decode_params(st, tok, fu, out, out_s);
   p.pos_hint = position;
+  if (records) p.parts = records;
   return check_hip(tao::launch_decode_step(p, st->head_dim, selected, (hipStream_t)stream),
                    "tao_decode_step");
 }

@@ -135,9 +135,11 @@ hipError_t launch_coarse_fold(const CoarseFoldParams& p, int head_dim, hipStream
 
 // tao_decode_step with the step's cursor given by the caller (position >= 0)
 // instead of read from header[0] on the device; used by the stream driver.
+// records: the step's per-head records (B * H * step_floats(D) floats), or
+// null for the state's workspace (then required).
 int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
                    int32_t selected, void* out, const int64_t* out_s, void* stream,
-                   long long position);
+                   long long position, float* records = nullptr);
 
 struct StageParams {
   TokView src[5];

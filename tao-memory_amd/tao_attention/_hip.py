@@ -102,6 +102,9 @@ _SIGNATURES = {
     "tao_workspace_init": ([ctypes.POINTER(StateDev), _vp], _i32),
     "tao_decode_step": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens),
                          ctypes.POINTER(Fusion), _i32, _vp, ctypes.POINTER(_i64), _vp], _i32),
+    "tao_decode_step_noalloc": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens),
+                                 ctypes.POINTER(Fusion), _i32, _vp, ctypes.POINTER(_i64), _vp],
+                                _i32),
     "tao_fold_route": ([ctypes.POINTER(StateDev), _i32, _vp], _i32),
     "tao_page_coarse": ([ctypes.POINTER(StateDev), _i32, _i32, _vp], _i32),
     "tao_fold_coarse": ([ctypes.POINTER(StateDev), _i32, _vp], _i32),

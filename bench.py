@@ -2,17 +2,19 @@
 """TaoMemory operator benchmark on one MI355X.
 
 Headline (``value``): advancing decode tok/s of one request x layer from a
-131072-token state, 32 heads x 128, bf16, page memo, 256 tokens one at a
-time (the timed region includes route refreshes and
-the seal). Each step is issued by the native C++ driver as direct kernel
-launches, which on ROCm costs the host less than a hipGraphLaunch; the
-hipGraph preset is timed on the same steps and reported as decode_graph. Also reported: prefill tokens/s of a
-16384-token prompt through tao_attention_prefill, batched
-streaming decode of 32 ragged requests (configs[4], decode_batch), a cold-cache
-decode variant that cycles 8 independent 128K states (> 4 GB working set,
-beyond the 256 MB Infinity Cache), the roofline of the dominant kernels
-measured live with HIP events on the launch stream, and the CPU oracle
-(reference arithmetic in torch eager) on a bounded sample.
+131072-token state, 32 heads x 128, bf16, page memo (BASELINE.json
+configs[3]): --warmup untimed single-token steps, then --steps timed ones
+(default 16 + 256: the timed steps hold 11 route refreshes and the seal at
+position 131327; config.workload states the counts of the run). Each step
+is issued by the native C++ driver as direct kernel launches; the hipGraph
+preset is timed on the same steps and reported as decode_graph. Also
+reported: prefill tokens/s of a 16384-token prompt through
+tao_attention_prefill, batched streaming decode of 32 ragged
+requests (configs[4], decode_batch), a cold-cache decode variant that
+cycles 32 independent 128K states (their touched bytes per cycle exceed the
+256 MB Infinity Cache), the roofline of the dominant kernels measured live
+with HIP events on the launch stream, and the CPU oracle (reference
+arithmetic in torch eager) on bounded samples of decode and prefill.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16]
 """
@@ -148,8 +150,10 @@ def decode_loop(torch, state, xs, fa, fb, start, steps):
 def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
     """Headline decode: direct launches by the native driver (graph=False).
 
-    The same steps are then replayed through the hipGraph preset from the same
-    snapshot (reported as decode_graph), and once more eagerly with the GPU
+    The state takes `warmup` untimed decode steps (the first call's one-time
+    setup falls there), then `steps` timed ones. The hipGraph preset runs the
+    same steps from the same snapshot on its own state (reported as
+    decode_graph), and the eager steps are replayed once more with the GPU
     pre-loaded for kernel timing.
     """
     from tao_attention import StreamCache, new_state, tao_attention_decode
@@ -162,16 +166,17 @@ def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
     log(f"decode state built: position {state.get_pos()}, route size {state.route_size}")
     snap = state.export()
     graph_snap = dict(snap, config=dict(snap["config"], q1_history_region_graph=True))
-    # Warm-up on independent copies (eager and graph), same tokens.
-    for s in (snap, graph_snap):
-        warm = StreamCache.from_export(s)
-        warm, _ = decode_loop(torch, warm, xs, fa, fb, context, args.warmup)
-        warm.release_execution()
-        del warm
-    state, seconds = decode_loop(torch, state, xs, fa, fb, context, args.steps)
+    first = context + args.warmup
+    state, _ = decode_loop(torch, state, xs, fa, fb, context, args.warmup)
+    state, seconds = decode_loop(torch, state, xs, fa, fb, first, args.steps)
     graph_state = StreamCache.from_export(graph_snap)
-    graph_state, graph_seconds = decode_loop(torch, graph_state, xs, fa, fb, context,
-                                             args.steps)
+    graph_state, _ = decode_loop(torch, graph_state, xs, fa, fb, context, args.warmup)
+    region = graph_state.history_region
+    before = dict(region.counts) if region is not None else {}
+    graph_state, graph_seconds = decode_loop(torch, graph_state, xs, fa, fb, first, args.steps)
+    after = graph_state.history_region.observation()
+    graph_timed = {key: after[key] - before.get(key, 0)
+                   for key in ("epochs", "eager_warm", "captures", "replays")}
     graph_state.release_execution()
     del graph_state, graph_snap
     # Device time per step: replay the same steps eagerly on an imported copy
@@ -181,14 +186,15 @@ def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
     q, k, v, rq, rk = xs
     timed = StreamCache.from_export(snap)
     del snap
+    timed, _ = decode_loop(torch, timed, xs, fa, fb, context, args.warmup)
     steps_bytes = []
     groups = []
-    i = context
-    while i < context + args.steps:
+    i = first
+    while i < first + args.steps:
         torch.cuda._sleep(SPIN_CYCLES)
         start = torch.cuda.Event(enable_timing=True)
         start.record()
-        count = min(STEPS_PER_SPIN, context + args.steps - i)
+        count = min(STEPS_PER_SPIN, first + args.steps - i)
         for _ in range(count):
             sl = slice(i, i + 1)
             _, timed = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
@@ -202,20 +208,31 @@ def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
     torch.cuda.synchronize()
     probe.events["decode_step"] = groups
     timed.release_execution()
-    return state, xs, fa, fb, seconds, graph_seconds, steps_bytes
+    return state, xs, fa, fb, seconds, graph_seconds, steps_bytes, graph_timed
 
 
 def run_cold(torch, args, device, cfg, heads, width, context, n_states, probe):
-    from tao_attention import new_state, tao_attention_decode
+    """Decode steps cycling through `n_states` independent 128K states, so a
+    step's buffers were last touched n_states - 1 steps earlier: with 32
+    states the bytes touched per cycle (each state's ring window, folded
+    route, records and refresh reads) exceed the 256 MB Infinity Cache. The
+    states are imports of one writer-only state (distinct device buffers,
+    equal contents); every state decodes its own random tokens."""
+    from tao_attention import StreamCache, new_state, tao_attention_decode
     from tao_attention.presets import index_only_page_memo
+    xs, fa, fb = make_tokens(torch, context, heads, width, 100, device)
+    base = new_state(0, index_only_page_memo(graph=False))
+    base._ingest(*xs)
+    del xs
+    snap = base.export()
+    del base
     states, toks = [], []
+    g = torch.Generator(device=device).manual_seed(101)
     for j in range(n_states):
-        xs, fa, fb = make_tokens(torch, context + args.steps, heads, width, 100 + j, device)
-        st = new_state(0, index_only_page_memo(graph=False))
-        st._ingest(*(x[:, :context] for x in xs))
-        toks.append([x[:, context:].clone() for x in xs])
-        del xs
-        states.append(st)
+        states.append(StreamCache.from_export(snap))
+        toks.append([torch.randn((1, args.steps + 2, heads, width), generator=g,
+                                 device=device).to(torch.bfloat16) for _ in range(5)])
+    del snap
     torch.cuda.synchronize()
     log(f"cold: {n_states} states built")
     for j, st in enumerate(states):        # warm every state
@@ -575,6 +592,47 @@ def cpu_model():
     return "unknown"
 
 
+def cpu_cores():
+    """Threads for the CPU baseline: the CPUs this process may run on, capped
+    by OMP_NUM_THREADS when the environment sets it (the GPU box's share)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+def cpu_prefill_baseline(torch, tokens, width, sample_heads, heads, runs=3):
+    """Oracle prefill (torch eager on the host) of a `tokens`-token prompt
+    (configs[2] inputs: N(0,1), unit-norm raw_k rows) at `sample_heads` of the
+    `heads` heads: every head's work is independent and identical in kind, so
+    the H32 rate is the sample's tokens/s x sample_heads / heads. One warm-up
+    on 1024 tokens, then the median of `runs` runs."""
+    from oracle import tao_oracle as O
+    from tao_attention.presets import index_only_page_memo
+    g = torch.Generator().manual_seed(3)
+    xs = [torch.randn(1, tokens, sample_heads, width, generator=g) for _ in range(5)]
+    xs[4] = xs[4] / xs[4].norm(dim=-1, keepdim=True)
+    xs = [x.to(torch.bfloat16) for x in xs]
+    fa = torch.randn(sample_heads, width, 3, generator=g) * 0.02
+    fb = torch.randn(sample_heads, width, 3, generator=g) * 0.02
+    geo = O.Geometry.from_config(index_only_page_memo())
+    O.OracleStream(0, geo).prefill(*(x[:, :1024] for x in xs), fa, fb, 0.5)
+    times = []
+    for _ in range(runs):
+        ora = O.OracleStream(0, geo)
+        t0 = time.perf_counter_ns()
+        ora.prefill(*xs, fa, fb, 0.5)
+        times.append((time.perf_counter_ns() - t0) * 1e-9)
+    times.sort()
+    sec = times[len(times) // 2]
+    return {"tok_s": tokens / sec * sample_heads / heads,
+            "sample": f"median of {runs} oracle prefills of the full {tokens}-token prompt at "
+                      f"H{sample_heads} D{width} ({sec:.2f} s each, after a 1024-token warm-up), "
+                      f"scaled to H{heads} by x{sample_heads}/{heads} (heads are independent); "
+                      f"CPU {cpu_model()}"}
+
+
 def cpu_baseline(torch, state, xs, fa, fb, steps, runs=3):
     """Oracle decode (torch eager on the host) from the GPU state's snapshot.
 
@@ -613,8 +671,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--context", type=int, default=131072)
     ap.add_argument("--prefill-tokens", type=int, default=16384)
-    ap.add_argument("--cold-states", type=int, default=8)
+    ap.add_argument("--cold-states", type=int, default=32)
     ap.add_argument("--cpu-steps", type=int, default=64)
+    ap.add_argument("--cpu-prefill-heads", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cold", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
@@ -647,8 +706,15 @@ def main():
     probe = Probe(torch)
 
     log("decode: building 128K state")
-    state, xs, fa, fb, seconds, graph_seconds, steps_bytes = run_decode(
+    state, xs, fa, fb, seconds, graph_seconds, steps_bytes, graph_timed = run_decode(
         torch, args, device, cfg, heads, width, args.context, 4, probe)
+    from tao_attention import schedule
+    first, last = args.context + args.warmup, args.context + args.warmup + args.steps
+    refreshes = schedule.count_turns(first, last, 0, cfg)
+    seals = schedule.fines_at(last, cfg) - schedule.fines_at(first, cfg)
+    window = (f"{args.steps} single-token steps timed (positions {first}..{last - 1}, after "
+              f"{args.warmup} untimed warm-up steps from {args.context}): {refreshes} route "
+              f"refreshes and {seals} seal{'s' if seals != 1 else ''} inside the timed steps")
     tok_s = args.steps / seconds
     n_step = probe.count("decode_step")
     step_ms = probe.total_ms("decode_step") / max(n_step, 1)
@@ -670,14 +736,15 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic N(0,1) bf16 operands (seeded); state built writer-only",
-        "config": {"workload": "configs[3]: advancing decode of one request x layer from a "
-                               "131072-token state, H32 D128, 256 single-token steps; "
+        "config": {"workload": f"configs[3]: advancing decode of one request x layer from a "
+                               f"{args.context}-token state, H32 D128; {window}; "
                                "index_only_page_memo(graph=False): each step is issued by "
                                "the native C++ driver as direct launches (the hipGraph "
                                "replay preset is timed on the same steps as decode_graph)",
                    "context": args.context, "heads": heads, "head_dim": width,
-                   "selected_fines": state.route_size},
-        "roofline": {"bound": "hbm", "kernel": "decode_units_kernel<128> + decode_combine_kernel<128> (one decode step, incl. amortised route refreshes and seal)",
+                   "selected_fines": state.route_size, "timed_refreshes": refreshes,
+                   "timed_seals": seals},
+        "roofline": {"bound": "hbm", "kernel": "decode_units_kernel<128> + decode_combine_kernel<128> per step, with the %d route refreshes (route_kernel + fold_kernel) and %d seals (writer + epilogue + fold) of the timed steps amortised" % (refreshes, seals),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": DECODE_STEP_TRAFFIC_BYTES if args.context == 131072 else None,
@@ -689,7 +756,8 @@ def main():
                      "own_GBs": round(own_bytes / (step_ms * 1e-3) / 1e9, 1)},
         "decode_graph": {"preset": "index_only_page_memo(graph=True)",
                          "tok_s": round(args.steps / graph_seconds, 2),
-                         "ms_per_step": round(graph_seconds / args.steps * 1e3, 4)},
+                         "ms_per_step": round(graph_seconds / args.steps * 1e3, 4),
+                         "timed_steps": graph_timed},
     }
     if not args.no_cold:
         log("cold decode: building states")
@@ -697,11 +765,16 @@ def main():
         steps, cold_s, cold_sel = run_cold(torch, args, device, cfg, heads, width,
                                            args.context, args.cold_states, probe)
         cold_ms = probe.total_ms("decode_step") / max(probe.count("decode_step"), 1)
-        cold_bytes, _ = decode_bytes(cfg, heads, width, cold_sel, args.context + 9)
+        cold_bytes, cold_own = decode_bytes(cfg, heads, width, cold_sel, args.context + 9)
         result["decode_cold"] = {
             "states": args.cold_states, "tok_s": round(steps / cold_s, 2),
             "kernel_us": round(cold_ms * 1e3, 3),
-            "achieved_GBs": round(cold_bytes / (cold_ms * 1e-3) / 1e9, 1)}
+            "achieved_GBs": round(cold_bytes / (cold_ms * 1e-3) / 1e9, 1),
+            "touched_bytes_per_cycle": int(cold_own * args.cold_states),
+            "note": "steps cycle through independent 128K states (no refresh in these steps); "
+                    "a cycle touches touched_bytes_per_cycle bytes (each state's ring window, "
+                    "folded route and records), above the 256 MB Infinity Cache when it "
+                    "exceeds 268435456"}
         log(f"cold: {steps / cold_s:.1f} tok/s, kernel {cold_ms * 1e3:.2f} us")
         xs = None
     if not args.no_prefill:
@@ -779,6 +852,8 @@ def main():
         log(f"writers: {result['writers']}")
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, torch eager on host cores)")
+        cores = cpu_cores()
+        torch.set_num_threads(cores)
         xs_cpu, _, _ = make_tokens(torch, 1 + 3 * args.cpu_steps, heads, width, 7, device)
         cpu_tok_s, sample = cpu_baseline(torch, state, xs_cpu, fa, fb, args.cpu_steps)
         result["cpu_baseline"] = {
@@ -786,9 +861,18 @@ def main():
             "kind": "port",
             "sample": f"median of 3 runs of {sample} single-token decodes (after 1 warm-up) "
                       f"of the oracle (torch eager) from the GPU state's snapshot at position "
-                      f"{state.get_pos()} (H32 D128); CPU {cpu_model()}; torch "
-                      f"{torch.__version__}"}
-        log(f"cpu baseline: {cpu_tok_s:.3f} tok/s")
+                      f"{state.get_pos()} (H32 D128); torch.set_num_threads({cores}) = the "
+                      f"CPUs this process may run on (sched_getaffinity, capped by "
+                      f"OMP_NUM_THREADS when set); CPU {cpu_model()}; torch {torch.__version__}"}
+        log(f"cpu baseline: {cpu_tok_s:.3f} tok/s on {cores} threads")
+        if not args.no_prefill:
+            pre_cpu = cpu_prefill_baseline(torch, args.prefill_tokens, width,
+                                           args.cpu_prefill_heads, heads)
+            result["cpu_baseline_prefill"] = {
+                "value": round(pre_cpu["tok_s"], 2), "unit": "tokens/s",
+                "cores": torch.get_num_threads(), "kind": "port",
+                "sample": pre_cpu["sample"]}
+            log(f"cpu prefill baseline: {pre_cpu['tok_s']:.1f} tokens/s (H32-equivalent)")
     state.release_execution()
     if args.calibrate_copy_mib:
         n = args.calibrate_copy_mib * (1 << 20) // 4

@@ -8,9 +8,10 @@
 // decode_units_kernel: per (batch, head) local_units(D) local-attention
 //   workgroups and fine_units(D) fine-read workgroups.
 //   local workgroup j takes keys [j*K, (j+1)*K) (K = local_keys(D)) of the
-//   exact window (K and V rows from the ring, or the new token), runs one
-//   online softmax per key row and merges the rows into a record (m, l,
-//   o[D]); workgroup 0 also appends the new token to the ring. Its only
+//   exact window (K and V rows from the ring, or the new token), scores
+//   them (row sums on DPP lane moves), weights each thread's keys against
+//   their maximum and merges the rows into a record (m, l, o[D]) with m in
+//   log2 units; workgroup 0 also appends the new token to the ring. Its only
 //   scalar input is the cursor (a kernel argument in eager launches,
 //   header[0] in graphs).
 //   fine-read workgroup f reads 32 rows of the folded route:
@@ -68,11 +69,17 @@ TAO_DEV void unpack8(const uint4& u, float out[8]) {
   }
 }
 
-// Sum over the CH consecutive lanes that share one row.
+// Sum over the CH (8 or 16) consecutive lanes that share one key row, on
+// DPP lane moves (no LDS round trips): the two quad swaps give quad sums, the
+// half-row mirror adds the other quad of 8 lanes, the row mirror the other
+// 8 lanes of 16. Every lane of the row ends with the row's sum.
 template <int CH>
-TAO_DEV float group_sum(float v) {
-#pragma unroll
-  for (int off = CH / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+TAO_DEV float row_sum(float v) {
+  static_assert(CH == 8 || CH == 16, "a key row spans 8 or 16 lanes");
+  v += dpp_partner<0xB1>(v);
+  v += dpp_partner<0x4E>(v);
+  v += dpp_partner<0x141>(v);
+  if constexpr (CH == 16) v += dpp_partner<0x140>(v);
   return v;
 }
 
@@ -209,10 +216,10 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
       q.ring_raw[off + d] = q.rk[d];
     }
   }
-  const float scale = (float)(1.0 / __builtin_sqrt((double)D));
-  float m = -__builtin_inff(), l = 0.0f, acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  // Scores in log2 units (1/sqrt(D) and log2 e folded into one scale), each
+  // reduced over its row's lanes; keys past the window score -inf.
+  const float scale2 = (float)(1.4426950408889634 / __builtin_sqrt((double)D));
+  float sc[G::KPT];
 #pragma unroll
   for (int i = 0; i < G::KPT; ++i) {
     float kv[8];
@@ -220,41 +227,55 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
     float part = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) part = fmaf(qv[e], kv[e], part);
-    const float s = group_sum<G::CH>(part) * scale;
-    if (k0 + r + i * G::ROWS < n) {
-      const float mn = fmaxf(m, s);
-      const float keep_f = __expf(m - mn);
-      const float w = __expf(s - mn);
+    sc[i] = row_sum<G::CH>(part) * scale2;
+    if (k0 + r + i * G::ROWS >= n) sc[i] = -__builtin_inff();
+  }
+  // This thread's keys: one maximum, then independent weights (no chain of
+  // rescales).
+  float m = sc[0];
+#pragma unroll
+  for (int i = 1; i < G::KPT; ++i) m = fmaxf(m, sc[i]);
+  float l = 0.0f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  if (m != -__builtin_inff()) {
+#pragma unroll
+    for (int i = 0; i < G::KPT; ++i) {
+      const float w = __builtin_amdgcn_exp2f(sc[i] - m);   // 0 for a -inf score
       float vv[8];
       unpack8(vraw[i], vv);
-      l = fmaf(l, keep_f, w);
+      l += w;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = fmaf(acc[e], keep_f, w * vv[e]);
-      m = mn;
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, vv[e], acc[e]);
     }
   }
-  // Merge the per-row online softmax states.
+  // Merge the rows: a common maximum, the rescaled partial sums through LDS,
+  // and the rescaled row weights summed by wave 0 on DPP moves.
   if (chn == 0) { sm.rm[r] = m; sm.rl[r] = l; }
   __syncthreads();
   float top = -__builtin_inff();
 #pragma unroll
   for (int rr = 0; rr < G::ROWS; ++rr)
     if (sm.rl[rr] > 0.0f) top = fmaxf(top, sm.rm[rr]);
-  const float f = l > 0.0f ? __expf(m - top) : 0.0f;
+  const float f = l > 0.0f ? __builtin_amdgcn_exp2f(m - top) : 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) sm.red[r][chn * 8 + e] = acc[e] * f;
   __syncthreads();
   if (tid < D) {
     float s = 0.0f;
+#pragma unroll
     for (int rr = 0; rr < G::ROWS; ++rr) s += sm.red[rr][tid];
     rec[kStepRec + tid] = s;
   }
-  if (tid == 0) {
-    float lsum = 0.0f;
-    for (int rr = 0; rr < G::ROWS; ++rr)
-      if (sm.rl[rr] > 0.0f) lsum = fmaf(__expf(sm.rm[rr] - top), sm.rl[rr], lsum);
-    rec[0] = top;
-    rec[1] = lsum;
+  if (tid < 64) {
+    const float x = tid < G::ROWS && sm.rl[tid] > 0.0f
+                        ? __builtin_amdgcn_exp2f(sm.rm[tid] - top) * sm.rl[tid]
+                        : 0.0f;
+    const float lsum = wave_fold_sum(x);
+    if (tid == 0) {
+      rec[0] = top;
+      rec[1] = lsum;
+    }
   }
 }
 
@@ -347,14 +368,16 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
     if (ml[j][1] > 0.0f) top = fmaxf(top, ml[j][0]);
   float pl = 0.0f;
 #pragma unroll
-  for (int i = 0; i < LPG; ++i) pl += l_g[i] > 0.0f ? __expf(m_g[i] - top) * o_g[i] : 0.0f;
+  for (int i = 0; i < LPG; ++i)
+    pl += l_g[i] > 0.0f ? __builtin_amdgcn_exp2f(m_g[i] - top) * o_g[i] : 0.0f;
   part_loc[g][dc] = pl;
   __syncthreads();
   if (g == 0) {
     float den_local = 0.0f;
 #pragma unroll
     for (int j = 0; j < NLOC; ++j)
-      if (ml[j][1] > 0.0f) den_local = fmaf(__expf(ml[j][0] - top), ml[j][1], den_local);
+      if (ml[j][1] > 0.0f)
+        den_local = fmaf(__builtin_amdgcn_exp2f(ml[j][0] - top), ml[j][1], den_local);
     float nl = 0.0f;
 #pragma unroll
     for (int gg = 0; gg < G; ++gg) nl += part_loc[gg][dc];

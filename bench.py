@@ -133,16 +133,18 @@ def decode_bytes(cfg, heads, width, selected, position, layer=0):
 
 
 def decode_loop(torch, state, xs, fa, fb, start, steps):
-    """`steps` single-token tao_attention_decode calls; returns (state, seconds)."""
+    """`steps` single-token tao_attention_decode calls; returns (state, seconds).
+
+    Each step's operands are [1, 1, H, D] views taken before the timed
+    region: a model hands the layer freshly projected tensors, so the
+    caller's own slicing (about 1 us per view) is not part of the step."""
     from tao_attention import tao_attention_decode
-    q, k, v, rq, rk = xs
+    rows = [tuple(x[:, i:i + 1] for x in xs) for i in range(start, start + steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(start, start + steps):
-        sl = slice(i, i + 1)
-        _, state = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
-                                        raw_k=rk[:, sl], fusion_a=fa, fusion_b=fb, alpha=0.5,
-                                        state=state, position=state.get_pos())
+    for q, k, v, rq, rk in rows:
+        _, state = tao_attention_decode(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa, fusion_b=fb,
+                                        alpha=0.5, state=state, position=state.get_pos())
     torch.cuda.synchronize()
     return state, time.perf_counter() - t0
 

@@ -465,10 +465,18 @@ __global__ __launch_bounds__(kThreads) void batch_combine_kernel(BatchStepParams
 
 // Fold: one workgroup per (batch, head, ROWS rows of G^T). Thread (row r,
 // chunk c) accumulates G^T[e0 + r][8c .. 8c + 8) over the selected slots in
-// slot order (fp32); eight slots' loads are in flight at a time.
+// slot order (fp32), with w_m[d] = pw[page(m)][d] * sw[m][d]. A refresh is a
+// chain of memory latencies, so every load of a stage is issued before any
+// of them is used: the stage's ids, then its weights (staged in LDS once per
+// workgroup) together with all its C rows (kFoldStage slots).
+constexpr int kFoldStage = 36;
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void fold_kernel(FoldParams p) {
-  constexpr int CH = D / 8, ROWS = kThreads / CH, CHUNKS = D / ROWS, U = 8;
+  constexpr int CH = D / 8, ROWS = kThreads / CH, CHUNKS = D / ROWS, U = kFoldStage;
+  constexpr int WPT = (U * CH + kThreads - 1) / kThreads;   // weight chunks per thread
+  __shared__ float wts[U][D];
+  __shared__ int ids[U];
   const int bh = blockIdx.x / CHUNKS;
   const int e0 = (blockIdx.x % CHUNKS) * ROWS;
   const int tid = threadIdx.x, c = tid % CH, r = tid / CH;
@@ -480,28 +488,50 @@ __global__ __launch_bounds__(kThreads) void fold_kernel(FoldParams p) {
   float acc[8], den[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) { acc[k] = 0.0f; den[k] = 0.0f; }
-  for (int m0 = 0; m0 < p.M; m0 += U) {
-    uint4 cv[U], wp[U], ws[U];
+  for (int s0 = 0; s0 < p.M; s0 += U) {
+    const int staged = min(U, p.M - s0);
+    __syncthreads();                  // the previous stage is consumed
+    if (tid < staged) ids[tid] = sel[s0 + tid];
+    __syncthreads();
+    uint4 wp[WPT], ws[WPT], cv[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int m = min(m0 + u, p.M - 1);
-      const int id = sel[m];
-      cv[u] = *(const uint4*)(bank + ((size_t)id * D + e) * D + c * 8);
-      wp[u] = *(const uint4*)(pw + (size_t)(id / p.group) * D + c * 8);
-      ws[u] = *(const uint4*)(sw + (size_t)id * D + c * 8);
+    for (int k = 0; k < WPT; ++k) {
+      const int i = tid + k * kThreads;
+      if (i < staged * CH) {
+        const int id = ids[i / CH], cc = i % CH;
+        wp[k] = *(const uint4*)(pw + (size_t)(id / p.group) * D + cc * 8);
+        ws[k] = *(const uint4*)(sw + (size_t)id * D + cc * 8);
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (m0 + u < p.M) {
-        float cf[8], pf[8], sf[8];
+      const int m = min(u, staged - 1);
+      cv[u] = *(const uint4*)(bank + ((size_t)ids[m] * D + e) * D + c * 8);
+    }
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+      const int i = tid + k * kThreads;
+      if (i < staged * CH) {
+        float pf[8], sf[8];
+        unpack8(wp[k], pf);
+        unpack8(ws[k], sf);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wts[i / CH][(i % CH) * 8 + j] = pf[j] * sf[j];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (u < staged) {
+        float cf[8];
         unpack8(cv[u], cf);
-        unpack8(wp[u], pf);
-        unpack8(ws[u], sf);
+        const float4 wa = *(const float4*)&wts[u][c * 8];
+        const float4 wb = *(const float4*)&wts[u][c * 8 + 4];
+        const float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-          const float w = pf[k] * sf[k];
-          acc[k] = fmaf(w, cf[k], acc[k]);
-          den[k] += w;
+          acc[k] = fmaf(w[k], cf[k], acc[k]);
+          den[k] += w[k];
         }
       }
     }

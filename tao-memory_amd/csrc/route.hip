@@ -115,15 +115,29 @@ TAO_DEV void query_weights(const bf16_t* rq, int lane, float* h) {
   for (int k = 0; k < PER; ++k) h[e0 + 64 * k] = rbf(e[k] / s);
 }
 
+// Number of keys larger than `mine` among keys[0, n) (keys are unique).
+TAO_DEV int key_rank(const unsigned long long* keys, int n, unsigned long long mine) {
+  int r = 0;
+  int j = 0;
+  for (; j + 8 <= n; j += 8) {
+    unsigned long long k8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) k8[i] = keys[j + i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r += k8[i] > mine;
+  }
+  for (; j < n; ++j) r += keys[j] > mine;
+  return r;
+}
+
 // Stable descending selection of the top `count` keys (unique 64-bit keys:
 // score << 32 | ~index). Writes the selected keys, best first, to dst.
-__device__ void select_top(unsigned long long* keys, int n, int count,
+TAO_DEV void select_top(unsigned long long* keys, int n, int count,
                            unsigned long long* dst) {
   if (n <= kRankMax) {
     for (int i = threadIdx.x; i < n; i += kRouteThreads) {
       const unsigned long long mine = keys[i];
-      int rank = 0;
-      for (int j = 0; j < n; ++j) rank += keys[j] > mine;
+      const int rank = key_rank(keys, n, mine);
       if (rank < count) dst[rank] = mine;
     }
     __syncthreads();
@@ -256,6 +270,126 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Single-turn refresh of a stream (the decode driver's route turns) with its
+// rows staged in LDS: the same arithmetic, candidate order, butterfly sums
+// and stable selections as route_kernel, but every row is fetched with
+// coalesced 16-byte loads into LDS, so a refresh costs two memory round
+// trips: (1) the page weights of the completed and pending pages, the
+// pending fines' segment weights and the anchor query; (2) the segment
+// weights of the chosen pages' fines. Serves states with at most
+// kRefreshPages pages and kRefreshRows candidates; route_kernel serves the
+// rest.
+constexpr int kRefreshPages = 128;
+constexpr int kRefreshRows = 128;
+
+template <int D>
+struct RefreshSmem {
+  bf16_t pw[kRefreshPages][D];         // page weights, completed then pending page
+  bf16_t sw[kRefreshRows][D];          // segment weights of the candidates, in order
+  float h[D];
+  unsigned long long keys[kRefreshRows];
+  unsigned long long top[kRefreshRows];
+  int chosen[kRefreshRows / 8 + 1];
+};
+
+// Mass of one staged row on one wave (bit-reversed channel layout, the
+// butterfly sum of wave_masses): r(sum_D r(h * pw_row) [* sw_row]).
+template <int D>
+TAO_DEV float staged_mass(const float* h, const bf16_t* pw_row, const bf16_t* sw_row, int lane) {
+  constexpr int PER = D / 64;
+  const int e0 = fold_lane(lane);
+  float v[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const float hv = rbf(h[e0 + 64 * k] * bf2f(pw_row[e0 + 64 * k]));
+    v[k] = sw_row ? rbf(hv * bf2f(sw_row[e0 + 64 * k])) : hv;
+  }
+  float s = v[0];
+#pragma unroll
+  for (int k = 1; k < PER; ++k) s += v[k];
+  return rbf(wave_fold_sum(s));
+}
+
+template <int D>
+__global__ __launch_bounds__(kRouteThreads) void route_refresh_kernel(RouteParams p) {
+  __shared__ RefreshSmem<D> sm;
+  constexpr int C16 = D / 8;            // 16-byte chunks per row
+  const int bh = blockIdx.x;
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int K = p.completed, pending = p.pending, coarse = p.coarse, selected = p.selected;
+  const int group = p.group;
+  const int P = K + (pending > 0 ? 1 : 0);
+  const int E = group * coarse + pending;
+  const bf16_t* pw = p.pw + (size_t)bh * p.page_cap * D;
+  const bf16_t* sw = p.sw + (size_t)bh * p.fine_cap * D;
+  // ---- round trip 1: page weights, pending segment weights, anchor query
+  // (every load issued before any store to LDS)
+  constexpr int PW_PT = (kRefreshPages * C16 + kRouteThreads - 1) / kRouteThreads;
+  constexpr int SW_PT = (kRefreshRows * C16 + kRouteThreads - 1) / kRouteThreads;
+  // Loads are unconditional (indices clamped to a valid row) so the
+  // scheduler can issue them all before the guarded LDS stores.
+#pragma unroll
+  for (int k = 0; k < PW_PT; ++k) {
+    const int i = tid + k * kRouteThreads;
+    const int ic = min(i, P * C16 - 1);
+    const uint4 v = *(const uint4*)(pw + (size_t)(ic / C16) * D + (ic % C16) * 8);
+    if (i < P * C16) *(uint4*)&sm.pw[i / C16][(i % C16) * 8] = v;
+  }
+  if (pending > 0) {
+    const int ic = min(tid, pending * C16 - 1);
+    const uint4 v = *(const uint4*)(sw + (size_t)(K * group + ic / C16) * D + (ic % C16) * 8);
+    if (tid < pending * C16) *(uint4*)&sm.sw[group * coarse + tid / C16][(tid % C16) * 8] = v;
+  }
+  if (wave == 0) query_weights<D>(p.rq + b * p.rq_sb + h * p.rq_sh, lane, sm.h);
+  __syncthreads();
+  // ---- coarse pages: stable top-`coarse` by page mass, then ascending
+  if (coarse > 0) {
+    for (int pg = wave; pg < K; pg += kWaves) {
+      const float mass = staged_mass<D>(sm.h, sm.pw[pg], nullptr, lane);
+      if (lane == 0) sm.keys[pg] = score_key(mass, pg);
+    }
+    __syncthreads();
+    select_top(sm.keys, K, coarse, sm.top);
+    if (tid < coarse) {
+      const int mine = key_index(sm.top[tid]);
+      int rank = 0;
+      for (int j = 0; j < coarse; ++j) rank += key_index(sm.top[j]) < mine;
+      sm.chosen[rank] = mine;
+    }
+    __syncthreads();
+    // ---- round trip 2: segment weights of the chosen pages' fines
+#pragma unroll
+    for (int k = 0; k < SW_PT; ++k) {
+      const int i = tid + k * kRouteThreads;
+      const int ic = min(i, group * coarse * C16 - 1);
+      const int row = ic / C16;
+      const int id = sm.chosen[row / group] * group + row % group;
+      const uint4 v = *(const uint4*)(sw + (size_t)id * D + (ic % C16) * 8);
+      if (i < group * coarse * C16) *(uint4*)&sm.sw[i / C16][(i % C16) * 8] = v;
+    }
+    __syncthreads();
+  }
+  // ---- candidate masses: 8 fines of each chosen page, then the pending fines
+  for (int j = wave; j < E; j += kWaves) {
+    const int page = j < group * coarse ? sm.chosen[j / group] : K;
+    const float mass = staged_mass<D>(sm.h, sm.pw[page], sm.sw[j], lane);
+    if (lane == 0) sm.keys[j] = score_key(mass, j);
+  }
+  __syncthreads();
+  select_top(sm.keys, E, selected, sm.top);
+  int32_t* sel_out = p.sel + (size_t)bh * p.sel_cap;
+  for (int m = tid; m < selected; m += kRouteThreads) {
+    const int j = key_index(sm.top[m]);
+    sel_out[m] = j < group * coarse ? sm.chosen[j / group] * group + j % group
+                                    : K * group + (j - group * coarse);
+  }
+  for (int i = tid; i < coarse; i += kRouteThreads)
+    p.chosen[(size_t)bh * p.chosen_cap + i] = sm.chosen[i];
+  if (bh == 0 && tid == 0) p.header[1] = selected;
+}
+
+// ---------------------------------------------------------------------------
 // Per-query routes of the full-sequence read (route_interval = 1 in
 // _read_training_group, tao_stream.py:596-665, with candidate_scores,
 // routing_scores.py:7-47): every history query of a read tile routes itself
@@ -285,21 +419,6 @@ TAO_DEV void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Number of keys larger than `mine` among keys[0, n) (keys are unique).
-TAO_DEV int key_rank(const unsigned long long* keys, int n, unsigned long long mine) {
-  int r = 0;
-  int j = 0;
-  for (; j + 8 <= n; j += 8) {
-    unsigned long long k8[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) k8[i] = keys[j + i];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r += k8[i] > mine;
-  }
-  for (; j < n; ++j) r += keys[j] > mine;
-  return r;
 }
 
 template <int D>
@@ -703,6 +822,19 @@ hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s) {
       hipLaunchKernelGGL(route_turns_kernel<128>, tgrid, dim3(kQThreads), 0, s, p);
     else if (head_dim == 64)
       hipLaunchKernelGGL(route_turns_kernel<64>, tgrid, dim3(kQThreads), 0, s, p);
+    else
+      return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
+  // Single turn (a stream's refresh): the LDS-staged kernel when its rows fit.
+  const int pages = p.completed + (p.pending > 0 ? 1 : 0);
+  if (!p.turns && pages <= kRefreshPages && p.group * p.coarse + p.pending <= kRefreshRows &&
+      p.group <= 8) {
+    const dim3 rgrid((unsigned)(p.B * p.H));
+    if (head_dim == 128)
+      hipLaunchKernelGGL(route_refresh_kernel<128>, rgrid, dim3(kRouteThreads), 0, s, p);
+    else if (head_dim == 64)
+      hipLaunchKernelGGL(route_refresh_kernel<64>, rgrid, dim3(kRouteThreads), 0, s, p);
     else
       return hipErrorInvalidValue;
     return hipGetLastError();

@@ -45,6 +45,7 @@ TAO_DEV int key_index(unsigned long long key) {
 constexpr int kRouteThreads = 512;   // 8 waves
 constexpr int kWaves = kRouteThreads / 64;
 constexpr int kBatch = 8;            // rows whose loads one wave issues together
+constexpr int kRefreshBatch = 10;    // staged rows one wave reduces together
 constexpr int kRankMax = 512;        // rank-count selection up to this many keys
 
 // Masses of up to kBatch rows per wave: every lane loads its two (or one)
@@ -134,6 +135,21 @@ TAO_DEV int key_rank(const unsigned long long* keys, int n, unsigned long long m
 // score << 32 | ~index). Writes the selected keys, best first, to dst.
 TAO_DEV void select_top(unsigned long long* keys, int n, int count,
                            unsigned long long* dst) {
+  if (n <= 2 * kRouteThreads / 8) {
+    // T lanes per key (8 for n <= 64, 4 for n <= 128): lane part p counts
+    // the larger keys among keys p, p + T, ...; DPP adds the T parts.
+    const int T = n <= kRouteThreads / 8 ? 8 : 4;
+    const int i = threadIdx.x / T, part = threadIdx.x % T;
+    const unsigned long long mine = keys[min(i, n - 1)];
+    int cnt = 0;
+    for (int j = part; j < n; j += T) cnt += keys[j] > mine;
+    cnt += __builtin_amdgcn_update_dpp(0, cnt, 0xB1, 0xF, 0xF, false);
+    cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x4E, 0xF, 0xF, false);
+    if (T == 8) cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x141, 0xF, 0xF, false);
+    if (i < n && part == 0 && cnt < count) dst[cnt] = mine;
+    __syncthreads();
+    return;
+  }
   if (n <= kRankMax) {
     for (int i = threadIdx.x; i < n; i += kRouteThreads) {
       const unsigned long long mine = keys[i];
@@ -292,22 +308,50 @@ struct RefreshSmem {
   int chosen[kRefreshRows / 8 + 1];
 };
 
-// Mass of one staged row on one wave (bit-reversed channel layout, the
-// butterfly sum of wave_masses): r(sum_D r(h * pw_row) [* sw_row]).
+// Masses of kBatch staged rows on one wave (bit-reversed channel layout,
+// the butterfly sum of wave_masses): r(sum_D r(h * pw_row) [* sw_row]).
+// The rows' reductions are independent and unrolled, so their latencies
+// overlap. Rows past `count` (wave-uniform) give 0 and are not used; this
+// wave's lane r < count receives row r's mass.
 template <int D>
-TAO_DEV float staged_mass(const float* h, const bf16_t* pw_row, const bf16_t* sw_row, int lane) {
+TAO_DEV float staged_masses(const float* h, const bf16_t* const* pw_rows,
+                            const bf16_t* const* sw_rows, int count, int lane) {
   constexpr int PER = D / 64;
   const int e0 = fold_lane(lane);
-  float v[PER];
+  float hq[PER];
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const float hv = rbf(h[e0 + 64 * k] * bf2f(pw_row[e0 + 64 * k]));
-    v[k] = sw_row ? rbf(hv * bf2f(sw_row[e0 + 64 * k])) : hv;
+  for (int k = 0; k < PER; ++k) hq[k] = h[e0 + 64 * k];
+  // Rows past `count` repeat the last row (callers clamp), so every read is
+  // unconditional and the reads of all rows are in flight together.
+  bf16_t pv[kRefreshBatch][PER], sv[kRefreshBatch][PER];
+#pragma unroll
+  for (int r = 0; r < kRefreshBatch; ++r)
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      pv[r][k] = pw_rows[r][e0 + 64 * k];
+      sv[r][k] = sw_rows ? sw_rows[r][e0 + 64 * k] : (bf16_t)0;
+    }
+  float part[kRefreshBatch];
+#pragma unroll
+  for (int r = 0; r < kRefreshBatch; ++r) {
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const float hv = rbf(hq[k] * bf2f(pv[r][k]));
+      v[k] = sw_rows ? rbf(hv * bf2f(sv[r][k])) : hv;
+    }
+    float s = v[0];
+#pragma unroll
+    for (int k = 1; k < PER; ++k) s += v[k];
+    part[r] = s;
   }
-  float s = v[0];
+  wave_fold_sum_n<kRefreshBatch>(part);
+  float mine = 0.0f;
 #pragma unroll
-  for (int k = 1; k < PER; ++k) s += v[k];
-  return rbf(wave_fold_sum(s));
+  for (int r = 0; r < kRefreshBatch; ++r)
+    if (lane == r) mine = rbf(part[r]);
+  (void)count;
+  return mine;
 }
 
 template <int D>
@@ -318,7 +362,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_refresh_kernel(RouteParam
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int K = p.completed, pending = p.pending, coarse = p.coarse, selected = p.selected;
-  const int group = p.group;
+  constexpr int group = 8;          // coarse_group (checked at launch)
   const int P = K + (pending > 0 ? 1 : 0);
   const int E = group * coarse + pending;
   const bf16_t* pw = p.pw + (size_t)bh * p.page_cap * D;
@@ -345,9 +389,13 @@ __global__ __launch_bounds__(kRouteThreads) void route_refresh_kernel(RouteParam
   __syncthreads();
   // ---- coarse pages: stable top-`coarse` by page mass, then ascending
   if (coarse > 0) {
-    for (int pg = wave; pg < K; pg += kWaves) {
-      const float mass = staged_mass<D>(sm.h, sm.pw[pg], nullptr, lane);
-      if (lane == 0) sm.keys[pg] = score_key(mass, pg);
+    for (int base = wave * kRefreshBatch; base < K; base += kWaves * kRefreshBatch) {
+      const int count = min(kRefreshBatch, K - base);
+      const bf16_t* rows[kRefreshBatch];
+#pragma unroll
+      for (int r = 0; r < kRefreshBatch; ++r) rows[r] = sm.pw[base + min(r, count - 1)];
+      const float mass = staged_masses<D>(sm.h, rows, nullptr, count, lane);
+      if (lane < count) sm.keys[base + lane] = score_key(mass, base + lane);
     }
     __syncthreads();
     select_top(sm.keys, K, coarse, sm.top);
@@ -371,10 +419,18 @@ __global__ __launch_bounds__(kRouteThreads) void route_refresh_kernel(RouteParam
     __syncthreads();
   }
   // ---- candidate masses: 8 fines of each chosen page, then the pending fines
-  for (int j = wave; j < E; j += kWaves) {
-    const int page = j < group * coarse ? sm.chosen[j / group] : K;
-    const float mass = staged_mass<D>(sm.h, sm.pw[page], sm.sw[j], lane);
-    if (lane == 0) sm.keys[j] = score_key(mass, j);
+  for (int base = wave * kRefreshBatch; base < E; base += kWaves * kRefreshBatch) {
+    const int count = min(kRefreshBatch, E - base);
+    const bf16_t* prow[kRefreshBatch];
+    const bf16_t* srow[kRefreshBatch];
+#pragma unroll
+    for (int r = 0; r < kRefreshBatch; ++r) {
+      const int j = base + min(r, count - 1);
+      prow[r] = sm.pw[j < group * coarse ? sm.chosen[j / group] : K];
+      srow[r] = sm.sw[j];
+    }
+    const float mass = staged_masses<D>(sm.h, prow, srow, count, lane);
+    if (lane < count) sm.keys[base + lane] = score_key(mass, base + lane);
   }
   __syncthreads();
   select_top(sm.keys, E, selected, sm.top);
@@ -829,7 +885,7 @@ hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s) {
   // Single turn (a stream's refresh): the LDS-staged kernel when its rows fit.
   const int pages = p.completed + (p.pending > 0 ? 1 : 0);
   if (!p.turns && pages <= kRefreshPages && p.group * p.coarse + p.pending <= kRefreshRows &&
-      p.group <= 8) {
+      p.group == 8) {
     const dim3 rgrid((unsigned)(p.B * p.H));
     if (head_dim == 128)
       hipLaunchKernelGGL(route_refresh_kernel<128>, rgrid, dim3(kRouteThreads), 0, s, p);

@@ -116,6 +116,30 @@ TAO_DEV float wave_fold_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// wave_fold_sum of N independent values at once, level by level across the
+// values so their DPP steps interleave (no hazard stalls between the steps
+// of one chain). Each result equals wave_fold_sum of that value bit for bit.
+template <int N>
+TAO_DEV void wave_fold_sum_n(float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_partner<0xB1>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_partner<0x4E>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_partner<0x141>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_partner<0x140>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int bits = __builtin_bit_cast(int, v[i]);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 48));
+    v[i] = (r0 + r1) + (r2 + r3);
+  }
+}
+
 // Maximum over the wave with the same DPP pattern (order-free).
 TAO_DEV float wave_fold_max(float v) {
   v = fmaxf(v, dpp_partner<0xB1>(v));

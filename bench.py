@@ -6,8 +6,9 @@ Headline (``value``): advancing decode tok/s of one request x layer from a
 configs[3]): --warmup untimed single-token steps, then --steps timed ones
 (default 16 + 256: the timed steps hold 11 route refreshes and the seal at
 position 131327; config.workload states the counts of the run). Each step
-is issued by the native C++ driver as direct kernel launches; the hipGraph
-preset is timed on the same steps and reported as decode_graph. Also
+is issued by the native C++ driver as direct kernel launches; the graph
+preset (both replay mechanisms) is timed on the same steps and reported as
+decode_graph. Also
 reported: prefill tokens/s of a 16384-token prompt through
 tao_attention_prefill, batched streaming decode of 32 ragged
 requests (configs[4], decode_batch), a cold-cache decode variant that
@@ -153,10 +154,10 @@ def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
     """Headline decode: direct launches by the native driver (graph=False).
 
     The state takes `warmup` untimed decode steps (the first call's one-time
-    setup falls there), then `steps` timed ones. The hipGraph preset runs the
-    same steps from the same snapshot on its own state (reported as
-    decode_graph), and the eager steps are replayed once more with the GPU
-    pre-loaded for kernel timing.
+    setup falls there), then `steps` timed ones. The graph preset runs the
+    same steps from the same snapshot on its own state, once per replay
+    mechanism (reported as decode_graph), and the eager steps are replayed
+    once more with the GPU pre-loaded for kernel timing.
     """
     from tao_attention import StreamCache, new_state, tao_attention_decode
     from tao_attention.presets import index_only_page_memo
@@ -171,16 +172,30 @@ def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
     first = context + args.warmup
     state, _ = decode_loop(torch, state, xs, fa, fb, context, args.warmup)
     state, seconds = decode_loop(torch, state, xs, fa, fb, first, args.steps)
-    graph_state = StreamCache.from_export(graph_snap)
-    graph_state, _ = decode_loop(torch, graph_state, xs, fa, fb, context, args.warmup)
-    region = graph_state.history_region
-    before = dict(region.counts) if region is not None else {}
-    graph_state, graph_seconds = decode_loop(torch, graph_state, xs, fa, fb, first, args.steps)
-    after = graph_state.history_region.observation()
-    graph_timed = {key: after[key] - before.get(key, 0)
-                   for key in ("epochs", "eager_warm", "captures", "replays")}
-    graph_state.release_execution()
-    del graph_state, graph_snap
+    graph = {}
+    for replay in ("dispatch", "hipgraph"):
+        saved = os.environ.get("TAO_GRAPH_REPLAY")
+        os.environ["TAO_GRAPH_REPLAY"] = replay
+        try:
+            graph_state = StreamCache.from_export(graph_snap)
+        finally:
+            if saved is None:
+                del os.environ["TAO_GRAPH_REPLAY"]
+            else:
+                os.environ["TAO_GRAPH_REPLAY"] = saved
+        graph_state, _ = decode_loop(torch, graph_state, xs, fa, fb, context, args.warmup)
+        region = graph_state.history_region
+        before = dict(region.counts) if region is not None else {}
+        graph_state, graph_seconds = decode_loop(torch, graph_state, xs, fa, fb, first,
+                                                 args.steps)
+        after = graph_state.history_region.observation()
+        timed_counts = {key: after[key] - before.get(key, 0)
+                        for key in ("epochs", "eager_warm", "captures", "replays", "id_copies",
+                                    "invalidations")}
+        graph[replay] = (graph_seconds, timed_counts)
+        graph_state.release_execution()
+        del graph_state
+    del graph_snap
     # Device time per step: replay the same steps eagerly on an imported copy
     # with the GPU pre-loaded by a bounded spin kernel, and bracket each group
     # of STEPS_PER_SPIN back-to-back steps with HIP events on the launch
@@ -210,7 +225,7 @@ def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
     torch.cuda.synchronize()
     probe.events["decode_step"] = groups
     timed.release_execution()
-    return state, xs, fa, fb, seconds, graph_seconds, steps_bytes, graph_timed
+    return state, xs, fa, fb, seconds, graph, steps_bytes
 
 
 def run_cold(torch, args, device, cfg, heads, width, context, n_states, probe):
@@ -708,7 +723,7 @@ def main():
     probe = Probe(torch)
 
     log("decode: building 128K state")
-    state, xs, fa, fb, seconds, graph_seconds, steps_bytes, graph_timed = run_decode(
+    state, xs, fa, fb, seconds, graph, steps_bytes = run_decode(
         torch, args, device, cfg, heads, width, args.context, 4, probe)
     from tao_attention import schedule
     first, last = args.context + args.warmup, args.context + args.warmup + args.steps
@@ -723,8 +738,10 @@ def main():
     alg_bytes = sum(b for b, _ in steps_bytes) / len(steps_bytes)
     own_bytes = sum(o for _, o in steps_bytes) / len(steps_bytes)
     achieved = alg_bytes / (step_ms * 1e-3) / 1e9
-    log(f"decode: {tok_s:.1f} tok/s (hipGraph preset {args.steps / graph_seconds:.1f}), "
-        f"step kernel {step_ms * 1e3:.2f} us, {achieved:.0f} GB/s")
+    log(f"decode: {tok_s:.1f} tok/s (graph preset: dispatch replay "
+        f"{args.steps / graph['dispatch'][0]:.1f}, hipGraph replay "
+        f"{args.steps / graph['hipgraph'][0]:.1f}), step kernel {step_ms * 1e3:.2f} us, "
+        f"{achieved:.0f} GB/s")
     result = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -741,8 +758,8 @@ def main():
         "config": {"workload": f"configs[3]: advancing decode of one request x layer from a "
                                f"{args.context}-token state, H32 D128; {window}; "
                                "index_only_page_memo(graph=False): each step is issued by "
-                               "the native C++ driver as direct launches (the hipGraph "
-                               "replay preset is timed on the same steps as decode_graph)",
+                               "the native C++ driver as direct launches (the graph preset "
+                               "is timed on the same steps as decode_graph)",
                    "context": args.context, "heads": heads, "head_dim": width,
                    "selected_fines": state.route_size, "timed_refreshes": refreshes,
                    "timed_seals": seals},
@@ -757,9 +774,17 @@ def main():
                      "own_bytes_per_step": int(own_bytes),
                      "own_GBs": round(own_bytes / (step_ms * 1e-3) / 1e9, 1)},
         "decode_graph": {"preset": "index_only_page_memo(graph=True)",
-                         "tok_s": round(args.steps / graph_seconds, 2),
-                         "ms_per_step": round(graph_seconds / args.steps * 1e3, 4),
-                         "timed_steps": graph_timed},
+                         "replay": "dispatch (default): the epoch's recorded step "
+                                   "arguments dispatched directly",
+                         "tok_s": round(args.steps / graph["dispatch"][0], 2),
+                         "ms_per_step": round(graph["dispatch"][0] / args.steps * 1e3, 4),
+                         "timed_steps": graph["dispatch"][1],
+                         "hipgraph": {"replay": "TAO_GRAPH_REPLAY=hipgraph: hipGraphLaunch "
+                                                "of the captured copy + step",
+                                      "tok_s": round(args.steps / graph["hipgraph"][0], 2),
+                                      "ms_per_step": round(graph["hipgraph"][0] / args.steps
+                                                           * 1e3, 4),
+                                      "timed_steps": graph["hipgraph"][1]}},
     }
     if not args.no_cold:
         log("cold decode: building states")

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 6
+#define TAO_ABI_VERSION 7
 
 enum tao_status {
   TAO_OK = 0,
@@ -278,11 +278,14 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok,
 int tao_ring_append(const tao_state_dev* st, const tao_tokens* tok,
                     int32_t first, int32_t count, int64_t pos, void* stream);
 
-/* hipGraph of the decode step (replaces HistoryRegionGraph,
- * history_region_graph.py:10-113). The graph captures one copy of the
- * operands into stable staging buffers plus tao_decode_step; header-driven
- * counts let it replay across seals and refreshes. staging: bf16 device
- * buffer of 5 * B * H * D elements; out_stage: bf16 [B,1,H,D]. */
+/* hipGraph of the decode step (the captured region of HistoryRegionGraph,
+ * history_region_graph.py:95-113). The graph holds one copy of the operands
+ * into stable staging buffers (its root node) followed by tao_decode_step;
+ * tao_graph_launch points the root node at the call's operands
+ * (hipGraphExecKernelNodeSetParams) and replays. Header-driven counts would
+ * let it replay across seals and refreshes; the stream driver still ends
+ * its epoch at each one, as the reference does. staging: bf16 device buffer
+ * of 5 * B * H * D elements; out_stage: bf16 [B,1,H,D]. */
 int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu,
                      int32_t selected, void* staging, void* out_stage,
                      void* stream, void** graph_out);
@@ -294,7 +297,9 @@ int tao_graph_destroy(void* graph);
 typedef struct tao_stream_cfg {
   int32_t layer, local_keep, fine_tokens, coarse_group, route_period, layer_stagger;
   int32_t budget_root_scale, budget_offset;
-  int32_t use_graph;   /* replay the decode step from a hipGraph */
+  int32_t use_graph;   /* decode-graph epochs (history_region_graph.py:66-113):
+                          0 off; 1 replay by direct dispatch of the recorded
+                          step; 2 replay a hipGraph (tao_graph_create) */
 } tao_stream_cfg;
 
 /* Plan of one tao_prefill call for tokens [pos0, pos0 + tokens) of a
@@ -387,14 +392,21 @@ int tao_numerics_selftest(int32_t op, const void* x, void* y, int64_t n, void* s
 int tao_stream_open(const tao_state_dev* st, const tao_stream_cfg* cfg, int64_t position,
                     int32_t route_coarse, int32_t route_size, void* staging,
                     void* out_stage, void** handle);
-/* Re-point the driver after the host grew buffers, prefilled or imported. */
+/* Re-point the driver after the host grew buffers, prefilled or imported.
+ * An open graph epoch sees the advance as the reference's prefill does: its
+ * route refreshes copy ids (or end the epoch on a new route size), a seal
+ * ends it; moved buffers end it as an epoch change. */
 int tao_stream_sync(void* handle, const tao_state_dev* st, int64_t position,
                     int32_t route_coarse, int32_t route_size);
-/* One new token: route refresh on turn positions, the decode step (graph
- * replay or eager; with a graph the heads land in out_stage), and the seal
- * when the local window fills. info (int64[7]) receives: position after the
- * call, route coarse count, route size, refreshed, sealed, used_graph,
- * captured. */
+/* One new token: route refresh on turn positions, the decode step, and the
+ * seal when the local window fills. With use_graph the non-refresh steps of
+ * one epoch (same state version, route size and fusion parameters) follow
+ * HistoryRegionGraph.run (history_region_graph.py:66-113): three eager
+ * steps into out, then one capture and replays whose heads land in
+ * out_stage; a refresh step copies its route into the epoch (or ends it
+ * when the route size changed) and a seal ends it. out is always required.
+ * info (int64[7]) receives: position after the call, route coarse count,
+ * route size, refreshed, sealed, heads in out_stage (replay), captured. */
 int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu, void* out,
                       const int64_t* out_s, void* stream, int64_t* info);
 /* Batched decode of `count` independent requests of one layer (no reference
@@ -418,7 +430,46 @@ int tao_batch_decode(void* batch, const tao_tokens* tok, const tao_fusion* fu, v
                      const int64_t* out_s, void* stream, int64_t* info);
 int tao_batch_close(void* batch);
 
-/* Destroy the driver's captured graph (semantic state is untouched). */
+/* Why a decode-graph epoch ended (HistoryRegionGraph.invalidate callers:
+ * history_region_graph.py:60, 78; tao_stream.py:406, 445, 841, and this
+ * library's buffer growth). */
+enum tao_graph_reason {
+  TAO_GRAPH_SEAL = 0,
+  TAO_GRAPH_SELECTED_SHAPE = 1,
+  TAO_GRAPH_EPOCH_CHANGE = 2,
+  TAO_GRAPH_MEMO_REPLACE = 3,
+  TAO_GRAPH_REQUEST_END = 4,
+  TAO_GRAPH_RESET = 5,
+  TAO_GRAPH_CAPACITY = 6,
+  TAO_GRAPH_REASONS = 7
+};
+/* Epoch counters of the driver (HistoryRegionGraph.counts and observation(),
+ * history_region_graph.py:19-37), as int64 words at these indices; last
+ * action: 0 uninitialized, 1 eager_warm, 2 capture_replay, 3 replay,
+ * 4 route_copy, 5 invalidate (last reason in TAO_GS_LAST_REASON). */
+enum tao_graph_stat {
+  TAO_GS_EPOCHS = 0,
+  TAO_GS_EAGER_WARM = 1,
+  TAO_GS_CAPTURES = 2,
+  TAO_GS_REPLAYS = 3,
+  TAO_GS_ID_COPIES = 4,
+  TAO_GS_INVALIDATIONS = 5,
+  TAO_GS_ACTIVE_GRAPH = 6,      /* a captured step exists */
+  TAO_GS_ACTIVE_EPOCH = 7,      /* an epoch is open (its staging is bound) */
+  TAO_GS_EPOCH_VERSION = 8,     /* state version of the open epoch, or -1 */
+  TAO_GS_WARM = 9,              /* eager steps of the open epoch */
+  TAO_GS_LAST_ACTION = 10,
+  TAO_GS_LAST_REASON = 11,
+  TAO_GS_REASON0 = 12,          /* + tao_graph_reason: invalidations by reason */
+  TAO_GRAPH_STATS = 12 + TAO_GRAPH_REASONS
+};
+/* End the open epoch for `reason` (counted once, as
+ * HistoryRegionGraph.invalidate) and destroy its captured step; the
+ * semantic state is untouched. No-op when no epoch is open. */
+int tao_stream_invalidate(void* handle, int32_t reason);
+/* Copy min(n, TAO_GRAPH_STATS) epoch counters into stats. */
+int tao_stream_graph_stats(void* handle, int64_t* stats, int32_t n);
+/* tao_stream_invalidate(handle, TAO_GRAPH_REQUEST_END). */
 int tao_stream_release(void* handle);
 int tao_stream_close(void* handle);
 

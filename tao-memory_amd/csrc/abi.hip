@@ -216,6 +216,8 @@ struct DecodeGraph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   tao::StageParams stage{};
+  hipGraphNode_t stage_node = nullptr;   // root node: the operand copy
+  hipKernelNodeParams stage_kp{};        // its launch shape (arguments set per launch)
   int batch = 0, heads = 0, head_dim = 0;
 };
 
@@ -255,6 +257,37 @@ int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fus
   if (records) p.parts = records;
   return check_hip(tao::launch_decode_step(p, st->head_dim, selected, (hipStream_t)stream),
                    "tao_decode_step");
+}
+
+int decode_record(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
+                  int32_t selected, void* out, const int64_t* out_s, DecodeParams* rec) {
+  int rc = check_state(st);
+  if (!rc) rc = check_tokens(tok);
+  if (!rc) rc = check_fusion(fu);
+  if (rc) return rc;
+  if (tok->tokens != 1) return fail(TAO_E_SHAPE, "decode step takes exactly one token");
+  if (!out || !out_s || !rec) return fail(TAO_E_ARGUMENT, "null output");
+  if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected count exceeds sel_cap");
+  if (fu->coarse_on && !st->coarse_g)
+    return fail(TAO_E_ARGUMENT, "coarse_on needs a state with the coarse value branch");
+  *rec = decode_params(st, tok, fu, out, out_s);
+  return TAO_OK;
+}
+
+int decode_replay(const DecodeParams& rec, const tao_tokens* tok, int head_dim,
+                  int32_t selected, long long position, void* stream) {
+  int rc = check_tokens(tok);
+  if (rc) return rc;
+  if (tok->tokens != 1) return fail(TAO_E_SHAPE, "decode step takes exactly one token");
+  DecodeParams p = rec;
+  p.q = view(tok->q, tok->q_s);
+  p.k = view(tok->k, tok->k_s);
+  p.v = view(tok->v, tok->v_s);
+  p.rq = view(tok->raw_q, tok->rq_s);
+  p.rk = view(tok->raw_k, tok->rk_s);
+  p.pos_hint = position;
+  return check_hip(tao::launch_decode_step(p, head_dim, selected, (hipStream_t)stream),
+                   "decode replay");
 }
 
 }  // namespace tao
@@ -867,13 +900,30 @@ int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu, int32_t sele
   g->batch = B; g->heads = H; g->head_dim = D;
   g->stage.dst = stg;
   g->stage.B = B; g->stage.H = H; g->stage.D = D;
+  // Captured with the staging rows as their own sources (in bounds); every
+  // launch replaces the sources before the graph runs.
+  tao::StageParams sp = g->stage;
+  for (int i = 0; i < 5; ++i) sp.src[i] = view(ptrs[i], s);
   hipStream_t cs = nullptr;
   hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
   if (e == hipSuccess) {
-    hipError_t le = tao::launch_decode_step(p, D, selected, cs);
+    hipError_t le = tao::launch_stage_tokens(sp, cs);
+    if (le == hipSuccess) le = tao::launch_decode_step(p, D, selected, cs);
     e = hipStreamEndCapture(cs, &g->graph);
     if (e == hipSuccess) e = le;
+  }
+  // The copy is the graph's only root (the step's kernels follow it in
+  // stream order).
+  if (e == hipSuccess) {
+    size_t roots = 0;
+    e = hipGraphGetRootNodes(g->graph, nullptr, &roots);
+    if (e == hipSuccess && roots != 1) e = hipErrorInvalidValue;
+    if (e == hipSuccess) e = hipGraphGetRootNodes(g->graph, &g->stage_node, &roots);
+    hipGraphNodeType type = hipGraphNodeTypeEmpty;
+    if (e == hipSuccess) e = hipGraphNodeGetType(g->stage_node, &type);
+    if (e == hipSuccess && type != hipGraphNodeTypeKernel) e = hipErrorInvalidValue;
+    if (e == hipSuccess) e = hipGraphKernelNodeGetParams(g->stage_node, &g->stage_kp);
   }
   if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
   if (cs) (void)hipStreamDestroy(cs);
@@ -899,7 +949,13 @@ int tao_graph_launch(void* graph, const tao_tokens* tok, void* stream) {
   sp.src[2] = view(tok->v, tok->v_s);
   sp.src[3] = view(tok->raw_q, tok->rq_s);
   sp.src[4] = view(tok->raw_k, tok->rk_s);
-  hipError_t e = tao::launch_stage_tokens(sp, (hipStream_t)stream);
+  // Point the root copy at this call's operands; launches already queued
+  // keep the arguments they were launched with.
+  void* args[1] = {&sp};
+  hipKernelNodeParams kp = g->stage_kp;
+  kp.kernelParams = args;
+  kp.extra = nullptr;
+  hipError_t e = hipGraphExecKernelNodeSetParams(g->exec, g->stage_node, &kp);
   if (e == hipSuccess) e = hipGraphLaunch(g->exec, (hipStream_t)stream);
   return check_hip(e, "tao_graph_launch");
 }

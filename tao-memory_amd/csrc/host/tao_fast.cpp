@@ -29,7 +29,7 @@ class DecodeCall {
   DecodeCall(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& rq,
              const at::Tensor& rk, const at::Tensor& fa, const at::Tensor& fb, double alpha,
              uintptr_t fn, uintptr_t last_error, uintptr_t handle, uintptr_t tok,
-             uintptr_t fu, uintptr_t info, uintptr_t out_s, bool graph, int64_t first_fine)
+             uintptr_t fu, uintptr_t info, uintptr_t out_s)
       : sizes_(q.sizes().vec()),
         device_(q.device()),
         fa_impl_(fa.unsafeGetTensorImpl()),
@@ -43,15 +43,14 @@ class DecodeCall {
         tok_(reinterpret_cast<tao_tokens*>(tok)),
         fu_(reinterpret_cast<const tao_fusion*>(fu)),
         info_(reinterpret_cast<int64_t*>(info)),
-        out_s_(reinterpret_cast<const int64_t*>(out_s)),
-        graph_(graph),
-        first_fine_(first_fine) {
+        out_s_(reinterpret_cast<const int64_t*>(out_s)) {
     const at::Tensor* ts[5] = {&q, &k, &v, &rq, &rk};
     for (int i = 0; i < 5; ++i) strides_[i] = ts[i]->strides().vec();
   }
 
   // Returns the output tensor (eager), True (graph replay: the heads are in
-  // the graph's output buffer) or None (layout differs: take the full path).
+  // the epoch's output buffer, info[5]) or None (layout differs: take the
+  // full path).
   py::object call(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                   const at::Tensor& rq, const at::Tensor& rk, const at::Tensor& fa,
                   const at::Tensor& fb, double alpha, int64_t position, uintptr_t stream) {
@@ -73,18 +72,13 @@ class DecodeCall {
     tok_->v = ptrs[2];
     tok_->raw_q = ptrs[3];
     tok_->raw_k = ptrs[4];
-    const bool graph = graph_ && position >= first_fine_;
-    at::Tensor out;
-    void* out_ptr = nullptr;
-    if (!graph) {
-      out = at::empty_like(q);
-      out_ptr = out.data_ptr();
-    }
-    const int rc = fn_(handle_, tok_, fu_, out_ptr, graph ? nullptr : out_s_,
+    (void)position;
+    at::Tensor out = at::empty_like(q);
+    const int rc = fn_(handle_, tok_, fu_, out.data_ptr(), out_s_,
                        reinterpret_cast<void*>(stream), info_);
     if (rc < 0) throw py::value_error(last_error_());
     if (rc > 0) throw std::runtime_error(std::string("HIP error: ") + last_error_());
-    if (graph) return py::bool_(true);
+    if (info_[5]) return py::bool_(true);
     return py::cast(out);
   }
 
@@ -104,8 +98,6 @@ class DecodeCall {
   const tao_fusion* fu_;
   int64_t* info_;
   const int64_t* out_s_;
-  bool graph_;
-  int64_t first_fine_;
 };
 
 }  // namespace
@@ -114,7 +106,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   py::class_<DecodeCall>(m, "DecodeCall")
       .def(py::init<const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
                     const at::Tensor&, const at::Tensor&, const at::Tensor&, double, uintptr_t,
-                    uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, bool,
-                    int64_t>())
+                    uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t>())
       .def("__call__", &DecodeCall::call);
 }

@@ -5,12 +5,14 @@
 // -> _read_reused / HistoryRegionGraph.run -> seal; operator.py:130-138,
 // tao_stream.py:196-249, 919-969, history_region_graph.py:66-113) in C++, so
 // one ctypes call per token issues every launch: a route refresh on turn
-// positions, the fused decode step (eagerly or by replaying a hipGraph), and
+// positions, the fused decode step (eagerly, or replayed within a graph
+// epoch: a recorded argument block dispatched directly or a hipGraph), and
 // the seal (writer + epilogue) when the local window reaches serve_limit; a
 // seal that completes a page also builds its value matrix and refolds the
 // coarse read when the state carries the coarse value branch.
 // Every count is a closed form of the cursor (the same formulas as the
 // Python host's schedule module).
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -40,6 +42,27 @@ using tao::sched::fines_at;
 using tao::sched::is_turn;
 using tao::sched::local_len_at;
 
+// Eager steps of an epoch before its capture (history_region_graph.py:90).
+constexpr int kWarmSteps = 3;
+
+enum Action { kUninitialized = 0, kEagerWarm, kCaptureReplay, kReplay, kRouteCopy, kInvalidate };
+
+// One epoch of the decode graph (HistoryRegionGraph, history_region_graph.py:
+// 10-113): the non-refresh steps of one state version, route size and
+// fusion parameter set. The captured step is either a recorded kernel
+// argument block dispatched directly (use_graph 1) or a hipGraph (2).
+struct Epoch {
+  bool open = false;
+  int64_t version = -1;        // fines_at(cursor) when the epoch opened
+  int32_t selected = -1;
+  tao_fusion fusion{};
+  int32_t warm = 0;
+  bool recorded = false;       // use_graph 1: rec holds the captured step
+  tao::DecodeParams rec{};
+  void* graph = nullptr;       // use_graph 2
+  int64_t stats[TAO_GRAPH_STATS] = {};
+};
+
 struct Stream {
   tao_state_dev st;
   tao_stream_cfg cfg;
@@ -47,9 +70,7 @@ struct Stream {
   int32_t route_coarse = 0, route_size = 0;
   void* staging = nullptr;
   void* out_stage = nullptr;
-  void* graph = nullptr;
-  int32_t graph_selected = -1;
-  tao_fusion graph_fusion;
+  Epoch ep;
   int64_t* seal_start = nullptr;   // device int64 (first word of the plan region)
   int64_t seal_host = 0;           // host copy staged by the seal's upload
 };
@@ -61,14 +82,47 @@ int stream_fail(int code, const char* msg) {
 
 bool same_fusion(const tao_fusion& a, const tao_fusion& b) {
   return a.fusion_a == b.fusion_a && a.fusion_b == b.fusion_b && a.dtype == b.dtype &&
-         a.gain == b.gain && std::memcmp(a.a_s, b.a_s, sizeof(a.a_s)) == 0 &&
+         a.gain == b.gain && a.coarse_on == b.coarse_on && a.fine_on == b.fine_on &&
+         std::memcmp(a.a_s, b.a_s, sizeof(a.a_s)) == 0 &&
          std::memcmp(a.b_s, b.b_s, sizeof(a.b_s)) == 0;
 }
 
 void drop_graph(Stream* s) {
-  if (s->graph) tao_graph_destroy(s->graph);
-  s->graph = nullptr;
-  s->graph_selected = -1;
+  Epoch& ep = s->ep;
+  if (ep.graph) tao_graph_destroy(ep.graph);
+  ep.graph = nullptr;
+  ep.recorded = false;
+}
+
+// HistoryRegionGraph.invalidate (history_region_graph.py:39-57): counted
+// once per open epoch. The caller's stream order keeps queued replays valid:
+// nothing they read is freed here (the staging and output buffers belong to
+// the caller; a destroyed hipGraphExec's queued launches complete).
+void end_epoch(Stream* s, int reason) {
+  Epoch& ep = s->ep;
+  if (!ep.open) return;
+  drop_graph(s);
+  ep.open = false;
+  ep.version = -1;
+  ep.selected = -1;
+  ep.warm = 0;
+  ep.stats[TAO_GS_INVALIDATIONS] += 1;
+  ep.stats[TAO_GS_REASON0 + reason] += 1;
+  ep.stats[TAO_GS_LAST_ACTION] = kInvalidate;
+  ep.stats[TAO_GS_LAST_REASON] = reason;
+}
+
+// HistoryRegionGraph.update_routes (history_region_graph.py:56-64), called
+// by every route refresh (tao_stream.py:358-359).
+void route_update(Stream* s, int32_t selected) {
+  Epoch& ep = s->ep;
+  if (!ep.open) return;
+  if (selected != ep.selected) {
+    end_epoch(s, TAO_GRAPH_SELECTED_SHAPE);
+    return;
+  }
+  ep.stats[TAO_GS_ID_COPIES] += 1;
+  ep.stats[TAO_GS_LAST_ACTION] = kRouteCopy;
 }
 
 // Route refresh due at the stream's cursor (before its decode step).
@@ -90,6 +144,7 @@ int pre_step(Stream* s, const tao_tokens* tok, void* stream, int* refreshed) {
     s->route_coarse = coarse;
     s->route_size = selected;
     *refreshed = 1;
+    route_update(s, selected);
   }
   return TAO_OK;
 }
@@ -120,9 +175,87 @@ int post_step(Stream* s, const tao_tokens* tok, void* stream, int* sealed) {
     }
     if (rc) return rc;
     *sealed = 1;
+    end_epoch(s, TAO_GRAPH_SEAL);     // append_fine (tao_stream.py:444-445)
   }
   s->position = pos + 1;
   return TAO_OK;
+}
+
+// One non-refresh step under use_graph (HistoryRegionGraph.run,
+// history_region_graph.py:66-113). *staged = 1 when the heads are in
+// out_stage (capture or replay), 0 when they are in out (eager warm step).
+int region_step(Stream* s, const tao_tokens* tok, const tao_fusion* f, int32_t selected,
+                void* out, const int64_t* out_s, void* stream, int* staged, int* captured) {
+  Epoch& ep = s->ep;
+  const int64_t version = fines_at(s->cfg, s->position);
+  if (ep.open && (ep.version != version || ep.selected != selected || !same_fusion(ep.fusion, *f)))
+    end_epoch(s, TAO_GRAPH_EPOCH_CHANGE);
+  if (!ep.open) {
+    // A new epoch stages the current route ids (history_region_graph.py:78-89).
+    ep.open = true;
+    ep.version = version;
+    ep.selected = selected;
+    ep.fusion = *f;
+    ep.warm = 0;
+    ep.stats[TAO_GS_EPOCHS] += 1;
+    ep.stats[TAO_GS_ID_COPIES] += 1;
+  }
+  *staged = 0;
+  *captured = 0;
+  if (ep.warm < kWarmSteps) {
+    const int rc = tao::decode_step_at(&s->st, tok, f, selected, out, out_s, stream, s->position);
+    if (rc) return rc;
+    ep.warm += 1;
+    ep.stats[TAO_GS_EAGER_WARM] += 1;
+    ep.stats[TAO_GS_LAST_ACTION] = kEagerWarm;
+    return TAO_OK;
+  }
+  const tao_stream_cfg& c = s->cfg;
+  const int64_t stage_s[3] = {(int64_t)s->st.heads * s->st.head_dim, 0, (int64_t)s->st.head_dim};
+  int rc = TAO_OK;
+  if (c.use_graph == 2) {
+    if (!ep.graph) {
+      rc = tao_graph_create(&s->st, f, selected, s->staging, s->out_stage, stream, &ep.graph);
+      if (rc) return rc;
+      *captured = 1;
+    }
+    rc = tao_graph_launch(ep.graph, tok, stream);
+  } else {
+    if (!ep.recorded) {
+      rc = tao::decode_record(&s->st, tok, f, selected, s->out_stage, stage_s, &ep.rec);
+      if (rc) return rc;
+      ep.recorded = true;
+      *captured = 1;
+    }
+    rc = tao::decode_replay(ep.rec, tok, s->st.head_dim, selected, s->position, stream);
+  }
+  if (rc) return rc;
+  if (*captured) ep.stats[TAO_GS_CAPTURES] += 1;
+  ep.stats[TAO_GS_REPLAYS] += 1;
+  ep.stats[TAO_GS_LAST_ACTION] = *captured ? kCaptureReplay : kReplay;
+  *staged = 1;
+  return TAO_OK;
+}
+
+// The reference's prefill path over an open epoch (tao_stream.py:196-249):
+// the refreshes of positions [s->position, to) copy route ids (or end the
+// epoch on a new route size) until the first seal, which ends it.
+void epoch_advance(Stream* s, int64_t to) {
+  const tao_stream_cfg& c = s->cfg;
+  for (int64_t t = s->position; t < to && s->ep.open; ++t) {
+    const int64_t fines = fines_at(c, t);
+    if (fines != s->ep.version) {
+      end_epoch(s, TAO_GRAPH_SEAL);
+      break;
+    }
+    if (fines > 0 && is_turn(c, t)) {
+      int64_t coarse = 0, eligible = 0, selected = 0;
+      tao::sched::routed_counts(c, fines / c.coarse_group, fines % c.coarse_group, &coarse,
+                                &eligible, &selected);
+      route_update(s, (int32_t)selected);
+    }
+  }
+  if (s->ep.open && fines_at(c, to) != s->ep.version) end_epoch(s, TAO_GRAPH_SEAL);
 }
 
 struct Batch {
@@ -192,6 +325,7 @@ int tao_stream_open(const tao_state_dev* st, const tao_stream_cfg* cfg, int64_t 
   s->route_size = route_size;
   s->staging = staging;
   s->out_stage = out_stage;
+  s->ep.stats[TAO_GS_LAST_REASON] = -1;
   const tao::WorkspaceLayout lay =
       tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
   s->seal_start = (int64_t*)((char*)st->workspace + lay.plan_off);
@@ -203,7 +337,10 @@ int tao_stream_sync(void* handle, const tao_state_dev* st, int64_t position,
                     int32_t route_coarse, int32_t route_size) {
   if (!handle) return stream_fail(TAO_E_ARGUMENT, "null stream");
   Stream* s = (Stream*)handle;
+  if (position < s->position) end_epoch(s, TAO_GRAPH_EPOCH_CHANGE);
+  else epoch_advance(s, position);
   if (st && std::memcmp(st, &s->st, sizeof(*st)) != 0) {
+    end_epoch(s, TAO_GRAPH_EPOCH_CHANGE);
     drop_graph(s);
     s->st = *st;
     const tao::WorkspaceLayout lay =
@@ -231,18 +368,13 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
   tao_fusion f = *fu;
   f.coarse_on = coarse_values && fines >= c.coarse_group;   // a completed page exists
   f.fine_on = fines > 0;
-  int used_graph = 0, captured = 0;
-  if (c.use_graph && !coarse_values && fines > 0 && s->staging && s->out_stage) {
-    if (!s->graph || s->graph_selected != selected || !same_fusion(s->graph_fusion, f)) {
-      drop_graph(s);
-      rc = tao_graph_create(&s->st, &f, selected, s->staging, s->out_stage, stream, &s->graph);
-      if (rc) return rc;
-      s->graph_selected = selected;
-      s->graph_fusion = f;
-      captured = 1;
-    }
-    rc = tao_graph_launch(s->graph, tok, stream);
-    used_graph = 1;
+  int staged = 0, captured = 0;
+  // The graph serves the memo-backed index-only read of non-refresh steps
+  // (tao_stream.py:238-249); refresh steps run eagerly.
+  if (c.use_graph && !coarse_values && fines > 0 && !refreshed) {
+    if (!s->staging || !s->out_stage)
+      return stream_fail(TAO_E_ARGUMENT, "decode graph needs the staging and output buffers");
+    rc = region_step(s, tok, &f, selected, out, out_s, stream, &staged, &captured);
   } else {
     rc = tao::decode_step_at(&s->st, tok, &f, selected, out, out_s, stream, pos);
   }
@@ -254,7 +386,7 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
   info[2] = s->route_size;
   info[3] = refreshed;
   info[4] = sealed;
-  info[5] = used_graph;
+  info[5] = staged;
   info[6] = captured;
   return TAO_OK;
 }
@@ -402,11 +534,30 @@ int tao_batch_close(void* batch) {
   return TAO_OK;
 }
 
-int tao_stream_release(void* handle) {
+int tao_stream_invalidate(void* handle, int32_t reason) {
   if (!handle) return TAO_OK;
-  drop_graph((Stream*)handle);
+  if (reason < 0 || reason >= TAO_GRAPH_REASONS)
+    return stream_fail(TAO_E_ARGUMENT, "unknown graph invalidation reason");
+  Stream* s = (Stream*)handle;
+  end_epoch(s, reason);
+  drop_graph(s);
   return TAO_OK;
 }
+
+int tao_stream_graph_stats(void* handle, int64_t* stats, int32_t n) {
+  if (!handle || !stats || n < 0) return stream_fail(TAO_E_ARGUMENT, "null graph stats argument");
+  const Stream* s = (const Stream*)handle;
+  int64_t all[TAO_GRAPH_STATS];
+  std::memcpy(all, s->ep.stats, sizeof(all));
+  all[TAO_GS_ACTIVE_GRAPH] = (s->ep.graph != nullptr || s->ep.recorded) ? 1 : 0;
+  all[TAO_GS_ACTIVE_EPOCH] = s->ep.open ? 1 : 0;
+  all[TAO_GS_EPOCH_VERSION] = s->ep.open ? s->ep.version : -1;
+  all[TAO_GS_WARM] = s->ep.warm;
+  std::memcpy(stats, all, sizeof(int64_t) * (size_t)std::min<int32_t>(n, TAO_GRAPH_STATS));
+  return TAO_OK;
+}
+
+int tao_stream_release(void* handle) { return tao_stream_invalidate(handle, TAO_GRAPH_REQUEST_END); }
 
 int tao_stream_close(void* handle) {
   if (!handle) return TAO_OK;

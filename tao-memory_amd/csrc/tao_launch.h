@@ -141,6 +141,14 @@ int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fus
                    int32_t selected, void* out, const int64_t* out_s, void* stream,
                    long long position, float* records = nullptr);
 
+// The decode step's kernel arguments for a state, fusion and output buffer,
+// recorded once (decode_record) and dispatched per token with that token's
+// operands and cursor patched in (decode_replay).
+int decode_record(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
+                  int32_t selected, void* out, const int64_t* out_s, DecodeParams* rec);
+int decode_replay(const DecodeParams& rec, const tao_tokens* tok, int head_dim,
+                  int32_t selected, long long position, void* stream);
+
 struct StageParams {
   TokView src[5];
   bf16_t* dst;          // 5 x [B, H, D] contiguous

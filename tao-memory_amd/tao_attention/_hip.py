@@ -134,6 +134,8 @@ _SIGNATURES = {
     "tao_stream_decode": ([_vp, ctypes.POINTER(Tokens), ctypes.POINTER(Fusion), _vp,
                            ctypes.POINTER(_i64), _vp, ctypes.POINTER(_i64)], _i32),
     "tao_stream_release": ([_vp], _i32),
+    "tao_stream_invalidate": ([_vp, _i32], _i32),
+    "tao_stream_graph_stats": ([_vp, ctypes.POINTER(_i64), _i32], _i32),
     "tao_stream_close": ([_vp], _i32),
     "tao_graph_create": ([ctypes.POINTER(StateDev), ctypes.POINTER(Fusion), _i32, _vp, _vp,
                           _vp, ctypes.POINTER(_vp)], _i32),
@@ -160,6 +162,15 @@ _SIGNATURES = {
 }
 
 EXPORTED = tuple(_SIGNATURES)
+
+ABI_VERSION = 7                # TAO_ABI_VERSION of include/tao_memory.h
+
+# Decode-graph epoch counters (enum tao_graph_stat / tao_graph_reason).
+GRAPH_STATS = 19
+GRAPH_REASONS = ("seal", "selected_shape", "epoch_change", "memo_replace", "request_end",
+                 "reset", "capacity")
+GRAPH_ACTIONS = ("uninitialized", "eager_warm", "capture_replay", "replay", "route_copy",
+                 "invalidate")
 
 
 _fast = None
@@ -205,6 +216,9 @@ def lib():
             fn = getattr(handle, name)
             fn.argtypes = args
             fn.restype = res
+        if handle.tao_abi_version() != ABI_VERSION:
+            raise ImportError(f"{_LIB_PATH} has ABI {handle.tao_abi_version()}, these "
+                              f"bindings ABI {ABI_VERSION}: rebuild the library")
         _lib = handle
     return _lib
 

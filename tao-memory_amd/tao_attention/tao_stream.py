@@ -27,6 +27,7 @@ cursor (schedule.py), so no device-to-host synchronisation is needed.
 import contextlib
 import ctypes
 import itertools
+import os
 
 import numpy as np
 import torch
@@ -184,44 +185,84 @@ class _DeviceState:
 
 
 class HistoryRegionGraph:
-    """Counters of the decode-step hipGraph (history_region_graph.py:10-113).
+    """The decode-graph epochs of one request x layer (history_region_graph.py:10-113).
 
-    The graph itself lives in the native stream driver (stream.hip): one
-    captured graph per (state buffers, route size, fusion parameters), replayed
-    across seals and refreshes because the position and route ids are
-    device-resident. These counters keep the reference's observation() keys.
+    The epochs live in the native stream driver (stream.hip), which follows
+    HistoryRegionGraph.run: the non-refresh steps of one state version,
+    route size and fusion parameter set form an epoch; its first three steps
+    run eagerly, the fourth captures the step and replays it, later steps
+    replay; a refresh copies its route ids into the epoch (or ends it when
+    the route size changed), a seal ends it, and so do release_execution,
+    reset and buffer growth. This object reads the driver's counters and
+    keeps the reference's counts and observation() keys.
+
+    Replays dispatch the captured step: by default the recorded kernel
+    arguments (the two step kernels, state and output addresses fixed for
+    the epoch, the token's operands patched in per call); with
+    TAO_GRAPH_REPLAY=hipgraph in the environment a hipGraph whose root node
+    copies the operands into fixed staging (hipGraphExecKernelNodeSetParams
+    per call). Both write the heads into the epoch's fixed output buffer,
+    which the next replay overwrites, as the reference's captured outputs.
     """
 
-    def __init__(self):
-        self.counts = dict(epochs=0, eager_warm=0, captures=0, replays=0,
-                           id_copies=0, invalidations=0)
-        self.reasons = {}
-        self.last_action = "uninitialized"
-        self.active = False
+    capture_address_scope = ("State banks, route buffers and the driver's staging/output "
+                             "buffers of the current state version only; the captured step "
+                             "is dropped at every seal, route-size change and release")
+
+    def __init__(self, owner):
+        self._owner = owner
+        self._last = [0] * _hip.GRAPH_STATS
+        self._last[8] = self._last[11] = -1
+
+    def _stats(self):
+        handle = self._owner._handle
+        if handle is not None:
+            buf = (ctypes.c_int64 * _hip.GRAPH_STATS)()
+            _hip.check(_hip.lib().tao_stream_graph_stats(handle, buf, _hip.GRAPH_STATS))
+            self._last = list(buf)
+        return self._last
+
+    @property
+    def counts(self):
+        st = self._stats()
+        names = ("epochs", "eager_warm", "captures", "replays", "id_copies", "invalidations")
+        return {n: int(st[i]) for i, n in enumerate(names)}
+
+    @property
+    def reasons(self):
+        st = self._stats()
+        base = _hip.GRAPH_STATS - len(_hip.GRAPH_REASONS)
+        return {r: int(st[base + i]) for i, r in enumerate(_hip.GRAPH_REASONS)
+                if st[base + i]}
+
+    @property
+    def last_action(self):
+        st = self._stats()
+        action = _hip.GRAPH_ACTIONS[int(st[10])]
+        if action == "invalidate":
+            return "invalidate:" + _hip.GRAPH_REASONS[int(st[11])]
+        return action
+
+    @property
+    def warm_count(self):
+        return int(self._stats()[9])
 
     def observation(self):
-        return {**self.counts, "active_graph": self.active,
-                "last_action": self.last_action,
-                "invalidation_reasons": dict(self.reasons)}
+        st = self._stats()
+        return {**self.counts, "active_graph": bool(st[6]), "active_staging": bool(st[7]),
+                "epoch_state_version": None if st[8] < 0 else int(st[8]),
+                "epoch_warm_count": int(st[9]), "last_action": self.last_action,
+                "invalidation_reasons": self.reasons,
+                # Staging and output buffers are bound to the state for its
+                # life (fixed addresses across epochs); the captured step of a
+                # closed epoch is destroyed, so no retired execution tensors
+                # exist.
+                "last_retired_execution_tensors_alive": 0,
+                "python_owned_semantic_tensor_references": 0,
+                "capture_address_scope": self.capture_address_scope}
 
-    def record(self, used_graph, captured):
-        if captured:
-            self.counts["captures"] += 1
-            self.counts["epochs"] += 1
-            self.last_action = "capture_replay"
-        elif used_graph:
-            self.last_action = "replay"
-        if used_graph:
-            self.counts["replays"] += 1
-            self.active = True
 
-    def invalidate(self, reason):
-        if not self.active:
-            return
-        self.active = False
-        self.counts["invalidations"] += 1
-        self.reasons[reason] = self.reasons.get(reason, 0) + 1
-        self.last_action = "invalidate:" + reason
+_GRAPH_REPLAY = {"dispatch": 1, "hipgraph": 2}
 
 
 class StreamCache:
@@ -262,10 +303,14 @@ class StreamCache:
         self._native = None          # native decode entry (tao_fast.cpp)
         self._fast_limit = -1
         # The regional graph serves the memo-backed index-only read only
-        # (tao_stream.py:238-248).
-        self._graph_mode = bool(config.q1_history_region_graph
-                                and config.q1_page_normalization_memo
-                                and config.coarse_index_only)
+        # (tao_stream.py:238-248). Replay mechanism: see HistoryRegionGraph.
+        self._graph_mode = 0
+        if (config.q1_history_region_graph and config.q1_page_normalization_memo
+                and config.coarse_index_only):
+            replay = os.environ.get("TAO_GRAPH_REPLAY", "dispatch")
+            if replay not in _GRAPH_REPLAY:
+                raise ValueError(f"TAO_GRAPH_REPLAY must be one of {sorted(_GRAPH_REPLAY)}")
+            self._graph_mode = _GRAPH_REPLAY[replay]
         self._first_fine = self.config.first_fine
         self._graph_buffers = None
         self._log = []               # call log of the diagnostics counters
@@ -302,17 +347,21 @@ class StreamCache:
         self._run_open = True
 
     def _release_graph(self, reason):
-        if self.history_region is not None:
-            self.history_region.invalidate(reason)
+        """End the open graph epoch (HistoryRegionGraph.invalidate): the
+        caller's stream is drained first, as the reference does before it
+        drops captured addresses (history_region_graph.py:42-45)."""
         if self._handle is not None:
             if self._dev is not None:
                 torch.cuda.current_stream(self._dev.device).synchronize()
-            _hip.check(_hip.lib().tao_stream_release(self._handle))
+            _hip.check(_hip.lib().tao_stream_invalidate(
+                self._handle, _hip.GRAPH_REASONS.index(reason)))
 
     def _close_driver(self):
         if self._handle is not None:
             if self._dev is not None:
                 torch.cuda.current_stream(self._dev.device).synchronize()
+            if self.history_region is not None:
+                self.history_region._stats()         # keep the final counters
             _hip.lib().tao_stream_close(self._handle)
             self._handle = None
             self._handle_dirty = True
@@ -507,6 +556,10 @@ class StreamCache:
         self.position = end
         self._dev.header[0:1].fill_(end)
         self._handle_dirty = True
+        if self._handle is not None:
+            # The driver's graph epoch sees this advance now (its refreshes
+            # and seal), before any later release.
+            self._driver(self._dev)
         self._fold()
 
     def _fold(self):
@@ -529,7 +582,7 @@ class StreamCache:
         if self._handle is None:
             scfg = self._stream_cfg()
             staging = out_stage = None
-            if cfg.q1_history_region_graph:
+            if self._graph_mode:
                 B, H, D = dev.B, dev.H, dev.D
                 staging = torch.empty(5 * B * H * D, dtype=torch.bfloat16, device=dev.device)
                 out_stage = torch.empty((B, 1, H, D), dtype=torch.bfloat16, device=dev.device)
@@ -556,9 +609,9 @@ class StreamCache:
         computes its own local attention, so neither it nor its graph can
         take a plugin's output).
 
-        With the hipGraph preset the returned tensor is the graph's output
+        With the graph preset a replayed step returns the epoch's output
         buffer, overwritten by the next replay (as the reference's regional
-        graph returns its captured outputs).
+        graph returns its captured outputs); eager steps return new tensors.
 
         Fast path: the operand shapes, dtypes, devices and strides, the fusion
         parameter tensors and the driver binding are compared with the
@@ -635,8 +688,7 @@ class StreamCache:
                     _hip.function_address("tao_stream_decode"),
                     _hip.function_address("tao_last_error"), self._handle.value,
                     ctypes.addressof(self._tok), ctypes.addressof(fu),
-                    ctypes.addressof(self._info), ctypes.addressof(self._out_s),
-                    self._graph_mode, self._first_fine)
+                    ctypes.addressof(self._info), ctypes.addressof(self._out_s))
             except TypeError:
                 self._native = None
         return self._decode_launch(q)
@@ -644,12 +696,8 @@ class StreamCache:
     def _decode_launch(self, q):
         """Issue one token through the native driver and book-keep counters."""
         pos = self.position
-        graph = self._graph_mode and pos >= self._first_fine
-        if graph:
-            out, out_ptr, out_s = None, None, None
-        else:
-            out = torch.empty_like(q)
-            out_ptr, out_s = out.data_ptr(), self._out_s
+        out = torch.empty_like(q)
+        out_ptr, out_s = out.data_ptr(), self._out_s
         info = self._info
         stream = _hip.raw_stream(self._stream_index)
         if self._probe is None:
@@ -661,9 +709,9 @@ class StreamCache:
                                 stream, info)
         if rc:
             _hip.check(rc)
-        return self._book(pos, graph, out)
+        return self._book(pos, bool(info[5]), out)
 
-    def _book(self, pos, graph, out):
+    def _book(self, pos, staged, out):
         """Cursor and counters after one driver call (info from the driver)."""
         if not self._run_open:
             self._open_run()
@@ -683,11 +731,9 @@ class StreamCache:
             self.fusion_no_history_local_returns += 1
             if info[4]:
                 self.fine_seal_events += 1
-        if graph or info[6]:
-            if self.history_region is None:
-                self.history_region = HistoryRegionGraph()
-            self.history_region.record(info[5], info[6])
-        if graph:
+        if self._graph_mode and pos >= self._first_fine and self.history_region is None:
+            self.history_region = HistoryRegionGraph(self)
+        if staged:
             return self._graph_buffers[1]
         return out
 

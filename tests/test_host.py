@@ -82,7 +82,7 @@ def test_library_exports_every_header_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert sorted(_hip.EXPORTED) == declared
-    assert lib.tao_abi_version() == 6
+    assert lib.tao_abi_version() == _hip.ABI_VERSION == 7
 
 
 def test_workspace_size_and_error_convention():
@@ -256,3 +256,16 @@ def test_native_train_plan_matches_read_training_tiling():
                 assert (coarse, m, erel, split, on, cpages) == (
                     c, sel, visible - 1, (visible // 8) * 8, 1, visible // 8)
             assert starts == list(range(0, tokens, 32))
+
+
+def test_graph_stat_layout_matches_header():
+    """The Python view of the driver's epoch counters uses the header's enums."""
+    text = open(os.path.join(ROOT, "include", "tao_memory.h")).read()
+    reasons = re.findall(r"TAO_GRAPH_(\w+) = (\d+),", text)
+    names = {name.lower(): int(value) for name, value in reasons}
+    assert [names[r] for r in _hip.GRAPH_REASONS] == list(range(len(_hip.GRAPH_REASONS)))
+    assert int(re.search(r"TAO_GRAPH_REASONS = (\d+)", text).group(1)) == len(_hip.GRAPH_REASONS)
+    stats = dict(re.findall(r"(TAO_GS_\w+) = (\d+)", text))
+    assert int(stats["TAO_GS_REASON0"]) + len(_hip.GRAPH_REASONS) == _hip.GRAPH_STATS
+    assert (int(stats["TAO_GS_LAST_ACTION"]), int(stats["TAO_GS_LAST_REASON"])) == (10, 11)
+    assert int(stats["TAO_GS_EPOCH_VERSION"]) == 8 and int(stats["TAO_GS_WARM"]) == 9

@@ -416,6 +416,13 @@ class OracleStream:
             elements -= self.completed * d * d
         return elements * b * heads * 2
 
+    def pending_writer_bytes(self):
+        """LayerState.pending_writer_bytes (tao_stream.py:514-516): the
+        regularized writer's pending gram and cross sums, counted at the
+        reference's fp32 (4 bytes an element; the oracle holds them in fp64)."""
+        return sum(t.numel() * 4 for t in (self.pending_gram, self.pending_cross)
+                   if t is not None)
+
     def release_execution(self):
         """StreamCache.release_execution (:838-844): drops the memo."""
         self.memo = False
@@ -491,7 +498,7 @@ class OracleStream:
         self.diag["fine_candidate_scores"] += self.last_route_queries * eligible
         self.diag["peak_local_length_tokens"] = max(self.diag["peak_local_length_tokens"],
                                                     all_k.shape[1])
-        history = self.logical_bytes(b, heads, d)
+        history = self.logical_bytes(b, heads, d) + self.pending_writer_bytes()   # :953-958
         key_bytes = all_k.numel() * 2
         self._preseal = (history + 2 * key_bytes, history + 3 * key_bytes)
         if all_k.shape[1] == self.g.serve_limit:
@@ -503,6 +510,13 @@ class OracleStream:
                           all_raw[:, -keep:].clone())
         else:
             self.local = (all_k, all_v, all_raw)
+        if self.writer == "regularized_association":
+            # :969-978: the first pending sums of a new page count in the
+            # peak; the pre-seal peak stays when a completed page drops them.
+            after = self.logical_bytes(b, heads, d) + self.pending_writer_bytes()
+            local_bytes = self.local[0].numel() * 2
+            self._preseal = (max(self._preseal[0], after + 2 * local_bytes),
+                             max(self._preseal[1], after + 3 * local_bytes))
         return local, coarse, fine, c_on, f_on
 
     def prefill(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,

@@ -62,6 +62,16 @@ def _history_bytes(completed, pending, B, H, D, config):
     return elements * B * H * 2
 
 
+def _pending_writer_bytes(fines, B, H, D, config):
+    """LayerState.pending_writer_bytes (tao_stream.py:514-516) of the
+    regularized writer after `fines` seals: the fp32 gram and cross sums,
+    present from the first seal until a completed page drops them (never
+    dropped in the index-only preset, tao_stream.py:486-497)."""
+    fines = np.asarray(fines, dtype=np.int64)
+    present = (fines > 0) & ((fines % config.coarse_group > 0) | config.coarse_index_only)
+    return np.where(present, 2 * B * H * D * D * 4, 0)
+
+
 def _segment(c, positions, widths, single, route_size, layer, B, H, D, config):
     """Account the chunks starting at `positions` (widths `widths`); `single`
     marks one-token calls. Returns the route size after the last chunk."""
@@ -122,9 +132,23 @@ def _segment(c, positions, widths, single, route_size, layer, B, H, D, config):
     c.peak_local_length_tokens = max(c.peak_local_length_tokens, int(all_k.max()))
     hist = _history_bytes(completed, pending, B, H, D, config)
     key = B * all_k * H * D * 2
-    c.peak_logical_cache_bytes = max(c.peak_logical_cache_bytes, int((hist + 2 * key).max()))
+    logical, physical = hist + 2 * key, hist + 3 * key
+    if config.fine_writer == "regularized_association":
+        # The pending gram and cross sums (tao_stream.py:953-958, 969-978):
+        # counted before the chunk and, at a seal, after it (the first sums
+        # of a new page; the pre-seal peak stays when a page drops them).
+        logical = logical + _pending_writer_bytes(f, B, H, D, config)
+        physical = physical + _pending_writer_bytes(f, B, H, D, config)
+        sealed = all_k == config.serve_limit
+        f1 = f + sealed
+        after = (_history_bytes(f1 // group, f1 % group, B, H, D, config)
+                 + _pending_writer_bytes(f1, B, H, D, config))
+        keep = B * config.local_keep * H * D * 2
+        logical = np.where(sealed, np.maximum(logical, after + 2 * keep), logical)
+        physical = np.where(sealed, np.maximum(physical, after + 3 * keep), physical)
+    c.peak_logical_cache_bytes = max(c.peak_logical_cache_bytes, int(logical.max()))
     c.peak_physical_cache_tensor_bytes = max(c.peak_physical_cache_tensor_bytes,
-                                             int((hist + 3 * key).max()))
+                                             int(physical.max()))
     # Page-normalisation memo: built by a non-refresh one-token read with
     # history (memo preset, index-only), dropped by a seal after the read.
     memo_cfg = config.q1_page_normalization_memo and config.coarse_index_only

@@ -975,6 +975,14 @@ class StreamCache:
         route_bytes = (8 * batch * heads * (self.route_coarse + self.route_size)
                        if self.route_size else 0)
         logical_local = local_tokens * 2 * heads * width * 2 * batch
+        # The regularized writer's pending sums (fp32 [B, H, D, D] gram and
+        # cross), counted while the reference holds them (tao_stream.py:463-499,
+        # 514-516; the rule export follows).
+        pending_writer = 0
+        if dev is not None and dev.association:
+            pending_writer = int(diagnostics._pending_writer_bytes(fines, batch, heads, width,
+                                                                   cfg))
+        pending_cross = pending_writer // 2
         physical_local = 0
         unique = 0
         if dev is not None:
@@ -985,12 +993,13 @@ class StreamCache:
                 dev.page_z, dev.page_w, dev.sel, dev.chosen, dev.header, dev.fold_g,
                 dev.fold_den, dev.workspace) if t is not None)
             unique += sum(t.numel() * t.element_size()
-                          for t in (dev.page_c, dev.coarse_g) if t is not None)
+                          for t in (dev.page_c, dev.coarse_g, dev.pending_gram,
+                                    dev.pending_cross, dev.stats) if t is not None)
         return {"history_bytes": history,
                 "page_normalization_memo_bytes": memo,
-                "pending_writer_bytes": 0,
-                "pending_gram_cross_bytes": 0,
-                "pending_cross_bytes": 0,
+                "pending_writer_bytes": pending_writer,
+                "pending_gram_cross_bytes": pending_writer,
+                "pending_cross_bytes": pending_cross,
                 "pending_square_mass_bytes": 0,
                 "pending_feature_mass_bytes": 0,
                 "fused_fine": self.fused_fine,
@@ -1010,9 +1019,10 @@ class StreamCache:
                 "fine_seal_events": self.fine_seal_events,
                 "route_integer_bytes": route_bytes,
                 "logical_local_bf16_kv_bytes": logical_local,
-                "logical_retained_bytes": history + logical_local,
+                "logical_retained_bytes": history + pending_writer + logical_local,
                 "physical_local_including_raw_key_bytes": physical_local,
-                "allocated_cache_tensor_bytes": history + physical_local + route_bytes + memo,
+                "allocated_cache_tensor_bytes": (history + pending_writer + physical_local
+                                                 + route_bytes + memo),
                 "unique_allocated_cache_storage_bytes": unique,
                 "local_length_tokens": local_tokens,
                 "completed_coarse_pages": completed,

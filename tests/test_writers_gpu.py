@@ -262,6 +262,15 @@ def test_stream_regularized_writer(device, index_only, width, batch):
         got, want = snap[key], osnap[key]
         assert got is not None and got.dtype == torch.float32
         close(got, want, 1e-3)
+    diag = state.bytes()
+    assert diag["pending_writer_bytes"] == ora.pending_writer_bytes() == \
+        2 * batch * heads * width * width * 4
+    assert diag["pending_gram_cross_bytes"] == diag["pending_writer_bytes"]
+    assert diag["pending_cross_bytes"] == diag["pending_writer_bytes"] // 2
+    assert diag["logical_retained_bytes"] == (diag["history_bytes"] + diag["pending_writer_bytes"]
+                                              + diag["logical_local_bf16_kv_bytes"])
+    for key in ("peak_logical_cache_bytes", "peak_physical_cache_tensor_bytes"):
+        assert diag[key] == ora.diag[key], key
     restored = StreamCache.from_export(snap)
     tok = [x[:, tokens - 1:tokens] for x in d]
     nxt = []

@@ -185,3 +185,38 @@ def test_oracle_stream_regularized_writer_pages_and_pending():
         back = O.OracleStream.from_export(snap, 0, O.Geometry(coarse_index_only=index_only))
         assert back.writer == "regularized_association"
         assert torch.equal(back.pending_gram.float(), snap["pending_gram"])
+
+
+@pytest.mark.parametrize("index_only", [False, True])
+def test_regularized_writer_peak_counts_pending_sums(index_only):
+    """The pending gram/cross sums enter the peak cache bytes
+    (tao_stream.py:953-958, 969-978), in the oracle and in the product's
+    closed-form diagnostics. Closed form at B1 H2 D128 for a 768-token
+    prefill: the third 256-token chunk seals the first fine; before it the
+    peak is 2 x 768 key rows, after it one fine's bytes + the fp32 sums +
+    2 x 512 key rows, which is larger:
+      before = 2 * 768 * H * D * 2                         = 786432
+      after  = (D*D + D) * H * 2 + 2 * H * D * D * 4 + 2 * 512 * H * D * 2
+             = 66048 + 262144 + 524288                      = 852480
+    Physical counts three key rows, and there the pre-seal figure stays:
+      max(3 * 768 * H * D * 2, 66048 + 262144 + 3 * 512 * H * D * 2)
+      = max(1179648, 1114624)."""
+    from oracle import tao_oracle as O
+    from tao_attention import TaoConfig, diagnostics
+    h, d, t = 2, 128, 768
+    g = torch.Generator().manual_seed(3)
+    xs = [torch.randn(1, t, h, d, generator=g).to(BF16) for _ in range(5)]
+    fa = torch.zeros(h, d, 3)
+    s = O.OracleStream(0, O.Geometry(coarse_index_only=index_only),
+                       writer="regularized_association")
+    s.prefill(*xs, fa, fa, 0.5)
+    assert s.pending_writer_bytes() == 2 * h * d * d * 4
+    assert s.diag["peak_logical_cache_bytes"] == 852480
+    assert s.diag["peak_physical_cache_tensor_bytes"] == 1179648
+    soft = O.OracleStream(0, O.Geometry(coarse_index_only=index_only))
+    soft.prefill(*xs, fa, fa, 0.5)
+    assert soft.diag["peak_logical_cache_bytes"] == 786432
+    cfg = TaoConfig(fine_writer="regularized_association", coarse_index_only=index_only)
+    c = diagnostics.counters(cfg, 0, 1, h, d, [("call", 0, t, 0)], t)
+    assert (c.peak_logical_cache_bytes, c.peak_physical_cache_tensor_bytes) == (
+        s.diag["peak_logical_cache_bytes"], s.diag["peak_physical_cache_tensor_bytes"])

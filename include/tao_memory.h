@@ -7,7 +7,8 @@
  * tao_attention package, or any FFI) owns every buffer: the library never
  * allocates or frees caller memory. All tensors are device pointers with
  * element strides; the head dimension is contiguous. All arithmetic is on
- * bf16 storage with fp32 accumulation.
+ * bf16 storage with fp32 accumulation, except tao_full_sequence_f32 (fp32
+ * operands and fp32 rounding points).
  *
  * Return convention: 0 = ok; negative = contract error (the Python host
  * raises ValueError); positive = HIP runtime error code (RuntimeError).
@@ -375,6 +376,27 @@ size_t tao_train_bwd_workspace_bytes(const tao_state_dev* st, int64_t tokens, in
 int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
                        const tao_prefill_pools* pools, const tao_train_bwd* args,
                        void* stream);
+
+/* fp32 full-sequence read: tao_attention on fp32 operands (replaces the
+ * reference's read_training + _fuse_training at fp32, operator.py:21-54,
+ * tao_stream.py:80-123, 530-787). tok: fp32 [B, T, H, D] views (element
+ * strides, channel stride 1; tokens = T). fu: fusion parameters of any
+ * tao_dtype; gain = fp32(2 alpha). out: fp32 [B, T, H, D]. cfg: the
+ * geometry (512/256/8) and the budget; layer, route_period, layer_stagger
+ * and use_graph are unused. coarse_values: 0 for coarse_index_only.
+ * Every rounding point of the bf16 contract rounds to fp32, and routing
+ * sums keep the bf16 path's orders, so routes are reproducible bit for
+ * bit. Forward only. At most 64 pages and 256 route candidates per query
+ * (TAO_E_CAPACITY beyond). sel_out (optional, int32 [B, T, H, sel_cap]):
+ * each query's selected fine ids in score order, -1 padded (-1 throughout
+ * before first_fine). workspace: tao_full_sequence_f32_workspace_bytes()
+ * bytes of device memory, fully written before it is read. */
+size_t tao_full_sequence_f32_workspace_bytes(int32_t batch, int32_t heads, int32_t head_dim,
+                                             int64_t tokens, int32_t coarse_values);
+int tao_full_sequence_f32(const tao_stream_cfg* cfg, const tao_tokens* tok, const tao_fusion* fu,
+                          int32_t batch, int32_t heads, int32_t head_dim, int32_t coarse_values,
+                          void* out, const int64_t* out_s, int32_t* sel_out, int32_t sel_cap,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* Numerics self-test (no reference counterpart): y[i] = the library's
  * bf16(correctly rounded fp32 exp(x[i])) (op 0) or log (op 1) for n bf16

@@ -249,40 +249,43 @@ def coarse_read(h, page_z_completed, page_c):
 # ----------------------------------------------------------------------------
 
 def fusion(raw_q, local, coarse, fine, fusion_a, fusion_b, alpha,
-           coarse_on, fine_on):
-    """Three-branch presence-aware fusion with every bf16 cast explicit.
+           coarse_on, fine_on, arith=BF16):
+    """Three-branch presence-aware fusion with every cast explicit.
 
-    Kernel math is bf16 regardless of the stream dtype (Triton casts,
-    fusion_pointwise.py:103-121, 151-166); results are stored in raw_q's dtype.
+    Streaming (arith=bf16): the kernel math is bf16 regardless of the stream
+    dtype (Triton casts, fusion_pointwise.py:103-121, 151-166); results are
+    stored in raw_q's dtype. tao_attention's _fuse_training (operator.py:
+    21-38) rounds every torch op to the operand dtype instead: arith =
+    raw_q.dtype (the two agree for bf16 operands).
     """
     dtype = raw_q.dtype
     q = raw_q.to(F32)
-    a = rnd(fusion_a.to(F32)).to(F32)                       # [H, D, 3]
-    bias = rnd(fusion_b.to(F32)).to(F32)
+    a = rnd(fusion_a.to(F32), arith).to(F32)                # [H, D, 3]
+    bias = rnd(fusion_b.to(F32), arith).to(F32)
     present = int(coarse_on) + int(fine_on)
     local_bias = rnd(torch.tensor(math.log(present) if present else 0.0,
-                                  dtype=F32)).to(F32)
+                                  dtype=torch.float64), arith).to(F32)
     scores = []
     for branch in range(3):
-        prod = rnd(a[..., branch] * q).to(F32)
-        s = rnd(prod + bias[..., branch])
+        prod = rnd(a[..., branch] * q, arith).to(F32)
+        s = rnd(prod + bias[..., branch], arith)
         if branch == 0:
-            s = rnd(s.to(F32) + local_bias)
+            s = rnd(s.to(F32) + local_bias, arith)
         if (branch == 1 and not coarse_on) or (branch == 2 and not fine_on):
             s = torch.full_like(s, NEG_INF)
         scores.append(s)
     score = rnd(torch.stack(scores, -1), dtype)            # stored in dtype
     rho = rnd(softmax(score, -1), dtype)                    # F.softmax + .to
-    gain = rnd(torch.tensor(2 * alpha, dtype=F32), dtype).to(F32)
+    gain = rnd(torch.tensor(2 * alpha, dtype=torch.float64), dtype).to(F32)
     rl, rc, rf = (rho[..., i].to(F32) for i in range(3))
-    local_twice = rnd(2.0 * local.to(F32)).to(F32)
-    coarse_scaled = rnd(gain * coarse.to(F32)).to(F32)
-    fine_scaled = rnd(gain * fine.to(F32)).to(F32)
-    lt = rnd(rl * local_twice).to(F32)
-    ct = rnd(rc * coarse_scaled).to(F32)
-    ft = rnd(rf * fine_scaled).to(F32)
-    first = rnd(lt + ct).to(F32)
-    return rnd(rnd(first + ft), dtype)
+    local_twice = rnd(2.0 * local.to(F32), arith).to(F32)
+    coarse_scaled = rnd(gain * coarse.to(F32), arith).to(F32)
+    fine_scaled = rnd(gain * fine.to(F32), arith).to(F32)
+    lt = rnd(rl * local_twice, arith).to(F32)
+    ct = rnd(rc * coarse_scaled, arith).to(F32)
+    ft = rnd(rf * fine_scaled, arith).to(F32)
+    first = rnd(lt + ct, arith).to(F32)
+    return rnd(rnd(first + ft, arith), dtype)
 
 
 # ----------------------------------------------------------------------------
@@ -753,7 +756,8 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
             coarse = torch.zeros_like(fine)
         if coarse_on or fine_on:
             out[:, start:end] = fusion(raw_q[:, start:end], local[:, start:end], coarse,
-                                       fine, fusion_a, fusion_b, alpha, coarse_on, fine_on)
+                                       fine, fusion_a, fusion_b, alpha, coarse_on, fine_on,
+                                       arith=raw_q.dtype)
     return (out, routes) if return_routes else out
 
 

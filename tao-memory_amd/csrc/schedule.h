@@ -9,6 +9,14 @@
 
 #include "../../include/tao_memory.h"
 
+// The route-size closed forms also run on the device (the fp32 full-sequence
+// read derives each tile's counts in its kernel).
+#if defined(__HIPCC__)
+#define TAO_SCHED __host__ __device__ inline
+#else
+#define TAO_SCHED inline
+#endif
+
 namespace tao {
 namespace sched {
 
@@ -44,7 +52,7 @@ inline int64_t next_turn(const tao_stream_cfg& c, int64_t p) {
 }
 
 // budget(n) = min(n, ceil(sqrt(scale * n)) + offset) (config.py:54-60).
-inline int64_t budget(const tao_stream_cfg& c, int64_t n) {
+TAO_SCHED int64_t budget(const tao_stream_cfg& c, int64_t n) {
   if (n <= 0) return 0;
   const int64_t target = (int64_t)c.budget_root_scale * n;
   int64_t r = 0;
@@ -55,8 +63,9 @@ inline int64_t budget(const tao_stream_cfg& c, int64_t n) {
 }
 
 // (coarse pages, eligible fines, selected M) of a route (tao_stream.py:29-37).
-inline void routed_counts(const tao_stream_cfg& c, int64_t completed, int64_t pending,
-                          int64_t* coarse_out, int64_t* eligible_out, int64_t* selected_out) {
+TAO_SCHED void routed_counts(const tao_stream_cfg& c, int64_t completed, int64_t pending,
+                             int64_t* coarse_out, int64_t* eligible_out,
+                             int64_t* selected_out) {
   const int64_t g = c.coarse_group;
   const int64_t cb = budget(c, g * completed);
   int64_t coarse = (2 * cb + g - 1) / g;

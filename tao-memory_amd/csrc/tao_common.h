@@ -77,6 +77,9 @@ TAO_DEV float log_bf(float x) {
 // Correctly rounded fp32 exp (fp64 evaluation).
 TAO_DEV float exp_cr(float x) { return (float)exp((double)x); }
 
+// Correctly rounded fp32 natural log (fp64 evaluation).
+TAO_DEV float log_cr(float x) { return (float)log((double)x); }
+
 // ---------------------------------------------------------------- wave ops
 TAO_DEV float wave_sum_fold(float v) {
 #pragma unroll

@@ -149,6 +149,36 @@ int decode_record(const tao_state_dev* st, const tao_tokens* tok, const tao_fusi
 int decode_replay(const DecodeParams& rec, const tao_tokens* tok, int head_dim,
                   int32_t selected, long long position, void* stream);
 
+// fp32 full-sequence read (full_f32.hip): operand views in fp32 elements,
+// the call's workspace carved by f32_layout.
+struct F32View {
+  const float* p;
+  int64_t sb, st, sh;
+};
+
+struct F32Params {
+  F32View q, k, v, rq, rk;
+  const void* fa; const void* fb; int f_dtype;
+  int64_t fa_s[3], fb_s[3];
+  float gain;
+  float* out; int64_t out_sb, out_st, out_sh;
+  float* local;    // [B, T, H, D]
+  float* fine_z;   // [B, H, S, D]
+  float* bank;     // [B, H, S, D, D], C[d][e]
+  float* pz;       // [B, H, P8, 8, D]: logsumexp of each page's first n fines
+  float* swt;      // [B, H, P8, 36, D]: segment weights under each prefix
+  float* pc;       // [B, H, Pc, D, D] completed pages' value matrices, or null
+  int32_t* sel_out;   // optional [B, T, H, sel_cap] selections (score order, -1 pad)
+  int sel_cap;
+  tao_stream_cfg cfg;
+  int B, H, D, T, S, P8, Pc, coarse_values;
+};
+size_t f32_workspace_floats(int B, int H, int D, int64_t T, int coarse_values);
+int f32_layout(F32Params& p, float* ws, int64_t T, int coarse_values);
+// 1 when T fits the read kernel's LDS tables (pages, candidates, selections).
+int f32_limits(const tao_stream_cfg& cfg, int64_t T, int64_t* pages, int64_t* cand);
+hipError_t launch_full_f32(const F32Params& p, hipStream_t s);
+
 struct StageParams {
   TokView src[5];
   bf16_t* dst;          // 5 x [B, H, D] contiguous

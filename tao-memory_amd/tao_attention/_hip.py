@@ -142,6 +142,10 @@ _SIGNATURES = {
     "tao_graph_launch": ([_vp, ctypes.POINTER(Tokens), _vp], _i32),
     "tao_graph_destroy": ([_vp], _i32),
     "tao_numerics_selftest": ([_i32, _vp, _vp, _i64, _vp], _i32),
+    "tao_full_sequence_f32_workspace_bytes": ([_i32, _i32, _i32, _i64, _i32], _sz),
+    "tao_full_sequence_f32": ([ctypes.POINTER(StreamCfg), ctypes.POINTER(Tokens),
+                               ctypes.POINTER(Fusion), _i32, _i32, _i32, _i32, _vp,
+                               ctypes.POINTER(_i64), _vp, _i32, _vp, _sz, _vp], _i32),
     "tao_batch_table_bytes": ([_i32], _sz),
     "tao_batch_open": ([ctypes.POINTER(_vp), _i32, _vp, _sz, _vp, ctypes.POINTER(_vp)], _i32),
     "tao_batch_sync": ([_vp, _vp], _i32),

@@ -20,7 +20,9 @@ def tao_attention(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b, alpha,
                   config=DEFAULT_CONFIG, local_flash=None):
     """Full sequence read with fresh routing at every query (operator.py:40-52).
 
-    Forward and backward on the HIP library (training.py). A caller
+    Forward and backward on the HIP library (training.py) for bf16
+    operands; fp32 operands take the forward-only fp32 read
+    (training.forward_f32: every rounding point at fp32). A caller
     local_flash plugin computes the local attention with the reference's
     tiling (tao_stream.py:760-787) and is differentiated by autograd; the
     rest stays on the HIP path.

@@ -34,7 +34,7 @@ from .config import TaoConfig
 _VALUE_WRITERS = ("softmax", "regularized_association")
 
 
-def _check(q, k, v, raw_q, raw_k, config):
+def _check(q, k, v, raw_q, raw_k, config, dtype=torch.bfloat16):
     if config.fine_writer not in _VALUE_WRITERS:
         raise NotImplementedError(
             f"the HIP full-sequence read implements the fine writers {_VALUE_WRITERS}")
@@ -44,8 +44,8 @@ def _check(q, k, v, raw_q, raw_k, config):
     shape = q.shape
     if q.dim() != 4 or any(t.shape != shape for t in (k, v, raw_q, raw_k)):
         raise ValueError("q, k, v, raw_q and raw_k must share one [B, T, H, D] shape")
-    if any(t.dtype != torch.bfloat16 for t in (q, k, v, raw_q, raw_k)):
-        raise TypeError("the HIP path computes on bf16 operands")
+    if any(t.dtype != dtype for t in (q, k, v, raw_q, raw_k)):
+        raise TypeError("the HIP full-sequence read takes five bf16 or five fp32 operands")
     if shape[-1] not in (64, 128):
         raise ValueError("head width must be 64 or 128")
     for t in (q, k, v, raw_q, raw_k):
@@ -205,6 +205,55 @@ def forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_rou
     if return_routes:
         return out, None if ws.qsel is None else ws.qsel.clone()
     return out
+
+
+def forward_f32(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_routes=False):
+    """tao_attention on fp32 operands (tao_full_sequence_f32), forward only.
+
+    The reference's torch operations follow the operand dtype
+    (operator.py:21-39, tao_stream.py:668-757); here every rounding point of
+    the bf16 contract rounds to fp32, with the routing sums in the bf16
+    path's orders, so routes are reproducible bit for bit and the output is
+    within 1e-4 of exact arithmetic. Returns fp32 [B, T, H, D] and, with
+    return_routes, each query's selected fine ids in score order (int32
+    [B, T, H, M_max], -1 padded)."""
+    if config.fine_writer != "softmax":
+        raise NotImplementedError("the fp32 full-sequence read implements the softmax writer")
+    _check(q, k, v, raw_q, raw_k, config, dtype=torch.float32)
+    b, tokens, heads, d = q.shape
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    sel = None
+    if return_routes:
+        # The last tile's route is the largest (routed counts grow with the
+        # visible fines).
+        from . import schedule
+        tiles = -(-tokens // config.fine_tokens)
+        vmax = max(0, tiles - 1 - config.visibility_tiles)
+        group = config.coarse_group
+        m = schedule.routed_counts(vmax // group, vmax % group, config)[2] if vmax else 1
+        sel = torch.empty((b, tokens, heads, max(1, m)), dtype=torch.int32, device=q.device)
+    if tokens == 0:
+        return (out, sel) if return_routes else out
+    ops = tuple(t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v, raw_q, raw_k))
+    coarse = int(not config.coarse_index_only)
+    lib = _hip.lib()
+    nbytes = lib.tao_full_sequence_f32_workspace_bytes(b, heads, d, tokens, coarse)
+    scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    tok = _hip.tokens(*ops)
+    fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
+    fu32 = _hip.Fusion.from_buffer_copy(fu)
+    # gain = torch.full((), 2 * alpha, dtype=float32) (operator.py:34)
+    fu32.gain = float(torch.full((), 2 * float(alpha), dtype=torch.float32))
+    scfg = _hip.StreamCfg(0, config.local_keep, config.fine_tokens, config.coarse_group,
+                          config.route_period, config.layer_stagger,
+                          config.budget_root_scale, config.budget_offset, 0)
+    out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
+    _hip.check(lib.tao_full_sequence_f32(
+        ctypes.byref(scfg), ctypes.byref(tok), ctypes.byref(fu32), b, heads, d, coarse,
+        out.data_ptr(), out_s, None if sel is None else sel.data_ptr(),
+        0 if sel is None else sel.shape[-1], scratch.data_ptr(), nbytes,
+        _hip.stream_ptr(q.device)))
+    return (out, sel) if return_routes else out
 
 
 def _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config,
@@ -388,6 +437,14 @@ def full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
     tensors = (q, k, v, raw_q, raw_k, fusion_a, fusion_b)
     alpha_grad = torch.is_tensor(alpha) and alpha.requires_grad
     grad = torch.is_grad_enabled() and (alpha_grad or any(t.requires_grad for t in tensors))
+    if q.dtype == torch.float32:
+        if local_flash is not None:
+            raise NotImplementedError("a local_flash plugin with fp32 operands")
+        if grad:
+            raise NotImplementedError(
+                "the fp32 full-sequence read is forward-only: run it under torch.no_grad() "
+                "or on bf16 operands for gradients")
+        return forward_f32(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config)
     if local_flash is not None:
         from .flash_attention import plugin_training_local
         _check(q, k, v, raw_q, raw_k, config)

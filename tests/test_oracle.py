@@ -549,3 +549,27 @@ def test_training_smooth_forward_is_the_rounded_forward(index_only, tokens):
     grads = torch.autograd.grad(smooth.square().sum(), leaves + [fa64, fb64])
     for gr in grads:
         assert torch.isfinite(gr).all() and gr.abs().sum() > 0
+
+
+@pytest.mark.parametrize("tokens,index_only", [(1300, True), (2900, False)])
+def test_training_forward_fp32_matches_fp64_at_its_routes(tokens, index_only):
+    """The fp32 semantics of tao_attention (every rounding point at fp32):
+    training_forward on fp32 operands agrees with the independent fp64
+    evaluation training_forward_smooth at the fp32 forward's own routes to
+    fp32 accuracy (1e-5), pages, coarse read and both fusion biases
+    included; and the bf16 and fp32 runs of the same inputs differ by bf16
+    rounding only. A dropped term, a wrong index or a bf16 rounding left in
+    the fp32 path would exceed 1e-5."""
+    g = O.Geometry(coarse_index_only=index_only)
+    gen = torch.Generator().manual_seed(5)
+    h, d = 2, 16
+    xs = [torch.randn(1, tokens, h, d, generator=gen) for _ in range(5)]
+    fa = torch.randn(h, d, 3, generator=gen) * 0.02
+    fb = torch.randn(h, d, 3, generator=gen) * 0.02
+    out, routes = O.training_forward(*xs, fa, fb, 0.5, g, return_routes=True)
+    assert out.dtype == torch.float32
+    smooth = O.training_forward_smooth(*(x.double() for x in xs), fa.double(), fb.double(), 0.5,
+                                       routes, g)
+    assert (out.double() - smooth).abs().max() < 1e-5
+    low = O.training_forward(*(x.to(torch.bfloat16) for x in xs), fa, fb, 0.5, g)
+    assert (low.double() - smooth).abs().max() > 1e-3

@@ -148,7 +148,9 @@ int tao_fold_coarse(const tao_state_dev* st, int32_t completed, void* stream);
  * ring, reads the folded route (fold_g / fold_den, see tao_fold_route) when
  * `selected` > 0 (0 before the first seal: output = local attention),
  * adds the folded coarse read (coarse_g) when fu->coarse_on, writes out
- * [B,1,H,D] (element strides out_s) and advances header[0]. */
+ * [B,1,H,D] (element strides out_s) and advances header[0]. One launch: its
+ * workgroups meet on arrival counters in the workspace, which
+ * tao_workspace_init zeroes and every step leaves at zero. */
 int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok,
                     const tao_fusion* fu, int32_t selected, void* out,
                     const int64_t* out_s, void* stream);
@@ -156,12 +158,15 @@ int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok,
 /* tao_decode_step without allocation: no reference counterpart. For callers
  * that cannot allocate device memory (code under hipGraph capture, tight
  * serving loops, harnesses that forbid hipMalloc): the same decode step,
- * arguments and results as tao_decode_step, with the step's records in a
- * 4 MiB library-owned static device array instead of st->workspace (which
- * may be null). Limit: batch * heads <= 567 at head_dim 128, <= 593 at 64
- * (TAO_E_CAPACITY beyond). Allocates nothing. Every call on one device
- * shares the array: calls that overlap on one device race and must be
- * serialised by the caller; no state needs clearing between calls. */
+ * arguments and results as tao_decode_step, with the step's records and
+ * arrival counters in library-owned static device arrays (4 MiB, and 1024
+ * counters on 128-byte lines) instead of st->workspace (which may be null).
+ * Limit:
+ * batch * heads <= 567 at head_dim 128, <= 593 at 64 (TAO_E_CAPACITY
+ * beyond). Allocates nothing. Every call on one device shares the arrays:
+ * calls that overlap on one device race and must be serialised by the
+ * caller; each step leaves its counters at zero, so nothing needs clearing
+ * between calls. */
 int tao_decode_step_noalloc(const tao_state_dev* st, const tao_tokens* tok,
                             const tao_fusion* fu, int32_t selected, void* out,
                             const int64_t* out_s, void* stream);

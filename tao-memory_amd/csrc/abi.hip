@@ -111,6 +111,12 @@ tao::DecodeParams decode_params(const tao_state_dev* st, const tao_tokens* tok,
   p.out_sb = out_s[0];
   p.out_sh = out_s[2];
   p.parts = st->workspace ? parts_of(st) : nullptr;
+  p.counters = nullptr;
+  if (st->workspace) {
+    const tao::WorkspaceLayout lay =
+        tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
+    p.counters = (unsigned*)((char*)st->workspace + lay.count_off);
+  }
   p.fold_g = (const float*)st->fold_g;
   p.fold_den = (const float*)st->fold_den;
   p.coarse_g = (const float*)st->coarse_g;
@@ -234,7 +240,9 @@ WorkspaceLayout workspace_layout(int batch, int heads, int head_dim, int sel_cap
   const size_t bh = (size_t)batch * heads;
   lay.parts_off = 0;
   const size_t parts = bh * step_floats(head_dim, sel_cap) * sizeof(float);
-  lay.plan_off = align(parts);
+  lay.count_off = align(parts);
+  lay.plan_off =
+      align(lay.count_off + step_counters(batch, heads) * kCounterStride * sizeof(unsigned));
   lay.plan_words = plan_words > 0 ? (size_t)plan_words : 0;
   lay.total = align(lay.plan_off + lay.plan_words * sizeof(int64_t));
   return lay;
@@ -242,7 +250,9 @@ WorkspaceLayout workspace_layout(int batch, int heads, int head_dim, int sel_cap
 
 int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
                    int32_t selected, void* out, const int64_t* out_s, void* stream,
-                   long long position, float* records) {
+                   long long position, float* records, unsigned* counters) {
+  if ((records == nullptr) != (counters == nullptr))
+    return fail(TAO_E_ARGUMENT, "decode step: records and counters go together");
   int rc = check_state(st, records == nullptr);
   if (!rc) rc = check_tokens(tok);
   if (!rc) rc = check_fusion(fu);
@@ -254,7 +264,10 @@ int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fus
     return fail(TAO_E_ARGUMENT, "coarse_on needs a state with the coarse value branch");
   tao::DecodeParams p = decode_params(st, tok, fu, out, out_s);
   p.pos_hint = position;
-  if (records) p.parts = records;
+  if (records) {
+    p.parts = records;
+    p.counters = counters;
+  }
   return check_hip(tao::launch_decode_step(p, st->head_dim, selected, (hipStream_t)stream),
                    "tao_decode_step");
 }

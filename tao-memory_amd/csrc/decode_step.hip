@@ -1,11 +1,11 @@
 // Fused single-token decode step for gfx950, and the route fold it reads.
 //
-// Two launches per new token (replace, per request x layer, the reference's
+// One launch per new token (replaces, per request x layer, the reference's
 // q1 page-memo region tao_stream.py:418-433 + query_fresh_fine.py:8-75, the
 // local SDPA flash_attention.py:25-29 over torch.cat'ed K/V
 // tao_stream.py:927-930, and the fusion kernels fusion_pointwise.py:10-117):
 //
-// decode_units_kernel: per (batch, head) local_units(D) local-attention
+// decode_step_kernel: per (batch, head) local_units(D) local-attention
 //   workgroups and fine_units(D) fine-read workgroups.
 //   local workgroup j takes keys [j*K, (j+1)*K) (K = local_keys(D)) of the
 //   exact window (K and V rows from the ring, or the new token), scores
@@ -18,11 +18,12 @@
 //   num[e] = h . G^T[e], and den = r(h . g) (h = r(softmax_D(raw_q)));
 //   with the coarse value branch on, fine_units(D) more workgroups read 32
 //   rows each of the folded coarse matrix the same way (coarse.hip).
-// decode_combine_kernel: one workgroup per (batch, head, 32 channels):
-//   merges the local records in a fixed order, fine = r(r(num) / den),
-//   coarse = r(h . Gc^T[e]), applies the fusion epilogue and advances
-//   header[0] (the stream position), so the pair can be replayed from a
-//   hipGraph.
+//   Every workgroup publishes its record with device-coherent stores and
+//   counts itself in on its head's arrival counter; the head's last
+//   workgroup merges the local records in a fixed order,
+//   fine = r(r(num) / den), coarse = r(h . Gc^T[e]), applies the fusion
+//   epilogue for all D channels; the last head advances header[0] (the
+//   cursor graph replays read).
 //
 // fold_kernel (per route refresh and per seal, not per token): the q1 read
 // is linear in ch_m = h * w_m with w_m = pw[page(m)] * sw[m] independent of
@@ -33,9 +34,9 @@
 // (query_fresh_fine.py:38-40, 47-48, 67); the fold keeps w and the sums in
 // fp32, which moves the fine read by well under one bf16 ulp of its inputs.
 //
-// The kernel boundary publishes the records across the eight XCD L2 caches:
-// a device-scope release fence per workgroup (last-block combine) costs far
-// more than the second launch on this part.
+// The records cross the eight XCD L2 caches as agent-scope stores and loads
+// (coherent without an L2 write-back); a device-scope release fence per
+// workgroup would cost more than a second launch on this part.
 #include "tao_launch.h"
 #include "tao_common.h"
 #include "tao_fusion.h"
@@ -139,7 +140,7 @@ __device__ void fine_read(const bf16_t* rq, int f, float* frec, float* hq, const
     }
     if (with_den) {
       dsum = wave_sum_fold(dsum);
-      if (tid == 0) frec[0] = rbf(dsum);
+      if (tid == 0) st_agent(&frec[0], rbf(dsum));
     }
   }
   __syncthreads();
@@ -149,7 +150,7 @@ __device__ void fine_read(const bf16_t* rq, int f, float* frec, float* hq, const
   acc += __shfl_xor(acc, 1, 64);
   acc += __shfl_xor(acc, 2, 64);
   acc += __shfl_xor(acc, 4, 64);
-  if (part == 0) frec[kStepRec + e] = acc;
+  if (part == 0) st_agent(&frec[kStepRec + e], acc);
 }
 
 // Workgroup j of one (request, head): j < NLOC local attention over keys
@@ -182,7 +183,7 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
   const int first_slot = (int)((position - n_old) % L);
   const int k0 = j * G::KEYS;
   if (k0 >= n) {   // past the window: an empty record
-    if (tid == 0) { rec[0] = -__builtin_inff(); rec[1] = 0.0f; }
+    if (tid == 0) { st_agent(&rec[0], -__builtin_inff()); st_agent(&rec[1], 0.0f); }
     return;
   }
   // Issue every load first: KPT key and value rows, the q chunk.
@@ -265,7 +266,7 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
     float s = 0.0f;
 #pragma unroll
     for (int rr = 0; rr < G::ROWS; ++rr) s += sm.red[rr][tid];
-    rec[kStepRec + tid] = s;
+    st_agent(&rec[kStepRec + tid], s);
   }
   if (tid < 64) {
     const float x = tid < G::ROWS && sm.rl[tid] > 0.0f
@@ -273,22 +274,22 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
                         : 0.0f;
     const float lsum = wave_fold_sum(x);
     if (tid == 0) {
-      rec[0] = top;
-      rec[1] = lsum;
+      st_agent(&rec[0], top);
+      st_agent(&rec[1], lsum);
     }
   }
 }
 
-// Kernel A: per (batch, head) NLOC local-attention workgroups (the window
-// split by keys), NFINE fine-read workgroups and, with coarse_on, NFINE
-// coarse-read workgroups; no cross-workgroup communication.
+// The units of one launch: per (batch, head) NLOC local-attention
+// workgroups (the window split by keys), NFINE fine-read workgroups and,
+// with coarse_on, NFINE coarse-read workgroups. Returns the (batch, head).
 template <int D>
-__global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, int M) {
+__device__ int decode_units(const DecodeParams& p, int M) {
   using G = Geo<D>;
   __shared__ StepSmem<D> sm;
   const int per_head = G::NLOC + G::NFINE * (p.coarse_on ? 2 : 1);
-  const int bh = blockIdx.x / per_head;
-  const int j = blockIdx.x % per_head;
+  int bh, j;
+  xcd_unit(blockIdx.x, p.B * p.H, per_head, bh, j);
   const int b = bh / p.H, h = bh % p.H;
   StepReq q;
   q.q = p.q.p + b * p.q.sb + h * p.q.sh;
@@ -307,14 +308,15 @@ __global__ __launch_bounds__(kThreads) void decode_units_kernel(DecodeParams p, 
   q.recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
   q.position = p.pos_hint >= 0 ? p.pos_hint : p.header[0];
   units_body<D>(q, j, M, p.coarse_on, p.keep, p.fine, p.H * D, sm);
+  return bh;
 }
 
-// Kernel B: one 256-thread workgroup per (batch, head, 32 channels). Thread
-// group g = tid / 32 owns local records j = g (mod 8), channel dc = tid % 32;
-// the groups merge in ascending g (fixed order), then the fine and coarse
-// records and the fusion epilogue give the output.
+// The merge: thread group g = tid / COLS owns local records j = g
+// (mod 256 / COLS), channel dc = tid % COLS; the groups merge in ascending g
+// (fixed order), then the fine and coarse records and the fusion epilogue
+// give the output. The batched step runs it as its own kernel, one
+// workgroup per (request, head, kCombineCols channels).
 constexpr int kCombineCols = 32;
-constexpr int kCombineGroups = kThreads / kCombineCols;
 
 struct CombineArgs {
   const void* fa; const void* fb; int f_dtype;
@@ -322,34 +324,40 @@ struct CombineArgs {
   float gain;
 };
 
-template <int D>
+// COLS channels (from chunk * COLS) of one (request, head): G = 256 / COLS
+// thread groups share the local records. AGENT: the records were published
+// by other workgroups of the same launch (device-coherent loads).
+template <int D, int COLS, bool AGENT>
 __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, int h, int chunk,
                              int M, int coarse_on, const CombineArgs& c) {
   using Gm = Geo<D>;
-  constexpr int STRIDE = D + kStepRec, G = kCombineGroups;
+  constexpr int STRIDE = D + kStepRec, G = kThreads / COLS;
   constexpr int NLOC = Gm::NLOC, LPG = (NLOC + G - 1) / G;
   __shared__ float ml[NLOC][2];
-  __shared__ float part_loc[G][kCombineCols];
-  const int tid = threadIdx.x, dc = tid % kCombineCols, g = tid / kCombineCols;
-  const int d = chunk * kCombineCols + dc;
+  __shared__ float part_loc[G][COLS];
+  const int tid = threadIdx.x, dc = tid % COLS, g = tid / COLS;
+  const int d = chunk * COLS + dc;
+  auto ld = [](const float* x) __attribute__((always_inline)) {
+    return AGENT ? ld_agent(x) : *x;
+  };
 
   // Loads first: local records, the fine and coarse records, fusion operands.
   float m_g[LPG], l_g[LPG], o_g[LPG];
 #pragma unroll
   for (int i = 0; i < LPG; ++i) {
     const int j = g + i * G;
-    m_g[i] = j < NLOC ? recs[j * STRIDE] : -__builtin_inff();
-    l_g[i] = j < NLOC ? recs[j * STRIDE + 1] : 0.0f;
-    o_g[i] = j < NLOC ? recs[j * STRIDE + kStepRec + d] : 0.0f;
+    m_g[i] = j < NLOC ? ld(recs + j * STRIDE) : -__builtin_inff();
+    l_g[i] = j < NLOC ? ld(recs + j * STRIDE + 1) : 0.0f;
+    o_g[i] = j < NLOC ? ld(recs + j * STRIDE + kStepRec + d) : 0.0f;
   }
   float q = 0.0f, num = 0.0f, den = 1.0f, craw = 0.0f, a[3], bb[3];
   if (g == 0) {
     q = bf2f(rq[d]);
     if (M > 0) {
-      den = recs[NLOC * STRIDE];
-      num = recs[NLOC * STRIDE + kStepRec + d];
+      den = ld(recs + NLOC * STRIDE);
+      num = ld(recs + NLOC * STRIDE + kStepRec + d);
     }
-    if (coarse_on) craw = recs[(NLOC + 1) * STRIDE + kStepRec + d];
+    if (coarse_on) craw = ld(recs + (NLOC + 1) * STRIDE + kStepRec + d);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       a[i] = load_param(c.fa, c.f_dtype, h * c.fa_s[0] + d * c.fa_s[1] + i * c.fa_s[2]);
@@ -394,18 +402,42 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
   }
 }
 
+// The single-launch step: the units of every (batch, head) publish their
+// records with device-coherent stores, wait for them to complete and count
+// themselves in on the head's arrival counter; the head's last workgroup
+// merges the records and applies the fusion for all D channels. The
+// counters (p.counters: one per head, one for the launch) start at zero and
+// are reset by their last arrival, so every step starts from zero. The head that completes last advances the cursor in header[0].
 template <int D>
-__global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p, int M) {
-  constexpr int CHUNKS = D / kCombineCols;
-  const int bh = blockIdx.x / CHUNKS;
-  const int chunk = blockIdx.x % CHUNKS;
+__global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, int M) {
+  __shared__ int last;
+  const int per_head = Geo<D>::NLOC + Geo<D>::NFINE * (p.coarse_on ? 2 : 1);
+  const int bh = decode_units<D>(p, M);
+  float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
+  unsigned* head_count = p.counters + (size_t)bh * kCounterStride;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // this thread's stores done
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(head_count, 1u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) == (unsigned)per_head - 1u;
+  __syncthreads();
+  if (!last) return;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(head_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int b = bh / p.H, h = bh % p.H;
   const CombineArgs c = {p.fa, p.fb, p.f_dtype, p.fa_s, p.fb_s, p.gain};
-  combine_body<D>(p.parts + (size_t)bh * step_floats(D, p.sel_cap),
-                  p.rq.p + b * p.rq.sb + h * p.rq.sh, p.out + b * p.out_sb + h * p.out_sh, h,
-                  chunk, M, p.coarse_on, c);
-  // Kernel A of this step has finished reading the position: advance it.
-  if (blockIdx.x == 0 && threadIdx.x == 0) p.header[0] = p.header[0] + 1;
+  combine_body<D, D, true>(recs, p.rq.p + b * p.rq.sb + h * p.rq.sh,
+                           p.out + b * p.out_sb + h * p.out_sh, h, 0, M, p.coarse_on, c);
+  if (threadIdx.x == 0) {
+    // The stream position advances once per step (graph replays read it);
+    // every workgroup of the launch read the cursor before it arrived.
+    unsigned* all_count = p.counters + (size_t)p.B * p.H * kCounterStride;
+    if (__hip_atomic_fetch_add(all_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        (unsigned)(p.B * p.H) - 1u) {
+      __hip_atomic_store(all_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      p.header[0] = p.header[0] + 1;
+    }
+  }
 }
 
 // Batched step over R requests (one state each, batch 1): request r's token
@@ -419,8 +451,8 @@ __global__ __launch_bounds__(kThreads) void batch_units_kernel(BatchStepParams p
   using G = Geo<D>;
   __shared__ StepSmem<D> sm;
   const int per_head = G::NLOC + G::NFINE * (p.coarse_values ? 2 : 1);
-  const int rh = blockIdx.x / per_head;
-  const int j = blockIdx.x % per_head;
+  int rh, j;
+  xcd_unit(blockIdx.x, p.R * p.H, per_head, rh, j);
   const int r = rh / p.H, h = rh % p.H;
   const BatchReq& t = p.table[r];
   StepReq q;
@@ -450,16 +482,17 @@ __global__ __launch_bounds__(kThreads) void batch_units_kernel(BatchStepParams p
 template <int D>
 __global__ __launch_bounds__(kThreads) void batch_combine_kernel(BatchStepParams p) {
   constexpr int CHUNKS = D / kCombineCols;
-  const int rh = blockIdx.x / CHUNKS;
-  const int chunk = blockIdx.x % CHUNKS;
+  int rh, chunk;
+  xcd_unit(blockIdx.x, p.R * p.H, CHUNKS, rh, chunk);
   const int r = rh / p.H, h = rh % p.H;
   const BatchReq& t = p.table[r];
   const float* recs = t.parts + (size_t)h * step_floats(D, 0);
   const int M = (int)recs[2];
   const int coarse_on = recs[3] != 0.0f;
   const CombineArgs c = {p.fa, p.fb, p.f_dtype, p.fa_s, p.fb_s, p.gain};
-  combine_body<D>(recs, p.rq.p + r * p.rq.sb + h * p.rq.sh, p.out + r * p.out_sb + h * p.out_sh,
-                  h, chunk, M, coarse_on, c);
+  combine_body<D, kCombineCols, false>(recs, p.rq.p + r * p.rq.sb + h * p.rq.sh,
+                                       p.out + r * p.out_sb + h * p.out_sh, h, chunk, M,
+                                       coarse_on, c);
   if (h == 0 && chunk == 0 && threadIdx.x == 0) t.header[0] = t.header[0] + 1;
 }
 
@@ -477,8 +510,9 @@ __global__ __launch_bounds__(kThreads) void fold_kernel(FoldParams p) {
   constexpr int WPT = (U * CH + kThreads - 1) / kThreads;   // weight chunks per thread
   __shared__ float wts[U][D];
   __shared__ int ids[U];
-  const int bh = blockIdx.x / CHUNKS;
-  const int e0 = (blockIdx.x % CHUNKS) * ROWS;
+  int bh, e_chunk;
+  xcd_unit(blockIdx.x, p.B * p.H, CHUNKS, bh, e_chunk);
+  const int e0 = e_chunk * ROWS;
   const int tid = threadIdx.x, c = tid % CH, r = tid / CH;
   const int e = e0 + r;
   const int32_t* sel = p.sel + (size_t)bh * p.sel_cap;
@@ -588,15 +622,13 @@ hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStr
   if (M < 0 || M > p.sel_cap) return hipErrorInvalidValue;
   if (p.keep + p.fine > kMaxWindow) return hipErrorInvalidValue;
   if (p.coarse_on && !p.coarse_g) return hipErrorInvalidValue;
+  if (!p.parts || !p.counters) return hipErrorInvalidValue;
   const int per_head = local_units(head_dim) + fine_units(head_dim) * (p.coarse_on ? 2 : 1);
   const dim3 units((unsigned)(p.B * p.H * per_head));
-  const dim3 cols((unsigned)(p.B * p.H * (head_dim / kCombineCols)));
   if (head_dim == 128) {
-    hipLaunchKernelGGL(decode_units_kernel<128>, units, dim3(kThreads), 0, s, p, M);
-    hipLaunchKernelGGL(decode_combine_kernel<128>, cols, dim3(kThreads), 0, s, p, M);
+    hipLaunchKernelGGL(decode_step_kernel<128>, units, dim3(kThreads), 0, s, p, M);
   } else if (head_dim == 64) {
-    hipLaunchKernelGGL(decode_units_kernel<64>, units, dim3(kThreads), 0, s, p, M);
-    hipLaunchKernelGGL(decode_combine_kernel<64>, cols, dim3(kThreads), 0, s, p, M);
+    hipLaunchKernelGGL(decode_step_kernel<64>, units, dim3(kThreads), 0, s, p, M);
   } else {
     return hipErrorInvalidValue;
   }

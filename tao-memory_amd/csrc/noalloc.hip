@@ -1,19 +1,20 @@
 // tao_decode_step_noalloc: the single-token decode step for callers that
 // cannot allocate device memory (code under graph capture, tight serving
-// loops, harnesses that forbid hipMalloc). It runs the same two kernels as
-// tao_decode_step; only the step's per-head records move from the state's
-// workspace into a file-scope device array of fixed size, so the caller's
-// state needs no workspace at all.
+// loops, harnesses that forbid hipMalloc). It runs the same kernel as
+// tao_decode_step; only the step's per-head records and its arrival
+// counters move from the state's workspace into two file-scope device
+// arrays of fixed size, so the caller's state needs no workspace at all.
 //
-// The array holds kScratchBytes per device for the life of the process. Its
-// address is resolved once per device with hipGetSymbolAddress (with that
-// device current) and kept; host code passes that address, never the
-// array's name, to the kernels. Every call on one device shares the array:
-// calls that overlap on one device (two streams, two host threads) race and
-// must be serialised by the caller. Nothing in it must start at zero: each
-// step writes every record it reads (an empty local record carries l = 0,
-// and the combine ignores its values), so the last call's contents are
-// harmless.
+// The arrays hold kScratchBytes and kMaxCounters counters per device for the
+// life of the process. Their addresses are resolved once per device with
+// hipGetSymbolAddress (with that device current) and kept; host code passes
+// those addresses, never the arrays' names, to the kernel. Every call on one
+// device shares them: calls that overlap on one device (two streams, two
+// host threads) race and must be serialised by the caller. The records need
+// no initial value (each step writes every record it reads; an empty local
+// record carries l = 0). The counters must be zero between steps: device
+// arrays start zeroed when the library loads, and every step's last arrival
+// resets each counter it used.
 #include <mutex>
 #include <string>
 
@@ -22,20 +23,24 @@
 namespace {
 
 constexpr size_t kScratchBytes = size_t(4) << 20;   // 4 MiB per device
+constexpr int kMaxCounters = 1024;                   // heads + 1 per step
 constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+static __device__ __align__(256) unsigned scratch_counters[kMaxCounters * tao::kCounterStride];
 
 std::mutex g_scratch_lock;
 float* g_scratch[kMaxDevices] = {};
+unsigned* g_counters[kMaxDevices] = {};
 
 int fail(int code, const std::string& msg) {
   tao::set_error(msg.c_str());
   return code;
 }
 
-// The current device's copy of `scratch` (resolved on the first call there).
-int device_scratch(float** out) {
+// The current device's copies of `scratch` and `scratch_counters` (resolved
+// on the first call there).
+int device_scratch(float** out, unsigned** counters) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess)
@@ -51,9 +56,17 @@ int device_scratch(float** out) {
       return fail(e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol,
                   std::string("tao_decode_step_noalloc: hipGetSymbolAddress: ") +
                       hipGetErrorString(e));
+    void* cptr = nullptr;
+    e = hipGetSymbolAddress(&cptr, HIP_SYMBOL(scratch_counters));
+    if (e != hipSuccess || !cptr)
+      return fail(e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol,
+                  std::string("tao_decode_step_noalloc: hipGetSymbolAddress: ") +
+                      hipGetErrorString(e));
     g_scratch[dev] = (float*)ptr;
+    g_counters[dev] = (unsigned*)cptr;
   }
   *out = g_scratch[dev];
+  *counters = g_counters[dev];
   return TAO_OK;
 }
 
@@ -76,8 +89,12 @@ extern "C" int tao_decode_step_noalloc(const tao_state_dev* st, const tao_tokens
                     " needs " + std::to_string(need) + " bytes of step records, above the " +
                     std::to_string(kScratchBytes) +
                     "-byte static scratch (at most 567 heads at D128, 593 at D64)");
+  if (tao::step_counters(st->batch, st->heads) > (size_t)kMaxCounters)
+    return fail(TAO_E_CAPACITY, "tao_decode_step_noalloc: more heads than the static "
+                                "scratch counts");
   float* records = nullptr;
-  const int rc = device_scratch(&records);
+  unsigned* counters = nullptr;
+  const int rc = device_scratch(&records, &counters);
   if (rc) return rc;
-  return tao::decode_step_at(st, tok, fu, selected, out, out_s, stream, -1, records);
+  return tao::decode_step_at(st, tok, fu, selected, out, out_s, stream, -1, records, counters);
 }

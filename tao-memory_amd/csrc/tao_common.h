@@ -157,6 +157,35 @@ TAO_DEV float wave_fold_max(float v) {
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// Device-coherent (agent-scope) relaxed accesses: once a store made this way
+// has completed (s_waitcnt), an agent-scope load on any XCD returns it. The
+// single-launch decode step publishes its per-workgroup records with them,
+// so no L2 write-back fence is needed between its workgroups.
+TAO_DEV void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+TAO_DEV float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// XCD-affine workgroup numbering. The dispatcher hands workgroup i to XCD
+// i % 8 (round-robin over the eight XCDs); remapping i so that the `per`
+// workgroups of unit u (a batch-row x head) all get u % 8 keeps a head's
+// decode kernels, its route fold and its combine on one XCD, so the data one
+// kernel writes for a head (records, the folded route) and the ring window
+// it re-reads every step sit in that XCD's L2. Returns (u, j), j < per; a
+// bijection of [0, units * per). Units not a multiple of 8: plain order.
+TAO_DEV void xcd_unit(int i, int units, int per, int& u, int& j) {
+  if (units & 7) {
+    u = i / per;
+    j = i % per;
+    return;
+  }
+  const int n = i >> 3;
+  u = (i & 7) + 8 * (n / per);
+  j = n % per;
+}
+
 TAO_DEV float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

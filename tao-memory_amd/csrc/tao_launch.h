@@ -46,11 +46,22 @@ __host__ __device__ inline size_t step_floats(int head_dim, int sel_cap) {
 }
 
 // Workspace layout (bytes from the start of tao_state_dev::workspace):
-//   [0, plan_off)         fp32 decode scratch [B*H][step_floats(D, sel_cap)]
+//   [0, count_off)        fp32 decode scratch [B*H][step_floats(D, sel_cap)]
+//   [count_off, plan_off) uint32 arrival counters of the decode step: one per
+//                         (batch, head), then one for the launch, each on
+//                         its own 128-byte line (zero between steps)
 //   [plan_off, total)     int64 prefill plan (plan_words)
 struct WorkspaceLayout {
-  size_t parts_off, plan_off, plan_words, total;
+  size_t parts_off, count_off, plan_off, plan_words, total;
 };
+
+// Decode-step arrival counters for B*H heads, one per 128-byte line (the
+// heads' atomics never share a cache line): counter i at word
+// i * kCounterStride.
+constexpr int kCounterStride = 32;
+__host__ __device__ inline size_t step_counters(int batch, int heads) {
+  return (size_t)batch * heads + 1;
+}
 
 WorkspaceLayout workspace_layout(int batch, int heads, int head_dim, int sel_cap,
                                  int plan_words);
@@ -72,6 +83,8 @@ struct DecodeParams {
   float gain;
   bf16_t* out; int64_t out_sb, out_sh;
   float* parts;
+  unsigned* counters;   // step_counters(B, H) arrival counters, kCounterStride apart
+                        // (zero between steps)
   const float* fold_g; const float* fold_den;   // folded route (G^T, den weights)
   const float* coarse_g;   // folded coarse read (G^T), read when coarse_on
   long long pos_hint;   // cursor of this step, or -1: read header[0]
@@ -135,11 +148,13 @@ hipError_t launch_coarse_fold(const CoarseFoldParams& p, int head_dim, hipStream
 
 // tao_decode_step with the step's cursor given by the caller (position >= 0)
 // instead of read from header[0] on the device; used by the stream driver.
-// records: the step's per-head records (B * H * step_floats(D) floats), or
-// null for the state's workspace (then required).
+// records / counters: the step's per-head records (B * H * step_floats(D)
+// floats) and its step_counters(B, H) arrival counters, or both null for the
+// state's workspace (then required).
 int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,
                    int32_t selected, void* out, const int64_t* out_s, void* stream,
-                   long long position, float* records = nullptr);
+                   long long position, float* records = nullptr,
+                   unsigned* counters = nullptr);
 
 // The decode step's kernel arguments for a state, fusion and output buffer,
 // recorded once (decode_record) and dispatched per token with that token's

@@ -186,7 +186,16 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
     if (tid == 0) { st_agent(&rec[0], -__builtin_inff()); st_agent(&rec[1], 0.0f); }
     return;
   }
-  // Issue every load first: KPT key and value rows, the q chunk.
+  // Issue every load first: the new token's row for the ring append
+  // (workgroup 0), KPT key and value rows, the q chunk.
+  static_assert(D <= kThreads, "one append element per thread");
+  const bool appends = j == 0 && tid < D;
+  bf16_t app_k = 0, app_v = 0, app_r = 0;
+  if (appends) {
+    app_k = q.k[tid];
+    app_v = q.v[tid];
+    app_r = q.rk[tid];
+  }
   uint4 kraw[G::KPT], vraw[G::KPT];
 #pragma unroll
   for (int i = 0; i < G::KPT; ++i) {
@@ -205,17 +214,15 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
   }
   float qv[8];
   unpack8(*(const uint4*)(q.q + chn * 8), qv);
-  if (j == 0) {
+  if (appends) {
     // Append the new token at slot position % L. No key of this step's
     // window occupies that slot (window length n_old <= L - 1).
     int slot = first_slot + n_old;
     slot = slot >= L ? slot - L : slot;
     const size_t off = (size_t)slot * slot_stride;
-    for (int d = tid; d < D; d += kThreads) {
-      q.ring_k[off + d] = q.k[d];
-      q.ring_v[off + d] = q.v[d];
-      q.ring_raw[off + d] = q.rk[d];
-    }
+    q.ring_k[off + tid] = app_k;
+    q.ring_v[off + tid] = app_v;
+    q.ring_raw[off + tid] = app_r;
   }
   // Scores in log2 units (1/sqrt(D) and log2 e folded into one scale), each
   // reduced over its row's lanes; keys past the window score -inf.
@@ -324,12 +331,31 @@ struct CombineArgs {
   float gain;
 };
 
+// The fusion operands of channel d: the raw query element and the branch
+// parameters.
+struct FuseOps {
+  float q, a[3], b[3];
+};
+
+TAO_DEV FuseOps load_fuse_ops(const bf16_t* rq, int h, int d, const CombineArgs& c) {
+  FuseOps f;
+  f.q = bf2f(rq[d]);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    f.a[i] = load_param(c.fa, c.f_dtype, h * c.fa_s[0] + d * c.fa_s[1] + i * c.fa_s[2]);
+    f.b[i] = load_param(c.fb, c.f_dtype, h * c.fb_s[0] + d * c.fb_s[1] + i * c.fb_s[2]);
+  }
+  return f;
+}
+
 // COLS channels (from chunk * COLS) of one (request, head): G = 256 / COLS
 // thread groups share the local records. AGENT: the records were published
-// by other workgroups of the same launch (device-coherent loads).
+// by other workgroups of the same launch (device-coherent loads). pre: the
+// fusion operands of group 0's channel, loaded earlier (else loaded here).
 template <int D, int COLS, bool AGENT>
 __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, int h, int chunk,
-                             int M, int coarse_on, const CombineArgs& c) {
+                             int M, int coarse_on, const CombineArgs& c,
+                             const FuseOps* pre = nullptr) {
   using Gm = Geo<D>;
   constexpr int STRIDE = D + kStepRec, G = kThreads / COLS;
   constexpr int NLOC = Gm::NLOC, LPG = (NLOC + G - 1) / G;
@@ -350,19 +376,15 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
     l_g[i] = j < NLOC ? ld(recs + j * STRIDE + 1) : 0.0f;
     o_g[i] = j < NLOC ? ld(recs + j * STRIDE + kStepRec + d) : 0.0f;
   }
-  float q = 0.0f, num = 0.0f, den = 1.0f, craw = 0.0f, a[3], bb[3];
+  float num = 0.0f, den = 1.0f, craw = 0.0f;
+  FuseOps ops{};
   if (g == 0) {
-    q = bf2f(rq[d]);
     if (M > 0) {
       den = ld(recs + NLOC * STRIDE);
       num = ld(recs + NLOC * STRIDE + kStepRec + d);
     }
     if (coarse_on) craw = ld(recs + (NLOC + 1) * STRIDE + kStepRec + d);
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      a[i] = load_param(c.fa, c.f_dtype, h * c.fa_s[0] + d * c.fa_s[1] + i * c.fa_s[2]);
-      bb[i] = load_param(c.fb, c.f_dtype, h * c.fb_s[0] + d * c.fb_s[1] + i * c.fb_s[2]);
-    }
+    ops = pre ? *pre : load_fuse_ops(rq, h, d, c);
   }
   if (dc == 0) {
 #pragma unroll
@@ -393,8 +415,8 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
     bf16_t result;
     if (M > 0 || coarse_on) {
       const float fine_v = M > 0 ? rbf(rbf(num) / den) : 0.0f;
-      result = fuse_element(q, local, rbf(craw), fine_v, a, bb, c.gain, coarse_on ? 1 : 0,
-                            M > 0 ? 1 : 0);
+      result = fuse_element(ops.q, local, rbf(craw), fine_v, ops.a, ops.b, c.gain,
+                            coarse_on ? 1 : 0, M > 0 ? 1 : 0);
     } else {
       result = f2bf(local);
     }
@@ -412,6 +434,15 @@ template <int D>
 __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, int M) {
   __shared__ int last;
   const int per_head = Geo<D>::NLOC + Geo<D>::NFINE * (p.coarse_on ? 2 : 1);
+  // The fusion operands, in case this workgroup arrives last: loaded now so
+  // their latency overlaps the units' work.
+  int bh0, j0;
+  xcd_unit(blockIdx.x, p.B * p.H, per_head, bh0, j0);
+  const CombineArgs c = {p.fa, p.fb, p.f_dtype, p.fa_s, p.fb_s, p.gain};
+  FuseOps pre{};
+  if (threadIdx.x < D)
+    pre = load_fuse_ops(p.rq.p + (bh0 / p.H) * p.rq.sb + (bh0 % p.H) * p.rq.sh, bh0 % p.H,
+                        threadIdx.x, c);
   const int bh = decode_units<D>(p, M);
   float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
   unsigned* head_count = p.counters + (size_t)bh * kCounterStride;
@@ -425,9 +456,8 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, i
   if (threadIdx.x == 0)
     __hip_atomic_store(head_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int b = bh / p.H, h = bh % p.H;
-  const CombineArgs c = {p.fa, p.fb, p.f_dtype, p.fa_s, p.fb_s, p.gain};
   combine_body<D, D, true>(recs, p.rq.p + b * p.rq.sb + h * p.rq.sh,
-                           p.out + b * p.out_sb + h * p.out_sh, h, 0, M, p.coarse_on, c);
+                           p.out + b * p.out_sb + h * p.out_sh, h, 0, M, p.coarse_on, c, &pre);
   if (threadIdx.x == 0) {
     // The stream position advances once per step (graph replays read it);
     // every workgroup of the launch read the cursor before it arrived.

@@ -37,6 +37,8 @@
 // The records cross the eight XCD L2 caches as agent-scope stores and loads
 // (coherent without an L2 write-back); a device-scope release fence per
 // workgroup would cost more than a second launch on this part.
+#include <type_traits>
+
 #include "tao_launch.h"
 #include "tao_common.h"
 #include "tao_fusion.h"
@@ -91,14 +93,31 @@ struct StepReq {
   bf16_t* ring_k; bf16_t* ring_v; bf16_t* ring_raw;   // slot 0 of this (state row, head)
   const float* fold_g; const float* fold_den; const float* coarse_g;   // this head's
   float* recs;                                        // this (request, head)'s records
-  long long position;
+  int n_old, first_slot;   // window before the new token: keys in ring slots
+                           // first_slot, first_slot + 1, ... (mod keep + fine)
 };
+
+// The window of the step at `position` (local_len_at and its ring slots).
+// Positions below 2^31 take 32-bit arithmetic.
+TAO_DEV void step_window(long long position, int keep, int fine, int& n_old, int& first_slot) {
+  const int L = keep + fine;
+  if (position < 0x7FFFFFFFLL) {
+    const int pos = (int)position;
+    n_old = pos < L ? pos : keep + (pos - L) % fine;
+    first_slot = (pos - n_old) % L;
+  } else {
+    n_old = local_len_at(position, keep, fine);
+    first_slot = (int)((position - n_old) % L);
+  }
+}
 
 // Fine-read workgroup f: num[e] = h . G^T[e] for rows e in
 // [f * kFineRows, (f + 1) * kFineRows) of the folded matrix gmat (this
 // head's), thread (row tid / 8, part tid % 8); with gden (the fine read)
 // workgroup 0 also writes den = r(h . g). h = r(softmax_D(raw_q)) with the
-// exp correctly rounded in fp32.
+// exp correctly rounded in fp32. Wave 0 computes h on the bit-reversed
+// layout (lane L holds channels fold_lane(L) + 64 k), so its sums are the
+// fold order of the natural layout on DPP moves (no LDS round trips).
 template <int D>
 __device__ void fine_read(const bf16_t* rq, int f, float* frec, float* hq, const float* gmat,
                           const float* gden) {
@@ -114,32 +133,33 @@ __device__ void fine_read(const bf16_t* rq, int f, float* frec, float* hq, const
     gv[k] = v.x; gv[k + 1] = v.y; gv[k + 2] = v.z; gv[k + 3] = v.w;
   }
   if (tid < 64) {
+    const int c0 = fold_lane(tid);
     float xr[PER], gd[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-      xr[k] = bf2f(rq[tid + 64 * k]);
-      gd[k] = with_den ? gden[tid + 64 * k] : 0.0f;
+      xr[k] = bf2f(rq[c0 + 64 * k]);
+      gd[k] = with_den ? gden[c0 + 64 * k] : 0.0f;
     }
     float top = -__builtin_inff();
 #pragma unroll
     for (int k = 0; k < PER; ++k) top = fmaxf(top, xr[k]);
-    top = wave_max(top);
+    top = wave_fold_max(top);
     float ex[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) ex[k] = exp_cr(xr[k] - top);
     float s = ex[0];
 #pragma unroll
     for (int k = 1; k < PER; ++k) s += ex[k];
-    s = wave_sum_fold(s);
+    s = wave_fold_sum(s);
     float dsum = 0.0f;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       const float hv = rbf(ex[k] / s);
-      hq[tid + 64 * k] = hv;
+      hq[c0 + 64 * k] = hv;
       dsum = k == 0 ? hv * gd[k] : fmaf(hv, gd[k], dsum);
     }
     if (with_den) {
-      dsum = wave_sum_fold(dsum);
+      dsum = wave_fold_sum(dsum);
       if (tid == 0) st_agent(&frec[0], rbf(dsum));
     }
   }
@@ -147,9 +167,7 @@ __device__ void fine_read(const bf16_t* rq, int f, float* frec, float* hq, const
   float acc = 0.0f;
 #pragma unroll
   for (int k = 0; k < DP; ++k) acc = fmaf(hq[part * DP + k], gv[k], acc);
-  acc += __shfl_xor(acc, 1, 64);
-  acc += __shfl_xor(acc, 2, 64);
-  acc += __shfl_xor(acc, 4, 64);
+  acc = row_sum<8>(acc);    // the xor-1, xor-2, xor-4 butterfly over the row's 8 parts
   if (part == 0) st_agent(&frec[kStepRec + e], acc);
 }
 
@@ -177,10 +195,8 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
   float* rec = recs + j * (D + kStepRec);
   const int tid = threadIdx.x, chn = tid % G::CH, r = tid / G::CH;
   const int L = keep + fine;
-  const long long position = q.position;
-  const int n_old = local_len_at(position, keep, fine);
+  const int n_old = q.n_old, first_slot = q.first_slot;
   const int n = n_old + 1;
-  const int first_slot = (int)((position - n_old) % L);
   const int k0 = j * G::KEYS;
   if (k0 >= n) {   // past the window: an empty record
     if (tid == 0) { st_agent(&rec[0], -__builtin_inff()); st_agent(&rec[1], 0.0f); }
@@ -214,16 +230,6 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
   }
   float qv[8];
   unpack8(*(const uint4*)(q.q + chn * 8), qv);
-  if (appends) {
-    // Append the new token at slot position % L. No key of this step's
-    // window occupies that slot (window length n_old <= L - 1).
-    int slot = first_slot + n_old;
-    slot = slot >= L ? slot - L : slot;
-    const size_t off = (size_t)slot * slot_stride;
-    q.ring_k[off + tid] = app_k;
-    q.ring_v[off + tid] = app_v;
-    q.ring_raw[off + tid] = app_r;
-  }
   // Scores in log2 units (1/sqrt(D) and log2 e folded into one scale), each
   // reduced over its row's lanes; keys past the window score -inf.
   const float scale2 = (float)(1.4426950408889634 / __builtin_sqrt((double)D));
@@ -239,7 +245,8 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
     if (k0 + r + i * G::ROWS >= n) sc[i] = -__builtin_inff();
   }
   // This thread's keys: one maximum, then independent weights (no chain of
-  // rescales).
+  // rescales). A thread whose keys are all past the window keeps m = -inf
+  // and l = 0; every other thread has l >= 1.
   float m = sc[0];
 #pragma unroll
   for (int i = 1; i < G::KPT; ++i) m = fmaxf(m, sc[i]);
@@ -257,15 +264,19 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
       for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, vv[e], acc[e]);
     }
   }
-  // Merge the rows: a common maximum, the rescaled partial sums through LDS,
-  // and the rescaled row weights summed by wave 0 on DPP moves.
+  // Merge the rows: a common maximum (row 0 holds key k0 < n, so it is
+  // finite; rows with m = -inf weigh exp2(-inf) = 0), the rescaled partial
+  // sums through LDS, and the rescaled row weights summed by wave 0 on DPP
+  // moves.
   if (chn == 0) { sm.rm[r] = m; sm.rl[r] = l; }
   __syncthreads();
   float top = -__builtin_inff();
 #pragma unroll
-  for (int rr = 0; rr < G::ROWS; ++rr)
-    if (sm.rl[rr] > 0.0f) top = fmaxf(top, sm.rm[rr]);
-  const float f = l > 0.0f ? __builtin_amdgcn_exp2f(m - top) : 0.0f;
+  for (int rr = 0; rr < G::ROWS; rr += 4) {
+    const float4 m4 = *(const float4*)&sm.rm[rr];
+    top = fmaxf(top, fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w)));
+  }
+  const float f = __builtin_amdgcn_exp2f(m - top);
 #pragma unroll
   for (int e = 0; e < 8; ++e) sm.red[r][chn * 8 + e] = acc[e] * f;
   __syncthreads();
@@ -276,14 +287,24 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
     st_agent(&rec[kStepRec + tid], s);
   }
   if (tid < 64) {
-    const float x = tid < G::ROWS && sm.rl[tid] > 0.0f
-                        ? __builtin_amdgcn_exp2f(sm.rm[tid] - top) * sm.rl[tid]
-                        : 0.0f;
+    const float x = tid < G::ROWS ? __builtin_amdgcn_exp2f(sm.rm[tid] - top) * sm.rl[tid] : 0.0f;
     const float lsum = wave_fold_sum(x);
     if (tid == 0) {
       st_agent(&rec[0], top);
       st_agent(&rec[1], lsum);
     }
+  }
+  if (appends) {
+    // Append the new token at ring slot position % L, after this step's
+    // reads: no key of this step's window occupies that slot (window
+    // length n_old <= L - 1), and the stores are last so that no load
+    // above waits for them.
+    int slot = first_slot + n_old;
+    slot = slot >= L ? slot - L : slot;
+    const size_t off = (size_t)slot * slot_stride;
+    q.ring_k[off + tid] = app_k;
+    q.ring_v[off + tid] = app_v;
+    q.ring_raw[off + tid] = app_r;
   }
 }
 
@@ -313,7 +334,12 @@ __device__ int decode_units(const DecodeParams& p, int M) {
   q.fold_den = p.fold_den + (size_t)bh * D;
   q.coarse_g = p.coarse_g ? p.coarse_g + (size_t)bh * D * D : nullptr;
   q.recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
-  q.position = p.pos_hint >= 0 ? p.pos_hint : p.header[0];
+  if (p.pos_hint >= 0) {
+    q.n_old = p.win_n_old;
+    q.first_slot = p.win_first;
+  } else {
+    step_window(p.header[0], p.keep, p.fine, q.n_old, q.first_slot);
+  }
   units_body<D>(q, j, M, p.coarse_on, p.keep, p.fine, p.H * D, sm);
   return bh;
 }
@@ -327,35 +353,43 @@ constexpr int kCombineCols = 32;
 
 struct CombineArgs {
   const void* fa; const void* fb; int f_dtype;
-  const int64_t* fa_s; const int64_t* fb_s;
+  int64_t fa_s[3], fb_s[3];
   float gain;
 };
 
-// The fusion operands of channel d: the raw query element and the branch
-// parameters.
-struct FuseOps {
-  float q, a[3], b[3];
-};
-
-TAO_DEV FuseOps load_fuse_ops(const bf16_t* rq, int h, int d, const CombineArgs& c) {
-  FuseOps f;
-  f.q = bf2f(rq[d]);
+template <typename P>
+TAO_DEV CombineArgs combine_args(const P& p) {
+  CombineArgs c;
+  c.fa = p.fa;
+  c.fb = p.fb;
+  c.f_dtype = p.f_dtype;
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
-    f.a[i] = load_param(c.fa, c.f_dtype, h * c.fa_s[0] + d * c.fa_s[1] + i * c.fa_s[2]);
-    f.b[i] = load_param(c.fb, c.f_dtype, h * c.fb_s[0] + d * c.fb_s[1] + i * c.fb_s[2]);
+    c.fa_s[i] = p.fa_s[i];
+    c.fb_s[i] = p.fb_s[i];
   }
-  return f;
+  c.gain = p.gain;
+  return c;
+}
+
+// Fusion parameter element `off` of dtype FDT (a launch-time constant, so
+// the loads of one channel's six parameters issue back to back).
+template <int FDT>
+TAO_DEV float param_at(const void* p, int64_t off) {
+  if constexpr (FDT == TAO_FP32) return ((const float*)p)[off];
+  else if constexpr (FDT == TAO_FP16) return (float)((const _Float16*)p)[off];
+  else return bf2f(((const bf16_t*)p)[off]);
 }
 
 // COLS channels (from chunk * COLS) of one (request, head): G = 256 / COLS
 // thread groups share the local records. AGENT: the records were published
-// by other workgroups of the same launch (device-coherent loads). pre: the
-// fusion operands of group 0's channel, loaded earlier (else loaded here).
-template <int D, int COLS, bool AGENT>
+// by other workgroups of the same launch (device-coherent loads). FDT: the
+// fusion parameters' dtype. Empty records (past the window) hold m = -inf
+// and l = 0, so they take part in the maxima and weights as exp2(-inf) = 0;
+// record 0 always holds the new token, so the common maximum is finite.
+template <int D, int COLS, bool AGENT, int FDT>
 __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, int h, int chunk,
-                             int M, int coarse_on, const CombineArgs& c,
-                             const FuseOps* pre = nullptr) {
+                             int M, int coarse_on, const CombineArgs& c) {
   using Gm = Geo<D>;
   constexpr int STRIDE = D + kStepRec, G = kThreads / COLS;
   constexpr int NLOC = Gm::NLOC, LPG = (NLOC + G - 1) / G;
@@ -377,14 +411,19 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
     o_g[i] = j < NLOC ? ld(recs + j * STRIDE + kStepRec + d) : 0.0f;
   }
   float num = 0.0f, den = 1.0f, craw = 0.0f;
-  FuseOps ops{};
+  float qx = 0.0f, fa3[3] = {}, fb3[3] = {};
   if (g == 0) {
     if (M > 0) {
       den = ld(recs + NLOC * STRIDE);
       num = ld(recs + NLOC * STRIDE + kStepRec + d);
     }
     if (coarse_on) craw = ld(recs + (NLOC + 1) * STRIDE + kStepRec + d);
-    ops = pre ? *pre : load_fuse_ops(rq, h, d, c);
+    qx = bf2f(rq[d]);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      fa3[i] = param_at<FDT>(c.fa, h * c.fa_s[0] + d * c.fa_s[1] + i * c.fa_s[2]);
+      fb3[i] = param_at<FDT>(c.fb, h * c.fb_s[0] + d * c.fb_s[1] + i * c.fb_s[2]);
+    }
   }
   if (dc == 0) {
 #pragma unroll
@@ -392,10 +431,9 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
       if (g + i * G < NLOC) { ml[g + i * G][0] = m_g[i]; ml[g + i * G][1] = l_g[i]; }
   }
   __syncthreads();
-  float top = -__builtin_inff();
+  float top = ml[0][0];
 #pragma unroll
-  for (int j = 0; j < NLOC; ++j)
-    if (ml[j][1] > 0.0f) top = fmaxf(top, ml[j][0]);
+  for (int j = 1; j < NLOC; ++j) top = fmaxf(top, ml[j][0]);
   float pl = 0.0f;
 #pragma unroll
   for (int i = 0; i < LPG; ++i)
@@ -406,8 +444,7 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
     float den_local = 0.0f;
 #pragma unroll
     for (int j = 0; j < NLOC; ++j)
-      if (ml[j][1] > 0.0f)
-        den_local = fmaf(__builtin_amdgcn_exp2f(ml[j][0] - top), ml[j][1], den_local);
+      den_local = fmaf(__builtin_amdgcn_exp2f(ml[j][0] - top), ml[j][1], den_local);
     float nl = 0.0f;
 #pragma unroll
     for (int gg = 0; gg < G; ++gg) nl += part_loc[gg][dc];
@@ -415,7 +452,7 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
     bf16_t result;
     if (M > 0 || coarse_on) {
       const float fine_v = M > 0 ? rbf(rbf(num) / den) : 0.0f;
-      result = fuse_element(ops.q, local, rbf(craw), fine_v, ops.a, ops.b, c.gain,
+      result = fuse_element(qx, local, rbf(craw), fine_v, fa3, fb3, c.gain,
                             coarse_on ? 1 : 0, M > 0 ? 1 : 0);
     } else {
       result = f2bf(local);
@@ -430,19 +467,10 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
 // merges the records and applies the fusion for all D channels. The
 // counters (p.counters: one per head, one for the launch) start at zero and
 // are reset by their last arrival, so every step starts from zero. The head that completes last advances the cursor in header[0].
-template <int D>
+template <int D, int FDT>
 __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, int M) {
   __shared__ int last;
   const int per_head = Geo<D>::NLOC + Geo<D>::NFINE * (p.coarse_on ? 2 : 1);
-  // The fusion operands, in case this workgroup arrives last: loaded now so
-  // their latency overlaps the units' work.
-  int bh0, j0;
-  xcd_unit(blockIdx.x, p.B * p.H, per_head, bh0, j0);
-  const CombineArgs c = {p.fa, p.fb, p.f_dtype, p.fa_s, p.fb_s, p.gain};
-  FuseOps pre{};
-  if (threadIdx.x < D)
-    pre = load_fuse_ops(p.rq.p + (bh0 / p.H) * p.rq.sb + (bh0 % p.H) * p.rq.sh, bh0 % p.H,
-                        threadIdx.x, c);
   const int bh = decode_units<D>(p, M);
   float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
   unsigned* head_count = p.counters + (size_t)bh * kCounterStride;
@@ -456,8 +484,9 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, i
   if (threadIdx.x == 0)
     __hip_atomic_store(head_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int b = bh / p.H, h = bh % p.H;
-  combine_body<D, D, true>(recs, p.rq.p + b * p.rq.sb + h * p.rq.sh,
-                           p.out + b * p.out_sb + h * p.out_sh, h, 0, M, p.coarse_on, c, &pre);
+  combine_body<D, D, true, FDT>(recs, p.rq.p + b * p.rq.sb + h * p.rq.sh,
+                                p.out + b * p.out_sb + h * p.out_sh, h, 0, M, p.coarse_on,
+                                combine_args(p));
   if (threadIdx.x == 0) {
     // The stream position advances once per step (graph replays read it);
     // every workgroup of the launch read the cursor before it arrived.
@@ -498,8 +527,9 @@ __global__ __launch_bounds__(kThreads) void batch_units_kernel(BatchStepParams p
   q.fold_den = t.fold_den + (size_t)h * D;
   q.coarse_g = t.coarse_g ? t.coarse_g + (size_t)h * D * D : nullptr;
   q.recs = t.parts + (size_t)h * step_floats(D, 0);
-  q.position = t.header[0];
-  const long long fines = fines_before(q.position, p.keep, p.fine);
+  const long long position = t.header[0];
+  step_window(position, p.keep, p.fine, q.n_old, q.first_slot);
+  const long long fines = fines_before(position, p.keep, p.fine);
   const int M = fines > 0 ? (int)t.header[1] : 0;
   const int coarse_on = q.coarse_g != nullptr && fines >= p.group;
   if (j == 0 && threadIdx.x == 0) {
@@ -509,7 +539,7 @@ __global__ __launch_bounds__(kThreads) void batch_units_kernel(BatchStepParams p
   units_body<D>(q, j, M, coarse_on, p.keep, p.fine, p.H * D, sm);
 }
 
-template <int D>
+template <int D, int FDT>
 __global__ __launch_bounds__(kThreads) void batch_combine_kernel(BatchStepParams p) {
   constexpr int CHUNKS = D / kCombineCols;
   int rh, chunk;
@@ -519,8 +549,8 @@ __global__ __launch_bounds__(kThreads) void batch_combine_kernel(BatchStepParams
   const float* recs = t.parts + (size_t)h * step_floats(D, 0);
   const int M = (int)recs[2];
   const int coarse_on = recs[3] != 0.0f;
-  const CombineArgs c = {p.fa, p.fb, p.f_dtype, p.fa_s, p.fb_s, p.gain};
-  combine_body<D, kCombineCols, false>(recs, p.rq.p + r * p.rq.sb + h * p.rq.sh,
+  const CombineArgs c = combine_args(p);
+  combine_body<D, kCombineCols, false, FDT>(recs, p.rq.p + r * p.rq.sb + h * p.rq.sh,
                                        p.out + r * p.out_sb + h * p.out_sh, h, chunk, M,
                                        coarse_on, c);
   if (h == 0 && chunk == 0 && threadIdx.x == 0) t.header[0] = t.header[0] + 1;
@@ -648,39 +678,60 @@ __global__ __launch_bounds__(kThreads) void ring_append_kernel(AppendParams p) {
 
 }  // namespace
 
+// Calls f(std::integral_constant<int, FDT>{}) for the fusion dtype.
+template <typename F>
+hipError_t with_fusion_dtype(int dtype, F&& f) {
+  switch (dtype) {
+    case TAO_BF16: f(std::integral_constant<int, TAO_BF16>{}); break;
+    case TAO_FP32: f(std::integral_constant<int, TAO_FP32>{}); break;
+    case TAO_FP16: f(std::integral_constant<int, TAO_FP16>{}); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStream_t s) {
   if (M < 0 || M > p.sel_cap) return hipErrorInvalidValue;
   if (p.keep + p.fine > kMaxWindow) return hipErrorInvalidValue;
   if (p.coarse_on && !p.coarse_g) return hipErrorInvalidValue;
   if (!p.parts || !p.counters) return hipErrorInvalidValue;
-  const int per_head = local_units(head_dim) + fine_units(head_dim) * (p.coarse_on ? 2 : 1);
-  const dim3 units((unsigned)(p.B * p.H * per_head));
-  if (head_dim == 128) {
-    hipLaunchKernelGGL(decode_step_kernel<128>, units, dim3(kThreads), 0, s, p, M);
-  } else if (head_dim == 64) {
-    hipLaunchKernelGGL(decode_step_kernel<64>, units, dim3(kThreads), 0, s, p, M);
-  } else {
-    return hipErrorInvalidValue;
+  if (head_dim != 128 && head_dim != 64) return hipErrorInvalidValue;
+  DecodeParams q = p;
+  if (q.pos_hint >= 0) {
+    // The window of this step, from the cursor the host passes.
+    const long long L = q.keep + q.fine;
+    const long long n_old = q.pos_hint < L ? q.pos_hint : q.keep + (q.pos_hint - L) % q.fine;
+    q.win_n_old = (int)n_old;
+    q.win_first = (int)((q.pos_hint - n_old) % L);
   }
-  return hipGetLastError();
+  const int per_head = local_units(head_dim) + fine_units(head_dim) * (q.coarse_on ? 2 : 1);
+  const dim3 units((unsigned)(q.B * q.H * per_head));
+  return with_fusion_dtype(q.f_dtype, [&](auto fdt) {
+    constexpr int FDT = decltype(fdt)::value;
+    if (head_dim == 128)
+      hipLaunchKernelGGL((decode_step_kernel<128, FDT>), units, dim3(kThreads), 0, s, q, M);
+    else
+      hipLaunchKernelGGL((decode_step_kernel<64, FDT>), units, dim3(kThreads), 0, s, q, M);
+  });
 }
 
 hipError_t launch_batch_step(const BatchStepParams& p, int head_dim, hipStream_t s) {
   if (p.R <= 0) return hipSuccess;
   if (p.keep + p.fine > kMaxWindow) return hipErrorInvalidValue;
+  if (head_dim != 128 && head_dim != 64) return hipErrorInvalidValue;
   const int per_head = local_units(head_dim) + fine_units(head_dim) * (p.coarse_values ? 2 : 1);
   const dim3 units((unsigned)(p.R * p.H * per_head));
   const dim3 cols((unsigned)(p.R * p.H * (head_dim / kCombineCols)));
-  if (head_dim == 128) {
-    hipLaunchKernelGGL(batch_units_kernel<128>, units, dim3(kThreads), 0, s, p);
-    hipLaunchKernelGGL(batch_combine_kernel<128>, cols, dim3(kThreads), 0, s, p);
-  } else if (head_dim == 64) {
-    hipLaunchKernelGGL(batch_units_kernel<64>, units, dim3(kThreads), 0, s, p);
-    hipLaunchKernelGGL(batch_combine_kernel<64>, cols, dim3(kThreads), 0, s, p);
-  } else {
-    return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  return with_fusion_dtype(p.f_dtype, [&](auto fdt) {
+    constexpr int FDT = decltype(fdt)::value;
+    if (head_dim == 128) {
+      hipLaunchKernelGGL(batch_units_kernel<128>, units, dim3(kThreads), 0, s, p);
+      hipLaunchKernelGGL((batch_combine_kernel<128, FDT>), cols, dim3(kThreads), 0, s, p);
+    } else {
+      hipLaunchKernelGGL(batch_units_kernel<64>, units, dim3(kThreads), 0, s, p);
+      hipLaunchKernelGGL((batch_combine_kernel<64, FDT>), cols, dim3(kThreads), 0, s, p);
+    }
+  });
 }
 
 hipError_t launch_fold(const FoldParams& p, int head_dim, hipStream_t s) {

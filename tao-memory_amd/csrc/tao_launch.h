@@ -90,6 +90,7 @@ struct DecodeParams {
   long long pos_hint;   // cursor of this step, or -1: read header[0]
   int B, H, keep, fine, group, fine_cap, page_cap, sel_cap;
   int coarse_on;
+  int win_n_old, win_first;   // the window at pos_hint (set by launch_decode_step)
 };
 
 // M = selected fines of the current route (0 before the first seal: no

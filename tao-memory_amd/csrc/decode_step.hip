@@ -111,6 +111,37 @@ TAO_DEV void step_window(long long position, int keep, int fine, int& n_old, int
   }
 }
 
+// The fusion arguments of a step (copied out of the kernel arguments).
+struct CombineArgs {
+  const void* fa; const void* fb; int f_dtype;
+  int64_t fa_s[3], fb_s[3];
+  float gain;
+};
+
+template <typename P>
+TAO_DEV CombineArgs combine_args(const P& p) {
+  CombineArgs c;
+  c.fa = p.fa;
+  c.fb = p.fb;
+  c.f_dtype = p.f_dtype;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    c.fa_s[i] = p.fa_s[i];
+    c.fb_s[i] = p.fb_s[i];
+  }
+  c.gain = p.gain;
+  return c;
+}
+
+// Fusion parameter element `off` of dtype FDT (a launch-time constant, so
+// the loads of one channel's six parameters issue back to back).
+template <int FDT>
+TAO_DEV float param_at(const void* p, int64_t off) {
+  if constexpr (FDT == TAO_FP32) return ((const float*)p)[off];
+  else if constexpr (FDT == TAO_FP16) return (float)((const _Float16*)p)[off];
+  else return bf2f(((const bf16_t*)p)[off]);
+}
+
 // Fine-read workgroup f: num[e] = h . G^T[e] for rows e in
 // [f * kFineRows, (f + 1) * kFineRows) of the folded matrix gmat (this
 // head's), thread (row tid / 8, part tid % 8); with gden (the fine read)
@@ -175,21 +206,43 @@ __device__ void fine_read(const bf16_t* rq, int f, float* frec, float* hq, const
 // [j*K, (j+1)*K) of the window (workgroup 0 also appends the new token to
 // the ring), then NFINE fine-read workgroups (M > 0) and, with coarse_on,
 // NFINE coarse-read workgroups.
-template <int D>
+template <int D, int FDT>
 __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int keep, int fine,
-                           int slot_stride, StepSmem<D>& sm) {
+                           int slot_stride, StepSmem<D>& sm, const CombineArgs* fuse, int h) {
   using G = Geo<D>;
+  constexpr int STRIDE = D + kStepRec;
   float* recs = q.recs;
   if (j >= G::NLOC + G::NFINE) {
     if (coarse_on)
-      fine_read<D>(q.rq, j - G::NLOC - G::NFINE, recs + (G::NLOC + 1) * (D + kStepRec),
-                   sm.red[0], q.coarse_g, nullptr);
+      fine_read<D>(q.rq, j - G::NLOC - G::NFINE, recs + (G::NLOC + 1) * STRIDE, sm.red[0],
+                   q.coarse_g, nullptr);
     return;
   }
   if (j >= G::NLOC) {
+    // Fine-read workgroup f; with `fuse`, its first kFineRows threads also
+    // write the branch weights of channels f * kFineRows + tid (records
+    // NLOC + 2 .. NLOC + 4), loading their operands before the read and
+    // combining them after it.
+    const int f = j - G::NLOC;
+    const int e = f * kFineRows + (int)threadIdx.x;
+    const bool weights = fuse != nullptr && (M > 0 || coarse_on) && threadIdx.x < kFineRows;
+    float fq = 0.0f, fa3[3] = {}, fb3[3] = {};
+    if (weights) {
+      fq = bf2f(q.rq[e]);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        fa3[i] = param_at<FDT>(fuse->fa, h * fuse->fa_s[0] + e * fuse->fa_s[1] + i * fuse->fa_s[2]);
+        fb3[i] = param_at<FDT>(fuse->fb, h * fuse->fb_s[0] + e * fuse->fb_s[1] + i * fuse->fb_s[2]);
+      }
+    }
     if (M > 0)
-      fine_read<D>(q.rq, j - G::NLOC, recs + G::NLOC * (D + kStepRec), sm.red[0], q.fold_g,
-                   q.fold_den);
+      fine_read<D>(q.rq, f, recs + G::NLOC * STRIDE, sm.red[0], q.fold_g, q.fold_den);
+    if (weights) {
+      const FuseWeights w = fuse_weights(fq, fa3, fb3, coarse_on, M > 0 ? 1 : 0);
+      st_agent(recs + (G::NLOC + 2) * STRIDE + kStepRec + e, w.r0);
+      st_agent(recs + (G::NLOC + 3) * STRIDE + kStepRec + e, w.r1);
+      st_agent(recs + (G::NLOC + 4) * STRIDE + kStepRec + e, w.r2);
+    }
     return;
   }
   float* rec = recs + j * (D + kStepRec);
@@ -311,8 +364,8 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
 // The units of one launch: per (batch, head) NLOC local-attention
 // workgroups (the window split by keys), NFINE fine-read workgroups and,
 // with coarse_on, NFINE coarse-read workgroups. Returns the (batch, head).
-template <int D>
-__device__ int decode_units(const DecodeParams& p, int M) {
+template <int D, int FDT>
+__device__ int decode_units(const DecodeParams& p, int M, const CombineArgs& c) {
   using G = Geo<D>;
   __shared__ StepSmem<D> sm;
   const int per_head = G::NLOC + G::NFINE * (p.coarse_on ? 2 : 1);
@@ -340,7 +393,7 @@ __device__ int decode_units(const DecodeParams& p, int M) {
   } else {
     step_window(p.header[0], p.keep, p.fine, q.n_old, q.first_slot);
   }
-  units_body<D>(q, j, M, p.coarse_on, p.keep, p.fine, p.H * D, sm);
+  units_body<D, FDT>(q, j, M, p.coarse_on, p.keep, p.fine, p.H * D, sm, &c, h);
   return bh;
 }
 
@@ -351,43 +404,13 @@ __device__ int decode_units(const DecodeParams& p, int M) {
 // workgroup per (request, head, kCombineCols channels).
 constexpr int kCombineCols = 32;
 
-struct CombineArgs {
-  const void* fa; const void* fb; int f_dtype;
-  int64_t fa_s[3], fb_s[3];
-  float gain;
-};
-
-template <typename P>
-TAO_DEV CombineArgs combine_args(const P& p) {
-  CombineArgs c;
-  c.fa = p.fa;
-  c.fb = p.fb;
-  c.f_dtype = p.f_dtype;
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    c.fa_s[i] = p.fa_s[i];
-    c.fb_s[i] = p.fb_s[i];
-  }
-  c.gain = p.gain;
-  return c;
-}
-
-// Fusion parameter element `off` of dtype FDT (a launch-time constant, so
-// the loads of one channel's six parameters issue back to back).
-template <int FDT>
-TAO_DEV float param_at(const void* p, int64_t off) {
-  if constexpr (FDT == TAO_FP32) return ((const float*)p)[off];
-  else if constexpr (FDT == TAO_FP16) return (float)((const _Float16*)p)[off];
-  else return bf2f(((const bf16_t*)p)[off]);
-}
-
 // COLS channels (from chunk * COLS) of one (request, head): G = 256 / COLS
 // thread groups share the local records. AGENT: the records were published
 // by other workgroups of the same launch (device-coherent loads). FDT: the
 // fusion parameters' dtype. Empty records (past the window) hold m = -inf
 // and l = 0, so they take part in the maxima and weights as exp2(-inf) = 0;
 // record 0 always holds the new token, so the common maximum is finite.
-template <int D, int COLS, bool AGENT, int FDT>
+template <int D, int COLS, bool AGENT, int FDT, bool WEIGHTED>
 __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, int h, int chunk,
                              int M, int coarse_on, const CombineArgs& c) {
   using Gm = Geo<D>;
@@ -412,17 +435,26 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
   }
   float num = 0.0f, den = 1.0f, craw = 0.0f;
   float qx = 0.0f, fa3[3] = {}, fb3[3] = {};
+  FuseWeights wts{};
   if (g == 0) {
     if (M > 0) {
       den = ld(recs + NLOC * STRIDE);
       num = ld(recs + NLOC * STRIDE + kStepRec + d);
     }
     if (coarse_on) craw = ld(recs + (NLOC + 1) * STRIDE + kStepRec + d);
-    qx = bf2f(rq[d]);
+    if (WEIGHTED) {
+      if (M > 0 || coarse_on) {
+        wts.r0 = ld(recs + (NLOC + 2) * STRIDE + kStepRec + d);
+        wts.r1 = ld(recs + (NLOC + 3) * STRIDE + kStepRec + d);
+        wts.r2 = ld(recs + (NLOC + 4) * STRIDE + kStepRec + d);
+      }
+    } else {
+      qx = bf2f(rq[d]);
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      fa3[i] = param_at<FDT>(c.fa, h * c.fa_s[0] + d * c.fa_s[1] + i * c.fa_s[2]);
-      fb3[i] = param_at<FDT>(c.fb, h * c.fb_s[0] + d * c.fb_s[1] + i * c.fb_s[2]);
+      for (int i = 0; i < 3; ++i) {
+        fa3[i] = param_at<FDT>(c.fa, h * c.fa_s[0] + d * c.fa_s[1] + i * c.fa_s[2]);
+        fb3[i] = param_at<FDT>(c.fb, h * c.fb_s[0] + d * c.fb_s[1] + i * c.fb_s[2]);
+      }
     }
   }
   if (dc == 0) {
@@ -452,8 +484,8 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
     bf16_t result;
     if (M > 0 || coarse_on) {
       const float fine_v = M > 0 ? rbf(rbf(num) / den) : 0.0f;
-      result = fuse_element(qx, local, rbf(craw), fine_v, fa3, fb3, c.gain,
-                            coarse_on ? 1 : 0, M > 0 ? 1 : 0);
+      if (!WEIGHTED) wts = fuse_weights(qx, fa3, fb3, coarse_on ? 1 : 0, M > 0 ? 1 : 0);
+      result = fuse_mix(wts, local, rbf(craw), fine_v, c.gain);
     } else {
       result = f2bf(local);
     }
@@ -471,7 +503,8 @@ template <int D, int FDT>
 __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, int M) {
   __shared__ int last;
   const int per_head = Geo<D>::NLOC + Geo<D>::NFINE * (p.coarse_on ? 2 : 1);
-  const int bh = decode_units<D>(p, M);
+  const CombineArgs c = combine_args(p);
+  const int bh = decode_units<D, FDT>(p, M, c);
   float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
   unsigned* head_count = p.counters + (size_t)bh * kCounterStride;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // this thread's stores done
@@ -484,9 +517,9 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, i
   if (threadIdx.x == 0)
     __hip_atomic_store(head_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int b = bh / p.H, h = bh % p.H;
-  combine_body<D, D, true, FDT>(recs, p.rq.p + b * p.rq.sb + h * p.rq.sh,
-                                p.out + b * p.out_sb + h * p.out_sh, h, 0, M, p.coarse_on,
-                                combine_args(p));
+  combine_body<D, D, true, FDT, true>(recs, p.rq.p + b * p.rq.sb + h * p.rq.sh,
+                                      p.out + b * p.out_sb + h * p.out_sh, h, 0, M, p.coarse_on,
+                                      c);
   if (threadIdx.x == 0) {
     // The stream position advances once per step (graph replays read it);
     // every workgroup of the launch read the cursor before it arrived.
@@ -536,7 +569,7 @@ __global__ __launch_bounds__(kThreads) void batch_units_kernel(BatchStepParams p
     q.recs[2] = (float)M;
     q.recs[3] = (float)coarse_on;
   }
-  units_body<D>(q, j, M, coarse_on, p.keep, p.fine, p.H * D, sm);
+  units_body<D, TAO_BF16>(q, j, M, coarse_on, p.keep, p.fine, p.H * D, sm, nullptr, h);
 }
 
 template <int D, int FDT>
@@ -550,7 +583,7 @@ __global__ __launch_bounds__(kThreads) void batch_combine_kernel(BatchStepParams
   const int M = (int)recs[2];
   const int coarse_on = recs[3] != 0.0f;
   const CombineArgs c = combine_args(p);
-  combine_body<D, kCombineCols, false, FDT>(recs, p.rq.p + r * p.rq.sb + h * p.rq.sh,
+  combine_body<D, kCombineCols, false, FDT, false>(recs, p.rq.p + r * p.rq.sb + h * p.rq.sh,
                                        p.out + r * p.out_sb + h * p.out_sh, h, chunk, M,
                                        coarse_on, c);
   if (h == 0 && chunk == 0 && threadIdx.x == 0) t.header[0] = t.header[0] + 1;

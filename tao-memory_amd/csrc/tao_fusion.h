@@ -23,9 +23,15 @@ TAO_DEV float load_param(const void* p, int dtype, int64_t off) {
 // are present (fusion_pointwise.py:114-117, operator.py branch count).
 constexpr float kLogTwoBf16 = 0.69140625f;
 
-TAO_DEV bf16_t fuse_element(float q, float local, float coarse, float fine,
-                            const float a[3], const float b[3], float gain,
-                            int coarse_on, int fine_on) {
+// The branch weights of one channel (fusion_pointwise.py:10-117): they
+// depend on the raw query element and the parameters only, not on the
+// branch values, so a decode step computes them beside its reads.
+struct FuseWeights {
+  float r0, r1, r2;   // local, coarse, fine
+};
+
+TAO_DEV FuseWeights fuse_weights(float q, const float a[3], const float b[3], int coarse_on,
+                                 int fine_on) {
   const float ninf = -__builtin_inff();
   float s[3];
 #pragma unroll
@@ -43,11 +49,21 @@ TAO_DEV bf16_t fuse_element(float q, float local, float coarse, float fine,
   float e2 = fine_on ? __expf(s[2] - top) : 0.0f;
   float total = (e0 + e2) + e1;   // butterfly order over [e0, e1, e2, 0]
   const float inv = __builtin_amdgcn_rcpf(total);
-  float r0 = rbf(e0 * inv), r1 = rbf(e1 * inv), r2 = rbf(e2 * inv);
-  float lt = rbf(r0 * rbf(2.0f * local));
-  float ct = rbf(r1 * rbf(gain * coarse));
-  float ft = rbf(r2 * rbf(gain * fine));
+  return {rbf(e0 * inv), rbf(e1 * inv), rbf(e2 * inv)};
+}
+
+// The weighted mix of the branch values with the channel's weights.
+TAO_DEV bf16_t fuse_mix(const FuseWeights& w, float local, float coarse, float fine, float gain) {
+  float lt = rbf(w.r0 * rbf(2.0f * local));
+  float ct = rbf(w.r1 * rbf(gain * coarse));
+  float ft = rbf(w.r2 * rbf(gain * fine));
   return f2bf(rbf(lt + ct) + ft);
+}
+
+TAO_DEV bf16_t fuse_element(float q, float local, float coarse, float fine,
+                            const float a[3], const float b[3], float gain,
+                            int coarse_on, int fine_on) {
+  return fuse_mix(fuse_weights(q, a, b, coarse_on, fine_on), local, coarse, fine, gain);
 }
 
 }  // namespace tao

@@ -38,11 +38,12 @@ __host__ __device__ constexpr int local_units(int head_dim) {
 __host__ __device__ constexpr int fine_units(int head_dim) { return head_dim / kFineRows; }
 
 // Per (batch, head) decode scratch, in floats: local_units(D) local-attention
-// records, one fine record (den in the header, num[D]) and one coarse record
-// (coarse[D]), each of (kStepRec + D) floats.
+// records, one fine record (den in the header, num[D]), one coarse record
+// (coarse[D]) and three fusion-weight records (the local, coarse and fine
+// branch weights of every channel), each of (kStepRec + D) floats.
 __host__ __device__ inline size_t step_floats(int head_dim, int sel_cap) {
   (void)sel_cap;
-  return (size_t)(local_units(head_dim) + 2) * (head_dim + kStepRec);
+  return (size_t)(local_units(head_dim) + 5) * (head_dim + kStepRec);
 }
 
 // Workspace layout (bytes from the start of tao_state_dev::workspace):

@@ -176,14 +176,11 @@ TAO_DEV float ld_agent(const float* p) {
 // it re-reads every step sit in that XCD's L2. Returns (u, j), j < per; a
 // bijection of [0, units * per). Units not a multiple of 8: plain order.
 TAO_DEV void xcd_unit(int i, int units, int per, int& u, int& j) {
-  if (units & 7) {
-    u = i / per;
-    j = i % per;
-    return;
-  }
-  const int n = i >> 3;
-  u = (i & 7) + 8 * (n / per);
-  j = n % per;
+  const bool plain = (units & 7) != 0;      // selects, not branches: one division
+  const int n = plain ? i : i >> 3;
+  const int q = n / per;
+  j = n - q * per;
+  u = plain ? q : (i & 7) + 8 * q;
 }
 
 TAO_DEV float wave_max(float v) {

@@ -520,9 +520,14 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, i
   combine_body<D, D, true, FDT, true>(recs, p.rq.p + b * p.rq.sb + h * p.rq.sh,
                                       p.out + b * p.out_sb + h * p.out_sh, h, 0, M, p.coarse_on,
                                       c);
-  if (threadIdx.x == 0) {
-    // The stream position advances once per step (graph replays read it);
-    // every workgroup of the launch read the cursor before it arrived.
+  if (p.pos_hint >= 0) {
+    // The stream position advances once per step (graph replays read it).
+    // With the cursor given by the host no workgroup reads it, so head 0's
+    // merge stores the next one.
+    if (bh == 0 && threadIdx.x == 0) p.header[0] = p.pos_hint + 1;
+  } else if (threadIdx.x == 0) {
+    // Every workgroup of the launch read the cursor before it arrived: the
+    // last head advances it.
     unsigned* all_count = p.counters + (size_t)p.B * p.H * kCounterStride;
     if (__hip_atomic_fetch_add(all_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
         (unsigned)(p.B * p.H) - 1u) {

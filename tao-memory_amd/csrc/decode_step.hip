@@ -57,10 +57,12 @@ struct Geo {
 };
 static_assert(kThreads == 256, "thread layouts below assume 256 threads");
 
+constexpr int kWaves = kThreads / 64;
+
 template <int D>
 struct StepSmem {
-  float red[Geo<D>::ROWS][D];     // cross-row reduction
-  float rm[Geo<D>::ROWS], rl[Geo<D>::ROWS];
+  float wo[kWaves][D];            // each wave's weighted value sums
+  float wm[kWaves], wl[kWaves];   // each wave's maximum and weight sum
 };
 
 TAO_DEV void unpack8(const uint4& u, float out[8]) {
@@ -84,6 +86,34 @@ TAO_DEV float row_sum(float v) {
   v += dpp_partner<0x141>(v);
   if constexpr (CH == 16) v += dpp_partner<0x140>(v);
   return v;
+}
+
+// Sum (max) over the rows of key data one wave holds: CH lanes per row,
+// 64 / CH rows. Row pairs combine on lane swaps (row_ror:8 inside a 16-lane
+// row for CH = 8, then v_permlane16_swap and v_permlane32_swap), in the
+// fixed order ((r0 + r1) + (r2 + r3)) ...; every lane ends with the total.
+template <int CH>
+TAO_DEV float wave_rows_sum(float v) {
+  static_assert(CH == 8 || CH == 16, "a key row spans 8 or 16 lanes");
+  if constexpr (CH == 8) v += dpp_partner<0x128>(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int CH>
+TAO_DEV float wave_rows_max(float v) {
+  static_assert(CH == 8 || CH == 16, "a key row spans 8 or 16 lanes");
+  if constexpr (CH == 8) v = fmaxf(v, dpp_partner<0x128>(v));
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // One (request, head)'s operands of one decode step, shared by the
@@ -214,7 +244,7 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
   float* recs = q.recs;
   if (j >= G::NLOC + G::NFINE) {
     if (coarse_on)
-      fine_read<D>(q.rq, j - G::NLOC - G::NFINE, recs + (G::NLOC + 1) * STRIDE, sm.red[0],
+      fine_read<D>(q.rq, j - G::NLOC - G::NFINE, recs + (G::NLOC + 1) * STRIDE, sm.wo[0],
                    q.coarse_g, nullptr);
     return;
   }
@@ -236,7 +266,7 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
       }
     }
     if (M > 0)
-      fine_read<D>(q.rq, f, recs + G::NLOC * STRIDE, sm.red[0], q.fold_g, q.fold_den);
+      fine_read<D>(q.rq, f, recs + G::NLOC * STRIDE, sm.wo[0], q.fold_g, q.fold_den);
     if (weights) {
       const FuseWeights w = fuse_weights(fq, fa3, fb3, coarse_on, M > 0 ? 1 : 0);
       st_agent(recs + (G::NLOC + 2) * STRIDE + kStepRec + e, w.r0);
@@ -297,12 +327,13 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
     sc[i] = row_sum<G::CH>(part) * scale2;
     if (k0 + r + i * G::ROWS >= n) sc[i] = -__builtin_inff();
   }
-  // This thread's keys: one maximum, then independent weights (no chain of
-  // rescales). A thread whose keys are all past the window keeps m = -inf
-  // and l = 0; every other thread has l >= 1.
+  // Weights against the wave's maximum over its rows' keys (one value for
+  // the whole wave, so no rescale inside it); a wave whose keys are all
+  // past the window contributes nothing.
   float m = sc[0];
 #pragma unroll
   for (int i = 1; i < G::KPT; ++i) m = fmaxf(m, sc[i]);
+  m = wave_rows_max<G::CH>(m);
   float l = 0.0f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
@@ -317,31 +348,31 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
       for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, vv[e], acc[e]);
     }
   }
-  // Merge the rows: a common maximum (row 0 holds key k0 < n, so it is
-  // finite; rows with m = -inf weigh exp2(-inf) = 0), the rescaled partial
-  // sums through LDS, and the rescaled row weights summed by wave 0 on DPP
-  // moves.
-  if (chn == 0) { sm.rm[r] = m; sm.rl[r] = l; }
-  __syncthreads();
-  float top = -__builtin_inff();
+  // The wave's rows summed on lane swaps (no LDS), then the waves meet once
+  // in LDS: a common maximum (wave 0 holds key k0 < n, so it is finite;
+  // empty waves weigh exp2(-inf) = 0) and the rescaled sums in wave order.
+  l = wave_rows_sum<G::CH>(l);
 #pragma unroll
-  for (int rr = 0; rr < G::ROWS; rr += 4) {
-    const float4 m4 = *(const float4*)&sm.rm[rr];
-    top = fmaxf(top, fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w)));
+  for (int e = 0; e < 8; ++e) acc[e] = wave_rows_sum<G::CH>(acc[e]);
+  const int wave = tid / 64, lane = tid % 64;
+  if (lane < G::CH) {
+    *(float4*)&sm.wo[wave][chn * 8] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *(float4*)&sm.wo[wave][chn * 8 + 4] = make_float4(acc[4], acc[5], acc[6], acc[7]);
   }
-  const float f = __builtin_amdgcn_exp2f(m - top);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) sm.red[r][chn * 8 + e] = acc[e] * f;
+  if (lane == 0) { sm.wm[wave] = m; sm.wl[wave] = l; }
   __syncthreads();
   if (tid < D) {
-    float s = 0.0f;
+    float top = sm.wm[0];
 #pragma unroll
-    for (int rr = 0; rr < G::ROWS; ++rr) s += sm.red[rr][tid];
-    st_agent(&rec[kStepRec + tid], s);
-  }
-  if (tid < 64) {
-    const float x = tid < G::ROWS ? __builtin_amdgcn_exp2f(sm.rm[tid] - top) * sm.rl[tid] : 0.0f;
-    const float lsum = wave_fold_sum(x);
+    for (int w = 1; w < kWaves; ++w) top = fmaxf(top, sm.wm[w]);
+    float sum = 0.0f, lsum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = __builtin_amdgcn_exp2f(sm.wm[w] - top);
+      sum = fmaf(f, sm.wo[w][tid], sum);
+      lsum = fmaf(f, sm.wl[w], lsum);
+    }
+    st_agent(&rec[kStepRec + tid], sum);
     if (tid == 0) {
       st_agent(&rec[0], top);
       st_agent(&rec[1], lsum);

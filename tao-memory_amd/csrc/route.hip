@@ -45,7 +45,9 @@ TAO_DEV int key_index(unsigned long long key) {
 constexpr int kRouteThreads = 512;   // 8 waves
 constexpr int kWaves = kRouteThreads / 64;
 constexpr int kBatch = 8;            // rows whose loads one wave issues together
-constexpr int kRefreshBatch = 10;    // staged rows one wave reduces together
+constexpr int kRefreshThreads = 1024;   // the refresh: 16 waves per (batch, head)
+constexpr int kRefreshWaves = kRefreshThreads / 64;
+constexpr int kRefreshRowsPerWave = 5;   // staged rows one refresh wave reduces together
 constexpr int kRankMax = 512;        // rank-count selection up to this many keys
 
 // Masses of up to kBatch rows per wave: every lane loads its two (or one)
@@ -132,17 +134,25 @@ TAO_DEV int key_rank(const unsigned long long* keys, int n, unsigned long long m
 }
 
 // Stable descending selection of the top `count` keys (unique 64-bit keys:
-// score << 32 | ~index). Writes the selected keys, best first, to dst.
-TAO_DEV void select_top(unsigned long long* keys, int n, int count,
-                           unsigned long long* dst) {
-  if (n <= 2 * kRouteThreads / 8) {
-    // T lanes per key (8 for n <= 64, 4 for n <= 128): lane part p counts
-    // the larger keys among keys p, p + T, ...; DPP adds the T parts.
-    const int T = n <= kRouteThreads / 8 ? 8 : 4;
+// score << 32 | ~index) by a workgroup of NT threads. Writes the selected
+// keys, best first, to dst.
+template <int NT>
+TAO_DEV void select_top_n(unsigned long long* keys, int n, int count, unsigned long long* dst) {
+  if (n <= 2 * NT / 8) {
+    // T lanes per key (8 for n <= NT / 8, else 4): lane part p counts the
+    // larger keys among keys p, p + T, ... (four reads in flight at a time;
+    // 0 is below every key); DPP adds the T parts.
+    const int T = n <= NT / 8 ? 8 : 4;
     const int i = threadIdx.x / T, part = threadIdx.x % T;
     const unsigned long long mine = keys[min(i, n - 1)];
     int cnt = 0;
-    for (int j = part; j < n; j += T) cnt += keys[j] > mine;
+    for (int j0 = part; j0 < n; j0 += 4 * T) {
+      unsigned long long k4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) k4[u] = j0 + u * T < n ? keys[j0 + u * T] : 0ull;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) cnt += k4[u] > mine;
+    }
     cnt += __builtin_amdgcn_update_dpp(0, cnt, 0xB1, 0xF, 0xF, false);
     cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x4E, 0xF, 0xF, false);
     if (T == 8) cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x141, 0xF, 0xF, false);
@@ -151,7 +161,7 @@ TAO_DEV void select_top(unsigned long long* keys, int n, int count,
     return;
   }
   if (n <= kRankMax) {
-    for (int i = threadIdx.x; i < n; i += kRouteThreads) {
+    for (int i = threadIdx.x; i < n; i += NT) {
       const unsigned long long mine = keys[i];
       const int rank = key_rank(keys, n, mine);
       if (rank < count) dst[rank] = mine;
@@ -161,11 +171,11 @@ TAO_DEV void select_top(unsigned long long* keys, int n, int count,
   }
   int np = 1;
   while (np < n) np <<= 1;
-  for (int i = n + threadIdx.x; i < np; i += kRouteThreads) keys[i] = 0ull;
+  for (int i = n + threadIdx.x; i < np; i += NT) keys[i] = 0ull;
   __syncthreads();
   for (int k = 2; k <= np; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < np; i += kRouteThreads) {
+      for (int i = threadIdx.x; i < np; i += NT) {
         const int ixj = i ^ j;
         if (ixj > i) {
           const unsigned long long a = keys[i], b = keys[ixj];
@@ -176,8 +186,12 @@ TAO_DEV void select_top(unsigned long long* keys, int n, int count,
       __syncthreads();
     }
   }
-  for (int i = threadIdx.x; i < count; i += kRouteThreads) dst[i] = keys[i];
+  for (int i = threadIdx.x; i < count; i += NT) dst[i] = keys[i];
   __syncthreads();
+}
+
+TAO_DEV void select_top(unsigned long long* keys, int n, int count, unsigned long long* dst) {
+  select_top_n<kRouteThreads>(keys, n, count, dst);
 }
 
 template <int D>
@@ -313,7 +327,7 @@ struct RefreshSmem {
 // The rows' reductions are independent and unrolled, so their latencies
 // overlap. Rows past `count` (wave-uniform) give 0 and are not used; this
 // wave's lane r < count receives row r's mass.
-template <int D>
+template <int D, int NB>
 TAO_DEV float staged_masses(const float* h, const bf16_t* const* pw_rows,
                             const bf16_t* const* sw_rows, int count, int lane) {
   constexpr int PER = D / 64;
@@ -323,17 +337,17 @@ TAO_DEV float staged_masses(const float* h, const bf16_t* const* pw_rows,
   for (int k = 0; k < PER; ++k) hq[k] = h[e0 + 64 * k];
   // Rows past `count` repeat the last row (callers clamp), so every read is
   // unconditional and the reads of all rows are in flight together.
-  bf16_t pv[kRefreshBatch][PER], sv[kRefreshBatch][PER];
+  bf16_t pv[NB][PER], sv[NB][PER];
 #pragma unroll
-  for (int r = 0; r < kRefreshBatch; ++r)
+  for (int r = 0; r < NB; ++r)
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       pv[r][k] = pw_rows[r][e0 + 64 * k];
       sv[r][k] = sw_rows ? sw_rows[r][e0 + 64 * k] : (bf16_t)0;
     }
-  float part[kRefreshBatch];
+  float part[NB];
 #pragma unroll
-  for (int r = 0; r < kRefreshBatch; ++r) {
+  for (int r = 0; r < NB; ++r) {
     float v[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
@@ -345,17 +359,17 @@ TAO_DEV float staged_masses(const float* h, const bf16_t* const* pw_rows,
     for (int k = 1; k < PER; ++k) s += v[k];
     part[r] = s;
   }
-  wave_fold_sum_n<kRefreshBatch>(part);
+  wave_fold_sum_n<NB>(part);
   float mine = 0.0f;
 #pragma unroll
-  for (int r = 0; r < kRefreshBatch; ++r)
+  for (int r = 0; r < NB; ++r)
     if (lane == r) mine = rbf(part[r]);
   (void)count;
   return mine;
 }
 
 template <int D>
-__global__ __launch_bounds__(kRouteThreads) void route_refresh_kernel(RouteParams p) {
+__global__ __launch_bounds__(kRefreshThreads) void route_refresh_kernel(RouteParams p) {
   __shared__ RefreshSmem<D> sm;
   constexpr int C16 = D / 8;            // 16-byte chunks per row
   const int bh = blockIdx.x;
@@ -369,13 +383,13 @@ __global__ __launch_bounds__(kRouteThreads) void route_refresh_kernel(RouteParam
   const bf16_t* sw = p.sw + (size_t)bh * p.fine_cap * D;
   // ---- round trip 1: page weights, pending segment weights, anchor query
   // (every load issued before any store to LDS)
-  constexpr int PW_PT = (kRefreshPages * C16 + kRouteThreads - 1) / kRouteThreads;
-  constexpr int SW_PT = (kRefreshRows * C16 + kRouteThreads - 1) / kRouteThreads;
+  constexpr int PW_PT = (kRefreshPages * C16 + kRefreshThreads - 1) / kRefreshThreads;
+  constexpr int SW_PT = (kRefreshRows * C16 + kRefreshThreads - 1) / kRefreshThreads;
   // Loads are unconditional (indices clamped to a valid row) so the
   // scheduler can issue them all before the guarded LDS stores.
 #pragma unroll
   for (int k = 0; k < PW_PT; ++k) {
-    const int i = tid + k * kRouteThreads;
+    const int i = tid + k * kRefreshThreads;
     const int ic = min(i, P * C16 - 1);
     const uint4 v = *(const uint4*)(pw + (size_t)(ic / C16) * D + (ic % C16) * 8);
     if (i < P * C16) *(uint4*)&sm.pw[i / C16][(i % C16) * 8] = v;
@@ -389,16 +403,16 @@ __global__ __launch_bounds__(kRouteThreads) void route_refresh_kernel(RouteParam
   __syncthreads();
   // ---- coarse pages: stable top-`coarse` by page mass, then ascending
   if (coarse > 0) {
-    for (int base = wave * kRefreshBatch; base < K; base += kWaves * kRefreshBatch) {
-      const int count = min(kRefreshBatch, K - base);
-      const bf16_t* rows[kRefreshBatch];
+    for (int base = wave * kRefreshRowsPerWave; base < K; base += kRefreshWaves * kRefreshRowsPerWave) {
+      const int count = min(kRefreshRowsPerWave, K - base);
+      const bf16_t* rows[kRefreshRowsPerWave];
 #pragma unroll
-      for (int r = 0; r < kRefreshBatch; ++r) rows[r] = sm.pw[base + min(r, count - 1)];
-      const float mass = staged_masses<D>(sm.h, rows, nullptr, count, lane);
+      for (int r = 0; r < kRefreshRowsPerWave; ++r) rows[r] = sm.pw[base + min(r, count - 1)];
+      const float mass = staged_masses<D, kRefreshRowsPerWave>(sm.h, rows, nullptr, count, lane);
       if (lane < count) sm.keys[base + lane] = score_key(mass, base + lane);
     }
     __syncthreads();
-    select_top(sm.keys, K, coarse, sm.top);
+    select_top_n<kRefreshThreads>(sm.keys, K, coarse, sm.top);
     if (tid < coarse) {
       const int mine = key_index(sm.top[tid]);
       int rank = 0;
@@ -409,7 +423,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_refresh_kernel(RouteParam
     // ---- round trip 2: segment weights of the chosen pages' fines
 #pragma unroll
     for (int k = 0; k < SW_PT; ++k) {
-      const int i = tid + k * kRouteThreads;
+      const int i = tid + k * kRefreshThreads;
       const int ic = min(i, group * coarse * C16 - 1);
       const int row = ic / C16;
       const int id = sm.chosen[row / group] * group + row % group;
@@ -419,28 +433,28 @@ __global__ __launch_bounds__(kRouteThreads) void route_refresh_kernel(RouteParam
     __syncthreads();
   }
   // ---- candidate masses: 8 fines of each chosen page, then the pending fines
-  for (int base = wave * kRefreshBatch; base < E; base += kWaves * kRefreshBatch) {
-    const int count = min(kRefreshBatch, E - base);
-    const bf16_t* prow[kRefreshBatch];
-    const bf16_t* srow[kRefreshBatch];
+  for (int base = wave * kRefreshRowsPerWave; base < E; base += kRefreshWaves * kRefreshRowsPerWave) {
+    const int count = min(kRefreshRowsPerWave, E - base);
+    const bf16_t* prow[kRefreshRowsPerWave];
+    const bf16_t* srow[kRefreshRowsPerWave];
 #pragma unroll
-    for (int r = 0; r < kRefreshBatch; ++r) {
+    for (int r = 0; r < kRefreshRowsPerWave; ++r) {
       const int j = base + min(r, count - 1);
       prow[r] = sm.pw[j < group * coarse ? sm.chosen[j / group] : K];
       srow[r] = sm.sw[j];
     }
-    const float mass = staged_masses<D>(sm.h, prow, srow, count, lane);
+    const float mass = staged_masses<D, kRefreshRowsPerWave>(sm.h, prow, srow, count, lane);
     if (lane < count) sm.keys[base + lane] = score_key(mass, base + lane);
   }
   __syncthreads();
-  select_top(sm.keys, E, selected, sm.top);
+  select_top_n<kRefreshThreads>(sm.keys, E, selected, sm.top);
   int32_t* sel_out = p.sel + (size_t)bh * p.sel_cap;
-  for (int m = tid; m < selected; m += kRouteThreads) {
+  for (int m = tid; m < selected; m += kRefreshThreads) {
     const int j = key_index(sm.top[m]);
     sel_out[m] = j < group * coarse ? sm.chosen[j / group] * group + j % group
                                     : K * group + (j - group * coarse);
   }
-  for (int i = tid; i < coarse; i += kRouteThreads)
+  for (int i = tid; i < coarse; i += kRefreshThreads)
     p.chosen[(size_t)bh * p.chosen_cap + i] = sm.chosen[i];
   if (bh == 0 && tid == 0) p.header[1] = selected;
 }
@@ -888,9 +902,9 @@ hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s) {
       p.group == 8) {
     const dim3 rgrid((unsigned)(p.B * p.H));
     if (head_dim == 128)
-      hipLaunchKernelGGL(route_refresh_kernel<128>, rgrid, dim3(kRouteThreads), 0, s, p);
+      hipLaunchKernelGGL(route_refresh_kernel<128>, rgrid, dim3(kRefreshThreads), 0, s, p);
     else if (head_dim == 64)
-      hipLaunchKernelGGL(route_refresh_kernel<64>, rgrid, dim3(kRouteThreads), 0, s, p);
+      hipLaunchKernelGGL(route_refresh_kernel<64>, rgrid, dim3(kRefreshThreads), 0, s, p);
     else
       return hipErrorInvalidValue;
     return hipGetLastError();

@@ -43,7 +43,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # per dispatch) scaled by the same counters over a 256 MiB plain copy
 # (FETCH_SIZE reads 0.5000x the copied bytes, WRITE_SIZE 1.0000x); the
 # summary and commands are under profiles/.
-DECODE_STEP_TRAFFIC_BYTES = 13_757_720
+DECODE_STEP_TRAFFIC_BYTES = 13_570_800
 
 
 def log(msg):
@@ -127,7 +127,7 @@ def decode_bytes(cfg, heads, width, selected, position, layer=0):
     keys = schedule.local_len_at(position, cfg) + 1
     local = keys * heads * width * 2 * 2                  # ring K and V
     folded = heads * width * (width + 1) * 4 if fines > 0 else 0
-    records = 2 * 12 * heads * (width + 4) * 4            # written, then merged
+    records = 2 * 16 * heads * (width + 4) * 4            # written, then merged
     tokens = 5 * heads * width * 2 + 3 * heads * width * 2 + heads * width * 2
     own = local + folded + records + tokens + fold
     return ref, own
@@ -763,7 +763,7 @@ def main():
                    "context": args.context, "heads": heads, "head_dim": width,
                    "selected_fines": state.route_size, "timed_refreshes": refreshes,
                    "timed_seals": seals},
-        "roofline": {"bound": "hbm", "kernel": "decode_units_kernel<128> + decode_combine_kernel<128> per step, with the %d route refreshes (route_kernel + fold_kernel) and %d seals (writer + epilogue + fold) of the timed steps amortised" % (refreshes, seals),
+        "roofline": {"bound": "hbm", "kernel": "decode_step_kernel<128> per step (one launch: the units and the last workgroup's merge per head), with the %d route refreshes (route_refresh_kernel + fold_kernel) and %d seals (writer + epilogue + fold) of the timed steps amortised" % (refreshes, seals),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": DECODE_STEP_TRAFFIC_BYTES if args.context == 131072 else None,

@@ -547,6 +547,67 @@ def run_full_sequence(torch, args, device):
                 width=d)
 
 
+def config0_inputs(torch, device):
+    """B1 x T2048 x H4 x D64 fp32, q/k/v/raw_q/raw_k N(0,1) from seed
+    0 with RoPE applied by the caller to q and k, fusion_a/b N(0, 0.02)."""
+    b, t, h, d = 1, 2048, 4, 64
+    g = torch.Generator().manual_seed(0)
+    xs = [torch.randn(b, t, h, d, generator=g) for _ in range(5)]
+    fa = torch.randn(h, d, 3, generator=g) * 0.02
+    fb = torch.randn(h, d, 3, generator=g) * 0.02
+    inv = 10000.0 ** (-torch.arange(0, d // 2, dtype=torch.float64) * 2 / d)
+    ang = torch.arange(t, dtype=torch.float64)[:, None] * inv[None, :]
+    cos = torch.cat((ang.cos(), ang.cos()), -1)[None, :, None, :]
+    sin = torch.cat((ang.sin(), ang.sin()), -1)[None, :, None, :]
+    for i in (0, 1):
+        x = xs[i]
+        rot = torch.cat((-x[..., d // 2:], x[..., :d // 2]), -1)
+        xs[i] = (x.double() * cos + rot.double() * sin).float()
+    return [x.to(device) for x in xs], fa.to(device), fb.to(device)
+
+
+def run_full_sequence_f32(torch, device):
+    """configs[0] on the GPU: tao_attention forward with fp32 operands and
+    index_only_page_memo(graph=False); mean of 10 event-bracketed calls."""
+    from tao_attention import tao_attention
+    from tao_attention.presets import index_only_page_memo
+    xs, fa, fb = config0_inputs(torch, device)
+    cfg = index_only_page_memo(graph=False)
+
+    def call():
+        return tao_attention(*xs[:3], raw_q=xs[3], raw_k=xs[4], fusion_a=fa, fusion_b=fb,
+                             alpha=0.5, config=cfg)
+
+    with torch.no_grad():
+        for _ in range(2):
+            call()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        runs = 10
+        start.record()
+        for _ in range(runs):
+            call()
+        end.record()
+        torch.cuda.synchronize()
+    return start.elapsed_time(end) / runs * 1e-3
+
+
+def cpu_full_sequence_f32(torch, runs=3):
+    """configs[0] as defined: the oracle's full-sequence forward (torch eager,
+    fp32) on the host cores; 1 warm-up, then the median of `runs`."""
+    from oracle import tao_oracle as O
+    from tao_attention.presets import index_only_page_memo
+    xs, fa, fb = config0_inputs(torch, torch.device("cpu"))
+    geo = O.Geometry.from_config(index_only_page_memo(graph=False))
+    O.training_forward(*xs, fa, fb, 0.5, geo)
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        O.training_forward(*xs, fa, fb, 0.5, geo)
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
 def run_writers(torch, device):
     """The non-preset writers' operators at the configs[2] block shape: the
     62 sealed 256-token blocks of a 16K prefill, H32, D128, taken as one batch
@@ -873,6 +934,15 @@ def main():
         log(f"full-sequence forward: {fs['seconds'] * 1e3:.3f} ms, "
             f"{fs['batch'] * fs['tokens'] / fs['seconds']:.1f} tok/s; forward + backward "
             f"{fs['train_seconds'] * 1e3:.3f} ms")
+    if not args.no_full_sequence:
+        log("fp32 full-sequence forward (configs[0])")
+        f32_s = run_full_sequence_f32(torch, device)
+        result["full_sequence_f32"] = {
+            "workload": "configs[0]: tao_attention forward B1 x T2048 x H4 x D64 fp32, "
+                        "index_only_page_memo(graph=False), seed 0, RoPE on q/k; fp32 "
+                        "semantics: every bf16 rounding point of the bf16 path rounds to fp32",
+            "ms": round(f32_s * 1e3, 4), "tokens_per_s": round(2048 / f32_s, 1)}
+        log(f"fp32 forward: {f32_s * 1e3:.3f} ms")
     if not args.no_writers:
         log("non-preset writer operators (configs[2] block shape)")
         result["writers"] = run_writers(torch, device)
@@ -900,6 +970,15 @@ def main():
                 "cores": torch.get_num_threads(), "kind": "port",
                 "sample": pre_cpu["sample"]}
             log(f"cpu prefill baseline: {pre_cpu['tok_s']:.1f} tokens/s (H32-equivalent)")
+        if not args.no_full_sequence:
+            f32_cpu = cpu_full_sequence_f32(torch)
+            result["cpu_baseline_full_sequence_f32"] = {
+                "value": round(2048 / f32_cpu, 1), "unit": "tokens/s",
+                "cores": torch.get_num_threads(), "kind": "port",
+                "sample": f"configs[0] as defined (B1 x T2048 x H4 x D64 fp32): median of 3 "
+                          f"oracle forwards after 1 warm-up, {f32_cpu:.3f} s each; CPU "
+                          f"{cpu_model()}"}
+            log(f"cpu configs[0] baseline: {f32_cpu:.3f} s per forward")
     state.release_execution()
     if args.calibrate_copy_mib:
         n = args.calibrate_copy_mib * (1 << 20) // 4

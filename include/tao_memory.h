@@ -162,7 +162,7 @@ int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok,
  * arrival counters in library-owned static device arrays (4 MiB, and 1024
  * counters on 128-byte lines) instead of st->workspace (which may be null).
  * Limit:
- * batch * heads <= 567 at head_dim 128, <= 593 at 64 (TAO_E_CAPACITY
+ * batch * heads <= 467 at head_dim 128, <= 531 at 64 (TAO_E_CAPACITY
  * beyond). Allocates nothing. Every call on one device shares the arrays:
  * calls that overlap on one device race and must be serialised by the
  * caller; each step leaves its counters at zero, so nothing needs clearing

@@ -88,7 +88,7 @@ extern "C" int tao_decode_step_noalloc(const tao_state_dev* st, const tao_tokens
                     std::to_string((long long)st->batch * st->heads) +
                     " needs " + std::to_string(need) + " bytes of step records, above the " +
                     std::to_string(kScratchBytes) +
-                    "-byte static scratch (at most 567 heads at D128, 593 at D64)");
+                    "-byte static scratch (at most 467 heads at D128, 531 at D64)");
   if (tao::step_counters(st->batch, st->heads) > (size_t)kMaxCounters)
     return fail(TAO_E_CAPACITY, "tao_decode_step_noalloc: more heads than the static "
                                 "scratch counts");

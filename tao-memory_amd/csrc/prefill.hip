@@ -89,27 +89,6 @@ __global__ __launch_bounds__(kThreads) void epochs_kernel(EpochParams p) {
   }
 }
 
-// Turn-group read: one 512-thread workgroup per (8 consecutive read tiles,
-// batch, head); wave w owns tile w (<= 32 queries sharing one route, its
-// own seal epoch and segment-weight source). The workgroup reads each fine
-// of the union of the 8 selected sets once: C^T is staged into padded LDS
-// (double-buffered, the next fine's rows in flight in registers), and every
-// wave whose tile selected that fine builds its A operand
-//   ch[q][d] = r(r(h_q[d] * pw[page][d]) * sw[fine][d])
-// in registers (MFMA A layout; r(h * pw) is kept per page) and runs
-// 4 x 8 v_mfma_f32_32x32x16_bf16 into its 32 x D accumulator, plus one
-// against a column of ones for den[q] = sum over the tile's fines of
-// sum_d ch; fine = r(r(num) / r(den)), then the fusion epilogue. With the
-// coarse value branch (COARSE), each e-tile of a tile whose chunk has
-// completed pages also runs 8 MFMAs of the wave's h against the folded
-// coarse matrix of its page count (coarse.hip) before the fusion.
-//
-// PERQ (the full-sequence read, every query routed by itself): selections
-// are per-query bitmasks (route_queries_kernel). The union and the per-wave
-// masks come from the OR of the wave's bitmasks, and each A row is zeroed
-// unless its own query selected the fine, so a wave's 32 queries still share
-// every staged C^T and MFMA; the numerator and denominator of a query sum
-// exactly its selected fines (selected_read.py:156-173).
 constexpr int kGroupWaves = 8;
 constexpr int kGroupThreads = 64 * kGroupWaves;
 constexpr int kBitWords = kMaxFineIds / 32;
@@ -123,14 +102,14 @@ struct GroupSmem {
       int pre[kBitWords];
       uint32_t wbits[kGroupWaves][kBitWords];   // PERQ: OR of each wave's bitmasks
     } setup;
-    bf16_t c[2][D][D + 8];        // staged C^T, rows padded by 16 bytes
+    bf16_t c[2][D][D + 8];        // staged weighted C^T, rows padded by 16 bytes
   } u;
-  bf16_t pwsw[kGroupWaves][2][2][D];   // per wave, per buffer: pw row, sw row
-  bf16_t hq[kGroupWaves][32][D + 8];   // per wave: h of its queries (bf16, padded rows)
+  bf16_t wr[2][D];                     // per buffer: the staged fine's weights r(pw * sw)
   int ids[kGroupWaves][kMaxM];
   int uni[kMaxUnion];
   uint32_t mask[kMaxUnion / 4];        // byte u: bit w set if wave w selected uni[u]
   int n_union;
+  int erels[kGroupWaves];              // each wave's tile epoch, -1 without a read
 };
 
 TAO_DEV void unpack8f(const uint4& u, float out[8]) {
@@ -142,10 +121,57 @@ TAO_DEV void unpack8f(const uint4& u, float out[8]) {
   }
 }
 
+// Eight bf16 weights r(pw * sw) of one 16-byte slice, packed.
+TAO_DEV uint4 slice_weights(const uint4& pw, const uint4& sw) {
+  float a[8], b[8];
+  unpack8f(pw, a);
+  unpack8f(sw, b);
+  return make_uint4(pack_bf16x2(a[0] * b[0], a[1] * b[1]), pack_bf16x2(a[2] * b[2], a[3] * b[3]),
+                    pack_bf16x2(a[4] * b[4], a[5] * b[5]), pack_bf16x2(a[6] * b[6], a[7] * b[7]));
+}
+
+// One 16-byte slice of C^T scaled by the slice's weights, rounded to bf16.
+TAO_DEV uint4 scale_slice(const uint4& c, const uint4& wr) {
+  float a[8], b[8];
+  unpack8f(c, a);
+  unpack8f(wr, b);
+  return make_uint4(pack_bf16x2(a[0] * b[0], a[1] * b[1]), pack_bf16x2(a[2] * b[2], a[3] * b[3]),
+                    pack_bf16x2(a[4] * b[4], a[5] * b[5]), pack_bf16x2(a[6] * b[6], a[7] * b[7]));
+}
+
+// Turn-group read: one 512-thread workgroup per (8 consecutive read tiles,
+// batch, head); wave w owns tile w (<= 32 queries sharing one route, its
+// own seal epoch and segment-weight source). The read of a fine is linear in
+// its channel weights, num[q][e] = sum_d h_q[d] w[d] C^T[e][d] with
+// w = r(pw[page] * sw[fine]) shared by every tile of one seal epoch, so the
+// workgroup stages each fine's C^T already weighted (r(C^T * w), padded LDS,
+// double-buffered, the next fine's rows and weight slices in flight in
+// registers) and every tile's A operand is its queries' h, which stays in
+// registers for the whole kernel: a selecting wave runs 4 x 8
+// v_mfma_f32_32x32x16_bf16 into its 32 x D accumulator plus 8 against the
+// weights for den[q] = sum over its fines of h_q . w, with no per-fine VALU.
+// The workgroup takes one pass per distinct epoch among its tiles (a group
+// straddles at most a seal): each pass streams the union of its tiles'
+// selected sets. fine = r(r(num) / r(den)), then the fusion epilogue. The
+// reference rounds h * pw and then the product with sw to bf16 before its
+// fp32 sums (selected_read.py:31, 48); here the product of the two weights
+// is rounded and folded into C, which moves the read within its bf16
+// tolerance. With the coarse value branch (COARSE), each e-tile of a tile
+// whose chunk has completed pages also runs 8 MFMAs of the wave's h against
+// the folded coarse matrix of its page count (coarse.hip) before the fusion.
+//
+// PERQ (the full-sequence read, every query routed by itself): selections
+// are per-query bitmasks (route_queries_kernel). The union and the per-wave
+// masks come from the OR of the wave's bitmasks, and each A row is zeroed
+// unless its own query selected the fine, so a wave's 32 queries still share
+// every staged C^T and MFMA; the numerator and denominator of a query sum
+// exactly its selected fines (selected_read.py:156-173).
 template <int D, bool COARSE, bool PERQ>
 __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesParams p) {
   constexpr int KK = D / 16, ET = D / 32, CPR = D / 8;   // k-steps, e-tiles, uint4 per row
   constexpr int CPT = D * CPR / kGroupThreads;           // C^T uint4 per thread
+  static_assert(CPT == 1 || CPT == 4, "head width 64 or 128");
+  static_assert(kGroupThreads % CPR == 0, "a thread's C^T chunks share one column slice");
   __shared__ GroupSmem<D> sm;
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
@@ -155,13 +181,14 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
   const int li = lane & 31, hl = lane >> 5;
   const int t0 = grp * kGroupWaves;
   const int nt = min(kGroupWaves, p.n_tiles - t0);
+  const int cc = tid % CPR;                              // this thread's column slice
 
   // This wave's tile.
-  int q_first = 0, nq = 0, slot = 0, M = 0, erel = 0, sw_split = 0, fine_on = 0, cpages = 0;
+  int q_first = 0, nq = 0, slot = 0, M = 0, erel = 0, fine_on = 0, cpages = 0;
   if (w < nt) {
     const int64_t* desc = p.tiles + 8 * (t0 + w);
     q_first = (int)desc[0]; nq = (int)desc[1]; slot = (int)desc[2]; M = (int)desc[3];
-    erel = (int)desc[4]; sw_split = (int)desc[5]; fine_on = (int)desc[6];
+    erel = (int)desc[4]; fine_on = (int)desc[6];
     cpages = (int)desc[7];
   }
   const bool reads = w < nt && fine_on;
@@ -174,87 +201,14 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
           *(const uint4*)(p.local + (((size_t)b * p.T + t) * p.H + h) * D + c * 8);
     }
   }
+  if (lane == 0) sm.erels[w] = reads ? erel : -1;
 
-  // ---- union of the selected sets (ascending fine id) and per-wave masks
-  for (int i = tid; i < kBitWords; i += kGroupThreads) sm.u.setup.bits[i] = 0;
-  for (int i = tid; i < kMaxUnion / 4; i += kGroupThreads) sm.mask[i] = 0;
-  // PERQ: this lane's query bitmask (rows li >= nq select nothing).
-  const uint32_t* qbits = nullptr;
-  if constexpr (PERQ) {
-    for (int i = tid; i < kGroupWaves * kBitWords; i += kGroupThreads)
-      (&sm.u.setup.wbits[0][0])[i] = 0u;
-    if (reads)
-      qbits = p.qsel + ((size_t)(b * p.T + q_first + min(li, nq - 1)) * p.H + h) * p.qsel_words;
-  } else if (reads) {
-    const int32_t* sel = p.sel_pool + ((size_t)slot * BH + bh) * p.sel_cap;
-    for (int m = lane; m < M; m += 64) sm.ids[w][m] = sel[m];
-  }
-  __syncthreads();
-  if constexpr (PERQ) {
-    if (reads) {
-      const int words = (p.first_epoch + erel + 31) >> 5;
-      for (int i = 0; i < words; ++i) {
-        uint32_t v = (lane < 32 && li < nq) ? qbits[i] : 0u;
+  // ---- h of this wave's queries in the MFMA A layout, kept in registers:
+  // lane (li, hl) holds row q = li, channels d = 16 kk + 8 hl + j (packed
+  // bf16); rows past the tile are zero.
+  uint4 hA[KK];
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) v |= __shfl_xor(v, off, 64);
-        if (lane == 0) {
-          sm.u.setup.wbits[w][i] = v;
-          atomicOr(&sm.u.setup.bits[i], v);
-        }
-      }
-    }
-  } else if (reads) {
-    for (int m = lane; m < M; m += 64) {
-      const int id = sm.ids[w][m];
-      atomicOr(&sm.u.setup.bits[id >> 5], 1u << (id & 31));
-    }
-  }
-  __syncthreads();
-  if (w == 0) {
-    constexpr int WPL = kBitWords / 64;
-    int cnt[WPL], total = 0;
-#pragma unroll
-    for (int i = 0; i < WPL; ++i) { cnt[i] = __popc(sm.u.setup.bits[lane * WPL + i]); total += cnt[i]; }
-    int incl = total;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int v = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += v;
-    }
-    int run = incl - total;
-#pragma unroll
-    for (int i = 0; i < WPL; ++i) { sm.u.setup.pre[lane * WPL + i] = run; run += cnt[i]; }
-    if (lane == 63) sm.n_union = incl;
-  }
-  __syncthreads();
-  for (int i = tid; i < kBitWords; i += kGroupThreads) {
-    uint32_t bits = sm.u.setup.bits[i];
-    int r = sm.u.setup.pre[i];
-    while (bits) {
-      const int bit = __ffs(bits) - 1;
-      sm.uni[r] = i * 32 + bit;
-      if constexpr (PERQ) {
-        uint32_t byte = 0;
-#pragma unroll
-        for (int v = 0; v < kGroupWaves; ++v) byte |= ((sm.u.setup.wbits[v][i] >> bit) & 1u) << v;
-        atomicOr(&sm.mask[r >> 2], byte << ((r & 3) * 8));
-      }
-      ++r;
-      bits &= bits - 1;
-    }
-  }
-  if (!PERQ && reads)
-    for (int m = lane; m < M; m += 64) {
-      const int id = sm.ids[w][m];
-      const uint32_t word = sm.u.setup.bits[id >> 5];
-      const int rank = sm.u.setup.pre[id >> 5] + __popc(word & ((1u << (id & 31)) - 1u));
-      atomicOr(&sm.mask[rank >> 2], 1u << ((rank & 3) * 8 + w));
-    }
-  __syncthreads();
-  const int U = sm.n_union;
-
-  // ---- h of this wave's queries in the MFMA A layout: lane (li, hl) holds
-  // row q = li, channels d = 16 kk + 8 hl + j (packed bf16).
+  for (int kk = 0; kk < KK; ++kk) hA[kk] = make_uint4(0u, 0u, 0u, 0u);
   if (reads) {
     const int q = li < nq ? li : nq - 1;
     const bf16_t* rq = p.rq.p + b * p.rq.sb + (int64_t)(q_first + q) * p.rq.st + h * p.rq.sh;
@@ -273,65 +227,24 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
 #pragma unroll
       for (int j = 0; j < 8; ++j) { x[kk][j] = __expf(x[kk][j] - mx); sum += x[kk][j]; }
     sum += __shfl_xor(sum, 32, 64);
-    const float inv_valid = li < nq ? 1.0f : 0.0f;
+    // One reciprocal per row: h only shapes the read (within its tolerance),
+    // never a route.
+    const float inv = li < nq ? __builtin_amdgcn_rcpf(sum) : 0.0f;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       uint32_t wv[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        wv[j] = pack_bf16x2(x[kk][2 * j] / sum * inv_valid, x[kk][2 * j + 1] / sum * inv_valid);
-      *(uint4*)&sm.hq[w][li][16 * kk + 8 * hl] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+        wv[j] = pack_bf16x2(x[kk][2 * j] * inv, x[kk][2 * j + 1] * inv);
+      hA[kk] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
     }
   }
-
-  // ---- stream the union
-  const bf16_t* bank = p.bank + (size_t)bh * p.fine_cap * D * D;
-  const bf16_t* pw_base = p.pw_pool + ((size_t)erel * BH + bh) * p.pool_pcap * D;
-  const bf16_t* psw_base = p.psw_pool ? p.psw_pool + ((size_t)erel * BH + bh) * 8 * D : nullptr;
-  const bf16_t* sw_base = p.sw + (size_t)bh * p.fine_cap * D;
-  auto active = [&](int u) __attribute__((always_inline)) { return reads && ((sm.mask[u >> 2] >> ((u & 3) * 8 + w)) & 1u); };
-  // C^T rows of union entry u: thread tid moves uint4 chunks tid + i * 512,
-  // i < CPT, into one of two named register sets (X = a or b).
-  static_assert(CPT == 1 || CPT == 4, "head width 64 or 128");
-#define TAO_C_CHUNK(i_) (bank + (size_t)cid * D * D + (size_t)(tid + (i_) * kGroupThreads) * 8)
-#define TAO_LOAD_C(u, X)                                                 \
-  do {                                                                   \
-    const int cid = sm.uni[(u)];                                         \
-    X##0 = *(const uint4*)TAO_C_CHUNK(0);                                \
-    if constexpr (CPT == 4) {                                            \
-      X##1 = *(const uint4*)TAO_C_CHUNK(1);                              \
-      X##2 = *(const uint4*)TAO_C_CHUNK(2);                              \
-      X##3 = *(const uint4*)TAO_C_CHUNK(3);                              \
-    }                                                                    \
-  } while (0)
-#define TAO_C_SLOT(buf, i_)                                              \
-  (*(uint4*)&sm.u.c[(buf)][(tid + (i_) * kGroupThreads) / CPR]           \
-                  [((tid + (i_) * kGroupThreads) % CPR) * 8])
-#define TAO_STORE_C(buf, X)                                              \
-  do {                                                                   \
-    TAO_C_SLOT(buf, 0) = X##0;                                           \
-    if constexpr (CPT == 4) {                                            \
-      TAO_C_SLOT(buf, 1) = X##1;                                         \
-      TAO_C_SLOT(buf, 2) = X##2;                                         \
-      TAO_C_SLOT(buf, 3) = X##3;                                         \
-    }                                                                    \
-  } while (0)
-  // pw / sw rows of fine id for this wave: lane l < D / 2 moves 4 bytes of each.
-  auto load_w = [&](int u, uint32_t& pwv, uint32_t& swv) __attribute__((always_inline)) {
-    const int id = sm.uni[u];
-    const bf16_t* pw = pw_base + (size_t)(id / p.group) * D;
-    const bf16_t* sw = id < sw_split ? sw_base + (size_t)id * D : psw_base + (size_t)(id - sw_split) * D;
-    if (lane < D / 2) {
-      pwv = *(const uint32_t*)(pw + 2 * lane);
-      swv = *(const uint32_t*)(sw + 2 * lane);
-    }
-  };
-  auto store_w = [&](int buf, uint32_t pwv, uint32_t swv) __attribute__((always_inline)) {
-    if (lane < D / 2) {
-      *(uint32_t*)&sm.pwsw[w][buf][0][2 * lane] = pwv;
-      *(uint32_t*)&sm.pwsw[w][buf][1][2 * lane] = swv;
-    }
-  };
+  // PERQ: this lane's query bitmask (rows li >= nq select nothing).
+  const uint32_t* qbits = nullptr;
+  if constexpr (PERQ) {
+    if (reads)
+      qbits = p.qsel + ((size_t)(b * p.T + q_first + min(li, nq - 1)) * p.H + h) * p.qsel_words;
+  }
 
   floatx16 acc[ET];
 #pragma unroll
@@ -341,110 +254,201 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
   floatx16 acc_den;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc_den[i] = 0.0f;
-  // Pipeline: while fine u is consumed from LDS buffer u & 1, fine u + 1
-  // waits in one register set (stored to LDS at the end of the iteration)
-  // and fine u + 2's loads are in flight in the other, so each global load
-  // has a whole iteration to arrive.
-  uint4 a0, a1, a2, a3, b0, b1, b2, b3;
-  uint32_t pwa = 0, swa = 0, pwb = 0, swb = 0;
-  // Per wave: t = r(h * pw[page]) of the page last used, packed in the A
-  // layout (consecutive union fines mostly share a page).
-  uint4 tpk[KK];
-  int cached_page = -1;
-  const bf16x8 ones = as_bf16x8(make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u));
-  // PERQ: the lane's bitmask word of the current fine (ids ascend).
-  int qword_at = -1;
-  uint32_t qword = 0u;
-  auto consume = [&](int u) __attribute__((always_inline)) {
-    if (!active(u)) return;
-    const int buf = u & 1;
-    const int page = sm.uni[u] / p.group;
-    uint32_t keep = 0xFFFFFFFFu;
-    if constexpr (PERQ) {
-      const int id = sm.uni[u];
-      if ((id >> 5) != qword_at) {
-        qword_at = id >> 5;
-        qword = li < nq ? qbits[qword_at] : 0u;
-      }
-      keep = ((qword >> (id & 31)) & 1u) ? 0xFFFFFFFFu : 0u;
+
+  const bf16_t* bank = p.bank + (size_t)bh * p.fine_cap * D * D;
+  const bf16_t* sw_base = p.sw + (size_t)bh * p.fine_cap * D;
+  __syncthreads();   // sm.erels
+
+  // ---- one pass per distinct epoch of the group's reading tiles, ascending
+  for (int pass_erel = -1;;) {
+    int next = 0x7FFFFFFF;
+#pragma unroll
+    for (int v = 0; v < kGroupWaves; ++v) {
+      const int e = sm.erels[v];
+      if (e > pass_erel && e < next) next = e;
     }
-    if (page != cached_page) {
-      const bf16_t* pwr = sm.pwsw[w][buf][0];
+    if (next == 0x7FFFFFFF) break;
+    pass_erel = next;
+    const bool in_pass = reads && erel == pass_erel;
+    // The pass's page weights (its epoch pool) and segment-weight source:
+    // fines below the epoch's completed pages read the state's weights, the
+    // pending page's fines the epoch's pool rows.
+    const int pass_epoch = p.first_epoch + pass_erel;
+    const int sw_split = (pass_epoch / p.group) * p.group;
+    const bf16_t* pw_base = p.pw_pool + ((size_t)pass_erel * BH + bh) * p.pool_pcap * D;
+    const bf16_t* psw_base =
+        p.psw_pool ? p.psw_pool + ((size_t)pass_erel * BH + bh) * 8 * D : nullptr;
+
+    // ---- union of the pass's selected sets (ascending fine id), per-wave masks
+    for (int i = tid; i < kBitWords; i += kGroupThreads) sm.u.setup.bits[i] = 0;
+    for (int i = tid; i < kMaxUnion / 4; i += kGroupThreads) sm.mask[i] = 0;
+    if constexpr (PERQ) {
+      for (int i = tid; i < kGroupWaves * kBitWords; i += kGroupThreads)
+        (&sm.u.setup.wbits[0][0])[i] = 0u;
+    } else if (in_pass) {
+      const int32_t* sel = p.sel_pool + ((size_t)slot * BH + bh) * p.sel_cap;
+      for (int m = lane; m < M; m += 64) sm.ids[w][m] = sel[m];
+    }
+    __syncthreads();
+    if constexpr (PERQ) {
+      if (in_pass) {
+        const int words = (pass_epoch + 31) >> 5;
+        for (int i = 0; i < words; ++i) {
+          uint32_t v = (lane < 32 && li < nq) ? qbits[i] : 0u;
+#pragma unroll
+          for (int off = 1; off < 64; off <<= 1) v |= __shfl_xor(v, off, 64);
+          if (lane == 0) {
+            sm.u.setup.wbits[w][i] = v;
+            atomicOr(&sm.u.setup.bits[i], v);
+          }
+        }
+      }
+    } else if (in_pass) {
+      for (int m = lane; m < M; m += 64) {
+        const int id = sm.ids[w][m];
+        atomicOr(&sm.u.setup.bits[id >> 5], 1u << (id & 31));
+      }
+    }
+    __syncthreads();
+    if (w == 0) {
+      constexpr int WPL = kBitWords / 64;
+      int cnt[WPL], total = 0;
+#pragma unroll
+      for (int i = 0; i < WPL; ++i) {
+        cnt[i] = __popc(sm.u.setup.bits[lane * WPL + i]);
+        total += cnt[i];
+      }
+      int incl = total;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += v;
+      }
+      int run = incl - total;
+#pragma unroll
+      for (int i = 0; i < WPL; ++i) { sm.u.setup.pre[lane * WPL + i] = run; run += cnt[i]; }
+      if (lane == 63) sm.n_union = incl;
+    }
+    __syncthreads();
+    for (int i = tid; i < kBitWords; i += kGroupThreads) {
+      uint32_t bits = sm.u.setup.bits[i];
+      int r = sm.u.setup.pre[i];
+      while (bits) {
+        const int bit = __ffs(bits) - 1;
+        sm.uni[r] = i * 32 + bit;
+        if constexpr (PERQ) {
+          uint32_t byte = 0;
+#pragma unroll
+          for (int v = 0; v < kGroupWaves; ++v)
+            byte |= ((sm.u.setup.wbits[v][i] >> bit) & 1u) << v;
+          atomicOr(&sm.mask[r >> 2], byte << ((r & 3) * 8));
+        }
+        ++r;
+        bits &= bits - 1;
+      }
+    }
+    if (!PERQ && in_pass)
+      for (int m = lane; m < M; m += 64) {
+        const int id = sm.ids[w][m];
+        const uint32_t word = sm.u.setup.bits[id >> 5];
+        const int rank = sm.u.setup.pre[id >> 5] + __popc(word & ((1u << (id & 31)) - 1u));
+        atomicOr(&sm.mask[rank >> 2], 1u << ((rank & 3) * 8 + w));
+      }
+    __syncthreads();
+    const int U = sm.n_union;
+
+    // ---- stream the union. Thread tid moves C^T chunks tid + i * 512 (i <
+    // CPT, all in column slice cc) and that slice of the fine's pw and sw
+    // rows through one of two named register sets (X = a or b).
+    auto active = [&](int u) __attribute__((always_inline)) {
+      return in_pass && ((sm.mask[u >> 2] >> ((u & 3) * 8 + w)) & 1u);
+    };
+#define TAO_C_CHUNK(i_) (bank + (size_t)cid * D * D + (size_t)(tid + (i_) * kGroupThreads) * 8)
+#define TAO_LOAD_C(u, X)                                                           \
+  do {                                                                             \
+    const int cid = sm.uni[(u)];                                                   \
+    const bf16_t* swr_ = cid < sw_split ? sw_base + (size_t)cid * D                \
+                                        : psw_base + (size_t)(cid - sw_split) * D; \
+    X##p = *(const uint4*)(pw_base + (size_t)(cid / p.group) * D + cc * 8);        \
+    X##s = *(const uint4*)(swr_ + cc * 8);                                         \
+    X##0 = *(const uint4*)TAO_C_CHUNK(0);                                          \
+    if constexpr (CPT == 4) {                                                      \
+      X##1 = *(const uint4*)TAO_C_CHUNK(1);                                        \
+      X##2 = *(const uint4*)TAO_C_CHUNK(2);                                        \
+      X##3 = *(const uint4*)TAO_C_CHUNK(3);                                        \
+    }                                                                              \
+  } while (0)
+#define TAO_C_SLOT(buf, i_)                                              \
+  (*(uint4*)&sm.u.c[(buf)][(tid + (i_) * kGroupThreads) / CPR][cc * 8])
+#define TAO_STORE_C(buf, X)                                              \
+  do {                                                                   \
+    const uint4 wr_ = slice_weights(X##p, X##s);                         \
+    if (tid < CPR) *(uint4*)&sm.wr[(buf)][cc * 8] = wr_;                 \
+    TAO_C_SLOT(buf, 0) = scale_slice(X##0, wr_);                         \
+    if constexpr (CPT == 4) {                                            \
+      TAO_C_SLOT(buf, 1) = scale_slice(X##1, wr_);                       \
+      TAO_C_SLOT(buf, 2) = scale_slice(X##2, wr_);                       \
+      TAO_C_SLOT(buf, 3) = scale_slice(X##3, wr_);                       \
+    }                                                                    \
+  } while (0)
+
+    // PERQ: the lane's bitmask word of the current fine (ids ascend).
+    int qword_at = -1;
+    uint32_t qword = 0u;
+    auto consume = [&](int u) __attribute__((always_inline)) {
+      if (!active(u)) return;
+      const int buf = u & 1;
+      uint32_t keep = 0xFFFFFFFFu;
+      if constexpr (PERQ) {
+        const int id = sm.uni[u];
+        if ((id >> 5) != qword_at) {
+          qword_at = id >> 5;
+          qword = li < nq ? qbits[qword_at] : 0u;
+        }
+        keep = ((qword >> (id & 31)) & 1u) ? 0xFFFFFFFFu : 0u;
+      }
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         const int d0 = 16 * kk + 8 * hl;
-        float hv[8], pv[8];
-        unpack8f(*(const uint4*)&sm.hq[w][li][d0], hv);
-        unpack8f(*(const uint4*)(pwr + d0), pv);
-        uint32_t t1[4];
+        uint4 av = hA[kk];
+        if constexpr (PERQ) { av.x &= keep; av.y &= keep; av.z &= keep; av.w &= keep; }
+        const bf16x8 a = as_bf16x8(av);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          t1[j] = pack_bf16x2(hv[2 * j] * pv[2 * j], hv[2 * j + 1] * pv[2 * j + 1]);
-        tpk[kk] = make_uint4(t1[0], t1[1], t1[2], t1[3]);
+        for (int t = 0; t < ET; ++t) {
+          const bf16x8 bq = as_bf16x8(*(const uint4*)&sm.u.c[buf][32 * t + li][d0]);
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq, acc[t], 0, 0, 0);
+        }
+        // den: the same A against the fine's weights in every column.
+        const bf16x8 wq = as_bf16x8(*(const uint4*)&sm.wr[buf][d0]);
+        acc_den = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, wq, acc_den, 0, 0, 0);
       }
-      cached_page = page;
-    }
-    const bf16_t* swr = sm.pwsw[w][buf][1];
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      const int d0 = 16 * kk + 8 * hl;
-      float tv[8], sv[8];
-      unpack8f(tpk[kk], tv);
-      unpack8f(*(const uint4*)(swr + d0), sv);
-      uint32_t ch[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        ch[j] = pack_bf16x2(tv[2 * j] * sv[2 * j], tv[2 * j + 1] * sv[2 * j + 1]) & keep;
-      const bf16x8 a = as_bf16x8(make_uint4(ch[0], ch[1], ch[2], ch[3]));
-#pragma unroll
-      for (int t = 0; t < ET; ++t) {
-        const bf16x8 bq = as_bf16x8(*(const uint4*)&sm.u.c[buf][32 * t + li][d0]);
-        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq, acc[t], 0, 0, 0);
-      }
-      // den: the same A against a column of ones.
-      acc_den = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, ones, acc_den, 0, 0, 0);
-    }
-  };
-  if (U > 0) {
-    TAO_LOAD_C(0, a);
-    if (active(0)) load_w(0, pwa, swa);
-    TAO_STORE_C(0, a);
-    if (active(0)) store_w(0, pwa, swa);
-  }
-  if (U > 1) {
-    TAO_LOAD_C(1, b);
-    if (active(1)) load_w(1, pwb, swb);
-  }
-  __syncthreads();
-  // Even u: fine u + 2 -> set a, fine u + 1 (set b) -> LDS; odd u: the reverse.
-  for (int u = 0; u < U; u += 2) {
-    if (u + 2 < U) {
-      TAO_LOAD_C(u + 2, a);
-      if (active(u + 2)) load_w(u + 2, pwa, swa);
-    }
-    consume(u);
-    if (u + 1 < U) {
-      TAO_STORE_C(1, b);
-      if (active(u + 1)) store_w(1, pwb, swb);
-    }
-    __syncthreads();
-    if (u + 1 >= U) break;
-    if (u + 3 < U) {
-      TAO_LOAD_C(u + 3, b);
-      if (active(u + 3)) load_w(u + 3, pwb, swb);
-    }
-    consume(u + 1);
-    if (u + 2 < U) {
+    };
+    uint4 a0, a1, a2, a3, ap, as, b0, b1, b2, b3, bp, bs;
+    if (U > 0) {
+      TAO_LOAD_C(0, a);
       TAO_STORE_C(0, a);
-      if (active(u + 2)) store_w(0, pwa, swa);
     }
+    if (U > 1) TAO_LOAD_C(1, b);
     __syncthreads();
-  }
-
+    // Even u: fine u + 2 -> set a, fine u + 1 (set b) -> LDS; odd u: the reverse.
+    for (int u = 0; u < U; u += 2) {
+      if (u + 2 < U) TAO_LOAD_C(u + 2, a);
+      consume(u);
+      if (u + 1 < U) TAO_STORE_C(1, b);
+      __syncthreads();
+      if (u + 1 >= U) break;
+      if (u + 3 < U) TAO_LOAD_C(u + 3, b);
+      consume(u + 1);
+      if (u + 2 < U) TAO_STORE_C(0, a);
+      __syncthreads();
+    }
 #undef TAO_LOAD_C
 #undef TAO_STORE_C
 #undef TAO_C_SLOT
 #undef TAO_C_CHUNK
+    __syncthreads();   // the next pass's setup reuses the staging buffers
+  }
+
   // ---- epilogue: fine = r(r(num) / r(den)), the coarse read, the fusion.
   if (!reads) return;
   const bool coarse_on = COARSE && cpages >= 1;
@@ -473,10 +477,20 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
           gb[kk] = *(const uint4*)(gc + (size_t)e * D + 16 * kk + 8 * hl);
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk)
-          cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              as_bf16x8(*(const uint4*)&sm.hq[w][li][16 * kk + 8 * hl]), as_bf16x8(gb[kk]),
-              cacc, 0, 0, 0);
+          cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(hA[kk]), as_bf16x8(gb[kk]),
+                                                         cacc, 0, 0, 0);
       }
+    }
+    // Every operand of the 16 outputs first (rows past the tile clamped),
+    // so the loads are in flight together rather than one round trip per
+    // output behind the previous output's store.
+    float lv[16], xv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int q = min(8 * (i / 4) + 4 * hl + (i % 4), nq - 1);
+      const int tq = q_first + q;
+      lv[i] = bf2f(p.local[(((size_t)b * p.T + tq) * p.H + h) * D + e]);
+      xv[i] = bf2f(p.rq.p[b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + e]);
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -490,10 +504,393 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
           p.save_coarse[row * D + e] = f2bf(rbf(cacc[i]));
           if (e == 0) p.save_den[row] = rbf(acc_den[i]);
         }
-        const float local = bf2f(p.local[(((size_t)b * p.T + tq) * p.H + h) * D + e]);
-        const float x = bf2f(p.rq.p[b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + e]);
         p.out[b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + e] =
-            fuse_element(x, local, rbf(cacc[i]), fine, ae, be, p.gain, coarse_on ? 1 : 0, 1);
+            fuse_element(xv[i], lv[i], rbf(cacc[i]), fine, ae, be, p.gain, coarse_on ? 1 : 0, 1);
+      }
+    }
+  };
+  static_assert(ET == 2 || ET == 4, "head width 64 or 128");
+  emit(acc[0], 0);
+  emit(acc[1], 1);
+  if constexpr (ET == 4) {
+    emit(acc[2], 2);
+    emit(acc[3], 3);
+  }
+}
+
+
+// ---- Turn-route read with a ring of fines staged by direct loads into LDS.
+//
+// read_stream_kernel serves the prefill (turn routes; per-query routes take
+// read_groups_kernel). It is read_groups_kernel's turn-group read with the
+// staging replaced: each fine's C^T goes from HBM straight into one of
+// kRing LDS slots (global_load_lds_dwordx4: lane i of a wave writes 16
+// bytes at the slot's base + 16 i, so the lane picks which global chunk
+// lands there; rows are stored with their 16-byte chunks XOR-swizzled by the
+// row index, which keeps the B-operand reads free of bank conflicts), and
+// fine u + kRing - 1 is loaded while fine u is consumed. Wave 0 also moves
+// the fine's pw and sw rows into LDS and turns them into the fine's weights
+// w = r(pw * sw) one iteration before the fine is read. A selecting wave's
+// A operand is r(h * w) (its queries' h in fp32 registers), so den[q] is
+// A against a column of ones as before. One barrier per fine.
+//
+// The ring and the staged weight rows are LDS written by the loads
+// themselves, which the compiler cannot order against its own LDS reads: it
+// would drain every load in flight before each read and each barrier. So
+// the kernel reads them with explicit ds_read_b128 and orders them itself:
+// a wave waits for its own loads of a fine (s_waitcnt vmcnt) before the
+// barrier that publishes it, and for its reads (lgkmcnt) before using them.
+constexpr int kRing = 4;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int D>
+struct StreamSmem {
+  uint32_t bits[kBitWords];
+  int pre[kBitWords];
+  bf16_t wr[kRing][D];               // per slot: the fine's weights r(pw * sw)
+  int ids[kGroupWaves][kMaxM];
+  int uni[kMaxUnion];
+  uint32_t mask[kMaxUnion / 4];
+  int n_union;
+  int erels[kGroupWaves];
+};
+
+// s_waitcnt with vmcnt <= N (expcnt and lgkmcnt not waited for).
+template <int N>
+TAO_DEV void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// This wave's loads of the fine issued `after` fines before the latest have
+// completed: per fine, a wave issues PER loads.
+template <int PER>
+TAO_DEV void wait_fines(int after) {
+  if (after <= 0) wait_vmcnt<0>();
+  else if (after == 1) wait_vmcnt<PER>();
+  else wait_vmcnt<2 * PER>();
+}
+
+// 16 bytes from LDS byte address `addr`, not waited for.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+TAO_DEV u32x4 lds_read16(uint32_t addr) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+// s_waitcnt lgkmcnt(0), tied to the values it makes ready (so nothing that
+// reads them is scheduled above it).
+TAO_DEV void wait_lds(u32x4& a, u32x4& b) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b)::"memory");
+}
+TAO_DEV void wait_lds(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)::"memory");
+}
+TAO_DEV uint4 as_uint4(const u32x4& v) { return make_uint4(v.x, v.y, v.z, v.w); }
+TAO_DEV void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+TAO_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+template <int D, bool COARSE>
+__global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesParams p) {
+  constexpr int KK = D / 16, ET = D / 32, CPR = D / 8;   // k-steps, e-tiles, chunks per row
+  constexpr int CPT = D * CPR / (64 * kGroupWaves);      // 1 KB wave loads per fine and wave
+  static_assert(CPT * 64 * kGroupWaves == D * CPR, "whole wave loads per fine");
+  static_assert(kRing == 4, "wait_fines counts at most two fines in flight behind");
+  __shared__ StreamSmem<D> sm;
+  __shared__ __attribute__((aligned(16))) bf16_t ring[kRing][D * D];   // staged C^T, swizzled
+  __shared__ __attribute__((aligned(16))) bf16_t pwsw[kRing][2][D];     // staged pw and sw rows
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int grp = blockIdx.x / BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
+  const int t0 = grp * kGroupWaves;
+  const int nt = min(kGroupWaves, p.n_tiles - t0);
+
+  // This wave's tile.
+  int q_first = 0, nq = 0, slot = 0, M = 0, erel = 0, fine_on = 0, cpages = 0;
+  if (w < nt) {
+    const int64_t* desc = p.tiles + 8 * (t0 + w);
+    q_first = (int)desc[0]; nq = (int)desc[1]; slot = (int)desc[2]; M = (int)desc[3];
+    erel = (int)desc[4]; fine_on = (int)desc[6];
+    cpages = (int)desc[7];
+  }
+  const bool reads = w < nt && fine_on;
+  if (w < nt && !fine_on) {
+    // Before the first seal the output is the local attention.
+    for (int i = lane; i < nq * (D / 8); i += 64) {
+      const int q = i / (D / 8), c = i % (D / 8);
+      const int t = q_first + q;
+      *(uint4*)(p.out + b * p.out_sb + (int64_t)t * p.out_st + h * p.out_sh + c * 8) =
+          *(const uint4*)(p.local + (((size_t)b * p.T + t) * p.H + h) * D + c * 8);
+    }
+  }
+  if (lane == 0) sm.erels[w] = reads ? erel : -1;
+
+  // ---- h of this wave's queries in fp32, in the MFMA A layout: lane (li, hl)
+  // holds row q = li, channels d = 16 kk + 8 hl + j; rows past the tile are 0.
+  float hf[KK][8];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) hf[kk][j] = 0.0f;
+  if (reads) {
+    const int q = li < nq ? li : nq - 1;
+    const bf16_t* rq = p.rq.p + b * p.rq.sb + (int64_t)(q_first + q) * p.rq.st + h * p.rq.sh;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      unpack8f(*(const uint4*)(rq + 16 * kk + 8 * hl), hf[kk]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, hf[kk][j]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { hf[kk][j] = __expf(hf[kk][j] - mx); sum += hf[kk][j]; }
+    sum += __shfl_xor(sum, 32, 64);
+    // h = r(softmax); it only shapes the read, never a route.
+    const float inv = li < nq ? __builtin_amdgcn_rcpf(sum) : 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) hf[kk][j] = rbf(hf[kk][j] * inv);
+  }
+
+  floatx16 acc[ET];
+#pragma unroll
+  for (int t = 0; t < ET; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+  floatx16 acc_den;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc_den[i] = 0.0f;
+  const bf16x8 ones = as_bf16x8(make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u));
+
+  const bf16_t* bank = p.bank + (size_t)bh * p.fine_cap * D * D;
+  const bf16_t* sw_base = p.sw + (size_t)bh * p.fine_cap * D;
+  __syncthreads();   // sm.erels
+
+  // ---- one pass per distinct epoch of the group's reading tiles, ascending
+  for (int pass_erel = -1;;) {
+    int next = 0x7FFFFFFF;
+#pragma unroll
+    for (int v = 0; v < kGroupWaves; ++v) {
+      const int e = sm.erels[v];
+      if (e > pass_erel && e < next) next = e;
+    }
+    if (next == 0x7FFFFFFF) break;
+    pass_erel = next;
+    const bool in_pass = reads && erel == pass_erel;
+    const int pass_epoch = p.first_epoch + pass_erel;
+    const int sw_split = (pass_epoch / p.group) * p.group;
+    const bf16_t* pw_base = p.pw_pool + ((size_t)pass_erel * BH + bh) * p.pool_pcap * D;
+    const bf16_t* psw_base =
+        p.psw_pool ? p.psw_pool + ((size_t)pass_erel * BH + bh) * 8 * D : nullptr;
+
+    // ---- union of the pass's selected sets (ascending fine id), per-wave masks
+    for (int i = tid; i < kBitWords; i += kGroupThreads) sm.bits[i] = 0;
+    for (int i = tid; i < kMaxUnion / 4; i += kGroupThreads) sm.mask[i] = 0;
+    if (in_pass) {
+      const int32_t* sel = p.sel_pool + ((size_t)slot * BH + bh) * p.sel_cap;
+      for (int m = lane; m < M; m += 64) sm.ids[w][m] = sel[m];
+    }
+    __syncthreads();
+    if (in_pass)
+      for (int m = lane; m < M; m += 64) {
+        const int id = sm.ids[w][m];
+        atomicOr(&sm.bits[id >> 5], 1u << (id & 31));
+      }
+    __syncthreads();
+    if (w == 0) {
+      constexpr int WPL = kBitWords / 64;
+      int cnt[WPL], total = 0;
+#pragma unroll
+      for (int i = 0; i < WPL; ++i) {
+        cnt[i] = __popc(sm.bits[lane * WPL + i]);
+        total += cnt[i];
+      }
+      int incl = total;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += v;
+      }
+      int run = incl - total;
+#pragma unroll
+      for (int i = 0; i < WPL; ++i) { sm.pre[lane * WPL + i] = run; run += cnt[i]; }
+      if (lane == 63) sm.n_union = incl;
+    }
+    __syncthreads();
+    for (int i = tid; i < kBitWords; i += kGroupThreads) {
+      uint32_t bits = sm.bits[i];
+      int r = sm.pre[i];
+      while (bits) {
+        sm.uni[r++] = i * 32 + __ffs(bits) - 1;
+        bits &= bits - 1;
+      }
+    }
+    if (in_pass)
+      for (int m = lane; m < M; m += 64) {
+        const int id = sm.ids[w][m];
+        const uint32_t word = sm.bits[id >> 5];
+        const int rank = sm.pre[id >> 5] + __popc(word & ((1u << (id & 31)) - 1u));
+        atomicOr(&sm.mask[rank >> 2], 1u << ((rank & 3) * 8 + w));
+      }
+    __syncthreads();
+    const int U = sm.n_union;
+
+    // ---- stream the union through the ring
+    auto issue = [&](int f) __attribute__((always_inline)) {
+      const int s = f % kRing;
+      const int fid = sm.uni[f];
+      const bf16_t* base = bank + (size_t)fid * D * D;
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int J = w * CPT + i;            // this wave's 1 KB block of the slot
+        const int L = J * 64 + lane;          // 16-byte chunk index in the slot
+        const int row = L / CPR, pos = L % CPR;
+        __builtin_amdgcn_global_load_lds(base + (size_t)row * D + (pos ^ (row % CPR)) * 8,
+                                         (lds_void_t*)(&ring[s][0] + J * 64 * 8), 16, 0, 0);
+      }
+      if (w == 0 && lane < 2 * CPR) {
+        const bf16_t* src =
+            lane < CPR ? pw_base + (size_t)(fid / p.group) * D + lane * 8
+                       : (fid < sw_split ? sw_base + (size_t)fid * D
+                                         : psw_base + (size_t)(fid - sw_split) * D) +
+                             (lane - CPR) * 8;
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)&pwsw[s][0][0], 16, 0, 0);
+      }
+    };
+    // Waits until this wave's loads of the fine `after` fines behind the
+    // latest issued have landed.
+    auto wait_behind = [&](int after) __attribute__((always_inline)) {
+      if (w == 0) wait_fines<CPT + 1>(after);
+      else wait_fines<CPT>(after);
+    };
+    // Wave 0 turns the fine's pw and sw rows into its weights.
+    auto make_wr = [&](int f) __attribute__((always_inline)) {
+      const int s = f % kRing;
+      if (w == 0 && lane < CPR) {
+        u32x4 pwv = lds_read16(lds_addr(&pwsw[s][0][lane * 8]));
+        u32x4 swv = lds_read16(lds_addr(&pwsw[s][1][lane * 8]));
+        wait_lds(pwv, swv);
+        *(uint4*)&sm.wr[s][lane * 8] = slice_weights(as_uint4(pwv), as_uint4(swv));
+      }
+    };
+    auto consume = [&](int u) __attribute__((always_inline)) {
+      if (!(in_pass && ((sm.mask[u >> 2] >> ((u & 3) * 8 + w)) & 1u))) return;
+      const int s = u % kRing;
+      const uint32_t cs = lds_addr(&ring[s][0]);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const int c = 2 * kk + hl;             // logical chunk of d0 = 16 kk + 8 hl
+        u32x4 bq[ET];
+#pragma unroll
+        for (int t = 0; t < ET; ++t) {
+          const int row = 32 * t + li;
+          bq[t] = lds_read16(cs + (uint32_t)(row * D + 8 * (c ^ (row % CPR))) * 2);
+        }
+        float wv[8];
+        unpack8f(*(const uint4*)&sm.wr[s][8 * c], wv);
+        const bf16x8 a = as_bf16x8(make_uint4(
+            pack_bf16x2(hf[kk][0] * wv[0], hf[kk][1] * wv[1]),
+            pack_bf16x2(hf[kk][2] * wv[2], hf[kk][3] * wv[3]),
+            pack_bf16x2(hf[kk][4] * wv[4], hf[kk][5] * wv[5]),
+            pack_bf16x2(hf[kk][6] * wv[6], hf[kk][7] * wv[7])));
+        if constexpr (ET == 4) wait_lds(bq[0], bq[1], bq[2], bq[3]);
+        else wait_lds(bq[0], bq[1]);
+#pragma unroll
+        for (int t = 0; t < ET; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(as_uint4(bq[t])), acc[t],
+                                                           0, 0, 0);
+        acc_den = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, ones, acc_den, 0, 0, 0);
+      }
+    };
+    // Barrier that publishes the ring: the caller has waited for its own
+    // loads; the weights written by wave 0 are ordinary LDS stores.
+    auto ring_barrier = [&]() __attribute__((always_inline)) {
+      wait_lds();
+      __builtin_amdgcn_s_barrier();
+    };
+    const int pre = min(U, kRing - 1);
+    for (int f = 0; f < pre; ++f) issue(f);
+    if (U > 0) {
+      wait_behind(pre - 1);
+      make_wr(0);
+    }
+    ring_barrier();
+    for (int u = 0; u < U; ++u) {
+      if (u + kRing - 1 < U) issue(u + kRing - 1);
+      consume(u);
+      if (u + 1 < U) {
+        wait_behind(min(U - 1, u + kRing - 1) - (u + 1));
+        make_wr(u + 1);
+      }
+      ring_barrier();
+    }
+    wait_vmcnt<0>();
+    __syncthreads();   // the next pass's setup
+  }
+
+  // ---- epilogue: fine = r(r(num) / r(den)), the coarse read, the fusion.
+  if (!reads) return;
+  const bool coarse_on = COARSE && cpages >= 1;
+  const bf16_t* gc =
+      coarse_on ? p.coarse_pool + ((size_t)(cpages - p.coarse_first) * BH + bh) * D * D : nullptr;
+  auto emit = [&](const floatx16& av, int t) __attribute__((always_inline)) {
+    const int e = 32 * t + li;
+    float ae[3], be[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      ae[i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + e * p.fa_s[1] + i * p.fa_s[2]);
+      be[i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + e * p.fb_s[1] + i * p.fb_s[2]);
+    }
+    floatx16 cacc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) cacc[i] = 0.0f;
+    if constexpr (COARSE) {
+      if (coarse_on) {
+        uint4 gb[KK];
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+          gb[kk] = *(const uint4*)(gc + (size_t)e * D + 16 * kk + 8 * hl);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          const bf16x8 a = as_bf16x8(make_uint4(
+              pack_bf16x2(hf[kk][0], hf[kk][1]), pack_bf16x2(hf[kk][2], hf[kk][3]),
+              pack_bf16x2(hf[kk][4], hf[kk][5]), pack_bf16x2(hf[kk][6], hf[kk][7])));
+          cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(gb[kk]), cacc, 0, 0, 0);
+        }
+      }
+    }
+    float lv[16], xv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int q = min(8 * (i / 4) + 4 * hl + (i % 4), nq - 1);
+      const int tq = q_first + q;
+      lv[i] = bf2f(p.local[(((size_t)b * p.T + tq) * p.H + h) * D + e]);
+      xv[i] = bf2f(p.rq.p[b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + e]);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int q = 8 * (i / 4) + 4 * hl + (i % 4);
+      if (q < nq) {
+        const int tq = q_first + q;
+        const float fine = rbf(rbf(av[i]) * __builtin_amdgcn_rcpf(rbf(acc_den[i])));
+        const size_t row = ((size_t)b * p.T + tq) * p.H + h;
+        if (p.save_fine) {
+          p.save_fine[row * D + e] = f2bf(fine);
+          p.save_coarse[row * D + e] = f2bf(rbf(cacc[i]));
+          if (e == 0) p.save_den[row] = rbf(acc_den[i]);
+        }
+        p.out[b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + e] =
+            fuse_element(xv[i], lv[i], rbf(cacc[i]), fine, ae, be, p.gain, coarse_on ? 1 : 0, 1);
       }
     }
   };
@@ -546,21 +943,24 @@ hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t
   if (perq && (p.qsel_words < 1 || p.qsel_words > kBitWords)) return hipErrorInvalidValue;
 #define TAO_READ_LAUNCH(D_, C_, Q_)                                                           \
   hipLaunchKernelGGL((read_groups_kernel<D_, C_, Q_>), grid, dim3(kGroupThreads), 0, s, p)
+#define TAO_STREAM_LAUNCH(D_, C_)                                                             \
+  hipLaunchKernelGGL((read_stream_kernel<D_, C_>), grid, dim3(kGroupThreads), 0, s, p)
   if (head_dim != 128 && head_dim != 64) return hipErrorInvalidValue;
   if (head_dim == 128) {
     if (perq) {
       if (coarse) TAO_READ_LAUNCH(128, true, true); else TAO_READ_LAUNCH(128, false, true);
     } else {
-      if (coarse) TAO_READ_LAUNCH(128, true, false); else TAO_READ_LAUNCH(128, false, false);
+      if (coarse) TAO_STREAM_LAUNCH(128, true); else TAO_STREAM_LAUNCH(128, false);
     }
   } else {
     if (perq) {
       if (coarse) TAO_READ_LAUNCH(64, true, true); else TAO_READ_LAUNCH(64, false, true);
     } else {
-      if (coarse) TAO_READ_LAUNCH(64, true, false); else TAO_READ_LAUNCH(64, false, false);
+      if (coarse) TAO_STREAM_LAUNCH(64, true); else TAO_STREAM_LAUNCH(64, false);
     }
   }
 #undef TAO_READ_LAUNCH
+#undef TAO_STREAM_LAUNCH
   return hipGetLastError();
 }
 

@@ -547,7 +547,7 @@ template <int D>
 struct StreamSmem {
   uint32_t bits[kBitWords];
   int pre[kBitWords];
-  bf16_t wr[kRing][D];               // per slot: the fine's weights r(pw * sw)
+  float wf[kRing][D];                // per slot: the fine's weights r(pw * sw), widened
   int ids[kGroupWaves][kMaxM];
   int uni[kMaxUnion];
   uint32_t mask[kMaxUnion / 4];
@@ -586,6 +586,13 @@ TAO_DEV void wait_lds(u32x4& a, u32x4& b) {
 TAO_DEV void wait_lds(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)::"memory");
 }
+// s_waitcnt lgkmcnt(N): every LDS read but the newest N has landed, which
+// covers a and b when N reads were issued after them.
+template <int N>
+TAO_DEV void wait_lds_behind(u32x4& a, u32x4& b) {
+  if constexpr (N == 4) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(a), "+v"(b)::"memory");
+  else asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(a), "+v"(b)::"memory");
+}
 TAO_DEV uint4 as_uint4(const u32x4& v) { return make_uint4(v.x, v.y, v.z, v.w); }
 TAO_DEV void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 TAO_DEV uint32_t lds_addr(const void* p) {
@@ -599,7 +606,12 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
   static_assert(CPT * 64 * kGroupWaves == D * CPR, "whole wave loads per fine");
   static_assert(kRing == 4, "wait_fines counts at most two fines in flight behind");
   __shared__ StreamSmem<D> sm;
-  __shared__ __attribute__((aligned(16))) bf16_t ring[kRing][D * D];   // staged C^T, swizzled
+  // The ring of staged C^T (swizzled rows); after the last pass, each wave's
+  // fine and coarse tiles for the epilogue's transpose.
+  constexpr int kRingElems = kRing * D * D, kEpiElems = kGroupWaves * 2 * 32 * D;
+  __shared__ __attribute__((aligned(16))) bf16_t ring_mem[kRingElems > kEpiElems ? kRingElems
+                                                                                 : kEpiElems];
+  bf16_t (*ring)[D * D] = reinterpret_cast<bf16_t (*)[D * D]>(ring_mem);
   __shared__ __attribute__((aligned(16))) bf16_t pwsw[kRing][2][D];     // staged pw and sw rows
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
@@ -780,36 +792,58 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
         u32x4 pwv = lds_read16(lds_addr(&pwsw[s][0][lane * 8]));
         u32x4 swv = lds_read16(lds_addr(&pwsw[s][1][lane * 8]));
         wait_lds(pwv, swv);
-        *(uint4*)&sm.wr[s][lane * 8] = slice_weights(as_uint4(pwv), as_uint4(swv));
+        float wv[8];
+        unpack8f(slice_weights(as_uint4(pwv), as_uint4(swv)), wv);
+        *(float4*)&sm.wf[s][lane * 8] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+        *(float4*)&sm.wf[s][lane * 8 + 4] = make_float4(wv[4], wv[5], wv[6], wv[7]);
       }
     };
     auto consume = [&](int u) __attribute__((always_inline)) {
       if (!(in_pass && ((sm.mask[u >> 2] >> ((u & 3) * 8 + w)) & 1u))) return;
       const int s = u % kRing;
       const uint32_t cs = lds_addr(&ring[s][0]);
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
+      const uint32_t ws = lds_addr(&sm.wf[s][8 * hl]);
+      // The operands of step kk + 1 (the weights at d = 16 kk + 8 hl, then the
+      // C^T rows e = 32 t + li there) are read while step kk's MFMAs run; step
+      // kk + 1 waits for its weights, builds its A operand while its rows land,
+      // then waits for those.
+      auto reads = [&](int kk, u32x4(&bq)[ET], u32x4& w0, u32x4& w1) __attribute__((always_inline)) {
         const int c = 2 * kk + hl;             // logical chunk of d0 = 16 kk + 8 hl
-        u32x4 bq[ET];
+        w0 = lds_read16(ws + 64 * kk);
+        w1 = lds_read16(ws + 64 * kk + 16);
 #pragma unroll
         for (int t = 0; t < ET; ++t) {
           const int row = 32 * t + li;
           bq[t] = lds_read16(cs + (uint32_t)(row * D + 8 * (c ^ (row % CPR))) * 2);
         }
-        float wv[8];
-        unpack8f(*(const uint4*)&sm.wr[s][8 * c], wv);
+      };
+      u32x4 bq[ET], w0, w1;
+      reads(0, bq, w0, w1);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        wait_lds_behind<ET>(w0, w1);
         const bf16x8 a = as_bf16x8(make_uint4(
-            pack_bf16x2(hf[kk][0] * wv[0], hf[kk][1] * wv[1]),
-            pack_bf16x2(hf[kk][2] * wv[2], hf[kk][3] * wv[3]),
-            pack_bf16x2(hf[kk][4] * wv[4], hf[kk][5] * wv[5]),
-            pack_bf16x2(hf[kk][6] * wv[6], hf[kk][7] * wv[7])));
+            pack_bf16x2(hf[kk][0] * __uint_as_float(w0.x), hf[kk][1] * __uint_as_float(w0.y)),
+            pack_bf16x2(hf[kk][2] * __uint_as_float(w0.z), hf[kk][3] * __uint_as_float(w0.w)),
+            pack_bf16x2(hf[kk][4] * __uint_as_float(w1.x), hf[kk][5] * __uint_as_float(w1.y)),
+            pack_bf16x2(hf[kk][6] * __uint_as_float(w1.z), hf[kk][7] * __uint_as_float(w1.w))));
         if constexpr (ET == 4) wait_lds(bq[0], bq[1], bq[2], bq[3]);
         else wait_lds(bq[0], bq[1]);
+        u32x4 bn[ET], n0, n1;
+        if (kk + 1 < KK) reads(kk + 1, bn, n0, n1);
+        // num^T[e][q]: the C^T rows are the A operand, so lane li ends up
+        // holding query li (and den[li] in every element of acc_den).
 #pragma unroll
         for (int t = 0; t < ET; ++t)
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(as_uint4(bq[t])), acc[t],
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(as_uint4(bq[t])), a, acc[t],
                                                            0, 0, 0);
-        acc_den = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, ones, acc_den, 0, 0, 0);
+        acc_den = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, a, acc_den, 0, 0, 0);
+        if (kk + 1 < KK) {
+#pragma unroll
+          for (int t = 0; t < ET; ++t) bq[t] = bn[t];
+          w0 = n0;
+          w1 = n1;
+        }
       }
     };
     // Barrier that publishes the ring: the caller has waited for its own
@@ -839,67 +873,100 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
   }
 
   // ---- epilogue: fine = r(r(num) / r(den)), the coarse read, the fusion.
+  // Lane li holds query li's values for e = 32 t + 8 g + 4 hl + (0..3). They
+  // go through this wave's part of the (now idle) ring as [q][e] tiles whose
+  // 16-byte units are XOR-swizzled by the row, so the fusion reads whole
+  // 8-channel units and loads and stores 16 bytes per lane.
   if (!reads) return;
   const bool coarse_on = COARSE && cpages >= 1;
   const bf16_t* gc =
       coarse_on ? p.coarse_pool + ((size_t)(cpages - p.coarse_first) * BH + bh) * D * D : nullptr;
-  auto emit = [&](const floatx16& av, int t) __attribute__((always_inline)) {
-    const int e = 32 * t + li;
-    float ae[3], be[3];
+  bf16_t* tile_f = ring_mem + (size_t)w * 2 * 32 * D;
+  bf16_t* tile_c = tile_f + 32 * D;
+  const float den = acc_den[0];
+  const float rden = __builtin_amdgcn_rcpf(rbf(den));
+  if (p.save_fine && hl == 0 && li < nq) p.save_den[((size_t)b * p.T + q_first + li) * p.H + h] = rbf(den);
+  auto unit_at = [&](int row, int unit) __attribute__((always_inline)) {
+    return row * D + 8 * (unit ^ (row % CPR));
+  };
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      ae[i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + e * p.fa_s[1] + i * p.fa_s[2]);
-      be[i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + e * p.fb_s[1] + i * p.fb_s[2]);
+  for (int t = 0; t < ET; ++t) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int at = unit_at(li, 4 * t + g) + 4 * hl;
+      float f[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) f[k] = rbf(rbf(acc[t][4 * g + k]) * rden);
+      *(uint2*)&tile_f[at] = make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]));
     }
-    floatx16 cacc;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) cacc[i] = 0.0f;
     if constexpr (COARSE) {
       if (coarse_on) {
+        floatx16 cacc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) cacc[i] = 0.0f;
         uint4 gb[KK];
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk)
-          gb[kk] = *(const uint4*)(gc + (size_t)e * D + 16 * kk + 8 * hl);
+          gb[kk] = *(const uint4*)(gc + (size_t)(32 * t + li) * D + 16 * kk + 8 * hl);
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
           const bf16x8 a = as_bf16x8(make_uint4(
               pack_bf16x2(hf[kk][0], hf[kk][1]), pack_bf16x2(hf[kk][2], hf[kk][3]),
               pack_bf16x2(hf[kk][4], hf[kk][5]), pack_bf16x2(hf[kk][6], hf[kk][7])));
-          cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(gb[kk]), cacc, 0, 0, 0);
+          cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(gb[kk]), a, cacc, 0, 0, 0);
         }
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *(uint2*)&tile_c[unit_at(li, 4 * t + g) + 4 * hl] =
+              make_uint2(pack_bf16x2(cacc[4 * g], cacc[4 * g + 1]),
+                         pack_bf16x2(cacc[4 * g + 2], cacc[4 * g + 3]));
       }
     }
-    float lv[16], xv[16];
+  }
+  // Row phase: lane (row r, unit c) fuses channels 8 c .. 8 c + 7 of query r.
+  constexpr int RPI = 64 / CPR;                 // rows per pass of the wave
+  const int c = lane % CPR;
+  float ae[8][3], be[8][3];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int q = min(8 * (i / 4) + 4 * hl + (i % 4), nq - 1);
-      const int tq = q_first + q;
-      lv[i] = bf2f(p.local[(((size_t)b * p.T + tq) * p.H + h) * D + e]);
-      xv[i] = bf2f(p.rq.p[b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + e]);
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      ae[j][i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + (8 * c + j) * p.fa_s[1] + i * p.fa_s[2]);
+      be[j][i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + (8 * c + j) * p.fb_s[1] + i * p.fb_s[2]);
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int q = 8 * (i / 4) + 4 * hl + (i % 4);
-      if (q < nq) {
-        const int tq = q_first + q;
-        const float fine = rbf(rbf(av[i]) * __builtin_amdgcn_rcpf(rbf(acc_den[i])));
-        const size_t row = ((size_t)b * p.T + tq) * p.H + h;
-        if (p.save_fine) {
-          p.save_fine[row * D + e] = f2bf(fine);
-          p.save_coarse[row * D + e] = f2bf(rbf(cacc[i]));
-          if (e == 0) p.save_den[row] = rbf(acc_den[i]);
-        }
-        p.out[b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + e] =
-            fuse_element(xv[i], lv[i], rbf(cacc[i]), fine, ae, be, p.gain, coarse_on ? 1 : 0, 1);
-      }
+  for (int it = 0; it < 32 / RPI; ++it) {
+    const int r = lane / CPR + RPI * it;
+    if (r >= nq) break;
+    const int tq = q_first + r;
+    const size_t row = ((size_t)b * p.T + tq) * p.H + h;
+    const uint4 fu = *(const uint4*)&tile_f[unit_at(r, c)];
+    uint4 cu = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (COARSE) {
+      if (coarse_on) cu = *(const uint4*)&tile_c[unit_at(r, c)];
     }
-  };
-  static_assert(ET == 2 || ET == 4, "head width 64 or 128");
-  emit(acc[0], 0);
-  emit(acc[1], 1);
-  if constexpr (ET == 4) {
-    emit(acc[2], 2);
-    emit(acc[3], 3);
+    const uint4 lu = *(const uint4*)(p.local + row * D + 8 * c);
+    const uint4 xu = *(const uint4*)(p.rq.p + b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + 8 * c);
+    float fv[8], cv[8], lv[8], xv[8];
+    unpack8f(fu, fv);
+    unpack8f(cu, cv);
+    unpack8f(lu, lv);
+    unpack8f(xu, xv);
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16_t lo = fuse_element(xv[2 * j], lv[2 * j], cv[2 * j], fv[2 * j], ae[2 * j], be[2 * j],
+                                     p.gain, coarse_on ? 1 : 0, 1);
+      const bf16_t hi = fuse_element(xv[2 * j + 1], lv[2 * j + 1], cv[2 * j + 1], fv[2 * j + 1],
+                                     ae[2 * j + 1], be[2 * j + 1], p.gain, coarse_on ? 1 : 0, 1);
+      o[j] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+    *(uint4*)(p.out + b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + 8 * c) =
+        make_uint4(o[0], o[1], o[2], o[3]);
+    if (p.save_fine) {
+      *(uint4*)(p.save_fine + row * D + 8 * c) = fu;
+      *(uint4*)(p.save_coarse + row * D + 8 * c) = cu;
+    }
   }
 }
 

@@ -389,7 +389,7 @@ def run_model(torch, args, device, cfg):
     all 12 layers. Context only: the published whole-model figures are from
     another GPU and model weights."""
     import torch.nn.functional as F
-    from tao_attention import new_state, tao_attention_decode
+    from tao_attention import WholeStepGraph, new_state, tao_attention_decode
     L, width, heads, dim, vocab = 12, 768, 6, 128, 32768
     g = torch.Generator(device=device).manual_seed(17)
 
@@ -410,24 +410,27 @@ def run_model(torch, args, device, cfg):
         del xs
         states.append(st)
     inv = 1.0 / (10000.0 ** (torch.arange(0, dim, 2, device=device).float() / dim))
-    span = torch.arange(ctx, ctx + args.model_steps + 16, device=device).float()[:, None] * inv
+    span = torch.arange(ctx, ctx + 2 * args.model_steps + 32, device=device).float()[:, None] * inv
     cos_t = torch.cat((span.cos(), span.cos()), -1).to(torch.bfloat16)
     sin_t = torch.cat((-span.sin(), span.sin()), -1).to(torch.bfloat16)
 
-    def rope(x, pos):
+    def rope(x, row):
         # rotate-half RoPE from precomputed tables: x * cos + swap(x) * (-sin, sin)
-        return x * cos_t[pos - ctx] + x.roll(dim // 2, -1) * sin_t[pos - ctx]
+        return (x * cos_t.index_select(0, row) + x.roll(dim // 2, -1) * sin_t.index_select(0, row))
 
     def step(token):
-        x = embed[token].view(1, 1, width)
+        # Positions come from each state's device cursor, so the same step
+        # runs eagerly and as a captured whole-step graph.
+        x = embed.index_select(0, token.view(1)).view(1, 1, width)
         for lw, st in zip(layers, states):
-            pos = st.get_pos()
+            row = (st.device_position() - ctx).view(1)
             h = F.rms_norm(x, (width,))
             raw_q, raw_k, v = (h @ lw["qkv"]).view(1, 1, 3, heads, dim).unbind(2)
-            q = rope(F.rms_norm(raw_q, (dim,)), pos)
-            k = rope(F.rms_norm(raw_k, (dim,)), pos)
+            q = rope(F.rms_norm(raw_q, (dim,)), row)
+            k = rope(F.rms_norm(raw_k, (dim,)), row)
             a, _ = tao_attention_decode(q, k, v, raw_q=raw_q, raw_k=raw_k, fusion_a=lw["fa"],
-                                        fusion_b=lw["fb"], alpha=0.5, state=st, position=pos)
+                                        fusion_b=lw["fb"], alpha=0.5, state=st,
+                                        position=st.get_pos())
             x = x + a.reshape(1, 1, width) @ lw["o"]
             h = F.rms_norm(x, (width,))
             x = x + F.relu(h @ lw["up"]).square() @ lw["down"]
@@ -442,9 +445,25 @@ def run_model(torch, args, device, cfg):
         token = step(token)
     torch.cuda.synchronize()
     seconds = time.perf_counter() - t0
+    # The same decode continued through one captured graph of the whole
+    # step (WholeStepGraph): refresh and seal tokens still run eagerly.
+    graph = WholeStepGraph(states)
+    for _ in range(8):
+        token = graph.step(step, token)
+    torch.cuda.synchronize()
+    r0, e0 = graph.replays, graph.eager_steps
+    t0 = time.perf_counter()
+    for _ in range(args.model_steps):
+        token = graph.step(step, token)
+    torch.cuda.synchronize()
+    graph_seconds = time.perf_counter() - t0
+    replays, eager = graph.replays - r0, graph.eager_steps - e0
+    graph.release()
     for st in states:
         st.release_execution()
-    return {"tok_s": args.model_steps / seconds, "seconds": seconds}
+    return {"tok_s": args.model_steps / seconds, "seconds": seconds,
+            "graph_tok_s": args.model_steps / graph_seconds, "graph_replays": replays,
+            "graph_eager_steps": eager}
 
 
 def run_prefill(torch, device, cfg, heads, width, tokens, probe):
@@ -912,11 +931,17 @@ def main():
                      "published benchmark shape), random bf16 weights, batch 1",
             "context": args.model_context, "steps": args.model_steps,
             "tok_s": round(md["tok_s"], 1),
-            "note": "caller-side greedy decode through all 12 layers (eager, "
-                    "index_only_page_memo); the reference publishes 107.192 tok/s (memo) and "
+            "whole_step_graph_tok_s": round(md["graph_tok_s"], 1),
+            "whole_step_graph_tokens": {"replayed": md["graph_replays"],
+                                        "eager (refresh/seal/capture)": md["graph_eager_steps"]},
+            "note": "caller-side greedy decode through all 12 layers (eager, then the same "
+                    "decode continued through one captured graph of the whole step, "
+                    "WholeStepGraph; index_only_page_memo); the reference publishes 107.192 "
+                    "tok/s (memo) and "
                     "123.816 tok/s (memo + regional graph) at 128K for its trained model on an "
                     "RTX 4090 (docs/benchmarks.md:94): context, not a like-for-like baseline"}
-        log(f"whole-model decode: {md['tok_s']:.1f} tok/s at {args.model_context} context")
+        log(f"whole-model decode: {md['tok_s']:.1f} tok/s eager, {md['graph_tok_s']:.1f} tok/s "
+            f"whole-step graph at {args.model_context} context")
     if not args.no_full_sequence:
         log("full-sequence read (tao_attention forward, configs[1] shape)")
         fs = run_full_sequence(torch, args, device)

@@ -436,6 +436,26 @@ int tao_stream_sync(void* handle, const tao_state_dev* st, int64_t position,
  * route size, refreshed, sealed, heads in out_stage (replay), captured. */
 int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu, void* out,
                       const int64_t* out_s, void* stream, int64_t* info);
+/* Device-cursor steps for a caller's whole-step graph across layers (the
+ * caller-side multi-layer decode of docs/benchmarks.md:15, 89-94; no
+ * reference entry point: the reference captures one layer's region only,
+ * history_region_graph.py:95-113).
+ * tao_stream_plan_step: the driver's next token. info (int64[6]) receives
+ *   its position, whether a route refresh is due before its step, whether a
+ *   seal is due after it, the route size its step reads, and the fine and
+ *   coarse presence flags of its fusion.
+ * tao_stream_graph_step: launches the next token's decode step with the
+ *   cursor read on the device (header[0], advanced by the step), so a
+ *   caller may capture it in a hipGraph and replay it for successive plain
+ *   tokens (no refresh before, no seal after: the caller checks with
+ *   tao_stream_plan_step and runs other tokens through tao_stream_decode).
+ *   Fails for a token that is not plain. The host cursor does not move.
+ * tao_stream_advance: moves the host cursor over `count` plain tokens that
+ *   ran as device-cursor steps (fails if one of them is not plain). */
+int tao_stream_plan_step(void* handle, int64_t* info);
+int tao_stream_graph_step(void* handle, const tao_tokens* tok, const tao_fusion* fu, void* out,
+                          const int64_t* out_s, void* stream);
+int tao_stream_advance(void* handle, int64_t count);
 /* Batched decode of `count` independent requests of one layer (no reference
  * counterpart: the reference decodes one request per call; this serves
  * many streams, BASELINE config 5, with one decode step launch pair).

@@ -353,6 +353,66 @@ int tao_stream_sync(void* handle, const tao_state_dev* st, int64_t position,
   return TAO_OK;
 }
 
+namespace {
+
+// The token at `pos` is a plain step: no route refresh before it and no seal
+// after it, so its whole work is the decode step.
+bool plain_at(const tao_stream_cfg& c, int64_t pos) {
+  const bool refresh = fines_at(c, pos) > 0 && is_turn(c, pos);
+  const bool seal = local_len_at(c, pos) + 1 == c.local_keep + c.fine_tokens;
+  return !refresh && !seal;
+}
+
+// The fusion flags of a step at `pos` (as tao_stream_decode sets them).
+tao_fusion step_fusion(const Stream* s, const tao_fusion& fu, int64_t pos) {
+  const int64_t fines = fines_at(s->cfg, pos);
+  tao_fusion f = fu;
+  f.coarse_on = s->st.page_c != nullptr && fines >= s->cfg.coarse_group;
+  f.fine_on = fines > 0;
+  return f;
+}
+
+}  // namespace
+
+int tao_stream_plan_step(void* handle, int64_t* info) {
+  if (!handle || !info) return stream_fail(TAO_E_ARGUMENT, "null plan argument");
+  const Stream* s = (const Stream*)handle;
+  const tao_stream_cfg& c = s->cfg;
+  const int64_t pos = s->position, fines = fines_at(c, pos);
+  info[0] = pos;
+  info[1] = fines > 0 && is_turn(c, pos);
+  info[2] = local_len_at(c, pos) + 1 == c.local_keep + c.fine_tokens;
+  info[3] = fines > 0 ? s->route_size : 0;
+  info[4] = fines > 0;
+  info[5] = s->st.page_c != nullptr && fines >= c.coarse_group;
+  return TAO_OK;
+}
+
+int tao_stream_graph_step(void* handle, const tao_tokens* tok, const tao_fusion* fu, void* out,
+                          const int64_t* out_s, void* stream) {
+  if (!handle || !tok || !fu) return stream_fail(TAO_E_ARGUMENT, "null decode argument");
+  Stream* s = (Stream*)handle;
+  if (!plain_at(s->cfg, s->position))
+    return stream_fail(TAO_E_ARGUMENT,
+                       "the next token refreshes its route or seals: it cannot be a device-cursor step");
+  const tao_fusion f = step_fusion(s, *fu, s->position);
+  const int32_t selected = fines_at(s->cfg, s->position) > 0 ? s->route_size : 0;
+  return tao::decode_step_at(&s->st, tok, &f, selected, out, out_s, stream, -1);
+}
+
+int tao_stream_advance(void* handle, int64_t count) {
+  if (!handle) return stream_fail(TAO_E_ARGUMENT, "null stream");
+  Stream* s = (Stream*)handle;
+  if (count < 0) return stream_fail(TAO_E_ARGUMENT, "negative step count");
+  for (int64_t i = 0; i < count; ++i)
+    if (!plain_at(s->cfg, s->position + i))
+      return stream_fail(TAO_E_ARGUMENT, "advance over a route refresh or a seal");
+  // A device-cursor step changes nothing the driver's graph epoch keys on.
+  epoch_advance(s, s->position + count);
+  s->position += count;
+  return TAO_OK;
+}
+
 int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu, void* out,
                       const int64_t* out_s, void* stream, int64_t* info) {
   if (!handle || !tok || !fu || !info) return stream_fail(TAO_E_ARGUMENT, "null decode argument");

@@ -8,6 +8,8 @@ from .operator import (new_state, tao_attention, tao_attention_decode,
                        tao_attention_decode_batch, tao_attention_prefill)
 from .tao_stream import StreamCache
 from .config import TaoConfig
+from .step_graph import WholeStepGraph
 
 __all__ = ["new_state", "tao_attention", "tao_attention_prefill",
-           "tao_attention_decode", "tao_attention_decode_batch", "StreamCache", "TaoConfig"]
+           "tao_attention_decode", "tao_attention_decode_batch", "StreamCache", "TaoConfig",
+           "WholeStepGraph"]

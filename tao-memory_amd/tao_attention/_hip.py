@@ -133,6 +133,10 @@ _SIGNATURES = {
     "tao_stream_sync": ([_vp, ctypes.POINTER(StateDev), _i64, _i32, _i32], _i32),
     "tao_stream_decode": ([_vp, ctypes.POINTER(Tokens), ctypes.POINTER(Fusion), _vp,
                            ctypes.POINTER(_i64), _vp, ctypes.POINTER(_i64)], _i32),
+    "tao_stream_plan_step": ([_vp, ctypes.POINTER(_i64)], _i32),
+    "tao_stream_graph_step": ([_vp, ctypes.POINTER(Tokens), ctypes.POINTER(Fusion), _vp,
+                               ctypes.POINTER(_i64), _vp], _i32),
+    "tao_stream_advance": ([_vp, _i64], _i32),
     "tao_stream_release": ([_vp], _i32),
     "tao_stream_invalidate": ([_vp, _i32], _i32),
     "tao_stream_graph_stats": ([_vp, ctypes.POINTER(_i64), _i32], _i32),

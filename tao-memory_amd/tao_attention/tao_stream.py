@@ -313,6 +313,8 @@ class StreamCache:
             self._graph_mode = _GRAPH_REPLAY[replay]
         self._first_fine = self.config.first_fine
         self._graph_buffers = None
+        self._capturing = False      # inside a WholeStepGraph capture (step_graph.py)
+        self._capture_keep = []      # operands of the captured step, kept for its graph
         self._log = []               # call log of the diagnostics counters
         self._run_open = False       # the last log entry is an open one-token run
         self._info = (ctypes.c_int64 * 7)()
@@ -619,6 +621,8 @@ class StreamCache:
         """
         if local_flash is not None:
             return self.prefill(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, local_flash)
+        if self._capturing:
+            return self._decode_captured(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
         nat = self._native
         if nat is not None and self.position < self._fast_limit and not self._handle_dirty:
             pos = self.position
@@ -710,6 +714,72 @@ class StreamCache:
         if rc:
             _hip.check(rc)
         return self._book(pos, bool(info[5]), out)
+
+    # ------------------------------------------------- caller whole-step graphs
+    def device_position(self):
+        """This request's cursor on the device: a 0-dim int64 view of the
+        state header that every decode step advances, so code captured in
+        a graph can derive per-token positions (RoPE) from it."""
+        if self._dev is None:
+            raise RuntimeError("the state has no device buffers yet")
+        return self._dev.header[0]
+
+    def _plan_next(self):
+        """The driver's view of the next token (tao_stream_plan_step), or
+        None while the driver is not bound to the current buffers."""
+        if self._handle is None or self._handle_dirty:
+            return None
+        info = (ctypes.c_int64 * 6)()
+        _hip.check(_hip.lib().tao_stream_plan_step(self._handle, info))
+        return tuple(info)
+
+    def _plain_next(self):
+        """The next token is a plain step: no route refresh before it and no
+        seal after it (tao_stream_plan_step)."""
+        info = self._plan_next()
+        return info is not None and info[0] == self.position and not info[1] and not info[2]
+
+    def _graph_key(self):
+        """What a captured device-cursor step bakes in: route size, fusion
+        presence flags and the state's device buffers."""
+        info = self._plan_next()
+        return (info[3], info[4], info[5], bytes(self._dev.struct)) if info else None
+
+    def _decode_captured(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
+        """The next token's decode step with the cursor read on the device
+        (tao_stream_graph_step), for a caller's stream capture; the host
+        cursor moves when the caller reports the replays (_advance_replayed)."""
+        shape = q.shape
+        if (k.shape, v.shape, raw_q.shape, raw_k.shape) != (shape, shape, shape, shape):
+            raise ValueError("q, k, v, raw_q and raw_k must share one [B, 1, H, D] shape")
+        self._check_supported(q)
+        if not self._plain_next():
+            raise RuntimeError("the next token is not a plain step; decode it eagerly")
+        q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
+        tok = _hip.tokens(q, k, v, raw_q, raw_k)
+        fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
+        out = torch.empty_like(q)
+        out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
+        index = q.device.index if q.device.index is not None else torch.cuda.current_device()
+        _hip.check(_hip.lib().tao_stream_graph_step(
+            self._handle, ctypes.byref(tok), ctypes.byref(fu), out.data_ptr(), out_s,
+            _hip.raw_stream(index)))
+        self._capture_keep.append((q, k, v, raw_q, raw_k, tok, fu, out_s))
+        return out
+
+    def _advance_replayed(self, count):
+        """Book `count` plain tokens that ran as replays of a captured
+        device-cursor step: driver cursor (tao_stream_advance), host cursor
+        and the counters a driver call would have moved."""
+        _hip.check(_hip.lib().tao_stream_advance(self._handle, count))
+        if not self._run_open:
+            self._open_run()
+        for _ in range(count):
+            if self.position >= self._first_fine:
+                self.fusion_pointwise_calls += 1
+            else:
+                self.fusion_no_history_local_returns += 1
+            self.position += 1
 
     def _book(self, pos, staged, out):
         """Cursor and counters after one driver call (info from the driver)."""

@@ -234,6 +234,26 @@ def selected_read(hv, fine_sw, selected, bank_c, group):
     return fine, ch
 
 
+FEATURE_WRITERS = ("feature_mass_association", "structured_gram_association")
+
+
+def mass_descriptor(mass):
+    """Descriptor of a feature mass: r(log mass) (tao_stream.py:60-65, 483)."""
+    return rnd(torch.log(mass.double()), torch.bfloat16)
+
+
+def feature_read(h, read_z, matrices):
+    """Numerator-only mixture read of the feature writers (tao_stream.py:
+    301-305, 362-367): coef = feature_read_coefficients(h, z) per query and
+    matrix, out = r(sum_p sum_d coef[p, d] M_p[d, e]) with no denominator.
+    h [B, Q, H, D]; read_z [B, H, P, D]; matrices [B, H, P, D, D]."""
+    from . import writers as W
+    coef = W.feature_read_coefficients(h, read_z.unsqueeze(1))       # [B,Q,H,P,D]
+    out = torch.einsum("bqhpd,bhpde->bqhe", coef.to(torch.float64),
+                       matrices.to(torch.float64))
+    return rnd(out, h.dtype)
+
+
 def coarse_read(h, page_z_completed, page_c):
     """Coarse value read (non-index-only), tao_stream.py:299-305."""
     dtype = h.dtype
@@ -323,8 +343,9 @@ class OracleStream:
     def __init__(self, layer_index, geometry=None, writer="softmax"):
         self.layer = layer_index
         self.g = geometry or Geometry()
-        self.writer = writer           # "softmax" or "regularized_association"
+        self.writer = writer           # a TaoConfig.fine_writer
         self.pending_gram = self.pending_cross = None
+        self.pending_mass = self.pending_square = None   # feature writers
         self.position = 0
         self.local = None            # (k, v, raw_k) [B, n, H, D]
         self.fine_z = []             # [B, H, D] per sealed fine
@@ -357,11 +378,16 @@ class OracleStream:
         return len(self.fine_z) - self.completed * self.g.coarse_group
 
     def page_descriptors(self):
-        """page_z over completed pages plus the pending summary (:267-290)."""
+        """page_z over completed pages plus the pending summary (:267-290):
+        r(logsumexp) of the pending fines' z, or for the feature writers
+        r(log) of their summed feature mass (:280-283)."""
         parts = list(self.page_z)
         if self.pending:
-            start = self.completed * self.g.coarse_group
-            parts.append(page_summary(torch.stack(self.fine_z[start:], 2)))
+            if self.writer in FEATURE_WRITERS:
+                parts.append(mass_descriptor(self.pending_mass))
+            else:
+                start = self.completed * self.g.coarse_group
+                parts.append(page_summary(torch.stack(self.fine_z[start:], 2)))
         return torch.stack(parts, 2)
 
     def fine_segment_weights(self, page_z):
@@ -382,6 +408,9 @@ class OracleStream:
         of the block's statistics; the statistics add to the pending sums in
         seal order; a completed page's matrix is association_matrix of the
         sums, which then restart (never, index-only, as in the reference)."""
+        if self.writer in FEATURE_WRITERS:
+            self._seal_feature(raw_k, v)
+            return
         z, c = seal_softmax(raw_k, v)
         if self.writer == "regularized_association":
             from . import writers as W
@@ -410,6 +439,43 @@ class OracleStream:
             elif not self.g.coarse_index_only:
                 self.page_c.append(page_coarse_matrix(
                     zs, pz, torch.stack(self.fine_c[start:], 2)))
+
+    def _seal_feature(self, raw_k, v):
+        """_seal for the feature writers (tao_stream.py:56-65) and their
+        pending sums and page descriptors (:463-499): z = r(log mass); C =
+        association_matrix (feature mass) or structured_matrix (structured
+        Gram) of the block's statistics; the mass (and the gram / square
+        mass and cross) add up in seal order; a completed page's z is
+        r(log) of its summed mass and its matrix (non-index-only) comes from
+        the summed statistics, which then restart."""
+        from . import writers as W
+        if self.writer == "structured_gram_association":
+            square, cross, mass = W.structured_statistics(raw_k, v)
+            c = W.structured_matrix(square, cross, mass, self.g.fine_tokens)[1]
+            self.pending_square = square if self.pending_square is None else \
+                self.pending_square + square
+        else:
+            gram, cross, mass = W.association_statistics(raw_k, v, with_mass=True)
+            c = W.association_matrix(gram, cross)[1]
+            self.pending_gram = gram if self.pending_gram is None else self.pending_gram + gram
+        self.pending_cross = cross if self.pending_cross is None else self.pending_cross + cross
+        self.pending_mass = mass if self.pending_mass is None else self.pending_mass + mass
+        self.fine_z.append(mass_descriptor(mass))
+        self.fine_c.append(c.to(raw_k.dtype))
+        self._bank = None
+        self.state_version += 1
+        group = self.g.coarse_group
+        if self.pending == group:
+            self.page_z.append(mass_descriptor(self.pending_mass))
+            if not self.g.coarse_index_only:
+                if self.writer == "structured_gram_association":
+                    pc = W.structured_matrix(self.pending_square, self.pending_cross,
+                                             self.pending_mass, self.g.fine_tokens * group)[1]
+                else:
+                    pc = W.association_matrix(self.pending_gram, self.pending_cross)[1]
+                self.page_c.append(pc.to(raw_k.dtype))
+            self.pending_gram = self.pending_cross = None
+            self.pending_mass = self.pending_square = None
 
     def logical_bytes(self, b, heads, d):
         """LayerState.logical_bytes (tao_stream.py:518-527), bf16."""
@@ -447,7 +513,11 @@ class OracleStream:
         h = query_weights(raw_q)
         hv = page_values(h, pw)                               # [B,T,H,P,D]
         coarse_on = bool(self.page_z) and not self.g.coarse_index_only
-        if coarse_on:
+        feature = self.writer in FEATURE_WRITERS
+        if coarse_on and feature:
+            coarse = feature_read(h, page_z[:, :, :self.completed],
+                                  torch.stack(self.page_c, 2))
+        elif coarse_on:
             coarse = coarse_read(h, page_z[:, :, :self.completed],
                                  torch.stack(self.page_c, 2))
         else:
@@ -469,9 +539,16 @@ class OracleStream:
                 self.memo = True                                      # :292-295
             self.last_fine_contractions += b * count * heads * self.route_ids[1].shape[-1]
             self.diag["fused_fine_calls"] += 1                        # :244, :370
-            part, _ = selected_read(hv[:, offset:offset + count], sw,
-                                    self.route_ids[1][:, 0], bank,
-                                    self.g.coarse_group)
+            sel = self.route_ids[1][:, 0]
+            if feature:
+                b_, heads_, m_ = sel.shape
+                z_all = torch.stack(self.fine_z, 2)
+                z_sel = torch.gather(z_all, 2, sel.unsqueeze(-1).expand(b_, heads_, m_, d))
+                c_sel = torch.gather(bank, 2, sel[..., None, None].expand(b_, heads_, m_, d, d))
+                part = feature_read(h[:, offset:offset + count], z_sel, c_sel)
+            else:
+                part, _ = selected_read(hv[:, offset:offset + count], sw, sel, bank,
+                                        self.g.coarse_group)
             fine[:, offset:offset + count] = part
             offset += count
         return coarse, fine, coarse_on, True

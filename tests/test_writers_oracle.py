@@ -220,3 +220,70 @@ def test_regularized_writer_peak_counts_pending_sums(index_only):
     c = diagnostics.counters(cfg, 0, 1, h, d, [("call", 0, t, 0)], t)
     assert (c.peak_logical_cache_bytes, c.peak_physical_cache_tensor_bytes) == (
         s.diag["peak_logical_cache_bytes"], s.diag["peak_physical_cache_tensor_bytes"])
+
+
+@pytest.mark.parametrize("writer", ["feature_mass_association", "structured_gram_association"])
+def test_oracle_stream_feature_writers(writer):
+    """OracleStream with a feature writer (tao_stream.py:56-65, 280-305,
+    362-367, 463-499), pinned by checks that do not restate it:
+    - a fine's z is within half a bf16 ulp of the log of the block's mass,
+      which sums to the block length over the channels;
+    - a completed page's z is the log of its eight fines' summed mass: it
+      matches logsumexp of their z (fp64) within the fines' bf16 rounding,
+      which catches a mean, a max or a missing fine, and equals r(log) of
+      the mass of the page's 2048 tokens taken at once;
+    - the page matrix (non-index-only) is the writer's matrix of the 2048
+      tokens' statistics taken at once;
+    - the fine read of a query against one selected fine is r(h @ C): the
+      mixture of one matrix is 1;
+    - with two fines whose z are equal the read is the plain mean of the
+      two matrices' reads (mixture 1/2 each)."""
+    from oracle import tao_oracle as O
+    g = torch.Generator().manual_seed(11)
+    t, h, d = 2900, 2, 8
+    xs = [torch.randn(1, t, h, d, generator=g).to(BF16) for _ in range(5)]
+    fa = torch.randn(h, d, 3, generator=g) * 0.02
+    fb = torch.randn(h, d, 3, generator=g) * 0.02
+    for index_only in (False, True):
+        s = O.OracleStream(0, O.Geometry(coarse_index_only=index_only), writer=writer)
+        pos = 0
+        while pos < t:
+            w = s.next_chunk(t - pos)
+            s.prefill(*(x[:, pos:pos + w] for x in xs), fa, fb, 0.5)
+            pos += w
+        rk, v = xs[4], xs[2]
+        assert len(s.fine_z) == 9 and len(s.page_z) == 1
+        for f in (0, 8):
+            blk = slice(f * 256, (f + 1) * 256)
+            mass = W.association_statistics(rk[:, blk], v[:, blk], with_mass=True)[2]
+            assert torch.allclose(mass.sum(-1), torch.full_like(mass.sum(-1), 256.0), rtol=4e-3)
+            exact = mass.log()
+            assert ((s.fine_z[f].double() - exact).abs() <= 2 ** -8 * exact.abs()).all()
+        lse = torch.logsumexp(torch.stack(s.fine_z[:8], 2).double(), 2)
+        assert (s.page_z[0].double() - lse).abs().max() <= 2 ** -7 * lse.abs().max() + 2 ** -7
+        assert not torch.equal(s.page_z[0], torch.stack(s.fine_z[:8], 2).amax(2))
+        # the page's mass is the mass of its 2048 tokens taken at once
+        page_mass = W.association_statistics(rk[:, :2048], v[:, :2048], with_mass=True)[2]
+        assert torch.equal(s.page_z[0], page_mass.log().to(BF16))
+        if index_only:
+            assert s.page_c == []
+        else:
+            if writer == "structured_gram_association":
+                sq, cross, mass = W.structured_statistics(rk[:, :2048], v[:, :2048])
+                want = W.structured_matrix(sq, cross, mass, 2048)[1]
+            else:
+                want = W.association_matrix(*W.association_statistics(rk[:, :2048],
+                                                                     v[:, :2048]))[1]
+            assert (s.page_c[0].double() - want.double()).abs().max() <= \
+                2 ** -7 * want.double().abs().max()
+        # the mixture read against hand-picked fines
+        hq = O.query_weights(xs[3][:, :1])                          # [1, 1, H, D]
+        z_all, c_all = torch.stack(s.fine_z, 2), torch.stack(s.fine_c, 2)
+        one = O.feature_read(hq, z_all[:, :, 3:4], c_all[:, :, 3:4])
+        want = torch.einsum("bqhd,bhde->bqhe", hq.double(), c_all[:, :, 3].double())
+        assert torch.equal(one, want.to(BF16))
+        pair_z = z_all[:, :, 3:4].expand(-1, -1, 2, -1)
+        two = O.feature_read(hq, pair_z, c_all[:, :, 3:5])
+        half = (O.rnd(hq.double() * 0.5, BF16).double())
+        want = torch.einsum("bqhd,bhpde->bqhe", half, c_all[:, :, 3:5].double())
+        assert torch.equal(two, want.to(BF16))

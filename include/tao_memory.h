@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 7
+#define TAO_ABI_VERSION 8
 
 enum tao_status {
   TAO_OK = 0,
@@ -81,7 +81,22 @@ typedef struct tao_state_dev {
   float* pending_cross;  /* fp32 [B, H, D, D] */
   float* stats;          /* fp32 scratch [2][stats_cap * B][H][D][D] */
   int32_t stats_cap;     /* blocks per pass through the scratch (>= 1) */
+  /* Feature writers (feature_mass_association, structured_gram_association;
+   * tao_stream.py:56-65, 280-283, 362-367, 463-499): fine_writer selects
+   * them, fine_mass holds each sealed fine's fp32 feature mass (its z is
+   * r(log mass); page descriptors are r(log) of summed masses) and the read
+   * is the numerator-only mixture. They need stats (and stats_cap), plus
+   * [stats_cap * B][H][D] floats of mass scratch after its two halves.
+   * TAO_WRITER_VALUE (0): softmax descriptors (softmax and regularized). */
+  int32_t fine_writer;   /* enum tao_fine_writer */
+  float* fine_mass;      /* fp32 [B, H, fine_cap, D]; feature writers only */
 } tao_state_dev;
+
+enum tao_fine_writer {
+  TAO_WRITER_VALUE = 0,
+  TAO_WRITER_FEATURE_MASS = 1,
+  TAO_WRITER_STRUCTURED = 2
+};
 
 /* New-token operands: q/k/v/raw_q/raw_k, each [B, T, H, D] bf16 with
  * element strides (batch, token, head); D contiguous. */

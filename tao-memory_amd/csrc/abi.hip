@@ -27,11 +27,32 @@ int check_hip(hipError_t e, const char* where) {
 // Regularized association writer (state buffers set, tao_memory.h).
 bool assoc_writer(const tao_state_dev* st) { return st->pending_gram != nullptr; }
 
+// Feature writers (fine_writer TAO_WRITER_FEATURE_MASS / _STRUCTURED).
+bool feature_writer(const tao_state_dev* st) { return st->fine_writer != TAO_WRITER_VALUE; }
+
 int check_assoc(const tao_state_dev* st) {
-  const bool any = st->pending_gram || st->pending_cross || st->stats;
+  const bool any = st->pending_gram || st->pending_cross || (st->stats && !feature_writer(st));
   if (any && (!st->pending_gram || !st->pending_cross || !st->stats || st->stats_cap < 1))
     return fail(TAO_E_ARGUMENT,
                 "the regularized writer needs pending_gram, pending_cross and stats (stats_cap >= 1)");
+  return TAO_OK;
+}
+
+int check_feature(const tao_state_dev* st) {
+  if (st->fine_writer != TAO_WRITER_VALUE && st->fine_writer != TAO_WRITER_FEATURE_MASS &&
+      st->fine_writer != TAO_WRITER_STRUCTURED)
+    return fail(TAO_E_ARGUMENT, "unknown fine_writer");
+  if (!feature_writer(st)) {
+    if (st->fine_mass) return fail(TAO_E_ARGUMENT, "fine_mass is set without a feature writer");
+    return TAO_OK;
+  }
+  if (!st->fine_mass || !st->stats || st->stats_cap < 1)
+    return fail(TAO_E_ARGUMENT, "a feature writer needs fine_mass and stats (stats_cap >= 1)");
+  if (st->pending_gram || st->pending_cross)
+    return fail(TAO_E_ARGUMENT, "a feature writer keeps no pending gram / cross sums");
+  if (st->page_c)
+    return fail(TAO_E_ARGUMENT,
+                "the coarse value branch with a feature writer is not built (index-only only)");
   return TAO_OK;
 }
 
@@ -52,6 +73,7 @@ int check_state(const tao_state_dev* st, bool need_workspace = true) {
   if (st->sel_cap > 512) return fail(TAO_E_CAPACITY, "sel_cap above 512");
   if (st->coarse_group != 8) return fail(TAO_E_SHAPE, "HIP kernels implement coarse_group=8");
   if (int rc = check_assoc(st)) return rc;
+  if (int rc = check_feature(st)) return rc;
   const tao::WorkspaceLayout lay =
       tao::workspace_layout(st->batch, st->heads, st->head_dim, st->sel_cap, 0);
   if (need_workspace && st->workspace_bytes < lay.plan_off)
@@ -214,6 +236,86 @@ hipError_t assoc_seal(const tao_state_dev* st, const tao::TokView& rk, const tao
       e = tao::launch_association_solve(pg, D, s);
       if (e != hipSuccess) return e;
     }
+  }
+  return hipSuccess;
+}
+
+// The feature writers' part of `count` seals (fine slots first_slot ..):
+// block statistics with the feature mass, C^T into the bank slots
+// (association_matrix for the feature-mass writer, structured_matrix over
+// the block's 256 tokens for the structured one), z = r(log mass) and the
+// fp32 mass for the page descriptors (tao_stream.py:56-65).
+hipError_t feature_seal(const tao_state_dev* st, const tao::TokView& rk, const tao::TokView& v,
+                        int64_t new_base, const int64_t* starts, int first_slot, int count,
+                        hipStream_t s) {
+  const int B = st->batch, H = st->heads, D = st->head_dim;
+  const bool structured = st->fine_writer == TAO_WRITER_STRUCTURED;
+  const size_t mats = (size_t)st->stats_cap * B * H;
+  float* first = st->stats;                      // gram, or the square mass
+  float* cross = st->stats + mats * D * D;
+  float* mass = st->stats + 2 * mats * D * D;
+  for (int done = 0; done < count; done += st->stats_cap) {
+    const int n = std::min(st->stats_cap, count - done);
+    tao::WriterStatsParams sp{};
+    sp.k = rk.p;
+    sp.v = v.p;
+    sp.k_s[0] = rk.sb; sp.k_s[1] = rk.st; sp.k_s[2] = rk.sh;
+    sp.v_s[0] = v.sb; sp.v_s[1] = v.st; sp.v_s[2] = v.sh;
+    sp.N = n * B;
+    sp.T = st->fine_tokens;
+    sp.H = H;
+    sp.mode = structured ? 1 : 0;
+    sp.gram = first;
+    sp.cross = cross;
+    sp.mass = mass;
+    sp.starts = starts + done;
+    sp.new_base = new_base;
+    sp.ring_raw = (const bf16_t*)st->ring_raw;
+    sp.ring_v = (const bf16_t*)st->ring_v;
+    sp.L = st->local_keep + st->fine_tokens;
+    sp.B = B;
+    hipError_t e = tao::launch_writer_stats(sp, D, s);
+    if (e != hipSuccess) return e;
+    if (structured) {
+      tao::StructuredParams tp{};
+      tp.square = first;
+      tp.cross = cross;
+      tp.mass = mass;
+      tp.count_mats = n * B * H;
+      tp.count = (float)st->fine_tokens;
+      tp.out = (bf16_t*)st->bank_c;
+      tp.to_slots = 1;
+      tp.B = B;
+      tp.H = H;
+      tp.cap = st->fine_cap;
+      tp.first_slot = first_slot + done;
+      e = tao::launch_structured_matrix(tp, D, s);
+    } else {
+      tao::AssocSolveParams fp{};
+      fp.gram = first;
+      fp.cross = cross;
+      fp.count = n * B * H;
+      fp.out = (bf16_t*)st->bank_c;
+      fp.to_slots = 1;
+      fp.B = B;
+      fp.H = H;
+      fp.cap = st->fine_cap;
+      fp.first_slot = first_slot + done;
+      fp.group = st->coarse_group;
+      e = tao::launch_association_solve(fp, D, s);
+    }
+    if (e != hipSuccess) return e;
+    tao::FeatureDescParams dp{};
+    dp.mass = mass;
+    dp.fine_z = (bf16_t*)st->fine_z;
+    dp.fine_mass = st->fine_mass;
+    dp.count = n;
+    dp.B = B;
+    dp.H = H;
+    dp.cap = st->fine_cap;
+    dp.first_slot = first_slot + done;
+    e = tao::launch_feature_descriptors(dp, D, s);
+    if (e != hipSuccess) return e;
   }
   return hipSuccess;
 }
@@ -458,6 +560,10 @@ int tao_write_fine(const tao_state_dev* st, const tao_tokens* tok, int64_t new_b
   p.first_slot = first_slot;
   p.count = count;
   p.z_only = assoc_writer(st) ? 1 : 0;
+  if (feature_writer(st))
+    return check_hip(feature_seal(st, p.rk, p.v, new_base, start_pos, first_slot, count,
+                                  (hipStream_t)stream),
+                     "tao_write_fine");
   hipError_t e = tao::launch_writer(p, st->head_dim, (hipStream_t)stream);
   if (e == hipSuccess && assoc_writer(st) && count > 0)
     e = assoc_seal(st, p.rk, p.v, new_base, start_pos, first_slot, count, (hipStream_t)stream);
@@ -476,6 +582,7 @@ int tao_seal_epilogue(const tao_state_dev* st, int32_t slot, int32_t pages, int3
   p.fine_sw = (bf16_t*)st->fine_sw;
   p.page_z = (bf16_t*)st->page_z;
   p.page_w = (bf16_t*)st->page_w;
+  p.fine_mass = st->fine_mass;
   p.B = st->batch;
   p.H = st->heads;
   p.fine_cap = st->fine_cap;
@@ -687,7 +794,12 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   wp.first_slot = (int)first_slot;
   wp.count = (int)n_write;
   wp.z_only = external_values || assoc_writer(st);
-  e = tao::launch_writer(wp, D, s);
+  if (feature_writer(st)) {
+    if (external_values) return fail(TAO_E_ARGUMENT, "external values with a feature writer");
+    e = feature_seal(st, wp.rk, wp.v, pos0, wp.starts, (int)first_slot, (int)n_write, s);
+  } else {
+    e = tao::launch_writer(wp, D, s);
+  }
   if (e != hipSuccess) return check_hip(e, "tao_prefill writer");
   if (assoc_writer(st) && n_write > 0) {
     e = assoc_seal(st, wp.rk, wp.v, pos0, wp.starts, (int)first_slot, (int)n_write, s);
@@ -698,6 +810,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   pp.fine_z = (const bf16_t*)st->fine_z;
   pp.fine_sw = (bf16_t*)st->fine_sw;
   pp.page_z = (bf16_t*)st->page_z;
+  pp.fine_mass = st->fine_mass;
   pp.B = st->batch;
   pp.H = st->heads;
   pp.fine_cap = st->fine_cap;
@@ -742,6 +855,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
     ep.fine_sw = (bf16_t*)st->fine_sw;
     ep.page_z = (bf16_t*)st->page_z;
     ep.page_w = (bf16_t*)st->page_w;
+    ep.fine_mass = st->fine_mass;
     ep.pw_pool = (bf16_t*)pools->pw_pool;
     ep.psw_pool = (bf16_t*)pools->psw_pool;
     ep.pool_pcap = pools->pool_pcap;
@@ -841,6 +955,9 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   rt.save_coarse = pools ? (bf16_t*)pools->coarse_out : nullptr;
   rt.save_fine = pools ? (bf16_t*)pools->fine_out : nullptr;
   rt.save_den = pools ? pools->den_out : nullptr;
+  rt.fine_z = feature_writer(st) ? (const bf16_t*)st->fine_z : nullptr;
+  if (feature_writer(st) && (query_routes || rt.save_fine))
+    return fail(TAO_E_ARGUMENT, "a feature writer reads turn routes without saves only");
   e = tao::launch_read_tiles(rt, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill read");
   tao::AppendParams app{};

@@ -366,11 +366,36 @@ __global__ __launch_bounds__(D) void structured_matrix_kernel(StructuredParams p
     const float hb = cr[(size_t)i * D + e] / diag[i] + tv[i] * t_cross / safe_sum;
     mass_hb = fmaf(mv[i], hb, mass_hb);
   }
+  if (p.to_slots) {
+    // C^T into the fine bank: row e of slot first_slot + blk.
+    const int blk = mat / (p.B * p.H), b = mat / p.H % p.B, h = mat % p.H;
+    bf16_t* out = p.out + ((((size_t)b * p.H + h) * p.cap + p.first_slot + blk) * D + e) * D;
+    for (int i = 0; i < D; ++i) {
+      const float hb = cr[(size_t)i * D + e] / diag[i] + tv[i] * t_cross / safe_sum;
+      out[i] = f2bf(hb - hmv[i] * mass_hb / denominator);
+    }
+    return;
+  }
   bf16_t* out = p.out + (size_t)mat * D * D;
   for (int i = 0; i < D; ++i) {
     const float hb = cr[(size_t)i * D + e] / diag[i] + tv[i] * t_cross / safe_sum;
     out[(size_t)i * D + e] = f2bf(hb - hmv[i] * mass_hb / denominator);
   }
+}
+
+// One thread per (seal block, batch, head, channel): z = r(log mass), and the
+// fp32 mass kept for the page descriptors.
+template <int D>
+__global__ __launch_bounds__(256) void feature_desc_kernel(FeatureDescParams p) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)p.count * p.B * p.H * D) return;
+  const int d = (int)(i % D);
+  const int64_t mat = i / D;
+  const int blk = (int)(mat / (p.B * p.H)), b = (int)(mat / p.H % p.B), h = (int)(mat % p.H);
+  const float m = p.mass[i];
+  const size_t dst = (((size_t)b * p.H + h) * p.cap + p.first_slot + blk) * D + d;
+  p.fine_z[dst] = f2bf(log_bf(m));
+  p.fine_mass[dst] = m;
 }
 
 __global__ __launch_bounds__(256) void chrono_sum_kernel(const float* x, float* out, int64_t outer,
@@ -483,6 +508,19 @@ hipError_t launch_structured_matrix(const StructuredParams& p, int head_dim, hip
     hipLaunchKernelGGL(structured_matrix_kernel<128>, dim3((unsigned)p.count_mats), dim3(128), 0, s, p);
   else if (head_dim == 64)
     hipLaunchKernelGGL(structured_matrix_kernel<64>, dim3((unsigned)p.count_mats), dim3(64), 0, s, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_feature_descriptors(const FeatureDescParams& p, int head_dim, hipStream_t s) {
+  if (p.count <= 0) return hipSuccess;
+  const int64_t n = (int64_t)p.count * p.B * p.H * head_dim;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (head_dim == 128)
+    hipLaunchKernelGGL(feature_desc_kernel<128>, grid, dim3(256), 0, s, p);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL(feature_desc_kernel<64>, grid, dim3(256), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -40,7 +40,9 @@ __global__ __launch_bounds__(kThreads) void pages_kernel(PagesParams p) {
   const bf16_t* z = p.fine_z + (size_t)bh * p.fine_cap * D;
   float zv[8];
   for (int i = 0; i < 8; ++i) zv[i] = bf2f(z[(size_t)(g * p.group + i) * D + d]);
-  const float pz = group_logsumexp(zv, 8);
+  const float pz =
+      p.fine_mass ? mass_page_z(p.fine_mass + ((size_t)bh * p.fine_cap + g * p.group) * D + d, 8, D)
+                  : group_logsumexp(zv, 8);
   p.page_z[((size_t)bh * p.page_cap + g) * D + d] = f2bf(pz);
   for (int i = 0; i < 8; ++i)
     p.fine_sw[((size_t)bh * p.fine_cap + g * p.group + i) * D + d] = f2bf(exp_bf(rbf(zv[i] - pz)));
@@ -65,7 +67,10 @@ __global__ __launch_bounds__(kThreads) void epochs_kernel(EpochParams p) {
   if (tid < D && pend > 0) {
     float zv[8];
     for (int i = 0; i < 8; ++i) zv[i] = i < pend ? bf2f(z[(size_t)(K * p.group + i) * D + tid]) : 0.0f;
-    const float pz = group_logsumexp(zv, pend);
+    const float pz =
+        p.fine_mass
+            ? mass_page_z(p.fine_mass + ((size_t)bh * p.fine_cap + K * p.group) * D + tid, pend, D)
+            : group_logsumexp(zv, pend);
     pend_pz[tid] = pz;
     for (int i = 0; i < pend; ++i) {
       const bf16_t w = f2bf(exp_bf(rbf(zv[i] - pz)));
@@ -580,6 +585,7 @@ TAO_DEV u32x4 lds_read16(uint32_t addr) {
 }
 // s_waitcnt lgkmcnt(0), tied to the values it makes ready (so nothing that
 // reads them is scheduled above it).
+TAO_DEV void wait_lds(u32x4& a) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a)::"memory"); }
 TAO_DEV void wait_lds(u32x4& a, u32x4& b) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b)::"memory");
 }
@@ -599,8 +605,9 @@ TAO_DEV uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
 
-template <int D, bool COARSE>
+template <int D, bool COARSE, bool FEAT>
 __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesParams p) {
+  static_assert(!(COARSE && FEAT), "feature writers read index-only states");
   constexpr int KK = D / 16, ET = D / 32, CPR = D / 8;   // k-steps, e-tiles, chunks per row
   constexpr int CPT = D * CPR / (64 * kGroupWaves);      // 1 KB wave loads per fine and wave
   static_assert(CPT * 64 * kGroupWaves == D * CPR, "whole wave loads per fine");
@@ -672,6 +679,30 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
     for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
       for (int j = 0; j < 8; ++j) hf[kk][j] = rbf(hf[kk][j] * inv);
+  }
+
+  // Feature writers: the mixture's normaliser for query li, the sum over the
+  // wave's selected fines of mass = sum_d h[d] exp(z[d]) (fp32, the same
+  // order as the per-fine mass of the read below).
+  float tot = 0.0f;
+  if constexpr (FEAT) {
+    if (reads) {
+      const int32_t* sel = p.sel_pool + ((size_t)slot * BH + bh) * p.sel_cap;
+      const bf16_t* zb = p.fine_z + (size_t)bh * p.fine_cap * D;
+      for (int m = 0; m < M; ++m) {
+        const int fid = sel[m];
+        float part = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          float zf[8];
+          unpack8f(*(const uint4*)(zb + (size_t)fid * D + 16 * kk + 8 * hl), zf);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) part += hf[kk][j] * expf(zf[j]);
+        }
+        part += __shfl_xor(part, 32, 64);
+        tot += part;
+      }
+    }
   }
 
   floatx16 acc[ET];
@@ -770,7 +801,10 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
         __builtin_amdgcn_global_load_lds(base + (size_t)row * D + (pos ^ (row % CPR)) * 8,
                                          (lds_void_t*)(&ring[s][0] + J * 64 * 8), 16, 0, 0);
       }
-      if (w == 0 && lane < 2 * CPR) {
+      if (FEAT && w == 0 && lane < CPR) {
+        const bf16_t* src = p.fine_z + ((size_t)bh * p.fine_cap + fid) * D + lane * 8;
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)&pwsw[s][0][0], 16, 0, 0);
+      } else if (!FEAT && w == 0 && lane < 2 * CPR) {
         const bf16_t* src =
             lane < CPR ? pw_base + (size_t)(fid / p.group) * D + lane * 8
                        : (fid < sw_split ? sw_base + (size_t)fid * D
@@ -788,7 +822,17 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
     // Wave 0 turns the fine's pw and sw rows into its weights.
     auto make_wr = [&](int f) __attribute__((always_inline)) {
       const int s = f % kRing;
-      if (w == 0 && lane < CPR) {
+      if (FEAT && w == 0 && lane < CPR) {
+        // Feature writers: exp(z) of the fine's descriptor.
+        u32x4 zv = lds_read16(lds_addr(&pwsw[s][0][lane * 8]));
+        wait_lds(zv);
+        float wv[8];
+        unpack8f(as_uint4(zv), wv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wv[j] = expf(wv[j]);
+        *(float4*)&sm.wf[s][lane * 8] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+        *(float4*)&sm.wf[s][lane * 8 + 4] = make_float4(wv[4], wv[5], wv[6], wv[7]);
+      } else if (!FEAT && w == 0 && lane < CPR) {
         u32x4 pwv = lds_read16(lds_addr(&pwsw[s][0][lane * 8]));
         u32x4 swv = lds_read16(lds_addr(&pwsw[s][1][lane * 8]));
         wait_lds(pwv, swv);
@@ -796,6 +840,43 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
         unpack8f(slice_weights(as_uint4(pwv), as_uint4(swv)), wv);
         *(float4*)&sm.wf[s][lane * 8] = make_float4(wv[0], wv[1], wv[2], wv[3]);
         *(float4*)&sm.wf[s][lane * 8 + 4] = make_float4(wv[4], wv[5], wv[6], wv[7]);
+      }
+    };
+    // Feature writers: coef = r(mix * h) with mix = mass / tot of this fine
+    // (feature_read_coefficients), read against C^T with no denominator.
+    auto consume_feat = [&](int u) __attribute__((always_inline)) {
+      if (!(in_pass && ((sm.mask[u >> 2] >> ((u & 3) * 8 + w)) & 1u))) return;
+      const int s = u % kRing;
+      const uint32_t cs = lds_addr(&ring[s][0]);
+      float part = 0.0f;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const float4 e0 = *(const float4*)&sm.wf[s][16 * kk + 8 * hl];
+        const float4 e1 = *(const float4*)&sm.wf[s][16 * kk + 8 * hl + 4];
+        const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) part += hf[kk][j] * ev[j];
+      }
+      part += __shfl_xor(part, 32, 64);
+      const float mix = part / tot;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const int c = 2 * kk + hl;
+        u32x4 bq[ET];
+#pragma unroll
+        for (int t = 0; t < ET; ++t) {
+          const int row = 32 * t + li;
+          bq[t] = lds_read16(cs + (uint32_t)(row * D + 8 * (c ^ (row % CPR))) * 2);
+        }
+        const bf16x8 a = as_bf16x8(make_uint4(
+            pack_bf16x2(mix * hf[kk][0], mix * hf[kk][1]), pack_bf16x2(mix * hf[kk][2], mix * hf[kk][3]),
+            pack_bf16x2(mix * hf[kk][4], mix * hf[kk][5]), pack_bf16x2(mix * hf[kk][6], mix * hf[kk][7])));
+        if constexpr (ET == 4) wait_lds(bq[0], bq[1], bq[2], bq[3]);
+        else wait_lds(bq[0], bq[1]);
+#pragma unroll
+        for (int t = 0; t < ET; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(as_uint4(bq[t])), a, acc[t],
+                                                           0, 0, 0);
       }
     };
     auto consume = [&](int u) __attribute__((always_inline)) {
@@ -861,7 +942,8 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
     ring_barrier();
     for (int u = 0; u < U; ++u) {
       if (u + kRing - 1 < U) issue(u + kRing - 1);
-      consume(u);
+      if constexpr (FEAT) consume_feat(u);
+      else consume(u);
       if (u + 1 < U) {
         wait_behind(min(U - 1, u + kRing - 1) - (u + 1));
         make_wr(u + 1);
@@ -896,7 +978,8 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
       const int at = unit_at(li, 4 * t + g) + 4 * hl;
       float f[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) f[k] = rbf(rbf(acc[t][4 * g + k]) * rden);
+      for (int k = 0; k < 4; ++k)
+        f[k] = FEAT ? rbf(acc[t][4 * g + k]) : rbf(rbf(acc[t][4 * g + k]) * rden);
       *(uint2*)&tile_f[at] = make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]));
     }
     if constexpr (COARSE) {
@@ -1011,8 +1094,16 @@ hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t
 #define TAO_READ_LAUNCH(D_, C_, Q_)                                                           \
   hipLaunchKernelGGL((read_groups_kernel<D_, C_, Q_>), grid, dim3(kGroupThreads), 0, s, p)
 #define TAO_STREAM_LAUNCH(D_, C_)                                                             \
-  hipLaunchKernelGGL((read_stream_kernel<D_, C_>), grid, dim3(kGroupThreads), 0, s, p)
+  hipLaunchKernelGGL((read_stream_kernel<D_, C_, false>), grid, dim3(kGroupThreads), 0, s, p)
+#define TAO_FEATURE_LAUNCH(D_)                                                                \
+  hipLaunchKernelGGL((read_stream_kernel<D_, false, true>), grid, dim3(kGroupThreads), 0, s, p)
   if (head_dim != 128 && head_dim != 64) return hipErrorInvalidValue;
+  if (p.fine_z) {
+    // Feature writers: turn routes, index-only, no saves.
+    if (perq || coarse || p.save_fine) return hipErrorInvalidValue;
+    if (head_dim == 128) TAO_FEATURE_LAUNCH(128); else TAO_FEATURE_LAUNCH(64);
+    return hipGetLastError();
+  }
   if (head_dim == 128) {
     if (perq) {
       if (coarse) TAO_READ_LAUNCH(128, true, true); else TAO_READ_LAUNCH(128, false, true);

@@ -74,6 +74,14 @@ TAO_DEV float log_bf(float x) {
   return rbf(y);
 }
 
+// A feature-mass page descriptor (tao_stream.py:280-283, 483): r(log) of
+// the fp32 sum, in seal order, of the first n masses at stride `stride`.
+TAO_DEV float mass_page_z(const float* mass, int n, size_t stride) {
+  float s = mass[0];
+  for (int i = 1; i < n; ++i) s += mass[i * stride];
+  return log_bf(s);
+}
+
 // Correctly rounded fp32 exp (fp64 evaluation).
 TAO_DEV float exp_cr(float x) { return (float)exp((double)x); }
 

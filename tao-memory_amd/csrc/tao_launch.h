@@ -255,8 +255,11 @@ struct WriterParams {
 };
 hipError_t launch_writer(const WriterParams& p, int head_dim, hipStream_t s);
 
+// fine_mass (feature writers): a page's z is r(log) of its fines' fp32
+// masses summed in seal order instead of r(logsumexp) of their z.
 struct EpilogueParams {
   const bf16_t* fine_z; bf16_t* fine_sw; bf16_t* page_z; bf16_t* page_w;
+  const float* fine_mass;
   int B, H, fine_cap, page_cap, group, slot, pages;
   int recompute;                 // 0: keep page_z[slot's group] (snapshot import)
 };
@@ -278,6 +281,7 @@ hipError_t launch_local_attention(const AttnParams& p, int head_dim, hipStream_t
 // weights of pages [first_page, first_page + count).
 struct PagesParams {
   const bf16_t* fine_z; bf16_t* fine_sw; bf16_t* page_z;
+  const float* fine_mass;        // feature writers (see EpilogueParams)
   int B, H, fine_cap, page_cap, group, first_page, count;
 };
 hipError_t launch_pages(const PagesParams& p, int head_dim, hipStream_t s);
@@ -287,6 +291,7 @@ hipError_t launch_pages(const PagesParams& p, int head_dim, hipStream_t s);
 // page weights into the pools; the last epoch is also published to the state.
 struct EpochParams {
   const bf16_t* fine_z; bf16_t* fine_sw; bf16_t* page_z; bf16_t* page_w;
+  const float* fine_mass;        // feature writers (see EpilogueParams)
   bf16_t* pw_pool; bf16_t* psw_pool; int pool_pcap;
   int B, H, fine_cap, page_cap, group, first_epoch, count;
 };
@@ -315,6 +320,9 @@ struct ReadTilesParams {
   const uint32_t* qsel; int qsel_words; int first_epoch;
   // Optional saves (null = skip): pre-fusion heads [B, T, H, D], denominators [B, T, H].
   bf16_t* save_coarse; bf16_t* save_fine; float* save_den;
+  // Feature writers (turn routes, no coarse values): the state's fine
+  // descriptors [B, H, fine_cap, D]; the read is the numerator-only mixture.
+  const bf16_t* fine_z;
 };
 hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t s);
 
@@ -415,8 +423,21 @@ struct StructuredParams {
   int count_mats;
   float count;            // token count behind the statistics
   bf16_t* out;
+  // to_slots: matrix (blk, b, h) goes transposed into fine slot
+  // first_slot + blk of out viewed as [B, H, cap, D, D] (as AssocSolveParams).
+  int to_slots, B, H, cap, first_slot;
 };
 hipError_t launch_structured_matrix(const StructuredParams& p, int head_dim, hipStream_t s);
+
+// Feature-writer descriptors of `count` seals: matrix (blk, b, h) of the
+// mass scratch [count * B][H][D] gives fine slot first_slot + blk its
+// z = r(log mass) and its fp32 mass (tao_stream.py:60-65).
+struct FeatureDescParams {
+  const float* mass;
+  bf16_t* fine_z; float* fine_mass;
+  int count, B, H, cap, first_slot;
+};
+hipError_t launch_feature_descriptors(const FeatureDescParams& p, int head_dim, hipStream_t s);
 
 hipError_t launch_chrono_sum(const float* x, float* out, int64_t outer, int fines, int64_t inner,
                              hipStream_t s);

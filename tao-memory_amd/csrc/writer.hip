@@ -263,7 +263,10 @@ __global__ __launch_bounds__(kThreads) void epilogue_kernel(EpilogueParams p) {
       if (i < n) m = fmaxf(m, zv[i]);
     }
     if (__builtin_isinf(m)) m = 0.0f;
-    if (p.recompute) {
+    if (p.recompute && p.fine_mass) {
+      pz = mass_page_z(p.fine_mass + ((size_t)bh * p.fine_cap + first) * D + d, n, D);
+      p.page_z[((size_t)bh * p.page_cap + g) * D + d] = f2bf(pz);
+    } else if (p.recompute) {
       float e[8];
       for (int i = 0; i < 8; ++i) e[i] = i < n ? exp_bf(rbf(zv[i] - m)) : 0.0f;
       for (int w = 4; w >= 1; w >>= 1)

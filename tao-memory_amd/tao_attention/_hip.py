@@ -36,6 +36,7 @@ class StateDev(ctypes.Structure):
         ("page_c", _vp), ("coarse_g", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
         ("pending_gram", _vp), ("pending_cross", _vp), ("stats", _vp), ("stats_cap", _i32),
+        ("fine_writer", _i32), ("fine_mass", _vp),
     ]
 
 
@@ -171,7 +172,7 @@ _SIGNATURES = {
 
 EXPORTED = tuple(_SIGNATURES)
 
-ABI_VERSION = 7                # TAO_ABI_VERSION of include/tao_memory.h
+ABI_VERSION = 8                # TAO_ABI_VERSION of include/tao_memory.h
 
 # Decode-graph epoch counters (enum tao_graph_stat / tao_graph_reason).
 GRAPH_STATS = 19

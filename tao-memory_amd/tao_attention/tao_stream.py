@@ -40,7 +40,11 @@ _QTILE = 256
 _STATS_CAP = 8          # blocks per statistics pass of the regularized writer
 # Fine writers the stream implements: the softmax writer and the regularized
 # association writer (same z and read, association value matrices).
-_STREAM_WRITERS = ("softmax", "regularized_association")
+_STREAM_WRITERS = ("softmax", "regularized_association", "feature_mass_association",
+                   "structured_gram_association")
+# Writers whose descriptors are log feature masses and whose read is the
+# numerator-only mixture (tao_stream.py:56-65, 280-283, 362-367).
+_FEATURE_WRITERS = {"feature_mass_association": 1, "structured_gram_association": 2}
 # Process-wide serial numbers for buffer generations and native drivers: a
 # reset state reallocates its buffers and reopens its driver, and neither the
 # new handle's address nor a per-state counter is guaranteed to differ from
@@ -82,6 +86,14 @@ class _DeviceState:
             self.pending_cross = torch.zeros(dd, dtype=torch.float32, device=device)
             self.stats = torch.empty((2, _STATS_CAP * batch, heads, head_dim, head_dim),
                                      dtype=torch.float32, device=device)
+        # Feature writers: each sealed fine's fp32 feature mass (page
+        # descriptors sum them) and statistics scratch with a mass region.
+        self.feature = _FEATURE_WRITERS.get(config.fine_writer, 0)
+        self.fine_mass = None
+        if self.feature:
+            words = _STATS_CAP * batch * heads * head_dim
+            self.stats = torch.empty(words * (2 * head_dim + 1), dtype=torch.float32,
+                                     device=device)
         self.generation = next(_SERIAL)   # renewed whenever the buffers move
         self.fine_cap = 0
         self._allocate(fine_cap, copy_fines=0)
@@ -102,6 +114,8 @@ class _DeviceState:
         chosen = torch.zeros((B, H, chosen_cap), dtype=torch.int32, device=dev)
         page_c = (torch.empty((B, H, page_cap, D, D), dtype=bf16, device=dev)
                   if self.coarse_values else None)
+        fine_mass = (torch.zeros((B, H, fine_cap, D), dtype=torch.float32, device=dev)
+                     if self.feature else None)
         if copy_fines:
             n = copy_fines
             bank[:, :, :n].copy_(self.bank[:, :, :n])
@@ -117,6 +131,9 @@ class _DeviceState:
             if page_c is not None:
                 done = n // cfg.coarse_group
                 page_c[:, :, :done].copy_(self.page_c[:, :, :done])
+            if fine_mass is not None:
+                fine_mass[:, :, :n].copy_(self.fine_mass[:, :, :n])
+        self.fine_mass = fine_mass
         self.bank, self.fine_z, self.fine_sw = bank, fine_z, fine_sw
         self.page_z, self.page_w, self.sel, self.chosen = page_z, page_w, sel, chosen
         self.page_c = page_c
@@ -162,6 +179,9 @@ class _DeviceState:
         if self.association:
             st.pending_gram = self.pending_gram.data_ptr()
             st.pending_cross = self.pending_cross.data_ptr()
+            st.stats, st.stats_cap = self.stats.data_ptr(), _STATS_CAP
+        if self.feature:
+            st.fine_writer, st.fine_mass = self.feature, self.fine_mass.data_ptr()
             st.stats, st.stats_cap = self.stats.data_ptr(), _STATS_CAP
         st.workspace = self.workspace.data_ptr()
         st.workspace_bytes = self.workspace.numel()
@@ -391,6 +411,10 @@ class StreamCache:
                 f"the HIP streaming path implements the fine writers {_STREAM_WRITERS}")
         if cfg.fine_tokens != 256 or cfg.local_keep != 512:
             raise NotImplementedError("the HIP path implements fine_tokens=256, local_keep=512")
+        if cfg.fine_writer in _FEATURE_WRITERS and not cfg.coarse_index_only:
+            raise NotImplementedError(
+                "the HIP path implements the feature writers with coarse_index_only=True "
+                "(their coarse value read is not built)")
         if q.dtype != torch.bfloat16:
             raise TypeError("the HIP path computes on bf16 operands")
         if q.shape[-1] not in (64, 128):
@@ -621,6 +645,13 @@ class StreamCache:
         """
         if local_flash is not None:
             return self.prefill(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, local_flash)
+        if self.config.fine_writer in _FEATURE_WRITERS:
+            # The feature writers' read depends on each query (its mixture
+            # over the selected fines), so there is no folded route: a token
+            # runs as a one-token prefill.
+            if self._capturing:
+                raise NotImplementedError("device-cursor steps serve the folded-route read only")
+            return self.prefill(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
         if self._capturing:
             return self._decode_captured(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha)
         nat = self._native
@@ -899,6 +930,15 @@ class StreamCache:
         if dev is not None and dev.association and fines and (pending or not dev.coarse_values):
             pending_gram = dev.pending_gram.clone()
             pending_cross = dev.pending_cross.clone()
+        # Feature writers: the pending page's summed mass, in seal order (the
+        # reference's pending_mass). Their gram / square-mass and cross sums
+        # feed only the coarse value read, which this path does not build.
+        pending_mass = None
+        if dev is not None and dev.feature and pending:
+            base = completed * group
+            pending_mass = dev.fine_mass[:, :, base].clone()
+            for j in range(1, pending):
+                pending_mass = pending_mass + dev.fine_mass[:, :, base + j]
         return {
             "layer_index": self.layer_index,
             "config": cfg.export(),
@@ -911,7 +951,7 @@ class StreamCache:
             "pages": pages,
             "pending_z": pending_z,
             "pending_square_mass": None,
-            "pending_mass": None,
+            "pending_mass": pending_mass,
             "pending_gram": pending_gram,
             "pending_cross": pending_cross,
             "route_ids": route_ids,
@@ -930,6 +970,11 @@ class StreamCache:
         whose tensors are on the host is restored onto the current device.
         """
         config = TaoConfig(**saved["config"])
+        if config.fine_writer in _FEATURE_WRITERS and saved["pending_z"]:
+            # The page descriptors need each pending fine's mass; the schema
+            # keeps only their sum (pending_mass).
+            raise NotImplementedError(
+                "restoring a feature-writer snapshot with pending fines is not built")
         state = cls(saved["layer_index"], saved["route_interval"], saved["fusion_mode"],
                     fused_fine=saved["fused_fine"], config=config)
         position = saved["position"]

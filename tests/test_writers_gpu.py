@@ -280,3 +280,53 @@ def test_stream_regularized_writer(device, index_only, width, batch):
                                       alpha=0.5, state=s, position=s.get_pos())
         nxt.append(out)
     assert torch.equal(nxt[0], nxt[1])
+
+
+@pytest.mark.parametrize("writer,width", [("feature_mass_association", 64),
+                                          ("feature_mass_association", 128),
+                                          ("structured_gram_association", 128)])
+def test_stream_feature_writers(device, writer, width):
+    """Streaming prefill and decode with the feature writers (index-only):
+    z = r(log mass), page descriptors from summed masses (the step at 2559
+    seals the 8th fine and completes page 0), route ids bit-exact, the fine
+    matrices and outputs within the bf16 tolerance of the oracle, the
+    descriptors within one bf16 rounding of it (the GPU sums the masses in
+    fp32, the oracle in fp64), and the exported pending mass."""
+    from oracle import tao_oracle as O
+    from tao_attention import TaoConfig, new_state, tao_attention_decode, tao_attention_prefill
+    heads, tokens, batch = 2, 2826, 1
+    g = torch.Generator().manual_seed(83 + width)
+    xs = [torch.randn(batch, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
+    fa = torch.randn(heads, width, 3, generator=g) * 0.02
+    fb = torch.randn(heads, width, 3, generator=g) * 0.02
+    cfg = TaoConfig(fine_writer=writer, coarse_index_only=True)
+    geo = O.Geometry.from_config(cfg)
+    splits = [2540] + [1] * 30 + [250] + [1] * 5
+    d = [x.to(device) for x in xs]
+    state = new_state(0, cfg)
+    ora = O.OracleStream(0, geo, writer=writer)
+    outs, refs, start = [], [], 0
+    for w in splits:
+        sl = slice(start, start + w)
+        print(f"{writer} D{width}: tokens [{start}, {start + w})", flush=True)
+        fn = tao_attention_decode if w == 1 else tao_attention_prefill
+        out, state = fn(*(x[:, sl] for x in d[:3]), raw_q=d[3][:, sl], raw_k=d[4][:, sl],
+                        fusion_a=fa.to(device), fusion_b=fb.to(device), alpha=0.5,
+                        state=state, position=state.get_pos())
+        outs.append(out.cpu())
+        refs.append(ora.prefill(*(x[:, sl] for x in xs), fa, fb, 0.5))
+        start += w
+    torch.testing.assert_close(torch.cat(outs, 1).float(), torch.cat(refs, 1).float(),
+                               atol=2e-2, rtol=2e-2)
+    snap = state.export()
+    assert len(snap["pending_z"]) == 1 and len(snap["pages"]) == 1
+    assert torch.equal(snap["route_ids"][1].cpu(), ora.route_ids[1])
+    packed = snap["packed_fine_c"].cpu().float()
+    want = torch.stack(ora.fine_c, 2).float()
+    torch.testing.assert_close(packed, want, atol=2e-2, rtol=2e-2)
+    zs = [snap["pages"][0][0], snap["pages"][0][2], snap["pending_z"][0]]
+    wants = [ora.page_z[0], torch.stack(ora.fine_z[:8], 2), ora.fine_z[8]]
+    for got, ref in zip(zs, wants):
+        got, ref = got.cpu().double(), ref.double()
+        assert ((got - ref).abs() <= 2 ** -7 * ref.abs() + 1e-6).all()
+    close(snap["pending_mass"], ora.pending_mass, 1e-4)   # fp32 sums of 256 features

@@ -752,6 +752,12 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
     completed page, association_matrix of the in-order sums of its fines'
     statistics (oracle/writers.py).
 
+    The feature writers (index-only) follow _seal_training_all's feature
+    branches and _training_metadata (tao_stream.py:80-97, 543-549): z = r(log
+    mass), C from association_matrix / structured_matrix of the block, page
+    z = r(log) of the in-order mass sums, and each query's read the
+    numerator-only mixture over its selection (:656-662).
+
     Returns out [B, T, H, D] (and, with return_routes, a dict tile -> selected
     ids [B, Q, H, M] in score order).
     """
@@ -769,10 +775,22 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
     visible_max = max(0, n_tiles - 1 - lag)
     if total <= g.serve_limit or visible_max == 0:       # :682-688
         return (local, routes) if return_routes else local
-    zs, cs, stats = [], [], []
+    zs, cs, stats, masses = [], [], [], []
+    feature = writer in FEATURE_WRITERS
     for f in range(visible_max):
         kb, vb = raw_k[:, f * ft:(f + 1) * ft], v[:, f * ft:(f + 1) * ft]
-        z, c = seal_softmax(kb, vb)
+        if feature:
+            from . import writers as W
+            if writer == "structured_gram_association":
+                square, cross, mass = W.structured_statistics(kb, vb)
+                c = W.structured_matrix(square, cross, mass, ft)[1].to(kb.dtype)
+            else:
+                gram, cross, mass = W.association_statistics(kb, vb, with_mass=True)
+                c = W.association_matrix(gram, cross)[1].to(kb.dtype)
+            z = mass_descriptor(mass)
+            masses.append(mass)
+        else:
+            z, c = seal_softmax(kb, vb)
         if writer == "regularized_association":
             from . import writers as W
             stats.append(W.association_statistics(kb, vb))
@@ -782,8 +800,18 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
     fine_z = torch.stack(zs, 2)                          # [B, H, S, D]
     bank = torch.stack(cs, 2)                            # [B, H, S, D, D]
     full_pages = visible_max // group
-    page_z_full = [page_summary(fine_z[:, :, p * group:(p + 1) * group])
-                   for p in range(full_pages)]
+    def mass_sum(lo, hi):
+        total = masses[lo]
+        for i in range(lo + 1, hi):
+            total = total + masses[i]
+        return total
+
+    if feature:
+        page_z_full = [mass_descriptor(mass_sum(p * group, (p + 1) * group))
+                       for p in range(full_pages)]
+    else:
+        page_z_full = [page_summary(fine_z[:, :, p * group:(p + 1) * group])
+                       for p in range(full_pages)]
     page_c_full = []
     if not g.coarse_index_only and writer == "regularized_association":
         from . import writers as W
@@ -805,7 +833,9 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
             continue
         completed, pending = divmod(visible, group)
         parts = list(page_z_full[:completed])
-        if pending:
+        if pending and feature:
+            parts.append(mass_descriptor(mass_sum(completed * group, visible)))
+        elif pending:
             parts.append(page_summary(fine_z[:, :, completed * group:visible]))
         page_z = torch.stack(parts, 2)
         pw = page_weights(page_z)
@@ -822,7 +852,15 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
         fine = torch.empty_like(raw_q[:, start:end])
         tile_bank = bank[:, :, :visible]
         for i in range(nq):
-            part, _ = selected_read(hv[:, i:i + 1], sw, selected[:, i], tile_bank, group)
+            if feature:
+                sel = selected[:, i]                     # [B, H, M]
+                m_ = sel.shape[-1]
+                z_sel = torch.gather(fine_z[:, :, :visible], 2,
+                                     sel.unsqueeze(-1).expand(b, heads, m_, d))
+                c_sel = torch.gather(tile_bank, 2, sel[..., None, None].expand(b, heads, m_, d, d))
+                part = feature_read(h[:, i:i + 1], z_sel, c_sel)
+            else:
+                part, _ = selected_read(hv[:, i:i + 1], sw, selected[:, i], tile_bank, group)
             fine[:, i:i + 1] = part
         coarse_on = start >= first_coarse and not g.coarse_index_only
         fine_on = start >= g.serve_limit                 # first_fine

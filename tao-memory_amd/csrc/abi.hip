@@ -956,8 +956,8 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   rt.save_fine = pools ? (bf16_t*)pools->fine_out : nullptr;
   rt.save_den = pools ? pools->den_out : nullptr;
   rt.fine_z = feature_writer(st) ? (const bf16_t*)st->fine_z : nullptr;
-  if (feature_writer(st) && (query_routes || rt.save_fine))
-    return fail(TAO_E_ARGUMENT, "a feature writer reads turn routes without saves only");
+  if (feature_writer(st) && rt.save_fine)
+    return fail(TAO_E_ARGUMENT, "a feature writer's read keeps no saves (forward only)");
   e = tao::launch_read_tiles(rt, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill read");
   tao::AppendParams app{};

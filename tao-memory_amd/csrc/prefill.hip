@@ -49,7 +49,8 @@ __global__ __launch_bounds__(kThreads) void pages_kernel(PagesParams p) {
 }
 
 // One workgroup per (epoch, batch, head): the pending page summary with one
-// thread per channel, then the page weights with one wave per channel.
+// thread per channel, then the page weights, a segment of lanes (one lane
+// per page) per channel.
 template <int D>
 __global__ __launch_bounds__(kThreads) void epochs_kernel(EpochParams p) {
   __shared__ float pend_pz[D];
@@ -83,10 +84,35 @@ __global__ __launch_bounds__(kThreads) void epochs_kernel(EpochParams p) {
   if (P == 0) return;
   const bf16_t* pzg = p.page_z + (size_t)bh * p.page_cap * D;
   bf16_t* state_pw = p.page_w + (size_t)bh * p.page_cap * D;
+  auto desc = [&](int pg, int d) __attribute__((always_inline)) {
+    return pg == K ? pend_pz[d] : bf2f(pzg[(size_t)pg * D + d]);
+  };
+  if (P <= 64) {
+    // Segments of W = pow2 >= P lanes, one channel each (64 / W channels per
+    // pass of a wave). The lanes past P hold zeros, so the segment's xor fold
+    // adds exactly what wave_sum_fold adds over 64 lanes.
+    int W = 1;
+    while (W < P) W <<= 1;
+    const int per = 64 / W, pg = lane % W;
+    for (int d0 = wave * per; d0 < D; d0 += (kThreads / 64) * per) {
+      const int d = d0 + lane / W;
+      const float x = pg < P ? desc(pg, d) : -__builtin_inff();
+      float m = x;
+      for (int off = W / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+      const float e = pg < P ? exp_cr(x - m) : 0.0f;
+      float total = e;
+      for (int off = W / 2; off >= 1; off >>= 1) total += __shfl_xor(total, off, 64);
+      if (pg < P) {
+        const bf16_t w = f2bf(e / total);
+        pw[(size_t)pg * D + d] = w;
+        if (last) state_pw[(size_t)pg * D + d] = w;
+      }
+    }
+    return;
+  }
   for (int d = wave; d < D; d += kThreads / 64) {
     page_weights_wave(
-        lane, P,
-        [&](int pg) { return pg == K ? pend_pz[d] : bf2f(pzg[(size_t)pg * D + d]); },
+        lane, P, [&](int pg) { return desc(pg, d); },
         [&](int pg, bf16_t w) {
           pw[(size_t)pg * D + d] = w;
           if (last) state_pw[(size_t)pg * D + d] = w;
@@ -110,6 +136,7 @@ struct GroupSmem {
     bf16_t c[2][D][D + 8];        // staged weighted C^T, rows padded by 16 bytes
   } u;
   bf16_t wr[2][D];                     // per buffer: the staged fine's weights r(pw * sw)
+  float ez[2][D];                      // feature writers: exp(z) of the staged fine
   int ids[kGroupWaves][kMaxM];
   int uni[kMaxUnion];
   uint32_t mask[kMaxUnion / 4];        // byte u: bit w set if wave w selected uni[u]
@@ -171,8 +198,9 @@ TAO_DEV uint4 scale_slice(const uint4& c, const uint4& wr) {
 // unless its own query selected the fine, so a wave's 32 queries still share
 // every staged C^T and MFMA; the numerator and denominator of a query sum
 // exactly its selected fines (selected_read.py:156-173).
-template <int D, bool COARSE, bool PERQ>
+template <int D, bool COARSE, bool PERQ, bool FEAT>
 __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesParams p) {
+  static_assert(!FEAT || (PERQ && !COARSE), "the mixture read serves per-query index-only reads");
   constexpr int KK = D / 16, ET = D / 32, CPR = D / 8;   // k-steps, e-tiles, uint4 per row
   constexpr int CPT = D * CPR / kGroupThreads;           // C^T uint4 per thread
   static_assert(CPT == 1 || CPT == 4, "head width 64 or 128");
@@ -249,6 +277,36 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
   if constexpr (PERQ) {
     if (reads)
       qbits = p.qsel + ((size_t)(b * p.T + q_first + min(li, nq - 1)) * p.H + h) * p.qsel_words;
+  }
+
+  // Feature writers: the query's mixture normaliser, the sum over its
+  // selected fines (ascending id) of mass = sum_d h[d] exp(z[d]) in fp32,
+  // the same order as each fine's mass in the read.
+  auto h_of = [&](int kk, float hv[8]) __attribute__((always_inline)) { unpack8f(hA[kk], hv); };
+  float tot = 0.0f;
+  if constexpr (FEAT) {
+    if (reads && li < nq) {
+      const int words = (p.first_epoch + erel + 31) >> 5;
+      const bf16_t* zb = p.fine_z + (size_t)bh * p.fine_cap * D;
+      for (int i = 0; i < words; ++i) {
+        uint32_t bits = qbits[i];
+        while (bits) {
+          const int f = i * 32 + __ffs(bits) - 1;
+          bits &= bits - 1;
+          float part = 0.0f;
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) {
+            float hv[8], zf[8];
+            h_of(kk, hv);
+            unpack8f(*(const uint4*)(zb + (size_t)f * D + 16 * kk + 8 * hl), zf);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) part += hv[j] * expf(zf[j]);
+          }
+          part += __shfl_xor(part, 32, 64);
+          tot += part;
+        }
+      }
+    }
   }
 
   floatx16 acc[ET];
@@ -372,10 +430,14 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
 #define TAO_LOAD_C(u, X)                                                           \
   do {                                                                             \
     const int cid = sm.uni[(u)];                                                   \
-    const bf16_t* swr_ = cid < sw_split ? sw_base + (size_t)cid * D                \
-                                        : psw_base + (size_t)(cid - sw_split) * D; \
-    X##p = *(const uint4*)(pw_base + (size_t)(cid / p.group) * D + cc * 8);        \
-    X##s = *(const uint4*)(swr_ + cc * 8);                                         \
+    if constexpr (FEAT) {                                                          \
+      X##p = *(const uint4*)(p.fine_z + ((size_t)bh * p.fine_cap + cid) * D + cc * 8); \
+    } else {                                                                       \
+      const bf16_t* swr_ = cid < sw_split ? sw_base + (size_t)cid * D              \
+                                          : psw_base + (size_t)(cid - sw_split) * D; \
+      X##p = *(const uint4*)(pw_base + (size_t)(cid / p.group) * D + cc * 8);      \
+      X##s = *(const uint4*)(swr_ + cc * 8);                                       \
+    }                                                                              \
     X##0 = *(const uint4*)TAO_C_CHUNK(0);                                          \
     if constexpr (CPT == 4) {                                                      \
       X##1 = *(const uint4*)TAO_C_CHUNK(1);                                        \
@@ -387,6 +449,21 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
   (*(uint4*)&sm.u.c[(buf)][(tid + (i_) * kGroupThreads) / CPR][cc * 8])
 #define TAO_STORE_C(buf, X)                                              \
   do {                                                                   \
+    if constexpr (FEAT) {                                                \
+      if (tid < CPR) {                                                   \
+        float zf_[8];                                                    \
+        unpack8f(X##p, zf_);                                             \
+        _Pragma("unroll") for (int j_ = 0; j_ < 8; ++j_)                 \
+          sm.ez[(buf)][cc * 8 + j_] = expf(zf_[j_]);                     \
+      }                                                                  \
+      TAO_C_SLOT(buf, 0) = X##0;                                         \
+      if constexpr (CPT == 4) {                                          \
+        TAO_C_SLOT(buf, 1) = X##1;                                       \
+        TAO_C_SLOT(buf, 2) = X##2;                                       \
+        TAO_C_SLOT(buf, 3) = X##3;                                       \
+      }                                                                  \
+      break;                                                             \
+    }                                                                    \
     const uint4 wr_ = slice_weights(X##p, X##s);                         \
     if (tid < CPR) *(uint4*)&sm.wr[(buf)][cc * 8] = wr_;                 \
     TAO_C_SLOT(buf, 0) = scale_slice(X##0, wr_);                         \
@@ -411,6 +488,36 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
           qword = li < nq ? qbits[qword_at] : 0u;
         }
         keep = ((qword >> (id & 31)) & 1u) ? 0xFFFFFFFFu : 0u;
+      }
+      if constexpr (FEAT) {
+        // coef = r(mix * h) with mix = mass / tot of this fine, rows of
+        // queries that did not select it zero; no denominator.
+        float part = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          float hv[8];
+          h_of(kk, hv);
+          const float* ez = &sm.ez[buf][16 * kk + 8 * hl];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) part += hv[j] * ez[j];
+        }
+        part += __shfl_xor(part, 32, 64);
+        const float mix = keep ? part / tot : 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          const int d0 = 16 * kk + 8 * hl;
+          float hv[8];
+          h_of(kk, hv);
+          const bf16x8 a = as_bf16x8(make_uint4(
+              pack_bf16x2(mix * hv[0], mix * hv[1]), pack_bf16x2(mix * hv[2], mix * hv[3]),
+              pack_bf16x2(mix * hv[4], mix * hv[5]), pack_bf16x2(mix * hv[6], mix * hv[7])));
+#pragma unroll
+          for (int t = 0; t < ET; ++t) {
+            const bf16x8 bq = as_bf16x8(*(const uint4*)&sm.u.c[buf][32 * t + li][d0]);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq, acc[t], 0, 0, 0);
+          }
+        }
+        return;
       }
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
@@ -502,7 +609,8 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
       const int q = 8 * (i / 4) + 4 * hl + (i % 4);
       if (q < nq) {
         const int tq = q_first + q;
-        const float fine = rbf(rbf(av[i]) * __builtin_amdgcn_rcpf(rbf(acc_den[i])));
+        const float fine =
+            FEAT ? rbf(av[i]) : rbf(rbf(av[i]) * __builtin_amdgcn_rcpf(rbf(acc_den[i])));
         const size_t row = ((size_t)b * p.T + tq) * p.H + h;
         if (p.save_fine) {
           p.save_fine[row * D + e] = f2bf(fine);
@@ -1092,16 +1200,23 @@ hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t
   const bool perq = p.qsel != nullptr;
   if (perq && (p.qsel_words < 1 || p.qsel_words > kBitWords)) return hipErrorInvalidValue;
 #define TAO_READ_LAUNCH(D_, C_, Q_)                                                           \
-  hipLaunchKernelGGL((read_groups_kernel<D_, C_, Q_>), grid, dim3(kGroupThreads), 0, s, p)
+  hipLaunchKernelGGL((read_groups_kernel<D_, C_, Q_, false>), grid, dim3(kGroupThreads), 0, s, p)
+#define TAO_MIXTURE_LAUNCH(D_)                                                                \
+  hipLaunchKernelGGL((read_groups_kernel<D_, false, true, true>), grid, dim3(kGroupThreads), 0, \
+                     s, p)
 #define TAO_STREAM_LAUNCH(D_, C_)                                                             \
   hipLaunchKernelGGL((read_stream_kernel<D_, C_, false>), grid, dim3(kGroupThreads), 0, s, p)
 #define TAO_FEATURE_LAUNCH(D_)                                                                \
   hipLaunchKernelGGL((read_stream_kernel<D_, false, true>), grid, dim3(kGroupThreads), 0, s, p)
   if (head_dim != 128 && head_dim != 64) return hipErrorInvalidValue;
   if (p.fine_z) {
-    // Feature writers: turn routes, index-only, no saves.
-    if (perq || coarse || p.save_fine) return hipErrorInvalidValue;
-    if (head_dim == 128) TAO_FEATURE_LAUNCH(128); else TAO_FEATURE_LAUNCH(64);
+    // Feature writers: index-only, no saves; per-query or turn routes.
+    if (coarse || p.save_fine) return hipErrorInvalidValue;
+    if (perq) {
+      if (head_dim == 128) TAO_MIXTURE_LAUNCH(128); else TAO_MIXTURE_LAUNCH(64);
+    } else {
+      if (head_dim == 128) TAO_FEATURE_LAUNCH(128); else TAO_FEATURE_LAUNCH(64);
+    }
     return hipGetLastError();
   }
   if (head_dim == 128) {

@@ -34,8 +34,18 @@ from .config import TaoConfig
 _VALUE_WRITERS = ("softmax", "regularized_association")
 
 
+# Writers with log-mass descriptors and the numerator-only mixture read
+# (tao_stream.py:80-123, 600-662): forward only, index-only.
+_FEATURE_WRITERS = ("feature_mass_association", "structured_gram_association")
+
+
 def _check(q, k, v, raw_q, raw_k, config, dtype=torch.bfloat16):
-    if config.fine_writer not in _VALUE_WRITERS:
+    if config.fine_writer in _FEATURE_WRITERS:
+        if not config.coarse_index_only:
+            raise NotImplementedError(
+                "the HIP full-sequence read implements the feature writers with "
+                "coarse_index_only=True (their coarse value read is not built)")
+    elif config.fine_writer not in _VALUE_WRITERS:
         raise NotImplementedError(
             f"the HIP full-sequence read implements the fine writers {_VALUE_WRITERS}")
     if config.fine_tokens != 256 or config.local_keep != 512 or config.coarse_group != 8:
@@ -445,6 +455,10 @@ def full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
                 "the fp32 full-sequence read is forward-only: run it under torch.no_grad() "
                 "or on bf16 operands for gradients")
         return forward_f32(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config)
+    if grad and config.fine_writer in _FEATURE_WRITERS:
+        raise NotImplementedError(
+            "gradients through the feature writers are not built: run their full-sequence "
+            "read under torch.no_grad()")
     if local_flash is not None:
         from .flash_attention import plugin_training_local
         _check(q, k, v, raw_q, raw_k, config)

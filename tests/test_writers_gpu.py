@@ -330,3 +330,42 @@ def test_stream_feature_writers(device, writer, width):
         got, ref = got.cpu().double(), ref.double()
         assert ((got - ref).abs() <= 2 ** -7 * ref.abs() + 1e-6).all()
     close(snap["pending_mass"], ora.pending_mass, 1e-4)   # fp32 sums of 256 features
+
+
+@pytest.mark.parametrize("writer,width,tokens,batch", [
+    ("feature_mass_association", 64, 2900, 1), ("structured_gram_association", 128, 2900, 2),
+    ("feature_mass_association", 128, 1300, 1)])
+def test_full_sequence_feature_writers(device, writer, width, tokens, batch):
+    """tao_attention with the feature writers (index-only, forward): every
+    query's selected set bit-exact against the oracle's per-query routing
+    over log-mass descriptors, outputs within the bf16 tolerance of its
+    numerator-only mixture read; gradients raise."""
+    from oracle import tao_oracle as O
+    from tao_attention import TaoConfig, tao_attention, training
+    heads = 2
+    g = torch.Generator().manual_seed(97 + width + batch)
+    xs = [torch.randn(batch, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
+    fa = torch.randn(heads, width, 3, generator=g) * 0.02
+    fb = torch.randn(heads, width, 3, generator=g) * 0.02
+    cfg = TaoConfig(fine_writer=writer, coarse_index_only=True)
+    q, k, v, rq, rk = (x.to(device) for x in xs)
+    out, qsel = training.forward(q, k, v, rq, rk, fa.to(device), fb.to(device), 0.5, cfg,
+                                 return_routes=True)
+    ref, routes = O.training_forward(*xs, fa, fb, 0.5, O.Geometry.from_config(cfg),
+                                     return_routes=True, writer=writer)
+    assert routes, "the call must read history"
+    got = _bitmask_sets(qsel)
+    for tile, sel in routes.items():
+        s = tile * 256
+        part = got[:, s:s + sel.shape[1]]
+        want = torch.zeros_like(part)
+        want.scatter_(-1, sel, True)
+        assert torch.equal(part, want), f"selected sets of tile {tile}"
+    torch.testing.assert_close(out.cpu().float(), ref.float(), atol=2e-2, rtol=2e-2)
+    api = tao_attention(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.to(device),
+                        fusion_b=fb.to(device), alpha=0.5, config=cfg)
+    assert torch.equal(api, out)
+    qg = q.clone().requires_grad_()
+    with pytest.raises(NotImplementedError):
+        tao_attention(qg, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.to(device),
+                      fusion_b=fb.to(device), alpha=0.5, config=cfg)

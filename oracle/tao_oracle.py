@@ -877,7 +877,7 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
 
 
 def training_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, routes,
-                            geometry=None, intermediates=None):
+                            geometry=None, intermediates=None, writer="softmax"):
     """training_forward's function without bf16 rounding, for gradients.
 
     Same steps as training_forward (local attention per tile, the softmax
@@ -890,6 +890,11 @@ def training_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, ro
     forward's selections. Differentiable by torch autograd. A dict
     `intermediates` receives the fine descriptors "fine_z" [B, H, S, D] and
     the bank "bank" [B, H, S, D, D] (C[d][e]), to take gradients at them.
+
+    writer="regularized_association" (index-only) keeps the softmax writer's
+    z and takes C_f = solve(G + tr(G)/D I, X) with G = U^T U, X = U^T V,
+    U = softmax_D(raw_k) of the block (association_writer.py:11-32 without
+    its bf16 casts), differentiable through the solve.
     """
     g = geometry or Geometry()
     b, total, heads, d = q.shape
@@ -913,7 +918,15 @@ def training_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, ro
     for f in range(visible_max):
         kb, vb = raw_k[:, f * ft:(f + 1) * ft], v[:, f * ft:(f + 1) * ft]
         zs.append(torch.logsumexp(kb, 1))                           # [B, H, D]
-        cs.append(torch.einsum("bthd,bthe->bhde", torch.softmax(kb, 1), vb))
+        if writer == "regularized_association":
+            u = torch.softmax(kb, -1)                               # over channels
+            gram = torch.einsum("bthd,bthe->bhde", u, u)
+            cross = torch.einsum("bthd,bthe->bhde", u, vb)
+            ridge = gram.diagonal(dim1=-2, dim2=-1).sum(-1) / d
+            system = gram + ridge[..., None, None] * torch.eye(d, dtype=gram.dtype)
+            cs.append(torch.linalg.solve(system, cross))
+        else:
+            cs.append(torch.einsum("bthd,bthe->bhde", torch.softmax(kb, 1), vb))
     fine_z = torch.stack(zs, 2)
     bank = torch.stack(cs, 2)
     if intermediates is not None:

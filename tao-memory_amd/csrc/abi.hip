@@ -320,6 +320,72 @@ hipError_t feature_seal(const tao_state_dev* st, const tao::TokView& rk, const t
   return hipSuccess;
 }
 
+// The regularized writer's share of the backward (association_writer.py:
+// 11-32 under autograd): the fines' statistics again, Y = A^{-1} cross and
+// W = A^{-1} dC in fp32, S = dG + dG^T, then per block d raw_k's share
+// (written to dk_extra) and dv's (added to dv).
+hipError_t assoc_backward(const tao_state_dev* st, const tao_tokens* tok, char* ws,
+                          size_t stats_off, size_t y_off, size_t w_off, size_t s_off,
+                          size_t dk_off, size_t starts_off, const float* dc, float* dv,
+                          int fines, int T, hipStream_t s) {
+  const int B = st->batch, H = st->heads, D = st->head_dim, ft = st->fine_tokens;
+  const int mats = fines * B * H;
+  int64_t* starts = (int64_t*)(ws + starts_off);
+  hipError_t e = tao::launch_block_starts(starts, fines, ft, s);
+  if (e != hipSuccess) return e;
+  float* gram = (float*)(ws + stats_off);
+  float* cross = gram + (size_t)mats * D * D;
+  const tao::TokView rk = view(tok->raw_k, tok->rk_s), vv = view(tok->v, tok->v_s);
+  tao::WriterStatsParams sp{};
+  sp.k = rk.p;
+  sp.v = vv.p;
+  sp.k_s[0] = rk.sb; sp.k_s[1] = rk.st; sp.k_s[2] = rk.sh;
+  sp.v_s[0] = vv.sb; sp.v_s[1] = vv.st; sp.v_s[2] = vv.sh;
+  sp.N = fines * B;
+  sp.T = ft;
+  sp.H = H;
+  sp.gram = gram;
+  sp.cross = cross;
+  sp.starts = starts;
+  sp.new_base = 0;
+  sp.ring_raw = (const bf16_t*)st->ring_raw;
+  sp.ring_v = (const bf16_t*)st->ring_v;
+  sp.L = st->local_keep + st->fine_tokens;
+  sp.B = B;
+  e = tao::launch_writer_stats(sp, D, s);
+  if (e != hipSuccess) return e;
+  tao::AssocSolveParams fp{};
+  fp.gram = gram;
+  fp.cross = cross;
+  fp.count = mats;
+  fp.B = B;
+  fp.H = H;
+  fp.out_f32 = (float*)(ws + y_off);
+  e = tao::launch_association_solve(fp, D, s);
+  if (e != hipSuccess) return e;
+  fp.out_f32 = (float*)(ws + w_off);
+  fp.rhs_t = dc;
+  fp.rhs_cap = fines;
+  e = tao::launch_association_solve(fp, D, s);
+  if (e != hipSuccess) return e;
+  tao::AssocBwdParams bp{};
+  bp.w = (const float*)(ws + w_off);
+  bp.y = (const float*)(ws + y_off);
+  bp.s = (float*)(ws + s_off);
+  bp.raw_k = rk;
+  bp.v = vv;
+  bp.dk = (float*)(ws + dk_off);
+  bp.dv = dv;
+  bp.mats = mats;
+  bp.B = B;
+  bp.H = H;
+  bp.T = T;
+  bp.ft = ft;
+  e = tao::launch_assoc_gram_bwd(bp, D, s);
+  if (e != hipSuccess) return e;
+  return tao::launch_assoc_block_bwd(bp, D, s);
+}
+
 struct DecodeGraph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -1110,6 +1176,8 @@ struct TrainBwdLayout {
   size_t dlocal, h, delta, dden, dcoarse, dnum, drq, dh, dvf;   // per-token arrays
   size_t dpw, dsw_tile, dgc, dc, dsw, dpz, dz, dalpha;          // memory branch, d alpha
   size_t dalpha_parts;                                          // per fusion workgroup
+  // regularized writer: statistics, solutions Y and W, S, d raw_k share, starts
+  size_t stats, sol_y, sol_w, sgram, dk_extra, starts;
   size_t zero_begin, zero_end;                                  // accumulators to clear
   size_t total;
   int n_tiles, v_max;
@@ -1150,6 +1218,15 @@ TrainBwdLayout train_bwd_layout(const tao_state_dev* st, int64_t tokens, int fin
   l.dalpha = take(4);
   l.zero_end = off;
   l.dalpha_parts = take((size_t)tao::fuse_bwd_workgroups((int)T, (int)B, (int)H) * 4);
+  if (st->pending_gram && fines > 0) {
+    const size_t mats = (size_t)fines * BH, mat = D * D * 4;
+    l.stats = take(2 * mats * mat);
+    l.sol_y = take(mats * mat);
+    l.sol_w = take(mats * mat);
+    l.sgram = take(mats * mat);
+    l.dk_extra = take(rows * D * 4);
+    l.starts = take((size_t)fines * 8);
+  }
   l.total = off;
   return l;
 }
@@ -1194,6 +1271,12 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   }
   const TrainBwdLayout l = train_bwd_layout(st, T, fines, fines > 0 ? pools : nullptr);
   if (a->workspace_bytes < l.total) return fail(TAO_E_WORKSPACE, "backward workspace too small");
+  const bool regularized = assoc_writer(st) && fines > 0;
+  if (regularized && st->page_c)
+    return fail(TAO_E_ARGUMENT,
+                "gradients through the regularized writer's page matrices are not built "
+                "(index-only states only)");
+  if (feature_writer(st)) return fail(TAO_E_ARGUMENT, "gradients through a feature writer");
   const hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)a->workspace;
   const int D = st->head_dim, H = st->heads, B = st->batch;
@@ -1304,8 +1387,17 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   mp.page_cap = st->page_cap;
   mp.v_max = fines;
   mp.coarse_values = st->page_c != nullptr;
-  e = tao::launch_mem_bwd(mp, D, s);
+  e = tao::launch_mem_bwd_read(mp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_train_backward memory branch");
+  if (regularized) {
+    e = assoc_backward(st, tok, ws, l.stats, l.sol_y, l.sol_w, l.sgram, l.dk_extra, l.starts,
+                       mp.dc, mp.dv, fines, (int)T, s);
+    if (e != hipSuccess) return check_hip(e, "tao_train_backward association writer");
+    mp.values_external = 1;
+    mp.dk_extra = (const float*)(ws + l.dk_extra);
+  }
+  e = tao::launch_mem_bwd_writer(mp, D, s);
+  if (e != hipSuccess) return check_hip(e, "tao_train_backward writer branch");
   const size_t BHf = (size_t)B * H * fines;
   if (a->dz_out && fines > 0) {
     e = hipMemcpyAsync(a->dz_out, mp.dz, BHf * D * sizeof(float), hipMemcpyDeviceToDevice, s);

@@ -193,10 +193,15 @@ __global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocS
   SolveSmem<D>& sm = *reinterpret_cast<SolveSmem<D>*>(solve_smem);
   const int mat = blockIdx.x;
   const int tid = threadIdx.x;
-  const int blk = p.to_slots ? mat / (p.B * p.H) : 0;
+  const int blk = (p.to_slots || p.rhs_t) ? mat / (p.B * p.H) : 0;
   if (p.to_slots == 2 && (p.fine_first + blk) % p.group != p.group - 1) return;   // uniform
   const float* g = p.gram + (size_t)mat * D * D;
   const float* c = p.cross + (size_t)mat * D * D;
+  const float* rt = nullptr;   // transposed right-hand side ([e][d])
+  if (p.rhs_t) {
+    const int b = (mat / p.H) % p.B, h = mat % p.H;
+    rt = p.rhs_t + (((size_t)b * p.H + h) * p.rhs_cap + blk) * D * D;
+  }
   // ridge = trace / D
   float tr = 0.0f;
   for (int i = tid; i < D; i += kSolveThreads) tr += g[(size_t)i * D + i];
@@ -210,7 +215,7 @@ __global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocS
   for (int i = tid; i < D * D; i += kSolveThreads) {
     const int r = i / D, col = i % D;
     sm.a[r][col] = g[i] + (r == col ? ridge : 0.0f);
-    sm.x[r][col] = c[i];
+    sm.x[r][col] = rt ? rt[(size_t)col * D + r] : c[i];
   }
   // Blocked right-looking Cholesky, PB columns a step: wave 0 factors the
   // panel (rows >= jb, wave-synchronous), then all threads apply its rank-PB
@@ -310,6 +315,11 @@ __global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocS
       sm.x[k][e] = v;
     }
     __syncthreads();
+  }
+  if (p.out_f32) {
+    float* out = p.out_f32 + (size_t)mat * D * D;
+    for (int i = tid; i < D * D; i += kSolveThreads) out[i] = sm.x[i / D][i % D];
+    return;
   }
   if (!p.to_slots) {
     bf16_t* out = p.out + (size_t)mat * D * D;
@@ -523,6 +533,228 @@ hipError_t launch_feature_descriptors(const FeatureDescParams& p, int head_dim, 
     hipLaunchKernelGGL(feature_desc_kernel<64>, grid, dim3(256), 0, s, p);
   else
     return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// ---- regularized writer backward (see AssocBwdParams)
+
+__global__ __launch_bounds__(256) void block_starts_kernel(int64_t* starts, int count,
+                                                            int64_t step) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < count) starts[i] = (int64_t)i * step;
+}
+
+// One workgroup per matrix: S[i][j] = -(W Y^T + Y W^T)[i][j] + 2 tr(-W Y^T) / D
+// [i == j], with W and Y staged in LDS (rows padded by one float). Thread
+// entries run i fastest (distinct banks for W[i][.], Y[i][.]); S is
+// symmetric, so entry (i, j) is stored at [j][i] for coalesced stores.
+template <int D>
+struct GramBwdSmem {
+  float w[D][D + 1];
+  float y[D][D + 1];
+  float red[4];
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void assoc_gram_bwd_kernel(AssocBwdParams p) {
+  extern __shared__ __align__(16) unsigned char gram_bwd_smem[];
+  GramBwdSmem<D>& sm = *reinterpret_cast<GramBwdSmem<D>*>(gram_bwd_smem);
+  const int mat = blockIdx.x, tid = threadIdx.x;
+  const float* w = p.w + (size_t)mat * D * D;
+  const float* y = p.y + (size_t)mat * D * D;
+  float tr = 0.0f;
+  for (int i = tid; i < D * D; i += 256) {
+    const float wv = w[i], yv = y[i];
+    sm.w[i / D][i % D] = wv;
+    sm.y[i / D][i % D] = yv;
+    tr += wv * yv;
+  }
+  tr = wave_sum_fold(tr);
+  if ((tid & 63) == 0) sm.red[tid >> 6] = tr;
+  __syncthreads();
+  const float trace = -(sm.red[0] + sm.red[1] + sm.red[2] + sm.red[3]);   // tr(-W Y^T)
+  float* out = p.s + (size_t)mat * D * D;
+  for (int idx = tid; idx < D * D; idx += 256) {
+    const int i = idx % D, j = idx / D;
+    float acc = 0.0f;
+    for (int e = 0; e < D; ++e) acc += sm.w[i][e] * sm.y[j][e] + sm.y[i][e] * sm.w[j][e];
+    out[(size_t)j * D + i] = -acc + (i == j ? 2.0f * trace / (float)D : 0.0f);
+  }
+}
+
+// One workgroup per (fine block, batch, head), 8 waves x 32 tokens. Lane
+// (li, hl) of wave w holds token 32 w + li's channels 16 kk + 8 hl + j in
+// the MFMA A layout: u = r(softmax_D(raw_k)) and v. du = V W^T + U S (B
+// operand column d: row d of W, of S); dv += U W (column e: row e of W^T).
+template <int D>
+struct BlockBwdSmem {
+  bf16_t w[D][D + 8];    // W [d][e]
+  bf16_t wt[D][D + 8];   // W^T [e][d]
+  bf16_t sg[D][D + 8];   // S [d][d']
+  float mx[256], iz[256];   // per token: max and 1 / sum of exp
+};
+
+template <int D>
+__global__ __launch_bounds__(512) void assoc_block_bwd_kernel(AssocBwdParams p) {
+  constexpr int KK = D / 16, DT = D / 32;
+  extern __shared__ __align__(16) unsigned char block_bwd_smem[];
+  BlockBwdSmem<D>& sm = *reinterpret_cast<BlockBwdSmem<D>*>(block_bwd_smem);
+  const int mat = blockIdx.x;
+  const int f = mat / (p.B * p.H), b = (mat / p.H) % p.B, h = mat % p.H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
+  const float* wg = p.w + (size_t)mat * D * D;
+  const float* sg = p.s + (size_t)mat * D * D;
+  for (int i = tid; i < D * D; i += 512) {
+    const int r = i / D, c = i % D;
+    const bf16_t wv = f2bf(wg[i]);
+    sm.w[r][c] = wv;
+    sm.wt[c][r] = wv;
+    sm.sg[r][c] = f2bf(sg[i]);
+  }
+  const int tok0 = f * p.ft;
+  const int t_row = tok0 + 32 * w + li;
+  const bf16_t* krow = p.raw_k.p + b * p.raw_k.sb + (int64_t)t_row * p.raw_k.st + h * p.raw_k.sh;
+  const bf16_t* vrow = p.v.p + b * p.v.sb + (int64_t)t_row * p.v.st + h * p.v.sh;
+  // softmax over the channels of this lane's token (both halves of the row)
+  float kv[KK][8];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    const uint4 ku = *(const uint4*)(krow + 16 * kk + 8 * hl);
+    const uint32_t kw[4] = {ku.x, ku.y, ku.z, ku.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      kv[kk][2 * j] = __uint_as_float(kw[j] << 16);
+      kv[kk][2 * j + 1] = __uint_as_float(kw[j] & 0xFFFF0000u);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, kv[kk][j]);
+  }
+  m = fmaxf(m, __shfl_xor(m, 32, 64));
+  float z = 0.0f;
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { kv[kk][j] = __expf(kv[kk][j] - m); z += kv[kk][j]; }
+  z += __shfl_xor(z, 32, 64);
+  const float iz = 1.0f / z;
+  if (hl == 0) { sm.mx[32 * w + li] = m; sm.iz[32 * w + li] = iz; }
+  bf16x8 ua[KK], va[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    va[kk] = as_bf16x8(*(const uint4*)(vrow + 16 * kk + 8 * hl));
+    uint32_t pk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pk[j] = pack_bf16x2(kv[kk][2 * j] * iz, kv[kk][2 * j + 1] * iz);
+    ua[kk] = as_bf16x8(make_uint4(pk[0], pk[1], pk[2], pk[3]));
+  }
+  __syncthreads();
+  // du tiles (lane = column d = 32 t + li, rows = tokens 8 (i/4) + 4 hl + i%4)
+  floatx16 du[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) du[t][i] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      du[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          va[kk], as_bf16x8(*(const uint4*)&sm.w[32 * t + li][16 * kk + 8 * hl]), du[t], 0, 0, 0);
+      du[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          ua[kk], as_bf16x8(*(const uint4*)&sm.sg[32 * t + li][16 * kk + 8 * hl]), du[t], 0, 0, 0);
+    }
+  }
+  // p at the accumulator positions, and sum_d p du per token row
+  float pv[DT][16], part[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) part[i] = 0.0f;
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    const int d = 32 * t + li;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = 32 * w + 8 * (i / 4) + 4 * hl + (i % 4);
+      const float kx = bf2f(p.raw_k.p[b * p.raw_k.sb + (int64_t)(tok0 + r) * p.raw_k.st +
+                                      h * p.raw_k.sh + d]);
+      pv[t][i] = __expf(kx - sm.mx[r]) * sm.iz[r];
+      part[i] += pv[t][i] * du[t][i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) part[i] += __shfl_xor(part[i], off, 64);
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    const int d = 32 * t + li;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int tok = tok0 + 32 * w + 8 * (i / 4) + 4 * hl + (i % 4);
+      p.dk[(((size_t)b * p.T + tok) * p.H + h) * D + d] = pv[t][i] * (du[t][i] - part[i]);
+    }
+  }
+  // dv += U W (lane = column e)
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    floatx16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          ua[kk], as_bf16x8(*(const uint4*)&sm.wt[32 * t + li][16 * kk + 8 * hl]), acc, 0, 0, 0);
+    const int e = 32 * t + li;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int tok = tok0 + 32 * w + 8 * (i / 4) + 4 * hl + (i % 4);
+      p.dv[(((size_t)b * p.T + tok) * p.H + h) * D + e] += acc[i];
+    }
+  }
+}
+
+hipError_t launch_block_starts(int64_t* starts, int count, int64_t step, hipStream_t s) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(block_starts_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s,
+                     starts, count, step);
+  return hipGetLastError();
+}
+
+template <typename K>
+hipError_t big_lds(K kernel, size_t bytes) {
+  return hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)bytes);
+}
+
+hipError_t launch_assoc_gram_bwd(const AssocBwdParams& p, int head_dim, hipStream_t s) {
+  if (p.mats <= 0) return hipSuccess;
+  if (head_dim == 128) {
+    const size_t bytes = sizeof(GramBwdSmem<128>);
+    hipError_t e = big_lds(assoc_gram_bwd_kernel<128>, bytes);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(assoc_gram_bwd_kernel<128>, dim3((unsigned)p.mats), dim3(256), bytes, s, p);
+  } else if (head_dim == 64) {
+    hipLaunchKernelGGL(assoc_gram_bwd_kernel<64>, dim3((unsigned)p.mats), dim3(256),
+                       sizeof(GramBwdSmem<64>), s, p);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_assoc_block_bwd(const AssocBwdParams& p, int head_dim, hipStream_t s) {
+  if (p.mats <= 0) return hipSuccess;
+  if (p.ft != 256) return hipErrorInvalidValue;
+  if (head_dim == 128) {
+    const size_t bytes = sizeof(BlockBwdSmem<128>);
+    hipError_t e = big_lds(assoc_block_bwd_kernel<128>, bytes);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(assoc_block_bwd_kernel<128>, dim3((unsigned)p.mats), dim3(512), bytes, s, p);
+  } else if (head_dim == 64) {
+    hipLaunchKernelGGL(assoc_block_bwd_kernel<64>, dim3((unsigned)p.mats), dim3(512),
+                       sizeof(BlockBwdSmem<64>), s, p);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

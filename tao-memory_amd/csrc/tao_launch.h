@@ -381,8 +381,17 @@ struct MemBwdParams {
   float* dv;                     // [B, T, H, D] fp32 (local part in, writer part added)
   bf16_t* draw_q; bf16_t* draw_k; bf16_t* dv_out;
   int B, H, T, ft, keep, group, fine_cap, page_cap, v_max, coarse_values;
+  // Value matrices not from the softmax writer (regularized writer): the
+  // writer adjoint takes only the z path, and dk_extra (fp32 [B, T, H, D],
+  // nullable) is added to d raw_k of the block tokens.
+  int values_external;
+  const float* dk_extra;
 };
-hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s);
+// The memory branch in two parts: read_part (the read's adjoints down to dC
+// and dz) and writer_part (the writer adjoint and the finish); a caller may
+// change dC's consumers in between.
+hipError_t launch_mem_bwd_read(const MemBwdParams& p, int head_dim, hipStream_t s);
+hipError_t launch_mem_bwd_writer(const MemBwdParams& p, int head_dim, hipStream_t s);
 
 // ---- non-preset fine writers and the channel-given selected read
 
@@ -415,8 +424,33 @@ struct AssocSolveParams {
   // whose fine slot (fine_first + blk) completes a page (slot % group ==
   // group - 1), into page slot / group.
   int to_slots, B, H, cap, first_slot, fine_first, group;
+  // Optional (to_slots 0): the fp32 solution [count, D, D] (rows d) instead
+  // of the bf16 one; and a right-hand side other than cross: matrix
+  // mat = (blk * B + b) * H + h takes rhs_t[(b H + h) rhs_cap + blk] as
+  // its transpose ([e][d], fp32).
+  float* out_f32;
+  const float* rhs_t; int rhs_cap;
 };
 hipError_t launch_association_solve(const AssocSolveParams& p, int head_dim, hipStream_t s);
+
+// Regularized writer backward over the call's fine blocks (tao_train_backward;
+// association_writer.py:11-32 differentiated): matrix mat = (f B + b) H + h
+// belongs to tokens [ft f, ft f + ft) of batch row b, head h. With
+// A = gram + tr(gram)/D I, Y = A^{-1} cross (the fp32 C) and W = A^{-1} dC:
+//   S = dG + dG^T, dG = -W Y^T + tr(-W Y^T)/D I             (assoc_gram_bwd)
+//   du = V W^T + U S, dv += U W, dk = p (du - sum_d p du)   (assoc_block_bwd)
+// with u = r(p), p = softmax_D(raw_k) per token.
+struct AssocBwdParams {
+  const float* w; const float* y; float* s;   // [mats][D][D]
+  TokView raw_k, v;
+  float* dk;                     // [B, T, H, D] fp32, written for block tokens
+  float* dv;                     // [B, T, H, D] fp32, accumulated
+  int mats, B, H, T, ft;
+};
+hipError_t launch_assoc_gram_bwd(const AssocBwdParams& p, int head_dim, hipStream_t s);
+hipError_t launch_assoc_block_bwd(const AssocBwdParams& p, int head_dim, hipStream_t s);
+// starts[i] = i * step (the token blocks of a full-sequence call).
+hipError_t launch_block_starts(int64_t* starts, int count, int64_t step, hipStream_t s);
 
 struct StructuredParams {
   const float* square; const float* cross; const float* mass;

@@ -1350,10 +1350,11 @@ __global__ __launch_bounds__(kWbWaves * 64) void writer_bwd_kernel(MemBwdParams 
   const float* dcg = p.dc + ((size_t)bh * p.v_max + f) * D * D;               // dC^T [e][d]
   const bf16_t* c = p.bank + ((size_t)bh * p.fine_cap + f) * D * D;           // C^T [e][d]
   const float* dzf = p.dz + ((size_t)bh * p.v_max + f) * D;
-  // ---- stage dC^T (as is) and dC (transposed), bf16
+  // ---- stage dC^T (as is) and dC (transposed), bf16; zero when the value
+  // matrices are not this writer's (only its z path remains)
   for (int i = tid; i < D * D; i += NT) {
     const int e = i / D, d = i % D;
-    const bf16_t v = f2bf(dcg[i]);
+    const bf16_t v = p.values_external ? (bf16_t)0 : f2bf(dcg[i]);
     sm.dct[e][d] = v;
     sm.dc[d][e] = v;
   }
@@ -1368,9 +1369,11 @@ __global__ __launch_bounds__(kWbWaves * 64) void writer_bwd_kernel(MemBwdParams 
 #pragma unroll
     for (int i = 0; i < TPG; ++i) xv[i] = bf2f(col[(int64_t)(tok0 + tg * TPG + i) * p.raw_k.st]);
     float sdc = 0.0f;
+    if (!p.values_external) {
 #pragma unroll 4
-    for (int e = tg * EPG; e < (tg + 1) * EPG; ++e)
-      sdc = fmaf(dcg[(size_t)e * D + d], bf2f(c[(size_t)e * D + d]), sdc);
+      for (int e = tg * EPG; e < (tg + 1) * EPG; ++e)
+        sdc = fmaf(dcg[(size_t)e * D + d], bf2f(c[(size_t)e * D + d]), sdc);
+    }
     float m = -__builtin_inff();
 #pragma unroll
     for (int i = 0; i < TPG; ++i) m = fmaxf(m, xv[i]);
@@ -1435,7 +1438,8 @@ __global__ __launch_bounds__(kWbWaves * 64) void writer_bwd_kernel(MemBwdParams 
       const size_t row = ((size_t)b * p.T + tok) * p.H + h;
       const float kv = bf2f(p.raw_k.p[b * p.raw_k.sb + (int64_t)tok * p.raw_k.st + h * p.raw_k.sh + d]);
       const float pr = __expf(kv - sm.stat[0][d]) * sm.stat[1][d];
-      p.draw_k[row * D + d] = f2bf(pr * (dp[i] - sm.stat[2][d]));
+      const float extra = p.dk_extra ? p.dk_extra[row * D + d] : 0.0f;
+      p.draw_k[row * D + d] = f2bf(pr * (dp[i] - sm.stat[2][d]) + extra);
     }
   }
   // ---- dv[t][e] += sum_d P[t][d] dC[d][e] (accumulator: lane = e column)
@@ -1489,7 +1493,7 @@ __global__ __launch_bounds__(kThreads) void finish_bwd_kernel(MemBwdParams p) {
 }
 
 // The same with eight channels per lane (D / 8 lanes per row, 16-byte loads
-// and stores); launch_mem_bwd picks it when every row pointer is 16-byte
+// and stores); launch_mem_bwd_writer picks it when every row pointer is 16-byte
 // aligned.
 template <int D>
 __global__ __launch_bounds__(kThreads) void finish_bwd_vec_kernel(MemBwdParams p) {
@@ -1586,42 +1590,57 @@ hipError_t launch_attn_bwd(const AttnBwdParams& p, int head_dim, hipStream_t s) 
   return hipGetLastError();
 }
 
-hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s) {
+hipError_t launch_mem_bwd_read(const MemBwdParams& p, int head_dim, hipStream_t s) {
   const int BH = p.B * p.H;
   const int n_tiles = (p.T + p.ft - 1) / p.ft;
   // read_bwd keeps the tile's page adjoints in LDS: at most 64 pages.
   if (p.group != 8 || p.ft != 256 || p.v_max / p.group + 1 > 64) return hipErrorInvalidValue;
+  if (p.v_max <= 0) return hipSuccess;
   const int lag = p.keep / p.ft;
   const int dc_groups = (std::max(n_tiles - lag - 1, 1) + kObTiles - 1) / kObTiles;
   const int dg_groups = (p.group + kObTilesG - 1) / kObTilesG;
+#define TAO_MEM_BWD_READ(D_)                                                                 \
+  do {                                                                                       \
+    const int blocks = (p.T + kRbQ - 1) / kRbQ;                                              \
+    hipLaunchKernelGGL(read_bwd_kernel<D_>, dim3((unsigned)(blocks * BH)),                   \
+                       dim3(kRbWaves * 64), 0, s, p);                                        \
+    if (p.coarse_values && p.coarse_count > 0) {                                             \
+      hipLaunchKernelGGL((outer_bwd_kernel<D_, 1>),                                          \
+                         dim3((unsigned)(p.coarse_count * dg_groups * BH)), dim3(kThreads),  \
+                         0, s, p, 1);                                                        \
+      hipLaunchKernelGGL(coarse_page_bwd_kernel<D_>, dim3((unsigned)(p.coarse_count * BH)),  \
+                         dim3(kThreads), 0, s, p);                                           \
+    }                                                                                        \
+    hipLaunchKernelGGL((outer_bwd_kernel<D_, kObFines<D_>>),                                 \
+                       dim3((unsigned)(((p.v_max + kObFines<D_> - 1) / kObFines<D_>) *       \
+                                       dc_groups * BH)),                                     \
+                       dim3(kThreads), 0, s, p, 0);                                          \
+    hipLaunchKernelGGL(page_bwd_kernel<D_>, dim3((unsigned)(n_tiles * BH)), dim3(D_), 0, s,  \
+                       p);                                                                   \
+    if (p.v_max / p.group > 0)                                                               \
+      hipLaunchKernelGGL(zpage_bwd_kernel<D_>, dim3((unsigned)((p.v_max / p.group) * BH)),   \
+                         dim3(D_), 0, s, p);                                                 \
+  } while (0)
+  if (head_dim == 128)
+    TAO_MEM_BWD_READ(128);
+  else if (head_dim == 64)
+    TAO_MEM_BWD_READ(64);
+  else
+    return hipErrorInvalidValue;
+#undef TAO_MEM_BWD_READ
+  return hipGetLastError();
+}
+
+hipError_t launch_mem_bwd_writer(const MemBwdParams& p, int head_dim, hipStream_t s) {
+  const int BH = p.B * p.H;
   auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
   const bool fin_vec = al(p.h) && al(p.dh) && al(p.drq_fuse) && al(p.dv) && al(p.draw_q) &&
                        al(p.dv_out) && al(p.draw_k);
-#define TAO_MEM_BWD(D_)                                                                      \
+#define TAO_MEM_BWD_WRITER(D_)                                                               \
   do {                                                                                       \
-    if (p.v_max > 0) {                                                                       \
-      const int blocks = (p.T + kRbQ - 1) / kRbQ;                                            \
-      hipLaunchKernelGGL(read_bwd_kernel<D_>, dim3((unsigned)(blocks * BH)),                 \
-                         dim3(kRbWaves * 64), 0, s, p);                                      \
-      if (p.coarse_values && p.coarse_count > 0) {                                           \
-        hipLaunchKernelGGL((outer_bwd_kernel<D_, 1>),                                        \
-                           dim3((unsigned)(p.coarse_count * dg_groups * BH)), dim3(kThreads),\
-                           0, s, p, 1);                                                      \
-        hipLaunchKernelGGL(coarse_page_bwd_kernel<D_>, dim3((unsigned)(p.coarse_count * BH)),\
-                           dim3(kThreads), 0, s, p);                                         \
-      }                                                                                      \
-      hipLaunchKernelGGL((outer_bwd_kernel<D_, kObFines<D_>>),                               \
-                         dim3((unsigned)(((p.v_max + kObFines<D_> - 1) / kObFines<D_>) *     \
-                                         dc_groups * BH)),                                   \
-                         dim3(kThreads), 0, s, p, 0);                                        \
-      hipLaunchKernelGGL(page_bwd_kernel<D_>, dim3((unsigned)(n_tiles * BH)), dim3(D_), 0,   \
-                         s, p);                                                              \
-      if (p.v_max / p.group > 0)                                                             \
-        hipLaunchKernelGGL(zpage_bwd_kernel<D_>, dim3((unsigned)((p.v_max / p.group) * BH)), \
-                           dim3(D_), 0, s, p);                                               \
+    if (p.v_max > 0)                                                                         \
       hipLaunchKernelGGL(writer_bwd_kernel<D_>, dim3((unsigned)(p.v_max * BH)),              \
                          dim3(kWbWaves * 64), 0, s, p);                                      \
-    }                                                                                        \
     const int rows = p.B * p.T * p.H;                                                        \
     constexpr int vrows = kThreads / (D_ / 8);                                               \
     if (fin_vec)                                                                             \
@@ -1633,12 +1652,12 @@ hipError_t launch_mem_bwd(const MemBwdParams& p, int head_dim, hipStream_t s) {
                          dim3(kThreads), 0, s, p);                                           \
   } while (0)
   if (head_dim == 128)
-    TAO_MEM_BWD(128);
+    TAO_MEM_BWD_WRITER(128);
   else if (head_dim == 64)
-    TAO_MEM_BWD(64);
+    TAO_MEM_BWD_WRITER(64);
   else
     return hipErrorInvalidValue;
-#undef TAO_MEM_BWD
+#undef TAO_MEM_BWD_WRITER
   return hipGetLastError();
 }
 

@@ -273,12 +273,19 @@ def _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, conf
     pre-fusion coarse / fine heads and denominators. Returns (out, context
     for backward)."""
     _check(q, k, v, raw_q, raw_k, config)
-    if config.fine_writer != "softmax":
+    if config.fine_writer not in _VALUE_WRITERS:
         raise NotImplementedError(
-            "gradients of the full-sequence read are implemented for the softmax writer")
+            f"gradients of the full-sequence read are implemented for the writers "
+            f"{_VALUE_WRITERS}")
+    if config.fine_writer == "regularized_association" and not config.coarse_index_only:
+        raise NotImplementedError(
+            "gradients through the regularized writer's page matrices are not built: "
+            "use coarse_index_only=True")
     b, tokens, heads, d = q.shape
     ws = _Workspace(config, b, tokens, heads, d, q.device)
     q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
+    if config.fine_writer == "regularized_association":
+        _association_values(ws, raw_k, v, config)
     saves = dict(
         lse=torch.empty((b, tokens, heads), dtype=torch.float32, device=q.device),
         coarse=torch.zeros(q.shape, dtype=torch.bfloat16, device=q.device),

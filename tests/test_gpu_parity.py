@@ -617,7 +617,7 @@ def _reference_gradients(xs, fa, fb, grad, cfg, routes):
     leaves = [x.double().requires_grad_(True) for x in xs]
     fa64, fb64 = fa.double().requires_grad_(True), fb.double().requires_grad_(True)
     out = O.training_forward_smooth(*leaves, fa64, fb64, 0.5, routes,
-                                    O.Geometry.from_config(cfg))
+                                    O.Geometry.from_config(cfg), writer=cfg.fine_writer)
     every = leaves + [fa64, fb64]
     grads = torch.autograd.grad((out * grad.double()).sum(), every, allow_unused=True)
     return [torch.zeros_like(x) if g is None else g for g, x in zip(grads, every)]
@@ -660,6 +660,41 @@ def test_full_sequence_backward_matches_oracle(tokens, heads, width, index_only,
     for g in got:
         assert torch.isfinite(g.float()).all()
     _compare_gradients(got, want, 5e-2)
+
+
+@pytest.mark.parametrize("tokens,heads,width,seed", [(1300, 2, 64, 61), (2900, 2, 128, 62)])
+def test_full_sequence_backward_regularized_writer(tokens, heads, width, seed):
+    """tao_attention backward with fine_writer="regularized_association"
+    (index-only): the writer's share differentiates the association solve
+    (dC -> W = A^{-1} dC, dG from W and the fp32 C, then U, V and the
+    feature softmax), the z path stays the softmax writer's; all gradients
+    against fp64 autograd of the oracle's smooth forward through
+    torch.linalg.solve, at the bf16 forward's selections; the raw_k and v
+    gradients differ from the softmax writer's."""
+    from tao_attention import TaoConfig, tao_attention
+    xs, fa, fb = inputs(tokens, heads, width, seed)
+    cfg = TaoConfig(coarse_index_only=True, fine_writer="regularized_association")
+    grad = torch.randn(xs[0].shape, generator=torch.Generator().manual_seed(seed + 100)).to(BF16)
+    dev = [x.cuda().requires_grad_(True) for x in xs]
+    fa_d = fa.cuda().requires_grad_(True)
+    fb_d = fb.cuda().requires_grad_(True)
+    print(f"regularized-writer backward T{tokens} H{heads} D{width}", flush=True)
+    out = tao_attention(*dev[:3], raw_q=dev[3], raw_k=dev[4], fusion_a=fa_d, fusion_b=fb_d,
+                        alpha=0.5, config=cfg)
+    got = torch.autograd.grad(out, dev + [fa_d, fb_d], grad.cuda())
+    _, routes = O.training_forward(*xs, fa, fb, 0.5, O.Geometry.from_config(cfg),
+                                   return_routes=True, writer=cfg.fine_writer)
+    want = _reference_gradients(xs, fa, fb, grad, cfg, routes)
+    for g in got:
+        assert torch.isfinite(g.float()).all()
+    _compare_gradients(got, want, 5e-2)
+    soft = _reference_gradients(xs, fa, fb, grad, TaoConfig(coarse_index_only=True), routes)
+    for i in (2, 4):                                    # v, raw_k
+        assert (soft[i] - want[i]).norm() > 0.1 * want[i].norm()
+    cfg_pages = TaoConfig(coarse_index_only=False, fine_writer="regularized_association")
+    with pytest.raises(NotImplementedError):
+        tao_attention(*dev[:3], raw_q=dev[3], raw_k=dev[4], fusion_a=fa_d, fusion_b=fb_d,
+                      alpha=0.5, config=cfg_pages)
 
 
 @pytest.mark.parametrize("tokens,heads,width,index_only,seed", [

@@ -11,8 +11,9 @@
 // per fine against 32 pairs at a time, then sums the pairs of a query. Here a
 // workgroup owns a tile of queries of one (b, h) instead: the union of the
 // tile's selected ids (an LDS bitmask, ascending) is walked once, each fine's
-// C is staged in LDS once and every wave builds its MFMA A operand from the
-// channel rows of the queries that selected that fine (zero rows elsewhere),
+// C is staged in LDS once (the next fine's C and channel rows are loaded
+// while the current one runs) and every wave builds its MFMA A operand from
+// the channel rows of the queries that selected that fine (zero rows elsewhere),
 // so the numerator accumulates in one v_mfma_f32_32x32x16_bf16 accumulator
 // per (32 queries, 32 columns) and no pair buffer or sort is needed. A query
 // that lists one fine twice is handled exactly by one pass per occurrence.
@@ -49,6 +50,7 @@ struct SelSmem {
   uint32_t bits[kSelWords];
   int pre[kSelWords];
   int uni[kSelTileQ<D> * kSelMaxM];
+  int8_t ord[kSelTileQ<D>][kSelMaxM];     // forward: a row's slots by (id, slot) ascending
   int n_union, passes;
   bf16_t stage[4][32][40];                // grad-of-channel rows per wave (32 q x 32 d)
 };
@@ -117,7 +119,9 @@ TAO_DEV int find_slot(const SelSmem<D>& sm, int q, int M, int f, int r) {
 template <int D>
 __global__ __launch_bounds__(kSelThreads) void selected_fwd_kernel(SelectedParams p) {
   constexpr int KK = D / 16, ET = D / 32, TQ = kSelTileQ<D>;
-  constexpr int CJ = D * D / 8 / kSelThreads;            // uint4 of C per thread
+  constexpr int CPR = D / 8;                             // uint4 per row of C
+  constexpr int PJ = (D / 2) * CPR / kSelThreads;        // row-pair jobs per thread
+  static_assert(PJ * kSelThreads == (D / 2) * CPR, "whole row-pair jobs");
   __shared__ SelSmem<D> sm;
   const int n_tiles = (p.Q + TQ - 1) / TQ;
   const int tile = blockIdx.x % n_tiles, bh = blockIdx.x / n_tiles;
@@ -127,45 +131,99 @@ __global__ __launch_bounds__(kSelThreads) void selected_fwd_kernel(SelectedParam
   const int li = lane & 31, hl = lane >> 5;
   const int qg = w / ET, et = w % ET;
   tile_union<D>(sm, p, b, h, q0, nq, tid);
-  const int U = sm.n_union, R = sm.passes + 1;
+  // Each row's slots in ascending (id, slot) order: the union is walked in
+  // ascending id, so a lane finds its query's slots of fine f at a pointer
+  // (invalid ids sort first and are skipped).
+  for (int q = tid; q < nq; q += kSelThreads) {
+    for (int i = 0; i < p.M; ++i) sm.ord[q][i] = (int8_t)i;
+    for (int i = 1; i < p.M; ++i) {
+      const int8_t m = sm.ord[q][i];
+      const int key = sm.sid[q][m];
+      int j = i - 1;
+      while (j >= 0 && sm.sid[q][sm.ord[q][j]] > key) { sm.ord[q][j + 1] = sm.ord[q][j]; --j; }
+      sm.ord[q][j + 1] = m;
+    }
+  }
+  __syncthreads();
+  const int U = sm.n_union;
   const int ql = 32 * qg + li;                            // the lane's query row in the tile
   const bool qok = ql < nq;
+  int ptr = 0;
+  if (qok)
+    while (ptr < p.M && sm.sid[ql][sm.ord[ql][ptr]] < 0) ++ptr;
+  // Next slot of fine f in this lane's row, or -1.
+  auto next_slot = [&](int f) __attribute__((always_inline)) {
+    if (!qok || ptr >= p.M) return -1;
+    const int m = sm.ord[ql][ptr];
+    if (sm.sid[ql][m] != f) return -1;
+    ++ptr;
+    return m;
+  };
+  const bf16_t* chan = p.channel + (((size_t)b * p.Q + q0 + (qok ? ql : 0)) * p.H + h) * p.M * D;
+  auto load_row = [&](int m, uint4 (&r)[KK]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      r[kk] = m >= 0 ? *(const uint4*)(chan + (size_t)m * D + 16 * kk + 8 * hl)
+                     : make_uint4(0u, 0u, 0u, 0u);
+  };
   const bf16_t* bank = p.bank + ((size_t)(b % p.BB) * p.H + h) * p.S * D * D;
+  // C of a fine into registers: job j = row pair d = 2 (j % (D / 2)), chunk
+  // j / (D / 2), so consecutive threads write consecutive words of a C^T row.
+  uint4 c0[PJ], c1[PJ];
+  auto load_c = [&](int f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+      const int job = tid + j * kSelThreads;
+      const int d = 2 * (job % (D / 2)), e0 = 8 * (job / (D / 2));
+      const bf16_t* src = bank + (size_t)f * D * D + (size_t)d * D + e0;
+      c0[j] = *(const uint4*)src;
+      c1[j] = *(const uint4*)(src + D);
+    }
+  };
   floatx16 acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+  int m_next = -1;
+  uint4 row_next[KK];
+  if (U > 0) {
+    load_c(sm.uni[0]);
+    m_next = next_slot(sm.uni[0]);
+    load_row(m_next, row_next);
+  }
   for (int u = 0; u < U; ++u) {
     const int f = sm.uni[u];
-    // stage C^T[e][d] of fine f: thread moves 8 consecutive e of one row d
-    uint4 cv[CJ];
-#pragma unroll
-    for (int j = 0; j < CJ; ++j)
-      cv[j] = *(const uint4*)(bank + (size_t)f * D * D + (size_t)(tid + j * kSelThreads) * 8);
     __syncthreads();                                     // previous fine consumed
 #pragma unroll
-    for (int j = 0; j < CJ; ++j) {
-      const int idx = (tid + j * kSelThreads) * 8;
-      const int d = idx / D, e0 = idx % D;
-      const uint32_t wv[4] = {cv[j].x, cv[j].y, cv[j].z, cv[j].w};
+    for (int j = 0; j < PJ; ++j) {
+      const int job = tid + j * kSelThreads;
+      const int d = 2 * (job % (D / 2)), e0 = 8 * (job / (D / 2));
+      const uint32_t a[4] = {c0[j].x, c0[j].y, c0[j].z, c0[j].w};
+      const uint32_t bq[4] = {c1[j].x, c1[j].y, c1[j].z, c1[j].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sm.c[e0 + 2 * i][d] = (bf16_t)(wv[i] & 0xFFFFu);
-        sm.c[e0 + 2 * i + 1][d] = (bf16_t)(wv[i] >> 16);
+        *(uint32_t*)&sm.c[e0 + 2 * i][d] = (a[i] & 0xFFFFu) | (bq[i] << 16);
+        *(uint32_t*)&sm.c[e0 + 2 * i + 1][d] = (a[i] >> 16) | (bq[i] & 0xFFFF0000u);
       }
     }
     __syncthreads();
-    for (int r = 0; r < R; ++r) {
-      const int m = qok ? find_slot<D>(sm, ql, p.M, f, r) : -1;
-      const bf16_t* crow = p.channel +
-          ((((size_t)b * p.Q + q0 + ql) * p.H + h) * p.M + (m < 0 ? 0 : m)) * D;
-      if (!__any(m >= 0)) continue;                      // wave-uniform
+    if (u + 1 < U) load_c(sm.uni[u + 1]);                // in flight during this fine's MFMAs
+    int m = m_next;
+    uint4 row[KK];
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        const uint4 a = m >= 0 ? *(const uint4*)(crow + 16 * kk + 8 * hl) : make_uint4(0, 0, 0, 0);
+    for (int kk = 0; kk < KK; ++kk) row[kk] = row_next[kk];
+    // Every slot of f in the lane's row (a fine listed twice adds twice).
+    while (__any(m >= 0)) {
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            as_bf16x8(a), as_bf16x8(*(const uint4*)&sm.c[32 * et + li][16 * kk + 8 * hl]), acc,
-            0, 0, 0);
-      }
+            as_bf16x8(row[kk]), as_bf16x8(*(const uint4*)&sm.c[32 * et + li][16 * kk + 8 * hl]),
+            acc, 0, 0, 0);
+      m = m >= 0 ? next_slot(f) : -1;
+      load_row(m, row);
+    }
+    if (u + 1 < U) {
+      m_next = next_slot(sm.uni[u + 1]);
+      load_row(m_next, row_next);
     }
   }
   // rows q = 32 qg + 8 (i / 4) + 4 hl + i % 4, column e = 32 et + li

@@ -86,7 +86,11 @@ typedef struct tao_state_dev {
    * them, fine_mass holds each sealed fine's fp32 feature mass (its z is
    * r(log mass); page descriptors are r(log) of summed masses) and the read
    * is the numerator-only mixture. They need stats (and stats_cap), plus
-   * [stats_cap * B][H][D] floats of mass scratch after its two halves.
+   * [stats_cap * B][H][D] floats of mass scratch after its two halves. With
+   * page_c they also need pending_gram and pending_cross: the pending page's
+   * gram [B, H, D, D] (feature mass) or square mass and mass [2, B, H, D]
+   * (structured), and its cross sum [B, H, D, D]; the coarse read is then
+   * the mixture over pages (tao_stream.py:301-305).
    * TAO_WRITER_VALUE (0): softmax descriptors (softmax and regularized). */
   int32_t fine_writer;   /* enum tao_fine_writer */
   float* fine_mass;      /* fp32 [B, H, fine_cap, D]; feature writers only */

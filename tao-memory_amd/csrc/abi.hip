@@ -25,13 +25,16 @@ int check_hip(hipError_t e, const char* where) {
 }
 
 // Regularized association writer (state buffers set, tao_memory.h).
-bool assoc_writer(const tao_state_dev* st) { return st->pending_gram != nullptr; }
-
 // Feature writers (fine_writer TAO_WRITER_FEATURE_MASS / _STRUCTURED).
 bool feature_writer(const tao_state_dev* st) { return st->fine_writer != TAO_WRITER_VALUE; }
 
+bool assoc_writer(const tao_state_dev* st) {
+  return st->pending_gram != nullptr && !feature_writer(st);
+}
+
 int check_assoc(const tao_state_dev* st) {
-  const bool any = st->pending_gram || st->pending_cross || (st->stats && !feature_writer(st));
+  if (feature_writer(st)) return TAO_OK;   // check_feature covers its buffers
+  const bool any = st->pending_gram || st->pending_cross || st->stats;
   if (any && (!st->pending_gram || !st->pending_cross || !st->stats || st->stats_cap < 1))
     return fail(TAO_E_ARGUMENT,
                 "the regularized writer needs pending_gram, pending_cross and stats (stats_cap >= 1)");
@@ -48,11 +51,11 @@ int check_feature(const tao_state_dev* st) {
   }
   if (!st->fine_mass || !st->stats || st->stats_cap < 1)
     return fail(TAO_E_ARGUMENT, "a feature writer needs fine_mass and stats (stats_cap >= 1)");
-  if (st->pending_gram || st->pending_cross)
-    return fail(TAO_E_ARGUMENT, "a feature writer keeps no pending gram / cross sums");
-  if (st->page_c)
+  if ((st->page_c != nullptr) != (st->pending_gram != nullptr && st->pending_cross != nullptr))
     return fail(TAO_E_ARGUMENT,
-                "the coarse value branch with a feature writer is not built (index-only only)");
+                "a feature writer keeps pending sums exactly when it has page values: "
+                "pending_gram ([B, H, D, D], or [2, B, H, D] square mass and mass for the "
+                "structured writer) and pending_cross");
   return TAO_OK;
 }
 
@@ -316,6 +319,70 @@ hipError_t feature_seal(const tao_state_dev* st, const tao::TokView& rk, const t
     dp.first_slot = first_slot + done;
     e = tao::launch_feature_descriptors(dp, D, s);
     if (e != hipSuccess) return e;
+    // (After the descriptors, which read each block's own mass.) With page values: the statistics' sums in seal order (restarting at
+    // each page); a block that completes a page then holds its page's sums,
+    // and the page matrix is the writer's matrix of them (tao_stream.py:
+    // 463-499; structured: over fine_tokens * group tokens).
+    if (st->page_c) {
+      tao::AssocPendingParams pp{};
+      pp.B = B;
+      pp.H = H;
+      pp.count = n;
+      pp.first_slot = first_slot + done;
+      pp.group = st->coarse_group;
+      pp.reset_pages = 1;
+      if (structured) {
+        pp.gram = first;                       // square mass [.., D]
+        pp.cross = mass;                       // mass [.., D]
+        pp.pending_gram = st->pending_gram;
+        pp.pending_cross = st->pending_gram + (size_t)B * H * D;
+        e = tao::launch_pending_sums(pp, D, s);
+        if (e == hipSuccess) {
+          pp.gram = cross;
+          pp.cross = nullptr;
+          pp.pending_gram = st->pending_cross;
+          pp.pending_cross = nullptr;
+          e = tao::launch_pending_sums(pp, D * D, s);
+        }
+        if (e == hipSuccess) {
+          tao::StructuredParams tp{};
+          tp.square = first;
+          tp.cross = cross;
+          tp.mass = mass;
+          tp.count_mats = n * B * H;
+          tp.count = (float)(st->fine_tokens * st->coarse_group);
+          tp.out = (bf16_t*)st->page_c;
+          tp.to_slots = 2;
+          tp.B = B;
+          tp.H = H;
+          tp.cap = st->page_cap;
+          tp.first_slot = first_slot + done;
+          tp.group = st->coarse_group;
+          e = tao::launch_structured_matrix(tp, D, s);
+        }
+      } else {
+        pp.gram = first;
+        pp.cross = cross;
+        pp.pending_gram = st->pending_gram;
+        pp.pending_cross = st->pending_cross;
+        e = tao::launch_assoc_pending(pp, D, s);
+        if (e == hipSuccess) {
+          tao::AssocSolveParams pg{};
+          pg.gram = first;
+          pg.cross = cross;
+          pg.count = n * B * H;
+          pg.out = (bf16_t*)st->page_c;
+          pg.to_slots = 2;
+          pg.B = B;
+          pg.H = H;
+          pg.cap = st->page_cap;
+          pg.fine_first = first_slot + done;
+          pg.group = st->coarse_group;
+          e = tao::launch_association_solve(pg, D, s);
+        }
+      }
+      if (e != hipSuccess) return e;
+    }
   }
   return hipSuccess;
 }
@@ -886,7 +953,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   pp.count = (int)n_pages;
   e = tao::launch_pages(pp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill pages");
-  if (coarse_values && !external_values && !assoc_writer(st)) {
+  if (coarse_values && !external_values && !assoc_writer(st) && !feature_writer(st)) {
     tao::PageCoarseParams cp{};
     cp.bank = (const bf16_t*)st->bank_c;
     cp.sw = (const bf16_t*)st->fine_sw;
@@ -901,7 +968,7 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
     e = tao::launch_page_coarse(cp, D, s);
     if (e != hipSuccess) return check_hip(e, "tao_prefill page values");
   }
-  if (coarse_reads) {
+  if (coarse_reads && !feature_writer(st)) {   // feature writers mix pages per query
     tao::CoarseFoldParams cf{};
     cf.page_z = (const bf16_t*)st->page_z;
     cf.page_c = (const bf16_t*)st->page_c;
@@ -1022,6 +1089,12 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   rt.save_fine = pools ? (bf16_t*)pools->fine_out : nullptr;
   rt.save_den = pools ? pools->den_out : nullptr;
   rt.fine_z = feature_writer(st) ? (const bf16_t*)st->fine_z : nullptr;
+  if (feature_writer(st) && coarse_reads) {
+    rt.coarse_pool = nullptr;
+    rt.page_z = (const bf16_t*)st->page_z;
+    rt.page_c = (const bf16_t*)st->page_c;
+    rt.page_cap = st->page_cap;
+  }
   if (feature_writer(st) && rt.save_fine)
     return fail(TAO_E_ARGUMENT, "a feature writer's read keeps no saves (forward only)");
   e = tao::launch_read_tiles(rt, D, s);
@@ -1218,7 +1291,7 @@ TrainBwdLayout train_bwd_layout(const tao_state_dev* st, int64_t tokens, int fin
   l.dalpha = take(4);
   l.zero_end = off;
   l.dalpha_parts = take((size_t)tao::fuse_bwd_workgroups((int)T, (int)B, (int)H) * 4);
-  if (st->pending_gram && fines > 0) {
+  if (assoc_writer(st) && fines > 0) {
     const size_t mats = (size_t)fines * BH, mat = D * D * 4;
     l.stats = take(2 * mats * mat);
     l.sol_y = take(mats * mat);

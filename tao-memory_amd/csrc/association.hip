@@ -337,6 +337,8 @@ template <int D>
 __global__ __launch_bounds__(D) void structured_matrix_kernel(StructuredParams p) {
   __shared__ float diag[D], tv[D], mv[D], hmv[D], red[4][D / 64 > 0 ? D / 64 : 1];
   const int mat = blockIdx.x, d = threadIdx.x;
+  if (p.to_slots == 2 && (p.first_slot + mat / (p.B * p.H)) % p.group != p.group - 1)
+    return;   // uniform: only blocks that complete a page
   const float count = p.count;
   const float sq = p.square[(size_t)mat * D + d];
   const float ms = p.mass[(size_t)mat * D + d];
@@ -377,9 +379,11 @@ __global__ __launch_bounds__(D) void structured_matrix_kernel(StructuredParams p
     mass_hb = fmaf(mv[i], hb, mass_hb);
   }
   if (p.to_slots) {
-    // C^T into the fine bank: row e of slot first_slot + blk.
+    // C^T into the fine bank: row e of slot first_slot + blk (1), or of the
+    // page that fine slot completes (2).
     const int blk = mat / (p.B * p.H), b = mat / p.H % p.B, h = mat % p.H;
-    bf16_t* out = p.out + ((((size_t)b * p.H + h) * p.cap + p.first_slot + blk) * D + e) * D;
+    const int slot = p.to_slots == 1 ? p.first_slot + blk : (p.first_slot + blk) / p.group;
+    bf16_t* out = p.out + ((((size_t)b * p.H + h) * p.cap + slot) * D + e) * D;
     for (int i = 0; i < D; ++i) {
       const float hb = cr[(size_t)i * D + e] / diag[i] + tv[i] * t_cross / safe_sum;
       out[i] = f2bf(hb - hmv[i] * mass_hb / denominator);
@@ -452,29 +456,34 @@ __global__ __launch_bounds__(256) void assoc_pending_kernel(AssocPendingParams p
   const int64_t per = (int64_t)p.B * p.H * dd;
   if (i >= per) return;
   const int64_t bh = i / dd, e = i % dd;                // bh = b * H + h
-  float pg = p.pending_gram[i], pc = p.pending_cross[i];
+  const bool two = p.cross != nullptr;                  // a second statistic summed alike
+  float pg = p.pending_gram[i], pc = two ? p.pending_cross[i] : 0.0f;
   for (int blk = 0; blk < p.count; ++blk) {
     const int slot = p.first_slot + blk;
     const int64_t at = ((int64_t)blk * p.B * p.H + bh) * dd + e;   // (blk, b, h) = blk * B * H + bh
     const bool fresh = p.reset_pages ? slot % p.group == 0 : slot == 0;
     pg = fresh ? p.gram[at] : pg + p.gram[at];
-    pc = fresh ? p.cross[at] : pc + p.cross[at];
+    if (two) pc = fresh ? p.cross[at] : pc + p.cross[at];
     if (p.reset_pages && slot % p.group == p.group - 1) {
       p.gram[at] = pg;
-      p.cross[at] = pc;
+      if (two) p.cross[at] = pc;
     }
   }
   p.pending_gram[i] = pg;
-  p.pending_cross[i] = pc;
+  if (two) p.pending_cross[i] = pc;
 }
 
 }  // namespace
 
 hipError_t launch_assoc_pending(const AssocPendingParams& p, int head_dim, hipStream_t s) {
-  const int64_t n = (int64_t)p.B * p.H * head_dim * head_dim;
+  return launch_pending_sums(p, head_dim * head_dim, s);
+}
+
+hipError_t launch_pending_sums(const AssocPendingParams& p, int dd, hipStream_t s) {
+  const int64_t n = (int64_t)p.B * p.H * dd;
   if (n <= 0 || p.count <= 0) return hipSuccess;
   hipLaunchKernelGGL(assoc_pending_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p,
-                     head_dim * head_dim);
+                     dd);
   return hipGetLastError();
 }
 

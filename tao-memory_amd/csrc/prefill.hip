@@ -715,7 +715,7 @@ TAO_DEV uint32_t lds_addr(const void* p) {
 
 template <int D, bool COARSE, bool FEAT>
 __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesParams p) {
-  static_assert(!(COARSE && FEAT), "feature writers read index-only states");
+
   constexpr int KK = D / 16, ET = D / 32, CPR = D / 8;   // k-steps, e-tiles, chunks per row
   constexpr int CPT = D * CPR / (64 * kGroupWaves);      // 1 KB wave loads per fine and wave
   static_assert(CPT * 64 * kGroupWaves == D * CPR, "whole wave loads per fine");
@@ -1069,8 +1069,9 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
   // 8-channel units and loads and stores 16 bytes per lane.
   if (!reads) return;
   const bool coarse_on = COARSE && cpages >= 1;
-  const bf16_t* gc =
-      coarse_on ? p.coarse_pool + ((size_t)(cpages - p.coarse_first) * BH + bh) * D * D : nullptr;
+  const bf16_t* gc = coarse_on && !FEAT
+                         ? p.coarse_pool + ((size_t)(cpages - p.coarse_first) * BH + bh) * D * D
+                         : nullptr;
   bf16_t* tile_f = ring_mem + (size_t)w * 2 * 32 * D;
   bf16_t* tile_c = tile_f + 32 * D;
   const float den = acc_den[0];
@@ -1090,7 +1091,7 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
         f[k] = FEAT ? rbf(acc[t][4 * g + k]) : rbf(rbf(acc[t][4 * g + k]) * rden);
       *(uint2*)&tile_f[at] = make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]));
     }
-    if constexpr (COARSE) {
+    if constexpr (COARSE && !FEAT) {
       if (coarse_on) {
         floatx16 cacc;
 #pragma unroll
@@ -1112,6 +1113,55 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
               make_uint2(pack_bf16x2(cacc[4 * g], cacc[4 * g + 1]),
                          pack_bf16x2(cacc[4 * g + 2], cacc[4 * g + 3]));
       }
+    }
+  }
+  if constexpr (COARSE && FEAT) {
+    // Feature writers' coarse read (tao_stream.py:301-305): the mixture of
+    // the chunk's completed pages, coef = r(mass_p / sum_p mass_p * h) with
+    // mass_p = sum_d h[d] exp(page_z[p][d]) in fp32, against each page's C^T.
+    if (coarse_on) {
+      const bf16_t* pzb = p.page_z + (size_t)bh * p.page_cap * D;
+      const bf16_t* pcb = p.page_c + (size_t)bh * p.page_cap * D * D;
+      auto page_mass = [&](int pg) __attribute__((always_inline)) {
+        float part = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          float zf[8];
+          unpack8f(*(const uint4*)(pzb + (size_t)pg * D + 16 * kk + 8 * hl), zf);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) part += hf[kk][j] * expf(zf[j]);
+        }
+        return part + __shfl_xor(part, 32, 64);
+      };
+      float totc = 0.0f;
+      for (int pg = 0; pg < cpages; ++pg) totc += page_mass(pg);
+      floatx16 cacc[ET];
+#pragma unroll
+      for (int t = 0; t < ET; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) cacc[t][i] = 0.0f;
+      for (int pg = 0; pg < cpages; ++pg) {
+        const float mix = page_mass(pg) / totc;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          const bf16x8 a = as_bf16x8(make_uint4(
+              pack_bf16x2(mix * hf[kk][0], mix * hf[kk][1]), pack_bf16x2(mix * hf[kk][2], mix * hf[kk][3]),
+              pack_bf16x2(mix * hf[kk][4], mix * hf[kk][5]), pack_bf16x2(mix * hf[kk][6], mix * hf[kk][7])));
+#pragma unroll
+          for (int t = 0; t < ET; ++t) {
+            const uint4 gb =
+                *(const uint4*)(pcb + ((size_t)pg * D + 32 * t + li) * D + 16 * kk + 8 * hl);
+            cacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(gb), a, cacc[t], 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < ET; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *(uint2*)&tile_c[unit_at(li, 4 * t + g) + 4 * hl] =
+              make_uint2(pack_bf16x2(cacc[t][4 * g], cacc[t][4 * g + 1]),
+                         pack_bf16x2(cacc[t][4 * g + 2], cacc[t][4 * g + 3]));
     }
   }
   // Row phase: lane (row r, unit c) fuses channels 8 c .. 8 c + 7 of query r.
@@ -1206,16 +1256,23 @@ hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t
                      s, p)
 #define TAO_STREAM_LAUNCH(D_, C_)                                                             \
   hipLaunchKernelGGL((read_stream_kernel<D_, C_, false>), grid, dim3(kGroupThreads), 0, s, p)
-#define TAO_FEATURE_LAUNCH(D_)                                                                \
-  hipLaunchKernelGGL((read_stream_kernel<D_, false, true>), grid, dim3(kGroupThreads), 0, s, p)
+#define TAO_FEATURE_LAUNCH(D_, C_)                                                            \
+  hipLaunchKernelGGL((read_stream_kernel<D_, C_, true>), grid, dim3(kGroupThreads), 0, s, p)
   if (head_dim != 128 && head_dim != 64) return hipErrorInvalidValue;
   if (p.fine_z) {
-    // Feature writers: index-only, no saves; per-query or turn routes.
-    if (coarse || p.save_fine) return hipErrorInvalidValue;
+    // Feature writers, no saves: per-query routes index-only; turn routes
+    // with or without the page mixture (page_c).
+    if (p.save_fine) return hipErrorInvalidValue;
+    const bool pages = p.page_c != nullptr;
     if (perq) {
+      if (coarse || pages) return hipErrorInvalidValue;
       if (head_dim == 128) TAO_MIXTURE_LAUNCH(128); else TAO_MIXTURE_LAUNCH(64);
+    } else if (pages) {
+      if (!p.page_z) return hipErrorInvalidValue;
+      if (head_dim == 128) TAO_FEATURE_LAUNCH(128, true); else TAO_FEATURE_LAUNCH(64, true);
     } else {
-      if (head_dim == 128) TAO_FEATURE_LAUNCH(128); else TAO_FEATURE_LAUNCH(64);
+      if (coarse) return hipErrorInvalidValue;
+      if (head_dim == 128) TAO_FEATURE_LAUNCH(128, false); else TAO_FEATURE_LAUNCH(64, false);
     }
     return hipGetLastError();
   }

@@ -320,9 +320,12 @@ struct ReadTilesParams {
   const uint32_t* qsel; int qsel_words; int first_epoch;
   // Optional saves (null = skip): pre-fusion heads [B, T, H, D], denominators [B, T, H].
   bf16_t* save_coarse; bf16_t* save_fine; float* save_den;
-  // Feature writers (turn routes, no coarse values): the state's fine
-  // descriptors [B, H, fine_cap, D]; the read is the numerator-only mixture.
+  // Feature writers: the state's fine descriptors [B, H, fine_cap, D]; the
+  // read is the numerator-only mixture. With page values (turn routes), the
+  // coarse read mixes the completed pages of a tile's chunk from the state's
+  // page descriptors and page matrices (C^T) in place of coarse_pool.
   const bf16_t* fine_z;
+  const bf16_t* page_z; const bf16_t* page_c; int page_cap;
 };
 hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t s);
 
@@ -457,9 +460,10 @@ struct StructuredParams {
   int count_mats;
   float count;            // token count behind the statistics
   bf16_t* out;
-  // to_slots: matrix (blk, b, h) goes transposed into fine slot
-  // first_slot + blk of out viewed as [B, H, cap, D, D] (as AssocSolveParams).
-  int to_slots, B, H, cap, first_slot;
+  // to_slots 1: matrix (blk, b, h) goes transposed into fine slot
+  // first_slot + blk of out viewed as [B, H, cap, D, D] (as AssocSolveParams);
+  // 2: only blocks whose slot completes a page, into page slot / group.
+  int to_slots, B, H, cap, first_slot, group;
 };
 hipError_t launch_structured_matrix(const StructuredParams& p, int head_dim, hipStream_t s);
 
@@ -486,6 +490,9 @@ struct AssocPendingParams {
   int count, B, H, first_slot, group, reset_pages;
 };
 hipError_t launch_assoc_pending(const AssocPendingParams& p, int head_dim, hipStream_t s);
+// The same in-order sums over dd elements per (b, h); cross / pending_cross
+// may be null (one statistic).
+hipError_t launch_pending_sums(const AssocPendingParams& p, int dd, hipStream_t s);
 
 // h [B, T, H, D] (strides h_s), read_z element strides z_s (b, t, h, page),
 // zero for broadcast axes; out bf16 [B, T, H, P, D] contiguous.

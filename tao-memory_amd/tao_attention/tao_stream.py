@@ -94,6 +94,14 @@ class _DeviceState:
             words = _STATS_CAP * batch * heads * head_dim
             self.stats = torch.empty(words * (2 * head_dim + 1), dtype=torch.float32,
                                      device=device)
+            if self.coarse_values:
+                # The pending page's statistic sums (the reference's pending
+                # gram / square mass, mass and cross), for its page matrix.
+                first = ((batch, heads, head_dim, head_dim) if self.feature == 1
+                         else (2, batch, heads, head_dim))
+                self.pending_gram = torch.zeros(first, dtype=torch.float32, device=device)
+                self.pending_cross = torch.zeros((batch, heads, head_dim, head_dim),
+                                                 dtype=torch.float32, device=device)
         self.generation = next(_SERIAL)   # renewed whenever the buffers move
         self.fine_cap = 0
         self._allocate(fine_cap, copy_fines=0)
@@ -183,6 +191,9 @@ class _DeviceState:
         if self.feature:
             st.fine_writer, st.fine_mass = self.feature, self.fine_mass.data_ptr()
             st.stats, st.stats_cap = self.stats.data_ptr(), _STATS_CAP
+            if self.coarse_values:
+                st.pending_gram = self.pending_gram.data_ptr()
+                st.pending_cross = self.pending_cross.data_ptr()
         st.workspace = self.workspace.data_ptr()
         st.workspace_bytes = self.workspace.numel()
         return st
@@ -411,10 +422,6 @@ class StreamCache:
                 f"the HIP streaming path implements the fine writers {_STREAM_WRITERS}")
         if cfg.fine_tokens != 256 or cfg.local_keep != 512:
             raise NotImplementedError("the HIP path implements fine_tokens=256, local_keep=512")
-        if cfg.fine_writer in _FEATURE_WRITERS and not cfg.coarse_index_only:
-            raise NotImplementedError(
-                "the HIP path implements the feature writers with coarse_index_only=True "
-                "(their coarse value read is not built)")
         if q.dtype != torch.bfloat16:
             raise TypeError("the HIP path computes on bf16 operands")
         if q.shape[-1] not in (64, 128):

@@ -284,10 +284,11 @@ def test_stream_regularized_writer(device, index_only, width, batch):
     assert torch.equal(nxt[0], nxt[1])
 
 
-@pytest.mark.parametrize("writer,width", [("feature_mass_association", 64),
-                                          ("feature_mass_association", 128),
-                                          ("structured_gram_association", 128)])
-def test_stream_feature_writers(device, writer, width):
+@pytest.mark.parametrize("writer,width,index_only", [
+    ("feature_mass_association", 64, True), ("feature_mass_association", 128, True),
+    ("structured_gram_association", 128, True), ("feature_mass_association", 128, False),
+    ("structured_gram_association", 64, False)])
+def test_stream_feature_writers(device, writer, width, index_only):
     """Streaming prefill and decode with the feature writers (index-only):
     z = r(log mass), page descriptors from summed masses (the step at 2559
     seals the 8th fine and completes page 0), route ids bit-exact, the fine
@@ -296,14 +297,17 @@ def test_stream_feature_writers(device, writer, width):
     fp32, the oracle in fp64), and the exported pending mass."""
     from oracle import tao_oracle as O
     from tao_attention import TaoConfig, new_state, tao_attention_decode, tao_attention_prefill
-    heads, tokens, batch = 2, 2826, 1
+    heads, batch = 2, 1
+    tokens = 2826 if index_only else 3128
     g = torch.Generator().manual_seed(83 + width)
     xs = [torch.randn(batch, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
     fa = torch.randn(heads, width, 3, generator=g) * 0.02
     fb = torch.randn(heads, width, 3, generator=g) * 0.02
-    cfg = TaoConfig(fine_writer=writer, coarse_index_only=True)
+    cfg = TaoConfig(fine_writer=writer, coarse_index_only=index_only)
     geo = O.Geometry.from_config(cfg)
-    splits = [2540] + [1] * 30 + [250] + [1] * 5
+    # without index_only the tokens after 2816 read page 0's matrix (the
+    # mixture over completed pages)
+    splits = [2540] + [1] * 30 + [250] + [1] * 5 + ([] if index_only else [300, 1, 1])
     d = [x.to(device) for x in xs]
     state = new_state(0, cfg)
     ora = O.OracleStream(0, geo, writer=writer)
@@ -321,8 +325,11 @@ def test_stream_feature_writers(device, writer, width):
     torch.testing.assert_close(torch.cat(outs, 1).float(), torch.cat(refs, 1).float(),
                                atol=2e-2, rtol=2e-2)
     snap = state.export()
-    assert len(snap["pending_z"]) == 1 and len(snap["pages"]) == 1
+    assert len(snap["pending_z"]) == (1 if index_only else 2) and len(snap["pages"]) == 1
     assert torch.equal(snap["route_ids"][1].cpu(), ora.route_ids[1])
+    if not index_only:
+        pc = snap["pages"][0][1]
+        torch.testing.assert_close(pc.cpu().float(), ora.page_c[0].float(), atol=2e-2, rtol=2e-2)
     packed = snap["packed_fine_c"].cpu().float()
     want = torch.stack(ora.fine_c, 2).float()
     torch.testing.assert_close(packed, want, atol=2e-2, rtol=2e-2)

@@ -784,9 +784,11 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
             if writer == "structured_gram_association":
                 square, cross, mass = W.structured_statistics(kb, vb)
                 c = W.structured_matrix(square, cross, mass, ft)[1].to(kb.dtype)
+                stats.append((square, cross))
             else:
                 gram, cross, mass = W.association_statistics(kb, vb, with_mass=True)
                 c = W.association_matrix(gram, cross)[1].to(kb.dtype)
+                stats.append((gram, cross))
             z = mass_descriptor(mass)
             masses.append(mass)
         else:
@@ -813,7 +815,18 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
         page_z_full = [page_summary(fine_z[:, :, p * group:(p + 1) * group])
                        for p in range(full_pages)]
     page_c_full = []
-    if not g.coarse_index_only and writer == "regularized_association":
+    if not g.coarse_index_only and feature:
+        from . import writers as W
+        for p in range(full_pages):
+            first = sum(stats[p * group + i][0] for i in range(group))
+            cross = sum(stats[p * group + i][1] for i in range(group))
+            if writer == "structured_gram_association":
+                pc = W.structured_matrix(first, cross, mass_sum(p * group, (p + 1) * group),
+                                         ft * group)[1]
+            else:
+                pc = W.association_matrix(first, cross)[1]
+            page_c_full.append(pc.to(raw_k.dtype))
+    elif not g.coarse_index_only and writer == "regularized_association":
         from . import writers as W
         for p in range(full_pages):
             gram = sum(stats[p * group + i][0] for i in range(group))
@@ -864,7 +877,10 @@ def training_forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
             fine[:, i:i + 1] = part
         coarse_on = start >= first_coarse and not g.coarse_index_only
         fine_on = start >= g.serve_limit                 # first_fine
-        if coarse_on:
+        if coarse_on and feature:
+            coarse = feature_read(h, page_z[:, :, :completed],
+                                  torch.stack(page_c_full[:completed], 2))
+        elif coarse_on:
             coarse = coarse_read(h, page_z[:, :, :completed],
                                  torch.stack(page_c_full[:completed], 2))
         else:

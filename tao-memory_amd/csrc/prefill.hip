@@ -200,7 +200,7 @@ TAO_DEV uint4 scale_slice(const uint4& c, const uint4& wr) {
 // exactly its selected fines (selected_read.py:156-173).
 template <int D, bool COARSE, bool PERQ, bool FEAT>
 __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesParams p) {
-  static_assert(!FEAT || (PERQ && !COARSE), "the mixture read serves per-query index-only reads");
+  static_assert(!FEAT || PERQ, "the group read's mixture serves per-query reads");
   constexpr int KK = D / 16, ET = D / 32, CPR = D / 8;   // k-steps, e-tiles, uint4 per row
   constexpr int CPT = D * CPR / kGroupThreads;           // C^T uint4 per thread
   static_assert(CPT == 1 || CPT == 4, "head width 64 or 128");
@@ -564,8 +564,30 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
   // ---- epilogue: fine = r(r(num) / r(den)), the coarse read, the fusion.
   if (!reads) return;
   const bool coarse_on = COARSE && cpages >= 1;
-  const bf16_t* gc =
-      coarse_on ? p.coarse_pool + ((size_t)(cpages - p.coarse_first) * BH + bh) * D * D : nullptr;
+  const bf16_t* gc = coarse_on && !FEAT
+                         ? p.coarse_pool + ((size_t)(cpages - p.coarse_first) * BH + bh) * D * D
+                         : nullptr;
+  // Feature writers with page values: the mixture of the chunk's completed
+  // pages (tao_stream.py:301-305, 609-615), mass_p = sum_d h[d] exp(page_z[p][d]).
+  const bf16_t* pzb = FEAT && coarse_on ? p.page_z + (size_t)bh * p.page_cap * D : nullptr;
+  const bf16_t* pcb = FEAT && coarse_on ? p.page_c + (size_t)bh * p.page_cap * D * D : nullptr;
+  auto page_mass = [&](int pg) __attribute__((always_inline)) {
+    float part = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      float hv[8], zf[8];
+      h_of(kk, hv);
+      unpack8f(*(const uint4*)(pzb + (size_t)pg * D + 16 * kk + 8 * hl), zf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) part += hv[j] * expf(zf[j]);
+    }
+    return part + __shfl_xor(part, 32, 64);
+  };
+  float totc = 0.0f;
+  if constexpr (FEAT && COARSE) {
+    if (coarse_on)
+      for (int pg = 0; pg < cpages; ++pg) totc += page_mass(pg);
+  }
   // One e-tile of the accumulator (called with constant t, so acc stays in
   // registers).
   auto emit = [&](const floatx16& av, int t) __attribute__((always_inline)) {
@@ -581,7 +603,23 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
     floatx16 cacc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) cacc[i] = 0.0f;
-    if constexpr (COARSE) {
+    if constexpr (COARSE && FEAT) {
+      if (coarse_on) {
+        for (int pg = 0; pg < cpages; ++pg) {
+          const float mix = page_mass(pg) / totc;
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) {
+            float hv[8];
+            h_of(kk, hv);
+            const bf16x8 a = as_bf16x8(make_uint4(
+                pack_bf16x2(mix * hv[0], mix * hv[1]), pack_bf16x2(mix * hv[2], mix * hv[3]),
+                pack_bf16x2(mix * hv[4], mix * hv[5]), pack_bf16x2(mix * hv[6], mix * hv[7])));
+            const uint4 gb = *(const uint4*)(pcb + ((size_t)pg * D + e) * D + 16 * kk + 8 * hl);
+            cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(gb), cacc, 0, 0, 0);
+          }
+        }
+      }
+    } else if constexpr (COARSE) {
       if (coarse_on) {
         uint4 gb[KK];
 #pragma unroll
@@ -1251,9 +1289,8 @@ hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t
   if (perq && (p.qsel_words < 1 || p.qsel_words > kBitWords)) return hipErrorInvalidValue;
 #define TAO_READ_LAUNCH(D_, C_, Q_)                                                           \
   hipLaunchKernelGGL((read_groups_kernel<D_, C_, Q_, false>), grid, dim3(kGroupThreads), 0, s, p)
-#define TAO_MIXTURE_LAUNCH(D_)                                                                \
-  hipLaunchKernelGGL((read_groups_kernel<D_, false, true, true>), grid, dim3(kGroupThreads), 0, \
-                     s, p)
+#define TAO_MIXTURE_LAUNCH(D_, C_)                                                            \
+  hipLaunchKernelGGL((read_groups_kernel<D_, C_, true, true>), grid, dim3(kGroupThreads), 0, s, p)
 #define TAO_STREAM_LAUNCH(D_, C_)                                                             \
   hipLaunchKernelGGL((read_stream_kernel<D_, C_, false>), grid, dim3(kGroupThreads), 0, s, p)
 #define TAO_FEATURE_LAUNCH(D_, C_)                                                            \
@@ -1265,8 +1302,12 @@ hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t
     if (p.save_fine) return hipErrorInvalidValue;
     const bool pages = p.page_c != nullptr;
     if (perq) {
-      if (coarse || pages) return hipErrorInvalidValue;
-      if (head_dim == 128) TAO_MIXTURE_LAUNCH(128); else TAO_MIXTURE_LAUNCH(64);
+      if (coarse || (pages && !p.page_z)) return hipErrorInvalidValue;
+      if (pages) {
+        if (head_dim == 128) TAO_MIXTURE_LAUNCH(128, true); else TAO_MIXTURE_LAUNCH(64, true);
+      } else {
+        if (head_dim == 128) TAO_MIXTURE_LAUNCH(128, false); else TAO_MIXTURE_LAUNCH(64, false);
+      }
     } else if (pages) {
       if (!p.page_z) return hipErrorInvalidValue;
       if (head_dim == 128) TAO_FEATURE_LAUNCH(128, true); else TAO_FEATURE_LAUNCH(64, true);

@@ -35,16 +35,13 @@ _VALUE_WRITERS = ("softmax", "regularized_association")
 
 
 # Writers with log-mass descriptors and the numerator-only mixture read
-# (tao_stream.py:80-123, 600-662): forward only, index-only.
+# (tao_stream.py:80-123, 600-662): forward only.
 _FEATURE_WRITERS = ("feature_mass_association", "structured_gram_association")
 
 
 def _check(q, k, v, raw_q, raw_k, config, dtype=torch.bfloat16):
     if config.fine_writer in _FEATURE_WRITERS:
-        if not config.coarse_index_only:
-            raise NotImplementedError(
-                "the HIP full-sequence read implements the feature writers with "
-                "coarse_index_only=True (their coarse value read is not built)")
+        pass
     elif config.fine_writer not in _VALUE_WRITERS:
         raise NotImplementedError(
             f"the HIP full-sequence read implements the fine writers {_VALUE_WRITERS}")

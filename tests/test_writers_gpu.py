@@ -341,10 +341,13 @@ def test_stream_feature_writers(device, writer, width, index_only):
     close(snap["pending_mass"], ora.pending_mass, 1e-4)   # fp32 sums of 256 features
 
 
-@pytest.mark.parametrize("writer,width,tokens,batch", [
-    ("feature_mass_association", 64, 2900, 1), ("structured_gram_association", 128, 2900, 2),
-    ("feature_mass_association", 128, 1300, 1)])
-def test_full_sequence_feature_writers(device, writer, width, tokens, batch):
+@pytest.mark.parametrize("writer,width,tokens,batch,index_only", [
+    ("feature_mass_association", 64, 2900, 1, True),
+    ("structured_gram_association", 128, 2900, 2, True),
+    ("feature_mass_association", 128, 1300, 1, True),
+    ("feature_mass_association", 128, 3100, 1, False),
+    ("structured_gram_association", 64, 3100, 2, False)])
+def test_full_sequence_feature_writers(device, writer, width, tokens, batch, index_only):
     """tao_attention with the feature writers (index-only, forward): every
     query's selected set bit-exact against the oracle's per-query routing
     over log-mass descriptors, outputs within the bf16 tolerance of its
@@ -356,7 +359,7 @@ def test_full_sequence_feature_writers(device, writer, width, tokens, batch):
     xs = [torch.randn(batch, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
     fa = torch.randn(heads, width, 3, generator=g) * 0.02
     fb = torch.randn(heads, width, 3, generator=g) * 0.02
-    cfg = TaoConfig(fine_writer=writer, coarse_index_only=True)
+    cfg = TaoConfig(fine_writer=writer, coarse_index_only=index_only)
     q, k, v, rq, rk = (x.to(device) for x in xs)
     out, qsel = training.forward(q, k, v, rq, rk, fa.to(device), fb.to(device), 0.5, cfg,
                                  return_routes=True)

@@ -907,10 +907,11 @@ def training_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, ro
     `intermediates` receives the fine descriptors "fine_z" [B, H, S, D] and
     the bank "bank" [B, H, S, D, D] (C[d][e]), to take gradients at them.
 
-    writer="regularized_association" (index-only) keeps the softmax writer's
-    z and takes C_f = solve(G + tr(G)/D I, X) with G = U^T U, X = U^T V,
-    U = softmax_D(raw_k) of the block (association_writer.py:11-32 without
-    its bf16 casts), differentiable through the solve.
+    writer="regularized_association" keeps the softmax writer's z and takes
+    C_f = solve(G + tr(G)/D I, X) with G = U^T U, X = U^T V, U = softmax_D(raw_k)
+    of the block (association_writer.py:11-32 without its bf16 casts), and a
+    completed page's matrix from the sums of its fines' G and X,
+    differentiable through the solves.
     """
     g = geometry or Geometry()
     b, total, heads, d = q.shape
@@ -930,7 +931,7 @@ def training_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, ro
     visible_max = max(0, n_tiles - 1 - lag)
     if total <= g.serve_limit or visible_max == 0:
         return local
-    zs, cs = [], []
+    zs, cs, grams, crosses = [], [], [], []
     for f in range(visible_max):
         kb, vb = raw_k[:, f * ft:(f + 1) * ft], v[:, f * ft:(f + 1) * ft]
         zs.append(torch.logsumexp(kb, 1))                           # [B, H, D]
@@ -941,6 +942,8 @@ def training_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, ro
             ridge = gram.diagonal(dim1=-2, dim2=-1).sum(-1) / d
             system = gram + ridge[..., None, None] * torch.eye(d, dtype=gram.dtype)
             cs.append(torch.linalg.solve(system, cross))
+            grams.append(gram)
+            crosses.append(cross)
         else:
             cs.append(torch.einsum("bthd,bthe->bhde", torch.softmax(kb, 1), vb))
     fine_z = torch.stack(zs, 2)
@@ -950,7 +953,14 @@ def training_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, ro
     full = visible_max // group
     pz_full = [torch.logsumexp(fine_z[:, :, p * group:(p + 1) * group], 2) for p in range(full)]
     pc_full = []
-    if not g.coarse_index_only:
+    if not g.coarse_index_only and writer == "regularized_association":
+        for p in range(full):
+            gram = sum(grams[p * group + i] for i in range(group))
+            cross = sum(crosses[p * group + i] for i in range(group))
+            ridge = gram.diagonal(dim1=-2, dim2=-1).sum(-1) / d
+            system = gram + ridge[..., None, None] * torch.eye(d, dtype=gram.dtype)
+            pc_full.append(torch.linalg.solve(system, cross))
+    elif not g.coarse_index_only:
         for p in range(full):
             w = torch.exp(fine_z[:, :, p * group:(p + 1) * group] - pz_full[p].unsqueeze(2))
             pc_full.append(torch.einsum("bhsd,bhsde->bhde", w, bank[:, :, p * group:(p + 1) * group]))

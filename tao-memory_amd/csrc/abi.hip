@@ -391,10 +391,16 @@ hipError_t feature_seal(const tao_state_dev* st, const tao::TokView& rk, const t
 // 11-32 under autograd): the fines' statistics again, Y = A^{-1} cross and
 // W = A^{-1} dC in fp32, S = dG + dG^T, then per block d raw_k's share
 // (written to dk_extra) and dv's (added to dv).
+struct AssocPages {
+  size_t stats, y, w, s;   // workspace offsets
+  const float* dpc;        // d page_c [B*H][pages][e][d]
+  int pages;
+};
+
 hipError_t assoc_backward(const tao_state_dev* st, const tao_tokens* tok, char* ws,
                           size_t stats_off, size_t y_off, size_t w_off, size_t s_off,
                           size_t dk_off, size_t starts_off, const float* dc, float* dv,
-                          int fines, int T, hipStream_t s) {
+                          int fines, int T, const AssocPages& pg, hipStream_t s) {
   const int B = st->batch, H = st->heads, D = st->head_dim, ft = st->fine_tokens;
   const int mats = fines * B * H;
   int64_t* starts = (int64_t*)(ws + starts_off);
@@ -450,6 +456,41 @@ hipError_t assoc_backward(const tao_state_dev* st, const tao_tokens* tok, char* 
   bp.ft = ft;
   e = tao::launch_assoc_gram_bwd(bp, D, s);
   if (e != hipSuccess) return e;
+  if (pg.pages > 0) {
+    // Page g's matrix is the solve of its fines' summed statistics: its
+    // adjoints W_g and S_g add to each of its fines' (the sums' gradient).
+    const int G = st->coarse_group, pmats = pg.pages * B * H;
+    float* pgram = (float*)(ws + pg.stats);
+    float* pcross = pgram + (size_t)pmats * D * D;
+    e = tao::launch_page_sum(gram, pgram, pg.pages, G, B, H, (int64_t)D * D, s);
+    if (e == hipSuccess) e = tao::launch_page_sum(cross, pcross, pg.pages, G, B, H, (int64_t)D * D, s);
+    if (e != hipSuccess) return e;
+    tao::AssocSolveParams pp{};
+    pp.gram = pgram;
+    pp.cross = pcross;
+    pp.count = pmats;
+    pp.B = B;
+    pp.H = H;
+    pp.out_f32 = (float*)(ws + pg.y);
+    e = tao::launch_association_solve(pp, D, s);
+    if (e != hipSuccess) return e;
+    pp.out_f32 = (float*)(ws + pg.w);
+    pp.rhs_t = pg.dpc;
+    pp.rhs_cap = pg.pages;
+    e = tao::launch_association_solve(pp, D, s);
+    if (e != hipSuccess) return e;
+    tao::AssocBwdParams gp = bp;
+    gp.w = (const float*)(ws + pg.w);
+    gp.y = (const float*)(ws + pg.y);
+    gp.s = (float*)(ws + pg.s);
+    gp.mats = pmats;
+    e = tao::launch_assoc_gram_bwd(gp, D, s);
+    if (e == hipSuccess)
+      e = tao::launch_page_to_fines((float*)(ws + w_off), (float*)(ws + s_off),
+                                    (const float*)(ws + pg.w), (const float*)(ws + pg.s), fines, G,
+                                    B, H, (int64_t)D * D, s);
+    if (e != hipSuccess) return e;
+  }
   return tao::launch_assoc_block_bwd(bp, D, s);
 }
 
@@ -1249,8 +1290,10 @@ struct TrainBwdLayout {
   size_t dlocal, h, delta, dden, dcoarse, dnum, drq, dh, dvf;   // per-token arrays
   size_t dpw, dsw_tile, dgc, dc, dsw, dpz, dz, dalpha;          // memory branch, d alpha
   size_t dalpha_parts;                                          // per fusion workgroup
-  // regularized writer: statistics, solutions Y and W, S, d raw_k share, starts
+  // regularized writer: statistics, solutions Y and W, S, d raw_k share, starts;
+  // with page values, the pages' statistic sums, Y, W, S and d page_c
   size_t stats, sol_y, sol_w, sgram, dk_extra, starts;
+  size_t pstats, psol_y, psol_w, psgram, dpc;
   size_t zero_begin, zero_end;                                  // accumulators to clear
   size_t total;
   int n_tiles, v_max;
@@ -1288,6 +1331,8 @@ TrainBwdLayout train_bwd_layout(const tao_state_dev* st, int64_t tokens, int fin
   l.dsw = take(BH * (size_t)fines * D * 4);
   l.dpz = take(BH * (size_t)st->page_cap * D * 4);
   l.dz = take(BH * (size_t)fines * D * 4);
+  const size_t pages = (assoc_writer(st) && st->page_c) ? (size_t)fines / st->coarse_group : 0;
+  l.dpc = take(BH * pages * D * D * 4);
   l.dalpha = take(4);
   l.zero_end = off;
   l.dalpha_parts = take((size_t)tao::fuse_bwd_workgroups((int)T, (int)B, (int)H) * 4);
@@ -1299,6 +1344,11 @@ TrainBwdLayout train_bwd_layout(const tao_state_dev* st, int64_t tokens, int fin
     l.sgram = take(mats * mat);
     l.dk_extra = take(rows * D * 4);
     l.starts = take((size_t)fines * 8);
+    const size_t pmats = pages * BH;
+    l.pstats = take(2 * pmats * mat);
+    l.psol_y = take(pmats * mat);
+    l.psol_w = take(pmats * mat);
+    l.psgram = take(pmats * mat);
   }
   l.total = off;
   return l;
@@ -1345,10 +1395,6 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   const TrainBwdLayout l = train_bwd_layout(st, T, fines, fines > 0 ? pools : nullptr);
   if (a->workspace_bytes < l.total) return fail(TAO_E_WORKSPACE, "backward workspace too small");
   const bool regularized = assoc_writer(st) && fines > 0;
-  if (regularized && st->page_c)
-    return fail(TAO_E_ARGUMENT,
-                "gradients through the regularized writer's page matrices are not built "
-                "(index-only states only)");
   if (feature_writer(st)) return fail(TAO_E_ARGUMENT, "gradients through a feature writer");
   const hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)a->workspace;
@@ -1460,13 +1506,18 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   mp.page_cap = st->page_cap;
   mp.v_max = fines;
   mp.coarse_values = st->page_c != nullptr;
+  if (regularized) {
+    mp.values_external = 1;
+    mp.dpc = (float*)(ws + l.dpc);
+    mp.dpc_cap = st->page_c ? fines / G : 0;
+  }
   e = tao::launch_mem_bwd_read(mp, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_train_backward memory branch");
   if (regularized) {
+    AssocPages pg{l.pstats, l.psol_y, l.psol_w, l.psgram, mp.dpc, mp.dpc_cap};
     e = assoc_backward(st, tok, ws, l.stats, l.sol_y, l.sol_w, l.sgram, l.dk_extra, l.starts,
-                       mp.dc, mp.dv, fines, (int)T, s);
+                       mp.dc, mp.dv, fines, (int)T, pg, s);
     if (e != hipSuccess) return check_hip(e, "tao_train_backward association writer");
-    mp.values_external = 1;
     mp.dk_extra = (const float*)(ws + l.dk_extra);
   }
   e = tao::launch_mem_bwd_writer(mp, D, s);

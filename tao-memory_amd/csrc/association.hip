@@ -721,6 +721,48 @@ __global__ __launch_bounds__(512) void assoc_block_bwd_kernel(AssocBwdParams p) 
   }
 }
 
+__global__ __launch_bounds__(256) void page_sum_kernel(const float* x, float* out, int pages,
+                                                        int group, int B, int H, int64_t dd) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per = (int64_t)B * H * dd;
+  if (i >= (int64_t)pages * per) return;
+  const int64_t g = i / per, r = i % per;               // r = (b H + h) dd + e
+  float acc = x[(g * group) * per + r];
+  for (int k = 1; k < group; ++k) acc += x[(g * group + k) * per + r];
+  out[i] = acc;
+}
+
+__global__ __launch_bounds__(256) void page_to_fines_kernel(float* w, float* s, const float* wp,
+                                                            const float* sp, int fines, int group,
+                                                            int B, int H, int64_t dd) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per = (int64_t)B * H * dd;
+  const int full = (fines / group) * group;             // fines of completed pages
+  if (i >= (int64_t)full * per) return;
+  const int64_t f = i / per, r = i % per;
+  const int64_t at = (f / group) * per + r;
+  w[i] += wp[at];
+  s[i] += sp[at];
+}
+
+hipError_t launch_page_sum(const float* x, float* out, int pages, int group, int B, int H,
+                           int64_t dd, hipStream_t s) {
+  const int64_t n = (int64_t)pages * B * H * dd;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(page_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, out,
+                     pages, group, B, H, dd);
+  return hipGetLastError();
+}
+
+hipError_t launch_page_to_fines(float* w, float* s_, const float* wp, const float* sp, int fines,
+                                int group, int B, int H, int64_t dd, hipStream_t s) {
+  const int64_t n = (int64_t)((fines / group) * group) * B * H * dd;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(page_to_fines_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w,
+                     s_, wp, sp, fines, group, B, H, dd);
+  return hipGetLastError();
+}
+
 hipError_t launch_block_starts(int64_t* starts, int count, int64_t step, hipStream_t s) {
   if (count <= 0) return hipSuccess;
   hipLaunchKernelGGL(block_starts_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s,

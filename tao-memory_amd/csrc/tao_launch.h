@@ -389,6 +389,9 @@ struct MemBwdParams {
   // nullable) is added to d raw_k of the block tokens.
   int values_external;
   const float* dk_extra;
+  // With values_external and page values: d page_c (C^T layout, fp32
+  // [B*H][dpc_cap][D][D], zeroed by the caller) accumulates here.
+  float* dpc; int dpc_cap;
 };
 // The memory branch in two parts: read_part (the read's adjoints down to dC
 // and dz) and writer_part (the writer adjoint and the finish); a caller may
@@ -451,6 +454,14 @@ struct AssocBwdParams {
   int mats, B, H, T, ft;
 };
 hipError_t launch_assoc_gram_bwd(const AssocBwdParams& p, int head_dim, hipStream_t s);
+// Pages of the regularized writer: page_sum writes the in-order sums of each
+// completed page's group fines' statistics (x: [fines * B][H][dd] in (f, b, h)
+// order -> out [pages * B][H][dd]); page_to_fines adds a page's W and S to
+// each of its fines' (w, s: [fines * B][H][D][D], page ones after them).
+hipError_t launch_page_sum(const float* x, float* out, int pages, int group, int B, int H,
+                           int64_t dd, hipStream_t s);
+hipError_t launch_page_to_fines(float* w, float* s_, const float* wp, const float* sp, int fines,
+                                int group, int B, int H, int64_t dd, hipStream_t s);
 hipError_t launch_assoc_block_bwd(const AssocBwdParams& p, int head_dim, hipStream_t s);
 // starts[i] = i * step (the token blocks of a full-sequence call).
 hipError_t launch_block_starts(int64_t* starts, int count, int64_t step, hipStream_t s);

@@ -1177,7 +1177,9 @@ __global__ __launch_bounds__(kThreads) void outer_bwd_kernel(MemBwdParams p, int
     if (mode == 0 && f >= p.v_max) break;
     float* out = mode == 0 ? p.dc + ((size_t)bh * p.v_max + f) * D * D
                            : p.dgc + ((size_t)item * BH + bh) * D * D;
-    const bool coarse_share = mode == 0 && tg == 0 && p.coarse_values && f < G * (p.v_max / G);
+    // (Only the softmax writer's page matrices are sums of its fines' C.)
+    const bool coarse_share = mode == 0 && tg == 0 && p.coarse_values && !p.values_external &&
+                              f < G * (p.v_max / G);
     const int g = f / G;
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
@@ -1287,6 +1289,16 @@ __global__ __launch_bounds__(kThreads) void coarse_page_bwd_kernel(MemBwdParams 
   for (int g = part; g < K; g += PARTS) {
     const float cw = __expf(bf2f(pz[(size_t)g * D + d]) - m) / z;
     atomicAdd(p.dpz + ((size_t)bh * p.page_cap + g) * D + d, cw * (sdcw[g][d] - s));
+  }
+  if (p.values_external) {
+    // Page matrices not built from the fines' C (regularized writer): their
+    // adjoint d page_c[g] += cw[g] * dG (C^T layout), taken by the caller.
+    for (int g = part; g < K; g += PARTS) {
+      const float cw = __expf(bf2f(pz[(size_t)g * D + d]) - m) / z;
+      float* dst = p.dpc + ((size_t)bh * p.dpc_cap + g) * D * D;
+      for (int e = 0; e < D; ++e) atomicAdd(dst + (size_t)e * D + d, cw * dg[(size_t)e * D + d]);
+    }
+    return;
   }
   for (int f = part; f < K * G; f += PARTS) {
     const int g = f / G;

@@ -274,10 +274,6 @@ def _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, conf
         raise NotImplementedError(
             f"gradients of the full-sequence read are implemented for the writers "
             f"{_VALUE_WRITERS}")
-    if config.fine_writer == "regularized_association" and not config.coarse_index_only:
-        raise NotImplementedError(
-            "gradients through the regularized writer's page matrices are not built: "
-            "use coarse_index_only=True")
     b, tokens, heads, d = q.shape
     ws = _Workspace(config, b, tokens, heads, d, q.device)
     q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)

@@ -662,10 +662,12 @@ def test_full_sequence_backward_matches_oracle(tokens, heads, width, index_only,
     _compare_gradients(got, want, 5e-2)
 
 
-@pytest.mark.parametrize("tokens,heads,width,seed", [(1300, 2, 64, 61), (2900, 2, 128, 62)])
-def test_full_sequence_backward_regularized_writer(tokens, heads, width, seed):
+@pytest.mark.parametrize("tokens,heads,width,seed,index_only", [
+    (1300, 2, 64, 61, True), (2900, 2, 128, 62, True), (3100, 2, 64, 63, False)])
+def test_full_sequence_backward_regularized_writer(tokens, heads, width, seed, index_only):
     """tao_attention backward with fine_writer="regularized_association"
-    (index-only): the writer's share differentiates the association solve
+    (index-only, and with page values past 2,560 tokens: each page matrix's
+    adjoint adds to its fines'): the writer's share differentiates the association solve
     (dC -> W = A^{-1} dC, dG from W and the fp32 C, then U, V and the
     feature softmax), the z path stays the softmax writer's; all gradients
     against fp64 autograd of the oracle's smooth forward through
@@ -673,7 +675,7 @@ def test_full_sequence_backward_regularized_writer(tokens, heads, width, seed):
     gradients differ from the softmax writer's."""
     from tao_attention import TaoConfig, tao_attention
     xs, fa, fb = inputs(tokens, heads, width, seed)
-    cfg = TaoConfig(coarse_index_only=True, fine_writer="regularized_association")
+    cfg = TaoConfig(coarse_index_only=index_only, fine_writer="regularized_association")
     grad = torch.randn(xs[0].shape, generator=torch.Generator().manual_seed(seed + 100)).to(BF16)
     dev = [x.cuda().requires_grad_(True) for x in xs]
     fa_d = fa.cuda().requires_grad_(True)
@@ -688,13 +690,10 @@ def test_full_sequence_backward_regularized_writer(tokens, heads, width, seed):
     for g in got:
         assert torch.isfinite(g.float()).all()
     _compare_gradients(got, want, 5e-2)
-    soft = _reference_gradients(xs, fa, fb, grad, TaoConfig(coarse_index_only=True), routes)
+    soft = _reference_gradients(xs, fa, fb, grad, TaoConfig(coarse_index_only=index_only),
+                                routes)
     for i in (2, 4):                                    # v, raw_k
         assert (soft[i] - want[i]).norm() > 0.1 * want[i].norm()
-    cfg_pages = TaoConfig(coarse_index_only=False, fine_writer="regularized_association")
-    with pytest.raises(NotImplementedError):
-        tao_attention(*dev[:3], raw_q=dev[3], raw_k=dev[4], fusion_a=fa_d, fusion_b=fb_d,
-                      alpha=0.5, config=cfg_pages)
 
 
 @pytest.mark.parametrize("tokens,heads,width,index_only,seed", [

@@ -1213,6 +1213,17 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
       ae[j][i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + (8 * c + j) * p.fa_s[1] + i * p.fa_s[2]);
       be[j][i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + (8 * c + j) * p.fb_s[1] + i * p.fb_s[2]);
     }
+  // Without the coarse branch: the paired two-channel fusion on the rounded
+  // parameters and the signed-zero coarse term.
+  float ra[8][3], rb[8][3];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      ra[j][i] = rbf(ae[j][i]);
+      rb[j][i] = rbf(be[j][i]);
+    }
+  const float ct0 = rbf(0.0f * rbf(p.gain * 0.0f));
 #pragma unroll
   for (int it = 0; it < 32 / RPI; ++it) {
     const int r = lane / CPR + RPI * it;
@@ -1234,11 +1245,17 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
     uint32_t o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const bf16_t lo = fuse_element(xv[2 * j], lv[2 * j], cv[2 * j], fv[2 * j], ae[2 * j], be[2 * j],
-                                     p.gain, coarse_on ? 1 : 0, 1);
-      const bf16_t hi = fuse_element(xv[2 * j + 1], lv[2 * j + 1], cv[2 * j + 1], fv[2 * j + 1],
-                                     ae[2 * j + 1], be[2 * j + 1], p.gain, coarse_on ? 1 : 0, 1);
-      o[j] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+      if constexpr (!COARSE) {
+        o[j] = fuse_pair_local_fine(&xv[2 * j], &lv[2 * j], &fv[2 * j], &ra[2 * j], &rb[2 * j],
+                                    p.gain, ct0);
+      } else {
+        const bf16_t lo = fuse_element(xv[2 * j], lv[2 * j], cv[2 * j], fv[2 * j], ae[2 * j],
+                                       be[2 * j], p.gain, coarse_on ? 1 : 0, 1);
+        const bf16_t hi = fuse_element(xv[2 * j + 1], lv[2 * j + 1], cv[2 * j + 1], fv[2 * j + 1],
+                                       ae[2 * j + 1], be[2 * j + 1], p.gain, coarse_on ? 1 : 0, 1);
+        o[j] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+      }
     }
     *(uint4*)(p.out + b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + 8 * c) =
         make_uint4(o[0], o[1], o[2], o[3]);

@@ -66,4 +66,63 @@ TAO_DEV bf16_t fuse_element(float q, float local, float coarse, float fine,
   return fuse_mix(fuse_weights(q, a, b, coarse_on, fine_on), local, coarse, fine, gain);
 }
 
+// Rounds x and y to bf16 with one packed conversion.
+TAO_DEV void rbf2(float& x, float& y) {
+  const uint32_t pk = pack_bf16x2(x, y);
+  x = __uint_as_float(pk << 16);
+  y = __uint_as_float(pk & 0xFFFF0000u);
+}
+
+// Two adjacent channels of the fusion with the fine branch present and the
+// coarse branch absent, packed as bf16x2 (channel 0 low). Bit-identical to
+// fuse_element(q[j], local[j], 0, fine[j], a[j], b[j], gain, 0, 1) with
+// ra = rbf(a), rb = rbf(b): each rounding point is the same, paired over
+// the two channels, and the coarse terms are folded. Without the coarse
+// branch the local bias is 0, so rbf(s0 + 0) differs from s0 only in the
+// sign of a zero, which no later step sees (exp(s - top) is 1 for either
+// zero); the coarse weight is +0, so the total is e0 + e2, and the coarse
+// term is ct0 = rbf(+0 * rbf(gain * 0)), a signed zero that the caller
+// computes once, so rbf(lt + ct) = lt + ct0 (lt is already bf16).
+TAO_DEV uint32_t fuse_pair_local_fine(const float q[2], const float local[2], const float fine[2],
+                                      const float ra[2][3], const float rb[2][3], float gain,
+                                      float ct0) {
+  float p0[2], p2[2], e0[2], e2[2], l2[2], gf[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    p0[j] = ra[j][0] * q[j];
+    p2[j] = ra[j][2] * q[j];
+  }
+  rbf2(p0[0], p0[1]);
+  rbf2(p2[0], p2[1]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    p0[j] = p0[j] + rb[j][0];
+    p2[j] = p2[j] + rb[j][2];
+  }
+  rbf2(p0[0], p0[1]);
+  rbf2(p2[0], p2[1]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float top = fmaxf(p0[j], p2[j]);
+    const float x0 = __expf(p0[j] - top), x2 = __expf(p2[j] - top);
+    const float inv = __builtin_amdgcn_rcpf(x0 + x2);
+    e0[j] = x0 * inv;
+    e2[j] = x2 * inv;
+    l2[j] = 2.0f * local[j];
+    gf[j] = gain * fine[j];
+  }
+  rbf2(e0[0], e0[1]);
+  rbf2(e2[0], e2[1]);
+  rbf2(l2[0], l2[1]);
+  rbf2(gf[0], gf[1]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    l2[j] = e0[j] * l2[j];
+    gf[j] = e2[j] * gf[j];
+  }
+  rbf2(l2[0], l2[1]);
+  rbf2(gf[0], gf[1]);
+  return pack_bf16x2((l2[0] + ct0) + gf[0], (l2[1] + ct0) + gf[1]);
+}
+
 }  // namespace tao

@@ -27,6 +27,7 @@ cursor (schedule.py), so no device-to-host synchronisation is needed.
 import contextlib
 import ctypes
 import itertools
+import math
 import os
 
 import numpy as np
@@ -52,58 +53,76 @@ _FEATURE_WRITERS = {"feature_mass_association": 1, "structured_gram_association"
 _SERIAL = itertools.count(1)
 
 
+def _zeroed_views(device, specs):
+    """Zero-filled device buffers for specs [(shape, dtype) or None], carved
+    at 256-byte offsets out of one allocation, so a new state issues one fill
+    kernel instead of one per buffer (prefill latency). None stays None."""
+    offsets, total = [], 0
+    for spec in specs:
+        if spec is None:
+            offsets.append(None)
+            continue
+        shape, dtype = spec
+        nbytes = math.prod(shape) * dtype.itemsize
+        offsets.append((total, nbytes))
+        total += (nbytes + 255) // 256 * 256
+    arena = torch.zeros(max(total, 256), dtype=torch.uint8, device=device)
+    views = []
+    for spec, off in zip(specs, offsets):
+        if spec is None:
+            views.append(None)
+        else:
+            views.append(arena[off[0]:off[0] + off[1]].view(spec[1]).view(spec[0]))
+    return views
+
+
 class _DeviceState:
     """Device buffers of one state and the C-ABI view of them."""
 
-    def __init__(self, config, batch, heads, head_dim, device, fine_cap):
+    def __init__(self, config, batch, heads, head_dim, device, fine_cap, plan_words=4096):
         self.config = config
         self.B, self.H, self.D = batch, heads, head_dim
         self.device = device
         self.L = config.serve_limit
-        bf16 = torch.bfloat16
+        bf16, f32 = torch.bfloat16, torch.float32
         shape = (batch, self.L, heads, head_dim)
-        self.ring_k = torch.zeros(shape, dtype=bf16, device=device)
-        self.ring_v = torch.zeros(shape, dtype=bf16, device=device)
-        self.ring_raw = torch.zeros(shape, dtype=bf16, device=device)
-        self.header = torch.zeros(4, dtype=torch.int64, device=device)
-        self.starts = torch.zeros(1, dtype=torch.int64, device=device)
-        # Folded route (G^T and den weights), fixed size: survives capacity growth.
-        self.fold_g = torch.zeros((batch, heads, head_dim, head_dim), dtype=torch.float32,
-                                  device=device)
-        self.fold_den = torch.zeros((batch, heads, head_dim), dtype=torch.float32, device=device)
+        dd = (batch, heads, head_dim, head_dim)
         self.coarse_values = not config.coarse_index_only
-        self.coarse_g = (torch.zeros((batch, heads, head_dim, head_dim), dtype=torch.float32,
-                                     device=device) if self.coarse_values else None)
         self.page_c = None
         # Regularized association writer: the pending page's fp32 statistic
         # sums (the reference's pending_gram / pending_cross) and scratch for
         # the statistics of up to _STATS_CAP blocks per pass; fixed size.
         self.association = config.fine_writer == "regularized_association"
-        self.pending_gram = self.pending_cross = self.stats = None
-        if self.association:
-            dd = (batch, heads, head_dim, head_dim)
-            self.pending_gram = torch.zeros(dd, dtype=torch.float32, device=device)
-            self.pending_cross = torch.zeros(dd, dtype=torch.float32, device=device)
-            self.stats = torch.empty((2, _STATS_CAP * batch, heads, head_dim, head_dim),
-                                     dtype=torch.float32, device=device)
         # Feature writers: each sealed fine's fp32 feature mass (page
-        # descriptors sum them) and statistics scratch with a mass region.
+        # descriptors sum them) and statistics scratch with a mass region;
+        # with page values, the pending page's statistic sums (the
+        # reference's pending gram / square mass, mass and cross).
         self.feature = _FEATURE_WRITERS.get(config.fine_writer, 0)
         self.fine_mass = None
-        if self.feature:
+        pending = None
+        if self.association:
+            pending = (dd, dd)
+        elif self.feature and self.coarse_values:
+            pending = (dd if self.feature == 1 else (2, batch, heads, head_dim), dd)
+        # The ring, header, fold (G^T and den weights), coarse fold and
+        # pending sums: fixed size, they survive capacity growth.
+        (self.ring_k, self.ring_v, self.ring_raw, self.header, self.starts, self.fold_g,
+         self.fold_den, self.coarse_g, self.pending_gram, self.pending_cross) = _zeroed_views(
+            device, [(shape, bf16), (shape, bf16), (shape, bf16), ((4,), torch.int64),
+                     ((1,), torch.int64), (dd, f32), ((batch, heads, head_dim), f32),
+                     (dd, f32) if self.coarse_values else None,
+                     None if pending is None else (pending[0], f32),
+                     None if pending is None else (pending[1], f32)])
+        self.stats = None
+        if self.association:
+            self.stats = torch.empty((2, _STATS_CAP * batch, heads, head_dim, head_dim),
+                                     dtype=f32, device=device)
+        elif self.feature:
             words = _STATS_CAP * batch * heads * head_dim
-            self.stats = torch.empty(words * (2 * head_dim + 1), dtype=torch.float32,
-                                     device=device)
-            if self.coarse_values:
-                # The pending page's statistic sums (the reference's pending
-                # gram / square mass, mass and cross), for its page matrix.
-                first = ((batch, heads, head_dim, head_dim) if self.feature == 1
-                         else (2, batch, heads, head_dim))
-                self.pending_gram = torch.zeros(first, dtype=torch.float32, device=device)
-                self.pending_cross = torch.zeros((batch, heads, head_dim, head_dim),
-                                                 dtype=torch.float32, device=device)
+            self.stats = torch.empty(words * (2 * head_dim + 1), dtype=f32, device=device)
         self.generation = next(_SERIAL)   # renewed whenever the buffers move
         self.fine_cap = 0
+        self.plan_words = max(plan_words, 4096)
         self._allocate(fine_cap, copy_fines=0)
 
     def _allocate(self, fine_cap, copy_fines):
@@ -114,16 +133,13 @@ class _DeviceState:
         sel_cap = min(512, cfg.budget(fine_cap) + 1)
         chosen_cap = page_cap
         bank = torch.empty((B, H, fine_cap, D, D), dtype=bf16, device=dev)
-        fine_z = torch.zeros((B, H, fine_cap, D), dtype=bf16, device=dev)
-        fine_sw = torch.zeros((B, H, fine_cap, D), dtype=bf16, device=dev)
-        page_z = torch.zeros((B, H, page_cap, D), dtype=bf16, device=dev)
-        page_w = torch.zeros((B, H, page_cap, D), dtype=bf16, device=dev)
-        sel = torch.zeros((B, H, sel_cap), dtype=torch.int32, device=dev)
-        chosen = torch.zeros((B, H, chosen_cap), dtype=torch.int32, device=dev)
         page_c = (torch.empty((B, H, page_cap, D, D), dtype=bf16, device=dev)
                   if self.coarse_values else None)
-        fine_mass = (torch.zeros((B, H, fine_cap, D), dtype=torch.float32, device=dev)
-                     if self.feature else None)
+        fine_z, fine_sw, page_z, page_w, sel, chosen, fine_mass = _zeroed_views(
+            dev, [((B, H, fine_cap, D), bf16), ((B, H, fine_cap, D), bf16),
+                  ((B, H, page_cap, D), bf16), ((B, H, page_cap, D), bf16),
+                  ((B, H, sel_cap), torch.int32), ((B, H, chosen_cap), torch.int32),
+                  ((B, H, fine_cap, D), torch.float32) if self.feature else None])
         if copy_fines:
             n = copy_fines
             bank[:, :, :n].copy_(self.bank[:, :, :n])
@@ -148,8 +164,7 @@ class _DeviceState:
         self.generation = next(_SERIAL)
         self.fine_cap, self.page_cap, self.sel_cap, self.chosen_cap = (
             fine_cap, page_cap, sel_cap, chosen_cap)
-        self.plan_words = 0
-        self._workspace(4096)
+        self._workspace(self.plan_words)
 
     def _workspace(self, plan_words):
         ws_bytes = _hip.lib().tao_workspace_bytes(self.B, self.H, self.D, self.sel_cap,
@@ -428,14 +443,14 @@ class StreamCache:
             raise ValueError("head width must be 64 or 128")
         _hip.require_device(q)
 
-    def _device_for(self, q, total_positions):
+    def _device_for(self, q, total_positions, plan_words=4096):
         b, _, h, d = q.shape
         fines = schedule.fines_at(total_positions, self.config)
         if self._dev is None:
             cap = 16
             while cap < fines:
                 cap *= 2
-            self._dev = _DeviceState(self.config, b, h, d, q.device, cap)
+            self._dev = _DeviceState(self.config, b, h, d, q.device, cap, plan_words)
         elif not self._dev.matches(b, h, d, q.device):
             raise ValueError("batch/heads/width/device must stay fixed for a state")
         elif self._dev.reserve(fines, schedule.fines_at(self.position, self.config)):
@@ -494,9 +509,16 @@ class StreamCache:
         info = (ctypes.c_int64 * 10)()
         args = (ctypes.byref(scfg), pos0, tokens, self.route_coarse, self.route_size,
                 int(outputs))
-        _hip.check(lib.tao_prefill_plan(*args, None, 0, info))
-        plan = np.empty(info[0], dtype=np.int64)
-        _hip.check(lib.tao_prefill_plan(*args, plan.ctypes.data, info[0], info))
+        # One planner call when the plan fits a 64K-word guess (every prompt up
+        # to about 1M tokens); a second, sized one otherwise.
+        plan = np.empty(1 << 16, dtype=np.int64)
+        rc = lib.tao_prefill_plan(*args, plan.ctypes.data, plan.size, info)
+        if rc != 0 and not info[0] > plan.size:
+            _hip.check(rc)
+        if info[0] > plan.size:
+            plan = np.empty(info[0], dtype=np.int64)
+            _hip.check(lib.tao_prefill_plan(*args, plan.ctypes.data, info[0], info))
+        plan = plan[:info[0]]
         return plan, dict(epochs=info[1], turns=info[2], route=(info[3], info[4]),
                           pool_pcap=info[5], history_chunks=info[6], chunks=info[7],
                           coarse_first=info[8], coarse_count=info[9])
@@ -555,10 +577,10 @@ class StreamCache:
         cfg = self.config
         pos0 = self.position
         tokens = q.shape[1]
-        dev = self._device_for(q, pos0 + tokens)
+        plan, info = self._plan(pos0, tokens, outputs=True)
+        dev = self._device_for(q, pos0 + tokens, plan_words=len(plan))
         q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
-        plan, info = self._plan(pos0, tokens, outputs=True)
         if local_flash is not None:
             from .flash_attention import plugin_stream_local
             window = self._local_window()

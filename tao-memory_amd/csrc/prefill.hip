@@ -208,7 +208,9 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
   __shared__ GroupSmem<D> sm;
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
-  const int grp = blockIdx.x / BH;
+  // Tiles in reverse plan order: the latest tiles read the most fines, so
+  // they start first and the light early tiles fill the end of the launch.
+  const int grp = (p.n_tiles + kGroupWaves - 1) / kGroupWaves - 1 - (int)blockIdx.x / BH;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 31, hl = lane >> 5;
@@ -768,7 +770,9 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
   __shared__ __attribute__((aligned(16))) bf16_t pwsw[kRing][2][D];     // staged pw and sw rows
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
-  const int grp = blockIdx.x / BH;
+  // Tiles in reverse plan order: the latest tiles read the most fines, so
+  // they start first and the light early tiles fill the end of the launch.
+  const int grp = (p.n_tiles + kGroupWaves - 1) / kGroupWaves - 1 - (int)blockIdx.x / BH;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 31, hl = lane >> 5;

@@ -812,7 +812,8 @@ __global__ __launch_bounds__(kQThreads) void route_turns_kernel(RouteParams p) {
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   const int b = bh / p.H, h = bh % p.H;
-  const int t0 = (blockIdx.x / BH) * kTurnGroup;
+  // Turn groups in reverse order: the latest turns score the most rows.
+  const int t0 = ((p.n_turns + kTurnGroup - 1) / kTurnGroup - 1 - (int)blockIdx.x / BH) * kTurnGroup;
   const int t1 = min(p.n_turns, t0 + kTurnGroup);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   for (int s0 = t0; s0 < t1;) {

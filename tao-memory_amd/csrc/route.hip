@@ -757,7 +757,8 @@ __global__ __launch_bounds__(kQThreads) void route_tile_kernel(QueryRouteParams 
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   const int b = bh / p.H, h = bh % p.H;
-  const int64_t* desc = p.tiles + 8 * (blockIdx.x / BH);
+  // Tiles in reverse order: the latest tiles score the most keys.
+  const int64_t* desc = p.tiles + 8 * ((int)gridDim.x / BH - 1 - (int)blockIdx.x / BH);
   if (!desc[6]) return;                          // no history: workgroup-uniform
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int q_first = (int)desc[0], nq = (int)desc[1];

@@ -813,7 +813,8 @@ __global__ __launch_bounds__(kRbWaves * 64) void read_bwd_kernel(MemBwdParams p)
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   const int b = bh / p.H, h = bh % p.H;
-  const int q0 = (blockIdx.x / BH) * kRbQ;
+  // Query blocks in reverse order: the latest blocks read the most fines.
+  const int q0 = ((int)gridDim.x / BH - 1 - (int)blockIdx.x / BH) * kRbQ;
   const int tile = q0 / p.ft;
   const int V = tile_visible(tile, p.keep / p.ft);
   if (V == 0) return;

@@ -797,13 +797,13 @@ __global__ __launch_bounds__(kQThreads) void route_tile_kernel(QueryRouteParams 
 }
 
 // Turn routes of a prefill (route_kernel's turn mode) with the lane-per-pair
-// core: one 256-thread workgroup per (8 consecutive turns, batch, head). The
-// turns are split into runs that share a seal epoch (8 turns span at most
-// two); each run stages its epoch's rows once and routes its anchors
-// together. Outputs as route_kernel: ids in score order into the turn's
+// core: one 256-thread workgroup per (16 consecutive turns, batch, head).
+// The turns are split into runs that share a seal epoch (a run holds at most
+// the turns of one epoch, within the tile's 32 queries); each run stages its
+// epoch's rows once and routes its anchors together. Outputs as route_kernel: ids in score order into the turn's
 // sel_pool slot; the publishing turn also writes the state's route, chosen
 // pages and route size.
-constexpr int kTurnGroup = 8;
+constexpr int kTurnGroup = 16;
 
 template <int D>
 __global__ __launch_bounds__(kQThreads) void route_turns_kernel(RouteParams p) {

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 8
+#define TAO_ABI_VERSION 9
 
 enum tao_status {
   TAO_OK = 0,
@@ -83,17 +83,24 @@ typedef struct tao_state_dev {
   int32_t stats_cap;     /* blocks per pass through the scratch (>= 1) */
   /* Feature writers (feature_mass_association, structured_gram_association;
    * tao_stream.py:56-65, 280-283, 362-367, 463-499): fine_writer selects
-   * them, fine_mass holds each sealed fine's fp32 feature mass (its z is
-   * r(log mass); page descriptors are r(log) of summed masses) and the read
-   * is the numerator-only mixture. They need stats (and stats_cap), plus
-   * [stats_cap * B][H][D] floats of mass scratch after its two halves. With
-   * page_c they also need pending_gram and pending_cross: the pending page's
-   * gram [B, H, D, D] (feature mass) or square mass and mass [2, B, H, D]
-   * (structured), and its cross sum [B, H, D, D]; the coarse read is then
-   * the mixture over pages (tao_stream.py:301-305).
+   * them and the read is the numerator-only mixture. A fine's z is
+   * r(log mass) of its own fp32 feature mass; fine_mass[slot] holds the fp32
+   * total, in seal order, of the masses of the run through that fine (the
+   * reference's pending_mass after that seal), and a page or pending
+   * descriptor is r(log) of it at the page's last fine. A run starts at fine
+   * 0 and, with page_c (and in the full-sequence path), again at each
+   * page's first fine; the streaming index-only state sums from fine 0 on,
+   * as the reference clears pending_mass only when it builds page values
+   * (tao_stream.py:488-497). They need stats (and stats_cap), plus
+   * [stats_cap * B][H][D] floats of mass scratch after its two halves.
+   * pending_gram and pending_cross (required with page_c, optional
+   * index-only) hold the statistic sums of the same run: gram [B, H, D, D]
+   * (feature mass) or square mass and mass [2, B, H, D] (structured), and
+   * cross [B, H, D, D]; with page_c the coarse read is the mixture over
+   * pages (tao_stream.py:301-305).
    * TAO_WRITER_VALUE (0): softmax descriptors (softmax and regularized). */
   int32_t fine_writer;   /* enum tao_fine_writer */
-  float* fine_mass;      /* fp32 [B, H, fine_cap, D]; feature writers only */
+  float* fine_mass;      /* fp32 [B, H, fine_cap, D] run totals; feature writers only */
 } tao_state_dev;
 
 enum tao_fine_writer {

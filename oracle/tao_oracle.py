@@ -238,8 +238,9 @@ FEATURE_WRITERS = ("feature_mass_association", "structured_gram_association")
 
 
 def mass_descriptor(mass):
-    """Descriptor of a feature mass: r(log mass) (tao_stream.py:60-65, 483)."""
-    return rnd(torch.log(mass.double()), torch.bfloat16)
+    """Descriptor of an fp32 feature mass: r(log mass), the fp32 log rounded
+    once more to bf16 (tao_stream.py:60-65, 280-283, 483)."""
+    return rnd(log32(mass.float()), torch.bfloat16)
 
 
 def feature_read(h, read_z, matrices):
@@ -444,10 +445,13 @@ class OracleStream:
         """_seal for the feature writers (tao_stream.py:56-65) and their
         pending sums and page descriptors (:463-499): z = r(log mass); C =
         association_matrix (feature mass) or structured_matrix (structured
-        Gram) of the block's statistics; the mass (and the gram / square
-        mass and cross) add up in seal order; a completed page's z is
-        r(log) of its summed mass and its matrix (non-index-only) comes from
-        the summed statistics, which then restart."""
+        Gram) of the block's statistics; the fp32 mass (and the gram /
+        square mass and cross) add up in seal order; a completed page's z is
+        r(log) of the summed mass. With page values the page's matrix comes
+        from the summed statistics, and the sums then restart; index-only,
+        they never restart (the reference clears them only in its page-value
+        branch, :488-497), so page z and the pending descriptor are r(log) of
+        the mass summed over every fine sealed so far."""
         from . import writers as W
         if self.writer == "structured_gram_association":
             square, cross, mass = W.structured_statistics(raw_k, v)
@@ -474,8 +478,8 @@ class OracleStream:
                 else:
                     pc = W.association_matrix(self.pending_gram, self.pending_cross)[1]
                 self.page_c.append(pc.to(raw_k.dtype))
-            self.pending_gram = self.pending_cross = None
-            self.pending_mass = self.pending_square = None
+                self.pending_gram = self.pending_cross = None
+                self.pending_mass = self.pending_square = None
 
     def logical_bytes(self, b, heads, d):
         """LayerState.logical_bytes (tao_stream.py:518-527), bf16."""
@@ -487,9 +491,11 @@ class OracleStream:
 
     def pending_writer_bytes(self):
         """LayerState.pending_writer_bytes (tao_stream.py:514-516): the
-        regularized writer's pending gram and cross sums, counted at the
-        reference's fp32 (4 bytes an element; the oracle holds them in fp64)."""
-        return sum(t.numel() * 4 for t in (self.pending_gram, self.pending_cross)
+        pending gram, cross, feature mass and square mass sums the writer
+        holds, counted at the reference's fp32 (4 bytes an element; the
+        oracle holds gram and cross in fp64)."""
+        return sum(t.numel() * 4 for t in (self.pending_gram, self.pending_cross,
+                                           self.pending_mass, self.pending_square)
                    if t is not None)
 
     def release_execution(self):
@@ -590,7 +596,7 @@ class OracleStream:
                           all_raw[:, -keep:].clone())
         else:
             self.local = (all_k, all_v, all_raw)
-        if self.writer == "regularized_association":
+        if self.writer != "softmax":
             # :969-978: the first pending sums of a new page count in the
             # peak; the pre-seal peak stays when a completed page drops them.
             after = self.logical_bytes(b, heads, d) + self.pending_writer_bytes()
@@ -658,6 +664,7 @@ class OracleStream:
             pages.append((pz.clone(), None if pc is None else pc.clone(),
                           torch.stack(z[index * group:(index + 1) * group], 2)))
         pending = [zz.clone() for zz in z[self.completed * group:]]
+        f32 = lambda t: None if t is None else t.to(torch.float32).clone()
         return {
             "layer_index": self.layer if layer_index is None else layer_index,
             "config": dict(config),
@@ -669,12 +676,10 @@ class OracleStream:
             "packed_fine_c": packed,
             "pages": pages,
             "pending_z": pending,
-            "pending_square_mass": None,
-            "pending_mass": None,
-            "pending_gram": (None if self.pending_gram is None
-                             else self.pending_gram.to(torch.float32).clone()),
-            "pending_cross": (None if self.pending_cross is None
-                              else self.pending_cross.to(torch.float32).clone()),
+            "pending_square_mass": f32(self.pending_square),
+            "pending_mass": f32(self.pending_mass),
+            "pending_gram": f32(self.pending_gram),
+            "pending_cross": f32(self.pending_cross),
             "route_ids": None if self.route_ids is None else tuple(t.clone() for t in self.route_ids),
             "route_key": None,
             "state_version": self.state_version,
@@ -689,7 +694,12 @@ class OracleStream:
                     writer=saved.get("config", {}).get("fine_writer", "softmax"))
         if saved.get("pending_gram") is not None:
             state.pending_gram = saved["pending_gram"].double().clone()
+        if saved.get("pending_cross") is not None:
             state.pending_cross = saved["pending_cross"].double().clone()
+        if saved.get("pending_square_mass") is not None:
+            state.pending_square = saved["pending_square_mass"].float().clone()
+        if saved.get("pending_mass") is not None:
+            state.pending_mass = saved["pending_mass"].float().clone()
         group = state.g.coarse_group
         state.position = saved["position"]
         state.local = (None if saved["local"] is None

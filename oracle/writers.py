@@ -20,7 +20,10 @@ Restates (paths relative to the reference repository root):
 Every routine works in float64 on the reference's rounding points (the bf16
 feature cast of u, the final bf16 cast of C and of the read output), so the
 HIP path is held to the reference within the fp32-vs-fp64 gap plus one bf16
-rounding of the result.
+rounding of the result. Two inputs of routing are exact instead: the feature
+simplex u and the feature masses are fp32 in an order this build fixes
+(feature_simplex, feature_mass), so fine and page descriptors r(log mass)
+are bit-reproducible.
 
 Pinning (tests/test_oracle.py): association_matrix against numpy's dense
 solve and the residual of the regularised normal equations; structured_matrix
@@ -36,6 +39,8 @@ single rows of C.
 import numpy as np
 import torch
 
+from .numerics import exp32, sequential_sum
+
 BF16 = torch.bfloat16
 
 
@@ -44,19 +49,39 @@ def _bf16(x):
 
 
 def feature_simplex(k):
-    """u = bf16(softmax_D(k.float())) (association_writer.py:14)."""
-    return _bf16(torch.softmax(k.double(), dim=-1))
+    """u = bf16(softmax_D(k.float())) (association_writer.py:14).
+
+    The fp32 softmax's internals are the backend's; this build fixes them
+    (the HIP statistics kernel computes the same): e = correctly rounded fp32
+    exp(k - max); s = the D channels in 8 contiguous groups, each summed in
+    channel order, then the 8 group sums pairwise,
+    ((g0+g1)+(g2+g3))+((g4+g5)+(g6+g7)); u = r(e / s). Returned as fp64
+    (exact: u is bf16)."""
+    x = k.float()
+    e = exp32(x - x.amax(-1, keepdim=True))
+    d = e.shape[-1]
+    groups = sequential_sum(e.reshape(*e.shape[:-1], 8, d // 8), -1)
+    while groups.shape[-1] > 1:
+        groups = groups[..., 0::2] + groups[..., 1::2]
+    return _bf16(e / groups)
+
+
+def feature_mass(u):
+    """sum_t u (association_writer.py:18, structured_writer.py:9) in fp32,
+    tokens in order (axis -2 of u [N, H, T, D]); the reference's fp32
+    reduction order is its backend's, this build fixes token order."""
+    return sequential_sum(u.float(), -2)
 
 
 def association_statistics(k, v, with_mass=False):
     """k, v: [N, T, H, D] -> gram [N, H, D, D], cross [N, H, D, D] (fp64),
-    optional mass [N, H, D] (association_writer.py:11-18)."""
+    optional mass [N, H, D] (fp32, feature_mass) (association_writer.py:11-18)."""
     u = feature_simplex(k).transpose(1, 2)            # [N, H, T, D]
     values = v.double().transpose(1, 2)
     gram = u.transpose(-1, -2) @ u
     cross = u.transpose(-1, -2) @ values
     if with_mass:
-        return gram, cross, u.sum(dim=-2)
+        return gram, cross, feature_mass(u)
     return gram, cross
 
 
@@ -96,10 +121,11 @@ def feature_read_coefficients(h, read_z):
 
 def structured_statistics(k, v):
     """k, v: [N, T, H, D] -> square_mass [N, H, D], cross [N, H, D, D],
-    mass [N, H, D] (structured_writer.py:5-13)."""
+    mass [N, H, D] (structured_writer.py:5-13). The square mass and the mass
+    are fp32 sums in token order (u * u is exact in fp32); cross is fp64."""
     u = feature_simplex(k).transpose(1, 2)
     values = v.double().transpose(1, 2)
-    return (u * u).sum(-2), u.transpose(-1, -2) @ values, u.sum(-2)
+    return feature_mass(u * u), u.transpose(-1, -2) @ values, feature_mass(u)
 
 
 def structured_matrix(square_mass, cross, mass, count):

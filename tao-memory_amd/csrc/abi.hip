@@ -51,11 +51,12 @@ int check_feature(const tao_state_dev* st) {
   }
   if (!st->fine_mass || !st->stats || st->stats_cap < 1)
     return fail(TAO_E_ARGUMENT, "a feature writer needs fine_mass and stats (stats_cap >= 1)");
-  if ((st->page_c != nullptr) != (st->pending_gram != nullptr && st->pending_cross != nullptr))
+  if ((st->pending_gram != nullptr) != (st->pending_cross != nullptr) ||
+      (st->page_c != nullptr && st->pending_gram == nullptr))
     return fail(TAO_E_ARGUMENT,
-                "a feature writer keeps pending sums exactly when it has page values: "
-                "pending_gram ([B, H, D, D], or [2, B, H, D] square mass and mass for the "
-                "structured writer) and pending_cross");
+                "a feature writer's pending sums are both set or both null, and set with page "
+                "values: pending_gram ([B, H, D, D], or [2, B, H, D] square mass and mass for "
+                "the structured writer) and pending_cross");
   return TAO_OK;
 }
 
@@ -247,10 +248,15 @@ hipError_t assoc_seal(const tao_state_dev* st, const tao::TokView& rk, const tao
 // block statistics with the feature mass, C^T into the bank slots
 // (association_matrix for the feature-mass writer, structured_matrix over
 // the block's 256 tokens for the structured one), z = r(log mass) and the
-// fp32 mass for the page descriptors (tao_stream.py:56-65).
+// run's fp32 mass total for the page descriptors (tao_stream.py:56-65,
+// 463-499). page_runs: the mass run (and the statistic sums) restart at each
+// page, as with page values and in the full-sequence path; otherwise (the
+// streaming index-only state) they sum from the first seal on, as the
+// reference's pending_mass / pending_gram / pending_cross /
+// pending_square_mass do when no page values are built.
 hipError_t feature_seal(const tao_state_dev* st, const tao::TokView& rk, const tao::TokView& v,
                         int64_t new_base, const int64_t* starts, int first_slot, int count,
-                        hipStream_t s) {
+                        bool page_runs, hipStream_t s) {
   const int B = st->batch, H = st->heads, D = st->head_dim;
   const bool structured = st->fine_writer == TAO_WRITER_STRUCTURED;
   const size_t mats = (size_t)st->stats_cap * B * H;
@@ -317,20 +323,24 @@ hipError_t feature_seal(const tao_state_dev* st, const tao::TokView& rk, const t
     dp.H = H;
     dp.cap = st->fine_cap;
     dp.first_slot = first_slot + done;
+    dp.group = st->coarse_group;
+    dp.page_runs = page_runs ? 1 : 0;
     e = tao::launch_feature_descriptors(dp, D, s);
     if (e != hipSuccess) return e;
-    // (After the descriptors, which read each block's own mass.) With page values: the statistics' sums in seal order (restarting at
-    // each page); a block that completes a page then holds its page's sums,
-    // and the page matrix is the writer's matrix of them (tao_stream.py:
-    // 463-499; structured: over fine_tokens * group tokens).
-    if (st->page_c) {
+    // (After the descriptors, which read each block's own mass.) The
+    // statistics' sums in seal order (tao_stream.py:463-478), restarting at
+    // each page with page values; a block that completes a page then holds
+    // its page's sums, and the page matrix is the writer's matrix of them
+    // (:479-499; structured: over fine_tokens * group tokens). Index-only
+    // states that carry the sums keep them running for their snapshots.
+    if (st->pending_gram) {
       tao::AssocPendingParams pp{};
       pp.B = B;
       pp.H = H;
       pp.count = n;
       pp.first_slot = first_slot + done;
       pp.group = st->coarse_group;
-      pp.reset_pages = 1;
+      pp.reset_pages = page_runs ? 1 : 0;
       if (structured) {
         pp.gram = first;                       // square mass [.., D]
         pp.cross = mass;                       // mass [.., D]
@@ -344,7 +354,7 @@ hipError_t feature_seal(const tao_state_dev* st, const tao::TokView& rk, const t
           pp.pending_cross = nullptr;
           e = tao::launch_pending_sums(pp, D * D, s);
         }
-        if (e == hipSuccess) {
+        if (e == hipSuccess && st->page_c) {
           tao::StructuredParams tp{};
           tp.square = first;
           tp.cross = cross;
@@ -366,7 +376,7 @@ hipError_t feature_seal(const tao_state_dev* st, const tao::TokView& rk, const t
         pp.pending_gram = st->pending_gram;
         pp.pending_cross = st->pending_cross;
         e = tao::launch_assoc_pending(pp, D, s);
-        if (e == hipSuccess) {
+        if (e == hipSuccess && st->page_c) {
           tao::AssocSolveParams pg{};
           pg.gram = first;
           pg.cross = cross;
@@ -736,7 +746,7 @@ int tao_write_fine(const tao_state_dev* st, const tao_tokens* tok, int64_t new_b
   p.z_only = assoc_writer(st) ? 1 : 0;
   if (feature_writer(st))
     return check_hip(feature_seal(st, p.rk, p.v, new_base, start_pos, first_slot, count,
-                                  (hipStream_t)stream),
+                                  st->page_c != nullptr, (hipStream_t)stream),
                      "tao_write_fine");
   hipError_t e = tao::launch_writer(p, st->head_dim, (hipStream_t)stream);
   if (e == hipSuccess && assoc_writer(st) && count > 0)
@@ -970,7 +980,8 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
   wp.z_only = external_values || assoc_writer(st);
   if (feature_writer(st)) {
     if (external_values) return fail(TAO_E_ARGUMENT, "external values with a feature writer");
-    e = feature_seal(st, wp.rk, wp.v, pos0, wp.starts, (int)first_slot, (int)n_write, s);
+    e = feature_seal(st, wp.rk, wp.v, pos0, wp.starts, (int)first_slot, (int)n_write,
+                     st->page_c != nullptr || query_routes, s);
   } else {
     e = tao::launch_writer(wp, D, s);
   }

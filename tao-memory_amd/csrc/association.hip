@@ -110,9 +110,14 @@ __global__ __launch_bounds__(kStatThreads) void writer_stats_kernel(WriterStatsP
       for (int j = 0; j < CPL; ++j) mx = fmaxf(mx, x[j]);
 #pragma unroll
       for (int off = 1; off < LPT; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      // u = r(e / s): e = correctly rounded fp32 exp(k - max); s = each
+      // lane's CPL channels summed in channel order, then the 8 lanes'
+      // partial sums pairwise (xor 1, 2, 4). Both orders are fixed so the
+      // feature mass, and with it the descriptors that feed routing, are
+      // bit-reproducible.
       float s = 0.0f;
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) { x[j] = __expf(x[j] - mx); s += x[j]; }
+      for (int j = 0; j < CPL; ++j) { x[j] = exp_cr(x[j] - mx); s += x[j]; }
 #pragma unroll
       for (int off = 1; off < LPT; off <<= 1) s += __shfl_xor(s, off, 64);
 #pragma unroll
@@ -397,19 +402,31 @@ __global__ __launch_bounds__(D) void structured_matrix_kernel(StructuredParams p
   }
 }
 
-// One thread per (seal block, batch, head, channel): z = r(log mass), and the
-// fp32 mass kept for the page descriptors.
+// One thread per (batch, head, channel), the seal blocks in seal order: the
+// fine's z = r(log mass) from its own mass, and fine_mass[slot] = the run's
+// fp32 total through this fine, run + mass (tao_stream.py:463-467). A run
+// starts at fine 0 and, with page_runs, at every page's first fine; so
+// r(log fine_mass[last fine]) is the page (or pending) descriptor
+// (tao_stream.py:280-283, 483). The streaming index-only state never
+// restarts its run, as the reference clears pending_mass only when it
+// builds page values (:488-497); the full-sequence path sums per page
+// (:543-549).
 template <int D>
 __global__ __launch_bounds__(256) void feature_desc_kernel(FeatureDescParams p) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)p.count * p.B * p.H * D) return;
+  if (i >= (int64_t)p.B * p.H * D) return;
   const int d = (int)(i % D);
-  const int64_t mat = i / D;
-  const int blk = (int)(mat / (p.B * p.H)), b = (int)(mat / p.H % p.B), h = (int)(mat % p.H);
-  const float m = p.mass[i];
-  const size_t dst = (((size_t)b * p.H + h) * p.cap + p.first_slot + blk) * D + d;
-  p.fine_z[dst] = f2bf(log_bf(m));
-  p.fine_mass[dst] = m;
+  const int64_t bh = i / D;
+  const size_t row = (size_t)bh * p.cap * D + d;
+  float run = p.first_slot > 0 ? p.fine_mass[row + (size_t)(p.first_slot - 1) * D] : 0.0f;
+  for (int blk = 0; blk < p.count; ++blk) {
+    const int slot = p.first_slot + blk;
+    const float m = p.mass[((size_t)blk * p.B * p.H + bh) * D + d];
+    const bool fresh = p.page_runs ? slot % p.group == 0 : slot == 0;
+    run = fresh ? m : run + m;
+    p.fine_z[row + (size_t)slot * D] = f2bf(log_bf(m));
+    p.fine_mass[row + (size_t)slot * D] = run;
+  }
 }
 
 __global__ __launch_bounds__(256) void chrono_sum_kernel(const float* x, float* out, int64_t outer,
@@ -534,7 +551,7 @@ hipError_t launch_structured_matrix(const StructuredParams& p, int head_dim, hip
 
 hipError_t launch_feature_descriptors(const FeatureDescParams& p, int head_dim, hipStream_t s) {
   if (p.count <= 0) return hipSuccess;
-  const int64_t n = (int64_t)p.count * p.B * p.H * head_dim;
+  const int64_t n = (int64_t)p.B * p.H * head_dim;
   const dim3 grid((unsigned)((n + 255) / 256));
   if (head_dim == 128)
     hipLaunchKernelGGL(feature_desc_kernel<128>, grid, dim3(256), 0, s, p);

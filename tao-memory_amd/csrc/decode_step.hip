@@ -540,7 +540,13 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, i
   const int bh = decode_units<D, FDT>(p, M, c);
   float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
   unsigned* head_count = p.counters + (size_t)bh * kCounterStride;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // this thread's stores done
+  // Release of the records at agent scope without an L2 write-back: every
+  // record was stored with an agent-scope (write-through) store, so once
+  // each thread's stores are acknowledged (vmcnt 0) an agent-scope load on
+  // any XCD returns them. A workgroup-scope fence does not wait for them
+  // (gfx950 lowers it to an LDS wait), so every wave waits here, before the
+  // barrier that orders its stores before thread 0's arrival count.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0)
     last = __hip_atomic_fetch_add(head_count, 1u, __ATOMIC_RELAXED,

@@ -74,12 +74,12 @@ TAO_DEV float log_bf(float x) {
   return rbf(y);
 }
 
-// A feature-mass page descriptor (tao_stream.py:280-283, 483): r(log) of
-// the fp32 sum, in seal order, of the first n masses at stride `stride`.
+// A feature-mass page descriptor (tao_stream.py:280-283, 483) of the n
+// fines from `mass` (a page's first fine) at stride `stride`: r(log) of the
+// fp32 mass total that fine_mass holds at the n-th of them (the run's sum in
+// seal order through it).
 TAO_DEV float mass_page_z(const float* mass, int n, size_t stride) {
-  float s = mass[0];
-  for (int i = 1; i < n; ++i) s += mass[i * stride];
-  return log_bf(s);
+  return log_bf(mass[(size_t)(n - 1) * stride]);
 }
 
 // Correctly rounded fp32 exp (fp64 evaluation).
@@ -166,9 +166,11 @@ TAO_DEV float wave_fold_max(float v) {
 }
 
 // Device-coherent (agent-scope) relaxed accesses: once a store made this way
-// has completed (s_waitcnt), an agent-scope load on any XCD returns it. The
-// single-launch decode step publishes its per-workgroup records with them,
-// so no L2 write-back fence is needed between its workgroups.
+// has been acknowledged (the storing wave's `s_waitcnt vmcnt(0)`, which the
+// caller issues explicitly: a relaxed atomic carries no wait of its own), an
+// agent-scope load on any XCD returns it. The single-launch decode step
+// publishes its per-workgroup records with them, so no L2 write-back fence is
+// needed between its workgroups.
 TAO_DEV void st_agent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

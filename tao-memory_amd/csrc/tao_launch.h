@@ -255,8 +255,9 @@ struct WriterParams {
 };
 hipError_t launch_writer(const WriterParams& p, int head_dim, hipStream_t s);
 
-// fine_mass (feature writers): a page's z is r(log) of its fines' fp32
-// masses summed in seal order instead of r(logsumexp) of their z.
+// fine_mass (feature writers): a page's z is r(log) of its run's fp32 mass
+// total at the page's last fine (see FeatureDescParams) instead of
+// r(logsumexp) of its fines' z.
 struct EpilogueParams {
   const bf16_t* fine_z; bf16_t* fine_sw; bf16_t* page_z; bf16_t* page_w;
   const float* fine_mass;
@@ -480,11 +481,13 @@ hipError_t launch_structured_matrix(const StructuredParams& p, int head_dim, hip
 
 // Feature-writer descriptors of `count` seals: matrix (blk, b, h) of the
 // mass scratch [count * B][H][D] gives fine slot first_slot + blk its
-// z = r(log mass) and its fp32 mass (tao_stream.py:60-65).
+// z = r(log mass) (tao_stream.py:60-65) and fine_mass[slot] its run's fp32
+// mass total through it, in seal order. A run restarts at fine 0 and, with
+// page_runs, at each page's first fine (slot % group == 0).
 struct FeatureDescParams {
   const float* mass;
   bf16_t* fine_z; float* fine_mass;
-  int count, B, H, cap, first_slot;
+  int count, B, H, cap, first_slot, group, page_runs;
 };
 hipError_t launch_feature_descriptors(const FeatureDescParams& p, int head_dim, hipStream_t s);
 

@@ -62,14 +62,34 @@ def _history_bytes(completed, pending, B, H, D, config):
     return elements * B * H * 2
 
 
-def _pending_writer_bytes(fines, B, H, D, config):
-    """LayerState.pending_writer_bytes (tao_stream.py:514-516) of the
-    regularized writer after `fines` seals: the fp32 gram and cross sums,
-    present from the first seal until a completed page drops them (never
-    dropped in the index-only preset, tao_stream.py:486-497)."""
+def pending_writer_parts(B, H, D, config):
+    """Bytes of each fp32 pending sum config's writer holds
+    (tao_stream.py:463-478): gram and cross [B, H, D, D] (regularized and
+    feature-mass writers), cross, mass and square mass (structured), mass
+    (feature writers); none for the softmax writer."""
+    dd, d = B * H * D * D * 4, B * H * D * 4
+    writer = config.fine_writer
+    return {"gram": dd if writer in ("regularized_association",
+                                     "feature_mass_association") else 0,
+            "cross": dd if writer != "softmax" else 0,
+            "mass": d if writer in ("feature_mass_association",
+                                    "structured_gram_association") else 0,
+            "square": d if writer == "structured_gram_association" else 0}
+
+
+def pending_present(fines, config):
+    """Whether the pending sums exist after `fines` seals: from the first
+    seal until a completed page drops them, which only the page-value branch
+    does (never in the index-only preset, tao_stream.py:486-497)."""
     fines = np.asarray(fines, dtype=np.int64)
-    present = (fines > 0) & ((fines % config.coarse_group > 0) | config.coarse_index_only)
-    return np.where(present, 2 * B * H * D * D * 4, 0)
+    return (fines > 0) & ((fines % config.coarse_group > 0) | config.coarse_index_only)
+
+
+def _pending_writer_bytes(fines, B, H, D, config):
+    """LayerState.pending_writer_bytes (tao_stream.py:514-516) after `fines`
+    seals."""
+    total = sum(pending_writer_parts(B, H, D, config).values())
+    return np.where(pending_present(fines, config), total, 0)
 
 
 def _segment(c, positions, widths, single, route_size, layer, B, H, D, config):
@@ -133,8 +153,8 @@ def _segment(c, positions, widths, single, route_size, layer, B, H, D, config):
     hist = _history_bytes(completed, pending, B, H, D, config)
     key = B * all_k * H * D * 2
     logical, physical = hist + 2 * key, hist + 3 * key
-    if config.fine_writer == "regularized_association":
-        # The pending gram and cross sums (tao_stream.py:953-958, 969-978):
+    if config.fine_writer != "softmax":
+        # The pending statistic sums (tao_stream.py:953-958, 969-978):
         # counted before the chunk and, at a seal, after it (the first sums
         # of a new page; the pre-seal peak stays when a page drops them).
         logical = logical + _pending_writer_bytes(f, B, H, D, config)

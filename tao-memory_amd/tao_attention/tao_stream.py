@@ -93,16 +93,19 @@ class _DeviceState:
         # sums (the reference's pending_gram / pending_cross) and scratch for
         # the statistics of up to _STATS_CAP blocks per pass; fixed size.
         self.association = config.fine_writer == "regularized_association"
-        # Feature writers: each sealed fine's fp32 feature mass (page
-        # descriptors sum them) and statistics scratch with a mass region;
-        # with page values, the pending page's statistic sums (the
-        # reference's pending gram / square mass, mass and cross).
+        # Feature writers: per sealed fine, the fp32 feature-mass total of
+        # its run through it (the reference's pending_mass after that seal;
+        # r(log) of it at a page's last fine is the page descriptor),
+        # statistics scratch with a mass region, and the run's statistic
+        # sums (the reference's pending gram / square mass and cross). A run
+        # restarts at each page with page values and never index-only
+        # (tao_stream.py:463-499).
         self.feature = _FEATURE_WRITERS.get(config.fine_writer, 0)
         self.fine_mass = None
         pending = None
         if self.association:
             pending = (dd, dd)
-        elif self.feature and self.coarse_values:
+        elif self.feature:
             pending = (dd if self.feature == 1 else (2, batch, heads, head_dim), dd)
         # The ring, header, fold (G^T and den weights), coarse fold and
         # pending sums: fixed size, they survive capacity growth.
@@ -206,9 +209,8 @@ class _DeviceState:
         if self.feature:
             st.fine_writer, st.fine_mass = self.feature, self.fine_mass.data_ptr()
             st.stats, st.stats_cap = self.stats.data_ptr(), _STATS_CAP
-            if self.coarse_values:
-                st.pending_gram = self.pending_gram.data_ptr()
-                st.pending_cross = self.pending_cross.data_ptr()
+            st.pending_gram = self.pending_gram.data_ptr()
+            st.pending_cross = self.pending_cross.data_ptr()
         st.workspace = self.workspace.data_ptr()
         st.workspace_bytes = self.workspace.numel()
         return st
@@ -955,19 +957,18 @@ class StreamCache:
         # The regularized writer's pending statistics (fp32 [B, H, D, D]):
         # None until the first seal and, with page values, after each page
         # completion, as the reference keeps them (tao_stream.py:463-499).
-        pending_gram = pending_cross = None
-        if dev is not None and dev.association and fines and (pending or not dev.coarse_values):
+        pending_gram = pending_cross = pending_mass = pending_square = None
+        held = (dev is not None and fines and (pending or not dev.coarse_values))
+        if held and (dev.association or dev.feature == 1):
             pending_gram = dev.pending_gram.clone()
+        if held and (dev.association or dev.feature):
             pending_cross = dev.pending_cross.clone()
-        # Feature writers: the pending page's summed mass, in seal order (the
-        # reference's pending_mass). Their gram / square-mass and cross sums
-        # feed only the coarse value read, which this path does not build.
-        pending_mass = None
-        if dev is not None and dev.feature and pending:
-            base = completed * group
-            pending_mass = dev.fine_mass[:, :, base].clone()
-            for j in range(1, pending):
-                pending_mass = pending_mass + dev.fine_mass[:, :, base + j]
+        # Feature writers: the run's summed mass, in seal order (the
+        # reference's pending_mass), and the structured writer's square mass.
+        if held and dev.feature:
+            pending_mass = dev.fine_mass[:, :, fines - 1].clone()
+        if held and dev.feature == 2:
+            pending_square = dev.pending_gram[0].clone()
         return {
             "layer_index": self.layer_index,
             "config": cfg.export(),
@@ -979,7 +980,7 @@ class StreamCache:
             "packed_fine_c": packed,
             "pages": pages,
             "pending_z": pending_z,
-            "pending_square_mass": None,
+            "pending_square_mass": pending_square,
             "pending_mass": pending_mass,
             "pending_gram": pending_gram,
             "pending_cross": pending_cross,
@@ -999,11 +1000,6 @@ class StreamCache:
         whose tensors are on the host is restored onto the current device.
         """
         config = TaoConfig(**saved["config"])
-        if config.fine_writer in _FEATURE_WRITERS and saved["pending_z"]:
-            # The page descriptors need each pending fine's mass; the schema
-            # keeps only their sum (pending_mass).
-            raise NotImplementedError(
-                "restoring a feature-writer snapshot with pending fines is not built")
         state = cls(saved["layer_index"], saved["route_interval"], saved["fusion_mode"],
                     fused_fine=saved["fused_fine"], config=config)
         position = saved["position"]
@@ -1017,7 +1013,8 @@ class StreamCache:
             packed = move(packed)
             pages = [(move(pz), move(pc), move(fz)) for pz, pc, fz in pages]
             pending_z = [move(z) for z in pending_z]
-        pending_stats = (saved.get("pending_gram"), saved.get("pending_cross"))
+        pending_stats = (saved.get("pending_gram"), saved.get("pending_cross"),
+                         saved.get("pending_mass"), saved.get("pending_square_mass"))
         fines = len(pages) * config.coarse_group + len(pending_z)
         if fines != schedule.fines_at(position, config):
             raise ValueError("snapshot fine count does not match its position")
@@ -1036,8 +1033,31 @@ class StreamCache:
         slots = torch.arange(position - n, position, device=dev.device) % dev.L
         for buf, src in zip((dev.ring_k, dev.ring_v, dev.ring_raw), local):
             buf.index_copy_(1, slots, src.to(torch.bfloat16))
+        if dev.feature:
+            # The run's sums (tao_stream.py:463-499): present from the first
+            # seal and, with page values, while the pending page has fines.
+            gram, cross, mass, square = pending_stats
+            first = square if dev.feature == 2 else gram
+            held = fines and (not dev.coarse_values or fines % group)
+            if held and (first is None or cross is None or mass is None):
+                raise ValueError("feature-writer snapshot lacks its pending sums")
+            if held:
+                # fine_mass holds the run's total at its last fine: the page
+                # (and pending) descriptors of later seals continue from it.
+                f32 = lambda t: t.to(dev.device, torch.float32)
+                dev.fine_mass[:, :, fines - 1].copy_(f32(mass))
+                if dev.feature == 2:
+                    dev.pending_gram[0].copy_(f32(square))
+                    dev.pending_gram[1].copy_(f32(mass))
+                else:
+                    dev.pending_gram.copy_(f32(gram))
+                dev.pending_cross.copy_(f32(cross))
+            if dev.coarse_values and any(pc is None for _, pc, _ in pages):
+                raise NotImplementedError(
+                    "page value matrices of a feature writer cannot be rebuilt from a "
+                    "snapshot without them (its page statistics are not part of the schema)")
         if dev.association:
-            gram, cross = pending_stats
+            gram, cross = pending_stats[:2]
             if (gram is None) != (cross is None):
                 raise ValueError("snapshot has only one of pending_gram / pending_cross")
             if gram is None and fines and (not dev.coarse_values or fines % group):
@@ -1119,14 +1139,15 @@ class StreamCache:
         route_bytes = (8 * batch * heads * (self.route_coarse + self.route_size)
                        if self.route_size else 0)
         logical_local = local_tokens * 2 * heads * width * 2 * batch
-        # The regularized writer's pending sums (fp32 [B, H, D, D] gram and
-        # cross), counted while the reference holds them (tao_stream.py:463-499,
-        # 514-516; the rule export follows).
-        pending_writer = 0
-        if dev is not None and dev.association:
-            pending_writer = int(diagnostics._pending_writer_bytes(fines, batch, heads, width,
-                                                                   cfg))
-        pending_cross = pending_writer // 2
+        # The writer's pending sums (fp32 gram, cross, feature mass and
+        # square mass), counted while the reference holds them
+        # (tao_stream.py:463-499, 514-516; the rule export follows).
+        parts = diagnostics.pending_writer_parts(batch, heads, width, cfg)
+        held = bool(diagnostics.pending_present(fines, cfg))
+        pending_writer = sum(parts.values()) if held else 0
+        pending_cross = parts["cross"] if held else 0
+        pending_square = parts["square"] if held else 0
+        pending_mass = parts["mass"] if held else 0
         physical_local = 0
         unique = 0
         if dev is not None:
@@ -1142,10 +1163,10 @@ class StreamCache:
         return {"history_bytes": history,
                 "page_normalization_memo_bytes": memo,
                 "pending_writer_bytes": pending_writer,
-                "pending_gram_cross_bytes": pending_writer,
+                "pending_gram_cross_bytes": pending_writer - pending_mass - pending_square,
                 "pending_cross_bytes": pending_cross,
-                "pending_square_mass_bytes": 0,
-                "pending_feature_mass_bytes": 0,
+                "pending_square_mass_bytes": pending_square,
+                "pending_feature_mass_bytes": pending_mass,
                 "fused_fine": self.fused_fine,
                 "fused_fine_calls": c.fused_fine_calls if self.fused_fine else 0,
                 "fusion_mode": self.fusion_mode,

@@ -278,61 +278,113 @@ def test_stream_regularized_writer(device, index_only, width, batch):
     assert torch.equal(nxt[0], nxt[1])
 
 
-@pytest.mark.parametrize("writer,width,index_only", [
-    ("feature_mass_association", 64, True), ("feature_mass_association", 128, True),
-    ("structured_gram_association", 128, True), ("feature_mass_association", 128, False),
-    ("structured_gram_association", 64, False)])
-def test_stream_feature_writers(device, writer, width, index_only):
-    """Streaming prefill and decode with the feature writers (index-only):
-    z = r(log mass), page descriptors from summed masses (the step at 2559
-    seals the 8th fine and completes page 0), route ids bit-exact, the fine
-    matrices and outputs within the bf16 tolerance of the oracle, the
-    descriptors within one bf16 rounding of it (the GPU sums the masses in
-    fp32, the oracle in fp64), and the exported pending mass."""
+@pytest.mark.parametrize("writer,width,index_only,long", [
+    ("feature_mass_association", 64, True, True), ("feature_mass_association", 128, True, True),
+    ("structured_gram_association", 128, True, True),
+    ("structured_gram_association", 64, True, False),
+    ("feature_mass_association", 128, False, False),
+    ("structured_gram_association", 64, False, True)])
+def test_stream_feature_writers(device, writer, width, index_only, long):
+    """Streaming prefill and decode with the feature writers: z = r(log mass),
+    page and pending descriptors r(log) of the run's summed mass (index-only
+    the run never restarts, tao_stream.py:488-497; with page values it
+    restarts at each page), decode through route refreshes (the step at 2559
+    seals the 8th fine and completes page 0; the long cases go on to two
+    completed pages and two pending fines at 5125 and decode through three
+    more refreshes). Bit-exact against the oracle: every route after every
+    call, the fine, page and pending descriptors, and the exported pending
+    mass (the feature simplex and the fp32 mass sums follow the oracle's
+    fixed orders). Within the bf16 tolerance: the fine and page matrices and
+    the outputs. Export -> import (this build's snapshot and the oracle's,
+    in the reference schema) continues identically."""
     from oracle import tao_oracle as O
-    from tao_attention import TaoConfig, new_state, tao_attention_decode, tao_attention_prefill
+    from tao_attention import (StreamCache, TaoConfig, new_state, tao_attention_decode,
+                               tao_attention_prefill)
     heads, batch = 2, 1
-    tokens = 2826 if index_only else 3128
+    # without index_only the tokens after 2816 read page 0's matrix (the
+    # mixture over completed pages)
+    splits = [2540] + [1] * 30 + [250] + [1] * 5
+    if long:
+        splits += [2000, 300] + [1] * 75
+    elif not index_only:
+        splits += [300, 1, 1]
+    tokens = sum(splits) + 4
     g = torch.Generator().manual_seed(83 + width)
     xs = [torch.randn(batch, tokens, heads, width, generator=g).to(BF16) for _ in range(5)]
     fa = torch.randn(heads, width, 3, generator=g) * 0.02
     fb = torch.randn(heads, width, 3, generator=g) * 0.02
     cfg = TaoConfig(fine_writer=writer, coarse_index_only=index_only)
     geo = O.Geometry.from_config(cfg)
-    # without index_only the tokens after 2816 read page 0's matrix (the
-    # mixture over completed pages)
-    splits = [2540] + [1] * 30 + [250] + [1] * 5 + ([] if index_only else [300, 1, 1])
     d = [x.to(device) for x in xs]
     state = new_state(0, cfg)
     ora = O.OracleStream(0, geo, writer=writer)
+
+    def step(st, sl):
+        fn = tao_attention_decode if sl.stop - sl.start == 1 else tao_attention_prefill
+        return fn(*(x[:, sl] for x in d[:3]), raw_q=d[3][:, sl], raw_k=d[4][:, sl],
+                  fusion_a=fa.to(device), fusion_b=fb.to(device), alpha=0.5,
+                  state=st, position=st.get_pos())
+
     outs, refs, start = [], [], 0
     for w in splits:
         sl = slice(start, start + w)
         print(f"{writer} D{width}: tokens [{start}, {start + w})", flush=True)
-        fn = tao_attention_decode if w == 1 else tao_attention_prefill
-        out, state = fn(*(x[:, sl] for x in d[:3]), raw_q=d[3][:, sl], raw_k=d[4][:, sl],
-                        fusion_a=fa.to(device), fusion_b=fb.to(device), alpha=0.5,
-                        state=state, position=state.get_pos())
+        out, state = step(state, sl)
         outs.append(out.cpu())
         refs.append(ora.prefill(*(x[:, sl] for x in xs), fa, fb, 0.5))
         start += w
+        if ora.route_ids is not None:
+            snap = state.export()
+            assert torch.equal(snap["route_ids"][1].cpu(), ora.route_ids[1]), start
+            assert torch.equal(snap["route_ids"][0].cpu(), ora.route_ids[0]), start
     torch.testing.assert_close(torch.cat(outs, 1).float(), torch.cat(refs, 1).float(),
                                atol=2e-2, rtol=2e-2)
     snap = state.export()
-    assert len(snap["pending_z"]) == (1 if index_only else 2) and len(snap["pages"]) == 1
-    assert torch.equal(snap["route_ids"][1].cpu(), ora.route_ids[1])
-    if not index_only:
-        pc = snap["pages"][0][1]
-        torch.testing.assert_close(pc.cpu().float(), ora.page_c[0].float(), atol=2e-2, rtol=2e-2)
+    fines = len(ora.fine_z)
+    completed, pending = divmod(fines, 8)
+    assert len(snap["pending_z"]) == pending and len(snap["pages"]) == completed
+    assert completed == (2 if long else 1) and pending >= 1
+    for i in range(completed):
+        pz, pc, fz = snap["pages"][i]
+        assert torch.equal(pz.cpu(), ora.page_z[i]), f"page {i} descriptor"
+        assert torch.equal(fz.cpu(), torch.stack(ora.fine_z[8 * i:8 * i + 8], 2))
+        assert (pc is None) == index_only
+        if pc is not None:
+            torch.testing.assert_close(pc.cpu().float(), ora.page_c[i].float(),
+                                       atol=2e-2, rtol=2e-2)
+    for j, z in enumerate(snap["pending_z"]):
+        assert torch.equal(z.cpu(), ora.fine_z[8 * completed + j])
+    assert torch.equal(state._dev.page_z[:, :, completed].cpu(),
+                       ora.page_descriptors()[:, :, completed]), "pending descriptor"
+    assert torch.equal(snap["pending_mass"].cpu(), ora.pending_mass)
+    osnap = ora.export(config=cfg.export())
+    for key in ("pending_gram", "pending_cross", "pending_square_mass"):
+        got, want = snap[key], osnap[key]
+        assert (got is None) == (want is None), key
+        if got is not None:
+            assert got.dtype == torch.float32
+            close(got, want, 1e-3)
     packed = snap["packed_fine_c"].cpu().float()
     want = torch.stack(ora.fine_c, 2).float()
     torch.testing.assert_close(packed, want, atol=2e-2, rtol=2e-2)
-    zs = [snap["pages"][0][0], snap["pages"][0][2], snap["pending_z"][0]]
-    wants = [ora.page_z[0], torch.stack(ora.fine_z[:8], 2), ora.fine_z[8]]
-    for got, ref in zip(zs, wants):
-        got, ref = got.cpu().double(), ref.double()
-        assert ((got - ref).abs() <= 2 ** -7 * ref.abs() + 1e-6).all()
-    close(snap["pending_mass"], ora.pending_mass, 1e-4)   # fp32 sums of 256 features
+    diag = state.bytes()
+    assert diag["pending_writer_bytes"] == ora.pending_writer_bytes()
+    assert diag["pending_feature_mass_bytes"] == batch * heads * width * 4
+    assert diag["pending_square_mass_bytes"] == (
+        batch * heads * width * 4 if writer == "structured_gram_association" else 0)
+    # export -> import, of this build's snapshot and of the oracle's
+    restored = StreamCache.from_export(snap)
+    imported = StreamCache.from_export(osnap)
+    tail = slice(start, start + 4)
+    want = ora.prefill(*(x[:, tail] for x in xs), fa, fb, 0.5)
+    got = []
+    for st in (state, restored, imported):
+        o, st = step(st, slice(start, start + 3))
+        o2, st = step(st, slice(start + 3, start + 4))
+        got.append(torch.cat((o, o2), 1))
+        assert torch.equal(st.export()["route_ids"][1].cpu(), ora.route_ids[1])
+    assert torch.equal(got[0], got[1])
+    torch.testing.assert_close(got[2].cpu().float(), want.float(), atol=2e-2, rtol=2e-2)
 
 
 @pytest.mark.parametrize("writer,width,tokens,batch,index_only", [

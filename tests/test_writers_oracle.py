@@ -38,7 +38,42 @@ def test_association_statistics_invariants(d):
     assert torch.allclose(cross.sum(-2), want, rtol=1e-10, atol=1e-10)
     square, cross2, mass2 = W.structured_statistics(k, v)
     assert torch.equal(cross2, cross) and torch.equal(mass2, mass)
-    assert torch.allclose(square, gram.diagonal(dim1=-2, dim2=-1))
+    assert mass.dtype == square.dtype == torch.float32
+    assert torch.allclose(square.double(), gram.diagonal(dim1=-2, dim2=-1), rtol=256 * 2 ** -24)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_feature_simplex_and_mass_orders(d):
+    """The fp32 orders this build fixes for u and the feature mass, against
+    what the reference's arithmetic admits: u within one bf16 ulp of the
+    fp64 softmax rounded once (equal almost everywhere: only values whose
+    fp32 evaluation lands across a rounding boundary differ); the mass is
+    the fp32 left-to-right token sum (numpy's float32 cumsum, an
+    independent sequential sum, equals it bit for bit) and lies within
+    256 fp32 roundings of the exact sum."""
+    import numpy as np
+    k, v = kv(2, 256, 3, d, 9)
+    u = W.feature_simplex(k)
+    exact = torch.softmax(k.double(), -1)
+    ref = exact.to(BF16).double()
+    ulp = 2.0 ** (torch.floor(torch.log2(exact)) - 7)
+    assert ((u - ref).abs() <= ulp).all()
+    assert (u != ref).double().mean() < 1e-3
+    if d == 128:
+        # the group/pair order matters: a plain left-to-right sum over all D
+        # channels gives a different u on some rows
+        x = k.float()
+        e = torch.exp(x.double() - x.amax(-1, keepdim=True).double()).float()
+        flat = torch.zeros(e.shape[:-1])
+        for j in range(d):
+            flat = flat + e[..., j]
+        assert not torch.equal((e / flat.unsqueeze(-1)).to(BF16).double(), u)
+    mass = W.association_statistics(k, v, with_mass=True)[2]       # [N, H, D]
+    ut = u.float().transpose(1, 2).numpy()                         # [N, H, T, D]
+    seq = np.cumsum(ut, axis=2, dtype=np.float32)[:, :, -1]
+    assert np.array_equal(mass.numpy(), seq)
+    exact_mass = u.transpose(1, 2).sum(-2)
+    assert ((mass.double() - exact_mass).abs() <= 256 * 2 ** -24 * exact_mass).all()
 
 
 @pytest.mark.parametrize("d", [8, 64])
@@ -225,57 +260,96 @@ def test_regularized_writer_peak_counts_pending_sums(index_only):
 @pytest.mark.parametrize("writer", ["feature_mass_association", "structured_gram_association"])
 def test_oracle_stream_feature_writers(writer):
     """OracleStream with a feature writer (tao_stream.py:56-65, 280-305,
-    362-367, 463-499), pinned by checks that do not restate it:
-    - a fine's z is within half a bf16 ulp of the log of the block's mass,
-      which sums to the block length over the channels;
-    - a completed page's z is the log of its eight fines' summed mass: it
-      matches logsumexp of their z (fp64) within the fines' bf16 rounding,
-      which catches a mean, a max or a missing fine, and equals r(log) of
-      the mass of the page's 2048 tokens taken at once;
-    - the page matrix (non-index-only) is the writer's matrix of the 2048
-      tokens' statistics taken at once;
+    362-367, 463-499) over 17 fines (two completed pages and a pending
+    fine), pinned by checks that do not restate it:
+    - a fine's z is within half a bf16 ulp of the log of the block's exact
+      (fp64) mass, which sums to the block length over the channels;
+    - the mass runs: index-only the reference never clears pending_mass
+      (:488-497), so page p's z and the pending descriptor are the log of
+      the mass of every fine so far; with page values each page's run
+      restarts. Each descriptor is within one bf16 ulp of the log of the
+      exact mass of its run, equals r(log) of numpy's float32 running sum of
+      the fines' masses bit for bit, and lies far (about log 2) from the
+      log of the other rule's run, so either rule's mistake fails;
+    - the page matrices (non-index-only) are the writer's matrix of each
+      page's 2048 tokens' statistics taken at once;
+    - export -> import -> 300 more tokens equals the uninterrupted stream;
     - the fine read of a query against one selected fine is r(h @ C): the
       mixture of one matrix is 1;
     - with two fines whose z are equal the read is the plain mean of the
       two matrices' reads (mixture 1/2 each)."""
+    import numpy as np
     from oracle import tao_oracle as O
     g = torch.Generator().manual_seed(11)
-    t, h, d = 2900, 2, 8
-    xs = [torch.randn(1, t, h, d, generator=g).to(BF16) for _ in range(5)]
+    t, extra, h, d = 5000, 300, 2, 8
+    xs = [torch.randn(1, t + extra, h, d, generator=g).to(BF16) for _ in range(5)]
     fa = torch.randn(h, d, 3, generator=g) * 0.02
     fb = torch.randn(h, d, 3, generator=g) * 0.02
-    for index_only in (False, True):
-        s = O.OracleStream(0, O.Geometry(coarse_index_only=index_only), writer=writer)
-        pos = 0
-        while pos < t:
-            w = s.next_chunk(t - pos)
-            s.prefill(*(x[:, pos:pos + w] for x in xs), fa, fb, 0.5)
+
+    def run(s, lo, hi):
+        pos, outs = lo, []
+        while pos < hi:
+            w = s.next_chunk(hi - pos)
+            outs.append(s.prefill(*(x[:, pos:pos + w] for x in xs), fa, fb, 0.5))
             pos += w
+        return torch.cat(outs, 1)
+
+    def near(z, exact_log):        # within one bf16 ulp of the exact log
+        return ((z.double() - exact_log).abs() <= 2 ** -7 * exact_log.abs()).all()
+
+    for index_only in (False, True):
+        geo = O.Geometry(coarse_index_only=index_only)
+        s = O.OracleStream(0, geo, writer=writer)
+        run(s, 0, t)
         rk, v = xs[4], xs[2]
-        assert len(s.fine_z) == 9 and len(s.page_z) == 1
-        for f in (0, 8):
+        assert len(s.fine_z) == 17 and len(s.page_z) == 2
+        masses, exact = [], []
+        for f in range(17):
             blk = slice(f * 256, (f + 1) * 256)
-            mass = W.association_statistics(rk[:, blk], v[:, blk], with_mass=True)[2]
-            assert torch.allclose(mass.sum(-1), torch.full_like(mass.sum(-1), 256.0), rtol=4e-3)
-            exact = mass.log()
-            assert ((s.fine_z[f].double() - exact).abs() <= 2 ** -8 * exact.abs()).all()
-        lse = torch.logsumexp(torch.stack(s.fine_z[:8], 2).double(), 2)
-        assert (s.page_z[0].double() - lse).abs().max() <= 2 ** -7 * lse.abs().max() + 2 ** -7
-        assert not torch.equal(s.page_z[0], torch.stack(s.fine_z[:8], 2).amax(2))
-        # the page's mass is the mass of its 2048 tokens taken at once
-        page_mass = W.association_statistics(rk[:, :2048], v[:, :2048], with_mass=True)[2]
-        assert torch.equal(s.page_z[0], page_mass.log().to(BF16))
+            masses.append(W.association_statistics(rk[:, blk], v[:, blk], with_mass=True)[2])
+            exact.append(W.feature_simplex(rk[:, blk]).sum(1))             # fp64 [1, H, D]
+            assert torch.allclose(exact[f].sum(-1), torch.full_like(exact[f].sum(-1), 256.0),
+                                  rtol=4e-3)
+            assert ((s.fine_z[f].double() - exact[f].log()).abs()
+                    <= 2 ** -8 * exact[f].log().abs()).all()
+        stacked = np.stack([m.numpy() for m in masses])                     # [F, 1, H, D]
+
+        def descriptor(first, last):   # r(log) of numpy's float32 running sum
+            run_sum = np.cumsum(stacked[first:last + 1], axis=0, dtype=np.float32)[-1]
+            return torch.from_numpy(np.log(run_sum.astype(np.float64))).float().to(BF16)
+
+        def exact_log(first, last):
+            return sum(exact[first:last + 1]).log()
+
+        desc = s.page_descriptors()                                         # [1, H, 3, D]
+        for p, (lo, hi) in enumerate(((0, 7), (8, 15), (16, 16))):
+            first = 0 if index_only else lo
+            z = s.page_z[p] if p < 2 else desc[:, :, 2]
+            assert torch.equal(z, descriptor(first, hi))
+            assert near(z, exact_log(first, hi))
+            if p:
+                other = lo if index_only else 0
+                assert (z.double() - exact_log(other, hi)).abs().min() > 0.3
         if index_only:
             assert s.page_c == []
         else:
-            if writer == "structured_gram_association":
-                sq, cross, mass = W.structured_statistics(rk[:, :2048], v[:, :2048])
-                want = W.structured_matrix(sq, cross, mass, 2048)[1]
-            else:
-                want = W.association_matrix(*W.association_statistics(rk[:, :2048],
-                                                                     v[:, :2048]))[1]
-            assert (s.page_c[0].double() - want.double()).abs().max() <= \
-                2 ** -7 * want.double().abs().max()
+            for p in range(2):
+                tok = slice(p * 2048, (p + 1) * 2048)
+                if writer == "structured_gram_association":
+                    sq, cross, mass = W.structured_statistics(rk[:, tok], v[:, tok])
+                    want = W.structured_matrix(sq, cross, mass, 2048)[1]
+                else:
+                    want = W.association_matrix(*W.association_statistics(rk[:, tok],
+                                                                         v[:, tok]))[1]
+                assert (s.page_c[p].double() - want.double()).abs().max() <= \
+                    2 ** -7 * want.double().abs().max()
+        snap = s.export(config=None)
+        assert snap["pending_mass"] is not None and snap["pending_mass"].dtype == torch.float32
+        assert (snap["pending_square_mass"] is None) == (writer == "feature_mass_association")
+        assert (snap["pending_gram"] is None) == (writer == "structured_gram_association")
+        back = O.OracleStream.from_export(snap, 0, geo)
+        assert torch.equal(run(back, t, t + extra), run(s, t, t + extra))
+        assert all(torch.equal(a, b) for a, b in zip(back.page_z, s.page_z))
         # the mixture read against hand-picked fines
         hq = O.query_weights(xs[3][:, :1])                          # [1, 1, H, D]
         z_all, c_all = torch.stack(s.fine_z, 2), torch.stack(s.fine_c, 2)

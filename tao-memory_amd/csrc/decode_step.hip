@@ -437,9 +437,13 @@ __device__ int decode_units(const DecodeParams& p, int M, const CombineArgs& c) 
 // workgroup per (request, head, kCombineCols channels).
 constexpr int kCombineCols = 32;
 
-// COLS channels (from chunk * COLS) of one (request, head): G = 256 / COLS
-// thread groups share the local records. AGENT: the records were published
-// by other workgroups of the same launch (device-coherent loads). FDT: the
+// COLS channels (from chunk * COLS) of one (request, head). The first COLS
+// threads own one channel each; the others only stage the records' maxima
+// and weight sums (m, l) in LDS. Each channel's local numerator sums the
+// records in index order, so the merge gives the same bits for any COLS:
+// the single-request step (COLS = D) and the batched combine kernel
+// (COLS = kCombineCols) agree exactly. AGENT: the records were published by
+// other workgroups of the same launch (device-coherent loads). FDT: the
 // fusion parameters' dtype. Empty records (past the window) hold m = -inf
 // and l = 0, so they take part in the maxima and weights as exp2(-inf) = 0;
 // record 0 always holds the new token, so the common maximum is finite.
@@ -447,29 +451,30 @@ template <int D, int COLS, bool AGENT, int FDT, bool WEIGHTED>
 __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, int h, int chunk,
                              int M, int coarse_on, const CombineArgs& c) {
   using Gm = Geo<D>;
-  constexpr int STRIDE = D + kStepRec, G = kThreads / COLS;
-  constexpr int NLOC = Gm::NLOC, LPG = (NLOC + G - 1) / G;
+  constexpr int STRIDE = D + kStepRec;
+  constexpr int NLOC = Gm::NLOC;
+  static_assert(NLOC <= kThreads, "one thread stages each local record");
   __shared__ float ml[NLOC][2];
-  __shared__ float part_loc[G][COLS];
-  const int tid = threadIdx.x, dc = tid % COLS, g = tid / COLS;
-  const int d = chunk * COLS + dc;
+  const int tid = threadIdx.x;
+  const bool owner = tid < COLS;
+  const int d = chunk * COLS + (owner ? tid : 0);
   auto ld = [](const float* x) __attribute__((always_inline)) {
     return AGENT ? ld_agent(x) : *x;
   };
 
-  // Loads first: local records, the fine and coarse records, fusion operands.
-  float m_g[LPG], l_g[LPG], o_g[LPG];
-#pragma unroll
-  for (int i = 0; i < LPG; ++i) {
-    const int j = g + i * G;
-    m_g[i] = j < NLOC ? ld(recs + j * STRIDE) : -__builtin_inff();
-    l_g[i] = j < NLOC ? ld(recs + j * STRIDE + 1) : 0.0f;
-    o_g[i] = j < NLOC ? ld(recs + j * STRIDE + kStepRec + d) : 0.0f;
+  // Loads first: the records' (m, l), each channel's local sums, the fine
+  // and coarse records and the fusion operands.
+  if (tid < NLOC) {
+    ml[tid][0] = ld(recs + tid * STRIDE);
+    ml[tid][1] = ld(recs + tid * STRIDE + 1);
   }
+  float o_j[NLOC];
   float num = 0.0f, den = 1.0f, craw = 0.0f;
   float qx = 0.0f, fa3[3] = {}, fb3[3] = {};
   FuseWeights wts{};
-  if (g == 0) {
+  if (owner) {
+#pragma unroll
+    for (int j = 0; j < NLOC; ++j) o_j[j] = ld(recs + j * STRIDE + kStepRec + d);
     if (M > 0) {
       den = ld(recs + NLOC * STRIDE);
       num = ld(recs + NLOC * STRIDE + kStepRec + d);
@@ -490,40 +495,28 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
       }
     }
   }
-  if (dc == 0) {
-#pragma unroll
-    for (int i = 0; i < LPG; ++i)
-      if (g + i * G < NLOC) { ml[g + i * G][0] = m_g[i]; ml[g + i * G][1] = l_g[i]; }
-  }
-  __syncthreads();
+  __syncthreads();   // every thread: the (m, l) records are staged
+  if (!owner) return;
   float top = ml[0][0];
 #pragma unroll
   for (int j = 1; j < NLOC; ++j) top = fmaxf(top, ml[j][0]);
-  float pl = 0.0f;
+  float den_local = 0.0f, nl = 0.0f;
 #pragma unroll
-  for (int i = 0; i < LPG; ++i)
-    pl += l_g[i] > 0.0f ? __builtin_amdgcn_exp2f(m_g[i] - top) * o_g[i] : 0.0f;
-  part_loc[g][dc] = pl;
-  __syncthreads();
-  if (g == 0) {
-    float den_local = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NLOC; ++j)
-      den_local = fmaf(__builtin_amdgcn_exp2f(ml[j][0] - top), ml[j][1], den_local);
-    float nl = 0.0f;
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg) nl += part_loc[gg][dc];
-    const float local = rbf(nl / den_local);
-    bf16_t result;
-    if (M > 0 || coarse_on) {
-      const float fine_v = M > 0 ? rbf(rbf(num) / den) : 0.0f;
-      if (!WEIGHTED) wts = fuse_weights(qx, fa3, fb3, coarse_on ? 1 : 0, M > 0 ? 1 : 0);
-      result = fuse_mix(wts, local, rbf(craw), fine_v, c.gain);
-    } else {
-      result = f2bf(local);
-    }
-    out[d] = result;
+  for (int j = 0; j < NLOC; ++j) {
+    const float w = __builtin_amdgcn_exp2f(ml[j][0] - top);
+    den_local = fmaf(w, ml[j][1], den_local);
+    nl += ml[j][1] > 0.0f ? w * o_j[j] : 0.0f;
   }
+  const float local = rbf(nl / den_local);
+  bf16_t result;
+  if (M > 0 || coarse_on) {
+    const float fine_v = M > 0 ? rbf(rbf(num) / den) : 0.0f;
+    if (!WEIGHTED) wts = fuse_weights(qx, fa3, fb3, coarse_on ? 1 : 0, M > 0 ? 1 : 0);
+    result = fuse_mix(wts, local, rbf(craw), fine_v, c.gain);
+  } else {
+    result = f2bf(local);
+  }
+  out[d] = result;
 }
 
 // The single-launch step: the units of every (batch, head) publish their

@@ -69,16 +69,21 @@ def _long_state(tokens, heads, width, layer, seed, decode):
     (32768, 64, 1, False, (5, 18, 15)),
     (32768, 64, 1, True, (5, 18, 15)),
     (131072, 128, 0, False, (9, 34, 63)),
+    (131072, 128, 0, "hipgraph", (9, 34, 63)),
 ])
-def test_decode_from_long_state_matches_oracle(device, tokens, width, layer, graph, expect):
+def test_decode_from_long_state_matches_oracle(device, monkeypatch, tokens, width, layer, graph,
+                                               expect):
     """configs[3] regime at H2: prefill a 32K / 131K state, then 300 decode
     steps through at least 12 route refreshes and one seal (the local window
     holds 512 tokens at these cursors, so the seal is at +256). The graph
-    preset replays the captured step across them."""
+    preset replays the captured step across them, by recorded dispatch
+    (True) or by hipGraph launches ("hipgraph", configs[3]'s mode)."""
     heads, decode = 2, 300
     xs, fa, fb, splits, ora, ref = _long_state(tokens, heads, width, layer, 60 + width, decode)
     print(f"decode from {tokens} width={width} graph={graph}", flush=True)
-    state = new_state(layer, index_only_page_memo(graph=graph))
+    if graph == "hipgraph":
+        monkeypatch.setenv("TAO_GRAPH_REPLAY", "hipgraph")
+    state = new_state(layer, index_only_page_memo(graph=bool(graph)))
     d = to_dev(xs, device)
     out = run_hip(state, d, fa.to(device), fb.to(device), splits)
     assert _route_shape(state) == expect
@@ -87,7 +92,7 @@ def test_decode_from_long_state_matches_oracle(device, tokens, width, layer, gra
     compare_diagnostics(state, ora)
     if graph:
         obs = state.history_region.observation()
-        assert obs["replays"] > 0
+        assert obs["replays"] > 0 and obs["captures"] > 0
     state.release_execution()
 
 
@@ -154,13 +159,15 @@ def test_full_sequence_backward_batch2(tokens, width, index_only, seed):
     _compare_gradients(got, want, 5e-2)
 
 
-def test_batched_decode_ragged_long_matches_oracle(device):
+@pytest.mark.parametrize("width", [64, 128])
+def test_batched_decode_ragged_long_matches_oracle(device, width):
     """configs[4] regime at H2: four requests prefilled to ragged lengths in
     [16384, 32768] (seeded), 128 batched steps through their own route
     refreshes and seals; each request's outputs and final state against its
-    own oracle stream."""
+    own oracle stream. D128 is configs[4]'s width (the batch_units_kernel<128>
+    and batch_combine_kernel<128> its bench line times)."""
     from tao_attention import tao_attention_decode_batch
-    heads, width, steps = 2, 64, 128
+    heads, steps = 2, 128
     g = torch.Generator().manual_seed(81)
     lengths = torch.randint(16384, 32769, (4,), generator=g).tolist()
     seals = [(n - 768) % 256 + steps >= 256 for n in lengths]
@@ -168,7 +175,7 @@ def test_batched_decode_ragged_long_matches_oracle(device):
     fa = (torch.randn(heads, width, 3, generator=g) * 0.02)
     fb = (torch.randn(heads, width, 3, generator=g) * 0.02)
     xs = [inputs(n + steps, heads, width, seed=90 + r)[0] for r, n in enumerate(lengths)]
-    print(f"batched decode lengths={lengths}", flush=True)
+    print(f"batched decode lengths={lengths} width={width}", flush=True)
     states, oracles = [], []
     for x, n in zip(xs, lengths):
         st = new_state(0, PRESET)

@@ -348,13 +348,13 @@ def test_fold_sums_equal_the_oracle_fold_order(device):
         assert torch.equal(y.cpu(), want), op
 
 
-@pytest.mark.parametrize("coarse", [False, True])
-def test_batched_decode_equals_per_request(device, coarse):
+@pytest.mark.parametrize("coarse,width", [(False, 64), (True, 64), (False, 128), (True, 128)])
+def test_batched_decode_equals_per_request(device, coarse, width):
     """tao_attention_decode_batch == tao_attention_decode per request, bitwise:
     requests at different cursors (local-only, across a seal and refreshes,
     across the first page completion at 2560) and layers."""
     from tao_attention import TaoConfig, tao_attention_decode_batch
-    heads, width, steps = 2, 64, 40
+    heads, steps = 2, 40
     lengths, layers = [700, 1270, 2550], [0, 1, 3]
     cfg = TaoConfig() if coarse else index_only_page_memo()
     fa, fb = (torch.randn(heads, width, 3, generator=torch.Generator().manual_seed(9)) * 0.02
@@ -362,7 +362,7 @@ def test_batched_decode_equals_per_request(device, coarse):
     fa, fb = fa.to(device), fb.to(device)
     xs = [to_dev(inputs(n + steps, heads, width, seed=20 + r)[0], device)
           for r, n in enumerate(lengths)]
-    print(f"batched decode coarse={coarse}", flush=True)
+    print(f"batched decode coarse={coarse} width={width}", flush=True)
 
     def prefilled():
         out = []

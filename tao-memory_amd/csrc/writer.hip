@@ -1,22 +1,36 @@
 // Softmax fine writer and seal epilogue for gfx950.
 //
-// writer_kernel: one workgroup per (block, batch, head). Restates _seal's
-// softmax branch (tao_stream.py:66-77) for a 256-token block:
+// writer_kernel: one workgroup of D / 32 waves per (block, batch, head).
+// Restates _seal's softmax branch (tao_stream.py:66-77) for a 256-token
+// block:
 //   per channel d: m = max_t k, e = r(exp(r(k - m))), Z = r(sum_t e),
 //   P = r(e / Z), z = r(m + r(log Z)); C = r(P^T V) with fp32 accumulation.
 // z feeds routing and is bit-exact: the token sum uses the oracle's order
 // (four 64-token quarters summed sequentially, then (q0+q1)+(q2+q3)). C only
 // feeds reads (bf16 tolerance), so the kernel contracts the rounded e and
 // scales each column by 1/Z, C = r((sum_t e V) / Z), instead of rounding
-// P = e / Z element by element: one VALU pass fewer per block, within a
-// bf16 ulp of P's rounding.
-// Two workgroups per block and head, one per half of the key channels d
-// (the softmax is per channel): raw_k of the half and V are staged
-// transposed in LDS ([channel][token], token contiguous; V in 64-token
-// chunks) so both MFMA operands are 16-byte LDS reads; C^T = V^T E runs on
-// v_mfma_f32_32x32x16_bf16. The bank keeps C^T[e][d] so the contraction
-// index d is contiguous for every reader. C goes straight into its bank
-// slot: no repack.
+// P = e / Z element by element, within a bf16 ulp of P's rounding.
+//
+// C^T = V^T E runs on v_mfma_f32_32x32x16_bf16 with E as the B operand:
+// wave w owns key channels 32 w .. 32 w + 31, lane (i, hl) channel 32 w + i
+// and, for k-step ks, tokens 8 ks + 128 hl .. + 7 (a token permutation both
+// operands share), so lane half 0 holds tokens 0..127 and half 1 tokens
+// 128..255, each in order. The block's raw keys are copied from global
+// memory straight into LDS (global_load_lds_dwordx4; rows row-major, each
+// row's 16-byte chunks XOR-swizzled by 2 * row % (D / 8) so the reads below
+// meet distinct banks) and read into registers in that layout with
+// ds_read_b64_tr_b16 (4 consecutive tokens of one channel per read). The
+// values are then copied into the same 64 KB while the column softmax runs
+// in registers:
+//   m: the lane's 128 maxima, then its partner half's (a lane swap);
+//   e = r(exp(r(k - m))): the hardware exp, fp64 exp near a bf16 rounding
+//      boundary or for |x| > 8, one branch per 8 values;
+//   the quarter sums in token order as e is formed (quarters 0, 1 in lane
+//      half 0, quarters 2, 3 in half 1), then (q0+q1)+(q2+q3) by a swap.
+// Each wave then forms its 32 columns of C^T for all D value rows (V^T by
+// transposed reads), scales them by 1/Z and writes them into the bank slot
+// as C^T[e][d] (the contraction index d contiguous for every reader): no
+// repack.
 //
 // epilogue_kernel: one wave per (batch, head, channel) after sealing fine `slot`
 // (append_fine, tao_stream.py:477-501, plus the pending summary :277-290
@@ -26,32 +40,30 @@
 // pw = r(softmax over pages) for every current page.
 #include "tao_launch.h"
 #include "tao_common.h"
+#include "tao_lds.h"
 
 namespace tao {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBlock = 256;                 // tokens per fine block
-constexpr int kRowPad = kBlock + 8;         // K^T row stride in bf16 (528 B)
-constexpr int kVChunk = 64;                 // tokens per staged V^T chunk
-constexpr int kVPad = kVChunk + 4;          // V^T row stride in bf16 (34 dwords)
-constexpr int kWriterThreads = 256;         // 4 waves
 
-// One workgroup owns half of the key channels of one (block, batch, head):
-// DH = D / 2 channels of K^T (then E^T) for all 256 tokens, and V^T of all
-// D value channels streamed through one 64-token chunk. About 53 KB of LDS
-// at D = 128, so three workgroups share a CU and one's exp pass overlaps the
-// others' loads and MFMAs.
 template <int D>
-struct WriterSmem {
-  bf16_t kt[D / 2][kRowPad];   // raw keys of the half, then e = r(exp(r(k - m)))
-  bf16_t vt[D][kVPad];         // values of one token chunk, transposed
-  float part[4][D / 2];
-  float top[D / 2];
-  float inv_z[D / 2];          // 1 / Z per channel of the half
+struct WGeo {
+  static constexpr int WAVES = D / 32;                 // one 32-channel column tile each
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int CPR = D / 8;                    // 16-byte chunks per row
+  static constexpr int RB = D * 2;                     // bytes per row
+  static constexpr int TILE = kBlock * RB;             // bytes of the K (or V) block
+  static constexpr int CPW = TILE / 1024 / WAVES;      // 1 KB copies per wave and tile
+  static constexpr int KS = kBlock / 16;               // k-steps
+  static constexpr int RT = D / 32;                    // 32-row tiles of value channels
 };
+
+// Chunk c of row r sits at chunk position c ^ swz(r).
+template <int D>
+TAO_DEV int swz(int r) { return (2 * r) & (D / 8 - 1); }
 
 // Row of token `t` of a block: token rel + t of the call's operands when
 // rel + t >= 0 (rel = start - new_base), else ring slot (slot0 + t) mod L
@@ -65,182 +77,188 @@ TAO_DEV const bf16_t* block_row(const WriterParams& p, const TokView& tv, const 
   return ring + (((size_t)b * p.L + slot) * p.H + h) * D;
 }
 
-// Transposing LDS write of a token pair's 8 channels (16 bytes each):
-// rows ch0 .. ch0 + 7 of dst receive the pair as one 4-byte word at column t0.
-template <int STRIDE>
-TAO_DEV void store_pair_t(bf16_t* dst, int ch0, int t0, const uint4& a, const uint4& b) {
-  const uint32_t wa[4] = {a.x, a.y, a.z, a.w};
-  const uint32_t wb[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    *(uint32_t*)&dst[(ch0 + 2 * i) * STRIDE + t0] = (wa[i] & 0xFFFFu) | (wb[i] << 16);
-    *(uint32_t*)&dst[(ch0 + 2 * i + 1) * STRIDE + t0] = (wa[i] >> 16) | (wb[i] & 0xFFFF0000u);
-  }
-}
+TAO_DEV float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
+TAO_DEV float hi_bf(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
 template <int D>
-__global__ __launch_bounds__(kWriterThreads) void writer_kernel(WriterParams p) {
-  constexpr int DH = D / 2;                     // channels of this workgroup
-  constexpr int KJ = (kBlock / 2) * (DH / 8) / kWriterThreads;   // K token pairs per thread
-  constexpr int VJ = (kVChunk / 2) * (D / 8) / kWriterThreads;   // V token pairs per thread
-  constexpr int RT = D / 32, CT = DH / 32;      // 32 x 32 tiles of this half's C^T
-  static_assert(KJ >= 1 && VJ >= 1, "head width 64 or 128");
-  __shared__ WriterSmem<D> sm;
+__global__ __launch_bounds__(WGeo<D>::THREADS) void writer_kernel(WriterParams p) {
+  using G = WGeo<D>;
+  constexpr int CPR = G::CPR, RB = G::RB, CPW = G::CPW, KS = G::KS;
+  __shared__ __attribute__((aligned(1024))) unsigned char buf[G::TILE];
   const int BH = p.B * p.H;
-  const int half = blockIdx.x % 2;
-  const int bh = (blockIdx.x / 2) % BH;
-  const int blk = blockIdx.x / (2 * BH);
+  const int bh = blockIdx.x % BH;
+  const int blk = blockIdx.x / BH;
   const int b = bh / p.H, h = bh % p.H;
   const long long start = p.starts[blk];
   const int slot = p.first_slot + blk;
-  const int tid = threadIdx.x;
-  const int d0 = half * DH;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 31, hl = lane >> 5;
   const long long rel = start - p.new_base;
   const int slot0 = (int)(start % p.L);
+  const uint32_t base = lds_addr(buf);
 
-  // ---- issue the K half (all 256 tokens) and V chunk 0 loads. Job ->
-  // (channel chunk c, token pair): 128 consecutive K jobs / 32 consecutive V
-  // jobs share c, so the transposing writes fill consecutive words of a row.
-  uint4 ka[KJ], kb[KJ], va[VJ], vb[VJ];
+  // ---- copies of a K or V block into buf. Copy i of this wave fills 1 KB
+  // piece J = wave * CPW + i: lane L gets row (64 J + L) / CPR at chunk
+  // position (64 J + L) % CPR, which holds the row's chunk position ^ swz.
+  const bool fast = rel >= 0 && p.rk.st >= 0 && p.v.st >= 0 && p.rk.st < (1 << 21) &&
+                    p.v.st < (1 << 21);                          // workgroup-uniform
+  auto copy = [&](const TokView& tv, const bf16_t* ring) __attribute__((always_inline)) {
+    const char* src0 = (const char*)(tv.p + b * tv.sb + (fast ? rel : 0) * tv.st + h * tv.sh);
 #pragma unroll
-  for (int j = 0; j < KJ; ++j) {
-    const int job = tid + j * kWriterThreads;
-    const int c = job / (kBlock / 2), t0 = 2 * (job % (kBlock / 2));
-    ka[j] = *(const uint4*)(block_row(p, p.rk, p.ring_raw, b, h, rel, slot0, t0, D) + d0 + c * 8);
-    kb[j] = *(const uint4*)(block_row(p, p.rk, p.ring_raw, b, h, rel, slot0, t0 + 1, D) + d0 + c * 8);
-  }
-  auto load_v = [&](int chunk) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < VJ; ++j) {
-      const int job = tid + j * kWriterThreads;
-      const int c = job / (kVChunk / 2), t0 = chunk * kVChunk + 2 * (job % (kVChunk / 2));
-      va[j] = *(const uint4*)(block_row(p, p.v, p.ring_v, b, h, rel, slot0, t0, D) + c * 8);
-      vb[j] = *(const uint4*)(block_row(p, p.v, p.ring_v, b, h, rel, slot0, t0 + 1, D) + c * 8);
+    for (int i = 0; i < CPW; ++i) {
+      const int J = wave * CPW + i, q = J * 64 + lane, r = q / CPR, pos = q % CPR;
+      const int chunk = pos ^ swz<D>(r);
+      const void* src =
+          fast ? (const void*)(src0 + (uint32_t)(2 * (r * tv.st + chunk * 8)))
+               : (const void*)(block_row(p, tv, ring, b, h, rel, slot0, r, D) + chunk * 8);
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(buf + J * 1024), 16, 0, 0);
     }
   };
-  load_v(0);
-#pragma unroll
-  for (int j = 0; j < KJ; ++j) {
-    const int job = tid + j * kWriterThreads;
-    store_pair_t<kRowPad>(&sm.kt[0][0], (job / (kBlock / 2)) * 8, 2 * (job % (kBlock / 2)),
-                          ka[j], kb[j]);
-  }
+
+  // Transposed-read addresses: lane s of lane group g (gh = g % 2) reads
+  // rows 8 ks + 128 hl + 4 r + s / 4 (r = 0, 1), channels
+  // cbase + 16 gh + 4 (s % 4) .. + 3; k-steps are immediate offsets (8 ks
+  // rows move no swizzle).
+  const int s = lane & 15, gh = (lane >> 4) & 1;
+  auto tr_addr = [&](int cbase, int r) __attribute__((always_inline)) {
+    const int row = 128 * hl + 4 * r + (s >> 2);
+    const int chunk = (cbase >> 3) + 2 * gh + ((s & 3) >> 1);
+    return base + (uint32_t)(row * RB + ((chunk ^ swz<D>(row)) * 16) + (s & 1) * 8);
+  };
+
+  copy(p.rk, p.ring_raw);
+  wait_vm0();
   __syncthreads();
 
-  // ---- column softmax: jobs (channel d of the half, quarter of 64 tokens)
-  constexpr int QT = kBlock / 4;
-  for (int job = tid; job < 4 * DH; job += kWriterThreads) {
-    const int d = job % DH, qq = job / DH;
-    float m = -__builtin_inff();
-    for (int t = 0; t < QT; t += 8) {
-      const uint4 u = *(const uint4*)&sm.kt[d][qq * QT + t];
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  // ---- keys of channel 32 w + li, tokens of this lane half, as B operands
+  const uint32_t ak0 = tr_addr(32 * wave, 0), ak1 = tr_addr(32 * wave, 1);
+  u32x2 ev[KS][2];
+  unroll<KS>([&](auto ks_c) __attribute__((always_inline)) {
+    constexpr int K = decltype(ks_c)::value;
+    ev[K][0] = ds_read_tr8<K * 8 * RB>(ak0);
+    ev[K][1] = ds_read_tr8<K * 8 * RB>(ak1);
+  });
+  wait_lgkm<0>(ev[KS - 1][1]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        m = fmaxf(m, fmaxf(__uint_as_float(w[i] << 16), __uint_as_float(w[i] & 0xFFFF0000u)));
-    }
-    sm.part[qq][d] = m;
+  for (int k = 0; k < KS; ++k) {
+    after_waits(ev[k][0]);
+    if (k < KS - 1) after_waits(ev[k][1]);
   }
-  __syncthreads();
-  if (tid < DH)
-    sm.top[tid] = fmaxf(fmaxf(sm.part[0][tid], sm.part[1][tid]), fmaxf(sm.part[2][tid], sm.part[3][tid]));
-  __syncthreads();
-  for (int job = tid; job < 4 * DH; job += kWriterThreads) {
-    const int d = job % DH, qq = job / DH;
-    const float m = sm.top[d];
-    float acc = 0.0f;
-    for (int t = 0; t < QT; t += 8) {
-      uint4* cell = (uint4*)&sm.kt[d][qq * QT + t];
-      const uint4 u = *cell;
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-      // Eight exps, then one (rarely taken) branch for their fp64 fix-ups:
-      // the closest low half-word to the bf16 rounding boundary and the
-      // largest |x| of the eight decide it (exp_needs_exact for all eight).
-      float x[8], y[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[2 * i] = rbf(__uint_as_float(w[i] << 16) - m);
-        x[2 * i + 1] = rbf(__uint_as_float(w[i] & 0xFFFF0000u) - m);
-      }
-      uint32_t near = 0xFFFFFFFFu;
-      float big = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        y[i] = exp_fast(x[i]);
-        near = min(near, (__float_as_uint(y[i]) & 0xFFFFu) - 0x7FF0u);
-        big = fmaxf(big, __builtin_fabsf(x[i]));
-      }
-      if (near < 33u || !(big <= 8.0f)) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (exp_needs_exact(x[i], y[i])) y[i] = exp_exact(x[i]);
-      }
-      uint32_t o[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float e0 = rbf(y[2 * i]), e1 = rbf(y[2 * i + 1]);
-        acc += e0;
-        acc += e1;
-        o[i] = pack_bf16x2(e0, e1);
-      }
-      *cell = make_uint4(o[0], o[1], o[2], o[3]);
-    }
-    sm.part[qq][d] = acc;
-  }
-  __syncthreads();
-  if (tid < DH) {
-    const float total = rbf((sm.part[0][tid] + sm.part[1][tid]) + (sm.part[2][tid] + sm.part[3][tid]));
-    sm.inv_z[tid] = __builtin_amdgcn_rcpf(total);
-    const float z = rbf(sm.top[tid] + log_bf(total));
-    p.fine_z[((size_t)bh * p.fine_cap + slot) * D + d0 + tid] = f2bf(z);
-  }
-  if (p.z_only) return;                         // workgroup-uniform
+  __syncthreads();                         // every wave has its keys: buf is free
+  if (!p.z_only) copy(p.v, p.ring_v);      // values land while the softmax runs
 
-  // ---- C^T[e][d] = sum_t V^T[e][t] E[t][d] / Z[d] on MFMA 32x32x16: wave w
-  // owns row tile w (value channels 32w ..) and the half's CT column tiles;
-  // V^T arrives in 64-token chunks, the next chunk's loads in flight.
-  const int lane = tid & 63, wave = tid >> 6;
-  const int li = lane & 31, lk = (lane >> 5) * 8;
-  floatx16 acc[CT];
+  // ---- column maximum over the 256 tokens (lane half, then the partner)
+  float m = -__builtin_inff();
 #pragma unroll
-  for (int t = 0; t < CT; ++t)
+  for (int k = 0; k < KS; ++k)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
-#pragma unroll
-  for (int chunk = 0; chunk < kBlock / kVChunk; ++chunk) {
-    __syncthreads();   // e complete (chunk 0) / previous chunk consumed
-#pragma unroll
-    for (int j = 0; j < VJ; ++j) {
-      const int job = tid + j * kWriterThreads;
-      store_pair_t<kVPad>(&sm.vt[0][0], (job / (kVChunk / 2)) * 8, 2 * (job % (kVChunk / 2)),
-                          va[j], vb[j]);
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t w0 = ev[k][r].x, w1 = ev[k][r].y;
+      m = fmaxf(m, __builtin_fmaxf(fmaxf(lo_bf(w0), hi_bf(w0)), fmaxf(lo_bf(w1), hi_bf(w1))));
     }
-    __syncthreads();
-    if (chunk + 1 < kBlock / kVChunk) load_v(chunk + 1);
-    if (wave < RT) {
-#pragma unroll
-      for (int kk = 0; kk < kVChunk; kk += 16) {
-        const bf16x8 a = *(const bf16x8*)&sm.vt[wave * 32 + li][kk + lk];
-#pragma unroll
-        for (int t = 0; t < CT; ++t) {
-          const bf16x8 bv = *(const bf16x8*)&sm.kt[t * 32 + li][chunk * kVChunk + kk + lk];
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bv, acc[t], 0, 0, 0);
-        }
-      }
-    }
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false,
+                                                     false);
+    m = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
   }
-  if (wave >= RT) return;
-  // D layout: lane holds column li (d), rows (e) 8*(i/4) + 4*(lane/32) + i%4.
-  bf16_t* cdst = p.bank + ((size_t)bh * p.fine_cap + slot) * D * D;
+
+  // ---- e = r(exp(r(k - m))) in place, and the quarter sums in token order.
+  // Eight exps, then one (rarely taken) branch for their fp64 fix-ups: the
+  // closest low half-word to the bf16 rounding boundary and the largest |x|
+  // of the eight decide it (exp_needs_exact for all eight).
+  float qs[2] = {0.0f, 0.0f};
 #pragma unroll
-  for (int t = 0; t < CT; ++t) {
-    const float inv_z = sm.inv_z[t * 32 + li];
+  for (int k = 0; k < KS; ++k) {
+    const uint32_t w[4] = {ev[k][0].x, ev[k][0].y, ev[k][1].x, ev[k][1].y};
+    float x[8], y[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = rbf(lo_bf(w[i]) - m);
+      x[2 * i + 1] = rbf(hi_bf(w[i]) - m);
+    }
+    uint32_t near = 0xFFFFFFFFu;
+    float big = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      y[i] = exp_fast(x[i]);
+      near = min(near, (__float_as_uint(y[i]) & 0xFFFFu) - 0x7FF0u);
+      big = fmaxf(big, __builtin_fabsf(x[i]));
+    }
+    if (near < 33u || !(big <= 8.0f)) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (exp_needs_exact(x[i], y[i])) y[i] = exp_exact(x[i]);
+    }
+    uint32_t e[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      e[i] = pack_bf16x2(y[2 * i], y[2 * i + 1]);
+      qs[k / (KS / 2)] += lo_bf(e[i]);
+      qs[k / (KS / 2)] += hi_bf(e[i]);
+    }
+    ev[k][0].x = e[0];
+    ev[k][0].y = e[1];
+    ev[k][1].x = e[2];
+    ev[k][1].y = e[3];
+  }
+  float total;
+  {
+    // lane half 0: q0 + q1, half 1: q2 + q3; Z = r((q0 + q1) + (q2 + q3))
+    // (the swap returns the lane's own value and its partner's; the
+    // partner is whichever is not the own one, or either when they agree)
+    const float half_sum = qs[0] + qs[1];
+    const uint32_t own = __float_as_uint(half_sum);
+    const auto sw = __builtin_amdgcn_permlane32_swap(own, own, false, false);
+    const float partner = __uint_as_float(sw[0] == own ? sw[1] : sw[0]);
+    total = hl == 0 ? rbf(half_sum + partner) : rbf(partner + half_sum);
+  }
+  if (hl == 0)
+    p.fine_z[((size_t)bh * p.fine_cap + slot) * D + 32 * wave + li] = f2bf(rbf(m + log_bf(total)));
+  if (p.z_only) return;                    // workgroup-uniform
+
+  // ---- C^T[e][32 w + li] = sum_t V^T[e][t] E[t][32 w + li] / Z
+  wait_vm0();                              // this wave's value copies landed
+  __syncthreads();
+  uint32_t av[G::RT][2];
+#pragma unroll
+  for (int rt = 0; rt < G::RT; ++rt) {
+    av[rt][0] = tr_addr(32 * rt, 0);
+    av[rt][1] = tr_addr(32 * rt, 1);
+  }
+  floatx16 acc[G::RT];
+#pragma unroll
+  for (int rt = 0; rt < G::RT; ++rt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[rt][i] = 0.0f;
+  unroll<KS>([&](auto ks_c) __attribute__((always_inline)) {
+    constexpr int K = decltype(ks_c)::value;
+    u32x2 va[G::RT][2];
+#pragma unroll
+    for (int rt = 0; rt < G::RT; ++rt) {
+      va[rt][0] = ds_read_tr8<K * 8 * RB>(av[rt][0]);
+      va[rt][1] = ds_read_tr8<K * 8 * RB>(av[rt][1]);
+    }
+    wait_lgkm<0>(va[G::RT - 1][1]);
+    const bf16x8 eb = as_bf16x8(make_uint4(ev[K][0].x, ev[K][0].y, ev[K][1].x, ev[K][1].y));
+#pragma unroll
+    for (int rt = 0; rt < G::RT; ++rt) {
+      after_waits(va[rt][0]);
+      if (rt < G::RT - 1) after_waits(va[rt][1]);
+      acc[rt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          as_bf16x8(make_uint4(va[rt][0].x, va[rt][0].y, va[rt][1].x, va[rt][1].y)), eb, acc[rt],
+          0, 0, 0);
+    }
+  });
+  // D layout: lane holds column li (d), rows (e) 8*(i/4) + 4*hl + i%4.
+  const float inv = __builtin_amdgcn_rcpf(total);
+  bf16_t* cdst = p.bank + ((size_t)bh * p.fine_cap + slot) * D * D + 32 * wave + li;
+#pragma unroll
+  for (int rt = 0; rt < G::RT; ++rt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int row = wave * 32 + 8 * (i / 4) + 4 * (lane >> 5) + (i % 4);
-      cdst[(size_t)row * D + d0 + t * 32 + li] = f2bf(acc[t][i] * inv_z);
+      const int row = rt * 32 + 8 * (i / 4) + 4 * hl + (i % 4);
+      cdst[(size_t)row * D] = f2bf(acc[rt][i] * inv);
     }
-  }
 }
 
 // One wave per (batch, head, channel d); four channels per workgroup.
@@ -293,11 +311,11 @@ __global__ __launch_bounds__(kThreads) void epilogue_kernel(EpilogueParams p) {
 
 hipError_t launch_writer(const WriterParams& p, int head_dim, hipStream_t s) {
   if (p.count <= 0) return hipSuccess;
-  const dim3 grid((unsigned)(2 * p.count * p.B * p.H));
+  const dim3 grid((unsigned)(p.count * p.B * p.H));
   if (head_dim == 128)
-    hipLaunchKernelGGL(writer_kernel<128>, grid, dim3(kWriterThreads), 0, s, p);
+    hipLaunchKernelGGL(writer_kernel<128>, grid, dim3(WGeo<128>::THREADS), 0, s, p);
   else if (head_dim == 64)
-    hipLaunchKernelGGL(writer_kernel<64>, grid, dim3(kWriterThreads), 0, s, p);
+    hipLaunchKernelGGL(writer_kernel<64>, grid, dim3(WGeo<64>::THREADS), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -196,6 +196,7 @@ def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
         graph_state.release_execution()
         del graph_state
     del graph_snap
+    graph["launch_floor_us"] = graph_launch_floor(torch, device)
     # Device time per step: replay the same steps eagerly on an imported copy
     # with the GPU pre-loaded by a bounded spin kernel, and bracket each group
     # of STEPS_PER_SPIN back-to-back steps with HIP events on the launch
@@ -226,6 +227,37 @@ def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
     probe.events["decode_step"] = groups
     timed.release_execution()
     return state, xs, fa, fb, seconds, graph, steps_bytes
+
+
+def graph_launch_floor(torch, device, launches=2000):
+    """Host cost of one hipGraphLaunch on this runtime: torch.cuda.CUDAGraph
+    replays of two one-kernel graphs (a 1,024-element add), alternating as
+    the decode graph's two executable graphs do, timed back to back."""
+    x = torch.zeros(1024, device=device)
+    graphs = []
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        x.add_(1.0)                          # warm the kernel outside capture
+    torch.cuda.current_stream(device).wait_stream(side)
+    for _ in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            x.add_(1.0)
+        graphs.append(g)
+    for g in graphs:
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(launches):
+        graphs[i & 1].replay()
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / launches * 1e6
+    expect = 2 + launches + 1
+    if float(x[0]) != expect:
+        raise RuntimeError(f"graph replay count check failed: {float(x[0])} != {expect}")
+    del graphs
+    return us
 
 
 def run_cold(torch, args, device, cfg, heads, width, context, n_states, probe):
@@ -389,7 +421,7 @@ def run_model(torch, args, device, cfg):
     all 12 layers. Context only: the published whole-model figures are from
     another GPU and model weights."""
     import torch.nn.functional as F
-    from tao_attention import WholeStepGraph, new_state, tao_attention_decode
+    from tao_attention import WholeStepGraph, new_state, schedule, tao_attention_decode
     L, width, heads, dim, vocab = 12, 768, 6, 128, 32768
     g = torch.Generator(device=device).manual_seed(17)
 
@@ -402,8 +434,10 @@ def run_model(torch, args, device, cfg):
                    fb=w(heads, dim, 3).float()) for _ in range(L)]
     ctx = args.model_context
     states = []
-    for _ in range(L):
-        st = new_state(0, cfg)
+    for layer in range(L):
+        # Layer index l staggers the layer's route refreshes by 2 l tokens
+        # (tao_stream.py:202-208), as in the reference's model.
+        st = new_state(layer, cfg)
         xs = [torch.randn((1, ctx, heads, dim), generator=g, device=device).to(torch.bfloat16)
               for _ in range(5)]
         st._ingest(*xs)
@@ -446,12 +480,20 @@ def run_model(torch, args, device, cfg):
     torch.cuda.synchronize()
     seconds = time.perf_counter() - t0
     # The same decode continued through one captured graph of the whole
-    # step (WholeStepGraph): refresh and seal tokens still run eagerly.
+    # step (WholeStepGraph): refresh tokens replay their layers' gated
+    # refreshes; seal tokens and refreshes that change a route size run
+    # eagerly.
     graph = WholeStepGraph(states)
     for _ in range(8):
         token = graph.step(step, token)
     torch.cuda.synchronize()
     r0, e0 = graph.replays, graph.eager_steps
+    p0 = states[0].position
+    refresh_tokens = sum(
+        any(schedule.fines_at(p, cfg) > 0 and schedule.is_turn(p, st.layer_index, cfg)
+            for st in states) for p in range(p0, p0 + args.model_steps))
+    seal_tokens = sum(schedule.local_len_at(p, cfg) + 1 == cfg.serve_limit
+                      for p in range(p0, p0 + args.model_steps))
     t0 = time.perf_counter()
     for _ in range(args.model_steps):
         token = graph.step(step, token)
@@ -463,7 +505,8 @@ def run_model(torch, args, device, cfg):
         st.release_execution()
     return {"tok_s": args.model_steps / seconds, "seconds": seconds,
             "graph_tok_s": args.model_steps / graph_seconds, "graph_replays": replays,
-            "graph_eager_steps": eager}
+            "graph_eager_steps": eager, "refresh_tokens": refresh_tokens,
+            "seal_tokens": seal_tokens}
 
 
 def run_prefill(torch, device, cfg, heads, width, tokens, probe):
@@ -867,12 +910,19 @@ def main():
                          "tok_s": round(args.steps / graph["dispatch"][0], 2),
                          "ms_per_step": round(graph["dispatch"][0] / args.steps * 1e3, 4),
                          "timed_steps": graph["dispatch"][1],
-                         "hipgraph": {"replay": "TAO_GRAPH_REPLAY=hipgraph: hipGraphLaunch "
-                                                "of the captured copy + step",
+                         "hipgraph": {"replay": "TAO_GRAPH_REPLAY=hipgraph: per token one "
+                                                "hipGraphExecKernelNodeSetParams + "
+                                                "hipGraphLaunch of the one-node step graph "
+                                                "(two executable graphs alternating)",
                                       "tok_s": round(args.steps / graph["hipgraph"][0], 2),
                                       "ms_per_step": round(graph["hipgraph"][0] / args.steps
                                                            * 1e3, 4),
-                                      "timed_steps": graph["hipgraph"][1]}},
+                                      "timed_steps": graph["hipgraph"][1],
+                                      "launch_floor_us": round(graph["launch_floor_us"], 2),
+                                      "launch_floor": "host us per torch.cuda.CUDAGraph.replay "
+                                                      "of a one-kernel graph (two graphs "
+                                                      "alternating), the runtime's floor under "
+                                                      "any per-token graph replay"}},
     }
     if not args.no_cold:
         log("cold decode: building states")
@@ -943,7 +993,13 @@ def main():
             "tok_s": round(md["tok_s"], 1),
             "whole_step_graph_tok_s": round(md["graph_tok_s"], 1),
             "whole_step_graph_tokens": {"replayed": md["graph_replays"],
-                                        "eager (refresh/seal/capture)": md["graph_eager_steps"]},
+                                        "eager (seal / route-size change / warm-up before a "
+                                        "capture)": md["graph_eager_steps"],
+                                        "with a refresh in some layer": md["refresh_tokens"],
+                                        "with a seal": md["seal_tokens"]},
+            "layer_indices": "0..11: layer l refreshes at first_fine + 2 l + 24 k "
+                             "(tao_stream.py:202-208), so about half the tokens carry a "
+                             "refresh in some layer",
             "note": "caller-side greedy decode through all 12 layers (eager, then the same "
                     "decode continued through one captured graph of the whole step, "
                     "WholeStepGraph; index_only_page_memo); the reference publishes 107.192 "

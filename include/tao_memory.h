@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 9
+#define TAO_ABI_VERSION 10
 
 enum tao_status {
   TAO_OK = 0,
@@ -311,13 +311,15 @@ int tao_ring_append(const tao_state_dev* st, const tao_tokens* tok,
                     int32_t first, int32_t count, int64_t pos, void* stream);
 
 /* hipGraph of the decode step (the captured region of HistoryRegionGraph,
- * history_region_graph.py:95-113). The graph holds one copy of the operands
- * into stable staging buffers (its root node) followed by tao_decode_step;
- * tao_graph_launch points the root node at the call's operands
- * (hipGraphExecKernelNodeSetParams) and replays. Header-driven counts would
- * let it replay across seals and refreshes; the stream driver still ends
- * its epoch at each one, as the reference does. staging: bf16 device buffer
- * of 5 * B * H * D elements; out_stage: bf16 [B,1,H,D]. */
+ * history_region_graph.py:95-113). The graph holds one node, the decode step
+ * with its cursor read on the device, writing out_stage (bf16 [B,1,H,D]);
+ * it is instantiated twice and tao_graph_launch alternates between the two
+ * executable graphs, pointing the step at the call's operands
+ * (hipGraphExecKernelNodeSetParams) before each hipGraphLaunch. The
+ * reference copies its operands into static inputs instead (raw_input);
+ * reading them in place saves that copy and the graph edge after it. The
+ * stream driver ends the epoch at each refresh and seal, as the reference
+ * does. staging is unused (may be NULL). */
 int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu,
                      int32_t selected, void* staging, void* out_stage,
                      void* stream, void** graph_out);
@@ -440,8 +442,8 @@ int tao_numerics_selftest(int32_t op, const void* x, void* y, int64_t n, void* s
 /* Native per-token driver (replaces the Python control flow of one decode
  * call: operator.py:130-138, tao_stream.py:196-249 and 919-969,
  * history_region_graph.py:66-113). It keeps the cursor and the current route
- * size; staging (bf16, 5 * B * H * D) and out_stage (bf16 [B,1,H,D]) are
- * the caller's graph buffers (may be null when use_graph is 0). */
+ * size; out_stage (bf16 [B,1,H,D]) is the caller's graph output buffer (may
+ * be null when use_graph is 0); staging is unused (may be NULL). */
 int tao_stream_open(const tao_state_dev* st, const tao_stream_cfg* cfg, int64_t position,
                     int32_t route_coarse, int32_t route_size, void* staging,
                     void* out_stage, void** handle);
@@ -466,18 +468,25 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
  * caller-side multi-layer decode of docs/benchmarks.md:15, 89-94; no
  * reference entry point: the reference captures one layer's region only,
  * history_region_graph.py:95-113).
- * tao_stream_plan_step: the driver's next token. info (int64[6]) receives
+ * tao_stream_plan_step: the driver's next token. info (int64[7]) receives
  *   its position, whether a route refresh is due before its step, whether a
- *   seal is due after it, the route size its step reads, and the fine and
- *   coarse presence flags of its fusion.
- * tao_stream_graph_step: launches the next token's decode step with the
- *   cursor read on the device (header[0], advanced by the step), so a
- *   caller may capture it in a hipGraph and replay it for successive plain
- *   tokens (no refresh before, no seal after: the caller checks with
- *   tao_stream_plan_step and runs other tokens through tao_stream_decode).
- *   Fails for a token that is not plain. The host cursor does not move.
- * tao_stream_advance: moves the host cursor over `count` plain tokens that
- *   ran as device-cursor steps (fails if one of them is not plain). */
+ *   seal is due after it, the route size its step reads, the fine and
+ *   coarse presence flags of its fusion, and whether a refresh in its state
+ *   version keeps the current route (coarse count and size unchanged).
+ * tao_stream_graph_step: launches the next token's work with the cursor
+ *   read on the device (header[0], advanced by the step), so a caller may
+ *   capture it in a hipGraph and replay it for successive tokens of one
+ *   state version: when refreshes keep the route (info[6]), the route
+ *   refresh and fold kernels first, each exiting on the device unless the
+ *   cursor is a refresh turn of the stream's layer, then the decode step.
+ *   A captured launch replays correctly for every token of its state
+ *   version that has no seal after it and whose refresh, if any, keeps the
+ *   route; the caller checks with tao_stream_plan_step (no seal, and no
+ *   refresh or info[6]) and runs other tokens through tao_stream_decode.
+ *   Fails for a token that is not such a token. The host cursor does not
+ *   move.
+ * tao_stream_advance: moves the host cursor over `count` such tokens that
+ *   ran as device-cursor steps (fails if one of them is not). */
 int tao_stream_plan_step(void* handle, int64_t* info);
 int tao_stream_graph_step(void* handle, const tao_tokens* tok, const tao_fusion* fu, void* out,
                           const int64_t* out_s, void* stream);

@@ -504,13 +504,19 @@ hipError_t assoc_backward(const tao_state_dev* st, const tao_tokens* tok, char* 
   return tao::launch_assoc_block_bwd(bp, D, s);
 }
 
+// The captured decode step: one kernel node (the single-launch step with its
+// cursor read on the device) instantiated twice. Launches alternate between
+// the two executable graphs: re-launching one executable graph while its
+// previous launch is still queued makes hipGraphLaunch wait for that launch
+// (about 8 us of host time per token on this runtime), two do not.
 struct DecodeGraph {
   hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
-  tao::StageParams stage{};
-  hipGraphNode_t stage_node = nullptr;   // root node: the operand copy
-  hipKernelNodeParams stage_kp{};        // its launch shape (arguments set per launch)
-  int batch = 0, heads = 0, head_dim = 0;
+  hipGraphExec_t exec[2] = {nullptr, nullptr};
+  hipGraphNode_t step_node = nullptr;    // the graph's only node
+  hipKernelNodeParams step_kp{};         // its launch shape (arguments set per launch)
+  tao::DecodeParams params{};            // captured arguments; operands replaced per launch
+  int32_t selected = 0;
+  unsigned next = 0;                     // executable graph of the next launch
 };
 
 }  // namespace
@@ -589,6 +595,71 @@ int decode_replay(const DecodeParams& rec, const tao_tokens* tok, int head_dim,
                    "decode replay");
 }
 
+int fold_at(const tao_state_dev* st, int32_t selected, const TurnGate& gate, void* stream) {
+  int rc = check_state(st);
+  if (rc) return rc;
+  if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected count exceeds sel_cap");
+  FoldParams p{};
+  p.bank = (const bf16_t*)st->bank_c;
+  p.sw = (const bf16_t*)st->fine_sw;
+  p.pw = (const bf16_t*)st->page_w;
+  p.sel = st->sel;
+  p.fold_g = (float*)st->fold_g;
+  p.fold_den = (float*)st->fold_den;
+  p.B = st->batch;
+  p.H = st->heads;
+  p.group = st->coarse_group;
+  p.fine_cap = st->fine_cap;
+  p.page_cap = st->page_cap;
+  p.sel_cap = st->sel_cap;
+  p.M = selected;
+  p.gate = gate;
+  return check_hip(launch_fold(p, st->head_dim, (hipStream_t)stream), "tao_fold_route");
+}
+
+int route_at(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
+             int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
+             const TurnGate& gate, void* stream) {
+  int rc = check_state(st);
+  if (rc) return rc;
+  if (!raw_q_row || !rq_s) return fail(TAO_E_ARGUMENT, "null anchor query");
+  const int fines = completed * st->coarse_group + pending;
+  if (completed < 0 || pending < 0 || pending >= st->coarse_group || fines <= 0)
+    return fail(TAO_E_ARGUMENT, "route needs at least one sealed fine");
+  if (fines > st->fine_cap || completed + 1 > st->page_cap)
+    return fail(TAO_E_CAPACITY, "route counts exceed the state capacity");
+  if (coarse < 0 || coarse > completed || coarse > st->chosen_cap)
+    return fail(TAO_E_CAPACITY, "coarse count out of range");
+  const int eligible = coarse * st->coarse_group + pending;
+  if (selected <= 0 || selected > eligible || selected > st->sel_cap)
+    return fail(TAO_E_CAPACITY, "selected count out of range");
+  RouteParams p = {};
+  p.rq = (const bf16_t*)raw_q_row;
+  p.rq_sb = rq_s[0];
+  p.rq_st = 0;
+  p.rq_sh = rq_s[1];
+  p.turns = nullptr;
+  p.n_turns = 0;
+  p.pw = (const bf16_t*)st->page_w;
+  p.sw = (const bf16_t*)st->fine_sw;
+  p.sel = st->sel;
+  p.chosen = st->chosen;
+  p.header = st->header;
+  p.B = st->batch;
+  p.H = st->heads;
+  p.fine_cap = st->fine_cap;
+  p.page_cap = st->page_cap;
+  p.sel_cap = st->sel_cap;
+  p.chosen_cap = st->chosen_cap;
+  p.group = st->coarse_group;
+  p.completed = completed;
+  p.pending = pending;
+  p.coarse = coarse;
+  p.selected = selected;
+  p.gate = gate;
+  return check_hip(launch_route(p, st->head_dim, (hipStream_t)stream), "tao_route");
+}
+
 }  // namespace tao
 
 extern "C" {
@@ -615,24 +686,7 @@ int tao_decode_step(const tao_state_dev* st, const tao_tokens* tok, const tao_fu
 }
 
 int tao_fold_route(const tao_state_dev* st, int32_t selected, void* stream) {
-  int rc = check_state(st);
-  if (rc) return rc;
-  if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected count exceeds sel_cap");
-  tao::FoldParams p{};
-  p.bank = (const bf16_t*)st->bank_c;
-  p.sw = (const bf16_t*)st->fine_sw;
-  p.pw = (const bf16_t*)st->page_w;
-  p.sel = st->sel;
-  p.fold_g = (float*)st->fold_g;
-  p.fold_den = (float*)st->fold_den;
-  p.B = st->batch;
-  p.H = st->heads;
-  p.group = st->coarse_group;
-  p.fine_cap = st->fine_cap;
-  p.page_cap = st->page_cap;
-  p.sel_cap = st->sel_cap;
-  p.M = selected;
-  return check_hip(tao::launch_fold(p, st->head_dim, (hipStream_t)stream), "tao_fold_route");
+  return tao::fold_at(st, selected, tao::TurnGate{}, stream);
 }
 
 int tao_page_coarse(const tao_state_dev* st, int32_t first_page, int32_t count, void* stream) {
@@ -680,43 +734,8 @@ int tao_fold_coarse(const tao_state_dev* st, int32_t completed, void* stream) {
 int tao_route(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
               int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
               void* stream) {
-  int rc = check_state(st);
-  if (rc) return rc;
-  if (!raw_q_row || !rq_s) return fail(TAO_E_ARGUMENT, "null anchor query");
-  const int fines = completed * st->coarse_group + pending;
-  if (completed < 0 || pending < 0 || pending >= st->coarse_group || fines <= 0)
-    return fail(TAO_E_ARGUMENT, "route needs at least one sealed fine");
-  if (fines > st->fine_cap || completed + 1 > st->page_cap)
-    return fail(TAO_E_CAPACITY, "route counts exceed the state capacity");
-  if (coarse < 0 || coarse > completed || coarse > st->chosen_cap)
-    return fail(TAO_E_CAPACITY, "coarse count out of range");
-  const int eligible = coarse * st->coarse_group + pending;
-  if (selected <= 0 || selected > eligible || selected > st->sel_cap)
-    return fail(TAO_E_CAPACITY, "selected count out of range");
-  tao::RouteParams p = {};
-  p.rq = (const bf16_t*)raw_q_row;
-  p.rq_sb = rq_s[0];
-  p.rq_st = 0;
-  p.rq_sh = rq_s[1];
-  p.turns = nullptr;
-  p.n_turns = 0;
-  p.pw = (const bf16_t*)st->page_w;
-  p.sw = (const bf16_t*)st->fine_sw;
-  p.sel = st->sel;
-  p.chosen = st->chosen;
-  p.header = st->header;
-  p.B = st->batch;
-  p.H = st->heads;
-  p.fine_cap = st->fine_cap;
-  p.page_cap = st->page_cap;
-  p.sel_cap = st->sel_cap;
-  p.chosen_cap = st->chosen_cap;
-  p.group = st->coarse_group;
-  p.completed = completed;
-  p.pending = pending;
-  p.coarse = coarse;
-  p.selected = selected;
-  return check_hip(tao::launch_route(p, st->head_dim, (hipStream_t)stream), "tao_route");
+  return tao::route_at(st, raw_q_row, rq_s, completed, pending, coarse, selected,
+                       tao::TurnGate{}, stream);
 }
 
 int tao_write_fine(const tao_state_dev* st, const tao_tokens* tok, int64_t new_base,
@@ -1198,58 +1217,49 @@ int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu, int32_t sele
   int rc = check_state(st);
   if (!rc) rc = check_fusion(fu);
   if (rc) return rc;
-  if (!staging || !out_stage || !graph_out) return fail(TAO_E_ARGUMENT, "null graph buffers");
+  (void)staging;   // unused: the step reads the operands where the caller holds them
+  if (!out_stage || !graph_out) return fail(TAO_E_ARGUMENT, "null graph buffers");
   if (st->page_c || fu->coarse_on)
     return fail(TAO_E_ARGUMENT, "the decode hipGraph implements the index-only coarse preset");
   if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected out of range");
-  const int B = st->batch, H = st->heads, D = st->head_dim;
-  const size_t row = (size_t)B * H * D;
-  bf16_t* stg = (bf16_t*)staging;
+  const int D = st->head_dim;
+  // Captured with out_stage as every operand (a [B,1,H,D] buffer, so the
+  // captured arguments stay in bounds); each launch replaces them before the
+  // graph runs.
   tao_tokens tok{};
-  const void* ptrs[5];
-  for (int i = 0; i < 5; ++i) ptrs[i] = stg + i * row;
-  tok.q = ptrs[0]; tok.k = ptrs[1]; tok.v = ptrs[2]; tok.raw_q = ptrs[3]; tok.raw_k = ptrs[4];
-  const int64_t s[3] = {(int64_t)H * D, 0, (int64_t)D};
+  tok.q = tok.k = tok.v = tok.raw_q = tok.raw_k = out_stage;
+  const int64_t s[3] = {(int64_t)st->heads * D, 0, (int64_t)D};
   for (int i = 0; i < 3; ++i) {
     tok.q_s[i] = s[i]; tok.k_s[i] = s[i]; tok.v_s[i] = s[i]; tok.rq_s[i] = s[i]; tok.rk_s[i] = s[i];
   }
   tok.tokens = 1;
-  const int64_t out_s[3] = {(int64_t)H * D, 0, (int64_t)D};
-  const tao::DecodeParams p = decode_params(st, &tok, fu, out_stage, out_s);
-
   DecodeGraph* g = new DecodeGraph();
-  g->batch = B; g->heads = H; g->head_dim = D;
-  g->stage.dst = stg;
-  g->stage.B = B; g->stage.H = H; g->stage.D = D;
-  // Captured with the staging rows as their own sources (in bounds); every
-  // launch replaces the sources before the graph runs.
-  tao::StageParams sp = g->stage;
-  for (int i = 0; i < 5; ++i) sp.src[i] = view(ptrs[i], s);
+  g->params = decode_params(st, &tok, fu, out_stage, s);
+  g->selected = selected;
   hipStream_t cs = nullptr;
   hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
   if (e == hipSuccess) {
-    hipError_t le = tao::launch_stage_tokens(sp, cs);
-    if (le == hipSuccess) le = tao::launch_decode_step(p, D, selected, cs);
+    const hipError_t le = tao::launch_decode_step(g->params, D, selected, cs);
     e = hipStreamEndCapture(cs, &g->graph);
     if (e == hipSuccess) e = le;
   }
-  // The copy is the graph's only root (the step's kernels follow it in
-  // stream order).
   if (e == hipSuccess) {
-    size_t roots = 0;
-    e = hipGraphGetRootNodes(g->graph, nullptr, &roots);
-    if (e == hipSuccess && roots != 1) e = hipErrorInvalidValue;
-    if (e == hipSuccess) e = hipGraphGetRootNodes(g->graph, &g->stage_node, &roots);
+    size_t nodes = 0;
+    e = hipGraphGetNodes(g->graph, nullptr, &nodes);
+    if (e == hipSuccess && nodes != 1) e = hipErrorInvalidValue;
+    if (e == hipSuccess) e = hipGraphGetNodes(g->graph, &g->step_node, &nodes);
     hipGraphNodeType type = hipGraphNodeTypeEmpty;
-    if (e == hipSuccess) e = hipGraphNodeGetType(g->stage_node, &type);
+    if (e == hipSuccess) e = hipGraphNodeGetType(g->step_node, &type);
     if (e == hipSuccess && type != hipGraphNodeTypeKernel) e = hipErrorInvalidValue;
-    if (e == hipSuccess) e = hipGraphKernelNodeGetParams(g->stage_node, &g->stage_kp);
+    if (e == hipSuccess) e = hipGraphKernelNodeGetParams(g->step_node, &g->step_kp);
   }
-  if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  for (int i = 0; i < 2 && e == hipSuccess; ++i)
+    e = hipGraphInstantiate(&g->exec[i], g->graph, nullptr, nullptr, 0);
   if (cs) (void)hipStreamDestroy(cs);
   if (e != hipSuccess) {
-    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    for (hipGraphExec_t x : g->exec)
+      if (x) (void)hipGraphExecDestroy(x);
     if (g->graph) (void)hipGraphDestroy(g->graph);
     delete g;
     return check_hip(e, "tao_graph_create");
@@ -1263,21 +1273,25 @@ int tao_graph_launch(void* graph, const tao_tokens* tok, void* stream) {
   if (!graph) return fail(TAO_E_ARGUMENT, "null graph");
   int rc = check_tokens(tok);
   if (rc) return rc;
+  if (tok->tokens != 1) return fail(TAO_E_SHAPE, "decode step takes exactly one token");
   DecodeGraph* g = (DecodeGraph*)graph;
-  tao::StageParams sp = g->stage;
-  sp.src[0] = view(tok->q, tok->q_s);
-  sp.src[1] = view(tok->k, tok->k_s);
-  sp.src[2] = view(tok->v, tok->v_s);
-  sp.src[3] = view(tok->raw_q, tok->rq_s);
-  sp.src[4] = view(tok->raw_k, tok->rk_s);
-  // Point the root copy at this call's operands; launches already queued
-  // keep the arguments they were launched with.
-  void* args[1] = {&sp};
-  hipKernelNodeParams kp = g->stage_kp;
+  tao::DecodeParams p = g->params;
+  p.q = view(tok->q, tok->q_s);
+  p.k = view(tok->k, tok->k_s);
+  p.v = view(tok->v, tok->v_s);
+  p.rq = view(tok->raw_q, tok->rq_s);
+  p.rk = view(tok->raw_k, tok->rk_s);
+  // Point the step at this call's operands; launches already queued keep
+  // the arguments they were launched with.
+  int32_t selected = g->selected;
+  void* args[2] = {&p, &selected};
+  hipKernelNodeParams kp = g->step_kp;
   kp.kernelParams = args;
   kp.extra = nullptr;
-  hipError_t e = hipGraphExecKernelNodeSetParams(g->exec, g->stage_node, &kp);
-  if (e == hipSuccess) e = hipGraphLaunch(g->exec, (hipStream_t)stream);
+  hipGraphExec_t x = g->exec[g->next];
+  hipError_t e = hipGraphExecKernelNodeSetParams(x, g->step_node, &kp);
+  if (e == hipSuccess) e = hipGraphLaunch(x, (hipStream_t)stream);
+  if (e == hipSuccess) g->next ^= 1u;
   return check_hip(e, "tao_graph_launch");
 }
 
@@ -1285,7 +1299,11 @@ int tao_graph_destroy(void* graph) {
   if (!graph) return TAO_OK;
   DecodeGraph* g = (DecodeGraph*)graph;
   hipError_t e = hipSuccess;
-  if (g->exec) e = hipGraphExecDestroy(g->exec);
+  for (hipGraphExec_t x : g->exec)
+    if (x) {
+      const hipError_t d = hipGraphExecDestroy(x);
+      if (e == hipSuccess) e = d;
+    }
   if (g->graph) (void)hipGraphDestroy(g->graph);
   delete g;
   return check_hip(e, "tao_graph_destroy");

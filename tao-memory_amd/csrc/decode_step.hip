@@ -640,6 +640,7 @@ __global__ __launch_bounds__(kThreads) void fold_kernel(FoldParams p) {
   constexpr int WPT = (U * CH + kThreads - 1) / kThreads;   // weight chunks per thread
   __shared__ float wts[U][D];
   __shared__ int ids[U];
+  if (gate_closed(p.gate)) return;   // uniform: every thread reads one header word
   int bh, e_chunk;
   xcd_unit(blockIdx.x, p.B * p.H, CHUNKS, bh, e_chunk);
   const int e0 = e_chunk * ROWS;
@@ -708,27 +709,6 @@ __global__ __launch_bounds__(kThreads) void fold_kernel(FoldParams p) {
     *(float4*)dg = make_float4(den[0], den[1], den[2], den[3]);
     *(float4*)(dg + 4) = make_float4(den[4], den[5], den[6], den[7]);
   }
-}
-
-__global__ __launch_bounds__(kThreads) void stage_tokens_kernel(StageParams p) {
-  // One 16-byte chunk per thread: q, k, v, raw_q, raw_k rows of token 0.
-  const int per_row = p.D / 8;
-  const int bhn = p.B * p.H;
-  const int i = blockIdx.x * kThreads + threadIdx.x;
-  if (i >= 5 * bhn * per_row) return;
-  const int c = i % per_row, row = i / per_row;
-  const int which = row / bhn, bh = row % bhn;
-  const int b = bh / p.H, h = bh % p.H;
-  TokView v;
-  switch (which) {
-    case 0: v = p.src[0]; break;
-    case 1: v = p.src[1]; break;
-    case 2: v = p.src[2]; break;
-    case 3: v = p.src[3]; break;
-    default: v = p.src[4]; break;
-  }
-  *(uint4*)(p.dst + ((size_t)which * bhn + bh) * p.D + c * 8) =
-      *(const uint4*)(v.p + b * v.sb + h * v.sh + c * 8);
 }
 
 __global__ __launch_bounds__(kThreads) void ring_append_kernel(AppendParams p) {
@@ -840,13 +820,6 @@ hipError_t launch_fold(const FoldParams& p, int head_dim, hipStream_t s) {
   } else {
     return hipErrorInvalidValue;
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_stage_tokens(const StageParams& p, hipStream_t s) {
-  const int chunks = 5 * p.B * p.H * (p.D / 8);
-  hipLaunchKernelGGL(stage_tokens_kernel, dim3((unsigned)((chunks + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, s, p);
   return hipGetLastError();
 }
 

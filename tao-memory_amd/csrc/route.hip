@@ -198,6 +198,7 @@ template <int D>
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteParams p) {
   __shared__ RouteSmem<D> sm;
   __shared__ unsigned long long top[kMaxSort];
+  if (gate_closed(p.gate)) return;   // uniform: every thread reads one header word
   constexpr int PER = D / 64;
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
@@ -371,6 +372,7 @@ TAO_DEV float staged_masses(const float* h, const bf16_t* const* pw_rows,
 template <int D>
 __global__ __launch_bounds__(kRefreshThreads) void route_refresh_kernel(RouteParams p) {
   __shared__ RefreshSmem<D> sm;
+  if (gate_closed(p.gate)) return;   // uniform: every thread reads one header word
   constexpr int C16 = D / 8;            // 16-byte chunks per row
   const int bh = blockIdx.x;
   const int b = bh / p.H, h = bh % p.H;
@@ -887,6 +889,7 @@ hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s) {
   if (p.completed > kMaxSort || p.group * p.coarse + p.pending > kMaxSort)
     return hipErrorInvalidValue;
   // Turn mode: the lane-per-pair kernel when every turn's rows fit its LDS.
+  if (p.turns && p.gate.header) return hipErrorInvalidValue;   // gates serve single turns
   if (p.turns && p.n_turns > 0 && p.group == 8 && p.max_epoch >= 1 &&
       p.max_epoch / 8 + 1 + p.max_epoch <= (head_dim == 64 ? kTurnRows<64> : kTurnRows<128>)) {
     const dim3 tgrid((unsigned)(p.B * p.H * ((p.n_turns + kTurnGroup - 1) / kTurnGroup)));

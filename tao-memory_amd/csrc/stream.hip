@@ -39,8 +39,10 @@ extern "C" int tao_graph_destroy(void* graph);
 namespace {
 
 using tao::sched::fines_at;
+using tao::sched::first_turn;
 using tao::sched::is_turn;
 using tao::sched::local_len_at;
+using tao::sched::serve_limit;
 
 // Eager steps of an epoch before its capture (history_region_graph.py:90).
 constexpr int kWarmSteps = 3;
@@ -355,12 +357,32 @@ int tao_stream_sync(void* handle, const tao_state_dev* st, int64_t position,
 
 namespace {
 
-// The token at `pos` is a plain step: no route refresh before it and no seal
-// after it, so its whole work is the decode step.
-bool plain_at(const tao_stream_cfg& c, int64_t pos) {
+bool seal_after(const tao_stream_cfg& c, int64_t pos) {
+  return local_len_at(c, pos) + 1 == c.local_keep + c.fine_tokens;
+}
+
+// A route refresh at a turn in pos's state version keeps the current route's
+// coarse count and size (routed_counts of the version equal them), so a
+// device-cursor step may carry it gated on the device cursor: the route
+// kernels' counts and the step's route size hold for every turn of the
+// version.
+bool route_kept(const Stream* s, int64_t pos) {
+  const tao_stream_cfg& c = s->cfg;
+  const int64_t fines = fines_at(c, pos);
+  if (fines <= 0) return false;
+  int64_t coarse = 0, eligible = 0, selected = 0;
+  tao::sched::routed_counts(c, fines / c.coarse_group, fines % c.coarse_group, &coarse,
+                            &eligible, &selected);
+  return coarse == s->route_coarse && selected == s->route_size;
+}
+
+// The token at `pos` can run as a device-cursor step: no seal after it, and
+// either no route refresh before it or one that keeps the route.
+bool replayable_at(const Stream* s, int64_t pos) {
+  const tao_stream_cfg& c = s->cfg;
+  if (seal_after(c, pos)) return false;
   const bool refresh = fines_at(c, pos) > 0 && is_turn(c, pos);
-  const bool seal = local_len_at(c, pos) + 1 == c.local_keep + c.fine_tokens;
-  return !refresh && !seal;
+  return !refresh || route_kept(s, pos);
 }
 
 // The fusion flags of a step at `pos` (as tao_stream_decode sets them).
@@ -381,10 +403,11 @@ int tao_stream_plan_step(void* handle, int64_t* info) {
   const int64_t pos = s->position, fines = fines_at(c, pos);
   info[0] = pos;
   info[1] = fines > 0 && is_turn(c, pos);
-  info[2] = local_len_at(c, pos) + 1 == c.local_keep + c.fine_tokens;
+  info[2] = seal_after(c, pos);
   info[3] = fines > 0 ? s->route_size : 0;
   info[4] = fines > 0;
   info[5] = s->st.page_c != nullptr && fines >= c.coarse_group;
+  info[6] = route_kept(s, pos);
   return TAO_OK;
 }
 
@@ -392,11 +415,26 @@ int tao_stream_graph_step(void* handle, const tao_tokens* tok, const tao_fusion*
                           const int64_t* out_s, void* stream) {
   if (!handle || !tok || !fu) return stream_fail(TAO_E_ARGUMENT, "null decode argument");
   Stream* s = (Stream*)handle;
-  if (!plain_at(s->cfg, s->position))
+  const tao_stream_cfg& c = s->cfg;
+  const int64_t pos = s->position;
+  if (!replayable_at(s, pos))
     return stream_fail(TAO_E_ARGUMENT,
-                       "the next token refreshes its route or seals: it cannot be a device-cursor step");
-  const tao_fusion f = step_fusion(s, *fu, s->position);
-  const int32_t selected = fines_at(s->cfg, s->position) > 0 ? s->route_size : 0;
+                       "the next token seals or changes its route: it cannot be a device-cursor step");
+  const int64_t fines = fines_at(c, pos);
+  if (route_kept(s, pos)) {
+    // The version's refresh, run on the device only when the cursor the step
+    // reads is a turn of this layer (pre_step's route + fold).
+    const tao::TurnGate gate{s->st.header, (long long)first_turn(c), (long long)c.route_period,
+                             (long long)serve_limit(c)};
+    const int64_t rq_s[2] = {tok->rq_s[0], tok->rq_s[2]};
+    int rc = tao::route_at(&s->st, tok->raw_q, rq_s, (int32_t)(fines / c.coarse_group),
+                           (int32_t)(fines % c.coarse_group), s->route_coarse, s->route_size,
+                           gate, stream);
+    if (!rc) rc = tao::fold_at(&s->st, s->route_size, gate, stream);
+    if (rc) return rc;
+  }
+  const tao_fusion f = step_fusion(s, *fu, pos);
+  const int32_t selected = fines > 0 ? s->route_size : 0;
   return tao::decode_step_at(&s->st, tok, &f, selected, out, out_s, stream, -1);
 }
 
@@ -405,9 +443,10 @@ int tao_stream_advance(void* handle, int64_t count) {
   Stream* s = (Stream*)handle;
   if (count < 0) return stream_fail(TAO_E_ARGUMENT, "negative step count");
   for (int64_t i = 0; i < count; ++i)
-    if (!plain_at(s->cfg, s->position + i))
-      return stream_fail(TAO_E_ARGUMENT, "advance over a route refresh or a seal");
-  // A device-cursor step changes nothing the driver's graph epoch keys on.
+    if (!replayable_at(s, s->position + i))
+      return stream_fail(TAO_E_ARGUMENT, "advance over a seal or a route change");
+  // A device-cursor step keeps the route size and counts, which is all the
+  // driver tracks of a refresh (epoch_advance books its route update).
   epoch_advance(s, s->position + count);
   s->position += count;
   return TAO_OK;
@@ -432,8 +471,8 @@ int tao_stream_decode(void* handle, const tao_tokens* tok, const tao_fusion* fu,
   // The graph serves the memo-backed index-only read of non-refresh steps
   // (tao_stream.py:238-249); refresh steps run eagerly.
   if (c.use_graph && !coarse_values && fines > 0 && !refreshed) {
-    if (!s->staging || !s->out_stage)
-      return stream_fail(TAO_E_ARGUMENT, "decode graph needs the staging and output buffers");
+    if (!s->out_stage)
+      return stream_fail(TAO_E_ARGUMENT, "decode graph needs the output buffer");
     rc = region_step(s, tok, &f, selected, out, out_s, stream, &staged, &captured);
   } else {
     rc = tao::decode_step_at(&s->st, tok, &f, selected, out, out_s, stream, pos);

@@ -121,11 +121,29 @@ struct BatchStepParams {
 };
 hipError_t launch_batch_step(const BatchStepParams& p, int head_dim, hipStream_t s);
 
+// Route refresh gated on the device cursor, for a decode step captured in a
+// graph and replayed for later tokens: a kernel given a gate with a header
+// reads the cursor header[0] (the position of the token about to be
+// decoded) and exits at once unless it is a refresh turn of the stream's
+// layer: limit, or first + k * period for k >= 0 (the stagger of
+// tao_stream.py:202-208). Without a header the kernel always runs.
+struct TurnGate {
+  const int64_t* header;
+  long long first, period, limit;
+};
+
+__device__ inline bool gate_closed(const TurnGate& g) {
+  if (!g.header) return false;
+  const long long pos = g.header[0];
+  return !(pos == g.limit || (pos >= g.first && (pos - g.first) % g.period == 0));
+}
+
 struct FoldParams {
   const bf16_t* bank; const bf16_t* sw; const bf16_t* pw;
   const int32_t* sel;
   float* fold_g; float* fold_den;
   int B, H, group, fine_cap, page_cap, sel_cap, M;
+  TurnGate gate;
 };
 hipError_t launch_fold(const FoldParams& p, int head_dim, hipStream_t s);
 
@@ -157,6 +175,12 @@ int decode_step_at(const tao_state_dev* st, const tao_tokens* tok, const tao_fus
                    int32_t selected, void* out, const int64_t* out_s, void* stream,
                    long long position, float* records = nullptr,
                    unsigned* counters = nullptr);
+
+// tao_route / tao_fold_route with a turn gate (TurnGate{} = ungated).
+int route_at(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
+             int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
+             const TurnGate& gate, void* stream);
+int fold_at(const tao_state_dev* st, int32_t selected, const TurnGate& gate, void* stream);
 
 // The decode step's kernel arguments for a state, fusion and output buffer,
 // recorded once (decode_record) and dispatched per token with that token's
@@ -196,13 +220,6 @@ int f32_layout(F32Params& p, float* ws, int64_t T, int coarse_values);
 int f32_limits(const tao_stream_cfg& cfg, int64_t T, int64_t* pages, int64_t* cand);
 hipError_t launch_full_f32(const F32Params& p, hipStream_t s);
 
-struct StageParams {
-  TokView src[5];
-  bf16_t* dst;          // 5 x [B, H, D] contiguous
-  int B, H, D;
-};
-hipError_t launch_stage_tokens(const StageParams& p, hipStream_t s);
-
 struct AppendParams {
   TokView k, v, rk;
   bf16_t* ring_k; bf16_t* ring_v; bf16_t* ring_raw;
@@ -226,6 +243,7 @@ struct RouteParams {
   int B, H, fine_cap, page_cap, sel_cap, chosen_cap, group;
   int completed, pending, coarse, selected;
   int max_epoch;                 // turn mode: largest epoch of any turn (0: unknown)
+  TurnGate gate;                 // single-turn mode only
 };
 hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s);
 

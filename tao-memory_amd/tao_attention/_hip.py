@@ -172,7 +172,7 @@ _SIGNATURES = {
 
 EXPORTED = tuple(_SIGNATURES)
 
-ABI_VERSION = 9                # TAO_ABI_VERSION of include/tao_memory.h
+ABI_VERSION = 10               # TAO_ABI_VERSION of include/tao_memory.h
 
 # Decode-graph epoch counters (enum tao_graph_stat / tao_graph_reason).
 GRAPH_STATS = 19

@@ -5,12 +5,15 @@ TaoMemory state per layer (docs/benchmarks.md:15) and captures only one
 layer's history region (history_region_graph.py:95-113, "not whole-model
 graph capture", docs/benchmarks.md:89-94). WholeStepGraph captures a caller's
 whole model step -- every layer's projections, its TaoMemory decode and the
-rest of the block -- as one graph and replays it for every token whose
-decode is a plain step in every layer (no route refresh before it, no seal
-after it). Those tokens launch each layer's decode step with the cursor read
-on the device (the state header, which the step advances), so one capture
-serves successive tokens; refresh and seal tokens run the step eagerly
-through the layers' drivers, as do the tokens before the first capture.
+rest of the block -- as one graph and replays it for every token that no
+layer seals after and whose route refreshes keep the layers' route sizes.
+Those tokens launch each layer's work with the cursor read on the device
+(the state header, which the step advances): the layer's route refresh and
+fold kernels exit unless the cursor is a refresh turn of that layer (the
+layers' turns are staggered, tao_stream.py:202-208), then its decode step
+runs. One capture thus serves every such token of a state version; seal
+tokens and refreshes that change a route size run eagerly through the
+layers' drivers, as do the tokens before the first capture.
 
 The step function must take its per-token positions from the device
 (StreamCache.device_position()), not from host integers, since host values
@@ -81,11 +84,12 @@ class WholeStepGraph:
         self.captures += 1
 
     def step(self, fn, *inputs):
-        """The next token through fn: replayed when every layer's decode is a
-        plain step and the captured key still holds, eager otherwise (the
-        first plain token under a new key runs eagerly, the next captures)."""
+        """The next token through fn: replayed when every layer can run it as
+        a device-cursor step and the captured key still holds, eager
+        otherwise (the first such token under a new key runs eagerly, the
+        next captures)."""
         self._position()
-        if not all(st._plain_next() for st in self.states):
+        if not all(st._replayable_next() for st in self.states):
             self.eager_steps += 1
             return fn(*inputs)
         key = tuple(st._graph_key() for st in self.states)

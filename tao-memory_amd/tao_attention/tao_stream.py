@@ -247,14 +247,15 @@ class HistoryRegionGraph:
     Replays dispatch the captured step: by default the recorded kernel
     arguments (the two step kernels, state and output addresses fixed for
     the epoch, the token's operands patched in per call); with
-    TAO_GRAPH_REPLAY=hipgraph in the environment a hipGraph whose root node
-    copies the operands into fixed staging (hipGraphExecKernelNodeSetParams
-    per call). Both write the heads into the epoch's fixed output buffer,
-    which the next replay overwrites, as the reference's captured outputs.
+    TAO_GRAPH_REPLAY=hipgraph in the environment a one-node hipGraph of the
+    step, instantiated twice and launched alternately, its operands set per
+    call (hipGraphExecKernelNodeSetParams). Both write the heads into the
+    epoch's fixed output buffer, which the next replay overwrites, as the
+    reference's captured outputs.
     """
 
-    capture_address_scope = ("State banks, route buffers and the driver's staging/output "
-                             "buffers of the current state version only; the captured step "
+    capture_address_scope = ("State banks, route buffers and the driver's output "
+                             "buffer of the current state version only; the captured step "
                              "is dropped at every seal, route-size change and release")
 
     def __init__(self, owner):
@@ -638,16 +639,15 @@ class StreamCache:
         cfg = self.config
         if self._handle is None:
             scfg = self._stream_cfg()
-            staging = out_stage = None
+            out_stage = None
             if self._graph_mode:
-                B, H, D = dev.B, dev.H, dev.D
-                staging = torch.empty(5 * B * H * D, dtype=torch.bfloat16, device=dev.device)
-                out_stage = torch.empty((B, 1, H, D), dtype=torch.bfloat16, device=dev.device)
-                self._graph_buffers = (staging, out_stage)
+                out_stage = torch.empty((dev.B, 1, dev.H, dev.D), dtype=torch.bfloat16,
+                                        device=dev.device)
+                self._graph_buffers = (None, out_stage)
             handle = ctypes.c_void_p()
             _hip.check(_hip.lib().tao_stream_open(
                 ctypes.byref(dev.struct), ctypes.byref(scfg), self.position, self.route_coarse,
-                self.route_size, staging.data_ptr() if staging is not None else None,
+                self.route_size, None,
                 out_stage.data_ptr() if out_stage is not None else None, ctypes.byref(handle)))
             self._handle = handle
             self._handle_serial = next(_SERIAL)
@@ -791,21 +791,28 @@ class StreamCache:
         None while the driver is not bound to the current buffers."""
         if self._handle is None or self._handle_dirty:
             return None
-        info = (ctypes.c_int64 * 6)()
+        info = (ctypes.c_int64 * 7)()
         _hip.check(_hip.lib().tao_stream_plan_step(self._handle, info))
         return tuple(info)
 
-    def _plain_next(self):
-        """The next token is a plain step: no route refresh before it and no
-        seal after it (tao_stream_plan_step)."""
+    def _replayable_next(self):
+        """The next token can run as a device-cursor step
+        (tao_stream_graph_step): no seal after it, and either no route
+        refresh before it or one that keeps the route (tao_stream_plan_step)."""
         info = self._plan_next()
-        return info is not None and info[0] == self.position and not info[1] and not info[2]
+        return (info is not None and info[0] == self.position and not info[2]
+                and (not info[1] or info[6]))
 
     def _graph_key(self):
         """What a captured device-cursor step bakes in: route size, fusion
-        presence flags and the state's device buffers."""
+        presence flags, whether it carries the version's gated refresh (and
+        then the state version, whose counts the refresh kernels take), and
+        the state's device buffers."""
         info = self._plan_next()
-        return (info[3], info[4], info[5], bytes(self._dev.struct)) if info else None
+        if not info:
+            return None
+        version = self.state_version if info[6] else None
+        return (info[3], info[4], info[5], info[6], version, bytes(self._dev.struct))
 
     def _decode_captured(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
         """The next token's decode step with the cursor read on the device
@@ -815,8 +822,8 @@ class StreamCache:
         if (k.shape, v.shape, raw_q.shape, raw_k.shape) != (shape, shape, shape, shape):
             raise ValueError("q, k, v, raw_q and raw_k must share one [B, 1, H, D] shape")
         self._check_supported(q)
-        if not self._plain_next():
-            raise RuntimeError("the next token is not a plain step; decode it eagerly")
+        if not self._replayable_next():
+            raise RuntimeError("the next token seals or changes its route; decode it eagerly")
         q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
         fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
@@ -830,15 +837,20 @@ class StreamCache:
         return out
 
     def _advance_replayed(self, count):
-        """Book `count` plain tokens that ran as replays of a captured
+        """Book `count` tokens that ran as replays of a captured
         device-cursor step: driver cursor (tao_stream_advance), host cursor
-        and the counters a driver call would have moved."""
+        and the counters a driver call would have moved (a refresh turn
+        among them ran its gated refresh on the device, keeping the route)."""
         _hip.check(_hip.lib().tao_stream_advance(self._handle, count))
         if not self._run_open:
             self._open_run()
+        cfg = self.config
         for _ in range(count):
             if self.position >= self._first_fine:
                 self.fusion_pointwise_calls += 1
+                if schedule.is_turn(self.position, self.layer_index, cfg):
+                    self.route_refreshes += 1
+                    self.peak_selected_fine = max(self.peak_selected_fine, self.route_size)
             else:
                 self.fusion_no_history_local_returns += 1
             self.position += 1

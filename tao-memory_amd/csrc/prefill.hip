@@ -18,6 +18,7 @@ namespace tao {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTileQ = 32;
@@ -684,8 +685,10 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
 // fine u + kRing - 1 is loaded while fine u is consumed. Wave 0 also moves
 // the fine's pw and sw rows into LDS and turns them into the fine's weights
 // w = r(pw * sw) one iteration before the fine is read. A selecting wave's
-// A operand is r(h * w) (its queries' h in fp32 registers), so den[q] is
-// A against a column of ones as before. One barrier per fine.
+// A operand is r(h * w) (its queries' h in fp32 registers), and den[q] is the
+// fp32 sum of that operand's row (bf16 pair dot products against ones on the
+// VALU). One barrier per fine: a version whose waves ran apart through
+// per-slot LDS counters measured slower (waits for slot refills dominated).
 //
 // The ring and the staged weight rows are LDS written by the loads
 // themselves, which the compiler cannot order against its own LDS reads: it
@@ -768,6 +771,11 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
                                                                                  : kEpiElems];
   bf16_t (*ring)[D * D] = reinterpret_cast<bf16_t (*)[D * D]>(ring_mem);
   __shared__ __attribute__((aligned(16))) bf16_t pwsw[kRing][2][D];     // staged pw and sw rows
+  // D = 128: the head's fusion parameters, widened, fpar[0][d][i] =
+  // a[h][d][i] and fpar[1][d][i] = b[h][d][i], loaded at the start and read
+  // by the epilogue (not for D = 64, whose LDS would then exceed half a CU's).
+  constexpr bool kStageParams = D == 128;
+  __shared__ __attribute__((aligned(16))) float fpar[2][kStageParams ? D * 3 : 4];
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   // Tiles in reverse plan order: the latest tiles read the most fines, so
@@ -798,6 +806,12 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
     }
   }
   if (lane == 0) sm.erels[w] = reads ? erel : -1;
+  for (int i = tid; kStageParams && i < 2 * D * 3; i += kGroupThreads) {
+    const int which = i / (D * 3), d = (i % (D * 3)) / 3, j = i % 3;
+    fpar[which][d * 3 + j] =
+        which == 0 ? load_param(p.fa, p.f_dtype, h * p.fa_s[0] + d * p.fa_s[1] + j * p.fa_s[2])
+                   : load_param(p.fb, p.f_dtype, h * p.fb_s[0] + d * p.fb_s[1] + j * p.fb_s[2]);
+  }
 
   // ---- h of this wave's queries in fp32, in the MFMA A layout: lane (li, hl)
   // holds row q = li, channels d = 16 kk + 8 hl + j; rows past the tile are 0.
@@ -860,10 +874,11 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
   for (int t = 0; t < ET; ++t)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
-  floatx16 acc_den;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) acc_den[i] = 0.0f;
-  const bf16x8 ones = as_bf16x8(make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u));
+  // den of query li, this lane's half of the channels: the fp32 sum of the
+  // A operand's elements (bf16 pairs against ones on the VALU, which leaves
+  // the matrix core to the numerator).
+  float den_part = 0.0f;
+  const bf16x2 ones2 = __builtin_bit_cast(bf16x2, 0x3F803F80u);
 
   const bf16_t* bank = p.bank + (size_t)bh * p.fine_cap * D * D;
   const bf16_t* sw_base = p.sw + (size_t)bh * p.fine_cap * D;
@@ -1063,12 +1078,20 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
         u32x4 bn[ET], n0, n1;
         if (kk + 1 < KK) reads(kk + 1, bn, n0, n1);
         // num^T[e][q]: the C^T rows are the A operand, so lane li ends up
-        // holding query li (and den[li] in every element of acc_den).
+        // holding query li.
 #pragma unroll
         for (int t = 0; t < ET; ++t)
           acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(as_uint4(bq[t])), a, acc[t],
                                                            0, 0, 0);
-        acc_den = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, a, acc_den, 0, 0, 0);
+        const uint4 au = __builtin_bit_cast(uint4, a);
+        den_part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, au.x), ones2,
+                                                   den_part, false);
+        den_part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, au.y), ones2,
+                                                   den_part, false);
+        den_part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, au.z), ones2,
+                                                   den_part, false);
+        den_part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, au.w), ones2,
+                                                   den_part, false);
         if (kk + 1 < KK) {
 #pragma unroll
           for (int t = 0; t < ET; ++t) bq[t] = bn[t];
@@ -1116,7 +1139,7 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
                          : nullptr;
   bf16_t* tile_f = ring_mem + (size_t)w * 2 * 32 * D;
   bf16_t* tile_c = tile_f + 32 * D;
-  const float den = acc_den[0];
+  const float den = den_part + __shfl_xor(den_part, 32, 64);
   const float rden = __builtin_amdgcn_rcpf(rbf(den));
   if (p.save_fine && hl == 0 && li < nq) p.save_den[((size_t)b * p.T + q_first + li) * p.H + h] = rbf(den);
   auto unit_at = [&](int row, int unit) __attribute__((always_inline)) {
@@ -1210,13 +1233,27 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
   constexpr int RPI = 64 / CPR;                 // rows per pass of the wave
   const int c = lane % CPR;
   float ae[8][3], be[8][3];
+  if constexpr (kStageParams) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+    for (int v = 0; v < 6; ++v) {
+      const float4 av = *(const float4*)&fpar[0][24 * c + 4 * v];
+      const float4 bv = *(const float4*)&fpar[1][24 * c + 4 * v];
+      const float af[4] = {av.x, av.y, av.z, av.w}, bf[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      ae[j][i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + (8 * c + j) * p.fa_s[1] + i * p.fa_s[2]);
-      be[j][i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + (8 * c + j) * p.fb_s[1] + i * p.fb_s[2]);
+      for (int e = 0; e < 4; ++e) {
+        ae[(4 * v + e) / 3][(4 * v + e) % 3] = af[e];
+        be[(4 * v + e) / 3][(4 * v + e) % 3] = bf[e];
+      }
     }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        ae[j][i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + (8 * c + j) * p.fa_s[1] + i * p.fa_s[2]);
+        be[j][i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + (8 * c + j) * p.fb_s[1] + i * p.fb_s[2]);
+      }
+  }
   // Without the coarse branch: the paired two-channel fusion on the rounded
   // parameters and the signed-zero coarse term.
   float ra[8][3], rb[8][3];
@@ -1228,8 +1265,19 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
       rb[j][i] = rbf(be[j][i]);
     }
   const float ct0 = rbf(0.0f * rbf(p.gain * 0.0f));
+  // Every pass's local and query rows are loaded first (rows past the tile
+  // read its last row), so the passes do not wait on memory one by one
+  // behind the previous pass's stores.
+  constexpr int ITS = 32 / RPI;
+  uint4 lus[ITS], xus[ITS];
 #pragma unroll
-  for (int it = 0; it < 32 / RPI; ++it) {
+  for (int it = 0; it < ITS; ++it) {
+    const int tq = q_first + min(lane / CPR + RPI * it, nq - 1);
+    lus[it] = *(const uint4*)(p.local + (((size_t)b * p.T + tq) * p.H + h) * D + 8 * c);
+    xus[it] = *(const uint4*)(p.rq.p + b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + 8 * c);
+  }
+#pragma unroll
+  for (int it = 0; it < ITS; ++it) {
     const int r = lane / CPR + RPI * it;
     if (r >= nq) break;
     const int tq = q_first + r;
@@ -1239,8 +1287,8 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
     if constexpr (COARSE) {
       if (coarse_on) cu = *(const uint4*)&tile_c[unit_at(r, c)];
     }
-    const uint4 lu = *(const uint4*)(p.local + row * D + 8 * c);
-    const uint4 xu = *(const uint4*)(p.rq.p + b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + 8 * c);
+    const uint4 lu = lus[it];
+    const uint4 xu = xus[it];
     float fv[8], cv[8], lv[8], xv[8];
     unpack8f(fu, fv);
     unpack8f(cu, cv);

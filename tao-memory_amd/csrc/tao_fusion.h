@@ -103,8 +103,13 @@ TAO_DEV uint32_t fuse_pair_local_fine(const float q[2], const float local[2], co
   rbf2(p2[0], p2[1]);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const float top = fmaxf(p0[j], p2[j]);
-    const float x0 = __expf(p0[j] - top), x2 = __expf(p2[j] - top);
+    // exp(p - top) of the larger branch is exp(0) = 1 exactly, so only the
+    // other one's exp is computed (a NaN lands in that exp, so it still
+    // makes both weights NaN).
+    const bool first = p0[j] >= p2[j];
+    const float top = first ? p0[j] : p2[j], low = first ? p2[j] : p0[j];
+    const float xl = __expf(low - top);
+    const float x0 = first ? 1.0f : xl, x2 = first ? xl : 1.0f;
     const float inv = __builtin_amdgcn_rcpf(x0 + x2);
     e0[j] = x0 * inv;
     e2[j] = x2 * inv;

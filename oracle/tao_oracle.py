@@ -922,7 +922,18 @@ def training_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, ro
     of the block (association_writer.py:11-32 without its bf16 casts), and a
     completed page's matrix from the sums of its fines' G and X,
     differentiable through the solves.
+
+    The feature writers (tao_stream.py:56-65, 543-549, 600-662) take
+    z_f = log(m_f) with m_f = sum_t U_t, C_f from the solve (feature mass)
+    or structured_matrix of the block's statistics (structured Gram), page
+    z = log of the summed masses and page C from the summed statistics; a
+    query's fine read is the mixture sum_m w_m h C_m with
+    w_m = (h . exp z_m) / sum_m' (h . exp z_m') over its selection, and its
+    coarse read the same mixture over the completed pages (no denominator).
     """
+    if writer in FEATURE_WRITERS:
+        return _feature_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
+                                       routes, geometry or Geometry(), writer, intermediates)
     g = geometry or Geometry()
     b, total, heads, d = q.shape
     ft, keep, group = g.fine_tokens, g.local_keep, g.coarse_group
@@ -1002,6 +1013,119 @@ def training_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, ro
             cw = torch.softmax(page_z[:, :, :completed], 2)
             coarse = torch.einsum("bqhd,bhpd,bhpde->bqhe", h, cw,
                                   torch.stack(pc_full[:completed], 2))
+        else:
+            coarse = torch.zeros_like(fine)
+        present = 1 + int(coarse_on)
+        scores = []
+        for branch in range(3):
+            s = fusion_a[..., branch] * rq + fusion_b[..., branch]
+            if branch == 0:
+                s = s + math.log(present)
+            if branch == 1 and not coarse_on:
+                s = torch.full_like(s, NEG_INF)
+            scores.append(s)
+        rho = torch.softmax(torch.stack(scores, -1), -1)
+        lo = local[:, start:end]
+        outs.append(rho[..., 0] * 2 * lo + rho[..., 1] * gain * coarse + rho[..., 2] * gain * fine)
+    return torch.cat(outs, 1)
+
+
+def _smooth_local(q, k, v, g):
+    """Per-tile suffix-causal local attention without rounding (the local
+    part of training_forward_smooth)."""
+    b, total, heads, d = q.shape
+    ft, keep = g.fine_tokens, g.local_keep
+    parts = []
+    for start in range(0, total, ft):
+        end = min(total, start + ft)
+        k0 = max(0, start - keep)
+        s = torch.einsum("bqhd,bkhd->bhqk", q[:, start:end], k[:, k0:end]) / math.sqrt(d)
+        rows = (end - k0) - (end - start) + torch.arange(end - start)
+        allowed = torch.arange(end - k0)[None, :] <= rows[:, None]
+        p = torch.softmax(s.masked_fill(~allowed, NEG_INF), -1)
+        parts.append(torch.einsum("bhqk,bkhd->bqhd", p, v[:, k0:end]))
+    return torch.cat(parts, 1)
+
+
+def _smooth_mixture(h, z, matrices, mask=None):
+    """sum_m w_m sum_d h[d] M_m[d][e] with w_m = (h . exp z_m) / sum over the
+    (masked) items; h [B, Q, H, D], z [B, H, P, D], matrices [B, H, P, D, D],
+    mask [B, Q, H, P] or None (every item)."""
+    mass = torch.einsum("bqhd,bhpd->bqhp", h, torch.exp(z))
+    if mask is not None:
+        mass = mass * mask
+    w = mass / mass.sum(-1, keepdim=True)
+    return torch.einsum("bqhp,bqhd,bhpde->bqhe", w, h, matrices)
+
+
+def _feature_forward_smooth(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, routes, g,
+                            writer, intermediates):
+    """training_forward_smooth for the feature writers (see there)."""
+    from . import writers as W
+    b, total, heads, d = q.shape
+    ft, keep, group = g.fine_tokens, g.local_keep, g.coarse_group
+    local = _smooth_local(q, k, v, g)
+    n_tiles = -(-total // ft)
+    lag = keep // ft
+    visible_max = max(0, n_tiles - 1 - lag)
+    if total <= g.serve_limit or visible_max == 0:
+        return local
+    structured = writer == "structured_gram_association"
+    zs, cs, firsts, crosses, masses = [], [], [], [], []
+    for f in range(visible_max):
+        kb, vb = raw_k[:, f * ft:(f + 1) * ft], v[:, f * ft:(f + 1) * ft]
+        u = torch.softmax(kb, -1)                                   # over channels
+        mass = u.sum(1)                                             # [B, H, D]
+        cross = torch.einsum("bthd,bthe->bhde", u, vb)
+        if structured:
+            first = (u * u).sum(1)
+            cs.append(W.structured_matrix(first, cross, mass, ft)[0])
+        else:
+            first = torch.einsum("bthd,bthe->bhde", u, u)
+            ridge = first.diagonal(dim1=-2, dim2=-1).sum(-1) / d
+            system = first + ridge[..., None, None] * torch.eye(d, dtype=first.dtype)
+            cs.append(torch.linalg.solve(system, cross))
+        zs.append(torch.log(mass))
+        firsts.append(first)
+        crosses.append(cross)
+        masses.append(mass)
+    fine_z = torch.stack(zs, 2)
+    bank = torch.stack(cs, 2)
+    if intermediates is not None:
+        intermediates["fine_z"], intermediates["bank"] = fine_z, bank
+    full = visible_max // group
+    pz_full, pc_full = [], []
+    for p in range(full):
+        idx = range(p * group, (p + 1) * group)
+        mass = sum(masses[i] for i in idx)
+        pz_full.append(torch.log(mass))
+        if g.coarse_index_only:
+            continue
+        first = sum(firsts[i] for i in idx)
+        cross = sum(crosses[i] for i in idx)
+        if structured:
+            pc_full.append(W.structured_matrix(first, cross, mass, ft * group)[0])
+        else:
+            ridge = first.diagonal(dim1=-2, dim2=-1).sum(-1) / d
+            system = first + ridge[..., None, None] * torch.eye(d, dtype=first.dtype)
+            pc_full.append(torch.linalg.solve(system, cross))
+    first_coarse = keep + group * ft
+    gain = 2.0 * alpha
+    outs = [local[:, :min(total, (lag + 1) * ft)]]
+    for tile in range(lag + 1, n_tiles):
+        start, end = tile * ft, min(total, tile * ft + ft)
+        visible = tile - lag
+        completed = visible // group
+        rq = raw_q[:, start:end]
+        h = torch.softmax(rq, -1)
+        sel = routes[tile]
+        mask = torch.zeros((*sel.shape[:3], visible), dtype=h.dtype)
+        mask.scatter_(-1, sel, 1.0)
+        fine = _smooth_mixture(h, fine_z[:, :, :visible], bank[:, :, :visible], mask)
+        coarse_on = start >= first_coarse and not g.coarse_index_only
+        if coarse_on:
+            coarse = _smooth_mixture(h, torch.stack(pz_full[:completed], 2),
+                                     torch.stack(pc_full[:completed], 2))
         else:
             coarse = torch.zeros_like(fine)
         present = 1 + int(coarse_on)

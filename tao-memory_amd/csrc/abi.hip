@@ -407,10 +407,20 @@ struct AssocPages {
   int pages;
 };
 
+// Feature-mass writer (fm non-null): the statistics pass also writes the
+// fines' masses, and d mass (from d z of the fines and of the pages' mass
+// descriptors) reaches the block adjoint.
+struct FeatureMass {
+  float* mass; float* dmass;       // [fines * B][H][D]
+  const float* dz; const float* dpz;
+  int pages;
+};
+
 hipError_t assoc_backward(const tao_state_dev* st, const tao_tokens* tok, char* ws,
                           size_t stats_off, size_t y_off, size_t w_off, size_t s_off,
                           size_t dk_off, size_t starts_off, const float* dc, float* dv,
-                          int fines, int T, const AssocPages& pg, hipStream_t s) {
+                          int fines, int T, const AssocPages& pg, hipStream_t s,
+                          const FeatureMass* fm = nullptr) {
   const int B = st->batch, H = st->heads, D = st->head_dim, ft = st->fine_tokens;
   const int mats = fines * B * H;
   int64_t* starts = (int64_t*)(ws + starts_off);
@@ -435,6 +445,7 @@ hipError_t assoc_backward(const tao_state_dev* st, const tao_tokens* tok, char* 
   sp.ring_v = (const bf16_t*)st->ring_v;
   sp.L = st->local_keep + st->fine_tokens;
   sp.B = B;
+  if (fm) sp.mass = fm->mass;
   e = tao::launch_writer_stats(sp, D, s);
   if (e != hipSuccess) return e;
   tao::AssocSolveParams fp{};
@@ -501,7 +512,124 @@ hipError_t assoc_backward(const tao_state_dev* st, const tao_tokens* tok, char* 
                                     B, H, (int64_t)D * D, s);
     if (e != hipSuccess) return e;
   }
+  if (fm) {
+    e = tao::launch_mass_grad(fm->dz, fm->dpz, fm->mass, nullptr, fm->dmass, fines, fm->pages,
+                              st->coarse_group, B, H, D, s);
+    if (e != hipSuccess) return e;
+    bp.dmass = fm->dmass;
+  }
   return tao::launch_assoc_block_bwd(bp, D, s);
+}
+
+// The structured-Gram writer's share of the backward: the fines' statistics
+// (square mass, cross, mass) again, the closed form's adjoint per fine and,
+// with page values, per completed page (added to its fines'), d mass from
+// d z, then per block W = d cross and S = diag(2 d square) through the block
+// adjoint (d raw_k's share into dk_off, dv added).
+struct StructuredWs {
+  size_t stats, mass, w, s, dsq, dms, dmass;        // fines
+  size_t pstats, pw, pdsq, pdms;                    // pages
+};
+
+hipError_t structured_backward(const tao_state_dev* st, const tao_tokens* tok, char* ws,
+                               const StructuredWs& o, size_t dk_off, size_t starts_off,
+                               const float* dc, const float* dpc, const float* dz,
+                               const float* dpz, float* dv, int fines, int pages, int T,
+                               hipStream_t s) {
+  const int B = st->batch, H = st->heads, D = st->head_dim, ft = st->fine_tokens;
+  const int G = st->coarse_group, mats = fines * B * H;
+  int64_t* starts = (int64_t*)(ws + starts_off);
+  hipError_t e = tao::launch_block_starts(starts, fines, ft, s);
+  if (e != hipSuccess) return e;
+  float* square = (float*)(ws + o.stats);
+  float* cross = square + (size_t)mats * D * D;
+  float* mass = (float*)(ws + o.mass);
+  const tao::TokView rk = view(tok->raw_k, tok->rk_s), vv = view(tok->v, tok->v_s);
+  tao::WriterStatsParams sp{};
+  sp.k = rk.p;
+  sp.v = vv.p;
+  sp.k_s[0] = rk.sb; sp.k_s[1] = rk.st; sp.k_s[2] = rk.sh;
+  sp.v_s[0] = vv.sb; sp.v_s[1] = vv.st; sp.v_s[2] = vv.sh;
+  sp.N = fines * B;
+  sp.T = ft;
+  sp.H = H;
+  sp.mode = 1;
+  sp.gram = square;
+  sp.cross = cross;
+  sp.mass = mass;
+  sp.starts = starts;
+  sp.new_base = 0;
+  sp.ring_raw = (const bf16_t*)st->ring_raw;
+  sp.ring_v = (const bf16_t*)st->ring_v;
+  sp.L = st->local_keep + st->fine_tokens;
+  sp.B = B;
+  e = tao::launch_writer_stats(sp, D, s);
+  if (e != hipSuccess) return e;
+  tao::StructuredBwdParams bp{};
+  bp.square = square;
+  bp.cross = cross;
+  bp.mass = mass;
+  bp.dct = dc;
+  bp.dct_cap = fines;
+  bp.B = B;
+  bp.H = H;
+  bp.count_mats = mats;
+  bp.count = (float)ft;
+  bp.dsquare = (float*)(ws + o.dsq);
+  bp.dcross = (float*)(ws + o.w);
+  bp.dmass = (float*)(ws + o.dms);
+  e = tao::launch_structured_bwd(bp, D, s);
+  if (e != hipSuccess) return e;
+  if (pages > 0) {
+    // Page p's matrix is the closed form of its fines' summed statistics:
+    // its adjoints add to each of its fines'.
+    const int pmats = pages * B * H;
+    float* psq = (float*)(ws + o.pstats);
+    float* pcr = psq + (size_t)pmats * D;
+    float* pms = pcr + (size_t)pmats * D * D;
+    e = tao::launch_page_sum(square, psq, pages, G, B, H, (int64_t)D, s);
+    if (e == hipSuccess) e = tao::launch_page_sum(cross, pcr, pages, G, B, H, (int64_t)D * D, s);
+    if (e == hipSuccess) e = tao::launch_page_sum(mass, pms, pages, G, B, H, (int64_t)D, s);
+    if (e != hipSuccess) return e;
+    tao::StructuredBwdParams pp = bp;
+    pp.square = psq;
+    pp.cross = pcr;
+    pp.mass = pms;
+    pp.dct = dpc;
+    pp.dct_cap = pages;
+    pp.count_mats = pmats;
+    pp.count = (float)(ft * G);
+    pp.dsquare = (float*)(ws + o.pdsq);
+    pp.dcross = (float*)(ws + o.pw);
+    pp.dmass = (float*)(ws + o.pdms);
+    e = tao::launch_structured_bwd(pp, D, s);
+    if (e == hipSuccess)
+      e = tao::launch_page_add(bp.dsquare, pp.dsquare, pages, G, B, H, (int64_t)D, s);
+    if (e == hipSuccess)
+      e = tao::launch_page_add(bp.dcross, pp.dcross, pages, G, B, H, (int64_t)D * D, s);
+    if (e == hipSuccess)
+      e = tao::launch_page_add(bp.dmass, pp.dmass, pages, G, B, H, (int64_t)D, s);
+    if (e != hipSuccess) return e;
+  }
+  e = tao::launch_square_diag(bp.dsquare, (float*)(ws + o.s), mats, D, s);
+  if (e == hipSuccess)
+    e = tao::launch_mass_grad(dz, dpz, mass, bp.dmass, (float*)(ws + o.dmass), fines, pages, G, B,
+                              H, D, s);
+  if (e != hipSuccess) return e;
+  tao::AssocBwdParams kb{};
+  kb.w = bp.dcross;
+  kb.s = (float*)(ws + o.s);
+  kb.raw_k = rk;
+  kb.v = vv;
+  kb.dk = (float*)(ws + dk_off);
+  kb.dv = dv;
+  kb.mats = mats;
+  kb.B = B;
+  kb.H = H;
+  kb.T = T;
+  kb.ft = ft;
+  kb.dmass = (const float*)(ws + o.dmass);
+  return tao::launch_assoc_block_bwd(kb, D, s);
 }
 
 // The captured decode step: one kernel node (the single-launch step with its
@@ -1166,8 +1294,8 @@ int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion
     rt.page_c = (const bf16_t*)st->page_c;
     rt.page_cap = st->page_cap;
   }
-  if (feature_writer(st) && rt.save_fine)
-    return fail(TAO_E_ARGUMENT, "a feature writer's read keeps no saves (forward only)");
+  if (feature_writer(st) && rt.save_fine && !query_routes)
+    return fail(TAO_E_ARGUMENT, "a feature writer's turn-route read keeps no saves");
   e = tao::launch_read_tiles(rt, D, s);
   if (e != hipSuccess) return check_hip(e, "tao_prefill read");
   tao::AppendParams app{};
@@ -1323,6 +1451,9 @@ struct TrainBwdLayout {
   // with page values, the pages' statistic sums, Y, W, S and d page_c
   size_t stats, sol_y, sol_w, sgram, dk_extra, starts;
   size_t pstats, psol_y, psol_w, psgram, dpc;
+  // feature writers: masses, d mass, structured adjoints, d z of the fines'
+  // and pages' descriptors, the mixture weights and d masses per query rank
+  size_t fmass, fdmass, fdsq, fdms, fdz, fdpz, wv, dmv, pdsq, pdms;
   size_t zero_begin, zero_end;                                  // accumulators to clear
   size_t total;
   int n_tiles, v_max;
@@ -1360,12 +1491,14 @@ TrainBwdLayout train_bwd_layout(const tao_state_dev* st, int64_t tokens, int fin
   l.dsw = take(BH * (size_t)fines * D * 4);
   l.dpz = take(BH * (size_t)st->page_cap * D * 4);
   l.dz = take(BH * (size_t)fines * D * 4);
-  const size_t pages = (assoc_writer(st) && st->page_c) ? (size_t)fines / st->coarse_group : 0;
+  const bool feat = feature_writer(st) && fines > 0;
+  const size_t pages =
+      ((assoc_writer(st) || feat) && st->page_c) ? (size_t)fines / st->coarse_group : 0;
   l.dpc = take(BH * pages * D * D * 4);
   l.dalpha = take(4);
   l.zero_end = off;
   l.dalpha_parts = take((size_t)tao::fuse_bwd_workgroups((int)T, (int)B, (int)H) * 4);
-  if (assoc_writer(st) && fines > 0) {
+  if ((assoc_writer(st) || feat) && fines > 0) {
     const size_t mats = (size_t)fines * BH, mat = D * D * 4;
     l.stats = take(2 * mats * mat);
     l.sol_y = take(mats * mat);
@@ -1378,9 +1511,71 @@ TrainBwdLayout train_bwd_layout(const tao_state_dev* st, int64_t tokens, int fin
     l.psol_y = take(pmats * mat);
     l.psol_w = take(pmats * mat);
     l.psgram = take(pmats * mat);
+    if (feat) {
+      const size_t vec = mats * D * 4, pvec = pmats * D * 4;
+      l.pstats = take(2 * pmats * mat + 2 * pvec);   // also square, cross, mass sums
+      l.fmass = take(vec);
+      l.fdmass = take(vec);
+      l.fdsq = take(vec);
+      l.fdms = take(vec);
+      l.fdz = take(vec);
+      l.fdpz = take(pvec);
+      l.wv = take(rows * tao::kMixMaxRank * 4);
+      l.dmv = take(rows * tao::kMixMaxRank * 4);
+      l.pdsq = take(pvec);
+      l.pdms = take(pvec);
+    }
   }
   l.total = off;
   return l;
+}
+
+// The feature writers' mixture reads backward (mix_bwd.hip): d C^T and d z
+// of the fines from d fine (the fusion adjoint's dnum, den being 1) and, with
+// page values, of the completed pages from d coarse; dh accumulates both.
+hipError_t feature_read_backward(const tao_state_dev* st, const tao_prefill_pools* pools,
+                                 const TrainBwdLayout& l, char* ws, const tao::MemBwdParams& mp,
+                                 const tao::TrainBwdParams& fp, int fines, int T,
+                                 hipStream_t s) {
+  const int B = st->batch, H = st->heads, D = st->head_dim, G = st->coarse_group;
+  hipError_t e = hipMemsetAsync(mp.dh, 0, (size_t)B * T * H * D * sizeof(float), s);
+  if (e != hipSuccess) return e;
+  tao::MixBwdParams mx{};
+  mx.h = fp.h;
+  mx.dout = fp.dnum;
+  mx.z = (const bf16_t*)st->fine_z;
+  mx.mats = (const bf16_t*)st->bank_c;
+  mx.cap = st->fine_cap;
+  mx.qsel = pools->qsel;
+  mx.qsel_words = pools->qsel_words;
+  mx.dh = mp.dh;
+  mx.wv = (float*)(ws + l.wv);
+  mx.dmv = (float*)(ws + l.dmv);
+  mx.R = tao::kMixMaxRank;
+  mx.dmat = mp.dc;
+  mx.dz = (float*)(ws + l.fdz);
+  mx.n_items = fines;
+  mx.B = B;
+  mx.H = H;
+  mx.T = T;
+  mx.ft = st->fine_tokens;
+  mx.keep = st->local_keep;
+  mx.group = G;
+  mx.first_query = st->local_keep + st->fine_tokens;
+  e = tao::launch_mix_bwd(mx, D, s);
+  if (e != hipSuccess || !st->page_c || fines / G < 1) return e;
+  tao::MixBwdParams mc = mx;
+  mc.dout = fp.dcoarse;
+  mc.z = (const bf16_t*)st->page_z;
+  mc.mats = (const bf16_t*)st->page_c;
+  mc.cap = st->page_cap;
+  mc.qsel = nullptr;
+  mc.qsel_words = 0;
+  mc.dmat = (float*)(ws + l.dpc);
+  mc.dz = (float*)(ws + l.fdpz);
+  mc.n_items = fines / G;
+  mc.first_query = st->local_keep + G * st->fine_tokens;
+  return tao::launch_mix_bwd(mc, D, s);
 }
 
 }  // namespace
@@ -1424,7 +1619,7 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   const TrainBwdLayout l = train_bwd_layout(st, T, fines, fines > 0 ? pools : nullptr);
   if (a->workspace_bytes < l.total) return fail(TAO_E_WORKSPACE, "backward workspace too small");
   const bool regularized = assoc_writer(st) && fines > 0;
-  if (feature_writer(st)) return fail(TAO_E_ARGUMENT, "gradients through a feature writer");
+  const bool featured = feature_writer(st) && fines > 0;
   const hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)a->workspace;
   const int D = st->head_dim, H = st->heads, B = st->batch;
@@ -1540,7 +1735,29 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
     mp.dpc = (float*)(ws + l.dpc);
     mp.dpc_cap = st->page_c ? fines / G : 0;
   }
-  e = tao::launch_mem_bwd_read(mp, D, s);
+  if (featured) {
+    e = feature_read_backward(st, pools, l, ws, mp, fp, fines, (int)T, s);
+    if (e != hipSuccess) return check_hip(e, "tao_train_backward mixture reads");
+    const int pages = st->page_c ? fines / G : 0;
+    if (st->fine_writer == TAO_WRITER_FEATURE_MASS) {
+      AssocPages pg{l.pstats, l.psol_y, l.psol_w, l.psgram, (const float*)(ws + l.dpc), pages};
+      FeatureMass fm{(float*)(ws + l.fmass), (float*)(ws + l.fdmass),
+                     (const float*)(ws + l.fdz), (const float*)(ws + l.fdpz), pages};
+      e = assoc_backward(st, tok, ws, l.stats, l.sol_y, l.sol_w, l.sgram, l.dk_extra, l.starts,
+                         mp.dc, mp.dv, fines, (int)T, pg, s, &fm);
+    } else {
+      StructuredWs o{l.stats, l.fmass, l.sol_w, l.sgram, l.fdsq, l.fdms, l.fdmass,
+                     l.pstats, l.psol_w, l.pdsq, l.pdms};
+      e = structured_backward(st, tok, ws, o, l.dk_extra, l.starts, mp.dc,
+                              (const float*)(ws + l.dpc), (const float*)(ws + l.fdz),
+                              (const float*)(ws + l.fdpz), mp.dv, fines, pages, (int)T, s);
+    }
+    if (e != hipSuccess) return check_hip(e, "tao_train_backward feature writer");
+    mp.values_external = 1;
+    mp.dk_extra = (const float*)(ws + l.dk_extra);
+  } else {
+    e = tao::launch_mem_bwd_read(mp, D, s);
+  }
   if (e != hipSuccess) return check_hip(e, "tao_train_backward memory branch");
   if (regularized) {
     AssocPages pg{l.pstats, l.psol_y, l.psol_w, l.psgram, mp.dpc, mp.dpc_cap};
@@ -1553,7 +1770,8 @@ int tao_train_backward(const tao_state_dev* st, const tao_tokens* tok, const tao
   if (e != hipSuccess) return check_hip(e, "tao_train_backward writer branch");
   const size_t BHf = (size_t)B * H * fines;
   if (a->dz_out && fines > 0) {
-    e = hipMemcpyAsync(a->dz_out, mp.dz, BHf * D * sizeof(float), hipMemcpyDeviceToDevice, s);
+    const void* dz = featured ? (const void*)(ws + l.fdz) : (const void*)mp.dz;
+    e = hipMemcpyAsync(a->dz_out, dz, BHf * D * sizeof(float), hipMemcpyDeviceToDevice, s);
     if (e != hipSuccess) return check_hip(e, "tao_train_backward dz copy");
   }
   if (a->dc_out && fines > 0) {

@@ -690,6 +690,15 @@ __global__ __launch_bounds__(512) void assoc_block_bwd_kernel(AssocBwdParams p) 
           ua[kk], as_bf16x8(*(const uint4*)&sm.sg[32 * t + li][16 * kk + 8 * hl]), du[t], 0, 0, 0);
     }
   }
+  // Feature writers: d of the block's mass sum_t u_t reaches every token's u.
+  if (p.dmass) {
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const float dm = p.dmass[(size_t)mat * D + 32 * t + li];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) du[t][i] += dm;
+    }
+  }
   // p at the accumulator positions, and sum_d p du per token row
   float pv[DT][16], part[16];
 #pragma unroll

@@ -656,7 +656,9 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
         if (p.save_fine) {
           p.save_fine[row * D + e] = f2bf(fine);
           p.save_coarse[row * D + e] = f2bf(rbf(cacc[i]));
-          if (e == 0) p.save_den[row] = rbf(acc_den[i]);
+          // The mixture read has no denominator: 1 keeps the fusion
+          // adjoint's d num = d fine / den exact.
+          if (e == 0) p.save_den[row] = FEAT ? 1.0f : rbf(acc_den[i]);
         }
         p.out[b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + e] =
             fuse_element(xv[i], lv[i], rbf(cacc[i]), fine, ae, be, p.gain, coarse_on ? 1 : 0, 1);
@@ -1367,8 +1369,9 @@ hipError_t launch_read_tiles(const ReadTilesParams& p, int head_dim, hipStream_t
   if (head_dim != 128 && head_dim != 64) return hipErrorInvalidValue;
   if (p.fine_z) {
     // Feature writers, no saves: per-query routes index-only; turn routes
-    // with or without the page mixture (page_c).
-    if (p.save_fine) return hipErrorInvalidValue;
+    // with or without the page mixture (page_c). Saves (the backward's
+    // pre-fusion heads) only with per-query routes.
+    if (p.save_fine && !perq) return hipErrorInvalidValue;
     const bool pages = p.page_c != nullptr;
     if (perq) {
       if (coarse || (pages && !p.page_z)) return hipErrorInvalidValue;

@@ -471,6 +471,9 @@ struct AssocBwdParams {
   float* dk;                     // [B, T, H, D] fp32, written for block tokens
   float* dv;                     // [B, T, H, D] fp32, accumulated
   int mats, B, H, T, ft;
+  // Feature writers (nullable): d of the block's feature mass sum_t u_t
+  // [mats][D], added to every token's du before the feature softmax.
+  const float* dmass;
 };
 hipError_t launch_assoc_gram_bwd(const AssocBwdParams& p, int head_dim, hipStream_t s);
 // Pages of the regularized writer: page_sum writes the in-order sums of each
@@ -496,6 +499,69 @@ struct StructuredParams {
   int to_slots, B, H, cap, first_slot, group;
 };
 hipError_t launch_structured_matrix(const StructuredParams& p, int head_dim, hipStream_t s);
+
+// ---- feature writers' read adjoint (mix_bwd.hip)
+// The numerator-only mixture read of the full-sequence path
+// (tao_stream.py:600-662 with feature_read_coefficients,
+// association_writer.py:46-53): query q reads items m (its selected fines, or
+// for the coarse read the completed pages of its tile) with
+// mass_m = sum_d h[d] exp(z_m[d]), w_m = mass_m / sum_m' mass_m' and
+// out[e] = sum_m sum_d r(w_m h[d]) C_m[d][e]. Given d out, with
+// dch_m[d] = sum_e dout[e] C_m[d][e] and dw_m = sum_d dch_m[d] h[d]:
+//   dC_m[d][e] += r(w_m h[d]) dout[e],
+//   dmass_m = (dw_m - sum_m' w_m' dw_m') / sum_m' mass_m',
+//   dh[d] += sum_m (w_m dch_m[d] + dmass_m exp(z_m[d])),
+//   dz_m[d] += sum_q dmass_m h[d] exp(z_m[d]).
+struct MixBwdParams {
+  const bf16_t* h;        // [B, T, H, D] the read's query weights
+  const float* dout;      // [B, T, H, D] d fine (or d coarse)
+  const bf16_t* z;        // [B, H, cap, D] item descriptors (fine_z or page_z)
+  const bf16_t* mats;     // [B, H, cap, D, D] item matrices, C^T (bank or page_c)
+  int cap;
+  const uint32_t* qsel; int qsel_words;   // fine items: selection words; null: pages
+  float* dh;              // [B, T, H, D] accumulated
+  float* wv; float* dmv;  // [B, T, H, R] per query and item rank: w_m and dmass_m
+  int R;                  // <= kMixMaxRank
+  float* dmat;            // [B*H][n_items][D][D] d C^T (written)
+  float* dz;              // [B*H][n_items][D] d z (written)
+  int n_items;            // visible fines, or completed pages
+  int B, H, T, ft, keep, group;
+  int first_query;        // first token with this read (first_fine or first_coarse)
+};
+constexpr int kMixMaxRank = 64;      // items one query reads
+constexpr int kMixMaxItems = 512;    // fine ids a query block can select
+hipError_t launch_mix_bwd(const MixBwdParams& p, int head_dim, hipStream_t s);
+
+// d mass of the feature writers' fines [mats][D] in (fine, b, h) order:
+// dz_f / mass_f (z = r(log mass)) plus, for fines of the first `pages`
+// completed pages, the page descriptor's dpz_p / mass_p with mass_p the sum
+// of its fines' masses. dz: [B*H][fines][D]; dpz: [B*H][pages][D];
+// mass: [mats][D]; extra (nullable): a further d mass [mats][D] added.
+hipError_t launch_mass_grad(const float* dz, const float* dpz, const float* mass,
+                            const float* extra, float* dmass, int fines, int pages, int group,
+                            int B, int H, int head_dim, hipStream_t s);
+
+// Structured-Gram matrix adjoint (structured_writer.py:16-34 under
+// autograd): for `count_mats` matrices in (blk, b, h) order, from d C^T
+// ([e][d] per matrix) at the statistics (square [mats][D], cross
+// [mats][D][D] rows d, mass [mats][D], token count) to d square, d cross
+// [mats][d][e] and d mass.
+struct StructuredBwdParams {
+  const float* square; const float* cross; const float* mass;
+  const float* dct;       // matrix (blk, b, h) at [(b * H + h) * dct_cap + blk]
+  int dct_cap, B, H;
+  int count_mats;
+  float count;
+  float* dsquare; float* dcross; float* dmass;
+};
+hipError_t launch_structured_bwd(const StructuredBwdParams& p, int head_dim, hipStream_t s);
+// S = diag(2 dsquare) as [mats][D][D] (the block adjoint's U S term).
+hipError_t launch_square_diag(const float* dsquare, float* s_, int mats, int head_dim,
+                              hipStream_t st);
+// Adds each completed page's [pages * B][H][n] adjoint to its group fines'
+// ([fines * B][H][n], (fine, b, h) order).
+hipError_t launch_page_add(float* fine, const float* page, int pages, int group, int B, int H,
+                           int64_t n, hipStream_t s);
 
 // Feature-writer descriptors of `count` seals: matrix (blk, b, h) of the
 // mass scratch [count * B][H][D] gives fine slot first_slot + blk its

@@ -35,7 +35,7 @@ _VALUE_WRITERS = ("softmax", "regularized_association")
 
 
 # Writers with log-mass descriptors and the numerator-only mixture read
-# (tao_stream.py:80-123, 600-662): forward only.
+# (tao_stream.py:80-123, 600-662).
 _FEATURE_WRITERS = ("feature_mass_association", "structured_gram_association")
 
 
@@ -270,10 +270,6 @@ def _forward_for_backward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, conf
     pre-fusion coarse / fine heads and denominators. Returns (out, context
     for backward)."""
     _check(q, k, v, raw_q, raw_k, config)
-    if config.fine_writer not in _VALUE_WRITERS:
-        raise NotImplementedError(
-            f"gradients of the full-sequence read are implemented for the writers "
-            f"{_VALUE_WRITERS}")
     b, tokens, heads, d = q.shape
     ws = _Workspace(config, b, tokens, heads, d, q.device)
     q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
@@ -455,10 +451,6 @@ def full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
                 "the fp32 full-sequence read is forward-only: run it under torch.no_grad() "
                 "or on bf16 operands for gradients")
         return forward_f32(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config)
-    if grad and config.fine_writer in _FEATURE_WRITERS:
-        raise NotImplementedError(
-            "gradients through the feature writers are not built: run their full-sequence "
-            "read under torch.no_grad()")
     if local_flash is not None:
         from .flash_attention import plugin_training_local
         _check(q, k, v, raw_q, raw_k, config)

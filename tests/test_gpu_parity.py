@@ -696,6 +696,42 @@ def test_full_sequence_backward_regularized_writer(tokens, heads, width, seed, i
         assert (soft[i] - want[i]).norm() > 0.1 * want[i].norm()
 
 
+@pytest.mark.parametrize("writer,tokens,width,index_only,seed", [
+    ("feature_mass_association", 1300, 64, True, 71),
+    ("feature_mass_association", 2900, 128, False, 72),
+    ("structured_gram_association", 1300, 128, True, 73),
+    ("structured_gram_association", 3100, 64, False, 74)])
+def test_full_sequence_backward_feature_writers(writer, tokens, width, index_only, seed):
+    """tao_attention backward through the feature writers (index-only, and
+    with the page mixture past 2,560 tokens): the mixture reads' adjoints
+    (coefficients r(w_m h), w_m from h . exp(z_m)), z = log mass, the
+    association solve or the structured closed form of each block and page,
+    the feature softmax; every gradient against fp64 autograd of the
+    oracle's smooth forward at the bf16 forward's selections."""
+    from tao_attention import TaoConfig, tao_attention
+    heads = 2
+    xs, fa, fb = inputs(tokens, heads, width, seed)
+    cfg = TaoConfig(coarse_index_only=index_only, fine_writer=writer)
+    grad = torch.randn(xs[0].shape, generator=torch.Generator().manual_seed(seed + 100)).to(BF16)
+    dev = [x.cuda().requires_grad_(True) for x in xs]
+    fa_d = fa.cuda().requires_grad_(True)
+    fb_d = fb.cuda().requires_grad_(True)
+    print(f"{writer} backward T{tokens} H{heads} D{width} index_only={index_only}", flush=True)
+    out = tao_attention(*dev[:3], raw_q=dev[3], raw_k=dev[4], fusion_a=fa_d, fusion_b=fb_d,
+                        alpha=0.5, config=cfg)
+    got = torch.autograd.grad(out, dev + [fa_d, fb_d], grad.cuda())
+    _, routes = O.training_forward(*xs, fa, fb, 0.5, O.Geometry.from_config(cfg),
+                                   return_routes=True, writer=writer)
+    want = _reference_gradients(xs, fa, fb, grad, cfg, routes)
+    for g in got:
+        assert torch.isfinite(g.float()).all()
+    _compare_gradients(got, want, 5e-2)
+    soft = _reference_gradients(xs, fa, fb, grad, TaoConfig(coarse_index_only=index_only),
+                                routes)
+    for i in (2, 3, 4):                                 # v, raw_q, raw_k
+        assert (soft[i] - want[i]).norm() > 0.1 * want[i].norm()
+
+
 @pytest.mark.parametrize("tokens,heads,width,index_only,seed", [
     (2100, 2, 64, True, 48), (2900, 2, 128, False, 49)])
 def test_full_sequence_alpha_gradient(tokens, heads, width, index_only, seed):
@@ -749,18 +785,23 @@ def test_full_sequence_alpha_gradient(tokens, heads, width, index_only, seed):
     assert abs(d1.item() - fd) <= 1e-2 * abs(fd)
 
 
-@pytest.mark.parametrize("tokens,heads,width,index_only,seed", [
-    (2100, 2, 64, True, 46), (2900, 2, 128, False, 47)])
-def test_full_sequence_memory_adjoints_match_oracle(tokens, heads, width, index_only, seed):
+@pytest.mark.parametrize("writer,tokens,heads,width,index_only,seed", [
+    ("softmax", 2100, 2, 64, True, 46), ("softmax", 2900, 2, 128, False, 47),
+    ("feature_mass_association", 2100, 2, 128, True, 75),
+    ("structured_gram_association", 2900, 2, 64, False, 76)])
+def test_full_sequence_memory_adjoints_match_oracle(writer, tokens, heads, width, index_only,
+                                                    seed):
     """The memory branch's adjoints before the writer, d fine_z (segment
     weights, page weights, page / pending logsumexps, coarse weights and page
-    value matrices) and d C (selected read and coarse read), against fp64
-    autograd at the oracle's fine_z and bank: each path that the end-to-end
-    gradients cannot resolve (the page-weight softmax is ~0.2 % of d raw_k)
-    is a large part of these."""
+    value matrices; for the feature writers the mixture weights'
+    h . exp(z) path) and d C (selected read and coarse read; the mixture
+    read), against fp64 autograd at the oracle's fine_z and bank: each path
+    that the end-to-end gradients cannot resolve (the page-weight softmax is
+    ~0.2 % of d raw_k, the feature writers' descriptor path ~1 %) is a large
+    part of these."""
     from tao_attention import TaoConfig, training
     xs, fa, fb = inputs(tokens, heads, width, seed)
-    cfg = TaoConfig(coarse_index_only=index_only)
+    cfg = TaoConfig(coarse_index_only=index_only, fine_writer=writer)
     grad = torch.randn(xs[0].shape, generator=torch.Generator().manual_seed(seed + 100)).to(BF16)
     dev = to_dev(xs, "cuda")
     print(f"memory adjoints T{tokens} D{width} index_only={index_only}", flush=True)
@@ -768,11 +809,12 @@ def test_full_sequence_memory_adjoints_match_oracle(tokens, heads, width, index_
     mem = {}
     training.backward(data, grad.cuda(), fa.cuda(), fb.cuda(), 0.5, memory_adjoints=mem)
     geo = O.Geometry.from_config(cfg)
-    _, routes = O.training_forward(*xs, fa, fb, 0.5, geo, return_routes=True)
+    _, routes = O.training_forward(*xs, fa, fb, 0.5, geo, return_routes=True, writer=writer)
     leaves = [x.double() for x in xs]
     inter = {}
     out = O.training_forward_smooth(*leaves[:4], leaves[4].requires_grad_(True), fa.double(),
-                                    fb.double(), 0.5, routes, geo, intermediates=inter)
+                                    fb.double(), 0.5, routes, geo, intermediates=inter,
+                                    writer=writer)
     dz, dc = torch.autograd.grad((out * grad.double()).sum(), [inter["fine_z"], inter["bank"]])
     for name, got, want in (("dz", mem["dz"], dz), ("dc", mem["dc"], dc)):
         rel = ((got.cpu().double() - want).norm() / want.norm()).item()

@@ -551,6 +551,30 @@ def test_training_smooth_forward_is_the_rounded_forward(index_only, tokens):
         assert torch.isfinite(gr).all() and gr.abs().sum() > 0
 
 
+@pytest.mark.parametrize("writer", ["feature_mass_association", "structured_gram_association"])
+@pytest.mark.parametrize("index_only,tokens", [(True, 1400), (False, 2700)])
+def test_training_smooth_forward_feature_writers(writer, index_only, tokens):
+    """The feature writers' fp64 function (log-mass z, solve / structured
+    matrices, mixture reads) equals their bf16 forward to bf16 tolerance at
+    its selections (with the coarse mixture past first_coarse = 2560), and
+    autograd reaches every operand; the softmax writer's smooth function at
+    the same selections does not match (so the writer branch is taken)."""
+    xs, fa, fb = _stream_inputs(tokens, seed=13)
+    g = O.Geometry(coarse_index_only=index_only)
+    out, routes = O.training_forward(*xs, fa, fb, 0.5, g, return_routes=True, writer=writer)
+    leaves = [x.double().requires_grad_(True) for x in xs]
+    fa64, fb64 = fa.double().requires_grad_(True), fb.double().requires_grad_(True)
+    smooth = O.training_forward_smooth(*leaves, fa64, fb64, 0.5, routes, g, writer=writer)
+    torch.testing.assert_close(smooth.float(), out.float(), atol=3e-2, rtol=3e-2)
+    soft = O.training_forward_smooth(*(x.double() for x in xs), fa.double(), fb.double(), 0.5,
+                                     routes, g)
+    tail = slice(768, None)
+    assert (soft[:, tail] - smooth[:, tail].detach()).abs().max() > 0.1
+    grads = torch.autograd.grad(smooth.square().sum(), leaves + [fa64, fb64])
+    for gr in grads:
+        assert torch.isfinite(gr).all() and gr.abs().sum() > 0
+
+
 @pytest.mark.parametrize("tokens,index_only", [(1300, True), (2900, False)])
 def test_training_forward_fp32_matches_fp64_at_its_routes(tokens, index_only):
     """The fp32 semantics of tao_attention (every rounding point at fp32):

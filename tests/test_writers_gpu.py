@@ -423,7 +423,3 @@ def test_full_sequence_feature_writers(device, writer, width, tokens, batch, ind
     api = tao_attention(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.to(device),
                         fusion_b=fb.to(device), alpha=0.5, config=cfg)
     assert torch.equal(api, out)
-    qg = q.clone().requires_grad_()
-    with pytest.raises(NotImplementedError):
-        tao_attention(qg, k, v, raw_q=rq, raw_k=rk, fusion_a=fa.to(device),
-                      fusion_b=fb.to(device), alpha=0.5, config=cfg)

@@ -368,7 +368,12 @@ int tao_train_plan(const tao_stream_cfg* cfg, int64_t tokens, int64_t* plan,
  * through tao_attention: _fuse_training, operator.py:21-38; the local SDPA,
  * tao_stream.py:760-787; _SelectedRead.backward, selected_read.py:175-187;
  * the page / segment softmaxes and logsumexps, tao_stream.py:530-665; the
- * softmax writer, tao_stream.py:80-123). st, tok, fu and pools are the
+ * writers, tao_stream.py:80-123: softmax, regularized association through
+ * its solve, and the feature writers through their mixture reads
+ * (feature_read_coefficients and selected_fine_numerator,
+ * association_writer.py:46-53, indirect_fine.py:65-120), log-mass
+ * descriptors and the solve or structured closed form,
+ * structured_writer.py:16-34). st, tok, fu and pools are the
  * forward's tao_prefill arguments (same buffers, unchanged since), and the
  * forward was run with pools.local_lse / coarse_out / fine_out / den_out set
  * (local: its local-attention scratch). grad: upstream gradient bf16
@@ -386,7 +391,9 @@ typedef struct tao_train_bwd {
   void* workspace; size_t workspace_bytes;
   /* Optional (null = skip): the memory adjoints before the writer,
    * d fine_z fp32 [B][H][fines][D] and d C^T fp32 [B][H][fines][D][D]
-   * ([e][d], the bank's layout), for callers that inspect them. */
+   * ([e][d], the bank's layout), for callers that inspect them (feature
+   * writers: d fine_z of the fine mixture read; the page descriptors' share
+   * goes to the masses directly). */
   float* dz_out; float* dc_out;
   /* Optional (null = skip): fp32 [1] receives d out / d alpha . grad through
    * gain = 2 alpha (no reference counterpart: the reference takes alpha as a

@@ -275,11 +275,15 @@ def run_cold(torch, args, device, cfg, heads, width, context, n_states, probe):
     del xs
     snap = base.export()
     del base
+    # Every state is visited at least twice in the timed steps (a state's
+    # first visit after the warm-up pass would otherwise be its only one).
+    steps = max(args.steps // 2, 2 * n_states)
+    per_state = 2 * (steps // n_states + 2) + 2          # token rows both passes read
     states, toks = [], []
     g = torch.Generator(device=device).manual_seed(101)
     for j in range(n_states):
         states.append(StreamCache.from_export(snap))
-        toks.append([torch.randn((1, args.steps + 2, heads, width), generator=g,
+        toks.append([torch.randn((1, per_state, heads, width), generator=g,
                                  device=device).to(torch.bfloat16) for _ in range(5)])
     del snap
     torch.cuda.synchronize()
@@ -289,7 +293,6 @@ def run_cold(torch, args, device, cfg, heads, width, context, n_states, probe):
         _, states[j] = tao_attention_decode(q[:, :1], k[:, :1], v[:, :1], raw_q=rq[:, :1],
                                             raw_k=rk[:, :1], fusion_a=fa, fusion_b=fb,
                                             alpha=0.5, state=st, position=st.get_pos())
-    steps = args.steps // 2
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
@@ -936,10 +939,12 @@ def main():
             "kernel_us": round(cold_ms * 1e3, 3),
             "achieved_GBs": round(cold_bytes / (cold_ms * 1e-3) / 1e9, 1),
             "touched_bytes_per_cycle": int(cold_own * args.cold_states),
-            "note": "steps cycle through independent 128K states (no refresh in these steps); "
-                    "a cycle touches touched_bytes_per_cycle bytes (each state's ring window, "
-                    "folded route and records), above the 256 MB Infinity Cache when it "
-                    "exceeds 268435456"}
+            "timed_steps": steps, "visits_per_state": steps // args.cold_states,
+            "note": "timed steps cycle through independent 128K states (no refresh in these "
+                    "steps), each state visited visits_per_state times after a warm-up "
+                    "visit; a cycle touches touched_bytes_per_cycle bytes (each state's ring "
+                    "window, folded route and records), above the 256 MB Infinity Cache when "
+                    "it exceeds 268435456"}
         log(f"cold: {steps / cold_s:.1f} tok/s, kernel {cold_ms * 1e3:.2f} us")
         xs = None
     if not args.no_prefill:

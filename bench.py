@@ -229,6 +229,137 @@ def run_decode(torch, args, device, cfg, heads, width, context, seed, probe):
     return state, xs, fa, fb, seconds, graph, steps_bytes
 
 
+def run_timeline(torch, args, device, cfg, heads, width):
+    """Per-phase timeline of the decode step from the kernel's clock stamps.
+
+    The library's diagnostic recorder (tao_step_stamps) has every workgroup
+    of an eager decode step write the device's 100 MHz clock at entry, after
+    a local unit's scores (its window loads landed), after its record stores
+    issued, after their acknowledgement barrier, after its arrival count and,
+    for each head's last arrival, after the merge. The steps are the bench's
+    timed decode steps, launched back to back behind a bounded spin (as for
+    the step kernel's timing), from the same 128K state. Returns the summary
+    (medians over the steps of per-launch means, in microseconds)."""
+    import numpy as np
+    from tao_attention import _hip, new_state, tao_attention_decode
+    lib = _hip.lib()
+    context = args.context
+    total = context + args.warmup + args.steps
+    xs, fa, fb = make_tokens(torch, total, heads, width, 4, device)
+    state = new_state(0, cfg)
+    state._ingest(*(x[:, :context] for x in xs))
+    state, _ = decode_loop(torch, state, xs, fa, fb, context, args.warmup)
+    nloc, nfine = 768 // 64, width // 32          # local_units(128), fine_units(128)
+    grid_max = heads * (nloc + 2 * nfine)
+    words = grid_max * 8
+    buf = torch.zeros(args.steps, words, dtype=torch.int64, device=device)
+    _hip.check(lib.tao_step_stamps(buf.data_ptr(), args.steps, words))
+    q, k, v, rq, rk = xs
+    first = context + args.warmup
+    groups = []
+    i = first
+    try:
+        while i < first + args.steps:
+            torch.cuda._sleep(SPIN_CYCLES)
+            start = torch.cuda.Event(enable_timing=True)
+            start.record()
+            count = min(STEPS_PER_SPIN, first + args.steps - i)
+            launches0 = lib.tao_step_stamps_count()
+            for _ in range(count):
+                sl = slice(i, i + 1)
+                _, state = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
+                                                raw_k=rk[:, sl], fusion_a=fa, fusion_b=fb,
+                                                alpha=0.5, state=state,
+                                                position=state.get_pos())
+                i += 1
+            end = torch.cuda.Event(enable_timing=True)
+            end.record()
+            groups.append((start, end, launches0, lib.tao_step_stamps_count()))
+        torch.cuda.synchronize()
+        launches = lib.tao_step_stamps_count()
+    finally:
+        _hip.check(lib.tao_step_stamps(None, 0, 0))
+    if launches != args.steps:
+        raise RuntimeError(f"{launches} stamped launches for {args.steps} steps")
+    raw = buf.cpu().numpy().view(np.uint64).reshape(args.steps, grid_max, 8)
+    if args.timeline_raw:
+        np.save(args.timeline_raw, raw)
+    ticks_per_us = 100.0                             # s_memrealtime: 100 MHz
+    rows = []
+    for f in range(args.steps):
+        fr = raw[f]
+        live = fr[:, 0] != 0
+        fr = fr[live]
+        t = fr[:, :6].astype(np.int64)
+        j = (fr[:, 6] >> np.uint64(32)).astype(np.int64)
+        merged = t[:, 5] != 0
+        t0 = t[:, 0].min()
+        rows.append(dict(t=(t - t0) / ticks_per_us, j=j, merged=merged,
+                         start=t0, end=t[merged, 5].max(),
+                         xcc=(fr[:, 7] >> np.uint64(32)).astype(np.int64),
+                         smid=(fr[:, 7] & np.uint64(0xFFFFFFFF)).astype(np.int64)))
+    med = lambda xs: float(np.median(np.asarray(xs)))   # noqa: E731
+
+    def phase(sel_fn, a, b):
+        return round(med([np.mean(r["t"][sel_fn(r), b] - r["t"][sel_fn(r), a]) for r in rows]), 3)
+
+    local = lambda r: (r["j"] < nloc) & (r["t"][:, 1] != r["t"][:, 2])   # noqa: E731
+    empty = lambda r: (r["j"] < nloc) & (r["t"][:, 1] == r["t"][:, 2])   # noqa: E731
+    fine = lambda r: r["j"] >= nloc                                       # noqa: E731
+    merge = lambda r: r["merged"]                                         # noqa: E731
+    gaps = []
+    spans = []
+    for start, end, a, b in groups:
+        for f in range(a + 1, b):
+            gaps.append((int(rows[f]["start"]) - int(rows[f - 1]["end"])) / ticks_per_us)
+        spans.append(((int(rows[b - 1]["end"]) - int(rows[a]["start"])) / ticks_per_us,
+                      start.elapsed_time(end) * 1e3))
+    crit, crit_local = [], 0
+    for r in rows:
+        w = int(np.argmax(np.where(r["merged"], r["t"][:, 5], -1.0)))
+        crit.append(r["t"][w])
+        crit_local += int(r["j"][w] < nloc)
+    crit = np.asarray(crit)
+    cus = med([len(set(zip(r["xcc"].tolist(), r["smid"].tolist()))) for r in rows])
+    summary = {
+        "steps": args.steps, "grid": int(len(rows[0]["j"])),
+        "clock": "s_memrealtime at 100 MHz (10 ns ticks); medians over the steps of "
+                 "per-launch means",
+        "stamped_over_event_span": round(sum(a for a, _ in spans) / sum(b for _, b in spans), 4),
+        "kernel_span_us": round(med([(r["end"] - r["start"]) / ticks_per_us for r in rows]), 3),
+        "launch_gap_us": round(med(gaps), 3) if gaps else None,
+        "last_start_us": round(med([r["t"][:, 0].max() for r in rows]), 3),
+        "cus_used": cus,
+        "local_units": {"start_us": round(med([np.mean(r["t"][local(r), 0]) for r in rows]), 3),
+                        "loads_and_scores_us": phase(local, 0, 1),
+                        "softmax_values_record_us": phase(local, 1, 2),
+                        "store_ack_us": phase(local, 2, 3),
+                        "arrival_count_us": phase(local, 3, 4),
+                        "per_launch": round(med([local(r).sum() for r in rows]), 1)},
+        "empty_local_units": {"start_us": round(med([np.mean(r["t"][empty(r), 0])
+                                                     if empty(r).any() else 0.0
+                                                     for r in rows]), 3),
+                              "per_launch": round(med([empty(r).sum() for r in rows]), 1)},
+        "fine_units": {"start_us": round(med([np.mean(r["t"][fine(r), 0]) for r in rows]), 3),
+                       "read_and_record_us": phase(fine, 0, 2),
+                       "store_ack_us": phase(fine, 2, 3),
+                       "arrival_count_us": phase(fine, 3, 4),
+                       "per_launch": round(med([fine(r).sum() for r in rows]), 1)},
+        "merge": {"arrival_us": round(med([np.mean(r["t"][merge(r), 4]) for r in rows]), 3),
+                  "merge_us": phase(merge, 4, 5),
+                  "last_local_arrival_us": round(med([np.max(r["t"][local(r), 4])
+                                                      for r in rows]), 3),
+                  "last_fine_arrival_us": round(med([np.max(r["t"][fine(r), 4])
+                                                     for r in rows]), 3)},
+        "us_per_step_stamped": round(sum(b for _, b in spans) / args.steps, 3),
+        "critical_workgroup": {"local_unit_frac": round(crit_local / len(rows), 3),
+                               "start_us": round(float(np.median(crit[:, 0])), 3),
+                               "arrival_us": round(float(np.median(crit[:, 4])), 3),
+                               "end_us": round(float(np.median(crit[:, 5])), 3)},
+    }
+    return summary
+
+
 def graph_launch_floor(torch, device, launches=2000):
     """Host cost of one hipGraphLaunch on this runtime: torch.cuda.CUDAGraph
     replays of two one-kernel graphs (a 1,024-element add), alternating as
@@ -837,6 +968,12 @@ def main():
     ap.add_argument("--full-sequence-tokens", type=int, default=8192)
     ap.add_argument("--no-full-sequence", action="store_true")
     ap.add_argument("--no-writers", action="store_true")
+    ap.add_argument("--timeline", action="store_true",
+                    help="only the decode step's per-phase clock-stamp timeline (diagnostic: "
+                         "prints its summary as the JSON line instead of the bench result)")
+    ap.add_argument("--timeline-raw", default=None,
+                    help="with --timeline: also save the raw stamp frames (uint64 "
+                         "[steps, workgroups, 8]) to this .npy path")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB 4 times (a plain "
                          "copy kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -855,6 +992,12 @@ def main():
     cfg = index_only_page_memo(graph=False)
     heads, width = 32, 128
     probe = Probe(torch)
+    if args.timeline:
+        log("decode timeline: building 128K state")
+        summary = run_timeline(torch, args, device, cfg, heads, width)
+        print(json.dumps({"decode_timeline": summary, "context": args.context,
+                          "heads": heads, "head_dim": width}), flush=True)
+        return
 
     log("decode: building 128K state")
     state, xs, fa, fb, seconds, graph, steps_bytes = run_decode(

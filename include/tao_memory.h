@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 10
+#define TAO_ABI_VERSION 11
 
 enum tao_status {
   TAO_OK = 0,
@@ -325,6 +325,20 @@ int tao_graph_create(const tao_state_dev* st, const tao_fusion* fu,
                      void* stream, void** graph_out);
 int tao_graph_launch(void* graph, const tao_tokens* tok, void* stream);
 int tao_graph_destroy(void* graph);
+
+/* Diagnostic clock stamps of eager decode steps; no counterpart in the
+ * reference (it is for latency timelines of the single-launch step). While
+ * on, decode step i with a host cursor writes frame i % frames of buf
+ * (uint64, frame_words words per frame): per workgroup 8 words at
+ * blockIdx * 8, the device's 100 MHz clock (s_memrealtime) at entry, after
+ * a local unit's scores, after its record stores issued, after their
+ * acknowledgement barrier, after its arrival count, after the merge (the
+ * head's last arrival only, else 0), then (unit << 32 | batch * H + head)
+ * and (XCC << 32 | __smid()). A launch whose grid does not fit a frame records nothing.
+ * buf NULL turns it off; the count restarts at every call. Host state of
+ * the library, not thread-safe. */
+int tao_step_stamps(void* buf, int64_t frames, int64_t frame_words);
+int64_t tao_step_stamps_count(void);
 
 /* Streaming geometry of one request x layer (reference TaoConfig fields,
  * config.py:7-19, and the layer index that staggers route refreshes). */

@@ -1437,6 +1437,15 @@ int tao_graph_destroy(void* graph) {
   return check_hip(e, "tao_graph_destroy");
 }
 
+int tao_step_stamps(void* buf, int64_t frames, int64_t frame_words) {
+  if (tao::step_stamps_set(buf, frames, frame_words))
+    return fail(TAO_E_ARGUMENT, "tao_step_stamps: frames must be positive and frames of at "
+                                "least 8 words");
+  return TAO_OK;
+}
+
+int64_t tao_step_stamps_count(void) { return tao::step_stamps_count(); }
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------

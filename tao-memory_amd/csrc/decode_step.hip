@@ -237,10 +237,12 @@ __device__ void fine_read(const bf16_t* rq, int f, float* frec, float* hq, const
 // Workgroup j of one (request, head): j < NLOC local attention over keys
 // [j*K, (j+1)*K) of the window (workgroup 0 also appends the new token to
 // the ring), then NFINE fine-read workgroups (M > 0) and, with coarse_on,
-// NFINE coarse-read workgroups.
+// NFINE coarse-read workgroups. With `stamping` (diagnostic launches) a
+// local unit returns the device clock after its scores, other units 0.
 template <int D, int FDT>
-__device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int keep, int fine,
-                           int slot_stride, StepSmem<D>& sm, const CombineArgs* fuse, int h) {
+__device__ unsigned long long units_body(const StepReq& q, int j, int M, int coarse_on, int keep,
+                                         int fine, int slot_stride, StepSmem<D>& sm,
+                                         const CombineArgs* fuse, int h, bool stamping = false) {
   using G = Geo<D>;
   constexpr int STRIDE = D + kStepRec;
   float* recs = q.recs;
@@ -248,7 +250,7 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
     if (coarse_on)
       fine_read<D>(q.rq, j - G::NLOC - G::NFINE, recs + (G::NLOC + 1) * STRIDE, sm.wo[0],
                    q.coarse_g, nullptr);
-    return;
+    return 0ull;
   }
   if (j >= G::NLOC) {
     // Fine-read workgroup f; with `fuse`, its first kFineRows threads also
@@ -275,7 +277,7 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
       st_agent(recs + (G::NLOC + 3) * STRIDE + kStepRec + e, w.r1);
       st_agent(recs + (G::NLOC + 4) * STRIDE + kStepRec + e, w.r2);
     }
-    return;
+    return 0ull;
   }
   float* rec = recs + j * (D + kStepRec);
   const int tid = threadIdx.x, chn = tid % G::CH, r = tid / G::CH;
@@ -285,7 +287,7 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
   const int k0 = j * G::KEYS;
   if (k0 >= n) {   // past the window: an empty record
     if (tid == 0) { st_agent(&rec[0], -__builtin_inff()); st_agent(&rec[1], 0.0f); }
-    return;
+    return 0ull;
   }
   // Issue every load first: the new token's row for the ring append
   // (workgroup 0), KPT key and value rows, the q chunk.
@@ -329,6 +331,7 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
     sc[i] = row_sum<G::CH>(part) * scale2;
     if (k0 + r + i * G::ROWS >= n) sc[i] = -__builtin_inff();
   }
+  const unsigned long long scored = stamping ? __builtin_amdgcn_s_memrealtime() : 0ull;
   // Weights against the wave's maximum over its rows' keys (one value for
   // the whole wave, so no rescale inside it); a wave whose keys are all
   // past the window contributes nothing.
@@ -392,13 +395,15 @@ __device__ void units_body(const StepReq& q, int j, int M, int coarse_on, int ke
     q.ring_v[off + tid] = app_v;
     q.ring_raw[off + tid] = app_r;
   }
+  return scored;
 }
 
 // The units of one launch: per (batch, head) NLOC local-attention
 // workgroups (the window split by keys), NFINE fine-read workgroups and,
 // with coarse_on, NFINE coarse-read workgroups. Returns the (batch, head).
 template <int D, int FDT>
-__device__ int decode_units(const DecodeParams& p, int M, const CombineArgs& c) {
+__device__ int decode_units(const DecodeParams& p, int M, const CombineArgs& c,
+                            bool stamping, unsigned long long& scored) {
   using G = Geo<D>;
   __shared__ StepSmem<D> sm;
   const int per_head = G::NLOC + G::NFINE * (p.coarse_on ? 2 : 1);
@@ -426,22 +431,24 @@ __device__ int decode_units(const DecodeParams& p, int M, const CombineArgs& c) 
   } else {
     step_window(p.header[0], p.keep, p.fine, q.n_old, q.first_slot);
   }
-  units_body<D, FDT>(q, j, M, p.coarse_on, p.keep, p.fine, p.H * D, sm, &c, h);
+  scored = units_body<D, FDT>(q, j, M, p.coarse_on, p.keep, p.fine, p.H * D, sm, &c, h,
+                              stamping);
   return bh;
 }
 
-// The merge: thread group g = tid / COLS owns local records j = g
-// (mod 256 / COLS), channel dc = tid % COLS; the groups merge in ascending g
-// (fixed order), then the fine and coarse records and the fusion epilogue
-// give the output. The batched step runs it as its own kernel, one
+// The merge of one (request, head)'s records into its output channels and
+// the fusion epilogue. The batched step runs it as its own kernel, one
 // workgroup per (request, head, kCombineCols channels).
 constexpr int kCombineCols = 32;
 
-// COLS channels (from chunk * COLS) of one (request, head). The first COLS
-// threads own one channel each; the others only stage the records' maxima
-// and weight sums (m, l) in LDS. Each channel's local numerator sums the
-// records in index order, so the merge gives the same bits for any COLS:
-// the single-request step (COLS = D) and the batched combine kernel
+// COLS channels (from chunk * COLS) of one (request, head); the first COLS
+// threads own one channel each and the others return at once. An owner
+// loads every record's maximum and weight sum (m, l) itself (one address per
+// wave, so one request per wave) together with its channel's local sums,
+// the fine and coarse records and the fusion operands: one round of loads,
+// then registers only (no LDS, no barrier). Each channel's local numerator
+// sums the records in index order, so the merge gives the same bits for any
+// COLS: the single-request step (COLS = D) and the batched combine kernel
 // (COLS = kCombineCols) agree exactly. AGENT: the records were published by
 // other workgroups of the same launch (device-coherent loads). FDT: the
 // fusion parameters' dtype. Empty records (past the window) hold m = -inf
@@ -453,66 +460,58 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
   using Gm = Geo<D>;
   constexpr int STRIDE = D + kStepRec;
   constexpr int NLOC = Gm::NLOC;
-  static_assert(NLOC <= kThreads, "one thread stages each local record");
-  __shared__ float ml[NLOC][2];
   const int tid = threadIdx.x;
-  const bool owner = tid < COLS;
-  const int d = chunk * COLS + (owner ? tid : 0);
+  if (tid >= COLS) return;
+  const int d = chunk * COLS + tid;
   auto ld = [](const float* x) __attribute__((always_inline)) {
     return AGENT ? ld_agent(x) : *x;
   };
 
-  // Loads first: the records' (m, l), each channel's local sums, the fine
-  // and coarse records and the fusion operands.
-  if (tid < NLOC) {
-    ml[tid][0] = ld(recs + tid * STRIDE);
-    ml[tid][1] = ld(recs + tid * STRIDE + 1);
+  float m_j[NLOC], l_j[NLOC], o_j[NLOC];
+#pragma unroll
+  for (int j = 0; j < NLOC; ++j) {
+    m_j[j] = ld(recs + j * STRIDE);
+    l_j[j] = ld(recs + j * STRIDE + 1);
+    o_j[j] = ld(recs + j * STRIDE + kStepRec + d);
   }
-  float o_j[NLOC];
-  float num = 0.0f, den = 1.0f, craw = 0.0f;
+  // The fine, coarse and weight records are loaded whatever M and
+  // coarse_on say (every step's scratch holds them), so that no load waits
+  // behind a branch; values of records this step did not write are only
+  // ever discarded by selects below, never multiplied.
+  const float den_r = ld(recs + NLOC * STRIDE);
+  const float num_r = ld(recs + NLOC * STRIDE + kStepRec + d);
+  const float craw_r = ld(recs + (NLOC + 1) * STRIDE + kStepRec + d);
   float qx = 0.0f, fa3[3] = {}, fb3[3] = {};
   FuseWeights wts{};
-  if (owner) {
+  if (WEIGHTED) {
+    wts.r0 = ld(recs + (NLOC + 2) * STRIDE + kStepRec + d);
+    wts.r1 = ld(recs + (NLOC + 3) * STRIDE + kStepRec + d);
+    wts.r2 = ld(recs + (NLOC + 4) * STRIDE + kStepRec + d);
+  } else {
+    qx = bf2f(rq[d]);
 #pragma unroll
-    for (int j = 0; j < NLOC; ++j) o_j[j] = ld(recs + j * STRIDE + kStepRec + d);
-    if (M > 0) {
-      den = ld(recs + NLOC * STRIDE);
-      num = ld(recs + NLOC * STRIDE + kStepRec + d);
-    }
-    if (coarse_on) craw = ld(recs + (NLOC + 1) * STRIDE + kStepRec + d);
-    if (WEIGHTED) {
-      if (M > 0 || coarse_on) {
-        wts.r0 = ld(recs + (NLOC + 2) * STRIDE + kStepRec + d);
-        wts.r1 = ld(recs + (NLOC + 3) * STRIDE + kStepRec + d);
-        wts.r2 = ld(recs + (NLOC + 4) * STRIDE + kStepRec + d);
-      }
-    } else {
-      qx = bf2f(rq[d]);
-#pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        fa3[i] = param_at<FDT>(c.fa, h * c.fa_s[0] + d * c.fa_s[1] + i * c.fa_s[2]);
-        fb3[i] = param_at<FDT>(c.fb, h * c.fb_s[0] + d * c.fb_s[1] + i * c.fb_s[2]);
-      }
+    for (int i = 0; i < 3; ++i) {
+      fa3[i] = param_at<FDT>(c.fa, h * c.fa_s[0] + d * c.fa_s[1] + i * c.fa_s[2]);
+      fb3[i] = param_at<FDT>(c.fb, h * c.fb_s[0] + d * c.fb_s[1] + i * c.fb_s[2]);
     }
   }
-  __syncthreads();   // every thread: the (m, l) records are staged
-  if (!owner) return;
-  float top = ml[0][0];
+  float top = m_j[0];
 #pragma unroll
-  for (int j = 1; j < NLOC; ++j) top = fmaxf(top, ml[j][0]);
+  for (int j = 1; j < NLOC; ++j) top = fmaxf(top, m_j[j]);
   float den_local = 0.0f, nl = 0.0f;
 #pragma unroll
   for (int j = 0; j < NLOC; ++j) {
-    const float w = __builtin_amdgcn_exp2f(ml[j][0] - top);
-    den_local = fmaf(w, ml[j][1], den_local);
-    nl += ml[j][1] > 0.0f ? w * o_j[j] : 0.0f;
+    const float w = __builtin_amdgcn_exp2f(m_j[j] - top);
+    den_local = fmaf(w, l_j[j], den_local);
+    nl += l_j[j] > 0.0f ? w * o_j[j] : 0.0f;
   }
   const float local = rbf(nl / den_local);
   bf16_t result;
   if (M > 0 || coarse_on) {
-    const float fine_v = M > 0 ? rbf(rbf(num) / den) : 0.0f;
+    const float fine_v = M > 0 ? rbf(rbf(num_r) / den_r) : 0.0f;
+    const float coarse_v = coarse_on ? rbf(craw_r) : 0.0f;
     if (!WEIGHTED) wts = fuse_weights(qx, fa3, fb3, coarse_on ? 1 : 0, M > 0 ? 1 : 0);
-    result = fuse_mix(wts, local, rbf(craw), fine_v, c.gain);
+    result = fuse_mix(wts, local, coarse_v, fine_v, c.gain);
   } else {
     result = f2bf(local);
   }
@@ -528,9 +527,14 @@ __device__ void combine_body(const float* recs, const bf16_t* rq, bf16_t* out, i
 template <int D, int FDT>
 __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, int M) {
   __shared__ int last;
+  // Diagnostic clock stamps (p.stamps is null in production launches).
+  const bool stamping = p.stamps != nullptr;
+  const unsigned long long t0 = stamping ? __builtin_amdgcn_s_memrealtime() : 0ull;
   const int per_head = Geo<D>::NLOC + Geo<D>::NFINE * (p.coarse_on ? 2 : 1);
   const CombineArgs c = combine_args(p);
-  const int bh = decode_units<D, FDT>(p, M, c);
+  unsigned long long t1;
+  const int bh = decode_units<D, FDT>(p, M, c, stamping, t1);
+  const unsigned long long t2 = stamping ? __builtin_amdgcn_s_memrealtime() : 0ull;
   float* recs = p.parts + (size_t)bh * step_floats(D, p.sel_cap);
   unsigned* head_count = p.counters + (size_t)bh * kCounterStride;
   // Release of the records at agent scope without an L2 write-back: every
@@ -541,11 +545,28 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, i
   // barrier that orders its stores before thread 0's arrival count.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  const unsigned long long t3 = stamping ? __builtin_amdgcn_s_memrealtime() : 0ull;
   if (threadIdx.x == 0)
     last = __hip_atomic_fetch_add(head_count, 1u, __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT) == (unsigned)per_head - 1u;
   __syncthreads();
-  if (!last) return;
+  const unsigned long long t4 = stamping ? __builtin_amdgcn_s_memrealtime() : 0ull;
+  // The unit's stamp frame: its five stamps, the merge's end (the head's
+  // last arrival only), its identity and its placement.
+  auto stamp = [&](unsigned long long t5) __attribute__((always_inline)) {
+    if (!stamping || threadIdx.x != 0) return;
+    int u, j;
+    xcd_unit(blockIdx.x, p.B * p.H, per_head, u, j);
+    const unsigned xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20);   // XCC_ID[3:0]
+    ulonglong4* f = (ulonglong4*)(p.stamps + (size_t)blockIdx.x * kStampWords);
+    f[0] = make_ulonglong4(t0, t1 ? t1 : t2, t2, t3);   // fine units: no scores stamp
+    f[1] = make_ulonglong4(t4, t5, ((unsigned long long)j << 32) | (unsigned)u,
+                           ((unsigned long long)xcc << 32) | __smid());
+  };
+  if (!last) {
+    stamp(0ull);
+    return;
+  }
   if (threadIdx.x == 0)
     __hip_atomic_store(head_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int b = bh / p.H, h = bh % p.H;
@@ -567,6 +588,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeParams p, i
       p.header[0] = p.header[0] + 1;
     }
   }
+  if (stamping) stamp(__builtin_amdgcn_s_memrealtime());
 }
 
 // Batched step over R requests (one state each, batch 1): request r's token
@@ -763,6 +785,43 @@ hipError_t with_fusion_dtype(int dtype, F&& f) {
   return hipGetLastError();
 }
 
+namespace {
+
+// The diagnostic stamp recorder (host state; see step_stamps_set).
+struct StampRecorder {
+  unsigned long long* buf = nullptr;
+  long long frames = 0, frame_words = 0, launches = 0;
+};
+StampRecorder g_stamps;
+
+}  // namespace
+
+int step_stamps_set(void* buf, long long frames, long long frame_words) {
+  if (buf && (frames <= 0 || frame_words < kStampWords)) return -1;
+  g_stamps.buf = (unsigned long long*)buf;
+  g_stamps.frames = buf ? frames : 0;
+  g_stamps.frame_words = buf ? frame_words : 0;
+  g_stamps.launches = 0;
+  return 0;
+}
+
+long long step_stamps_count() { return g_stamps.launches; }
+
+namespace {
+
+// Stamp frame of the next eager launch of `units` workgroups (graph
+// captures and device-cursor steps record none), or null.
+unsigned long long* next_stamp_frame(const DecodeParams& p, unsigned units) {
+  if (!g_stamps.buf || p.pos_hint < 0) return nullptr;
+  if ((long long)units * kStampWords > g_stamps.frame_words) return nullptr;
+  unsigned long long* f =
+      g_stamps.buf + (size_t)(g_stamps.launches % g_stamps.frames) * g_stamps.frame_words;
+  ++g_stamps.launches;
+  return f;
+}
+
+}  // namespace
+
 hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStream_t s) {
   if (M < 0 || M > p.sel_cap) return hipErrorInvalidValue;
   if (p.keep + p.fine > kMaxWindow) return hipErrorInvalidValue;
@@ -779,6 +838,7 @@ hipError_t launch_decode_step(const DecodeParams& p, int head_dim, int M, hipStr
   }
   const int per_head = local_units(head_dim) + fine_units(head_dim) * (q.coarse_on ? 2 : 1);
   const dim3 units((unsigned)(q.B * q.H * per_head));
+  q.stamps = next_stamp_frame(q, units.x);
   return with_fusion_dtype(q.f_dtype, [&](auto fdt) {
     constexpr int FDT = decltype(fdt)::value;
     if (head_dim == 128)

@@ -92,7 +92,23 @@ struct DecodeParams {
   int B, H, keep, fine, group, fine_cap, page_cap, sel_cap;
   int coarse_on;
   int win_n_old, win_first;   // the window at pos_hint (set by launch_decode_step)
+  unsigned long long* stamps;   // diagnostic clock stamps of this launch (null: none;
+                                // set by launch_decode_step while a recorder is on)
 };
+
+// Words per workgroup of a decode step's stamp frame: the 100 MHz device
+// clock (s_memrealtime) at entry, after the loads of a local unit landed
+// (its scores), after the unit's record stores issued, after they were
+// acknowledged (the release barrier), after the arrival count, after the
+// merge (the head's last arrival only, else 0); then the unit's identity
+// (j << 32 | batch * H + head) and its placement (XCC << 32 | __smid()).
+constexpr int kStampWords = 8;
+
+// Diagnostic stamp recorder of eager decode steps (single-threaded use):
+// launch i with a host cursor writes frame i % frames of buf (frame_words
+// words each, at least grid * kStampWords). A null buf stops it.
+int step_stamps_set(void* buf, long long frames, long long frame_words);
+long long step_stamps_count();
 
 // M = selected fines of the current route (0 before the first seal: no
 // fine read). The fine read uses the folded route (launch_fold); with

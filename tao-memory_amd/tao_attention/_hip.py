@@ -146,6 +146,8 @@ _SIGNATURES = {
                           _vp, ctypes.POINTER(_vp)], _i32),
     "tao_graph_launch": ([_vp, ctypes.POINTER(Tokens), _vp], _i32),
     "tao_graph_destroy": ([_vp], _i32),
+    "tao_step_stamps": ([_vp, _i64, _i64], _i32),
+    "tao_step_stamps_count": ([], _i64),
     "tao_numerics_selftest": ([_i32, _vp, _vp, _i64, _vp], _i32),
     "tao_full_sequence_f32_workspace_bytes": ([_i32, _i32, _i32, _i64, _i32], _sz),
     "tao_full_sequence_f32": ([ctypes.POINTER(StreamCfg), ctypes.POINTER(Tokens),
@@ -172,7 +174,7 @@ _SIGNATURES = {
 
 EXPORTED = tuple(_SIGNATURES)
 
-ABI_VERSION = 10               # TAO_ABI_VERSION of include/tao_memory.h
+ABI_VERSION = 11               # TAO_ABI_VERSION of include/tao_memory.h
 
 # Decode-graph epoch counters (enum tao_graph_stat / tao_graph_reason).
 GRAPH_STATS = 19

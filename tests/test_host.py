@@ -71,7 +71,7 @@ def test_schedule_local_and_fines_follow_oracle_stream():
 
 def _header_functions():
     text = open(os.path.join(ROOT, "include", "tao_memory.h")).read()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(tao_\w+)\(",
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t|const char\*)\s+(tao_\w+)\(",
                                  text, flags=re.M)))
 
 
@@ -82,7 +82,7 @@ def test_library_exports_every_header_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert sorted(_hip.EXPORTED) == declared
-    assert lib.tao_abi_version() == _hip.ABI_VERSION == 10
+    assert lib.tao_abi_version() == _hip.ABI_VERSION == 11
 
 
 def test_workspace_size_and_error_convention():

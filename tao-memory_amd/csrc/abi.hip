@@ -5,6 +5,7 @@
 // translates the plain-pointer structs into kernel parameter blocks and owns
 // the only library-side resources: hipGraphExec objects of the decode step.
 #include <algorithm>
+#include <cstdlib>
 #include <string>
 
 #include "tao_launch.h"
@@ -723,10 +724,9 @@ int decode_replay(const DecodeParams& rec, const tao_tokens* tok, int head_dim,
                    "decode replay");
 }
 
-int fold_at(const tao_state_dev* st, int32_t selected, const TurnGate& gate, void* stream) {
-  int rc = check_state(st);
-  if (rc) return rc;
-  if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected count exceeds sel_cap");
+namespace {
+
+FoldParams fold_params(const tao_state_dev* st, int32_t selected, const TurnGate& gate) {
   FoldParams p{};
   p.bank = (const bf16_t*)st->bank_c;
   p.sw = (const bf16_t*)st->fine_sw;
@@ -742,14 +742,13 @@ int fold_at(const tao_state_dev* st, int32_t selected, const TurnGate& gate, voi
   p.sel_cap = st->sel_cap;
   p.M = selected;
   p.gate = gate;
-  return check_hip(launch_fold(p, st->head_dim, (hipStream_t)stream), "tao_fold_route");
+  return p;
 }
 
-int route_at(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
-             int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
-             const TurnGate& gate, void* stream) {
-  int rc = check_state(st);
-  if (rc) return rc;
+// Checks a single-turn route of the state and fills its parameters.
+int route_params(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
+                 int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
+                 const TurnGate& gate, RouteParams* out) {
   if (!raw_q_row || !rq_s) return fail(TAO_E_ARGUMENT, "null anchor query");
   const int fines = completed * st->coarse_group + pending;
   if (completed < 0 || pending < 0 || pending >= st->coarse_group || fines <= 0)
@@ -785,7 +784,50 @@ int route_at(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s
   p.coarse = coarse;
   p.selected = selected;
   p.gate = gate;
+  *out = p;
+  return TAO_OK;
+}
+
+}  // namespace
+
+int fold_at(const tao_state_dev* st, int32_t selected, const TurnGate& gate, void* stream) {
+  int rc = check_state(st);
+  if (rc) return rc;
+  if (selected < 0 || selected > st->sel_cap) return fail(TAO_E_CAPACITY, "selected count exceeds sel_cap");
+  return check_hip(launch_fold(fold_params(st, selected, gate), st->head_dim, (hipStream_t)stream),
+                   "tao_fold_route");
+}
+
+int route_at(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
+             int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
+             const TurnGate& gate, void* stream) {
+  int rc = check_state(st);
+  if (rc) return rc;
+  RouteParams p;
+  rc = route_params(st, raw_q_row, rq_s, completed, pending, coarse, selected, gate, &p);
+  if (rc) return rc;
   return check_hip(launch_route(p, st->head_dim, (hipStream_t)stream), "tao_route");
+}
+
+int refresh_fold_at(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
+                    int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
+                    const TurnGate& gate, void* stream) {
+  int rc = check_state(st);
+  if (rc) return rc;
+  RouteParams p;
+  rc = route_params(st, raw_q_row, rq_s, completed, pending, coarse, selected, gate, &p);
+  if (rc) return rc;
+  const FoldParams f = fold_params(st, selected, gate);
+  // TAO_REFRESH_FOLD=0 keeps the two launches (the fused kernel computes the
+  // same route and fold; the switch exists to compare them).
+  const char* env = getenv("TAO_REFRESH_FOLD");
+  hipError_t e = hipErrorNotSupported;
+  if (!(env && env[0] == '0')) e = launch_refresh_fold(p, f, st->head_dim, (hipStream_t)stream);
+  if (e == hipErrorNotSupported) {
+    e = launch_route(p, st->head_dim, (hipStream_t)stream);
+    if (e == hipSuccess) e = launch_fold(f, st->head_dim, (hipStream_t)stream);
+  }
+  return check_hip(e, "route refresh");
 }
 
 }  // namespace tao

@@ -369,12 +369,17 @@ TAO_DEV float staged_masses(const float* h, const bf16_t* const* pw_rows,
   return mine;
 }
 
-template <int D>
-__global__ __launch_bounds__(kRefreshThreads) void route_refresh_kernel(RouteParams p) {
-  __shared__ RefreshSmem<D> sm;
-  if (gate_closed(p.gate)) return;   // uniform: every thread reads one header word
+// The refresh's selection for (batch, head) bh by a workgroup of NT
+// threads: the route of RouteParams' single turn, left in LDS (sm.top: the
+// selected candidates' keys, best first; sm.chosen: the chosen pages,
+// ascending; sm.pw / sm.sw: the page weights and the candidates' segment
+// weights). Each mass is a butterfly sum inside one wave, so the result does
+// not depend on NT. With `write_out` the selection is also stored in the
+// state (sel, chosen; header[1] by head 0).
+template <int D, int NT>
+TAO_DEV void refresh_select(const RouteParams& p, int bh, RefreshSmem<D>& sm, bool write_out) {
   constexpr int C16 = D / 8;            // 16-byte chunks per row
-  const int bh = blockIdx.x;
+  constexpr int NW = NT / 64;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int K = p.completed, pending = p.pending, coarse = p.coarse, selected = p.selected;
@@ -385,27 +390,41 @@ __global__ __launch_bounds__(kRefreshThreads) void route_refresh_kernel(RoutePar
   const bf16_t* sw = p.sw + (size_t)bh * p.fine_cap * D;
   // ---- round trip 1: page weights, pending segment weights, anchor query
   // (every load issued before any store to LDS)
-  constexpr int PW_PT = (kRefreshPages * C16 + kRefreshThreads - 1) / kRefreshThreads;
-  constexpr int SW_PT = (kRefreshRows * C16 + kRefreshThreads - 1) / kRefreshThreads;
+  constexpr int PW_PT = (kRefreshPages * C16 + NT - 1) / NT;
+  constexpr int SW_PT = (kRefreshRows * C16 + NT - 1) / NT;
+  constexpr int PD_PT = (8 * C16 + NT - 1) / NT;   // pending fines: fewer than 8 rows
   // Loads are unconditional (indices clamped to a valid row) so the
   // scheduler can issue them all before the guarded LDS stores.
+  uint4 pwv[PW_PT], pdv[PD_PT];
 #pragma unroll
   for (int k = 0; k < PW_PT; ++k) {
-    const int i = tid + k * kRefreshThreads;
-    const int ic = min(i, P * C16 - 1);
-    const uint4 v = *(const uint4*)(pw + (size_t)(ic / C16) * D + (ic % C16) * 8);
-    if (i < P * C16) *(uint4*)&sm.pw[i / C16][(i % C16) * 8] = v;
+    const int ic = min(tid + k * NT, P * C16 - 1);
+    pwv[k] = *(const uint4*)(pw + (size_t)(ic / C16) * D + (ic % C16) * 8);
   }
   if (pending > 0) {
-    const int ic = min(tid, pending * C16 - 1);
-    const uint4 v = *(const uint4*)(sw + (size_t)(K * group + ic / C16) * D + (ic % C16) * 8);
-    if (tid < pending * C16) *(uint4*)&sm.sw[group * coarse + tid / C16][(tid % C16) * 8] = v;
+#pragma unroll
+    for (int k = 0; k < PD_PT; ++k) {
+      const int ic = min(tid + k * NT, pending * C16 - 1);
+      pdv[k] = *(const uint4*)(sw + (size_t)(K * group + ic / C16) * D + (ic % C16) * 8);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < PW_PT; ++k) {
+    const int i = tid + k * NT;
+    if (i < P * C16) *(uint4*)&sm.pw[i / C16][(i % C16) * 8] = pwv[k];
+  }
+  if (pending > 0) {
+#pragma unroll
+    for (int k = 0; k < PD_PT; ++k) {
+      const int i = tid + k * NT;
+      if (i < pending * C16) *(uint4*)&sm.sw[group * coarse + i / C16][(i % C16) * 8] = pdv[k];
+    }
   }
   if (wave == 0) query_weights<D>(p.rq + b * p.rq_sb + h * p.rq_sh, lane, sm.h);
   __syncthreads();
   // ---- coarse pages: stable top-`coarse` by page mass, then ascending
   if (coarse > 0) {
-    for (int base = wave * kRefreshRowsPerWave; base < K; base += kRefreshWaves * kRefreshRowsPerWave) {
+    for (int base = wave * kRefreshRowsPerWave; base < K; base += NW * kRefreshRowsPerWave) {
       const int count = min(kRefreshRowsPerWave, K - base);
       const bf16_t* rows[kRefreshRowsPerWave];
 #pragma unroll
@@ -414,7 +433,7 @@ __global__ __launch_bounds__(kRefreshThreads) void route_refresh_kernel(RoutePar
       if (lane < count) sm.keys[base + lane] = score_key(mass, base + lane);
     }
     __syncthreads();
-    select_top_n<kRefreshThreads>(sm.keys, K, coarse, sm.top);
+    select_top_n<NT>(sm.keys, K, coarse, sm.top);
     if (tid < coarse) {
       const int mine = key_index(sm.top[tid]);
       int rank = 0;
@@ -423,19 +442,23 @@ __global__ __launch_bounds__(kRefreshThreads) void route_refresh_kernel(RoutePar
     }
     __syncthreads();
     // ---- round trip 2: segment weights of the chosen pages' fines
+    uint4 swv[SW_PT];
 #pragma unroll
     for (int k = 0; k < SW_PT; ++k) {
-      const int i = tid + k * kRefreshThreads;
-      const int ic = min(i, group * coarse * C16 - 1);
+      const int ic = min(tid + k * NT, group * coarse * C16 - 1);
       const int row = ic / C16;
       const int id = sm.chosen[row / group] * group + row % group;
-      const uint4 v = *(const uint4*)(sw + (size_t)id * D + (ic % C16) * 8);
-      if (i < group * coarse * C16) *(uint4*)&sm.sw[i / C16][(i % C16) * 8] = v;
+      swv[k] = *(const uint4*)(sw + (size_t)id * D + (ic % C16) * 8);
+    }
+#pragma unroll
+    for (int k = 0; k < SW_PT; ++k) {
+      const int i = tid + k * NT;
+      if (i < group * coarse * C16) *(uint4*)&sm.sw[i / C16][(i % C16) * 8] = swv[k];
     }
     __syncthreads();
   }
   // ---- candidate masses: 8 fines of each chosen page, then the pending fines
-  for (int base = wave * kRefreshRowsPerWave; base < E; base += kRefreshWaves * kRefreshRowsPerWave) {
+  for (int base = wave * kRefreshRowsPerWave; base < E; base += NW * kRefreshRowsPerWave) {
     const int count = min(kRefreshRowsPerWave, E - base);
     const bf16_t* prow[kRefreshRowsPerWave];
     const bf16_t* srow[kRefreshRowsPerWave];
@@ -449,16 +472,94 @@ __global__ __launch_bounds__(kRefreshThreads) void route_refresh_kernel(RoutePar
     if (lane < count) sm.keys[base + lane] = score_key(mass, base + lane);
   }
   __syncthreads();
-  select_top_n<kRefreshThreads>(sm.keys, E, selected, sm.top);
+  select_top_n<NT>(sm.keys, E, selected, sm.top);
+  if (!write_out) return;
   int32_t* sel_out = p.sel + (size_t)bh * p.sel_cap;
-  for (int m = tid; m < selected; m += kRefreshThreads) {
+  for (int m = tid; m < selected; m += NT) {
     const int j = key_index(sm.top[m]);
     sel_out[m] = j < group * coarse ? sm.chosen[j / group] * group + j % group
                                     : K * group + (j - group * coarse);
   }
-  for (int i = tid; i < coarse; i += kRefreshThreads)
+  for (int i = tid; i < coarse; i += NT)
     p.chosen[(size_t)bh * p.chosen_cap + i] = sm.chosen[i];
   if (bh == 0 && tid == 0) p.header[1] = selected;
+}
+
+template <int D>
+__global__ __launch_bounds__(kRefreshThreads) void route_refresh_kernel(RouteParams p) {
+  __shared__ RefreshSmem<D> sm;
+  if (gate_closed(p.gate)) return;   // uniform: every thread reads one header word
+  refresh_select<D, kRefreshThreads>(p, blockIdx.x, sm, true);
+}
+
+// Route refresh and fold in one launch: the fold's CHUNKS workgroups of a
+// (batch, head) each compute the head's selection (refresh_select on 16
+// waves; the same arithmetic gives every workgroup the same route, and
+// chunk 0 stores it), then fold their ROWS rows of G^T over the selected
+// fines with fold_kernel's arithmetic and order: in slot order m, w_m[d] =
+// pw[page(m)][d] * sw[m][d] (from the rows the selection staged in LDS,
+// kRefreshFoldStage slots at a time), G^T[e][d] += w_m[d] * C^T_m[e][d] as
+// one fp32 FMA, g[d] += w_m[d]. Thread (row, column pair) loads 4 bytes of
+// each selected C^T row, so a wave reads one 256-byte row per slot. One
+// launch instead of two removes a launch gap and the fold's wait for the
+// route kernel's last workgroup.
+constexpr int kRefreshFoldStage = 36;
+
+template <int D>
+__global__ __launch_bounds__(kRefreshThreads) void refresh_fold_kernel(RouteParams p,
+                                                                        FoldParams f) {
+  constexpr int NT = kRefreshThreads;
+  constexpr int CP = D / 2, ROWS = NT / CP, CHUNKS = D / ROWS, U = kRefreshFoldStage;
+  constexpr int group = 8;
+  __shared__ RefreshSmem<D> sm;
+  __shared__ float wts[U][D];
+  __shared__ int slot_id[U];
+  if (gate_closed(p.gate)) return;   // uniform: every thread reads one header word
+  int bh, e_chunk;
+  xcd_unit(blockIdx.x, p.B * p.H, CHUNKS, bh, e_chunk);
+  refresh_select<D, NT>(p, bh, sm, e_chunk == 0);
+  const int tid = threadIdx.x, cp = tid % CP, r = tid / CP;
+  const int e = e_chunk * ROWS + r;
+  const int K = p.completed, coarse = p.coarse, M = p.selected;
+  const bf16_t* bank = f.bank + (size_t)bh * f.fine_cap * D * D;
+  float acc0 = 0.0f, acc1 = 0.0f, den0 = 0.0f, den1 = 0.0f;
+  for (int s0 = 0; s0 < M; s0 += U) {
+    const int staged = min(U, M - s0);
+    __syncthreads();                  // the previous stage is consumed (or the selection done)
+    if (tid < staged) {
+      const int j = key_index(sm.top[s0 + tid]);
+      slot_id[tid] = j < group * coarse ? sm.chosen[j / group] * group + j % group
+                                        : K * group + (j - group * coarse);
+    }
+    __syncthreads();
+    // The stage's C^T loads first, then its weights (slot u's page row and
+    // candidate row, both staged) while the loads are in flight.
+    uint32_t cv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int m = min(u, staged - 1);
+      cv[u] = *(const uint32_t*)(bank + ((size_t)slot_id[m] * D + e) * D + cp * 2);
+    }
+    for (int i = tid; i < staged * D; i += NT) {
+      const int u = i / D, d = i % D;
+      const int j = key_index(sm.top[s0 + u]);
+      const int prow = j < group * coarse ? sm.chosen[j / group] : K;
+      wts[u][d] = bf2f(sm.pw[prow][d]) * bf2f(sm.sw[j][d]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (u < staged) {
+        const float2 w = *(const float2*)&wts[u][cp * 2];
+        acc0 = fmaf(w.x, __uint_as_float(cv[u] << 16), acc0);
+        acc1 = fmaf(w.y, __uint_as_float(cv[u] & 0xFFFF0000u), acc1);
+        den0 += w.x;
+        den1 += w.y;
+      }
+    }
+  }
+  *(float2*)(f.fold_g + ((size_t)bh * D + e) * D + cp * 2) = make_float2(acc0, acc1);
+  if (e == 0) *(float2*)(f.fold_den + (size_t)bh * D + cp * 2) = make_float2(den0, den1);
 }
 
 // ---------------------------------------------------------------------------
@@ -921,6 +1022,29 @@ hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s) {
     hipLaunchKernelGGL(route_kernel<64>, grid, dim3(kRouteThreads), 0, s, p);
   else
     return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// The refresh and its fold in one launch when the route fits the staged
+// refresh (single turn, group 8, rows within kRefreshPages / kRefreshRows);
+// returns hipErrorNotSupported otherwise (the caller launches the two).
+hipError_t launch_refresh_fold(const RouteParams& p, const FoldParams& f, int head_dim,
+                               hipStream_t s) {
+  const int pages = p.completed + (p.pending > 0 ? 1 : 0);
+  if (p.turns || pages > kRefreshPages || p.group * p.coarse + p.pending > kRefreshRows ||
+      p.group != 8 || f.group != 8 || p.selected != f.M || p.selected <= 0)
+    return hipErrorNotSupported;
+  if (head_dim == 128) {
+    constexpr int CHUNKS = 128 / (kRefreshThreads / 64);
+    hipLaunchKernelGGL(refresh_fold_kernel<128>, dim3((unsigned)(p.B * p.H * CHUNKS)),
+                       dim3(kRefreshThreads), 0, s, p, f);
+  } else if (head_dim == 64) {
+    constexpr int CHUNKS = 64 / (kRefreshThreads / 32);
+    hipLaunchKernelGGL(refresh_fold_kernel<64>, dim3((unsigned)(p.B * p.H * CHUNKS)),
+                       dim3(kRefreshThreads), 0, s, p, f);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

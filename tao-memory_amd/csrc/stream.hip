@@ -139,9 +139,9 @@ int pre_step(Stream* s, const tao_tokens* tok, void* stream, int* refreshed) {
     tao::sched::routed_counts(c, completed, pending, &coarse64, &eligible, &selected64);
     const int32_t coarse = (int32_t)coarse64, selected = (int32_t)selected64;
     const int64_t rq_s[2] = {tok->rq_s[0], tok->rq_s[2]};
-    int rc = tao_route(&s->st, tok->raw_q, rq_s, (int32_t)completed, (int32_t)pending, coarse,
-                       selected, stream);
-    if (!rc) rc = tao_fold_route(&s->st, selected, stream);
+    const int rc = tao::refresh_fold_at(&s->st, tok->raw_q, rq_s, (int32_t)completed,
+                                        (int32_t)pending, coarse, selected, tao::TurnGate{},
+                                        stream);
     if (rc) return rc;
     s->route_coarse = coarse;
     s->route_size = selected;
@@ -427,10 +427,10 @@ int tao_stream_graph_step(void* handle, const tao_tokens* tok, const tao_fusion*
     const tao::TurnGate gate{s->st.header, (long long)first_turn(c), (long long)c.route_period,
                              (long long)serve_limit(c)};
     const int64_t rq_s[2] = {tok->rq_s[0], tok->rq_s[2]};
-    int rc = tao::route_at(&s->st, tok->raw_q, rq_s, (int32_t)(fines / c.coarse_group),
-                           (int32_t)(fines % c.coarse_group), s->route_coarse, s->route_size,
-                           gate, stream);
-    if (!rc) rc = tao::fold_at(&s->st, s->route_size, gate, stream);
+    const int rc = tao::refresh_fold_at(&s->st, tok->raw_q, rq_s,
+                                        (int32_t)(fines / c.coarse_group),
+                                        (int32_t)(fines % c.coarse_group), s->route_coarse,
+                                        s->route_size, gate, stream);
     if (rc) return rc;
   }
   const tao_fusion f = step_fusion(s, *fu, pos);

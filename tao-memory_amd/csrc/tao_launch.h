@@ -197,6 +197,11 @@ int route_at(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s
              int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
              const TurnGate& gate, void* stream);
 int fold_at(const tao_state_dev* st, int32_t selected, const TurnGate& gate, void* stream);
+// route_at then fold_at of the same route, as one launch where the route
+// fits the fused kernel (launch_refresh_fold).
+int refresh_fold_at(const tao_state_dev* st, const void* raw_q_row, const int64_t* rq_s,
+                    int32_t completed, int32_t pending, int32_t coarse, int32_t selected,
+                    const TurnGate& gate, void* stream);
 
 // The decode step's kernel arguments for a state, fusion and output buffer,
 // recorded once (decode_record) and dispatched per token with that token's
@@ -262,6 +267,11 @@ struct RouteParams {
   TurnGate gate;                 // single-turn mode only
 };
 hipError_t launch_route(const RouteParams& p, int head_dim, hipStream_t s);
+// A single-turn route refresh and its fold in one launch (both parameter
+// sets describe the same state and route size); hipErrorNotSupported when
+// the route does not fit the fused kernel.
+hipError_t launch_refresh_fold(const RouteParams& p, const FoldParams& f, int head_dim,
+                               hipStream_t s);
 
 // Per-query routes of the full-sequence read: every history query of a read
 // tile routes itself against its tile's epoch; selections are bitmasks

@@ -124,6 +124,33 @@ def test_decode_matches_oracle_across_seal_and_refresh(device):
     compare_diagnostics(state, ora)
 
 
+@pytest.mark.parametrize("heads,width", [(4, 128), (2, 64)])
+def test_fused_refresh_fold_equals_two_launches(device, monkeypatch, heads, width):
+    """The route refresh and its fold as one launch give the same route ids
+    and the same outputs, bit for bit, as the route kernel followed by the
+    fold kernel, through refreshes with completed pages (coarse selection)
+    and a seal."""
+    xs, fa, fb = inputs(4700, heads, width, seed=17, unit_raw_k=True)
+    d = to_dev(xs, device)
+    fa_d, fb_d = fa.to(device), fb.to(device)
+    splits = [4600] + [1] * 100          # 4 refreshes and the seal at position 4607
+    print(f"fused refresh+fold H{heads} D{width}", flush=True)
+    runs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("TAO_REFRESH_FOLD", mode)
+        state = new_state(2, index_only_page_memo(graph=False))
+        out = run_hip(state, d, fa_d, fb_d, splits)
+        runs[mode] = (out, state.export())
+    assert torch.equal(runs["0"][0], runs["1"][0])
+    for a, b in zip(runs["0"][1]["route_ids"], runs["1"][1]["route_ids"]):
+        assert torch.equal(a, b)
+    assert runs["1"][1]["route_ids"][0].numel() > 0, "coarse selection must be active"
+    ora, ref = run_oracle(2, xs, fa, fb, splits,
+                          geometry=O.Geometry.from_config(index_only_page_memo()))
+    torch.testing.assert_close(runs["1"][0].cpu().float(), ref.float(), **TOL)
+    compare_snapshots(runs["1"][1], ora.export())
+
+
 def test_chunked_prefill_and_page_routing(device):
     """Arbitrary chunking plus completed pages (coarse selection active)."""
     heads, width = 2, 64

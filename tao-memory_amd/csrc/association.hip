@@ -13,10 +13,12 @@
 //   matmul. mass = sum_t u and square_mass = sum_t u^2 are per-channel fp32
 //   sums over the staged rows.
 // association_solve_kernel (association_writer.py:21-32): one workgroup per
-//   [D, D] pair. The system gram + (trace / D) I is factored in LDS by a
-//   blocked right-looking Cholesky (8-column panels factored by one wave,
-//   rank-8 trailing updates by all threads), then cross is solved in place by
-//   forward and back substitution, 8 rows a step; C = bf16(X).
+//   [D, D] pair, loaded in one round of float4 loads. The system
+//   gram + (trace / D) I is factored in LDS by a blocked right-looking
+//   Cholesky (16-column panels: the diagonal block by one wave in
+//   registers, the rows below it one thread each, rank-16 trailing updates
+//   on 4 x 4 register tiles), then cross is solved in place by forward and
+//   back substitution, 16 rows a step with 4 x 4 tiles; C = bf16(X).
 // structured_matrix_kernel (structured_writer.py:16-34): one workgroup per
 //   pair; per-channel vectors and their sums in LDS, then thread e walks
 //   column e of cross twice (hb and mass . hb, then the result).
@@ -183,14 +185,31 @@ __global__ __launch_bounds__(kStatThreads) void writer_stats_kernel(WriterStatsP
   }
 }
 
-constexpr int kSolveThreads = 1024;   // one workgroup per CU at D128 (132 KB LDS): 16 waves
+constexpr int kSolveThreads = 1024;   // one workgroup per CU at D128 (135 KB LDS): 16 waves
+constexpr int kSolvePanel = 16;       // Cholesky panel width and substitution block
 
 template <int D>
 struct SolveSmem {
-  float a[D][D + 1];     // system, then its lower factor
-  float x[D][D + 1];     // cross, then Y, then X
+  float a[D][D + 4];     // system, then its lower factor (rows 16-byte aligned)
+  float x[D][D + 4];     // cross, then Y, then X
+  float inv[D];          // reciprocal square roots of the pivots (1 / L[j][j])
   float red[kSolveThreads / 64];
 };
+
+TAO_DEV float read_lane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// acc[i] -= l[i] * r (componentwise), as one fp32 FMA per element.
+TAO_DEV void sub_outer(float4 (&acc)[4], const float (&l)[4], const float4& r) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc[i].x = fmaf(-l[i], r.x, acc[i].x);
+    acc[i].y = fmaf(-l[i], r.y, acc[i].y);
+    acc[i].z = fmaf(-l[i], r.z, acc[i].z);
+    acc[i].w = fmaf(-l[i], r.w, acc[i].w);
+  }
+}
 
 template <int D>
 __global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocSolveParams p) {
@@ -207,73 +226,149 @@ __global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocS
     const int b = (mat / p.H) % p.B, h = mat % p.H;
     rt = p.rhs_t + (((size_t)b * p.H + h) * p.rhs_cap + blk) * D * D;
   }
-  // ridge = trace / D
-  float tr = 0.0f;
-  for (int i = tid; i < D; i += kSolveThreads) tr += g[(size_t)i * D + i];
-  tr = wave_sum_fold(tr);
+  // Every load of the system in one round: the diagonal (for the ridge),
+  // then gram and the right-hand side as float4 (rows of D floats).
+  constexpr int V4 = D * D / 4 / kSolveThreads;   // float4 per thread and matrix
+  static_assert(D * D % (4 * kSolveThreads) == 0, "whole float4 per thread");
+  const float gd = tid < D ? g[(size_t)tid * D + tid] : 0.0f;
+  float4 gv[V4], cv[V4];
+#pragma unroll
+  for (int k = 0; k < V4; ++k) {
+    const int i4 = tid + k * kSolveThreads;
+    gv[k] = ((const float4*)g)[i4];
+    cv[k] = ((const float4*)(rt ? rt : c))[i4];
+  }
+#pragma unroll
+  for (int k = 0; k < V4; ++k) {
+    const int i = 4 * (tid + k * kSolveThreads), r = i / D, col = i % D;
+    *(float4*)&sm.a[r][col] = gv[k];
+    if (rt) {   // rt[e][d] with e = r, d = col .. col + 3: x[d][e]
+      sm.x[col][r] = cv[k].x;
+      sm.x[col + 1][r] = cv[k].y;
+      sm.x[col + 2][r] = cv[k].z;
+      sm.x[col + 3][r] = cv[k].w;
+    } else {
+      *(float4*)&sm.x[r][col] = cv[k];
+    }
+  }
+  // ridge = trace / D, added to the staged diagonal
+  const float tr = wave_sum_fold(gd);
   if ((tid & 63) == 0) sm.red[tid >> 6] = tr;
   __syncthreads();
   float trace = 0.0f;
 #pragma unroll
   for (int i = 0; i < kSolveThreads / 64; ++i) trace += sm.red[i];
   const float ridge = trace / (float)D;
-  for (int i = tid; i < D * D; i += kSolveThreads) {
-    const int r = i / D, col = i % D;
-    sm.a[r][col] = g[i] + (r == col ? ridge : 0.0f);
-    sm.x[r][col] = rt ? rt[(size_t)col * D + r] : c[i];
-  }
-  // Blocked right-looking Cholesky, PB columns a step: wave 0 factors the
-  // panel (rows >= jb, wave-synchronous), then all threads apply its rank-PB
-  // update to the trailing lower triangle; two workgroup barriers a panel.
-  constexpr int PB = 8;
+  if (tid < D) sm.a[tid][tid] = gd + ridge;
+  // Blocked right-looking Cholesky, PB columns a step. Wave 0 factors the
+  // panel's PB x PB diagonal block in registers (lane l holds row jb + l;
+  // the pivot and the multipliers L[jb + c2][j] come from their lanes by
+  // readlane); then thread t solves row jb + PB + t of the panel against
+  // it, column by column; then every thread applies the rank-PB update to
+  // 4 x 4 tiles of the trailing lower triangle from float4 rows (the upper
+  // triangle is never read, so diagonal tiles are updated whole). Each
+  // element sees the operations of the unblocked factorization in the same
+  // order: one fp32 FMA per earlier column, in column order, then the
+  // scaling by its column's pivot. Pivots are taken by v_rsq_f32 (about
+  // 1 ulp): L[j][j] = pivot * rsq(pivot), and every division by L[j][j],
+  // here and in the substitutions, is a product with rsq(pivot) (kept in
+  // sm.inv); these ulp-level differences sit far below the bf16 rounding of
+  // the result.
+  constexpr int PB = kSolvePanel;
+  static_assert(D % PB == 0 && PB <= 64, "panel layout");
   int bad = 0;
   const int lane = tid & 63;
   for (int jb = 0; jb < D; jb += PB) {
     __syncthreads();
     if (tid < 64) {
+      float pr[PB];
+      const int rowk = jb + lane;
+#pragma unroll
+      for (int c = 0; c < PB; ++c) pr[c] = lane < PB ? sm.a[rowk][jb + c] : 0.0f;
 #pragma unroll
       for (int c = 0; c < PB; ++c) {
         const int j = jb + c;
-        const float piv = sm.a[j][j];
+        const float piv = read_lane(pr[c], c);           // row j: lane c
         if (!(piv > 0.0f)) bad = bad ? bad : j + 1;
-        const float dj = __builtin_sqrtf(piv);
-        __builtin_amdgcn_wave_barrier();
-        for (int k = j + 1 + lane; k < D; k += 64) sm.a[k][j] = sm.a[k][j] / dj;
-        if (lane == 0) sm.a[j][j] = dj;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // the rest of the panel: columns j' in (j, jb + PB), rows k >= j'
-        for (int k = j + 1 + lane; k < D; k += 64) {
-          const float akj = sm.a[k][j];
+        const float rj = __builtin_amdgcn_rsqf(piv);
+        if (lane > c) pr[c] = pr[c] * rj;
+        if (lane == c) pr[c] = piv * rj;
+        if (lane == 0) sm.inv[j] = rj;
 #pragma unroll
-          for (int c2 = c + 1; c2 < PB; ++c2) {
-            const int j2 = jb + c2;
-            if (k >= j2) sm.a[k][j2] = fmaf(-akj, sm.a[j2][j], sm.a[k][j2]);
-          }
+        for (int c2 = c + 1; c2 < PB; ++c2) {
+          const float f = read_lane(pr[c], c2);          // L[jb + c2][j]
+          if (lane >= c2) pr[c2] = fmaf(-pr[c], f, pr[c2]);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+      if (lane < PB) {
+#pragma unroll
+        for (int c = 0; c < PB; ++c)
+          if (c <= lane) sm.a[rowk][jb + c] = pr[c];
       }
     }
     __syncthreads();
-    const int r0 = jb + PB, R = D - r0;
-    for (int idx = tid; idx < R * R; idx += kSolveThreads) {
-      const int k = r0 + idx / R, c = r0 + idx % R;
-      if (c <= k) {
-        float v = sm.a[k][c];
+    if (tid < D - jb - PB) {
+      const int rowk = jb + PB + tid;
+      float l[PB];
 #pragma unroll
-        for (int t = 0; t < PB; ++t) v = fmaf(-sm.a[k][jb + t], sm.a[c][jb + t], v);
-        sm.a[k][c] = v;
+      for (int q = 0; q < PB / 4; ++q) {
+        const float4 v = *(const float4*)&sm.a[rowk][jb + 4 * q];
+        l[4 * q] = v.x; l[4 * q + 1] = v.y; l[4 * q + 2] = v.z; l[4 * q + 3] = v.w;
       }
+#pragma unroll
+      for (int c = 0; c < PB; ++c) {
+        float v = l[c];
+#pragma unroll
+        for (int u = 0; u < c; ++u) v = fmaf(-l[u], sm.a[jb + c][jb + u], v);
+        l[c] = v * sm.inv[jb + c];
+      }
+#pragma unroll
+      for (int q = 0; q < PB / 4; ++q)
+        *(float4*)&sm.a[rowk][jb + 4 * q] = make_float4(l[4 * q], l[4 * q + 1], l[4 * q + 2],
+                                                        l[4 * q + 3]);
+    }
+    __syncthreads();
+    const int r0 = jb + PB, nt = (D - r0) / 4;
+    for (int t = tid; t < nt * (nt + 1) / 2; t += kSolveThreads) {
+      int kt = (int)((__builtin_sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);
+      while (kt * (kt + 1) / 2 > t) --kt;
+      while ((kt + 1) * (kt + 2) / 2 <= t) ++kt;
+      const int ct = t - kt * (kt + 1) / 2;
+      const int k0 = r0 + 4 * kt, c0 = r0 + 4 * ct;
+      float4 acc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = *(const float4*)&sm.a[k0 + i][c0];
+#pragma unroll
+      for (int q = 0; q < PB / 4; ++q) {
+        float4 lk[4], lc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lk[i] = *(const float4*)&sm.a[k0 + i][jb + 4 * q];
+          lc[i] = *(const float4*)&sm.a[c0 + i][jb + 4 * q];
+        }
+        // column jb + 4q + s: acc[i][j] -= L[k0 + i][.] * L[c0 + j][.]
+        const float lks[4][4] = {{lk[0].x, lk[1].x, lk[2].x, lk[3].x},
+                                 {lk[0].y, lk[1].y, lk[2].y, lk[3].y},
+                                 {lk[0].z, lk[1].z, lk[2].z, lk[3].z},
+                                 {lk[0].w, lk[1].w, lk[2].w, lk[3].w}};
+        const float4 lcs[4] = {make_float4(lc[0].x, lc[1].x, lc[2].x, lc[3].x),
+                               make_float4(lc[0].y, lc[1].y, lc[2].y, lc[3].y),
+                               make_float4(lc[0].z, lc[1].z, lc[2].z, lc[3].z),
+                               make_float4(lc[0].w, lc[1].w, lc[2].w, lc[3].w)};
+#pragma unroll
+        for (int sidx = 0; sidx < 4; ++sidx) sub_outer(acc, lks[sidx], lcs[sidx]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *(float4*)&sm.a[k0 + i][c0] = acc[i];
     }
   }
   __syncthreads();
   if (p.info && tid == 0) p.info[mat] = bad;
   // Forward (L Y = X) then back (L^T X = Y) substitution, PB rows a step:
-  // thread e finishes the step's rows of column e, then every thread removes
-  // them from the remaining rows; two barriers a step.
+  // thread e solves the step's rows of column e, then every thread removes
+  // them from a 4 x 4 tile of the remaining rows (one FMA per solved row, in
+  // row order); two barriers a step.
+  constexpr int NCT = D / 4;
   for (int ib = 0; ib < D; ib += PB) {
     if (tid < D) {
       const int e = tid;
@@ -283,18 +378,32 @@ __global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocS
         float v = sm.x[ib + t][e];
 #pragma unroll
         for (int u = 0; u < t; ++u) v = fmaf(-sm.a[ib + t][ib + u], y[u], v);
-        y[t] = v / sm.a[ib + t][ib + t];
+        y[t] = v * sm.inv[ib + t];
         sm.x[ib + t][e] = y[t];
       }
     }
     __syncthreads();
     const int r0 = ib + PB;
-    for (int idx = tid; idx < (D - r0) * D; idx += kSolveThreads) {
-      const int k = r0 + idx / D, e = idx % D;
-      float v = sm.x[k][e];
+    for (int t = tid; t < (D - r0) / 4 * NCT; t += kSolveThreads) {
+      const int k0 = r0 + 4 * (t / NCT), e0 = 4 * (t % NCT);
+      float4 acc[4];
 #pragma unroll
-      for (int t = 0; t < PB; ++t) v = fmaf(-sm.a[k][ib + t], sm.x[ib + t][e], v);
-      sm.x[k][e] = v;
+      for (int i = 0; i < 4; ++i) acc[i] = *(const float4*)&sm.x[k0 + i][e0];
+#pragma unroll
+      for (int q = 0; q < PB / 4; ++q) {
+        float4 lk[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lk[i] = *(const float4*)&sm.a[k0 + i][ib + 4 * q];
+        const float lks[4][4] = {{lk[0].x, lk[1].x, lk[2].x, lk[3].x},
+                                 {lk[0].y, lk[1].y, lk[2].y, lk[3].y},
+                                 {lk[0].z, lk[1].z, lk[2].z, lk[3].z},
+                                 {lk[0].w, lk[1].w, lk[2].w, lk[3].w}};
+#pragma unroll
+        for (int sidx = 0; sidx < 4; ++sidx)
+          sub_outer(acc, lks[sidx], *(const float4*)&sm.x[ib + 4 * q + sidx][e0]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *(float4*)&sm.x[k0 + i][e0] = acc[i];
     }
     __syncthreads();
   }
@@ -307,17 +416,25 @@ __global__ __launch_bounds__(kSolveThreads) void association_solve_kernel(AssocS
         float v = sm.x[ib + t][e];
 #pragma unroll
         for (int u = t + 1; u < PB; ++u) v = fmaf(-sm.a[ib + u][ib + t], xv[u], v);
-        xv[t] = v / sm.a[ib + t][ib + t];
+        xv[t] = v * sm.inv[ib + t];
         sm.x[ib + t][e] = xv[t];
       }
     }
     __syncthreads();
-    for (int idx = tid; idx < ib * D; idx += kSolveThreads) {
-      const int k = idx / D, e = idx % D;
-      float v = sm.x[k][e];
+    for (int t = tid; t < ib / 4 * NCT; t += kSolveThreads) {
+      const int k0 = 4 * (t / NCT), e0 = 4 * (t % NCT);
+      float4 acc[4];
 #pragma unroll
-      for (int t = 0; t < PB; ++t) v = fmaf(-sm.a[ib + t][k], sm.x[ib + t][e], v);
-      sm.x[k][e] = v;
+      for (int i = 0; i < 4; ++i) acc[i] = *(const float4*)&sm.x[k0 + i][e0];
+#pragma unroll
+      for (int t2 = 0; t2 < PB; ++t2) {
+        // row ib + t2 of L, columns k0 .. k0 + 3 (L^T[k][ib + t2])
+        const float4 lr = *(const float4*)&sm.a[ib + t2][k0];
+        const float l4[4] = {lr.x, lr.y, lr.z, lr.w};
+        sub_outer(acc, l4, *(const float4*)&sm.x[ib + t2][e0]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *(float4*)&sm.x[k0 + i][e0] = acc[i];
     }
     __syncthreads();
   }

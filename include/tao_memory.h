@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 11
+#define TAO_ABI_VERSION 12
 
 enum tao_status {
   TAO_OK = 0,
@@ -363,6 +363,22 @@ typedef struct tao_stream_cfg {
 int tao_prefill_plan(const tao_stream_cfg* cfg, int64_t pos0, int64_t tokens,
                      int32_t route_coarse, int32_t route_size, int32_t outputs,
                      int64_t* plan, int64_t plan_cap, int64_t* info);
+
+/* Local attention of a call whose window holds only the call's own tokens,
+ * without a state (the same kernel and tiles as tao_prefill's local
+ * attention), so that a caller can start it before it allocates a new
+ * state: the reference's first chunks of a prompt (flash_attn_func,
+ * flash_attention.py:16-37, over the window of tao_stream.py:927-930 at
+ * position 0). The tiles are those of the call's tao_prefill_plan attention
+ * section (the schedule's chunks of cfg from pos0 over tok.tokens); each
+ * must lie in the call's tokens (key_start >= pos0: no key from a ring,
+ * which holds for pos0 = 0) and is written to tiles_dev (device int64,
+ * tiles_cap words, at least 3 per tile) on the stream. local: bf16
+ * [B, tok.tokens, H, D] contiguous. The caller then passes tao_prefill the
+ * plan without its attention section and this local output. */
+int tao_prompt_attention(const tao_stream_cfg* cfg, int32_t batch, int32_t heads,
+                         int32_t head_dim, const tao_tokens* tok, int64_t pos0,
+                         void* tiles_dev, int64_t tiles_cap, void* local, void* stream);
 
 /* Plan of the full-sequence read of tokens [0, tokens) (replaces the host
  * tiling of read_training, tao_stream.py:668-757, and of

@@ -7,7 +7,9 @@
 #include <algorithm>
 #include <cstdlib>
 #include <string>
+#include <vector>
 
+#include "schedule.h"
 #include "tao_launch.h"
 
 namespace {
@@ -993,6 +995,49 @@ int tao_local_attention(const tao_state_dev* st, const tao_tokens* tok, int64_t 
   p.n_tiles = n_tiles;
   return check_hip(tao::launch_local_attention(p, st->head_dim, (hipStream_t)stream),
                    "tao_local_attention");
+}
+
+int tao_prompt_attention(const tao_stream_cfg* cfg, int32_t batch, int32_t heads,
+                         int32_t head_dim, const tao_tokens* tok, int64_t pos0,
+                         void* tiles_dev, int64_t tiles_cap, void* local, void* stream) {
+  int rc = check_tokens(tok);
+  if (rc) return rc;
+  if (!cfg || batch < 1 || heads < 1 || (head_dim != 64 && head_dim != 128) ||
+      cfg->local_keep < 0 || cfg->fine_tokens < 1)
+    return fail(TAO_E_ARGUMENT, "prompt attention: bad geometry");
+  if (!local || !tiles_dev || pos0 < 0) return fail(TAO_E_ARGUMENT, "prompt attention: null tiles or output");
+  const int64_t L = tao::sched::serve_limit(*cfg), T = tok->tokens;
+  std::vector<int64_t> tiles;
+  bool inside = true;
+  tao::sched::attention_tiles(*cfg, pos0, T, [&](int64_t row, int64_t n, int64_t key_start) {
+    inside = inside && key_start >= pos0 && key_start <= pos0 + row && pos0 + row + n - key_start <= L;
+    tiles.insert(tiles.end(), {row, n, key_start});
+  });
+  if (!inside) return fail(TAO_E_ARGUMENT, "prompt attention: the window reaches before the call");
+  const int64_t n_tiles = (int64_t)tiles.size() / 3;
+  if (3 * n_tiles > tiles_cap) return fail(TAO_E_CAPACITY, "prompt attention: tiles_cap too small");
+  if (n_tiles == 0) return TAO_OK;
+  const hipStream_t s = (hipStream_t)stream;
+  hipError_t e = hipMemcpyAsync(tiles_dev, tiles.data(), tiles.size() * sizeof(int64_t),
+                                hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return check_hip(e, "tao_prompt_attention");
+  tao::AttnParams ap{};
+  ap.q = view(tok->q, tok->q_s);
+  ap.k = view(tok->k, tok->k_s);
+  ap.v = view(tok->v, tok->v_s);
+  ap.ring_k = nullptr;   // every key is one of the call's (checked above)
+  ap.ring_v = nullptr;
+  ap.out = (bf16_t*)local;
+  ap.tiles = (const int64_t*)tiles_dev;
+  ap.qpos0 = pos0;
+  ap.kpos0 = pos0;
+  ap.B = batch;
+  ap.H = heads;
+  ap.L = (int)L;
+  ap.T = (int)T;
+  ap.n_tiles = (int)n_tiles;
+  ap.lse = nullptr;
+  return check_hip(tao::launch_local_attention(ap, head_dim, s), "tao_prompt_attention");
 }
 
 int tao_prefill(const tao_state_dev* st, const tao_tokens* tok, const tao_fusion* fu,

@@ -13,7 +13,6 @@
 
 namespace {
 
-constexpr int64_t kAttnTile = 256;   // queries per local-attention tile
 constexpr int64_t kReadTile = 32;    // queries per read tile (one wave)
 
 }  // namespace
@@ -44,15 +43,11 @@ extern "C" int tao_prefill_plan(const tao_stream_cfg* cfg, int64_t pos0, int64_t
   }
   std::vector<int64_t> attn, reads, turns;
   int64_t history_chunks = 0;
-  for (const Chunk& ch : chunks) {
-    history_chunks += ch.epoch > 0;
-    if (!outputs) continue;
-    const int64_t key_start = ch.start - local_len_at(c, ch.start);
-    for (int64_t qs = ch.start; qs < ch.start + ch.width; qs += kAttnTile) {
-      const int64_t n = ch.start + ch.width - qs;
-      attn.insert(attn.end(), {qs - pos0, n < kAttnTile ? n : kAttnTile, key_start});
-    }
-  }
+  for (const Chunk& ch : chunks) history_chunks += ch.epoch > 0;
+  if (outputs)
+    attention_tiles(c, pos0, tokens, [&](int64_t row, int64_t n, int64_t key_start) {
+      attn.insert(attn.end(), {row, n, key_start});
+    });
   // Epochs read by this call plus the published final epoch.
   int64_t first_epoch = 0;
   if (f1 >= 1) {
@@ -196,8 +191,9 @@ extern "C" int tao_train_plan(const tao_stream_cfg* cfg, int64_t tokens, int64_t
   for (int64_t t = 0; t < n_tiles; ++t) {
     const int64_t s = t * ft, e = s + ft < tokens ? s + ft : tokens;
     const int64_t key_start = s > c.local_keep ? s - c.local_keep : 0;
-    for (int64_t qs = s; qs < e; qs += kAttnTile)
-      attn.insert(attn.end(), {qs, e - qs < kAttnTile ? e - qs : kAttnTile, key_start});
+    constexpr int64_t kTile = tao::sched::kAttnTile;
+    for (int64_t qs = s; qs < e; qs += kTile)
+      attn.insert(attn.end(), {qs, e - qs < kTile ? e - qs : kTile, key_start});
     const int64_t visible = t > lag ? t - lag : 0;
     int64_t coarse = 0, eligible = 0, selected = 0;
     if (visible) {

@@ -85,5 +85,24 @@ inline int64_t next_chunk(const tao_stream_cfg& c, int64_t p, int64_t desired) {
   return w < room ? w : room;
 }
 
+// The local-attention tiles of a call [pos0, pos0 + tokens): its chunks
+// (next_chunk) cut into kAttnTile queries, each tile (first query row - pos0,
+// count, key_start = the chunk's start - its window). emit(row, count,
+// key_start) per tile, in order; the prefill plan's attention section.
+constexpr int64_t kAttnTile = 256;
+template <typename Emit>
+inline void attention_tiles(const tao_stream_cfg& c, int64_t pos0, int64_t tokens, Emit&& emit) {
+  const int64_t end = pos0 + tokens;
+  for (int64_t start = pos0; start < end;) {
+    const int64_t w = next_chunk(c, start, end - start);
+    const int64_t key_start = start - local_len_at(c, start);
+    for (int64_t qs = start; qs < start + w; qs += kAttnTile) {
+      const int64_t n = start + w - qs;
+      emit(qs - pos0, n < kAttnTile ? n : kAttnTile, key_start);
+    }
+    start += w;
+  }
+}
+
 }  // namespace sched
 }  // namespace tao

@@ -114,6 +114,8 @@ _SIGNATURES = {
     "tao_write_fine": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i64, _vp,
                         _i32, _i32, _vp], _i32),
     "tao_seal_epilogue": ([ctypes.POINTER(StateDev), _i32, _i32, _i32, _vp], _i32),
+    "tao_prompt_attention": ([ctypes.POINTER(StreamCfg), _i32, _i32, _i32, ctypes.POINTER(Tokens),
+                              _i64, _vp, _i64, _vp, _vp], _i32),
     "tao_local_attention": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), _i64, _i64,
                              _vp, _i32, _vp, _vp], _i32),
     "tao_prefill": ([ctypes.POINTER(StateDev), ctypes.POINTER(Tokens), ctypes.POINTER(Fusion),
@@ -174,7 +176,7 @@ _SIGNATURES = {
 
 EXPORTED = tuple(_SIGNATURES)
 
-ABI_VERSION = 11               # TAO_ABI_VERSION of include/tao_memory.h
+ABI_VERSION = 12               # TAO_ABI_VERSION of include/tao_memory.h
 
 # Decode-graph epoch counters (enum tao_graph_stat / tao_graph_reason).
 GRAPH_STATS = 19

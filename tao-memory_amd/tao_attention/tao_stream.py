@@ -580,11 +580,20 @@ class StreamCache:
         cfg = self.config
         pos0 = self.position
         tokens = q.shape[1]
-        plan, info = self._plan(pos0, tokens, outputs=True)
-        dev = self._device_for(q, pos0 + tokens, plan_words=len(plan))
         q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
-        if local_flash is not None:
+        local = None
+        if (local_flash is None and self._dev is None and pos0 == 0 and
+                os.environ.get("TAO_EARLY_LOCAL", "1") != "0"):
+            # A new state's first call: its window holds only the call's own
+            # keys, so its local attention starts now, on the stream, and the
+            # plan and the state's buffers are made while it runs.
+            local = self._prompt_attention(q, tok)
+        plan, info = self._plan(pos0, tokens, outputs=True)
+        if local is not None:
+            plan = _hip.without_attention(plan)
+        dev = self._device_for(q, pos0 + tokens, plan_words=len(plan))
+        if local is None and local_flash is not None:
             from .flash_attention import plugin_stream_local
             window = self._local_window()
             empty = q[:, :0]
@@ -594,7 +603,7 @@ class StreamCache:
             if local.shape != q.shape:
                 raise ValueError("local_flash returned a local output of the wrong shape")
             plan = _hip.without_attention(plan)
-        else:
+        elif local is None:
             local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
         out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
         fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
@@ -603,6 +612,20 @@ class StreamCache:
         self.fusion_pointwise_calls += info["history_chunks"]
         self.fusion_no_history_local_returns += info["chunks"] - info["history_chunks"]
         return out
+
+    def _prompt_attention(self, q, tok):
+        """Local attention of a call at position 0 without a state
+        (tao_prompt_attention): every tile's keys are the call's own, and the
+        tiles are those of the call's plan."""
+        b, t, h, d = q.shape
+        words = 3 * (2 * (t // 256) + 4)     # chunks of at most 256, two per 256 tokens
+        local = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+        tiles_dev = torch.empty(words, dtype=torch.int64, device=q.device)
+        scfg = self._stream_cfg()
+        _hip.check(_hip.lib().tao_prompt_attention(
+            ctypes.byref(scfg), b, h, d, ctypes.byref(tok), 0, tiles_dev.data_ptr(), words,
+            local.data_ptr(), _hip.stream_ptr(q.device)))
+        return local   # tiles_dev: the caching allocator keeps it stream-ordered
 
     def _advance(self, pos0, tokens, info):
         cfg = self.config

@@ -151,6 +151,43 @@ def test_fused_refresh_fold_equals_two_launches(device, monkeypatch, heads, widt
     compare_snapshots(runs["1"][1], ora.export())
 
 
+def _assert_same_export(a, b):
+    if isinstance(a, dict):
+        assert a.keys() == b.keys()
+        for key in a:
+            _assert_same_export(a[key], b[key])
+    elif isinstance(a, (list, tuple)):
+        assert len(a) == len(b)
+        for x, y in zip(a, b):
+            _assert_same_export(x, y)
+    elif isinstance(a, torch.Tensor):
+        assert torch.equal(a, b)
+    else:
+        assert a == b
+
+
+@pytest.mark.parametrize("heads,width,tokens", [(4, 128, 3000), (2, 64, 1300)])
+def test_prompt_attention_before_the_state_equals_in_plan(device, monkeypatch, heads, width,
+                                                          tokens):
+    """A new state's first prefill starts its local attention before the
+    state's buffers exist (tao_prompt_attention); its outputs, later decode
+    steps and exported state equal, bit for bit, those of the local attention
+    run inside tao_prefill."""
+    xs, fa, fb = inputs(tokens, heads, width, seed=19)
+    d = to_dev(xs, device)
+    fa_d, fb_d = fa.to(device), fb.to(device)
+    splits = [tokens - 24] + [1] * 24
+    print(f"prompt attention H{heads} D{width} T{tokens}", flush=True)
+    runs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("TAO_EARLY_LOCAL", mode)
+        state = new_state(1, index_only_page_memo(graph=False))
+        out = run_hip(state, d, fa_d, fb_d, splits)
+        runs[mode] = (out, state.export())
+    assert torch.equal(runs["0"][0], runs["1"][0])
+    _assert_same_export(runs["0"][1], runs["1"][1])
+
+
 def test_chunked_prefill_and_page_routing(device):
     """Arbitrary chunking plus completed pages (coarse selection active)."""
     heads, width = 2, 64

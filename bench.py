@@ -295,6 +295,7 @@ def run_timeline(torch, args, device, cfg, heads, width):
         merged = t[:, 5] != 0
         t0 = t[:, 0].min()
         rows.append(dict(t=(t - t0) / ticks_per_us, j=j, merged=merged,
+                         u=(fr[:, 6] & np.uint64(0xFFFFFFFF)).astype(np.int64),
                          start=t0, end=t[merged, 5].max(),
                          xcc=(fr[:, 7] >> np.uint64(32)).astype(np.int64),
                          smid=(fr[:, 7] & np.uint64(0xFFFFFFFF)).astype(np.int64)))
@@ -321,6 +322,10 @@ def run_timeline(torch, args, device, cfg, heads, width):
         crit_local += int(r["j"][w] < nloc)
     crit = np.asarray(crit)
     cus = med([len(set(zip(r["xcc"].tolist(), r["smid"].tolist()))) for r in rows])
+    u_of = lambda r: r["u"]                                               # noqa: E731
+    one_xcd = sum(int(len(np.unique(r["xcc"][u_of(r) == hh])) == 1)
+                  for r in rows for hh in np.unique(u_of(r)))
+    head_steps = sum(len(np.unique(u_of(r))) for r in rows)
     summary = {
         "steps": args.steps, "grid": int(len(rows[0]["j"])),
         "clock": "s_memrealtime at 100 MHz (10 ns ticks); medians over the steps of "
@@ -330,6 +335,7 @@ def run_timeline(torch, args, device, cfg, heads, width):
         "launch_gap_us": round(med(gaps), 3) if gaps else None,
         "last_start_us": round(med([r["t"][:, 0].max() for r in rows]), 3),
         "cus_used": cus,
+        "heads_on_one_xcd_frac": round(one_xcd / max(head_steps, 1), 4),
         "local_units": {"start_us": round(med([np.mean(r["t"][local(r), 0]) for r in rows]), 3),
                         "loads_and_scores_us": phase(local, 0, 1),
                         "softmax_values_record_us": phase(local, 1, 2),

@@ -41,24 +41,28 @@ constexpr int kSelWords = kSelMaxS / 32;
 
 template <int D> constexpr int kSelQG = 128 / D;          // 32-query groups per tile
 template <int D> constexpr int kSelTileQ = 32 * kSelQG<D>;
+// The forward's tile: each wave owns 32 queries and every column of them,
+// so a staged C^T serves kSelThreads / 64 * 32 queries.
+constexpr int kSelFwdQ = 32 * (kSelThreads / 64);
 
-template <int D>
+template <int D, int TQ = kSelTileQ<D>, bool STAGE = true>
 struct SelSmem {
+  static constexpr int kUni = TQ * kSelMaxM < kSelMaxS ? TQ * kSelMaxM : kSelMaxS;
   bf16_t c[D][D + 8];                     // staged C^T (forward) or C (grad of channel)
-  int16_t sid[kSelTileQ<D>][kSelMaxM];    // the tile's selected ids
-  int8_t occ[kSelTileQ<D>][kSelMaxM];     // occurrence index of sid[q][m] in its row
+  int16_t sid[TQ][kSelMaxM];              // the tile's selected ids
+  int8_t occ[TQ][kSelMaxM];               // occurrence index of sid[q][m] in its row
   uint32_t bits[kSelWords];
   int pre[kSelWords];
-  int uni[kSelTileQ<D> * kSelMaxM];
-  int8_t ord[kSelTileQ<D>][kSelMaxM];     // forward: a row's slots by (id, slot) ascending
+  int16_t uni[kUni];                      // the union: at most S and TQ * M ids (S < 2^15)
+  int8_t ord[TQ][kSelMaxM];               // forward: a row's slots by (id, slot) ascending
   int n_union, passes;
-  bf16_t stage[4][32][40];                // grad-of-channel rows per wave (32 q x 32 d)
+  bf16_t stage[STAGE ? 4 : 1][32][40];    // grad-of-channel rows per wave (32 q x 32 d)
 };
 
 // Shared setup: ids of the tile into LDS, occurrence indices, the union
 // (ascending) and the number of passes (largest occurrence count).
-template <int D>
-TAO_DEV void tile_union(SelSmem<D>& sm, const SelectedParams& p, int b, int h, int q0, int nq,
+template <typename Smem>
+TAO_DEV void tile_union(Smem& sm, const SelectedParams& p, int b, int h, int q0, int nq,
                         int tid) {
   for (int i = tid; i < kSelWords; i += kSelThreads) sm.bits[i] = 0u;
   if (tid == 0) sm.passes = 0;
@@ -101,7 +105,7 @@ TAO_DEV void tile_union(SelSmem<D>& sm, const SelectedParams& p, int b, int h, i
     uint32_t bits = sm.bits[i];
     int r = sm.pre[i];
     while (bits) {
-      sm.uni[r++] = i * 32 + __ffs(bits) - 1;
+      sm.uni[r++] = (int16_t)(i * 32 + __ffs(bits) - 1);
       bits &= bits - 1;
     }
   }
@@ -109,28 +113,27 @@ TAO_DEV void tile_union(SelSmem<D>& sm, const SelectedParams& p, int b, int h, i
 }
 
 // Slot of fine f (occurrence r) in query row q, or -1.
-template <int D>
-TAO_DEV int find_slot(const SelSmem<D>& sm, int q, int M, int f, int r) {
+template <typename Smem>
+TAO_DEV int find_slot(const Smem& sm, int q, int M, int f, int r) {
   for (int m = 0; m < M; ++m)
     if (sm.sid[q][m] == f && sm.occ[q][m] == r) return m;
   return -1;
 }
 
 template <int D>
-__global__ __launch_bounds__(kSelThreads) void selected_fwd_kernel(SelectedParams p) {
-  constexpr int KK = D / 16, ET = D / 32, TQ = kSelTileQ<D>;
+__global__ __launch_bounds__(kSelThreads, 2) void selected_fwd_kernel(SelectedParams p) {
+  constexpr int KK = D / 16, ET = D / 32, TQ = kSelFwdQ;
   constexpr int CPR = D / 8;                             // uint4 per row of C
   constexpr int PJ = (D / 2) * CPR / kSelThreads;        // row-pair jobs per thread
   static_assert(PJ * kSelThreads == (D / 2) * CPR, "whole row-pair jobs");
-  __shared__ SelSmem<D> sm;
+  __shared__ SelSmem<D, TQ, false> sm;
   const int n_tiles = (p.Q + TQ - 1) / TQ;
   const int tile = blockIdx.x % n_tiles, bh = blockIdx.x / n_tiles;
   const int b = bh / p.H, h = bh % p.H;
   const int q0 = tile * TQ, nq = min(TQ, p.Q - q0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 31, hl = lane >> 5;
-  const int qg = w / ET, et = w % ET;
-  tile_union<D>(sm, p, b, h, q0, nq, tid);
+  tile_union(sm, p, b, h, q0, nq, tid);
   // Each row's slots in ascending (id, slot) order: the union is walked in
   // ascending id, so a lane finds its query's slots of fine f at a pointer
   // (invalid ids sort first and are skipped).
@@ -146,7 +149,7 @@ __global__ __launch_bounds__(kSelThreads) void selected_fwd_kernel(SelectedParam
   }
   __syncthreads();
   const int U = sm.n_union;
-  const int ql = 32 * qg + li;                            // the lane's query row in the tile
+  const int ql = 32 * w + li;                             // the lane's query row in the tile
   const bool qok = ql < nq;
   int ptr = 0;
   if (qok)
@@ -180,9 +183,11 @@ __global__ __launch_bounds__(kSelThreads) void selected_fwd_kernel(SelectedParam
       c1[j] = *(const uint4*)(src + D);
     }
   };
-  floatx16 acc;
+  floatx16 acc[ET];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+  for (int t = 0; t < ET; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
   int m_next = -1;
   uint4 row_next[KK];
   if (U > 0) {
@@ -215,9 +220,11 @@ __global__ __launch_bounds__(kSelThreads) void selected_fwd_kernel(SelectedParam
     while (__any(m >= 0)) {
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            as_bf16x8(row[kk]), as_bf16x8(*(const uint4*)&sm.c[32 * et + li][16 * kk + 8 * hl]),
-            acc, 0, 0, 0);
+#pragma unroll
+        for (int et = 0; et < ET; ++et)
+          acc[et] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              as_bf16x8(row[kk]),
+              as_bf16x8(*(const uint4*)&sm.c[32 * et + li][16 * kk + 8 * hl]), acc[et], 0, 0, 0);
       m = m >= 0 ? next_slot(f) : -1;
       load_row(m, row);
     }
@@ -226,12 +233,15 @@ __global__ __launch_bounds__(kSelThreads) void selected_fwd_kernel(SelectedParam
       load_row(m_next, row_next);
     }
   }
-  // rows q = 32 qg + 8 (i / 4) + 4 hl + i % 4, column e = 32 et + li
+  // rows q = 32 w + 8 (i / 4) + 4 hl + i % 4, column e = 32 et + li
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int q = 32 * qg + 8 * (i / 4) + 4 * hl + (i % 4);
-    if (q < nq) p.out[(((size_t)b * p.Q + q0 + q) * p.H + h) * D + 32 * et + li] = f2bf(acc[i]);
-  }
+  for (int et = 0; et < ET; ++et)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int q = 32 * w + 8 * (i / 4) + 4 * hl + (i % 4);
+      if (q < nq)
+        p.out[(((size_t)b * p.Q + q0 + q) * p.H + h) * D + 32 * et + li] = f2bf(acc[et][i]);
+    }
 }
 
 // d channel: A = the tile's grad rows (loaded once), B = rows of C (k = e).
@@ -247,7 +257,7 @@ __global__ __launch_bounds__(kSelThreads) void selected_bwd_a_kernel(SelectedPar
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 31, hl = lane >> 5;
   const int qg = w / ET, dt = w % ET;
-  tile_union<D>(sm, p, b, h, q0, nq, tid);
+  tile_union(sm, p, b, h, q0, nq, tid);
   const int U = sm.n_union, R = sm.passes + 1;
   const int ql = 32 * qg + li;
   const bool qok = ql < nq;
@@ -299,7 +309,7 @@ __global__ __launch_bounds__(kSelThreads) void selected_bwd_a_kernel(SelectedPar
       const uint4 lo = *(const uint4*)&sm.stage[w][li][16 * hl];
       const uint4 hi = *(const uint4*)&sm.stage[w][li][16 * hl + 8];
       for (int r = 0; r < R; ++r) {
-        const int m = find_slot<D>(sm, ql, p.M, f, r);
+        const int m = find_slot(sm, ql, p.M, f, r);
         if (m < 0) continue;
         bf16_t* dst = p.grad_channel +
             ((((size_t)b * p.Q + q0 + ql) * p.H + h) * p.M + m) * D + 32 * dt + 16 * hl;
@@ -434,7 +444,7 @@ hipError_t launch_selected_numerator(const SelectedParams& p, int head_dim, hipS
   if (p.B * p.Q * p.H == 0) return hipSuccess;
 #define TAO_SEL_FWD(D_)                                                                       \
   hipLaunchKernelGGL(selected_fwd_kernel<D_>,                                                 \
-                     dim3((unsigned)(((p.Q + kSelTileQ<D_> - 1) / kSelTileQ<D_>) * p.B * p.H)), \
+                     dim3((unsigned)(((p.Q + kSelFwdQ - 1) / kSelFwdQ) * p.B * p.H)),        \
                      dim3(kSelThreads), 0, s, p)
   if (head_dim == 128)
     TAO_SEL_FWD(128);

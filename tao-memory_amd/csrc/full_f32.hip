@@ -39,6 +39,7 @@ constexpr int kKeep = 512;          // local_keep
 constexpr int kRowsPerPage = 36;    // segment-weight rows of a page: prefixes n = 1..8
 constexpr int kChunk = 16;          // queries per read block
 constexpr int kKeyStage = 16;       // keys per local-attention LDS stage
+constexpr int kVChunk = 32;         // value rows per writer LDS stage
 constexpr float kLogTwoF32 = 0.693147180559945309f;   // fp32(log 2)
 
 TAO_DEV float ld(const F32View& v, int b, int64_t t, int h, int d) {
@@ -88,17 +89,27 @@ TAO_DEV float slot_fold(float (&x)[K], int n) {
 // --------------------------------------------------------------- local tiles
 // Query t of tile j attends causally to keys [max(0, 256 j - 512), t]
 // (_local_training_corrected_4k and its ragged fallback); softmax scale
-// 1/sqrt(D) as SDPA's default.
+// 1/sqrt(D) as SDPA's default. A workgroup takes 64 queries (lane t0 + i of
+// every wave holds query t0 + i) and splits their key range by 16-key stages
+// over its kLocalWaves(D) waves (stage s to wave s % waves), each wave with
+// its own LDS stage and online softmax (m, l, acc); the waves' partials are
+// merged in wave order: M = max m_w, l = sum l_w e^(m_w - M),
+// o = sum acc_w e^(m_w - M) / l.
+template <int D> constexpr int kLocalWaves = D == 64 ? 8 : 4;
+constexpr int kMergeCols = 16;       // channels per merge round
+
 template <int D>
-__global__ __launch_bounds__(64) void f32_local_kernel(F32Params p) {
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(64 * kLocalWaves<D>) void f32_local_kernel(F32Params p) {
+  constexpr int NW = kLocalWaves<D>;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int h = blockIdx.y, b = blockIdx.z;
   const int t0 = blockIdx.x * 64;
   const int t = t0 + lane;
   const bool active = t < p.T;
   const int k0 = max(0, (t0 / kFine) * kFine - kKeep);
   const int k1 = min(p.T, t0 + 64);
-  __shared__ float ks[kKeyStage][D], vs[kKeyStage][D];
+  __shared__ float ks[NW][kKeyStage][D], vs[NW][kKeyStage][D];
+  __shared__ float wm[NW][64], wl[NW][64];
   const float scale = 1.0f / sqrtf((float)D);
   float q[D], acc[D];
 #pragma unroll
@@ -107,14 +118,18 @@ __global__ __launch_bounds__(64) void f32_local_kernel(F32Params p) {
     acc[d] = 0.0f;
   }
   float m = -__builtin_inff(), l = 0.0f;
-  for (int kb = k0; kb < k1; kb += kKeyStage) {
-    __syncthreads();
+  for (int kb = k0 + w * kKeyStage; kb < k1; kb += NW * kKeyStage) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     for (int i = lane; i < kKeyStage * D; i += 64) {
       const int j = i / D, d = i % D, key = kb + j;
-      ks[j][d] = key < k1 ? ld(p.k, b, key, h, d) : 0.0f;
-      vs[j][d] = key < k1 ? ld(p.v, b, key, h, d) : 0.0f;
+      ks[w][j][d] = key < k1 ? ld(p.k, b, key, h, d) : 0.0f;
+      vs[w][j][d] = key < k1 ? ld(p.v, b, key, h, d) : 0.0f;
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float s[kKeyStage];
     float cm = -__builtin_inff();
 #pragma unroll
@@ -123,7 +138,7 @@ __global__ __launch_bounds__(64) void f32_local_kernel(F32Params p) {
       if (active && kb + j <= t) {
         float dot = 0.0f;
 #pragma unroll
-        for (int d = 0; d < D; ++d) dot = fmaf(q[d], ks[j][d], dot);
+        for (int d = 0; d < D; ++d) dot = fmaf(q[d], ks[w][j][d], dot);
         s[j] = dot * scale;
         cm = fmaxf(cm, s[j]);
       }
@@ -136,18 +151,45 @@ __global__ __launch_bounds__(64) void f32_local_kernel(F32Params p) {
       for (int d = 0; d < D; ++d) acc[d] *= corr;
 #pragma unroll
       for (int j = 0; j < kKeyStage; ++j) {
-        const float w = expf(s[j] - mn);
-        l += w;
+        const float wgt = expf(s[j] - mn);
+        l += wgt;
 #pragma unroll
-        for (int d = 0; d < D; ++d) acc[d] = fmaf(w, vs[j][d], acc[d]);
+        for (int d = 0; d < D; ++d) acc[d] = fmaf(wgt, vs[w][j][d], acc[d]);
       }
       m = mn;
     }
   }
-  if (active) {
-    float* o = p.local + (((size_t)b * p.T + t) * p.H + h) * D;
+  // Merge the waves' partials (a wave with no key of a query has m = -inf
+  // and weighs 0; every query sees its own key, so M is finite).
+  wm[w][lane] = m;
+  wl[w][lane] = l;
+  __syncthreads();
+  float top = wm[0][lane];
 #pragma unroll
-    for (int d = 0; d < D; ++d) o[d] = acc[d] / l;
+  for (int v = 1; v < NW; ++v) top = fmaxf(top, wm[v][lane]);
+  const float f = m > -__builtin_inff() ? expf(m - top) : 0.0f;
+  float lsum = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NW; ++v)
+    lsum += wm[v][lane] > -__builtin_inff() ? wl[v][lane] * expf(wm[v][lane] - top) : 0.0f;
+  // Channel rounds through the (now free) key stages: wave w's scaled
+  // partials of kMergeCols channels, then lane i of wave w sums query i's
+  // channels w, w + NW, ... of the round over the waves in order.
+  float* red = &ks[0][0][0];                       // [NW][64][kMergeCols]
+  static_assert(NW * 64 * kMergeCols <= NW * kKeyStage * D, "merge buffer fits the stages");
+  float* o = p.local + (((size_t)b * p.T + (active ? t : 0)) * p.H + h) * D;
+#pragma unroll
+  for (int c0 = 0; c0 < D; c0 += kMergeCols) {
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < kMergeCols; ++c) red[(w * 64 + lane) * kMergeCols + c] = acc[c0 + c] * f;
+    __syncthreads();
+    for (int c = w; c < kMergeCols; c += NW) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) sum += red[(v * 64 + lane) * kMergeCols + c];
+      if (active) o[c0 + c] = sum / lsum;
+    }
   }
 }
 
@@ -162,6 +204,7 @@ __global__ __launch_bounds__(4 * D) void f32_writer_kernel(F32Params p) {
   const int d = tid % D, quarter = tid / D;
   __shared__ float prob[kFine][D];
   __shared__ float red[4][D];
+  __shared__ float vchunk[kVChunk][D];
   const int64_t base = (int64_t)f * kFine;
   float top = -__builtin_inff();
   for (int i = 0; i < 64; ++i) top = fmaxf(top, ld(p.rk, b, base + quarter * 64 + i, h, d));
@@ -191,11 +234,19 @@ __global__ __launch_bounds__(4 * D) void f32_writer_kernel(F32Params p) {
   float c[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) c[e] = 0.0f;
-  for (int t = 0; t < kFine; ++t) {
-    const float pr = prob[t][row];
-    const float* vr = p.v.p + b * p.v.sb + (base + t) * p.v.st + h * p.v.sh + part * E;
+  // v staged kVChunk tokens at a time (the token order of the sums is kept).
+  for (int c0 = 0; c0 < kFine; c0 += kVChunk) {
+    __syncthreads();
+    for (int i = tid; i < kVChunk * D; i += 4 * D) {
+      const int tt = i / D, e = i % D;
+      vchunk[tt][e] = ld(p.v, b, base + c0 + tt, h, e);
+    }
+    __syncthreads();
+    for (int tt = 0; tt < kVChunk; ++tt) {
+      const float pr = prob[c0 + tt][row];
 #pragma unroll
-    for (int e = 0; e < E; ++e) c[e] = fmaf(pr, vr[e], c[e]);
+      for (int e = 0; e < E; ++e) c[e] = fmaf(pr, vchunk[tt][part * E + e], c[e]);
+    }
   }
   float* out = p.bank + ((bh * p.S + f) * D + row) * D + part * E;
 #pragma unroll
@@ -264,6 +315,14 @@ __global__ __launch_bounds__(D) void f32_pages_kernel(F32Params p) {
 // the fusion.
 constexpr int kMaxPages = 64;
 constexpr int kMaxCand = 256;
+constexpr int kReadWaves = 4;        // waves per block; wave w reads queries t0 + w + 4 k
+
+// Orders one wave's LDS accesses across its lanes (scratch private to a wave).
+TAO_DEV void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 TAO_DEV int stable_rank(float mine, int idx, int n, const float* all) {
   int r = 0;
@@ -275,9 +334,9 @@ TAO_DEV int stable_rank(float mine, int idx, int n, const float* all) {
 }
 
 template <int D>
-__global__ __launch_bounds__(64) void f32_read_kernel(F32Params p) {
+__global__ __launch_bounds__(64 * kReadWaves) void f32_read_kernel(F32Params p) {
   constexpr int R = D / 64;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int h = blockIdx.y, b = blockIdx.z;
   const int t0 = blockIdx.x * kChunk;
   const int tend = min(p.T, t0 + kChunk);
@@ -289,7 +348,7 @@ __global__ __launch_bounds__(64) void f32_read_kernel(F32Params p) {
   };
   const float* local = p.local;
   if (!visible) {   // neither history branch present: the output is local
-    for (int t = t0; t < tend; ++t) {
+    for (int t = t0 + w; t < tend; t += kReadWaves) {
 #pragma unroll
       for (int r = 0; r < R; ++r)
         *out_at(t, lane + 64 * r) = local[(((size_t)b * p.T + t) * p.H + h) * D + lane + 64 * r];
@@ -308,14 +367,19 @@ __global__ __launch_bounds__(64) void f32_read_kernel(F32Params p) {
 
   __shared__ float pw[kMaxPages][D];
   __shared__ float cw[kMaxPages][D];
-  __shared__ float mass_s[kMaxCand];
-  __shared__ int cand_id[kMaxCand];
-  __shared__ int sel_id[kMaxCand];
-  __shared__ float row_s[D];
+  __shared__ float mass_all[kReadWaves][kMaxCand];
+  __shared__ int cand_all[kReadWaves][kMaxCand];
+  __shared__ int sel_all[kReadWaves][kMaxCand];
+  __shared__ float row_all[kReadWaves][D];
+  float* mass_s = mass_all[w];                 // this wave's query scratch
+  int* cand_id = cand_all[w];
+  int* sel_id = sel_all[w];
+  float* row_s = row_all[w];
 
-  // Page z the tile sees, page weights and coarse weights (lanes = pages).
+  // Page z the tile sees, page weights and coarse weights (lanes = pages;
+  // the waves take the channels in turn).
   const float* pzt = p.pz + bh * p.P8 * kGroup * D;
-  for (int d = 0; d < D; ++d) {
+  for (int d = w; d < D; d += kReadWaves) {
     const float zp = lane < completed ? pzt[((size_t)lane * kGroup + kGroup - 1) * D + d]
                    : (lane == completed && pending)
                        ? pzt[((size_t)completed * kGroup + pending - 1) * D + d]
@@ -352,7 +416,7 @@ __global__ __launch_bounds__(64) void f32_read_kernel(F32Params p) {
       fb[r][i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + d * p.fb_s[1] + i * p.fb_s[2]);
     }
 
-  for (int t = t0; t < tend; ++t) {
+  for (int t = t0 + w; t < tend; t += kReadWaves) {
     // h = softmax over channels of raw_q
     float x[R], hq[R];
 #pragma unroll
@@ -377,20 +441,20 @@ __global__ __launch_bounds__(64) void f32_read_kernel(F32Params p) {
         const float m = channel_fold<R>(hv);
         if (lane == 0) mass_s[pg] = m;
       }
-      __syncthreads();
+      wave_sync();
       const bool mine = lane < completed;
       const int rank = mine ? stable_rank(mass_s[lane], lane, completed, mass_s) : kMaxCand;
       const bool chosen = rank < coarse;
       const unsigned long long bal = __ballot(chosen);
       const int pos = __popcll(bal & ((1ull << lane) - 1ull));
-      __syncthreads();
+      wave_sync();
       if (chosen)
         for (int s = 0; s < kGroup; ++s) cand_id[pos * kGroup + s] = lane * kGroup + s;
       E = coarse * kGroup;
     }
     if (lane < pending) cand_id[E + lane] = completed * kGroup + lane;
     E += pending;
-    __syncthreads();
+    wave_sync();
 
     // Candidate masses sum_d (h pw[page]) sw[fine], then the stable top-M.
     for (int c = 0; c < E; ++c) {
@@ -406,12 +470,12 @@ __global__ __launch_bounds__(64) void f32_read_kernel(F32Params p) {
       const float m = channel_fold<R>(ch);
       if (lane == 0) mass_s[c] = m;
     }
-    __syncthreads();
+    wave_sync();
     for (int c = lane; c < E; c += 64) {
       const int rank = stable_rank(mass_s[c], c, E, mass_s);
       if (rank < M) sel_id[rank] = cand_id[c];
     }
-    __syncthreads();
+    wave_sync();
     if (p.sel_out)
       for (int m = lane; m < p.sel_cap; m += 64)
         p.sel_out[(((size_t)b * p.T + t) * p.H + h) * p.sel_cap + m] = m < M ? sel_id[m] : -1;
@@ -433,14 +497,14 @@ __global__ __launch_bounds__(64) void f32_read_kernel(F32Params p) {
       }
       const float ps = channel_fold<R>(ch);
       if ((m & 63) == lane) slot[m >> 6] = ps;
-      __syncthreads();
+      wave_sync();
       const float* c = bank + (size_t)id * D * D;
       for (int dd = 0; dd < D; ++dd) {
         const float w = row_s[dd];
 #pragma unroll
         for (int r = 0; r < R; ++r) num[r] = fmaf(w, c[dd * D + lane + 64 * r], num[r]);
       }
-      __syncthreads();
+      wave_sync();
     }
     const float den = slot_fold<4>(slot, M);
     float fine[R];
@@ -453,7 +517,7 @@ __global__ __launch_bounds__(64) void f32_read_kernel(F32Params p) {
       for (int pg = 0; pg < completed; ++pg) {
 #pragma unroll
         for (int r = 0; r < R; ++r) row_s[lane + 64 * r] = hq[r] * cw[pg][lane + 64 * r];
-        __syncthreads();
+        wave_sync();
         const float* c = pcb + (size_t)pg * D * D;
         for (int dd = 0; dd < D; ++dd) {
           const float w = row_s[dd];
@@ -461,7 +525,7 @@ __global__ __launch_bounds__(64) void f32_read_kernel(F32Params p) {
           for (int r = 0; r < R; ++r)
             coarse_v[r] = fmaf(w, c[dd * D + lane + 64 * r], coarse_v[r]);
         }
-        __syncthreads();
+        wave_sync();
       }
     }
 
@@ -539,20 +603,23 @@ hipError_t launch_full_f32(const F32Params& p, hipStream_t s) {
   const dim3 heads((unsigned)p.H, (unsigned)p.B);
   auto grid = [&](int64_t x) { return dim3((unsigned)x, heads.x, heads.y); };
   if (p.D == 64) {
-    hipLaunchKernelGGL(f32_local_kernel<64>, grid((p.T + 63) / 64), dim3(64), 0, s, p);
+    hipLaunchKernelGGL(f32_local_kernel<64>, grid((p.T + 63) / 64), dim3(64 * kLocalWaves<64>), 0,
+                       s, p);
     if (p.S) {
       hipLaunchKernelGGL(f32_writer_kernel<64>, grid(p.S), dim3(256), 0, s, p);
       hipLaunchKernelGGL(f32_pages_kernel<64>, grid(p.P8), dim3(64), 0, s, p);
     }
-    hipLaunchKernelGGL(f32_read_kernel<64>, grid((p.T + kChunk - 1) / kChunk), dim3(64), 0, s, p);
+    hipLaunchKernelGGL(f32_read_kernel<64>, grid((p.T + kChunk - 1) / kChunk), dim3(64 * kReadWaves),
+                       0, s, p);
   } else if (p.D == 128) {
-    hipLaunchKernelGGL(f32_local_kernel<128>, grid((p.T + 63) / 64), dim3(64), 0, s, p);
+    hipLaunchKernelGGL(f32_local_kernel<128>, grid((p.T + 63) / 64), dim3(64 * kLocalWaves<128>),
+                       0, s, p);
     if (p.S) {
       hipLaunchKernelGGL(f32_writer_kernel<128>, grid(p.S), dim3(512), 0, s, p);
       hipLaunchKernelGGL(f32_pages_kernel<128>, grid(p.P8), dim3(128), 0, s, p);
     }
-    hipLaunchKernelGGL(f32_read_kernel<128>, grid((p.T + kChunk - 1) / kChunk), dim3(64), 0, s,
-                       p);
+    hipLaunchKernelGGL(f32_read_kernel<128>, grid((p.T + kChunk - 1) / kChunk),
+                       dim3(64 * kReadWaves), 0, s, p);
   } else {
     return hipErrorInvalidValue;
   }

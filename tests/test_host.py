@@ -97,6 +97,32 @@ def test_workspace_size_and_error_convention():
         _hip.check(rc)
 
 
+def test_prompt_attention_and_step_stamps_argument_checks():
+    """tao_prompt_attention refuses a call whose window reaches before the
+    call (a continuing prefill needs the state's ring), too few tile words
+    and bad geometry, before any device work; tao_step_stamps refuses
+    frames of fewer than 8 words and turns off with a null buffer."""
+    lib = _hip.lib()
+    cfg = _hip.StreamCfg(0, 512, 256, 8, 24, 2, 1, 2, 0)
+    tok = _hip.Tokens()
+    for name in ("q", "k", "v", "raw_q", "raw_k"):
+        setattr(tok, name, 0x1000)          # never dereferenced: checks come first
+    tok.tokens = 300
+    fake = ctypes.c_void_p(0x2000)
+    rc = lib.tao_prompt_attention(ctypes.byref(cfg), 1, 4, 128, ctypes.byref(tok), 1000,
+                                  fake, 1 << 20, fake, None)
+    assert rc < 0 and b"window" in lib.tao_last_error()
+    rc = lib.tao_prompt_attention(ctypes.byref(cfg), 1, 4, 128, ctypes.byref(tok), 0,
+                                  fake, 2, fake, None)
+    assert rc < 0 and b"tiles_cap" in lib.tao_last_error()
+    rc = lib.tao_prompt_attention(ctypes.byref(cfg), 1, 4, 96, ctypes.byref(tok), 0,
+                                  fake, 1 << 20, fake, None)
+    assert rc < 0 and b"geometry" in lib.tao_last_error()
+    assert lib.tao_step_stamps(fake, 4, 7) < 0
+    assert lib.tao_step_stamps(fake, 0, 64) < 0
+    assert lib.tao_step_stamps(None, 0, 0) == 0 and lib.tao_step_stamps_count() == 0
+
+
 def test_product_has_no_oracle_or_cpu_path():
     pkg = os.path.join(ROOT, "tao-memory_amd", "tao_attention")
     for name in os.listdir(pkg):

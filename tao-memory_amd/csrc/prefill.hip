@@ -675,6 +675,109 @@ __global__ __launch_bounds__(kGroupThreads) void read_groups_kernel(ReadTilesPar
 }
 
 
+// The fusion row phase of a turn-group read: lane (row r, unit c) fuses
+// channels 8 c .. 8 c + 7 of query r of the wave's tile from the tile's fine
+// and coarse values in LDS ([q][e], 16-byte units XOR-swizzled by the row),
+// the local attention and the raw query, and stores the output. STAGED: the
+// fusion parameters come from LDS, fpar[0][d][i] = a[h][d][i] and
+// fpar[1][d][i] = b[h][d][i].
+template <int D, bool COARSE, bool STAGED>
+TAO_DEV void fuse_rows(const ReadTilesParams& p, const float (*fpar)[D * 3], const bf16_t* tile_f,
+                       const bf16_t* tile_c, int lane, int b, int h, int q_first, int nq,
+                       bool coarse_on) {
+  constexpr int CPR = D / 8;
+  auto unit_at = [&](int row, int unit) __attribute__((always_inline)) {
+    return row * D + 8 * (unit ^ (row % CPR));
+  };
+  // Row phase: lane (row r, unit c) fuses channels 8 c .. 8 c + 7 of query r.
+  constexpr int RPI = 64 / CPR;                 // rows per pass of the wave
+  const int c = lane % CPR;
+  float ae[8][3], be[8][3];
+  if constexpr (STAGED) {
+#pragma unroll
+    for (int v = 0; v < 6; ++v) {
+      const float4 av = *(const float4*)&fpar[0][24 * c + 4 * v];
+      const float4 bv = *(const float4*)&fpar[1][24 * c + 4 * v];
+      const float af[4] = {av.x, av.y, av.z, av.w}, bf[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ae[(4 * v + e) / 3][(4 * v + e) % 3] = af[e];
+        be[(4 * v + e) / 3][(4 * v + e) % 3] = bf[e];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        ae[j][i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + (8 * c + j) * p.fa_s[1] + i * p.fa_s[2]);
+        be[j][i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + (8 * c + j) * p.fb_s[1] + i * p.fb_s[2]);
+      }
+  }
+  // Without the coarse branch: the paired two-channel fusion on the rounded
+  // parameters and the signed-zero coarse term.
+  float ra[8][3], rb[8][3];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      ra[j][i] = rbf(ae[j][i]);
+      rb[j][i] = rbf(be[j][i]);
+    }
+  const float ct0 = rbf(0.0f * rbf(p.gain * 0.0f));
+  // Every pass's local and query rows are loaded first (rows past the tile
+  // read its last row), so the passes do not wait on memory one by one
+  // behind the previous pass's stores.
+  constexpr int ITS = 32 / RPI;
+  uint4 lus[ITS], xus[ITS];
+#pragma unroll
+  for (int it = 0; it < ITS; ++it) {
+    const int tq = q_first + min(lane / CPR + RPI * it, nq - 1);
+    lus[it] = *(const uint4*)(p.local + (((size_t)b * p.T + tq) * p.H + h) * D + 8 * c);
+    xus[it] = *(const uint4*)(p.rq.p + b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + 8 * c);
+  }
+#pragma unroll
+  for (int it = 0; it < ITS; ++it) {
+    const int r = lane / CPR + RPI * it;
+    if (r >= nq) break;
+    const int tq = q_first + r;
+    const size_t row = ((size_t)b * p.T + tq) * p.H + h;
+    const uint4 fu = *(const uint4*)&tile_f[unit_at(r, c)];
+    uint4 cu = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (COARSE) {
+      if (coarse_on) cu = *(const uint4*)&tile_c[unit_at(r, c)];
+    }
+    const uint4 lu = lus[it];
+    const uint4 xu = xus[it];
+    float fv[8], cv[8], lv[8], xv[8];
+    unpack8f(fu, fv);
+    unpack8f(cu, cv);
+    unpack8f(lu, lv);
+    unpack8f(xu, xv);
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (!COARSE) {
+        o[j] = fuse_pair_local_fine(&xv[2 * j], &lv[2 * j], &fv[2 * j], &ra[2 * j], &rb[2 * j],
+                                    p.gain, ct0);
+      } else {
+        const bf16_t lo = fuse_element(xv[2 * j], lv[2 * j], cv[2 * j], fv[2 * j], ae[2 * j],
+                                       be[2 * j], p.gain, coarse_on ? 1 : 0, 1);
+        const bf16_t hi = fuse_element(xv[2 * j + 1], lv[2 * j + 1], cv[2 * j + 1], fv[2 * j + 1],
+                                       ae[2 * j + 1], be[2 * j + 1], p.gain, coarse_on ? 1 : 0, 1);
+        o[j] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+      }
+    }
+    *(uint4*)(p.out + b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + 8 * c) =
+        make_uint4(o[0], o[1], o[2], o[3]);
+    if (p.save_fine) {
+      *(uint4*)(p.save_fine + row * D + 8 * c) = fu;
+      *(uint4*)(p.save_coarse + row * D + 8 * c) = cu;
+    }
+  }
+}
+
 // ---- Turn-route read with a ring of fines staged by direct loads into LDS.
 //
 // read_stream_kernel serves the prefill (turn routes; per-query routes take
@@ -736,6 +839,25 @@ TAO_DEV u32x4 lds_read16(uint32_t addr) {
   asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
   return r;
 }
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in
+// order: a loop whose body needs its index as a constant.
+template <typename F, int... I>
+TAO_DEV void static_for_seq(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+TAO_DEV void static_for(F&& f) {
+  static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+// The same at addr + OFF (the instruction's immediate offset, so one
+// address register serves several reads).
+template <int OFF>
+TAO_DEV u32x4 lds_read16_at(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "16-bit LDS offset");
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+  return r;
+}
 // s_waitcnt lgkmcnt(0), tied to the values it makes ready (so nothing that
 // reads them is scheduled above it).
 TAO_DEV void wait_lds(u32x4& a) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a)::"memory"); }
@@ -746,11 +868,16 @@ TAO_DEV void wait_lds(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)::"memory");
 }
 // s_waitcnt lgkmcnt(N): every LDS read but the newest N has landed, which
-// covers a and b when N reads were issued after them.
+// covers the values tied to it when N reads were issued after them.
 template <int N>
 TAO_DEV void wait_lds_behind(u32x4& a, u32x4& b) {
-  if constexpr (N == 4) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(a), "+v"(b)::"memory");
-  else asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(a), "+v"(b)::"memory");
+  static_assert(N >= 0 && N < 16, "lgkmcnt is four bits");
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
+}
+template <int N>
+TAO_DEV void wait_lds_behind(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is four bits");
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
 }
 TAO_DEV uint4 as_uint4(const u32x4& v) { return make_uint4(v.x, v.y, v.z, v.w); }
 TAO_DEV void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
@@ -846,6 +973,14 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
 #pragma unroll
       for (int j = 0; j < 8; ++j) hf[kk][j] = rbf(hf[kk][j] * inv);
   }
+  // The same h as bf16 pairs (exact: h is rounded to bf16), channel 2 i of
+  // the lane's eight in the low half of hp[kk][i]: the index-only read keeps
+  // these instead of hf, which leaves registers for its operand pipeline.
+  uint32_t hp[KK][4];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hp[kk][i] = pack_bf16x2(hf[kk][2 * i], hf[kk][2 * i + 1]);
 
   // Feature writers: the mixture's normaliser for query li, the sum over the
   // wave's selected fines of mass = sum_d h[d] exp(z[d]) (fp32, the same
@@ -1051,56 +1186,107 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
       const int s = u % kRing;
       const uint32_t cs = lds_addr(&ring[s][0]);
       const uint32_t ws = lds_addr(&sm.wf[s][8 * hl]);
-      // The operands of step kk + 1 (the weights at d = 16 kk + 8 hl, then the
-      // C^T rows e = 32 t + li there) are read while step kk's MFMAs run; step
-      // kk + 1 waits for its weights, builds its A operand while its rows land,
-      // then waits for those.
-      auto reads = [&](int kk, u32x4(&bq)[ET], u32x4& w0, u32x4& w1) __attribute__((always_inline)) {
-        const int c = 2 * kk + hl;             // logical chunk of d0 = 16 kk + 8 hl
-        w0 = lds_read16(ws + 64 * kk);
-        w1 = lds_read16(ws + 64 * kk + 16);
-#pragma unroll
-        for (int t = 0; t < ET; ++t) {
-          const int row = 32 * t + li;
-          bq[t] = lds_read16(cs + (uint32_t)(row * D + 8 * (c ^ (row % CPR))) * 2);
+      // Step kk runs the ET MFMAs of k-step kk and, between them, builds the
+      // A operand of step kk + 1 (r(h * w), two channels per MFMA gap) and
+      // adds step kk's operand into den, so the VALU work issues while the
+      // matrix core is busy. Operands are read two steps ahead: stage kk is
+      // step kk's C^T rows and step kk + 1's weights.
+      //
+      // Row e = 32 t + li keeps logical chunk c at c ^ (e % CPR) = c ^ (li % CPR)
+      // (32 t is a multiple of CPR), so one address per step serves every t
+      // through the read's immediate offset.
+      static_assert(32 % CPR == 0, "row swizzle independent of the e-tile");
+      const uint32_t rowb = cs + (uint32_t)(li * D) * 2;
+      auto read_c = [&](auto kkc, u32x4(&bq)[ET]) __attribute__((always_inline)) {
+        constexpr int kk = decltype(kkc)::value;
+        const uint32_t at = rowb + (uint32_t)((2 * kk + hl) ^ (li % CPR)) * 16;
+        bq[0] = lds_read16_at<0>(at);
+        bq[1] = lds_read16_at<32 * D * 2>(at);
+        if constexpr (ET == 4) {
+          bq[2] = lds_read16_at<64 * D * 2>(at);
+          bq[3] = lds_read16_at<96 * D * 2>(at);
         }
       };
-      u32x4 bq[ET], w0, w1;
-      reads(0, bq, w0, w1);
+      auto read_w = [&](auto kkc, u32x4& w0, u32x4& w1) __attribute__((always_inline)) {
+        constexpr int kk = decltype(kkc)::value;
+        w0 = lds_read16_at<64 * kk>(ws);
+        w1 = lds_read16_at<64 * kk + 16>(ws);
+      };
+      // Stage kk's reads: the rows, then the next step's weights if any.
+      auto stage = [&](auto kkc, u32x4(&bq)[ET], u32x4& w0, u32x4& w1) __attribute__((always_inline)) {
+        constexpr int kk = decltype(kkc)::value;
+        read_c(kkc, bq);
+        if constexpr (kk + 1 < KK) read_w(std::integral_constant<int, kk + 1>{}, w0, w1);
+      };
+      auto stage_reads = [](int kk) constexpr { return ET + (kk + 1 < KK ? 2 : 0); };
+      // Channel pair i of step kk's A operand.
+      auto a_pair = [&](int kk, int i, const u32x4& w0, const u32x4& w1) __attribute__((always_inline)) {
+        const u32x4& wv = i < 2 ? w0 : w1;
+        const uint32_t x = (i & 1) ? wv.z : wv.x, y = (i & 1) ? wv.w : wv.y;
+        const uint32_t hv = hp[kk][i];
+        return pack_bf16x2(__uint_as_float(hv << 16) * __uint_as_float(x),
+                           __uint_as_float(hv & 0xFFFF0000u) * __uint_as_float(y));
+      };
+
+      // hp is loop-invariant: left visible, the compiler hoists its
+      // unpacking out of the fine loop and holds all of hf again.
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        wait_lds_behind<ET>(w0, w1);
-        const bf16x8 a = as_bf16x8(make_uint4(
-            pack_bf16x2(hf[kk][0] * __uint_as_float(w0.x), hf[kk][1] * __uint_as_float(w0.y)),
-            pack_bf16x2(hf[kk][2] * __uint_as_float(w0.z), hf[kk][3] * __uint_as_float(w0.w)),
-            pack_bf16x2(hf[kk][4] * __uint_as_float(w1.x), hf[kk][5] * __uint_as_float(w1.y)),
-            pack_bf16x2(hf[kk][6] * __uint_as_float(w1.z), hf[kk][7] * __uint_as_float(w1.w))));
-        if constexpr (ET == 4) wait_lds(bq[0], bq[1], bq[2], bq[3]);
-        else wait_lds(bq[0], bq[1]);
-        u32x4 bn[ET], n0, n1;
-        if (kk + 1 < KK) reads(kk + 1, bn, n0, n1);
-        // num^T[e][q]: the C^T rows are the A operand, so lane li ends up
-        // holding query li.
+      for (int kk = 0; kk < KK; ++kk)
+        asm volatile("" : "+v"(hp[kk][0]), "+v"(hp[kk][1]), "+v"(hp[kk][2]), "+v"(hp[kk][3]));
+      uint32_t a_cur[4];
+      {
+        u32x4 w0, w1;
+        read_w(std::integral_constant<int, 0>{}, w0, w1);
+        wait_lds(w0, w1);
 #pragma unroll
-        for (int t = 0; t < ET; ++t)
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(as_uint4(bq[t])), a, acc[t],
-                                                           0, 0, 0);
-        const uint4 au = __builtin_bit_cast(uint4, a);
-        den_part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, au.x), ones2,
-                                                   den_part, false);
-        den_part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, au.y), ones2,
-                                                   den_part, false);
-        den_part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, au.z), ones2,
-                                                   den_part, false);
-        den_part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, au.w), ones2,
-                                                   den_part, false);
-        if (kk + 1 < KK) {
-#pragma unroll
-          for (int t = 0; t < ET; ++t) bq[t] = bn[t];
-          w0 = n0;
-          w1 = n1;
-        }
+        for (int i = 0; i < 4; ++i) a_cur[i] = a_pair(0, i, w0, w1);
       }
+      u32x4 c0[ET], v0a, v0b, c1[ET], v1a, v1b;
+      stage(std::integral_constant<int, 0>{}, c0, v0a, v0b);
+      if constexpr (KK > 1) stage(std::integral_constant<int, 1>{}, c1, v1a, v1b);
+      static_for<KK>([&](auto kkc) __attribute__((always_inline)) {
+        constexpr int kk = decltype(kkc)::value;
+        // Stage kk has landed when only stage kk + 1's reads are in flight.
+        constexpr int behind = kk + 1 < KK ? stage_reads(kk + 1) : 0;
+        if constexpr (ET == 4) wait_lds_behind<behind>(c0[0], c0[1], c0[2], c0[3]);
+        else wait_lds_behind<behind>(c0[0], c0[1]);
+        wait_lds_behind<behind>(v0a, v0b);
+        u32x4 c2[ET], v2a, v2b;
+        if constexpr (kk + 2 < KK) stage(std::integral_constant<int, kk + 2>{}, c2, v2a, v2b);
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t a_next[4];
+        const bf16x8 a = as_bf16x8(make_uint4(a_cur[0], a_cur[1], a_cur[2], a_cur[3]));
+#pragma unroll
+        for (int t = 0; t < ET; ++t) {
+          // num^T[e][q]: the C^T rows are the A operand, so lane li ends up
+          // holding query li.
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(as_uint4(c0[t])), a, acc[t],
+                                                           0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = t * 4 / ET; i < (t + 1) * 4 / ET; ++i)
+            if constexpr (kk + 1 < KK) a_next[i] = a_pair(kk + 1, i, v0a, v0b);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          den_part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a_cur[i]), ones2,
+                                                     den_part, false);
+        if constexpr (kk + 1 < KK) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a_cur[i] = a_next[i];
+#pragma unroll
+          for (int t = 0; t < ET; ++t) c0[t] = c1[t];
+          v0a = v1a;
+          v0b = v1b;
+        }
+        if constexpr (kk + 2 < KK) {
+#pragma unroll
+          for (int t = 0; t < ET; ++t) c1[t] = c2[t];
+          v1a = v2a;
+          v1b = v2b;
+        }
+      });
     };
     // Barrier that publishes the ring: the caller has waited for its own
     // loads; the weights written by wave 0 are ordinary LDS stores.
@@ -1116,9 +1302,11 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
     }
     ring_barrier();
     for (int u = 0; u < U; ++u) {
-      if (u + kRing - 1 < U) issue(u + kRing - 1);
+      // A selecting wave consumes first: its issue waits for the memory
+      // pipeline that the other waves' issues have just filled.
       if constexpr (FEAT) consume_feat(u);
       else consume(u);
+      if (u + kRing - 1 < U) issue(u + kRing - 1);
       if (u + 1 < U) {
         wait_behind(min(U - 1, u + kRing - 1) - (u + 1));
         make_wr(u + 1);
@@ -1169,9 +1357,7 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
           gb[kk] = *(const uint4*)(gc + (size_t)(32 * t + li) * D + 16 * kk + 8 * hl);
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-          const bf16x8 a = as_bf16x8(make_uint4(
-              pack_bf16x2(hf[kk][0], hf[kk][1]), pack_bf16x2(hf[kk][2], hf[kk][3]),
-              pack_bf16x2(hf[kk][4], hf[kk][5]), pack_bf16x2(hf[kk][6], hf[kk][7])));
+          const bf16x8 a = as_bf16x8(make_uint4(hp[kk][0], hp[kk][1], hp[kk][2], hp[kk][3]));
           cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(gb[kk]), a, cacc, 0, 0, 0);
         }
 #pragma unroll
@@ -1231,94 +1417,13 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
                          pack_bf16x2(cacc[t][4 * g + 2], cacc[t][4 * g + 3]));
     }
   }
-  // Row phase: lane (row r, unit c) fuses channels 8 c .. 8 c + 7 of query r.
-  constexpr int RPI = 64 / CPR;                 // rows per pass of the wave
-  const int c = lane % CPR;
-  float ae[8][3], be[8][3];
-  if constexpr (kStageParams) {
-#pragma unroll
-    for (int v = 0; v < 6; ++v) {
-      const float4 av = *(const float4*)&fpar[0][24 * c + 4 * v];
-      const float4 bv = *(const float4*)&fpar[1][24 * c + 4 * v];
-      const float af[4] = {av.x, av.y, av.z, av.w}, bf[4] = {bv.x, bv.y, bv.z, bv.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        ae[(4 * v + e) / 3][(4 * v + e) % 3] = af[e];
-        be[(4 * v + e) / 3][(4 * v + e) % 3] = bf[e];
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        ae[j][i] = load_param(p.fa, p.f_dtype, h * p.fa_s[0] + (8 * c + j) * p.fa_s[1] + i * p.fa_s[2]);
-        be[j][i] = load_param(p.fb, p.f_dtype, h * p.fb_s[0] + (8 * c + j) * p.fb_s[1] + i * p.fb_s[2]);
-      }
-  }
-  // Without the coarse branch: the paired two-channel fusion on the rounded
-  // parameters and the signed-zero coarse term.
-  float ra[8][3], rb[8][3];
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      ra[j][i] = rbf(ae[j][i]);
-      rb[j][i] = rbf(be[j][i]);
-    }
-  const float ct0 = rbf(0.0f * rbf(p.gain * 0.0f));
-  // Every pass's local and query rows are loaded first (rows past the tile
-  // read its last row), so the passes do not wait on memory one by one
-  // behind the previous pass's stores.
-  constexpr int ITS = 32 / RPI;
-  uint4 lus[ITS], xus[ITS];
-#pragma unroll
-  for (int it = 0; it < ITS; ++it) {
-    const int tq = q_first + min(lane / CPR + RPI * it, nq - 1);
-    lus[it] = *(const uint4*)(p.local + (((size_t)b * p.T + tq) * p.H + h) * D + 8 * c);
-    xus[it] = *(const uint4*)(p.rq.p + b * p.rq.sb + (int64_t)tq * p.rq.st + h * p.rq.sh + 8 * c);
-  }
-#pragma unroll
-  for (int it = 0; it < ITS; ++it) {
-    const int r = lane / CPR + RPI * it;
-    if (r >= nq) break;
-    const int tq = q_first + r;
-    const size_t row = ((size_t)b * p.T + tq) * p.H + h;
-    const uint4 fu = *(const uint4*)&tile_f[unit_at(r, c)];
-    uint4 cu = make_uint4(0u, 0u, 0u, 0u);
-    if constexpr (COARSE) {
-      if (coarse_on) cu = *(const uint4*)&tile_c[unit_at(r, c)];
-    }
-    const uint4 lu = lus[it];
-    const uint4 xu = xus[it];
-    float fv[8], cv[8], lv[8], xv[8];
-    unpack8f(fu, fv);
-    unpack8f(cu, cv);
-    unpack8f(lu, lv);
-    unpack8f(xu, xv);
-    uint32_t o[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if constexpr (!COARSE) {
-        o[j] = fuse_pair_local_fine(&xv[2 * j], &lv[2 * j], &fv[2 * j], &ra[2 * j], &rb[2 * j],
-                                    p.gain, ct0);
-      } else {
-        const bf16_t lo = fuse_element(xv[2 * j], lv[2 * j], cv[2 * j], fv[2 * j], ae[2 * j],
-                                       be[2 * j], p.gain, coarse_on ? 1 : 0, 1);
-        const bf16_t hi = fuse_element(xv[2 * j + 1], lv[2 * j + 1], cv[2 * j + 1], fv[2 * j + 1],
-                                       ae[2 * j + 1], be[2 * j + 1], p.gain, coarse_on ? 1 : 0, 1);
-        o[j] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-      }
-    }
-    *(uint4*)(p.out + b * p.out_sb + (int64_t)tq * p.out_st + h * p.out_sh + 8 * c) =
-        make_uint4(o[0], o[1], o[2], o[3]);
-    if (p.save_fine) {
-      *(uint4*)(p.save_fine + row * D + 8 * c) = fu;
-      *(uint4*)(p.save_coarse + row * D + 8 * c) = cu;
-    }
-  }
+  if constexpr (kStageParams)
+    fuse_rows<D, COARSE, true>(p, fpar, tile_f, tile_c, lane, b, h, q_first, nq, coarse_on);
+  else
+    fuse_rows<D, COARSE, false>(p, nullptr, tile_f, tile_c, lane, b, h, q_first, nq, coarse_on);
 }
+
+
 
 }  // namespace
 

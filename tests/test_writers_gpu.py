@@ -397,7 +397,8 @@ def test_full_sequence_feature_writers(device, writer, width, tokens, batch, ind
     """tao_attention with the feature writers (index-only, forward): every
     query's selected set bit-exact against the oracle's per-query routing
     over log-mass descriptors, outputs within the bf16 tolerance of its
-    numerator-only mixture read; gradients raise."""
+    numerator-only mixture read (their gradients are checked in
+    test_gpu_parity.py::test_full_sequence_backward_feature_writers)."""
     from oracle import tao_oracle as O
     from tao_attention import TaoConfig, tao_attention, training
     heads = 2

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TAO_ABI_VERSION 12
+#define TAO_ABI_VERSION 13
 
 enum tao_status {
   TAO_OK = 0,
@@ -467,6 +467,18 @@ int tao_full_sequence_f32(const tao_stream_cfg* cfg, const tao_tokens* tok, cons
                           int32_t batch, int32_t heads, int32_t head_dim, int32_t coarse_values,
                           void* out, const int64_t* out_s, int32_t* sel_out, int32_t sel_cap,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* tao_full_sequence_f32 with the local attention supplied by the caller
+ * (the reference's read_training called with a local_flash plugin on fp32
+ * operands, operator.py:40-52, tao_stream.py:760-787): local is fp32
+ * [B, T, H, D] contiguous, read only; the read, routes and fusion are those
+ * of tao_full_sequence_f32. */
+int tao_full_sequence_f32_local(const tao_stream_cfg* cfg, const tao_tokens* tok,
+                                const tao_fusion* fu, int32_t batch, int32_t heads,
+                                int32_t head_dim, int32_t coarse_values, const void* local,
+                                void* out, const int64_t* out_s, int32_t* sel_out,
+                                int32_t sel_cap, void* workspace, size_t workspace_bytes,
+                                void* stream);
 
 /* Numerics self-test (no reference counterpart): y[i] = the library's
  * bf16(correctly rounded fp32 exp(x[i])) (op 0) or log (op 1) for n bf16

@@ -599,12 +599,13 @@ int f32_limits(const tao_stream_cfg& cfg, int64_t T, int64_t* pages, int64_t* ca
   return *pages <= kMaxPages && *cand <= kMaxCand && sel <= kMaxCand;
 }
 
-hipError_t launch_full_f32(const F32Params& p, hipStream_t s) {
+hipError_t launch_full_f32(const F32Params& p, hipStream_t s, bool own_local) {
   const dim3 heads((unsigned)p.H, (unsigned)p.B);
   auto grid = [&](int64_t x) { return dim3((unsigned)x, heads.x, heads.y); };
   if (p.D == 64) {
-    hipLaunchKernelGGL(f32_local_kernel<64>, grid((p.T + 63) / 64), dim3(64 * kLocalWaves<64>), 0,
-                       s, p);
+    if (own_local)
+      hipLaunchKernelGGL(f32_local_kernel<64>, grid((p.T + 63) / 64), dim3(64 * kLocalWaves<64>),
+                         0, s, p);
     if (p.S) {
       hipLaunchKernelGGL(f32_writer_kernel<64>, grid(p.S), dim3(256), 0, s, p);
       hipLaunchKernelGGL(f32_pages_kernel<64>, grid(p.P8), dim3(64), 0, s, p);
@@ -612,8 +613,9 @@ hipError_t launch_full_f32(const F32Params& p, hipStream_t s) {
     hipLaunchKernelGGL(f32_read_kernel<64>, grid((p.T + kChunk - 1) / kChunk), dim3(64 * kReadWaves),
                        0, s, p);
   } else if (p.D == 128) {
-    hipLaunchKernelGGL(f32_local_kernel<128>, grid((p.T + 63) / 64), dim3(64 * kLocalWaves<128>),
-                       0, s, p);
+    if (own_local)
+      hipLaunchKernelGGL(f32_local_kernel<128>, grid((p.T + 63) / 64), dim3(64 * kLocalWaves<128>),
+                         0, s, p);
     if (p.S) {
       hipLaunchKernelGGL(f32_writer_kernel<128>, grid(p.S), dim3(512), 0, s, p);
       hipLaunchKernelGGL(f32_pages_kernel<128>, grid(p.P8), dim3(128), 0, s, p);
@@ -655,10 +657,16 @@ size_t tao_full_sequence_f32_workspace_bytes(int32_t batch, int32_t heads, int32
          sizeof(float);
 }
 
-int tao_full_sequence_f32(const tao_stream_cfg* cfg, const tao_tokens* tok, const tao_fusion* fu,
-                          int32_t batch, int32_t heads, int32_t head_dim, int32_t coarse_values,
-                          void* out, const int64_t* out_s, int32_t* sel_out, int32_t sel_cap,
-                          void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// tao_full_sequence_f32 and tao_full_sequence_f32_local: local null computes
+// the local attention, else the read takes it from `local`.
+int full_f32(const tao_stream_cfg* cfg, const tao_tokens* tok, const tao_fusion* fu,
+             int32_t batch, int32_t heads, int32_t head_dim, int32_t coarse_values,
+             const void* local, void* out, const int64_t* out_s, int32_t* sel_out,
+             int32_t sel_cap, void* workspace, size_t workspace_bytes, void* stream) {
   if (!cfg || !tok || !fu || !out || !out_s || !workspace)
     return f32_fail(TAO_E_ARGUMENT, "null fp32 full-sequence argument");
   if (!tok->q || !tok->k || !tok->v || !tok->raw_q || !tok->raw_k)
@@ -708,9 +716,33 @@ int tao_full_sequence_f32(const tao_stream_cfg* cfg, const tao_tokens* tok, cons
   p.H = heads;
   p.D = head_dim;
   tao::f32_layout(p, (float*)workspace, T, coarse_values ? 1 : 0);
-  const hipError_t e = tao::launch_full_f32(p, (hipStream_t)stream);
+  if (local) p.local = const_cast<float*>((const float*)local);   // read only
+  const hipError_t e = tao::launch_full_f32(p, (hipStream_t)stream, local == nullptr);
   if (e != hipSuccess) return f32_fail((int)e, hipGetErrorString(e));
   return TAO_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tao_full_sequence_f32(const tao_stream_cfg* cfg, const tao_tokens* tok, const tao_fusion* fu,
+                          int32_t batch, int32_t heads, int32_t head_dim, int32_t coarse_values,
+                          void* out, const int64_t* out_s, int32_t* sel_out, int32_t sel_cap,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  return full_f32(cfg, tok, fu, batch, heads, head_dim, coarse_values, nullptr, out, out_s,
+                  sel_out, sel_cap, workspace, workspace_bytes, stream);
+}
+
+int tao_full_sequence_f32_local(const tao_stream_cfg* cfg, const tao_tokens* tok,
+                                const tao_fusion* fu, int32_t batch, int32_t heads,
+                                int32_t head_dim, int32_t coarse_values, const void* local,
+                                void* out, const int64_t* out_s, int32_t* sel_out,
+                                int32_t sel_cap, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+  if (!local) return f32_fail(TAO_E_ARGUMENT, "null local attention output");
+  return full_f32(cfg, tok, fu, batch, heads, head_dim, coarse_values, local, out, out_s,
+                  sel_out, sel_cap, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -239,7 +239,9 @@ size_t f32_workspace_floats(int B, int H, int D, int64_t T, int coarse_values);
 int f32_layout(F32Params& p, float* ws, int64_t T, int coarse_values);
 // 1 when T fits the read kernel's LDS tables (pages, candidates, selections).
 int f32_limits(const tao_stream_cfg& cfg, int64_t T, int64_t* pages, int64_t* cand);
-hipError_t launch_full_f32(const F32Params& p, hipStream_t s);
+// own_local: run the fp32 local attention into p.local first (else the
+// caller's local attention output is there).
+hipError_t launch_full_f32(const F32Params& p, hipStream_t s, bool own_local);
 
 struct AppendParams {
   TokView k, v, rk;

@@ -155,6 +155,9 @@ _SIGNATURES = {
     "tao_full_sequence_f32": ([ctypes.POINTER(StreamCfg), ctypes.POINTER(Tokens),
                                ctypes.POINTER(Fusion), _i32, _i32, _i32, _i32, _vp,
                                ctypes.POINTER(_i64), _vp, _i32, _vp, _sz, _vp], _i32),
+    "tao_full_sequence_f32_local": ([ctypes.POINTER(StreamCfg), ctypes.POINTER(Tokens),
+                                     ctypes.POINTER(Fusion), _i32, _i32, _i32, _i32, _vp, _vp,
+                                     ctypes.POINTER(_i64), _vp, _i32, _vp, _sz, _vp], _i32),
     "tao_batch_table_bytes": ([_i32], _sz),
     "tao_batch_open": ([ctypes.POINTER(_vp), _i32, _vp, _sz, _vp, ctypes.POINTER(_vp)], _i32),
     "tao_batch_sync": ([_vp, _vp], _i32),
@@ -176,7 +179,7 @@ _SIGNATURES = {
 
 EXPORTED = tuple(_SIGNATURES)
 
-ABI_VERSION = 12               # TAO_ABI_VERSION of include/tao_memory.h
+ABI_VERSION = 13               # TAO_ABI_VERSION of include/tao_memory.h
 
 # Decode-graph epoch counters (enum tao_graph_stat / tao_graph_reason).
 GRAPH_STATS = 19

@@ -24,8 +24,8 @@ def tao_attention(q, k, v, *, raw_q, raw_k, fusion_a, fusion_b, alpha,
     operands; fp32 operands take the forward-only fp32 read
     (training.forward_f32: every rounding point at fp32). A caller
     local_flash plugin computes the local attention with the reference's
-    tiling (tao_stream.py:760-787) and is differentiated by autograd; the
-    rest stays on the HIP path.
+    tiling (tao_stream.py:760-787), on the operands' dtype, and is
+    differentiated by autograd (bf16); the rest stays on the HIP path.
     """
     return training.full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b,
                                        alpha, config, local_flash=caller_plugin(local_flash))

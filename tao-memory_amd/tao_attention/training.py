@@ -214,7 +214,8 @@ def forward(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_rou
     return out
 
 
-def forward_f32(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_routes=False):
+def forward_f32(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return_routes=False,
+                local=None):
     """tao_attention on fp32 operands (tao_full_sequence_f32), forward only.
 
     The reference's torch operations follow the operand dtype
@@ -223,11 +224,18 @@ def forward_f32(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return
     path's orders, so routes are reproducible bit for bit and the output is
     within 1e-4 of exact arithmetic. Returns fp32 [B, T, H, D] and, with
     return_routes, each query's selected fine ids in score order (int32
-    [B, T, H, M_max], -1 padded)."""
+    [B, T, H, M_max], -1 padded). local: a caller plugin's local attention
+    output (fp32 [B, T, H, D]), taken in place of the library's
+    (tao_full_sequence_f32_local)."""
     if config.fine_writer != "softmax":
         raise NotImplementedError("the fp32 full-sequence read implements the softmax writer")
     _check(q, k, v, raw_q, raw_k, config, dtype=torch.float32)
     b, tokens, heads, d = q.shape
+    if local is not None:
+        if local.shape != q.shape or local.dtype != torch.float32 or local.device != q.device:
+            raise ValueError(f"the local attention output must be fp32 {tuple(q.shape)} on "
+                             f"{q.device}, got {local.dtype} {tuple(local.shape)}")
+        local = local.contiguous()
     out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
     sel = None
     if return_routes:
@@ -255,11 +263,14 @@ def forward_f32(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, return
                           config.route_period, config.layer_stagger,
                           config.budget_root_scale, config.budget_offset, 0)
     out_s = (ctypes.c_int64 * 3)(*_hip.strides_bth(out))
-    _hip.check(lib.tao_full_sequence_f32(
-        ctypes.byref(scfg), ctypes.byref(tok), ctypes.byref(fu32), b, heads, d, coarse,
-        out.data_ptr(), out_s, None if sel is None else sel.data_ptr(),
-        0 if sel is None else sel.shape[-1], scratch.data_ptr(), nbytes,
-        _hip.stream_ptr(q.device)))
+    tail = (out.data_ptr(), out_s, None if sel is None else sel.data_ptr(),
+            0 if sel is None else sel.shape[-1], scratch.data_ptr(), nbytes,
+            _hip.stream_ptr(q.device))
+    head = (ctypes.byref(scfg), ctypes.byref(tok), ctypes.byref(fu32), b, heads, d, coarse)
+    if local is None:
+        _hip.check(lib.tao_full_sequence_f32(*head, *tail))
+    else:
+        _hip.check(lib.tao_full_sequence_f32_local(*head, local.data_ptr(), *tail))
     return (out, sel) if return_routes else out
 
 
@@ -444,13 +455,16 @@ def full_sequence_read(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha,
     alpha_grad = torch.is_tensor(alpha) and alpha.requires_grad
     grad = torch.is_grad_enabled() and (alpha_grad or any(t.requires_grad for t in tensors))
     if q.dtype == torch.float32:
-        if local_flash is not None:
-            raise NotImplementedError("a local_flash plugin with fp32 operands")
         if grad:
             raise NotImplementedError(
                 "the fp32 full-sequence read is forward-only: run it under torch.no_grad() "
                 "or on bf16 operands for gradients")
-        return forward_f32(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config)
+        local = None
+        if local_flash is not None:
+            from .flash_attention import plugin_training_local
+            _check(q, k, v, raw_q, raw_k, config, dtype=torch.float32)
+            local = plugin_training_local(local_flash, q, k, v, config)
+        return forward_f32(q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha, config, local=local)
     if local_flash is not None:
         from .flash_attention import plugin_training_local
         _check(q, k, v, raw_q, raw_k, config)

@@ -101,6 +101,46 @@ def test_fp32_bf16_fusion_parameters_and_strided_operands():
     torch.testing.assert_close(got.cpu(), ref, **TOL32)
 
 
+@pytest.mark.parametrize("tokens,cfg", [(2048, index_only_page_memo()), (2100, TaoConfig())])
+def test_fp32_with_a_local_flash_plugin(tokens, cfg):
+    """fp32 operands with a caller plugin (operator.py:40-52 passes
+    local_flash to read_training at any dtype): the plugin is called with the
+    reference's tiling on the fp32 operands (here the reference adapter's
+    SDPA modes in fp32, recorded), the read takes its fp32 output
+    (tao_full_sequence_f32_local), routes stay bit-exact and the output is
+    within the fp32 tolerance of the oracle."""
+    from types import SimpleNamespace
+    from test_gpu_plugin import sdpa_fp32
+    xs, fa, fb = config0_inputs(1, tokens, 2, 64, 21)
+    dev = [x.cuda() for x in xs]
+    calls = []
+
+    def recorded(q, k, v, causal=True, window_size=(-1, 0)):
+        assert q.dtype == torch.float32 and k.dtype == torch.float32
+        calls.append((q.shape[1], k.shape[1]))
+        return sdpa_fp32(q, k, v, causal=causal, window_size=window_size)
+
+    plugin = SimpleNamespace(flash_attn_func=recorded)
+    print(f"fp32 with plugin T{tokens} index_only={cfg.coarse_index_only}", flush=True)
+    with torch.no_grad():
+        out = tao_attention(*dev[:3], raw_q=dev[3], raw_k=dev[4], fusion_a=fa.cuda(),
+                            fusion_b=fb.cuda(), alpha=0.5, config=cfg, local_flash=plugin)
+        own = tao_attention(*dev[:3], raw_q=dev[3], raw_k=dev[4], fusion_a=fa.cuda(),
+                            fusion_b=fb.cuda(), alpha=0.5, config=cfg)
+        from tao_attention.flash_attention import plugin_training_local
+        local = plugin_training_local(SimpleNamespace(flash_attn_func=sdpa_fp32), *dev[:3], cfg)
+        _, sel = training.forward_f32(*dev, fa.cuda(), fb.cuda(), 0.5, cfg,
+                                      return_routes=True, local=local)
+    assert out.dtype == torch.float32 and calls
+    ref, routes = O.training_forward(*xs, fa, fb, 0.5, O.Geometry.from_config(cfg),
+                                     return_routes=True)
+    check_routes(sel, routes, tokens)
+    torch.testing.assert_close(out.cpu(), ref, **TOL32)
+    torch.testing.assert_close(out, own, **TOL32)
+    with pytest.raises(ValueError):
+        training.forward_f32(*dev, fa.cuda(), fb.cuda(), 0.5, cfg, local=local[:, 1:])
+
+
 def test_fp32_contract_errors():
     xs, fa, fb = config0_inputs(1, 300, 2, 64, 12)
     dev = [x.cuda() for x in xs]

@@ -82,7 +82,7 @@ def test_library_exports_every_header_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert sorted(_hip.EXPORTED) == declared
-    assert lib.tao_abi_version() == _hip.ABI_VERSION == 12
+    assert lib.tao_abi_version() == _hip.ABI_VERSION == 13
 
 
 def test_workspace_size_and_error_convention():

@@ -1301,6 +1301,27 @@ class DecodeBatch:
         elif gens != self._gens:
             _hip.check(lib.tao_batch_sync(self._handle, stream))
             self._gens = gens
+        # What the next steps may skip re-checking (_bound): the operands'
+        # geometry, each state's driver and buffers, and the last position
+        # whose token its bank holds without growing.
+        cfg = first.config
+        self._sig = (q.dtype, q.shape[2], q.shape[3], q.device)
+        self._serials = tuple(st._handle_serial for st in self.states)
+        self._limits = tuple(cfg.serve_limit + st._dev.fine_cap * cfg.fine_tokens - 1
+                             for st in self.states)
+
+    def _bound(self, q):
+        """True when the last _bind holds for this step: the same operand
+        geometry, no state re-opened, resized or advanced outside the batch
+        since, and every bank large enough for this token."""
+        if self._handle is None or self._sig != (q.dtype, q.shape[2], q.shape[3], q.device):
+            return False
+        for st, gen, serial, limit in zip(self.states, self._gens, self._serials, self._limits):
+            dev = st._dev
+            if (dev is None or dev.generation != gen or st._handle_serial != serial
+                    or st._handle_dirty or st._handle is None or st.position + 1 > limit):
+                return False
+        return True
 
     def decode(self, q, k, v, raw_q, raw_k, fusion_a, fusion_b, alpha):
         """One token for each request: operands [R, 1, H, D]; returns [R, 1, H, D]."""
@@ -1316,7 +1337,8 @@ class DecodeBatch:
         if len({id(st) for st in self.states}) != R:
             raise ValueError("a state appears twice in the batch")
         q, k, v, raw_q, raw_k = _hip.vector_operands(q, k, v, raw_q, raw_k)
-        self._bind(q)
+        if not self._bound(q):
+            self._bind(q)
         tok = _hip.tokens(q, k, v, raw_q, raw_k)
         fu = _hip.fusion(fusion_a, fusion_b, alpha, False, True, like=q)
         out = torch.empty_like(q)

@@ -430,19 +430,22 @@ def run_cold(torch, args, device, cfg, heads, width, context, n_states, probe):
         _, states[j] = tao_attention_decode(q[:, :1], k[:, :1], v[:, :1], raw_q=rq[:, :1],
                                             raw_k=rk[:, :1], fusion_a=fa, fusion_b=fb,
                                             alpha=0.5, state=st, position=st.get_pos())
+    # Each step's [1, 1, H, D] operand views are taken before the timed
+    # region, as in decode_loop.
+    rows = [tuple(x[:, 1 + i // n_states:2 + i // n_states] for x in toks[i % n_states])
+            for i in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         j = i % n_states
         st = states[j]
-        q, k, v, rq, rk = toks[j]
-        t = 1 + i // n_states
-        sl = slice(t, t + 1)
-        _, states[j] = tao_attention_decode(q[:, sl], k[:, sl], v[:, sl], raw_q=rq[:, sl],
-                                            raw_k=rk[:, sl], fusion_a=fa, fusion_b=fb,
-                                            alpha=0.5, state=st, position=st.get_pos())
+        q, k, v, rq, rk = rows[i]
+        _, states[j] = tao_attention_decode(q, k, v, raw_q=rq, raw_k=rk, fusion_a=fa,
+                                            fusion_b=fb, alpha=0.5, state=st,
+                                            position=st.get_pos())
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    del rows
     # Device time per step, GPU pre-loaded (see run_decode).
     probe.reset()
     groups = []

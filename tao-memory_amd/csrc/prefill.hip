@@ -1294,23 +1294,25 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
       wait_lds();
       __builtin_amdgcn_s_barrier();
     };
-    const int pre = min(U, kRing - 1);
-    for (int f = 0; f < pre; ++f) issue(f);
-    if (U > 0) {
-      wait_behind(pre - 1);
-      make_wr(0);
-    }
+    // Fines go in pairs, one barrier per pair: pair (u, u + 1) is read from
+    // ring slots u % 4 and (u + 1) % 4 while fines u + 2 and u + 3 load into
+    // the two slots the previous pair freed. A wave's time per barrier is
+    // then its consume of two fines, and the two fines' slowest waves are
+    // often different ones.
+    for (int f = 0; f < min(U, 2); ++f) issue(f);
+    wait_vmcnt<0>();
+    for (int f = 0; f < min(U, 2); ++f) make_wr(f);
     ring_barrier();
-    for (int u = 0; u < U; ++u) {
-      // A selecting wave consumes first: its issue waits for the memory
-      // pipeline that the other waves' issues have just filled.
+    for (int u = 0; u < U; u += 2) {
+      for (int f = u + 2; f < min(U, u + 4); ++f) issue(f);
       if constexpr (FEAT) consume_feat(u);
       else consume(u);
-      if (u + kRing - 1 < U) issue(u + kRing - 1);
       if (u + 1 < U) {
-        wait_behind(min(U - 1, u + kRing - 1) - (u + 1));
-        make_wr(u + 1);
+        if constexpr (FEAT) consume_feat(u + 1);
+        else consume(u + 1);
       }
+      wait_vmcnt<0>();        // this wave's loads of fines u + 2 and u + 3
+      for (int f = u + 2; f < min(U, u + 4); ++f) make_wr(f);
       ring_barrier();
     }
     wait_vmcnt<0>();

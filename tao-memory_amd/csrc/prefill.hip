@@ -1304,9 +1304,11 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
     for (int f = 0; f < min(U, 2); ++f) make_wr(f);
     ring_barrier();
     for (int u = 0; u < U; u += 2) {
-      for (int f = u + 2; f < min(U, u + 4); ++f) issue(f);
+      // A wave that reads fine u issues after it: the other waves' issues
+      // have just filled the memory pipeline.
       if constexpr (FEAT) consume_feat(u);
       else consume(u);
+      for (int f = u + 2; f < min(U, u + 4); ++f) issue(f);
       if (u + 1 < U) {
         if constexpr (FEAT) consume_feat(u + 1);
         else consume(u + 1);

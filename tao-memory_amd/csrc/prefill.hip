@@ -786,14 +786,15 @@ TAO_DEV void fuse_rows(const ReadTilesParams& p, const float (*fpar)[D * 3], con
 // kRing LDS slots (global_load_lds_dwordx4: lane i of a wave writes 16
 // bytes at the slot's base + 16 i, so the lane picks which global chunk
 // lands there; rows are stored with their 16-byte chunks XOR-swizzled by the
-// row index, which keeps the B-operand reads free of bank conflicts), and
-// fine u + kRing - 1 is loaded while fine u is consumed. Wave 0 also moves
-// the fine's pw and sw rows into LDS and turns them into the fine's weights
-// w = r(pw * sw) one iteration before the fine is read. A selecting wave's
-// A operand is r(h * w) (its queries' h in fp32 registers), and den[q] is the
-// fp32 sum of that operand's row (bf16 pair dot products against ones on the
-// VALU). One barrier per fine: a version whose waves ran apart through
-// per-slot LDS counters measured slower (waits for slot refills dominated).
+// row index, which keeps the B-operand reads free of bank conflicts). Fines
+// go in pairs: fines u and u + 1 are read from two slots while u + 2 and
+// u + 3 load into the other two, one barrier per pair. Wave 0 also moves a
+// fine's pw and sw rows into LDS and turns them into the fine's weights
+// w = r(pw * sw) before the barrier that publishes the fine. A selecting
+// wave's A operand is r(h * w), and den[q] is the fp32 sum of that operand's
+// row (bf16 pair dot products against ones on the VALU). A version whose
+// waves ran apart through per-slot LDS counters instead of the barrier
+// measured slower (waits for slot refills dominated).
 //
 // The ring and the staged weight rows are LDS written by the loads
 // themselves, which the compiler cannot order against its own LDS reads: it
@@ -821,15 +822,6 @@ template <int N>
 TAO_DEV void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is six bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// This wave's loads of the fine issued `after` fines before the latest have
-// completed: per fine, a wave issues PER loads.
-template <int PER>
-TAO_DEV void wait_fines(int after) {
-  if (after <= 0) wait_vmcnt<0>();
-  else if (after == 1) wait_vmcnt<PER>();
-  else wait_vmcnt<2 * PER>();
 }
 
 // 16 bytes from LDS byte address `addr`, not waited for.
@@ -891,7 +883,7 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
   constexpr int KK = D / 16, ET = D / 32, CPR = D / 8;   // k-steps, e-tiles, chunks per row
   constexpr int CPT = D * CPR / (64 * kGroupWaves);      // 1 KB wave loads per fine and wave
   static_assert(CPT * 64 * kGroupWaves == D * CPR, "whole wave loads per fine");
-  static_assert(kRing == 4, "wait_fines counts at most two fines in flight behind");
+  static_assert(kRing == 4, "two fines read while two load");
   __shared__ StreamSmem<D> sm;
   // The ring of staged C^T (swizzled rows); after the last pass, each wave's
   // fine and coarse tiles for the epilogue's transpose.
@@ -1114,12 +1106,6 @@ __global__ __launch_bounds__(kGroupThreads) void read_stream_kernel(ReadTilesPar
                              (lane - CPR) * 8;
         __builtin_amdgcn_global_load_lds(src, (lds_void_t*)&pwsw[s][0][0], 16, 0, 0);
       }
-    };
-    // Waits until this wave's loads of the fine `after` fines behind the
-    // latest issued have landed.
-    auto wait_behind = [&](int after) __attribute__((always_inline)) {
-      if (w == 0) wait_fines<CPT + 1>(after);
-      else wait_fines<CPT>(after);
     };
     // Wave 0 turns the fine's pw and sw rows into its weights.
     auto make_wr = [&](int f) __attribute__((always_inline)) {
